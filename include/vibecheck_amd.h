@@ -1,0 +1,289 @@
+/*
+ * vibecheck_amd -- C ABI of the MI355X (gfx950) batched linear-bound-
+ * propagation library.
+ *
+ * Conventions
+ *   - All tensors are fp32 (flags uint8, indices int32/int64), device
+ *     pointers, row-major, contiguous.  "B" is the number of domains
+ *     (boxes); "R" is the number of backward rows per domain (spec queries
+ *     Q, or 2k seeded rows); a backward row m belongs to domain m / R.
+ *   - Every call is asynchronous on the given HIP stream (hipStream_t passed
+ *     as void*) and returns a status code (VC_OK on success).  No call
+ *     allocates device memory; scratch comes from caller workspaces.
+ *   - Each entry point names the reference function it replaces
+ *     (src/vibecheck/<file>:<line>).
+ */
+#ifndef VIBECHECK_AMD_H
+#define VIBECHECK_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VC_OK 0
+#define VC_ERR_ARG 1         /* bad shape / null pointer / size limit */
+#define VC_ERR_OOM 2         /* workspace too small */
+#define VC_ERR_UNSUPPORTED 3 /* op or layout not supported */
+#define VC_ERR_LAUNCH 4      /* HIP launch / runtime error */
+
+typedef void *vc_stream_t;
+
+/* Library version, for the host to check the ABI it loaded. */
+int vc_abi_version(void);
+
+/* ---- ReLU relaxation ------------------------------------------------- */
+
+/* CROWN adaptive slopes, elementwise over n values.
+ * Replaces _make_slopes (verify_zono_bnb.py:503-522). */
+int vc_make_slopes(const float *lo, const float *hi, int64_t n, float *lo_s,
+                   float *up_s, float *up_t, uint8_t *active, uint8_t *dead,
+                   uint8_t *unstable, vc_stream_t stream);
+
+/* ---- IBP forward ----------------------------------------------------- */
+
+/* fc layer of the interval forward: mid/rad through W and |W|.
+ * l, h (B, n_in); W (n_out, n_in); bias (n_out) or NULL; lo, hi (B, n_out).
+ * Replaces the fc branch of _ibp_forward_graph_batched
+ * (verify_zono_bnb.py:1108-1113). */
+int vc_ibp_fc(const float *l, const float *h, int64_t B, int n_in,
+              const float *W, const float *bias, int n_out, float *lo,
+              float *hi, vc_stream_t stream);
+
+/* conv layer of the interval forward (NCHW, square stride/pad pairs).
+ * kernel (C_out, C_in, kh, kw); bias (C_out) or NULL.
+ * Replaces the conv branch of _ibp_forward_graph_batched
+ * (verify_zono_bnb.py:1098-1107). */
+int vc_ibp_conv(const float *l, const float *h, int64_t B, int C_in, int H,
+                int W, const float *kernel, const float *bias, int C_out,
+                int kh, int kw, int sh, int sw, int ph, int pw, int H_out,
+                int W_out, float *lo, float *hi, vc_stream_t stream);
+
+/* relu of the interval forward: intersect root bounds (n, nullable) and
+ * split clamps (B, n, nullable), repair hi = max(hi, lo), write the
+ * pre-activation bounds sb_lo/sb_hi (B, n) and, when post_lo/post_hi are
+ * non-NULL, the clamp(min=0) outputs.
+ * Replaces the relu branch of _ibp_forward_graph_batched
+ * (verify_zono_bnb.py:1114-1129). */
+int vc_ibp_relu(const float *l, const float *h, int64_t B, int n,
+                const float *root_lo, const float *root_hi, const float *cl,
+                const float *ch, float *sb_lo, float *sb_hi, float *post_lo,
+                float *post_hi, vc_stream_t stream);
+
+/* ---- Zonotope forward ------------------------------------------------ */
+
+/* Input zonotope: c = (xl+xh)/2 (B, n); G (B, n, K) with one column per
+ * input dim listed in var_idx (K entries), G[b, var_idx[k], k] = radius.
+ * Replaces verify_zono_bnb.py:3093-3110. */
+int vc_zono_input(const float *xl, const float *xh, int64_t B, int n,
+                  const int32_t *var_idx, int K, float *c, float *G,
+                  vc_stream_t stream);
+
+/* fc layer: c_out = c W^T + bias (B, n_out); G_out[b] = W G[b]
+ * (B, n_out, K).  Replaces verify_zono_bnb.py:3169-3173. */
+int vc_zono_fc(const float *c, const float *G, int64_t B, int n_in, int K,
+               const float *W, const float *bias, int n_out, float *c_out,
+               float *G_out, vc_stream_t stream);
+
+/* conv layer: c_out = conv2d(c, kernel) + bias; each generator column of
+ * G (B, n_in, Kg) convolved without bias into G_out (B, n_out, Kg).
+ * Replaces verify_zono_bnb.py:3400-3425. */
+int vc_zono_conv(const float *c, const float *G, int64_t B, int Kg, int C_in,
+                 int H, int W, const float *kernel, const float *bias,
+                 int C_out, int kh, int kw, int sh, int sw, int ph, int pw,
+                 int H_out, int W_out, float *c_out, float *G_out,
+                 vc_stream_t stream);
+
+/* relu stage 1: lo/hi = c -/+ sum_k |G| (B, n), and per-domain unstable
+ * counts cnt (B) plus unstable ranks rank (B, n) (exclusive count of
+ * unstable neurons before j in domain b).
+ * Replaces verify_zono_bnb.py:3175-3199. */
+int vc_zono_relu_bounds(const float *c, const float *G, int64_t B, int n,
+                        int K, float *lo, float *hi, int32_t *rank,
+                        int32_t *cnt, vc_stream_t stream);
+
+/* relu stage 2: c_out = lam c + mu; G_out (B, n, K + K_new) = [lam G | new]
+ * with new[b, j, rank[b, j]] = mu for unstable j.
+ * Replaces verify_zono_bnb.py:3185-3210. */
+int vc_zono_relu_apply(const float *c, const float *G, const float *lo,
+                       const float *hi, const int32_t *rank, int64_t B, int n,
+                       int K, int K_new, float *c_out, float *G_out,
+                       vc_stream_t stream);
+
+/* ---- CROWN backward -------------------------------------------------- */
+
+/* One backward step through [relu ->] fc, fused.
+ *   ew_in  (M, n_out), M = B * R rows; row m belongs to domain m / R.
+ *   If relu_lo/relu_hi (B, n_out) are non-NULL the rows are first relaxed
+ *   with the CROWN slopes of those pre-activation bounds:
+ *       e = pos(ew) * ls + neg(ew) * up_s [+ beta],  acc += neg(ew) . up_t
+ *   with ls = active + unstable * alpha when alpha is non-NULL (alpha is
+ *   (B, n_out), or (M, n_out) when alpha_per_row != 0), else the adaptive
+ *   lower slope; beta (B, n_out) is optional.  Then
+ *       acc += e . bias (bias nullable),  ew_out (M, n_in) = e W,
+ *   with W (n_out, n_in).  When relax_out is non-NULL the relaxed rows e
+ *   are also written there (M, n_out).  With ew_bcast != 0, ew_in is (R,
+ *   n_out) and shared by every domain (row m reads row m % R).
+ * Replaces the fc and relu branches of _spec_backward_graph_batched
+ * (verify_zono_bnb.py:4379-4453). */
+int vc_backward_fc(const float *ew_in, int64_t M, int R, int n_out,
+                   const float *relu_lo, const float *relu_hi,
+                   const float *alpha, int alpha_per_row, const float *beta,
+                   const float *W, const float *bias, int n_in, float *ew_out,
+                   float *acc, float *relax_out, int ew_bcast,
+                   vc_stream_t stream);
+
+/* relu backward step alone (for a relu that is not fed by an fc):
+ * ew_out (M, n) = relaxed rows, acc += neg(ew) . up_t.  Same arguments as
+ * the relu part of vc_backward_fc.  Replaces verify_zono_bnb.py:4409-4453. */
+int vc_backward_relu(const float *ew_in, int64_t M, int R, int n,
+                     const float *relu_lo, const float *relu_hi,
+                     const float *alpha, int alpha_per_row, const float *beta,
+                     float *ew_out, float *acc, vc_stream_t stream);
+
+/* conv backward: acc += sum ew * bias[channel]; ew_out = conv_transpose2d
+ * of ew (M, C_out*H_out*W_out) to (M, C_in*H*W).
+ * Replaces verify_zono_bnb.py:4568-4593. */
+int vc_backward_conv(const float *ew_in, int64_t M, const float *kernel,
+                     const float *bias, int C_out, int H_out, int W_out,
+                     int C_in, int H, int W, int kh, int kw, int sh, int sw,
+                     int ph, int pw, float *ew_out, float *acc,
+                     vc_stream_t stream);
+
+/* Concretization over the input boxes:
+ *   lb[m] = acc[m] + sum_i pos(A[m,i]) xl[b,i] + neg(A[m,i]) xh[b,i].
+ * A (M, n_in), acc/lb (M), xl/xh (B, n_in), M = B * R.  With a_bcast != 0,
+ * A is (R, n_in) and shared by every domain.
+ * Replaces verify_zono_bnb.py:5117-5134. */
+int vc_concretize(const float *A, const float *acc, const float *xl,
+                  const float *xh, int64_t M, int R, int n_in, int a_bcast,
+                  float *lb, vc_stream_t stream);
+
+/* CROWN intermediate-bound intersection for one seeded chunk:
+ *   lo[b, idx[t]] = max(lo, sl[b, t]); hi = max(min(hi, -sl[b, k+t]), lo')
+ * sl (B, 2k) from a backward seeded with [+I_k; -I_k]; lo/hi (B, n) in place.
+ * Replaces verify_zono_bnb.py:4140-4145. */
+int vc_crown_intersect(const float *sl, const int32_t *idx, int k, int64_t B,
+                       int n, float *lo, float *hi, vc_stream_t stream);
+
+/* Union over domains of unstable neurons: flag[j] = any_b lo<0<hi.
+ * Replaces verify_zono_bnb.py:4123. */
+int vc_unstable_union(const float *lo, const float *hi, int64_t B, int n,
+                      uint8_t *flag, vc_stream_t stream);
+
+/* ---- alpha-CROWN ----------------------------------------------------- */
+
+/* alpha initialisation alpha = (up_s > 0.5) * unstable over n neurons.
+ * Replaces verify_zono_bnb.py:5169-5173. */
+int vc_alpha_init(const float *lo, const float *hi, int64_t n, float *alpha,
+                  vc_stream_t stream);
+
+/* Gradient sweep step through one relu of the alpha backward, fused with
+ * the next fc's transposed product (forward direction):
+ *   gP (M, n) = gE * (mpos * ls + mneg * up_s) + mneg * up_t, where P is
+ *   the stored pre-relaxation rows ((M, n), or (R, n) shared by all domains
+ *   when p_bcast != 0), mpos = P >= 0, mneg = P <= 0 (torch's clamp
+ *   subgradient at 0), ls = active + unstable * alpha (alpha (B, n) or NULL
+ *   for the adaptive slope);  g_out (M, n_next) = gP W_next^T + bias_next,
+ *   W_next (n_next, n), bias_next nullable.
+ * With vc_alpha_grad_reduce and vc_alpha_grad_input this is the autograd
+ * of _spec_backward_graph_batched w.r.t. alpha (verify_zono_bnb.py:5261). */
+int vc_alpha_grad_step(const float *gE, const float *P, int64_t M, int R, int n,
+                       const float *relu_lo, const float *relu_hi,
+                       const float *alpha, int p_bcast, const float *W_next,
+                       const float *bias_next, int n_next, float *g_out,
+                       vc_stream_t stream);
+
+/* d lb / d alpha for one layer: galpha[b, j] = sum over the R rows of b of
+ * gE[m, j] * pos(P[m, j]), zero where the neuron is not unstable;
+ * gbeta[b, j] (nullable) = sum over rows of gE[m, j] (d lb / d beta).
+ * P as in vc_alpha_grad_step. */
+int vc_alpha_grad_reduce(const float *gE, const float *P, int p_bcast,
+                         int64_t B, int R, int n, const float *relu_lo,
+                         const float *relu_hi, float *galpha, float *gbeta,
+                         vc_stream_t stream);
+
+/* Input-side gradient of the concretization and the first fc:
+ * g (M, n_in) = xl * (A >= 0) + xh * (A <= 0) (torch's clamp subgradient),
+ * g_out (M, n1) = g W0^T + bias0 with W0 (n1, n_in), bias0 (n1) nullable. */
+int vc_alpha_grad_input(const float *A, const float *xl, const float *xh,
+                        int64_t M, int R, int n_in, const float *W0,
+                        const float *bias0, int n1, float *g_out,
+                        vc_stream_t stream);
+
+/* Adam step on n parameters with torch.optim.Adam's update order
+ * (betas b1, b2, eps; step is the 1-based step count), minimising
+ * -lb: grad = -sign_grad, followed by the projection clamp to
+ * [lo_clamp, hi_clamp].  step_size = lr / (1 - b1^step) and
+ * bc2_sqrt = sqrt(1 - b2^step) are passed in as host-computed doubles. */
+int vc_adam_step(float *param, const float *lb_grad, float *exp_avg,
+                 float *exp_avg_sq, int64_t n, float b1, float b2, float eps,
+                 double step_size, double bc2_sqrt, float lo_clamp,
+                 float hi_clamp, vc_stream_t stream);
+
+/* best = max(best, lb) elementwise (first call: copy when init != 0), and
+ * out[0] = max over best, out[1] = 1.0 if all best > 0 else 0.0.
+ * Replaces verify_zono_bnb.py:5252-5259. */
+int vc_best_update(float *best, const float *lb, int64_t n, int init,
+                   float *out2, vc_stream_t stream);
+
+/* ---- Input-split BaB step ---------------------------------------------- */
+
+/* Closure: closed[b] = AND over disjuncts d of (OR over q in d of
+ * lb[b, q] > 0); disjunct d owns q_idx[d_ptr[d] .. d_ptr[d+1]).
+ * Replaces verify_graph.py:12899-12908. */
+int vc_closure(const float *lb, int64_t B, int Q, const int32_t *d_ptr,
+               const int32_t *q_idx, int n_disj, uint8_t *closed,
+               vc_stream_t stream);
+
+/* Halfspace box clip of {x in [xl, xh] : A_q x + b_q <= 0 for q in D} per
+ * disjunct D, and the bounding box of the union over feasible disjuncts
+ * (single disjunct: plain clip).  A (B, Q, n), b (B, Q).
+ * Replaces _clip_box_by_halfspaces_batched (verify_graph.py:12363-12426)
+ * and the multi-disjunct union (verify_graph.py:13040-13074). */
+int vc_clip_box(const float *xl, const float *xh, const float *A,
+                const float *b, int64_t B, int Q, int n, const int32_t *d_ptr,
+                const int32_t *q_idx, int n_disj, float *xl_out,
+                float *xh_out, uint8_t *feasible, vc_stream_t stream);
+
+/* Ascending stream compaction: idx_out[0..count) = positions of non-zero
+ * flags (of zero flags when select_zero != 0); count_out[0] = count.
+ * workspace >= vc_compact_workspace(n) bytes.
+ * Replaces torch.nonzero on the closure / feasibility / usable masks
+ * (verify_graph.py:12986, 13115, 13372). */
+int64_t vc_compact_workspace(int64_t n);
+int vc_compact(const uint8_t *flags, int64_t n, int select_zero,
+               int64_t *idx_out, int64_t *count_out, void *workspace,
+               int64_t ws_bytes, vc_stream_t stream);
+
+/* Max-merge of row blocks: rows[idx[r], :] = max(rows[idx[r], :], src[r, :])
+ * over rows of q floats.  Replaces the alpha-CROWN merge
+ * spec_lbs_b[close_idx] = max(old, new) (verify_graph.py:12966-12967). */
+int vc_scatter_max_rows(float *rows, const int64_t *idx, const float *src,
+                        int64_t n_rows, int q, vc_stream_t stream);
+
+/* Row gather: out[r] = in[idx[r]] for rows of `cols` floats. */
+int vc_gather_rows(const float *in, const int64_t *idx, int64_t n_rows,
+                   int cols, float *out, vc_stream_t stream);
+
+/* Widest-dimension selection: ax[b] = first argmax_i (xh - xl)[b, i];
+ * usable[b] = (xh - xl)[b, ax] > 1e-12.
+ * Replaces verify_graph.py:13291 and 13366-13369. */
+int vc_widest_axis(const float *xl, const float *xh, int64_t B, int n,
+                   int64_t *ax, uint8_t *usable, vc_stream_t stream);
+
+/* Bisection of the usable leaves listed in u_idx (n_u entries): children
+ * low = (xl, xh with ax = mid) and high = (xl with ax = mid, xh),
+ * mid = (lo + hi) * 0.5.  Outputs are (n_u, n) each.
+ * Replaces verify_graph.py:13370-13382. */
+int vc_bisect(const float *xl, const float *xh, const int64_t *ax,
+              const int64_t *u_idx, int64_t n_u, int n, float *low_xl,
+              float *low_xh, float *high_xl, float *high_xh,
+              vc_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VIBECHECK_AMD_H */

@@ -1,0 +1,56 @@
+"""The C-ABI library loads on the CPU host and exports every entry point
+declared in include/*.h; the ctypes table matches the declarations."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from vibecheck_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    names = {}
+    for h in glob.glob(os.path.join(ROOT, 'include', '*.h')):
+        text = open(h).read()
+        text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+        for m in re.finditer(r'\b(int|int64_t)\s+(vc_\w+)\s*\(([^)]*)\)\s*;', text):
+            args = [a for a in m.group(3).split(',') if a.strip() and a.strip() != 'void']
+            names[m.group(2)] = len(args)
+    return names
+
+
+def test_header_declares_entry_points():
+    assert len(_declared()) >= 30
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail('libvibecheck_amd.so is not built (run __graft_entry__.build())')
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_ctypes_table_matches_header():
+    decl = _declared()
+    assert set(decl) == set(_lib.SIGNATURES), set(decl) ^ set(_lib.SIGNATURES)
+    for name, nargs in decl.items():
+        assert len(_lib.SIGNATURES[name]) == nargs, name
+
+
+def test_abi_version_callable_without_gpu():
+    lib = _lib.load()
+    assert lib.vc_abi_version() == 1
+
+
+def test_argument_errors_map_to_exceptions():
+    # null pointers are rejected before any launch: no GPU needed
+    with pytest.raises(ValueError):
+        _lib.call('vc_make_slopes', None, None, 4, None, None, None, None,
+                  None, None, None)
+    lib = _lib.load()
+    assert lib.vc_compact_workspace(1 << 20) >= 8

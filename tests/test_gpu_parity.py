@@ -1,0 +1,299 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle on the
+same seeded inputs.  Bounds: |gpu - ref| <= 1e-6 + 1e-5 |ref| (fp32);
+masks, indices, counts and verdicts: exact."""
+import pytest
+import torch
+
+from oracle import ref_bab as rbab
+from oracle import ref_bound as rb
+from vibecheck_amd import verify_graph as vg
+from vibecheck_amd import verify_zono_bnb as vz
+from vibecheck_amd import workloads as wk
+from vibecheck_amd._lib import call, ptr
+
+import _util
+
+pytestmark = pytest.mark.gpu
+F32 = torch.float32
+RTOL, ATOL = 1e-5, 1e-6
+
+
+def assert_bounds(gpu_t, ref_t, what, rtol=RTOL, atol=ATOL):
+    ok = _util.rel_err_ok(gpu_t, ref_t, rtol, atol)
+    if not bool(ok.all()):
+        g = gpu_t.detach().double().cpu()
+        r = ref_t.detach().double().cpu()
+        err = (g - r).abs()
+        i = int(err.reshape(-1).argmax())
+        raise AssertionError(
+            f'{what}: {int((~ok).sum())}/{ok.numel()} outside tolerance; '
+            f'worst |d|={float(err.reshape(-1)[i]):.3e} at flat {i}: '
+            f'gpu={float(g.reshape(-1)[i]):.8e} ref={float(r.reshape(-1)[i]):.8e}')
+
+
+def cpu(t):
+    return t.detach().cpu()
+
+
+def acas(gpu, B, seed=1, scale=1.0):
+    gg_c = wk.acas_gg(dtype=F32)
+    gg_g = wk.acas_gg(device=gpu, dtype=F32)
+    xl, xh = wk.acas_boxes(B, seed=seed, dtype=F32)
+    if scale != 1.0:
+        c, r = (xl + xh) / 2, (xh - xl) / 2
+        xl, xh = c - r * scale, c + r * scale
+    return gg_c, gg_g, xl, xh
+
+
+def spec_pair(n_out, gpu, one_disjunct=True):
+    se_c, dq = _util.spec_for(n_out, one_disjunct, dtype=F32)
+    se_g = {k: (w.to(gpu), b) for k, (w, b) in se_c.items()}
+    return se_c, se_g, dq
+
+
+# ----------------------------------------------------------------- GEMM core
+def test_gemm_mfma_layout_against_fp64(gpu):
+    g = torch.Generator().manual_seed(0)
+    for (M, R, n_out, n_in) in [(200, 4, 70, 90), (64, 8, 50, 50), (130, 2, 5, 50),
+                                (33, 1, 1024, 17)]:
+        ew = torch.randn(M, n_out, generator=g)
+        W = torch.randn(n_out, n_in, generator=g)
+        b = torch.randn(n_out, generator=g)
+        acc = torch.randn(M, generator=g)
+        ref_out = (ew.double() @ W.double()).float()
+        ref_acc = (acc.double() + ew.double() @ b.double()).float()
+        ew_g, W_g, b_g, acc_g = ew.to(gpu), W.to(gpu), b.to(gpu), acc.to(gpu)
+        out = torch.empty(M, n_in, device=gpu)
+        call('vc_backward_fc', ptr(ew_g), M, R, n_out, None, None, None, 0, None,
+             ptr(W_g), ptr(b_g), n_in, ptr(out), ptr(acc_g), None, 0,
+             torch.cuda.current_stream().cuda_stream)
+        scale = (ew.abs().double() @ W.abs().double()).float()
+        assert bool(((cpu(out) - ref_out).abs() <= 1e-5 * scale + 1e-6).all()), (M, n_out, n_in)
+        assert bool(((cpu(acc_g) - ref_acc).abs() <= 1e-5 * (acc.abs() + ew.abs() @ b.abs()) + 1e-6).all())
+
+
+# ----------------------------------------------------------------- a1
+def test_make_slopes_bit_exact(gpu):
+    g = torch.Generator().manual_seed(1)
+    lo = torch.randn(100000, generator=g) * 3
+    hi = lo + torch.rand(100000, generator=g) * 4
+    lo = torch.cat([lo, torch.tensor([0.0, -5e-9, -1e-8, 0.0, -1.0, -2.0, -0.0])])
+    hi = torch.cat([hi, torch.tensor([0.0, -1e-9, 0.0, 1e-30, 1.0, 2.0, 0.0])])
+    ref = rb.make_slopes(lo, hi)
+    got = vz._make_slopes(lo.to(gpu), hi.to(gpu))
+    for r, t, nm in zip(ref, got, ['lo_s', 'up_s', 'up_t', 'active', 'dead', 'unstable']):
+        assert torch.equal(cpu(t), r), nm
+
+
+# ----------------------------------------------------------------- a2
+def test_ibp_parity_mlp_and_clamps(gpu):
+    gg_c = wk.deep_mlp_gg(dtype=F32)
+    gg_g = wk.deep_mlp_gg(device=gpu, dtype=F32)
+    xl, xh = wk.linf_boxes(64, 784, 0.03, seed=1, dtype=F32)
+    sb_root = rb.ibp_forward_batched(xl[:1], xh[:1], gg_c)
+    unst = [(L, int(j)) for L, (lo, hi) in sb_root.items()
+            for j in ((lo[0] < 0) & (hi[0] > 0)).nonzero().flatten().tolist()]
+    lay, neu, side = wk.relu_split_domains(unst, n_domains=64, n_splits=8, seed=2)
+    clamps = wk.relu_clamps_from_splits(lay, neu, side, [256] * 6, dtype=F32)
+    root = {L: (lo[0], hi[0]) for L, (lo, hi) in sb_root.items()}
+    ref = rb.ibp_forward_batched(xl, xh, gg_c, relu_clamps=clamps, root_sb=root)
+    got = vz._ibp_forward_graph_batched(
+        xl.to(gpu), xh.to(gpu), gg_g, gpu, F32,
+        relu_clamps={L: (a.to(gpu), b.to(gpu)) for L, (a, b) in clamps.items()},
+        root_sb={L: (a.to(gpu), b.to(gpu)) for L, (a, b) in root.items()})
+    for L in ref:
+        assert_bounds(got[L][0], ref[L][0], f'ibp lo L{L}')
+        assert_bounds(got[L][1], ref[L][1], f'ibp hi L{L}')
+
+
+def test_ibp_parity_cnn(gpu):
+    gg_c = wk.cifar_cnn_gg(dtype=F32)
+    gg_g = wk.cifar_cnn_gg(device=gpu, dtype=F32)
+    xl, xh = wk.cifar_cnn_boxes(4, dtype=F32)
+    ref = rb.ibp_forward_batched(xl, xh, gg_c)
+    got = vz._ibp_forward_graph_batched(xl.to(gpu), xh.to(gpu), gg_g, gpu, F32)
+    for L in ref:
+        assert_bounds(got[L][0], ref[L][0], f'cnn ibp lo L{L}')
+        assert_bounds(got[L][1], ref[L][1], f'cnn ibp hi L{L}')
+
+
+# ----------------------------------------------------------------- a3
+def test_zono_parity_acas(gpu):
+    gg_c, gg_g, xl, xh = acas(gpu, 512, scale=3.0)
+    ref, (rc, rG) = rb.zono_forward_batched(xl, xh, gg_c)
+    got, (gc, gG) = vz._forward_zonotope_graph_batched(xl.to(gpu), xh.to(gpu), gg_g, gpu, F32)
+    for L in ref:
+        assert_bounds(got[L][0], ref[L][0], f'zono lo L{L}')
+        assert_bounds(got[L][1], ref[L][1], f'zono hi L{L}')
+    assert gG.shape == rG.shape
+    assert_bounds(gc, rc, 'zono centre')
+    assert_bounds(gG.abs().sum(-1), rG.abs().sum(-1), 'zono radius')
+
+
+# ----------------------------------------------------------------- a5-a8
+def test_spec_backward_parity_same_bounds(gpu):
+    gg_c, gg_g, xl, xh = acas(gpu, 1024, scale=3.0)
+    se_c, se_g, _ = spec_pair(5, gpu)
+    tight = rb.crown_intermediate_batched(gg_c, xl, xh)
+    tight_g = {L: (a.to(gpu), b.to(gpu)) for L, (a, b) in tight.items()}
+    lb, A, acc = rb.spec_backward_batched(tight, xl, xh, gg_c, se_c, return_input_linear=True)
+    glb, gA, gacc = vz._spec_backward_graph_batched(tight_g, xl.to(gpu), xh.to(gpu), gg_g,
+                                                    se_g, gpu, F32, return_input_linear=True)
+    assert_bounds(glb, lb, 'spec lb')
+    assert_bounds(gacc, acc, 'spec acc')
+    assert_bounds(gA, A, 'spec A')
+    # with alpha and beta
+    g = torch.Generator().manual_seed(5)
+    alpha = {L: torch.rand(lo.shape, generator=g) for L, (lo, hi) in tight.items()}
+    beta = {L: torch.randn(lo.shape, generator=g) * 0.1 for L, (lo, hi) in tight.items()}
+    lb2 = rb.spec_backward_batched(tight, xl, xh, gg_c, se_c, alpha_at_layer=alpha,
+                                   relu_split_beta=beta)
+    glb2 = vz._spec_backward_graph_batched(
+        tight_g, xl.to(gpu), xh.to(gpu), gg_g, se_g, gpu, F32,
+        alpha_at_layer={L: a.to(gpu) for L, a in alpha.items()},
+        relu_split_beta={L: b.to(gpu) for L, b in beta.items()})
+    assert_bounds(glb2, lb2, 'spec lb alpha/beta')
+
+
+def test_spec_backward_parity_cnn(gpu):
+    gg_c = _util.tiny_cnn(seed=4, dtype=F32)
+    gg_g = _util.to_dev(gg_c, gpu)
+    for op_c, op_g in zip(gg_c['ops'], gg_g['ops']):
+        if op_c['type'] == 'conv':
+            op_c['bias'] = torch.linspace(-0.2, 0.3, op_c['bias'].numel())
+            op_g['bias'] = op_c['bias'].to(gpu)
+    g = torch.Generator().manual_seed(3)
+    c = torch.rand(8, gg_c['input_n'], generator=g) * 2 - 1
+    xl, xh = c - 0.2, c + 0.2
+    se_c, se_g, _ = spec_pair(2, gpu)
+    sb = rb.ibp_forward_batched(xl, xh, gg_c)
+    sbg = {L: (a.to(gpu), b.to(gpu)) for L, (a, b) in sb.items()}
+    lb, A, acc = rb.spec_backward_batched(sb, xl, xh, gg_c, se_c, return_input_linear=True)
+    glb, gA, gacc = vz._spec_backward_graph_batched(sbg, xl.to(gpu), xh.to(gpu), gg_g, se_g,
+                                                    gpu, F32, return_input_linear=True)
+    assert_bounds(glb, lb, 'cnn spec lb')
+    assert_bounds(gA, A, 'cnn spec A')
+
+
+# ----------------------------------------------------------------- a4
+def test_crown_intermediate_parity_acas(gpu):
+    gg_c, gg_g, xl, xh = acas(gpu, 512, scale=2.0)
+    sb, _ = rb.zono_forward_batched(xl, xh, gg_c)
+    ref = rb.crown_intermediate_batched(gg_c, xl, xh, sb=sb)
+    sbg = {L: (a.to(gpu), b.to(gpu)) for L, (a, b) in sb.items()}
+    got = vz._crown_intermediate_batched(gg_g, xl.to(gpu), xh.to(gpu), gpu, F32, sb=sbg)
+    for L in ref:
+        assert_bounds(got[L][0], ref[L][0], f'crown-int lo L{L}')
+        assert_bounds(got[L][1], ref[L][1], f'crown-int hi L{L}')
+
+
+def test_crown_intermediate_parity_mlp_chunked(gpu):
+    gg_c = wk.deep_mlp_gg(dtype=F32)
+    gg_g = wk.deep_mlp_gg(device=gpu, dtype=F32)
+    xl, xh = wk.linf_boxes(3, 784, 0.01, seed=4, dtype=F32)
+    sb = rb.ibp_forward_batched(xl, xh, gg_c)
+    ref = rb.crown_intermediate_batched(gg_c, xl, xh, chunk=64, sb=sb)
+    sbg = {L: (a.to(gpu), b.to(gpu)) for L, (a, b) in sb.items()}
+    got = vz._crown_intermediate_batched(gg_g, xl.to(gpu), xh.to(gpu), gpu, F32,
+                                         chunk=64, sb=sbg)
+    for L in ref:
+        assert_bounds(got[L][0], ref[L][0], f'mlp crown-int lo L{L}')
+        assert_bounds(got[L][1], ref[L][1], f'mlp crown-int hi L{L}')
+
+
+# ----------------------------------------------------------------- a9
+def test_alpha_gradient_matches_autograd(gpu):
+    gg_c, gg_g, xl, xh = acas(gpu, 64, scale=4.0)
+    se_c, se_g, _ = spec_pair(5, gpu)
+    sb, _ = rb.zono_forward_batched(xl, xh, gg_c)
+    g = torch.Generator().manual_seed(7)
+    alpha = {L: torch.rand(lo.shape, generator=g, dtype=torch.float64)
+             for L, (lo, hi) in sb.items()}
+    a_ref = {L: a.clone().requires_grad_(True) for L, a in alpha.items()}
+    sb64 = {L: (lo.double(), hi.double()) for L, (lo, hi) in sb.items()}
+    gg64 = _util.to_dev(gg_c, 'cpu', torch.float64)
+    lb = rb.spec_backward_batched(sb64, xl.double(), xh.double(), gg64,
+                                  {k: (w.double(), b) for k, (w, b) in se_c.items()},
+                                  alpha_at_layer=a_ref)
+    lb.sum().backward()
+    sbg = {L: (a.to(gpu), b.to(gpu)) for L, (a, b) in sb.items()}
+    Wq, bq = vz._spec_rows(se_g, gpu)
+    a_g = {L: a.float().to(gpu) for L, a in alpha.items()}
+    ga = {L: torch.zeros_like(a) for L, a in a_g.items()}
+    glb = vz._alpha_backward_and_grad(sbg, xl.to(gpu), xh.to(gpu), gg_g, Wq, bq, a_g, True, ga)
+    assert_bounds(glb, lb.detach().float(), 'alpha lb', rtol=1e-4, atol=1e-5)
+    for L in alpha:
+        ref_g = a_ref[L].grad.float()
+        scale = ref_g.abs().max().clamp(min=1.0)
+        err = (cpu(ga[L]) - ref_g).abs().max() / scale
+        assert float(err) < 1e-4, (L, float(err))
+
+
+def test_alpha_crown_parity_acas(gpu):
+    gg_c, gg_g, xl, xh = acas(gpu, 128, scale=4.0)
+    se_c, se_g, _ = spec_pair(5, gpu)
+    ref, n_ref = rb.alpha_crown_batched(xl, xh, gg_c, se_c, n_iters=20, lr=0.1,
+                                        return_trace=True)
+    got, n_got = vz._run_alpha_crown_inputsplit_batched(
+        xl.to(gpu), xh.to(gpu), gg_g, se_g, gpu, F32, n_iters=20, lr=0.1, return_trace=True)
+    assert n_got == n_ref
+    assert_bounds(got, ref, 'alpha best lb', rtol=1e-4, atol=1e-5)
+
+
+# ----------------------------------------------------------------- a11-a14
+def test_clip_parity_identical_inputs(gpu):
+    g = torch.Generator().manual_seed(3)
+    B, Q, n = 4096, 4, 5
+    xl = torch.rand(B, n, generator=g) - 1
+    xh = xl + torch.rand(B, n, generator=g) + 0.01
+    A = torch.randn(B, Q, n, generator=g)
+    b = torch.randn(B, Q, generator=g) - 1.0
+    rl, rh, rf = rbab.clip_box_by_halfspaces_batched(xl, xh, A, b)
+    gl, gh, gf = vg._clip_box_by_halfspaces_batched(xl.to(gpu), xh.to(gpu), A.to(gpu), b.to(gpu))
+    assert torch.equal(cpu(gf), rf)
+    assert_bounds(gl, rl, 'clip xl')
+    assert_bounds(gh, rh, 'clip xh')
+    dq = {0: [0, 2], 1: [1], 2: [3]}
+    rl, rh, rf = rbab.clip_leaves(xl, xh, A, b, dq)
+    tab = vg.DisjunctTable(dq, gpu)
+    gl, gh, gf = vg._clip(xl.to(gpu), xh.to(gpu), A.to(gpu), b.to(gpu), tab)
+    assert torch.equal(cpu(gf), rf)
+    assert_bounds(gl, rl, 'clip union xl')
+    assert_bounds(gh, rh, 'clip union xh')
+
+
+def test_split_and_compaction_bit_exact(gpu):
+    g = torch.Generator().manual_seed(8)
+    B, n = 100003, 5
+    xl = torch.rand(B, n, generator=g)
+    w = torch.randint(0, 4, (B, n), generator=g).float() * 0.25   # many ties
+    xh = xl + w
+    ax_ref = rbab.widest_axis(xl, xh)
+    n_deg, low, high = rbab.bisect(xl, xh, ax_ref)
+    ngd, ax, glow, ghigh = vg._widest_and_bisect(xl.to(gpu), xh.to(gpu))
+    assert torch.equal(cpu(ax), ax_ref)
+    assert ngd == n_deg
+    for a, b in zip(glow + ghigh, low + high):
+        assert torch.equal(cpu(a), b)
+    flags = torch.rand(B, generator=g) < 0.3
+    assert torch.equal(cpu(vg._compact(flags.to(gpu))), flags.nonzero(as_tuple=True)[0])
+    assert torch.equal(cpu(vg._compact(flags.to(gpu), select_zero=True)),
+                       (~flags).nonzero(as_tuple=True)[0])
+    lb = torch.randn(B, 4, generator=g)
+    tab = vg.DisjunctTable({0: [0, 1, 2, 3]}, gpu)
+    assert torch.equal(cpu(vg._closure(lb.to(gpu), tab)), rbab.closure(lb, {0: [0, 1, 2, 3]}))
+
+
+def test_bab_step_parity_c0(gpu):
+    """Config-0 shape: 4096 ACAS boxes, CROWN intermediate, clip, split."""
+    gg_c, gg_g, xl, xh = acas(gpu, 4096)
+    se_c, se_g, dq = spec_pair(5, gpu)
+    ref = rbab.bab_step(xl, xh, gg_c, se_c, dq)
+    got = vg.bab_step(xl.to(gpu), xh.to(gpu), gg_g, se_g, vg.DisjunctTable(dq, gpu))
+    assert_bounds(got['lb'], ref['lb'], 'C0 lb')
+    assert torch.equal(cpu(got['closed']), ref['closed'])
+    assert torch.equal(cpu(got['unclosed']), ref['unclosed'])
+    assert torch.equal(cpu(got['feasible']), ref['feasible'])
+    assert torch.equal(cpu(got['ax']), ref['ax'])
+    for a, b in zip(got['low'] + got['high'], ref['low'] + ref['high']):
+        assert_bounds(a, b, 'C0 children')

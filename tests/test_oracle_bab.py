@@ -1,0 +1,179 @@
+"""Pins the CPU oracle's BaB-step logic (oracle/ref_bab.py): closure,
+halfspace clipping, widest-axis choice, bisection, compaction order, LIFO
+chunk worklist, query dedup.  Hand-computed cases and brute force."""
+import numpy as np
+import torch
+
+from oracle import ref_bab as rbab
+from oracle import ref_bound as rb
+from vibecheck_amd import workloads as wk
+from vibecheck_amd.spec import (Conjunct, Constraint, PairwiseConstraint,
+                                VNNSpec, dedup_queries)
+
+import _util
+
+DT = torch.float64
+
+
+def _t(v, dt=DT):
+    return torch.tensor(v, dtype=dt)
+
+
+def test_closure_any_within_all_across():
+    lb = _t([[1.0, -1.0, -1.0], [-1.0, 2.0, 2.0], [-1.0, -1.0, -1.0],
+             [0.0, 3.0, 0.0]])
+    one = {0: [0, 1, 2]}
+    assert rbab.closure(lb, one).tolist() == [True, True, False, True]
+    each = {0: [0], 1: [1], 2: [2]}
+    assert rbab.closure(lb, each).tolist() == [False, False, False, False]
+    two = {0: [0, 1], 1: [2]}
+    assert rbab.closure(lb, two).tolist() == [False, True, False, False]
+    lb2 = _t([[0.5, 0.1, 0.2]])
+    assert rbab.closure(lb2, each).tolist() == [True]
+
+
+def test_clip_hand_computed():
+    # x0 + 0.5 <= 0 on [0,1]^2 is empty (min 0.5 > 0); x0 - 0.5 <= 0 gives x0 <= 0.5
+    xl, xh = _t([[0.0, 0.0]]), _t([[1.0, 1.0]])
+    A = _t([[[1.0, 0.0]]])
+    l, h, f = rbab.clip_box_by_halfspaces_batched(xl, xh, A, _t([[0.5]]))
+    assert not bool(f[0])
+    l, h, f = rbab.clip_box_by_halfspaces_batched(xl, xh, A, _t([[-0.5]]))
+    assert bool(f[0])
+    torch.testing.assert_close(h, _t([[0.5, 1.0]]))
+    torch.testing.assert_close(l, _t([[0.0, 0.0]]))
+    # -x0 - x1 + 1.5 <= 0 -> x0 >= 0.5 and x1 >= 0.5
+    l, h, f = rbab.clip_box_by_halfspaces_batched(xl, xh, _t([[[-1.0, -1.0]]]),
+                                                  _t([[1.5]]))
+    torch.testing.assert_close(l, _t([[0.5, 0.5]]))
+
+
+def test_clip_brute_force_contains_feasible_points():
+    g = torch.Generator().manual_seed(3)
+    B, Q, n = 64, 3, 3
+    xl = torch.rand(B, n, generator=g, dtype=DT) - 1
+    xh = xl + torch.rand(B, n, generator=g, dtype=DT) + 0.1
+    A = torch.randn(B, Q, n, generator=g, dtype=DT)
+    b = torch.randn(B, Q, generator=g, dtype=DT)
+    l, h, f = rbab.clip_box_by_halfspaces_batched(xl, xh, A, b)
+    pts = _util.sample_box(xl, xh, 4000, seed=2)
+    val = torch.einsum('bqn,bpn->bpq', A, pts) + b.unsqueeze(1)
+    ok = (val <= 0).all(-1)                                    # (B, P)
+    for i in range(B):
+        inside = pts[i][ok[i]]
+        if inside.numel():
+            assert bool(f[i])
+            assert bool((inside >= l[i] - 1e-12).all() and (inside <= h[i] + 1e-12).all())
+    assert bool((l >= xl).all() and (h <= xh).all())
+
+
+def test_clip_multi_disjunct_union():
+    xl, xh = _t([[0.0, 0.0]]), _t([[1.0, 1.0]])
+    A = _t([[[1.0, 0.0], [-1.0, 0.0]]])
+    b = _t([[-0.25, 0.75]])          # d0: x0 <= 0.25 ; d1: x0 >= 0.75
+    l, h, f = rbab.clip_leaves(xl, xh, A, b, {0: [0], 1: [1]})
+    assert bool(f[0])
+    torch.testing.assert_close(l, _t([[0.0, 0.0]]))
+    torch.testing.assert_close(h, _t([[1.0, 1.0]]))
+    b2 = _t([[0.5, 0.75]])           # d0 empty -> union is d1's box
+    l, h, f = rbab.clip_leaves(xl, xh, A, b2, {0: [0], 1: [1]})
+    torch.testing.assert_close(l, _t([[0.75, 0.0]]))
+    torch.testing.assert_close(h, _t([[1.0, 1.0]]))
+    b3 = _t([[0.5, 1.5]])            # both empty -> infeasible, box kept
+    l, h, f = rbab.clip_leaves(xl, xh, A, b3, {0: [0], 1: [1]})
+    assert not bool(f[0])
+    torch.testing.assert_close(l, xl)
+
+
+def test_widest_axis_first_max():
+    xl = _t([[0.0, 0.0, 0.0], [0.0, 0.0, 0.0]])
+    xh = _t([[1.0, 2.0, 2.0], [3.0, 1.0, 3.0]])
+    assert rbab.widest_axis(xl, xh).tolist() == [1, 0]
+
+
+def test_bisect_children_partition_parent():
+    g = torch.Generator().manual_seed(0)
+    xl = torch.rand(20, 4, generator=g)
+    xh = xl + torch.rand(20, 4, generator=g)
+    xh[3] = xl[3]                                    # degenerate leaf
+    ax = rbab.widest_axis(xl, xh)
+    n_deg, (lxl, lxh), (hxl, hxh) = rbab.bisect(xl, xh, ax)
+    assert n_deg == 1
+    keep = [i for i in range(20) if i != 3]
+    for r, i in enumerate(keep):
+        a = int(ax[i])
+        mid = (xl[i, a] + xh[i, a]) * 0.5
+        assert torch.equal(lxl[r], xl[i]) and torch.equal(hxh[r], xh[i])
+        assert float(lxh[r, a]) == float(mid) == float(hxl[r, a])
+        others = [k for k in range(4) if k != a]
+        assert torch.equal(lxh[r, others], xh[i, others])
+        assert torch.equal(hxl[r, others], xl[i, others])
+
+
+def test_worklist_lifo_chunks():
+    wl = rbab.ChunkWorklist(_t([0.0]), _t([1.0]))
+    wl.pop(1)
+    a = torch.arange(6, dtype=DT).reshape(3, 2)
+    b = torch.arange(6, 10, dtype=DT).reshape(2, 2)
+    wl.push(a, a)
+    wl.push(b, b)
+    xl, _ = wl.pop(3)                   # all of b (last pushed) then last row of a
+    assert xl.tolist() == [[6, 7], [8, 9], [4, 5]]
+    assert wl.size() == 2
+    xl, _ = wl.pop(2)
+    assert xl.tolist() == [[0, 1], [2, 3]]
+    assert not wl
+
+
+def test_compaction_ascending():
+    closed = torch.tensor([True, False, False, True, False])
+    assert (~closed).nonzero(as_tuple=True)[0].tolist() == [1, 2, 4]
+
+
+def test_spec_queries_and_dedup():
+    spec = VNNSpec([0.0], [1.0], [
+        Conjunct([PairwiseConstraint(0, 1), Constraint(2, '>=', 0.5)]),
+        Conjunct([PairwiseConstraint(0, 1), Constraint(1, '<=', -2.0)])])
+    q = spec.as_linear_queries(3)
+    assert [d for d, _, _ in q] == [0, 0, 1, 1]
+    np.testing.assert_array_equal(q[0][1], [1.0, -1.0, 0.0])
+    np.testing.assert_array_equal(q[1][1], [0.0, 0.0, -1.0])
+    assert q[1][2] == 0.5
+    np.testing.assert_array_equal(q[3][1], [0.0, 1.0, 0.0])
+    assert q[3][2] == 2.0
+    uq, dq = dedup_queries(q)
+    assert len(uq) == 3 and dq == {0: [0, 1], 1: [0, 2]}
+
+
+def test_bab_step_sound_split_of_unclosed_only():
+    """One C0-shaped step: closed leaves are never split; every child box
+    lies inside its parent; the children of a leaf partition it."""
+    gg = wk.acas_gg(dtype=DT)
+    xl, xh = wk.acas_boxes(64, seed=1, dtype=DT)
+    spec_ew, dq = _util.spec_for(5)
+    st = rbab.bab_step(xl, xh, gg, spec_ew, dq)
+    closed = st['closed']
+    pts = _util.sample_box(xl, xh, 300, seed=9)
+    Wq = torch.stack([spec_ew[q][0] for q in sorted(spec_ew)])
+    for b in range(64):
+        y, _ = rb.point_forward(pts[b], gg)
+        if bool(closed[b]):            # verified: every sample is safe
+            assert bool(((y @ Wq.T) > 0).any(1).all())
+    n_u = st['unclosed'].numel()
+    assert n_u == int((~closed).sum())
+    (lxl, lxh), (hxl, hxh) = st['low'], st['high']
+    assert lxl.shape[0] + st['n_degenerate'] <= n_u
+    assert bool((lxh >= lxl).all() and (hxh >= hxl).all())
+
+
+def test_input_split_driver_closes_small_problem():
+    gg = wk.acas_gg(dtype=torch.float32)
+    spec = wk.acas_spec([0.1, 0.1, 0.1, 0.1, 0.1], [0.14, 0.14, 0.14, 0.14, 0.14])
+    uq, dq = dedup_queries(spec.as_linear_queries(5))
+    spec_ew = {i: (torch.tensor(w, dtype=torch.float32), b) for i, (w, b) in enumerate(uq)}
+    xl0 = torch.tensor(spec.x_lo, dtype=torch.float32)
+    xh0 = torch.tensor(spec.x_hi, dtype=torch.float32)
+    verdict, det, trace = rbab.input_split_batched(xl0, xh0, gg, spec_ew, dq,
+                                                   max_iters=30)
+    assert verdict in ('verified', 'unknown')
+    assert det['batched_n_iters'] == len(trace) >= 1

@@ -1,0 +1,393 @@
+"""Pins the CPU oracle's bound primitives (oracle/ref_bound.py).
+
+Checks are closed forms, the reference's own known-answer tests
+(tests/test_bnb.py:159-199 and tests/test_ibp_crown.py of the reference),
+hand-computed small cases, and sampled ground truth: each is chosen so that
+a dropped term, a sign error or a transposed operand in the oracle fails.
+All CPU, float64 unless stated.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref_bound as rb
+from vibecheck_amd import workloads as wk
+
+import _util
+
+DT = torch.float64
+
+
+def _t(v):
+    return torch.tensor(v, dtype=DT)
+
+
+# ---------------------------------------------------------------- slopes
+class TestMakeSlopes:
+    """Known answers of the reference's TestMakeSlopes."""
+
+    def test_active(self):
+        lo_s, up_s, up_t, a, d, u = rb.make_slopes(_t([1.0, 2.0]), _t([3.0, 4.0]))
+        assert a.all() and not d.any() and not u.any()
+        assert torch.equal(lo_s, _t([1.0, 1.0]))
+
+    def test_dead(self):
+        lo_s, up_s, up_t, a, d, u = rb.make_slopes(_t([-3.0, -2.0]), _t([-1.0, -0.5]))
+        assert d.all() and not a.any()
+        assert torch.equal(lo_s, _t([0.0, 0.0]))
+
+    def test_unstable(self):
+        lo_s, up_s, up_t, a, d, u = rb.make_slopes(_t([-1.0]), _t([3.0]))
+        assert u.all()
+        torch.testing.assert_close(up_s, _t([0.75]))
+        torch.testing.assert_close(up_t, _t([0.75]))
+        torch.testing.assert_close(lo_s, _t([1.0]))
+
+    def test_mixed(self):
+        lo_s, up_s, up_t, a, d, u = rb.make_slopes(_t([1.0, -1.0, -3.0]),
+                                                   _t([2.0, 1.0, -1.0]))
+        assert a.tolist() == [True, False, False]
+        assert d.tolist() == [False, False, True]
+        assert u.tolist() == [False, True, False]
+
+    def test_upper_line_is_chord(self):
+        # the upper relaxation passes through (lo, 0) and (hi, hi)
+        g = torch.Generator().manual_seed(0)
+        lo = -torch.rand(1000, generator=g, dtype=DT) * 5 - 1e-3
+        hi = torch.rand(1000, generator=g, dtype=DT) * 5 + 1e-3
+        _, up_s, up_t, _, _, u = rb.make_slopes(lo, hi)
+        assert u.all()
+        torch.testing.assert_close(up_s * lo + up_t, torch.zeros_like(lo),
+                                   atol=1e-12, rtol=0)
+        torch.testing.assert_close(up_s * hi + up_t, hi)
+
+    def test_lower_slope_minimises_area(self):
+        # lo_s = 1 iff hi > -lo (the relaxation of smaller area)
+        lo_s, *_ = rb.make_slopes(_t([-1.0, -3.0, -2.0]), _t([3.0, 1.0, 2.0]))
+        assert lo_s.tolist() == [1.0, 0.0, 0.0]
+
+    def test_zero_interval_is_active_and_dead(self):
+        lo_s, up_s, up_t, a, d, u = rb.make_slopes(_t([0.0]), _t([0.0]))
+        assert bool(a[0]) and bool(d[0]) and not bool(u[0])
+        assert float(lo_s[0]) == 1.0
+
+    def test_tiny_negative_dead_edge(self):
+        # lb_r + 1e-8 > 0 gives a dead neuron a non-zero upper slope
+        lo_s, up_s, up_t, a, d, u = rb.make_slopes(_t([-5e-9]), _t([-1e-9]))
+        assert bool(d[0]) and float(lo_s[0]) == 0.0
+        assert float(up_s[0]) == pytest.approx(0.5, rel=1e-9)
+
+
+# ---------------------------------------------------------------- IBP
+def _box(n, B, eps, seed):
+    g = torch.Generator().manual_seed(seed)
+    c = torch.rand(B, n, generator=g, dtype=DT) * 2 - 1
+    return c - eps, c + eps
+
+
+@pytest.mark.parametrize('net', ['mlp', 'cnn'])
+def test_ibp_sound_and_first_layer_exact(net):
+    gg = _util.tiny_mlp([4, 8, 8, 3], seed=3) if net == 'mlp' else _util.tiny_cnn()
+    n = gg['input_n']
+    xl, xh = _box(n, 3, 0.3, 1)
+    sb = rb.ibp_forward_batched(xl, xh, gg)
+    pts = _util.sample_box(xl, xh, 200, seed=7)
+    for b in range(3):
+        _, pre = rb.point_forward(pts[b], gg)
+        for L, (lo, hi) in sb.items():
+            assert bool((pre[L] >= lo[b] - 1e-9).all())
+            assert bool((pre[L] <= hi[b] + 1e-9).all())
+    # exactness of the first affine layer: endpoint-wise interval sum
+    op = gg['ops'][0]
+    if op['type'] == 'fc':
+        W, bias = op['W'], op['bias']
+        lo_ex = (torch.minimum(W * xl[:, None, :], W * xh[:, None, :])).sum(-1) + bias
+        hi_ex = (torch.maximum(W * xl[:, None, :], W * xh[:, None, :])).sum(-1) + bias
+    else:
+        # dense matrix of the conv from the unit basis
+        basis = torch.eye(n, dtype=DT)
+        y0 = torch.nn.functional.conv2d(torch.zeros(1, *op['in_shape'], dtype=DT),
+                                        op['kernel'], op['bias'], stride=op['stride'],
+                                        padding=op['padding']).reshape(-1)
+        Wd = (torch.nn.functional.conv2d(basis.reshape(n, *op['in_shape']),
+                                         op['kernel'], op['bias'], stride=op['stride'],
+                                         padding=op['padding']).reshape(n, -1) - y0).T
+        lo_ex = torch.minimum(Wd * xl[:, None, :], Wd * xh[:, None, :]).sum(-1) + y0
+        hi_ex = torch.maximum(Wd * xl[:, None, :], Wd * xh[:, None, :]).sum(-1) + y0
+    torch.testing.assert_close(sb[0][0], lo_ex)
+    torch.testing.assert_close(sb[0][1], hi_ex)
+
+
+def test_ibp_clamps_root_and_repair():
+    gg = _util.tiny_mlp([4, 8, 8, 3], seed=3)
+    xl, xh = _box(4, 1, 0.5, 2)
+    sb = rb.ibp_forward_batched(xl, xh, gg)
+    B = 3
+    xlb, xhb = xl.expand(B, -1).clone(), xh.expand(B, -1).clone()
+    lo0, hi0 = sb[0][0][0], sb[0][1][0]
+    j = int(((lo0 < 0) & (hi0 > 0)).nonzero()[0])
+    n0 = lo0.numel()
+    cl = torch.full((B, n0), -np.inf, dtype=DT)
+    ch = torch.full((B, n0), np.inf, dtype=DT)
+    ch[1, j] = 0.0
+    root = {L: (lo[0], hi[0]) for L, (lo, hi) in sb.items()}
+    sbc = rb.ibp_forward_batched(xlb, xhb, gg, relu_clamps={0: (cl, ch)}, root_sb=root)
+    assert float(sbc[0][1][1, j]) == 0.0
+    torch.testing.assert_close(sbc[0][1][0], hi0)
+    assert bool((sbc[1][0][1] >= sb[1][0][0] - 1e-12).all())
+    assert bool((sbc[1][1][1] <= sb[1][1][0] + 1e-12).all())
+    jp = (lo0 > 0).nonzero()
+    if jp.numel():
+        ch2 = torch.full((B, n0), np.inf, dtype=DT)
+        ch2[2, int(jp[0])] = 0.0
+        sbe = rb.ibp_forward_batched(xlb, xhb, gg, relu_clamps={0: (cl, ch2)}, root_sb=root)
+        assert bool((sbe[0][1][2] >= sbe[0][0][2]).all())
+
+
+def test_ibp_unsupported_raises():
+    gg = _util.tiny_mlp([2, 2, 1], seed=0)
+    gg['ops'].insert(0, {'name': 's', 'type': 'sigmoid', 'inputs': ['X']})
+    with pytest.raises(NotImplementedError):
+        rb.ibp_forward_batched(torch.zeros(1, 2, dtype=DT), torch.ones(1, 2, dtype=DT), gg)
+
+
+# ---------------------------------------------------------------- zonotope
+def _chain(ws, bs):
+    return wk.mlp_gg([torch.tensor(w, dtype=DT) for w in ws],
+                     [torch.tensor(b, dtype=DT) for b in bs], dtype=DT)
+
+
+def test_zono_hand_computed():
+    # x in [-1, 1]; z0 = x -> relu: lam = 1/2, mu = 1/4 -> zonotope of the
+    # relu output: c = 1/4, G = [1/2, 1/4] -> z1 = y0 in [-1/2, 1].
+    gg = _chain([[[1.0]], [[1.0]], [[1.0]]], [[0.0], [0.0], [0.0]])
+    sb, (c, G) = rb.zono_forward_batched(_t([[-1.0]]), _t([[1.0]]), gg)
+    torch.testing.assert_close(sb[0][0], _t([[-1.0]]))
+    torch.testing.assert_close(sb[0][1], _t([[1.0]]))
+    torch.testing.assert_close(sb[1][0], _t([[-0.5]]))
+    torch.testing.assert_close(sb[1][1], _t([[1.0]]))
+    # second relu on [-1/2, 1]: lam = 2/3, mu = 1/6; c' = 2/3*1/4 + 1/6 = 1/3
+    torch.testing.assert_close(c, _t([[1.0 / 3.0]]))
+    torch.testing.assert_close(G.abs().sum(-1), _t([[2.0 / 3.0 * 0.75 + 1.0 / 6.0]]))
+
+
+def test_zono_hand_computed_two_dims():
+    # z0 = [x0 + x1, x0 - x1], x in [0,1]x[-1,1]; z0a in [-1, 2], z0b in [-1, 2]
+    # relu: lam = 2/3, mu = 1/3 each; z1 = z0a' + z0b' has centre
+    # 2/3*(0.5+0.5) + 2/3 = 4/3, generators x0: 2/3*(0.5+0.5) = 2/3,
+    # x1: 2/3*(1-1) = 0, new: 1/3 + 1/3 -> radius 4/3 -> [0, 8/3]
+    gg = _chain([[[1.0, 1.0], [1.0, -1.0]], [[1.0, 1.0]], [[1.0]]],
+                [[0.0, 0.0], [0.0], [0.0]])
+    sb, _ = rb.zono_forward_batched(_t([[0.0, -1.0]]), _t([[1.0, 1.0]]), gg)
+    torch.testing.assert_close(sb[0][0], _t([[-1.0, -1.0]]))
+    torch.testing.assert_close(sb[0][1], _t([[2.0, 2.0]]))
+    torch.testing.assert_close(sb[1][0], _t([[0.0]]))
+    torch.testing.assert_close(sb[1][1], _t([[8.0 / 3.0]]))
+
+
+def test_zono_contains_samples_and_matches_ibp_at_first_layer():
+    gg = wk.acas_gg(dtype=DT)
+    xl, xh = wk.acas_boxes(16, seed=5, dtype=DT)
+    xl, xh = xl * 4, xh * 4  # wider boxes: many unstable neurons
+    sb, _ = rb.zono_forward_batched(xl, xh, gg)
+    sbi = rb.ibp_forward_batched(xl, xh, gg)
+    torch.testing.assert_close(sb[0][0], sbi[0][0])
+    torch.testing.assert_close(sb[0][1], sbi[0][1])
+    pts = _util.sample_box(xl, xh, 300, seed=3)
+    for b in range(16):
+        _, pre = rb.point_forward(pts[b], gg)
+        for L, (lo, hi) in sb.items():
+            assert bool((pre[L] >= lo[b] - 1e-9).all())
+            assert bool((pre[L] <= hi[b] + 1e-9).all())
+
+
+# ---------------------------------------------------------------- CROWN
+def test_crown_hand_computed():
+    # y = relu(x), x in [-1, 3]: lower line y >= x (up_s = 3/4 > 1/2),
+    # upper line y <= 3/4 x + 3/4.  min y bound = -1, min(-y) bound = -3.
+    gg = _chain([[[1.0]], [[1.0]]], [[0.0], [0.0]])
+    xl, xh = _t([[-1.0]]), _t([[3.0]])
+    sb = rb.ibp_forward_batched(xl, xh, gg)
+    spec = {0: (_t([1.0]), 0.0), 1: (_t([-1.0]), 0.0)}
+    lb, A, acc = rb.spec_backward_batched(sb, xl, xh, gg, spec, return_input_linear=True)
+    torch.testing.assert_close(lb, _t([[-1.0, -3.0]]))
+    torch.testing.assert_close(A, _t([[[1.0], [-0.75]]]))
+    torch.testing.assert_close(acc, _t([[0.0, -0.75]]))
+
+
+def test_crown_sound_and_linear_bound_pointwise():
+    gg = wk.acas_gg(dtype=DT)
+    xl, xh = wk.acas_boxes(8, seed=2, dtype=DT)
+    xl, xh = xl * 3, xh * 3
+    spec_ew, _ = _util.spec_for(5)
+    sb, _ = rb.zono_forward_batched(xl, xh, gg)
+    lb, A, acc = rb.spec_backward_batched(sb, xl, xh, gg, spec_ew, return_input_linear=True)
+    Wq = torch.stack([spec_ew[q][0] for q in sorted(spec_ew)])
+    pts = _util.sample_box(xl, xh, 500, seed=4)
+    for b in range(8):
+        y, _ = rb.point_forward(pts[b], gg)
+        val = y @ Wq.T                                   # (P, Q)
+        lin = pts[b] @ A[b].T + acc[b]                   # (P, Q)
+        assert bool((lin <= val + 1e-9).all())           # linear lower bound holds
+        assert bool((lb[b] <= val.min(0).values + 1e-9).all())
+        assert bool((lb[b] <= lin.min(0).values + 1e-9).all())
+
+
+def _conv_as_dense(gg):
+    """Same network with every conv replaced by its dense fc matrix."""
+    ops = []
+    for op in gg['ops']:
+        if op['type'] == 'conv':
+            n = int(np.prod(op['in_shape']))
+            y0 = torch.nn.functional.conv2d(torch.zeros(1, *op['in_shape'], dtype=DT),
+                                            op['kernel'], op['bias'], stride=op['stride'],
+                                            padding=op['padding']).reshape(-1)
+            basis = torch.eye(n, dtype=DT).reshape(n, *op['in_shape'])
+            Wd = (torch.nn.functional.conv2d(basis, op['kernel'], op['bias'],
+                                             stride=op['stride'],
+                                             padding=op['padding']).reshape(n, -1) - y0).T
+            ops.append({'name': op['name'], 'type': 'fc', 'inputs': op['inputs'],
+                        'W': Wd.contiguous(), 'bias': y0})
+        else:
+            ops.append(op)
+    out = dict(gg)
+    out['ops'] = ops
+    return out
+
+
+def test_crown_conv_equals_dense_equivalent():
+    gg = _util.tiny_cnn(seed=4)
+    for op in gg['ops']:
+        if op['type'] == 'conv':
+            op['bias'] = torch.randn(op['bias'].shape, dtype=DT,
+                                     generator=torch.Generator().manual_seed(1)) * 0.2
+    dense = _conv_as_dense(gg)
+    xl, xh = _box(gg['input_n'], 2, 0.2, 3)
+    spec_ew, _ = _util.spec_for(2)
+    sb = rb.ibp_forward_batched(xl, xh, gg)
+    sbd = rb.ibp_forward_batched(xl, xh, dense)
+    for L in sb:
+        torch.testing.assert_close(sb[L][0], sbd[L][0])
+    lb, A, acc = rb.spec_backward_batched(sb, xl, xh, gg, spec_ew, return_input_linear=True)
+    lbd, Ad, accd = rb.spec_backward_batched(sb, xl, xh, dense, spec_ew,
+                                             return_input_linear=True)
+    torch.testing.assert_close(lb, lbd)
+    torch.testing.assert_close(A, Ad)
+    torch.testing.assert_close(acc, accd)
+
+
+def test_beta_zero_is_plain_and_beta_sound():
+    """tests/test_ibp_crown.py:246-288 of the reference, on an MLP."""
+    gg = _util.tiny_mlp([2, 6, 6, 2], seed=11)
+    xl, xh = _t([[-1.0, -1.0]]), _t([[1.0, 1.0]])
+    sb = rb.ibp_forward_batched(xl, xh, gg)
+    spec = {0: (_t([1.0, -1.0]), 0.0)}
+    lb_plain = rb.spec_backward_batched(sb, xl, xh, gg, spec)
+    n0 = sb[0][0].shape[1]
+    lb_b0 = rb.spec_backward_batched(sb, xl, xh, gg, spec,
+                                     relu_split_beta={0: torch.zeros(1, n0, dtype=DT)})
+    torch.testing.assert_close(lb_plain, lb_b0)
+    lo0, hi0 = sb[0][0][0], sb[0][1][0]
+    j = int(((lo0 < 0) & (hi0 > 0)).nonzero()[0])
+    cl = torch.full((1, n0), -np.inf, dtype=DT)
+    ch = torch.full((1, n0), np.inf, dtype=DT)
+    ch[0, j] = 0.0
+    root = {L: (lo[0], hi[0]) for L, (lo, hi) in sb.items()}
+    sbc = rb.ibp_forward_batched(xl, xh, gg, relu_clamps={0: (cl, ch)}, root_sb=root)
+    g = np.linspace(-1, 1, 201)
+    X = torch.tensor(np.stack(np.meshgrid(g, g), -1).reshape(-1, 2), dtype=DT)
+    y, pre = rb.point_forward(X, gg)
+    inside = pre[0][:, j] <= 0
+    true_min = float((y[inside] @ spec[0][0]).min())
+    sgn = torch.zeros(1, n0, dtype=DT)
+    sgn[0, j] = 1.0
+    for beta in (0.0, 0.05, 0.5, 5.0):
+        lb = float(rb.spec_backward_batched(sbc, xl, xh, gg, spec,
+                                            relu_split_beta={0: sgn * beta})[0, 0])
+        assert lb <= true_min + 1e-6
+
+
+# ------------------------------------------------ CROWN intermediate bounds
+def test_crown_intermediate_chunk_invariant_brackets_and_tightens():
+    gg = wk.acas_gg(dtype=DT)
+    xl, xh = wk.acas_boxes(6, seed=9, dtype=DT)
+    xl, xh = xl * 3, xh * 3
+    sb, _ = rb.zono_forward_batched(xl, xh, gg)
+    t1 = rb.crown_intermediate_batched(gg, xl, xh, chunk=1)
+    t2 = rb.crown_intermediate_batched(gg, xl, xh, chunk=4096)
+    pts = _util.sample_box(xl, xh, 300, seed=1)
+    for L in sb:
+        torch.testing.assert_close(t1[L][0], t2[L][0], atol=1e-9, rtol=0)
+        torch.testing.assert_close(t1[L][1], t2[L][1], atol=1e-9, rtol=0)
+        assert bool((t2[L][0] >= sb[L][0] - 1e-12).all())
+        assert bool((t2[L][1] <= sb[L][1] + 1e-12).all())
+    assert any(bool((t2[L][1] - t2[L][0] < sb[L][1] - sb[L][0] - 1e-9).any()) for L in sb)
+    for b in range(6):
+        _, pre = rb.point_forward(pts[b], gg)
+        for L in sb:
+            assert bool((pre[L] >= t2[L][0][b] - 1e-9).all())
+            assert bool((pre[L] <= t2[L][1][b] + 1e-9).all())
+
+
+def test_crown_intermediate_all_stable_layer_unchanged():
+    # positive weights/biases and a positive box: every neuron active
+    gg = _chain([np.full((3, 2), 0.5), np.full((3, 3), 0.5), np.full((1, 3), 1.0)],
+                [[0.1] * 3, [0.1] * 3, [0.0]])
+    xl, xh = _t([[0.5, 0.5]]), _t([[1.0, 1.0]])
+    sb, _ = rb.zono_forward_batched(xl, xh, gg)
+    t = rb.crown_intermediate_batched(gg, xl, xh)
+    for L in sb:
+        assert torch.equal(t[L][0], sb[L][0]) and torch.equal(t[L][1], sb[L][1])
+
+
+def test_crown_intermediate_union_seeding():
+    """A neuron unstable in only one domain is re-derived in every domain:
+    the batch result differs from per-domain runs only on stable neurons,
+    and never in the spec bound."""
+    gg = wk.acas_gg(dtype=DT)
+    xl, xh = wk.acas_boxes(4, seed=12, dtype=DT)
+    xl[0] *= 6
+    xh[0] *= 6
+    spec_ew, _ = _util.spec_for(5)
+    tb = rb.crown_intermediate_batched(gg, xl, xh)
+    lb_b = rb.spec_backward_batched(tb, xl, xh, gg, spec_ew)
+    for b in range(4):
+        ts = rb.crown_intermediate_batched(gg, xl[b:b + 1], xh[b:b + 1])
+        lb_s = rb.spec_backward_batched(ts, xl[b:b + 1], xh[b:b + 1], gg, spec_ew)
+        torch.testing.assert_close(lb_b[b:b + 1], lb_s, atol=1e-9, rtol=1e-9)
+        for L in ts:
+            ust = (ts[L][0][0] < 0) & (ts[L][1][0] > 0)
+            torch.testing.assert_close(tb[L][0][b][ust], ts[L][0][0][ust], atol=1e-9, rtol=0)
+
+
+# ---------------------------------------------------------------- alpha
+def test_alpha_first_iteration_is_crown_and_best_monotone():
+    gg = wk.acas_gg(dtype=DT)
+    xl, xh = wk.acas_boxes(8, seed=21, dtype=DT)
+    xl, xh = xl * 3, xh * 3
+    spec_ew, _ = _util.spec_for(5)
+    sb, _ = rb.zono_forward_batched(xl, xh, gg)
+    plain = rb.spec_backward_batched(sb, xl, xh, gg, spec_ew)
+    b1, n1 = rb.alpha_crown_batched(xl, xh, gg, spec_ew, n_iters=1, return_trace=True)
+    torch.testing.assert_close(b1, plain)
+    prev = b1
+    for k in (3, 6, 12):
+        bk = rb.alpha_crown_batched(xl, xh, gg, spec_ew, n_iters=k, early_stop_eps=-1.0)
+        assert bool((bk >= prev - 1e-12).all())
+        prev = bk
+    assert bool((prev > plain + 1e-6).any())
+    pts = _util.sample_box(xl, xh, 400, seed=5)
+    Wq = torch.stack([spec_ew[q][0] for q in sorted(spec_ew)])
+    for b in range(8):
+        y, _ = rb.point_forward(pts[b], gg)
+        assert bool((prev[b] <= (y @ Wq.T).min(0).values + 1e-9).all())
+
+
+def test_alpha_early_stop_on_global_max():
+    """A batch whose best bound cannot move stops after two iterations
+    (verify_zono_bnb.py:5283: global max improvement below eps)."""
+    gg = _chain([[[1.0]], [[1.0]]], [[0.5], [0.0]])
+    xl, xh = _t([[1.0]]), _t([[2.0]])                    # all stable
+    spec = {0: (_t([-1.0]), 0.0)}
+    _, n = rb.alpha_crown_batched(xl, xh, gg, spec, n_iters=20, return_trace=True)
+    assert n == 2

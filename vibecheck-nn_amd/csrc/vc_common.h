@@ -1,0 +1,37 @@
+// Shared helpers for the vibecheck_amd HIP library (gfx950 / CDNA4 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vibecheck_amd.h"
+
+#define VC_WAVE 64
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// One 16x16x4 fp32 MFMA step on a single 16x16 block.
+// Operand layout for lane l (0..63), g = l / 16, r = l % 16:
+//   a  = A[row r][k g]          (A is 16 x 4)
+//   b  = B[k g][col r]          (B is 4 x 16)
+//   acc[i] = D[row 4*g + i][col r]
+__device__ __forceinline__ v4f mfma16x16x4(float a, float b, v4f acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+}
+
+#define VC_LAUNCH_CHECK()                                   \
+  do {                                                      \
+    hipError_t _e = hipGetLastError();                      \
+    if (_e != hipSuccess) return VC_ERR_LAUNCH;             \
+  } while (0)
+
+static inline int vc_blocks(int64_t n, int threads) {
+  int64_t b = (n + threads - 1) / threads;
+  if (b < 1) b = 1;
+  if (b > 1048576) b = 1048576;
+  return (int)b;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}

@@ -1,0 +1,725 @@
+// Elementwise, reduction and integer/indexing kernels: ReLU relaxation,
+// IBP relu, concretization, CROWN intersection, alpha-CROWN reductions and
+// Adam, closure, halfspace clipping, compaction, widest-axis bisection.
+#include "vc_common.h"
+#include "vc_relax.h"
+
+namespace {
+
+constexpr int NT = 256;
+
+__global__ void k_fill_u8(uint8_t* p, int64_t n, uint8_t v) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+__global__ void k_make_slopes(const float* lo, const float* hi, int64_t n, float* lo_s,
+                              float* up_s, float* up_t, uint8_t* act, uint8_t* dead,
+                              uint8_t* unst) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    Relax s = relax(lo[i], hi[i]);
+    lo_s[i] = s.lo_s;
+    up_s[i] = s.up_s;
+    up_t[i] = s.up_t;
+    if (act) act[i] = s.active;
+    if (dead) dead[i] = s.dead;
+    if (unst) unst[i] = s.unstable;
+  }
+}
+
+__global__ void k_alpha_init(const float* lo, const float* hi, int64_t n, float* alpha) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    Relax s = relax(lo[i], hi[i]);
+    alpha[i] = (s.unstable && s.up_s > 0.5f) ? 1.f : 0.f;
+  }
+}
+
+__global__ void k_ibp_relu(const float* l, const float* h, int64_t B, int n,
+                           const float* rlo, const float* rhi, const float* cl,
+                           const float* ch, float* sb_lo, float* sb_hi, float* post_lo,
+                           float* post_hi) {
+  const int64_t total = B * (int64_t)n;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int j = (int)(i % n);
+    float lo = l[i], hi = h[i];
+    if (rlo) {
+      lo = fmaxf(lo, rlo[j]);
+      hi = fminf(hi, rhi[j]);
+    }
+    if (cl) {
+      lo = fmaxf(lo, cl[i]);
+      hi = fminf(hi, ch[i]);
+    }
+    hi = fmaxf(hi, lo);
+    sb_lo[i] = lo;
+    sb_hi[i] = hi;
+    if (post_lo) {
+      post_lo[i] = fmaxf(lo, 0.f);
+      post_hi[i] = fmaxf(hi, 0.f);
+    }
+  }
+}
+
+// lb[m] = acc[m] + sum_i pos(A) xl + sum_i neg(A) xh ; one wave per row.
+__global__ void k_concretize_wave(const float* A, int a_bcast, const float* acc, const float* xl,
+                                  const float* xh, int64_t M, int R, int n, float* lb) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+  if (m >= M) return;
+  const int64_t d = m / R;
+  float s1 = 0.f, s2 = 0.f;
+  for (int i = lane; i < n; i += 64) {
+    const float a = A[(a_bcast ? m % R : m) * n + i];
+    s1 += fmaxf(a, 0.f) * xl[d * n + i];
+    s2 += fminf(a, 0.f) * xh[d * n + i];
+  }
+  s1 = wave_sum(s1);
+  s2 = wave_sum(s2);
+  if (lane == 0) lb[m] = (acc[m] + s1) + s2;
+}
+
+__global__ void k_concretize_thread(const float* A, int a_bcast, const float* acc, const float* xl,
+                                    const float* xh, int64_t M, int R, int n, float* lb) {
+  const int64_t m = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (m >= M) return;
+  const int64_t d = m / R;
+  float s1 = 0.f, s2 = 0.f;
+  for (int i = 0; i < n; ++i) {
+    const float a = A[(a_bcast ? m % R : m) * n + i];
+    s1 += fmaxf(a, 0.f) * xl[d * n + i];
+    s2 += fminf(a, 0.f) * xh[d * n + i];
+  }
+  lb[m] = (acc[m] + s1) + s2;
+}
+
+// Standalone relu backward: one wave per row.
+__global__ void k_backward_relu(const float* ew, int64_t M, int R, int n, const float* lo,
+                                const float* hi, const float* alpha, int alpha_per_row,
+                                const float* beta, float* out, float* acc) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+  if (m >= M) return;
+  const int64_t d = m / R;
+  float p = 0.f;
+  for (int j = lane; j < n; j += 64) {
+    const int64_t bi = d * n + j;
+    const float x = ew[m * n + j];
+    Relax s = relax(lo[bi], hi[bi]);
+    float ls = s.lo_s;
+    if (alpha) {
+      const float a = alpha_per_row ? alpha[m * n + j] : alpha[bi];
+      ls = s.active ? 1.f : (s.unstable ? a : 0.f);
+    }
+    const float ep = fmaxf(x, 0.f), en = fminf(x, 0.f);
+    float e = ep * ls + en * s.up_s;
+    if (beta) e = e + beta[bi];
+    out[m * n + j] = e;
+    p += en * s.up_t;
+  }
+  p = wave_sum(p);
+  if (lane == 0) acc[m] += p;
+}
+
+__global__ void k_crown_intersect(const float* sl, const int32_t* idx, int k, int64_t B,
+                                  int n, float* lo, float* hi) {
+  const int64_t total = B * (int64_t)k;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = i / k;
+    const int t = (int)(i % k);
+    const int64_t o = b * n + idx[t];
+    const float lc = fmaxf(lo[o], sl[b * 2 * k + t]);
+    const float hc = fmaxf(fminf(hi[o], -sl[b * 2 * k + k + t]), lc);
+    lo[o] = lc;
+    hi[o] = hc;
+  }
+}
+
+__global__ void k_unstable_union(const float* lo, const float* hi, int64_t B, int n,
+                                 uint8_t* flag) {
+  const int64_t total = B * (int64_t)n;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    if (lo[i] < 0.f && hi[i] > 0.f) flag[i % n] = 1;
+  }
+}
+
+__global__ void k_alpha_grad_reduce(const float* gE, const float* P, int p_bcast, int64_t B,
+                                    int R, int n, const float* lo, const float* hi, float* ga,
+                                    float* gb) {
+  const int64_t total = B * (int64_t)n;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t d = i / n;
+    const int j = (int)(i % n);
+    float sa = 0.f, sb = 0.f;
+    for (int q = 0; q < R; ++q) {
+      const int64_t o = (d * R + q) * n + j;
+      const float ge = gE[o];
+      sa += ge * fmaxf(P[p_bcast ? (int64_t)q * n + j : o], 0.f);
+      sb += ge;
+    }
+    Relax s = relax(lo[i], hi[i]);
+    if (ga) ga[i] = s.unstable ? sa : 0.f;
+    if (gb) gb[i] = sb;
+  }
+}
+
+// torch.optim.Adam (amsgrad off, no weight decay) on the loss -lb, then
+// the projection clamp.  Contractions are disabled so each torch op rounds.
+__global__ void k_adam(float* p, const float* lbg, float* m, float* v, int64_t n, float b1,
+                       float b2, float eps, float neg_step, float bc2, float lo_c,
+                       float hi_c) {
+#pragma clang fp contract(off)
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float g = -lbg[i];
+    float mi = m[i];
+    mi = mi + (1.f - b1) * (g - mi);
+    float vi = v[i] * b2;
+    vi = vi + ((1.f - b2) * g) * g;
+    const float denom = sqrtf(vi) / bc2 + eps;
+    float pi = p[i] + neg_step * (mi / denom);
+    pi = fminf(fmaxf(pi, lo_c), hi_c);
+    m[i] = mi;
+    v[i] = vi;
+    p[i] = pi;
+  }
+}
+
+__global__ void k_best_update(float* best, const float* lb, int64_t n, int init, float* out2) {
+  __shared__ float smax[16];
+  __shared__ int sneg[16];
+  float mx = -INFINITY;
+  int notpos = 0;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    const float x = lb[i];
+    const float b = init ? x : fmaxf(best[i], x);
+    best[i] = b;
+    mx = fmaxf(mx, b);
+    notpos |= !(b > 0.f);
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    notpos |= __shfl_xor(notpos, o, 64);
+  }
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) {
+    smax[w] = mx;
+    sneg[w] = notpos;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int nw = blockDim.x >> 6;
+    float a = smax[0];
+    int b = sneg[0];
+    for (int i = 1; i < nw; ++i) {
+      a = fmaxf(a, smax[i]);
+      b |= sneg[i];
+    }
+    out2[0] = a;
+    out2[1] = b ? 0.f : 1.f;
+  }
+}
+
+__global__ void k_closure(const float* lb, int64_t B, int Q, const int32_t* dptr,
+                          const int32_t* qidx, int nd, uint8_t* closed) {
+  const int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  bool all = true;
+  for (int d = 0; d < nd; ++d) {
+    bool any = false;
+    for (int t = dptr[d]; t < dptr[d + 1]; ++t) any |= lb[b * Q + qidx[t]] > 0.f;
+    all &= any;
+  }
+  closed[b] = all;
+}
+
+// One thread per domain.  For each disjunct D: total_q = pos(A_q).xl +
+// neg(A_q).xh; per dim i the projection threshold
+// thr = (-b_q - (total_q - contrib_qi)) / A_qi; xh' = min(xh, min over
+// A_qi > 1e-12 of thr), xl' = max(xl, max over A_qi < -1e-12 of thr);
+// feasible iff no total_q + b_q > 0 and no xl' > xh'.
+__device__ __forceinline__ void clip_dim(const float* A, const float* bq, const float* tot,
+                                         const int32_t* qs, int nq, int n, int i, float xl,
+                                         float xh, float& lo_o, float& hi_o) {
+  float hmin = INFINITY, lmax = -INFINITY;
+  for (int t = 0; t < nq; ++t) {
+    const int q = qs[t];
+    const float a = A[q * n + i];
+    const float contrib = fmaxf(a, 0.f) * xl + fminf(a, 0.f) * xh;
+    const float other = tot[t] - contrib;
+    const float safe = fabsf(a) > 1e-12f ? a : 1.f;
+    const float thr = (-bq[q] - other) / safe;
+    const float hq = a > 1e-12f ? thr : xh;
+    const float lq = a < -1e-12f ? thr : xl;
+    hmin = fminf(hmin, hq);
+    lmax = fmaxf(lmax, lq);
+  }
+  hi_o = fminf(hmin, xh);
+  lo_o = fmaxf(lmax, xl);
+}
+
+constexpr int CLIP_MAXQ = 64;
+
+__global__ void k_clip(const float* xl, const float* xh, const float* A, const float* bv,
+                       int64_t B, int Q, int n, const int32_t* dptr, const int32_t* qidx,
+                       int nd, float* xlo, float* xho, uint8_t* feas) {
+  const int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const float* Ab = A + b * (int64_t)Q * n;
+  const float* bb = bv + b * (int64_t)Q;
+  const float* l = xl + b * n;
+  const float* h = xh + b * n;
+  float* lo_o = xlo + b * n;
+  float* hi_o = xho + b * n;
+  float tot[CLIP_MAXQ];
+  bool any_feas = false;
+  for (int d = 0; d < nd; ++d) {
+    const int32_t* qs = qidx + dptr[d];
+    const int nq = dptr[d + 1] - dptr[d];
+    bool empty = false;
+    for (int t = 0; t < nq; ++t) {
+      const int q = qs[t];
+      float s1 = 0.f, s2 = 0.f;
+      for (int i = 0; i < n; ++i) {
+        const float a = Ab[q * n + i];
+        s1 += fmaxf(a, 0.f) * l[i];
+        s2 += fminf(a, 0.f) * h[i];
+      }
+      tot[t] = s1 + s2;
+      empty |= (tot[t] + bb[q]) > 0.f;
+    }
+    for (int i = 0; i < n; ++i) {
+      float lo, hi;
+      clip_dim(Ab, bb, tot, qs, nq, n, i, l[i], h[i], lo, hi);
+      empty |= lo > hi;
+    }
+    const bool fd = !empty;
+    if (nd == 1) {
+      for (int i = 0; i < n; ++i) clip_dim(Ab, bb, tot, qs, nq, n, i, l[i], h[i], lo_o[i], hi_o[i]);
+      feas[b] = fd;
+      return;
+    }
+    if (fd) {
+      for (int i = 0; i < n; ++i) {
+        float lo, hi;
+        clip_dim(Ab, bb, tot, qs, nq, n, i, l[i], h[i], lo, hi);
+        if (!any_feas) {
+          lo_o[i] = lo;
+          hi_o[i] = hi;
+        } else {
+          lo_o[i] = fminf(lo_o[i], lo);
+          hi_o[i] = fmaxf(hi_o[i], hi);
+        }
+      }
+      any_feas = true;
+    }
+  }
+  if (!any_feas) {
+    for (int i = 0; i < n; ++i) {
+      lo_o[i] = l[i];
+      hi_o[i] = h[i];
+    }
+  }
+  feas[b] = any_feas;
+}
+
+// ---- compaction: ascending positions of non-zero flags -------------------
+constexpr int CPT = 4;               // flags per thread
+constexpr int CCH = NT * CPT;        // flags per block
+
+__device__ __forceinline__ int block_excl_scan(int v, int* total) {
+  __shared__ int wsum[NT / 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int x = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[w] = x;
+  __syncthreads();
+  int off = 0, tot = 0;
+  for (int i = 0; i < NT / 64; ++i) {
+    if (i < w) off += wsum[i];
+    tot += wsum[i];
+  }
+  __syncthreads();
+  *total = tot;
+  return off + x - v;
+}
+
+__device__ __forceinline__ bool sel_hit(const uint8_t* f, int64_t i, int64_t n, int zero) {
+  return i < n && ((f[i] != 0) != (zero != 0));
+}
+
+__global__ void k_compact_count(const uint8_t* f, int64_t n, int zero, int64_t* bcnt) {
+  const int64_t base = blockIdx.x * (int64_t)CCH + threadIdx.x * CPT;
+  int c = 0;
+  for (int e = 0; e < CPT; ++e)
+    if (sel_hit(f, base + e, n, zero)) ++c;
+  int tot;
+  block_excl_scan(c, &tot);
+  if (threadIdx.x == 0) bcnt[blockIdx.x] = tot;
+}
+
+__global__ void k_compact_scan(int64_t* bcnt, int64_t nb, int64_t* count_out) {
+  // single block: exclusive scan of nb block counts in chunks of NT
+  __shared__ int64_t carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < nb; c0 += NT) {
+    const int64_t i = c0 + threadIdx.x;
+    const int64_t v = i < nb ? bcnt[i] : 0;
+    __shared__ int64_t buf[NT];
+    buf[threadIdx.x] = v;
+    __syncthreads();
+    for (int o = 1; o < NT; o <<= 1) {
+      const int64_t y = threadIdx.x >= o ? buf[threadIdx.x - o] : 0;
+      __syncthreads();
+      buf[threadIdx.x] += y;
+      __syncthreads();
+    }
+    if (i < nb) bcnt[i] = carry + buf[threadIdx.x] - v;
+    __syncthreads();
+    if (threadIdx.x == NT - 1) carry += buf[NT - 1];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) count_out[0] = carry;
+}
+
+__global__ void k_compact_write(const uint8_t* f, int64_t n, int zero, const int64_t* boff,
+                                int64_t* idx) {
+  const int64_t base = blockIdx.x * (int64_t)CCH + threadIdx.x * CPT;
+  int c = 0;
+  for (int e = 0; e < CPT; ++e)
+    if (sel_hit(f, base + e, n, zero)) ++c;
+  int tot;
+  int off = block_excl_scan(c, &tot);
+  int64_t o = boff[blockIdx.x] + off;
+  for (int e = 0; e < CPT; ++e)
+    if (sel_hit(f, base + e, n, zero)) idx[o++] = base + e;
+}
+
+// rows[idx[r]] = max(rows[idx[r]], src[r]) over rows of q floats.
+__global__ void k_scatter_max_rows(float* rows, const int64_t* idx, const float* src, int64_t nr,
+                                   int q) {
+  const int64_t total = nr * (int64_t)q;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / q;
+    const int c = (int)(i % q);
+    float* d = rows + idx[r] * q + c;
+    *d = fmaxf(*d, src[i]);
+  }
+}
+
+__global__ void k_gather_rows(const float* in, const int64_t* idx, int64_t nr, int cols,
+                              float* out) {
+  const int64_t total = nr * (int64_t)cols;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / cols;
+    const int c = (int)(i % cols);
+    out[i] = in[idx[r] * cols + c];
+  }
+}
+
+// First index of the maximum width (NaN counts as maximal, like argmax).
+__global__ void k_widest(const float* xl, const float* xh, int64_t B, int n, int64_t* ax,
+                         uint8_t* usable) {
+  const int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  int best = 0;
+  float bw = xh[b * n] - xl[b * n];
+  if (!isnan(bw)) {
+    for (int i = 1; i < n; ++i) {
+      const float w = xh[b * n + i] - xl[b * n + i];
+      if (isnan(w)) {
+        best = i;
+        bw = w;
+        break;
+      }
+      if (w > bw) {
+        bw = w;
+        best = i;
+      }
+    }
+  }
+  ax[b] = best;
+  if (usable) usable[b] = (xh[b * n + best] - xl[b * n + best]) > 1e-12f;
+}
+
+__global__ void k_bisect(const float* xl, const float* xh, const int64_t* ax,
+                         const int64_t* uidx, int64_t nu, int n, float* lxl, float* lxh,
+                         float* hxl, float* hxh) {
+  const int64_t total = nu * (int64_t)n;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / n;
+    const int c = (int)(i % n);
+    const int64_t src = uidx[r];
+    const int a = (int)ax[src];
+    const float l = xl[src * n + c], h = xh[src * n + c];
+    const float mid = (xl[src * n + a] + xh[src * n + a]) * 0.5f;
+    lxl[i] = l;
+    lxh[i] = c == a ? mid : h;
+    hxl[i] = c == a ? mid : l;
+    hxh[i] = h;
+  }
+}
+
+__global__ void k_zono_input(const float* xl, const float* xh, int64_t B, int n,
+                             const int32_t* vidx, int K, float* c, float* G) {
+  const int64_t total = B * (int64_t)n;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    c[i] = (xl[i] + xh[i]) / 2.f;
+  }
+  const int64_t tg = total * (int64_t)K;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < tg;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t bi = i / K;
+    const int k = (int)(i % K);
+    const int j = (int)(bi % n);
+    G[i] = (vidx[k] == j) ? (xh[bi] - xl[bi]) / 2.f : 0.f;
+  }
+}
+
+}  // namespace
+
+extern "C" int vc_abi_version(void) { return 1; }
+
+extern "C" int vc_make_slopes(const float* lo, const float* hi, int64_t n, float* lo_s,
+                              float* up_s, float* up_t, uint8_t* active, uint8_t* dead,
+                              uint8_t* unstable, vc_stream_t stream) {
+  if (n < 0 || (n > 0 && (!lo || !hi || !lo_s || !up_s || !up_t))) return VC_ERR_ARG;
+  if (n == 0) return VC_OK;
+  hipLaunchKernelGGL(k_make_slopes, dim3(vc_blocks(n, NT)), dim3(NT), 0, (hipStream_t)stream,
+                     lo, hi, n, lo_s, up_s, up_t, active, dead, unstable);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_alpha_init(const float* lo, const float* hi, int64_t n, float* alpha,
+                             vc_stream_t stream) {
+  if (n < 0 || (n > 0 && (!lo || !hi || !alpha))) return VC_ERR_ARG;
+  if (n == 0) return VC_OK;
+  hipLaunchKernelGGL(k_alpha_init, dim3(vc_blocks(n, NT)), dim3(NT), 0, (hipStream_t)stream,
+                     lo, hi, n, alpha);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_ibp_relu(const float* l, const float* h, int64_t B, int n,
+                           const float* root_lo, const float* root_hi, const float* cl,
+                           const float* ch, float* sb_lo, float* sb_hi, float* post_lo,
+                           float* post_hi, vc_stream_t stream) {
+  if (!l || !h || !sb_lo || !sb_hi || B < 0 || n <= 0) return VC_ERR_ARG;
+  if ((root_lo == nullptr) != (root_hi == nullptr) || (cl == nullptr) != (ch == nullptr) ||
+      (post_lo == nullptr) != (post_hi == nullptr))
+    return VC_ERR_ARG;
+  const int64_t total = B * (int64_t)n;
+  if (total == 0) return VC_OK;
+  hipLaunchKernelGGL(k_ibp_relu, dim3(vc_blocks(total, NT)), dim3(NT), 0, (hipStream_t)stream,
+                     l, h, B, n, root_lo, root_hi, cl, ch, sb_lo, sb_hi, post_lo, post_hi);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_concretize(const float* A, const float* acc, const float* xl,
+                             const float* xh, int64_t M, int R, int n_in, int a_bcast,
+                             float* lb, vc_stream_t stream) {
+  if (!A || !acc || !xl || !xh || !lb || R <= 0 || n_in <= 0 || M < 0 || M % R) return VC_ERR_ARG;
+  if (M == 0) return VC_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (n_in <= 32) {
+    hipLaunchKernelGGL(k_concretize_thread, dim3(vc_blocks(M, NT)), dim3(NT), 0, st, A, a_bcast,
+                       acc, xl, xh, M, R, n_in, lb);
+  } else {
+    hipLaunchKernelGGL(k_concretize_wave, dim3(vc_blocks(M * 64, NT)), dim3(NT), 0, st, A,
+                       a_bcast, acc, xl, xh, M, R, n_in, lb);
+  }
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_backward_relu(const float* ew_in, int64_t M, int R, int n,
+                                const float* relu_lo, const float* relu_hi,
+                                const float* alpha, int alpha_per_row, const float* beta,
+                                float* ew_out, float* acc, vc_stream_t stream) {
+  if (!ew_in || !relu_lo || !relu_hi || !ew_out || !acc || R <= 0 || n <= 0 || M < 0 || M % R)
+    return VC_ERR_ARG;
+  if (M == 0) return VC_OK;
+  hipLaunchKernelGGL(k_backward_relu, dim3(vc_blocks(M * 64, NT)), dim3(NT), 0,
+                     (hipStream_t)stream, ew_in, M, R, n, relu_lo, relu_hi, alpha,
+                     alpha_per_row, beta, ew_out, acc);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_crown_intersect(const float* sl, const int32_t* idx, int k, int64_t B,
+                                  int n, float* lo, float* hi, vc_stream_t stream) {
+  if (!sl || !idx || !lo || !hi || k < 0 || B < 0 || n <= 0) return VC_ERR_ARG;
+  if ((int64_t)k * B == 0) return VC_OK;
+  hipLaunchKernelGGL(k_crown_intersect, dim3(vc_blocks(B * k, NT)), dim3(NT), 0,
+                     (hipStream_t)stream, sl, idx, k, B, n, lo, hi);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_unstable_union(const float* lo, const float* hi, int64_t B, int n,
+                                 uint8_t* flag, vc_stream_t stream) {
+  if (!lo || !hi || !flag || B < 0 || n <= 0) return VC_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_fill_u8, dim3(vc_blocks(n, NT)), dim3(NT), 0, st, flag, (int64_t)n,
+                     (uint8_t)0);
+  if (B > 0)
+    hipLaunchKernelGGL(k_unstable_union, dim3(vc_blocks(B * n, NT)), dim3(NT), 0, st, lo, hi,
+                       B, n, flag);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_alpha_grad_reduce(const float* gE, const float* P, int p_bcast, int64_t B,
+                                    int R, int n, const float* relu_lo, const float* relu_hi,
+                                    float* galpha, float* gbeta, vc_stream_t stream) {
+  if (!gE || !P || !relu_lo || !relu_hi || R <= 0 || n <= 0 || B < 0) return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  hipLaunchKernelGGL(k_alpha_grad_reduce, dim3(vc_blocks(B * n, NT)), dim3(NT), 0,
+                     (hipStream_t)stream, gE, P, p_bcast, B, R, n, relu_lo, relu_hi, galpha,
+                     gbeta);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_adam_step(float* param, const float* lb_grad, float* exp_avg,
+                            float* exp_avg_sq, int64_t n, float b1, float b2, float eps,
+                            double step_size, double bc2_sqrt, float lo_clamp, float hi_clamp,
+                            vc_stream_t stream) {
+  if (!param || !lb_grad || !exp_avg || !exp_avg_sq || n < 0) return VC_ERR_ARG;
+  if (n == 0) return VC_OK;
+  hipLaunchKernelGGL(k_adam, dim3(vc_blocks(n, NT)), dim3(NT), 0, (hipStream_t)stream, param,
+                     lb_grad, exp_avg, exp_avg_sq, n, b1, b2, eps, (float)(-step_size),
+                     (float)bc2_sqrt, lo_clamp, hi_clamp);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_best_update(float* best, const float* lb, int64_t n, int init, float* out2,
+                              vc_stream_t stream) {
+  if (!best || !lb || !out2 || n <= 0) return VC_ERR_ARG;
+  hipLaunchKernelGGL(k_best_update, dim3(1), dim3(1024), 0, (hipStream_t)stream, best, lb, n,
+                     init, out2);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_closure(const float* lb, int64_t B, int Q, const int32_t* d_ptr,
+                          const int32_t* q_idx, int n_disj, uint8_t* closed,
+                          vc_stream_t stream) {
+  if (!lb || !d_ptr || !q_idx || !closed || B < 0 || Q <= 0 || n_disj < 0) return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  hipLaunchKernelGGL(k_closure, dim3(vc_blocks(B, NT)), dim3(NT), 0, (hipStream_t)stream, lb,
+                     B, Q, d_ptr, q_idx, n_disj, closed);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_clip_box(const float* xl, const float* xh, const float* A, const float* b,
+                           int64_t B, int Q, int n, const int32_t* d_ptr,
+                           const int32_t* q_idx, int n_disj, float* xl_out, float* xh_out,
+                           uint8_t* feasible, vc_stream_t stream) {
+  if (!xl || !xh || !A || !b || !d_ptr || !q_idx || !xl_out || !xh_out || !feasible)
+    return VC_ERR_ARG;
+  if (B < 0 || Q <= 0 || n <= 0 || n_disj <= 0) return VC_ERR_ARG;
+  if (Q > CLIP_MAXQ) return VC_ERR_UNSUPPORTED;
+  if (B == 0) return VC_OK;
+  hipLaunchKernelGGL(k_clip, dim3(vc_blocks(B, 64)), dim3(64), 0, (hipStream_t)stream, xl, xh,
+                     A, b, B, Q, n, d_ptr, q_idx, n_disj, xl_out, xh_out, feasible);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int64_t vc_compact_workspace(int64_t n) {
+  const int64_t nb = (n + CCH - 1) / CCH;
+  return (nb < 1 ? 1 : nb) * (int64_t)sizeof(int64_t);
+}
+
+extern "C" int vc_scatter_max_rows(float* rows, const int64_t* idx, const float* src,
+                                   int64_t n_rows, int q, vc_stream_t stream) {
+  if (!rows || !idx || !src || n_rows < 0 || q <= 0) return VC_ERR_ARG;
+  if (n_rows == 0) return VC_OK;
+  hipLaunchKernelGGL(k_scatter_max_rows, dim3(vc_blocks(n_rows * q, NT)), dim3(NT), 0,
+                     (hipStream_t)stream, rows, idx, src, n_rows, q);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_compact(const uint8_t* flags, int64_t n, int select_zero, int64_t* idx_out,
+                          int64_t* count_out, void* workspace, int64_t ws_bytes,
+                          vc_stream_t stream) {
+  if (!flags || !idx_out || !count_out || !workspace || n < 0) return VC_ERR_ARG;
+  if (ws_bytes < vc_compact_workspace(n)) return VC_ERR_OOM;
+  hipStream_t st = (hipStream_t)stream;
+  int64_t nb = (n + CCH - 1) / CCH;
+  if (nb < 1) nb = 1;
+  if (nb > 2147483647LL) return VC_ERR_ARG;
+  int64_t* bc = (int64_t*)workspace;
+  hipLaunchKernelGGL(k_compact_count, dim3((unsigned)nb), dim3(NT), 0, st, flags, n, select_zero,
+                     bc);
+  hipLaunchKernelGGL(k_compact_scan, dim3(1), dim3(NT), 0, st, bc, nb, count_out);
+  hipLaunchKernelGGL(k_compact_write, dim3((unsigned)nb), dim3(NT), 0, st, flags, n, select_zero,
+                     bc, idx_out);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_gather_rows(const float* in, const int64_t* idx, int64_t n_rows, int cols,
+                              float* out, vc_stream_t stream) {
+  if (!in || !idx || !out || n_rows < 0 || cols <= 0) return VC_ERR_ARG;
+  if (n_rows == 0) return VC_OK;
+  hipLaunchKernelGGL(k_gather_rows, dim3(vc_blocks(n_rows * cols, NT)), dim3(NT), 0,
+                     (hipStream_t)stream, in, idx, n_rows, cols, out);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_widest_axis(const float* xl, const float* xh, int64_t B, int n, int64_t* ax,
+                              uint8_t* usable, vc_stream_t stream) {
+  if (!xl || !xh || !ax || B < 0 || n <= 0) return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  hipLaunchKernelGGL(k_widest, dim3(vc_blocks(B, NT)), dim3(NT), 0, (hipStream_t)stream, xl,
+                     xh, B, n, ax, usable);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_bisect(const float* xl, const float* xh, const int64_t* ax,
+                         const int64_t* u_idx, int64_t n_u, int n, float* low_xl,
+                         float* low_xh, float* high_xl, float* high_xh, vc_stream_t stream) {
+  if (!xl || !xh || !ax || !u_idx || !low_xl || !low_xh || !high_xl || !high_xh || n_u < 0 ||
+      n <= 0)
+    return VC_ERR_ARG;
+  if (n_u == 0) return VC_OK;
+  hipLaunchKernelGGL(k_bisect, dim3(vc_blocks(n_u * n, NT)), dim3(NT), 0, (hipStream_t)stream,
+                     xl, xh, ax, u_idx, n_u, n, low_xl, low_xh, high_xl, high_xh);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_zono_input(const float* xl, const float* xh, int64_t B, int n,
+                             const int32_t* var_idx, int K, float* c, float* G,
+                             vc_stream_t stream) {
+  if (!xl || !xh || !c || B < 0 || n <= 0 || K < 0) return VC_ERR_ARG;
+  if (K > 0 && (!var_idx || !G)) return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  hipLaunchKernelGGL(k_zono_input, dim3(vc_blocks(B * (int64_t)n * (K > 0 ? K : 1), NT)),
+                     dim3(NT), 0, (hipStream_t)stream, xl, xh, B, n, var_idx, K, c, G);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}

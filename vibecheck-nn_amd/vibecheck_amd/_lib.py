@@ -1,0 +1,170 @@
+"""ctypes binding of libvibecheck_amd.so (the C ABI in include/vibecheck_amd.h).
+
+The library is the only compute path: if it is missing, or a tensor is not
+on the GPU, calls raise instead of falling back to anything else.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, 'libvibecheck_amd.so')
+
+VC_OK, VC_ERR_ARG, VC_ERR_OOM, VC_ERR_UNSUPPORTED, VC_ERR_LAUNCH = 0, 1, 2, 3, 4
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+_D = ctypes.c_double
+
+# name -> argtypes (restype int unless listed in _RESTYPE)
+SIGNATURES = {
+    'vc_abi_version': [],
+    'vc_make_slopes': [_P, _P, _L, _P, _P, _P, _P, _P, _P, _P],
+    'vc_ibp_fc': [_P, _P, _L, _I, _P, _P, _I, _P, _P, _P],
+    'vc_ibp_conv': [_P, _P, _L, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _I,
+                    _I, _I, _I, _P, _P, _P],
+    'vc_ibp_relu': [_P, _P, _L, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    'vc_zono_input': [_P, _P, _L, _I, _P, _I, _P, _P, _P],
+    'vc_zono_fc': [_P, _P, _L, _I, _I, _P, _P, _I, _P, _P, _P],
+    'vc_zono_conv': [_P, _P, _L, _I, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I,
+                     _I, _I, _I, _I, _P, _P, _P],
+    'vc_zono_relu_bounds': [_P, _P, _L, _I, _I, _P, _P, _P, _P, _P],
+    'vc_zono_relu_apply': [_P, _P, _P, _P, _P, _L, _I, _I, _I, _P, _P, _P],
+    'vc_backward_fc': [_P, _L, _I, _I, _P, _P, _P, _I, _P, _P, _P, _I, _P,
+                       _P, _P, _I, _P],
+    'vc_backward_relu': [_P, _L, _I, _I, _P, _P, _P, _I, _P, _P, _P, _P],
+    'vc_backward_conv': [_P, _L, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I,
+                         _I, _I, _I, _P, _P, _P],
+    'vc_concretize': [_P, _P, _P, _P, _L, _I, _I, _I, _P, _P],
+    'vc_crown_intersect': [_P, _P, _I, _L, _I, _P, _P, _P],
+    'vc_unstable_union': [_P, _P, _L, _I, _P, _P],
+    'vc_alpha_init': [_P, _P, _L, _P, _P],
+    'vc_alpha_grad_step': [_P, _P, _L, _I, _I, _P, _P, _P, _I, _P, _P, _I,
+                           _P, _P],
+    'vc_alpha_grad_reduce': [_P, _P, _I, _L, _I, _I, _P, _P, _P, _P, _P],
+    'vc_alpha_grad_input': [_P, _P, _P, _L, _I, _I, _P, _P, _I, _P, _P],
+    'vc_adam_step': [_P, _P, _P, _P, _L, _F, _F, _F, _D, _D, _F, _F, _P],
+    'vc_best_update': [_P, _P, _L, _I, _P, _P],
+    'vc_closure': [_P, _L, _I, _P, _P, _I, _P, _P],
+    'vc_clip_box': [_P, _P, _P, _P, _L, _I, _I, _P, _P, _I, _P, _P, _P, _P],
+    'vc_compact_workspace': [_L],
+    'vc_compact': [_P, _L, _I, _P, _P, _P, _L, _P],
+    'vc_scatter_max_rows': [_P, _P, _P, _L, _I, _P],
+    'vc_gather_rows': [_P, _P, _L, _I, _P, _P],
+    'vc_widest_axis': [_P, _P, _L, _I, _P, _P, _P],
+    'vc_bisect': [_P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P],
+}
+_RESTYPE = {'vc_compact_workspace': ctypes.c_int64}
+
+_lib = None
+
+
+class HipLibraryMissing(ImportError):
+    pass
+
+
+def load():
+    """Load (once) and return the ctypes library handle."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise HipLibraryMissing(
+            f'{LIB_PATH} is not built; run __graft_entry__.build() or '
+            f'make -C vibecheck-nn_amd/csrc')
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPE.get(name, ctypes.c_int)
+    _lib = lib
+    return lib
+
+
+def check(rc, name):
+    if rc == VC_OK:
+        return
+    msg = f'{name} failed with status {rc}'
+    if rc == VC_ERR_OOM:
+        raise torch.cuda.OutOfMemoryError(msg)
+    if rc == VC_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    if rc == VC_ERR_ARG:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+# Algorithmic work per launch, from the call's arguments (used by the
+# optional per-entry-point timing below).
+_FLOPS = {
+    # 2 * M * n_out * n_in
+    'vc_backward_fc': lambda a: 2.0 * a[1] * a[3] * a[11],
+}
+
+_timing = None
+
+
+def timing_begin(names):
+    """Record HIP events around every call of the named entry points (on the
+    current stream, which is the launch stream)."""
+    global _timing
+    _timing = {n: [] for n in names}
+
+
+def timing_end():
+    """Stop recording; returns {name: {'launches', 'seconds', 'flops'}}."""
+    global _timing
+    rec, _timing = _timing, None
+    torch.cuda.synchronize()
+    out = {}
+    for n, lst in (rec or {}).items():
+        secs = sum(s.elapsed_time(e) for s, e, _ in lst) / 1e3
+        out[n] = {'launches': len(lst), 'seconds': secs,
+                  'flops': sum(f for _, _, f in lst)}
+    return out
+
+
+def call(name, *args):
+    lib = load()
+    if _timing is not None and name in _timing:
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        rc = getattr(lib, name)(*args)
+        e.record()
+        _timing[name].append((s, e, _FLOPS.get(name, lambda a: 0.0)(args)))
+        check(rc, name)
+        return
+    check(getattr(lib, name)(*args), name)
+
+
+def ptr(t):
+    """Device pointer of a contiguous GPU tensor (or None)."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise RuntimeError('vibecheck_amd: tensor is not on the GPU '
+                           '(the HIP library is the only compute path)')
+    if not t.is_contiguous():
+        raise ValueError('vibecheck_amd: tensor must be contiguous')
+    return t.data_ptr()
+
+
+def f32(t):
+    """Contiguous fp32 GPU view of t (raises for other dtypes)."""
+    if t is None:
+        return None
+    if t.dtype != torch.float32:
+        raise NotImplementedError(
+            f'vibecheck_amd computes in fp32 only, got {t.dtype}')
+    if not t.is_cuda:
+        raise RuntimeError('vibecheck_amd: tensor is not on the GPU '
+                           '(the HIP library is the only compute path)')
+    return t.contiguous()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream

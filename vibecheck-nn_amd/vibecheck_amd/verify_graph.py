@@ -1,0 +1,350 @@
+"""Input-split branch-and-bound on the GPU, with the reference's function
+names and signatures (verify_graph.py of the reference).
+
+``_input_split_batched`` runs the reference's worklist loop
+(verify_graph.py:12466-13464) for the bound engine's settings: CROWN or
+zonotope intermediate bounds, domain clipping, batched alpha-CROWN on
+unclosed leaves, widest-dimension bisection.  Closure, clipping,
+compaction, branching and bisection run as HIP kernels; the worklist is a
+LIFO list of device-resident 2-D chunks.  Root/leaf PGD, SB branching and
+LP/MILP escalation are not part of this engine.
+"""
+import time
+
+import torch
+
+from ._lib import call, f32, ptr, stream
+from . import _lib
+from .spec import dedup_queries
+from .verify_zono_bnb import (_crown_intermediate_batched,
+                              _forward_zonotope_graph_batched,
+                              _run_alpha_crown_inputsplit_batched,
+                              _spec_backward_graph_batched)
+
+__all__ = ['_clip_box_by_halfspaces_batched', '_input_split_batched',
+           'DisjunctTable', 'bab_step', 'ChunkWorklist']
+
+
+class DisjunctTable:
+    """Device CSR of disjunct -> query positions (verify_graph.py:12658-12682)."""
+
+    MAX_GROUP = 64  # per-disjunct query limit of the clip kernel
+
+    def __init__(self, disj_q_idx, device):
+        self.groups = [list(v) for v in disj_q_idx.values()]
+        if any(len(g) > self.MAX_GROUP for g in self.groups):
+            raise NotImplementedError(
+                f'vibecheck_amd: a disjunct has more than {self.MAX_GROUP} queries')
+        ptrs = [0]
+        flat = []
+        for g in self.groups:
+            flat.extend(g)
+            ptrs.append(len(flat))
+        self.d_ptr = torch.tensor(ptrs, dtype=torch.int32, device=device)
+        self.q_idx = torch.tensor(flat if flat else [0], dtype=torch.int32,
+                                  device=device)
+        self.n = len(self.groups)
+
+
+def _compact(flags, select_zero=False):
+    """Ascending positions of the set (or, with select_zero, clear) flags."""
+    n = flags.numel()
+    dev = flags.device
+    lib = _lib.load()
+    ws_bytes = int(lib.vc_compact_workspace(n))
+    ws = torch.empty(max(ws_bytes, 8), dtype=torch.uint8, device=dev)
+    idx = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
+    cnt = torch.empty(1, dtype=torch.int64, device=dev)
+    call('vc_compact', ptr(flags), n, 1 if select_zero else 0, ptr(idx),
+         ptr(cnt), ptr(ws), ws_bytes, stream())
+    return idx[:int(cnt.item())]
+
+
+def _gather(t, idx):
+    """Rows t[idx] (any trailing shape), by the HIP row gather."""
+    n = idx.numel()
+    cols = 1
+    for s in t.shape[1:]:
+        cols *= s
+    out = torch.empty((n,) + tuple(t.shape[1:]), dtype=t.dtype, device=t.device)
+    if n > 0:
+        call('vc_gather_rows', ptr(f32(t)), ptr(idx), n, cols, ptr(out),
+             stream())
+    return out
+
+
+def _closure(lb, table):
+    B, Q = lb.shape
+    closed = torch.empty(B, dtype=torch.bool, device=lb.device)
+    if B > 0:
+        call('vc_closure', ptr(lb.contiguous()), B, Q, ptr(table.d_ptr),
+             ptr(table.q_idx), table.n, ptr(closed), stream())
+    return closed
+
+
+def _clip(xl, xh, A, b, table):
+    B, Q, n = A.shape
+    xl_o = torch.empty_like(xl)
+    xh_o = torch.empty_like(xh)
+    feas = torch.empty(B, dtype=torch.bool, device=xl.device)
+    if B > 0:
+        call('vc_clip_box', ptr(xl), ptr(xh), ptr(A.contiguous()),
+             ptr(b.contiguous()), B, Q, n, ptr(table.d_ptr), ptr(table.q_idx),
+             table.n, ptr(xl_o), ptr(xh_o), ptr(feas), stream())
+    return xl_o, xh_o, feas
+
+
+def _clip_box_by_halfspaces_batched(xl, xh, A, b):
+    """Bounding box of {x in [xl, xh] : A_q.x + b_q <= 0 for all q}
+    (verify_graph.py:12363-12426).  Returns (xl', xh', feasible)."""
+    xl, xh, A, b = f32(xl), f32(xh), f32(A), f32(b)
+    Q = A.shape[1]
+    table = DisjunctTable({0: list(range(Q))}, xl.device)
+    return _clip(xl, xh, A, b, table)
+
+
+def _widest_and_bisect(xl, xh):
+    """Widest-axis split of every leaf: returns (n_degenerate, ax, low, high)
+    (verify_graph.py:13291, 13366-13382)."""
+    B, n = xl.shape
+    dev = xl.device
+    ax = torch.empty(B, dtype=torch.int64, device=dev)
+    usable = torch.empty(B, dtype=torch.bool, device=dev)
+    if B == 0:
+        e = xl[:0]
+        return 0, ax, (e, e), (e, e)
+    call('vc_widest_axis', ptr(xl), ptr(xh), B, n, ptr(ax), ptr(usable),
+         stream())
+    u = _compact(usable)
+    nu = u.numel()
+    low_xl = torch.empty(nu, n, device=dev)
+    low_xh = torch.empty_like(low_xl)
+    high_xl = torch.empty_like(low_xl)
+    high_xh = torch.empty_like(low_xl)
+    if nu > 0:
+        call('vc_bisect', ptr(xl), ptr(xh), ptr(ax), ptr(u), nu, n,
+             ptr(low_xl), ptr(low_xh), ptr(high_xl), ptr(high_xh), stream())
+    return B - nu, ax, (low_xl, low_xh), (high_xl, high_xh)
+
+
+class ChunkWorklist:
+    """LIFO worklist of device-resident 2-D chunks
+    (verify_graph.py:12695-12726)."""
+
+    def __init__(self, xl0, xh0):
+        self.xl = [xl0.reshape(1, -1)]
+        self.xh = [xh0.reshape(1, -1)]
+
+    def size(self):
+        return sum(int(c.shape[0]) for c in self.xl)
+
+    def push(self, xl, xh):
+        self.xl.append(xl)
+        self.xh.append(xh)
+
+    def pop(self, n):
+        got = 0
+        pl, ph = [], []
+        while got < n:
+            cl, ch = self.xl[-1], self.xh[-1]
+            m = int(cl.shape[0])
+            if got + m <= n:
+                pl.append(cl)
+                ph.append(ch)
+                self.xl.pop()
+                self.xh.pop()
+                got += m
+            else:
+                need = n - got
+                pl.append(cl[-need:])
+                ph.append(ch[-need:])
+                self.xl[-1] = cl[:-need]
+                self.xh[-1] = ch[:-need]
+                got = n
+        if len(pl) == 1:
+            return pl[0].contiguous(), ph[0].contiguous()
+        return torch.cat(pl, 0), torch.cat(ph, 0)
+
+    def __bool__(self):
+        return bool(self.xl)
+
+
+def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
+             clip_enabled=True, alpha_iters=0, alpha_all=False, alpha_eps=0.0,
+             alpha_max_leaves=200, alpha_lr=0.25, alpha_lr_decay=0.98,
+             timers=None):
+    """One BaB iteration on a popped batch (verify_graph.py:12855-13382):
+    bound, closure, optional alpha-CROWN on unclosed leaves, one clip
+    iteration, widest-axis bisection.  Returns a dict of device tensors
+    (same keys as the oracle's bab_step)."""
+    dev = xl.device
+    dt = torch.float32
+    sync_t = (lambda: (torch.cuda.synchronize(), time.perf_counter())[1]) \
+        if timers is not None else None
+    if timers is not None:
+        t0 = sync_t()
+    if crown_intermediate:
+        sb = _crown_intermediate_batched(gg, xl, xh, dev, dt)
+    else:
+        sb, _ = _forward_zonotope_graph_batched(xl, xh, gg, dev, dt)
+    if clip_enabled:
+        lb, A, acc = _spec_backward_graph_batched(sb, xl, xh, gg, spec_ew, dev,
+                                                  dt, return_input_linear=True)
+    else:
+        lb = _spec_backward_graph_batched(sb, xl, xh, gg, spec_ew, dev, dt)
+        A = acc = None
+    lb = lb.contiguous()
+    closed = _closure(lb, table)
+    n_al = n_ait = 0
+    if timers is not None:
+        t1 = sync_t()
+        timers['bound'] = timers.get('bound', 0.0) + t1 - t0
+        t0 = t1
+    if alpha_iters > 0 and (alpha_all or alpha_eps > 0):
+        open_idx = _compact(closed, select_zero=True)
+        if open_idx.numel() > 0:
+            if not alpha_all:
+                raise NotImplementedError(
+                    'vibecheck_amd: boundary-band alpha selection '
+                    '(alpha_all=False) is not supported')
+            new, n_ait = _run_alpha_crown_inputsplit_batched(
+                _gather(xl, open_idx), _gather(xh, open_idx), gg, spec_ew,
+                dev, dt, n_iters=alpha_iters, lr=alpha_lr,
+                lr_decay=alpha_lr_decay, return_trace=True)
+            n_al = int(open_idx.numel())
+            call('vc_scatter_max_rows', ptr(lb), ptr(open_idx),
+                 ptr(new.contiguous()), n_al, lb.shape[1], stream())
+            closed = _closure(lb, table)
+    if timers is not None:
+        t1 = sync_t()
+        timers['alpha'] = timers.get('alpha', 0.0) + t1 - t0
+        t0 = t1
+    unclosed = _compact(closed, select_zero=True)
+    out = {'lb': lb, 'A': A, 'acc': acc, 'closed': closed,
+           'unclosed': unclosed, 'n_alpha_leaves': n_al,
+           'n_alpha_iters': n_ait}
+    if clip_enabled and unclosed.numel() > 0 and A is not None:
+        xl_u, xh_u = _gather(xl, unclosed), _gather(xh, unclosed)
+        xl_c, xh_c, feas = _clip(xl_u, xh_u, _gather(A, unclosed),
+                                 _gather(acc, unclosed), table)
+        fidx = _compact(feas)
+        out['feasible'] = feas
+        xl_s, xh_s = _gather(xl_c, fidx), _gather(xh_c, fidx)
+    else:
+        out['feasible'] = None
+        xl_s, xh_s = _gather(xl, unclosed), _gather(xh, unclosed)
+    if timers is not None:
+        t1 = sync_t()
+        timers['clip'] = timers.get('clip', 0.0) + t1 - t0
+        t0 = t1
+    out['xl_split'], out['xh_split'] = xl_s, xh_s
+    n_deg, ax, low, high = _widest_and_bisect(xl_s, xh_s)
+    out.update(ax=ax, n_degenerate=n_deg, low=low, high=high)
+    if timers is not None:
+        timers['split'] = timers.get('split', 0.0) + sync_t() - t0
+    return out
+
+
+def _setting(settings, name, default):
+    if settings is None:
+        return default
+    if isinstance(settings, dict):
+        return settings.get(name, default)
+    return getattr(settings, name, default)
+
+
+def _input_split_batched(graph, spec, settings, gg, device, dtype):
+    """Worklist input-split BaB with batched leaf evaluation
+    (verify_graph.py:12466-13464).
+
+    Returns (verdict in {'verified', 'unknown'}, details).  Knobs read from
+    ``settings`` (attribute or dict): total_timeout, input_split_batch_size,
+    input_split_batched_max_worklist, input_split_batched_clip_enabled,
+    input_split_crown_intermediate, input_split_batched_alpha_iters,
+    input_split_batched_alpha_all_leaves, input_split_batched_alpha_lr
+    (extension; reference hard-codes 0.25), input_split_batched_max_iters
+    (extension: stop after that many iterations).
+    """
+    if dtype != torch.float32:
+        raise NotImplementedError('vibecheck_amd computes in fp32 only')
+    t_start = time.perf_counter()
+    total_budget = float(_setting(settings, 'total_timeout', 60.0))
+    batch_size = int(_setting(settings, 'input_split_batch_size', 4096))
+    max_worklist = int(_setting(settings,
+                                'input_split_batched_max_worklist', 200_000))
+    clip_enabled = bool(_setting(settings,
+                                 'input_split_batched_clip_enabled', True))
+    crown_int = bool(_setting(settings, 'input_split_crown_intermediate',
+                              False))
+    alpha_iters = int(_setting(settings, 'input_split_batched_alpha_iters', 0))
+    alpha_all = bool(_setting(settings,
+                              'input_split_batched_alpha_all_leaves', False))
+    alpha_eps = float(_setting(settings,
+                               'input_split_batched_alpha_boundary_eps', 0.0))
+    alpha_lr = float(_setting(settings, 'input_split_batched_alpha_lr', 0.25))
+    max_iters = _setting(settings, 'input_split_batched_max_iters', None)
+    dev = torch.device(device)
+
+    xc = ((torch.as_tensor(spec.x_lo, dtype=dtype, device=dev)
+           + torch.as_tensor(spec.x_hi, dtype=dtype, device=dev)) / 2
+          ).reshape(1, -1)
+    _, (c_probe, _) = _forward_zonotope_graph_batched(xc, xc, gg, dev, dtype)
+    n_output = int(c_probe.shape[-1])
+    queries = spec.as_linear_queries(n_output)
+    if not queries:
+        return 'verified', {'phase': 'batched_no_queries'}
+    uniq, disj_q_idx = dedup_queries(queries)
+    spec_ew = {pos: (torch.as_tensor(w, dtype=dtype, device=dev), b)
+               for pos, (w, b) in enumerate(uniq)}
+    table = DisjunctTable(disj_q_idx, dev)
+
+    xl0 = torch.as_tensor(spec.x_lo, dtype=dtype, device=dev).flatten()
+    xh0 = torch.as_tensor(spec.x_hi, dtype=dtype, device=dev).flatten()
+    wl = ChunkWorklist(xl0, xh0)
+    n_leaves = n_iters = n_open = 0
+    while wl:
+        if max_iters is not None and n_iters >= int(max_iters):
+            break
+        wl_n = wl.size()
+        if time.perf_counter() - t_start > total_budget - 0.5:
+            n_open = wl_n
+            break
+        B = min(batch_size, wl_n)
+        xl_b, xh_b = wl.pop(B)
+        try:
+            st = bab_step(xl_b, xh_b, gg, spec_ew, table, crown_int,
+                          clip_enabled, alpha_iters, alpha_all, alpha_eps,
+                          alpha_lr=alpha_lr)
+        except torch.cuda.OutOfMemoryError:
+            new_bs = max(1, batch_size // 2)
+            if new_bs == batch_size:
+                if bool(_setting(settings, 'raise_on_oom', True)):
+                    raise
+                return 'unknown', {'phase': 'batched_oom',
+                                   'batch_size': batch_size}
+            wl.push(xl_b, xh_b)
+            batch_size = new_bs
+            continue
+        n_leaves += B
+        n_open += st['n_degenerate']
+        low, high = st['low'], st['high']
+        if low[0].shape[0] > 0:
+            wl.push(*low)
+            wl.push(*high)
+        n_iters += 1
+        if wl.size() > max_worklist:
+            return 'unknown', {'phase': 'batched_worklist_overflow',
+                               'batched_n_leaves': n_leaves,
+                               'batched_n_iters': n_iters,
+                               'worklist_size': wl.size()}
+    if not wl and n_open == 0:
+        return 'verified', {'phase': 'batched_verified',
+                            'batched_n_leaves': n_leaves,
+                            'batched_n_iters': n_iters,
+                            'batched_batch_size': batch_size}
+    return 'unknown', {'phase': 'batched_timeout',
+                       'batched_n_leaves': n_leaves,
+                       'batched_n_iters': n_iters,
+                       'batched_worklist_left': wl.size(),
+                       'batched_open_degenerate': n_open,
+                       'batched_batch_size': batch_size}

@@ -1,0 +1,643 @@
+"""Batched bound primitives on the GPU (HIP library), with the reference's
+function names and signatures (verify_zono_bnb.py of the reference).
+
+Every function takes the reference's ``gg`` dict (fc / relu / conv /
+reshape ops) and fp32 GPU tensors, computes with the kernels of
+libvibecheck_amd.so, and returns new tensors.  Unsupported ops raise
+NotImplementedError, fp64 raises NotImplementedError, CPU tensors raise
+RuntimeError: there is no other compute path.
+"""
+import torch
+
+from . import _lib
+from ._lib import call, f32, ptr, stream
+
+__all__ = ['_make_slopes', '_ibp_forward_graph_batched',
+           '_forward_zonotope_graph_batched', '_crown_intermediate_batched',
+           '_spec_backward_graph_batched',
+           '_run_alpha_crown_inputsplit_batched']
+
+
+def _check_dtype(dtype):
+    if dtype is not None and dtype != torch.float32:
+        raise NotImplementedError(
+            f'vibecheck_amd computes in fp32 only, got {dtype}')
+
+
+# --------------------------------------------------------------------------
+# Device copies of the network parameters, cached on the gg dict
+# --------------------------------------------------------------------------
+
+def _op_params(op, device):
+    """fp32 contiguous device copies of an op's tensors (cached on the op,
+    like the reference caches converted biases on op dicts,
+    verify_zono_bnb.py:4482-4486)."""
+    key = '_vc_amd_params'
+    cached = op.get(key)
+    if cached is not None and cached['device'] == device:
+        return cached
+    p = {'device': device}
+    if op['type'] == 'fc':
+        p['W'] = op['W'].detach().to(device=device, dtype=torch.float32).contiguous()
+        b = op.get('bias')
+        p['b'] = (None if b is None else
+                  torch.as_tensor(b).detach().to(device=device, dtype=torch.float32)
+                  .reshape(-1).contiguous())
+        p['n_out'], p['n_in'] = p['W'].shape
+    elif op['type'] == 'conv':
+        k = op['kernel'].detach().to(device=device, dtype=torch.float32).contiguous()
+        if k.dim() != 4:
+            raise NotImplementedError('vibecheck_amd: conv kernels must be 4-D')
+        p['K'] = k
+        b = op.get('bias')
+        p['b'] = (None if b is None else
+                  torch.as_tensor(b).detach().to(device=device, dtype=torch.float32)
+                  .reshape(-1).contiguous())
+        C_in, H, W = op['in_shape']
+        C_out, Ho, Wo = op['out_shape']
+        kh, kw = k.shape[2], k.shape[3]
+        sh, sw = _pair(op['stride'])
+        ph, pw = _pair(op['padding'])
+        p['geom'] = (C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, Ho, Wo)
+        p['n_in'] = C_in * H * W
+        p['n_out'] = C_out * Ho * Wo
+    op[key] = p
+    return p
+
+
+def _pair(v):
+    if isinstance(v, int):
+        return v, v
+    v = tuple(int(x) for x in v)
+    return (v[0], v[0]) if len(v) == 1 else (v[0], v[1])
+
+
+def _unsupported(fn, op):
+    raise NotImplementedError(
+        f'{fn}: unsupported op {op["type"]!r} at {op["name"]!r} -- silently '
+        f'skipping would certify unsound bounds')
+
+
+# --------------------------------------------------------------------------
+# a1: ReLU relaxation
+# --------------------------------------------------------------------------
+
+def _make_slopes(lo, hi):
+    """CROWN adaptive slopes (verify_zono_bnb.py:503-522).
+
+    Returns (lo_s, up_s, up_t, active, dead, unstable) like the reference.
+    """
+    lo, hi = f32(lo), f32(hi)
+    if lo.shape != hi.shape:
+        raise ValueError('lo/hi shape mismatch')
+    outs = [torch.empty_like(lo) for _ in range(3)]
+    masks = [torch.empty(lo.shape, dtype=torch.bool, device=lo.device)
+             for _ in range(3)]
+    call('vc_make_slopes', ptr(lo), ptr(hi), lo.numel(),
+         *[ptr(t) for t in outs], *[ptr(t) for t in masks], stream())
+    return (*outs, *masks)
+
+
+# --------------------------------------------------------------------------
+# a2: IBP forward
+# --------------------------------------------------------------------------
+
+def _ibp_forward_graph_batched(xl, xh, gg, device, dtype, relu_clamps=None,
+                               root_sb=None):
+    """Batched interval forward (verify_zono_bnb.py:1066-1153).
+
+    Returns {layer_idx: (lo, hi)} of (B, n_L) pre-activation bounds after
+    root intersection, split clamps and crossing repair.
+    """
+    _check_dtype(dtype)
+    xl, xh = f32(xl), f32(xh)
+    B = xl.shape[0]
+    dev = xl.device
+    lo = {gg['input_name']: xl}
+    hi = {gg['input_name']: xh}
+    sb = {}
+    st = stream()
+    for op in gg['ops']:
+        t = op['type']
+        name = op['name']
+        l, h = lo[op['inputs'][0]], hi[op['inputs'][0]]
+        if t == 'fc':
+            p = _op_params(op, dev)
+            lo_o = torch.empty(B, p['n_out'], device=dev)
+            hi_o = torch.empty_like(lo_o)
+            call('vc_ibp_fc', ptr(l), ptr(h), B, p['n_in'], ptr(p['W']),
+                 ptr(p['b']), p['n_out'], ptr(lo_o), ptr(hi_o), st)
+            lo[name], hi[name] = lo_o, hi_o
+        elif t == 'conv':
+            p = _op_params(op, dev)
+            C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, Ho, Wo = p['geom']
+            lo_o = torch.empty(B, p['n_out'], device=dev)
+            hi_o = torch.empty_like(lo_o)
+            call('vc_ibp_conv', ptr(l), ptr(h), B, C_in, H, W, ptr(p['K']),
+                 ptr(p['b']), C_out, kh, kw, sh, sw, ph, pw, Ho, Wo,
+                 ptr(lo_o), ptr(hi_o), st)
+            lo[name], hi[name] = lo_o, hi_o
+        elif t == 'relu':
+            L = op.get('layer_idx')
+            n = l.shape[1]
+            rlo = rhi = cl = ch = None
+            if L is not None and root_sb is not None and L in root_sb:
+                rlo = f32(root_sb[L][0]).reshape(-1)
+                rhi = f32(root_sb[L][1]).reshape(-1)
+            if L is not None and relu_clamps is not None and L in relu_clamps:
+                cl = f32(relu_clamps[L][0])
+                ch = f32(relu_clamps[L][1])
+            sl = torch.empty_like(l)
+            sh_ = torch.empty_like(l)
+            pl = torch.empty_like(l)
+            ph_ = torch.empty_like(l)
+            call('vc_ibp_relu', ptr(l), ptr(h), B, n, ptr(rlo), ptr(rhi),
+                 ptr(cl), ptr(ch), ptr(sl), ptr(sh_), ptr(pl), ptr(ph_), st)
+            if L is not None:
+                sb[L] = (sl, sh_)
+            lo[name], hi[name] = pl, ph_
+        elif t == 'reshape':
+            lo[name], hi[name] = l, h
+        else:
+            raise NotImplementedError(
+                f'_ibp_forward_graph_batched: unsupported op {t!r} at '
+                f'{name!r} -- silently skipping would certify unsound bounds')
+    return sb
+
+
+# --------------------------------------------------------------------------
+# a3: zonotope forward
+# --------------------------------------------------------------------------
+
+def _forward_zonotope_graph_batched(xl, xh, gg, device, dtype):
+    """Batched zonotope forward (verify_zono_bnb.py:3079-4075, fc/relu/conv/
+    reshape).  Returns (sb, (c, G)); G is (B, n, K) with the new generator
+    columns of each ReLU padded to the batch maximum, as in the reference.
+    """
+    _check_dtype(dtype)
+    xl, xh = f32(xl), f32(xh)
+    B, n_in = xl.shape
+    dev = xl.device
+    st = stream()
+    varying = ((xh - xl) / 2).abs().amax(dim=0) > 0 if B > 0 else \
+        torch.zeros(n_in, dtype=torch.bool, device=dev)
+    vidx = varying.nonzero(as_tuple=True)[0].to(torch.int32).contiguous()
+    K = int(vidx.numel())
+    c = torch.empty(B, n_in, device=dev)
+    G = torch.empty(B, n_in, K, device=dev)
+    call('vc_zono_input', ptr(xl), ptr(xh), B, n_in, ptr(vidx), K, ptr(c),
+         ptr(G), st)
+    state = {gg['input_name']: (c, G)}
+    sb = {}
+    for op in gg['ops']:
+        t = op['type']
+        name = op['name']
+        c_in, G_in = state[op['inputs'][0]]
+        Kc = G_in.shape[2]
+        if t == 'fc':
+            p = _op_params(op, dev)
+            c_o = torch.empty(B, p['n_out'], device=dev)
+            G_o = torch.empty(B, p['n_out'], Kc, device=dev)
+            call('vc_zono_fc', ptr(c_in), ptr(G_in), B, p['n_in'], Kc,
+                 ptr(p['W']), ptr(p['b']), p['n_out'], ptr(c_o), ptr(G_o), st)
+            state[name] = (c_o, G_o)
+        elif t == 'conv':
+            p = _op_params(op, dev)
+            C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, Ho, Wo = p['geom']
+            c_o = torch.empty(B, p['n_out'], device=dev)
+            G_o = torch.empty(B, p['n_out'], Kc, device=dev)
+            call('vc_zono_conv', ptr(c_in), ptr(G_in), B, Kc, C_in, H, W,
+                 ptr(p['K']), ptr(p['b']), C_out, kh, kw, sh, sw, ph, pw, Ho,
+                 Wo, ptr(c_o), ptr(G_o), st)
+            state[name] = (c_o, G_o)
+        elif t == 'relu':
+            n = c_in.shape[1]
+            lo = torch.empty(B, n, device=dev)
+            hi = torch.empty_like(lo)
+            rank = torch.empty(B, n, dtype=torch.int32, device=dev)
+            cnt = torch.empty(B, dtype=torch.int32, device=dev)
+            call('vc_zono_relu_bounds', ptr(c_in), ptr(G_in), B, n, Kc,
+                 ptr(lo), ptr(hi), ptr(rank), ptr(cnt), st)
+            k_new = int(cnt.max().item()) if B > 0 else 0
+            c_o = torch.empty(B, n, device=dev)
+            G_o = torch.empty(B, n, Kc + k_new, device=dev)
+            call('vc_zono_relu_apply', ptr(c_in), ptr(G_in), ptr(lo), ptr(hi),
+                 ptr(rank), B, n, Kc, k_new, ptr(c_o), ptr(G_o), st)
+            state[name] = (c_o, G_o)
+            if 'layer_idx' in op:
+                sb[op['layer_idx']] = (lo, hi)
+        elif t == 'reshape':
+            state[name] = (c_in, G_in)
+        else:
+            raise ValueError(f'batched zono forward: unknown op type {t!r}')
+    _forward_zonotope_graph_batched.last_bilinear_op_bounds = {}
+    return sb, state[gg['ops'][-1]['name']]
+
+
+# --------------------------------------------------------------------------
+# a5-a8: CROWN backward + concretization
+# --------------------------------------------------------------------------
+
+class _Rows:
+    """Backward coefficient rows at one graph node.
+
+    ``ew`` is (R, n) when ``shared`` (identical for every domain, before the
+    first per-domain relaxation) else (B*R, n).  ``relu`` names a relu layer
+    whose relaxation is still to be applied (it is fused into the next fc).
+    ``alpha``/``beta`` belong to that pending relu.
+    """
+    __slots__ = ('ew', 'shared', 'relu', 'alpha', 'alpha_row', 'beta')
+
+    def __init__(self, ew, shared):
+        self.ew = ew
+        self.shared = shared
+        self.relu = None
+        self.alpha = None
+        self.alpha_row = 0
+        self.beta = None
+
+
+class BackwardTrace:
+    """Per-relu stored pre-relaxation rows of one backward, for the alpha
+    gradient sweep: entries (L, P, p_shared) in backward order."""
+
+    def __init__(self):
+        self.relus = []
+        self.fcs = []
+
+
+def _expand_rows(t, B):
+    """(R, n) shared rows -> (B*R, n) per-domain rows."""
+    R, n = t.shape
+    return t.unsqueeze(0).expand(B, R, n).reshape(B * R, n).contiguous()
+
+
+def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
+              alpha_at_layer=None, relu_split_beta=None, trace=None):
+    """Walk the ops backward from ``seed_name`` and concretize.
+
+    seed: (R, n) rows when ``seed_shared`` else (B*R, n); acc0: (R,) when
+    shared else (B*R,).  Returns (lb (B, R), A, a_shared, acc (B*R,)).
+    """
+    B, n_in = xl.shape
+    dev = xl.device
+    st = stream()
+    R = seed.shape[0] if seed_shared else seed.shape[0] // max(B, 1)
+    acc = acc0.clone()
+    acc_shared = seed_shared
+    ew_at = {seed_name: _Rows(seed, seed_shared)}
+    ops = gg['ops']
+
+    def per_domain_acc():
+        nonlocal acc, acc_shared
+        if acc_shared:
+            acc = acc.unsqueeze(0).expand(B, R).reshape(B * R).contiguous()
+            acc_shared = False
+
+    def materialize(rows):
+        """Apply a pending relu relaxation with the standalone kernel."""
+        if rows.relu is None:
+            return rows
+        L = rows.relu
+        lo, hi = tight[L]
+        lo, hi = f32(lo), f32(hi)
+        n = lo.shape[1]
+        ew = _expand_rows(rows.ew, B) if rows.shared else rows.ew
+        per_domain_acc()
+        if trace is not None:
+            trace.relus.append((L, rows.ew, rows.shared))
+        out = torch.empty(B * R, n, device=dev)
+        call('vc_backward_relu', ptr(ew), B * R, R, n, ptr(lo), ptr(hi),
+             ptr(rows.alpha), rows.alpha_row, ptr(rows.beta), ptr(out),
+             ptr(acc), st)
+        return _Rows(out, False)
+
+    for op in reversed(ops):
+        name = op['name']
+        if name not in ew_at:
+            continue
+        rows = ew_at.pop(name)
+        t = op['type']
+        inp = op['inputs'][0]
+        if inp in ew_at:
+            raise NotImplementedError(
+                'vibecheck_amd: fan-in (skip connections) is not supported')
+        if t == 'fc':
+            p = _op_params(op, dev)
+            if rows.relu is not None:
+                L = rows.relu
+                lo, hi = f32(tight[L][0]), f32(tight[L][1])
+                per_domain_acc()
+                M = B * R
+                out = torch.empty(M, p['n_in'], device=dev)
+                if trace is not None:
+                    trace.relus.append((L, rows.ew, rows.shared))
+                    trace.fcs.append(op)
+                call('vc_backward_fc', ptr(rows.ew), M, R, p['n_out'],
+                     ptr(lo), ptr(hi), ptr(rows.alpha), rows.alpha_row,
+                     ptr(rows.beta), ptr(p['W']), ptr(p['b']), p['n_in'],
+                     ptr(out), ptr(acc), None, 1 if rows.shared else 0, st)
+                ew_at[inp] = _Rows(out, False)
+            else:
+                if not rows.shared:
+                    per_domain_acc()
+                M = R if rows.shared else B * R
+                out = torch.empty(M, p['n_in'], device=dev)
+                if trace is not None:
+                    trace.fcs.append(op)
+                call('vc_backward_fc', ptr(rows.ew), M, R, p['n_out'], None,
+                     None, None, 0, None, ptr(p['W']), ptr(p['b']),
+                     p['n_in'], ptr(out), ptr(acc), None, 0, st)
+                ew_at[inp] = _Rows(out, rows.shared)
+        elif t == 'relu':
+            if 'layer_idx' in op:
+                rows = materialize(rows)
+                L = op['layer_idx']
+                rows.relu = L
+                if alpha_at_layer is not None and L in alpha_at_layer:
+                    a = f32(alpha_at_layer[L])
+                    if a.dim() == 3:
+                        rows.alpha = a.reshape(B * R, -1)
+                        rows.alpha_row = 1
+                    else:
+                        rows.alpha = a
+                        rows.alpha_row = 0
+                if relu_split_beta is not None and L in relu_split_beta:
+                    rows.beta = f32(relu_split_beta[L])
+            ew_at[inp] = rows
+        elif t == 'conv':
+            rows = materialize(rows)
+            p = _op_params(op, dev)
+            C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, Ho, Wo = p['geom']
+            if not rows.shared:
+                per_domain_acc()
+            M = R if rows.shared else B * R
+            out = torch.empty(M, p['n_in'], device=dev)
+            call('vc_backward_conv', ptr(rows.ew), M, ptr(p['K']),
+                 ptr(p['b']), C_out, Ho, Wo, C_in, H, W, kh, kw, sh, sw, ph,
+                 pw, ptr(out), ptr(acc), st)
+            ew_at[inp] = _Rows(out, rows.shared)
+        elif t == 'reshape':
+            ew_at[inp] = rows
+        else:
+            raise ValueError(f'batched spec backward: unknown op {t!r}')
+
+    rows = ew_at.get(gg['input_name'])
+    if rows is None:
+        per_domain_acc()
+        return acc.reshape(B, R).clone(), None, False, acc
+    rows = materialize(rows)
+    A = rows.ew
+    per_domain_acc()
+    lb = torch.empty(B * R, device=dev)
+    call('vc_concretize', ptr(A), ptr(acc), ptr(xl), ptr(xh), B * R, R, n_in,
+         1 if rows.shared else 0, ptr(lb), st)
+    return lb.reshape(B, R), A, rows.shared, acc
+
+
+def _spec_rows(spec_ew, dev):
+    qids = sorted(spec_ew.keys())
+    Wq = torch.stack([torch.as_tensor(spec_ew[q][0]).reshape(-1)
+                      .to(device=dev, dtype=torch.float32) for q in qids])
+    bq = torch.tensor([float(spec_ew[q][1]) for q in qids],
+                      dtype=torch.float32, device=dev)
+    return Wq.contiguous(), bq
+
+
+def _spec_backward_graph_batched(tight, xl, xh, gg, spec_ew, device, dtype,
+                                 return_input_linear=False,
+                                 alpha_at_layer=None, relu_split_beta=None,
+                                 alpha_mccormick=None, alpha_recip=None,
+                                 bilinear_op_bounds=None, seed_ew_at=None,
+                                 seed_acc=None):
+    """Batched CROWN spec backward + concretization
+    (verify_zono_bnb.py:4270-5134; fc/relu/conv/reshape ops).
+
+    Returns lb (B, Q), or (lb, A (B, Q, n_in), acc (B, Q)) with
+    ``return_input_linear``.
+    """
+    _check_dtype(dtype)
+    if alpha_mccormick or alpha_recip or bilinear_op_bounds:
+        raise NotImplementedError(
+            'vibecheck_amd: bilinear / reciprocal relaxations are not '
+            'supported (Linear/Conv/ReLU networks only)')
+    xl, xh = f32(xl), f32(xh)
+    B, n_in = xl.shape
+    dev = xl.device
+    if seed_ew_at is not None:
+        if len(seed_ew_at) != 1:
+            raise NotImplementedError('vibecheck_amd: one seed node only')
+        seed_name, seed = next(iter(seed_ew_at.items()))
+        Q = seed.shape[1]
+        if seed.dim() == 3 and seed.stride(0) == 0:
+            rows, shared = f32(seed[0]).contiguous(), True
+        else:
+            rows, shared = f32(seed).reshape(B * Q, -1).contiguous(), False
+        if seed_acc is None:
+            acc0 = torch.zeros(Q if shared else B * Q, device=dev)
+        else:
+            sa = f32(seed_acc)
+            if shared and sa.stride(0) == 0:
+                acc0 = sa[0].contiguous().clone()
+            else:
+                if shared:
+                    rows, shared = _expand_rows(rows, B), False
+                acc0 = sa.reshape(B * Q).contiguous().clone()
+    else:
+        rows, acc0 = _spec_rows(spec_ew, dev)
+        seed_name, shared = gg['ops'][-1]['name'], True
+        Q = rows.shape[0]
+    lb, A, a_shared, acc = _backward(tight, xl, xh, gg, seed_name, rows,
+                                     shared, acc0, alpha_at_layer,
+                                     relu_split_beta)
+    if not return_input_linear:
+        return lb
+    if A is None:
+        return lb, torch.zeros(B, Q, n_in, device=dev), acc.reshape(B, Q)
+    if a_shared:
+        A = A.unsqueeze(0).expand(B, Q, n_in).contiguous()
+    else:
+        A = A.reshape(B, Q, n_in)
+    return lb, A, acc.reshape(B, Q)
+
+
+# --------------------------------------------------------------------------
+# a4: CROWN intermediate bounds
+# --------------------------------------------------------------------------
+
+def _crown_intermediate_batched(gg, xl, xh, device, dtype, chunk=2048,
+                                sb=None):
+    """Backward-CROWN intermediate pre-ReLU bounds
+    (verify_zono_bnb.py:4077-4147).
+
+    For each ReLU layer L in ascending order: seed [+I; -I] at L's input for
+    the neurons unstable in ANY domain of the batch, in chunks of ``chunk``,
+    propagate through the already-tightened earlier layers and intersect.
+    The seeded rows are identical for every domain until the first ReLU, so
+    that prefix is computed once (R rows) and broadcast.  ``sb`` (extension)
+    replaces the zonotope starting bounds, e.g. by IBP bounds.
+    """
+    _check_dtype(dtype)
+    xl, xh = f32(xl), f32(xh)
+    dev = xl.device
+    if sb is None:
+        sb, _ = _forward_zonotope_graph_batched(xl, xh, gg, device, dtype)
+    tight = {L: (f32(lo).clone(), f32(hi).clone()) for L, (lo, hi) in sb.items()}
+    relu_by_L = {op['layer_idx']: op for op in gg['ops']
+                 if op['type'] == 'relu' and 'layer_idx' in op}
+    B = xl.shape[0]
+    st = stream()
+    ch = max(1, int(chunk))
+    for L in sorted(tight):
+        if L not in relu_by_L:
+            continue
+        feed = relu_by_L[L]['inputs'][0]
+        lo_L, hi_L = tight[L]
+        n = lo_L.shape[1]
+        flag = torch.empty(n, dtype=torch.uint8, device=dev)
+        call('vc_unstable_union', ptr(lo_L), ptr(hi_L), B, n, ptr(flag), st)
+        idx = flag.nonzero(as_tuple=True)[0].to(torch.int32)
+        m = int(idx.numel())
+        if m == 0:
+            continue
+        new_lo, new_hi = lo_L.clone(), hi_L.clone()
+        for c0 in range(0, m, ch):
+            cidx = idx[c0:c0 + ch].contiguous()
+            k = int(cidx.numel())
+            seed = torch.zeros(2 * k, n, device=dev)
+            ar = torch.arange(k, device=dev)
+            seed[ar, cidx.long()] = 1.0
+            seed[ar + k, cidx.long()] = -1.0
+            acc0 = torch.zeros(2 * k, device=dev)
+            sl, _, _, _ = _backward(tight, xl, xh, gg, feed, seed, True, acc0)
+            sl = sl.contiguous()
+            call('vc_crown_intersect', ptr(sl), ptr(cidx), k, B, n,
+                 ptr(new_lo), ptr(new_hi), st)
+        tight[L] = (new_lo, new_hi)
+    return tight
+
+
+# --------------------------------------------------------------------------
+# a9: alpha-CROWN
+# --------------------------------------------------------------------------
+
+def _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, want_grad, galpha):
+    """One alpha-CROWN evaluation: lb (B, Q); when ``want_grad`` also fills
+    ``galpha[L]`` with d(sum lb)/d alpha_L (the autograd of the reference's
+    backward, torch clamp subgradients included)."""
+    B, n_in = xl.shape
+    Q = Wq.shape[0]
+    dev = xl.device
+    st = stream()
+    trace = BackwardTrace() if want_grad else None
+    lb, A, a_shared, _ = _backward(sb, xl, xh, gg, gg['ops'][-1]['name'], Wq,
+                                   True, bq, alpha, None, trace)
+    if not want_grad:
+        return lb
+    if A is None or a_shared:
+        raise NotImplementedError('vibecheck_amd: alpha gradient needs a relu')
+    # trace.relus: (L, P, shared) in backward order (top relu first);
+    # trace.fcs: fc ops in backward order.  Sequential fc/relu nets only:
+    # fcs[i] sits below relus[i-1] ... check the chain shape.
+    relus = trace.relus
+    fcs = trace.fcs
+    if len(fcs) != len(relus) + 1:
+        raise NotImplementedError(
+            'vibecheck_amd: alpha-CROWN gradient supports fc/relu chains')
+    M = B * Q
+    # input side: gE_0 = gA W_0^T + b_0, W_0 = fcs[-1]
+    f0 = _op_params(fcs[-1], dev)
+    g = torch.empty(M, f0['n_out'], device=dev)
+    call('vc_alpha_grad_input', ptr(A), ptr(xl), ptr(xh), M, Q, n_in,
+         ptr(f0['W']), ptr(f0['b']), f0['n_out'], ptr(g), st)
+    for i in range(len(relus) - 1, -1, -1):
+        L, P, p_shared = relus[i]
+        lo, hi = f32(sb[L][0]), f32(sb[L][1])
+        n = lo.shape[1]
+        a = f32(alpha[L]) if (alpha is not None and L in alpha) else None
+        if galpha is not None and L in galpha:
+            call('vc_alpha_grad_reduce', ptr(g), ptr(P), 1 if p_shared else 0,
+                 B, Q, n, ptr(lo), ptr(hi), ptr(galpha[L]), None, st)
+        if i > 0:
+            fn = _op_params(fcs[i], dev)
+            g2 = torch.empty(M, fn['n_out'], device=dev)
+            call('vc_alpha_grad_step', ptr(g), ptr(P), M, Q, n, ptr(lo),
+                 ptr(hi), ptr(a), 1 if p_shared else 0, ptr(fn['W']),
+                 ptr(fn['b']), fn['n_out'], ptr(g2), st)
+            g = g2
+    return lb
+
+
+def _run_alpha_crown_inputsplit_batched(xl, xh, gg, spec_ew, device, dtype,
+                                        n_iters=10, lr=0.25, lr_decay=0.98,
+                                        early_stop_eps=1e-6, sb=None,
+                                        return_trace=False):
+    """Batched alpha-CROWN with Adam (verify_zono_bnb.py:5137-5288).
+
+    Same schedule as the reference: alpha starts at (up_s > 0.5)*unstable on
+    the zonotope bounds; per iteration: evaluate, keep the best lb, stop if
+    every best lb > 0, Adam step (torch.optim.Adam defaults) on -sum(lb),
+    clamp alpha to [0, 1], stop if the global max of the best lb improved by
+    less than ``early_stop_eps`` (from the second iteration), decay lr.
+    The gradient is computed analytically by the HIP gradient sweep.
+    ``sb`` (extension) replaces the zonotope bounds; ``return_trace`` also
+    returns the number of evaluated iterations.
+    """
+    _check_dtype(dtype)
+    xl, xh = f32(xl), f32(xh)
+    B = xl.shape[0]
+    dev = xl.device
+    st = stream()
+    if sb is None:
+        sb, _ = _forward_zonotope_graph_batched(xl, xh, gg, device, dtype)
+    sb = {L: (f32(lo), f32(hi)) for L, (lo, hi) in sb.items()}
+    Wq, bq = _spec_rows(spec_ew, dev)
+    Q = Wq.shape[0]
+    Ls = sorted(sb)
+    sizes = [sb[L][0].numel() for L in Ls]
+    total = sum(sizes)
+    if total == 0:
+        lb = _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, None, False,
+                                      None)
+        return (lb, 1) if return_trace else lb
+    flat = torch.empty(total, device=dev)
+    gflat = torch.zeros(total, device=dev)
+    m1 = torch.zeros(total, device=dev)
+    m2 = torch.zeros(total, device=dev)
+    alpha, galpha = {}, {}
+    off = 0
+    for L, sz in zip(Ls, sizes):
+        alpha[L] = flat[off:off + sz].view(sb[L][0].shape)
+        galpha[L] = gflat[off:off + sz].view(sb[L][0].shape)
+        call('vc_alpha_init', ptr(sb[L][0]), ptr(sb[L][1]), sz,
+             ptr(alpha[L]), st)
+        off += sz
+    best = torch.empty(B, Q, device=dev)
+    red = torch.empty(2, device=dev)
+    b1, b2, eps = 0.9, 0.999, 1e-8
+    prev_max = -float('inf')
+    n_eval = 0
+    step = 0
+    cur_lr = float(lr)
+    for it in range(n_iters):
+        lb = _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, True,
+                                      galpha)
+        n_eval += 1
+        call('vc_best_update', ptr(best), ptr(lb.contiguous()), B * Q,
+             1 if it == 0 else 0, ptr(red), st)
+        r = red.tolist()
+        curr_max, all_pos = r[0], r[1] > 0.5
+        if all_pos:
+            break
+        step += 1
+        bc1 = 1 - b1 ** step
+        bc2 = 1 - b2 ** step
+        call('vc_adam_step', ptr(flat), ptr(gflat), ptr(m1), ptr(m2), total,
+             b1, b2, eps, cur_lr / bc1, bc2 ** 0.5, 0.0, 1.0, st)
+        if it > 0 and curr_max - prev_max < early_stop_eps:
+            break
+        prev_max = curr_max
+        cur_lr *= lr_decay
+    if return_trace:
+        return best, n_eval
+    return best
