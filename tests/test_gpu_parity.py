@@ -1,6 +1,13 @@
 """GPU parity: the HIP path (through the C ABI) against the CPU oracle on the
-same seeded inputs.  Bounds: |gpu - ref| <= 1e-6 + 1e-5 |ref| (fp32);
-masks, indices, counts and verdicts: exact."""
+same seeded inputs.
+
+Bounds: |gpu - ref32| <= 1e-6 + 1e-5 |ref32| against the fp32 oracle (the
+reference's own precision).  Where a test also runs the oracle in fp64 on
+the same (fp32-valued) inputs, an entry outside that band still passes when
+the GPU value is at least as close to the fp64 value as the fp32 oracle is:
+fp32 sums of hundreds of cancelling terms carry ~1e-6 of reduction-order
+noise, and the GPU's compensated sums are then the more accurate side.
+Masks, indices, counts and verdicts: exact."""
 import pytest
 import torch
 
@@ -18,8 +25,13 @@ F32 = torch.float32
 RTOL, ATOL = 1e-5, 1e-6
 
 
-def assert_bounds(gpu_t, ref_t, what, rtol=RTOL, atol=ATOL):
+def assert_bounds(gpu_t, ref_t, what, rtol=RTOL, atol=ATOL, ref64=None):
     ok = _util.rel_err_ok(gpu_t, ref_t, rtol, atol)
+    if ref64 is not None and not bool(ok.all()):
+        g = gpu_t.detach().double().cpu()
+        e_gpu = (g - ref64.detach().double().cpu()).abs()
+        e_ref = (ref_t.detach().double().cpu() - ref64.detach().double().cpu()).abs()
+        ok = ok | (e_gpu <= e_ref)
     if not bool(ok.all()):
         g = gpu_t.detach().double().cpu()
         r = ref_t.detach().double().cpu()
@@ -148,11 +160,18 @@ def test_spec_backward_parity_same_bounds(gpu):
     beta = {L: torch.randn(lo.shape, generator=g) * 0.1 for L, (lo, hi) in tight.items()}
     lb2 = rb.spec_backward_batched(tight, xl, xh, gg_c, se_c, alpha_at_layer=alpha,
                                    relu_split_beta=beta)
+    d64 = torch.float64
+    lb64 = rb.spec_backward_batched(
+        {L: (a.double(), b.double()) for L, (a, b) in tight.items()}, xl.double(),
+        xh.double(), _util.to_dev(gg_c, 'cpu', d64),
+        {k: (w.double(), b) for k, (w, b) in se_c.items()},
+        alpha_at_layer={L: a.double() for L, a in alpha.items()},
+        relu_split_beta={L: b.double() for L, b in beta.items()})
     glb2 = vz._spec_backward_graph_batched(
         tight_g, xl.to(gpu), xh.to(gpu), gg_g, se_g, gpu, F32,
         alpha_at_layer={L: a.to(gpu) for L, a in alpha.items()},
         relu_split_beta={L: b.to(gpu) for L, b in beta.items()})
-    assert_bounds(glb2, lb2, 'spec lb alpha/beta')
+    assert_bounds(glb2, lb2, 'spec lb alpha/beta', ref64=lb64)
 
 
 def test_spec_backward_parity_cnn(gpu):
@@ -193,12 +212,15 @@ def test_crown_intermediate_parity_mlp_chunked(gpu):
     xl, xh = wk.linf_boxes(3, 784, 0.01, seed=4, dtype=F32)
     sb = rb.ibp_forward_batched(xl, xh, gg_c)
     ref = rb.crown_intermediate_batched(gg_c, xl, xh, chunk=64, sb=sb)
+    ref64 = rb.crown_intermediate_batched(
+        _util.to_dev(gg_c, 'cpu', torch.float64), xl.double(), xh.double(), chunk=64,
+        sb={L: (a.double(), b.double()) for L, (a, b) in sb.items()})
     sbg = {L: (a.to(gpu), b.to(gpu)) for L, (a, b) in sb.items()}
     got = vz._crown_intermediate_batched(gg_g, xl.to(gpu), xh.to(gpu), gpu, F32,
                                          chunk=64, sb=sbg)
     for L in ref:
-        assert_bounds(got[L][0], ref[L][0], f'mlp crown-int lo L{L}')
-        assert_bounds(got[L][1], ref[L][1], f'mlp crown-int hi L{L}')
+        assert_bounds(got[L][0], ref[L][0], f'mlp crown-int lo L{L}', ref64=ref64[L][0])
+        assert_bounds(got[L][1], ref[L][1], f'mlp crown-int hi L{L}', ref64=ref64[L][1])
 
 
 # ----------------------------------------------------------------- a9
@@ -290,8 +312,8 @@ def test_bab_step_parity_c0(gpu):
     se_c, se_g, dq = spec_pair(5, gpu)
     ref = rbab.bab_step(xl, xh, gg_c, se_c, dq)
     got = vg.bab_step(xl.to(gpu), xh.to(gpu), gg_g, se_g, vg.DisjunctTable(dq, gpu))
-    assert_bounds(got['lb'], ref['lb'], 'C0 lb')
     assert torch.equal(cpu(got['closed']), ref['closed'])
+    assert_bounds(got['lb'], ref['lb'], 'C0 lb')
     assert torch.equal(cpu(got['unclosed']), ref['unclosed'])
     assert torch.equal(cpu(got['feasible']), ref['feasible'])
     assert torch.equal(cpu(got['ax']), ref['ax'])

@@ -31,6 +31,35 @@ static inline int vc_blocks(int64_t n, int threads) {
   return (int)b;
 }
 
+// Compensated accumulation (Knuth TwoSum): s holds the rounded running sum,
+// c the accumulated rounding error; the result is s + c.  Exact as written
+// because the library is compiled without contraction or reassociation.
+__device__ __forceinline__ void two_sum_acc(float& s, float& c, float t) {
+  const float x = s + t;
+  const float bp = x - s;
+  const float err = (s - (x - bp)) + (t - bp);
+  s = x;
+  c += err;
+}
+
+struct KSum {
+  float s = 0.f, c = 0.f;
+  __device__ __forceinline__ void add(float t) { two_sum_acc(s, c, t); }
+  __device__ __forceinline__ float value() const { return s + c; }
+};
+
+// Wave-wide sum of compensated partials, compensated through the tree.
+__device__ __forceinline__ float wave_sum_comp(KSum k) {
+  float s = k.s, c = k.c;
+  for (int o = 32; o > 0; o >>= 1) {
+    const float so = __shfl_xor(s, o, 64);
+    const float co = __shfl_xor(c, o, 64);
+    two_sum_acc(s, c, so);
+    c += co;
+  }
+  return s + c;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;

@@ -27,7 +27,7 @@ __global__ void k_ibp_conv(const float* l, const float* h, int64_t B, ConvGeom g
     const int co = o / (g.Ho * g.Wo);
     const int yo = (o / g.Wo) % g.Ho;
     const int xo = o % g.Wo;
-    float sm = 0.f, sr = 0.f;
+    KSum sm, sr;
     const float* lb = l + b * n_in;
     const float* hb = h + b * n_in;
     for (int ci = 0; ci < g.C_in; ++ci)
@@ -40,13 +40,14 @@ __global__ void k_ibp_conv(const float* l, const float* h, int64_t B, ConvGeom g
           const int64_t e = ((int64_t)ci * g.H + yi) * g.W + xi;
           const float lv = lb[e], hv = hb[e];
           const float kv = K[((co * g.C_in + ci) * g.kh + ky) * g.kw + kx];
-          sm += kv * ((lv + hv) / 2.f);
-          sr += fabsf(kv) * ((hv - lv) / 2.f);
+          sm.add(kv * ((lv + hv) / 2.f));
+          sr.add(fabsf(kv) * ((hv - lv) / 2.f));
         }
       }
-    const float mc = bias ? sm + bias[co] : sm;
-    lo[i] = mc - sr;
-    hi[i] = mc + sr;
+    const float mv = sm.value(), rv = sr.value();
+    const float mc = bias ? mv + bias[co] : mv;
+    lo[i] = mc - rv;
+    hi[i] = mc + rv;
   }
 }
 
@@ -66,7 +67,7 @@ __global__ void k_zono_conv_gen(const float* G, int64_t B, int Kg, ConvGeom g, c
     const int co = o / (g.Ho * g.Wo);
     const int yo = (o / g.Wo) % g.Ho;
     const int xo = o % g.Wo;
-    float s = 0.f;
+    KSum s;
     for (int ci = 0; ci < g.C_in; ++ci)
       for (int ky = 0; ky < g.kh; ++ky) {
         const int yi = yo * g.sh - g.ph + ky;
@@ -75,10 +76,10 @@ __global__ void k_zono_conv_gen(const float* G, int64_t B, int Kg, ConvGeom g, c
           const int xi = xo * g.sw - g.pw + kx;
           if (xi < 0 || xi >= g.W) continue;
           const int64_t e = ((int64_t)ci * g.H + yi) * g.W + xi;
-          s += K[((co * g.C_in + ci) * g.kh + ky) * g.kw + kx] * G[(b * n_in + e) * Kg + k];
+          s.add(K[((co * g.C_in + ci) * g.kh + ky) * g.kw + kx] * G[(b * n_in + e) * Kg + k]);
         }
       }
-    Go[i] = s;
+    Go[i] = s.value();
   }
 }
 
@@ -94,7 +95,7 @@ __global__ void k_conv_center(const float* c, int64_t B, ConvGeom g, const float
     const int co = o / (g.Ho * g.Wo);
     const int yo = (o / g.Wo) % g.Ho;
     const int xo = o % g.Wo;
-    float s = 0.f;
+    KSum s;
     for (int ci = 0; ci < g.C_in; ++ci)
       for (int ky = 0; ky < g.kh; ++ky) {
         const int yi = yo * g.sh - g.ph + ky;
@@ -102,11 +103,12 @@ __global__ void k_conv_center(const float* c, int64_t B, ConvGeom g, const float
         for (int kx = 0; kx < g.kw; ++kx) {
           const int xi = xo * g.sw - g.pw + kx;
           if (xi < 0 || xi >= g.W) continue;
-          s += K[((co * g.C_in + ci) * g.kh + ky) * g.kw + kx] *
-               c[b * n_in + ((int64_t)ci * g.H + yi) * g.W + xi];
+          s.add(K[((co * g.C_in + ci) * g.kh + ky) * g.kw + kx] *
+                c[b * n_in + ((int64_t)ci * g.H + yi) * g.W + xi]);
         }
       }
-    co_out[i] = bias ? s + bias[co] : s;
+    const float sv = s.value();
+    co_out[i] = bias ? sv + bias[co] : sv;
   }
 }
 
@@ -124,7 +126,7 @@ __global__ void k_conv_transpose(const float* ew, int64_t M, ConvGeom g, const f
     const int ci = e / (g.H * g.W);
     const int yi = (e / g.W) % g.H;
     const int xi = e % g.W;
-    float s = 0.f;
+    KSum s;
     const float* em = ew + m * n_out;
     for (int ky = 0; ky < g.kh; ++ky) {
       const int ty = yi + g.ph - ky;
@@ -137,11 +139,11 @@ __global__ void k_conv_transpose(const float* ew, int64_t M, ConvGeom g, const f
         const int xo = tx / g.sw;
         if (xo >= g.Wo) continue;
         for (int co = 0; co < g.C_out; ++co)
-          s += em[((int64_t)co * g.Ho + yo) * g.Wo + xo] *
-               K[((co * g.C_in + ci) * g.kh + ky) * g.kw + kx];
+          s.add(em[((int64_t)co * g.Ho + yo) * g.Wo + xo] *
+                K[((co * g.C_in + ci) * g.kh + ky) * g.kw + kx]);
       }
     }
-    out[i] = s;
+    out[i] = s.value();
   }
 }
 
@@ -152,9 +154,9 @@ __global__ void k_conv_bias_dot(const float* ew, int64_t M, int C_out, int sp,
   const int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
   if (m >= M) return;
   const int64_t n = (int64_t)C_out * sp;
-  float s = 0.f;
-  for (int64_t j = lane; j < n; j += 64) s += ew[m * n + j] * bias[j / sp];
-  s = wave_sum(s);
+  KSum ks;
+  for (int64_t j = lane; j < n; j += 64) ks.add(ew[m * n + j] * bias[j / sp]);
+  const float s = wave_sum_comp(ks);
   if (lane == 0) acc[m] += s;
 }
 

@@ -71,15 +71,17 @@ __global__ void k_concretize_wave(const float* A, int a_bcast, const float* acc,
   const int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
   if (m >= M) return;
   const int64_t d = m / R;
-  float s1 = 0.f, s2 = 0.f;
+  // one compensated sum over acc and both products, so that large
+  // cancelling positive/negative parts do not lose the small result
+  KSum s;
+  if (lane == 0) s.add(acc[m]);
   for (int i = lane; i < n; i += 64) {
     const float a = A[(a_bcast ? m % R : m) * n + i];
-    s1 += fmaxf(a, 0.f) * xl[d * n + i];
-    s2 += fminf(a, 0.f) * xh[d * n + i];
+    s.add(fmaxf(a, 0.f) * xl[d * n + i]);
+    s.add(fminf(a, 0.f) * xh[d * n + i]);
   }
-  s1 = wave_sum(s1);
-  s2 = wave_sum(s2);
-  if (lane == 0) lb[m] = (acc[m] + s1) + s2;
+  const float t = wave_sum_comp(s);
+  if (lane == 0) lb[m] = t;
 }
 
 __global__ void k_concretize_thread(const float* A, int a_bcast, const float* acc, const float* xl,
@@ -87,13 +89,14 @@ __global__ void k_concretize_thread(const float* A, int a_bcast, const float* ac
   const int64_t m = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (m >= M) return;
   const int64_t d = m / R;
-  float s1 = 0.f, s2 = 0.f;
+  KSum s;
+  s.add(acc[m]);
   for (int i = 0; i < n; ++i) {
     const float a = A[(a_bcast ? m % R : m) * n + i];
-    s1 += fmaxf(a, 0.f) * xl[d * n + i];
-    s2 += fminf(a, 0.f) * xh[d * n + i];
+    s.add(fmaxf(a, 0.f) * xl[d * n + i]);
+    s.add(fminf(a, 0.f) * xh[d * n + i]);
   }
-  lb[m] = (acc[m] + s1) + s2;
+  lb[m] = s.value();
 }
 
 // Standalone relu backward: one wave per row.
@@ -104,7 +107,7 @@ __global__ void k_backward_relu(const float* ew, int64_t M, int R, int n, const 
   const int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
   if (m >= M) return;
   const int64_t d = m / R;
-  float p = 0.f;
+  KSum p;
   for (int j = lane; j < n; j += 64) {
     const int64_t bi = d * n + j;
     const float x = ew[m * n + j];
@@ -118,10 +121,10 @@ __global__ void k_backward_relu(const float* ew, int64_t M, int R, int n, const 
     float e = ep * ls + en * s.up_s;
     if (beta) e = e + beta[bi];
     out[m * n + j] = e;
-    p += en * s.up_t;
+    p.add(en * s.up_t);
   }
-  p = wave_sum(p);
-  if (lane == 0) acc[m] += p;
+  const float ps = wave_sum_comp(p);
+  if (lane == 0) acc[m] += ps;
 }
 
 __global__ void k_crown_intersect(const float* sl, const int32_t* idx, int k, int64_t B,

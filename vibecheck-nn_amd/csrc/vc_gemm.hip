@@ -36,15 +36,22 @@ __global__ __launch_bounds__(NT) void gemm_kernel(int64_t M, int N, int K,
   const int64_t m0 = (int64_t)blockIdx.y * BM;
   const int n0 = bx * BN;
 
-  v4f acc[NA][2][2];
+  // Running sums with TwoSum compensation: each BK-deep K-tile is reduced
+  // by MFMA into a fresh accumulator and then folded into (acc, cmp), so
+  // the rounding error no longer grows with K (the fp32 sums are at least
+  // as accurate as a blocked CPU BLAS).
+  v4f acc[NA][2][2], cmp[NA][2][2];
 #pragma unroll
   for (int a = 0; a < NA; ++a)
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[a][i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < 2; ++j) {
+        acc[a][i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        cmp[a][i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+      }
 
-  float rowpart[4] = {0.f, 0.f, 0.f, 0.f};
+  KSum rowpart[4];
   const bool do_rows = ACC_ROWS && (bx == 0) && acc_rows != nullptr;
 
   for (int k0 = 0; k0 < K; k0 += BK) {
@@ -62,7 +69,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(int64_t M, int N, int K,
 #pragma unroll
         for (int a = 0; a < NA; ++a) v[a] = 0.f;
       }
-      if (do_rows) rowpart[i] += part;
+      if (do_rows) rowpart[i].add(part);
 #pragma unroll
       for (int a = 0; a < NA; ++a) As[a][kk][mm] = v[a];
     }
@@ -90,9 +97,14 @@ __global__ __launch_bounds__(NT) void gemm_kernel(int64_t M, int N, int K,
     }
     __syncthreads();
 #pragma unroll
-    for (int ks = 0; ks < BK / 4; ++ks) {
+    for (int a = 0; a < NA; ++a) {
+      v4f t[2][2];
 #pragma unroll
-      for (int a = 0; a < NA; ++a) {
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) t[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < BK / 4; ++ks) {
         float af[2], bf[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) af[i] = As[a][ks * 4 + g][wm * 32 + i * 16 + r];
@@ -101,16 +113,33 @@ __global__ __launch_bounds__(NT) void gemm_kernel(int64_t M, int N, int K,
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j) acc[a][i][j] = mfma16x16x4(af[i], bf[j], acc[a][i][j]);
+          for (int j = 0; j < 2; ++j) t[i][j] = mfma16x16x4(af[i], bf[j], t[i][j]);
       }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float s = acc[a][i][j][e], c = cmp[a][i][j][e];
+            two_sum_acc(s, c, t[i][j][e]);
+            acc[a][i][j][e] = s;
+            cmp[a][i][j][e] = c;
+          }
     }
     __syncthreads();
   }
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[a][i][j] += cmp[a][i][j];
 
   if (do_rows) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float p = rowpart[i];
+      float p = rowpart[i].value();
       p += __shfl_xor(p, 8, 16);
       p += __shfl_xor(p, 4, 16);
       p += __shfl_xor(p, 2, 16);

@@ -15,9 +15,9 @@ __global__ void k_zono_bounds(const float* c, const float* G, int64_t rows, int 
   const int lane = threadIdx.x & 63;
   const int64_t row = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
   if (row >= rows) return;
-  float s = 0.f;
-  for (int k = lane; k < K; k += 64) s += fabsf(G[row * K + k]);
-  s = wave_sum(s);
+  KSum ks;
+  for (int k = lane; k < K; k += 64) ks.add(fabsf(G[row * K + k]));
+  const float s = wave_sum_comp(ks);
   if (lane == 0) {
     const float l = c[row] - s, h = c[row] + s;
     lo[row] = l;
