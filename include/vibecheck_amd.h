@@ -228,6 +228,77 @@ int vc_adam_step(float *param, const float *lb_grad, float *exp_avg,
 int vc_best_update(float *best, const float *lb, int64_t n, int init,
                    float *out2, vc_stream_t stream);
 
+/* ---- Whole-network kernels for narrow fc/ReLU chains ------------------- */
+/* dims (host array, n_relu + 1 entries): dims[0] = inputs, dims[l + 1] =
+ * width of ReLU layer l (the output of fc_l); every width <= 64,
+ * 1 <= n_relu <= 16.  The final fc (to the network outputs) is not part of
+ * these kernels; the caller folds it into the spec rows.  Weight fragments
+ * are packed once per network; bias_cat concatenates the biases of
+ * fc_0 .. fc_{n_relu-1}.  Per-layer tensors are passed as host arrays of
+ * n_relu device pointers.  Return VC_ERR_UNSUPPORTED for shapes outside
+ * these limits (the caller then uses the layer-wise entry points). */
+
+/* Number of floats of the packed fragments (negative status on error). */
+int64_t vc_mlp_frag_floats(const int32_t *dims, int n_relu, int forward);
+
+/* Pack fc_0 .. fc_{n_relu-1} (W[l]: dims[l+1] x dims[l], device) into MFMA
+ * A-operand fragments: forward (zonotope, A = W) or backward (CROWN, A = W^T). */
+int vc_mlp_pack(const float *const *W, const int32_t *dims, int n_relu,
+                int forward, float *frag, vc_stream_t stream);
+
+/* Zonotope pre-activation bounds of every ReLU layer, one wavefront per
+ * domain with the generator matrix in registers (per-domain generator
+ * count, up to 128 columns including the centre).  lo_out/hi_out[l]
+ * (B, dims[l+1]).  overflow[b] = 1 when domain b needs more generator
+ * columns; its bounds are then incomplete and must be recomputed with the
+ * layer-wise entry points.
+ * Replaces the ReLU bounds of _forward_zonotope_graph_batched
+ * (verify_zono_bnb.py:3079-3211). */
+int vc_mlp_zono_bounds(const int32_t *dims, int n_relu, const float *frag_fwd,
+                       const float *bias_cat, int64_t B, const float *xl,
+                       const float *xh, float *const *lo_out,
+                       float *const *hi_out, int32_t *overflow,
+                       vc_stream_t stream);
+
+/* CROWN intermediate bounds and the spec backward, whole network per
+ * wavefront.  With do_crown != 0, layer L is tightened by seeding
+ * [+I; -I] at its pre-activation for the idx_cnt[L] neurons listed in
+ * idx_all (concatenated per layer), intersecting with lo_in/hi_in and
+ * writing lo_out/hi_out[L] (B, dims[L+1]); with do_crown == 0 the bounds
+ * lo_in/hi_in are used as given.  With Q > 0 (Q <= 32) the spec rows
+ * spec_rows (Q, dims[n_relu]) and their constants spec_acc (Q) -- the spec
+ * already folded through the final fc -- are propagated to the input:
+ * lb_out (B, Q), and when non-NULL A_out (B, Q, dims[0]), acc_out (B, Q).
+ * Replaces _crown_intermediate_batched (verify_zono_bnb.py:4077-4147) and
+ * _spec_backward_graph_batched with return_input_linear
+ * (verify_zono_bnb.py:4270-4453, 5117-5134). */
+int vc_mlp_crown(const int32_t *dims, int n_relu, const float *frag_bwd,
+                 const float *bias_cat, int64_t B, const float *xl,
+                 const float *xh, const float *const *lo_in,
+                 const float *const *hi_in, float *const *lo_out,
+                 float *const *hi_out, const int32_t *idx_all,
+                 const int32_t *idx_cnt, int do_crown, int Q,
+                 const float *spec_rows, const float *spec_acc, float *lb_out,
+                 float *A_out, float *acc_out, vc_stream_t stream);
+
+/* One batched alpha-CROWN Adam iteration, whole network per wavefront
+ * (n_relu <= 7, 1 <= Q <= 16): evaluates lb_out (B, Q) with lower slopes
+ * active + unstable * alpha on the bounds lo/hi, computes d(sum lb)/d alpha
+ * analytically (torch's clamp subgradients) and applies torch.optim.Adam on
+ * -sum lb (betas b1, b2, eps; step_size = lr / (1 - b1^step), bc2_sqrt =
+ * sqrt(1 - b2^step)) followed by the clamp to [0, 1].  alpha, exp_avg,
+ * exp_avg_sq: per-layer (B, dims[l+1]) device arrays, updated in place.
+ * Replaces one iteration of _run_alpha_crown_inputsplit_batched
+ * (verify_zono_bnb.py:5248-5266). */
+int vc_mlp_alpha_iter(const int32_t *dims, int n_relu, const float *frag_bwd,
+                      const float *bias_cat, int64_t B, const float *xl,
+                      const float *xh, const float *const *lo,
+                      const float *const *hi, float *const *alpha,
+                      float *const *exp_avg, float *const *exp_avg_sq, int Q,
+                      const float *spec_rows, const float *spec_acc,
+                      float *lb_out, float b1, float b2, float eps,
+                      double step_size, double bc2_sqrt, vc_stream_t stream);
+
 /* ---- Input-split BaB step ---------------------------------------------- */
 
 /* Closure: closed[b] = AND over disjuncts d of (OR over q in d of
@@ -266,6 +337,10 @@ int vc_scatter_max_rows(float *rows, const int64_t *idx, const float *src,
 /* Row gather: out[r] = in[idx[r]] for rows of `cols` floats. */
 int vc_gather_rows(const float *in, const int64_t *idx, int64_t n_rows,
                    int cols, float *out, vc_stream_t stream);
+
+/* Row scatter: out[idx[r]] = in[r] for rows of `cols` floats. */
+int vc_scatter_rows(const float *in, const int64_t *idx, int64_t n_rows,
+                    int cols, float *out, vc_stream_t stream);
 
 /* Widest-dimension selection: ax[b] = first argmax_i (xh - xl)[b, i];
  * usable[b] = (xh - xl)[b, ax] > 1e-12.

@@ -432,6 +432,17 @@ __global__ void k_gather_rows(const float* in, const int64_t* idx, int64_t nr, i
   }
 }
 
+__global__ void k_scatter_rows(const float* in, const int64_t* idx, int64_t nr, int cols,
+                               float* out) {
+  const int64_t total = nr * (int64_t)cols;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / cols;
+    const int c = (int)(i % cols);
+    out[idx[r] * cols + c] = in[i];
+  }
+}
+
 // First index of the maximum width (NaN counts as maximal, like argmax).
 __global__ void k_widest(const float* xl, const float* xh, int64_t B, int n, int64_t* ax,
                          uint8_t* usable) {
@@ -687,6 +698,16 @@ extern "C" int vc_gather_rows(const float* in, const int64_t* idx, int64_t n_row
   if (!in || !idx || !out || n_rows < 0 || cols <= 0) return VC_ERR_ARG;
   if (n_rows == 0) return VC_OK;
   hipLaunchKernelGGL(k_gather_rows, dim3(vc_blocks(n_rows * cols, NT)), dim3(NT), 0,
+                     (hipStream_t)stream, in, idx, n_rows, cols, out);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_scatter_rows(const float* in, const int64_t* idx, int64_t n_rows, int cols,
+                               float* out, vc_stream_t stream) {
+  if (!in || !idx || !out || n_rows < 0 || cols <= 0) return VC_ERR_ARG;
+  if (n_rows == 0) return VC_OK;
+  hipLaunchKernelGGL(k_scatter_rows, dim3(vc_blocks(n_rows * cols, NT)), dim3(NT), 0,
                      (hipStream_t)stream, in, idx, n_rows, cols, out);
   VC_LAUNCH_CHECK();
   return VC_OK;

@@ -54,10 +54,26 @@ SIGNATURES = {
     'vc_compact': [_P, _L, _I, _P, _P, _P, _L, _P],
     'vc_scatter_max_rows': [_P, _P, _P, _L, _I, _P],
     'vc_gather_rows': [_P, _P, _L, _I, _P, _P],
+    'vc_scatter_rows': [_P, _P, _L, _I, _P, _P],
+    'vc_mlp_frag_floats': [_P, _I, _I],
+    'vc_mlp_pack': [_P, _P, _I, _I, _P, _P],
+    'vc_mlp_zono_bounds': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P],
+    'vc_mlp_crown': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _I,
+                     _I, _P, _P, _P, _P, _P, _P],
+    'vc_mlp_alpha_iter': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
+                          _P, _P, _P, _F, _F, _F, _D, _D, _P],
     'vc_widest_axis': [_P, _P, _L, _I, _P, _P, _P],
     'vc_bisect': [_P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P],
 }
-_RESTYPE = {'vc_compact_workspace': ctypes.c_int64}
+_RESTYPE = {'vc_compact_workspace': ctypes.c_int64,
+            'vc_mlp_frag_floats': ctypes.c_int64}
+
+
+def host_array(ctype, values):
+    """ctypes array of host values; returns (array, address) -- keep the
+    array alive for the duration of the call."""
+    arr = (ctype * max(1, len(values)))(*values)
+    return arr, ctypes.addressof(arr)
 
 _lib = None
 
@@ -97,11 +113,33 @@ def check(rc, name):
     raise RuntimeError(msg)
 
 
+def mlp_crown_flops(dims, n, B, cnt, do_crown, Q):
+    """Algorithmic flops of one vc_mlp_crown launch: every seeded row of
+    layer L (2 cnt[L] rows) goes through fc_{L-1} .. fc_0 backward, every
+    spec row through fc_{n-1} .. fc_0; a row through fc_l costs
+    2 d[l] d[l+1]."""
+    step = [2.0 * dims[l] * dims[l + 1] for l in range(n)]
+    per_dom = 0.0
+    if do_crown:
+        for L in range(n):
+            per_dom += 2 * cnt[L] * sum(step[:L])
+    per_dom += Q * sum(step)
+    return per_dom * B
+
+
+def _flops_mlp_crown(a):
+    n = a[1]
+    dims = list((ctypes.c_int32 * (n + 1)).from_address(a[0]))
+    cnt = list((ctypes.c_int32 * n).from_address(a[12])) if a[13] else [0] * n
+    return mlp_crown_flops(dims, n, a[4], cnt, a[13], a[14])
+
+
 # Algorithmic work per launch, from the call's arguments (used by the
 # optional per-entry-point timing below).
 _FLOPS = {
     # 2 * M * n_out * n_in
     'vc_backward_fc': lambda a: 2.0 * a[1] * a[3] * a[11],
+    'vc_mlp_crown': _flops_mlp_crown,
 }
 
 _timing = None

@@ -1,0 +1,258 @@
+"""Host side of the whole-network kernels for narrow fc/ReLU chains.
+
+A network qualifies when its ops are fc, relu, fc, relu, ..., fc (every
+relu fed by the preceding fc and carrying layer_idx 0, 1, ...), every width
+is <= 64 and there are 1..16 ReLU layers -- the 5-50x6-5 ACAS-Xu shape.
+For those nets the zonotope bounds, the CROWN intermediate bounds and the
+spec backward run as one wavefront per domain (vc_mlp_* entry points);
+other nets use the layer-wise kernels.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import call, host_array, ptr, stream
+
+MAX_W = 64
+MAX_L = 16
+PLAN_KEY = '_vc_amd_mlp_plan'
+
+
+class MlpPlan:
+    """Packed weights of a qualifying network on one device."""
+
+    def __init__(self, gg, device):
+        ops = gg['ops']
+        fcs = [op for op in ops if op['type'] == 'fc']
+        self.n = len(fcs) - 1
+        Ws = [op['W'].detach().to(device=device, dtype=torch.float32).contiguous()
+              for op in fcs]
+        bs = []
+        for op, W in zip(fcs, Ws):
+            b = op.get('bias')
+            bs.append(torch.zeros(W.shape[0], device=device) if b is None else
+                      torch.as_tensor(b).detach().to(device=device, dtype=torch.float32)
+                      .reshape(-1).contiguous())
+        self.dims = [int(Ws[0].shape[1])] + [int(W.shape[0]) for W in Ws[:-1]]
+        self.n_out = int(Ws[-1].shape[0])
+        self.W_last, self.b_last = Ws[-1], bs[-1]
+        self.Ws, self.bs = Ws[:-1], bs[:-1]
+        self.bias_cat = torch.cat(self.bs).contiguous()
+        self.device = device
+        self._dims_arr, self.dims_p = host_array(ctypes.c_int32, self.dims)
+        wp_arr, wp = host_array(ctypes.c_void_p, [ptr(W) for W in self.Ws])
+        lib = _lib.load()
+        self.frag = {}
+        for fwd in (0, 1):
+            nf = int(lib.vc_mlp_frag_floats(self.dims_p, self.n, fwd))
+            if nf <= 0:
+                raise NotImplementedError('vibecheck_amd: network shape not fused')
+            buf = torch.empty(nf, device=device)
+            call('vc_mlp_pack', wp, self.dims_p, self.n, fwd, ptr(buf), stream())
+            self.frag[fwd] = buf
+        del wp_arr
+
+
+def plan_for(gg, device):
+    """The cached MlpPlan of gg on ``device``, or None if not eligible."""
+    device = torch.device(device)
+    cached = gg.get(PLAN_KEY)
+    if cached is not None:
+        if cached == 'no':
+            return None
+        if cached.device == device:
+            return cached
+    if not _eligible(gg):
+        gg[PLAN_KEY] = 'no'
+        return None
+    plan = MlpPlan(gg, device)
+    gg[PLAN_KEY] = plan
+    return plan
+
+
+def _eligible(gg):
+    ops = gg['ops']
+    if len(ops) < 3 or len(ops) % 2 == 0:
+        return False
+    prev = gg['input_name']
+    n_relu = 0
+    for k, op in enumerate(ops):
+        want = 'fc' if k % 2 == 0 else 'relu'
+        if op['type'] != want or op['inputs'] != [prev]:
+            return False
+        if want == 'relu':
+            if op.get('layer_idx') != n_relu:
+                return False
+            n_relu += 1
+        else:
+            W = op['W']
+            if W.dim() != 2:
+                return False
+            if k < len(ops) - 1 and (W.shape[0] > MAX_W or W.shape[1] > MAX_W):
+                return False
+            if k == len(ops) - 1 and W.shape[1] > MAX_W:
+                return False
+        prev = op['name']
+    return 1 <= n_relu <= MAX_L
+
+
+def zono_bounds(plan, xl, xh, fallback):
+    """Zonotope pre-activation bounds {L: (lo, hi)} for every ReLU layer.
+    ``fallback(xl_sub, xh_sub)`` computes the layer-wise bounds for the
+    domains whose generator matrix exceeds the register capacity."""
+    B = xl.shape[0]
+    dev = xl.device
+    lo = [torch.empty(B, plan.dims[l + 1], device=dev) for l in range(plan.n)]
+    hi = [torch.empty_like(t) for t in lo]
+    ovf = torch.empty(B, dtype=torch.int32, device=dev)
+    lo_a, lo_p = host_array(ctypes.c_void_p, [ptr(t) for t in lo])
+    hi_a, hi_p = host_array(ctypes.c_void_p, [ptr(t) for t in hi])
+    call('vc_mlp_zono_bounds', plan.dims_p, plan.n, ptr(plan.frag[1]),
+         ptr(plan.bias_cat), B, ptr(xl), ptr(xh), lo_p, hi_p, ptr(ovf), stream())
+    del lo_a, hi_a
+    from .verify_graph import _compact, _gather
+    bad = _compact(ovf.to(torch.uint8))
+    if bad.numel() > 0:
+        sub = fallback(_gather(xl, bad), _gather(xh, bad))
+        for L in range(plan.n):
+            call('vc_scatter_rows', ptr(sub[L][0].contiguous()), ptr(bad), bad.numel(),
+                 plan.dims[L + 1], ptr(lo[L]), stream())
+            call('vc_scatter_rows', ptr(sub[L][1].contiguous()), ptr(bad), bad.numel(),
+                 plan.dims[L + 1], ptr(hi[L]), stream())
+    return {L: (lo[L], hi[L]) for L in range(plan.n)}, int(bad.numel())
+
+
+def union_idx(plan, sb):
+    """Per layer, the neurons unstable in any domain (one host sync)."""
+    dev = plan.device
+    flags = torch.empty(sum(plan.dims[1:]), dtype=torch.uint8, device=dev)
+    off = 0
+    for L in range(plan.n):
+        n = plan.dims[L + 1]
+        lo, hi = sb[L]
+        call('vc_unstable_union', ptr(lo), ptr(hi), lo.shape[0], n,
+             ptr(flags[off:off + n]), stream())
+        off += n
+    f = flags.cpu()
+    idx, cnt = [], []
+    off = 0
+    for L in range(plan.n):
+        n = plan.dims[L + 1]
+        sel = f[off:off + n].nonzero(as_tuple=True)[0].tolist()
+        idx.extend(sel)
+        cnt.append(len(sel))
+        off += n
+    idx_t = torch.tensor(idx if idx else [0], dtype=torch.int32).to(dev)
+    return idx_t, cnt
+
+
+def fold_spec(plan, Wq, bq):
+    """Spec rows through the final fc: S = Wq W_last (Q, d_n), acc0 = bq +
+    Wq b_last, by the backward fc kernel on the shared rows."""
+    Q = Wq.shape[0]
+    S = torch.empty(Q, plan.dims[plan.n], device=plan.device)
+    acc = bq.clone()
+    call('vc_backward_fc', ptr(Wq), Q, Q, plan.n_out, None, None, None, 0, None,
+         ptr(plan.W_last), ptr(plan.b_last), plan.dims[plan.n], ptr(S), ptr(acc),
+         None, 0, stream())
+    return S, acc
+
+
+ALPHA_MAX_L = 7
+ALPHA_MAX_Q = 16
+
+
+def alpha_supported(plan, Q):
+    return plan.n <= ALPHA_MAX_L and 1 <= Q <= ALPHA_MAX_Q
+
+
+def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps):
+    """Batched alpha-CROWN with the reference's schedule
+    (verify_zono_bnb.py:5137-5288), one fused kernel launch per Adam
+    iteration.  Returns (best (B, Q), evaluated iterations)."""
+    B = xl.shape[0]
+    dev = xl.device
+    st = stream()
+    S, acc0 = fold_spec(plan, Wq, bq)
+    Q = S.shape[0]
+    lo = [sb[L][0].contiguous() for L in range(plan.n)]
+    hi = [sb[L][1].contiguous() for L in range(plan.n)]
+    alpha = [torch.empty_like(t) for t in lo]
+    m1 = [torch.zeros_like(t) for t in lo]
+    m2 = [torch.zeros_like(t) for t in lo]
+    for L in range(plan.n):
+        call('vc_alpha_init', ptr(lo[L]), ptr(hi[L]), lo[L].numel(), ptr(alpha[L]), st)
+    keep = []
+    ptrs = []
+    for lst in (lo, hi, alpha, m1, m2):
+        a, p = host_array(ctypes.c_void_p, [ptr(t) for t in lst])
+        keep.append(a)
+        ptrs.append(p)
+    lb = torch.empty(B, Q, device=dev)
+    best = torch.empty(B, Q, device=dev)
+    red = torch.empty(2, device=dev)
+    b1, b2, eps = 0.9, 0.999, 1e-8
+    prev_max = -float('inf')
+    cur_lr = float(lr)
+    n_eval = 0
+    for it in range(n_iters):
+        step = it + 1
+        call('vc_mlp_alpha_iter', plan.dims_p, plan.n, ptr(plan.frag[0]), ptr(plan.bias_cat),
+             B, ptr(xl), ptr(xh), *ptrs, Q, ptr(S), ptr(acc0), ptr(lb), b1, b2, eps,
+             cur_lr / (1 - b1 ** step), (1 - b2 ** step) ** 0.5, st)
+        n_eval += 1
+        call('vc_best_update', ptr(best), ptr(lb), B * Q, 1 if it == 0 else 0, ptr(red), st)
+        curr_max, all_pos = red.tolist()
+        if all_pos > 0.5:
+            break
+        if it > 0 and curr_max - prev_max < early_stop_eps:
+            break
+        prev_max = curr_max
+        cur_lr *= lr_decay
+    return best, n_eval
+
+
+def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False):
+    """CROWN intermediate bounds (do_crown) and/or the spec backward.
+
+    Returns (tight {L: (lo, hi)} or None, lb (B, Q) or None, A, acc)."""
+    B = xl.shape[0]
+    dev = xl.device
+    lo_in = [sb[L][0].contiguous() for L in range(plan.n)]
+    hi_in = [sb[L][1].contiguous() for L in range(plan.n)]
+    keep = []                       # host arrays alive until the call
+    a, lin_p = host_array(ctypes.c_void_p, [ptr(t) for t in lo_in])
+    keep.append(a)
+    a, hin_p = host_array(ctypes.c_void_p, [ptr(t) for t in hi_in])
+    keep.append(a)
+    lo_out = hi_out = None
+    lout_p = hout_p = None
+    idx_t = None
+    cnt_p = None
+    if do_crown:
+        idx_t, cnt = union_idx(plan, sb)
+        a, cnt_p = host_array(ctypes.c_int32, cnt)
+        keep.append(a)
+        lo_out = [torch.empty_like(t) for t in lo_in]
+        hi_out = [torch.empty_like(t) for t in hi_in]
+        a, lout_p = host_array(ctypes.c_void_p, [ptr(t) for t in lo_out])
+        keep.append(a)
+        a, hout_p = host_array(ctypes.c_void_p, [ptr(t) for t in hi_out])
+        keep.append(a)
+    Q = 0
+    S = acc0 = lb = A = acc = None
+    if spec is not None:
+        S, acc0 = fold_spec(plan, *spec)
+        Q = S.shape[0]
+        lb = torch.empty(B, Q, device=dev)
+        if want_linear:
+            A = torch.empty(B, Q, plan.dims[0], device=dev)
+            acc = torch.empty(B, Q, device=dev)
+    call('vc_mlp_crown', plan.dims_p, plan.n, ptr(plan.frag[0]), ptr(plan.bias_cat), B,
+         ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
+         1 if do_crown else 0, Q, ptr(S), ptr(acc0), ptr(lb), ptr(A), ptr(acc), stream())
+    tight = None
+    if do_crown:
+        tight = {L: (lo_out[L], hi_out[L]) for L in range(plan.n)}
+    return tight, lb, A, acc

@@ -16,10 +16,10 @@ import torch
 from ._lib import call, f32, ptr, stream
 from . import _lib
 from .spec import dedup_queries
-from .verify_zono_bnb import (_crown_intermediate_batched,
+from .verify_zono_bnb import (_bound_crown_spec,
                               _forward_zonotope_graph_batched,
                               _run_alpha_crown_inputsplit_batched,
-                              _spec_backward_graph_batched)
+                              _spec_backward_graph_batched, _zono_sb)
 
 __all__ = ['_clip_box_by_halfspaces_batched', '_input_split_batched',
            'DisjunctTable', 'bab_step', 'ChunkWorklist']
@@ -183,16 +183,21 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
         if timers is not None else None
     if timers is not None:
         t0 = sync_t()
+    A = acc = None
     if crown_intermediate:
-        sb = _crown_intermediate_batched(gg, xl, xh, dev, dt)
+        out = _bound_crown_spec(gg, xl, xh, spec_ew, dev, dt,
+                                return_input_linear=clip_enabled)
+        if clip_enabled:
+            _, lb, A, acc = out
+        else:
+            _, lb = out
     else:
-        sb, _ = _forward_zonotope_graph_batched(xl, xh, gg, dev, dt)
-    if clip_enabled:
-        lb, A, acc = _spec_backward_graph_batched(sb, xl, xh, gg, spec_ew, dev,
-                                                  dt, return_input_linear=True)
-    else:
-        lb = _spec_backward_graph_batched(sb, xl, xh, gg, spec_ew, dev, dt)
-        A = acc = None
+        sb = _zono_sb(gg, xl, xh, dev, dt)
+        if clip_enabled:
+            lb, A, acc = _spec_backward_graph_batched(sb, xl, xh, gg, spec_ew, dev,
+                                                      dt, return_input_linear=True)
+        else:
+            lb = _spec_backward_graph_batched(sb, xl, xh, gg, spec_ew, dev, dt)
     lb = lb.contiguous()
     closed = _closure(lb, table)
     n_al = n_ait = 0

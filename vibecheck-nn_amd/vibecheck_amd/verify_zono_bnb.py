@@ -9,13 +9,33 @@ RuntimeError: there is no other compute path.
 """
 import torch
 
-from . import _lib
+from . import _lib, mlp_fused
 from ._lib import call, f32, ptr, stream
 
 __all__ = ['_make_slopes', '_ibp_forward_graph_batched',
            '_forward_zonotope_graph_batched', '_crown_intermediate_batched',
            '_spec_backward_graph_batched',
            '_run_alpha_crown_inputsplit_batched']
+
+# Use the whole-network kernels for narrow fc/ReLU chains (<= 64 wide).
+# Switching this off routes those nets through the layer-wise kernels.
+FUSED_MLP = True
+
+
+def _plan(gg, dev):
+    return mlp_fused.plan_for(gg, dev) if FUSED_MLP else None
+
+
+def _zono_sb(gg, xl, xh, device, dtype):
+    """Zonotope pre-activation bounds only (the fused kernel when the net
+    qualifies, else the layer-wise forward)."""
+    plan = _plan(gg, xl.device)
+    if plan is not None:
+        sb, _ = mlp_fused.zono_bounds(
+            plan, xl, xh,
+            lambda a, b: _forward_zonotope_graph_batched(a, b, gg, device, dtype)[0])
+        return sb
+    return _forward_zonotope_graph_batched(xl, xh, gg, device, dtype)[0]
 
 
 def _check_dtype(dtype):
@@ -173,6 +193,8 @@ def _forward_zonotope_graph_batched(xl, xh, gg, device, dtype):
     """Batched zonotope forward (verify_zono_bnb.py:3079-4075, fc/relu/conv/
     reshape).  Returns (sb, (c, G)); G is (B, n, K) with the new generator
     columns of each ReLU padded to the batch maximum, as in the reference.
+    (The (c, G) output needs the layer-wise kernels; bound-only callers use
+    the fused kernel through _zono_sb.)
     """
     _check_dtype(dtype)
     xl, xh = f32(xl), f32(xh)
@@ -424,6 +446,14 @@ def _spec_backward_graph_batched(tight, xl, xh, gg, spec_ew, device, dtype,
     xl, xh = f32(xl), f32(xh)
     B, n_in = xl.shape
     dev = xl.device
+    plan = _plan(gg, dev)
+    if (plan is not None and seed_ew_at is None and alpha_at_layer is None
+            and relu_split_beta is None and len(spec_ew) <= 32):
+        Wq, bq = _spec_rows(spec_ew, dev)
+        sb = {L: (f32(tight[L][0]), f32(tight[L][1])) for L in range(plan.n)}
+        _, lb, A, acc = mlp_fused.crown(plan, xl, xh, sb, False, spec=(Wq, bq),
+                                        want_linear=return_input_linear)
+        return (lb, A, acc) if return_input_linear else lb
     if seed_ew_at is not None:
         if len(seed_ew_at) != 1:
             raise NotImplementedError('vibecheck_amd: one seed node only')
@@ -481,7 +511,12 @@ def _crown_intermediate_batched(gg, xl, xh, device, dtype, chunk=2048,
     xl, xh = f32(xl), f32(xh)
     dev = xl.device
     if sb is None:
-        sb, _ = _forward_zonotope_graph_batched(xl, xh, gg, device, dtype)
+        sb = _zono_sb(gg, xl, xh, device, dtype)
+    plan = _plan(gg, dev)
+    if plan is not None:
+        tight, _, _, _ = mlp_fused.crown(
+            plan, xl, xh, {L: (f32(sb[L][0]), f32(sb[L][1])) for L in range(plan.n)}, True)
+        return tight
     tight = {L: (f32(lo).clone(), f32(hi).clone()) for L, (lo, hi) in sb.items()}
     relu_by_L = {op['layer_idx']: op for op in gg['ops']
                  if op['type'] == 'relu' and 'layer_idx' in op}
@@ -589,10 +624,15 @@ def _run_alpha_crown_inputsplit_batched(xl, xh, gg, spec_ew, device, dtype,
     dev = xl.device
     st = stream()
     if sb is None:
-        sb, _ = _forward_zonotope_graph_batched(xl, xh, gg, device, dtype)
+        sb = _zono_sb(gg, xl, xh, device, dtype)
     sb = {L: (f32(lo), f32(hi)) for L, (lo, hi) in sb.items()}
     Wq, bq = _spec_rows(spec_ew, dev)
     Q = Wq.shape[0]
+    plan = _plan(gg, dev)
+    if plan is not None and mlp_fused.alpha_supported(plan, Q):
+        best, n_eval = mlp_fused.alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr,
+                                             lr_decay, early_stop_eps)
+        return (best, n_eval) if return_trace else best
     Ls = sorted(sb)
     sizes = [sb[L][0].numel() for L in Ls]
     total = sum(sizes)
@@ -641,3 +681,26 @@ def _run_alpha_crown_inputsplit_batched(xl, xh, gg, spec_ew, device, dtype,
     if return_trace:
         return best, n_eval
     return best
+
+
+def _bound_crown_spec(gg, xl, xh, spec_ew, device, dtype,
+                      return_input_linear=False):
+    """CROWN intermediate bounds followed by the spec bound -- the 'bound'
+    phase of an input-split BaB iteration (verify_graph.py:12855-12871).
+    For narrow fc/ReLU chains both run in one whole-network kernel launch.
+    Returns (tight, lb) or (tight, lb, A, acc)."""
+    _check_dtype(dtype)
+    xl, xh = f32(xl), f32(xh)
+    plan = _plan(gg, xl.device)
+    if plan is not None and len(spec_ew) <= 32:
+        sb = _zono_sb(gg, xl, xh, device, dtype)
+        Wq, bq = _spec_rows(spec_ew, xl.device)
+        tight, lb, A, acc = mlp_fused.crown(plan, xl, xh, sb, True, spec=(Wq, bq),
+                                            want_linear=return_input_linear)
+        return (tight, lb, A, acc) if return_input_linear else (tight, lb)
+    tight = _crown_intermediate_batched(gg, xl, xh, device, dtype)
+    out = _spec_backward_graph_batched(tight, xl, xh, gg, spec_ew, device, dtype,
+                                       return_input_linear=return_input_linear)
+    if return_input_linear:
+        return (tight,) + tuple(out)
+    return tight, out
