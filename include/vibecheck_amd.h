@@ -248,7 +248,9 @@ int vc_mlp_pack(const float *const *W, const int32_t *dims, int n_relu,
 
 /* Zonotope pre-activation bounds of every ReLU layer, one wavefront per
  * domain with the generator matrix in registers (per-domain generator
- * count, up to 128 columns including the centre).  lo_out/hi_out[l]
+ * count: up to 128 columns including the centre, then a second pass with
+ * one 4-wave workgroup and up to 512 columns per domain over the domains
+ * that did not fit).  lo_out/hi_out[l]
  * (B, dims[l+1]).  overflow[b] = 1 when domain b needs more generator
  * columns; its bounds are then incomplete and must be recomputed with the
  * layer-wise entry points.

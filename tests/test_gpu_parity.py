@@ -244,12 +244,26 @@ def mlp_path(request):
     vz.FUSED_MLP = old
 
 
-def test_fused_zono_bounds_parity_with_overflow(gpu):
-    """Whole-network zonotope kernel; wide boxes push some domains past the
-    128-column register capacity, which then take the layer-wise path."""
-    gg_c, gg_g, xl, xh = acas(gpu, 1024, scale=3.0)
-    xl[:64] = xl[:64] * 40.0 - 20.0      # very wide boxes: many unstable neurons
-    xh[:64] = xl[:64] + 40.0
+@pytest.mark.parametrize('case', ['acas_wide_boxes', 'deep_64_fallback'])
+def test_fused_zono_bounds_parity_with_overflow(gpu, case):
+    """Whole-network zonotope kernel.  acas_wide_boxes: very wide boxes push
+    domains past the 128 generator columns of one wavefront; they are
+    redone by the 4-wave cooperative pass (<= 512 columns).  deep_64_fallback:
+    ten 64-wide layers exceed even that, so those domains take the
+    layer-wise kernels."""
+    if case == 'acas_wide_boxes':
+        gg_c, gg_g, xl, xh = acas(gpu, 1024, scale=3.0)
+        xl[:64] = xl[:64] * 40.0 - 20.0
+        xh[:64] = xl[:64] + 40.0
+    else:
+        Ws, bs = wk.mlp_params([6] + [64] * 10 + [3], seed=7, bias_std=0.05)
+        gg_c = wk.mlp_gg(Ws, bs, dtype=F32)
+        gg_g = wk.mlp_gg(Ws, bs, device=gpu, dtype=F32)
+        g = torch.Generator().manual_seed(11)
+        c = torch.rand(256, 6, generator=g) * 2 - 1
+        w = torch.rand(256, 6, generator=g) * 0.05
+        w[:32] = 3.0
+        xl, xh = c - w, c + w
     ref, _ = rb.zono_forward_batched(xl, xh, gg_c)
     ref64, _ = rb.zono_forward_batched(xl.double(), xh.double(), d64(gg_c))
     plan = vz.mlp_fused.plan_for(gg_g, gpu)
@@ -257,10 +271,13 @@ def test_fused_zono_bounds_parity_with_overflow(gpu):
     got, n_ovf = vz.mlp_fused.zono_bounds(
         plan, xl.to(gpu), xh.to(gpu),
         lambda a, b: vz._forward_zonotope_graph_batched(a, b, gg_g, gpu, F32)[0])
-    print(f'overflow domains: {n_ovf}')
-    assert n_ovf > 0
+    print(f'{case}: layer-wise fallback domains: {n_ovf}')
+    if case == 'acas_wide_boxes':
+        assert n_ovf == 0
+    else:
+        assert n_ovf > 0
     for L in ref:
-        assert_interval(got[L], ref[L], f'fused zono L{L}', ref64=ref64[L])
+        assert_interval(got[L], ref[L], f'fused zono L{L} ({case})', ref64=ref64[L])
 
 
 # ----------------------------------------------------------------- a4

@@ -27,8 +27,8 @@ namespace {
 constexpr int FW = 64;     // max layer width
 constexpr int MAXL = 16;   // max relu layers
 constexpr int NWAVE = 8;   // waves (domains in flight) per workgroup
-constexpr int NPAR = 2;    // row N-tiles chained together per wave
-constexpr int ZNT = 8;     // generator capacity of the zonotope kernel (N-tiles)
+constexpr int NPAR = 4;    // row N-tiles chained together per wave
+constexpr int ZNT_NARROW = 8;   // 128 generator columns, 8 waves per workgroup
 
 struct Net {
   int n;                 // relu layers
@@ -63,6 +63,27 @@ __global__ void k_pack(const float* W, int d_out, int d_in, int bwd, float* frag
   }
 }
 
+// Stage the packed fragments (nfrag * 64 floats, 16-byte aligned) and the
+// biases into LDS with 16-byte loads, several in flight per thread.
+__device__ __forceinline__ void stage_weights(float* sfrag, float* sbias, const float* gfrag,
+                                              const float* gbias, int nfrag, int nbias) {
+  const int n4 = nfrag * 16;
+  const float4* src = reinterpret_cast<const float4*>(gfrag);
+  float4* dst = reinterpret_cast<float4*>(sfrag);
+  int e = threadIdx.x;
+  for (; e + 3 * (int)blockDim.x < n4; e += 4 * blockDim.x) {
+    const float4 a = src[e], b = src[e + blockDim.x], c = src[e + 2 * blockDim.x],
+                 d = src[e + 3 * blockDim.x];
+    dst[e] = a;
+    dst[e + blockDim.x] = b;
+    dst[e + 2 * blockDim.x] = c;
+    dst[e + 3 * blockDim.x] = d;
+  }
+  for (; e < n4; e += blockDim.x) dst[e] = src[e];
+  for (int k = threadIdx.x; k < nbias; k += blockDim.x) sbias[k] = gbias[k];
+  __syncthreads();
+}
+
 __device__ __forceinline__ float group_bcast(float v, int lane) {
   return __shfl(v, lane & 48, 64);  // value of lane 16 g (r = 0) of the group
 }
@@ -83,22 +104,27 @@ struct ZonoArgs {
   float* hi[MAXL];
 };
 
-__global__ __launch_bounds__(NWAVE * 64) void k_mlp_zono(Net net, const float* __restrict__ gfrag,
-                                                         const float* __restrict__ gbias, int64_t B,
-                                                         const float* __restrict__ xl,
-                                                         const float* __restrict__ xh,
-                                                         ZonoArgs out, int32_t* overflow) {
+// ZNT: generator capacity in 16-column tiles (centre included).  NW: waves
+// per workgroup.  only_flagged: process only domains whose overflow flag
+// is set (the wide second pass); every processed domain gets its flag
+// rewritten (1 = still does not fit).
+template <int ZNT, int NW>
+__global__ __launch_bounds__(NW * 64) void k_mlp_zono(Net net, const float* __restrict__ gfrag,
+                                                      const float* __restrict__ gbias, int64_t B,
+                                                      const float* __restrict__ xl,
+                                                      const float* __restrict__ xh,
+                                                      ZonoArgs out, int32_t* overflow,
+                                                      int only_flagged) {
   extern __shared__ float smem[];
   float* sfrag = smem;
   float* sbias = smem + net.nfrag * 64;
-  for (int e = threadIdx.x; e < net.nfrag * 64; e += blockDim.x) sfrag[e] = gfrag[e];
-  for (int e = threadIdx.x; e < net.nbias; e += blockDim.x) sbias[e] = gbias[e];
-  __syncthreads();
+  stage_weights(sfrag, sbias, gfrag, gbias, net.nfrag, net.nbias);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int d0 = net.d[0];
 
-  for (int64_t dom = (int64_t)blockIdx.x * NWAVE + wv; dom < B; dom += (int64_t)gridDim.x * NWAVE) {
+  for (int64_t dom = (int64_t)blockIdx.x * NW + wv; dom < B; dom += (int64_t)gridDim.x * NW) {
+    if (only_flagged && overflow[dom] == 0) continue;
     v4f G[ZNT][4];
     // initial block: rows = input dims, col 0 = centre, col 1 + j = radius j
 #pragma unroll
@@ -123,27 +149,40 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_zono(Net net, const float* _
       const int KS = ks_count(dK), MT = (dM + 15) / 16;
       const int ntu = (Kc + 15) / 16;
       const float* fr = sfrag + net.foff[l] * 64 + lane;
-      // fc_l on every used column tile; column 0 also gets the bias
+      // fc_l on every used column tile (two tiles at a time, K-step outer
+      // so consecutive MFMAs write independent accumulators); column 0
+      // also gets the bias
 #pragma unroll
-      for (int nt = 0; nt < ZNT; ++nt) {
-        if (nt < ntu) {
-          v4f o[4];
+      for (int nt0 = 0; nt0 < ZNT; nt0 += 2) {
+        if (nt0 < ntu) {
+          const bool two = nt0 + 1 < ntu;
+          v4f o[2][4];
 #pragma unroll
-          for (int mt = 0; mt < 4; ++mt) o[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+          for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) o[p][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int ks = 4 * t + i;
+              if (ks < KS) {
+                float a[4];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) a[mt] = mt < MT ? fr[(mt * KS + ks) * 64] : 0.f;
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+                  if (mt < MT) {
+                    o[0][mt] = mfma16x16x4(a[mt], G[nt0][t][i], o[0][mt]);
+                    if (two) o[1][mt] = mfma16x16x4(a[mt], G[nt0 + 1][t][i], o[1][mt]);
+                  }
+              }
+            }
 #pragma unroll
           for (int mt = 0; mt < 4; ++mt) {
-            if (mt < MT) {
-#pragma unroll
-              for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                  const int ks = 4 * t + i;
-                  if (ks < KS) o[mt] = mfma16x16x4(fr[(mt * KS + ks) * 64], G[nt][t][i], o[mt]);
-                }
-            }
+            G[nt0][mt] = o[0][mt];
+            if (two) G[nt0 + 1][mt] = o[1][mt];
           }
-#pragma unroll
-          for (int mt = 0; mt < 4; ++mt) G[nt][mt] = o[mt];
         }
       }
       if (r == 0) {
@@ -230,6 +269,208 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_zono(Net net, const float* _
   }
 }
 
+// Zonotope bounds of the domains flagged in `overflow`, one workgroup of
+// ZC_W waves per domain: wave w holds generator columns [128 w, 128 w + 128)
+// (column 0 = centre), so up to ZC_W * 128 columns.  The per-neuron |G|
+// sums are reduced across waves through LDS in a fixed order, so every
+// wave derives the same lo/hi, lambda, mu and unstable set.
+constexpr int ZC_W = 4;
+constexpr int ZC_T = 8;  // tiles per wave
+
+__global__ __launch_bounds__(ZC_W * 64) void k_mlp_zono_coop(
+    Net net, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
+    const float* __restrict__ xl, const float* __restrict__ xh, ZonoArgs out, int32_t* overflow) {
+  extern __shared__ float smem[];
+  float* sfrag = smem;
+  float* sbias = smem + net.nfrag * 64;
+  float* sred = sbias + ((net.nbias + 63) & ~63);  // [ZC_W][2][FW]: (s, c) partials
+  float* scen = sred + ZC_W * 2 * FW;              // centre column [FW]
+  stage_weights(sfrag, sbias, gfrag, gbias, net.nfrag, net.nbias);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int d0 = net.d[0];
+  const int cap = ZC_W * ZC_T * 16;
+
+  // Each workgroup owns a contiguous range of domains; chunks of the range
+  // are scanned in parallel and the flagged domains compacted into LDS.
+  __shared__ int s_list[ZC_W * 64];
+  __shared__ int s_wcnt[ZC_W];
+  const int64_t per = (B + gridDim.x - 1) / gridDim.x;
+  const int64_t beg = (int64_t)blockIdx.x * per;
+  const int64_t end = beg + per < B ? beg + per : B;
+  for (int64_t c0 = beg; c0 < end; c0 += ZC_W * 64) {
+    const int64_t dsc = c0 + threadIdx.x;
+    const bool flagged = dsc < end && overflow[dsc] != 0;
+    const uint64_t bal = __ballot(flagged);
+    if (lane == 0) s_wcnt[wv] = __popcll(bal);
+    __syncthreads();
+    int off = 0, tot = 0;
+    for (int w2 = 0; w2 < ZC_W; ++w2) {
+      if (w2 < wv) off += s_wcnt[w2];
+      tot += s_wcnt[w2];
+    }
+    if (flagged) s_list[off + __popcll(bal & ((1ull << lane) - 1ull))] = (int)(dsc - c0);
+    __syncthreads();
+  for (int k = 0; k < tot; ++k) {
+    const int64_t dom = c0 + s_list[k];
+    v4f G[ZC_T][4];
+#pragma unroll
+    for (int nt = 0; nt < ZC_T; ++nt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = 16 * t + 4 * g + i, col = 128 * wv + 16 * nt + r;
+          float v = 0.f;
+          if (row < d0) {
+            const float l = xl[dom * d0 + row], h = xh[dom * d0 + row];
+            if (col == 0) v = (l + h) / 2.f;
+            else if (col == 1 + row) v = (h - l) / 2.f;
+          }
+          G[nt][t][i] = v;
+        }
+    int Kc = 1 + d0;
+    bool ovf = Kc > cap;
+    for (int l = 0; l < net.n && !ovf; ++l) {
+      const int dK = net.d[l], dM = net.d[l + 1];
+      const int KS = ks_count(dK), MT = (dM + 15) / 16;
+      // tiles of this wave in use
+      int ntu = (Kc + 15) / 16 - ZC_T * wv;
+      ntu = ntu < 0 ? 0 : (ntu > ZC_T ? ZC_T : ntu);
+      const float* fr = sfrag + net.foff[l] * 64 + lane;
+#pragma unroll
+      for (int nt0 = 0; nt0 < ZC_T; nt0 += 2) {
+        if (nt0 < ntu) {
+          const bool two = nt0 + 1 < ntu;
+          v4f o[2][4];
+#pragma unroll
+          for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) o[p][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int ks = 4 * t + i;
+              if (ks < KS) {
+                float a[4];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) a[mt] = mt < MT ? fr[(mt * KS + ks) * 64] : 0.f;
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+                  if (mt < MT) {
+                    o[0][mt] = mfma16x16x4(a[mt], G[nt0][t][i], o[0][mt]);
+                    if (two) o[1][mt] = mfma16x16x4(a[mt], G[nt0 + 1][t][i], o[1][mt]);
+                  }
+              }
+            }
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) {
+            G[nt0][mt] = o[0][mt];
+            if (two) G[nt0 + 1][mt] = o[1][mt];
+          }
+        }
+      }
+      if (wv == 0 && r == 0) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = 16 * t + 4 * g + i;
+            if (j < dM) G[0][t][i] = G[0][t][i] + sbias[net.boff[l] + j];
+            scen[j] = G[0][t][i];
+          }
+      }
+      // per-wave partial |G| sums over this wave's generator columns
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          KSum s;
+#pragma unroll
+          for (int nt = 0; nt < ZC_T; ++nt)
+            if (nt < ntu && (wv > 0 || nt > 0 || r > 0)) s.add(fabsf(G[nt][t][i]));
+          float ss = s.s, sc = s.c;
+          for (int o = 8; o > 0; o >>= 1) {
+            const float so = __shfl_xor(ss, o, 64), co = __shfl_xor(sc, o, 64);
+            two_sum_acc(ss, sc, so);
+            sc += co;
+          }
+          if (r == 0) {
+            const int j = 16 * t + 4 * g + i;
+            sred[(wv * 2) * FW + j] = ss;
+            sred[(wv * 2 + 1) * FW + j] = sc;
+          }
+        }
+      __syncthreads();
+      float lam[4][4], mu[4][4];
+      uint64_t umask = 0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = 16 * t + 4 * g + i;
+          float ss = sred[j], sc = sred[FW + j];
+          for (int w2 = 1; w2 < ZC_W; ++w2) {
+            two_sum_acc(ss, sc, sred[(w2 * 2) * FW + j]);
+            sc += sred[(w2 * 2 + 1) * FW + j];
+          }
+          const float rad = ss + sc;
+          const float c = scen[j];
+          const float lo = c - rad, hi = c + rad;
+          const bool valid = j < dM;
+          const bool ust = valid && lo < 0.f && hi > 0.f;
+          const bool dead = hi <= 0.f;
+          if (valid && r == 0 && wv == 0) {
+            out.lo[l][dom * dM + j] = lo;
+            out.hi[l][dom * dM + j] = hi;
+          }
+          lam[t][i] = ust ? hi / (hi - lo) : (dead ? 0.f : 1.f);
+          mu[t][i] = ust ? (-hi * lo) / (2.f * (hi - lo)) : 0.f;
+          const uint64_t bal = __ballot(ust && r == 0);
+#pragma unroll
+          for (int gg = 0; gg < 4; ++gg)
+            if ((bal >> (16 * gg)) & 1ull) umask |= 1ull << (16 * t + 4 * gg + i);
+        }
+      __syncthreads();  // sred / scen are rewritten by the next layer
+      const int cnt = __popcll(umask);
+      if (l == net.n - 1) break;
+      if (Kc + cnt > cap) {
+        ovf = true;
+        break;
+      }
+#pragma unroll
+      for (int nt = 0; nt < ZC_T; ++nt)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (wv == 0 && nt == 0 && r == 0) G[nt][t][i] = lam[t][i] * G[nt][t][i] + mu[t][i];
+            else G[nt][t][i] = G[nt][t][i] * lam[t][i];
+          }
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = 16 * t + 4 * g + i;
+          if ((umask >> j) & 1ull) {
+            const int col = Kc + __popcll(umask & ((1ull << j) - 1ull));
+            if ((col >> 7) == wv && (col & 15) == r) {
+              const int tile = (col & 127) >> 4;
+#pragma unroll
+              for (int nt = 0; nt < ZC_T; ++nt)
+                if (nt == tile) G[nt][t][i] = mu[t][i];
+            }
+          }
+        }
+      Kc += cnt;
+    }
+    if (threadIdx.x == 0) overflow[dom] = ovf ? 1 : 0;
+  }
+    __syncthreads();  // s_list / s_wcnt are rewritten by the next chunk
+  }
+}
+
 // ------------------------------------------------------------ CROWN kernel
 struct CrownArgs {
   const float* lo_in[MAXL];
@@ -240,12 +481,14 @@ struct CrownArgs {
   int idx_cnt[MAXL];
 };
 
-// One relaxation + fc backward step through relu layer l and fc_l for NPAR
-// row tiles held in F (values of neurons of relu l), leaving in F the rows
-// at fc_l's input.  acc partials collect neg . up_t and e . bias.
+// One relaxation + fc backward step through relu layer l and fc_l for the
+// first np (<= NPAR) row tiles held in F (values of neurons of relu l),
+// leaving in F the rows at fc_l's input.  acc partials collect neg . up_t
+// and e . bias.  The MFMAs run K-step outer, (M-tile, row tile) inner, so
+// consecutive MFMAs write independent accumulators.
 __device__ __forceinline__ void relax_fc(const Net& net, int l, const float* sfrag,
                                          const float* sbias, const float* ssl, int lane, int g,
-                                         v4f (&F)[NPAR][4], KSum (&accp)[NPAR]) {
+                                         int np, v4f (&F)[NPAR][4], KSum (&accp)[NPAR]) {
   const int dK = net.d[l + 1], dM = net.d[l];
   const int KS = ks_count(dK), MT = (dM + 15) / 16;
   const float* sl = ssl + l * 3 * FW;
@@ -259,12 +502,14 @@ __device__ __forceinline__ void relax_fc(const Net& net, int l, const float* sfr
         const float bj = sbias[net.boff[l] + j];
 #pragma unroll
         for (int p = 0; p < NPAR; ++p) {
-          const float x = F[p][t][i];
-          const float ep = fmaxf(x, 0.f), en = fminf(x, 0.f);
-          const float e = ep * ls + en * us;
-          accp[p].add(en * ut);
-          accp[p].add(e * bj);
-          F[p][t][i] = e;
+          if (p < np) {
+            const float x = F[p][t][i];
+            const float ep = fmaxf(x, 0.f), en = fminf(x, 0.f);
+            const float e = ep * ls + en * us;
+            accp[p].add(en * ut);
+            accp[p].add(e * bj);
+            F[p][t][i] = e;
+          }
         }
       }
     }
@@ -275,21 +520,23 @@ __device__ __forceinline__ void relax_fc(const Net& net, int l, const float* sfr
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) o[p][mt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    if (mt < MT) {
+  for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+    for (int i = 0; i < 4; ++i) {
+      const int ks = 4 * t + i;
+      if (ks < KS) {
+        float a[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int ks = 4 * t + i;
-          if (ks < KS) {
-            const float a = fr[(mt * KS + ks) * 64];
+        for (int mt = 0; mt < 4; ++mt) a[mt] = mt < MT ? fr[(mt * KS + ks) * 64] : 0.f;
 #pragma unroll
-            for (int p = 0; p < NPAR; ++p) o[p][mt] = mfma16x16x4(a, F[p][t][i], o[p][mt]);
+        for (int mt = 0; mt < 4; ++mt)
+          if (mt < MT) {
+#pragma unroll
+            for (int p = 0; p < NPAR; ++p)
+              if (p < np) o[p][mt] = mfma16x16x4(a[mt], F[p][t][i], o[p][mt]);
           }
-        }
+      }
     }
-  }
 #pragma unroll
   for (int p = 0; p < NPAR; ++p)
 #pragma unroll
@@ -298,10 +545,13 @@ __device__ __forceinline__ void relax_fc(const Net& net, int l, const float* sfr
 
 // lb = acc + sum_i pos(F_i) xl_i + neg(F_i) xh_i over the d0 input dims.
 __device__ __forceinline__ void concretize_rows(int d0, const float* xl, const float* xh, int g,
-                                                const v4f (&F)[NPAR][4], KSum (&accp)[NPAR],
-                                                float (&lb)[NPAR], float (&accv)[NPAR]) {
+                                                int np, const v4f (&F)[NPAR][4],
+                                                KSum (&accp)[NPAR], float (&lb)[NPAR],
+                                                float (&accv)[NPAR]) {
 #pragma unroll
   for (int p = 0; p < NPAR; ++p) {
+    lb[p] = accv[p] = 0.f;
+    if (p >= np) continue;
     accv[p] = group_sum4(accp[p].s, accp[p].c);
     KSum c = accp[p];
 #pragma unroll
@@ -351,9 +601,7 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_crown(
   float* ssl = wbase;                       // slopes [layer][3][FW]
   float* slb = wbase + net.n * 3 * FW;      // seeded-row bounds (2 * FW)
   float* stl = slb + 2 * FW;                // current layer lo/hi (2 * FW)
-  for (int e = threadIdx.x; e < net.nfrag * 64; e += blockDim.x) sfrag[e] = gfrag[e];
-  for (int e = threadIdx.x; e < net.nbias; e += blockDim.x) sbias[e] = gbias[e];
-  __syncthreads();
+  stage_weights(sfrag, sbias, gfrag, gbias, net.nfrag, net.nbias);
   const int d0 = net.d[0];
 
   for (int64_t dom = (int64_t)blockIdx.x * NWAVE + wv; dom < B; dom += (int64_t)gridDim.x * NWAVE) {
@@ -372,7 +620,9 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_crown(
       const int32_t* idx = idx_all + (do_crown ? ca.idx_off[L] : 0);
       const int R = 2 * m;
       const int dS = net.d[L];  // width of the seeded rows after fc_L
-      for (int nt0 = 0; nt0 * 16 < R; nt0 += NPAR) {
+      const int ntiles = (R + 15) / 16;
+      for (int nt0 = 0; nt0 < ntiles; nt0 += NPAR) {
+        const int np = ntiles - nt0 < NPAR ? ntiles - nt0 : NPAR;
         v4f F[NPAR][4];
         KSum accp[NPAR];
         // seed rows: row q < m is +W_L[idx[q]], row m + q is -W_L[idx[q]],
@@ -403,9 +653,10 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_crown(
             }
           if (live && g == 0) accp[p].add(sg * sbias[net.boff[L] + j]);
         }
-        for (int l = L - 1; l >= 0; --l) relax_fc(net, l, sfrag, sbias, ssl, lane, g, F, accp);
+        for (int l = L - 1; l >= 0; --l)
+          relax_fc(net, l, sfrag, sbias, ssl, lane, g, np, F, accp);
         float lb[NPAR], accv[NPAR];
-        concretize_rows(d0, dxl, dxh, g, F, accp, lb, accv);
+        concretize_rows(d0, dxl, dxh, g, np, F, accp, lb, accv);
 #pragma unroll
         for (int p = 0; p < NPAR; ++p) {
           const int row = 16 * (nt0 + p) + r;
@@ -448,9 +699,11 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_crown(
           }
         if (row < Q && g == 0) accp[p].add(spec_acc[row]);
       }
-      for (int l = net.n - 1; l >= 0; --l) relax_fc(net, l, sfrag, sbias, ssl, lane, g, F, accp);
+      const int np = (Q + 15) / 16;
+      for (int l = net.n - 1; l >= 0; --l)
+        relax_fc(net, l, sfrag, sbias, ssl, lane, g, np, F, accp);
       float lb[NPAR], accv[NPAR];
-      concretize_rows(d0, dxl, dxh, g, F, accp, lb, accv);
+      concretize_rows(d0, dxl, dxh, g, np, F, accp, lb, accv);
 #pragma unroll
       for (int p = 0; p < NPAR; ++p) {
         const int row = 16 * p + r;
@@ -484,6 +737,7 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_crown(
 // gP_l = gE_l (mpos ls + mneg up_s) + mneg up_t (torch's clamp subgradient),
 // and torch.optim.Adam's update of alpha on -sum lb, clamped to [0, 1].
 constexpr int AL_MAXL = 7;  // P_l for 8 layers would spill registers
+constexpr int NWAVE_A = 4;  // one wave per SIMD: the full register file per wave
 
 struct AlphaArgs {
   const float* lo[MAXL];
@@ -507,7 +761,7 @@ __device__ __forceinline__ float fwd_a(const float* sfrag, const Net& net, int l
 
 // NL: the exact number of ReLU layers (P_l rows live in NL x 16 registers).
 template <int NL>
-__global__ __launch_bounds__(NWAVE * 64) void k_mlp_alpha(
+__global__ __launch_bounds__(NWAVE_A * 64) void k_mlp_alpha(
     Net net, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
     const float* __restrict__ xl, const float* __restrict__ xh, AlphaArgs aa, int Q,
     const float* __restrict__ spec_rows, const float* __restrict__ spec_acc,
@@ -519,23 +773,28 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_alpha(
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int nb_pad = (net.nbias + 63) & ~63;
-  float* ssl = sbias + nb_pad + wv * (net.n * 4 * FW);  // [layer][ls, us, ut, unst][FW]
-  for (int e = threadIdx.x; e < net.nfrag * 64; e += blockDim.x) sfrag[e] = gfrag[e];
-  for (int e = threadIdx.x; e < net.nbias; e += blockDim.x) sbias[e] = gbias[e];
-  __syncthreads();
+  // per wave: slopes [layer][ls, us, ut, unst][FW], Adam state [layer][alpha, m, v][FW]
+  float* ssl = sbias + nb_pad + wv * (net.n * 7 * FW);
+  float* sad = ssl + net.n * 4 * FW;
+  stage_weights(sfrag, sbias, gfrag, gbias, net.nfrag, net.nbias);
   const int d0 = net.d[0], n = net.n;
 
-  for (int64_t dom = (int64_t)blockIdx.x * NWAVE + wv; dom < B; dom += (int64_t)gridDim.x * NWAVE) {
+  for (int64_t dom = (int64_t)blockIdx.x * NWAVE_A + wv; dom < B;
+       dom += (int64_t)gridDim.x * NWAVE_A) {
     const float* dxl = xl + dom * d0;
     const float* dxh = xh + dom * d0;
     for (int l = 0; l < n; ++l) {
       const int dW = net.d[l + 1];
       float* sl = ssl + l * 4 * FW;
+      float* sa = sad + l * 3 * FW;
       for (int j = lane; j < FW; j += 64) {
-        float ls = 0.f, us = 0.f, ut = 0.f, un = 0.f;
+        float ls = 0.f, us = 0.f, ut = 0.f, un = 0.f, a = 0.f, m1 = 0.f, m2 = 0.f;
         if (j < dW) {
-          Relax s = relax(aa.lo[l][dom * dW + j], aa.hi[l][dom * dW + j]);
-          const float a = aa.alpha[l][dom * dW + j];
+          const int64_t ai = dom * dW + j;
+          Relax s = relax(aa.lo[l][ai], aa.hi[l][ai]);
+          a = aa.alpha[l][ai];
+          m1 = aa.m1[l][ai];
+          m2 = aa.m2[l][ai];
           ls = s.active ? 1.f : (s.unstable ? a : 0.f);
           us = s.up_s;
           ut = s.up_t;
@@ -545,6 +804,9 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_alpha(
         sl[FW + j] = us;
         sl[2 * FW + j] = ut;
         sl[3 * FW + j] = un;
+        sa[j] = a;
+        sa[FW + j] = m1;
+        sa[2 * FW + j] = m2;
       }
     }
     __threadfence_block();
@@ -589,15 +851,15 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_alpha(
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) o[mt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-          if (mt < MT) {
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
+          for (int i = 0; i < 4; ++i) {
+            const int ks = 4 * t + i;
+            if (ks < KS) {
 #pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                const int ks = 4 * t + i;
-                if (ks < KS) o[mt] = mfma16x16x4(fr[(mt * KS + ks) * 64], F[t][i], o[mt]);
-              }
+              for (int mt = 0; mt < 4; ++mt)
+                if (mt < MT) o[mt] = mfma16x16x4(fr[(mt * KS + ks) * 64], F[t][i], o[mt]);
+            }
           }
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) F[mt] = o[mt];
@@ -633,15 +895,13 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_alpha(
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) o[mt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-        if (mt < MT) {
+      for (int t = 0; t < 4; ++t)
+        if (t < T) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t)
-            if (t < T) {
+          for (int i = 0; i < 4; ++i)
 #pragma unroll
-              for (int i = 0; i < 4; ++i)
-                o[mt] = mfma16x16x4(fwd_a(sfrag, net, l, mt, t, i, lane), G[t][i], o[mt]);
-            }
+            for (int mt = 0; mt < 4; ++mt)
+              if (mt < MT) o[mt] = mfma16x16x4(fwd_a(sfrag, net, l, mt, t, i, lane), G[t][i], o[mt]);
         }
       const float* sl = ssl + l * 4 * FW;
       const int dW = dM;
@@ -666,18 +926,18 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_alpha(
           }
           const float ga = s + cs;
           if (r == 0 && j < dW && sl[3 * FW + j] != 0.f) {
-            const int64_t ai = dom * dW + j;
+            float* sa = sad + l * 3 * FW;
             const float gr = -ga;
-            float mi = aa.m1[l][ai];
+            float mi = sa[FW + j];
             mi = mi + (1.f - b1) * (gr - mi);
-            float vi = aa.m2[l][ai] * b2;
+            float vi = sa[2 * FW + j] * b2;
             vi = vi + ((1.f - b2) * gr) * gr;
             const float denom = sqrtf(vi) / bc2 + eps;
-            float pa = aa.alpha[l][ai] + neg_step * (mi / denom);
+            float pa = sa[j] + neg_step * (mi / denom);
             pa = fminf(fmaxf(pa, 0.f), 1.f);
-            aa.m1[l][ai] = mi;
-            aa.m2[l][ai] = vi;
-            aa.alpha[l][ai] = pa;
+            sa[FW + j] = mi;
+            sa[2 * FW + j] = vi;
+            sa[j] = pa;
           }
           const bool mp = pv >= 0.f, mn = pv <= 0.f;
           float gp = ge * ((mp ? sl[j] : 0.f) + (mn ? sl[FW + j] : 0.f));
@@ -685,6 +945,19 @@ __global__ __launch_bounds__(NWAVE * 64) void k_mlp_alpha(
           G[t][i] = (live_row && j < dW) ? gp : 0.f;
         }
     }
+    // write the updated Adam state back (coalesced)
+    __threadfence_block();
+    for (int l = 0; l < n; ++l) {
+      const int dW = net.d[l + 1];
+      const float* sa = sad + l * 3 * FW;
+      for (int j = lane; j < dW; j += 64) {
+        const int64_t ai = dom * dW + j;
+        aa.alpha[l][ai] = sa[j];
+        aa.m1[l][ai] = sa[FW + j];
+        aa.m2[l][ai] = sa[2 * FW + j];
+      }
+    }
+    __threadfence_block();
   }
 }
 
@@ -736,12 +1009,12 @@ int cu_count() {
 
 // Persistent grid: as many workgroups as fit on the CUs at once given the
 // LDS footprint (160 KB per CU), capped by the amount of work.
-int persistent_grid(int64_t B, size_t lds_bytes) {
+int persistent_grid(int64_t B, size_t lds_bytes, int nwave = NWAVE) {
   int per_cu = (int)((160 * 1024) / (lds_bytes > 0 ? lds_bytes : 1));
   if (per_cu < 1) per_cu = 1;
   if (per_cu > 2) per_cu = 2;
   int64_t grid = (int64_t)cu_count() * per_cu;
-  const int64_t need = (B + NWAVE - 1) / NWAVE;
+  const int64_t need = (B + nwave - 1) / nwave;
   if (need < grid) grid = need;
   return (int)(grid < 1 ? 1 : grid);
 }
@@ -782,7 +1055,7 @@ extern "C" int vc_mlp_zono_bounds(const int32_t* dims, int n_relu, const float* 
   if (rc != VC_OK) return rc;
   if (!frag_fwd || !bias_cat || !xl || !xh || !lo_out || !hi_out || !overflow || B < 0)
     return VC_ERR_ARG;
-  if (net.d[0] + 1 > ZNT * 16) return VC_ERR_UNSUPPORTED;
+  if (net.d[0] + 1 > ZNT_NARROW * 16) return VC_ERR_UNSUPPORTED;
   if (B == 0) return VC_OK;
   ZonoArgs za;
   for (int l = 0; l < MAXL; ++l) {
@@ -792,11 +1065,26 @@ extern "C" int vc_mlp_zono_bounds(const int32_t* dims, int n_relu, const float* 
   }
   const size_t lds = ((size_t)net.nfrag * 64 + net.nbias) * sizeof(float);
   if (lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_mlp_zono),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  const size_t lds_c = lds + ((size_t)((net.nbias + 63) & ~63) - net.nbias +
+                              (size_t)ZC_W * 2 * FW + FW) * sizeof(float);
+  if (lds_c > 160 * 1024) return VC_ERR_UNSUPPORTED;
+  const void* fn_n = reinterpret_cast<const void*>(&k_mlp_zono<ZNT_NARROW, NWAVE>);
+  const void* fn_c = reinterpret_cast<const void*>(&k_mlp_zono_coop);
+  if (hipFuncSetAttribute(fn_n, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+          hipSuccess ||
+      hipFuncSetAttribute(fn_c, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_c) !=
+          hipSuccess)
     return VC_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(k_mlp_zono, dim3(persistent_grid(B, lds)), dim3(NWAVE * 64), lds,
-                     (hipStream_t)stream, net, frag_fwd, bias_cat, B, xl, xh, za, overflow);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL((k_mlp_zono<ZNT_NARROW, NWAVE>), dim3(persistent_grid(B, lds)),
+                     dim3(NWAVE * 64), lds, st, net, frag_fwd, bias_cat, B, xl, xh, za,
+                     overflow, 0);
+  // second pass over the domains that did not fit: one workgroup per
+  // flagged domain, each workgroup scanning a strided share of the flags
+  int64_t gw = cu_count();
+  if (gw > B) gw = B;
+  hipLaunchKernelGGL(k_mlp_zono_coop, dim3((unsigned)gw), dim3(ZC_W * 64), lds_c, st, net,
+                     frag_fwd, bias_cat, B, xl, xh, za, overflow);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }
@@ -828,7 +1116,7 @@ extern "C" int vc_mlp_alpha_iter(const int32_t* dims, int n_relu, const float* f
     if (in && (!aa.lo[l] || !aa.hi[l] || !aa.alpha[l] || !aa.m1[l] || !aa.m2[l])) return VC_ERR_ARG;
   }
   const size_t lds = ((size_t)net.nfrag * 64 + ((net.nbias + 63) & ~63) +
-                      (size_t)NWAVE * net.n * 4 * FW) * sizeof(float);
+                      (size_t)NWAVE_A * net.n * 7 * FW) * sizeof(float);
   if (lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
   const void* fn = nullptr;
   switch (n_relu) {
@@ -842,7 +1130,7 @@ extern "C" int vc_mlp_alpha_iter(const int32_t* dims, int n_relu, const float* f
   }
   if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return VC_ERR_UNSUPPORTED;
-  const dim3 grid(persistent_grid(B, lds)), block(NWAVE * 64);
+  const dim3 grid(persistent_grid(B, lds, NWAVE_A)), block(NWAVE_A * 64);
   const float ns = (float)(-step_size), b2s = (float)bc2_sqrt;
   hipStream_t st = (hipStream_t)stream;
 #define VC_ALPHA_CASE(NLV)                                                                   \
