@@ -63,9 +63,12 @@ int vc_ibp_conv(const float *l, const float *h, int64_t B, int C_in, int H,
 /* relu of the interval forward: intersect root bounds (n, nullable) and
  * split clamps (B, n, nullable), repair hi = max(hi, lo), write the
  * pre-activation bounds sb_lo/sb_hi (B, n) and, when post_lo/post_hi are
- * non-NULL, the clamp(min=0) outputs.
+ * non-NULL, the clamp(min=0) outputs.  l/h NULL (both) means an unbounded
+ * input interval; the root bounds are then required and the result is the
+ * root broadcast to B domains intersected with the clamps.
  * Replaces the relu branch of _ibp_forward_graph_batched
- * (verify_zono_bnb.py:1114-1129). */
+ * (verify_zono_bnb.py:1114-1129) and, with l/h NULL, the clamped layers of
+ * the no-reforward domain bounds (verify_milp.py:2706-2717). */
 int vc_ibp_relu(const float *l, const float *h, int64_t B, int n,
                 const float *root_lo, const float *root_hi, const float *cl,
                 const float *ch, float *sb_lo, float *sb_hi, float *post_lo,
@@ -212,15 +215,45 @@ int vc_alpha_grad_input(const float *A, const float *xl, const float *xh,
                         const float *bias0, int n1, float *g_out,
                         vc_stream_t stream);
 
-/* Adam step on n parameters with torch.optim.Adam's update order
- * (betas b1, b2, eps; step is the 1-based step count), minimising
- * -lb: grad = -sign_grad, followed by the projection clamp to
- * [lo_clamp, hi_clamp].  step_size = lr / (1 - b1^step) and
- * bc2_sqrt = sqrt(1 - b2^step) are passed in as host-computed doubles. */
+/* Adam step on n parameters with torch.optim.Adam's update order and
+ * rounding (betas b1, b2, eps as the Python floats torch holds; the weights
+ * 1 - b are formed in double and rounded to fp32), minimising -lb: the
+ * gradient is -lb_grad; m = fma(1-b1, g - m, m), v = fma((1-b2) g, g, v b2),
+ * p += (-step_size * m) / (sqrt(v) / bc2_sqrt + eps), then the projection
+ * clamp to [lo_clamp, hi_clamp].  step_size = lr / (1 - b1^step) and
+ * bc2_sqrt = sqrt(1 - b2^step) (step 1-based) are host-computed doubles. */
 int vc_adam_step(float *param, const float *lb_grad, float *exp_avg,
-                 float *exp_avg_sq, int64_t n, float b1, float b2, float eps,
+                 float *exp_avg_sq, int64_t n, double b1, double b2, double eps,
                  double step_size, double bc2_sqrt, float lo_clamp,
                  float hi_clamp, vc_stream_t stream);
+
+/* ReLU-split beta, one Adam step on n parameters: the backward sees the
+ * signed beta (beta * sign), lb_grad_signed is d lb / d signed (the gbeta of
+ * vc_alpha_grad_reduce), so the parameter gradient is sign * lb_grad_signed.
+ * torch.optim.Adam update order on -lb as vc_adam_step, then beta clamped
+ * to >= 0 and beta_signed = beta * sign written for the next evaluation.
+ * Replaces the beta half of the Adam loop of verify_milp.py:2785-2807
+ * (rsb = beta * sign at :2791, opt.step() and beta.clamp_(min=0)). */
+int vc_beta_adam_step(float *beta, const float *sign,
+                      const float *lb_grad_signed, float *exp_avg,
+                      float *exp_avg_sq, int64_t n, double b1, double b2,
+                      double eps, double step_size, double bc2_sqrt,
+                      float *beta_signed, vc_stream_t stream);
+
+/* sign (n) of each split neuron from dense clamps cl/ch (n): -1 where
+ * cl == 0 (ON), else +1 where ch == 0 (OFF), else 0.
+ * Replaces verify_milp.py:2777-2784. */
+int vc_split_beta_sign(const float *cl, const float *ch, int64_t n,
+                       float *sign, vc_stream_t stream);
+
+/* Dense clamps of relu layer L for D domains from per-domain split lists
+ * layer/neuron/side (D, S) int64 (layer -1 marks an unused slot; side 0 =
+ * OFF: z <= 0, side 1 = ON: z >= 0): cl/ch (D, n) get -inf/+inf except 0
+ * at the split neurons, and sign (nullable) as vc_split_beta_sign.
+ * Replaces the per-domain clamp-building loop of verify_milp.py:2738-2752. */
+int vc_split_clamps(const int64_t *layer, const int64_t *neuron,
+                    const int64_t *side, int64_t D, int S, int64_t L, int n,
+                    float *cl, float *ch, float *sign, vc_stream_t stream);
 
 /* best = max(best, lb) elementwise (first call: copy when init != 0), and
  * out[0] = max over best, out[1] = 1.0 if all best > 0 else 0.0.
@@ -298,7 +331,7 @@ int vc_mlp_alpha_iter(const int32_t *dims, int n_relu, const float *frag_bwd,
                       const float *const *hi, float *const *alpha,
                       float *const *exp_avg, float *const *exp_avg_sq, int Q,
                       const float *spec_rows, const float *spec_acc,
-                      float *lb_out, float b1, float b2, float eps,
+                      float *lb_out, double b1, double b2, double eps,
                       double step_size, double bc2_sqrt, vc_stream_t stream);
 
 /* ---- Input-split BaB step ---------------------------------------------- */

@@ -393,19 +393,52 @@ def alpha_crown_batched(xl, xh, gg, spec_ew, n_iters=10, lr=0.25,
     return best
 
 
+def split_domain_bounds(xl, xh, gg, sb_root, relu_clamps, no_reforward=False):
+    """Pre-relu bounds of a batch of ReLU-split domains (the inner
+    ``_sb_for_domains`` of verify_milp.py:2698-2721).
+
+    ``no_reforward``: the root bounds broadcast to every domain, intersected
+    with the split clamps where a layer has any (then crossing repair).
+    Otherwise an IBP forward of the (B, n_in) boxes with the clamps and the
+    root bounds intersected at every relu."""
+    if no_reforward:
+        B = xl.shape[0]
+        sb = {}
+        for L, (lo_r, hi_r) in sb_root.items():
+            lo = lo_r.reshape(1, -1).expand(B, -1).clone()
+            hi = hi_r.reshape(1, -1).expand(B, -1).clone()
+            if relu_clamps and L in relu_clamps:
+                cl, ch = relu_clamps[L]
+                lo = torch.maximum(lo, cl)
+                hi = torch.minimum(hi, ch)
+                hi = torch.maximum(hi, lo)
+            sb[L] = (lo, hi)
+        return sb
+    root = {L: (lo.reshape(-1), hi.reshape(-1)) for L, (lo, hi) in sb_root.items()}
+    return ibp_forward_batched(xl, xh, gg, relu_clamps=relu_clamps or None,
+                               root_sb=root)
+
+
 def beta_crown_bound(sb, xl, xh, gg, spec_ew, beta_sign, n_iters=10, lr=0.25,
-                     return_trace=False):
+                     return_trace=False, alpha_init=None):
     """Per-domain joint alpha/beta bound of one batch of ReLU-split domains
     (verify_milp.py:2762-2807).
 
-    alpha starts at (up_s > 0.5) * unstable on ``sb``; beta starts at 0 and
-    enters the backward as beta * sign at each split neuron (sign +1 for an
-    OFF split, -1 for ON).  Adam on -sum(lb); alpha clamped to [0, 1], beta
-    to >= 0; stops when every best lb is > 0.  Returns best (B, Q).
+    alpha starts at the root alpha ``alpha_init[L]`` (n_L,) broadcast to
+    every domain where given, else at (up_s > 0.5) * unstable on ``sb``;
+    beta starts at 0 and enters the backward as beta * sign at each split
+    neuron (sign +1 for an OFF split, -1 for ON).  Adam on -sum(lb); alpha
+    clamped to [0, 1], beta to >= 0; stops when every best lb is > 0.
+    Returns best (B, Q); with ``return_trace`` also the number of
+    evaluated iterations.
     """
     dt = xl.dtype
     alpha = {}
     for L, (lo, hi) in sb.items():
+        if alpha_init is not None and L in alpha_init:
+            a0 = alpha_init[L].to(dt).reshape(1, -1).expand(lo.shape[0], -1)
+            alpha[L] = a0.detach().clone().requires_grad_(True)
+            continue
         _, up_s, _, _, _, unstable = make_slopes(lo, hi)
         alpha[L] = ((up_s > 0.5).to(dt) * unstable.to(dt)).detach().clone() \
             .requires_grad_(True)

@@ -1,0 +1,314 @@
+"""GPU parity of the ReLU-split alpha/beta bound (the batch body of the
+reference's _ibp_crown_bab, verify_milp.py:2698-2807) against the oracle.
+
+Clamps and beta signs: exact.  Domain bounds: the interval tolerance of
+test_gpu_parity.  One evaluation with given alpha/beta (bound, both
+gradients, Adam update): the strict tolerances of the teacher-forced test.
+Free-running best bounds: 1e-4 rel / 1e-5 abs after one Adam step, the
+Adam drift criterion of test_gpu_parity after more.  Evaluation counts:
+exact."""
+import pytest
+import torch
+
+from oracle import ref_bound as rb
+from vibecheck_amd import verify_milp as vm
+from vibecheck_amd import verify_zono_bnb as vz
+from vibecheck_amd import workloads as wk
+from vibecheck_amd._lib import call, ptr, stream
+
+import _util
+from test_gpu_parity import (assert_adam_drift, assert_bounds, assert_interval, cpu,
+                             spec_scale)
+from test_oracle_bounds import beta_known_answer_net
+
+pytestmark = pytest.mark.gpu
+F32 = torch.float32
+# best lb after one or two evaluations (one Adam step in between)
+RTOL_LB, ATOL_LB = 1e-4, 1e-5
+
+
+def split_case(widths, D, S, eps, seed, gpu):
+    """A C4-shaped case: one box, root IBP bounds, D domains of S splits
+    drawn from the root-unstable neurons."""
+    Ws, bs = wk.mlp_params(widths, seed=seed, bias_std=0.05)
+    gg_c = wk.mlp_gg(Ws, bs, dtype=F32)
+    gg_g = wk.mlp_gg(Ws, bs, device=gpu, dtype=F32)
+    xl, xh = wk.linf_boxes(1, widths[0], eps, seed=seed + 1, dtype=F32)
+    root = rb.ibp_forward_batched(xl, xh, gg_c)
+    root = {L: (lo[0], hi[0]) for L, (lo, hi) in root.items()}
+    un = [(L, int(j)) for L in sorted(root)
+          for j in ((root[L][0] < 0) & (root[L][1] > 0)).nonzero().flatten()]
+    layer, neuron, side = wk.relu_split_domains(un, n_domains=D, n_splits=S, seed=seed + 2)
+    return gg_c, gg_g, xl[0], xh[0], root, (layer, neuron, side)
+
+
+def test_split_clamps_and_signs_bit_exact(gpu):
+    widths = [20, 24, 24, 24, 3]
+    _, _, _, _, root, (layer, neuron, side) = split_case(widths, 300, 8, 0.5, 3, gpu)
+    # unused slots (-1) must be ignored
+    layer = layer.clone()
+    layer[::7, -1] = -1
+    ref = wk.relu_clamps_from_splits(layer, neuron, side, widths[1:-1])
+    ref_sg = rb.beta_signs_from_clamps(ref)
+    got, got_sg = vm._split_clamps_batched(layer.to(gpu), neuron.to(gpu), side.to(gpu),
+                                           widths[1:-1], gpu)
+    assert sorted(got) == sorted(ref)
+    for L in ref:
+        assert torch.equal(cpu(got[L][0]), ref[L][0])
+        assert torch.equal(cpu(got[L][1]), ref[L][1])
+        assert torch.equal(cpu(got_sg[L]), ref_sg[L])
+        sg2 = torch.empty_like(got_sg[L])
+        call('vc_split_beta_sign', ptr(got[L][0]), ptr(got[L][1]), sg2.numel(), ptr(sg2),
+             stream())
+        assert torch.equal(cpu(sg2), ref_sg[L])
+
+
+@pytest.mark.parametrize('no_reforward', [False, True])
+def test_sb_for_domains_parity(gpu, no_reforward):
+    widths = [40, 32, 32, 32, 5]
+    gg_c, gg_g, xl, xh, root, (layer, neuron, side) = split_case(widths, 200, 6, 0.3, 5, gpu)
+    clamps = wk.relu_clamps_from_splits(layer, neuron, side, widths[1:-1])
+    D = layer.shape[0]
+    xlb, xhb = xl.expand(D, -1).clone(), xh.expand(D, -1).clone()
+    ref = rb.split_domain_bounds(xlb, xhb, gg_c, root, clamps, no_reforward=no_reforward)
+    got = vm._sb_for_domains(
+        xl.to(gpu), xh.to(gpu), gg_g, {L: (a.to(gpu), b.to(gpu)) for L, (a, b) in root.items()},
+        {L: (a.to(gpu), b.to(gpu)) for L, (a, b) in clamps.items()}, D, gpu, F32,
+        no_reforward=no_reforward)
+    assert sorted(got) == sorted(ref)
+    for L in ref:
+        assert_interval((cpu(got[L][0]), cpu(got[L][1])), ref[L], f'split sb L{L}')
+
+
+def test_beta_gradient_matches_autograd(gpu):
+    widths = [6, 30, 30, 30, 4]
+    gg_c, gg_g, xl, xh, root, (layer, neuron, side) = split_case(widths, 64, 5, 0.5, 9, gpu)
+    clamps = wk.relu_clamps_from_splits(layer, neuron, side, widths[1:-1])
+    D = layer.shape[0]
+    xlb, xhb = xl.expand(D, -1).clone(), xh.expand(D, -1).clone()
+    sb = rb.split_domain_bounds(xlb, xhb, gg_c, root, clamps)
+    sgn = rb.beta_signs_from_clamps(clamps)
+    g = torch.Generator().manual_seed(11)
+    alpha = {L: torch.rand(lo.shape, generator=g, dtype=torch.float64) for L, (lo, _) in sb.items()}
+    beta = {L: torch.rand(s.shape, generator=g, dtype=torch.float64) * 0.5 * s.double()
+            for L, s in sgn.items()}
+    a_ref = {L: a.clone().requires_grad_(True) for L, a in alpha.items()}
+    b_ref = {L: b.clone().requires_grad_(True) for L, b in beta.items()}
+    spec, _ = _util.spec_for(4)
+    gg64 = _util.to_dev(gg_c, 'cpu', torch.float64)
+    sb64 = {L: (lo.double(), hi.double()) for L, (lo, hi) in sb.items()}
+    lb = rb.spec_backward_batched(sb64, xlb.double(), xhb.double(), gg64, spec,
+                                  alpha_at_layer=a_ref, relu_split_beta=b_ref)
+    lb.sum().backward()
+    se_g = {q: (w.float().to(gpu), b) for q, (w, b) in spec.items()}
+    Wq, bq = vz._spec_rows(se_g, gpu)
+    sbg = {L: (lo.to(gpu), hi.to(gpu)) for L, (lo, hi) in sb.items()}
+    a_g = {L: a.float().to(gpu) for L, a in alpha.items()}
+    b_g = {L: b.float().to(gpu) for L, b in beta.items()}
+    ga = {L: torch.zeros_like(a) for L, a in a_g.items()}
+    gb = {L: torch.zeros_like(b) for L, b in b_g.items()}
+    glb = vz._alpha_backward_and_grad(sbg, xlb.to(gpu), xhb.to(gpu), gg_g, Wq, bq, a_g, True,
+                                      ga, beta=b_g, gbeta=gb)
+    assert_bounds(glb, lb.detach().float(), 'alpha/beta lb', rtol=1e-4, atol=1e-5)
+    for name, got, ref in (('alpha', ga, a_ref), ('beta', gb, b_ref)):
+        for L in ref:
+            r = ref[L].grad.float()
+            scale = r.abs().max().clamp(min=1.0)
+            err = (cpu(got[L]) - r).abs().max() / scale
+            assert float(err) < 1e-4, (name, L, float(err))
+
+
+def test_beta_known_answer(gpu):
+    """The crafted net of the oracle's known-answer test: the OFF child
+    closes through beta at the 5th evaluation with lb ~ 0.4, the ON child
+    stays exactly at its true min -1.6, and without beta the OFF child
+    stays at -1.6."""
+    gg = _util.to_dev(beta_known_answer_net(), gpu)
+    inf = float('inf')
+    xl = torch.tensor([-1.0, -1.0], device=gpu)
+    xh = torch.tensor([1.0, 1.0], device=gpu)
+    root = rb.ibp_forward_batched(xl.cpu().double()[None], xh.cpu().double()[None],
+                                  beta_known_answer_net())
+    root = {L: (lo[0].float().to(gpu), hi[0].float().to(gpu)) for L, (lo, hi) in root.items()}
+    cl = torch.tensor([[-inf, -inf], [0.0, -inf]], device=gpu)
+    ch = torch.tensor([[0.0, inf], [inf, inf]], device=gpu)
+    spec = {0: (torch.tensor([1.0], device=gpu), 0.0)}
+    best, n = vm._ibp_crown_bab_bound(gg, xl, xh, root, {0: (cl, ch)}, spec, gpu, F32,
+                                      alpha_iters=20, lr=0.25, return_trace=True)
+    assert n == 20
+    assert float(best[1, 0]) == -1.6 or abs(float(best[1, 0]) + 1.6) < 1e-6
+    assert 0.39 < float(best[0, 0]) <= 0.4 + 1e-6
+    best5, n5 = vm._ibp_crown_bab_bound(gg, xl, xh, root, {0: (cl[:1], ch[:1])}, spec, gpu,
+                                        F32, alpha_iters=20, lr=0.25, return_trace=True)
+    assert n5 == 5
+    assert 0.39 < float(best5[0, 0]) <= 0.4 + 1e-6
+    nob = vm._ibp_crown_bab_bound(gg, xl, xh, root, {0: (cl, ch)}, spec, gpu, F32,
+                                  alpha_iters=20, lr=0.25,
+                                  beta_sign={0: torch.zeros(2, 2, device=gpu)})
+    assert abs(float(nob[0, 0]) + 1.6) < 1e-6
+
+
+def reduced_c4(gpu, seed=13):
+    """784 -> [96]x3 -> 10, one box of eps 0.03, 256 domains of 8 splits."""
+    widths = [784, 96, 96, 96, 10]
+    gg_c, gg_g, xl, xh, root, (layer, neuron, side) = split_case(widths, 256, 8, 0.03, seed, gpu)
+    clamps = wk.relu_clamps_from_splits(layer, neuron, side, widths[1:-1])
+    D = layer.shape[0]
+    xlb, xhb = xl.expand(D, -1).clone(), xh.expand(D, -1).clone()
+    return widths, gg_c, gg_g, xlb, xhb, root, (layer, neuron, side), clamps
+
+
+def assert_ulps(got, ref, what, old=None, n_ulp=2):
+    """|got - ref| <= n_ulp units in the last place (fp32) of the larger of
+    |ref| and |old| (the value before the update: an update that cancels
+    most of it keeps the absolute rounding of its terms)."""
+    g = cpu(got).float()
+    r = ref.detach().float()
+    mag = r.abs() if old is None else torch.maximum(r.abs(), cpu(old).float().abs())
+    ulp = torch.nextafter(mag, torch.tensor(float('inf'))) - mag
+    ok = (g - r).abs() <= n_ulp * ulp
+    n_bad = int((~ok).sum())
+    assert n_bad == 0, (what, n_bad, float((g - r).abs().max()))
+    if n_bad == 0 and not torch.equal(g, r):
+        print(f'{what}: {float((g == r).float().mean()):.4f} bit-exact')
+
+
+def test_alpha_beta_step_map_teacher_forced(gpu):
+    """Each iteration of the joint alpha/beta loop, fed the oracle's exact
+    state: the lb of the backward with alpha and the signed beta (bound
+    tolerance), d lb / d alpha and d lb / d beta (1e-4 of the layer's
+    largest gradient, as the alpha gradient test), and one Adam update of
+    both parameter sets from torch.optim.Adam's own state: within 2 ulps
+    (the kernels use torch's operation order -- fused lerp and addcmul,
+    (-step * m) / denom -- and reproduce torch's CPU update bit for bit on
+    all but ~0.4% of entries, where torch's vectorised denominator differs
+    by one ulp)."""
+    widths, gg_c, gg_g, xlb, xhb, root, _, clamps = reduced_c4(gpu)
+    sb = rb.split_domain_bounds(xlb, xhb, gg_c, root, clamps)
+    sgn = rb.beta_signs_from_clamps(clamps)
+    spec, _ = _util.spec_for(10, dtype=F32)
+    alpha = {}
+    for L, (lo, hi) in sb.items():
+        _, up_s, _, _, _, un = rb.make_slopes(lo, hi)
+        alpha[L] = ((up_s > 0.5).float() * un.float()).requires_grad_(True)
+    beta = {L: torch.zeros_like(s).requires_grad_(True) for L, s in sgn.items()}
+    params = list(alpha.values()) + list(beta.values())
+    opt = torch.optim.Adam(params, lr=0.25)
+    se_g = {q: (w.to(gpu), b) for q, (w, b) in spec.items()}
+    Wq, bq = vz._spec_rows(se_g, gpu)
+    sbg = {L: (lo.to(gpu), hi.to(gpu)) for L, (lo, hi) in sb.items()}
+    sg_g = {L: s.to(gpu) for L, s in sgn.items()}
+    xl_g, xh_g = xlb.to(gpu), xhb.to(gpu)
+    gg64 = _util.to_dev(gg_c, 'cpu', torch.float64)
+    sb64 = {L: (lo.double(), hi.double()) for L, (lo, hi) in sb.items()}
+    spec64 = {q: (w.double(), b) for q, (w, b) in spec.items()}
+    for it in range(6):
+        opt.zero_grad()
+        rsb = {L: beta[L] * sgn[L] for L in beta}
+        lb, A, acc = rb.spec_backward_batched(sb, xlb, xhb, gg_c, spec, alpha_at_layer=alpha,
+                                              relu_split_beta=rsb, return_input_linear=True)
+        a_g = {L: a.detach().to(gpu) for L, a in alpha.items()}
+        bs_g = {L: r.detach().to(gpu) for L, r in rsb.items()}
+        ga = {L: torch.zeros_like(a) for L, a in a_g.items()}
+        gb = {L: torch.zeros_like(b) for L, b in bs_g.items()}
+        glb = vz._alpha_backward_and_grad(sbg, xl_g, xh_g, gg_g, Wq, bq, a_g, True, ga,
+                                          beta=bs_g, gbeta=gb)
+        assert_bounds(glb, lb.detach(), f'step map lb, it {it}',
+                      scale=spec_scale(A, acc, xlb, xhb))
+        (-lb.sum()).backward()
+        # gradients against fp64 autograd of the same state: torch's clamp
+        # subgradient switches on the sign of each pre-relaxation entry, so an
+        # entry within fp32 noise of 0 flips between any two fp32 evaluations
+        a64 = {L: a.detach().double().requires_grad_(True) for L, a in alpha.items()}
+        b64 = {L: b.detach().double().requires_grad_(True) for L, b in beta.items()}
+        lb64 = rb.spec_backward_batched(
+            sb64, xlb.double(), xhb.double(), gg64, spec64, alpha_at_layer=a64,
+            relu_split_beta={L: b64[L] * sgn[L].double() for L in b64})
+        lb64.sum().backward()
+        for name, got, ref in (('alpha', {L: ga[L] for L in alpha}, a64),
+                               ('beta', {L: gb[L] * sg_g[L] for L in beta}, b64)):
+            for L in ref:
+                r = ref[L].grad.float()                   # d lb / d param
+                scale = r.abs().max().clamp(min=1.0)
+                err = (cpu(got[L]) - r).abs().max() / scale
+                assert float(err) < 1e-4, (it, name, L, float(err))
+        # one Adam step of both parameter sets from torch's state, on torch's gradient
+        st = opt.state
+        b1, b2, eps, lr = 0.9, 0.999, 1e-8, 0.25
+        step = it + 1
+        dev_state = {}
+        before = {}
+        for p in params:
+            m = st[p]['exp_avg'].clone() if p in st else torch.zeros_like(p)
+            v = st[p]['exp_avg_sq'].clone() if p in st else torch.zeros_like(p)
+            before[p] = (p.detach().clone(), m.clone(), v.clone())
+            dev_state[p] = (p.detach().clone().to(gpu), m.to(gpu), v.to(gpu),
+                            (-p.grad).contiguous().to(gpu))
+        opt.step()
+        with torch.no_grad():
+            for a in alpha.values():
+                a.clamp_(0.0, 1.0)
+            for b in beta.values():
+                b.clamp_(min=0.0)
+        bc1, bc2 = 1 - b1 ** step, (1 - b2 ** step) ** 0.5
+        for L, a in alpha.items():
+            pg, m, v, g = dev_state[a]
+            call('vc_adam_step', ptr(pg), ptr(g), ptr(m), ptr(v), pg.numel(), b1, b2, eps,
+                 lr / bc1, bc2, 0.0, 1.0, stream())
+            p0, m0, v0 = before[a]
+            assert_ulps(pg, a.detach(), (it, 'alpha', L), old=p0)
+            assert_ulps(m, st[a]['exp_avg'], (it, 'alpha m', L), old=m0)
+            assert_ulps(v, st[a]['exp_avg_sq'], (it, 'alpha v', L), old=v0)
+        for L, b in beta.items():
+            pg, m, v, _ = dev_state[b]
+            # the kernel takes d lb / d signed beta; torch's grad is d(-lb)/d beta
+            gsig = (-b.grad * sgn[L]).contiguous().to(gpu)
+            out_s = torch.empty_like(pg)
+            call('vc_beta_adam_step', ptr(pg), ptr(sg_g[L]), ptr(gsig), ptr(m), ptr(v),
+                 pg.numel(), b1, b2, eps, lr / bc1, bc2, ptr(out_s), stream())
+            p0 = before[b][0]
+            assert_ulps(pg, b.detach(), (it, 'beta', L), old=p0)
+            assert_ulps(out_s, (b * sgn[L]).detach(), (it, 'signed beta', L), old=p0)
+
+
+@pytest.mark.parametrize('mode', ['reforward_q9', 'reforward_q1', 'no_reforward_warm'])
+def test_ibp_crown_bab_bound_parity(gpu, mode):
+    """The free-running loop on a reduced ReLU-split workload: the evaluation
+    count matches the oracle exactly; the best lb after 1 and 2 evaluations
+    within the bound tolerance; after 5 and 10, where Adam's per-component
+    normalisation has turned fp32 reduction noise in near-zero gradient
+    components into full +-lr steps (the fp32 oracle itself drifts from the
+    fp64 oracle by up to 1e-4 relative after 10 steps on this case), at
+    least 99% of the entries within 1e-4 relative and all within 1e-3.
+    The step map itself is pinned exactly by the teacher-forced test."""
+    widths = [784, 96, 96, 96, 10]
+    gg_c, gg_g, xl, xh, root, (layer, neuron, side) = split_case(widths, 256, 8, 0.03, 13, gpu)
+    clamps = wk.relu_clamps_from_splits(layer, neuron, side, widths[1:-1])
+    D = layer.shape[0]
+    spec, _ = _util.spec_for(10, dtype=F32)
+    if mode == 'reforward_q1':
+        spec = {0: spec[0]}
+    no_ref = mode == 'no_reforward_warm'
+    g = torch.Generator().manual_seed(17)
+    a_init = ({L: torch.rand(lo.shape, generator=g) for L, (lo, _) in root.items()}
+              if no_ref else None)
+    xlb, xhb = xl.expand(D, -1).clone(), xh.expand(D, -1).clone()
+    sb = rb.split_domain_bounds(xlb, xhb, gg_c, root, clamps, no_reforward=no_ref)
+    sgn = rb.beta_signs_from_clamps(clamps)
+    lay_g, neu_g, sid_g = layer.to(gpu), neuron.to(gpu), side.to(gpu)
+    cl_g, _ = vm._split_clamps_batched(lay_g, neu_g, sid_g, widths[1:-1], gpu)
+    root_g = {L: (a.to(gpu), b.to(gpu)) for L, (a, b) in root.items()}
+    se_g = {q: (w.to(gpu), b) for q, (w, b) in spec.items()}
+    for k in (1, 2, 5, 10):
+        ref, n_ref = rb.beta_crown_bound(sb, xlb, xhb, gg_c, spec, sgn, n_iters=k, lr=0.25,
+                                         return_trace=True, alpha_init=a_init)
+        got, n_got = vm._ibp_crown_bab_bound(
+            gg_g, xl.to(gpu), xh.to(gpu), root_g, cl_g, se_g, gpu, F32, alpha_iters=k,
+            lr=0.25, no_reforward=no_ref,
+            alpha_init=None if a_init is None else {L: a.to(gpu) for L, a in a_init.items()},
+            return_trace=True)
+        assert n_got == n_ref, (k, n_got, n_ref)
+        if k <= 2:
+            assert_bounds(got, ref, f'{mode} best lb, {k} it', rtol=RTOL_LB, atol=ATOL_LB)
+        else:
+            assert_adam_drift(got, ref, f'{mode} best lb, {k} it')

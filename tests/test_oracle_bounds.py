@@ -307,6 +307,117 @@ def test_beta_zero_is_plain_and_beta_sound():
         assert lb <= true_min + 1e-6
 
 
+# ------------------------------------------------ ReLU-split alpha/beta bound
+def test_split_domain_bounds_no_reforward_hand_computed():
+    """Root bounds broadcast, clamps intersected, crossings repaired, layers
+    without clamps left as the root (verify_milp.py:2706-2717)."""
+    inf = float('inf')
+    root = {0: (_t([-1.0, -2.0, 0.5]), _t([1.0, 3.0, 1.0])),
+            1: (_t([-4.0]), _t([2.0]))}
+    cl = _t([[-inf, 0.0, -inf], [-inf, -inf, -inf]])
+    ch = _t([[0.0, inf, 0.0], [inf, inf, inf]])
+    x = torch.zeros(2, 1, dtype=DT)
+    sb = rb.split_domain_bounds(x, x, None, root, {0: (cl, ch)}, no_reforward=True)
+    # domain 0: OFF on j0, ON on j1, OFF on the root-active j2 (crossing -> point)
+    torch.testing.assert_close(sb[0][0], _t([[-1.0, 0.0, 0.5], [-1.0, -2.0, 0.5]]))
+    torch.testing.assert_close(sb[0][1], _t([[0.0, 3.0, 0.5], [1.0, 3.0, 1.0]]))
+    torch.testing.assert_close(sb[1][0], _t([[-4.0], [-4.0]]))
+    torch.testing.assert_close(sb[1][1], _t([[2.0], [2.0]]))
+
+
+def beta_known_answer_net():
+    """x in [-1,1]^2; h1 = relu(x1 + x2) (the split neuron), h2 = relu(x1 +
+    x2 + 2) (active on the box); y = -h2 + 2.4 = 0.4 - (x1 + x2).
+    On the OFF side (x1 + x2 <= 0) min y = 0.4; on the ON side -1.6."""
+    return _chain([[[1.0, 1.0], [1.0, 1.0]], [[0.0, -1.0]]], [[0.0, 2.0], [2.4]])
+
+
+def test_beta_crown_bound_known_answer():
+    """The OFF child closes only through beta: lb(beta) = 2 beta - 1.6 for
+    beta < 1, and Adam moves beta by ~lr per step from 0, so the 5th
+    evaluation (beta ~ 1) is the first with lb > 0, at ~0.4.  The ON child
+    is exact at its true min -1.6: its gradient pushes beta below 0 and the
+    clamp beta >= 0 holds it there (without the clamp the bound would pass
+    the true min).  Without beta (sign 0) the OFF child stays at -1.6."""
+    gg = beta_known_answer_net()
+    inf = float('inf')
+    xl = _t([[-1.0, -1.0], [-1.0, -1.0]])
+    xh = _t([[1.0, 1.0], [1.0, 1.0]])
+    root = rb.ibp_forward_batched(xl[:1], xh[:1], gg)
+    root = {L: (lo[0], hi[0]) for L, (lo, hi) in root.items()}
+    cl = _t([[-inf, -inf], [0.0, -inf]])                 # domain 1: ON
+    ch = _t([[0.0, inf], [inf, inf]])                    # domain 0: OFF
+    clamps = {0: (cl, ch)}
+    sb = rb.split_domain_bounds(xl, xh, gg, root, clamps)
+    sgn = rb.beta_signs_from_clamps(clamps)
+    torch.testing.assert_close(sgn[0], _t([[1.0, 0.0], [-1.0, 0.0]]))
+    spec = {0: (_t([1.0]), 0.0)}
+    best, n = rb.beta_crown_bound(sb, xl, xh, gg, spec, sgn, n_iters=20, lr=0.25,
+                                  return_trace=True)
+    assert n == 20                                       # the ON child never closes
+    assert abs(float(best[1, 0]) + 1.6) < 1e-12
+    assert 0.39 < float(best[0, 0]) <= 0.4 + 1e-12
+    sb_off = {L: (lo[:1], hi[:1]) for L, (lo, hi) in sb.items()}
+    best5, n5 = rb.beta_crown_bound(sb_off, xl[:1], xh[:1], gg, spec, {0: sgn[0][:1]},
+                                    n_iters=20, lr=0.25, return_trace=True)
+    assert n5 == 5
+    assert 0.39 < float(best5[0, 0]) <= 0.4 + 1e-12
+    nob = rb.beta_crown_bound(sb, xl, xh, gg, spec, {0: torch.zeros_like(sgn[0])},
+                              n_iters=20, lr=0.25)
+    assert abs(float(nob[0, 0]) + 1.6) < 1e-12
+
+
+def test_beta_crown_bound_first_iteration_monotone_and_sound():
+    """First evaluation = plain CROWN on the split bounds (alpha init is the
+    adaptive slope, beta = 0); the best bound is non-decreasing in the
+    iteration count; it never exceeds the true min over the points of the
+    box that satisfy the domain's split constraints."""
+    gg = _util.tiny_mlp([2, 8, 8, 3], seed=23)
+    inf = float('inf')
+    x0l, x0h = _t([[-1.0, -1.0]]), _t([[1.0, 1.0]])
+    root = rb.ibp_forward_batched(x0l, x0h, gg)
+    un = [(L, int(j)) for L in sorted(root)
+          for j in ((root[L][0][0] < 0) & (root[L][1][0] > 0)).nonzero().flatten()]
+    assert len(un) >= 3
+    picks = [un[0], un[len(un) // 2], un[-1]]
+    doms = [[(picks[0], s0), (picks[1], s1), (picks[2], s2)]
+            for s0 in (0, 1) for s1 in (0, 1) for s2 in (0, 1)]
+    B = len(doms)
+    clamps = {}
+    for b, dom in enumerate(doms):
+        for (L, j), side in dom:
+            if L not in clamps:
+                n_L = root[L][0].shape[1]
+                clamps[L] = (torch.full((B, n_L), -inf, dtype=DT),
+                             torch.full((B, n_L), inf, dtype=DT))
+            clamps[L][1 if side == 0 else 0][b, j] = 0.0
+    xl, xh = x0l.expand(B, -1).clone(), x0h.expand(B, -1).clone()
+    rootv = {L: (lo[0], hi[0]) for L, (lo, hi) in root.items()}
+    sb = rb.split_domain_bounds(xl, xh, gg, rootv, clamps)
+    sgn = rb.beta_signs_from_clamps(clamps)
+    spec, _ = _util.spec_for(3)
+    plain = rb.spec_backward_batched(sb, xl, xh, gg, spec)
+    b1, n1 = rb.beta_crown_bound(sb, xl, xh, gg, spec, sgn, n_iters=1, return_trace=True)
+    assert n1 == 1
+    torch.testing.assert_close(b1, plain)
+    prev = b1
+    for k in (3, 8, 20):
+        bk = rb.beta_crown_bound(sb, xl, xh, gg, spec, sgn, n_iters=k)
+        assert bool((bk >= prev - 1e-12).all())
+        prev = bk
+    g = np.linspace(-1, 1, 161)
+    X = torch.tensor(np.stack(np.meshgrid(g, g), -1).reshape(-1, 2), dtype=DT)
+    y, pre = rb.point_forward(X, gg)
+    Wq = torch.stack([spec[q][0] for q in sorted(spec)])
+    vals = y @ Wq.T
+    for b, dom in enumerate(doms):
+        m = torch.ones(X.shape[0], dtype=torch.bool)
+        for (L, j), side in dom:
+            m &= (pre[L][:, j] <= 0) if side == 0 else (pre[L][:, j] >= 0)
+        if bool(m.any()):
+            assert bool((prev[b] <= vals[m].min(0).values + 1e-9).all())
+
+
 # ------------------------------------------------ CROWN intermediate bounds
 def test_crown_intermediate_chunk_invariant_brackets_and_tightens():
     gg = wk.acas_gg(dtype=DT)

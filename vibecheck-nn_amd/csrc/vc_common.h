@@ -64,3 +64,38 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+
+// torch.optim.Adam's scalars (amsgrad off, no weight decay), rounded to fp32
+// the way torch rounds them: the lerp/addcmul weights 1 - beta are formed in
+// double and then cast, like torch's Python-float scalars.
+struct AdamConst {
+  float w1, b2, w2, eps, neg_step, bc2;
+};
+
+static inline AdamConst adam_const(double b1, double b2, double eps, double step_size,
+                                   double bc2_sqrt) {
+  AdamConst c;
+  c.w1 = (float)(1.0 - b1);
+  c.b2 = (float)b2;
+  c.w2 = (float)(1.0 - b2);
+  c.eps = (float)eps;
+  c.neg_step = (float)(-step_size);
+  c.bc2 = (float)bc2_sqrt;
+  return c;
+}
+
+// One Adam update of one parameter p with gradient g (of the loss), in
+// torch's operation order and rounding:
+//   exp_avg.lerp_(g, w1)             m = fma(w1, g - m, m)   (w1 < 0.5)
+//   exp_avg_sq.mul_(b2).addcmul_(g, g, value=w2)
+//                                    v = fma(w2 * g, g, v * b2)
+//   denom = sqrt(v) / bc2 + eps;  p.addcdiv_(m, denom, value=-step)
+//                                    p + (-step * m) / denom
+// sqrt and divide correctly rounded.
+__device__ __forceinline__ float adam_update(float p, float g, float& m, float& v,
+                                             const AdamConst& c) {
+  m = c.w1 < 0.5f ? __builtin_fmaf(c.w1, g - m, m) : __builtin_fmaf(c.w1 - 1.f, g - m, g);
+  v = __builtin_fmaf(c.w2 * g, g, v * c.b2);
+  const float denom = __fdiv_rn(__fsqrt_rn(v), c.bc2) + c.eps;
+  return p + __fdiv_rn(c.neg_step * m, denom);
+}

@@ -45,7 +45,8 @@ __global__ void k_ibp_relu(const float* l, const float* h, int64_t B, int n,
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int j = (int)(i % n);
-    float lo = l[i], hi = h[i];
+    // NULL l/h: an unbounded input interval, so the root bounds give it.
+    float lo = l ? l[i] : -INFINITY, hi = h ? h[i] : INFINITY;
     if (rlo) {
       lo = fmaxf(lo, rlo[j]);
       hi = fminf(hi, rhi[j]);
@@ -172,25 +173,74 @@ __global__ void k_alpha_grad_reduce(const float* gE, const float* P, int p_bcast
   }
 }
 
-// torch.optim.Adam (amsgrad off, no weight decay) on the loss -lb, then
-// the projection clamp.  Contractions are disabled so each torch op rounds.
-__global__ void k_adam(float* p, const float* lbg, float* m, float* v, int64_t n, float b1,
-                       float b2, float eps, float neg_step, float bc2, float lo_c,
-                       float hi_c) {
-#pragma clang fp contract(off)
+// Adam on the loss -lb, then the projection clamp.
+__global__ void k_adam(float* p, const float* lbg, float* m, float* v, int64_t n, AdamConst c,
+                       float lo_c, float hi_c) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const float g = -lbg[i];
-    float mi = m[i];
-    mi = mi + (1.f - b1) * (g - mi);
-    float vi = v[i] * b2;
-    vi = vi + ((1.f - b2) * g) * g;
-    const float denom = sqrtf(vi) / bc2 + eps;
-    float pi = p[i] + neg_step * (mi / denom);
+    float mi = m[i], vi = v[i];
+    float pi = adam_update(p[i], -lbg[i], mi, vi, c);
     pi = fminf(fmaxf(pi, lo_c), hi_c);
     m[i] = mi;
     v[i] = vi;
     p[i] = pi;
+  }
+}
+
+// Split beta: the backward sees the signed beta (beta * sign), so
+// d lb / d beta = sign * d lb / d signed.  Adam on -lb, clamp beta >= 0,
+// then write the signed beta for the next evaluation.
+__global__ void k_beta_adam(float* beta, const float* sign, const float* gsum, float* m,
+                            float* v, int64_t n, AdamConst c, float* signed_out) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float s = sign[i];
+    float mi = m[i], vi = v[i];
+    float pi = adam_update(beta[i], -(gsum[i] * s), mi, vi, c);
+    pi = fmaxf(pi, 0.f);
+    m[i] = mi;
+    v[i] = vi;
+    beta[i] = pi;
+    signed_out[i] = pi * s;
+  }
+}
+
+// sign +1 where the upper clamp is 0 (OFF split: z <= 0), -1 where the lower
+// clamp is 0 (ON split: z >= 0; it wins when both are 0), else 0.
+__device__ __forceinline__ float split_sign(float cl, float ch) {
+  return cl == 0.f ? -1.f : (ch == 0.f ? 1.f : 0.f);
+}
+
+__global__ void k_split_beta_sign(const float* cl, const float* ch, int64_t n, float* sign) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    sign[i] = split_sign(cl[i], ch[i]);
+}
+
+// Dense clamps of one relu layer from per-domain split lists (D, S): entry
+// (d, s) clamps neuron `neuron` of layer `layer` (-1 = unused slot) OFF
+// (side 0: upper clamp 0) or ON (side 1: lower clamp 0).
+__global__ void k_split_clamps(const int64_t* layer, const int64_t* neuron, const int64_t* side,
+                               int64_t D, int S, int64_t L, int n, float* cl, float* ch,
+                               float* sign) {
+  const int64_t total = D * (int64_t)n;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t d = i / n;
+    const int64_t j = i % n;
+    float lo = -INFINITY, hi = INFINITY;
+    for (int s = 0; s < S; ++s) {
+      const int64_t e = d * S + s;
+      if (layer[e] == L && neuron[e] == j) {
+        if (side[e] == 0)
+          hi = 0.f;
+        else
+          lo = 0.f;
+      }
+    }
+    cl[i] = lo;
+    ch[i] = hi;
+    if (sign) sign[i] = split_sign(lo, hi);
   }
 }
 
@@ -533,7 +583,8 @@ extern "C" int vc_ibp_relu(const float* l, const float* h, int64_t B, int n,
                            const float* root_lo, const float* root_hi, const float* cl,
                            const float* ch, float* sb_lo, float* sb_hi, float* post_lo,
                            float* post_hi, vc_stream_t stream) {
-  if (!l || !h || !sb_lo || !sb_hi || B < 0 || n <= 0) return VC_ERR_ARG;
+  if (!sb_lo || !sb_hi || B < 0 || n <= 0) return VC_ERR_ARG;
+  if ((l == nullptr) != (h == nullptr) || (!l && !root_lo)) return VC_ERR_ARG;
   if ((root_lo == nullptr) != (root_hi == nullptr) || (cl == nullptr) != (ch == nullptr) ||
       (post_lo == nullptr) != (post_hi == nullptr))
     return VC_ERR_ARG;
@@ -612,14 +663,52 @@ extern "C" int vc_alpha_grad_reduce(const float* gE, const float* P, int p_bcast
 }
 
 extern "C" int vc_adam_step(float* param, const float* lb_grad, float* exp_avg,
-                            float* exp_avg_sq, int64_t n, float b1, float b2, float eps,
+                            float* exp_avg_sq, int64_t n, double b1, double b2, double eps,
                             double step_size, double bc2_sqrt, float lo_clamp, float hi_clamp,
                             vc_stream_t stream) {
   if (!param || !lb_grad || !exp_avg || !exp_avg_sq || n < 0) return VC_ERR_ARG;
   if (n == 0) return VC_OK;
   hipLaunchKernelGGL(k_adam, dim3(vc_blocks(n, NT)), dim3(NT), 0, (hipStream_t)stream, param,
-                     lb_grad, exp_avg, exp_avg_sq, n, b1, b2, eps, (float)(-step_size),
-                     (float)bc2_sqrt, lo_clamp, hi_clamp);
+                     lb_grad, exp_avg, exp_avg_sq, n, adam_const(b1, b2, eps, step_size, bc2_sqrt),
+                     lo_clamp, hi_clamp);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_beta_adam_step(float* beta, const float* sign, const float* lb_grad_signed,
+                                 float* exp_avg, float* exp_avg_sq, int64_t n, double b1,
+                                 double b2, double eps, double step_size, double bc2_sqrt,
+                                 float* beta_signed, vc_stream_t stream) {
+  if (n < 0) return VC_ERR_ARG;
+  if (n == 0) return VC_OK;
+  if (!beta || !sign || !lb_grad_signed || !exp_avg || !exp_avg_sq || !beta_signed)
+    return VC_ERR_ARG;
+  hipLaunchKernelGGL(k_beta_adam, dim3(vc_blocks(n, NT)), dim3(NT), 0, (hipStream_t)stream, beta,
+                     sign, lb_grad_signed, exp_avg, exp_avg_sq, n,
+                     adam_const(b1, b2, eps, step_size, bc2_sqrt), beta_signed);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_split_beta_sign(const float* cl, const float* ch, int64_t n, float* sign,
+                                  vc_stream_t stream) {
+  if (n < 0) return VC_ERR_ARG;
+  if (n == 0) return VC_OK;
+  if (!cl || !ch || !sign) return VC_ERR_ARG;
+  hipLaunchKernelGGL(k_split_beta_sign, dim3(vc_blocks(n, NT)), dim3(NT), 0, (hipStream_t)stream,
+                     cl, ch, n, sign);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_split_clamps(const int64_t* layer, const int64_t* neuron, const int64_t* side,
+                               int64_t D, int S, int64_t L, int n, float* cl, float* ch,
+                               float* sign, vc_stream_t stream) {
+  if (D < 0 || S < 0 || n <= 0 || L < 0) return VC_ERR_ARG;
+  if (D == 0) return VC_OK;
+  if (!cl || !ch || (S > 0 && (!layer || !neuron || !side))) return VC_ERR_ARG;
+  hipLaunchKernelGGL(k_split_clamps, dim3(vc_blocks(D * n, NT)), dim3(NT), 0,
+                     (hipStream_t)stream, layer, neuron, side, D, S, L, n, cl, ch, sign);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }

@@ -765,7 +765,7 @@ __global__ __launch_bounds__(NWAVE_A * 64) void k_mlp_alpha(
     Net net, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
     const float* __restrict__ xl, const float* __restrict__ xh, AlphaArgs aa, int Q,
     const float* __restrict__ spec_rows, const float* __restrict__ spec_acc,
-    float* __restrict__ lb_out, float b1, float b2, float eps, float neg_step, float bc2) {
+    float* __restrict__ lb_out, AdamConst adam) {
 #pragma clang fp contract(off)
   extern __shared__ float smem[];
   float* sfrag = smem;
@@ -927,13 +927,8 @@ __global__ __launch_bounds__(NWAVE_A * 64) void k_mlp_alpha(
           const float ga = s + cs;
           if (r == 0 && j < dW && sl[3 * FW + j] != 0.f) {
             float* sa = sad + l * 3 * FW;
-            const float gr = -ga;
-            float mi = sa[FW + j];
-            mi = mi + (1.f - b1) * (gr - mi);
-            float vi = sa[2 * FW + j] * b2;
-            vi = vi + ((1.f - b2) * gr) * gr;
-            const float denom = sqrtf(vi) / bc2 + eps;
-            float pa = sa[j] + neg_step * (mi / denom);
+            float mi = sa[FW + j], vi = sa[2 * FW + j];
+            float pa = adam_update(sa[j], -ga, mi, vi, adam);
             pa = fminf(fmaxf(pa, 0.f), 1.f);
             sa[FW + j] = mi;
             sa[2 * FW + j] = vi;
@@ -1094,8 +1089,8 @@ extern "C" int vc_mlp_alpha_iter(const int32_t* dims, int n_relu, const float* f
                                  const float* xh, const float* const* lo, const float* const* hi,
                                  float* const* alpha, float* const* exp_avg,
                                  float* const* exp_avg_sq, int Q, const float* spec_rows,
-                                 const float* spec_acc, float* lb_out, float b1, float b2,
-                                 float eps, double step_size, double bc2_sqrt,
+                                 const float* spec_acc, float* lb_out, double b1, double b2,
+                                 double eps, double step_size, double bc2_sqrt,
                                  vc_stream_t stream) {
   Net net{};
   int rc = build_net(dims, n_relu, net);
@@ -1131,12 +1126,12 @@ extern "C" int vc_mlp_alpha_iter(const int32_t* dims, int n_relu, const float* f
   if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return VC_ERR_UNSUPPORTED;
   const dim3 grid(persistent_grid(B, lds, NWAVE_A)), block(NWAVE_A * 64);
-  const float ns = (float)(-step_size), b2s = (float)bc2_sqrt;
+  const AdamConst adam = adam_const(b1, b2, eps, step_size, bc2_sqrt);
   hipStream_t st = (hipStream_t)stream;
 #define VC_ALPHA_CASE(NLV)                                                                   \
   case NLV:                                                                                  \
     hipLaunchKernelGGL(k_mlp_alpha<NLV>, grid, block, lds, st, net, frag_bwd, bias_cat, B,   \
-                       xl, xh, aa, Q, spec_rows, spec_acc, lb_out, b1, b2, eps, ns, b2s);    \
+                       xl, xh, aa, Q, spec_rows, spec_acc, lb_out, adam);                   \
     break;
   switch (n_relu) {
     VC_ALPHA_CASE(1)

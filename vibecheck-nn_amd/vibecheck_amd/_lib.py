@@ -46,7 +46,10 @@ SIGNATURES = {
                            _P, _P],
     'vc_alpha_grad_reduce': [_P, _P, _I, _L, _I, _I, _P, _P, _P, _P, _P],
     'vc_alpha_grad_input': [_P, _P, _P, _L, _I, _I, _P, _P, _I, _P, _P],
-    'vc_adam_step': [_P, _P, _P, _P, _L, _F, _F, _F, _D, _D, _F, _F, _P],
+    'vc_adam_step': [_P, _P, _P, _P, _L, _D, _D, _D, _D, _D, _F, _F, _P],
+    'vc_beta_adam_step': [_P, _P, _P, _P, _P, _L, _D, _D, _D, _D, _D, _P, _P],
+    'vc_split_beta_sign': [_P, _P, _L, _P, _P],
+    'vc_split_clamps': [_P, _P, _P, _L, _I, _L, _I, _P, _P, _P, _P],
     'vc_best_update': [_P, _P, _L, _I, _P, _P],
     'vc_closure': [_P, _L, _I, _P, _P, _I, _P, _P],
     'vc_clip_box': [_P, _P, _P, _P, _L, _I, _I, _P, _P, _I, _P, _P, _P, _P],
@@ -61,7 +64,7 @@ SIGNATURES = {
     'vc_mlp_crown': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _I,
                      _I, _P, _P, _P, _P, _P, _P],
     'vc_mlp_alpha_iter': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
-                          _P, _P, _P, _F, _F, _F, _D, _D, _P],
+                          _P, _P, _P, _D, _D, _D, _D, _D, _P],
     'vc_widest_axis': [_P, _P, _L, _I, _P, _P, _P],
     'vc_bisect': [_P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P],
 }

@@ -556,17 +556,20 @@ def _crown_intermediate_batched(gg, xl, xh, device, dtype, chunk=2048,
 # a9: alpha-CROWN
 # --------------------------------------------------------------------------
 
-def _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, want_grad, galpha):
+def _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, want_grad, galpha,
+                             beta=None, gbeta=None):
     """One alpha-CROWN evaluation: lb (B, Q); when ``want_grad`` also fills
     ``galpha[L]`` with d(sum lb)/d alpha_L (the autograd of the reference's
-    backward, torch clamp subgradients included)."""
+    backward, torch clamp subgradients included).  ``beta`` is the signed
+    ReLU-split beta {L: (B, n_L)} added at each relu's input
+    (``relu_split_beta``); ``gbeta[L]`` receives d(sum lb)/d beta_L."""
     B, n_in = xl.shape
     Q = Wq.shape[0]
     dev = xl.device
     st = stream()
     trace = BackwardTrace() if want_grad else None
     lb, A, a_shared, _ = _backward(sb, xl, xh, gg, gg['ops'][-1]['name'], Wq,
-                                   True, bq, alpha, None, trace)
+                                   True, bq, alpha, beta, trace)
     if not want_grad:
         return lb
     if A is None or a_shared:
@@ -590,9 +593,11 @@ def _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, want_grad, galpha):
         lo, hi = f32(sb[L][0]), f32(sb[L][1])
         n = lo.shape[1]
         a = f32(alpha[L]) if (alpha is not None and L in alpha) else None
-        if galpha is not None and L in galpha:
+        ga = galpha.get(L) if galpha is not None else None
+        gb = gbeta.get(L) if gbeta is not None else None
+        if ga is not None or gb is not None:
             call('vc_alpha_grad_reduce', ptr(g), ptr(P), 1 if p_shared else 0,
-                 B, Q, n, ptr(lo), ptr(hi), ptr(galpha[L]), None, st)
+                 B, Q, n, ptr(lo), ptr(hi), ptr(ga), ptr(gb), st)
         if i > 0:
             fn = _op_params(fcs[i], dev)
             g2 = torch.empty(M, fn['n_out'], device=dev)
