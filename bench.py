@@ -81,6 +81,35 @@ def cpu_baseline(sample_B=2048, reps=3):
                       f'split) on the first {sample_B} of the 65,536 boxes, median of {reps}'}
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, 'profiles', 'k_mlp_crown_acas_65536_traffic.md')
+
+
+def measured_traffic():
+    """HBM bytes per k_mlp_crown launch on this workload, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (each counter scaled by what it
+    reads for a plain copy of known size); None when absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith('traffic_bytes_per_launch:'):
+                    return float(line.split(':', 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def copy_probe(mib):
+    """A plain device copy of known size (read mib MiB, write mib MiB), three
+    times: the calibration dispatch for the FETCH_SIZE / WRITE_SIZE counters."""
+    n = mib * (1 << 20) // 4
+    src = torch.rand(n, device='cuda:0')
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({'copy_probe_bytes_read': n * 4, 'copy_probe_bytes_written': n * 4}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -88,11 +117,16 @@ def main():
     ap.add_argument('--warmup', type=int, default=2)
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--cpu-sample', type=int, default=2048)
+    ap.add_argument('--copy-probe', type=int, default=0, metavar='MIB',
+                    help='only run a plain copy of MIB MiB (counter calibration)')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU only (this build has no multi-GPU path); '
               f'got --gpus {args.gpus}', file=sys.stderr)
         sys.exit(2)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
 
     from vibecheck_amd import _lib
     from vibecheck_amd import verify_graph as vg
@@ -141,7 +175,9 @@ def main():
                                'backward, whole network per wavefront, fp32 MFMA)',
                      'bound': 'mfma', 'achieved': achieved, 'peak': FP32_MFMA_PEAK,
                      'unit': 'TFLOP/s', 'frac': achieved / FP32_MFMA_PEAK,
-                     'traffic': None, 'launches_per_step': k['launches'] / args.steps,
+                     'traffic': measured_traffic(),
+                     'traffic_unit': 'bytes per launch (HBM, rocprofv3 FETCH_SIZE + WRITE_SIZE)',
+                     'launches_per_step': k['launches'] / args.steps,
                      'avg_launch_us': 1e6 * k['seconds'] / max(1, k['launches'])},
     }
     if not args.no_cpu_baseline:
