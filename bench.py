@@ -81,15 +81,13 @@ def cpu_baseline(sample_B=2048, reps=3):
                       f'split) on the first {sample_B} of the 65,536 boxes, median of {reps}'}
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, 'profiles', 'k_mlp_crown_acas_65536_traffic.md')
-
-
-def measured_traffic():
-    """HBM bytes per k_mlp_crown launch on this workload, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (each counter scaled by what it
-    reads for a plain copy of known size); None when absent."""
+def measured_traffic(kernel):
+    """HBM bytes per launch of the dominant kernel on this workload, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (each counter scaled
+    by what it reads for a plain copy of known size); None when absent."""
+    path = os.path.join(ROOT, 'profiles', f'{kernel}_acas_65536_traffic.md')
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(path) as f:
             for line in f:
                 if line.startswith('traffic_bytes_per_launch:'):
                     return float(line.split(':', 1)[1])
@@ -146,7 +144,7 @@ def main():
         run_rounds(gg, xl0, xh0, se, table)
     torch.cuda.synchronize()
 
-    _lib.timing_begin(['vc_mlp_crown'])
+    _lib.timing_begin(['vc_mlp_crown', 'vc_mlp_tiled_crown'])
     t0 = time.perf_counter()
     stats = None
     for _ in range(args.steps):
@@ -158,7 +156,9 @@ def main():
     per_step = wall / args.steps
     domains = sum(s['B'] for s in stats)
     alpha_iters = sum(s['alpha_iters'] for s in stats)
-    k = kt['vc_mlp_crown']
+    entry = max(kt, key=lambda n: kt[n]['launches'])
+    k = kt[entry]
+    kernel = {'vc_mlp_crown': 'k_mlp_crown', 'vc_mlp_tiled_crown': 'k_crown_tiled'}[entry]
     achieved = k['flops'] / k['seconds'] / 1e12 if k['seconds'] > 0 else 0.0
     out = {
         'metric': 'CROWN-bounded domains/sec at 1 GPU (5-50x6-5 MLP, 65,536 domains)',
@@ -171,11 +171,11 @@ def main():
                                'widest split', 'domains_per_step': domains},
         'alpha_iters_per_s': alpha_iters / per_step,
         'rounds': stats,
-        'roofline': {'kernel': 'k_mlp_crown (vc_mlp_crown: CROWN intermediate bounds + spec '
+        'roofline': {'kernel': f'{kernel} ({entry}: CROWN intermediate bounds + spec '
                                'backward, whole network per wavefront, fp32 MFMA)',
                      'bound': 'mfma', 'achieved': achieved, 'peak': FP32_MFMA_PEAK,
                      'unit': 'TFLOP/s', 'frac': achieved / FP32_MFMA_PEAK,
-                     'traffic': measured_traffic(),
+                     'traffic': measured_traffic(kernel),
                      'traffic_unit': 'bytes per launch (HBM, rocprofv3 FETCH_SIZE + WRITE_SIZE)',
                      'launches_per_step': k['launches'] / args.steps,
                      'avg_launch_us': 1e6 * k['seconds'] / max(1, k['launches'])},

@@ -316,6 +316,38 @@ int vc_mlp_crown(const int32_t *dims, int n_relu, const float *frag_bwd,
                  const float *spec_rows, const float *spec_acc, float *lb_out,
                  float *A_out, float *acc_out, vc_stream_t stream);
 
+/* Floats of the fragment buffer of vc_mlp_tiled_crown for this network, or
+ * minus a status when no shape-specialised kernel holds it (every hidden
+ * fc then needs K-steps and M-tiles beyond the largest instantiation).
+ * Part of the replacement of _crown_intermediate_batched
+ * (verify_zono_bnb.py:4077-4147). */
+int64_t vc_mlp_tiled_floats(const int32_t *dims, int n_relu);
+
+/* Pack fc_0 .. fc_{n_relu-1} (W[l] (dims[l+1], dims[l]), bias[l]
+ * (dims[l+1])) into the vc_mlp_tiled_crown layout: each fc's transposed
+ * weights plus its bias as one extra row of the MFMA A operand, hidden
+ * layers as [K-step][lane][M-tile]. */
+int vc_mlp_tiled_pack(const float *const *W, const float *const *bias,
+                      const int32_t *dims, int n_relu, float *frag,
+                      vc_stream_t stream);
+
+/* vc_mlp_crown with the tile shape fixed at compile time (same arguments
+ * and results; frag from vc_mlp_tiled_pack, Q <= 64): no MFMA under a
+ * runtime condition, the fc bias carried by the MFMA, the per-row constants
+ * accumulated in fp64.
+ * Replaces _crown_intermediate_batched (verify_zono_bnb.py:4077-4147) and
+ * _spec_backward_graph_batched with return_input_linear
+ * (verify_zono_bnb.py:4270-4453, 5117-5134). */
+int vc_mlp_tiled_crown(const int32_t *dims, int n_relu, const float *frag,
+                       const float *bias_cat, int64_t B, const float *xl,
+                       const float *xh, const float *const *lo_in,
+                       const float *const *hi_in, float *const *lo_out,
+                       float *const *hi_out, const int32_t *idx_all,
+                       const int32_t *idx_cnt, int do_crown, int Q,
+                       const float *spec_rows, const float *spec_acc,
+                       float *lb_out, float *A_out, float *acc_out,
+                       vc_stream_t stream);
+
 /* One batched alpha-CROWN Adam iteration, whole network per wavefront
  * (n_relu <= 7, 1 <= Q <= 16): evaluates lb_out (B, Q) with lower slopes
  * active + unstable * alpha on the bounds lo/hi, computes d(sum lb)/d alpha

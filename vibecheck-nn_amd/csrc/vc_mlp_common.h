@@ -1,0 +1,65 @@
+// Helpers shared by the whole-network MLP kernels (vc_mlp_fused.hip,
+// vc_mlp_tiled.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vcm {
+
+constexpr int FW = 64;    // max layer width
+constexpr int MAXL = 16;  // max relu layers
+
+// K-steps of a 16x16x4 MFMA chain over dk neurons in the permuted order
+// (K-step (t, i) contracts neuron 16 t + 4 g + i in lane group g).
+__host__ __device__ inline int ks_count(int dk) {
+  const int T = (dk + 15) / 16;
+  const int last = dk - 16 * (T - 1);
+  return 4 * (T - 1) + (last < 4 ? last : 4);
+}
+
+// Copy n4 float4s (16-byte aligned) from global memory into LDS, four loads
+// in flight per thread, then barrier.
+__device__ __forceinline__ void stage_float4(float* dst_lds, const float* src, int n4) {
+  const float4* s = reinterpret_cast<const float4*>(src);
+  float4* d = reinterpret_cast<float4*>(dst_lds);
+  int e = threadIdx.x;
+  for (; e + 3 * (int)blockDim.x < n4; e += 4 * blockDim.x) {
+    const float4 a = s[e], b = s[e + blockDim.x], c = s[e + 2 * blockDim.x],
+                 f = s[e + 3 * blockDim.x];
+    d[e] = a;
+    d[e + blockDim.x] = b;
+    d[e + 2 * blockDim.x] = c;
+    d[e + 3 * blockDim.x] = f;
+  }
+  for (; e < n4; e += blockDim.x) d[e] = s[e];
+}
+
+// Compute units of the current device (read once per device).
+inline int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Persistent grid: as many workgroups as fit on the CUs at once given the
+// LDS footprint (160 KB per CU, at most two per CU), capped by the work
+// (B domains, nwave per workgroup).
+inline int persistent_grid(int64_t B, size_t lds_bytes, int nwave) {
+  int per_cu = (int)((160 * 1024) / (lds_bytes > 0 ? lds_bytes : 1));
+  if (per_cu < 1) per_cu = 1;
+  if (per_cu > 2) per_cu = 2;
+  int64_t grid = (int64_t)cu_count() * per_cu;
+  const int64_t need = (B + nwave - 1) / nwave;
+  if (need < grid) grid = need;
+  return (int)(grid < 1 ? 1 : grid);
+}
+
+}  // namespace vcm

@@ -20,12 +20,15 @@
 //     5117-5134): seeded rows chained through relaxation + fc steps in
 //     registers, intersected per domain, slopes kept in LDS.
 #include "vc_common.h"
+#include "vc_mlp_common.h"
 #include "vc_relax.h"
 
 namespace {
 
-constexpr int FW = 64;     // max layer width
-constexpr int MAXL = 16;   // max relu layers
+using vcm::cu_count;
+using vcm::FW;
+using vcm::ks_count;
+using vcm::MAXL;
 constexpr int NWAVE = 8;   // waves (domains in flight) per workgroup
 constexpr int NPAR = 4;    // row N-tiles chained together per wave
 constexpr int ZNT_NARROW = 8;   // 128 generator columns, 8 waves per workgroup
@@ -37,12 +40,6 @@ struct Net {
   int boff[MAXL + 1];    // bias offset of fc_l
   int nfrag, nbias;
 };
-
-__host__ __device__ inline int ks_count(int dk) {  // valid (t, i) K-steps
-  const int T = (dk + 15) / 16;
-  const int last = dk - 16 * (T - 1);
-  return 4 * (T - 1) + (last < 4 ? last : 4);
-}
 
 // ----------------------------------------------------------------- packing
 // bwd: A[m][k] = W[k][m] (W: d_out x d_in), M = d_in, K = d_out
@@ -67,19 +64,7 @@ __global__ void k_pack(const float* W, int d_out, int d_in, int bwd, float* frag
 // biases into LDS with 16-byte loads, several in flight per thread.
 __device__ __forceinline__ void stage_weights(float* sfrag, float* sbias, const float* gfrag,
                                               const float* gbias, int nfrag, int nbias) {
-  const int n4 = nfrag * 16;
-  const float4* src = reinterpret_cast<const float4*>(gfrag);
-  float4* dst = reinterpret_cast<float4*>(sfrag);
-  int e = threadIdx.x;
-  for (; e + 3 * (int)blockDim.x < n4; e += 4 * blockDim.x) {
-    const float4 a = src[e], b = src[e + blockDim.x], c = src[e + 2 * blockDim.x],
-                 d = src[e + 3 * blockDim.x];
-    dst[e] = a;
-    dst[e + blockDim.x] = b;
-    dst[e + 2 * blockDim.x] = c;
-    dst[e + 3 * blockDim.x] = d;
-  }
-  for (; e < n4; e += blockDim.x) dst[e] = src[e];
+  vcm::stage_float4(sfrag, gfrag, nfrag * 16);
   for (int k = threadIdx.x; k < nbias; k += blockDim.x) sbias[k] = gbias[k];
   __syncthreads();
 }
@@ -989,29 +974,8 @@ int build_net_fwd(const int32_t* dims, int n_relu, Net& net) {
   return VC_OK;
 }
 
-int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
-// Persistent grid: as many workgroups as fit on the CUs at once given the
-// LDS footprint (160 KB per CU), capped by the amount of work.
 int persistent_grid(int64_t B, size_t lds_bytes, int nwave = NWAVE) {
-  int per_cu = (int)((160 * 1024) / (lds_bytes > 0 ? lds_bytes : 1));
-  if (per_cu < 1) per_cu = 1;
-  if (per_cu > 2) per_cu = 2;
-  int64_t grid = (int64_t)cu_count() * per_cu;
-  const int64_t need = (B + nwave - 1) / nwave;
-  if (need < grid) grid = need;
-  return (int)(grid < 1 ? 1 : grid);
+  return vcm::persistent_grid(B, lds_bytes, nwave);
 }
 
 }  // namespace

@@ -1,0 +1,563 @@
+// Whole-network CROWN kernel for narrow fc/ReLU chains with the tile shape
+// fixed at compile time (vc_mlp_tiled_crown).
+//
+// Same computation and register layout as k_mlp_crown in vc_mlp_fused.hip
+// (one wavefront per domain; activation rows held like the D operand of
+// v_mfma_f32_16x16x4_f32, so a layer's output registers feed the next
+// layer's B operand), restructured so that no MFMA sits under a runtime
+// condition:
+//   - every hidden fc layer uses the same MT M-tiles and KS K-steps (the
+//     template parameters; narrower layers are zero-padded), so the MFMA
+//     loops unroll completely;
+//   - a hidden layer's A fragments are stored [K-step][lane][M-tile], one
+//     16-byte LDS read per K-step;
+//   - the fc bias rides in the MFMA: row d_l of fc_l's A operand holds the
+//     bias (in the zero padding of the last M-tile), so the output row d_l
+//     is sum_k bias_k e_k, read out once per layer instead of a VALU dot
+//     (BROW; without a free padding row the dot runs on the VALU);
+//   - per-row constants (neg(ew) . up_t, bias dots, the concretization)
+//     accumulate in fp64: each fp32 product is rounded as torch rounds it,
+//     the sum of those products is held to ~1e-16 relative.
+//
+// fc_0 (M = input width, plus the bias row) is processed one M-tile at a
+// time and concretized on the fly.
+#include "vc_common.h"
+#include "vc_mlp_common.h"
+#include "vc_relax.h"
+
+namespace {
+
+using vcm::FW;
+using vcm::ks_count;
+using vcm::MAXL;
+
+constexpr int TNW = 12;  // waves per workgroup, one domain each (3 per SIMD)
+constexpr int TNP = 2;   // 16-row N-tiles chained together per wave
+
+// Kernel instantiations: hidden M-tiles, K-steps, bias row in the A operand.
+struct TVariant {
+  int MT, KS, brow;
+};
+constexpr TVariant kVariants[] = {{1, 4, 1},  {2, 8, 1},  {3, 12, 1},
+                                  {4, 14, 1}, {4, 16, 1}, {4, 16, 0}};
+constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
+
+struct TGeom {
+  int n;               // relu layers (fc_0 .. fc_{n-1}; the last fc is folded into the spec)
+  int d[MAXL + 2];     // d[0] = inputs, d[l+1] = width of relu l
+  int variant, MT, KS, brow;
+  int mt0;             // M-tiles of fc_0 (inputs plus the bias row)
+  int offh;            // float offset of the hidden fragments (fc_1 ...)
+  int nfloats;         // fragment floats
+  int boff[MAXL + 1];  // offset of fc_l's bias in the concatenated biases
+};
+
+// Pick the first instantiation that holds every layer.  Returns a VC_ status.
+int tiled_geom(const int32_t* dims, int n_relu, TGeom& G) {
+  if (!dims || n_relu < 1 || n_relu > MAXL) return VC_ERR_UNSUPPORTED;
+  G = TGeom{};
+  G.n = n_relu;
+  int bo = 0;
+  for (int l = 0; l <= n_relu; ++l) {
+    if (dims[l] <= 0) return VC_ERR_ARG;
+    if (dims[l] > FW) return VC_ERR_UNSUPPORTED;
+    G.d[l] = dims[l];
+  }
+  for (int l = 0; l < n_relu; ++l) {
+    G.boff[l] = bo;
+    bo += G.d[l + 1];
+  }
+  int ks_need = 0, mh = 0;
+  for (int l = 1; l <= n_relu; ++l) ks_need = ks_count(G.d[l]) > ks_need ? ks_count(G.d[l]) : ks_need;
+  for (int l = 1; l < n_relu; ++l) mh = G.d[l] > mh ? G.d[l] : mh;
+  G.variant = -1;
+  for (int v = 0; v < kNumVariants; ++v) {
+    const TVariant& k = kVariants[v];
+    if (k.KS >= ks_need && 16 * k.MT >= mh + k.brow) {
+      G.variant = v;
+      break;
+    }
+  }
+  if (G.variant < 0) return VC_ERR_UNSUPPORTED;
+  G.MT = kVariants[G.variant].MT;
+  G.KS = kVariants[G.variant].KS;
+  G.brow = kVariants[G.variant].brow;
+  G.mt0 = (G.d[0] + G.brow + 15) / 16;
+  G.offh = G.mt0 * G.KS * 64;
+  G.nfloats = G.offh + (n_relu - 1) * G.KS * 64 * 4;
+  return VC_OK;
+}
+
+// fc_l's backward A operand: A[m][k] = W[k][m] (W: d_out x d_in, m < d_in,
+// k < d_out), A[d_in][k] = bias[k] when brow; zero elsewhere.
+//   hidden (layout 1): [ks][lane][mt] float4, mt < 4
+//   fc_0   (layout 0): [mt][ks][lane]
+__global__ void k_tpack(const float* W, const float* bias, int d_out, int d_in, int KS, int MTt,
+                        int layout, int brow, float* frag) {
+  const int total = MTt * KS * 64;
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    int mt, ks, lane;
+    if (layout == 1) {
+      mt = e & 3;
+      lane = (e >> 2) & 63;
+      ks = e >> 8;
+    } else {
+      lane = e & 63;
+      ks = (e >> 6) % KS;
+      mt = (e >> 6) / KS;
+    }
+    const int t = ks >> 2, i = ks & 3, g = lane >> 4, r = lane & 15;
+    const int m = 16 * mt + r, k = 16 * t + 4 * g + i;
+    float v = 0.f;
+    if (k < d_out) {
+      if (m < d_in)
+        v = W[k * d_in + m];
+      else if (brow && m == d_in)
+        v = bias ? bias[k] : 0.f;
+    }
+    frag[e] = v;
+  }
+}
+
+struct TCrownArgs {
+  const float* lo_in[MAXL];
+  const float* hi_in[MAXL];
+  float* lo_out[MAXL];
+  float* hi_out[MAXL];
+  int idx_off[MAXL];
+  int idx_cnt[MAXL];
+};
+
+__device__ __forceinline__ double group_sum4_d(double v) {
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// Relaxation at one relu of the first NP row tiles of F (values of that
+// relu's neurons j = 16 t + 4 g + i at K-step 4 t + i):
+//   e = pos(x) ls + neg(x) us = x * (x < 0 ? us : ls),  acc += neg(x) ut
+// and, without the bias row, acc += e . bias.  sl: ls, us, ut [FW] each,
+// zero beyond the layer width; bl: the next fc's bias, zero-padded to FW.
+template <int KS, int NP, bool BROW>
+__device__ __forceinline__ void relax_rows(const float* sl, const float* bl, int g,
+                                           v4f (&F)[TNP][4], double (&acc)[TNP]) {
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int t = ks >> 2, i = ks & 3;
+    const int j = 16 * t + 4 * g + i;
+    const float ls = sl[j], us = sl[FW + j], ut = sl[2 * FW + j];
+    const float bj = BROW ? 0.f : bl[j];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const float x = F[p][t][i];
+      const bool ng = x < 0.f;
+      const float e = x * (ng ? us : ls);
+      const float en = ng ? x : 0.f;
+      acc[p] += (double)(en * ut);
+      if (!BROW) acc[p] += (double)(e * bj);
+      F[p][t][i] = e;
+    }
+  }
+}
+
+// Backward through hidden fc_l: F (rows at fc_l's output, relaxed) <- A F
+// with A = [W_l^T; bias_l]; with the bias row, its output (row mb = d_l,
+// held by lane group (mb % 16) / 4) is the bias dot and goes to acc.
+template <int MT, int KS, int NP, bool BROW>
+__device__ __forceinline__ void fc_hidden(const float4* fr, int lane, int g, int mb,
+                                          v4f (&F)[TNP][4], double (&acc)[TNP]) {
+  v4f o[TNP][MT];
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) o[p][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const float4 a4 = fr[ks * 64 + lane];
+    const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) o[p][mt] = mfma16x16x4(a[mt], F[p][ks >> 2][ks & 3], o[p][mt]);
+  }
+  if (BROW) {
+    const int mtb = mb >> 4, ib = mb & 3;
+    const bool mine = g == ((mb & 15) >> 2);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      float v = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v = (mt == mtb && i == ib) ? o[p][mt][i] : v;
+      if (mine) acc[p] += (double)v;
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) F[p][mt] = o[p][mt];
+}
+
+// Backward through fc_0 (A = [W_0^T; bias_0], stored per M-tile) and
+// concretization: cz += pos(A) xl + neg(A) xh over the d0 inputs, the bias
+// row to acc; optionally the input coefficients of live rows to A_rows
+// (row-major, d0 per row; row = 16 p + r).
+template <int KS, int NP, bool BROW>
+__device__ __forceinline__ void fc0_concretize(const float* fr0, int mt0, int d0, int lane, int g,
+                                               int r, const float* dxl, const float* dxh,
+                                               const v4f (&F)[TNP][4], double (&acc)[TNP],
+                                               double (&cz)[TNP], float* A_rows, int n_live) {
+  for (int mt = 0; mt < mt0; ++mt) {
+    v4f o[TNP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) o[p] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const float a = fr0[(mt * KS + ks) * 64 + lane];
+#pragma unroll
+      for (int p = 0; p < NP; ++p) o[p] = mfma16x16x4(a, F[p][ks >> 2][ks & 3], o[p]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * mt + 4 * g + i;
+      const bool in = m < d0;
+      const float xlv = in ? dxl[m] : 0.f, xhv = in ? dxh[m] : 0.f;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const float v = o[p][i];
+        if (in) {
+          cz[p] += (double)(fmaxf(v, 0.f) * xlv);
+          cz[p] += (double)(fminf(v, 0.f) * xhv);
+          const int row = 16 * p + r;
+          if (A_rows && row < n_live) A_rows[(int64_t)row * d0 + m] = v;
+        } else if (BROW && m == d0) {
+          acc[p] += (double)v;
+        }
+      }
+    }
+  }
+}
+
+template <int MT, int KS, int NP, bool BROW>
+__device__ __forceinline__ void chain_to_input(const TGeom& G, int Ltop, const float* fr0,
+                                               const float4* frh, const float* ssl,
+                                               const float* sbias, int lane, int g, int r,
+                                               const float* dxl, const float* dxh,
+                                               v4f (&F)[TNP][4], double (&acc)[TNP],
+                                               double (&cz)[TNP], float* A_rows, int n_live) {
+  // rows at relu Ltop's output: relax + fc_l for l = Ltop .. 1, then relu 0 + fc_0
+  for (int l = Ltop; l >= 1; --l) {
+    relax_rows<KS, NP, BROW>(ssl + l * 3 * FW, sbias + l * FW, g, F, acc);
+    fc_hidden<MT, KS, NP, BROW>(frh + (l - 1) * KS * 64, lane, g, G.d[l], F, acc);
+  }
+  relax_rows<KS, NP, BROW>(ssl, sbias, g, F, acc);
+  fc0_concretize<KS, NP, BROW>(fr0, G.mt0, G.d[0], lane, g, r, dxl, dxh, F, acc, cz, A_rows,
+                               n_live);
+}
+
+__device__ __forceinline__ void make_slopes_lds(float* sl, const float* lo, const float* hi, int n,
+                                                int lane) {
+  for (int j = lane; j < FW; j += 64) {
+    float ls = 0.f, us = 0.f, ut = 0.f;
+    if (j < n) {
+      const Relax s = relax(lo[j], hi[j]);
+      ls = s.lo_s;
+      us = s.up_s;
+      ut = s.up_t;
+    }
+    sl[j] = ls;
+    sl[FW + j] = us;
+    sl[2 * FW + j] = ut;
+  }
+}
+
+// One group of NP seeded row tiles of relu layer L (rows 16 nt0 .. of the
+// 2m seeds: row q < m is +W_L[idx[q]], row m + q is -W_L[idx[q]]) through
+// fc_L .. fc_0 and the concretization; lb of each row to slb.
+template <int MT, int KS, int NP, bool BROW>
+__device__ __forceinline__ void seeded_group(const TGeom& G, int L, int nt0, int m,
+                                             const int32_t* idx, const float* fr0,
+                                             const float4* frh, const float* ssl,
+                                             const float* sbias, float* slb, int lane, int g,
+                                             int r, const float* dxl, const float* dxh) {
+  const int R = 2 * m, d0 = G.d[0];
+  v4f F[TNP][4];
+  double acc[TNP], cz[TNP];
+  // W_L[j][k] = A_L[k][j]: K-step 4 (j / 16) + j % 4, lane group (j % 16) / 4,
+  // lane 4 g + i of it, component t for k = 16 t + 4 g + i
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int row = 16 * (nt0 + p) + r;
+    const bool live = row < R;
+    const int q = live ? (row < m ? row : row - m) : 0;
+    const float sg = row < m ? 1.f : -1.f;
+    const int j = live ? idx[q] : 0;
+    const int ksj = 4 * (j >> 4) + (j & 3), gj = (j & 15) >> 2;
+    acc[p] = (live && g == 0) ? (double)(sg * sbias[L * FW + j]) : 0.0;
+    cz[p] = 0.0;
+    if (L > 0) {
+      const float4* fl = frh + (L - 1) * KS * 64 + ksj * 64 + 16 * gj + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 w = live ? fl[i] : float4{0.f, 0.f, 0.f, 0.f};
+        F[p][0][i] = sg * w.x;
+        F[p][1][i] = sg * w.y;
+        F[p][2][i] = sg * w.z;
+        F[p][3][i] = sg * w.w;
+      }
+    } else if (live) {
+      // seeded at relu 0: the row is +-W_0[j] over the inputs
+      for (int mt = 0; mt < G.mt0; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int mi = 16 * mt + 4 * g + i;
+          if (mi < d0) {
+            const float v = sg * fr0[(mt * KS + ksj) * 64 + 16 * gj + 4 * g + i];
+            cz[p] += (double)(fmaxf(v, 0.f) * dxl[mi]);
+            cz[p] += (double)(fminf(v, 0.f) * dxh[mi]);
+          }
+        }
+    }
+  }
+  if (L > 0)
+    chain_to_input<MT, KS, NP, BROW>(G, L - 1, fr0, frh, ssl, sbias, lane, g, r, dxl, dxh, F, acc,
+                                     cz, nullptr, 0);
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const double lbd = group_sum4_d(acc[p] + cz[p]);
+    const int row = 16 * (nt0 + p) + r;
+    if (g == 0 && row < R) slb[row] = (float)lbd;
+  }
+}
+
+// One group of NP spec row tiles (rows q0 + 16 p + r of the Q shared rows)
+// through relu n-1 .. relu 0; lb, acc and the input coefficients out.
+template <int MT, int KS, int NP, bool BROW>
+__device__ __forceinline__ void spec_group(const TGeom& G, int q0, int Q, const float* spec_rows,
+                                           const float* spec_acc, const float* fr0,
+                                           const float4* frh, const float* ssl,
+                                           const float* sbias, int lane, int g, int r,
+                                           const float* dxl, const float* dxh, int64_t dom,
+                                           float* lb_out, float* A_out, float* acc_out) {
+  const int n = G.n, d0 = G.d[0], dN = G.d[n];
+  v4f F[TNP][4];
+  double acc[TNP], cz[TNP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int row = q0 + 16 * p + r;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int k = 16 * t + 4 * g + i;
+        F[p][t][i] = (row < Q && k < dN) ? spec_rows[row * dN + k] : 0.f;
+      }
+    acc[p] = (row < Q && g == 0) ? (double)spec_acc[row] : 0.0;
+    cz[p] = 0.0;
+  }
+  float* A_rows = A_out ? A_out + (dom * Q + q0) * d0 : nullptr;
+  chain_to_input<MT, KS, NP, BROW>(G, n - 1, fr0, frh, ssl, sbias, lane, g, r, dxl, dxh, F, acc,
+                                   cz, A_rows, Q - q0);
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const double a = group_sum4_d(acc[p]);
+    const double lbd = a + group_sum4_d(cz[p]);
+    const int row = q0 + 16 * p + r;
+    if (g == 0 && row < Q) {
+      lb_out[dom * Q + row] = (float)lbd;
+      if (acc_out) acc_out[dom * Q + row] = (float)a;
+    }
+  }
+}
+
+template <int MT, int KS, bool BROW>
+__global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
+    TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
+    const float* __restrict__ xl, const float* __restrict__ xh, TCrownArgs ca,
+    const int32_t* __restrict__ idx_all, int do_crown, int Q,
+    const float* __restrict__ spec_rows, const float* __restrict__ spec_acc,
+    float* __restrict__ lb_out, float* __restrict__ A_out, float* __restrict__ acc_out) {
+  extern __shared__ float smem[];
+  float* sfrag = smem;
+  float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int n = G.n, d0 = G.d[0];
+  float* ssl = sbias + n * FW + wv * (n * 3 * FW + 4 * FW);  // slopes [layer][3][FW]
+  float* slb = ssl + n * 3 * FW;                              // seeded-row bounds
+  float* stl = slb + 2 * FW;                                  // current layer lo / hi
+  vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
+  for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
+    const int l = k / FW, j = k % FW;
+    sbias[k] = j < G.d[l + 1] ? gbias[G.boff[l] + j] : 0.f;
+  }
+  __syncthreads();
+  const float* fr0 = sfrag;
+  const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
+
+  for (int64_t dom = (int64_t)blockIdx.x * TNW + wv; dom < B; dom += (int64_t)gridDim.x * TNW) {
+    const float* dxl = xl + dom * d0;
+    const float* dxh = xh + dom * d0;
+    for (int L = 0; L < n; ++L) {
+      const int dW = G.d[L + 1];
+      const float* lo_in = ca.lo_in[L] + dom * dW;
+      const float* hi_in = ca.hi_in[L] + dom * dW;
+      for (int j = lane; j < FW; j += 64) {
+        stl[j] = j < dW ? lo_in[j] : 0.f;
+        stl[FW + j] = j < dW ? hi_in[j] : 0.f;
+      }
+      __threadfence_block();
+      const int m = do_crown ? ca.idx_cnt[L] : 0;
+      const int32_t* idx = idx_all + (do_crown ? ca.idx_off[L] : 0);
+      const int R = 2 * m;
+      const int ntiles = (R + 15) / 16;
+      for (int nt0 = 0; nt0 < ntiles; nt0 += TNP) {
+        if (ntiles - nt0 >= TNP)
+          seeded_group<MT, KS, TNP, BROW>(G, L, nt0, m, idx, fr0, frh, ssl, sbias, slb, lane, g,
+                                          r, dxl, dxh);
+        else
+          seeded_group<MT, KS, 1, BROW>(G, L, nt0, m, idx, fr0, frh, ssl, sbias, slb, lane, g, r,
+                                        dxl, dxh);
+      }
+      __threadfence_block();
+      // intersect: lo = max(lo, lb+), hi = max(min(hi, -lb-), lo)
+      for (int q = lane; q < m; q += 64) {
+        const int j = idx[q];
+        const float lc = fmaxf(stl[j], slb[q]);
+        const float hc = fmaxf(fminf(stl[FW + j], -slb[m + q]), lc);
+        stl[j] = lc;
+        stl[FW + j] = hc;
+      }
+      __threadfence_block();
+      if (ca.lo_out[L]) {
+        for (int j = lane; j < dW; j += 64) {
+          ca.lo_out[L][dom * dW + j] = stl[j];
+          ca.hi_out[L][dom * dW + j] = stl[FW + j];
+        }
+      }
+      make_slopes_lds(ssl + L * 3 * FW, stl, stl + FW, dW, lane);
+      __threadfence_block();
+    }
+    for (int q0 = 0; q0 < Q; q0 += 16 * TNP) {
+      // spec rows (shared, Q x d[n]) through relu n-1 ... relu 0
+      if (Q - q0 > 16)
+        spec_group<MT, KS, TNP, BROW>(G, q0, Q, spec_rows, spec_acc, fr0, frh, ssl, sbias, lane,
+                                      g, r, dxl, dxh, dom, lb_out, A_out, acc_out);
+      else
+        spec_group<MT, KS, 1, BROW>(G, q0, Q, spec_rows, spec_acc, fr0, frh, ssl, sbias, lane, g,
+                                    r, dxl, dxh, dom, lb_out, A_out, acc_out);
+    }
+  }
+}
+
+template <int V>
+const void* crown_fn() {
+  return reinterpret_cast<const void*>(
+      &k_crown_tiled<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
+}
+
+}  // namespace
+
+extern "C" int64_t vc_mlp_tiled_floats(const int32_t* dims, int n_relu) {
+  TGeom G;
+  const int rc = tiled_geom(dims, n_relu, G);
+  if (rc != VC_OK) return -rc;
+  return G.nfloats;
+}
+
+extern "C" int vc_mlp_tiled_pack(const float* const* W, const float* const* bias,
+                                 const int32_t* dims, int n_relu, float* frag,
+                                 vc_stream_t stream) {
+  TGeom G;
+  const int rc = tiled_geom(dims, n_relu, G);
+  if (rc != VC_OK) return rc;
+  if (!W || !frag) return VC_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  for (int l = 0; l < n_relu; ++l) {
+    if (!W[l] || (G.brow && (!bias || !bias[l]))) return VC_ERR_ARG;
+    const float* b = G.brow ? bias[l] : nullptr;
+    if (l == 0) {
+      const int total = G.mt0 * G.KS * 64;
+      hipLaunchKernelGGL(k_tpack, dim3((total + 255) / 256), dim3(256), 0, st, W[0], b, G.d[1],
+                         G.d[0], G.KS, G.mt0, 0, G.brow, frag);
+    } else {
+      const int total = 4 * G.KS * 64;
+      hipLaunchKernelGGL(k_tpack, dim3((total + 255) / 256), dim3(256), 0, st, W[l], b,
+                         G.d[l + 1], G.d[l], G.KS, 4, 1, G.brow,
+                         frag + G.offh + (int64_t)(l - 1) * G.KS * 256);
+    }
+  }
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* frag,
+                                  const float* bias_cat, int64_t B, const float* xl,
+                                  const float* xh, const float* const* lo_in,
+                                  const float* const* hi_in, float* const* lo_out,
+                                  float* const* hi_out, const int32_t* idx_all,
+                                  const int32_t* idx_cnt, int do_crown, int Q,
+                                  const float* spec_rows, const float* spec_acc, float* lb_out,
+                                  float* A_out, float* acc_out, vc_stream_t stream) {
+  TGeom G;
+  int rc = tiled_geom(dims, n_relu, G);
+  if (rc != VC_OK) return rc;
+  if (!frag || !bias_cat || !xl || !xh || !lo_in || !hi_in || B < 0) return VC_ERR_ARG;
+  if (Q < 0 || Q > TNP * 16) return VC_ERR_UNSUPPORTED;
+  if (Q > 0 && (!spec_rows || !spec_acc || !lb_out)) return VC_ERR_ARG;
+  if (do_crown && (!idx_all || !idx_cnt || !lo_out || !hi_out)) return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  TCrownArgs ca;
+  int off = 0;
+  for (int l = 0; l < MAXL; ++l) {
+    const bool in = l < n_relu;
+    ca.lo_in[l] = in ? lo_in[l] : nullptr;
+    ca.hi_in[l] = in ? hi_in[l] : nullptr;
+    ca.lo_out[l] = (in && lo_out) ? lo_out[l] : nullptr;
+    ca.hi_out[l] = (in && hi_out) ? hi_out[l] : nullptr;
+    ca.idx_off[l] = off;
+    ca.idx_cnt[l] = (in && do_crown) ? idx_cnt[l] : 0;
+    if (in && (!ca.lo_in[l] || !ca.hi_in[l])) return VC_ERR_ARG;
+    if (in && (ca.idx_cnt[l] < 0 || ca.idx_cnt[l] > G.d[l + 1])) return VC_ERR_ARG;
+    off += ca.idx_cnt[l];
+  }
+  const size_t lds =
+      ((size_t)G.nfloats + (size_t)n_relu * FW + (size_t)TNW * (n_relu * 3 * FW + 4 * FW)) *
+      sizeof(float);
+  if (lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
+  const void* fn = nullptr;
+  switch (G.variant) {
+    case 0: fn = crown_fn<0>(); break;
+    case 1: fn = crown_fn<1>(); break;
+    case 2: fn = crown_fn<2>(); break;
+    case 3: fn = crown_fn<3>(); break;
+    case 4: fn = crown_fn<4>(); break;
+    case 5: fn = crown_fn<5>(); break;
+    default: return VC_ERR_UNSUPPORTED;
+  }
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return VC_ERR_UNSUPPORTED;
+  const dim3 grid(vcm::persistent_grid(B, lds, TNW)), block(TNW * 64);
+  hipStream_t st = (hipStream_t)stream;
+#define VC_TILED_CASE(V)                                                                     \
+  case V:                                                                                    \
+    hipLaunchKernelGGL((k_crown_tiled<kVariants[V].MT, kVariants[V].KS,                      \
+                                      kVariants[V].brow != 0>),                              \
+                       grid, block, lds, st, G, frag, bias_cat, B, xl, xh, ca, idx_all,      \
+                       do_crown, Q, spec_rows, spec_acc, lb_out, A_out, acc_out);            \
+    break;
+  switch (G.variant) {
+    VC_TILED_CASE(0)
+    VC_TILED_CASE(1)
+    VC_TILED_CASE(2)
+    VC_TILED_CASE(3)
+    VC_TILED_CASE(4)
+    VC_TILED_CASE(5)
+    default: return VC_ERR_UNSUPPORTED;
+  }
+#undef VC_TILED_CASE
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}

@@ -65,11 +65,16 @@ SIGNATURES = {
                      _I, _P, _P, _P, _P, _P, _P],
     'vc_mlp_alpha_iter': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
                           _P, _P, _P, _D, _D, _D, _D, _D, _P],
+    'vc_mlp_tiled_floats': [_P, _I],
+    'vc_mlp_tiled_pack': [_P, _P, _P, _I, _P, _P],
+    'vc_mlp_tiled_crown': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _I,
+                           _I, _P, _P, _P, _P, _P, _P],
     'vc_widest_axis': [_P, _P, _L, _I, _P, _P, _P],
     'vc_bisect': [_P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P],
 }
 _RESTYPE = {'vc_compact_workspace': ctypes.c_int64,
-            'vc_mlp_frag_floats': ctypes.c_int64}
+            'vc_mlp_frag_floats': ctypes.c_int64,
+            'vc_mlp_tiled_floats': ctypes.c_int64}
 
 
 def host_array(ctype, values):
@@ -143,6 +148,7 @@ _FLOPS = {
     # 2 * M * n_out * n_in
     'vc_backward_fc': lambda a: 2.0 * a[1] * a[3] * a[11],
     'vc_mlp_crown': _flops_mlp_crown,
+    'vc_mlp_tiled_crown': _flops_mlp_crown,
 }
 
 _timing = None

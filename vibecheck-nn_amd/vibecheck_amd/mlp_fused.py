@@ -18,6 +18,10 @@ MAX_W = 64
 MAX_L = 16
 PLAN_KEY = '_vc_amd_mlp_plan'
 
+# Use the shape-specialised CROWN kernel (vc_mlp_tiled_crown) when the net
+# has an instantiation; switching this off runs vc_mlp_crown.
+TILED = True
+
 
 class MlpPlan:
     """Packed weights of a qualifying network on one device."""
@@ -51,6 +55,14 @@ class MlpPlan:
             buf = torch.empty(nf, device=device)
             call('vc_mlp_pack', wp, self.dims_p, self.n, fwd, ptr(buf), stream())
             self.frag[fwd] = buf
+        # fragments of the shape-specialised CROWN kernel (None: no instantiation)
+        self.tfrag = None
+        nt = int(lib.vc_mlp_tiled_floats(self.dims_p, self.n))
+        if nt > 0:
+            bp_arr, bp = host_array(ctypes.c_void_p, [ptr(b) for b in self.bs])
+            self.tfrag = torch.empty(nt, device=device)
+            call('vc_mlp_tiled_pack', wp, bp, self.dims_p, self.n, ptr(self.tfrag), stream())
+            del bp_arr
         del wp_arr
 
 
@@ -249,7 +261,11 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False):
         if want_linear:
             A = torch.empty(B, Q, plan.dims[0], device=dev)
             acc = torch.empty(B, Q, device=dev)
-    call('vc_mlp_crown', plan.dims_p, plan.n, ptr(plan.frag[0]), ptr(plan.bias_cat), B,
+    if TILED and plan.tfrag is not None:
+        name, frag = 'vc_mlp_tiled_crown', plan.tfrag
+    else:
+        name, frag = 'vc_mlp_crown', plan.frag[0]
+    call(name, plan.dims_p, plan.n, ptr(frag), ptr(plan.bias_cat), B,
          ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
          1 if do_crown else 0, Q, ptr(S), ptr(acc0), ptr(lb), ptr(A), ptr(acc), stream())
     tight = None
