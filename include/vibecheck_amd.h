@@ -366,6 +366,22 @@ int vc_mlp_alpha_iter(const int32_t *dims, int n_relu, const float *frag_bwd,
                       float *lb_out, double b1, double b2, double eps,
                       double step_size, double bc2_sqrt, vc_stream_t stream);
 
+/* vc_mlp_alpha_iter with the tile shape fixed at compile time (same
+ * arguments and results; frag from vc_mlp_tiled_pack; n_relu <= 16 as the
+ * LDS allows, 1 <= Q <= 16): the pre-relaxation rows kept in LDS, the fc
+ * biases carried by the MFMA in both directions.
+ * Replaces one iteration of _run_alpha_crown_inputsplit_batched
+ * (verify_zono_bnb.py:5248-5266). */
+int vc_mlp_tiled_alpha_iter(const int32_t *dims, int n_relu, const float *frag,
+                            const float *bias_cat, int64_t B, const float *xl,
+                            const float *xh, const float *const *lo,
+                            const float *const *hi, float *const *alpha,
+                            float *const *exp_avg, float *const *exp_avg_sq,
+                            int Q, const float *spec_rows,
+                            const float *spec_acc, float *lb_out, double b1,
+                            double b2, double eps, double step_size,
+                            double bc2_sqrt, vc_stream_t stream);
+
 /* ---- Input-split BaB step ---------------------------------------------- */
 
 /* Closure: closed[b] = AND over disjuncts d of (OR over q in d of

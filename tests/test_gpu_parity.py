@@ -236,12 +236,17 @@ def test_spec_backward_parity_cnn(gpu):
     assert_bounds(gA, A, 'cnn spec A', scale=A.abs().amax(-1, keepdim=True))
 
 
-@pytest.fixture(params=['fused', 'layerwise'])
+@pytest.fixture(params=['fused', 'fused_untiled', 'layerwise'])
 def mlp_path(request):
-    old = vz.FUSED_MLP
-    vz.FUSED_MLP = request.param == 'fused'
+    """fused: the whole-network kernels with the shape-specialised CROWN and
+    alpha kernels; fused_untiled: the whole-network kernels with runtime
+    shapes; layerwise: one kernel per layer."""
+    from vibecheck_amd import mlp_fused
+    old = vz.FUSED_MLP, mlp_fused.TILED
+    vz.FUSED_MLP = request.param != 'layerwise'
+    mlp_fused.TILED = request.param == 'fused'
     yield request.param
-    vz.FUSED_MLP = old
+    vz.FUSED_MLP, mlp_fused.TILED = old
 
 
 @pytest.mark.parametrize('case', ['acas_wide_boxes', 'deep_64_fallback'])

@@ -452,6 +452,258 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
   }
 }
 
+// ------------------------------------------------------ alpha-CROWN kernel
+// One Adam iteration of batched alpha-CROWN per domain (verify_zono_bnb.py:
+// 5248-5287), tile shape fixed at compile time: the spec backward with
+// lower slopes active + unstable * alpha, keeping the pre-relaxation rows
+// P_l in LDS; fc_0 fused with the concretization and the first gradient
+// step gE_0 = W_0 gA + b_0, gA = xl [A >= 0] + xh [A <= 0]; then the
+// forward sweep dalpha_l = sum_rows gE_l pos(P_l) (unstable neurons),
+// gP_l = gE_l (mpos ls + mneg up_s) + mneg up_t (torch's clamp subgradient),
+// gE_{l+1} = W_{l+1} gP_l + b_{l+1}, and torch.optim.Adam on -sum lb with
+// the clamp to [0, 1].  Forward products read the backward fragments with a
+// lane permutation; with the bias row, the bias enters as a constant-1
+// entry of the gradient at index d_{l+1}.
+constexpr int ANW = 4;  // waves per workgroup
+
+struct TAlphaArgs {
+  const float* lo[MAXL];
+  const float* hi[MAXL];
+  float* alpha[MAXL];
+  float* m1[MAXL];
+  float* m2[MAXL];
+};
+
+// Set element j (runtime, < 16 MT) of a D-layout block to v in the lanes of
+// its group (the others keep their value).
+template <int MT>
+__device__ __forceinline__ void set_elem(v4f (&X)[4], int j, int g, float v) {
+  const int tb = j >> 4, gb = (j & 15) >> 2, ib = j & 3;
+  if (g != gb) return;
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) X[t][i] = (t == tb && i == ib) ? v : X[t][i];
+}
+
+// Forward product through hidden fc_l (l >= 1): out = W_l X over the
+// neurons of relu l-1 (K-tiles t < MT), read from fc_l's backward fragments
+// ([ks][lane][mt] float4: A[m][k] = W_l[k][m]).
+template <int MT, int KS>
+__device__ __forceinline__ void fc_forward(const float4* fr, int lane, int g, int r,
+                                           const v4f (&X)[4], v4f (&out)[4]) {
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) out[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int mo = 0; mo < MT; ++mo) {
+    const int ksf = 4 * mo + (r & 3);
+    const bool ok = ksf < KS;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 q = ok ? fr[ksf * 64 + 16 * (r >> 2) + 4 * g + i] : float4{0.f, 0.f, 0.f, 0.f};
+      const float a[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int t = 0; t < MT; ++t) out[mo] = mfma16x16x4(a[t], X[t][i], out[mo]);
+    }
+  }
+}
+
+template <int MT, int KS, bool BROW>
+__global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
+    TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
+    const float* __restrict__ xl, const float* __restrict__ xh, TAlphaArgs aa, int Q,
+    const float* __restrict__ spec_rows, const float* __restrict__ spec_acc,
+    float* __restrict__ lb_out, AdamConst adam) {
+  extern __shared__ float smem[];
+  float* sfrag = smem;
+  float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int n = G.n, d0 = G.d[0], dN = G.d[n];
+  const int wsz = n * 7 * FW + n * KS * 4 * Q + FW;
+  float* ssl = sbias + n * FW + wv * wsz;  // [l][ls_eff, us, ut, unstable][FW]
+  float* sad = ssl + n * 4 * FW;           // [l][alpha, m, v][FW]
+  float* sP = sad + n * 3 * FW;            // [l][ks][g][r < Q]
+  float* sga = sP + n * KS * 4 * Q;        // d lb / d alpha of one layer [FW]
+  vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
+  for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
+    const int l = k / FW, j = k % FW;
+    sbias[k] = j < G.d[l + 1] ? gbias[G.boff[l] + j] : 0.f;
+  }
+  __syncthreads();
+  const float* fr0 = sfrag;
+  const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
+  const bool live = r < Q;
+
+  for (int64_t dom = (int64_t)blockIdx.x * ANW + wv; dom < B; dom += (int64_t)gridDim.x * ANW) {
+    const float* dxl = xl + dom * d0;
+    const float* dxh = xh + dom * d0;
+    for (int l = 0; l < n; ++l) {
+      const int dW = G.d[l + 1];
+      float* sl = ssl + l * 4 * FW;
+      float* sa = sad + l * 3 * FW;
+      for (int j = lane; j < FW; j += 64) {
+        float ls = 0.f, us = 0.f, ut = 0.f, un = 0.f, a = 0.f, m1 = 0.f, m2 = 0.f;
+        if (j < dW) {
+          const int64_t ai = dom * dW + j;
+          const Relax s = relax(aa.lo[l][ai], aa.hi[l][ai]);
+          a = aa.alpha[l][ai];
+          m1 = aa.m1[l][ai];
+          m2 = aa.m2[l][ai];
+          ls = s.active ? 1.f : (s.unstable ? a : 0.f);
+          us = s.up_s;
+          ut = s.up_t;
+          un = s.unstable ? 1.f : 0.f;
+        }
+        sl[j] = ls;
+        sl[FW + j] = us;
+        sl[2 * FW + j] = ut;
+        sl[3 * FW + j] = un;
+        sa[j] = a;
+        sa[FW + j] = m1;
+        sa[2 * FW + j] = m2;
+      }
+    }
+    __threadfence_block();
+    // ---- spec backward with alpha, keeping P_l
+    v4f F[TNP][4];
+    double acc[TNP], cz[TNP];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int k = 16 * t + 4 * g + i;
+        F[0][t][i] = (live && k < dN) ? spec_rows[r * dN + k] : 0.f;
+      }
+    acc[0] = (live && g == 0) ? (double)spec_acc[r] : 0.0;
+    cz[0] = 0.0;
+    for (int l = n - 1; l >= 0; --l) {
+      if (live) {
+        float* pl = sP + l * KS * 4 * Q;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) pl[(ks * 4 + g) * Q + r] = F[0][ks >> 2][ks & 3];
+      }
+      relax_rows<KS, 1, BROW>(ssl + l * 4 * FW, sbias + l * FW, g, F, acc);
+      if (l > 0) fc_hidden<MT, KS, 1, BROW>(frh + (l - 1) * KS * 64, lane, g, G.d[l], F, acc);
+    }
+    // ---- fc_0, concretization and gE_0 = W_0 gA + b_0, one input tile at a time
+    v4f GE[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) GE[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < G.mt0; ++mt) {
+      v4f o = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) o = mfma16x16x4(fr0[(mt * KS + ks) * 64 + lane], F[0][ks >> 2][ks & 3], o);
+      float gA[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 16 * mt + 4 * g + i;
+        const float v = o[i];
+        gA[i] = 0.f;
+        if (m < d0) {
+          const float xlv = dxl[m], xhv = dxh[m];
+          cz[0] += (double)(fmaxf(v, 0.f) * xlv);
+          cz[0] += (double)(fminf(v, 0.f) * xhv);
+          float gv = 0.f;
+          if (v >= 0.f) gv += xlv;
+          if (v <= 0.f) gv += xhv;
+          gA[i] = live ? gv : 0.f;
+        } else if (BROW && m == d0) {
+          acc[0] += (double)v;
+          gA[i] = live ? 1.f : 0.f;
+        }
+      }
+      // A_fwd0[m'][k'] = A_0[k'][m']: lane (g, r), M-tile mo, K-step (mt, i)
+#pragma unroll
+      for (int mo = 0; mo < MT; ++mo) {
+        const int ksf = 4 * mo + (r & 3);
+        const bool ok = ksf < KS;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = ok ? fr0[(mt * KS + ksf) * 64 + 16 * (r >> 2) + 4 * g + i] : 0.f;
+          GE[mo] = mfma16x16x4(a, gA[i], GE[mo]);
+        }
+      }
+    }
+    {
+      const double lbd = group_sum4_d(acc[0] + cz[0]);
+      if (g == 0 && live) lb_out[dom * Q + r] = (float)lbd;
+    }
+    // ---- forward gradient sweep with the Adam update per layer
+    for (int l = 0; l < n; ++l) {
+      const int dW = G.d[l + 1];
+      const float* sl = ssl + l * 4 * FW;
+      if (!BROW) {
+        // bias of fc_l (l >= 0) added for live rows: gE_l += b_l
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            GE[t][i] = live ? GE[t][i] + sbias[l * FW + 16 * t + 4 * g + i] : 0.f;
+      }
+      const float* pl = sP + l * KS * 4 * Q;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int t = ks >> 2, i = ks & 3;
+        const int j = 16 * t + 4 * g + i;
+        const float pv = live ? pl[(ks * 4 + g) * Q + r] : 0.f;
+        const float ge = GE[t][i];
+        float s = ge * fmaxf(pv, 0.f);
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 4, 64);
+        s += __shfl_xor(s, 8, 64);
+        if (r == 0) sga[j] = s;
+        const bool mp = pv >= 0.f, mn = pv <= 0.f;
+        float gp = ge * ((mp ? sl[j] : 0.f) + (mn ? sl[FW + j] : 0.f));
+        if (mn) gp = gp + sl[2 * FW + j];
+        GE[t][i] = live ? gp : 0.f;
+      }
+      __threadfence_block();
+      {
+        float* sa = sad + l * 3 * FW;
+        const int j = lane;
+        if (j < dW && sl[3 * FW + j] != 0.f) {
+          float mi = sa[FW + j], vi = sa[2 * FW + j];
+          float pa = adam_update(sa[j], -sga[j], mi, vi, adam);
+          pa = fminf(fmaxf(pa, 0.f), 1.f);
+          sa[FW + j] = mi;
+          sa[2 * FW + j] = vi;
+          sa[j] = pa;
+        }
+      }
+      __threadfence_block();
+      if (l + 1 < n) {
+        // the rows at relu l's output (K of fc_{l+1}); with the bias row, a
+        // constant 1 at index d_{l+1} picks up b_{l+1}
+        if (BROW) set_elem<MT>(GE, dW, g, live ? 1.f : 0.f);
+        v4f nx[4];
+        fc_forward<MT, KS>(frh + l * KS * 64, lane, g, r, GE, nx);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) GE[mt] = nx[mt];
+      }
+    }
+    // write the updated Adam state back (coalesced)
+    for (int l = 0; l < n; ++l) {
+      const int dW = G.d[l + 1];
+      const float* sa = sad + l * 3 * FW;
+      for (int j = lane; j < dW; j += 64) {
+        const int64_t ai = dom * dW + j;
+        aa.alpha[l][ai] = sa[j];
+        aa.m1[l][ai] = sa[FW + j];
+        aa.m2[l][ai] = sa[2 * FW + j];
+      }
+    }
+    __threadfence_block();
+  }
+}
+
+template <int V>
+const void* alpha_fn() {
+  return reinterpret_cast<const void*>(
+      &k_alpha_tiled<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
+}
+
 template <int V>
 const void* crown_fn() {
   return reinterpret_cast<const void*>(
@@ -558,6 +810,72 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
     default: return VC_ERR_UNSUPPORTED;
   }
 #undef VC_TILED_CASE
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const float* frag,
+                                       const float* bias_cat, int64_t B, const float* xl,
+                                       const float* xh, const float* const* lo,
+                                       const float* const* hi, float* const* alpha,
+                                       float* const* exp_avg, float* const* exp_avg_sq, int Q,
+                                       const float* spec_rows, const float* spec_acc,
+                                       float* lb_out, double b1, double b2, double eps,
+                                       double step_size, double bc2_sqrt, vc_stream_t stream) {
+  TGeom G;
+  int rc = tiled_geom(dims, n_relu, G);
+  if (rc != VC_OK) return rc;
+  if (Q < 1 || Q > 16) return VC_ERR_UNSUPPORTED;
+  if (!frag || !bias_cat || !xl || !xh || !lo || !hi || !alpha || !exp_avg || !exp_avg_sq ||
+      !spec_rows || !spec_acc || !lb_out || B < 0)
+    return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  TAlphaArgs aa;
+  for (int l = 0; l < MAXL; ++l) {
+    const bool in = l < n_relu;
+    aa.lo[l] = in ? lo[l] : nullptr;
+    aa.hi[l] = in ? hi[l] : nullptr;
+    aa.alpha[l] = in ? alpha[l] : nullptr;
+    aa.m1[l] = in ? exp_avg[l] : nullptr;
+    aa.m2[l] = in ? exp_avg_sq[l] : nullptr;
+    if (in && (!aa.lo[l] || !aa.hi[l] || !aa.alpha[l] || !aa.m1[l] || !aa.m2[l]))
+      return VC_ERR_ARG;
+  }
+  const size_t wsz = (size_t)n_relu * 7 * FW + (size_t)n_relu * G.KS * 4 * Q + FW;
+  const size_t lds = ((size_t)G.nfloats + (size_t)n_relu * FW + ANW * wsz) * sizeof(float);
+  if (lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
+  const void* fn = nullptr;
+  switch (G.variant) {
+    case 0: fn = alpha_fn<0>(); break;
+    case 1: fn = alpha_fn<1>(); break;
+    case 2: fn = alpha_fn<2>(); break;
+    case 3: fn = alpha_fn<3>(); break;
+    case 4: fn = alpha_fn<4>(); break;
+    case 5: fn = alpha_fn<5>(); break;
+    default: return VC_ERR_UNSUPPORTED;
+  }
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return VC_ERR_UNSUPPORTED;
+  const dim3 grid(vcm::persistent_grid(B, lds, ANW)), block(ANW * 64);
+  const AdamConst adam = adam_const(b1, b2, eps, step_size, bc2_sqrt);
+  hipStream_t st = (hipStream_t)stream;
+#define VC_TALPHA_CASE(V)                                                                    \
+  case V:                                                                                    \
+    hipLaunchKernelGGL((k_alpha_tiled<kVariants[V].MT, kVariants[V].KS,                      \
+                                      kVariants[V].brow != 0>),                              \
+                       grid, block, lds, st, G, frag, bias_cat, B, xl, xh, aa, Q, spec_rows, \
+                       spec_acc, lb_out, adam);                                              \
+    break;
+  switch (G.variant) {
+    VC_TALPHA_CASE(0)
+    VC_TALPHA_CASE(1)
+    VC_TALPHA_CASE(2)
+    VC_TALPHA_CASE(3)
+    VC_TALPHA_CASE(4)
+    VC_TALPHA_CASE(5)
+    default: return VC_ERR_UNSUPPORTED;
+  }
+#undef VC_TALPHA_CASE
   VC_LAUNCH_CHECK();
   return VC_OK;
 }

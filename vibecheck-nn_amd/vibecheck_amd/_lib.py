@@ -69,6 +69,8 @@ SIGNATURES = {
     'vc_mlp_tiled_pack': [_P, _P, _P, _I, _P, _P],
     'vc_mlp_tiled_crown': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _I,
                            _I, _P, _P, _P, _P, _P, _P],
+    'vc_mlp_tiled_alpha_iter': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
+                                _P, _P, _P, _D, _D, _D, _D, _D, _P],
     'vc_widest_axis': [_P, _P, _L, _I, _P, _P, _P],
     'vc_bisect': [_P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P],
 }

@@ -175,8 +175,14 @@ ALPHA_MAX_L = 7
 ALPHA_MAX_Q = 16
 
 
+def _tiled(plan):
+    return TILED and plan.tfrag is not None
+
+
 def alpha_supported(plan, Q):
-    return plan.n <= ALPHA_MAX_L and 1 <= Q <= ALPHA_MAX_Q
+    if not 1 <= Q <= ALPHA_MAX_Q:
+        return False
+    return _tiled(plan) or plan.n <= ALPHA_MAX_L
 
 
 def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps):
@@ -208,9 +214,13 @@ def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps)
     prev_max = -float('inf')
     cur_lr = float(lr)
     n_eval = 0
+    if _tiled(plan):
+        name, frag = 'vc_mlp_tiled_alpha_iter', plan.tfrag
+    else:
+        name, frag = 'vc_mlp_alpha_iter', plan.frag[0]
     for it in range(n_iters):
         step = it + 1
-        call('vc_mlp_alpha_iter', plan.dims_p, plan.n, ptr(plan.frag[0]), ptr(plan.bias_cat),
+        call(name, plan.dims_p, plan.n, ptr(frag), ptr(plan.bias_cat),
              B, ptr(xl), ptr(xh), *ptrs, Q, ptr(S), ptr(acc0), ptr(lb), b1, b2, eps,
              cur_lr / (1 - b1 ** step), (1 - b2 ** step) ** 0.5, st)
         n_eval += 1
@@ -261,7 +271,7 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False):
         if want_linear:
             A = torch.empty(B, Q, plan.dims[0], device=dev)
             acc = torch.empty(B, Q, device=dev)
-    if TILED and plan.tfrag is not None:
+    if _tiled(plan):
         name, frag = 'vc_mlp_tiled_crown', plan.tfrag
     else:
         name, frag = 'vc_mlp_crown', plan.frag[0]
