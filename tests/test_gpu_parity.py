@@ -249,13 +249,25 @@ def mlp_path(request):
     vz.FUSED_MLP, mlp_fused.TILED = old
 
 
+@pytest.mark.parametrize('tiled', [True, False])
 @pytest.mark.parametrize('case', ['acas_wide_boxes', 'deep_64_fallback'])
-def test_fused_zono_bounds_parity_with_overflow(gpu, case):
-    """Whole-network zonotope kernel.  acas_wide_boxes: very wide boxes push
-    domains past the 128 generator columns of one wavefront; they are
-    redone by the 4-wave cooperative pass (<= 512 columns).  deep_64_fallback:
-    ten 64-wide layers exceed even that, so those domains take the
-    layer-wise kernels."""
+def test_fused_zono_bounds_parity_with_overflow(gpu, case, tiled):
+    """Whole-network zonotope kernel (tiled: the shape-specialised first
+    pass, bias row in the A operand for the ACAS shape, without it for the
+    64-wide net).  acas_wide_boxes: very wide boxes push domains past the
+    128 generator columns of one wavefront; they are redone by the 4-wave
+    cooperative pass (<= 512 columns).  deep_64_fallback: ten 64-wide layers
+    exceed even that, so those domains take the layer-wise kernels."""
+    from vibecheck_amd import mlp_fused
+    old_tiled = mlp_fused.TILED
+    mlp_fused.TILED = tiled
+    try:
+        _zono_overflow_case(gpu, case)
+    finally:
+        mlp_fused.TILED = old_tiled
+
+
+def _zono_overflow_case(gpu, case):
     if case == 'acas_wide_boxes':
         gg_c, gg_g, xl, xh = acas(gpu, 1024, scale=3.0)
         xl[:64] = xl[:64] * 40.0 - 20.0

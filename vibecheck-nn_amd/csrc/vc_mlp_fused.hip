@@ -1048,6 +1048,36 @@ extern "C" int vc_mlp_zono_bounds(const int32_t* dims, int n_relu, const float* 
   return VC_OK;
 }
 
+extern "C" int vc_mlp_zono_wide(const int32_t* dims, int n_relu, const float* frag_fwd,
+                                const float* bias_cat, int64_t B, const float* xl,
+                                const float* xh, float* const* lo_out, float* const* hi_out,
+                                int32_t* overflow, vc_stream_t stream) {
+  Net net{};
+  int rc = build_net_fwd(dims, n_relu, net);
+  if (rc != VC_OK) return rc;
+  if (!frag_fwd || !bias_cat || !xl || !xh || !lo_out || !hi_out || !overflow || B < 0)
+    return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  ZonoArgs za;
+  for (int l = 0; l < MAXL; ++l) {
+    za.lo[l] = l < n_relu ? lo_out[l] : nullptr;
+    za.hi[l] = l < n_relu ? hi_out[l] : nullptr;
+    if (l < n_relu && (!za.lo[l] || !za.hi[l])) return VC_ERR_ARG;
+  }
+  const size_t lds_c = ((size_t)net.nfrag * 64 + ((net.nbias + 63) & ~63) +
+                        (size_t)ZC_W * 2 * FW + FW) * sizeof(float);
+  if (lds_c > 160 * 1024) return VC_ERR_UNSUPPORTED;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_mlp_zono_coop),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_c) != hipSuccess)
+    return VC_ERR_UNSUPPORTED;
+  int64_t gw = cu_count();
+  if (gw > B) gw = B;
+  hipLaunchKernelGGL(k_mlp_zono_coop, dim3((unsigned)gw), dim3(ZC_W * 64), lds_c,
+                     (hipStream_t)stream, net, frag_fwd, bias_cat, B, xl, xh, za, overflow);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
 extern "C" int vc_mlp_alpha_iter(const int32_t* dims, int n_relu, const float* frag_bwd,
                                  const float* bias_cat, int64_t B, const float* xl,
                                  const float* xh, const float* const* lo, const float* const* hi,

@@ -486,25 +486,40 @@ __device__ __forceinline__ void set_elem(v4f (&X)[4], int j, int g, float v) {
     for (int i = 0; i < 4; ++i) X[t][i] = (t == tb && i == ib) ? v : X[t][i];
 }
 
-// Forward product through hidden fc_l (l >= 1): out = W_l X over the
-// neurons of relu l-1 (K-tiles t < MT), read from fc_l's backward fragments
-// ([ks][lane][mt] float4: A[m][k] = W_l[k][m]).
-template <int MT, int KS>
+// Forward product through hidden fc_l (l >= 1) of NX column tiles:
+// out = W_l X over the neurons of relu l-1 (K-tiles t < MT), read from
+// fc_l's backward fragments ([ks][lane][mt] float4: A[m][k] = W_l[k][m]):
+// lane (g, r) of output M-tile mo at K-step (t, i) needs
+// W_l[16 mo + r][16 t + 4 g + i], component t of the float4 at K-step
+// 4 mo + r % 4, lane 16 (r / 4) + 4 g + i.  The M-tiles of all NX tiles are
+// independent accumulators, interleaved.
+template <int MT, int KS, int NX, int NT>
 __device__ __forceinline__ void fc_forward(const float4* fr, int lane, int g, int r,
-                                           const v4f (&X)[4], v4f (&out)[4]) {
+                                           const v4f (&X)[NT][4], int x0, v4f (&out)[NX][4]) {
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) out[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int x = 0; x < NX; ++x)
 #pragma unroll
-  for (int mo = 0; mo < MT; ++mo) {
-    const int ksf = 4 * mo + (r & 3);
-    const bool ok = ksf < KS;
+    for (int mt = 0; mt < 4; ++mt) out[x][mt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 q = ok ? fr[ksf * 64 + 16 * (r >> 2) + 4 * g + i] : float4{0.f, 0.f, 0.f, 0.f};
-      const float a[4] = {q.x, q.y, q.z, q.w};
+  for (int i = 0; i < 4; ++i) {
+    float a[MT][4];
 #pragma unroll
-      for (int t = 0; t < MT; ++t) out[mo] = mfma16x16x4(a[t], X[t][i], out[mo]);
+    for (int mo = 0; mo < MT; ++mo) {
+      const int ksf = 4 * mo + (r & 3);
+      const float4 q = ksf < KS ? fr[ksf * 64 + 16 * (r >> 2) + 4 * g + i]
+                                : float4{0.f, 0.f, 0.f, 0.f};
+      a[mo][0] = q.x;
+      a[mo][1] = q.y;
+      a[mo][2] = q.z;
+      a[mo][3] = q.w;
     }
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int mo = 0; mo < MT; ++mo)
+#pragma unroll
+        for (int x = 0; x < NX; ++x)
+          out[x][mo] = mfma16x16x4(a[mo][t], X[x0 + x][t][i], out[x][mo]);
   }
 }
 
@@ -615,15 +630,13 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
       }
       // A_fwd0[m'][k'] = A_0[k'][m']: lane (g, r), M-tile mo, K-step (mt, i)
 #pragma unroll
-      for (int mo = 0; mo < MT; ++mo) {
-        const int ksf = 4 * mo + (r & 3);
-        const bool ok = ksf < KS;
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float a = ok ? fr0[(mt * KS + ksf) * 64 + 16 * (r >> 2) + 4 * g + i] : 0.f;
+        for (int mo = 0; mo < MT; ++mo) {
+          const int ksf = 4 * mo + (r & 3);
+          const float a = ksf < KS ? fr0[(mt * KS + ksf) * 64 + 16 * (r >> 2) + 4 * g + i] : 0.f;
           GE[mo] = mfma16x16x4(a, gA[i], GE[mo]);
         }
-      }
     }
     {
       const double lbd = group_sum4_d(acc[0] + cz[0]);
@@ -677,10 +690,12 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
         // the rows at relu l's output (K of fc_{l+1}); with the bias row, a
         // constant 1 at index d_{l+1} picks up b_{l+1}
         if (BROW) set_elem<MT>(GE, dW, g, live ? 1.f : 0.f);
-        v4f nx[4];
-        fc_forward<MT, KS>(frh + l * KS * 64, lane, g, r, GE, nx);
+        v4f xin[1][4], nx[1][4];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) GE[mt] = nx[mt];
+        for (int mt = 0; mt < 4; ++mt) xin[0][mt] = GE[mt];
+        fc_forward<MT, KS, 1, 1>(frh + l * KS * 64, lane, g, r, xin, 0, nx);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) GE[mt] = nx[0][mt];
       }
     }
     // write the updated Adam state back (coalesced)
@@ -702,6 +717,201 @@ template <int V>
 const void* alpha_fn() {
   return reinterpret_cast<const void*>(
       &k_alpha_tiled<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
+}
+
+// --------------------------------------------------------- zonotope kernel
+// Zonotope pre-activation bounds (verify_zono_bnb.py:3079-3211), one
+// wavefront per domain, tile shape fixed at compile time.  The generator
+// matrix lives in registers as ZT column tiles in the D layout (rows =
+// neurons, column 0 = centre, then the input generators, then one column
+// per unstable neuron appended at each relu).  fc products read the tiled
+// backward fragments in the forward direction; the bias enters through a
+// constant 1 in the centre column at the bias row.
+constexpr int ZNW = 8;  // waves per workgroup
+constexpr int ZT = 8;   // column tiles per wave: 128 columns, centre included
+
+struct TZonoArgs {
+  float* lo[MAXL];
+  float* hi[MAXL];
+};
+
+template <int MT, int KS, bool BROW>
+__global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* __restrict__ gfrag,
+                                                         const float* __restrict__ gbias,
+                                                         int64_t B, const float* __restrict__ xl,
+                                                         const float* __restrict__ xh,
+                                                         TZonoArgs out, int32_t* overflow) {
+  extern __shared__ float smem[];
+  float* sfrag = smem;
+  float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int n = G.n, d0 = G.d[0];
+  vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
+  for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
+    const int l = k / FW, j = k % FW;
+    sbias[k] = j < G.d[l + 1] ? gbias[G.boff[l] + j] : 0.f;
+  }
+  __syncthreads();
+  const float* fr0 = sfrag;
+  const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
+
+  for (int64_t dom = (int64_t)blockIdx.x * ZNW + wv; dom < B; dom += (int64_t)gridDim.x * ZNW) {
+    const float* dxl = xl + dom * d0;
+    const float* dxh = xh + dom * d0;
+    v4f Z[ZT][4];
+    int Kc = 1 + d0;
+    bool ovf = Kc > 16 * ZT;
+    // ---- fc_0 on the input block: column 0 = centre, column 1 + k = radius k
+#pragma unroll
+    for (int nt0 = 0; nt0 < ZT; nt0 += 2) {
+      v4f o[2][4];
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) o[p][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+      if (!ovf && 16 * nt0 < Kc) {
+        for (int mt = 0; mt < G.mt0; ++mt) {
+          float in[2][4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int k = 16 * mt + 4 * g + i;
+            float c = 0.f, rd = 0.f;
+            if (k < d0) {
+              const float lv = dxl[k], hv = dxh[k];
+              c = (lv + hv) / 2.f;
+              rd = (hv - lv) / 2.f;
+            } else if (BROW && k == d0) {
+              c = 1.f;
+            }
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+              const int col = 16 * (nt0 + p) + r;
+              in[p][i] = col == 0 ? c : (col == 1 + k && k < d0 ? rd : 0.f);
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int mo = 0; mo < MT; ++mo) {
+              const int ksf = 4 * mo + (r & 3);
+              const float a =
+                  ksf < KS ? fr0[(mt * KS + ksf) * 64 + 16 * (r >> 2) + 4 * g + i] : 0.f;
+#pragma unroll
+              for (int p = 0; p < 2; ++p) o[p][mo] = mfma16x16x4(a, in[p][i], o[p][mo]);
+            }
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        Z[nt0][mt] = o[0][mt];
+        Z[nt0 + 1][mt] = o[1][mt];
+      }
+    }
+    if (!BROW && r == 0) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Z[0][t][i] = Z[0][t][i] + sbias[16 * t + 4 * g + i];
+    }
+    for (int l = 0; l < n && !ovf; ++l) {
+      if (l > 0) {
+        // fc_l on the used column tiles; the centre column picks up b_l
+        if (BROW && r == 0) set_elem<MT>(Z[0], G.d[l], g, 1.f);
+        const float4* fr = frh + (l - 1) * KS * 64;
+#pragma unroll
+        for (int nt0 = 0; nt0 < ZT; nt0 += 2) {
+          if (16 * nt0 < Kc) {
+            v4f o[2][4];
+            fc_forward<MT, KS, 2, ZT>(fr, lane, g, r, Z, nt0, o);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+              Z[nt0][mt] = o[0][mt];
+              Z[nt0 + 1][mt] = o[1][mt];
+            }
+          }
+        }
+        if (!BROW && r == 0) {
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              Z[0][t][i] = Z[0][t][i] + sbias[l * FW + 16 * t + 4 * g + i];
+        }
+      }
+      // relu_l: rad_j = sum over generator columns of |G|; lo/hi = c -/+ rad
+      const int dM = G.d[l + 1];
+      float mu[MT][4];
+      uint64_t umask = 0;
+      const bool last = l == n - 1;
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          double sd = 0.0;
+#pragma unroll
+          for (int nt = 0; nt < ZT; ++nt)
+            if (nt > 0 || r > 0) sd += (double)fabsf(Z[nt][t][i]);
+          sd += __shfl_xor(sd, 1, 64);
+          sd += __shfl_xor(sd, 2, 64);
+          sd += __shfl_xor(sd, 4, 64);
+          sd += __shfl_xor(sd, 8, 64);
+          const float rad = (float)sd;
+          const float c = __shfl(Z[0][t][i], lane & 48, 64);
+          const int j = 16 * t + 4 * g + i;
+          const float lo = c - rad, hi = c + rad;
+          const bool valid = j < dM;
+          const bool ust = valid && lo < 0.f && hi > 0.f;
+          const bool dead = hi <= 0.f;
+          if (valid && r == 0) {
+            out.lo[l][dom * dM + j] = lo;
+            out.hi[l][dom * dM + j] = hi;
+          }
+          const float lam = ust ? hi / (hi - lo) : (dead ? 0.f : 1.f);
+          mu[t][i] = ust ? (-hi * lo) / (2.f * (hi - lo)) : 0.f;
+          // scale the row by lambda (centre: lambda c + mu); a domain that
+          // overflows below discards its matrix anyway
+          if (!last) {
+#pragma unroll
+            for (int nt = 0; nt < ZT; ++nt)
+              Z[nt][t][i] = (nt == 0 && r == 0) ? lam * Z[nt][t][i] + mu[t][i] : Z[nt][t][i] * lam;
+          }
+          const uint64_t bal = __ballot(ust && r == 0);
+#pragma unroll
+          for (int gg = 0; gg < 4; ++gg)
+            if ((bal >> (16 * gg)) & 1ull) umask |= 1ull << (16 * t + 4 * gg + i);
+        }
+      const int cnt = __popcll(umask);
+      if (last) break;  // the last relu's output is not propagated
+      if (Kc + cnt > 16 * ZT) {
+        ovf = true;
+        break;
+      }
+      // append one column per unstable neuron at position Kc + rank
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = 16 * t + 4 * g + i;
+          if ((umask >> j) & 1ull) {
+            const int col = Kc + __popcll(umask & ((1ull << j) - 1ull));
+            if ((col & 15) == r) {
+#pragma unroll
+              for (int nt = 0; nt < ZT; ++nt)
+                if (nt == (col >> 4)) Z[nt][t][i] = mu[t][i];
+            }
+          }
+        }
+      Kc += cnt;
+    }
+    if (lane == 0) overflow[dom] = ovf ? 1 : 0;
+  }
+}
+
+template <int V>
+const void* zono_fn() {
+  return reinterpret_cast<const void*>(
+      &k_zono_tiled<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
 }
 
 template <int V>
@@ -876,6 +1086,59 @@ extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const fl
     default: return VC_ERR_UNSUPPORTED;
   }
 #undef VC_TALPHA_CASE
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const float* frag,
+                                        const float* bias_cat, int64_t B, const float* xl,
+                                        const float* xh, float* const* lo_out,
+                                        float* const* hi_out, int32_t* overflow,
+                                        vc_stream_t stream) {
+  TGeom G;
+  int rc = tiled_geom(dims, n_relu, G);
+  if (rc != VC_OK) return rc;
+  if (!frag || !bias_cat || !xl || !xh || !lo_out || !hi_out || !overflow || B < 0)
+    return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  TZonoArgs za;
+  for (int l = 0; l < MAXL; ++l) {
+    za.lo[l] = l < n_relu ? lo_out[l] : nullptr;
+    za.hi[l] = l < n_relu ? hi_out[l] : nullptr;
+    if (l < n_relu && (!za.lo[l] || !za.hi[l])) return VC_ERR_ARG;
+  }
+  const size_t lds = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float);
+  if (lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
+  const void* fn = nullptr;
+  switch (G.variant) {
+    case 0: fn = zono_fn<0>(); break;
+    case 1: fn = zono_fn<1>(); break;
+    case 2: fn = zono_fn<2>(); break;
+    case 3: fn = zono_fn<3>(); break;
+    case 4: fn = zono_fn<4>(); break;
+    case 5: fn = zono_fn<5>(); break;
+    default: return VC_ERR_UNSUPPORTED;
+  }
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return VC_ERR_UNSUPPORTED;
+  const dim3 grid(vcm::persistent_grid(B, lds, ZNW)), block(ZNW * 64);
+  hipStream_t st = (hipStream_t)stream;
+#define VC_TZONO_CASE(V)                                                                     \
+  case V:                                                                                    \
+    hipLaunchKernelGGL((k_zono_tiled<kVariants[V].MT, kVariants[V].KS,                       \
+                                     kVariants[V].brow != 0>),                               \
+                       grid, block, lds, st, G, frag, bias_cat, B, xl, xh, za, overflow);    \
+    break;
+  switch (G.variant) {
+    VC_TZONO_CASE(0)
+    VC_TZONO_CASE(1)
+    VC_TZONO_CASE(2)
+    VC_TZONO_CASE(3)
+    VC_TZONO_CASE(4)
+    VC_TZONO_CASE(5)
+    default: return VC_ERR_UNSUPPORTED;
+  }
+#undef VC_TZONO_CASE
   VC_LAUNCH_CHECK();
   return VC_OK;
 }

@@ -120,8 +120,17 @@ def zono_bounds(plan, xl, xh, fallback):
     ovf = torch.empty(B, dtype=torch.int32, device=dev)
     lo_a, lo_p = host_array(ctypes.c_void_p, [ptr(t) for t in lo])
     hi_a, hi_p = host_array(ctypes.c_void_p, [ptr(t) for t in hi])
-    call('vc_mlp_zono_bounds', plan.dims_p, plan.n, ptr(plan.frag[1]),
-         ptr(plan.bias_cat), B, ptr(xl), ptr(xh), lo_p, hi_p, ptr(ovf), stream())
+    if _tiled(plan):
+        # one wavefront per domain (128 generator columns), then the 4-wave
+        # pass (512 columns) over the domains that did not fit
+        args = (B, ptr(xl), ptr(xh), lo_p, hi_p, ptr(ovf), stream())
+        call('vc_mlp_tiled_zono_bounds', plan.dims_p, plan.n, ptr(plan.tfrag),
+             ptr(plan.bias_cat), *args)
+        call('vc_mlp_zono_wide', plan.dims_p, plan.n, ptr(plan.frag[1]),
+             ptr(plan.bias_cat), *args)
+    else:
+        call('vc_mlp_zono_bounds', plan.dims_p, plan.n, ptr(plan.frag[1]),
+             ptr(plan.bias_cat), B, ptr(xl), ptr(xh), lo_p, hi_p, ptr(ovf), stream())
     del lo_a, hi_a
     from .verify_graph import _compact, _gather
     bad = _compact(ovf.to(torch.uint8))

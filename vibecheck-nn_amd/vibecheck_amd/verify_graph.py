@@ -184,13 +184,14 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
     if timers is not None:
         t0 = sync_t()
     A = acc = None
+    sb = None
     if crown_intermediate:
         out = _bound_crown_spec(gg, xl, xh, spec_ew, dev, dt,
-                                return_input_linear=clip_enabled)
+                                return_input_linear=clip_enabled, return_zono_sb=True)
         if clip_enabled:
-            _, lb, A, acc = out
+            _, lb, A, acc, sb = out
         else:
-            _, lb = out
+            _, lb, sb = out
     else:
         sb = _zono_sb(gg, xl, xh, dev, dt)
         if clip_enabled:
@@ -212,10 +213,14 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
                 raise NotImplementedError(
                     'vibecheck_amd: boundary-band alpha selection '
                     '(alpha_all=False) is not supported')
+            # alpha starts from the zonotope bounds of the same boxes, which
+            # the bound phase has already computed: gather their rows
+            sb_open = None if sb is None else {
+                L: (_gather(lo, open_idx), _gather(hi, open_idx)) for L, (lo, hi) in sb.items()}
             new, n_ait = _run_alpha_crown_inputsplit_batched(
                 _gather(xl, open_idx), _gather(xh, open_idx), gg, spec_ew,
                 dev, dt, n_iters=alpha_iters, lr=alpha_lr,
-                lr_decay=alpha_lr_decay, return_trace=True)
+                lr_decay=alpha_lr_decay, sb=sb_open, return_trace=True)
             n_al = int(open_idx.numel())
             call('vc_scatter_max_rows', ptr(lb), ptr(open_idx),
                  ptr(new.contiguous()), n_al, lb.shape[1], stream())

@@ -689,23 +689,25 @@ def _run_alpha_crown_inputsplit_batched(xl, xh, gg, spec_ew, device, dtype,
 
 
 def _bound_crown_spec(gg, xl, xh, spec_ew, device, dtype,
-                      return_input_linear=False):
+                      return_input_linear=False, return_zono_sb=False):
     """CROWN intermediate bounds followed by the spec bound -- the 'bound'
     phase of an input-split BaB iteration (verify_graph.py:12855-12871).
     For narrow fc/ReLU chains both run in one whole-network kernel launch.
-    Returns (tight, lb) or (tight, lb, A, acc)."""
+    Returns (tight, lb) or (tight, lb, A, acc); ``return_zono_sb``
+    (extension) appends the zonotope bounds the CROWN pass started from,
+    which the alpha-CROWN of the same boxes starts from as well."""
     _check_dtype(dtype)
     xl, xh = f32(xl), f32(xh)
     plan = _plan(gg, xl.device)
+    sb = _zono_sb(gg, xl, xh, device, dtype)
     if plan is not None and len(spec_ew) <= 32:
-        sb = _zono_sb(gg, xl, xh, device, dtype)
         Wq, bq = _spec_rows(spec_ew, xl.device)
         tight, lb, A, acc = mlp_fused.crown(plan, xl, xh, sb, True, spec=(Wq, bq),
                                             want_linear=return_input_linear)
-        return (tight, lb, A, acc) if return_input_linear else (tight, lb)
-    tight = _crown_intermediate_batched(gg, xl, xh, device, dtype)
-    out = _spec_backward_graph_batched(tight, xl, xh, gg, spec_ew, device, dtype,
-                                       return_input_linear=return_input_linear)
-    if return_input_linear:
-        return (tight,) + tuple(out)
-    return tight, out
+        out = (tight, lb, A, acc) if return_input_linear else (tight, lb)
+    else:
+        tight = _crown_intermediate_batched(gg, xl, xh, device, dtype, sb=sb)
+        res = _spec_backward_graph_batched(tight, xl, xh, gg, spec_ew, device, dtype,
+                                           return_input_linear=return_input_linear)
+        out = (tight,) + tuple(res) if return_input_linear else (tight, res)
+    return out + (sb,) if return_zono_sb else out
