@@ -317,6 +317,18 @@ int vc_mlp_tiled_zono_bounds(const int32_t *dims, int n_relu, const float *frag,
                              float *const *hi_out, int32_t *overflow,
                              vc_stream_t stream);
 
+/* vc_mlp_zono_wide with the tile shape fixed at compile time (frag from
+ * vc_mlp_tiled_pack): the domains with overflow[b] != 0, one 4-wave
+ * workgroup each, up to 512 generator columns dealt round-robin over the
+ * waves; overflow[b] rewritten (1 = still does not fit).
+ * Replaces the ReLU bounds of _forward_zonotope_graph_batched
+ * (verify_zono_bnb.py:3079-3211) for those domains. */
+int vc_mlp_tiled_zono_wide(const int32_t *dims, int n_relu, const float *frag,
+                           const float *bias_cat, int64_t B, const float *xl,
+                           const float *xh, float *const *lo_out,
+                           float *const *hi_out, int32_t *overflow,
+                           vc_stream_t stream);
+
 /* CROWN intermediate bounds and the spec backward, whole network per
  * wavefront.  With do_crown != 0, layer L is tightened by seeding
  * [+I; -I] at its pre-activation for the idx_cnt[L] neurons listed in

@@ -99,3 +99,37 @@ __device__ __forceinline__ float adam_update(float p, float g, float& m, float& 
   const float denom = __fdiv_rn(__fsqrt_rn(v), c.bc2) + c.eps;
   return p + __fdiv_rn(c.neg_step * m, denom);
 }
+
+// ---- reductions within a row of 16 lanes (lanes 16 g .. 16 g + 15) by DPP
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror:
+// each step adds the value of a partner lane of the same row, so after the
+// four steps every lane holds its row's total, bit-identical across the row.
+__device__ __forceinline__ int dpp_row_xchg(int v, int step) {
+  switch (step) {
+    case 0: return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);
+    case 1: return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);
+    case 2: return __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true);
+    default: return __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true);
+  }
+}
+
+__device__ __forceinline__ float row_sum16(float v) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) v += __int_as_float(dpp_row_xchg(__float_as_int(v), s));
+  return v;
+}
+
+__device__ __forceinline__ double row_sum16(double v) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const long long b = __double_as_longlong(v);
+    const int lo = dpp_row_xchg((int)(b & 0xffffffffll), s);
+    const int hi = dpp_row_xchg((int)(b >> 32), s);
+    v += __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+  }
+  return v;
+}
+
+// The value of lane 16 g (row position 0) in every lane of row g (exact:
+// the other lanes contribute zeros).
+__device__ __forceinline__ float row_bcast0(float v, int r) { return row_sum16(r == 0 ? v : 0.f); }

@@ -17,21 +17,21 @@ __host__ __device__ inline int ks_count(int dk) {
   return 4 * (T - 1) + (last < 4 ? last : 4);
 }
 
-// Copy n4 float4s (16-byte aligned) from global memory into LDS, four loads
-// in flight per thread, then barrier.
+// Copy n4 float4s (16-byte aligned) from global memory into LDS, eight
+// loads in flight per thread (no barrier: the caller synchronises).
 __device__ __forceinline__ void stage_float4(float* dst_lds, const float* src, int n4) {
   const float4* s = reinterpret_cast<const float4*>(src);
   float4* d = reinterpret_cast<float4*>(dst_lds);
+  const int bs = blockDim.x;
   int e = threadIdx.x;
-  for (; e + 3 * (int)blockDim.x < n4; e += 4 * blockDim.x) {
-    const float4 a = s[e], b = s[e + blockDim.x], c = s[e + 2 * blockDim.x],
-                 f = s[e + 3 * blockDim.x];
-    d[e] = a;
-    d[e + blockDim.x] = b;
-    d[e + 2 * blockDim.x] = c;
-    d[e + 3 * blockDim.x] = f;
+  for (; e + 7 * bs < n4; e += 8 * bs) {
+    float4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = s[e + k * bs];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) d[e + k * bs] = v[k];
   }
-  for (; e < n4; e += blockDim.x) d[e] = s[e];
+  for (; e < n4; e += bs) d[e] = s[e];
 }
 
 // Compute units of the current device (read once per device).

@@ -34,6 +34,14 @@ using vcm::MAXL;
 constexpr int TNW = 12;  // waves per workgroup, one domain each (3 per SIMD)
 constexpr int TNP = 2;   // 16-row N-tiles chained together per wave
 
+// LDS slot of lane L's fragment value at K-step ks.  The backward reads
+// (lane L, slot L) and the forward reads (lane (g, r) of M-tile mo reads
+// slot 16 (r / 4) + 4 g + i of K-step 4 mo + r % 4) both touch 16 distinct
+// bank groups per quarter-wave with this XOR swizzle (an involution).
+__host__ __device__ __forceinline__ int swz(int L, int ks) {
+  return L ^ (((L >> 4) << 2) | (ks & 3));
+}
+
 // Kernel instantiations: hidden M-tiles, K-steps, bias row in the A operand.
 struct TVariant {
   int MT, KS, brow;
@@ -90,22 +98,24 @@ int tiled_geom(const int32_t* dims, int n_relu, TGeom& G) {
 
 // fc_l's backward A operand: A[m][k] = W[k][m] (W: d_out x d_in, m < d_in,
 // k < d_out), A[d_in][k] = bias[k] when brow; zero elsewhere.
-//   hidden (layout 1): [ks][lane][mt] float4, mt < 4
-//   fc_0   (layout 0): [mt][ks][lane]
+//   hidden (layout 1): [ks][slot][mt] float4, mt < 4
+//   fc_0   (layout 0): [mt][ks][slot]
+// with lane L's value of K-step ks at slot swz(L, ks).
 __global__ void k_tpack(const float* W, const float* bias, int d_out, int d_in, int KS, int MTt,
                         int layout, int brow, float* frag) {
   const int total = MTt * KS * 64;
   for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
-    int mt, ks, lane;
+    int mt, ks, slot;
     if (layout == 1) {
       mt = e & 3;
-      lane = (e >> 2) & 63;
+      slot = (e >> 2) & 63;
       ks = e >> 8;
     } else {
-      lane = e & 63;
+      slot = e & 63;
       ks = (e >> 6) % KS;
       mt = (e >> 6) / KS;
     }
+    const int lane = swz(slot, ks);
     const int t = ks >> 2, i = ks & 3, g = lane >> 4, r = lane & 15;
     const int m = 16 * mt + r, k = 16 * t + 4 * g + i;
     float v = 0.f;
@@ -174,7 +184,7 @@ __device__ __forceinline__ void fc_hidden(const float4* fr, int lane, int g, int
     for (int mt = 0; mt < MT; ++mt) o[p][mt] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    const float4 a4 = fr[ks * 64 + lane];
+    const float4 a4 = fr[ks * 64 + swz(lane, ks)];
     const float a[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -215,7 +225,7 @@ __device__ __forceinline__ void fc0_concretize(const float* fr0, int mt0, int d0
     for (int p = 0; p < NP; ++p) o[p] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const float a = fr0[(mt * KS + ks) * 64 + lane];
+      const float a = fr0[(mt * KS + ks) * 64 + swz(lane, ks)];
 #pragma unroll
       for (int p = 0; p < NP; ++p) o[p] = mfma16x16x4(a, F[p][ks >> 2][ks & 3], o[p]);
     }
@@ -298,10 +308,10 @@ __device__ __forceinline__ void seeded_group(const TGeom& G, int L, int nt0, int
     acc[p] = (live && g == 0) ? (double)(sg * sbias[L * FW + j]) : 0.0;
     cz[p] = 0.0;
     if (L > 0) {
-      const float4* fl = frh + (L - 1) * KS * 64 + ksj * 64 + 16 * gj + 4 * g;
+      const float4* fl = frh + (L - 1) * KS * 64 + ksj * 64;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float4 w = live ? fl[i] : float4{0.f, 0.f, 0.f, 0.f};
+        const float4 w = live ? fl[swz(16 * gj + 4 * g + i, ksj)] : float4{0.f, 0.f, 0.f, 0.f};
         F[p][0][i] = sg * w.x;
         F[p][1][i] = sg * w.y;
         F[p][2][i] = sg * w.z;
@@ -314,7 +324,7 @@ __device__ __forceinline__ void seeded_group(const TGeom& G, int L, int nt0, int
         for (int i = 0; i < 4; ++i) {
           const int mi = 16 * mt + 4 * g + i;
           if (mi < d0) {
-            const float v = sg * fr0[(mt * KS + ksj) * 64 + 16 * gj + 4 * g + i];
+            const float v = sg * fr0[(mt * KS + ksj) * 64 + swz(16 * gj + 4 * g + i, ksj)];
             cz[p] += (double)(fmaxf(v, 0.f) * dxl[mi]);
             cz[p] += (double)(fminf(v, 0.f) * dxh[mi]);
           }
@@ -400,13 +410,17 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
   for (int64_t dom = (int64_t)blockIdx.x * TNW + wv; dom < B; dom += (int64_t)gridDim.x * TNW) {
     const float* dxl = xl + dom * d0;
     const float* dxh = xh + dom * d0;
+    // layer bounds are loaded one layer ahead (lane j holds neuron j)
+    float nlo = lane < G.d[1] ? ca.lo_in[0][dom * G.d[1] + lane] : 0.f;
+    float nhi = lane < G.d[1] ? ca.hi_in[0][dom * G.d[1] + lane] : 0.f;
     for (int L = 0; L < n; ++L) {
       const int dW = G.d[L + 1];
-      const float* lo_in = ca.lo_in[L] + dom * dW;
-      const float* hi_in = ca.hi_in[L] + dom * dW;
-      for (int j = lane; j < FW; j += 64) {
-        stl[j] = j < dW ? lo_in[j] : 0.f;
-        stl[FW + j] = j < dW ? hi_in[j] : 0.f;
+      stl[lane] = nlo;
+      stl[FW + lane] = nhi;
+      if (L + 1 < n) {
+        const int dn = G.d[L + 2];
+        nlo = lane < dn ? ca.lo_in[L + 1][dom * dn + lane] : 0.f;
+        nhi = lane < dn ? ca.hi_in[L + 1][dom * dn + lane] : 0.f;
       }
       __threadfence_block();
       const int m = do_crown ? ca.idx_cnt[L] : 0;
@@ -506,7 +520,7 @@ __device__ __forceinline__ void fc_forward(const float4* fr, int lane, int g, in
 #pragma unroll
     for (int mo = 0; mo < MT; ++mo) {
       const int ksf = 4 * mo + (r & 3);
-      const float4 q = ksf < KS ? fr[ksf * 64 + 16 * (r >> 2) + 4 * g + i]
+      const float4 q = ksf < KS ? fr[ksf * 64 + swz(16 * (r >> 2) + 4 * g + i, ksf)]
                                 : float4{0.f, 0.f, 0.f, 0.f};
       a[mo][0] = q.x;
       a[mo][1] = q.y;
@@ -553,6 +567,7 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
   for (int64_t dom = (int64_t)blockIdx.x * ANW + wv; dom < B; dom += (int64_t)gridDim.x * ANW) {
     const float* dxl = xl + dom * d0;
     const float* dxh = xh + dom * d0;
+#pragma unroll 4
     for (int l = 0; l < n; ++l) {
       const int dW = G.d[l + 1];
       float* sl = ssl + l * 4 * FW;
@@ -608,7 +623,8 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
     for (int mt = 0; mt < G.mt0; ++mt) {
       v4f o = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) o = mfma16x16x4(fr0[(mt * KS + ks) * 64 + lane], F[0][ks >> 2][ks & 3], o);
+      for (int ks = 0; ks < KS; ++ks)
+        o = mfma16x16x4(fr0[(mt * KS + ks) * 64 + swz(lane, ks)], F[0][ks >> 2][ks & 3], o);
       float gA[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -634,7 +650,7 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
 #pragma unroll
         for (int mo = 0; mo < MT; ++mo) {
           const int ksf = 4 * mo + (r & 3);
-          const float a = ksf < KS ? fr0[(mt * KS + ksf) * 64 + 16 * (r >> 2) + 4 * g + i] : 0.f;
+          const float a = ksf < KS ? fr0[(mt * KS + ksf) * 64 + swz(16 * (r >> 2) + 4 * g + i, ksf)] : 0.f;
           GE[mo] = mfma16x16x4(a, gA[i], GE[mo]);
         }
     }
@@ -661,11 +677,7 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
         const int j = 16 * t + 4 * g + i;
         const float pv = live ? pl[(ks * 4 + g) * Q + r] : 0.f;
         const float ge = GE[t][i];
-        float s = ge * fmaxf(pv, 0.f);
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        s += __shfl_xor(s, 4, 64);
-        s += __shfl_xor(s, 8, 64);
+        const float s = row_sum16(ge * fmaxf(pv, 0.f));
         if (r == 0) sga[j] = s;
         const bool mp = pv >= 0.f, mn = pv <= 0.f;
         float gp = ge * ((mp ? sl[j] : 0.f) + (mn ? sl[FW + j] : 0.f));
@@ -796,7 +808,7 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
             for (int mo = 0; mo < MT; ++mo) {
               const int ksf = 4 * mo + (r & 3);
               const float a =
-                  ksf < KS ? fr0[(mt * KS + ksf) * 64 + 16 * (r >> 2) + 4 * g + i] : 0.f;
+                  ksf < KS ? fr0[(mt * KS + ksf) * 64 + swz(16 * (r >> 2) + 4 * g + i, ksf)] : 0.f;
 #pragma unroll
               for (int p = 0; p < 2; ++p) o[p][mo] = mfma16x16x4(a, in[p][i], o[p][mo]);
             }
@@ -852,12 +864,9 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
 #pragma unroll
           for (int nt = 0; nt < ZT; ++nt)
             if (nt > 0 || r > 0) sd += (double)fabsf(Z[nt][t][i]);
-          sd += __shfl_xor(sd, 1, 64);
-          sd += __shfl_xor(sd, 2, 64);
-          sd += __shfl_xor(sd, 4, 64);
-          sd += __shfl_xor(sd, 8, 64);
+          sd = row_sum16(sd);
           const float rad = (float)sd;
-          const float c = __shfl(Z[0][t][i], lane & 48, 64);
+          const float c = row_bcast0(Z[0][t][i], r);
           const int j = 16 * t + 4 * g + i;
           const float lo = c - rad, hi = c + rad;
           const bool valid = j < dM;
@@ -912,6 +921,227 @@ template <int V>
 const void* zono_fn() {
   return reinterpret_cast<const void*>(
       &k_zono_tiled<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
+}
+
+// Second zonotope pass over the domains flagged by the first: one
+// workgroup of ZWW waves per domain and up to ZWW * ZWT * 16 generator
+// columns.  Column tile T lives in wave T % ZWW as its local tile T / ZWW
+// (round robin, so the used tiles spread over the waves); the per-neuron
+// |G| sums are reduced across waves through LDS in a fixed order, so every
+// wave derives the same bounds, lambda, mu and unstable set.
+constexpr int ZWW = 4;  // waves per domain
+constexpr int ZWT = 8;  // column tiles per wave: 512 columns
+
+template <int MT, int KS, bool BROW>
+__global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
+    TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
+    const float* __restrict__ xl, const float* __restrict__ xh, TZonoArgs out,
+    int32_t* overflow) {
+  extern __shared__ float smem[];
+  float* sfrag = smem;
+  float* sbias = smem + G.nfloats;                                // [n][FW]
+  double* sred = reinterpret_cast<double*>(sbias + G.n * FW);     // [ZWW][FW]
+  float* scen = reinterpret_cast<float*>(sred + ZWW * FW);        // centre column [FW]
+  __shared__ int s_list[ZWW * 64];
+  __shared__ int s_wcnt[ZWW];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int n = G.n, d0 = G.d[0];
+  const int cap = ZWW * ZWT * 16;
+  vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
+  for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
+    const int l = k / FW, j = k % FW;
+    sbias[k] = j < G.d[l + 1] ? gbias[G.boff[l] + j] : 0.f;
+  }
+  __syncthreads();
+  const float* fr0 = sfrag;
+  const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
+
+  // each workgroup scans a contiguous range of the flags, ZWW * 64 at a time
+  const int64_t per = (B + gridDim.x - 1) / gridDim.x;
+  const int64_t beg = (int64_t)blockIdx.x * per;
+  const int64_t end = beg + per < B ? beg + per : B;
+  for (int64_t c0 = beg; c0 < end; c0 += ZWW * 64) {
+    const int64_t dsc = c0 + threadIdx.x;
+    const bool flagged = dsc < end && overflow[dsc] != 0;
+    const uint64_t bal = __ballot(flagged);
+    if (lane == 0) s_wcnt[wv] = __popcll(bal);
+    __syncthreads();
+    int off = 0, tot = 0;
+    for (int w2 = 0; w2 < ZWW; ++w2) {
+      if (w2 < wv) off += s_wcnt[w2];
+      tot += s_wcnt[w2];
+    }
+    if (flagged) s_list[off + __popcll(bal & ((1ull << lane) - 1ull))] = (int)(dsc - c0);
+    __syncthreads();
+    for (int kd = 0; kd < tot; ++kd) {
+      const int64_t dom = c0 + s_list[kd];
+      const float* dxl = xl + dom * d0;
+      const float* dxh = xh + dom * d0;
+      v4f Z[ZWT][4];
+      int Kc = 1 + d0;
+      bool ovf = Kc > cap;
+      // ---- fc_0 on the input block
+#pragma unroll
+      for (int q0 = 0; q0 < ZWT; q0 += 2) {
+        v4f o[2][4];
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) o[p][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+        if (!ovf && 16 * (ZWW * q0 + wv) < Kc) {
+          for (int mt = 0; mt < G.mt0; ++mt) {
+            float in[2][4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int k = 16 * mt + 4 * g + i;
+              float c = 0.f, rd = 0.f;
+              if (k < d0) {
+                const float lv = dxl[k], hv = dxh[k];
+                c = (lv + hv) / 2.f;
+                rd = (hv - lv) / 2.f;
+              } else if (BROW && k == d0) {
+                c = 1.f;
+              }
+#pragma unroll
+              for (int p = 0; p < 2; ++p) {
+                const int col = 16 * (ZWW * (q0 + p) + wv) + r;
+                in[p][i] = col == 0 ? c : (col == 1 + k && k < d0 ? rd : 0.f);
+              }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int mo = 0; mo < MT; ++mo) {
+                const int ksf = 4 * mo + (r & 3);
+                const float a =
+                    ksf < KS ? fr0[(mt * KS + ksf) * 64 + swz(16 * (r >> 2) + 4 * g + i, ksf)] : 0.f;
+#pragma unroll
+                for (int p = 0; p < 2; ++p) o[p][mo] = mfma16x16x4(a, in[p][i], o[p][mo]);
+              }
+          }
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          Z[q0][mt] = o[0][mt];
+          Z[q0 + 1][mt] = o[1][mt];
+        }
+      }
+      const bool centre = wv == 0 && r == 0;  // lanes holding column 0
+      if (!BROW && centre) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Z[0][t][i] = Z[0][t][i] + sbias[16 * t + 4 * g + i];
+      }
+      for (int l = 0; l < n && !ovf; ++l) {
+        if (l > 0) {
+          if (BROW && centre) set_elem<MT>(Z[0], G.d[l], g, 1.f);
+          const float4* fr = frh + (l - 1) * KS * 64;
+#pragma unroll
+          for (int q0 = 0; q0 < ZWT; q0 += 2) {
+            if (16 * (ZWW * q0 + wv) < Kc) {
+              v4f o[2][4];
+              fc_forward<MT, KS, 2, ZWT>(fr, lane, g, r, Z, q0, o);
+#pragma unroll
+              for (int mt = 0; mt < 4; ++mt) {
+                Z[q0][mt] = o[0][mt];
+                Z[q0 + 1][mt] = o[1][mt];
+              }
+            }
+          }
+          if (!BROW && centre) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                Z[0][t][i] = Z[0][t][i] + sbias[l * FW + 16 * t + 4 * g + i];
+          }
+        }
+        // relu_l: partial |G| sums per wave, reduced in a fixed order
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            double sd = 0.0;
+#pragma unroll
+            for (int q = 0; q < ZWT; ++q)
+              if (q > 0 || !centre) sd += (double)fabsf(Z[q][t][i]);
+            sd = row_sum16(sd);
+            const int j = 16 * t + 4 * g + i;
+            if (r == 0) sred[wv * FW + j] = sd;
+            if (centre) scen[j] = Z[0][t][i];
+          }
+        __syncthreads();
+        const int dM = G.d[l + 1];
+        const bool last = l == n - 1;
+        float mu[MT][4];
+        uint64_t umask = 0;
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = 16 * t + 4 * g + i;
+            double sd = sred[j];
+#pragma unroll
+            for (int w2 = 1; w2 < ZWW; ++w2) sd += sred[w2 * FW + j];
+            const float rad = (float)sd;
+            const float c = scen[j];
+            const float lo = c - rad, hi = c + rad;
+            const bool valid = j < dM;
+            const bool ust = valid && lo < 0.f && hi > 0.f;
+            const bool dead = hi <= 0.f;
+            if (valid && centre) {
+              out.lo[l][dom * dM + j] = lo;
+              out.hi[l][dom * dM + j] = hi;
+            }
+            const float lam = ust ? hi / (hi - lo) : (dead ? 0.f : 1.f);
+            mu[t][i] = ust ? (-hi * lo) / (2.f * (hi - lo)) : 0.f;
+            if (!last) {
+#pragma unroll
+              for (int q = 0; q < ZWT; ++q)
+                Z[q][t][i] = (q == 0 && centre) ? lam * Z[q][t][i] + mu[t][i] : Z[q][t][i] * lam;
+            }
+            const uint64_t bal2 = __ballot(ust && r == 0);
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg)
+              if ((bal2 >> (16 * gg)) & 1ull) umask |= 1ull << (16 * t + 4 * gg + i);
+          }
+        __syncthreads();  // sred / scen are rewritten by the next layer
+        const int cnt = __popcll(umask);
+        if (last) break;
+        if (Kc + cnt > cap) {
+          ovf = true;
+          break;
+        }
+        // append one column per unstable neuron at position Kc + rank
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = 16 * t + 4 * g + i;
+            if ((umask >> j) & 1ull) {
+              const int col = Kc + __popcll(umask & ((1ull << j) - 1ull));
+              const int T = col >> 4;
+              if ((col & 15) == r && T % ZWW == wv) {
+#pragma unroll
+                for (int q = 0; q < ZWT; ++q)
+                  if (q == T / ZWW) Z[q][t][i] = mu[t][i];
+              }
+            }
+          }
+        Kc += cnt;
+      }
+      if (threadIdx.x == 0) overflow[dom] = ovf ? 1 : 0;
+    }
+    __syncthreads();  // s_list / s_wcnt are rewritten by the next chunk
+  }
+}
+
+template <int V>
+const void* zono_wide_fn() {
+  return reinterpret_cast<const void*>(
+      &k_zono_wide_tiled<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
 }
 
 template <int V>
@@ -1139,6 +1369,62 @@ extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const f
     default: return VC_ERR_UNSUPPORTED;
   }
 #undef VC_TZONO_CASE
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const float* frag,
+                                      const float* bias_cat, int64_t B, const float* xl,
+                                      const float* xh, float* const* lo_out,
+                                      float* const* hi_out, int32_t* overflow,
+                                      vc_stream_t stream) {
+  TGeom G;
+  int rc = tiled_geom(dims, n_relu, G);
+  if (rc != VC_OK) return rc;
+  if (!frag || !bias_cat || !xl || !xh || !lo_out || !hi_out || !overflow || B < 0)
+    return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  TZonoArgs za;
+  for (int l = 0; l < MAXL; ++l) {
+    za.lo[l] = l < n_relu ? lo_out[l] : nullptr;
+    za.hi[l] = l < n_relu ? hi_out[l] : nullptr;
+    if (l < n_relu && (!za.lo[l] || !za.hi[l])) return VC_ERR_ARG;
+  }
+  const size_t lds = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float) +
+                     (size_t)ZWW * FW * sizeof(double) + (size_t)FW * sizeof(float);
+  if (lds > 160 * 1024 - 2048) return VC_ERR_UNSUPPORTED;
+  const void* fn = nullptr;
+  switch (G.variant) {
+    case 0: fn = zono_wide_fn<0>(); break;
+    case 1: fn = zono_wide_fn<1>(); break;
+    case 2: fn = zono_wide_fn<2>(); break;
+    case 3: fn = zono_wide_fn<3>(); break;
+    case 4: fn = zono_wide_fn<4>(); break;
+    case 5: fn = zono_wide_fn<5>(); break;
+    default: return VC_ERR_UNSUPPORTED;
+  }
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return VC_ERR_UNSUPPORTED;
+  int64_t gw = vcm::cu_count();
+  if (gw > B) gw = B;
+  hipStream_t st = (hipStream_t)stream;
+#define VC_TWIDE_CASE(V)                                                                     \
+  case V:                                                                                    \
+    hipLaunchKernelGGL((k_zono_wide_tiled<kVariants[V].MT, kVariants[V].KS,                  \
+                                          kVariants[V].brow != 0>),                          \
+                       dim3((unsigned)gw), dim3(ZWW * 64), lds, st, G, frag, bias_cat, B, xl, \
+                       xh, za, overflow);                                                    \
+    break;
+  switch (G.variant) {
+    VC_TWIDE_CASE(0)
+    VC_TWIDE_CASE(1)
+    VC_TWIDE_CASE(2)
+    VC_TWIDE_CASE(3)
+    VC_TWIDE_CASE(4)
+    VC_TWIDE_CASE(5)
+    default: return VC_ERR_UNSUPPORTED;
+  }
+#undef VC_TWIDE_CASE
   VC_LAUNCH_CHECK();
   return VC_OK;
 }

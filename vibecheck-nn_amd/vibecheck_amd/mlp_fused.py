@@ -126,7 +126,7 @@ def zono_bounds(plan, xl, xh, fallback):
         args = (B, ptr(xl), ptr(xh), lo_p, hi_p, ptr(ovf), stream())
         call('vc_mlp_tiled_zono_bounds', plan.dims_p, plan.n, ptr(plan.tfrag),
              ptr(plan.bias_cat), *args)
-        call('vc_mlp_zono_wide', plan.dims_p, plan.n, ptr(plan.frag[1]),
+        call('vc_mlp_tiled_zono_wide', plan.dims_p, plan.n, ptr(plan.tfrag),
              ptr(plan.bias_cat), *args)
     else:
         call('vc_mlp_zono_bounds', plan.dims_p, plan.n, ptr(plan.frag[1]),
