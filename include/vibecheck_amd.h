@@ -261,6 +261,17 @@ int vc_split_clamps(const int64_t *layer, const int64_t *neuron,
 int vc_best_update(float *best, const float *lb, int64_t n, int init,
                    float *out2, vc_stream_t stream);
 
+/* The bookkeeping of alpha-CROWN iteration `it` (0-based) without a host
+ * round trip: best = lb (it == 0) or max(best, lb), then the loop control
+ * of the reference -- stop when every best bound is > 0, or (it > 0) when
+ * the global max of best rose by less than eps since the previous
+ * iteration.  ctl (4 floats, start {-inf, 0, 0, 0}) = {previous max,
+ * stopped, evaluated iterations, this max}; once stopped, later calls do
+ * nothing, and vc_mlp_tiled_alpha_iter given ctl skips its work.
+ * Replaces verify_zono_bnb.py:5252-5287 (best, the two breaks, prev_max). */
+int vc_alpha_control(float *best, const float *lb, int64_t n, int it,
+                     double eps, float *ctl, vc_stream_t stream);
+
 /* ---- Whole-network kernels for narrow fc/ReLU chains ------------------- */
 /* dims (host array, n_relu + 1 entries): dims[0] = inputs, dims[l + 1] =
  * width of ReLU layer l (the output of fc_l); every width <= 64,
@@ -365,10 +376,12 @@ int vc_mlp_tiled_pack(const float *const *W, const float *const *bias,
                       const int32_t *dims, int n_relu, float *frag,
                       vc_stream_t stream);
 
-/* vc_mlp_crown with the tile shape fixed at compile time (same arguments
- * and results; frag from vc_mlp_tiled_pack, Q <= 64): no MFMA under a
- * runtime condition, the fc bias carried by the MFMA, the per-row constants
- * accumulated in fp64.
+/* vc_mlp_crown with the tile shape fixed at compile time (same results;
+ * frag from vc_mlp_tiled_pack, Q <= 64): no MFMA under a runtime condition,
+ * the fc bias carried by the MFMA, the per-row constants accumulated in
+ * fp64.  The seeded neuron lists stay on the device: idx_meta (device,
+ * 2 * n_relu int32) holds the per-layer counts, then their offsets into
+ * idx_all, as written by vc_union_compact.
  * Replaces _crown_intermediate_batched (verify_zono_bnb.py:4077-4147) and
  * _spec_backward_graph_batched with return_input_linear
  * (verify_zono_bnb.py:4270-4453, 5117-5134). */
@@ -377,10 +390,25 @@ int vc_mlp_tiled_crown(const int32_t *dims, int n_relu, const float *frag,
                        const float *xh, const float *const *lo_in,
                        const float *const *hi_in, float *const *lo_out,
                        float *const *hi_out, const int32_t *idx_all,
-                       const int32_t *idx_cnt, int do_crown, int Q,
+                       const int32_t *idx_meta, int do_crown, int Q,
                        const float *spec_rows, const float *spec_acc,
                        float *lb_out, float *A_out, float *acc_out,
                        vc_stream_t stream);
+
+/* The neurons unstable in any domain, per layer, for the CROWN seeding of
+ * _crown_intermediate_batched (verify_zono_bnb.py:4123): flags (sum of
+ * widths, uint8) = 1 where some domain has lo < 0 < hi, for n_layers
+ * layers lo[L]/hi[L] (B, widths[L]) in one launch (flags cleared first). */
+int vc_unstable_union_layers(const float *const *lo, const float *const *hi,
+                             const int32_t *widths, int n_layers, int64_t B,
+                             uint8_t *flags, vc_stream_t stream);
+
+/* Compact the flags of vc_unstable_union_layers (n_layers <= 16): idx
+ * (device, sum of widths int32) lists layer L's flagged neurons in
+ * increasing order from offset off[L]; meta (device, 2 n_layers int32) =
+ * {cnt[0..n_layers), off[0..n_layers)}.  Part of verify_zono_bnb.py:4123. */
+int vc_union_compact(const uint8_t *flags, const int32_t *widths, int n_layers,
+                     int32_t *idx, int32_t *meta, vc_stream_t stream);
 
 /* One batched alpha-CROWN Adam iteration, whole network per wavefront
  * (n_relu <= 7, 1 <= Q <= 16): evaluates lb_out (B, Q) with lower slopes
@@ -403,7 +431,10 @@ int vc_mlp_alpha_iter(const int32_t *dims, int n_relu, const float *frag_bwd,
 /* vc_mlp_alpha_iter with the tile shape fixed at compile time (same
  * arguments and results; frag from vc_mlp_tiled_pack; n_relu <= 16 as the
  * LDS allows, 1 <= Q <= 16): the pre-relaxation rows kept in LDS, the fc
- * biases carried by the MFMA in both directions.
+ * biases carried by the MFMA in both directions.  init != 0 (the first
+ * iteration): alpha starts at (up_s > 0.5) * unstable and the Adam state at
+ * zero, whatever the arrays hold.  ctl (nullable): the loop state of
+ * vc_alpha_control; the call does nothing once it says stopped.
  * Replaces one iteration of _run_alpha_crown_inputsplit_batched
  * (verify_zono_bnb.py:5248-5266). */
 int vc_mlp_tiled_alpha_iter(const int32_t *dims, int n_relu, const float *frag,
@@ -414,7 +445,8 @@ int vc_mlp_tiled_alpha_iter(const int32_t *dims, int n_relu, const float *frag,
                             int Q, const float *spec_rows,
                             const float *spec_acc, float *lb_out, double b1,
                             double b2, double eps, double step_size,
-                            double bc2_sqrt, vc_stream_t stream);
+                            double bc2_sqrt, int init, const float *ctl,
+                            vc_stream_t stream);
 
 /* ---- Input-split BaB step ---------------------------------------------- */
 
@@ -454,6 +486,12 @@ int vc_scatter_max_rows(float *rows, const int64_t *idx, const float *src,
 /* Row gather: out[r] = in[idx[r]] for rows of `cols` floats. */
 int vc_gather_rows(const float *in, const int64_t *idx, int64_t n_rows,
                    int cols, float *out, vc_stream_t stream);
+
+/* vc_gather_rows for n_arrays (<= 32) arrays in one launch: out[a] (n_rows,
+ * cols[a]) = in[a][idx] with the same row list. */
+int vc_gather_rows_multi(const float *const *in, float *const *out,
+                         const int32_t *cols, int n_arrays, const int64_t *idx,
+                         int64_t n_rows, vc_stream_t stream);
 
 /* Row scatter: out[idx[r]] = in[r] for rows of `cols` floats. */
 int vc_scatter_rows(const float *in, const int64_t *idx, int64_t n_rows,

@@ -152,6 +152,77 @@ __global__ void k_unstable_union(const float* lo, const float* hi, int64_t B, in
   }
 }
 
+// ---- per-layer batches in one launch (blockIdx.y = layer / array) -------
+constexpr int VC_MAXA = 32;
+
+struct LayerPtrs {
+  const float* lo[VC_MAXA];
+  const float* hi[VC_MAXA];
+  int width[VC_MAXA];
+  int off[VC_MAXA];
+};
+
+__global__ void k_unstable_union_layers(LayerPtrs lp, int64_t B, uint8_t* flag) {
+  const int L = blockIdx.y;
+  const int n = lp.width[L];
+  const int64_t total = B * (int64_t)n;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    if (lp.lo[L][i] < 0.f && lp.hi[L][i] > 0.f) flag[lp.off[L] + i % n] = 1;
+  }
+}
+
+// Compact the union flags of every layer: wave L lists the set flags of
+// layer L in increasing order at idx[off[L] ..], with meta = {cnt[0..n),
+// off[0..n)}; off is the exclusive prefix sum of the counts.
+__global__ void k_union_compact(const uint8_t* flag, LayerPtrs lp, int n_layers, int32_t* idx,
+                                int32_t* meta) {
+  __shared__ int scnt[VC_MAXA];
+  const int L = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const bool mine = L < n_layers;
+  const int w = mine ? lp.width[L] : 0;
+  const uint8_t* f = flag + (mine ? lp.off[L] : 0);
+  int cnt = 0;
+  for (int c0 = 0; c0 < w; c0 += 64) {
+    const bool set = c0 + lane < w && f[c0 + lane] != 0;
+    cnt += __popcll(__ballot(set));
+  }
+  if (mine && lane == 0) scnt[L] = cnt;
+  __syncthreads();
+  if (!mine) return;
+  int off = 0;
+  for (int k = 0; k < L; ++k) off += scnt[k];
+  int run = off;
+  for (int c0 = 0; c0 < w; c0 += 64) {
+    const bool set = c0 + lane < w && f[c0 + lane] != 0;
+    const uint64_t bal = __ballot(set);
+    if (set) idx[run + __popcll(bal & ((1ull << lane) - 1ull))] = c0 + lane;
+    run += __popcll(bal);
+  }
+  if (lane == 0) {
+    meta[L] = cnt;
+    meta[n_layers + L] = off;
+  }
+}
+
+struct GatherPtrs {
+  const float* in[VC_MAXA];
+  float* out[VC_MAXA];
+  int cols[VC_MAXA];
+};
+
+__global__ void k_gather_rows_multi(GatherPtrs gp, const int64_t* idx, int64_t nr) {
+  const int a = blockIdx.y;
+  const int cols = gp.cols[a];
+  const int64_t total = nr * (int64_t)cols;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / cols;
+    const int c = (int)(i % cols);
+    gp.out[a][i] = gp.in[a][idx[r] * cols + c];
+  }
+}
+
 __global__ void k_alpha_grad_reduce(const float* gE, const float* P, int p_bcast, int64_t B,
                                     int R, int n, const float* lo, const float* hi, float* ga,
                                     float* gb) {
@@ -241,6 +312,52 @@ __global__ void k_split_clamps(const int64_t* layer, const int64_t* neuron, cons
     cl[i] = lo;
     ch[i] = hi;
     if (sign) sign[i] = split_sign(lo, hi);
+  }
+}
+
+// One alpha-CROWN iteration's bookkeeping on the device, with the loop
+// control of verify_zono_bnb.py:5252-5287: ctl = {previous global max of the
+// best bound, stopped flag, evaluated iterations, this iteration's max}.
+// Once stopped, later calls (and the fused alpha kernel) do nothing.
+__global__ void k_alpha_control(float* best, const float* lb, int64_t n, int it, double eps,
+                                float* ctl) {
+  __shared__ float smax[16];
+  __shared__ int sneg[16];
+  if (ctl[1] != 0.f) return;
+  float mx = -INFINITY;
+  int notpos = 0;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    const float x = lb[i];
+    const float b = it == 0 ? x : fmaxf(best[i], x);
+    best[i] = b;
+    mx = fmaxf(mx, b);
+    notpos |= !(b > 0.f);
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    notpos |= __shfl_xor(notpos, o, 64);
+  }
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) {
+    smax[w] = mx;
+    sneg[w] = notpos;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int nw = blockDim.x >> 6;
+    float a = smax[0];
+    int b = sneg[0];
+    for (int i = 1; i < nw; ++i) {
+      a = fmaxf(a, smax[i]);
+      b |= sneg[i];
+    }
+    const float prev = ctl[0];
+    bool stop = b == 0;  // every best bound > 0
+    if (!stop && it > 0 && (double)a - (double)prev < eps) stop = true;
+    ctl[0] = a;
+    ctl[1] = stop ? 1.f : 0.f;
+    ctl[2] = (float)(it + 1);
+    ctl[3] = a;
   }
 }
 
@@ -650,6 +767,70 @@ extern "C" int vc_unstable_union(const float* lo, const float* hi, int64_t B, in
   return VC_OK;
 }
 
+extern "C" int vc_unstable_union_layers(const float* const* lo, const float* const* hi,
+                                        const int32_t* widths, int n_layers, int64_t B,
+                                        uint8_t* flags, vc_stream_t stream) {
+  if (!lo || !hi || !widths || !flags || n_layers < 1 || n_layers > VC_MAXA || B < 0)
+    return VC_ERR_ARG;
+  LayerPtrs lp{};
+  int off = 0, wmax = 0;
+  for (int L = 0; L < n_layers; ++L) {
+    if (!lo[L] || !hi[L] || widths[L] <= 0) return VC_ERR_ARG;
+    lp.lo[L] = lo[L];
+    lp.hi[L] = hi[L];
+    lp.width[L] = widths[L];
+    lp.off[L] = off;
+    off += widths[L];
+    wmax = widths[L] > wmax ? widths[L] : wmax;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_fill_u8, dim3(vc_blocks(off, NT)), dim3(NT), 0, st, flags, (int64_t)off,
+                     (uint8_t)0);
+  if (B > 0)
+    hipLaunchKernelGGL(k_unstable_union_layers, dim3(vc_blocks(B * wmax, NT), n_layers),
+                       dim3(NT), 0, st, lp, B, flags);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_union_compact(const uint8_t* flags, const int32_t* widths, int n_layers,
+                                int32_t* idx, int32_t* meta, vc_stream_t stream) {
+  if (!flags || !widths || !idx || !meta || n_layers < 1 || n_layers > 16) return VC_ERR_ARG;
+  LayerPtrs lp{};
+  int off = 0;
+  for (int L = 0; L < n_layers; ++L) {
+    if (widths[L] <= 0) return VC_ERR_ARG;
+    lp.width[L] = widths[L];
+    lp.off[L] = off;
+    off += widths[L];
+  }
+  hipLaunchKernelGGL(k_union_compact, dim3(1), dim3(64 * n_layers), 0, (hipStream_t)stream,
+                     flags, lp, n_layers, idx, meta);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_gather_rows_multi(const float* const* in, float* const* out,
+                                    const int32_t* cols, int n_arrays, const int64_t* idx,
+                                    int64_t n_rows, vc_stream_t stream) {
+  if (!in || !out || !cols || !idx || n_arrays < 1 || n_arrays > VC_MAXA || n_rows < 0)
+    return VC_ERR_ARG;
+  if (n_rows == 0) return VC_OK;
+  GatherPtrs gp{};
+  int cmax = 0;
+  for (int a = 0; a < n_arrays; ++a) {
+    if (!in[a] || !out[a] || cols[a] <= 0) return VC_ERR_ARG;
+    gp.in[a] = in[a];
+    gp.out[a] = out[a];
+    gp.cols[a] = cols[a];
+    cmax = cols[a] > cmax ? cols[a] : cmax;
+  }
+  hipLaunchKernelGGL(k_gather_rows_multi, dim3(vc_blocks(n_rows * cmax, NT), n_arrays),
+                     dim3(NT), 0, (hipStream_t)stream, gp, idx, n_rows);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
 extern "C" int vc_alpha_grad_reduce(const float* gE, const float* P, int p_bcast, int64_t B,
                                     int R, int n, const float* relu_lo, const float* relu_hi,
                                     float* galpha, float* gbeta, vc_stream_t stream) {
@@ -718,6 +899,15 @@ extern "C" int vc_best_update(float* best, const float* lb, int64_t n, int init,
   if (!best || !lb || !out2 || n <= 0) return VC_ERR_ARG;
   hipLaunchKernelGGL(k_best_update, dim3(1), dim3(1024), 0, (hipStream_t)stream, best, lb, n,
                      init, out2);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_alpha_control(float* best, const float* lb, int64_t n, int it, double eps,
+                                float* ctl, vc_stream_t stream) {
+  if (!best || !lb || !ctl || n <= 0 || it < 0) return VC_ERR_ARG;
+  hipLaunchKernelGGL(k_alpha_control, dim3(1), dim3(1024), 0, (hipStream_t)stream, best, lb, n,
+                     it, eps, ctl);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }

@@ -134,8 +134,6 @@ struct TCrownArgs {
   const float* hi_in[MAXL];
   float* lo_out[MAXL];
   float* hi_out[MAXL];
-  int idx_off[MAXL];
-  int idx_cnt[MAXL];
 };
 
 __device__ __forceinline__ double group_sum4_d(double v) {
@@ -288,7 +286,7 @@ __device__ __forceinline__ void make_slopes_lds(float* sl, const float* lo, cons
 // fc_L .. fc_0 and the concretization; lb of each row to slb.
 template <int MT, int KS, int NP, bool BROW>
 __device__ __forceinline__ void seeded_group(const TGeom& G, int L, int nt0, int m,
-                                             const int32_t* idx, const float* fr0,
+                                             const int* idx, const float* fr0,
                                              const float4* frh, const float* ssl,
                                              const float* sbias, float* slb, int lane, int g,
                                              int r, const float* dxl, const float* dxh) {
@@ -386,8 +384,8 @@ template <int MT, int KS, bool BROW>
 __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
     TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
     const float* __restrict__ xl, const float* __restrict__ xh, TCrownArgs ca,
-    const int32_t* __restrict__ idx_all, int do_crown, int Q,
-    const float* __restrict__ spec_rows, const float* __restrict__ spec_acc,
+    const int32_t* __restrict__ idx_all, const int32_t* __restrict__ idx_meta, int do_crown,
+    int Q, const float* __restrict__ spec_rows, const float* __restrict__ spec_acc,
     float* __restrict__ lb_out, float* __restrict__ A_out, float* __restrict__ acc_out) {
   extern __shared__ float smem[];
   float* sfrag = smem;
@@ -395,21 +393,30 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int n = G.n, d0 = G.d[0];
-  float* ssl = sbias + n * FW + wv * (n * 3 * FW + 4 * FW);  // slopes [layer][3][FW]
-  float* slb = ssl + n * 3 * FW;                              // seeded-row bounds
-  float* stl = slb + 2 * FW;                                  // current layer lo / hi
+  // seeded neuron lists: counts idx_meta[L], offsets idx_meta[n + L]
+  int nmax = 0;
+  for (int l = 1; l <= n; ++l) nmax += G.d[l];
+  const int nidx = do_crown ? idx_meta[n + n - 1] + idx_meta[n - 1] : 0;
+  int* sidx = reinterpret_cast<int*>(sbias + n * FW);
+  float* ssl = sbias + n * FW + nmax + wv * (n * 3 * FW + 6 * FW);  // slopes [layer][3][FW]
+  float* slb = ssl + n * 3 * FW;                                    // seeded-row bounds
+  float* stl = slb + 2 * FW;                                        // current layer lo / hi
+  float* sx = stl + 2 * FW;                                         // the box: xl, xh [FW]
   vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
   for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
     const int l = k / FW, j = k % FW;
     sbias[k] = j < G.d[l + 1] ? gbias[G.boff[l] + j] : 0.f;
   }
+  for (int k = threadIdx.x; k < nidx && k < nmax; k += blockDim.x) sidx[k] = idx_all[k];
   __syncthreads();
   const float* fr0 = sfrag;
   const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
+  const float* dxl = sx;
+  const float* dxh = sx + FW;
 
   for (int64_t dom = (int64_t)blockIdx.x * TNW + wv; dom < B; dom += (int64_t)gridDim.x * TNW) {
-    const float* dxl = xl + dom * d0;
-    const float* dxh = xh + dom * d0;
+    sx[lane] = lane < d0 ? xl[dom * d0 + lane] : 0.f;
+    sx[FW + lane] = lane < d0 ? xh[dom * d0 + lane] : 0.f;
     // layer bounds are loaded one layer ahead (lane j holds neuron j)
     float nlo = lane < G.d[1] ? ca.lo_in[0][dom * G.d[1] + lane] : 0.f;
     float nhi = lane < G.d[1] ? ca.hi_in[0][dom * G.d[1] + lane] : 0.f;
@@ -423,8 +430,8 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
         nhi = lane < dn ? ca.hi_in[L + 1][dom * dn + lane] : 0.f;
       }
       __threadfence_block();
-      const int m = do_crown ? ca.idx_cnt[L] : 0;
-      const int32_t* idx = idx_all + (do_crown ? ca.idx_off[L] : 0);
+      const int m = do_crown ? min(idx_meta[L], dW) : 0;
+      const int* idx = sidx + (do_crown ? idx_meta[n + L] : 0);
       const int R = 2 * m;
       const int ntiles = (R + 15) / 16;
       for (int nt0 = 0; nt0 < ntiles; nt0 += TNP) {
@@ -542,18 +549,20 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
     TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
     const float* __restrict__ xl, const float* __restrict__ xh, TAlphaArgs aa, int Q,
     const float* __restrict__ spec_rows, const float* __restrict__ spec_acc,
-    float* __restrict__ lb_out, AdamConst adam) {
+    float* __restrict__ lb_out, AdamConst adam, int init, const float* __restrict__ ctl) {
+  if (ctl && ctl[1] != 0.f) return;  // the loop has stopped (vc_alpha_control)
   extern __shared__ float smem[];
   float* sfrag = smem;
   float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int n = G.n, d0 = G.d[0], dN = G.d[n];
-  const int wsz = n * 7 * FW + n * KS * 4 * Q + FW;
+  const int wsz = n * 7 * FW + n * KS * 4 * Q + 3 * FW;
   float* ssl = sbias + n * FW + wv * wsz;  // [l][ls_eff, us, ut, unstable][FW]
   float* sad = ssl + n * 4 * FW;           // [l][alpha, m, v][FW]
   float* sP = sad + n * 3 * FW;            // [l][ks][g][r < Q]
   float* sga = sP + n * KS * 4 * Q;        // d lb / d alpha of one layer [FW]
+  float* sx = sga + FW;                    // the box: xl, xh [FW]
   vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
   for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
     const int l = k / FW, j = k % FW;
@@ -564,9 +573,11 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
   const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
   const bool live = r < Q;
 
+  const float* dxl = sx;
+  const float* dxh = sx + FW;
   for (int64_t dom = (int64_t)blockIdx.x * ANW + wv; dom < B; dom += (int64_t)gridDim.x * ANW) {
-    const float* dxl = xl + dom * d0;
-    const float* dxh = xh + dom * d0;
+    sx[lane] = lane < d0 ? xl[dom * d0 + lane] : 0.f;
+    sx[FW + lane] = lane < d0 ? xh[dom * d0 + lane] : 0.f;
 #pragma unroll 4
     for (int l = 0; l < n; ++l) {
       const int dW = G.d[l + 1];
@@ -577,9 +588,14 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
         if (j < dW) {
           const int64_t ai = dom * dW + j;
           const Relax s = relax(aa.lo[l][ai], aa.hi[l][ai]);
-          a = aa.alpha[l][ai];
-          m1 = aa.m1[l][ai];
-          m2 = aa.m2[l][ai];
+          if (init) {
+            // first iteration: alpha = (up_s > 0.5) * unstable, Adam state zero
+            a = (s.unstable && s.up_s > 0.5f) ? 1.f : 0.f;
+          } else {
+            a = aa.alpha[l][ai];
+            m1 = aa.m1[l][ai];
+            m2 = aa.m2[l][ai];
+          }
           ls = s.active ? 1.f : (s.unstable ? a : 0.f);
           us = s.up_s;
           ut = s.up_t;
@@ -1190,34 +1206,31 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
                                   const float* xh, const float* const* lo_in,
                                   const float* const* hi_in, float* const* lo_out,
                                   float* const* hi_out, const int32_t* idx_all,
-                                  const int32_t* idx_cnt, int do_crown, int Q,
+                                  const int32_t* idx_meta, int do_crown, int Q,
                                   const float* spec_rows, const float* spec_acc, float* lb_out,
                                   float* A_out, float* acc_out, vc_stream_t stream) {
   TGeom G;
   int rc = tiled_geom(dims, n_relu, G);
   if (rc != VC_OK) return rc;
   if (!frag || !bias_cat || !xl || !xh || !lo_in || !hi_in || B < 0) return VC_ERR_ARG;
-  if (Q < 0 || Q > TNP * 16) return VC_ERR_UNSUPPORTED;
+  if (Q < 0 || Q > TNP * 16 * 2) return VC_ERR_UNSUPPORTED;
   if (Q > 0 && (!spec_rows || !spec_acc || !lb_out)) return VC_ERR_ARG;
-  if (do_crown && (!idx_all || !idx_cnt || !lo_out || !hi_out)) return VC_ERR_ARG;
+  if (do_crown && (!idx_all || !idx_meta || !lo_out || !hi_out)) return VC_ERR_ARG;
   if (B == 0) return VC_OK;
   TCrownArgs ca;
-  int off = 0;
+  int nmax = 0;
   for (int l = 0; l < MAXL; ++l) {
     const bool in = l < n_relu;
     ca.lo_in[l] = in ? lo_in[l] : nullptr;
     ca.hi_in[l] = in ? hi_in[l] : nullptr;
     ca.lo_out[l] = (in && lo_out) ? lo_out[l] : nullptr;
     ca.hi_out[l] = (in && hi_out) ? hi_out[l] : nullptr;
-    ca.idx_off[l] = off;
-    ca.idx_cnt[l] = (in && do_crown) ? idx_cnt[l] : 0;
     if (in && (!ca.lo_in[l] || !ca.hi_in[l])) return VC_ERR_ARG;
-    if (in && (ca.idx_cnt[l] < 0 || ca.idx_cnt[l] > G.d[l + 1])) return VC_ERR_ARG;
-    off += ca.idx_cnt[l];
+    if (in) nmax += G.d[l + 1];
   }
-  const size_t lds =
-      ((size_t)G.nfloats + (size_t)n_relu * FW + (size_t)TNW * (n_relu * 3 * FW + 4 * FW)) *
-      sizeof(float);
+  const size_t lds = ((size_t)G.nfloats + (size_t)n_relu * FW + (size_t)nmax +
+                      (size_t)TNW * (n_relu * 3 * FW + 6 * FW)) *
+                     sizeof(float);
   if (lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
   const void* fn = nullptr;
   switch (G.variant) {
@@ -1238,7 +1251,7 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
     hipLaunchKernelGGL((k_crown_tiled<kVariants[V].MT, kVariants[V].KS,                      \
                                       kVariants[V].brow != 0>),                              \
                        grid, block, lds, st, G, frag, bias_cat, B, xl, xh, ca, idx_all,      \
-                       do_crown, Q, spec_rows, spec_acc, lb_out, A_out, acc_out);            \
+                       idx_meta, do_crown, Q, spec_rows, spec_acc, lb_out, A_out, acc_out);  \
     break;
   switch (G.variant) {
     VC_TILED_CASE(0)
@@ -1261,7 +1274,8 @@ extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const fl
                                        float* const* exp_avg, float* const* exp_avg_sq, int Q,
                                        const float* spec_rows, const float* spec_acc,
                                        float* lb_out, double b1, double b2, double eps,
-                                       double step_size, double bc2_sqrt, vc_stream_t stream) {
+                                       double step_size, double bc2_sqrt, int init,
+                                       const float* ctl, vc_stream_t stream) {
   TGeom G;
   int rc = tiled_geom(dims, n_relu, G);
   if (rc != VC_OK) return rc;
@@ -1281,7 +1295,7 @@ extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const fl
     if (in && (!aa.lo[l] || !aa.hi[l] || !aa.alpha[l] || !aa.m1[l] || !aa.m2[l]))
       return VC_ERR_ARG;
   }
-  const size_t wsz = (size_t)n_relu * 7 * FW + (size_t)n_relu * G.KS * 4 * Q + FW;
+  const size_t wsz = (size_t)n_relu * 7 * FW + (size_t)n_relu * G.KS * 4 * Q + 3 * FW;
   const size_t lds = ((size_t)G.nfloats + (size_t)n_relu * FW + ANW * wsz) * sizeof(float);
   if (lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
   const void* fn = nullptr;
@@ -1304,7 +1318,7 @@ extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const fl
     hipLaunchKernelGGL((k_alpha_tiled<kVariants[V].MT, kVariants[V].KS,                      \
                                       kVariants[V].brow != 0>),                              \
                        grid, block, lds, st, G, frag, bias_cat, B, xl, xh, aa, Q, spec_rows, \
-                       spec_acc, lb_out, adam);                                              \
+                       spec_acc, lb_out, adam, init, ctl);                                   \
     break;
   switch (G.variant) {
     VC_TALPHA_CASE(0)

@@ -45,6 +45,7 @@ class MlpPlan:
         self.bias_cat = torch.cat(self.bs).contiguous()
         self.device = device
         self._dims_arr, self.dims_p = host_array(ctypes.c_int32, self.dims)
+        self._widths_arr, self.widths_p = host_array(ctypes.c_int32, self.dims[1:])
         wp_arr, wp = host_array(ctypes.c_void_p, [ptr(W) for W in self.Ws])
         lib = _lib.load()
         self.frag = {}
@@ -205,11 +206,23 @@ def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps)
     Q = S.shape[0]
     lo = [sb[L][0].contiguous() for L in range(plan.n)]
     hi = [sb[L][1].contiguous() for L in range(plan.n)]
-    alpha = [torch.empty_like(t) for t in lo]
-    m1 = [torch.zeros_like(t) for t in lo]
-    m2 = [torch.zeros_like(t) for t in lo]
-    for L in range(plan.n):
-        call('vc_alpha_init', ptr(lo[L]), ptr(hi[L]), lo[L].numel(), ptr(alpha[L]), st)
+    tiled = _tiled(plan)
+    # one allocation for alpha and the Adam state of every layer
+    sizes = [t.numel() for t in lo]
+    flat = torch.empty(3 * sum(sizes), device=dev)
+    views, off = [], 0
+    for _ in range(3):
+        row = []
+        for t, sz in zip(lo, sizes):
+            row.append(flat[off:off + sz].view(t.shape))
+            off += sz
+        views.append(row)
+    alpha, m1, m2 = views
+    if not tiled:
+        # the tiled kernel initialises alpha and the Adam state itself
+        flat[sum(sizes):].zero_()
+        for L in range(plan.n):
+            call('vc_alpha_init', ptr(lo[L]), ptr(hi[L]), lo[L].numel(), ptr(alpha[L]), st)
     keep = []
     ptrs = []
     for lst in (lo, hi, alpha, m1, m2):
@@ -223,10 +236,20 @@ def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps)
     prev_max = -float('inf')
     cur_lr = float(lr)
     n_eval = 0
-    if _tiled(plan):
-        name, frag = 'vc_mlp_tiled_alpha_iter', plan.tfrag
-    else:
-        name, frag = 'vc_mlp_alpha_iter', plan.frag[0]
+    if tiled:
+        # the loop control runs on the device: every iteration is launched,
+        # the ones after the stop do nothing, one host read at the end
+        ctl = torch.tensor([-float('inf'), 0.0, 0.0, 0.0], device=dev)
+        for it in range(n_iters):
+            step = it + 1
+            call('vc_mlp_tiled_alpha_iter', plan.dims_p, plan.n, ptr(plan.tfrag),
+                 ptr(plan.bias_cat), B, ptr(xl), ptr(xh), *ptrs, Q, ptr(S), ptr(acc0), ptr(lb),
+                 b1, b2, eps, cur_lr / (1 - b1 ** step), (1 - b2 ** step) ** 0.5,
+                 1 if it == 0 else 0, ptr(ctl), st)
+            call('vc_alpha_control', ptr(best), ptr(lb), B * Q, it, early_stop_eps, ptr(ctl), st)
+            cur_lr *= lr_decay
+        return best, int(ctl[2].item())
+    name, frag = 'vc_mlp_alpha_iter', plan.frag[0]
     for it in range(n_iters):
         step = it + 1
         call(name, plan.dims_p, plan.n, ptr(frag), ptr(plan.bias_cat),
@@ -261,10 +284,23 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False):
     lout_p = hout_p = None
     idx_t = None
     cnt_p = None
+    tiled = _tiled(plan)
     if do_crown:
-        idx_t, cnt = union_idx(plan, sb)
-        a, cnt_p = host_array(ctypes.c_int32, cnt)
-        keep.append(a)
+        if tiled:
+            # union of the unstable sets and its index lists, on the device
+            nw = sum(plan.dims[1:])
+            flags = torch.empty(nw, dtype=torch.uint8, device=dev)
+            call('vc_unstable_union_layers', lin_p, hin_p, plan.widths_p, plan.n, B,
+                 ptr(flags), stream())
+            idx_t = torch.empty(nw, dtype=torch.int32, device=dev)
+            meta = torch.empty(2 * plan.n, dtype=torch.int32, device=dev)
+            call('vc_union_compact', ptr(flags), plan.widths_p, plan.n, ptr(idx_t), ptr(meta),
+                 stream())
+            cnt_p = ptr(meta)
+        else:
+            idx_t, cnt = union_idx(plan, sb)
+            a, cnt_p = host_array(ctypes.c_int32, cnt)
+            keep.append(a)
         lo_out = [torch.empty_like(t) for t in lo_in]
         hi_out = [torch.empty_like(t) for t in hi_in]
         a, lout_p = host_array(ctypes.c_void_p, [ptr(t) for t in lo_out])
@@ -280,7 +316,7 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False):
         if want_linear:
             A = torch.empty(B, Q, plan.dims[0], device=dev)
             acc = torch.empty(B, Q, device=dev)
-    if _tiled(plan):
+    if tiled:
         name, frag = 'vc_mlp_tiled_crown', plan.tfrag
     else:
         name, frag = 'vc_mlp_crown', plan.frag[0]

@@ -9,11 +9,12 @@ compaction, branching and bisection run as HIP kernels; the worklist is a
 LIFO list of device-resident 2-D chunks.  Root/leaf PGD, SB branching and
 LP/MILP escalation are not part of this engine.
 """
+import ctypes
 import time
 
 import torch
 
-from ._lib import call, f32, ptr, stream
+from ._lib import call, f32, host_array, ptr, stream
 from . import _lib
 from .spec import dedup_queries
 from .verify_zono_bnb import (_bound_crown_spec,
@@ -71,6 +72,20 @@ def _gather(t, idx):
         call('vc_gather_rows', ptr(f32(t)), ptr(idx), n, cols, ptr(out),
              stream())
     return out
+
+
+def _gather_layers(sb, idx):
+    """{L: (lo[idx], hi[idx])} for every layer, in one launch."""
+    Ls = sorted(sb)
+    ins = [f32(t) for L in Ls for t in sb[L]]
+    outs = [torch.empty((idx.numel(),) + tuple(t.shape[1:]), device=t.device) for t in ins]
+    if idx.numel() > 0:
+        keep = [host_array(ctypes.c_void_p, [ptr(t) for t in ins]),
+                host_array(ctypes.c_void_p, [ptr(t) for t in outs]),
+                host_array(ctypes.c_int32, [t[0].numel() for t in ins])]
+        call('vc_gather_rows_multi', keep[0][1], keep[1][1], keep[2][1], len(ins), ptr(idx),
+             idx.numel(), stream())
+    return {L: (outs[2 * k], outs[2 * k + 1]) for k, L in enumerate(Ls)}
 
 
 def _closure(lb, table):
@@ -215,8 +230,7 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
                     '(alpha_all=False) is not supported')
             # alpha starts from the zonotope bounds of the same boxes, which
             # the bound phase has already computed: gather their rows
-            sb_open = None if sb is None else {
-                L: (_gather(lo, open_idx), _gather(hi, open_idx)) for L, (lo, hi) in sb.items()}
+            sb_open = None if sb is None else _gather_layers(sb, open_idx)
             new, n_ait = _run_alpha_crown_inputsplit_batched(
                 _gather(xl, open_idx), _gather(xh, open_idx), gg, spec_ew,
                 dev, dt, n_iters=alpha_iters, lr=alpha_lr,
