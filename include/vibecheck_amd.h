@@ -381,7 +381,13 @@ int vc_mlp_tiled_pack(const float *const *W, const float *const *bias,
  * the fc bias carried by the MFMA, the per-row constants accumulated in
  * fp64.  The seeded neuron lists stay on the device: idx_meta (device,
  * 2 * n_relu int32) holds the per-layer counts, then their offsets into
- * idx_all, as written by vc_union_compact.
+ * idx_all, as written by vc_union_compact.  per_domain != 0 seeds, in each
+ * domain, only the listed neurons with lo < 0 and hi > -1e-7 there: the
+ * spec bound, A, acc and every relaxation are those of seeding the whole
+ * list (the other neurons have slopes their tightening cannot change);
+ * lo_out/hi_out of the unseeded neurons keep lo_in/hi_in.  seed_rows
+ * (device, n_relu uint64, nullable) accumulates the seeded neurons per
+ * layer over all domains (the work done, for the roofline).
  * Replaces _crown_intermediate_batched (verify_zono_bnb.py:4077-4147) and
  * _spec_backward_graph_batched with return_input_linear
  * (verify_zono_bnb.py:4270-4453, 5117-5134). */
@@ -390,10 +396,10 @@ int vc_mlp_tiled_crown(const int32_t *dims, int n_relu, const float *frag,
                        const float *xh, const float *const *lo_in,
                        const float *const *hi_in, float *const *lo_out,
                        float *const *hi_out, const int32_t *idx_all,
-                       const int32_t *idx_meta, int do_crown, int Q,
-                       const float *spec_rows, const float *spec_acc,
+                       const int32_t *idx_meta, int do_crown, int per_domain,
+                       int Q, const float *spec_rows, const float *spec_acc,
                        float *lb_out, float *A_out, float *acc_out,
-                       vc_stream_t stream);
+                       uint64_t *seed_rows, vc_stream_t stream);
 
 /* The neurons unstable in any domain, per layer, for the CROWN seeding of
  * _crown_intermediate_batched (verify_zono_bnb.py:4123): flags (sum of

@@ -321,7 +321,7 @@ def test_bound_phase_parity_acas(gpu, mlp_path):
     lb64, A64, acc64 = rb.spec_backward_batched(t64, *x64, d64(gg_c), d64(se_c),
                                                 return_input_linear=True)
     gt, glb, gA, gacc = vz._bound_crown_spec(gg_g, xl.to(gpu), xh.to(gpu), se_g, gpu, F32,
-                                             return_input_linear=True)
+                                             return_input_linear=True, union_seeds=True)
     for L in tight:
         assert_interval(gt[L], tight[L], f'bound tight L{L} ({mlp_path})', ref64=t64[L])
     s = spec_scale(A, acc, xl, xh)
@@ -329,6 +329,33 @@ def test_bound_phase_parity_acas(gpu, mlp_path):
     assert_bounds(gacc, acc, f'bound acc ({mlp_path})', ref64=acc64, scale=s)
     assert_bounds(gA, A, f'bound A ({mlp_path})', ref64=A64,
                   scale=A.abs().amax(-1, keepdim=True))
+
+
+def test_bound_phase_per_domain_seeds_exact(gpu):
+    """Per-domain seeding (the default of the bound phase) against seeding
+    the batch union: bit-identical spec bound, A and acc; identical bounds
+    of every neuron unstable in its domain; identical unstable sets; the
+    other neurons keep their zonotope bounds, which contain the tightened
+    ones."""
+    gg_c, gg_g, xl, xh = acas(gpu, 4096, seed=9, scale=2.0)
+    _, se_g, _ = spec_pair(5, gpu)
+    xl, xh = xl.to(gpu), xh.to(gpu)
+    ut, ulb, uA, uacc, zsb = vz._bound_crown_spec(gg_g, xl, xh, se_g, gpu, F32,
+                                                  return_input_linear=True,
+                                                  return_zono_sb=True, union_seeds=True)
+    pt, plb, pA, pacc = vz._bound_crown_spec(gg_g, xl, xh, se_g, gpu, F32,
+                                             return_input_linear=True)
+    assert torch.equal(plb, ulb) and torch.equal(pA, uA) and torch.equal(pacc, uacc)
+    for L in ut:
+        zlo, zhi = zsb[L]
+        seeded = (zlo < 0) & (zhi > -1e-7)
+        assert torch.equal(pt[L][0][seeded], ut[L][0][seeded])
+        assert torch.equal(pt[L][1][seeded], ut[L][1][seeded])
+        assert torch.equal(pt[L][0][~seeded], zlo[~seeded])
+        assert torch.equal(pt[L][1][~seeded], zhi[~seeded])
+        assert bool((ut[L][0] >= pt[L][0]).all()) and bool((ut[L][1] <= pt[L][1]).all())
+        for t in (pt, ut):
+            assert torch.equal((t[L][0] < 0) & (t[L][1] > 0), (ut[L][0] < 0) & (ut[L][1] > 0))
 
 
 def test_crown_intermediate_parity_mlp_chunked(gpu):

@@ -385,8 +385,9 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
     TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
     const float* __restrict__ xl, const float* __restrict__ xh, TCrownArgs ca,
     const int32_t* __restrict__ idx_all, const int32_t* __restrict__ idx_meta, int do_crown,
-    int Q, const float* __restrict__ spec_rows, const float* __restrict__ spec_acc,
-    float* __restrict__ lb_out, float* __restrict__ A_out, float* __restrict__ acc_out) {
+    int per_domain, int Q, const float* __restrict__ spec_rows,
+    const float* __restrict__ spec_acc, float* __restrict__ lb_out, float* __restrict__ A_out,
+    float* __restrict__ acc_out, unsigned long long* __restrict__ seed_rows) {
   extern __shared__ float smem[];
   float* sfrag = smem;
   float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
@@ -398,10 +399,13 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
   for (int l = 1; l <= n; ++l) nmax += G.d[l];
   const int nidx = do_crown ? idx_meta[n + n - 1] + idx_meta[n - 1] : 0;
   int* sidx = reinterpret_cast<int*>(sbias + n * FW);
-  float* ssl = sbias + n * FW + nmax + wv * (n * 3 * FW + 6 * FW);  // slopes [layer][3][FW]
+  float* ssl = sbias + n * FW + nmax + wv * (n * 3 * FW + 7 * FW + MAXL);  // [layer][3][FW]
   float* slb = ssl + n * 3 * FW;                                    // seeded-row bounds
   float* stl = slb + 2 * FW;                                        // current layer lo / hi
   float* sx = stl + 2 * FW;                                         // the box: xl, xh [FW]
+  int* sseed = reinterpret_cast<int*>(sx + 2 * FW);                 // this domain's seeds
+  int* sscnt = sseed + FW;  // seeded neurons per layer, this wave's domains
+  if (lane < MAXL) sscnt[lane] = 0;
   vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
   for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
     const int l = k / FW, j = k % FW;
@@ -430,10 +434,26 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
         nhi = lane < dn ? ca.hi_in[L + 1][dom * dn + lane] : 0.f;
       }
       __threadfence_block();
-      const int m = do_crown ? min(idx_meta[L], dW) : 0;
+      int m = do_crown ? min(idx_meta[L], dW) : 0;
       const int* idx = sidx + (do_crown ? idx_meta[n + L] : 0);
+      if (per_domain && m > 0) {
+        // Seed only the union neurons whose slopes depend on their bounds in
+        // this domain: lo < 0 and hi > -1e-7.  An active neuron (lo >= 0)
+        // has slopes 1, 1, 0 and a dead one with hi <= -1e-7 has 0, 0, 0
+        // whatever the tightening does (lo only rises, hi only falls), so
+        // the spec bound and every relaxation are unchanged; only the
+        // reported bounds of those neurons stay the zonotope ones.
+        const int j = lane < m ? idx[lane] : 0;
+        const bool keep = lane < m && stl[j] < 0.f && stl[FW + j] > -1e-7f;
+        const uint64_t bal = __ballot(keep);
+        if (keep) sseed[__popcll(bal & ((1ull << lane) - 1ull))] = j;
+        m = __popcll(bal);
+        idx = sseed;
+        __threadfence_block();
+      }
       const int R = 2 * m;
       const int ntiles = (R + 15) / 16;
+      if (lane == 0) sscnt[L] += m;
       for (int nt0 = 0; nt0 < ntiles; nt0 += TNP) {
         if (ntiles - nt0 >= TNP)
           seeded_group<MT, KS, TNP, BROW>(G, L, nt0, m, idx, fr0, frh, ssl, sbias, slb, lane, g,
@@ -471,6 +491,9 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
                                     r, dxl, dxh, dom, lb_out, A_out, acc_out);
     }
   }
+  __threadfence_block();
+  if (seed_rows && lane < n && sscnt[lane] > 0)
+    atomicAdd(seed_rows + lane, (unsigned long long)sscnt[lane]);
 }
 
 // ------------------------------------------------------ alpha-CROWN kernel
@@ -1206,9 +1229,10 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
                                   const float* xh, const float* const* lo_in,
                                   const float* const* hi_in, float* const* lo_out,
                                   float* const* hi_out, const int32_t* idx_all,
-                                  const int32_t* idx_meta, int do_crown, int Q,
+                                  const int32_t* idx_meta, int do_crown, int per_domain, int Q,
                                   const float* spec_rows, const float* spec_acc, float* lb_out,
-                                  float* A_out, float* acc_out, vc_stream_t stream) {
+                                  float* A_out, float* acc_out, uint64_t* seed_rows,
+                                  vc_stream_t stream) {
   TGeom G;
   int rc = tiled_geom(dims, n_relu, G);
   if (rc != VC_OK) return rc;
@@ -1229,7 +1253,7 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
     if (in) nmax += G.d[l + 1];
   }
   const size_t lds = ((size_t)G.nfloats + (size_t)n_relu * FW + (size_t)nmax +
-                      (size_t)TNW * (n_relu * 3 * FW + 6 * FW)) *
+                      (size_t)TNW * (n_relu * 3 * FW + 7 * FW + MAXL)) *
                      sizeof(float);
   if (lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
   const void* fn = nullptr;
@@ -1251,7 +1275,8 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
     hipLaunchKernelGGL((k_crown_tiled<kVariants[V].MT, kVariants[V].KS,                      \
                                       kVariants[V].brow != 0>),                              \
                        grid, block, lds, st, G, frag, bias_cat, B, xl, xh, ca, idx_all,      \
-                       idx_meta, do_crown, Q, spec_rows, spec_acc, lb_out, A_out, acc_out);  \
+                       idx_meta, do_crown, per_domain, Q, spec_rows, spec_acc, lb_out, A_out,  \
+                       acc_out, reinterpret_cast<unsigned long long*>(seed_rows));           \
     break;
   switch (G.variant) {
     VC_TILED_CASE(0)

@@ -67,8 +67,8 @@ SIGNATURES = {
                           _P, _P, _P, _D, _D, _D, _D, _D, _P],
     'vc_mlp_tiled_floats': [_P, _I],
     'vc_mlp_tiled_pack': [_P, _P, _P, _I, _P, _P],
-    'vc_mlp_tiled_crown': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _I,
-                           _I, _P, _P, _P, _P, _P, _P],
+    'vc_mlp_tiled_crown': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I,
+                           _I, _P, _P, _P, _P, _P, _P, _P],
     'vc_mlp_tiled_alpha_iter': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
                                 _P, _P, _P, _D, _D, _D, _D, _D, _I, _P, _P],
     'vc_unstable_union_layers': [_P, _P, _P, _I, _L, _P, _P],
@@ -157,7 +157,7 @@ _FLOPS = {
     # 2 * M * n_out * n_in
     'vc_backward_fc': lambda a: 2.0 * a[1] * a[3] * a[11],
     'vc_mlp_crown': _flops_mlp_crown,
-    'vc_mlp_tiled_crown': _flops_mlp_crown,
+    'vc_mlp_tiled_crown': lambda a: 0.0,
 }
 
 _timing = None

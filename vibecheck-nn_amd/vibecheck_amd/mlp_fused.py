@@ -22,6 +22,10 @@ PLAN_KEY = '_vc_amd_mlp_plan'
 # has an instantiation; switching this off runs vc_mlp_crown.
 TILED = True
 
+# When set to a device int64 tensor of MAX_L entries, the shape-specialised
+# CROWN kernel adds its seeded neurons per layer to it (work accounting).
+SEED_COUNTER = None
+
 
 class MlpPlan:
     """Packed weights of a qualifying network on one device."""
@@ -267,9 +271,13 @@ def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps)
     return best, n_eval
 
 
-def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False):
+def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False, per_domain=False):
     """CROWN intermediate bounds (do_crown) and/or the spec backward.
 
+    ``per_domain``: seed, in each domain, only the union neurons whose
+    slopes depend on their bounds there (see vc_mlp_tiled_crown): identical
+    spec bound, A and acc; the returned bounds of the other neurons stay
+    the starting ones.  Ignored without the shape-specialised kernel.
     Returns (tight {L: (lo, hi)} or None, lb (B, Q) or None, A, acc)."""
     B = xl.shape[0]
     dev = xl.device
@@ -317,12 +325,14 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False):
             A = torch.empty(B, Q, plan.dims[0], device=dev)
             acc = torch.empty(B, Q, device=dev)
     if tiled:
-        name, frag = 'vc_mlp_tiled_crown', plan.tfrag
+        call('vc_mlp_tiled_crown', plan.dims_p, plan.n, ptr(plan.tfrag), ptr(plan.bias_cat), B,
+             ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
+             1 if do_crown else 0, 1 if per_domain else 0, Q, ptr(S), ptr(acc0), ptr(lb),
+             ptr(A), ptr(acc), ptr(SEED_COUNTER), stream())
     else:
-        name, frag = 'vc_mlp_crown', plan.frag[0]
-    call(name, plan.dims_p, plan.n, ptr(frag), ptr(plan.bias_cat), B,
-         ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
-         1 if do_crown else 0, Q, ptr(S), ptr(acc0), ptr(lb), ptr(A), ptr(acc), stream())
+        call('vc_mlp_crown', plan.dims_p, plan.n, ptr(plan.frag[0]), ptr(plan.bias_cat), B,
+             ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
+             1 if do_crown else 0, Q, ptr(S), ptr(acc0), ptr(lb), ptr(A), ptr(acc), stream())
     tight = None
     if do_crown:
         tight = {L: (lo_out[L], hi_out[L]) for L in range(plan.n)}

@@ -689,10 +689,16 @@ def _run_alpha_crown_inputsplit_batched(xl, xh, gg, spec_ew, device, dtype,
 
 
 def _bound_crown_spec(gg, xl, xh, spec_ew, device, dtype,
-                      return_input_linear=False, return_zono_sb=False):
+                      return_input_linear=False, return_zono_sb=False, union_seeds=False):
     """CROWN intermediate bounds followed by the spec bound -- the 'bound'
     phase of an input-split BaB iteration (verify_graph.py:12855-12871).
-    For narrow fc/ReLU chains both run in one whole-network kernel launch.
+    For narrow fc/ReLU chains both run in one whole-network kernel launch,
+    which by default seeds in each domain only the union neurons whose
+    slopes depend on their bounds there: the spec bound, A and acc are
+    those of the reference's union seeding, and so are the bounds of every
+    neuron unstable in the domain; the bounds of the domain's stable
+    neurons stay the zonotope ones (``union_seeds=True`` tightens them
+    too, as _crown_intermediate_batched does).
     Returns (tight, lb) or (tight, lb, A, acc); ``return_zono_sb``
     (extension) appends the zonotope bounds the CROWN pass started from,
     which the alpha-CROWN of the same boxes starts from as well."""
@@ -703,7 +709,8 @@ def _bound_crown_spec(gg, xl, xh, spec_ew, device, dtype,
     if plan is not None and len(spec_ew) <= 32:
         Wq, bq = _spec_rows(spec_ew, xl.device)
         tight, lb, A, acc = mlp_fused.crown(plan, xl, xh, sb, True, spec=(Wq, bq),
-                                            want_linear=return_input_linear)
+                                            want_linear=return_input_linear,
+                                            per_domain=not union_seeds)
         out = (tight, lb, A, acc) if return_input_linear else (tight, lb)
     else:
         tight = _crown_intermediate_batched(gg, xl, xh, device, dtype, sb=sb)
