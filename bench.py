@@ -127,6 +127,7 @@ def main():
         return
 
     from vibecheck_amd import _lib
+    from vibecheck_amd import mlp_fused as mf
     from vibecheck_amd import verify_graph as vg
     from vibecheck_amd import workloads as wk
     from vibecheck_amd.spec import dedup_queries
@@ -144,6 +145,11 @@ def main():
         run_rounds(gg, xl0, xh0, se, table)
     torch.cuda.synchronize()
 
+    # The shape-specialised CROWN kernel counts the neurons it seeds per
+    # layer (one atomic per wavefront per layer): the work of its seeded rows
+    # depends on each domain's bounds.
+    seeded = torch.zeros(16, dtype=torch.int64, device=dev)
+    mf.SEED_COUNTER = seeded
     _lib.timing_begin(['vc_mlp_crown', 'vc_mlp_tiled_crown'])
     t0 = time.perf_counter()
     stats = None
@@ -152,6 +158,11 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     kt = _lib.timing_end()
+    mf.SEED_COUNTER = None
+    if 'vc_mlp_tiled_crown' in kt:
+        # input width of every fc: d_0 .. d_n for the n ReLU layers
+        dims = [op['W'].shape[1] for op in gg['ops'] if op['type'] == 'fc']
+        kt['vc_mlp_tiled_crown']['flops'] += _lib.seed_flops(dims, seeded.tolist())
 
     per_step = wall / args.steps
     domains = sum(s['B'] for s in stats)

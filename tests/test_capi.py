@@ -54,3 +54,21 @@ def test_argument_errors_map_to_exceptions():
                   None, None, None)
     lib = _lib.load()
     assert lib.vc_compact_workspace(1 << 20) >= 8
+
+
+def test_work_accounting_closed_forms():
+    """Flop accounting of the whole-network CROWN launches: a 2-layer chain
+    worked by hand, and the per-layer seed totals of the shape-specialised
+    kernel (union seeding: B * cnt[L]) giving the same figure as the
+    argument-based count of the untiled kernel."""
+    dims = [3, 4, 5]
+    # fc_0: 2*3*4 = 24 per row, fc_1: 2*4*5 = 40 per row.
+    # layer 1 seeds 2 neurons -> 4 rows through fc_0; Q = 2 spec rows
+    # through fc_1, fc_0; B = 7 domains.
+    want = 7 * (4 * 24 + 2 * (24 + 40))
+    assert _lib.mlp_crown_flops(dims, 2, 7, [0, 2], 1, 2) == want
+    cnt = [5, 3]
+    B, Q = 11, 4
+    full = _lib.mlp_crown_flops(dims, 2, B, cnt, 1, Q)
+    spec = _lib.mlp_crown_flops(dims, 2, B, [0, 0], 0, Q)
+    assert spec + _lib.seed_flops(dims, [B * c for c in cnt] + [0] * 14) == full

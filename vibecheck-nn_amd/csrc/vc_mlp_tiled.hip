@@ -32,7 +32,8 @@ using vcm::ks_count;
 using vcm::MAXL;
 
 constexpr int TNW = 12;  // waves per workgroup, one domain each (3 per SIMD)
-constexpr int TNP = 2;   // 16-row N-tiles chained together per wave
+constexpr int TNP = 1;   // 16-row N-tiles chained together per wave
+constexpr int TQMAX = 64;  // spec rows per call (taken 16 at a time)
 
 // LDS slot of lane L's fragment value at K-step ks.  The backward reads
 // (lane L, slot L) and the forward reads (lane (g, r) of M-tile mo reads
@@ -778,8 +779,9 @@ const void* alpha_fn() {
 // per unstable neuron appended at each relu).  fc products read the tiled
 // backward fragments in the forward direction; the bias enters through a
 // constant 1 in the centre column at the bias row.
-constexpr int ZNW = 8;  // waves per workgroup
+constexpr int ZNW = 8;  // waves per workgroup (fewer when the LDS scratch does not fit)
 constexpr int ZT = 8;   // column tiles per wave: 128 columns, centre included
+constexpr int ZSCR = 20 * FW;  // relu scratch floats per wave
 
 struct TZonoArgs {
   float* lo[MAXL];
@@ -806,8 +808,16 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
   __syncthreads();
   const float* fr0 = sfrag;
   const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
+  // this wave's relu scratch: |G| partials [16 lanes][FW], centre, lambda,
+  // mu, new-column index [FW] each
+  float* zpart = sbias + n * FW + wv * ZSCR;
+  float* zcen = zpart + 16 * FW;
+  float* zlam = zcen + FW;
+  float* zmu = zlam + FW;
+  int* zcol = reinterpret_cast<int*>(zmu + FW);
 
-  for (int64_t dom = (int64_t)blockIdx.x * ZNW + wv; dom < B; dom += (int64_t)gridDim.x * ZNW) {
+  const int nwv = blockDim.x >> 6;
+  for (int64_t dom = (int64_t)blockIdx.x * nwv + wv; dom < B; dom += (int64_t)gridDim.x * nwv) {
     const float* dxl = xl + dom * d0;
     const float* dxh = xh + dom * d0;
     v4f Z[ZT][4];
@@ -890,63 +900,80 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
               Z[0][t][i] = Z[0][t][i] + sbias[l * FW + 16 * t + 4 * g + i];
         }
       }
-      // relu_l: rad_j = sum over generator columns of |G|; lo/hi = c -/+ rad
+      // relu_l, transposed through this wave's LDS scratch: lane (g, r)
+      // adds |G| over its generator columns (only the tiles below Kc hold
+      // any), then lane j owns neuron j -- radius, bounds, lambda, mu and
+      // the column of its new generator -- and the rows read lambda, mu
+      // and that column back for the scaling and the append.
       const int dM = G.d[l + 1];
-      float mu[MT][4];
-      uint64_t umask = 0;
-      const bool last = l == n - 1;
+      {
+        float ps[MT][4];
 #pragma unroll
-      for (int t = 0; t < MT; ++t)
+        for (int t = 0; t < MT; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          double sd = 0.0;
+          for (int i = 0; i < 4; ++i) ps[t][i] = 0.f;
 #pragma unroll
-          for (int nt = 0; nt < ZT; ++nt)
-            if (nt > 0 || r > 0) sd += (double)fabsf(Z[nt][t][i]);
-          sd = row_sum16(sd);
-          const float rad = (float)sd;
-          const float c = row_bcast0(Z[0][t][i], r);
-          const int j = 16 * t + 4 * g + i;
-          const float lo = c - rad, hi = c + rad;
-          const bool valid = j < dM;
-          const bool ust = valid && lo < 0.f && hi > 0.f;
-          const bool dead = hi <= 0.f;
-          if (valid && r == 0) {
-            out.lo[l][dom * dM + j] = lo;
-            out.hi[l][dom * dM + j] = hi;
+        for (int nt = 0; nt < ZT; ++nt)
+          if (16 * nt < Kc) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                ps[t][i] += (nt > 0 || r > 0) ? fabsf(Z[nt][t][i]) : 0.f;
           }
-          const float lam = ust ? hi / (hi - lo) : (dead ? 0.f : 1.f);
-          mu[t][i] = ust ? (-hi * lo) / (2.f * (hi - lo)) : 0.f;
-          // scale the row by lambda (centre: lambda c + mu); a domain that
-          // overflows below discards its matrix anyway
-          if (!last) {
 #pragma unroll
-            for (int nt = 0; nt < ZT; ++nt)
-              Z[nt][t][i] = (nt == 0 && r == 0) ? lam * Z[nt][t][i] + mu[t][i] : Z[nt][t][i] * lam;
-          }
-          const uint64_t bal = __ballot(ust && r == 0);
-#pragma unroll
-          for (int gg = 0; gg < 4; ++gg)
-            if ((bal >> (16 * gg)) & 1ull) umask |= 1ull << (16 * t + 4 * gg + i);
+        for (int t = 0; t < MT; ++t) {
+          *reinterpret_cast<float4*>(zpart + r * FW + 16 * t + 4 * g) =
+              make_float4(ps[t][0], ps[t][1], ps[t][2], ps[t][3]);
+          if (r == 0)
+            *reinterpret_cast<float4*>(zcen + 16 * t + 4 * g) =
+                make_float4(Z[0][t][0], Z[0][t][1], Z[0][t][2], Z[0][t][3]);
         }
+      }
+      __threadfence_block();
+      const int j = lane;
+      double sd = 0.0;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) sd += (double)zpart[q * FW + j];
+      const float rad = (float)sd;
+      const float c = zcen[j];
+      const float lo = c - rad, hi = c + rad;
+      const bool valid = j < dM;
+      const bool ust = valid && lo < 0.f && hi > 0.f;
+      const bool dead = hi <= 0.f;
+      if (valid) {
+        out.lo[l][dom * dM + j] = lo;
+        out.hi[l][dom * dM + j] = hi;
+      }
+      const uint64_t umask = __ballot(ust);
       const int cnt = __popcll(umask);
-      if (last) break;  // the last relu's output is not propagated
+      if (l == n - 1) break;  // the last relu's output is not propagated
       if (Kc + cnt > 16 * ZT) {
         ovf = true;
         break;
       }
-      // append one column per unstable neuron at position Kc + rank
+      zlam[j] = ust ? hi / (hi - lo) : (dead ? 0.f : 1.f);
+      zmu[j] = ust ? (-hi * lo) / (2.f * (hi - lo)) : 0.f;
+      zcol[j] = ust ? Kc + __popcll(umask & ((1ull << j) - 1ull)) : -1;
+      __threadfence_block();
+      // scale each row by lambda (centre: lambda c + mu) and put mu in the
+      // row's new column; tiles from Kc + cnt on stay zero
 #pragma unroll
-      for (int t = 0; t < MT; ++t)
+      for (int nt = 0; nt < ZT; ++nt)
+        if (16 * nt < Kc + cnt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j = 16 * t + 4 * g + i;
-          if ((umask >> j) & 1ull) {
-            const int col = Kc + __popcll(umask & ((1ull << j) - 1ull));
-            if ((col & 15) == r) {
+          for (int t = 0; t < MT; ++t) {
+            const float4 lm = *reinterpret_cast<const float4*>(zlam + 16 * t + 4 * g);
+            const float4 mv = *reinterpret_cast<const float4*>(zmu + 16 * t + 4 * g);
+            const int4 cv = *reinterpret_cast<const int4*>(zcol + 16 * t + 4 * g);
+            const float lam4[4] = {lm.x, lm.y, lm.z, lm.w};
+            const float mu4[4] = {mv.x, mv.y, mv.z, mv.w};
+            const int col4[4] = {cv.x, cv.y, cv.z, cv.w};
 #pragma unroll
-              for (int nt = 0; nt < ZT; ++nt)
-                if (nt == (col >> 4)) Z[nt][t][i] = mu[t][i];
+            for (int i = 0; i < 4; ++i) {
+              float z = Z[nt][t][i];
+              z = (nt == 0 && r == 0) ? lam4[i] * z + mu4[i] : z * lam4[i];
+              Z[nt][t][i] = col4[i] == 16 * nt + r ? mu4[i] : z;
             }
           }
         }
@@ -1237,7 +1264,7 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
   int rc = tiled_geom(dims, n_relu, G);
   if (rc != VC_OK) return rc;
   if (!frag || !bias_cat || !xl || !xh || !lo_in || !hi_in || B < 0) return VC_ERR_ARG;
-  if (Q < 0 || Q > TNP * 16 * 2) return VC_ERR_UNSUPPORTED;
+  if (Q < 0 || Q > TQMAX) return VC_ERR_UNSUPPORTED;
   if (Q > 0 && (!spec_rows || !spec_acc || !lb_out)) return VC_ERR_ARG;
   if (do_crown && (!idx_all || !idx_meta || !lo_out || !hi_out)) return VC_ERR_ARG;
   if (B == 0) return VC_OK;
@@ -1376,8 +1403,11 @@ extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const f
     za.hi[l] = l < n_relu ? hi_out[l] : nullptr;
     if (l < n_relu && (!za.lo[l] || !za.hi[l])) return VC_ERR_ARG;
   }
-  const size_t lds = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float);
-  if (lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
+  const size_t base = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float);
+  const size_t scr = (size_t)ZSCR * sizeof(float);
+  if (base + scr > 160 * 1024) return VC_ERR_UNSUPPORTED;
+  const int nw = (int)std::min<size_t>(ZNW, (160 * 1024 - base) / scr);
+  const size_t lds = base + (size_t)nw * scr;
   const void* fn = nullptr;
   switch (G.variant) {
     case 0: fn = zono_fn<0>(); break;
@@ -1390,7 +1420,7 @@ extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const f
   }
   if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return VC_ERR_UNSUPPORTED;
-  const dim3 grid(vcm::persistent_grid(B, lds, ZNW)), block(ZNW * 64);
+  const dim3 grid(vcm::persistent_grid(B, lds, nw)), block(nw * 64);
   hipStream_t st = (hipStream_t)stream;
 #define VC_TZONO_CASE(V)                                                                     \
   case V:                                                                                    \

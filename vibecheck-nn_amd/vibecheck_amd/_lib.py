@@ -151,13 +151,29 @@ def _flops_mlp_crown(a):
     return mlp_crown_flops(dims, n, a[4], cnt, a[13], a[14])
 
 
+def seed_flops(dims, seeded):
+    """Algorithmic flops of the seeded rows of vc_mlp_tiled_crown launches,
+    from the per-layer seeded-neuron totals of its seed_rows output (each
+    seeded neuron is two rows through fc_{L-1} .. fc_0)."""
+    step = [2.0 * dims[l] * dims[l + 1] for l in range(len(dims) - 1)]
+    return sum(2.0 * int(seeded[L]) * sum(step[:L]) for L in range(len(dims) - 1))
+
+
+def _flops_tiled_spec(a):
+    # Spec rows only: the seeded rows depend on each domain's bounds when
+    # per_domain is set, so they are counted by the kernel (seed_flops).
+    n = a[1]
+    dims = list((ctypes.c_int32 * (n + 1)).from_address(a[0]))
+    return mlp_crown_flops(dims, n, a[4], [0] * n, 0, a[15])
+
+
 # Algorithmic work per launch, from the call's arguments (used by the
 # optional per-entry-point timing below).
 _FLOPS = {
     # 2 * M * n_out * n_in
     'vc_backward_fc': lambda a: 2.0 * a[1] * a[3] * a[11],
     'vc_mlp_crown': _flops_mlp_crown,
-    'vc_mlp_tiled_crown': lambda a: 0.0,
+    'vc_mlp_tiled_crown': _flops_tiled_spec,
 }
 
 _timing = None
