@@ -318,26 +318,31 @@ int vc_mlp_zono_wide(const int32_t *dims, int n_relu, const float *frag_fwd,
 
 /* The first pass of vc_mlp_zono_bounds with the tile shape fixed at
  * compile time (frag from vc_mlp_tiled_pack): one wavefront per domain, up
- * to 128 generator columns including the centre; overflow[b] = 1 for the
- * domains that need more (to be finished by vc_mlp_zono_wide).
+ * to 128 generator columns including the centre; overflow[b] = 1 (a byte
+ * flag, as vc_compact reads) for the domains that need more (to be
+ * finished by vc_mlp_tiled_zono_wide).
  * Replaces the ReLU bounds of _forward_zonotope_graph_batched
  * (verify_zono_bnb.py:3079-3211). */
 int vc_mlp_tiled_zono_bounds(const int32_t *dims, int n_relu, const float *frag,
                              const float *bias_cat, int64_t B, const float *xl,
                              const float *xh, float *const *lo_out,
-                             float *const *hi_out, int32_t *overflow,
+                             float *const *hi_out, uint8_t *overflow,
                              vc_stream_t stream);
 
 /* vc_mlp_zono_wide with the tile shape fixed at compile time (frag from
- * vc_mlp_tiled_pack): the domains with overflow[b] != 0, one 4-wave
- * workgroup each, up to 512 generator columns dealt round-robin over the
- * waves; overflow[b] rewritten (1 = still does not fit).
+ * vc_mlp_tiled_pack): the *n_list domains list[0 .. *n_list) (device
+ * memory, as vc_compact writes them from the overflow flags), dealt
+ * round-robin over the workgroups, one 4-wave workgroup per domain with up
+ * to 512 generator columns spread over the waves; overflow[list[k]]
+ * rewritten (1 = still does not fit).  The count is read on the device, so
+ * the call needs no host synchronisation.
  * Replaces the ReLU bounds of _forward_zonotope_graph_batched
  * (verify_zono_bnb.py:3079-3211) for those domains. */
 int vc_mlp_tiled_zono_wide(const int32_t *dims, int n_relu, const float *frag,
                            const float *bias_cat, int64_t B, const float *xl,
                            const float *xh, float *const *lo_out,
-                           float *const *hi_out, int32_t *overflow,
+                           float *const *hi_out, uint8_t *overflow,
+                           const int64_t *list, const int64_t *n_list,
                            vc_stream_t stream);
 
 /* CROWN intermediate bounds and the spec backward, whole network per

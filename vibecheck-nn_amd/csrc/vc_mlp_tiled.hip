@@ -793,7 +793,7 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
                                                          const float* __restrict__ gbias,
                                                          int64_t B, const float* __restrict__ xl,
                                                          const float* __restrict__ xh,
-                                                         TZonoArgs out, int32_t* overflow) {
+                                                         TZonoArgs out, uint8_t* overflow) {
   extern __shared__ float smem[];
   float* sfrag = smem;
   float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
@@ -1002,18 +1002,20 @@ template <int MT, int KS, bool BROW>
 __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
     TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
     const float* __restrict__ xl, const float* __restrict__ xh, TZonoArgs out,
-    int32_t* overflow) {
+    uint8_t* overflow, const int64_t* __restrict__ list, const int64_t* __restrict__ n_list) {
   extern __shared__ float smem[];
   float* sfrag = smem;
   float* sbias = smem + G.nfloats;                                // [n][FW]
   double* sred = reinterpret_cast<double*>(sbias + G.n * FW);     // [ZWW][FW]
   float* scen = reinterpret_cast<float*>(sred + ZWW * FW);        // centre column [FW]
-  __shared__ int s_list[ZWW * 64];
-  __shared__ int s_wcnt[ZWW];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int n = G.n, d0 = G.d[0];
   const int cap = ZWW * ZWT * 16;
+  // workgroup k takes list entries k, k + grid, ...: the flagged domains
+  // spread evenly whatever their positions; idle workgroups leave at once
+  const int64_t nflag = *n_list;
+  if ((int64_t)blockIdx.x >= nflag) return;
   vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
   for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
     const int l = k / FW, j = k % FW;
@@ -1023,25 +1025,10 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
   const float* fr0 = sfrag;
   const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
 
-  // each workgroup scans a contiguous range of the flags, ZWW * 64 at a time
-  const int64_t per = (B + gridDim.x - 1) / gridDim.x;
-  const int64_t beg = (int64_t)blockIdx.x * per;
-  const int64_t end = beg + per < B ? beg + per : B;
-  for (int64_t c0 = beg; c0 < end; c0 += ZWW * 64) {
-    const int64_t dsc = c0 + threadIdx.x;
-    const bool flagged = dsc < end && overflow[dsc] != 0;
-    const uint64_t bal = __ballot(flagged);
-    if (lane == 0) s_wcnt[wv] = __popcll(bal);
-    __syncthreads();
-    int off = 0, tot = 0;
-    for (int w2 = 0; w2 < ZWW; ++w2) {
-      if (w2 < wv) off += s_wcnt[w2];
-      tot += s_wcnt[w2];
-    }
-    if (flagged) s_list[off + __popcll(bal & ((1ull << lane) - 1ull))] = (int)(dsc - c0);
-    __syncthreads();
-    for (int kd = 0; kd < tot; ++kd) {
-      const int64_t dom = c0 + s_list[kd];
+  {
+    for (int64_t q = blockIdx.x; q < nflag; q += gridDim.x) {
+      const int64_t dom = list[q];
+      if (dom < 0 || dom >= B) continue;
       const float* dxl = xl + dom * d0;
       const float* dxh = xh + dom * d0;
       v4f Z[ZWT][4];
@@ -1200,7 +1187,6 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
       }
       if (threadIdx.x == 0) overflow[dom] = ovf ? 1 : 0;
     }
-    __syncthreads();  // s_list / s_wcnt are rewritten by the next chunk
   }
 }
 
@@ -1389,7 +1375,7 @@ extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const fl
 extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const float* frag,
                                         const float* bias_cat, int64_t B, const float* xl,
                                         const float* xh, float* const* lo_out,
-                                        float* const* hi_out, int32_t* overflow,
+                                        float* const* hi_out, uint8_t* overflow,
                                         vc_stream_t stream) {
   TGeom G;
   int rc = tiled_geom(dims, n_relu, G);
@@ -1445,12 +1431,14 @@ extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const f
 extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const float* frag,
                                       const float* bias_cat, int64_t B, const float* xl,
                                       const float* xh, float* const* lo_out,
-                                      float* const* hi_out, int32_t* overflow,
+                                      float* const* hi_out, uint8_t* overflow,
+                                      const int64_t* list, const int64_t* n_list,
                                       vc_stream_t stream) {
   TGeom G;
   int rc = tiled_geom(dims, n_relu, G);
   if (rc != VC_OK) return rc;
-  if (!frag || !bias_cat || !xl || !xh || !lo_out || !hi_out || !overflow || B < 0)
+  if (!frag || !bias_cat || !xl || !xh || !lo_out || !hi_out || !overflow || !list ||
+      !n_list || B < 0)
     return VC_ERR_ARG;
   if (B == 0) return VC_OK;
   TZonoArgs za;
@@ -1482,7 +1470,7 @@ extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const flo
     hipLaunchKernelGGL((k_zono_wide_tiled<kVariants[V].MT, kVariants[V].KS,                  \
                                           kVariants[V].brow != 0>),                          \
                        dim3((unsigned)gw), dim3(ZWW * 64), lds, st, G, frag, bias_cat, B, xl, \
-                       xh, za, overflow);                                                    \
+                       xh, za, overflow, list, n_list);                                      \
     break;
   switch (G.variant) {
     VC_TWIDE_CASE(0)

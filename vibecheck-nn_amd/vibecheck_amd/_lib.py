@@ -77,7 +77,7 @@ SIGNATURES = {
     'vc_alpha_control': [_P, _P, _L, _I, _D, _P, _P],
     'vc_mlp_tiled_zono_bounds': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P],
     'vc_mlp_zono_wide': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P],
-    'vc_mlp_tiled_zono_wide': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P],
+    'vc_mlp_tiled_zono_wide': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P],
     'vc_widest_axis': [_P, _P, _L, _I, _P, _P, _P],
     'vc_bisect': [_P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P],
 }

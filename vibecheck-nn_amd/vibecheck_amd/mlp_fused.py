@@ -122,23 +122,27 @@ def zono_bounds(plan, xl, xh, fallback):
     dev = xl.device
     lo = [torch.empty(B, plan.dims[l + 1], device=dev) for l in range(plan.n)]
     hi = [torch.empty_like(t) for t in lo]
-    ovf = torch.empty(B, dtype=torch.int32, device=dev)
     lo_a, lo_p = host_array(ctypes.c_void_p, [ptr(t) for t in lo])
     hi_a, hi_p = host_array(ctypes.c_void_p, [ptr(t) for t in hi])
+    from .verify_graph import _compact, _compact_device, _gather
     if _tiled(plan):
         # one wavefront per domain (128 generator columns), then the 4-wave
-        # pass (512 columns) over the domains that did not fit
-        args = (B, ptr(xl), ptr(xh), lo_p, hi_p, ptr(ovf), stream())
+        # pass (512 columns) over the list of domains that did not fit,
+        # compacted on the device
+        ovf = torch.empty(B, dtype=torch.uint8, device=dev)
+        args = (B, ptr(xl), ptr(xh), lo_p, hi_p, ptr(ovf))
         call('vc_mlp_tiled_zono_bounds', plan.dims_p, plan.n, ptr(plan.tfrag),
-             ptr(plan.bias_cat), *args)
+             ptr(plan.bias_cat), *args, stream())
+        lst, cnt = _compact_device(ovf)
         call('vc_mlp_tiled_zono_wide', plan.dims_p, plan.n, ptr(plan.tfrag),
-             ptr(plan.bias_cat), *args)
+             ptr(plan.bias_cat), *args, ptr(lst), ptr(cnt), stream())
     else:
+        ovf = torch.empty(B, dtype=torch.int32, device=dev)
         call('vc_mlp_zono_bounds', plan.dims_p, plan.n, ptr(plan.frag[1]),
              ptr(plan.bias_cat), B, ptr(xl), ptr(xh), lo_p, hi_p, ptr(ovf), stream())
+        ovf = ovf.to(torch.uint8)
     del lo_a, hi_a
-    from .verify_graph import _compact, _gather
-    bad = _compact(ovf.to(torch.uint8))
+    bad = _compact(ovf)
     if bad.numel() > 0:
         sub = fallback(_gather(xl, bad), _gather(xh, bad))
         for L in range(plan.n):

@@ -47,8 +47,9 @@ class DisjunctTable:
         self.n = len(self.groups)
 
 
-def _compact(flags, select_zero=False):
-    """Ascending positions of the set (or, with select_zero, clear) flags."""
+def _compact_device(flags, select_zero=False):
+    """Ascending positions of the set (or clear) flags and their count, both
+    left on the device: idx (max(n, 1),) int64 valid up to cnt, cnt (1,)."""
     n = flags.numel()
     dev = flags.device
     lib = _lib.load()
@@ -58,6 +59,12 @@ def _compact(flags, select_zero=False):
     cnt = torch.empty(1, dtype=torch.int64, device=dev)
     call('vc_compact', ptr(flags), n, 1 if select_zero else 0, ptr(idx),
          ptr(cnt), ptr(ws), ws_bytes, stream())
+    return idx, cnt
+
+
+def _compact(flags, select_zero=False):
+    """Ascending positions of the set (or, with select_zero, clear) flags."""
+    idx, cnt = _compact_device(flags, select_zero)
     return idx[:int(cnt.item())]
 
 
