@@ -28,6 +28,11 @@ extern "C" {
 #define VC_ERR_UNSUPPORTED 3 /* op or layout not supported */
 #define VC_ERR_LAUNCH 4      /* HIP launch / runtime error */
 
+/* Generator columns (centre included) that vc_mlp_tiled_zono_wide holds
+ * per domain; a net whose 1 + d[0] + d[1] + ... + d[n-1] stays within it
+ * never leaves a domain to a layer-wise fallback. */
+#define VC_ZONO_WIDE_COLS 512
+
 typedef void *vc_stream_t;
 
 /* Library version, for the host to check the ABI it loaded. */
@@ -458,6 +463,24 @@ int vc_mlp_tiled_alpha_iter(const int32_t *dims, int n_relu, const float *frag,
                             double b2, double eps, double step_size,
                             double bc2_sqrt, int init, const float *ctl,
                             vc_stream_t stream);
+
+/* The whole loop of _run_alpha_crown_inputsplit_batched
+ * (verify_zono_bnb.py:5239-5287) in one call: n_iters >= 1 iterations of
+ * vc_mlp_tiled_alpha_iter, each followed by vc_alpha_control, launched
+ * back to back with the loop control on the device.  ctl (4 floats) is set
+ * here and ends as vc_alpha_control leaves it (ctl[2] = evaluated
+ * iterations); best (B, Q) = the best bound per spec row.  Torch Adam's
+ * schedule: step size lr_t / (1 - b1^t), bias correction (1 - b2^t)^0.5,
+ * lr_{t+1} = lr_t * lr_decay. */
+int vc_mlp_tiled_alpha_run(const int32_t *dims, int n_relu, const float *frag,
+                           const float *bias_cat, int64_t B, const float *xl,
+                           const float *xh, const float *const *lo,
+                           const float *const *hi, float *const *alpha,
+                           float *const *exp_avg, float *const *exp_avg_sq, int Q,
+                           const float *spec_rows, const float *spec_acc,
+                           float *lb_out, float *best, double b1, double b2,
+                           double eps, double lr, double lr_decay, int n_iters,
+                           double early_stop_eps, float *ctl, vc_stream_t stream);
 
 /* ---- Input-split BaB step ---------------------------------------------- */
 

@@ -72,3 +72,9 @@ def test_work_accounting_closed_forms():
     full = _lib.mlp_crown_flops(dims, 2, B, cnt, 1, Q)
     spec = _lib.mlp_crown_flops(dims, 2, B, [0, 0], 0, Q)
     assert spec + _lib.seed_flops(dims, [B * c for c in cnt] + [0] * 14) == full
+
+
+def test_zono_wide_capacity_matches_header():
+    text = open(os.path.join(ROOT, 'include', 'vibecheck_amd.h')).read()
+    m = re.search(r'#define VC_ZONO_WIDE_COLS (\d+)', text)
+    assert m and int(m.group(1)) == _lib.VC_ZONO_WIDE_COLS

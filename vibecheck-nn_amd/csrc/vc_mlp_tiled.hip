@@ -997,6 +997,7 @@ const void* zono_fn() {
 // wave derives the same bounds, lambda, mu and unstable set.
 constexpr int ZWW = 4;  // waves per domain
 constexpr int ZWT = 8;  // column tiles per wave: 512 columns
+static_assert(ZWW * ZWT * 16 == VC_ZONO_WIDE_COLS, "wide zonotope capacity");
 
 template <int MT, int KS, bool BROW>
 __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
@@ -1369,6 +1370,49 @@ extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const fl
   }
 #undef VC_TALPHA_CASE
   VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+namespace {
+__global__ void k_alpha_ctl_init(float* ctl) {
+  if (threadIdx.x == 0) {
+    ctl[0] = -INFINITY;
+    ctl[1] = 0.f;
+    ctl[2] = 0.f;
+    ctl[3] = 0.f;
+  }
+}
+}  // namespace
+
+extern "C" int vc_mlp_tiled_alpha_run(const int32_t* dims, int n_relu, const float* frag,
+                                      const float* bias_cat, int64_t B, const float* xl,
+                                      const float* xh, const float* const* lo,
+                                      const float* const* hi, float* const* alpha,
+                                      float* const* exp_avg, float* const* exp_avg_sq, int Q,
+                                      const float* spec_rows, const float* spec_acc,
+                                      float* lb_out, float* best, double b1, double b2,
+                                      double eps, double lr, double lr_decay, int n_iters,
+                                      double early_stop_eps, float* ctl, vc_stream_t stream) {
+  if (!best || !ctl || n_iters < 1) return VC_ERR_ARG;
+  if (B < 0) return VC_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_alpha_ctl_init, dim3(1), dim3(64), 0, st, ctl);
+  VC_LAUNCH_CHECK();
+  if (B == 0) return VC_OK;
+  // the schedule of torch Adam under the reference's loop: step sizes
+  // lr_t / (1 - b1^t) and (1 - b2^t)^0.5, lr decayed after every iteration
+  double cur_lr = lr;
+  for (int it = 0; it < n_iters; ++it) {
+    const double step = (double)(it + 1);
+    int rc = vc_mlp_tiled_alpha_iter(dims, n_relu, frag, bias_cat, B, xl, xh, lo, hi, alpha,
+                                     exp_avg, exp_avg_sq, Q, spec_rows, spec_acc, lb_out, b1, b2,
+                                     eps, cur_lr / (1.0 - pow(b1, step)),
+                                     pow(1.0 - pow(b2, step), 0.5), it == 0 ? 1 : 0, ctl, stream);
+    if (rc != VC_OK) return rc;
+    rc = vc_alpha_control(best, lb_out, B * (int64_t)Q, it, early_stop_eps, ctl, stream);
+    if (rc != VC_OK) return rc;
+    cur_lr *= lr_decay;
+  }
   return VC_OK;
 }
 

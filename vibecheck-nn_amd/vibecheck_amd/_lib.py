@@ -12,6 +12,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, 'libvibecheck_amd.so')
 
 VC_OK, VC_ERR_ARG, VC_ERR_OOM, VC_ERR_UNSUPPORTED, VC_ERR_LAUNCH = 0, 1, 2, 3, 4
+VC_ZONO_WIDE_COLS = 512     # generator columns of vc_mlp_tiled_zono_wide
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -71,6 +72,8 @@ SIGNATURES = {
                            _I, _P, _P, _P, _P, _P, _P, _P],
     'vc_mlp_tiled_alpha_iter': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
                                 _P, _P, _P, _D, _D, _D, _D, _D, _I, _P, _P],
+    'vc_mlp_tiled_alpha_run': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
+                               _P, _P, _P, _P, _D, _D, _D, _D, _D, _I, _D, _P, _P],
     'vc_unstable_union_layers': [_P, _P, _P, _I, _L, _P, _P],
     'vc_union_compact': [_P, _P, _I, _P, _P, _P],
     'vc_gather_rows_multi': [_P, _P, _P, _I, _P, _L, _P],

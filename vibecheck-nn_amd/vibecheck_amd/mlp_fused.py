@@ -122,6 +122,8 @@ def zono_bounds(plan, xl, xh, fallback):
     dev = xl.device
     lo = [torch.empty(B, plan.dims[l + 1], device=dev) for l in range(plan.n)]
     hi = [torch.empty_like(t) for t in lo]
+    # every relu but the last can append one generator per neuron
+    max_cols = 1 + sum(plan.dims[:plan.n])
     lo_a, lo_p = host_array(ctypes.c_void_p, [ptr(t) for t in lo])
     hi_a, hi_p = host_array(ctypes.c_void_p, [ptr(t) for t in hi])
     from .verify_graph import _compact, _compact_device, _gather
@@ -136,6 +138,11 @@ def zono_bounds(plan, xl, xh, fallback):
         lst, cnt = _compact_device(ovf)
         call('vc_mlp_tiled_zono_wide', plan.dims_p, plan.n, ptr(plan.tfrag),
              ptr(plan.bias_cat), *args, ptr(lst), ptr(cnt), stream())
+        if max_cols <= _lib.VC_ZONO_WIDE_COLS:
+            # the wide pass holds every generator this net can have: no
+            # domain is left over (and no host round trip to find out)
+            del lo_a, hi_a
+            return {L: (lo[L], hi[L]) for L in range(plan.n)}, 0
     else:
         ovf = torch.empty(B, dtype=torch.int32, device=dev)
         call('vc_mlp_zono_bounds', plan.dims_p, plan.n, ptr(plan.frag[1]),
@@ -179,13 +186,20 @@ def union_idx(plan, sb):
 
 def fold_spec(plan, Wq, bq):
     """Spec rows through the final fc: S = Wq W_last (Q, d_n), acc0 = bq +
-    Wq b_last, by the backward fc kernel on the shared rows."""
+    Wq b_last, by the backward fc kernel on the shared rows.  The last fold
+    is kept on the plan (keyed on the rows' identity and in-place version);
+    callers only read it."""
+    key = (id(Wq), Wq._version, id(bq), bq._version)
+    hit = getattr(plan, '_fold', None)
+    if hit is not None and hit[0] == key:
+        return hit[3], hit[4]
     Q = Wq.shape[0]
     S = torch.empty(Q, plan.dims[plan.n], device=plan.device)
     acc = bq.clone()
     call('vc_backward_fc', ptr(Wq), Q, Q, plan.n_out, None, None, None, 0, None,
          ptr(plan.W_last), ptr(plan.b_last), plan.dims[plan.n], ptr(S), ptr(acc),
          None, 0, stream())
+    plan._fold = (key, Wq, bq, S, acc)
     return S, acc
 
 
@@ -245,17 +259,16 @@ def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps)
     cur_lr = float(lr)
     n_eval = 0
     if tiled:
-        # the loop control runs on the device: every iteration is launched,
-        # the ones after the stop do nothing, one host read at the end
-        ctl = torch.tensor([-float('inf'), 0.0, 0.0, 0.0], device=dev)
-        for it in range(n_iters):
-            step = it + 1
-            call('vc_mlp_tiled_alpha_iter', plan.dims_p, plan.n, ptr(plan.tfrag),
-                 ptr(plan.bias_cat), B, ptr(xl), ptr(xh), *ptrs, Q, ptr(S), ptr(acc0), ptr(lb),
-                 b1, b2, eps, cur_lr / (1 - b1 ** step), (1 - b2 ** step) ** 0.5,
-                 1 if it == 0 else 0, ptr(ctl), st)
-            call('vc_alpha_control', ptr(best), ptr(lb), B * Q, it, early_stop_eps, ptr(ctl), st)
-            cur_lr *= lr_decay
+        # the whole loop in one call, its control on the device: every
+        # iteration is launched, the ones after the stop do nothing; one
+        # host read at the end
+        if n_iters < 1:
+            raise ValueError('alpha_crown: n_iters must be >= 1')
+        ctl = torch.empty(4, device=dev)
+        call('vc_mlp_tiled_alpha_run', plan.dims_p, plan.n, ptr(plan.tfrag),
+             ptr(plan.bias_cat), B, ptr(xl), ptr(xh), *ptrs, Q, ptr(S), ptr(acc0), ptr(lb),
+             ptr(best), b1, b2, eps, cur_lr, float(lr_decay), int(n_iters),
+             float(early_stop_eps), ptr(ctl), st)
         return best, int(ctl[2].item())
     name, frag = 'vc_mlp_alpha_iter', plan.frag[0]
     for it in range(n_iters):

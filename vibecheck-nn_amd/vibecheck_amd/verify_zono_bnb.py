@@ -417,13 +417,33 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
     return lb.reshape(B, R), A, rows.shared, acc
 
 
+_SPEC_CACHE = {}
+
+
 def _spec_rows(spec_ew, dev):
+    """The spec rows stacked (Q, n_out) and their offsets (Q,) on ``dev``.
+    Cached for tensor rows (keyed on each tensor's identity and in-place
+    version): building them copies the offsets from the host, which would
+    stall the stream once per bound call.  Callers only read the result."""
     qids = sorted(spec_ew.keys())
+    key = None
+    if all(torch.is_tensor(spec_ew[q][0]) and not torch.is_tensor(spec_ew[q][1])
+           for q in qids):
+        key = (str(dev), tuple((q, id(spec_ew[q][0]), spec_ew[q][0]._version,
+                                float(spec_ew[q][1])) for q in qids))
+        hit = _SPEC_CACHE.get(key)
+        if hit is not None:
+            return hit[1], hit[2]
     Wq = torch.stack([torch.as_tensor(spec_ew[q][0]).reshape(-1)
-                      .to(device=dev, dtype=torch.float32) for q in qids])
+                      .to(device=dev, dtype=torch.float32) for q in qids]).contiguous()
     bq = torch.tensor([float(spec_ew[q][1]) for q in qids],
                       dtype=torch.float32, device=dev)
-    return Wq.contiguous(), bq
+    if key is not None:
+        if len(_SPEC_CACHE) >= 32:
+            _SPEC_CACHE.pop(next(iter(_SPEC_CACHE)))
+        # the rows are held so that their identities stay unique
+        _SPEC_CACHE[key] = ([spec_ew[q][0] for q in qids], Wq, bq)
+    return Wq, bq
 
 
 def _spec_backward_graph_batched(tight, xl, xh, gg, spec_ew, device, dtype,
@@ -631,6 +651,10 @@ def _run_alpha_crown_inputsplit_batched(xl, xh, gg, spec_ew, device, dtype,
     if sb is None:
         sb = _zono_sb(gg, xl, xh, device, dtype)
     sb = {L: (f32(lo), f32(hi)) for L, (lo, hi) in sb.items()}
+    if n_iters < 1 and sb:
+        # every ReLU layer is an Adam parameter, the loop body never runs:
+        # no best bound (verify_zono_bnb.py:5169-5173, 5247-5288)
+        return (None, 0) if return_trace else None
     Wq, bq = _spec_rows(spec_ew, dev)
     Q = Wq.shape[0]
     plan = _plan(gg, dev)
