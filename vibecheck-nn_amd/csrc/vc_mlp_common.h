@@ -4,6 +4,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+#include <utility>
+#include <vector>
+
 namespace vcm {
 
 constexpr int FW = 64;    // max layer width
@@ -47,6 +51,26 @@ inline int cu_count() {
     cached[dev] = n;
   }
   return cached[dev];
+}
+
+// Raise a kernel's dynamic LDS limit to what the CU holds (160 KB less its
+// static LDS), once per kernel and device: the attribute call would
+// otherwise cost host time on every launch.
+inline bool allow_max_lds(const void* fn) {
+  static std::mutex mu;
+  static std::vector<std::pair<const void*, int>> done;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const auto& e : done)
+    if (e.first == fn && e.second == dev) return true;
+  hipFuncAttributes attr;
+  if (hipFuncGetAttributes(&attr, fn) != hipSuccess) return false;
+  const int cap = 160 * 1024 - (int)attr.sharedSizeBytes;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, cap) != hipSuccess)
+    return false;
+  done.emplace_back(fn, dev);
+  return true;
 }
 
 // Persistent grid: as many workgroups as fit on the CUs at once given the

@@ -788,6 +788,50 @@ struct TZonoArgs {
   float* hi[MAXL];
 };
 
+// fc_0 on the input block for NP column tiles, tile p starting at column
+// base + p * step: column 0 = centre (and the constant 1 of the bias row),
+// column 1 + k = radius k.
+template <int MT, int KS, int NP, bool BROW>
+__device__ __forceinline__ void zono_input_tiles(const TGeom& G, const float* fr0,
+                                                 const float* dxl, const float* dxh, int g,
+                                                 int r, int base, int step, v4f (&o)[NP][4]) {
+  const int d0 = G.d[0];
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) o[p][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < G.mt0; ++mt) {
+    float in[NP][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = 16 * mt + 4 * g + i;
+      float c = 0.f, rd = 0.f;
+      if (k < d0) {
+        const float lv = dxl[k], hv = dxh[k];
+        c = (lv + hv) / 2.f;
+        rd = (hv - lv) / 2.f;
+      } else if (BROW && k == d0) {
+        c = 1.f;
+      }
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int col = base + p * step + r;
+        in[p][i] = col == 0 ? c : (col == 1 + k && k < d0 ? rd : 0.f);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int mo = 0; mo < MT; ++mo) {
+        const int ksf = 4 * mo + (r & 3);
+        const float a =
+            ksf < KS ? fr0[(mt * KS + ksf) * 64 + swz(16 * (r >> 2) + 4 * g + i, ksf)] : 0.f;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) o[p][mo] = mfma16x16x4(a, in[p][i], o[p][mo]);
+      }
+  }
+}
+
 template <int MT, int KS, bool BROW>
 __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* __restrict__ gfrag,
                                                          const float* __restrict__ gbias,
@@ -823,44 +867,24 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
     v4f Z[ZT][4];
     int Kc = 1 + d0;
     bool ovf = Kc > 16 * ZT;
-    // ---- fc_0 on the input block: column 0 = centre, column 1 + k = radius k
+    // ---- fc_0 on the input block, one tile at a time past the last used
 #pragma unroll
     for (int nt0 = 0; nt0 < ZT; nt0 += 2) {
       v4f o[2][4];
+      if (!ovf && 16 * (nt0 + 1) < Kc) {
+        zono_input_tiles<MT, KS, 2, BROW>(G, fr0, dxl, dxh, g, r, 16 * nt0, 16, o);
+      } else {
+        v4f o1[1][4];
+        if (!ovf && 16 * nt0 < Kc) {
+          zono_input_tiles<MT, KS, 1, BROW>(G, fr0, dxl, dxh, g, r, 16 * nt0, 16, o1);
+        } else {
 #pragma unroll
-      for (int p = 0; p < 2; ++p)
+          for (int mt = 0; mt < 4; ++mt) o1[0][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) o[p][mt] = v4f{0.f, 0.f, 0.f, 0.f};
-      if (!ovf && 16 * nt0 < Kc) {
-        for (int mt = 0; mt < G.mt0; ++mt) {
-          float in[2][4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int k = 16 * mt + 4 * g + i;
-            float c = 0.f, rd = 0.f;
-            if (k < d0) {
-              const float lv = dxl[k], hv = dxh[k];
-              c = (lv + hv) / 2.f;
-              rd = (hv - lv) / 2.f;
-            } else if (BROW && k == d0) {
-              c = 1.f;
-            }
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-              const int col = 16 * (nt0 + p) + r;
-              in[p][i] = col == 0 ? c : (col == 1 + k && k < d0 ? rd : 0.f);
-            }
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int mo = 0; mo < MT; ++mo) {
-              const int ksf = 4 * mo + (r & 3);
-              const float a =
-                  ksf < KS ? fr0[(mt * KS + ksf) * 64 + swz(16 * (r >> 2) + 4 * g + i, ksf)] : 0.f;
-#pragma unroll
-              for (int p = 0; p < 2; ++p) o[p][mo] = mfma16x16x4(a, in[p][i], o[p][mo]);
-            }
+        for (int mt = 0; mt < 4; ++mt) {
+          o[0][mt] = o1[0][mt];
+          o[1][mt] = v4f{0.f, 0.f, 0.f, 0.f};
         }
       }
 #pragma unroll
@@ -882,7 +906,7 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
         const float4* fr = frh + (l - 1) * KS * 64;
 #pragma unroll
         for (int nt0 = 0; nt0 < ZT; nt0 += 2) {
-          if (16 * nt0 < Kc) {
+          if (16 * (nt0 + 1) < Kc) {
             v4f o[2][4];
             fc_forward<MT, KS, 2, ZT>(fr, lane, g, r, Z, nt0, o);
 #pragma unroll
@@ -890,6 +914,12 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
               Z[nt0][mt] = o[0][mt];
               Z[nt0 + 1][mt] = o[1][mt];
             }
+          } else if (16 * nt0 < Kc) {
+            // tile nt0 + 1 holds no generator (zeros stay zeros)
+            v4f o[1][4];
+            fc_forward<MT, KS, 1, ZT>(fr, lane, g, r, Z, nt0, o);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) Z[nt0][mt] = o[0][mt];
           }
         }
         if (!BROW && r == 0) {
@@ -1035,44 +1065,26 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
       v4f Z[ZWT][4];
       int Kc = 1 + d0;
       bool ovf = Kc > cap;
-      // ---- fc_0 on the input block
+      // ---- fc_0 on the input block (local tile q = global tile ZWW q + wv)
 #pragma unroll
       for (int q0 = 0; q0 < ZWT; q0 += 2) {
         v4f o[2][4];
+        if (!ovf && 16 * (ZWW * (q0 + 1) + wv) < Kc) {
+          zono_input_tiles<MT, KS, 2, BROW>(G, fr0, dxl, dxh, g, r, 16 * (ZWW * q0 + wv),
+                                            16 * ZWW, o);
+        } else {
+          v4f o1[1][4];
+          if (!ovf && 16 * (ZWW * q0 + wv) < Kc) {
+            zono_input_tiles<MT, KS, 1, BROW>(G, fr0, dxl, dxh, g, r, 16 * (ZWW * q0 + wv),
+                                              16 * ZWW, o1);
+          } else {
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
+            for (int mt = 0; mt < 4; ++mt) o1[0][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+          }
 #pragma unroll
-          for (int mt = 0; mt < 4; ++mt) o[p][mt] = v4f{0.f, 0.f, 0.f, 0.f};
-        if (!ovf && 16 * (ZWW * q0 + wv) < Kc) {
-          for (int mt = 0; mt < G.mt0; ++mt) {
-            float in[2][4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int k = 16 * mt + 4 * g + i;
-              float c = 0.f, rd = 0.f;
-              if (k < d0) {
-                const float lv = dxl[k], hv = dxh[k];
-                c = (lv + hv) / 2.f;
-                rd = (hv - lv) / 2.f;
-              } else if (BROW && k == d0) {
-                c = 1.f;
-              }
-#pragma unroll
-              for (int p = 0; p < 2; ++p) {
-                const int col = 16 * (ZWW * (q0 + p) + wv) + r;
-                in[p][i] = col == 0 ? c : (col == 1 + k && k < d0 ? rd : 0.f);
-              }
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-              for (int mo = 0; mo < MT; ++mo) {
-                const int ksf = 4 * mo + (r & 3);
-                const float a =
-                    ksf < KS ? fr0[(mt * KS + ksf) * 64 + swz(16 * (r >> 2) + 4 * g + i, ksf)] : 0.f;
-#pragma unroll
-                for (int p = 0; p < 2; ++p) o[p][mo] = mfma16x16x4(a, in[p][i], o[p][mo]);
-              }
+          for (int mt = 0; mt < 4; ++mt) {
+            o[0][mt] = o1[0][mt];
+            o[1][mt] = v4f{0.f, 0.f, 0.f, 0.f};
           }
         }
 #pragma unroll
@@ -1094,7 +1106,7 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
           const float4* fr = frh + (l - 1) * KS * 64;
 #pragma unroll
           for (int q0 = 0; q0 < ZWT; q0 += 2) {
-            if (16 * (ZWW * q0 + wv) < Kc) {
+            if (16 * (ZWW * (q0 + 1) + wv) < Kc) {
               v4f o[2][4];
               fc_forward<MT, KS, 2, ZWT>(fr, lane, g, r, Z, q0, o);
 #pragma unroll
@@ -1102,6 +1114,11 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
                 Z[q0][mt] = o[0][mt];
                 Z[q0 + 1][mt] = o[1][mt];
               }
+            } else if (16 * (ZWW * q0 + wv) < Kc) {
+              v4f o[1][4];
+              fc_forward<MT, KS, 1, ZWT>(fr, lane, g, r, Z, q0, o);
+#pragma unroll
+              for (int mt = 0; mt < 4; ++mt) Z[q0][mt] = o[0][mt];
             }
           }
           if (!BROW && centre) {
@@ -1280,8 +1297,7 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
     case 5: fn = crown_fn<5>(); break;
     default: return VC_ERR_UNSUPPORTED;
   }
-  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-    return VC_ERR_UNSUPPORTED;
+  if (!vcm::allow_max_lds(fn)) return VC_ERR_UNSUPPORTED;
   const dim3 grid(vcm::persistent_grid(B, lds, TNW)), block(TNW * 64);
   hipStream_t st = (hipStream_t)stream;
 #define VC_TILED_CASE(V)                                                                     \
@@ -1347,8 +1363,7 @@ extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const fl
     case 5: fn = alpha_fn<5>(); break;
     default: return VC_ERR_UNSUPPORTED;
   }
-  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-    return VC_ERR_UNSUPPORTED;
+  if (!vcm::allow_max_lds(fn)) return VC_ERR_UNSUPPORTED;
   const dim3 grid(vcm::persistent_grid(B, lds, ANW)), block(ANW * 64);
   const AdamConst adam = adam_const(b1, b2, eps, step_size, bc2_sqrt);
   hipStream_t st = (hipStream_t)stream;
@@ -1448,8 +1463,7 @@ extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const f
     case 5: fn = zono_fn<5>(); break;
     default: return VC_ERR_UNSUPPORTED;
   }
-  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-    return VC_ERR_UNSUPPORTED;
+  if (!vcm::allow_max_lds(fn)) return VC_ERR_UNSUPPORTED;
   const dim3 grid(vcm::persistent_grid(B, lds, nw)), block(nw * 64);
   hipStream_t st = (hipStream_t)stream;
 #define VC_TZONO_CASE(V)                                                                     \
@@ -1504,8 +1518,7 @@ extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const flo
     case 5: fn = zono_wide_fn<5>(); break;
     default: return VC_ERR_UNSUPPORTED;
   }
-  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-    return VC_ERR_UNSUPPORTED;
+  if (!vcm::allow_max_lds(fn)) return VC_ERR_UNSUPPORTED;
   int64_t gw = vcm::cu_count();
   if (gw > B) gw = B;
   hipStream_t st = (hipStream_t)stream;

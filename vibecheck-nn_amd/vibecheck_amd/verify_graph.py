@@ -81,10 +81,10 @@ def _gather(t, idx):
     return out
 
 
-def _gather_layers(sb, idx):
-    """{L: (lo[idx], hi[idx])} for every layer, in one launch."""
-    Ls = sorted(sb)
-    ins = [f32(t) for L in Ls for t in sb[L]]
+def _gather_many(ts, idx):
+    """[t[idx] for t in ts] (fp32 tensors with the same rows), in one
+    launch."""
+    ins = [f32(t) for t in ts]
     outs = [torch.empty((idx.numel(),) + tuple(t.shape[1:]), device=t.device) for t in ins]
     if idx.numel() > 0:
         keep = [host_array(ctypes.c_void_p, [ptr(t) for t in ins]),
@@ -92,6 +92,13 @@ def _gather_layers(sb, idx):
                 host_array(ctypes.c_int32, [t[0].numel() for t in ins])]
         call('vc_gather_rows_multi', keep[0][1], keep[1][1], keep[2][1], len(ins), ptr(idx),
              idx.numel(), stream())
+    return outs
+
+
+def _gather_layers(sb, idx):
+    """{L: (lo[idx], hi[idx])} for every layer, in one launch."""
+    Ls = sorted(sb)
+    outs = _gather_many([t for L in Ls for t in sb[L]], idx)
     return {L: (outs[2 * k], outs[2 * k + 1]) for k, L in enumerate(Ls)}
 
 
@@ -238,8 +245,9 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
             # alpha starts from the zonotope bounds of the same boxes, which
             # the bound phase has already computed: gather their rows
             sb_open = None if sb is None else _gather_layers(sb, open_idx)
+            xl_o, xh_o = _gather_many([xl, xh], open_idx)
             new, n_ait = _run_alpha_crown_inputsplit_batched(
-                _gather(xl, open_idx), _gather(xh, open_idx), gg, spec_ew,
+                xl_o, xh_o, gg, spec_ew,
                 dev, dt, n_iters=alpha_iters, lr=alpha_lr,
                 lr_decay=alpha_lr_decay, sb=sb_open, return_trace=True)
             n_al = int(open_idx.numel())
@@ -255,15 +263,14 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
            'unclosed': unclosed, 'n_alpha_leaves': n_al,
            'n_alpha_iters': n_ait}
     if clip_enabled and unclosed.numel() > 0 and A is not None:
-        xl_u, xh_u = _gather(xl, unclosed), _gather(xh, unclosed)
-        xl_c, xh_c, feas = _clip(xl_u, xh_u, _gather(A, unclosed),
-                                 _gather(acc, unclosed), table)
+        xl_u, xh_u, A_u, acc_u = _gather_many([xl, xh, A, acc], unclosed)
+        xl_c, xh_c, feas = _clip(xl_u, xh_u, A_u, acc_u, table)
         fidx = _compact(feas)
         out['feasible'] = feas
-        xl_s, xh_s = _gather(xl_c, fidx), _gather(xh_c, fidx)
+        xl_s, xh_s = _gather_many([xl_c, xh_c], fidx)
     else:
         out['feasible'] = None
-        xl_s, xh_s = _gather(xl, unclosed), _gather(xh, unclosed)
+        xl_s, xh_s = _gather_many([xl, xh], unclosed)
     if timers is not None:
         t1 = sync_t()
         timers['clip'] = timers.get('clip', 0.0) + t1 - t0
