@@ -145,11 +145,11 @@ def main():
         run_rounds(gg, xl0, xh0, se, table)
     torch.cuda.synchronize()
 
-    # The shape-specialised CROWN kernel counts the neurons it seeds per
-    # layer (one atomic per wavefront per layer): the work of its seeded rows
-    # depends on each domain's bounds.
-    seeded = torch.zeros(16, dtype=torch.int64, device=dev)
-    mf.SEED_COUNTER = seeded
+    # The shape-specialised CROWN kernels count the neurons they seed per
+    # layer (one atomic per wavefront per layer), one counter row per call:
+    # the work of the seeded rows depends on each domain's bounds.
+    seeded = torch.zeros(args.steps * N_ROUNDS + 8, 16, dtype=torch.int64, device=dev)
+    mf.SEED_COUNTER, mf.SEED_ROW = seeded, 0
     _lib.timing_begin(['vc_mlp_crown', 'vc_mlp_tiled_crown'])
     t0 = time.perf_counter()
     stats = None
@@ -159,10 +159,17 @@ def main():
     wall = time.perf_counter() - t0
     kt = _lib.timing_end()
     mf.SEED_COUNTER = None
-    if 'vc_mlp_tiled_crown' in kt:
-        # input width of every fc: d_0 .. d_n for the n ReLU layers
+    if kt.get('vc_mlp_tiled_crown', {}).get('launches'):
+        # the dominant kernel is k_crown_tiled, the one-wavefront-per-domain
+        # kernel of the large batches; the small rounds run k_crown_dom
+        lib = _lib.load()
         dims = [op['W'].shape[1] for op in gg['ops'] if op['type'] == 'fc']
-        kt['vc_mlp_tiled_crown']['flops'] += _lib.seed_flops(dims, seeded.tolist())
+        rows = seeded.tolist()
+        sel = [(sec, fl + _lib.seed_flops(dims, rows[k]))
+               for k, (sec, fl, a) in enumerate(kt['vc_mlp_tiled_crown']['per_launch'])
+               if lib.vc_mlp_tiled_crown_mode(a[4]) == 0]
+        kt = {'vc_mlp_tiled_crown': {'launches': len(sel), 'seconds': sum(x[0] for x in sel),
+                                     'flops': sum(x[1] for x in sel)}}
 
     per_step = wall / args.steps
     domains = sum(s['B'] for s in stats)

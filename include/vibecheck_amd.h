@@ -386,6 +386,13 @@ int vc_mlp_tiled_pack(const float *const *W, const float *const *bias,
                       const int32_t *dims, int n_relu, float *frag,
                       vc_stream_t stream);
 
+/* Which kernel vc_mlp_tiled_crown runs for B domains on the current
+ * device: 0 = one wavefront per domain (large batches), 1 = several
+ * wavefronts per domain, up to 4 domains per workgroup (B <= 4 x compute
+ * units).  Both compute the same rows with the same arithmetic.  No
+ * counterpart in the reference (a dispatch rule of this library). */
+int vc_mlp_tiled_crown_mode(int64_t B);
+
 /* vc_mlp_crown with the tile shape fixed at compile time (same results;
  * frag from vc_mlp_tiled_pack, Q <= 64): no MFMA under a runtime condition,
  * the fc bias carried by the MFMA, the per-row constants accumulated in
@@ -397,7 +404,9 @@ int vc_mlp_tiled_pack(const float *const *W, const float *const *bias,
  * list (the other neurons have slopes their tightening cannot change);
  * lo_out/hi_out of the unseeded neurons keep lo_in/hi_in.  seed_rows
  * (device, n_relu uint64, nullable) accumulates the seeded neurons per
- * layer over all domains (the work done, for the roofline).
+ * layer over all domains (the work done, for the roofline).  Batches with
+ * vc_mlp_tiled_crown_mode(B) == 1 spread each domain's row tiles over
+ * several wavefronts (identical results).
  * Replaces _crown_intermediate_batched (verify_zono_bnb.py:4077-4147) and
  * _spec_backward_graph_batched with return_input_linear
  * (verify_zono_bnb.py:4270-4453, 5117-5134). */

@@ -358,6 +358,30 @@ def test_bound_phase_per_domain_seeds_exact(gpu):
             assert torch.equal((t[L][0] < 0) & (t[L][1] > 0), (ut[L][0] < 0) & (ut[L][1] > 0))
 
 
+@pytest.mark.parametrize('n_small', [100, 300, 900])
+def test_crown_small_batch_kernel_matches_throughput_kernel(gpu, n_small):
+    """Small batches run the domain-parallel CROWN kernel (several
+    wavefronts per domain, 1, 2 or 4 domains per workgroup), large ones one
+    wavefront per domain.  With per-domain seeding a domain's rows do not
+    depend on the rest of its batch, so the first n_small boxes of an
+    8192-box batch give bit-identical spec bounds, A, acc and CROWN bounds
+    either way."""
+    gg_c, gg_g, xl, xh = acas(gpu, 8192, seed=17, scale=2.0)
+    _, se_g, _ = spec_pair(5, gpu)
+    xl, xh = xl.to(gpu), xh.to(gpu)
+    bt, blb, bA, bacc = vz._bound_crown_spec(gg_g, xl, xh, se_g, gpu, F32,
+                                             return_input_linear=True)
+    st, slb, sA, sacc = vz._bound_crown_spec(gg_g, xl[:n_small].contiguous(),
+                                             xh[:n_small].contiguous(), se_g, gpu, F32,
+                                             return_input_linear=True)
+    assert torch.equal(slb, blb[:n_small])
+    assert torch.equal(sA, bA[:n_small])
+    assert torch.equal(sacc, bacc[:n_small])
+    for L in bt:
+        assert torch.equal(st[L][0], bt[L][0][:n_small])
+        assert torch.equal(st[L][1], bt[L][1][:n_small])
+
+
 def test_crown_intermediate_parity_mlp_chunked(gpu):
     gg_c = wk.deep_mlp_gg(dtype=F32)
     gg_g = wk.deep_mlp_gg(device=gpu, dtype=F32)

@@ -497,6 +497,122 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
     atomicAdd(seed_rows + lane, (unsigned long long)sscnt[lane]);
 }
 
+// The same CROWN pass for small batches, where one wavefront per domain
+// leaves most of the device idle and each domain's chain of tiles sets the
+// time: a workgroup takes D domains with P = waves / D wavefronts each,
+// the P wavefronts split every layer's seeded tiles (and the spec tiles),
+// and the per-layer steps of each domain (seed filter, intersection,
+// slopes) run between workgroup barriers.  Same arithmetic per row as
+// k_crown_tiled.
+template <int MT, int KS, bool BROW>
+__global__ __launch_bounds__(TNW * 64) void k_crown_dom(
+    TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
+    const float* __restrict__ xl, const float* __restrict__ xh, TCrownArgs ca,
+    const int32_t* __restrict__ idx_all, const int32_t* __restrict__ idx_meta, int do_crown,
+    int per_domain, int Q, const float* __restrict__ spec_rows,
+    const float* __restrict__ spec_acc, float* __restrict__ lb_out, float* __restrict__ A_out,
+    float* __restrict__ acc_out, unsigned long long* __restrict__ seed_rows, int D) {
+  extern __shared__ float smem[];
+  __shared__ int s_m[TNW];
+  __shared__ int s_cnt[MAXL];
+  float* sfrag = smem;
+  float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int n = G.n, d0 = G.d[0];
+  const int P = nw / D, slot = wv / P, pw = wv - slot * P;
+  int nmax = 0;
+  for (int l = 1; l <= n; ++l) nmax += G.d[l];
+  const int nidx = do_crown ? idx_meta[n + n - 1] + idx_meta[n - 1] : 0;
+  int* sidx = reinterpret_cast<int*>(sbias + n * FW);
+  // domain slot: slopes [n][3][FW], seeded-row bounds [2 FW], layer lo / hi
+  // [2 FW], the box [2 FW], the seed list [FW]
+  float* ssl = sbias + n * FW + nmax + slot * (n * 3 * FW + 7 * FW);
+  float* slb = ssl + n * 3 * FW;
+  float* stl = slb + 2 * FW;
+  float* sx = stl + 2 * FW;
+  int* sseed = reinterpret_cast<int*>(sx + 2 * FW);
+  if (threadIdx.x < MAXL) s_cnt[threadIdx.x] = 0;
+  vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
+  for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
+    const int l = k / FW, j = k % FW;
+    sbias[k] = j < G.d[l + 1] ? gbias[G.boff[l] + j] : 0.f;
+  }
+  for (int k = threadIdx.x; k < nidx && k < nmax; k += blockDim.x) sidx[k] = idx_all[k];
+  __syncthreads();
+  const float* fr0 = sfrag;
+  const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
+  const float* dxl = sx;
+  const float* dxh = sx + FW;
+  const bool lead = pw == 0;  // the wavefront doing the domain's per-layer steps
+
+  for (int64_t base = (int64_t)blockIdx.x * D; base < B; base += (int64_t)gridDim.x * D) {
+    const int64_t dom = base + slot;
+    const bool has = slot < D && dom < B;
+    if (lead && has) {
+      sx[lane] = lane < d0 ? xl[dom * d0 + lane] : 0.f;
+      sx[FW + lane] = lane < d0 ? xh[dom * d0 + lane] : 0.f;
+    }
+    for (int L = 0; L < n; ++L) {
+      const int dW = G.d[L + 1];
+      const int mu = do_crown ? min(idx_meta[L], dW) : 0;
+      const int* uidx = sidx + (do_crown ? idx_meta[n + L] : 0);
+      if (lead && has) {
+        stl[lane] = lane < dW ? ca.lo_in[L][dom * dW + lane] : 0.f;
+        stl[FW + lane] = lane < dW ? ca.hi_in[L][dom * dW + lane] : 0.f;
+        __threadfence_block();
+        int m = mu;
+        if (per_domain && m > 0) {
+          // the union neurons whose slopes depend on this domain's bounds
+          // (lo < 0, hi > -1e-7); see k_crown_tiled
+          const int j = lane < mu ? uidx[lane] : 0;
+          const bool keep = lane < mu && stl[j] < 0.f && stl[FW + j] > -1e-7f;
+          const uint64_t bal = __ballot(keep);
+          if (keep) sseed[__popcll(bal & ((1ull << lane) - 1ull))] = j;
+          m = __popcll(bal);
+        }
+        if (lane == 0) {
+          s_m[slot] = m;
+          atomicAdd(&s_cnt[L], m);  // LDS: the lead wavefronts of all slots
+        }
+      }
+      __syncthreads();
+      const int m = has ? s_m[slot] : 0;
+      const int* idx = per_domain ? sseed : uidx;
+      const int ntiles = (2 * m + 15) / 16;
+      for (int nt = pw; nt < ntiles; nt += P)
+        seeded_group<MT, KS, 1, BROW>(G, L, nt, m, idx, fr0, frh, ssl, sbias, slb, lane, g, r,
+                                      dxl, dxh);
+      __syncthreads();
+      if (lead && has) {
+        for (int q = lane; q < m; q += 64) {
+          const int j = idx[q];
+          const float lc = fmaxf(stl[j], slb[q]);
+          const float hc = fmaxf(fminf(stl[FW + j], -slb[m + q]), lc);
+          stl[j] = lc;
+          stl[FW + j] = hc;
+        }
+        __threadfence_block();
+        if (ca.lo_out[L]) {
+          for (int j = lane; j < dW; j += 64) {
+            ca.lo_out[L][dom * dW + j] = stl[j];
+            ca.hi_out[L][dom * dW + j] = stl[FW + j];
+          }
+        }
+        make_slopes_lds(ssl + L * 3 * FW, stl, stl + FW, dW, lane);
+      }
+      __syncthreads();
+    }
+    if (has)
+      for (int t = pw; 16 * t < Q; t += P)
+        spec_group<MT, KS, 1, BROW>(G, 16 * t, Q, spec_rows, spec_acc, fr0, frh, ssl, sbias,
+                                    lane, g, r, dxl, dxh, dom, lb_out, A_out, acc_out);
+    __syncthreads();
+  }
+  if (seed_rows && threadIdx.x < n && s_cnt[threadIdx.x] > 0)
+    atomicAdd(seed_rows + threadIdx.x, (unsigned long long)s_cnt[threadIdx.x]);
+}
+
 // ------------------------------------------------------ alpha-CROWN kernel
 // One Adam iteration of batched alpha-CROWN per domain (verify_zono_bnb.py:
 // 5248-5287), tile shape fixed at compile time: the spec backward with
@@ -568,6 +684,223 @@ __device__ __forceinline__ void fc_forward(const float4* fr, int lane, int g, in
   }
 }
 
+// Per-wave LDS of the alpha kernels: slopes [l][ls_eff, us, ut, unstable][FW],
+// Adam state [l][alpha, m, v][FW], the pre-relaxation rows P_l
+// [l][ks][g][r < Q], d lb / d alpha of one layer [FW], the box [2 FW].
+__host__ __device__ inline int alpha_wsz(int n, int KS, int Q) {
+  return n * 7 * FW + n * KS * 4 * Q + 3 * FW;
+}
+
+struct AlphaLds {
+  float *ssl, *sad, *sP, *sga, *sx;
+};
+
+__device__ __forceinline__ AlphaLds alpha_lds_at(float* w, int n, int KS, int Q) {
+  AlphaLds a;
+  a.ssl = w;
+  a.sad = a.ssl + n * 4 * FW;
+  a.sP = a.sad + n * 3 * FW;
+  a.sga = a.sP + n * KS * 4 * Q;
+  a.sx = a.sga + FW;
+  return a;
+}
+
+// The box and the per-neuron state of domain dom into the wave's LDS: the
+// relaxation of the starting bounds and alpha with its Adam state (init:
+// alpha = (up_s > 0.5) * unstable, state zero).
+template <int KS>
+__device__ __forceinline__ void alpha_load(const TGeom& G, const TAlphaArgs& aa,
+                                           const float* xl, const float* xh, int64_t dom,
+                                           int init, const AlphaLds& w, int lane) {
+  const int n = G.n, d0 = G.d[0];
+  w.sx[lane] = lane < d0 ? xl[dom * d0 + lane] : 0.f;
+  w.sx[FW + lane] = lane < d0 ? xh[dom * d0 + lane] : 0.f;
+#pragma unroll 4
+  for (int l = 0; l < n; ++l) {
+    const int dW = G.d[l + 1];
+    float* sl = w.ssl + l * 4 * FW;
+    float* sa = w.sad + l * 3 * FW;
+    for (int j = lane; j < FW; j += 64) {
+      float ls = 0.f, us = 0.f, ut = 0.f, un = 0.f, a = 0.f, m1 = 0.f, m2 = 0.f;
+      if (j < dW) {
+        const int64_t ai = dom * dW + j;
+        const Relax s = relax(aa.lo[l][ai], aa.hi[l][ai]);
+        if (init) {
+          // first iteration: alpha = (up_s > 0.5) * unstable, Adam state zero
+          a = (s.unstable && s.up_s > 0.5f) ? 1.f : 0.f;
+        } else {
+          a = aa.alpha[l][ai];
+          m1 = aa.m1[l][ai];
+          m2 = aa.m2[l][ai];
+        }
+        ls = s.active ? 1.f : (s.unstable ? a : 0.f);
+        us = s.up_s;
+        ut = s.up_t;
+        un = s.unstable ? 1.f : 0.f;
+      }
+      sl[j] = ls;
+      sl[FW + j] = us;
+      sl[2 * FW + j] = ut;
+      sl[3 * FW + j] = un;
+      sa[j] = a;
+      sa[FW + j] = m1;
+      sa[2 * FW + j] = m2;
+    }
+  }
+}
+
+// One alpha-CROWN iteration of the wave's domain from its LDS state: the
+// spec backward keeping P_l, fc_0 with the concretization, the forward
+// gradient sweep and the Adam update of alpha (clamped to [0, 1]).  With
+// keep_ls the lower slopes of the unstable neurons follow the new alpha
+// (for a next iteration on the same LDS state).  Returns the lane's row
+// bound (rows r < Q, lanes g == 0).
+template <int MT, int KS, bool BROW>
+__device__ __forceinline__ double alpha_pass(const TGeom& G, const AlphaLds& w, const float* fr0,
+                                             const float4* frh, const float* sbias, int Q,
+                                             const float* spec_rows, const float* spec_acc,
+                                             const AdamConst& adam, bool keep_ls, int lane,
+                                             int g, int r) {
+  const int n = G.n, d0 = G.d[0], dN = G.d[n];
+  const bool live = r < Q;
+  float* ssl = w.ssl;
+  float* sad = w.sad;
+  float* sP = w.sP;
+  float* sga = w.sga;
+  const float* dxl = w.sx;
+  const float* dxh = w.sx + FW;
+  // ---- spec backward with alpha, keeping P_l
+  v4f F[TNP][4];
+  double acc[TNP], cz[TNP];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = 16 * t + 4 * g + i;
+      F[0][t][i] = (live && k < dN) ? spec_rows[r * dN + k] : 0.f;
+    }
+  acc[0] = (live && g == 0) ? (double)spec_acc[r] : 0.0;
+  cz[0] = 0.0;
+  for (int l = n - 1; l >= 0; --l) {
+    if (live) {
+      float* pl = sP + l * KS * 4 * Q;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) pl[(ks * 4 + g) * Q + r] = F[0][ks >> 2][ks & 3];
+    }
+    relax_rows<KS, 1, BROW>(ssl + l * 4 * FW, sbias + l * FW, g, F, acc);
+    if (l > 0) fc_hidden<MT, KS, 1, BROW>(frh + (l - 1) * KS * 64, lane, g, G.d[l], F, acc);
+  }
+  // ---- fc_0, concretization and gE_0 = W_0 gA + b_0, one input tile at a time
+  v4f GE[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) GE[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < G.mt0; ++mt) {
+    v4f o = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      o = mfma16x16x4(fr0[(mt * KS + ks) * 64 + swz(lane, ks)], F[0][ks >> 2][ks & 3], o);
+    float gA[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * mt + 4 * g + i;
+      const float v = o[i];
+      gA[i] = 0.f;
+      if (m < d0) {
+        const float xlv = dxl[m], xhv = dxh[m];
+        cz[0] += (double)(fmaxf(v, 0.f) * xlv);
+        cz[0] += (double)(fminf(v, 0.f) * xhv);
+        float gv = 0.f;
+        if (v >= 0.f) gv += xlv;
+        if (v <= 0.f) gv += xhv;
+        gA[i] = live ? gv : 0.f;
+      } else if (BROW && m == d0) {
+        acc[0] += (double)v;
+        gA[i] = live ? 1.f : 0.f;
+      }
+    }
+    // A_fwd0[m'][k'] = A_0[k'][m']: lane (g, r), M-tile mo, K-step (mt, i)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int mo = 0; mo < MT; ++mo) {
+        const int ksf = 4 * mo + (r & 3);
+        const float a =
+            ksf < KS ? fr0[(mt * KS + ksf) * 64 + swz(16 * (r >> 2) + 4 * g + i, ksf)] : 0.f;
+        GE[mo] = mfma16x16x4(a, gA[i], GE[mo]);
+      }
+  }
+  const double lbd = group_sum4_d(acc[0] + cz[0]);
+  // ---- forward gradient sweep with the Adam update per layer
+  for (int l = 0; l < n; ++l) {
+    const int dW = G.d[l + 1];
+    float* sl = ssl + l * 4 * FW;
+    if (!BROW) {
+      // bias of fc_l (l >= 0) added for live rows: gE_l += b_l
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          GE[t][i] = live ? GE[t][i] + sbias[l * FW + 16 * t + 4 * g + i] : 0.f;
+    }
+    const float* pl = sP + l * KS * 4 * Q;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int t = ks >> 2, i = ks & 3;
+      const int j = 16 * t + 4 * g + i;
+      const float pv = live ? pl[(ks * 4 + g) * Q + r] : 0.f;
+      const float ge = GE[t][i];
+      const float s = row_sum16(ge * fmaxf(pv, 0.f));
+      if (r == 0) sga[j] = s;
+      const bool mp = pv >= 0.f, mn = pv <= 0.f;
+      float gp = ge * ((mp ? sl[j] : 0.f) + (mn ? sl[FW + j] : 0.f));
+      if (mn) gp = gp + sl[2 * FW + j];
+      GE[t][i] = live ? gp : 0.f;
+    }
+    __threadfence_block();
+    {
+      float* sa = sad + l * 3 * FW;
+      const int j = lane;
+      if (j < dW && sl[3 * FW + j] != 0.f) {
+        float mi = sa[FW + j], vi = sa[2 * FW + j];
+        float pa = adam_update(sa[j], -sga[j], mi, vi, adam);
+        pa = fminf(fmaxf(pa, 0.f), 1.f);
+        sa[FW + j] = mi;
+        sa[2 * FW + j] = vi;
+        sa[j] = pa;
+        if (keep_ls) sl[j] = pa;  // unstable: ls_eff = alpha
+      }
+    }
+    __threadfence_block();
+    if (l + 1 < n) {
+      // the rows at relu l's output (K of fc_{l+1}); with the bias row, a
+      // constant 1 at index d_{l+1} picks up b_{l+1}
+      if (BROW) set_elem<MT>(GE, dW, g, live ? 1.f : 0.f);
+      v4f xin[1][4], nx[1][4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) xin[0][mt] = GE[mt];
+      fc_forward<MT, KS, 1, 1>(frh + l * KS * 64, lane, g, r, xin, 0, nx);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) GE[mt] = nx[0][mt];
+    }
+  }
+  return lbd;
+}
+
+// The updated Adam state of domain dom back to global memory (coalesced).
+__device__ __forceinline__ void alpha_store(const TGeom& G, const TAlphaArgs& aa, int64_t dom,
+                                            const AlphaLds& w, int lane) {
+  for (int l = 0; l < G.n; ++l) {
+    const int dW = G.d[l + 1];
+    const float* sa = w.sad + l * 3 * FW;
+    for (int j = lane; j < dW; j += 64) {
+      const int64_t ai = dom * dW + j;
+      aa.alpha[l][ai] = sa[j];
+      aa.m1[l][ai] = sa[FW + j];
+      aa.m2[l][ai] = sa[2 * FW + j];
+    }
+  }
+}
+
 template <int MT, int KS, bool BROW>
 __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
     TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
@@ -580,13 +913,8 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
   float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
-  const int n = G.n, d0 = G.d[0], dN = G.d[n];
-  const int wsz = n * 7 * FW + n * KS * 4 * Q + 3 * FW;
-  float* ssl = sbias + n * FW + wv * wsz;  // [l][ls_eff, us, ut, unstable][FW]
-  float* sad = ssl + n * 4 * FW;           // [l][alpha, m, v][FW]
-  float* sP = sad + n * 3 * FW;            // [l][ks][g][r < Q]
-  float* sga = sP + n * KS * 4 * Q;        // d lb / d alpha of one layer [FW]
-  float* sx = sga + FW;                    // the box: xl, xh [FW]
+  const int n = G.n;
+  const AlphaLds w = alpha_lds_at(sbias + n * FW + wv * alpha_wsz(n, KS, Q), n, KS, Q);
   vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
   for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
     const int l = k / FW, j = k % FW;
@@ -595,172 +923,13 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
   __syncthreads();
   const float* fr0 = sfrag;
   const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
-  const bool live = r < Q;
-
-  const float* dxl = sx;
-  const float* dxh = sx + FW;
   for (int64_t dom = (int64_t)blockIdx.x * ANW + wv; dom < B; dom += (int64_t)gridDim.x * ANW) {
-    sx[lane] = lane < d0 ? xl[dom * d0 + lane] : 0.f;
-    sx[FW + lane] = lane < d0 ? xh[dom * d0 + lane] : 0.f;
-#pragma unroll 4
-    for (int l = 0; l < n; ++l) {
-      const int dW = G.d[l + 1];
-      float* sl = ssl + l * 4 * FW;
-      float* sa = sad + l * 3 * FW;
-      for (int j = lane; j < FW; j += 64) {
-        float ls = 0.f, us = 0.f, ut = 0.f, un = 0.f, a = 0.f, m1 = 0.f, m2 = 0.f;
-        if (j < dW) {
-          const int64_t ai = dom * dW + j;
-          const Relax s = relax(aa.lo[l][ai], aa.hi[l][ai]);
-          if (init) {
-            // first iteration: alpha = (up_s > 0.5) * unstable, Adam state zero
-            a = (s.unstable && s.up_s > 0.5f) ? 1.f : 0.f;
-          } else {
-            a = aa.alpha[l][ai];
-            m1 = aa.m1[l][ai];
-            m2 = aa.m2[l][ai];
-          }
-          ls = s.active ? 1.f : (s.unstable ? a : 0.f);
-          us = s.up_s;
-          ut = s.up_t;
-          un = s.unstable ? 1.f : 0.f;
-        }
-        sl[j] = ls;
-        sl[FW + j] = us;
-        sl[2 * FW + j] = ut;
-        sl[3 * FW + j] = un;
-        sa[j] = a;
-        sa[FW + j] = m1;
-        sa[2 * FW + j] = m2;
-      }
-    }
+    alpha_load<KS>(G, aa, xl, xh, dom, init, w, lane);
     __threadfence_block();
-    // ---- spec backward with alpha, keeping P_l
-    v4f F[TNP][4];
-    double acc[TNP], cz[TNP];
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int k = 16 * t + 4 * g + i;
-        F[0][t][i] = (live && k < dN) ? spec_rows[r * dN + k] : 0.f;
-      }
-    acc[0] = (live && g == 0) ? (double)spec_acc[r] : 0.0;
-    cz[0] = 0.0;
-    for (int l = n - 1; l >= 0; --l) {
-      if (live) {
-        float* pl = sP + l * KS * 4 * Q;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) pl[(ks * 4 + g) * Q + r] = F[0][ks >> 2][ks & 3];
-      }
-      relax_rows<KS, 1, BROW>(ssl + l * 4 * FW, sbias + l * FW, g, F, acc);
-      if (l > 0) fc_hidden<MT, KS, 1, BROW>(frh + (l - 1) * KS * 64, lane, g, G.d[l], F, acc);
-    }
-    // ---- fc_0, concretization and gE_0 = W_0 gA + b_0, one input tile at a time
-    v4f GE[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) GE[mt] = v4f{0.f, 0.f, 0.f, 0.f};
-    for (int mt = 0; mt < G.mt0; ++mt) {
-      v4f o = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        o = mfma16x16x4(fr0[(mt * KS + ks) * 64 + swz(lane, ks)], F[0][ks >> 2][ks & 3], o);
-      float gA[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = 16 * mt + 4 * g + i;
-        const float v = o[i];
-        gA[i] = 0.f;
-        if (m < d0) {
-          const float xlv = dxl[m], xhv = dxh[m];
-          cz[0] += (double)(fmaxf(v, 0.f) * xlv);
-          cz[0] += (double)(fminf(v, 0.f) * xhv);
-          float gv = 0.f;
-          if (v >= 0.f) gv += xlv;
-          if (v <= 0.f) gv += xhv;
-          gA[i] = live ? gv : 0.f;
-        } else if (BROW && m == d0) {
-          acc[0] += (double)v;
-          gA[i] = live ? 1.f : 0.f;
-        }
-      }
-      // A_fwd0[m'][k'] = A_0[k'][m']: lane (g, r), M-tile mo, K-step (mt, i)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int mo = 0; mo < MT; ++mo) {
-          const int ksf = 4 * mo + (r & 3);
-          const float a = ksf < KS ? fr0[(mt * KS + ksf) * 64 + swz(16 * (r >> 2) + 4 * g + i, ksf)] : 0.f;
-          GE[mo] = mfma16x16x4(a, gA[i], GE[mo]);
-        }
-    }
-    {
-      const double lbd = group_sum4_d(acc[0] + cz[0]);
-      if (g == 0 && live) lb_out[dom * Q + r] = (float)lbd;
-    }
-    // ---- forward gradient sweep with the Adam update per layer
-    for (int l = 0; l < n; ++l) {
-      const int dW = G.d[l + 1];
-      const float* sl = ssl + l * 4 * FW;
-      if (!BROW) {
-        // bias of fc_l (l >= 0) added for live rows: gE_l += b_l
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            GE[t][i] = live ? GE[t][i] + sbias[l * FW + 16 * t + 4 * g + i] : 0.f;
-      }
-      const float* pl = sP + l * KS * 4 * Q;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int t = ks >> 2, i = ks & 3;
-        const int j = 16 * t + 4 * g + i;
-        const float pv = live ? pl[(ks * 4 + g) * Q + r] : 0.f;
-        const float ge = GE[t][i];
-        const float s = row_sum16(ge * fmaxf(pv, 0.f));
-        if (r == 0) sga[j] = s;
-        const bool mp = pv >= 0.f, mn = pv <= 0.f;
-        float gp = ge * ((mp ? sl[j] : 0.f) + (mn ? sl[FW + j] : 0.f));
-        if (mn) gp = gp + sl[2 * FW + j];
-        GE[t][i] = live ? gp : 0.f;
-      }
-      __threadfence_block();
-      {
-        float* sa = sad + l * 3 * FW;
-        const int j = lane;
-        if (j < dW && sl[3 * FW + j] != 0.f) {
-          float mi = sa[FW + j], vi = sa[2 * FW + j];
-          float pa = adam_update(sa[j], -sga[j], mi, vi, adam);
-          pa = fminf(fmaxf(pa, 0.f), 1.f);
-          sa[FW + j] = mi;
-          sa[2 * FW + j] = vi;
-          sa[j] = pa;
-        }
-      }
-      __threadfence_block();
-      if (l + 1 < n) {
-        // the rows at relu l's output (K of fc_{l+1}); with the bias row, a
-        // constant 1 at index d_{l+1} picks up b_{l+1}
-        if (BROW) set_elem<MT>(GE, dW, g, live ? 1.f : 0.f);
-        v4f xin[1][4], nx[1][4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) xin[0][mt] = GE[mt];
-        fc_forward<MT, KS, 1, 1>(frh + l * KS * 64, lane, g, r, xin, 0, nx);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) GE[mt] = nx[0][mt];
-      }
-    }
-    // write the updated Adam state back (coalesced)
-    for (int l = 0; l < n; ++l) {
-      const int dW = G.d[l + 1];
-      const float* sa = sad + l * 3 * FW;
-      for (int j = lane; j < dW; j += 64) {
-        const int64_t ai = dom * dW + j;
-        aa.alpha[l][ai] = sa[j];
-        aa.m1[l][ai] = sa[FW + j];
-        aa.m2[l][ai] = sa[2 * FW + j];
-      }
-    }
+    const double lbd = alpha_pass<MT, KS, BROW>(G, w, fr0, frh, sbias, Q, spec_rows, spec_acc,
+                                                adam, false, lane, g, r);
+    if (g == 0 && r < Q) lb_out[dom * Q + r] = (float)lbd;
+    alpha_store(G, aa, dom, w, lane);
     __threadfence_block();
   }
 }
@@ -1215,6 +1384,12 @@ const void* zono_wide_fn() {
 }
 
 template <int V>
+const void* crown_dom_fn() {
+  return reinterpret_cast<const void*>(
+      &k_crown_dom<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
+}
+
+template <int V>
 const void* crown_fn() {
   return reinterpret_cast<const void*>(
       &k_crown_tiled<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
@@ -1255,6 +1430,10 @@ extern "C" int vc_mlp_tiled_pack(const float* const* W, const float* const* bias
   return VC_OK;
 }
 
+extern "C" int vc_mlp_tiled_crown_mode(int64_t B) {
+  return B <= (int64_t)vcm::cu_count() * 4 ? 1 : 0;
+}
+
 extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* frag,
                                   const float* bias_cat, int64_t B, const float* xl,
                                   const float* xh, const float* const* lo_in,
@@ -1287,6 +1466,48 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
                       (size_t)TNW * (n_relu * 3 * FW + 7 * FW + MAXL)) *
                      sizeof(float);
   if (lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  // small batches: D domains per workgroup, the workgroup's wavefronts
+  // shared among them (every domain in flight at once)
+  const int cus = vcm::cu_count();
+  if (vc_mlp_tiled_crown_mode(B) == 1) {
+    const int D = (int)std::min<int64_t>(4, std::max<int64_t>(1, (B + cus - 1) / cus));
+    const size_t lds_d = ((size_t)G.nfloats + (size_t)n_relu * FW + (size_t)nmax +
+                          (size_t)D * (n_relu * 3 * FW + 7 * FW)) *
+                         sizeof(float);
+    const void* fd = nullptr;
+    switch (G.variant) {
+      case 0: fd = crown_dom_fn<0>(); break;
+      case 1: fd = crown_dom_fn<1>(); break;
+      case 2: fd = crown_dom_fn<2>(); break;
+      case 3: fd = crown_dom_fn<3>(); break;
+      case 4: fd = crown_dom_fn<4>(); break;
+      case 5: fd = crown_dom_fn<5>(); break;
+      default: return VC_ERR_UNSUPPORTED;
+    }
+    if (lds_d + 512 <= 160 * 1024 && vcm::allow_max_lds(fd)) {
+      const dim3 gd((unsigned)((B + D - 1) / D)), bd(TNW * 64);
+#define VC_TDOM_CASE(V)                                                                       \
+  case V:                                                                                     \
+    hipLaunchKernelGGL((k_crown_dom<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>), \
+                       gd, bd, lds_d, st, G, frag, bias_cat, B, xl, xh, ca, idx_all, idx_meta, \
+                       do_crown, per_domain, Q, spec_rows, spec_acc, lb_out, A_out, acc_out,   \
+                       reinterpret_cast<unsigned long long*>(seed_rows), D);                   \
+    break;
+      switch (G.variant) {
+        VC_TDOM_CASE(0)
+        VC_TDOM_CASE(1)
+        VC_TDOM_CASE(2)
+        VC_TDOM_CASE(3)
+        VC_TDOM_CASE(4)
+        VC_TDOM_CASE(5)
+        default: return VC_ERR_UNSUPPORTED;
+      }
+#undef VC_TDOM_CASE
+      VC_LAUNCH_CHECK();
+      return VC_OK;
+    }
+  }
   const void* fn = nullptr;
   switch (G.variant) {
     case 0: fn = crown_fn<0>(); break;
@@ -1299,7 +1520,6 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
   }
   if (!vcm::allow_max_lds(fn)) return VC_ERR_UNSUPPORTED;
   const dim3 grid(vcm::persistent_grid(B, lds, TNW)), block(TNW * 64);
-  hipStream_t st = (hipStream_t)stream;
 #define VC_TILED_CASE(V)                                                                     \
   case V:                                                                                    \
     hipLaunchKernelGGL((k_crown_tiled<kVariants[V].MT, kVariants[V].KS,                      \

@@ -74,6 +74,7 @@ SIGNATURES = {
                                 _P, _P, _P, _D, _D, _D, _D, _D, _I, _P, _P],
     'vc_mlp_tiled_alpha_run': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
                                _P, _P, _P, _P, _D, _D, _D, _D, _D, _I, _D, _P, _P],
+    'vc_mlp_tiled_crown_mode': [_L],
     'vc_unstable_union_layers': [_P, _P, _P, _I, _L, _P, _P],
     'vc_union_compact': [_P, _P, _I, _P, _P, _P],
     'vc_gather_rows_multi': [_P, _P, _P, _I, _P, _L, _P],
@@ -190,15 +191,16 @@ def timing_begin(names):
 
 
 def timing_end():
-    """Stop recording; returns {name: {'launches', 'seconds', 'flops'}}."""
+    """Stop recording; returns {name: {'launches', 'seconds', 'flops',
+    'per_launch': [(seconds, flops, args), ...]}}."""
     global _timing
     rec, _timing = _timing, None
     torch.cuda.synchronize()
     out = {}
     for n, lst in (rec or {}).items():
-        secs = sum(s.elapsed_time(e) for s, e, _ in lst) / 1e3
-        out[n] = {'launches': len(lst), 'seconds': secs,
-                  'flops': sum(f for _, _, f in lst)}
+        per = [(s.elapsed_time(e) / 1e3, f, a) for s, e, f, a in lst]
+        out[n] = {'launches': len(per), 'seconds': sum(p[0] for p in per),
+                  'flops': sum(p[1] for p in per), 'per_launch': per}
     return out
 
 
@@ -210,7 +212,7 @@ def call(name, *args):
         s.record()
         rc = getattr(lib, name)(*args)
         e.record()
-        _timing[name].append((s, e, _FLOPS.get(name, lambda a: 0.0)(args)))
+        _timing[name].append((s, e, _FLOPS.get(name, lambda a: 0.0)(args), args))
         check(rc, name)
         return
     check(getattr(lib, name)(*args), name)

@@ -22,9 +22,11 @@ PLAN_KEY = '_vc_amd_mlp_plan'
 # has an instantiation; switching this off runs vc_mlp_crown.
 TILED = True
 
-# When set to a device int64 tensor of MAX_L entries, the shape-specialised
-# CROWN kernel adds its seeded neurons per layer to it (work accounting).
+# When set to a zeroed device int64 tensor (calls, MAX_L), the k-th call of
+# the shape-specialised CROWN kernel adds its seeded neurons per layer to
+# row k (work accounting; SEED_ROW is the next row).
 SEED_COUNTER = None
+SEED_ROW = 0
 
 
 class MlpPlan:
@@ -342,10 +344,15 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False, per_domain=F
             A = torch.empty(B, Q, plan.dims[0], device=dev)
             acc = torch.empty(B, Q, device=dev)
     if tiled:
+        seeds = None
+        if SEED_COUNTER is not None:
+            global SEED_ROW
+            seeds = SEED_COUNTER[SEED_ROW]
+            SEED_ROW += 1
         call('vc_mlp_tiled_crown', plan.dims_p, plan.n, ptr(plan.tfrag), ptr(plan.bias_cat), B,
              ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
              1 if do_crown else 0, 1 if per_domain else 0, Q, ptr(S), ptr(acc0), ptr(lb),
-             ptr(A), ptr(acc), ptr(SEED_COUNTER), stream())
+             ptr(A), ptr(acc), ptr(seeds), stream())
     else:
         call('vc_mlp_crown', plan.dims_p, plan.n, ptr(plan.frag[0]), ptr(plan.bias_cat), B,
              ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
