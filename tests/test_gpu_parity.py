@@ -480,6 +480,33 @@ def test_alpha_crown_fused_matches_layerwise_every_iteration(gpu):
         vz.FUSED_MLP = old
 
 
+@pytest.mark.parametrize('n_iters', [1, 2, 20])
+def test_alpha_small_batch_kernel_matches_large_batch_kernel(gpu, n_iters):
+    """Up to 4 x CUs domains run the alpha iteration with a domain's work
+    spread over 4 wavefronts (own M-tiles, rows exchanged through LDS);
+    larger batches one wavefront per domain.  Without the early stops the
+    trajectories are per domain, so the first 600 of 3000 boxes bounded
+    alone must match their rows of the 3000-box run: after 1 and 2
+    iterations within the bound tolerance (the row constants are summed
+    in another order), after 20 within the Adam drift criterion."""
+    gg_c, gg_g, xl, xh = acas(gpu, 3000, seed=19, scale=4.0)
+    _, se_g, _ = spec_pair(5, gpu)
+    xl, xh = xl.to(gpu), xh.to(gpu)
+    big = vz._run_alpha_crown_inputsplit_batched(xl, xh, gg_g, se_g, gpu, F32,
+                                                 n_iters=n_iters, lr=0.1, early_stop_eps=-1.0)
+    small = vz._run_alpha_crown_inputsplit_batched(xl[:600].contiguous(), xh[:600].contiguous(),
+                                                   gg_g, se_g, gpu, F32, n_iters=n_iters,
+                                                   lr=0.1, early_stop_eps=-1.0)
+    assert not bool((big > 0).all())  # the all-positive stop did not cut the run
+    what = f'alpha 4-wave vs 1-wave kernel, {n_iters} it'
+    if n_iters == 1:
+        assert_bounds(small, big[:600], what, rtol=1e-5, atol=1e-6)
+    elif n_iters == 2:
+        assert_bounds(small, big[:600], what, rtol=1e-4, atol=1e-5)
+    else:
+        assert_adam_drift(small, big[:600], what)
+
+
 # ----------------------------------------------------------------- a11-a14
 def test_clip_parity_identical_inputs(gpu):
     g = torch.Generator().manual_seed(3)

@@ -934,6 +934,300 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
   }
 }
 
+// ------------------------------------------- alpha-CROWN, small batches
+// The iteration of k_alpha_tiled with every domain's work spread over MT
+// wavefronts (a "quad" for MT = 4): wavefront w owns the neurons of M-tile
+// w of every layer (16 w .. 16 w + 15).  It keeps their pre-relaxation
+// rows, relaxes them, runs only its output M-tile of each fc product (1 /
+// MT of the MFMAs), and does the gradient sweep and Adam update of its
+// neurons.  The relaxed rows (backward) and the gradient rows (forward)
+// are exchanged through LDS once per layer, double-buffered with one
+// workgroup barrier each.  A workgroup holds D domains.
+constexpr int AQD = 4;  // domains per workgroup at most
+
+__host__ __device__ inline int alpha_quad_floats(int n, int KS, int Q, int MT) {
+  // slopes [n][4][FW], Adam state [n][3][FW], P_l [n][KS][4][Q], d lb / d
+  // alpha [FW], box [2 FW], exchange [2][MT][4][Q][4], row sums [MT + 1][16]
+  // doubles
+  const int f = n * 7 * FW + n * KS * 4 * Q + 3 * FW + 2 * MT * 16 * Q + 2 * (MT + 1) * 16;
+  return (f + 3) & ~3;
+}
+
+template <int MT>
+__device__ __forceinline__ void quad_exchange(float* xbuf, int w, int g, int r, bool live, int Q,
+                                              const v4f& mine, v4f (&all)[4]) {
+  if (live)
+    *reinterpret_cast<float4*>(xbuf + ((w * 4 + g) * Q + r) * 4) =
+        make_float4(mine[0], mine[1], mine[2], mine[3]);
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (t < MT && live) {
+      const float4 v = *reinterpret_cast<const float4*>(xbuf + ((t * 4 + g) * Q + r) * 4);
+      all[t] = v4f{v.x, v.y, v.z, v.w};
+    } else {
+      all[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+}
+
+template <int MT, int KS, bool BROW>
+__global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
+    TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
+    const float* __restrict__ xl, const float* __restrict__ xh, TAlphaArgs aa, int Q,
+    const float* __restrict__ spec_rows, const float* __restrict__ spec_acc,
+    float* __restrict__ lb_out, AdamConst adam, int init, const float* __restrict__ ctl, int D) {
+  if (ctl && ctl[1] != 0.f) return;  // the loop has stopped (vc_alpha_control)
+  extern __shared__ float smem[];
+  float* sfrag = smem;
+  float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int qd = wid / MT, w = wid - qd * MT;  // domain slot, owned M-tile
+  const int g = lane >> 4, r = lane & 15;
+  const int n = G.n, d0 = G.d[0], dN = G.d[n];
+  const bool live = r < Q;
+  float* ssl = sbias + n * FW + qd * alpha_quad_floats(n, KS, Q, MT);  // [l][ls, us, ut, un][FW]
+  float* sad = ssl + n * 4 * FW;                                        // [l][alpha, m, v][FW]
+  float* sP = sad + n * 3 * FW;                                         // [l][ks][g][r < Q]
+  float* sga = sP + n * KS * 4 * Q;                                     // [FW]
+  float* sx = sga + FW;                                                 // xl, xh [FW]
+  float* xch = sx + 2 * FW;                                             // [2][MT][4][Q][4]
+  double* sacc = reinterpret_cast<double*>(xch + 2 * MT * 16 * Q);      // [MT + 1][16]
+  vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
+  for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
+    const int l = k / FW, j = k % FW;
+    sbias[k] = j < G.d[l + 1] ? gbias[G.boff[l] + j] : 0.f;
+  }
+  __syncthreads();
+  const float* fr0 = sfrag;
+  const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
+  const float* dxl = sx;
+  const float* dxh = sx + FW;
+
+  for (int64_t b0 = (int64_t)blockIdx.x * D; b0 < B; b0 += (int64_t)gridDim.x * D) {
+    const int64_t dom = b0 + qd;
+    const bool has = dom < B;
+    // ---- the box and the state of the owned neurons
+    if (has) {
+      if (w == 0) {
+        sx[lane] = lane < d0 ? xl[dom * d0 + lane] : 0.f;
+        sx[FW + lane] = lane < d0 ? xh[dom * d0 + lane] : 0.f;
+      }
+      for (int k = lane; k < n * 16; k += 64) {
+        const int l = k >> 4, j = 16 * w + (k & 15);
+        const int dW = G.d[l + 1];
+        float ls = 0.f, us = 0.f, ut = 0.f, un = 0.f, a = 0.f, m1 = 0.f, m2 = 0.f;
+        if (j < dW) {
+          const int64_t ai = dom * dW + j;
+          const Relax s = relax(aa.lo[l][ai], aa.hi[l][ai]);
+          if (init) {
+            a = (s.unstable && s.up_s > 0.5f) ? 1.f : 0.f;
+          } else {
+            a = aa.alpha[l][ai];
+            m1 = aa.m1[l][ai];
+            m2 = aa.m2[l][ai];
+          }
+          ls = s.active ? 1.f : (s.unstable ? a : 0.f);
+          us = s.up_s;
+          ut = s.up_t;
+          un = s.unstable ? 1.f : 0.f;
+        }
+        float* sl = ssl + l * 4 * FW;
+        float* sa = sad + l * 3 * FW;
+        sl[j] = ls;
+        sl[FW + j] = us;
+        sl[2 * FW + j] = ut;
+        sl[3 * FW + j] = un;
+        sa[j] = a;
+        sa[FW + j] = m1;
+        sa[2 * FW + j] = m2;
+      }
+    }
+    __syncthreads();
+    // ---- spec backward with alpha: the owned slice of the rows
+    v4f Fw;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = 16 * w + 4 * g + i;
+      Fw[i] = (has && live && k < dN) ? spec_rows[r * dN + k] : 0.f;
+    }
+    double acc = (has && live && g == 0 && w == 0) ? (double)spec_acc[r] : 0.0;
+    double cz = 0.0;
+    v4f GEw = v4f{0.f, 0.f, 0.f, 0.f};
+    int xb = 0;
+    for (int l = n - 1; l >= 0; --l) {
+      const float* sl = ssl + l * 4 * FW;
+      float* pl = sP + l * KS * 4 * Q;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ks = 4 * w + i;
+        if (ks < KS) {
+          if (has && live) pl[(ks * 4 + g) * Q + r] = Fw[i];
+          const int j = 16 * w + 4 * g + i;
+          const float ls = sl[j], us = sl[FW + j], ut = sl[2 * FW + j];
+          const float x = Fw[i];
+          const bool ng = x < 0.f;
+          const float e = x * (ng ? us : ls);
+          const float en = ng ? x : 0.f;
+          acc += (double)(en * ut);
+          if (!BROW) acc += (double)(e * sbias[l * FW + j]);
+          Fw[i] = e;
+        }
+      }
+      v4f F[4];
+      quad_exchange<MT>(xch + xb * MT * 16 * Q, w, g, r, has && live, Q, Fw, F);
+      xb ^= 1;
+      if (l > 0) {
+        // fc_l backward, the owned output M-tile
+        v4f o = v4f{0.f, 0.f, 0.f, 0.f};
+        const float* fa = reinterpret_cast<const float*>(frh + (l - 1) * KS * 64);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          o = mfma16x16x4(fa[(ks * 64 + swz(lane, ks)) * 4 + w], F[ks >> 2][ks & 3], o);
+        if (BROW) {
+          const int mb = G.d[l];
+          if ((mb >> 4) == w && g == ((mb & 15) >> 2)) acc += (double)o[mb & 3];
+        }
+        Fw = o;
+      } else {
+        // fc_0 and the concretization (every wavefront, identical), gA,
+        // and the owned slice of gE_0 = W_0 gA + b_0
+        for (int mt = 0; mt < G.mt0; ++mt) {
+          v4f o = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+            o = mfma16x16x4(fr0[(mt * KS + ks) * 64 + swz(lane, ks)], F[ks >> 2][ks & 3], o);
+          float gA[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int m = 16 * mt + 4 * g + i;
+            const float v = o[i];
+            gA[i] = 0.f;
+            if (m < d0) {
+              const float xlv = dxl[m], xhv = dxh[m];
+              cz += (double)(fmaxf(v, 0.f) * xlv);
+              cz += (double)(fminf(v, 0.f) * xhv);
+              float gv = 0.f;
+              if (v >= 0.f) gv += xlv;
+              if (v <= 0.f) gv += xhv;
+              gA[i] = live ? gv : 0.f;
+            } else if (BROW && m == d0) {
+              if (w == 0) acc += (double)v;
+              gA[i] = live ? 1.f : 0.f;
+            }
+          }
+          const int ksf = 4 * w + (r & 3);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float a =
+                ksf < KS ? fr0[(mt * KS + ksf) * 64 + swz(16 * (r >> 2) + 4 * g + i, ksf)] : 0.f;
+            GEw = mfma16x16x4(a, gA[i], GEw);
+          }
+        }
+      }
+    }
+    // ---- lb: the wavefronts' row constants and the concretization, summed
+    // in a fixed order
+    {
+      const double a = group_sum4_d(acc);
+      const double c = group_sum4_d(cz);
+      if (g == 0) {
+        sacc[w * 16 + r] = a;
+        if (w == 0) sacc[MT * 16 + r] = c;
+      }
+    }
+    __syncthreads();
+    if (has && w == 0 && g == 0 && live) {
+      double t = 0.0;
+#pragma unroll
+      for (int u = 0; u < MT; ++u) t += sacc[u * 16 + r];
+      lb_out[dom * Q + r] = (float)(t + sacc[MT * 16 + r]);
+    }
+    // ---- forward gradient sweep with the Adam update, owned neurons
+    for (int l = 0; l < n; ++l) {
+      const int dW = G.d[l + 1];
+      float* sl = ssl + l * 4 * FW;
+      if (!BROW) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          GEw[i] = live ? GEw[i] + sbias[l * FW + 16 * w + 4 * g + i] : 0.f;
+      }
+      const float* pl = sP + l * KS * 4 * Q;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ks = 4 * w + i;
+        if (ks < KS) {
+          const int j = 16 * w + 4 * g + i;
+          const float pv = (has && live) ? pl[(ks * 4 + g) * Q + r] : 0.f;
+          const float ge = GEw[i];
+          const float s = row_sum16(ge * fmaxf(pv, 0.f));
+          if (r == 0) sga[j] = s;
+          const bool mp = pv >= 0.f, mn = pv <= 0.f;
+          float gp = ge * ((mp ? sl[j] : 0.f) + (mn ? sl[FW + j] : 0.f));
+          if (mn) gp = gp + sl[2 * FW + j];
+          GEw[i] = live ? gp : 0.f;
+        }
+      }
+      __threadfence_block();
+      if (has && lane < 16) {
+        float* sa = sad + l * 3 * FW;
+        const int j = 16 * w + lane;
+        if (j < dW && sl[3 * FW + j] != 0.f) {
+          float mi = sa[FW + j], vi = sa[2 * FW + j];
+          float pa = adam_update(sa[j], -sga[j], mi, vi, adam);
+          pa = fminf(fmaxf(pa, 0.f), 1.f);
+          sa[FW + j] = mi;
+          sa[2 * FW + j] = vi;
+          sa[j] = pa;
+        }
+      }
+      if (l + 1 < n) {
+        // with the bias row, a constant 1 at index d_{l+1} picks up b_{l+1}
+        if (BROW && (dW >> 4) == w && g == ((dW & 15) >> 2)) GEw[dW & 3] = live ? 1.f : 0.f;
+        v4f X[4];
+        quad_exchange<MT>(xch + xb * MT * 16 * Q, w, g, r, has && live, Q, GEw, X);
+        xb ^= 1;
+        // fc_{l+1} forward, the owned output M-tile (fragments read
+        // transposed: K-step 4 w + r % 4, slot 16 (r / 4) + 4 g + i)
+        const float4* fr = frh + l * KS * 64;
+        const int ksf = 4 * w + (r & 3);
+        v4f o = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 q4 = ksf < KS ? fr[ksf * 64 + swz(16 * (r >> 2) + 4 * g + i, ksf)]
+                                     : float4{0.f, 0.f, 0.f, 0.f};
+          const float a[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+          for (int t = 0; t < MT; ++t) o = mfma16x16x4(a[t], X[t][i], o);
+        }
+        GEw = o;
+      }
+    }
+    // ---- the owned neurons' Adam state back (the wave's own LDS writes)
+    __threadfence_block();
+    if (has) {
+      for (int k = lane; k < n * 16; k += 64) {
+        const int l = k >> 4, j = 16 * w + (k & 15);
+        const int dW = G.d[l + 1];
+        if (j < dW) {
+          const float* sa = sad + l * 3 * FW;
+          const int64_t ai = dom * dW + j;
+          aa.alpha[l][ai] = sa[j];
+          aa.m1[l][ai] = sa[FW + j];
+          aa.m2[l][ai] = sa[2 * FW + j];
+        }
+      }
+    }
+    __syncthreads();  // the slot's LDS is rewritten by the next domain
+  }
+}
+
+template <int V>
+const void* alpha_quad_fn() {
+  return reinterpret_cast<const void*>(
+      &k_alpha_quad<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
+}
+
 template <int V>
 const void* alpha_fn() {
   return reinterpret_cast<const void*>(
@@ -1571,6 +1865,50 @@ extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const fl
       return VC_ERR_ARG;
   }
   const size_t wsz = (size_t)n_relu * 7 * FW + (size_t)n_relu * G.KS * 4 * Q + 3 * FW;
+  hipStream_t st = (hipStream_t)stream;
+  const AdamConst adam = adam_const(b1, b2, eps, step_size, bc2_sqrt);
+  {
+    // small batches: every domain in flight at once, MT wavefronts each
+    const int cus = vcm::cu_count();
+    const size_t fixed = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float);
+    const size_t per = (size_t)alpha_quad_floats(n_relu, G.KS, Q, G.MT) * sizeof(float);
+    const int fit = fixed + per <= 160 * 1024 ? (int)((160 * 1024 - fixed) / per) : 0;
+    const int D = (int)std::min<int64_t>(std::min(AQD, fit), (B + cus - 1) / cus);
+    if (B <= (int64_t)cus * AQD && D >= 1) {
+      const void* fq = nullptr;
+      switch (G.variant) {
+        case 0: fq = alpha_quad_fn<0>(); break;
+        case 1: fq = alpha_quad_fn<1>(); break;
+        case 2: fq = alpha_quad_fn<2>(); break;
+        case 3: fq = alpha_quad_fn<3>(); break;
+        case 4: fq = alpha_quad_fn<4>(); break;
+        case 5: fq = alpha_quad_fn<5>(); break;
+        default: return VC_ERR_UNSUPPORTED;
+      }
+      if (vcm::allow_max_lds(fq)) {
+        const size_t lds_q = fixed + (size_t)D * per;
+        const dim3 gq((unsigned)((B + D - 1) / D)), bq((unsigned)(D * G.MT * 64));
+#define VC_TQUAD_CASE(V)                                                                        \
+  case V:                                                                                       \
+    hipLaunchKernelGGL((k_alpha_quad<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>), \
+                       gq, bq, lds_q, st, G, frag, bias_cat, B, xl, xh, aa, Q, spec_rows,       \
+                       spec_acc, lb_out, adam, init, ctl, D);                                   \
+    break;
+        switch (G.variant) {
+          VC_TQUAD_CASE(0)
+          VC_TQUAD_CASE(1)
+          VC_TQUAD_CASE(2)
+          VC_TQUAD_CASE(3)
+          VC_TQUAD_CASE(4)
+          VC_TQUAD_CASE(5)
+          default: return VC_ERR_UNSUPPORTED;
+        }
+#undef VC_TQUAD_CASE
+        VC_LAUNCH_CHECK();
+        return VC_OK;
+      }
+    }
+  }
   const size_t lds = ((size_t)G.nfloats + (size_t)n_relu * FW + ANW * wsz) * sizeof(float);
   if (lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
   const void* fn = nullptr;
@@ -1585,8 +1923,6 @@ extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const fl
   }
   if (!vcm::allow_max_lds(fn)) return VC_ERR_UNSUPPORTED;
   const dim3 grid(vcm::persistent_grid(B, lds, ANW)), block(ANW * 64);
-  const AdamConst adam = adam_const(b1, b2, eps, step_size, bc2_sqrt);
-  hipStream_t st = (hipStream_t)stream;
 #define VC_TALPHA_CASE(V)                                                                    \
   case V:                                                                                    \
     hipLaunchKernelGGL((k_alpha_tiled<kVariants[V].MT, kVariants[V].KS,                      \
