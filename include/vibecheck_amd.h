@@ -273,9 +273,11 @@ int vc_best_update(float *best, const float *lb, int64_t n, int init,
  * iteration.  ctl (4 floats, start {-inf, 0, 0, 0}) = {previous max,
  * stopped, evaluated iterations, this max}; once stopped, later calls do
  * nothing, and vc_mlp_tiled_alpha_iter given ctl skips its work.
+ * stop_host (nullable, pinned host memory): set to 1 when the loop stops,
+ * a hint for the host thread that enqueues the iterations.
  * Replaces verify_zono_bnb.py:5252-5287 (best, the two breaks, prev_max). */
 int vc_alpha_control(float *best, const float *lb, int64_t n, int it,
-                     double eps, float *ctl, vc_stream_t stream);
+                     double eps, float *ctl, int32_t *stop_host, vc_stream_t stream);
 
 /* ---- Whole-network kernels for narrow fc/ReLU chains ------------------- */
 /* dims (host array, n_relu + 1 entries): dims[0] = inputs, dims[l + 1] =
@@ -480,7 +482,9 @@ int vc_mlp_tiled_alpha_iter(const int32_t *dims, int n_relu, const float *frag,
  * here and ends as vc_alpha_control leaves it (ctl[2] = evaluated
  * iterations); best (B, Q) = the best bound per spec row.  Torch Adam's
  * schedule: step size lr_t / (1 - b1^t), bias correction (1 - b2^t)^0.5,
- * lr_{t+1} = lr_t * lr_decay. */
+ * lr_{t+1} = lr_t * lr_decay.  stop_host (nullable, pinned host memory,
+ * zero on entry): vc_alpha_control sets it when the loop stops, and the
+ * iterations not yet enqueued then are skipped (they would do nothing). */
 int vc_mlp_tiled_alpha_run(const int32_t *dims, int n_relu, const float *frag,
                            const float *bias_cat, int64_t B, const float *xl,
                            const float *xh, const float *const *lo,
@@ -489,7 +493,8 @@ int vc_mlp_tiled_alpha_run(const int32_t *dims, int n_relu, const float *frag,
                            const float *spec_rows, const float *spec_acc,
                            float *lb_out, float *best, double b1, double b2,
                            double eps, double lr, double lr_decay, int n_iters,
-                           double early_stop_eps, float *ctl, vc_stream_t stream);
+                           double early_stop_eps, float *ctl, int32_t *stop_host,
+                           vc_stream_t stream);
 
 /* ---- Input-split BaB step ---------------------------------------------- */
 

@@ -320,7 +320,7 @@ __global__ void k_split_clamps(const int64_t* layer, const int64_t* neuron, cons
 // best bound, stopped flag, evaluated iterations, this iteration's max}.
 // Once stopped, later calls (and the fused alpha kernel) do nothing.
 __global__ void k_alpha_control(float* best, const float* lb, int64_t n, int it, double eps,
-                                float* ctl) {
+                                float* ctl, int32_t* stop_host) {
   __shared__ float smax[16];
   __shared__ int sneg[16];
   if (ctl[1] != 0.f) return;
@@ -358,6 +358,8 @@ __global__ void k_alpha_control(float* best, const float* lb, int64_t n, int it,
     ctl[1] = stop ? 1.f : 0.f;
     ctl[2] = (float)(it + 1);
     ctl[3] = a;
+    // a hint for the launching host thread (pinned host memory)
+    if (stop && stop_host) __hip_atomic_store(stop_host, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
@@ -904,10 +906,10 @@ extern "C" int vc_best_update(float* best, const float* lb, int64_t n, int init,
 }
 
 extern "C" int vc_alpha_control(float* best, const float* lb, int64_t n, int it, double eps,
-                                float* ctl, vc_stream_t stream) {
+                                float* ctl, int32_t* stop_host, vc_stream_t stream) {
   if (!best || !lb || !ctl || n <= 0 || it < 0) return VC_ERR_ARG;
   hipLaunchKernelGGL(k_alpha_control, dim3(1), dim3(1024), 0, (hipStream_t)stream, best, lb, n,
-                     it, eps, ctl);
+                     it, eps, ctl, stop_host);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }

@@ -1836,6 +1836,103 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
   return VC_OK;
 }
 
+namespace {
+// One alpha-CROWN iteration's launch, prepared once per batch: the kernel
+// (4 wavefronts per domain for batches that fit at once, else one), its
+// shape and the per-layer pointers.
+struct AlphaLaunch {
+  TGeom G;
+  TAlphaArgs aa;
+  const void* fn;
+  int quad, D;
+  dim3 grid, block;
+  size_t lds;
+};
+
+int alpha_prepare(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+                  int64_t B, const float* xl, const float* xh, const float* const* lo,
+                  const float* const* hi, float* const* alpha, float* const* exp_avg,
+                  float* const* exp_avg_sq, int Q, const float* spec_rows,
+                  const float* spec_acc, const float* lb_out, AlphaLaunch& L) {
+  TGeom& G = L.G;
+  int rc = tiled_geom(dims, n_relu, G);
+  if (rc != VC_OK) return rc;
+  if (Q < 1 || Q > 16) return VC_ERR_UNSUPPORTED;
+  if (!frag || !bias_cat || !xl || !xh || !lo || !hi || !alpha || !exp_avg || !exp_avg_sq ||
+      !spec_rows || !spec_acc || !lb_out || B < 0)
+    return VC_ERR_ARG;
+  for (int l = 0; l < MAXL; ++l) {
+    const bool in = l < n_relu;
+    L.aa.lo[l] = in ? lo[l] : nullptr;
+    L.aa.hi[l] = in ? hi[l] : nullptr;
+    L.aa.alpha[l] = in ? alpha[l] : nullptr;
+    L.aa.m1[l] = in ? exp_avg[l] : nullptr;
+    L.aa.m2[l] = in ? exp_avg_sq[l] : nullptr;
+    if (in && (!L.aa.lo[l] || !L.aa.hi[l] || !L.aa.alpha[l] || !L.aa.m1[l] || !L.aa.m2[l]))
+      return VC_ERR_ARG;
+  }
+  const size_t fixed = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float);
+  // small batches: every domain in flight at once, MT wavefronts each
+  const int cus = vcm::cu_count();
+  const size_t per = (size_t)alpha_quad_floats(n_relu, G.KS, Q, G.MT) * sizeof(float);
+  const int fit = fixed + per <= 160 * 1024 ? (int)((160 * 1024 - fixed) / per) : 0;
+  const int D = (int)std::min<int64_t>(std::min(AQD, fit), (B + cus - 1) / cus);
+  L.quad = 0;
+  if (B >= 1 && B <= (int64_t)cus * AQD && D >= 1) {
+    const void* fq = nullptr;
+    switch (G.variant) {
+      case 0: fq = alpha_quad_fn<0>(); break;
+      case 1: fq = alpha_quad_fn<1>(); break;
+      case 2: fq = alpha_quad_fn<2>(); break;
+      case 3: fq = alpha_quad_fn<3>(); break;
+      case 4: fq = alpha_quad_fn<4>(); break;
+      case 5: fq = alpha_quad_fn<5>(); break;
+      default: return VC_ERR_UNSUPPORTED;
+    }
+    if (vcm::allow_max_lds(fq)) {
+      L.fn = fq;
+      L.quad = 1;
+      L.D = D;
+      L.lds = fixed + (size_t)D * per;
+      L.grid = dim3((unsigned)((B + D - 1) / D));
+      L.block = dim3((unsigned)(D * G.MT * 64));
+      return VC_OK;
+    }
+  }
+  const size_t wsz = (size_t)alpha_wsz(n_relu, G.KS, Q);
+  L.lds = fixed + ANW * wsz * sizeof(float);
+  if (L.lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
+  switch (G.variant) {
+    case 0: L.fn = alpha_fn<0>(); break;
+    case 1: L.fn = alpha_fn<1>(); break;
+    case 2: L.fn = alpha_fn<2>(); break;
+    case 3: L.fn = alpha_fn<3>(); break;
+    case 4: L.fn = alpha_fn<4>(); break;
+    case 5: L.fn = alpha_fn<5>(); break;
+    default: return VC_ERR_UNSUPPORTED;
+  }
+  if (!vcm::allow_max_lds(L.fn)) return VC_ERR_UNSUPPORTED;
+  L.D = 1;
+  L.grid = dim3(vcm::persistent_grid(B, L.lds, ANW));
+  L.block = dim3(ANW * 64);
+  return VC_OK;
+}
+
+int alpha_launch(const AlphaLaunch& L, const float* frag, const float* bias_cat, int64_t B,
+                 const float* xl, const float* xh, int Q, const float* spec_rows,
+                 const float* spec_acc, float* lb_out, AdamConst adam, int init,
+                 const float* ctl, hipStream_t st) {
+  TGeom G = L.G;
+  TAlphaArgs aa = L.aa;
+  int D = L.D;
+  void* args[] = {&G,  (void*)&frag,      (void*)&bias_cat, &B,     (void*)&xl,
+                  (void*)&xh, &aa,         &Q,               (void*)&spec_rows,
+                  (void*)&spec_acc, (void*)&lb_out, &adam, &init, (void*)&ctl, &D};
+  if (hipLaunchKernel(L.fn, L.grid, L.block, args, L.lds, st) != hipSuccess) return VC_ERR_LAUNCH;
+  return VC_OK;
+}
+}  // namespace
+
 extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const float* frag,
                                        const float* bias_cat, int64_t B, const float* xl,
                                        const float* xh, const float* const* lo,
@@ -1845,103 +1942,14 @@ extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const fl
                                        float* lb_out, double b1, double b2, double eps,
                                        double step_size, double bc2_sqrt, int init,
                                        const float* ctl, vc_stream_t stream) {
-  TGeom G;
-  int rc = tiled_geom(dims, n_relu, G);
+  AlphaLaunch L;
+  int rc = alpha_prepare(dims, n_relu, frag, bias_cat, B, xl, xh, lo, hi, alpha, exp_avg,
+                         exp_avg_sq, Q, spec_rows, spec_acc, lb_out, L);
   if (rc != VC_OK) return rc;
-  if (Q < 1 || Q > 16) return VC_ERR_UNSUPPORTED;
-  if (!frag || !bias_cat || !xl || !xh || !lo || !hi || !alpha || !exp_avg || !exp_avg_sq ||
-      !spec_rows || !spec_acc || !lb_out || B < 0)
-    return VC_ERR_ARG;
   if (B == 0) return VC_OK;
-  TAlphaArgs aa;
-  for (int l = 0; l < MAXL; ++l) {
-    const bool in = l < n_relu;
-    aa.lo[l] = in ? lo[l] : nullptr;
-    aa.hi[l] = in ? hi[l] : nullptr;
-    aa.alpha[l] = in ? alpha[l] : nullptr;
-    aa.m1[l] = in ? exp_avg[l] : nullptr;
-    aa.m2[l] = in ? exp_avg_sq[l] : nullptr;
-    if (in && (!aa.lo[l] || !aa.hi[l] || !aa.alpha[l] || !aa.m1[l] || !aa.m2[l]))
-      return VC_ERR_ARG;
-  }
-  const size_t wsz = (size_t)n_relu * 7 * FW + (size_t)n_relu * G.KS * 4 * Q + 3 * FW;
-  hipStream_t st = (hipStream_t)stream;
-  const AdamConst adam = adam_const(b1, b2, eps, step_size, bc2_sqrt);
-  {
-    // small batches: every domain in flight at once, MT wavefronts each
-    const int cus = vcm::cu_count();
-    const size_t fixed = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float);
-    const size_t per = (size_t)alpha_quad_floats(n_relu, G.KS, Q, G.MT) * sizeof(float);
-    const int fit = fixed + per <= 160 * 1024 ? (int)((160 * 1024 - fixed) / per) : 0;
-    const int D = (int)std::min<int64_t>(std::min(AQD, fit), (B + cus - 1) / cus);
-    if (B <= (int64_t)cus * AQD && D >= 1) {
-      const void* fq = nullptr;
-      switch (G.variant) {
-        case 0: fq = alpha_quad_fn<0>(); break;
-        case 1: fq = alpha_quad_fn<1>(); break;
-        case 2: fq = alpha_quad_fn<2>(); break;
-        case 3: fq = alpha_quad_fn<3>(); break;
-        case 4: fq = alpha_quad_fn<4>(); break;
-        case 5: fq = alpha_quad_fn<5>(); break;
-        default: return VC_ERR_UNSUPPORTED;
-      }
-      if (vcm::allow_max_lds(fq)) {
-        const size_t lds_q = fixed + (size_t)D * per;
-        const dim3 gq((unsigned)((B + D - 1) / D)), bq((unsigned)(D * G.MT * 64));
-#define VC_TQUAD_CASE(V)                                                                        \
-  case V:                                                                                       \
-    hipLaunchKernelGGL((k_alpha_quad<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>), \
-                       gq, bq, lds_q, st, G, frag, bias_cat, B, xl, xh, aa, Q, spec_rows,       \
-                       spec_acc, lb_out, adam, init, ctl, D);                                   \
-    break;
-        switch (G.variant) {
-          VC_TQUAD_CASE(0)
-          VC_TQUAD_CASE(1)
-          VC_TQUAD_CASE(2)
-          VC_TQUAD_CASE(3)
-          VC_TQUAD_CASE(4)
-          VC_TQUAD_CASE(5)
-          default: return VC_ERR_UNSUPPORTED;
-        }
-#undef VC_TQUAD_CASE
-        VC_LAUNCH_CHECK();
-        return VC_OK;
-      }
-    }
-  }
-  const size_t lds = ((size_t)G.nfloats + (size_t)n_relu * FW + ANW * wsz) * sizeof(float);
-  if (lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
-  const void* fn = nullptr;
-  switch (G.variant) {
-    case 0: fn = alpha_fn<0>(); break;
-    case 1: fn = alpha_fn<1>(); break;
-    case 2: fn = alpha_fn<2>(); break;
-    case 3: fn = alpha_fn<3>(); break;
-    case 4: fn = alpha_fn<4>(); break;
-    case 5: fn = alpha_fn<5>(); break;
-    default: return VC_ERR_UNSUPPORTED;
-  }
-  if (!vcm::allow_max_lds(fn)) return VC_ERR_UNSUPPORTED;
-  const dim3 grid(vcm::persistent_grid(B, lds, ANW)), block(ANW * 64);
-#define VC_TALPHA_CASE(V)                                                                    \
-  case V:                                                                                    \
-    hipLaunchKernelGGL((k_alpha_tiled<kVariants[V].MT, kVariants[V].KS,                      \
-                                      kVariants[V].brow != 0>),                              \
-                       grid, block, lds, st, G, frag, bias_cat, B, xl, xh, aa, Q, spec_rows, \
-                       spec_acc, lb_out, adam, init, ctl);                                   \
-    break;
-  switch (G.variant) {
-    VC_TALPHA_CASE(0)
-    VC_TALPHA_CASE(1)
-    VC_TALPHA_CASE(2)
-    VC_TALPHA_CASE(3)
-    VC_TALPHA_CASE(4)
-    VC_TALPHA_CASE(5)
-    default: return VC_ERR_UNSUPPORTED;
-  }
-#undef VC_TALPHA_CASE
-  VC_LAUNCH_CHECK();
-  return VC_OK;
+  return alpha_launch(L, frag, bias_cat, B, xl, xh, Q, spec_rows, spec_acc, lb_out,
+                      adam_const(b1, b2, eps, step_size, bc2_sqrt), init, ctl,
+                      (hipStream_t)stream);
 }
 
 namespace {
@@ -1963,24 +1971,34 @@ extern "C" int vc_mlp_tiled_alpha_run(const int32_t* dims, int n_relu, const flo
                                       const float* spec_rows, const float* spec_acc,
                                       float* lb_out, float* best, double b1, double b2,
                                       double eps, double lr, double lr_decay, int n_iters,
-                                      double early_stop_eps, float* ctl, vc_stream_t stream) {
+                                      double early_stop_eps, float* ctl, int32_t* stop_host,
+                                      vc_stream_t stream) {
   if (!best || !ctl || n_iters < 1) return VC_ERR_ARG;
   if (B < 0) return VC_ERR_ARG;
+  AlphaLaunch L;
+  int rc = alpha_prepare(dims, n_relu, frag, bias_cat, B, xl, xh, lo, hi, alpha, exp_avg,
+                         exp_avg_sq, Q, spec_rows, spec_acc, lb_out, L);
+  if (rc != VC_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(k_alpha_ctl_init, dim3(1), dim3(64), 0, st, ctl);
   VC_LAUNCH_CHECK();
   if (B == 0) return VC_OK;
   // the schedule of torch Adam under the reference's loop: step sizes
-  // lr_t / (1 - b1^t) and (1 - b2^t)^0.5, lr decayed after every iteration
+  // lr_t / (1 - b1^t) and (1 - b2^t)^0.5, lr decayed after every iteration.
+  // Once the device has stopped (and said so in *stop_host), the remaining
+  // iterations, which would do nothing, are not enqueued.
+  volatile int32_t* sh = stop_host;
   double cur_lr = lr;
   for (int it = 0; it < n_iters; ++it) {
+    if (sh && *sh != 0) break;
     const double step = (double)(it + 1);
-    int rc = vc_mlp_tiled_alpha_iter(dims, n_relu, frag, bias_cat, B, xl, xh, lo, hi, alpha,
-                                     exp_avg, exp_avg_sq, Q, spec_rows, spec_acc, lb_out, b1, b2,
-                                     eps, cur_lr / (1.0 - pow(b1, step)),
-                                     pow(1.0 - pow(b2, step), 0.5), it == 0 ? 1 : 0, ctl, stream);
+    rc = alpha_launch(L, frag, bias_cat, B, xl, xh, Q, spec_rows, spec_acc, lb_out,
+                      adam_const(b1, b2, eps, cur_lr / (1.0 - pow(b1, step)),
+                                 pow(1.0 - pow(b2, step), 0.5)),
+                      it == 0 ? 1 : 0, ctl, st);
     if (rc != VC_OK) return rc;
-    rc = vc_alpha_control(best, lb_out, B * (int64_t)Q, it, early_stop_eps, ctl, stream);
+    rc = vc_alpha_control(best, lb_out, B * (int64_t)Q, it, early_stop_eps, ctl, stop_host,
+                          stream);
     if (rc != VC_OK) return rc;
     cur_lr *= lr_decay;
   }

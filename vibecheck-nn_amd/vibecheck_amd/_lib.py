@@ -73,12 +73,12 @@ SIGNATURES = {
     'vc_mlp_tiled_alpha_iter': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
                                 _P, _P, _P, _D, _D, _D, _D, _D, _I, _P, _P],
     'vc_mlp_tiled_alpha_run': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
-                               _P, _P, _P, _P, _D, _D, _D, _D, _D, _I, _D, _P, _P],
+                               _P, _P, _P, _P, _D, _D, _D, _D, _D, _I, _D, _P, _P, _P],
     'vc_mlp_tiled_crown_mode': [_L],
     'vc_unstable_union_layers': [_P, _P, _P, _I, _L, _P, _P],
     'vc_union_compact': [_P, _P, _I, _P, _P, _P],
     'vc_gather_rows_multi': [_P, _P, _P, _I, _P, _L, _P],
-    'vc_alpha_control': [_P, _P, _L, _I, _D, _P, _P],
+    'vc_alpha_control': [_P, _P, _L, _I, _D, _P, _P, _P],
     'vc_mlp_tiled_zono_bounds': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P],
     'vc_mlp_zono_wide': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P],
     'vc_mlp_tiled_zono_wide': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P],

@@ -219,6 +219,19 @@ def alpha_supported(plan, Q):
     return _tiled(plan) or plan.n <= ALPHA_MAX_L
 
 
+_STOP_WORD = None
+
+
+def _stop_word():
+    """A pinned host int32 the alpha loop's control kernel sets when the loop
+    stops, so that the host stops enqueueing iterations (one per process;
+    each alpha loop ends with a host read, so it is free again)."""
+    global _STOP_WORD
+    if _STOP_WORD is None:
+        _STOP_WORD = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    return _STOP_WORD
+
+
 def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps):
     """Batched alpha-CROWN with the reference's schedule
     (verify_zono_bnb.py:5137-5288), one fused kernel launch per Adam
@@ -267,10 +280,12 @@ def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps)
         if n_iters < 1:
             raise ValueError('alpha_crown: n_iters must be >= 1')
         ctl = torch.empty(4, device=dev)
+        stop = _stop_word()
+        stop[0] = 0
         call('vc_mlp_tiled_alpha_run', plan.dims_p, plan.n, ptr(plan.tfrag),
              ptr(plan.bias_cat), B, ptr(xl), ptr(xh), *ptrs, Q, ptr(S), ptr(acc0), ptr(lb),
              ptr(best), b1, b2, eps, cur_lr, float(lr_decay), int(n_iters),
-             float(early_stop_eps), ptr(ctl), st)
+             float(early_stop_eps), ptr(ctl), stop.data_ptr(), st)
         return best, int(ctl[2].item())
     name, frag = 'vc_mlp_alpha_iter', plan.frag[0]
     for it in range(n_iters):
