@@ -244,4 +244,5 @@ def f32(t):
 
 
 def stream():
-    return torch.cuda.current_stream().cuda_stream
+    """The current HIP stream of the current device (raw handle)."""
+    return torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice())

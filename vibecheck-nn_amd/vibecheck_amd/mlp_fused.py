@@ -232,7 +232,7 @@ def _stop_word():
     return _STOP_WORD
 
 
-def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps):
+def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps, lazy=False):
     """Batched alpha-CROWN with the reference's schedule
     (verify_zono_bnb.py:5137-5288), one fused kernel launch per Adam
     iteration.  Returns (best (B, Q), evaluated iterations)."""
@@ -244,26 +244,25 @@ def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps)
     lo = [sb[L][0].contiguous() for L in range(plan.n)]
     hi = [sb[L][1].contiguous() for L in range(plan.n)]
     tiled = _tiled(plan)
-    # one allocation for alpha and the Adam state of every layer
+    # one allocation for alpha and the Adam state of every layer: per layer
+    # pointers into it (alpha block, then m, then v)
     sizes = [t.numel() for t in lo]
-    flat = torch.empty(3 * sum(sizes), device=dev)
-    views, off = [], 0
-    for _ in range(3):
-        row = []
-        for t, sz in zip(lo, sizes):
-            row.append(flat[off:off + sz].view(t.shape))
-            off += sz
-        views.append(row)
-    alpha, m1, m2 = views
+    tot = sum(sizes)
+    flat = torch.empty(3 * tot, device=dev)
+    offs = [0]
+    for sz in sizes[:-1]:
+        offs.append(offs[-1] + sz)
+    base = flat.data_ptr()
+    state = [[base + 4 * (k * tot + o) for o in offs] for k in range(3)]
     if not tiled:
         # the tiled kernel initialises alpha and the Adam state itself
-        flat[sum(sizes):].zero_()
+        flat[tot:].zero_()
         for L in range(plan.n):
-            call('vc_alpha_init', ptr(lo[L]), ptr(hi[L]), lo[L].numel(), ptr(alpha[L]), st)
+            call('vc_alpha_init', ptr(lo[L]), ptr(hi[L]), sizes[L], state[0][L], st)
     keep = []
     ptrs = []
-    for lst in (lo, hi, alpha, m1, m2):
-        a, p = host_array(ctypes.c_void_p, [ptr(t) for t in lst])
+    for lst in ([ptr(t) for t in lo], [ptr(t) for t in hi], *state):
+        a, p = host_array(ctypes.c_void_p, lst)
         keep.append(a)
         ptrs.append(p)
     lb = torch.empty(B, Q, device=dev)
@@ -286,6 +285,18 @@ def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps)
              ptr(plan.bias_cat), B, ptr(xl), ptr(xh), *ptrs, Q, ptr(S), ptr(acc0), ptr(lb),
              ptr(best), b1, b2, eps, cur_lr, float(lr_decay), int(n_iters),
              float(early_stop_eps), ptr(ctl), stop.data_ptr(), st)
+        if lazy:
+            # the count travels to pinned memory in stream order; reading it
+            # after any later host synchronisation costs nothing
+            host = torch.empty(1, dtype=torch.float32, pin_memory=True)
+            host.copy_(ctl[2:3], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+
+            def n_eval():
+                ev.synchronize()
+                return int(host[0])
+            return best, n_eval
         return best, int(ctl[2].item())
     name, frag = 'vc_mlp_alpha_iter', plan.frag[0]
     for it in range(n_iters):

@@ -47,16 +47,18 @@ class DisjunctTable:
         self.n = len(self.groups)
 
 
-def _compact_device(flags, select_zero=False):
+def _compact_device(flags, select_zero=False, cnt=None):
     """Ascending positions of the set (or clear) flags and their count, both
-    left on the device: idx (max(n, 1),) int64 valid up to cnt, cnt (1,)."""
+    left on the device: idx (max(n, 1),) int64 valid up to cnt, cnt (1,)
+    (or the given one-element int64 slot)."""
     n = flags.numel()
     dev = flags.device
     lib = _lib.load()
     ws_bytes = int(lib.vc_compact_workspace(n))
     ws = torch.empty(max(ws_bytes, 8), dtype=torch.uint8, device=dev)
     idx = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
-    cnt = torch.empty(1, dtype=torch.int64, device=dev)
+    if cnt is None:
+        cnt = torch.empty(1, dtype=torch.int64, device=dev)
     call('vc_compact', ptr(flags), n, 1 if select_zero else 0, ptr(idx),
          ptr(cnt), ptr(ws), ws_bytes, stream())
     return idx, cnt
@@ -130,6 +132,36 @@ def _clip_box_by_halfspaces_batched(xl, xh, A, b):
     Q = A.shape[1]
     table = DisjunctTable({0: list(range(Q))}, xl.device)
     return _clip(xl, xh, A, b, table)
+
+
+def _split_feasible(xl, xh, feas):
+    """The feasible rows (feas) of clipped boxes, their widest axes and the
+    bisection of the usable ones, with one host read for both counts: the
+    widest axis is taken on every row, so the feasible and the split lists
+    are compacted together (verify_graph.py:13115-13121, 13291,
+    13366-13382).  Returns (xl_f, xh_f, n_degenerate, ax_f, low, high)."""
+    B, n = xl.shape
+    dev = xl.device
+    ax = torch.empty(B, dtype=torch.int64, device=dev)
+    usable = torch.empty(B, dtype=torch.bool, device=dev)
+    call('vc_widest_axis', ptr(xl), ptr(xh), B, n, ptr(ax), ptr(usable), stream())
+    split = feas & usable
+    cnts = torch.empty(2, dtype=torch.int64, device=dev)
+    fidx, _ = _compact_device(feas, cnt=cnts[0:1])
+    uidx, _ = _compact_device(split, cnt=cnts[1:2])
+    nf, nu = cnts.tolist()
+    fidx, uidx = fidx[:nf], uidx[:nu]
+    # the int64 axes travel as float pairs through the row gather (bit copy)
+    xl_f, xh_f, ax2 = _gather_many([xl, xh, ax.view(torch.float32).view(B, 2)], fidx)
+    ax_f = ax2.view(torch.int64).view(nf)
+    low_xl = torch.empty(nu, n, device=dev)
+    low_xh = torch.empty_like(low_xl)
+    high_xl = torch.empty_like(low_xl)
+    high_xh = torch.empty_like(low_xl)
+    if nu > 0:
+        call('vc_bisect', ptr(xl), ptr(xh), ptr(ax), ptr(uidx), nu, n,
+             ptr(low_xl), ptr(low_xh), ptr(high_xl), ptr(high_xh), stream())
+    return xl_f, xh_f, nf - nu, ax_f, (low_xl, low_xh), (high_xl, high_xh)
 
 
 def _widest_and_bisect(xl, xh):
@@ -249,7 +281,8 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
             new, n_ait = _run_alpha_crown_inputsplit_batched(
                 xl_o, xh_o, gg, spec_ew,
                 dev, dt, n_iters=alpha_iters, lr=alpha_lr,
-                lr_decay=alpha_lr_decay, sb=sb_open, return_trace=True)
+                lr_decay=alpha_lr_decay, sb=sb_open, return_trace=True,
+                lazy_trace=True)
             n_al = int(open_idx.numel())
             call('vc_scatter_max_rows', ptr(lb), ptr(open_idx),
                  ptr(new.contiguous()), n_al, lb.shape[1], stream())
@@ -259,24 +292,29 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
         timers['alpha'] = timers.get('alpha', 0.0) + t1 - t0
         t0 = t1
     unclosed = _compact(closed, select_zero=True)
+    # the alpha loop's evaluation count was copied to the host in stream
+    # order: the compaction's read above has waited for it
+    n_ait = n_ait() if callable(n_ait) else n_ait
     out = {'lb': lb, 'A': A, 'acc': acc, 'closed': closed,
            'unclosed': unclosed, 'n_alpha_leaves': n_al,
            'n_alpha_iters': n_ait}
     if clip_enabled and unclosed.numel() > 0 and A is not None:
         xl_u, xh_u, A_u, acc_u = _gather_many([xl, xh, A, acc], unclosed)
         xl_c, xh_c, feas = _clip(xl_u, xh_u, A_u, acc_u, table)
-        fidx = _compact(feas)
         out['feasible'] = feas
-        xl_s, xh_s = _gather_many([xl_c, xh_c], fidx)
+        xl_s, xh_s, n_deg, ax, low, high = _split_feasible(xl_c, xh_c, feas)
+        if timers is not None:
+            timers['clip'] = timers.get('clip', 0.0) + sync_t() - t0
+            t0 = sync_t()
     else:
         out['feasible'] = None
         xl_s, xh_s = _gather_many([xl, xh], unclosed)
-    if timers is not None:
-        t1 = sync_t()
-        timers['clip'] = timers.get('clip', 0.0) + t1 - t0
-        t0 = t1
+        if timers is not None:
+            t1 = sync_t()
+            timers['clip'] = timers.get('clip', 0.0) + t1 - t0
+            t0 = t1
+        n_deg, ax, low, high = _widest_and_bisect(xl_s, xh_s)
     out['xl_split'], out['xh_split'] = xl_s, xh_s
-    n_deg, ax, low, high = _widest_and_bisect(xl_s, xh_s)
     out.update(ax=ax, n_degenerate=n_deg, low=low, high=high)
     if timers is not None:
         timers['split'] = timers.get('split', 0.0) + sync_t() - t0

@@ -631,7 +631,7 @@ def _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, want_grad, galpha,
 def _run_alpha_crown_inputsplit_batched(xl, xh, gg, spec_ew, device, dtype,
                                         n_iters=10, lr=0.25, lr_decay=0.98,
                                         early_stop_eps=1e-6, sb=None,
-                                        return_trace=False):
+                                        return_trace=False, lazy_trace=False):
     """Batched alpha-CROWN with Adam (verify_zono_bnb.py:5137-5288).
 
     Same schedule as the reference: alpha starts at (up_s > 0.5)*unstable on
@@ -641,7 +641,9 @@ def _run_alpha_crown_inputsplit_batched(xl, xh, gg, spec_ew, device, dtype,
     less than ``early_stop_eps`` (from the second iteration), decay lr.
     The gradient is computed analytically by the HIP gradient sweep.
     ``sb`` (extension) replaces the zonotope bounds; ``return_trace`` also
-    returns the number of evaluated iterations.
+    returns the number of evaluated iterations; with ``lazy_trace`` that
+    number may come as a callable, to be called after a later host
+    synchronisation (it then costs no round trip of its own).
     """
     _check_dtype(dtype)
     xl, xh = f32(xl), f32(xh)
@@ -660,7 +662,7 @@ def _run_alpha_crown_inputsplit_batched(xl, xh, gg, spec_ew, device, dtype,
     plan = _plan(gg, dev)
     if plan is not None and mlp_fused.alpha_supported(plan, Q):
         best, n_eval = mlp_fused.alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr,
-                                             lr_decay, early_stop_eps)
+                                             lr_decay, early_stop_eps, lazy=lazy_trace)
         return (best, n_eval) if return_trace else best
     Ls = sorted(sb)
     sizes = [sb[L][0].numel() for L in Ls]
