@@ -33,6 +33,9 @@ extern "C" {
  * never leaves a domain to a layer-wise fallback. */
 #define VC_ZONO_WIDE_COLS 512
 
+/* Iterations vc_mlp_tiled_alpha_run may run in one launch. */
+#define VC_ALPHA_CHUNK 4
+
 typedef void *vc_stream_t;
 
 /* Library version, for the host to check the ABI it loaded. */
@@ -478,7 +481,11 @@ int vc_mlp_tiled_alpha_iter(const int32_t *dims, int n_relu, const float *frag,
 /* The whole loop of _run_alpha_crown_inputsplit_batched
  * (verify_zono_bnb.py:5239-5287) in one call: n_iters >= 1 iterations of
  * vc_mlp_tiled_alpha_iter, each followed by vc_alpha_control, launched
- * back to back with the loop control on the device.  ctl (4 floats) is set
+ * back to back with the loop control on the device.  Batches of at most
+ * 4 x compute units run up to VC_ALPHA_CHUNK iterations per launch on
+ * their LDS state; the control then takes those iterations in order and
+ * discards the ones after a stop (the result is that of stopping there).
+ * lb_out: scratch of VC_ALPHA_CHUNK x B x Q floats.  ctl (4 floats) is set
  * here and ends as vc_alpha_control leaves it (ctl[2] = evaluated
  * iterations); best (B, Q) = the best bound per spec row.  Torch Adam's
  * schedule: step size lr_t / (1 - b1^t), bias correction (1 - b2^t)^0.5,

@@ -72,6 +72,18 @@ struct AdamConst {
   float w1, b2, w2, eps, neg_step, bc2;
 };
 
+// The Adam constants of the (up to VC_ALPHA_CHUNK, vibecheck_amd.h)
+// iterations one alpha-CROWN launch runs back to back.
+struct AdamChunk {
+  AdamConst c[VC_ALPHA_CHUNK];
+  int n;
+};
+
+// vc_alpha_control over n_it consecutive iterations (lbs: n_it x n),
+// stopping at the first stop (vc_elementwise.hip).
+int alpha_control_chunk(float* best, const float* lbs, int64_t n, int it0, int n_it, double eps,
+                        float* ctl, int32_t* stop_host, hipStream_t stream);
+
 static inline AdamConst adam_const(double b1, double b2, double eps, double step_size,
                                    double bc2_sqrt) {
   AdamConst c;

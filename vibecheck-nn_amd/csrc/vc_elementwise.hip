@@ -319,47 +319,60 @@ __global__ void k_split_clamps(const int64_t* layer, const int64_t* neuron, cons
 // control of verify_zono_bnb.py:5252-5287: ctl = {previous global max of the
 // best bound, stopped flag, evaluated iterations, this iteration's max}.
 // Once stopped, later calls (and the fused alpha kernel) do nothing.
-__global__ void k_alpha_control(float* best, const float* lb, int64_t n, int it, double eps,
-                                float* ctl, int32_t* stop_host) {
+// The bookkeeping of n_it consecutive alpha-CROWN iterations it0 ..
+// it0 + n_it - 1 whose bounds are lbs[t] (n each), in order, up to the
+// first stop (the later ones are discarded): best update, global max, the
+// reference's two stop tests.
+__global__ void k_alpha_control(float* best, const float* lbs, int64_t n, int it0, int n_it,
+                                double eps, float* ctl, int32_t* stop_host) {
   __shared__ float smax[16];
   __shared__ int sneg[16];
+  __shared__ int s_stop;
   if (ctl[1] != 0.f) return;
-  float mx = -INFINITY;
-  int notpos = 0;
-  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
-    const float x = lb[i];
-    const float b = it == 0 ? x : fmaxf(best[i], x);
-    best[i] = b;
-    mx = fmaxf(mx, b);
-    notpos |= !(b > 0.f);
-  }
-  for (int o = 32; o > 0; o >>= 1) {
-    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    notpos |= __shfl_xor(notpos, o, 64);
-  }
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (lane == 0) {
-    smax[w] = mx;
-    sneg[w] = notpos;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int nw = blockDim.x >> 6;
-    float a = smax[0];
-    int b = sneg[0];
-    for (int i = 1; i < nw; ++i) {
-      a = fmaxf(a, smax[i]);
-      b |= sneg[i];
+  for (int t = 0; t < n_it; ++t) {
+    const int it = it0 + t;
+    const float* lb = lbs + (int64_t)t * n;
+    float mx = -INFINITY;
+    int notpos = 0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+      const float x = lb[i];
+      const float b = it == 0 ? x : fmaxf(best[i], x);
+      best[i] = b;
+      mx = fmaxf(mx, b);
+      notpos |= !(b > 0.f);
     }
-    const float prev = ctl[0];
-    bool stop = b == 0;  // every best bound > 0
-    if (!stop && it > 0 && (double)a - (double)prev < eps) stop = true;
-    ctl[0] = a;
-    ctl[1] = stop ? 1.f : 0.f;
-    ctl[2] = (float)(it + 1);
-    ctl[3] = a;
-    // a hint for the launching host thread (pinned host memory)
-    if (stop && stop_host) __hip_atomic_store(stop_host, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    for (int o = 32; o > 0; o >>= 1) {
+      mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      notpos |= __shfl_xor(notpos, o, 64);
+    }
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) {
+      smax[w] = mx;
+      sneg[w] = notpos;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int nw = blockDim.x >> 6;
+      float a = smax[0];
+      int b = sneg[0];
+      for (int i = 1; i < nw; ++i) {
+        a = fmaxf(a, smax[i]);
+        b |= sneg[i];
+      }
+      const float prev = ctl[0];
+      bool stop = b == 0;  // every best bound > 0
+      if (!stop && it > 0 && (double)a - (double)prev < eps) stop = true;
+      ctl[0] = a;
+      ctl[1] = stop ? 1.f : 0.f;
+      ctl[2] = (float)(it + 1);
+      ctl[3] = a;
+      // a hint for the launching host thread (pinned host memory)
+      if (stop && stop_host)
+        __hip_atomic_store(stop_host, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      s_stop = stop ? 1 : 0;
+    }
+    __syncthreads();
+    if (s_stop) return;
   }
 }
 
@@ -905,11 +918,20 @@ extern "C" int vc_best_update(float* best, const float* lb, int64_t n, int init,
   return VC_OK;
 }
 
+int alpha_control_chunk(float* best, const float* lbs, int64_t n, int it0, int n_it, double eps,
+                        float* ctl, int32_t* stop_host, hipStream_t stream) {
+  if (!best || !lbs || !ctl || n <= 0 || it0 < 0 || n_it < 1) return VC_ERR_ARG;
+  hipLaunchKernelGGL(k_alpha_control, dim3(1), dim3(1024), 0, stream, best, lbs, n, it0, n_it,
+                     eps, ctl, stop_host);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
 extern "C" int vc_alpha_control(float* best, const float* lb, int64_t n, int it, double eps,
                                 float* ctl, int32_t* stop_host, vc_stream_t stream) {
   if (!best || !lb || !ctl || n <= 0 || it < 0) return VC_ERR_ARG;
   hipLaunchKernelGGL(k_alpha_control, dim3(1), dim3(1024), 0, (hipStream_t)stream, best, lb, n,
-                     it, eps, ctl, stop_host);
+                     it, 1, eps, ctl, stop_host);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }

@@ -976,7 +976,7 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
     TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
     const float* __restrict__ xl, const float* __restrict__ xh, TAlphaArgs aa, int Q,
     const float* __restrict__ spec_rows, const float* __restrict__ spec_acc,
-    float* __restrict__ lb_out, AdamConst adam, int init, const float* __restrict__ ctl, int D) {
+    float* __restrict__ lb_out, AdamChunk ac, int init, const float* __restrict__ ctl, int D) {
   if (ctl && ctl[1] != 0.f) return;  // the loop has stopped (vc_alpha_control)
   extern __shared__ float smem[];
   float* sfrag = smem;
@@ -1044,6 +1044,10 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
       }
     }
     __syncthreads();
+    // ac.n iterations back to back on the state in LDS; iteration t's
+    // bounds go to lb_out + t B Q
+    for (int t_it = 0; t_it < ac.n; ++t_it) {
+    const AdamConst& adam = ac.c[t_it];
     // ---- spec backward with alpha: the owned slice of the rows
     v4f Fw;
 #pragma unroll
@@ -1141,7 +1145,7 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
       double t = 0.0;
 #pragma unroll
       for (int u = 0; u < MT; ++u) t += sacc[u * 16 + r];
-      lb_out[dom * Q + r] = (float)(t + sacc[MT * 16 + r]);
+      lb_out[(int64_t)t_it * B * Q + dom * Q + r] = (float)(t + sacc[MT * 16 + r]);
     }
     // ---- forward gradient sweep with the Adam update, owned neurons
     for (int l = 0; l < n; ++l) {
@@ -1179,6 +1183,7 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
           sa[FW + j] = mi;
           sa[2 * FW + j] = vi;
           sa[j] = pa;
+          sl[j] = pa;  // unstable: the next iteration's lower slope is alpha
         }
       }
       if (l + 1 < n) {
@@ -1203,6 +1208,7 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
         GEw = o;
       }
     }
+    }  // iterations
     // ---- the owned neurons' Adam state back (the wave's own LDS writes)
     __threadfence_block();
     if (has) {
@@ -1918,16 +1924,33 @@ int alpha_prepare(const int32_t* dims, int n_relu, const float* frag, const floa
   return VC_OK;
 }
 
+// ac.n iterations (the quad kernel; the one-wavefront kernel takes one);
+// iteration t's bounds to lb_out + t B Q.
 int alpha_launch(const AlphaLaunch& L, const float* frag, const float* bias_cat, int64_t B,
                  const float* xl, const float* xh, int Q, const float* spec_rows,
-                 const float* spec_acc, float* lb_out, AdamConst adam, int init,
+                 const float* spec_acc, float* lb_out, const AdamChunk& ac, int init,
                  const float* ctl, hipStream_t st) {
+  if (ac.n < 1 || ac.n > (L.quad ? VC_ALPHA_CHUNK : 1)) return VC_ERR_ARG;
   TGeom G = L.G;
   TAlphaArgs aa = L.aa;
   int D = L.D;
-  void* args[] = {&G,  (void*)&frag,      (void*)&bias_cat, &B,     (void*)&xl,
-                  (void*)&xh, &aa,         &Q,               (void*)&spec_rows,
-                  (void*)&spec_acc, (void*)&lb_out, &adam, &init, (void*)&ctl, &D};
+  AdamChunk acc = ac;
+  AdamConst a1 = ac.c[0];
+  void* args[] = {&G,
+                  (void*)&frag,
+                  (void*)&bias_cat,
+                  &B,
+                  (void*)&xl,
+                  (void*)&xh,
+                  &aa,
+                  &Q,
+                  (void*)&spec_rows,
+                  (void*)&spec_acc,
+                  (void*)&lb_out,
+                  L.quad ? (void*)&acc : (void*)&a1,
+                  &init,
+                  (void*)&ctl,
+                  &D};
   if (hipLaunchKernel(L.fn, L.grid, L.block, args, L.lds, st) != hipSuccess) return VC_ERR_LAUNCH;
   return VC_OK;
 }
@@ -1947,8 +1970,10 @@ extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const fl
                          exp_avg_sq, Q, spec_rows, spec_acc, lb_out, L);
   if (rc != VC_OK) return rc;
   if (B == 0) return VC_OK;
-  return alpha_launch(L, frag, bias_cat, B, xl, xh, Q, spec_rows, spec_acc, lb_out,
-                      adam_const(b1, b2, eps, step_size, bc2_sqrt), init, ctl,
+  AdamChunk ac;
+  ac.n = 1;
+  ac.c[0] = adam_const(b1, b2, eps, step_size, bc2_sqrt);
+  return alpha_launch(L, frag, bias_cat, B, xl, xh, Q, spec_rows, spec_acc, lb_out, ac, init, ctl,
                       (hipStream_t)stream);
 }
 
@@ -1987,20 +2012,28 @@ extern "C" int vc_mlp_tiled_alpha_run(const int32_t* dims, int n_relu, const flo
   // lr_t / (1 - b1^t) and (1 - b2^t)^0.5, lr decayed after every iteration.
   // Once the device has stopped (and said so in *stop_host), the remaining
   // iterations, which would do nothing, are not enqueued.
+  // The small-batch kernel runs up to VC_ALPHA_CHUNK iterations per launch
+  // on its LDS state; the control replays the stop tests over them in
+  // order and discards the ones after a stop.
   volatile int32_t* sh = stop_host;
+  const int K = L.quad ? VC_ALPHA_CHUNK : 1;
   double cur_lr = lr;
-  for (int it = 0; it < n_iters; ++it) {
+  for (int it0 = 0; it0 < n_iters; it0 += K) {
     if (sh && *sh != 0) break;
-    const double step = (double)(it + 1);
-    rc = alpha_launch(L, frag, bias_cat, B, xl, xh, Q, spec_rows, spec_acc, lb_out,
-                      adam_const(b1, b2, eps, cur_lr / (1.0 - pow(b1, step)),
-                                 pow(1.0 - pow(b2, step), 0.5)),
-                      it == 0 ? 1 : 0, ctl, st);
+    AdamChunk ac;
+    ac.n = std::min(K, n_iters - it0);
+    for (int t = 0; t < ac.n; ++t) {
+      const double step = (double)(it0 + t + 1);
+      ac.c[t] = adam_const(b1, b2, eps, cur_lr / (1.0 - pow(b1, step)),
+                           pow(1.0 - pow(b2, step), 0.5));
+      cur_lr *= lr_decay;
+    }
+    rc = alpha_launch(L, frag, bias_cat, B, xl, xh, Q, spec_rows, spec_acc, lb_out, ac,
+                      it0 == 0 ? 1 : 0, ctl, st);
     if (rc != VC_OK) return rc;
-    rc = vc_alpha_control(best, lb_out, B * (int64_t)Q, it, early_stop_eps, ctl, stop_host,
-                          stream);
+    rc = alpha_control_chunk(best, lb_out, B * (int64_t)Q, it0, ac.n, early_stop_eps, ctl,
+                             stop_host, st);
     if (rc != VC_OK) return rc;
-    cur_lr *= lr_decay;
   }
   return VC_OK;
 }

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(_HERE, 'libvibecheck_amd.so')
 
 VC_OK, VC_ERR_ARG, VC_ERR_OOM, VC_ERR_UNSUPPORTED, VC_ERR_LAUNCH = 0, 1, 2, 3, 4
 VC_ZONO_WIDE_COLS = 512     # generator columns of vc_mlp_tiled_zono_wide
+VC_ALPHA_CHUNK = 4          # iterations per launch of vc_mlp_tiled_alpha_run
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int

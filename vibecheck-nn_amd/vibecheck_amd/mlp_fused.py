@@ -265,7 +265,8 @@ def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps,
         a, p = host_array(ctypes.c_void_p, lst)
         keep.append(a)
         ptrs.append(p)
-    lb = torch.empty(B, Q, device=dev)
+    # per-iteration bounds: up to VC_ALPHA_CHUNK iterations per launch
+    lb = torch.empty(_lib.VC_ALPHA_CHUNK if tiled else 1, B, Q, device=dev)
     best = torch.empty(B, Q, device=dev)
     red = torch.empty(2, device=dev)
     b1, b2, eps = 0.9, 0.999, 1e-8
