@@ -330,13 +330,14 @@ int vc_mlp_zono_wide(const int32_t *dims, int n_relu, const float *frag_fwd,
  * compile time (frag from vc_mlp_tiled_pack): one wavefront per domain, up
  * to 128 generator columns including the centre; overflow[b] = 1 (a byte
  * flag, as vc_compact reads) for the domains that need more (to be
- * finished by vc_mlp_tiled_zono_wide).
+ * finished by vc_mlp_tiled_zono_wide).  queue: as for vc_mlp_tiled_crown
+ * (domains differ in cost by their generator counts).
  * Replaces the ReLU bounds of _forward_zonotope_graph_batched
  * (verify_zono_bnb.py:3079-3211). */
 int vc_mlp_tiled_zono_bounds(const int32_t *dims, int n_relu, const float *frag,
                              const float *bias_cat, int64_t B, const float *xl,
                              const float *xh, float *const *lo_out,
-                             float *const *hi_out, uint8_t *overflow,
+                             float *const *hi_out, uint8_t *overflow, int32_t *queue,
                              vc_stream_t stream);
 
 /* vc_mlp_zono_wide with the tile shape fixed at compile time (frag from
@@ -409,9 +410,12 @@ int vc_mlp_tiled_crown_mode(int64_t B);
  * list (the other neurons have slopes their tightening cannot change);
  * lo_out/hi_out of the unseeded neurons keep lo_in/hi_in.  seed_rows
  * (device, n_relu uint64, nullable) accumulates the seeded neurons per
- * layer over all domains (the work done, for the roofline).  Batches with
- * vc_mlp_tiled_crown_mode(B) == 1 spread each domain's row tiles over
- * several wavefronts (identical results).
+ * layer over all domains (the work done, for the roofline).  queue
+ * (device int32, nullable): a counter the call resets and then uses to hand
+ * the domains to wavefronts as they finish (domains differ in cost by
+ * their seed counts); calls that may overlap in time need distinct
+ * counters.  Batches with vc_mlp_tiled_crown_mode(B) == 1 spread each
+ * domain's row tiles over several wavefronts (identical results).
  * Replaces _crown_intermediate_batched (verify_zono_bnb.py:4077-4147) and
  * _spec_backward_graph_batched with return_input_linear
  * (verify_zono_bnb.py:4270-4453, 5117-5134). */
@@ -423,7 +427,7 @@ int vc_mlp_tiled_crown(const int32_t *dims, int n_relu, const float *frag,
                        const int32_t *idx_meta, int do_crown, int per_domain,
                        int Q, const float *spec_rows, const float *spec_acc,
                        float *lb_out, float *A_out, float *acc_out,
-                       uint64_t *seed_rows, vc_stream_t stream);
+                       uint64_t *seed_rows, int32_t *queue, vc_stream_t stream);
 
 /* The neurons unstable in any domain, per layer, for the CROWN seeding of
  * _crown_intermediate_batched (verify_zono_bnb.py:4123): flags (sum of

@@ -38,6 +38,15 @@ __device__ __forceinline__ void stage_float4(float* dst_lds, const float* src, i
   for (; e < n4; e += bs) d[e] = s[e];
 }
 
+// Dynamic domain queue: lane 0 of a wavefront takes the next ticket with a
+// vector atomic; callers take the following ticket while they process the
+// current domain and broadcast it (queue_bcast) only when they need it.
+__device__ __forceinline__ int queue_take(int* q, int lane) {
+  return lane == 0 ? atomicAdd(q, 1) : 0;
+}
+__device__ __forceinline__ int64_t queue_bcast(int t) { return (int64_t)__shfl(t, 0, 64); }
+
+
 // Compute units of the current device (read once per device).
 inline int cu_count() {
   static int cached[64] = {0};

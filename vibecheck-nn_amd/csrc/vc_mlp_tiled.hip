@@ -31,6 +31,11 @@ using vcm::FW;
 using vcm::ks_count;
 using vcm::MAXL;
 
+// The work counter of a queue-driven launch, reset on its stream.
+__global__ void k_queue_reset(int* q) {
+  if (threadIdx.x == 0) *q = 0;
+}
+
 constexpr int TNW = 12;  // waves per workgroup, one domain each (3 per SIMD)
 constexpr int TNP = 1;   // 16-row N-tiles chained together per wave
 constexpr int TQMAX = 64;  // spec rows per call (taken 16 at a time)
@@ -388,7 +393,7 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
     const int32_t* __restrict__ idx_all, const int32_t* __restrict__ idx_meta, int do_crown,
     int per_domain, int Q, const float* __restrict__ spec_rows,
     const float* __restrict__ spec_acc, float* __restrict__ lb_out, float* __restrict__ A_out,
-    float* __restrict__ acc_out, unsigned long long* __restrict__ seed_rows) {
+    float* __restrict__ acc_out, unsigned long long* __restrict__ seed_rows, int* queue) {
   extern __shared__ float smem[];
   float* sfrag = smem;
   float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
@@ -419,7 +424,13 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
   const float* dxl = sx;
   const float* dxh = sx + FW;
 
-  for (int64_t dom = (int64_t)blockIdx.x * TNW + wv; dom < B; dom += (int64_t)gridDim.x * TNW) {
+  // the first domain of every wavefront by its index, the rest from the
+  // work queue as wavefronts finish (domains differ in cost by their seed
+  // counts), else a fixed stride
+  const int64_t nwaves = (int64_t)gridDim.x * TNW;
+  int64_t dom = (int64_t)blockIdx.x * TNW + wv;
+  while (dom < B) {
+    const int tnext = (queue && B > nwaves) ? vcm::queue_take(queue, lane) : 0;
     sx[lane] = lane < d0 ? xl[dom * d0 + lane] : 0.f;
     sx[FW + lane] = lane < d0 ? xh[dom * d0 + lane] : 0.f;
     // layer bounds are loaded one layer ahead (lane j holds neuron j)
@@ -491,6 +502,7 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_tiled(
         spec_group<MT, KS, 1, BROW>(G, q0, Q, spec_rows, spec_acc, fr0, frh, ssl, sbias, lane, g,
                                     r, dxl, dxh, dom, lb_out, A_out, acc_out);
     }
+    dom = (queue && B > nwaves) ? nwaves + vcm::queue_bcast(tnext) : dom + nwaves;
   }
   __threadfence_block();
   if (seed_rows && lane < n && sscnt[lane] > 0)
@@ -1306,7 +1318,8 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
                                                          const float* __restrict__ gbias,
                                                          int64_t B, const float* __restrict__ xl,
                                                          const float* __restrict__ xh,
-                                                         TZonoArgs out, uint8_t* overflow) {
+                                                         TZonoArgs out, uint8_t* overflow,
+                                                         int* queue) {
   extern __shared__ float smem[];
   float* sfrag = smem;
   float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
@@ -1330,7 +1343,13 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
   int* zcol = reinterpret_cast<int*>(zmu + FW);
 
   const int nwv = blockDim.x >> 6;
-  for (int64_t dom = (int64_t)blockIdx.x * nwv + wv; dom < B; dom += (int64_t)gridDim.x * nwv) {
+  // the first domain of every wavefront by its index, the rest from the
+  // work queue as wavefronts finish (domains differ in cost by their
+  // generator counts), else a fixed stride
+  const int64_t nwaves = (int64_t)gridDim.x * nwv;
+  int64_t dom = (int64_t)blockIdx.x * nwv + wv;
+  while (dom < B) {
+    const int tnext = (queue && B > nwaves) ? vcm::queue_take(queue, lane) : 0;
     const float* dxl = xl + dom * d0;
     const float* dxh = xh + dom * d0;
     v4f Z[ZT][4];
@@ -1479,6 +1498,7 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
       Kc += cnt;
     }
     if (lane == 0) overflow[dom] = ovf ? 1 : 0;
+    dom = (queue && B > nwaves) ? nwaves + vcm::queue_bcast(tnext) : dom + nwaves;
   }
 }
 
@@ -1742,7 +1762,7 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
                                   const int32_t* idx_meta, int do_crown, int per_domain, int Q,
                                   const float* spec_rows, const float* spec_acc, float* lb_out,
                                   float* A_out, float* acc_out, uint64_t* seed_rows,
-                                  vc_stream_t stream) {
+                                  int32_t* queue, vc_stream_t stream) {
   TGeom G;
   int rc = tiled_geom(dims, n_relu, G);
   if (rc != VC_OK) return rc;
@@ -1820,13 +1840,14 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
   }
   if (!vcm::allow_max_lds(fn)) return VC_ERR_UNSUPPORTED;
   const dim3 grid(vcm::persistent_grid(B, lds, TNW)), block(TNW * 64);
+  if (queue) hipLaunchKernelGGL(k_queue_reset, dim3(1), dim3(64), 0, st, queue);
 #define VC_TILED_CASE(V)                                                                     \
   case V:                                                                                    \
     hipLaunchKernelGGL((k_crown_tiled<kVariants[V].MT, kVariants[V].KS,                      \
                                       kVariants[V].brow != 0>),                              \
                        grid, block, lds, st, G, frag, bias_cat, B, xl, xh, ca, idx_all,      \
                        idx_meta, do_crown, per_domain, Q, spec_rows, spec_acc, lb_out, A_out,  \
-                       acc_out, reinterpret_cast<unsigned long long*>(seed_rows));           \
+                       acc_out, reinterpret_cast<unsigned long long*>(seed_rows), queue);    \
     break;
   switch (G.variant) {
     VC_TILED_CASE(0)
@@ -2042,7 +2063,7 @@ extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const f
                                         const float* bias_cat, int64_t B, const float* xl,
                                         const float* xh, float* const* lo_out,
                                         float* const* hi_out, uint8_t* overflow,
-                                        vc_stream_t stream) {
+                                        int32_t* queue, vc_stream_t stream) {
   TGeom G;
   int rc = tiled_geom(dims, n_relu, G);
   if (rc != VC_OK) return rc;
@@ -2073,11 +2094,13 @@ extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const f
   if (!vcm::allow_max_lds(fn)) return VC_ERR_UNSUPPORTED;
   const dim3 grid(vcm::persistent_grid(B, lds, nw)), block(nw * 64);
   hipStream_t st = (hipStream_t)stream;
+  if (queue) hipLaunchKernelGGL(k_queue_reset, dim3(1), dim3(64), 0, st, queue);
 #define VC_TZONO_CASE(V)                                                                     \
   case V:                                                                                    \
     hipLaunchKernelGGL((k_zono_tiled<kVariants[V].MT, kVariants[V].KS,                       \
                                      kVariants[V].brow != 0>),                               \
-                       grid, block, lds, st, G, frag, bias_cat, B, xl, xh, za, overflow);    \
+                       grid, block, lds, st, G, frag, bias_cat, B, xl, xh, za, overflow,     \
+                       queue);                                                               \
     break;
   switch (G.variant) {
     VC_TZONO_CASE(0)

@@ -70,7 +70,7 @@ SIGNATURES = {
     'vc_mlp_tiled_floats': [_P, _I],
     'vc_mlp_tiled_pack': [_P, _P, _P, _I, _P, _P],
     'vc_mlp_tiled_crown': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I,
-                           _I, _P, _P, _P, _P, _P, _P, _P],
+                           _I, _P, _P, _P, _P, _P, _P, _P, _P],
     'vc_mlp_tiled_alpha_iter': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
                                 _P, _P, _P, _D, _D, _D, _D, _D, _I, _P, _P],
     'vc_mlp_tiled_alpha_run': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
@@ -80,7 +80,7 @@ SIGNATURES = {
     'vc_union_compact': [_P, _P, _I, _P, _P, _P],
     'vc_gather_rows_multi': [_P, _P, _P, _I, _P, _L, _P],
     'vc_alpha_control': [_P, _P, _L, _I, _D, _P, _P, _P],
-    'vc_mlp_tiled_zono_bounds': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P],
+    'vc_mlp_tiled_zono_bounds': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P],
     'vc_mlp_zono_wide': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P],
     'vc_mlp_tiled_zono_wide': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P],
     'vc_widest_axis': [_P, _P, _L, _I, _P, _P, _P],

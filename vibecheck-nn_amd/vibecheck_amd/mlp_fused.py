@@ -64,6 +64,9 @@ class MlpPlan:
             self.frag[fwd] = buf
         # fragments of the shape-specialised CROWN kernel (None: no instantiation)
         self.tfrag = None
+        # work counters of the shape-specialised CROWN and zonotope kernels
+        # (reset by each call; calls on one plan are ordered on one stream)
+        self.queue = torch.zeros(2, dtype=torch.int32, device=device)
         nt = int(lib.vc_mlp_tiled_floats(self.dims_p, self.n))
         if nt > 0:
             bp_arr, bp = host_array(ctypes.c_void_p, [ptr(b) for b in self.bs])
@@ -136,7 +139,7 @@ def zono_bounds(plan, xl, xh, fallback):
         ovf = torch.empty(B, dtype=torch.uint8, device=dev)
         args = (B, ptr(xl), ptr(xh), lo_p, hi_p, ptr(ovf))
         call('vc_mlp_tiled_zono_bounds', plan.dims_p, plan.n, ptr(plan.tfrag),
-             ptr(plan.bias_cat), *args, stream())
+             ptr(plan.bias_cat), *args, plan.queue[1:].data_ptr(), stream())
         lst, cnt = _compact_device(ovf)
         call('vc_mlp_tiled_zono_wide', plan.dims_p, plan.n, ptr(plan.tfrag),
              ptr(plan.bias_cat), *args, ptr(lst), ptr(cnt), stream())
@@ -379,7 +382,7 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False, per_domain=F
         call('vc_mlp_tiled_crown', plan.dims_p, plan.n, ptr(plan.tfrag), ptr(plan.bias_cat), B,
              ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
              1 if do_crown else 0, 1 if per_domain else 0, Q, ptr(S), ptr(acc0), ptr(lb),
-             ptr(A), ptr(acc), ptr(seeds), stream())
+             ptr(A), ptr(acc), ptr(seeds), plan.queue.data_ptr(), stream())
     else:
         call('vc_mlp_crown', plan.dims_p, plan.n, ptr(plan.frag[0]), ptr(plan.bias_cat), B,
              ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
