@@ -571,6 +571,46 @@ int vc_bisect(const float *xl, const float *xh, const int64_t *ax,
               float *low_xh, float *high_xl, float *high_xh,
               vc_stream_t stream);
 
+/* One input-split BaB round on the narrow-MLP kernels (the bound,
+ * alpha, clip and split phases of verify_graph.py:12855-13382, with
+ * crown intermediate bounds, the clip on and alpha-CROWN on every open leaf),
+ * orchestrated in host C++: every step is one of the entry points above on
+ * `stream`; the three counts the round needs (open, unclosed, feasible +
+ * split) are read with a stream synchronisation each.  frag, bias_cat: from
+ * vc_mlp_tiled_pack; spec_rows/spec_acc: the Q spec rows folded through the
+ * last fc; d_ptr/q_idx/n_disj: the disjunct table of vc_closure.  Outputs,
+ * device, sized for B rows: lb (B, Q), A (B, Q, n_in), acc (B, Q), closed
+ * (B), unclosed (the first counts[2] entries), feasible (per unclosed row),
+ * xl_split/xh_split/ax (the first counts[3] rows), low/high children (the
+ * first counts[4] rows).  counts (host int64[6]) = {open leaves, alpha
+ * iterations evaluated, unclosed, feasible, split, degenerate}.  work:
+ * vc_mlp_bab_round_workspace(dims, n_relu, B, Q) bytes of device memory;
+ * stop_host: as for vc_mlp_tiled_alpha_run.  seed_rows (nullable): as for
+ * vc_mlp_tiled_crown; crown_ev0/crown_ev1 (nullable hipEvent_t): recorded
+ * on `stream` around the vc_mlp_tiled_crown call (its timing).  pinned
+ * (nullable, pinned host memory, >= 2 int64): the GPU stores each count
+ * there and the host polls it (bounded, then a stream synchronisation)
+ * instead of a device-to-host copy and a synchronisation.  VC_ERR_UNSUPPORTED when the
+ * net can have more zonotope generators than VC_ZONO_WIDE_COLS.
+ * Replaces one iteration of _input_split_batched_inner's loop body
+ * (verify_graph.py:12855-13382), as bab_step restates it. */
+int64_t vc_mlp_bab_round_workspace(const int32_t *dims, int n_relu, int64_t B,
+                                   int Q);
+int vc_mlp_bab_round(const int32_t *dims, int n_relu, const float *frag,
+                     const float *bias_cat, int Q, const float *spec_rows,
+                     const float *spec_acc, const int32_t *d_ptr,
+                     const int32_t *q_idx, int n_disj, int64_t B,
+                     const float *xl, const float *xh, int alpha_iters,
+                     double alpha_lr, double alpha_lr_decay,
+                     double alpha_early_stop, float *lb, float *A, float *acc,
+                     uint8_t *closed, int64_t *unclosed, uint8_t *feasible,
+                     float *xl_split, float *xh_split, int64_t *ax,
+                     float *low_xl, float *low_xh, float *high_xl,
+                     float *high_xh, uint64_t *seed_rows, void *crown_ev0,
+                     void *crown_ev1, void *work, int64_t work_bytes,
+                     int32_t *stop_host, int64_t *pinned, int64_t *counts,
+                     vc_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -551,6 +551,39 @@ def test_split_and_compaction_bit_exact(gpu):
     assert torch.equal(cpu(vg._closure(lb.to(gpu), tab)), rbab.closure(lb, {0: [0, 1, 2, 3]}))
 
 
+@pytest.mark.parametrize('alpha_iters', [0, 20])
+def test_bab_round_native_matches_python_round(gpu, alpha_iters):
+    """The round as one native call (vc_mlp_bab_round) runs the same entry
+    points in the same order as bab_step's Python round: every output equal
+    bit for bit, every count equal."""
+    gg_c, gg_g, xl, xh = acas(gpu, 4096, seed=23, scale=2.0)
+    _, se_g, dq = spec_pair(5, gpu)
+    table = vg.DisjunctTable(dq, gpu)
+    xl, xh = xl.to(gpu), xh.to(gpu)
+    res = {}
+    old = vg.NATIVE_ROUND
+    try:
+        for native in (True, False):
+            vg.NATIVE_ROUND = native
+            res[native] = vg.bab_step(xl, xh, gg_g, se_g, table, crown_intermediate=True,
+                                      clip_enabled=True, alpha_iters=alpha_iters,
+                                      alpha_all=True, alpha_lr=0.1)
+    finally:
+        vg.NATIVE_ROUND = old
+    a, b = res[True], res[False]
+    print(f"alpha {alpha_iters}: {a['n_alpha_leaves']} leaves, {a['n_alpha_iters']} iterations, "
+          f"{a['unclosed'].numel()} unclosed, {a['xl_split'].shape[0]} feasible")
+    for k in ('n_alpha_leaves', 'n_alpha_iters', 'n_degenerate'):
+        assert a[k] == b[k], k
+    for k in ('lb', 'A', 'acc', 'closed', 'unclosed', 'xl_split', 'xh_split', 'ax'):
+        assert torch.equal(a[k], b[k]), k
+    assert (a['feasible'] is None) == (b['feasible'] is None)
+    if a['feasible'] is not None:
+        assert torch.equal(a['feasible'], b['feasible'])
+    for x, y in zip(a['low'] + a['high'], b['low'] + b['high']):
+        assert torch.equal(x, y)
+
+
 def test_bab_step_parity_c0(gpu, mlp_path):
     """Config-0 shape: 4096 ACAS boxes, CROWN intermediate, clip, split."""
     gg_c, gg_g, xl, xh = acas(gpu, 4096)

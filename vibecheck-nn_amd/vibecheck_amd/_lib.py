@@ -83,10 +83,15 @@ SIGNATURES = {
     'vc_mlp_tiled_zono_bounds': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P],
     'vc_mlp_zono_wide': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P],
     'vc_mlp_tiled_zono_wide': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P],
+    'vc_mlp_bab_round_workspace': [_P, _I, _L, _I],
+    'vc_mlp_bab_round': [_P, _I, _P, _P, _I, _P, _P, _P, _P, _I, _L, _P, _P, _I, _D, _D, _D,
+                         _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                         _L, _P, _P, _P, _P],
     'vc_widest_axis': [_P, _P, _L, _I, _P, _P, _P],
     'vc_bisect': [_P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P],
 }
 _RESTYPE = {'vc_compact_workspace': ctypes.c_int64,
+            'vc_mlp_bab_round_workspace': ctypes.c_int64,
             'vc_mlp_frag_floats': ctypes.c_int64,
             'vc_mlp_tiled_floats': ctypes.c_int64}
 
@@ -203,6 +208,23 @@ def timing_end():
         out[n] = {'launches': len(per), 'seconds': sum(p[0] for p in per),
                   'flops': sum(p[1] for p in per), 'per_launch': per}
     return out
+
+
+def timing_events(name):
+    """A recorded (start, end) event pair for a launch of `name` made inside
+    another entry point, when `name` is being timed (else None)."""
+    if _timing is None or name not in _timing:
+        return None
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()  # creates the events; the entry point records them again
+    e.record()
+    return s, e
+
+
+def timing_add(name, events, flops, args):
+    """File a launch timed with timing_events."""
+    _timing[name].append((events[0], events[1], flops, args))
 
 
 def call(name, *args):

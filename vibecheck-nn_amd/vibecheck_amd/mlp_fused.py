@@ -235,6 +235,18 @@ def _stop_word():
     return _STOP_WORD
 
 
+_PINNED_WORDS = None
+
+
+def _pinned_words():
+    """Pinned host int64 words the native BaB round's counts are stored in
+    (one set per process; each round ends with them read)."""
+    global _PINNED_WORDS
+    if _PINNED_WORDS is None:
+        _PINNED_WORDS = torch.zeros(4, dtype=torch.int64, pin_memory=True)
+    return _PINNED_WORDS
+
+
 def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps, lazy=False):
     """Batched alpha-CROWN with the reference's schedule
     (verify_zono_bnb.py:5137-5288), one fused kernel launch per Adam

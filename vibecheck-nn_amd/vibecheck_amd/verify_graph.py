@@ -230,6 +230,74 @@ class ChunkWorklist:
         return bool(self.xl)
 
 
+# Run bab_step's round as one native call (vc_mlp_bab_round) where it
+# applies; switching this off runs the same entry points from Python.
+NATIVE_ROUND = True
+
+
+def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_lr_decay):
+    """bab_step's round (crown intermediate bounds, clip, alpha-CROWN on
+    every open leaf) as one call of the native round orchestration, for
+    nets with the shape-specialised kernels; None where it does not apply.
+    Same entry points in the same order as the Python round, so the same
+    results."""
+    from . import mlp_fused
+    from . import verify_zono_bnb as vz
+    dev = xl.device
+    plan = mlp_fused.plan_for(gg, dev) if vz.FUSED_MLP else None
+    if plan is None or not mlp_fused._tiled(plan):
+        return None
+    if 1 + sum(plan.dims[:plan.n]) > _lib.VC_ZONO_WIDE_COLS or len(spec_ew) > 32:
+        return None
+    Wq, bq = vz._spec_rows(spec_ew, dev)
+    Q = Wq.shape[0]
+    if alpha_iters > 0 and not mlp_fused.alpha_supported(plan, Q):
+        return None
+    S, acc0 = mlp_fused.fold_spec(plan, Wq, bq)
+    xl, xh = f32(xl), f32(xh)
+    B, n_in = xl.shape
+    # the float outputs in one allocation: lb, acc, A, then 6 box arrays
+    Bm = max(B, 1)
+    flt = torch.empty(Bm * (2 * Q + Q * n_in + 6 * n_in), device=dev)
+    lb = flt[:B * Q].view(B, Q)
+    acc = flt[Bm * Q:Bm * Q + B * Q].view(B, Q)
+    A = flt[2 * Bm * Q:2 * Bm * Q + B * Q * n_in].view(B, Q, n_in)
+    boxes = flt[Bm * (2 * Q + Q * n_in):].view(6, Bm, n_in)
+    flags = torch.empty(2, Bm, dtype=torch.bool, device=dev)
+    closed, feas = flags[0, :B], flags[1]
+    idx = torch.empty(2, Bm, dtype=torch.int64, device=dev)
+    lib = _lib.load()
+    nws = int(lib.vc_mlp_bab_round_workspace(plan.dims_p, plan.n, B, Q))
+    ws = torch.empty(max(nws, 8), dtype=torch.uint8, device=dev)
+    counts = (ctypes.c_int64 * 6)()
+    stop = mlp_fused._stop_word()
+    # work accounting and timing of the CROWN launch, as mlp_fused.crown does
+    seeds = None
+    if mlp_fused.SEED_COUNTER is not None:
+        seeds = mlp_fused.SEED_COUNTER[mlp_fused.SEED_ROW]
+        mlp_fused.SEED_ROW += 1
+    ev = _lib.timing_events('vc_mlp_tiled_crown')
+    call('vc_mlp_bab_round', plan.dims_p, plan.n, ptr(plan.tfrag), ptr(plan.bias_cat), Q,
+         ptr(S), ptr(acc0), ptr(table.d_ptr), ptr(table.q_idx), table.n, B, ptr(xl), ptr(xh),
+         int(alpha_iters), float(alpha_lr), float(alpha_lr_decay), 1e-6, ptr(lb), ptr(A),
+         ptr(acc), ptr(closed), ptr(idx[0]), ptr(feas), ptr(boxes[0]), ptr(boxes[1]),
+         ptr(idx[1]), ptr(boxes[2]), ptr(boxes[3]), ptr(boxes[4]), ptr(boxes[5]), ptr(seeds),
+         ev[0].cuda_event if ev else None, ev[1].cuda_event if ev else None, ptr(ws),
+         nws, stop.data_ptr(), mlp_fused._pinned_words().data_ptr(), ctypes.addressof(counts),
+         stream())
+    if ev:
+        spec = _lib.mlp_crown_flops(plan.dims, plan.n, B, [0] * plan.n, 0, Q)
+        _lib.timing_add('vc_mlp_tiled_crown', ev, spec, (None, None, None, None, B))
+    n_open, n_eval, n_unc, nf, nu, n_deg = (int(c) for c in counts)
+    out = {'lb': lb, 'A': A, 'acc': acc, 'closed': closed, 'unclosed': idx[0, :n_unc],
+           'n_alpha_leaves': n_open, 'n_alpha_iters': n_eval,
+           'feasible': feas[:n_unc] if n_unc > 0 else None,
+           'xl_split': boxes[0, :nf], 'xh_split': boxes[1, :nf], 'ax': idx[1, :nf],
+           'n_degenerate': n_deg, 'low': (boxes[2, :nu], boxes[3, :nu]),
+           'high': (boxes[4, :nu], boxes[5, :nu])}
+    return out
+
+
 def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
              clip_enabled=True, alpha_iters=0, alpha_all=False, alpha_eps=0.0,
              alpha_max_leaves=200, alpha_lr=0.25, alpha_lr_decay=0.98,
@@ -238,6 +306,12 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
     bound, closure, optional alpha-CROWN on unclosed leaves, one clip
     iteration, widest-axis bisection.  Returns a dict of device tensors
     (same keys as the oracle's bab_step)."""
+    if (NATIVE_ROUND and timers is None and crown_intermediate and clip_enabled
+            and (alpha_iters == 0 or alpha_all)):
+        out = _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr,
+                                alpha_lr_decay)
+        if out is not None:
+            return out
     dev = xl.device
     dt = torch.float32
     sync_t = (lambda: (torch.cuda.synchronize(), time.perf_counter())[1]) \
