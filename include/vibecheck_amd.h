@@ -576,7 +576,7 @@ int vc_bisect(const float *xl, const float *xh, const int64_t *ax,
  * crown intermediate bounds, the clip on and alpha-CROWN on every open leaf),
  * orchestrated in host C++: every step is one of the entry points above on
  * `stream`; the three counts the round needs (open, unclosed, feasible +
- * split) are read with a stream synchronisation each.  frag, bias_cat: from
+ * split) are read on the host (see `pinned`).  frag, bias_cat: from
  * vc_mlp_tiled_pack; spec_rows/spec_acc: the Q spec rows folded through the
  * last fc; d_ptr/q_idx/n_disj: the disjunct table of vc_closure.  Outputs,
  * device, sized for B rows: lb (B, Q), A (B, Q, n_in), acc (B, Q), closed
