@@ -108,6 +108,216 @@ def copy_probe(mib):
     print(json.dumps({'copy_probe_bytes_read': n * 4, 'copy_probe_bytes_written': n * 4}))
 
 
+ROTATE_BYTES = 768 << 20  # > 2x the 256 MB Infinity Cache
+
+
+def _time_launches(fns, reps):
+    """Average seconds per launch of fns (cycled) over reps launches, HIP
+    events on the current stream (the launch stream of every entry point)."""
+    for f in fns:
+        f()
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(reps):
+        fns[i % len(fns)]()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / 1e3 / reps
+
+
+def _n_sets(bytes_per_set):
+    """Independent input/output sets cycled per launch, so that a launch
+    reads what the previous ones left in HBM, not in the 256 MB cache."""
+    return max(1, min(32, -(-ROTATE_BYTES // max(1, bytes_per_set))))
+
+
+def kernel_suite(reps):
+    """The layer-wise kernels one at a time at workload shapes: one JSON line
+    each with the algorithmic bytes (HBM-bound kernels) or FLOP (GEMM-shaped
+    kernels) per launch, the average launch time and the fraction of the
+    MI355X peak.  A plain device copy gives the achievable HBM rate."""
+    from vibecheck_amd import _lib
+    from vibecheck_amd._lib import call, ptr, stream
+
+    dev = torch.device('cuda:0')
+    _lib.load()
+    st = stream()
+    gen = torch.Generator(device=dev).manual_seed(7)
+
+    def rnd(*shape):
+        return torch.rand(*shape, device=dev, generator=gen)
+
+    def rndn(*shape):
+        return torch.randn(*shape, device=dev, generator=gen)
+
+    def bounds(*shape):
+        lo = rndn(*shape)
+        return lo, lo + rnd(*shape) * 2.0
+
+    def report(row, kernel, workload, sec, bound, amount):
+        if bound == 'hbm':
+            achieved, peak, unit = amount / sec / 1e9, HBM_PEAK_GBS, 'GB/s'
+        else:
+            achieved, peak, unit = amount / sec / 1e12, FP32_MFMA_PEAK, 'TFLOP/s'
+        print(json.dumps({
+            'row': row, 'kernel': kernel, 'workload': workload, 'bound': bound,
+            'avg_launch_us': sec * 1e6, 'achieved': achieved, 'peak': peak, 'unit': unit,
+            'frac': achieved / peak,
+            ('bytes' if bound == 'hbm' else 'flop'): amount}), flush=True)
+
+    # -- achievable: a plain 1 GiB device copy
+    n = (1 << 30) // 4
+    src = rnd(n)
+    dst = torch.empty_like(src)
+    sec = _time_launches([lambda: dst.copy_(src)], reps)
+    report('-', 'device copy (torch copy_)', '1 GiB read + 1 GiB write', sec, 'hbm', 2.0 * n * 4)
+    del src, dst
+
+    # -- a1: slopes of every (domain, neuron), 524,288 x 50
+    n = 524288 * 50
+    per = n * 23
+    sets = []
+    for _ in range(_n_sets(per)):
+        lo, hi = bounds(n)
+        outs = [torch.empty(n, device=dev) for _ in range(3)]
+        flags = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(3)]
+        sets.append((lo, hi, outs, flags))
+    fns = [lambda s=s: call('vc_make_slopes', ptr(s[0]), ptr(s[1]), n, *map(ptr, s[2]),
+                            *map(ptr, s[3]), st) for s in sets]
+    report('a1', 'k_make_slopes', '524,288 x 50 (lo, hi in; 3 slopes + 3 masks out)',
+           _time_launches(fns, reps), 'hbm', per)
+    del sets, fns
+
+    # -- a8: concretization, A (B*R, n_in)
+    for B, R, n_in, what in ((512, 2048, 784, '784-input MLP, 512 domains x 2048 seeded rows'),
+                             (524288, 4, 5, '5-input MLP, 524,288 domains x 4 spec rows')):
+        M = B * R
+        per = 4 * (M * n_in + 2 * M + 2 * B * n_in)
+        sets = []
+        for _ in range(_n_sets(per)):
+            A = rndn(M, n_in)
+            acc = rndn(M)
+            xl = rnd(B, n_in)
+            sets.append((A, acc, xl, xl + 0.05, torch.empty(M, device=dev)))
+        fns = [lambda s=s: call('vc_concretize', ptr(s[0]), ptr(s[1]), ptr(s[2]), ptr(s[3]),
+                                M, R, n_in, 0, ptr(s[4]), st) for s in sets]
+        kern = 'k_concretize_thread' if n_in <= 32 else 'k_concretize_wave'
+        report('a8', kern, what, _time_launches(fns, reps), 'hbm', per)
+        del sets, fns
+
+    # -- a6: relaxation alone (the relu before a conv), 64 domains x 128 rows
+    #    x 32,768 neurons (the 32x32x32 activation of the CNN)
+    B, R, nn = 64, 128, 32768
+    M = B * R
+    per = 8 * M * nn + 8 * B * nn + 8 * M
+    ew = rndn(M, nn)
+    lo, hi = bounds(B, nn)
+    out = torch.empty_like(ew)
+    acc = torch.zeros(M, device=dev)
+    fn = lambda: call('vc_backward_relu', ptr(ew), M, R, nn, ptr(lo), ptr(hi), None, 0, None,
+                      ptr(out), ptr(acc), st)
+    report('a6', 'k_backward_relu', '8,192 rows x 32,768 neurons (64 domains x 128 rows)',
+           _time_launches([fn], reps), 'hbm', per)
+    del ew, out, acc, lo, hi
+
+    # -- a9: Adam step over every alpha of 524,288 domains x 6 x 50
+    n = 524288 * 300
+    per = 28 * n
+    p, g, m, v = rnd(n), rndn(n), rndn(n) * 0.01, rnd(n) * 0.01
+    fn = lambda: call('vc_adam_step', ptr(p), ptr(g), ptr(m), ptr(v), n, 0.9, 0.999, 1e-8,
+                      0.1, 0.5, 0.0, 1.0, st)
+    report('a9', 'k_adam', '157,286,400 alphas (524,288 domains x 6 x 50)',
+           _time_launches([fn], reps), 'hbm', per)
+    del p, g, m, v
+
+    # -- a12-a14 on 524,288 5-dim boxes
+    B, Q, nd = 524288, 4, 5
+    d_ptr = torch.tensor([0, Q], dtype=torch.int32, device=dev)
+    q_idx = torch.arange(Q, dtype=torch.int32, device=dev)
+    per = B * (40 + 4 * Q * nd + 4 * Q + 40 + 1)
+    sets = []
+    for _ in range(_n_sets(per)):
+        xl = rnd(B, nd) * 2 - 1
+        xh = xl + rnd(B, nd) * 0.1
+        A = rndn(B, Q, nd)
+        b = rndn(B, Q) * 0.01 - 0.2
+        sets.append((xl, xh, A, b, torch.empty_like(xl), torch.empty_like(xh),
+                     torch.empty(B, dtype=torch.uint8, device=dev)))
+    fns = [lambda s=s: call('vc_clip_box', ptr(s[0]), ptr(s[1]), ptr(s[2]), ptr(s[3]), B, Q, nd,
+                            ptr(d_ptr), ptr(q_idx), 1, ptr(s[4]), ptr(s[5]), ptr(s[6]), st)
+           for s in sets]
+    report('a12', 'k_clip', '524,288 boxes, 5 dims, 4 halfspaces', _time_launches(fns, reps),
+           'hbm', per)
+    per = B * (40 + 8 + 1)
+    outs = [(torch.empty(B, dtype=torch.int64, device=dev),
+             torch.empty(B, dtype=torch.uint8, device=dev)) for _ in sets]
+    fns = [lambda s=s, o=o: call('vc_widest_axis', ptr(s[0]), ptr(s[1]), B, nd, ptr(o[0]),
+                                 ptr(o[1]), st) for s, o in zip(sets, outs)]
+    report('a13', 'k_widest', '524,288 boxes, 5 dims', _time_launches(fns, reps), 'hbm', per)
+    per = B * (40 + 8 + 8 + 80)
+    idx = torch.arange(B, dtype=torch.int64, device=dev)
+    kids = [[torch.empty(B, nd, device=dev) for _ in range(4)] for _ in sets]
+    fns = [lambda s=s, o=o, c=c: call('vc_bisect', ptr(s[0]), ptr(s[1]), ptr(o[0]), ptr(idx), B,
+                                      nd, *map(ptr, c), st)
+           for s, o, c in zip(sets, outs, kids)]
+    report('a14', 'k_bisect', '524,288 boxes, 5 dims', _time_launches(fns, reps), 'hbm', per)
+    del sets, outs, kids
+    flags = (rnd(B) < 0.5).to(torch.uint8)
+    cnt_true = int(flags.sum())
+    ws = torch.empty(max(8, _lib.load().vc_compact_workspace(B)), dtype=torch.uint8, device=dev)
+    cidx = torch.empty(B, dtype=torch.int64, device=dev)
+    cnt = torch.empty(1, dtype=torch.int64, device=dev)
+    fn = lambda: call('vc_compact', ptr(flags), B, 0, ptr(cidx), ptr(cnt), ptr(ws), ws.numel(),
+                      st)
+    report('a14', 'k_compact_count + k_compact_scan + k_compact_write',
+           '524,288 flags, half set', _time_launches([fn], reps), 'hbm', 2 * B + 8 * cnt_true)
+    del flags, ws, cidx
+
+    # -- a5 + a6: backward through fc with the relaxation fused (fp32 MFMA)
+    for B, R, n_out, n_in, what in (
+            (512, 512, 1024, 1024, '1024x1024 fc, 512 domains x 512 seeded rows'),
+            (8192, 9, 256, 256, '256x256 fc, 8,192 domains x 9 spec rows')):
+        M = B * R
+        ew = rndn(M, n_out)
+        lo, hi = bounds(B, n_out)
+        W = rndn(n_out, n_in) * (2.0 / n_in) ** 0.5
+        bias = rndn(n_out) * 0.01
+        out = torch.empty(M, n_in, device=dev)
+        acc = torch.zeros(M, device=dev)
+        fn = lambda: call('vc_backward_fc', ptr(ew), M, R, n_out, ptr(lo), ptr(hi), None, 0,
+                          None, ptr(W), ptr(bias), n_in, ptr(out), ptr(acc), None, 0, st)
+        report('a5', 'gemm_kernel (backward fc + relaxation)', what,
+               _time_launches([fn], max(3, reps // 4)), 'mfma', 2.0 * M * n_out * n_in)
+        del ew, out, acc
+
+    # -- a2: interval fc (two products: mid W^T, rad |W|^T)
+    B, n_in, n_out = 8192, 784, 256
+    l = rnd(B, n_in)
+    h = l + 0.06
+    W = rndn(n_out, n_in) * (2.0 / n_in) ** 0.5
+    bias = torch.zeros(n_out, device=dev)
+    lo, hi = torch.empty(B, n_out, device=dev), torch.empty(B, n_out, device=dev)
+    fn = lambda: call('vc_ibp_fc', ptr(l), ptr(h), B, n_in, ptr(W), ptr(bias), n_out, ptr(lo),
+                      ptr(hi), st)
+    report('a2', 'gemm_kernel (interval fc, two products)', '784->256 fc, 8,192 boxes',
+           _time_launches([fn], reps), 'mfma', 2.0 * 2 * B * n_in * n_out)
+
+    # -- a7: backward through conv(32->64, 4x4, s2, p1) as a transposed conv
+    M, C_in, H, C_out, Ho, k = 64 * 9, 32, 32, 64, 16, 4
+    ew = rndn(M, C_out * Ho * Ho)
+    K = rndn(C_out, C_in, k, k) * (2.0 / (C_in * k * k)) ** 0.5
+    bias = rndn(C_out) * 0.01
+    out = torch.empty(M, C_in * H * H, device=dev)
+    acc = torch.zeros(M, device=dev)
+    fn = lambda: call('vc_backward_conv', ptr(ew), M, ptr(K), ptr(bias), C_out, Ho, Ho, C_in, H,
+                      H, k, k, 2, 2, 1, 1, ptr(out), ptr(acc), st)
+    report('a7', 'k_conv_transpose', 'conv 32->64 4x4 s2 p1 (32x32 in), 576 rows '
+           '(64 domains x 9)', _time_launches([fn], max(3, reps // 4)), 'mfma',
+           2.0 * M * (C_out * Ho * Ho) * (C_in * k * k))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -117,6 +327,8 @@ def main():
     ap.add_argument('--cpu-sample', type=int, default=2048)
     ap.add_argument('--copy-probe', type=int, default=0, metavar='MIB',
                     help='only run a plain copy of MIB MiB (counter calibration)')
+    ap.add_argument('--kernels', action='store_true',
+                    help='only time the layer-wise kernels one at a time (one JSON line each)')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU only (this build has no multi-GPU path); '
@@ -124,6 +336,9 @@ def main():
         sys.exit(2)
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.kernels:
+        kernel_suite(max(4, args.steps * 4))
         return
 
     from vibecheck_amd import _lib

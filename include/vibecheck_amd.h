@@ -518,7 +518,8 @@ int vc_closure(const float *lb, int64_t B, int Q, const int32_t *d_ptr,
 
 /* Halfspace box clip of {x in [xl, xh] : A_q x + b_q <= 0 for q in D} per
  * disjunct D, and the bounding box of the union over feasible disjuncts
- * (single disjunct: plain clip).  A (B, Q, n), b (B, Q).
+ * (single disjunct: plain clip).  A (B, Q, n), b (B, Q); Q <= 64 and at
+ * most 64 queries per disjunct (VC_ERR_UNSUPPORTED beyond 64 queries).
  * Replaces _clip_box_by_halfspaces_batched (verify_graph.py:12363-12426)
  * and the multi-disjunct union (verify_graph.py:13040-13074). */
 int vc_clip_box(const float *xl, const float *xh, const float *A,

@@ -20,6 +20,7 @@ from vibecheck_amd import verify_graph as vg
 from vibecheck_amd import verify_zono_bnb as vz
 from vibecheck_amd import workloads as wk
 from vibecheck_amd._lib import call, ptr
+from vibecheck_amd._lib import stream as _lib_stream
 
 import _util
 
@@ -508,25 +509,143 @@ def test_alpha_small_batch_kernel_matches_large_batch_kernel(gpu, n_iters):
 
 
 # ----------------------------------------------------------------- a11-a14
-def test_clip_parity_identical_inputs(gpu):
+@pytest.mark.parametrize('n', [5, 12, 20])
+def test_clip_parity_identical_inputs(gpu, n):
+    """n = 5 and 12: the register kernels (boxes of at most 8 and 16 dims);
+    n = 20: the generic one.  B is not a multiple of the 64-box workgroup."""
     g = torch.Generator().manual_seed(3)
-    B, Q, n = 4096, 4, 5
+    B, Q = 4109, 4
     xl = torch.rand(B, n, generator=g) - 1
     xh = xl + torch.rand(B, n, generator=g) + 0.01
     A = torch.randn(B, Q, n, generator=g)
     b = torch.randn(B, Q, generator=g) - 1.0
+    # thresholds (-b - L_other) / A_qi cancel terms of the size of
+    # |b_q| + sum_k |A_qk| max(|xl_k|, |xh_k|), divided by |A_qi|: that is
+    # the scale of each clipped bound (largest over the queries acting on
+    # the dimension); entries outside the band also pass when at least as
+    # close to the fp64 oracle as the fp32 oracle is
+    Ad = A.double()
+    mag = b.double().abs() + (Ad.abs() * torch.maximum(xl.abs(), xh.abs()).double()
+                              .unsqueeze(1)).sum(-1)
+    act = Ad.abs() > 1e-12
+    sc = torch.where(act, mag.unsqueeze(-1) / Ad.abs().clamp(min=1e-12), torch.zeros_like(Ad))
+    sc = sc.amax(1)
     rl, rh, rf = rbab.clip_box_by_halfspaces_batched(xl, xh, A, b)
+    rl64, rh64, _ = rbab.clip_box_by_halfspaces_batched(xl.double(), xh.double(), A.double(),
+                                                         b.double())
     gl, gh, gf = vg._clip_box_by_halfspaces_batched(xl.to(gpu), xh.to(gpu), A.to(gpu), b.to(gpu))
     assert torch.equal(cpu(gf), rf)
-    assert_bounds(gl, rl, 'clip xl')
-    assert_bounds(gh, rh, 'clip xh')
+    assert_bounds(gl, rl, 'clip xl', ref64=rl64, scale=sc)
+    assert_bounds(gh, rh, 'clip xh', ref64=rh64, scale=sc)
     dq = {0: [0, 2], 1: [1], 2: [3]}
     rl, rh, rf = rbab.clip_leaves(xl, xh, A, b, dq)
+    rl64, rh64, _ = rbab.clip_leaves(xl.double(), xh.double(), A.double(), b.double(), dq)
     tab = vg.DisjunctTable(dq, gpu)
     gl, gh, gf = vg._clip(xl.to(gpu), xh.to(gpu), A.to(gpu), b.to(gpu), tab)
     assert torch.equal(cpu(gf), rf)
-    assert_bounds(gl, rl, 'clip union xl')
-    assert_bounds(gh, rh, 'clip union xh')
+    assert_bounds(gl, rl, 'clip union xl', ref64=rl64, scale=sc)
+    assert_bounds(gh, rh, 'clip union xh', ref64=rh64, scale=sc)
+
+
+@pytest.mark.parametrize('n', [1028, 36, 35])
+@pytest.mark.parametrize('alpha_mode', [None, 'domain', 'row'])
+@pytest.mark.parametrize('with_beta', [False, True])
+def test_relaxation_kernels_rows_and_domains(gpu, n, alpha_mode, with_beta):
+    """vc_backward_relu on every kernel it picks (n = 1028: one workgroup per
+    four rows; 36: a wavefront per two rows, float4; 35: the same, scalar),
+    R = 3 rows per domain so that row groups span domains, M = 21 rows not
+    a multiple of the group: each row against the slopes of the oracle."""
+    g = torch.Generator().manual_seed(n + 7)
+    B, R = 7, 3
+    M = B * R
+    ew = torch.randn(M, n, generator=g)
+    lo = torch.randn(B, n, generator=g)
+    hi = lo + torch.rand(B, n, generator=g) * 2
+    alpha = None
+    if alpha_mode == 'domain':
+        alpha = torch.rand(B, n, generator=g)
+    elif alpha_mode == 'row':
+        alpha = torch.rand(M, n, generator=g)
+    beta = torch.randn(B, n, generator=g) * 0.1 if with_beta else None
+    acc0 = torch.randn(M, generator=g)
+    out = torch.full((M, n), float('nan'), device=gpu)
+    acc = acc0.to(gpu)
+    # device copies held for the whole call (a temporary freed after ptr()
+    # hands its memory to the next allocation)
+    d_ew, d_lo, d_hi = ew.to(gpu), lo.to(gpu), hi.to(gpu)
+    d_al = None if alpha is None else alpha.to(gpu)
+    d_bt = None if beta is None else beta.to(gpu)
+    call('vc_backward_relu', ptr(d_ew), M, R, n, ptr(d_lo), ptr(d_hi), ptr(d_al),
+         1 if alpha_mode == 'row' else 0, ptr(d_bt), ptr(out), ptr(acc), _lib_stream())
+    lo_s, up_s, up_t, active, dead, unstable = rb.make_slopes(lo, hi)
+    dom = torch.arange(M) // R
+    ls = lo_s[dom]
+    if alpha is not None:
+        a = alpha if alpha_mode == 'row' else alpha[dom]
+        ls = torch.where(active[dom], torch.ones_like(a), torch.where(unstable[dom], a,
+                                                                      torch.zeros_like(a)))
+    want = ew.clamp(min=0) * ls + ew.clamp(max=0) * up_s[dom]
+    if beta is not None:
+        want = want + beta[dom]
+    assert torch.equal(cpu(out), want)
+    terms = (ew.clamp(max=0) * up_t[dom]).double()
+    want_acc = acc0.double() + terms.sum(-1)
+    assert_bounds(cpu(acc), want_acc.float(), 'relax acc',
+                  scale=acc0.double().abs() + terms.abs().sum(-1))
+
+
+def test_row_kernels_beyond_grid_cap(gpu):
+    """The one-wavefront-per-row kernels cover every row when there are more
+    rows than one launch has wavefronts (1,048,576 workgroups x 4 waves =
+    4,194,304 rows): relaxation, concretization (float4 and scalar row
+    paths) and the zonotope ReLU bounds.  Outputs start as NaN, so a row
+    left out fails."""
+    st = _lib_stream()
+    M = 4194304 + 37
+    gd = torch.Generator(device=gpu).manual_seed(11)
+    rows = torch.cat([torch.arange(0, 64), torch.arange(M - 4096, M)])
+    # relaxation, R = 1 (every row its own domain), float4 path (n = 4)
+    n = 4
+    ew = torch.randn(M, n, device=gpu, generator=gd)
+    lo = torch.randn(M, n, device=gpu, generator=gd)
+    hi = lo + torch.rand(M, n, device=gpu, generator=gd)
+    out = torch.full((M, n), float('nan'), device=gpu)
+    acc = torch.zeros(M, device=gpu)
+    call('vc_backward_relu', ptr(ew), M, 1, n, ptr(lo), ptr(hi), None, 0, None, ptr(out),
+         ptr(acc), st)
+    e, l_, h_ = cpu(ew[rows]), cpu(lo[rows]), cpu(hi[rows])
+    lo_s, up_s, up_t, *_ = rb.make_slopes(l_, h_)
+    want = e.clamp(min=0) * lo_s + e.clamp(max=0) * up_s
+    assert torch.equal(cpu(out[rows]), want)
+    assert_bounds(cpu(acc[rows]), (e.clamp(max=0) * up_t).sum(-1), 'relax acc')
+    assert not bool(out.isnan().any())
+    del ew, lo, hi, out, acc
+    # concretization: n = 36 (float4 rows) and n = 35 (scalar rows), R = 1
+    for n in (36, 35):
+        A = torch.randn(M, n, device=gpu, generator=gd)
+        xl = torch.rand(M, n, device=gpu, generator=gd)
+        xh = xl + 0.5
+        accv = torch.randn(M, device=gpu, generator=gd)
+        lb = torch.full((M,), float('nan'), device=gpu)
+        call('vc_concretize', ptr(A), ptr(accv), ptr(xl), ptr(xh), M, 1, n, 0, ptr(lb), st)
+        a = cpu(A[rows]).double()
+        want = (cpu(accv[rows]).double() + (a.clamp(min=0) * cpu(xl[rows]).double()).sum(-1)
+                + (a.clamp(max=0) * cpu(xh[rows]).double()).sum(-1))
+        assert_bounds(cpu(lb[rows]), want.float(), f'concretize n={n}')
+        assert not bool(lb.isnan().any())
+        del A, xl, xh, accv, lb
+    # zonotope ReLU bounds over B*n rows, K = 2 generators
+    B, n, K = 838861, 5, 2
+    c = torch.randn(B, n, device=gpu, generator=gd)
+    G = torch.randn(B, n, K, device=gpu, generator=gd)
+    zl = torch.full((B, n), float('nan'), device=gpu)
+    zh = torch.full((B, n), float('nan'), device=gpu)
+    rank = torch.empty(B, n, dtype=torch.int32, device=gpu)
+    cnt = torch.empty(B, dtype=torch.int32, device=gpu)
+    call('vc_zono_relu_bounds', ptr(c), ptr(G), B, n, K, ptr(zl), ptr(zh), ptr(rank), ptr(cnt),
+         st)
+    s = G.abs().sum(-1)
+    assert torch.equal(zl, c - s) and torch.equal(zh, c + s)
 
 
 def test_split_and_compaction_bit_exact(gpu):

@@ -24,6 +24,8 @@ __device__ __forceinline__ v4f mfma16x16x4(float a, float b, v4f acc) {
     if (_e != hipSuccess) return VC_ERR_LAUNCH;             \
   } while (0)
 
+static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 static inline int vc_blocks(int64_t n, int threads) {
   int64_t b = (n + threads - 1) / threads;
   if (b < 1) b = 1;

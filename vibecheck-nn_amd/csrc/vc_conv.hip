@@ -151,13 +151,14 @@ __global__ void k_conv_transpose(const float* ew, int64_t M, ConvGeom g, const f
 __global__ void k_conv_bias_dot(const float* ew, int64_t M, int C_out, int sp,
                                 const float* bias, float* acc) {
   const int lane = threadIdx.x & 63;
-  const int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
-  if (m >= M) return;
-  const int64_t n = (int64_t)C_out * sp;
-  KSum ks;
-  for (int64_t j = lane; j < n; j += 64) ks.add(ew[m * n + j] * bias[j / sp]);
-  const float s = wave_sum_comp(ks);
-  if (lane == 0) acc[m] += s;
+  for (int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6; m < M;
+       m += ((int64_t)gridDim.x * blockDim.x) >> 6) {
+    const int64_t n = (int64_t)C_out * sp;
+    KSum ks;
+    for (int64_t j = lane; j < n; j += 64) ks.add(ew[m * n + j] * bias[j / sp]);
+    const float s = wave_sum_comp(ks);
+    if (lane == 0) acc[m] += s;
+  }
 }
 
 int check_geom(const ConvGeom& g) {

@@ -65,67 +65,296 @@ __global__ void k_ibp_relu(const float* l, const float* h, int64_t B, int n,
   }
 }
 
-// lb[m] = acc[m] + sum_i pos(A) xl + sum_i neg(A) xh ; one wave per row.
-__global__ void k_concretize_wave(const float* A, int a_bcast, const float* acc, const float* xl,
-                                  const float* xh, int64_t M, int R, int n, float* lb) {
-  const int lane = threadIdx.x & 63;
-  const int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
-  if (m >= M) return;
-  const int64_t d = m / R;
-  // one compensated sum over acc and both products, so that large
-  // cancelling positive/negative parts do not lose the small result
-  KSum s;
-  if (lane == 0) s.add(acc[m]);
-  for (int i = lane; i < n; i += 64) {
-    const float a = A[(a_bcast ? m % R : m) * n + i];
-    s.add(fmaxf(a, 0.f) * xl[d * n + i]);
-    s.add(fminf(a, 0.f) * xh[d * n + i]);
-  }
-  const float t = wave_sum_comp(s);
-  if (lane == 0) lb[m] = t;
+// torch.clamp(min=0) / clamp(max=0): NaN stays NaN
+__device__ __forceinline__ float pos_part(float a) { return a < 0.f ? 0.f : a; }
+__device__ __forceinline__ float neg_part(float a) { return a > 0.f ? 0.f : a; }
+
+// One concretization term pos(a) l + neg(a) h.  Each product is rounded to
+// fp32 as torch rounds the elementwise products; at most one of them is
+// non-zero, so their fp32 sum is exact, and the sum over i runs in fp64.
+__device__ __forceinline__ double conc_term(float a, float l, float h) {
+  return (double)(pos_part(a) * l + neg_part(a) * h);
 }
 
-__global__ void k_concretize_thread(const float* A, int a_bcast, const float* acc, const float* xl,
-                                    const float* xh, int64_t M, int R, int n, float* lb) {
-  const int64_t m = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (m >= M) return;
-  const int64_t d = m / R;
-  KSum s;
-  s.add(acc[m]);
-  for (int i = 0; i < n; ++i) {
-    const float a = A[(a_bcast ? m % R : m) * n + i];
-    s.add(fmaxf(a, 0.f) * xl[d * n + i]);
-    s.add(fminf(a, 0.f) * xh[d * n + i]);
+// Sum over the wave (every lane active): DPP row sums, then the four row
+// totals read from lanes 0, 16, 32, 48 and added in a fixed order.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  v = row_sum16(v);
+  const long long b = __double_as_longlong(v);
+  double r[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), 16 * k);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), 16 * k);
+    r[k] = __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
   }
-  lb[m] = s.value();
+  return (r[0] + r[1]) + (r[2] + r[3]);
 }
 
-// Standalone relu backward: one wave per row.
-__global__ void k_backward_relu(const float* ew, int64_t M, int R, int n, const float* lo,
-                                const float* hi, const float* alpha, int alpha_per_row,
-                                const float* beta, float* out, float* acc) {
+// lb[m] = acc[m] + sum_i pos(A) xl + sum_i neg(A) xh.  One wave takes
+// CR = 4 consecutive rows at a time and keeps all their loads in flight.
+// VEC: n % 4 == 0 and 16-byte aligned rows, float4 loads (1 KB per wave
+// instruction); A is streamed once, so its loads bypass the caches that
+// hold the domains' xl/xh rows.
+constexpr int CR = 4;
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_concretize_wave(const float* A, int a_bcast,
+                                                         const float* acc, const float* xl,
+                                                         const float* xh, int64_t M, int R,
+                                                         int n, float* lb) {
   const int lane = threadIdx.x & 63;
-  const int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
-  if (m >= M) return;
-  const int64_t d = m / R;
-  KSum p;
-  for (int j = lane; j < n; j += 64) {
-    const int64_t bi = d * n + j;
-    const float x = ew[m * n + j];
-    Relax s = relax(lo[bi], hi[bi]);
-    float ls = s.lo_s;
-    if (alpha) {
-      const float a = alpha_per_row ? alpha[m * n + j] : alpha[bi];
-      ls = s.active ? 1.f : (s.unstable ? a : 0.f);
+  const int64_t w0 = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+  const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t m0 = w0 * CR; m0 < M; m0 += nw * CR) {
+    const float* a[CR];
+    const float* l[CR];
+    const float* h[CR];
+    double s[CR];
+#pragma unroll
+    for (int k = 0; k < CR; ++k) {
+      const int64_t m = min(m0 + k, M - 1);  // past the end: recompute the last row
+      const int64_t d = m / R;
+      a[k] = A + (a_bcast ? m % R : m) * (int64_t)n;
+      l[k] = xl + d * n;
+      h[k] = xh + d * n;
+      s[k] = 0.0;
     }
-    const float ep = fmaxf(x, 0.f), en = fminf(x, 0.f);
-    float e = ep * ls + en * s.up_s;
-    if (beta) e = e + beta[bi];
-    out[m * n + j] = e;
-    p.add(en * s.up_t);
+    if (VEC && l[0] == l[CR - 1]) {
+      // the CR rows share one domain: its xl/xh loaded once for all of them
+      const int n4 = n >> 2;
+#pragma unroll 2
+      for (int i = lane; i < n4; i += 64) {
+        v4f x[CR];
+#pragma unroll
+        for (int k = 0; k < CR; ++k)
+          x[k] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(a[k]) + i);
+        const v4f p = reinterpret_cast<const v4f*>(l[0])[i];
+        const v4f q = reinterpret_cast<const v4f*>(h[0])[i];
+#pragma unroll
+        for (int k = 0; k < CR; ++k)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) s[k] += conc_term(x[k][c], p[c], q[c]);
+      }
+    } else if (VEC) {
+      const int n4 = n >> 2;
+      for (int i = lane; i < n4; i += 64) {
+        v4f x[CR];
+#pragma unroll
+        for (int k = 0; k < CR; ++k)
+          x[k] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(a[k]) + i);
+#pragma unroll
+        for (int k = 0; k < CR; ++k) {
+          const v4f p = reinterpret_cast<const v4f*>(l[k])[i];
+          const v4f q = reinterpret_cast<const v4f*>(h[k])[i];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) s[k] += conc_term(x[k][c], p[c], q[c]);
+        }
+      }
+    } else {
+      for (int i = lane; i < n; i += 64) {
+#pragma unroll
+        for (int k = 0; k < CR; ++k) s[k] += conc_term(a[k][i], l[k][i], h[k][i]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < CR; ++k) {
+      const double t = wave_sum_f64(s[k]);
+      if (lane == k && m0 + k < M) lb[m0 + k] = (float)((double)acc[m0 + k] + t);
+    }
   }
-  const float ps = wave_sum_comp(p);
-  if (lane == 0) acc[m] += ps;
+}
+
+// Narrow inputs (n <= 32): one thread per row.
+constexpr int CT = 256, CT_MAXN = 32;
+
+__global__ __launch_bounds__(CT) void k_concretize_thread(const float* A, int a_bcast,
+                                                          const float* acc, const float* xl,
+                                                          const float* xh, int64_t M, int R,
+                                                          int n, float* lb) {
+  for (int64_t m = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; m < M;
+       m += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t d = m / R;
+    const float* a = A + (a_bcast ? m % R : m) * (int64_t)n;
+    double s = 0.0;
+    for (int i = 0; i < n; ++i) s += conc_term(a[i], xl[d * n + i], xh[d * n + i]);
+    lb[m] = (float)((double)acc[m] + s);
+  }
+}
+
+// One relaxed element: e = pos(x) lo_s + neg(x) up_s (+ beta), and the
+// neg(x) up_t term of acc, for the slopes s (ls: lo_s, or the alpha slope).
+__device__ __forceinline__ float relax_apply(float x, const Relax& s, float ls, bool has_beta,
+                                             float bt, double& p) {
+  const float ep = pos_part(x), en = neg_part(x);
+  float e = ep * ls + en * s.up_s;
+  if (has_beta) e = e + bt;
+  p += (double)(en * s.up_t);
+  return e;
+}
+
+__device__ __forceinline__ float lo_slope(const Relax& s, bool has_alpha, float a) {
+  return has_alpha ? (s.active ? 1.f : (s.unstable ? a : 0.f)) : s.lo_s;
+}
+
+// Standalone relu backward.  One wave takes two consecutive rows at a time;
+// when both belong to one domain (and alpha is per domain) the relaxation
+// of each neuron is computed once for both.  VEC as for k_concretize_wave.
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_backward_relu(const float* ew, int64_t M, int R, int n,
+                                                       const float* lo, const float* hi,
+                                                       const float* alpha, int alpha_per_row,
+                                                       const float* beta, float* out,
+                                                       float* acc) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w0 = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+  const int64_t nw = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const bool ha = alpha != nullptr, hb = beta != nullptr;
+  for (int64_t m0 = w0 * 2; m0 < M; m0 += nw * 2) {
+    const int64_t m1 = min(m0 + 1, M - 1);  // past the end: recompute the last row
+    const int64_t d0 = m0 / R, d1 = m1 / R;
+    const bool shared = d0 == d1 && !alpha_per_row;
+    const float* x0 = ew + m0 * n;
+    const float* x1 = ew + m1 * n;
+    float* o0 = out + m0 * n;
+    float* o1 = out + m1 * n;
+    const float* l0 = lo + d0 * n;
+    const float* h0 = hi + d0 * n;
+    const float* l1 = lo + d1 * n;
+    const float* h1 = hi + d1 * n;
+    const float* a0 = ha ? alpha + (alpha_per_row ? m0 : d0) * n : nullptr;
+    const float* a1 = ha ? alpha + (alpha_per_row ? m1 : d1) * n : nullptr;
+    const float* b0 = hb ? beta + d0 * n : nullptr;
+    const float* b1 = hb ? beta + d1 * n : nullptr;
+    double p0 = 0.0, p1 = 0.0;
+    if (VEC) {
+      const int n4 = n >> 2;
+      const v4f zero = {0.f, 0.f, 0.f, 0.f};
+      for (int i = lane; i < n4; i += 64) {
+        const v4f x = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(x0) + i);
+        const v4f y = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(x1) + i);
+        const v4f la = reinterpret_cast<const v4f*>(l0)[i];
+        const v4f ha4 = reinterpret_cast<const v4f*>(h0)[i];
+        const v4f aa = ha ? reinterpret_cast<const v4f*>(a0)[i] : zero;
+        const v4f ba = hb ? reinterpret_cast<const v4f*>(b0)[i] : zero;
+        v4f e, f;
+        if (shared) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const Relax r = relax(la[c], ha4[c]);
+            const float ls = lo_slope(r, ha, aa[c]);
+            e[c] = relax_apply(x[c], r, ls, hb, ba[c], p0);
+            f[c] = relax_apply(y[c], r, ls, hb, ba[c], p1);
+          }
+        } else {
+          const v4f lb4 = reinterpret_cast<const v4f*>(l1)[i];
+          const v4f hb4 = reinterpret_cast<const v4f*>(h1)[i];
+          const v4f ab = ha ? reinterpret_cast<const v4f*>(a1)[i] : zero;
+          const v4f bb = hb ? reinterpret_cast<const v4f*>(b1)[i] : zero;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const Relax r = relax(la[c], ha4[c]);
+            e[c] = relax_apply(x[c], r, lo_slope(r, ha, aa[c]), hb, ba[c], p0);
+            const Relax q = relax(lb4[c], hb4[c]);
+            f[c] = relax_apply(y[c], q, lo_slope(q, ha, ab[c]), hb, bb[c], p1);
+          }
+        }
+        __builtin_nontemporal_store(e, reinterpret_cast<v4f*>(o0) + i);
+        __builtin_nontemporal_store(f, reinterpret_cast<v4f*>(o1) + i);
+      }
+    } else {
+      for (int j = lane; j < n; j += 64) {
+        const Relax r = relax(l0[j], h0[j]);
+        o0[j] = relax_apply(x0[j], r, lo_slope(r, ha, ha ? a0[j] : 0.f), hb, hb ? b0[j] : 0.f,
+                            p0);
+        const Relax q = shared ? r : relax(l1[j], h1[j]);
+        o1[j] = relax_apply(x1[j], q, lo_slope(q, ha, ha ? a1[j] : 0.f), hb, hb ? b1[j] : 0.f,
+                            p1);
+      }
+    }
+    p0 = wave_sum_f64(p0);
+    p1 = wave_sum_f64(p1);
+    if (lane == 0) acc[m0] = (float)((double)acc[m0] + p0);
+    if (lane == 1 && m0 + 1 < M) acc[m1] = (float)((double)acc[m1] + p1);
+  }
+}
+
+// Wide rows (n >= 1024, float4-aligned): one workgroup of 4 waves takes
+// RB = 4 consecutive rows, each wave a quarter of the columns (interleaved
+// in 256-float4 strides), so the four waves stream neighbouring addresses;
+// the per-row acc terms are reduced through LDS.  The relaxation of each
+// neuron is computed once for the rows of one domain.
+constexpr int RB = 4;
+
+template <bool HA, bool HB>
+__global__ __launch_bounds__(256) void k_backward_relu_rows(
+    const float* __restrict__ ew, int64_t M, int R, int n, const float* __restrict__ lo,
+    const float* __restrict__ hi, const float* __restrict__ alpha, int alpha_per_row,
+    const float* __restrict__ beta, float* __restrict__ out, float* __restrict__ acc) {
+  __shared__ double red[4][RB];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int n4 = n >> 2;
+  for (int64_t m0 = (int64_t)blockIdx.x * RB; m0 < M; m0 += (int64_t)gridDim.x * RB) {
+    int64_t mr[RB], dr[RB];
+#pragma unroll
+    for (int k = 0; k < RB; ++k) {
+      mr[k] = min(m0 + k, M - 1);  // past the end: recompute the last row
+      dr[k] = mr[k] / R;
+    }
+    const bool shared = dr[0] == dr[RB - 1] && !alpha_per_row;
+    double p[RB];
+#pragma unroll
+    for (int k = 0; k < RB; ++k) p[k] = 0.0;
+    for (int i = threadIdx.x; i < n4; i += 256) {
+      v4f x[RB], e[RB];
+#pragma unroll
+      for (int k = 0; k < RB; ++k)
+        x[k] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(ew + mr[k] * n) + i);
+      if (shared) {
+        const v4f l4 = reinterpret_cast<const v4f*>(lo + dr[0] * n)[i];
+        const v4f h4 = reinterpret_cast<const v4f*>(hi + dr[0] * n)[i];
+        v4f a4 = {0.f, 0.f, 0.f, 0.f}, b4 = {0.f, 0.f, 0.f, 0.f};
+        if (HA) a4 = reinterpret_cast<const v4f*>(alpha + dr[0] * n)[i];
+        if (HB) b4 = reinterpret_cast<const v4f*>(beta + dr[0] * n)[i];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const Relax r = relax(l4[c], h4[c]);
+          const float ls = lo_slope(r, HA, a4[c]);
+#pragma unroll
+          for (int k = 0; k < RB; ++k) e[k][c] = relax_apply(x[k][c], r, ls, HB, b4[c], p[k]);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < RB; ++k) {
+          const v4f l4 = reinterpret_cast<const v4f*>(lo + dr[k] * n)[i];
+          const v4f h4 = reinterpret_cast<const v4f*>(hi + dr[k] * n)[i];
+          v4f a4 = {0.f, 0.f, 0.f, 0.f}, b4 = {0.f, 0.f, 0.f, 0.f};
+          if (HA) a4 = reinterpret_cast<const v4f*>(alpha + (alpha_per_row ? mr[k] : dr[k]) * n)[i];
+          if (HB) b4 = reinterpret_cast<const v4f*>(beta + dr[k] * n)[i];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const Relax r = relax(l4[c], h4[c]);
+            e[k][c] = relax_apply(x[k][c], r, lo_slope(r, HA, a4[c]), HB, b4[c], p[k]);
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < RB; ++k)
+        __builtin_nontemporal_store(e[k], reinterpret_cast<v4f*>(out + mr[k] * n) + i);
+    }
+#pragma unroll
+    for (int k = 0; k < RB; ++k) {
+      const double t = wave_sum_f64(p[k]);
+      if (lane == 0) red[wv][k] = t;
+    }
+    __syncthreads();
+    if (threadIdx.x < RB && m0 + threadIdx.x < M) {
+      const int k = threadIdx.x;
+      const double t = (red[0][k] + red[1][k]) + (red[2][k] + red[3][k]);
+      acc[m0 + k] = (float)((double)acc[m0 + k] + t);
+    }
+    __syncthreads();
+  }
 }
 
 __global__ void k_crown_intersect(const float* sl, const int32_t* idx, int k, int64_t B,
@@ -413,8 +642,8 @@ __global__ void k_best_update(float* best, const float* lb, int64_t n, int init,
 
 __global__ void k_closure(const float* lb, int64_t B, int Q, const int32_t* dptr,
                           const int32_t* qidx, int nd, uint8_t* closed) {
-  const int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (b >= B) return;
+  for (int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; b < B;
+       b += (int64_t)gridDim.x * blockDim.x) {
   bool all = true;
   for (int d = 0; d < nd; ++d) {
     bool any = false;
@@ -422,6 +651,7 @@ __global__ void k_closure(const float* lb, int64_t B, int Q, const int32_t* dptr
     all &= any;
   }
   closed[b] = all;
+  }
 }
 
 // One thread per domain.  For each disjunct D: total_q = pos(A_q).xl +
@@ -454,8 +684,8 @@ constexpr int CLIP_MAXQ = 64;
 __global__ void k_clip(const float* xl, const float* xh, const float* A, const float* bv,
                        int64_t B, int Q, int n, const int32_t* dptr, const int32_t* qidx,
                        int nd, float* xlo, float* xho, uint8_t* feas) {
-  const int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (b >= B) return;
+  for (int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; b < B;
+       b += (int64_t)gridDim.x * blockDim.x) {
   const float* Ab = A + b * (int64_t)Q * n;
   const float* bb = bv + b * (int64_t)Q;
   const float* l = xl + b * n;
@@ -463,10 +693,10 @@ __global__ void k_clip(const float* xl, const float* xh, const float* A, const f
   float* lo_o = xlo + b * n;
   float* hi_o = xho + b * n;
   float tot[CLIP_MAXQ];
-  bool any_feas = false;
+  bool any_feas = false, single = false;
   for (int d = 0; d < nd; ++d) {
     const int32_t* qs = qidx + dptr[d];
-    const int nq = dptr[d + 1] - dptr[d];
+    const int nq = min(dptr[d + 1] - dptr[d], CLIP_MAXQ);
     bool empty = false;
     for (int t = 0; t < nq; ++t) {
       const int q = qs[t];
@@ -488,7 +718,8 @@ __global__ void k_clip(const float* xl, const float* xh, const float* A, const f
     if (nd == 1) {
       for (int i = 0; i < n; ++i) clip_dim(Ab, bb, tot, qs, nq, n, i, l[i], h[i], lo_o[i], hi_o[i]);
       feas[b] = fd;
-      return;
+      single = true;
+      break;
     }
     if (fd) {
       for (int i = 0; i < n; ++i) {
@@ -505,6 +736,7 @@ __global__ void k_clip(const float* xl, const float* xh, const float* A, const f
       any_feas = true;
     }
   }
+  if (single) continue;
   if (!any_feas) {
     for (int i = 0; i < n; ++i) {
       lo_o[i] = l[i];
@@ -512,6 +744,121 @@ __global__ void k_clip(const float* xl, const float* xh, const float* A, const f
     }
   }
   feas[b] = any_feas;
+  }
+}
+
+// Boxes of at most NMAX dims: one thread per box.  The workgroup's rows of
+// A and b are copied to LDS with coalesced loads (one record of Q n + Q
+// floats per box, odd stride: conflict-free); the box, the per-dimension
+// running bounds and the union live in registers (loops over dims fully
+// unrolled), and each query's total is formed inside the query loop.  Same
+// arithmetic, in the same order per value, as k_clip / clip_dim.
+template <int NMAX>
+__global__ __launch_bounds__(64) void k_clip_reg(const float* xl, const float* xh,
+                                                 const float* A, const float* bv, int64_t B,
+                                                 int Q, int n, const int32_t* dptr,
+                                                 const int32_t* qidx, int nd, float* xlo,
+                                                 float* xho, uint8_t* feas) {
+  extern __shared__ float rec[];
+  const int qn = Q * n, w = qn + Q, rs = w | 1;
+  const float invw = 1.f / (float)w;
+  const int t = threadIdx.x;
+  const float* Ab = rec + t * rs;
+  const float* bb = Ab + qn;
+  for (int64_t b0 = (int64_t)blockIdx.x * 64; b0 < B; b0 += (int64_t)gridDim.x * 64) {
+    const int nb = (int)min((int64_t)64, B - b0);
+    // record r = [A row (Q n) | b row (Q)]; i = r w + c, c < w: the float
+    // quotient is at least 0.5 / w from an integer, far above its rounding
+    for (int i = t; i < nb * w; i += 64) {
+      const int r = (int)((i + 0.5f) * invw);
+      const int c = i - r * w;
+      rec[r * rs + c] = c < qn ? A[(b0 + r) * qn + c] : bv[(b0 + r) * Q + (c - qn)];
+    }
+    __syncthreads();
+    if (t < nb) {
+      const int64_t b = b0 + t;
+      float l[NMAX], h[NMAX], ol[NMAX], oh[NMAX];
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) {
+        l[i] = i < n ? xl[b * n + i] : 0.f;
+        h[i] = i < n ? xh[b * n + i] : 0.f;
+        ol[i] = l[i];
+        oh[i] = h[i];
+      }
+      bool any_feas = false;
+      for (int d = 0; d < nd; ++d) {
+        const int32_t* qs = qidx + dptr[d];
+        const int nq = dptr[d + 1] - dptr[d];
+        float hm[NMAX], lm[NMAX];
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          hm[i] = INFINITY;
+          lm[i] = -INFINITY;
+        }
+        bool empty = false;
+        for (int k = 0; k < nq; ++k) {
+          const int q = qs[k];
+          const float* aq = Ab + q * n;
+          float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+          for (int i = 0; i < NMAX; ++i) {
+            if (i < n) {
+              const float a = aq[i];
+              s1 += fmaxf(a, 0.f) * l[i];
+              s2 += fminf(a, 0.f) * h[i];
+            }
+          }
+          const float tq = s1 + s2;
+          const float bq = bb[q];
+          empty |= (tq + bq) > 0.f;
+#pragma unroll
+          for (int i = 0; i < NMAX; ++i) {
+            if (i < n) {
+              const float a = aq[i];
+              const float contrib = fmaxf(a, 0.f) * l[i] + fminf(a, 0.f) * h[i];
+              const float other = tq - contrib;
+              const float safe = fabsf(a) > 1e-12f ? a : 1.f;
+              const float thr = (-bq - other) / safe;
+              hm[i] = fminf(hm[i], a > 1e-12f ? thr : h[i]);
+              lm[i] = fmaxf(lm[i], a < -1e-12f ? thr : l[i]);
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < NMAX; ++i) {
+          hm[i] = fminf(hm[i], h[i]);
+          lm[i] = fmaxf(lm[i], l[i]);
+          if (i < n) empty |= lm[i] > hm[i];
+        }
+        if (nd == 1) {
+#pragma unroll
+          for (int i = 0; i < NMAX; ++i) {
+            ol[i] = lm[i];
+            oh[i] = hm[i];
+          }
+          any_feas = !empty;
+          break;
+        }
+        if (!empty) {
+#pragma unroll
+          for (int i = 0; i < NMAX; ++i) {
+            ol[i] = any_feas ? fminf(ol[i], lm[i]) : lm[i];
+            oh[i] = any_feas ? fmaxf(oh[i], hm[i]) : hm[i];
+          }
+          any_feas = true;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < NMAX; ++i) {
+        if (i < n) {
+          xlo[b * n + i] = ol[i];
+          xho[b * n + i] = oh[i];
+        }
+      }
+      feas[b] = any_feas;
+    }
+    __syncthreads();
+  }
 }
 
 // ---- compaction: ascending positions of non-zero flags -------------------
@@ -628,8 +975,8 @@ __global__ void k_scatter_rows(const float* in, const int64_t* idx, int64_t nr, 
 // First index of the maximum width (NaN counts as maximal, like argmax).
 __global__ void k_widest(const float* xl, const float* xh, int64_t B, int n, int64_t* ax,
                          uint8_t* usable) {
-  const int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (b >= B) return;
+  for (int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; b < B;
+       b += (int64_t)gridDim.x * blockDim.x) {
   int best = 0;
   float bw = xh[b * n] - xl[b * n];
   if (!isnan(bw)) {
@@ -648,6 +995,7 @@ __global__ void k_widest(const float* xl, const float* xh, int64_t B, int n, int
   }
   ax[b] = best;
   if (usable) usable[b] = (xh[b * n + best] - xl[b * n + best]) > 1e-12f;
+  }
 }
 
 __global__ void k_bisect(const float* xl, const float* xh, const int64_t* ax,
@@ -734,12 +1082,15 @@ extern "C" int vc_concretize(const float* A, const float* acc, const float* xl,
   if (!A || !acc || !xl || !xh || !lb || R <= 0 || n_in <= 0 || M < 0 || M % R) return VC_ERR_ARG;
   if (M == 0) return VC_OK;
   hipStream_t st = (hipStream_t)stream;
-  if (n_in <= 32) {
-    hipLaunchKernelGGL(k_concretize_thread, dim3(vc_blocks(M, NT)), dim3(NT), 0, st, A, a_bcast,
+  if (n_in <= CT_MAXN) {
+    hipLaunchKernelGGL(k_concretize_thread, dim3(vc_blocks(M, CT)), dim3(CT), 0, st, A, a_bcast,
                        acc, xl, xh, M, R, n_in, lb);
+  } else if (n_in % 4 == 0 && aligned16(A) && aligned16(xl) && aligned16(xh)) {
+    hipLaunchKernelGGL(k_concretize_wave<true>, dim3(vc_blocks((M + CR - 1) / CR * 64, NT)),
+                       dim3(NT), 0, st, A, a_bcast, acc, xl, xh, M, R, n_in, lb);
   } else {
-    hipLaunchKernelGGL(k_concretize_wave, dim3(vc_blocks(M * 64, NT)), dim3(NT), 0, st, A,
-                       a_bcast, acc, xl, xh, M, R, n_in, lb);
+    hipLaunchKernelGGL(k_concretize_wave<false>, dim3(vc_blocks((M + CR - 1) / CR * 64, NT)),
+                       dim3(NT), 0, st, A, a_bcast, acc, xl, xh, M, R, n_in, lb);
   }
   VC_LAUNCH_CHECK();
   return VC_OK;
@@ -752,9 +1103,29 @@ extern "C" int vc_backward_relu(const float* ew_in, int64_t M, int R, int n,
   if (!ew_in || !relu_lo || !relu_hi || !ew_out || !acc || R <= 0 || n <= 0 || M < 0 || M % R)
     return VC_ERR_ARG;
   if (M == 0) return VC_OK;
-  hipLaunchKernelGGL(k_backward_relu, dim3(vc_blocks(M * 64, NT)), dim3(NT), 0,
-                     (hipStream_t)stream, ew_in, M, R, n, relu_lo, relu_hi, alpha,
-                     alpha_per_row, beta, ew_out, acc);
+  const bool vec = n % 4 == 0 && aligned16(ew_in) && aligned16(relu_lo) && aligned16(relu_hi) &&
+                   aligned16(ew_out) && (!alpha || aligned16(alpha)) && (!beta || aligned16(beta));
+  if (vec && n >= 1024) {
+    const dim3 grid(vc_blocks((M + RB - 1) / RB, 1));
+    hipStream_t st = (hipStream_t)stream;
+    if (alpha && beta)
+      hipLaunchKernelGGL((k_backward_relu_rows<true, true>), grid, dim3(256), 0, st, ew_in, M, R,
+                         n, relu_lo, relu_hi, alpha, alpha_per_row, beta, ew_out, acc);
+    else if (alpha)
+      hipLaunchKernelGGL((k_backward_relu_rows<true, false>), grid, dim3(256), 0, st, ew_in, M, R,
+                         n, relu_lo, relu_hi, alpha, alpha_per_row, beta, ew_out, acc);
+    else if (beta)
+      hipLaunchKernelGGL((k_backward_relu_rows<false, true>), grid, dim3(256), 0, st, ew_in, M, R,
+                         n, relu_lo, relu_hi, alpha, alpha_per_row, beta, ew_out, acc);
+    else
+      hipLaunchKernelGGL((k_backward_relu_rows<false, false>), grid, dim3(256), 0, st, ew_in, M,
+                         R, n, relu_lo, relu_hi, alpha, alpha_per_row, beta, ew_out, acc);
+    VC_LAUNCH_CHECK();
+    return VC_OK;
+  }
+  hipLaunchKernelGGL(vec ? k_backward_relu<true> : k_backward_relu<false>,
+                     dim3(vc_blocks((M + 1) / 2 * 64, NT)), dim3(NT), 0, (hipStream_t)stream,
+                     ew_in, M, R, n, relu_lo, relu_hi, alpha, alpha_per_row, beta, ew_out, acc);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }
@@ -956,8 +1327,18 @@ extern "C" int vc_clip_box(const float* xl, const float* xh, const float* A, con
   if (B < 0 || Q <= 0 || n <= 0 || n_disj <= 0) return VC_ERR_ARG;
   if (Q > CLIP_MAXQ) return VC_ERR_UNSUPPORTED;
   if (B == 0) return VC_OK;
-  hipLaunchKernelGGL(k_clip, dim3(vc_blocks(B, 64)), dim3(64), 0, (hipStream_t)stream, xl, xh,
-                     A, b, B, Q, n, d_ptr, q_idx, n_disj, xl_out, xh_out, feasible);
+  const size_t rec_bytes = 64 * (size_t)((Q * n + Q) | 1) * sizeof(float);
+  if (n <= 8 && rec_bytes <= 32768)
+    hipLaunchKernelGGL(k_clip_reg<8>, dim3(vc_blocks(B, 64)), dim3(64), rec_bytes,
+                       (hipStream_t)stream, xl, xh, A, b, B, Q, n, d_ptr, q_idx, n_disj, xl_out,
+                       xh_out, feasible);
+  else if (n <= 16 && rec_bytes <= 32768)
+    hipLaunchKernelGGL(k_clip_reg<16>, dim3(vc_blocks(B, 64)), dim3(64), rec_bytes,
+                       (hipStream_t)stream, xl, xh, A, b, B, Q, n, d_ptr, q_idx, n_disj, xl_out,
+                       xh_out, feasible);
+  else
+    hipLaunchKernelGGL(k_clip, dim3(vc_blocks(B, 64)), dim3(64), 0, (hipStream_t)stream, xl, xh,
+                       A, b, B, Q, n, d_ptr, q_idx, n_disj, xl_out, xh_out, feasible);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }

@@ -13,16 +13,17 @@ constexpr int NT = 256;
 __global__ void k_zono_bounds(const float* c, const float* G, int64_t rows, int K, float* lo,
                               float* hi, int32_t* flag) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
-  if (row >= rows) return;
-  KSum ks;
-  for (int k = lane; k < K; k += 64) ks.add(fabsf(G[row * K + k]));
-  const float s = wave_sum_comp(ks);
-  if (lane == 0) {
-    const float l = c[row] - s, h = c[row] + s;
-    lo[row] = l;
-    hi[row] = h;
-    flag[row] = (l < 0.f && h > 0.f) ? 1 : 0;
+  for (int64_t row = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6; row < rows;
+       row += ((int64_t)gridDim.x * blockDim.x) >> 6) {
+    KSum ks;
+    for (int k = lane; k < K; k += 64) ks.add(fabsf(G[row * K + k]));
+    const float s = wave_sum_comp(ks);
+    if (lane == 0) {
+      const float l = c[row] - s, h = c[row] + s;
+      lo[row] = l;
+      hi[row] = h;
+      flag[row] = (l < 0.f && h > 0.f) ? 1 : 0;
+    }
   }
 }
 
@@ -97,11 +98,11 @@ extern "C" int vc_zono_relu_bounds(const float* c, const float* G, int64_t B, in
   if (!c || !lo || !hi || !rank || !cnt || B < 0 || n <= 0 || K < 0) return VC_ERR_ARG;
   if (K > 0 && !G) return VC_ERR_ARG;
   if (B == 0) return VC_OK;
+  if (B > 2147483647LL) return VC_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
   const int64_t rows = B * (int64_t)n;
   hipLaunchKernelGGL(k_zono_bounds, dim3(vc_blocks(rows * 64, NT)), dim3(NT), 0, st, c, G,
                      rows, K, lo, hi, rank);
-  if (B > 2147483647LL) return VC_ERR_ARG;
   hipLaunchKernelGGL(k_zono_rank, dim3((unsigned)B), dim3(NT), 0, st, rank, n, cnt);
   VC_LAUNCH_CHECK();
   return VC_OK;

@@ -158,10 +158,12 @@ def zono_bounds(plan, xl, xh, fallback):
     if bad.numel() > 0:
         sub = fallback(_gather(xl, bad), _gather(xh, bad))
         for L in range(plan.n):
-            call('vc_scatter_rows', ptr(sub[L][0].contiguous()), ptr(bad), bad.numel(),
-                 plan.dims[L + 1], ptr(lo[L]), stream())
-            call('vc_scatter_rows', ptr(sub[L][1].contiguous()), ptr(bad), bad.numel(),
-                 plan.dims[L + 1], ptr(hi[L]), stream())
+            # the sources are held in locals until both launches are queued
+            s_lo, s_hi = sub[L][0].contiguous(), sub[L][1].contiguous()
+            call('vc_scatter_rows', ptr(s_lo), ptr(bad), bad.numel(), plan.dims[L + 1],
+                 ptr(lo[L]), stream())
+            call('vc_scatter_rows', ptr(s_hi), ptr(bad), bad.numel(), plan.dims[L + 1],
+                 ptr(hi[L]), stream())
     return {L: (lo[L], hi[L]) for L in range(plan.n)}, int(bad.numel())
 
 
