@@ -275,7 +275,9 @@ def kernel_suite(reps):
            '524,288 flags, half set', _time_launches([fn], reps), 'hbm', 2 * B + 8 * cnt_true)
     del flags, ws, cidx
 
-    # -- a5 + a6: backward through fc with the relaxation fused (fp32 MFMA)
+    # -- a5 + a6: backward through relu -> fc (fp32 MFMA): the two-phase
+    #    step the layer-wise path runs (k_relax_rows streams the relaxed rows,
+    #    then the plain gemm_kernel), and the fused single-kernel form
     for B, R, n_out, n_in, what in (
             (512, 512, 1024, 1024, '1024x1024 fc, 512 domains x 512 seeded rows'),
             (8192, 9, 256, 256, '256x256 fc, 8,192 domains x 9 spec rows')):
@@ -286,11 +288,35 @@ def kernel_suite(reps):
         bias = rndn(n_out) * 0.01
         out = torch.empty(M, n_in, device=dev)
         acc = torch.zeros(M, device=dev)
-        fn = lambda: call('vc_backward_fc', ptr(ew), M, R, n_out, ptr(lo), ptr(hi), None, 0,
-                          None, ptr(W), ptr(bias), n_in, ptr(out), ptr(acc), None, 0, st)
-        report('a5', 'gemm_kernel (backward fc + relaxation)', what,
-               _time_launches([fn], max(3, reps // 4)), 'mfma', 2.0 * M * n_out * n_in)
-        del ew, out, acc
+        rel = torch.empty(M, n_out, device=dev)
+        for kern, r in (('k_relax_rows + gemm_kernel (two-phase backward fc)', rel),
+                        ('gemm_kernel (fused relaxation + backward fc)', None)):
+            fn = lambda r=r: call('vc_backward_fc', ptr(ew), M, R, n_out, ptr(lo), ptr(hi), None,
+                                  0, None, ptr(W), ptr(bias), n_in, ptr(out), ptr(acc), ptr(r),
+                                  0, st)
+            report('a5', kern, what, _time_launches([fn], max(3, reps // 4)), 'mfma',
+                   2.0 * M * n_out * n_in)
+        del ew, out, acc, rel
+
+    # -- a9: alpha gradient sweep step (relaxation subgradient + fc^T)
+    B, Q, n, n_next = 512, 9, 1024, 1024
+    M = B * Q
+    gE, P = rndn(M, n), rndn(M, n)
+    lo, hi = bounds(B, n)
+    alpha = rnd(B, n)
+    Wn = rndn(n_next, n) * (2.0 / n) ** 0.5
+    ls, us, ut = (torch.empty(B, n, device=dev) for _ in range(3))
+    g2 = torch.empty(M, n_next, device=dev)
+
+    def grad_step():
+        call('vc_relax_slopes', ptr(lo), ptr(hi), ptr(alpha), B * n, ptr(ls), ptr(us), ptr(ut),
+             st)
+        call('vc_alpha_grad_step_slopes', ptr(gE), ptr(P), M, Q, n, ptr(ls), ptr(us), ptr(ut),
+             0, ptr(Wn), None, n_next, ptr(g2), st)
+    report('a9', 'k_relax_slopes + gemm_kernel (alpha gradient step)',
+           '1024x1024 fc, 512 domains x 9 spec rows', _time_launches([grad_step], reps), 'mfma',
+           2.0 * M * n * n_next)
+    del gE, P, g2
 
     # -- a2: interval fc (two products: mid W^T, rad |W|^T)
     B, n_in, n_out = 8192, 784, 256

@@ -134,8 +134,12 @@ int vc_zono_relu_apply(const float *c, const float *G, const float *lo,
  *   lower slope; beta (B, n_out) is optional.  Then
  *       acc += e . bias (bias nullable),  ew_out (M, n_in) = e W,
  *   with W (n_out, n_in).  When relax_out is non-NULL the relaxed rows e
- *   are also written there (M, n_out).  With ew_bcast != 0, ew_in is (R,
- *   n_out) and shared by every domain (row m reads row m % R).
+ *   are also written there (M, n_out); with a relu and n_out >= 64 the step
+ *   then runs in two phases (the relaxation streams e into relax_out, and a
+ *   plain MFMA GEMM reads it back), which is faster than relaxing inside
+ *   the GEMM's loads, so callers that can spare the buffer should pass it.
+ *   With ew_bcast != 0, ew_in is (R, n_out) and shared by every domain
+ *   (row m reads row m % R).
  * Replaces the fc and relu branches of _spec_backward_graph_batched
  * (verify_zono_bnb.py:4379-4453). */
 int vc_backward_fc(const float *ew_in, int64_t M, int R, int n_out,
@@ -144,6 +148,16 @@ int vc_backward_fc(const float *ew_in, int64_t M, int R, int n_out,
                    const float *W, const float *bias, int n_in, float *ew_out,
                    float *acc, float *relax_out, int ew_bcast,
                    vc_stream_t stream);
+
+/* Slopes of a relu layer for the backward, elementwise over n (= B * n_L)
+ * pre-activation bounds: lo_s = active + unstable * alpha when alpha (same
+ * layout) is non-NULL, else the adaptive lower slope; up_s, up_t as in
+ * _make_slopes (verify_zono_bnb.py:503-522, with the alpha override of
+ * verify_zono_bnb.py:4422-4433).  Feeds vc_alpha_grad_step_slopes, which
+ * then does no per-element division. */
+int vc_relax_slopes(const float *relu_lo, const float *relu_hi,
+                    const float *alpha, int64_t n, float *lo_s, float *up_s,
+                    float *up_t, vc_stream_t stream);
 
 /* relu backward step alone (for a relu that is not fed by an fc):
  * ew_out (M, n) = relaxed rows, acc += neg(ew) . up_t.  Same arguments as
@@ -205,6 +219,16 @@ int vc_alpha_grad_step(const float *gE, const float *P, int64_t M, int R, int n,
                        const float *alpha, int p_bcast, const float *W_next,
                        const float *bias_next, int n_next, float *g_out,
                        vc_stream_t stream);
+
+/* vc_alpha_grad_step with the relaxation given as slopes (B, n) from
+ * vc_relax_slopes (lo_s carries the alpha override).  Bit-identical to
+ * vc_alpha_grad_step on the bounds and alpha the slopes came from. */
+int vc_alpha_grad_step_slopes(const float *gE, const float *P, int64_t M,
+                              int R, int n, const float *lo_s,
+                              const float *up_s, const float *up_t,
+                              int p_bcast, const float *W_next,
+                              const float *bias_next, int n_next,
+                              float *g_out, vc_stream_t stream);
 
 /* d lb / d alpha for one layer: galpha[b, j] = sum over the R rows of b of
  * gE[m, j] * pos(P[m, j]), zero where the neuron is not unstable;

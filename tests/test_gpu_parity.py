@@ -129,6 +129,120 @@ def test_gemm_mfma_layout_against_fp64(gpu):
         assert bool(((cpu(acc_g) - ref_acc).abs() <= 1e-5 * (acc.abs() + ew.abs() @ b.abs()) + 1e-6).all())
 
 
+def _relaxed_rows_oracle(ew, B, R, lo, hi, alpha, alpha_row, beta):
+    """Relaxed rows (M, n) and the relu's acc term in the oracle's fp32
+    arithmetic (oracle.ref_bound.spec_backward_batched's relu branch)."""
+    n = ew.shape[1]
+    lo_s, up_s, up_t, act, dead, uns = rb.make_slopes(lo, hi)
+    e3 = ew.reshape(B, R, n)
+    ep, en = e3.clamp(min=0), e3.clamp(max=0)
+    if alpha is None:
+        ls = lo_s.unsqueeze(1)
+    elif alpha_row:
+        ls = act.float().unsqueeze(1) + uns.float().unsqueeze(1) * alpha.reshape(B, R, n)
+    else:
+        ls = (act.float() + uns.float() * alpha).unsqueeze(1)
+    back = ep * ls + en * up_s.unsqueeze(1)
+    if beta is not None:
+        back = back + beta.unsqueeze(1)
+    return back.reshape(B * R, n), (en.double() * up_t.double().unsqueeze(1)).sum(-1).reshape(-1)
+
+
+@pytest.mark.parametrize('B,R,n_out,n_in,bcast,alpha_mode,with_beta', [
+    (7, 9, 256, 96, 0, None, False),      # float4 path, M % 4 != 0
+    (5, 3, 66, 70, 0, 'dom', True),       # scalar path (n_out % 4 != 0)
+    (6, 16, 128, 64, 1, None, False),     # rows shared by every domain
+    (4, 5, 80, 50, 0, 'row', True),       # per-row alpha
+    (3, 130, 1024, 33, 0, 'dom', False),  # rows of one domain over many row groups
+])
+def test_backward_fc_two_phase(gpu, B, R, n_out, n_in, bcast, alpha_mode, with_beta):
+    """vc_backward_fc with a relaxed-rows buffer (relaxation pass + plain
+    GEMM): the relaxed rows bit-exact with the oracle's fp32 relaxation, the
+    product and acc against fp64, and the fused single-kernel form
+    (no buffer) within the bound tolerance."""
+    g = torch.Generator().manual_seed(B * 1000 + n_out)
+    M = B * R
+    ew_rows = torch.randn(R if bcast else M, n_out, generator=g)
+    ew = ew_rows.repeat(B, 1) if bcast else ew_rows
+    lo = torch.randn(B, n_out, generator=g)
+    hi = lo + torch.rand(B, n_out, generator=g) * 2
+    lo[0, :5] = 0.0
+    hi[0, 5:9] = 0.0
+    alpha = None
+    if alpha_mode == 'dom':
+        alpha = torch.rand(B, n_out, generator=g)
+    elif alpha_mode == 'row':
+        alpha = torch.rand(M, n_out, generator=g)
+    beta = torch.randn(B, n_out, generator=g) * 0.1 if with_beta else None
+    W = torch.randn(n_out, n_in, generator=g) / n_out ** 0.5
+    b = torch.randn(n_out, generator=g) * 0.1
+    acc0 = torch.randn(M, generator=g)
+    rel_ref, up_part = _relaxed_rows_oracle(ew, B, R, lo, hi, alpha, alpha_mode == 'row', beta)
+    out_ref = rel_ref.double() @ W.double()
+    acc_ref = acc0.double() + up_part + rel_ref.double() @ b.double()
+    st = torch.cuda.current_stream().cuda_stream
+    d = {k: (v.to(gpu) if v is not None else None) for k, v in
+         dict(ew=ew_rows, lo=lo, hi=hi, alpha=alpha, beta=beta, W=W, b=b).items()}
+    outs = {}
+    for mode in ('two_phase', 'fused'):
+        out = torch.empty(M, n_in, device=gpu)
+        acc = acc0.to(gpu)
+        rel = torch.empty(M, n_out, device=gpu) if mode == 'two_phase' else None
+        call('vc_backward_fc', ptr(d['ew']), M, R, n_out, ptr(d['lo']), ptr(d['hi']),
+             ptr(d['alpha']), 1 if alpha_mode == 'row' else 0, ptr(d['beta']), ptr(d['W']),
+             ptr(d['b']), n_in, ptr(out), ptr(acc), ptr(rel), bcast, st)
+        torch.cuda.synchronize()
+        outs[mode] = (cpu(out), cpu(acc))
+        if rel is not None:
+            assert torch.equal(cpu(rel), rel_ref), 'relaxed rows differ from the oracle'
+    sc_out = rel_ref.abs().double() @ W.abs().double()
+    sc_acc = acc0.abs().double() + up_part.abs() + rel_ref.abs().double() @ b.abs().double()
+    for mode, (out, acc) in outs.items():
+        assert bool(((out.double() - out_ref).abs() <= 1e-6 + 1e-5 * sc_out).all()), mode
+        assert bool(((acc.double() - acc_ref).abs() <= 1e-6 + 1e-5 * sc_acc).all()), mode
+    d_out = (outs['two_phase'][0] - outs['fused'][0]).double().abs()
+    assert bool((d_out <= 1e-6 + 1e-5 * sc_out).all())
+
+
+def test_alpha_grad_step_slopes_matches_bounds_form(gpu):
+    """vc_relax_slopes bit-exact with the oracle's make_slopes (alpha
+    override applied), and the sweep step from slopes equal to the one from
+    bounds within the bound tolerance, both against fp64."""
+    g = torch.Generator().manual_seed(11)
+    B, Q, n, n_next = 37, 9, 132, 70
+    M = B * Q
+    gE = torch.randn(M, n, generator=g)
+    P = torch.randn(M, n, generator=g)
+    P[:, :4] = 0.0                         # clamp subgradient at 0: both sides
+    lo = torch.randn(B, n, generator=g)
+    hi = lo + torch.rand(B, n, generator=g) * 2
+    al = torch.rand(B, n, generator=g)
+    W = torch.randn(n_next, n, generator=g) / n ** 0.5
+    b = torch.randn(n_next, generator=g) * 0.1
+    lo_s, up_s, up_t, act, dead, uns = rb.make_slopes(lo, hi)
+    ls_ref = act.float() + uns.float() * al
+    d = {k: v.to(gpu) for k, v in dict(gE=gE, P=P, lo=lo, hi=hi, al=al, W=W, b=b).items()}
+    st = torch.cuda.current_stream().cuda_stream
+    ls, us, ut = (torch.empty(B, n, device=gpu) for _ in range(3))
+    call('vc_relax_slopes', ptr(d['lo']), ptr(d['hi']), ptr(d['al']), B * n, ptr(ls), ptr(us),
+         ptr(ut), st)
+    g1 = torch.empty(M, n_next, device=gpu)
+    g2 = torch.empty(M, n_next, device=gpu)
+    call('vc_alpha_grad_step_slopes', ptr(d['gE']), ptr(d['P']), M, Q, n, ptr(ls), ptr(us),
+         ptr(ut), 0, ptr(d['W']), ptr(d['b']), n_next, ptr(g1), st)
+    call('vc_alpha_grad_step', ptr(d['gE']), ptr(d['P']), M, Q, n, ptr(d['lo']), ptr(d['hi']),
+         ptr(d['al']), 0, ptr(d['W']), ptr(d['b']), n_next, ptr(g2), st)
+    torch.cuda.synchronize()
+    assert torch.equal(cpu(ls), ls_ref) and torch.equal(cpu(us), up_s) and torch.equal(cpu(ut), up_t)
+    mp, mn = (P >= 0).reshape(B, Q, n), (P <= 0).reshape(B, Q, n)
+    f = mp * ls_ref.unsqueeze(1) + mn * up_s.unsqueeze(1)
+    gP = gE.reshape(B, Q, n) * f + mn * up_t.unsqueeze(1)
+    ref = gP.reshape(M, n).double() @ W.double().T + b.double()
+    sc = gP.reshape(M, n).abs().double() @ W.abs().double().T + b.abs().double()
+    for got in (g1, g2):
+        assert bool(((cpu(got).double() - ref).abs() <= 1e-6 + 1e-5 * sc).all())
+
+
 # ----------------------------------------------------------------- a1
 def test_make_slopes_bit_exact(gpu):
     g = torch.Generator().manual_seed(1)

@@ -144,6 +144,21 @@ __device__ __forceinline__ double row_sum16(double v) {
   return v;
 }
 
+// Sum over the wave (every lane active): DPP row sums, then the four row
+// totals read from lanes 0, 16, 32, 48 and added in a fixed order.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  v = row_sum16(v);
+  const long long b = __double_as_longlong(v);
+  double r[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), 16 * k);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), 16 * k);
+    r[k] = __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+  }
+  return (r[0] + r[1]) + (r[2] + r[3]);
+}
+
 // The value of lane 16 g (row position 0) in every lane of row g (exact:
 // the other lanes contribute zeros).
 __device__ __forceinline__ float row_bcast0(float v, int r) { return row_sum16(r == 0 ? v : 0.f); }

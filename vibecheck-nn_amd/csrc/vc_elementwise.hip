@@ -76,20 +76,6 @@ __device__ __forceinline__ double conc_term(float a, float l, float h) {
   return (double)(pos_part(a) * l + neg_part(a) * h);
 }
 
-// Sum over the wave (every lane active): DPP row sums, then the four row
-// totals read from lanes 0, 16, 32, 48 and added in a fixed order.
-__device__ __forceinline__ double wave_sum_f64(double v) {
-  v = row_sum16(v);
-  const long long b = __double_as_longlong(v);
-  double r[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), 16 * k);
-    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), 16 * k);
-    r[k] = __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
-  }
-  return (r[0] + r[1]) + (r[2] + r[3]);
-}
 
 // lb[m] = acc[m] + sum_i pos(A) xl + sum_i neg(A) xh.  One wave takes
 // CR = 4 consecutive rows at a time and keeps all their loads in flight.

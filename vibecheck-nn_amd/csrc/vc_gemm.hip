@@ -1,204 +1,584 @@
 // Generic fp32 MFMA GEMM with fused prologues/epilogues.
 //
-// C[m, n] = sum_k A[m, k] * B[k, n] on a 64x64 workgroup tile, BK = 16,
-// 256 threads = 4 waves in a 2x2 arrangement, each wave owning a 32x32
-// sub-tile of 2x2 blocks of v_mfma_f32_16x16x4_f32.  A and B tiles are
-// staged through LDS; the A loader is a functor, so the ReLU relaxation of
-// the CROWN backward (pos/neg split, slope select, acc += neg . up_t and
-// acc += e . bias) runs in registers while the tile is loaded.
+// C[m, n] = sum_k A[m, k] * B[k, n].  A workgroup of 256 threads (4 waves,
+// 2 x 2) owns a (32 FM) x (32 FN) tile; each wave owns (16 FM) x (16 FN) as
+// FM x FN blocks of v_mfma_f32_16x16x4_f32.  Three tile shapes are built:
+// 64x64, 128x64 and 128x128; the launcher picks the largest one that still
+// gives the chip several waves of workgroups.
+//
+// K runs in BK = 16 tiles through two LDS buffers: the global loads of tile
+// t+1 are issued into registers before the MFMAs of tile t, and the
+// loader's arithmetic (e.g. the ReLU relaxation of a CROWN backward row)
+// and the LDS store of tile t+1 follow them, so one barrier per tile.
+// Operands arrive as quads of 4 consecutive elements along their contiguous
+// dimension (one 16-byte load when the host found every stride and base
+// aligned).  Per-row index math (domain of a row, broadcast rows) is done
+// once per tile, not per element.
+//
+// Each K-tile is reduced by MFMA into a fresh fp32 accumulator and folded
+// into an fp64 running sum (two VALU ops per element), so the rounding
+// error does not grow with K: the result is the 16-term tile partials
+// summed exactly enough to round once at the end (the fp32 sums are at
+// least as accurate as a blocked CPU BLAS).
+//
+// Tiles are dealt so that the workgroups of one XCD (blocks b with the same
+// b mod 8) take consecutive tiles: the column tiles of one row block share
+// that XCD's L2 for the A rows.
+#include <initializer_list>
+
 #include "vc_common.h"
 #include "vc_relax.h"
 
 namespace {
 
-constexpr int BM = 64, BN = 64, BK = 16;
-constexpr int LDA_S = BM + 16;  // padded LDS row stride (bank spread)
-constexpr int LDB_S = BN + 16;
 constexpr int NT = 256;
+constexpr int PAD = 16;  // LDS row padding: MFMA fragment reads hit distinct banks
+
+// LDS row of element kk (0 .. BK-1) of a K-tile.  Quads deliver 4
+// consecutive k; element j of quad q is stored at row (BK/4) j + q, so the
+// quads of a row block land in different banks.  A and B use the same map;
+// the order of k inside a tile does not change the product.
+template <int BK>
+__device__ __forceinline__ int krow(int kk) { return (BK / 4) * (kk & 3) + (kk >> 2); }
+
+// p[0 .. n-1] into o[0..3] (n <= 4), zeros past n; one 16-byte load when
+// VEC and n == 4 (VEC: the host checked 16-byte alignment of every quad).
+template <bool VEC>
+__device__ __forceinline__ void ld4(const float* p, int n, float* o) {
+  if (VEC && n == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    o[0] = v.x;
+    o[1] = v.y;
+    o[2] = v.z;
+    o[3] = v.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[j] = 0.f;
+      if (j < n) o[j] = p[j];
+    }
+  }
+}
+
+__device__ __forceinline__ int clamp4(int64_t v) { return v <= 0 ? 0 : (v >= 4 ? 4 : (int)v); }
+
+// Workgroup b of n (1-D grid) -> tile index: the blocks that run on one
+// XCD (same b mod 8) get one contiguous range of tiles.
+__device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t n) {
+  const int64_t q = n >> 3, rem = n & 7;
+  const int64_t x = b & 7, i = b >> 3;
+  return x * q + (x < rem ? x : rem) + i;
+}
 
 // ---------------------------------------------------------------- core
-// NA: number of A operands (1, or 2 for the dual IBP product).
-// TRANS_B: B is given as Bt[n][k] (k contiguous) instead of B[k][n].
-// ACC_ROWS: the loader returns a per-element row contribution summed into
-//   acc[m] by the blockIdx.y == 0 column of tiles.
-template <int NA, bool TRANS_B, bool ACC_ROWS, class LA, class LB, class EP>
-__global__ __launch_bounds__(NT) void gemm_kernel(int64_t M, int N, int K,
-                                                   int tiles_n, LA la, LB lb,
-                                                   EP ep, float* acc_rows) {
-  __shared__ float As[NA][BK][LDA_S];
-  __shared__ float Bs[NA][BK][LDB_S];
+// NA: number of A/B operand pairs (1, or 2 for the dual IBP product).
+// ACC_ROWS: the A loader also returns a per-element row contribution,
+//   summed into acc_rows[m] by the first column tile of each row block.
+// LA (A loader): Row row(bz, m, first_col_tile); Raw; fetch<VEC>(row, k, n, raw);
+//   finish(row, k, n, raw, v[NA][4], KSum&) for the quad A[m][k .. k+n-1].
+// LB (B loader): kTrans (quads along k of Bt[n][k], else along n of B[k][n]);
+//   const float* ptr(bz, k, n); finish(raw[4], v[NA][4]).
+// EP (epilogue): operator()(bz, m, n, c[NA]).
+template <int NA, bool ACC_ROWS, int FM, int FN, int BK, bool VEC, class LA, class LB, class EP>
+__global__ __launch_bounds__(NT) void gemm_kernel(int64_t M, int N, int K, int tiles_n,
+                                                   int64_t tiles_m, int64_t n_tiles, LA la,
+                                                   LB lb, EP ep, float* acc_rows) {
+  constexpr int BM = 32 * FM, BN = 32 * FN;
+  constexpr int SA = BM + PAD, SB = BN + PAD;
+  constexpr int QR = BK / 4;     // quads per row of a K-tile
+  constexpr int RP = NT / QR;    // rows covered by one pass of the workgroup
+  constexpr int QA = BM / RP;    // A quads per thread per K-tile
+  constexpr int QB = BN / RP;    // B quads per thread per K-tile
+  static_assert(QA * RP == BM && QB * RP == BN, "tile / thread mismatch");
+  constexpr bool TB = LB::kTrans;
+  __shared__ __align__(16) float As[2][NA][BK][SA];
+  __shared__ __align__(16) float Bs[2][NA][BK][SB];
+
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int wm = w >> 1, wn = w & 1;
-  const int64_t bz = blockIdx.x / tiles_n;
-  const int bx = blockIdx.x % tiles_n;
-  const int64_t m0 = (int64_t)blockIdx.y * BM;
-  const int n0 = bx * BN;
+  const int q4 = tid % QR;  // quad slot along k (A, and B when transposed)
+  const int r4 = tid / QR;  // row (A) or column (transposed B) of the quad
 
-  // Running sums with TwoSum compensation: each BK-deep K-tile is reduced
-  // by MFMA into a fresh accumulator and then folded into (acc, cmp), so
-  // the rounding error no longer grows with K (the fp32 sums are at least
-  // as accurate as a blocked CPU BLAS).
-  v4f acc[NA][2][2], cmp[NA][2][2];
-#pragma unroll
-  for (int a = 0; a < NA; ++a)
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        acc[a][i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-        cmp[a][i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-      }
+  for (int64_t blk = blockIdx.x; blk < n_tiles; blk += gridDim.x) {
+    int64_t t = xcd_tile(blk, n_tiles);
+    const int tn = (int)(t % tiles_n);
+    t /= tiles_n;
+    const int64_t tm = t % tiles_m;
+    const int64_t bz = t / tiles_m;
+    const int64_t m0 = tm * BM;
+    const int n0 = tn * BN;
+    const bool do_rows = ACC_ROWS && tn == 0 && acc_rows != nullptr;
 
-  KSum rowpart[4];
-  const bool do_rows = ACC_ROWS && (bx == 0) && acc_rows != nullptr;
-
-  for (int k0 = 0; k0 < K; k0 += BK) {
+    typename LA::Row arow[QA];
+    bool aok[QA];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + NT * i;
-      const int mm = idx >> 4, kk = idx & 15;
-      const int64_t m = m0 + mm;
-      const int k = k0 + kk;
-      float v[NA];
-      float part = 0.f;
-      if (m < M && k < K) {
-        la(bz, m, k, v, part);
-      } else {
-#pragma unroll
-        for (int a = 0; a < NA; ++a) v[a] = 0.f;
-      }
-      if (do_rows) rowpart[i].add(part);
-#pragma unroll
-      for (int a = 0; a < NA; ++a) As[a][kk][mm] = v[a];
+    for (int p = 0; p < QA; ++p) {
+      const int64_t m = m0 + r4 + RP * p;
+      aok[p] = m < M;
+      arow[p] = la.row(bz, aok[p] ? m : m0, tn == 0);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + NT * i;
-      int kk, nn;
-      if (TRANS_B) {
-        nn = idx >> 4;
-        kk = idx & 15;
-      } else {
-        kk = idx >> 6;
-        nn = idx & 63;
-      }
-      const int k = k0 + kk, n = n0 + nn;
-      float v[NA];
-      if (k < K && n < N) {
-        lb(bz, k, n, v);
-      } else {
-#pragma unroll
-        for (int a = 0; a < NA; ++a) v[a] = 0.f;
-      }
-#pragma unroll
-      for (int a = 0; a < NA; ++a) Bs[a][kk][nn] = v[a];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int a = 0; a < NA; ++a) {
-      v4f t[2][2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) t[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < BK / 4; ++ks) {
-        float af[2], bf[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) af[i] = As[a][ks * 4 + g][wm * 32 + i * 16 + r];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) bf[j] = Bs[a][ks * 4 + g][wn * 32 + j * 16 + r];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) t[i][j] = mfma16x16x4(af[i], bf[j], t[i][j]);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float s = acc[a][i][j][e], c = cmp[a][i][j][e];
-            two_sum_acc(s, c, t[i][j][e]);
-            acc[a][i][j][e] = s;
-            cmp[a][i][j][e] = c;
-          }
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int a = 0; a < NA; ++a)
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[a][i][j] += cmp[a][i][j];
 
-  if (do_rows) {
+    double acc[NA][FM][FN][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float p = rowpart[i].value();
-      p += __shfl_xor(p, 8, 16);
-      p += __shfl_xor(p, 4, 16);
-      p += __shfl_xor(p, 2, 16);
-      p += __shfl_xor(p, 1, 16);
-      const int64_t m = m0 + ((tid + NT * i) >> 4);
-      if ((tid & 15) == 0 && m < M) acc_rows[m] += p;
-    }
-  }
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[a][i][j][e] = 0.0;
+    KSum rowpart[QA];
 
+    typename LA::Raw araw[QA];
+    int acnt[QA];
+    float braw[QB][4];
+    int bcnt[QB];
+
+    auto fetch = [&](int k0) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+      for (int p = 0; p < QA; ++p) {
+        const int k = k0 + 4 * q4;
+        acnt[p] = aok[p] ? clamp4((int64_t)K - k) : 0;
+        la.template fetch<VEC>(arow[p], k, acnt[p], araw[p]);
+      }
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int p = 0; p < QB; ++p) {
+        int k, n;
+        if (TB) {
+          n = n0 + r4 + RP * p;
+          k = k0 + 4 * q4;
+          bcnt[p] = n < N ? clamp4((int64_t)K - k) : 0;
+        } else {
+          const int qi = tid + NT * p;
+          k = k0 + qi / (BN / 4);
+          n = n0 + 4 * (qi % (BN / 4));
+          bcnt[p] = k < K ? clamp4((int64_t)N - n) : 0;
+        }
+        ld4<VEC>(bcnt[p] ? lb.ptr(bz, k, n) : nullptr, bcnt[p], braw[p]);
+      }
+    };
+
+    auto store = [&](int k0, int buf) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t m = m0 + wm * 32 + i * 16 + 4 * g + e;
-        const int n = n0 + wn * 32 + j * 16 + r;
-        if (m < M && n < N) {
-          float c[NA];
+      for (int p = 0; p < QA; ++p) {
+        float v[NA][4];
+        la.template finish<VEC>(arow[p], k0 + 4 * q4, acnt[p], araw[p], v, rowpart[p], do_rows);
+        const int mm = r4 + RP * p;
 #pragma unroll
-          for (int a = 0; a < NA; ++a) c[a] = acc[a][i][j][e];
-          ep(bz, m, n, c);
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) As[buf][a][QR * j + q4][mm] = v[a][j];
+      }
+#pragma unroll
+      for (int p = 0; p < QB; ++p) {
+        float v[NA][4];
+        LB::finish(braw[p], v);
+        if (TB) {
+          const int nn = r4 + RP * p;
+#pragma unroll
+          for (int a = 0; a < NA; ++a)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) Bs[buf][a][QR * j + q4][nn] = v[a][j];
+        } else {
+          const int qi = tid + NT * p;
+          const int kk = qi / (BN / 4), nn = 4 * (qi % (BN / 4));
+#pragma unroll
+          for (int a = 0; a < NA; ++a)
+            *reinterpret_cast<float4*>(&Bs[buf][a][krow<BK>(kk)][nn]) =
+                make_float4(v[a][0], v[a][1], v[a][2], v[a][3]);
         }
       }
+    };
+
+    fetch(0);
+    store(0, 0);
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = 0; k0 < K; k0 += BK) {
+      const bool more = k0 + BK < K;
+      if (more) fetch(k0 + BK);
+#pragma unroll
+      for (int a = 0; a < NA; ++a) {
+        v4f tt[FM][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) tt[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < BK / 4; ++ks) {
+          float af[FM], bf[FN];
+#pragma unroll
+          for (int i = 0; i < FM; ++i) af[i] = As[buf][a][4 * ks + g][wm * 16 * FM + 16 * i + r];
+#pragma unroll
+          for (int j = 0; j < FN; ++j) bf[j] = Bs[buf][a][4 * ks + g][wn * 16 * FN + 16 * j + r];
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) tt[i][j] = mfma16x16x4(af[i], bf[j], tt[i][j]);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[a][i][j][e] += (double)tt[i][j][e];
+      }
+      if (more) store(k0 + BK, buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+    }
+
+    if (do_rows) {
+#pragma unroll
+      for (int p = 0; p < QA; ++p) {
+        float v = rowpart[p].value();
+#pragma unroll
+        for (int o = 1; o < QR; o <<= 1) v += __shfl_xor(v, o, 64);
+        if (q4 == 0 && aok[p]) acc_rows[m0 + r4 + RP * p] += v;
+      }
+    }
+
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t m = m0 + wm * 16 * FM + i * 16 + 4 * g + e;
+          const int n = n0 + wn * 16 * FN + j * 16 + r;
+          if (m < M && n < N) {
+            float c[NA];
+#pragma unroll
+            for (int a = 0; a < NA; ++a) c[a] = (float)acc[a][i][j][e];
+            ep(bz, m, n, c);
+          }
+        }
+  }
 }
 
-template <int NA, bool TRANS_B, bool ACC_ROWS, class LA, class LB, class EP>
-int launch_gemm(int64_t batch, int64_t M, int N, int K, LA la, LB lb, EP ep,
-                float* acc_rows, hipStream_t st) {
+constexpr int64_t kMaxGrid = 1 << 20;  // workgroups; tiles beyond loop (a multiple of 8)
+
+// vc_backward_fc runs its two-phase form (relaxed rows through relax_out)
+// from this row width up; narrower rows keep the fused prologue.
+constexpr int kTwoPhaseMinWidth = 64;
+
+// One tile shape, 64x64 (FM = FN = 2), for every GEMM: measured on MI355X
+// against 128x64 and 128x128 at the workload shapes (1024-wide fc backward,
+// 256-wide spec backward, 784->256 interval fc, 1024x1024 zonotope
+// generators), the small tile wins everywhere, because it keeps 3-4 waves
+// per SIMD to cover the global-load latency.  The K-tile depth comes from
+// the A loader: 32 for plain loads (fewer barriers, the fold every 32 k),
+// 16 when the loader's per-element arithmetic holds more registers.
+template <int NA, bool ACC_ROWS, class LA, class LB, class EP>
+int launch_gemm(int64_t batch, int64_t M, int N, int K, LA la, LB lb, EP ep, float* acc_rows,
+                bool vec, hipStream_t st) {
   if (M <= 0 || N <= 0 || batch <= 0) return VC_OK;
+  constexpr int FM = 2, FN = 2, BM = 32 * FM, BN = 32 * FN, BK = LA::kBK;
   const int tiles_n = (N + BN - 1) / BN;
   const int64_t tiles_m = (M + BM - 1) / BM;
-  if (tiles_m > 2147483647LL || batch * tiles_n > 2147483647LL) return VC_ERR_ARG;
-  dim3 grid((unsigned)(batch * tiles_n), (unsigned)tiles_m);
-  hipLaunchKernelGGL((gemm_kernel<NA, TRANS_B, ACC_ROWS, LA, LB, EP>), grid,
-                     dim3(NT), 0, st, M, N, K, tiles_n, la, lb, ep, acc_rows);
+  const int64_t n_tiles = batch * tiles_m * tiles_n;
+  const int64_t grid = n_tiles < kMaxGrid ? n_tiles : kMaxGrid;
+  if (vec)
+    hipLaunchKernelGGL((gemm_kernel<NA, ACC_ROWS, FM, FN, BK, true, LA, LB, EP>),
+                       dim3((unsigned)grid), dim3(NT), 0, st, M, N, K, tiles_n, tiles_m, n_tiles,
+                       la, lb, ep, acc_rows);
+  else
+    hipLaunchKernelGGL((gemm_kernel<NA, ACC_ROWS, FM, FN, BK, false, LA, LB, EP>),
+                       dim3((unsigned)grid), dim3(NT), 0, st, M, N, K, tiles_n, tiles_m, n_tiles,
+                       la, lb, ep, acc_rows);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }
 
-// ------------------------------------------------------------- functors
+// every pointer 16-byte aligned and every stride a multiple of 4 floats
+static inline bool vec_ok(std::initializer_list<const void*> ptrs,
+                          std::initializer_list<int64_t> strides) {
+  for (const void* p : ptrs)
+    if (p && !aligned16(p)) return false;
+  for (int64_t s : strides)
+    if (s % 4) return false;
+  return true;
+}
+
+// ------------------------------------------------------------- A loaders
 struct LoadMidRad {  // A = (mid, rad) of an interval row-block
+  static constexpr int kBK = 32;
   const float *l, *h;
   int ld;
-  __device__ void operator()(int64_t, int64_t m, int k, float* v, float&) const {
-    const float lo = l[m * ld + k], hi = h[m * ld + k];
-    v[0] = (lo + hi) / 2.f;
-    v[1] = (hi - lo) / 2.f;
+  struct Row {
+    int64_t o;
+  };
+  struct Raw {
+    float l[4], h[4];
+  };
+  __device__ Row row(int64_t, int64_t m, bool) const { return Row{m * ld}; }
+  template <bool VEC>
+  __device__ void fetch(const Row& rw, int k, int n, Raw& x) const {
+    ld4<VEC>(l + rw.o + k, n, x.l);
+    ld4<VEC>(h + rw.o + k, n, x.h);
+  }
+  template <bool VEC>
+  __device__ void finish(const Row&, int, int, const Raw& x, float (*v)[4], KSum&, bool) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[0][j] = (x.l[j] + x.h[j]) / 2.f;
+      v[1][j] = (x.h[j] - x.l[j]) / 2.f;
+    }
   }
 };
-struct LoadWtAbs {  // B[k][n] = (W[n][k], |W[n][k]|)
+
+struct LoadRow {  // A[m][k] plain (row-major, ld)
+  static constexpr int kBK = 32;
+  const float* A;
+  int ld;
+  struct Row {
+    int64_t o;
+  };
+  struct Raw {
+    float x[4];
+  };
+  __device__ Row row(int64_t, int64_t m, bool) const { return Row{m * ld}; }
+  template <bool VEC>
+  __device__ void fetch(const Row& rw, int k, int n, Raw& x) const {
+    ld4<VEC>(A + rw.o + k, n, x.x);
+  }
+  template <bool VEC>
+  __device__ void finish(const Row&, int, int, const Raw& x, float (*v)[4], KSum&, bool) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[0][j] = x.x[j];
+  }
+};
+
+// CROWN backward: relaxation of ew rows at a relu, then the fc product.
+// Per element: ep = max(x, 0), en = min(x, 0); e = ep * lo_s + en * up_s
+// (+ beta); row part en * up_t (+ e * bias[k]); lo_s from the alpha
+// override when given (active -> 1, unstable -> alpha, dead -> 0).
+struct LoadRelaxRow {
+  static constexpr int kBK = 16;
+  const float* ew;
+  int ld;  // n_out
+  int R;
+  const float *lo, *hi, *alpha, *beta, *bias;
+  int alpha_per_row;
+  float* relax_out;
+  int ew_bcast;  // rows shared by all domains: row m reads ew[m % R]
+  struct Row {
+    int64_t xo, dom, mo;  // offsets of the ew row, the domain's neurons, row m
+    bool ro;              // this tile writes relax_out
+  };
+  struct Raw {
+    float x[4], lo[4], hi[4];
+  };
+  __device__ Row row(int64_t, int64_t m, bool first) const {
+    const int64_t d = m / R;
+    return Row{(ew_bcast ? m - d * R : m) * ld, d * ld, m * ld, first && relax_out != nullptr};
+  }
+  template <bool VEC>
+  __device__ void fetch(const Row& rw, int k, int n, Raw& x) const {
+    ld4<VEC>(ew + rw.xo + k, n, x.x);
+    if (lo) {
+      ld4<VEC>(lo + rw.dom + k, n, x.lo);
+      ld4<VEC>(hi + rw.dom + k, n, x.hi);
+    }
+  }
+  template <bool VEC>
+  __device__ void finish(const Row& rw, int k, int n, const Raw& x, float (*v)[4], KSum& part,
+                         bool rows) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float e = x.x[j], p = 0.f;
+      if (j < n) {
+        if (lo) {
+          Relax s = relax(x.lo[j], x.hi[j]);
+          float ls = s.lo_s;
+          if (alpha) {
+            const float a = alpha[(alpha_per_row ? rw.mo : rw.dom) + k + j];
+            ls = s.active ? 1.f : (s.unstable ? a : 0.f);
+          }
+          const float ep = fmaxf(e, 0.f), en = fminf(e, 0.f);
+          e = ep * ls + en * s.up_s;
+          if (beta) e = e + beta[rw.dom + k + j];
+          p = en * s.up_t;
+        }
+        if (bias) p += e * bias[k + j];
+        if (rw.ro) relax_out[rw.mo + k + j] = e;
+        if (rows) part.add(p);
+      }
+      v[0][j] = e;
+    }
+  }
+};
+
+// alpha gradient sweep with precomputed slopes (ls with the alpha override).
+struct LoadGradSlopes {
+  static constexpr int kBK = 32;
+  const float *gE, *P;
+  int ld, R;
+  const float *ls, *us, *ut;
+  int p_bcast;
+  struct Row {
+    int64_t mo, po, dom;
+  };
+  struct Raw {
+    float ge[4], pv[4];
+  };
+  __device__ Row row(int64_t, int64_t m, bool) const {
+    const int64_t d = m / R;
+    return Row{m * ld, (p_bcast ? m - d * R : m) * ld, d * ld};
+  }
+  template <bool VEC>
+  __device__ void fetch(const Row& rw, int k, int n, Raw& x) const {
+    ld4<VEC>(gE + rw.mo + k, n, x.ge);
+    ld4<VEC>(P + rw.po + k, n, x.pv);
+  }
+  template <bool VEC>
+  __device__ void finish(const Row& rw, int k, int n, const Raw& x, float (*v)[4], KSum&,
+                         bool) const {
+    float sl[4], su[4], st[4];
+    ld4<VEC>(ls + rw.dom + k, n, sl);
+    ld4<VEC>(us + rw.dom + k, n, su);
+    ld4<VEC>(ut + rw.dom + k, n, st);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float gp = 0.f;
+      if (j < n) {
+        const bool mp = x.pv[j] >= 0.f, mn = x.pv[j] <= 0.f;
+        const float f = (mp ? sl[j] : 0.f) + (mn ? su[j] : 0.f);
+        gp = x.ge[j] * f;
+        if (mn) gp += st[j];
+      }
+      v[0][j] = gp;
+    }
+  }
+};
+
+// alpha gradient sweep: gP = gE * (mpos ls + mneg up_s) + mneg up_t.
+struct LoadGradRelax {
+  static constexpr int kBK = 16;
+  const float *gE, *P;
+  int ld, R;
+  const float *lo, *hi, *alpha;
+  int p_bcast;  // P shared by all domains: row m reads P[m % R]
+  struct Row {
+    int64_t mo, po, dom;
+  };
+  struct Raw {
+    float ge[4], pv[4], lo[4], hi[4];
+  };
+  __device__ Row row(int64_t, int64_t m, bool) const {
+    const int64_t d = m / R;
+    return Row{m * ld, (p_bcast ? m - d * R : m) * ld, d * ld};
+  }
+  template <bool VEC>
+  __device__ void fetch(const Row& rw, int k, int n, Raw& x) const {
+    ld4<VEC>(gE + rw.mo + k, n, x.ge);
+    ld4<VEC>(P + rw.po + k, n, x.pv);
+    ld4<VEC>(lo + rw.dom + k, n, x.lo);
+    ld4<VEC>(hi + rw.dom + k, n, x.hi);
+  }
+  template <bool VEC>
+  __device__ void finish(const Row& rw, int k, int n, const Raw& x, float (*v)[4], KSum&,
+                         bool) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float gp = 0.f;
+      if (j < n) {
+        Relax s = relax(x.lo[j], x.hi[j]);
+        float ls = s.lo_s;
+        if (alpha) ls = s.active ? 1.f : (s.unstable ? alpha[rw.dom + k + j] : 0.f);
+        const bool mp = x.pv[j] >= 0.f, mn = x.pv[j] <= 0.f;
+        const float f = (mp ? ls : 0.f) + (mn ? s.up_s : 0.f);
+        gp = x.ge[j] * f;
+        if (mn) gp += s.up_t;
+      }
+      v[0][j] = gp;
+    }
+  }
+};
+
+struct LoadGradInput {  // gA = xl [A >= 0] + xh [A <= 0]
+  static constexpr int kBK = 32;
+  const float *A, *xl, *xh;
+  int ld, R;
+  struct Row {
+    int64_t mo, dom;
+  };
+  struct Raw {
+    float a[4], l[4], h[4];
+  };
+  __device__ Row row(int64_t, int64_t m, bool) const { return Row{m * ld, (m / R) * ld}; }
+  template <bool VEC>
+  __device__ void fetch(const Row& rw, int k, int n, Raw& x) const {
+    ld4<VEC>(A + rw.mo + k, n, x.a);
+    ld4<VEC>(xl + rw.dom + k, n, x.l);
+    ld4<VEC>(xh + rw.dom + k, n, x.h);
+  }
+  template <bool VEC>
+  __device__ void finish(const Row&, int, int n, const Raw& x, float (*v)[4], KSum&,
+                         bool) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float gv = 0.f;
+      if (j < n) {
+        if (x.a[j] >= 0.f) gv += x.l[j];
+        if (x.a[j] <= 0.f) gv += x.h[j];
+      }
+      v[0][j] = gv;
+    }
+  }
+};
+
+// ------------------------------------------------------------- B loaders
+struct LoadWtAbs {  // B[k][n] = (W[n][k], |W[n][k]|), W (n_out, ld)
+  static constexpr bool kTrans = true;
   const float* W;
   int ld;
-  __device__ void operator()(int64_t, int k, int n, float* v) const {
-    const float w = W[(int64_t)n * ld + k];
-    v[0] = w;
-    v[1] = fabsf(w);
+  __device__ const float* ptr(int64_t, int k, int n) const { return W + (int64_t)n * ld + k; }
+  __device__ static void finish(const float* x, float (*v)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[0][j] = x[j];
+      v[1][j] = fabsf(x[j]);
+    }
   }
 };
+struct LoadWt {  // B[k][n] = W[n][k]
+  static constexpr bool kTrans = true;
+  const float* W;
+  int ld;
+  __device__ const float* ptr(int64_t, int k, int n) const { return W + (int64_t)n * ld + k; }
+  __device__ static void finish(const float* x, float (*v)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[0][j] = x[j];
+  }
+};
+struct LoadW {  // B[k][n] = W[k][n]
+  static constexpr bool kTrans = false;
+  const float* W;
+  int ld;
+  __device__ const float* ptr(int64_t, int k, int n) const { return W + (int64_t)k * ld + n; }
+  __device__ static void finish(const float* x, float (*v)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[0][j] = x[j];
+  }
+};
+struct LoadGen {  // B[k][n] = G[bz][k][n]
+  static constexpr bool kTrans = false;
+  const float* G;
+  int64_t stride_b;
+  int ld;
+  __device__ const float* ptr(int64_t bz, int k, int n) const {
+    return G + bz * stride_b + (int64_t)k * ld + n;
+  }
+  __device__ static void finish(const float* x, float (*v)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[0][j] = x[j];
+  }
+};
+
+// ------------------------------------------------------------- epilogues
 struct EpIbp {
   const float* bias;
   float *lo, *hi;
@@ -209,51 +589,12 @@ struct EpIbp {
     hi[m * ld + n] = mc + c[1];
   }
 };
-
-struct LoadRow {  // A[m][k] plain
-  const float* A;
-  int ld;
-  __device__ void operator()(int64_t, int64_t m, int k, float* v, float&) const {
-    v[0] = A[m * ld + k];
-  }
-};
-struct LoadWt {  // B[k][n] = W[n][k]
-  const float* W;
-  int ld;
-  __device__ void operator()(int64_t, int k, int n, float* v) const {
-    v[0] = W[(int64_t)n * ld + k];
-  }
-};
-struct LoadW {  // B[k][n] = W[k][n]
-  const float* W;
-  int ld;
-  __device__ void operator()(int64_t, int k, int n, float* v) const {
-    v[0] = W[(int64_t)k * ld + n];
-  }
-};
 struct EpStoreBias {
   const float* bias;
   float* out;
   int ld;
   __device__ void operator()(int64_t, int64_t m, int n, const float* c) const {
     out[m * ld + n] = bias ? c[0] + bias[n] : c[0];
-  }
-};
-
-// Zonotope generators: A = W (shared), B = G[b] (n_in x K), out G_out[b].
-struct LoadWshared {
-  const float* W;
-  int ld;
-  __device__ void operator()(int64_t, int64_t m, int k, float* v, float&) const {
-    v[0] = W[m * ld + k];
-  }
-};
-struct LoadGen {
-  const float* G;
-  int64_t stride_b;
-  int ld;
-  __device__ void operator()(int64_t bz, int k, int n, float* v) const {
-    v[0] = G[bz * stride_b + (int64_t)k * ld + n];
   }
 };
 struct EpGen {
@@ -265,70 +606,111 @@ struct EpGen {
   }
 };
 
-// CROWN backward: relaxation of ew rows at a relu, then the fc product.
-struct LoadRelaxRow {
-  const float* ew;
-  int ld;  // n_out
-  int R;
-  const float *lo, *hi, *alpha, *beta, *bias;
-  int alpha_per_row;
-  float* relax_out;
-  int ew_bcast;  // rows shared by all domains: row m reads ew[m % R]
-  __device__ void operator()(int64_t, int64_t m, int k, float* v, float& part) const {
-    const float x = ew[(ew_bcast ? m % R : m) * ld + k];
-    float e = x, p = 0.f;
-    if (lo) {
-      const int64_t d = m / R;
-      const int64_t bi = d * ld + k;
-      Relax s = relax(lo[bi], hi[bi]);
-      float ls = s.lo_s;
-      if (alpha) {
-        const float a = alpha_per_row ? alpha[m * ld + k] : alpha[bi];
-        ls = s.active ? 1.f : (s.unstable ? a : 0.f);
-      }
-      const float ep = fmaxf(x, 0.f), en = fminf(x, 0.f);
-      e = ep * ls + en * s.up_s;
-      if (beta) e = e + beta[bi];
-      p = en * s.up_t;
-    }
-    if (bias) p += e * bias[k];
-    if (relax_out) relax_out[m * ld + k] = e;
-    v[0] = e;
-    part = p;
-  }
-};
+// Phase 1 of the two-phase backward step (vc_backward_fc with relax_out):
+// the relaxed rows e = pos(ew) ls + neg(ew) up_s [+ beta] into out, and
+// acc[m] += sum_k (neg(ew) up_t + e bias[k]) in fp64.  A workgroup takes
+// RR consecutive rows and streams their columns in float4 quads (the four
+// waves read neighbouring addresses); when the rows belong to one domain
+// the relaxation of each neuron is computed once for all of them.  HBM
+// bound: 8 bytes per element plus the per-domain bounds.
+constexpr int RR = 4;
 
-// alpha gradient sweep: gP = gE * (mpos ls + mneg up_s) + mneg up_t.
-struct LoadGradRelax {
-  const float *gE, *P;
-  int ld, R;
-  const float *lo, *hi, *alpha;
-  int p_bcast;  // P shared by all domains: row m reads P[m % R]
-  __device__ void operator()(int64_t, int64_t m, int k, float* v, float&) const {
-    const int64_t bi = (m / R) * ld + k;
-    const float ge = gE[m * ld + k], pv = P[(p_bcast ? m % R : m) * ld + k];
-    Relax s = relax(lo[bi], hi[bi]);
-    float ls = s.lo_s;
-    if (alpha) ls = s.active ? 1.f : (s.unstable ? alpha[bi] : 0.f);
-    const bool mp = pv >= 0.f, mn = pv <= 0.f;
-    float f = (mp ? ls : 0.f) + (mn ? s.up_s : 0.f);
-    float gp = ge * f;
-    if (mn) gp += s.up_t;
-    v[0] = gp;
+template <bool VEC>
+__global__ __launch_bounds__(NT) void k_relax_rows(const float* ew, int64_t M, int R, int n,
+                                                   const float* lo, const float* hi,
+                                                   const float* alpha, int alpha_per_row,
+                                                   const float* beta, const float* bias,
+                                                   int ew_bcast, float* out, float* acc) {
+  __shared__ double red[NT / 64][RR];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int nq = (n + 3) >> 2;
+  for (int64_t m0 = (int64_t)blockIdx.x * RR; m0 < M; m0 += (int64_t)gridDim.x * RR) {
+    int64_t mr[RR], dr[RR], xr[RR];
+#pragma unroll
+    for (int k = 0; k < RR; ++k) {
+      mr[k] = m0 + k < M ? m0 + k : M - 1;  // past the end: recompute the last row, no store
+      dr[k] = mr[k] / R;
+      xr[k] = ew_bcast ? mr[k] - dr[k] * R : mr[k];
+    }
+    const bool shared = dr[0] == dr[RR - 1] && !(alpha && alpha_per_row);
+    double p[RR];
+#pragma unroll
+    for (int k = 0; k < RR; ++k) p[k] = 0.0;
+    for (int i = threadIdx.x; i < nq; i += NT) {
+      const int c = 4 * i;
+      const int cnt = n - c < 4 ? n - c : 4;
+      float x[RR][4], e[RR][4], bi[4];
+#pragma unroll
+      for (int k = 0; k < RR; ++k) ld4<VEC>(ew + xr[k] * n + c, cnt, x[k]);
+      if (bias) ld4<VEC>(bias + c, cnt, bi);
+#pragma unroll
+      for (int k = 0; k < RR; ++k) {
+        if (k > 0 && shared) break;
+        float l4[4], h4[4], a4[4], b4[4];
+        ld4<VEC>(lo + dr[k] * n + c, cnt, l4);
+        ld4<VEC>(hi + dr[k] * n + c, cnt, h4);
+        if (alpha) ld4<VEC>(alpha + (alpha_per_row ? mr[k] : dr[k]) * n + c, cnt, a4);
+        if (beta) ld4<VEC>(beta + dr[k] * n + c, cnt, b4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (j >= cnt) break;
+          const Relax r = relax(l4[j], h4[j]);
+          const float ls = alpha ? (r.active ? 1.f : (r.unstable ? a4[j] : 0.f)) : r.lo_s;
+#pragma unroll
+          for (int q = 0; q < RR; ++q) {
+            if (!(shared ? true : q == k)) continue;
+            const float ep = fmaxf(x[q][j], 0.f), en = fminf(x[q][j], 0.f);
+            float v = ep * ls + en * r.up_s;
+            if (beta) v = v + b4[j];
+            float pp = en * r.up_t;
+            if (bias) pp += v * bi[j];
+            p[q] += (double)pp;
+            e[q][j] = v;
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < RR; ++k) {
+        if (m0 + k >= M) break;
+        float* o = out + mr[k] * n + c;
+        if (VEC && cnt == 4) {
+          *reinterpret_cast<float4*>(o) = make_float4(e[k][0], e[k][1], e[k][2], e[k][3]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (j < cnt) o[j] = e[k][j];
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < RR; ++k) {
+      const double t = wave_sum_f64(p[k]);
+      if (lane == 0) red[wv][k] = t;
+    }
+    __syncthreads();
+    if (threadIdx.x < RR && m0 + threadIdx.x < M) {
+      const int k = threadIdx.x;
+      const double t = (red[0][k] + red[1][k]) + (red[2][k] + red[3][k]);
+      acc[m0 + k] = (float)((double)acc[m0 + k] + t);
+    }
+    __syncthreads();
   }
-};
-struct LoadGradInput {  // gA = xl [A >= 0] + xh [A <= 0]
-  const float *A, *xl, *xh;
-  int ld, R;
-  __device__ void operator()(int64_t, int64_t m, int k, float* v, float&) const {
-    const float a = A[m * ld + k];
-    const int64_t bi = (m / R) * ld + k;
-    float gv = 0.f;
-    if (a >= 0.f) gv += xl[bi];
-    if (a <= 0.f) gv += xh[bi];
-    v[0] = gv;
+}
+
+// lo_s (alpha override: active 1, unstable alpha, dead 0), up_s, up_t of
+// every (domain, neuron), the relax() arithmetic.
+__global__ void k_relax_slopes(const float* lo, const float* hi, const float* alpha, int64_t n,
+                               float* ls, float* us, float* ut) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const Relax s = relax(lo[i], hi[i]);
+    float l = s.lo_s;
+    if (alpha) l = s.active ? 1.f : (s.unstable ? alpha[i] : 0.f);
+    ls[i] = l;
+    us[i] = s.up_s;
+    ut[i] = s.up_t;
   }
-};
+}
 
 }  // namespace
 
@@ -336,9 +718,9 @@ extern "C" int vc_ibp_fc(const float* l, const float* h, int64_t B, int n_in,
                          const float* W, const float* bias, int n_out, float* lo,
                          float* hi, vc_stream_t stream) {
   if (!l || !h || !W || !lo || !hi || n_in <= 0 || n_out <= 0 || B < 0) return VC_ERR_ARG;
-  return launch_gemm<2, true, false>(1, B, n_out, n_in, LoadMidRad{l, h, n_in},
-                                     LoadWtAbs{W, n_in}, EpIbp{bias, lo, hi, n_out},
-                                     nullptr, (hipStream_t)stream);
+  const bool vec = vec_ok({l, h, W}, {n_in});
+  return launch_gemm<2, false>(1, B, n_out, n_in, LoadMidRad{l, h, n_in}, LoadWtAbs{W, n_in},
+                               EpIbp{bias, lo, hi, n_out}, nullptr, vec, (hipStream_t)stream);
 }
 
 extern "C" int vc_zono_fc(const float* c, const float* G, int64_t B, int n_in, int K,
@@ -346,13 +728,15 @@ extern "C" int vc_zono_fc(const float* c, const float* G, int64_t B, int n_in, i
                           float* G_out, vc_stream_t stream) {
   if (!c || !W || !c_out || n_in <= 0 || n_out <= 0 || B < 0 || K < 0) return VC_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
-  int rc = launch_gemm<1, true, false>(1, B, n_out, n_in, LoadRow{c, n_in}, LoadWt{W, n_in},
-                                       EpStoreBias{bias, c_out, n_out}, nullptr, st);
+  int rc = launch_gemm<1, false>(1, B, n_out, n_in, LoadRow{c, n_in}, LoadWt{W, n_in},
+                                 EpStoreBias{bias, c_out, n_out}, nullptr,
+                                 vec_ok({c, W}, {n_in}), st);
   if (rc != VC_OK || K == 0 || B == 0) return rc;
   if (!G || !G_out) return VC_ERR_ARG;
-  return launch_gemm<1, false, false>(B, n_out, K, n_in, LoadWshared{W, n_in},
-                                      LoadGen{G, (int64_t)n_in * K, K},
-                                      EpGen{G_out, (int64_t)n_out * K, K}, nullptr, st);
+  return launch_gemm<1, false>(B, n_out, K, n_in, LoadRow{W, n_in},
+                               LoadGen{G, (int64_t)n_in * K, K},
+                               EpGen{G_out, (int64_t)n_out * K, K}, nullptr,
+                               vec_ok({W, G}, {n_in, K}), st);
 }
 
 extern "C" int vc_backward_fc(const float* ew_in, int64_t M, int R, int n_out,
@@ -365,11 +749,36 @@ extern "C" int vc_backward_fc(const float* ew_in, int64_t M, int R, int n_out,
   if ((relu_lo == nullptr) != (relu_hi == nullptr)) return VC_ERR_ARG;
   if (M % R != 0) return VC_ERR_ARG;
   if ((relu_lo || bias) && !acc) return VC_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  if (M == 0) return VC_OK;
+  if (relu_lo && relax_out && n_out >= kTwoPhaseMinWidth) {
+    // Two phases: the relaxed rows go through HBM once (phase 1, into
+    // relax_out, which the contract fills anyway), and the product runs as
+    // a plain GEMM whose prologue holds no per-element arithmetic.
+    const bool v1 = vec_ok({ew_in, relu_lo, relu_hi, alpha, beta, bias, relax_out}, {n_out});
+    const int64_t grid = (M + RR - 1) / RR < kMaxGrid ? (M + RR - 1) / RR : kMaxGrid;
+    if (v1)
+      hipLaunchKernelGGL(k_relax_rows<true>, dim3((unsigned)grid), dim3(NT), 0, st, ew_in, M, R,
+                         n_out, relu_lo, relu_hi, alpha, alpha_per_row, beta, bias, ew_bcast,
+                         relax_out, acc);
+    else
+      hipLaunchKernelGGL(k_relax_rows<false>, dim3((unsigned)grid), dim3(NT), 0, st, ew_in, M, R,
+                         n_out, relu_lo, relu_hi, alpha, alpha_per_row, beta, bias, ew_bcast,
+                         relax_out, acc);
+    VC_LAUNCH_CHECK();
+    return launch_gemm<1, false>(1, M, n_in, n_out, LoadRow{relax_out, n_out}, LoadW{W, n_in},
+                                 EpStoreBias{nullptr, ew_out, n_in}, nullptr,
+                                 vec_ok({relax_out, W}, {n_out, n_in}), st);
+  }
+  if (!relu_lo && !bias && !relax_out && !ew_bcast)
+    return launch_gemm<1, false>(1, M, n_in, n_out, LoadRow{ew_in, n_out}, LoadW{W, n_in},
+                                 EpStoreBias{nullptr, ew_out, n_in}, nullptr,
+                                 vec_ok({ew_in, W}, {n_out, n_in}), st);
   LoadRelaxRow la{ew_in, n_out, R, relu_lo, relu_hi, alpha, beta, bias, alpha_per_row, relax_out,
                   ew_bcast};
-  return launch_gemm<1, false, true>(1, M, n_in, n_out, la, LoadW{W, n_in},
-                                     EpStoreBias{nullptr, ew_out, n_in}, acc,
-                                     (hipStream_t)stream);
+  const bool vec = vec_ok({ew_in, relu_lo, relu_hi, W}, {n_out, n_in});
+  return launch_gemm<1, true>(1, M, n_in, n_out, la, LoadW{W, n_in},
+                              EpStoreBias{nullptr, ew_out, n_in}, acc, vec, st);
 }
 
 extern "C" int vc_alpha_grad_step(const float* gE, const float* P, int64_t M, int R, int n,
@@ -381,9 +790,10 @@ extern "C" int vc_alpha_grad_step(const float* gE, const float* P, int64_t M, in
   if (M % R != 0) return VC_ERR_ARG;
   if (!W_next) return VC_ERR_UNSUPPORTED;
   LoadGradRelax la{gE, P, n, R, relu_lo, relu_hi, alpha, p_bcast};
-  return launch_gemm<1, true, false>(1, M, n_next, n, la, LoadWt{W_next, n},
-                                     EpStoreBias{bias_next, g_out, n_next}, nullptr,
-                                     (hipStream_t)stream);
+  const bool vec = vec_ok({gE, P, relu_lo, relu_hi, W_next}, {n});
+  return launch_gemm<1, false>(1, M, n_next, n, la, LoadWt{W_next, n},
+                               EpStoreBias{bias_next, g_out, n_next}, nullptr, vec,
+                               (hipStream_t)stream);
 }
 
 extern "C" int vc_alpha_grad_input(const float* A, const float* xl, const float* xh,
@@ -392,7 +802,35 @@ extern "C" int vc_alpha_grad_input(const float* A, const float* xl, const float*
                                    vc_stream_t stream) {
   if (!A || !xl || !xh || !W0 || !g_out || R <= 0 || n_in <= 0 || n1 <= 0) return VC_ERR_ARG;
   if (M % R != 0) return VC_ERR_ARG;
-  return launch_gemm<1, true, false>(1, M, n1, n_in, LoadGradInput{A, xl, xh, n_in, R},
-                                     LoadWt{W0, n_in}, EpStoreBias{bias0, g_out, n1},
-                                     nullptr, (hipStream_t)stream);
+  const bool vec = vec_ok({A, xl, xh, W0}, {n_in});
+  return launch_gemm<1, false>(1, M, n1, n_in, LoadGradInput{A, xl, xh, n_in, R},
+                               LoadWt{W0, n_in}, EpStoreBias{bias0, g_out, n1}, nullptr, vec,
+                               (hipStream_t)stream);
+}
+
+extern "C" int vc_relax_slopes(const float* relu_lo, const float* relu_hi, const float* alpha,
+                               int64_t n, float* lo_s, float* up_s, float* up_t,
+                               vc_stream_t stream) {
+  if (n < 0 || (n > 0 && (!relu_lo || !relu_hi || !lo_s || !up_s || !up_t))) return VC_ERR_ARG;
+  if (n == 0) return VC_OK;
+  hipLaunchKernelGGL(k_relax_slopes, dim3(vc_blocks(n, NT)), dim3(NT), 0, (hipStream_t)stream,
+                     relu_lo, relu_hi, alpha, n, lo_s, up_s, up_t);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_alpha_grad_step_slopes(const float* gE, const float* P, int64_t M, int R,
+                                         int n, const float* lo_s, const float* up_s,
+                                         const float* up_t, int p_bcast, const float* W_next,
+                                         const float* bias_next, int n_next, float* g_out,
+                                         vc_stream_t stream) {
+  if (!gE || !P || !lo_s || !up_s || !up_t || !g_out || R <= 0 || n <= 0 || M < 0)
+    return VC_ERR_ARG;
+  if (M % R != 0) return VC_ERR_ARG;
+  if (!W_next) return VC_ERR_UNSUPPORTED;
+  LoadGradSlopes la{gE, P, n, R, lo_s, up_s, up_t, p_bcast};
+  const bool vec = vec_ok({gE, P, lo_s, up_s, up_t, W_next}, {n});
+  return launch_gemm<1, false>(1, M, n_next, n, la, LoadWt{W_next, n},
+                               EpStoreBias{bias_next, g_out, n_next}, nullptr, vec,
+                               (hipStream_t)stream);
 }

@@ -288,6 +288,12 @@ class BackwardTrace:
         self.fcs = []
 
 
+# vc_backward_fc runs as relaxation pass + plain MFMA GEMM from this row
+# width up when given a relaxed-rows buffer (measured 2x faster on 1024-wide
+# layers than relaxing inside the GEMM's loads).
+_TWO_PHASE_MIN_WIDTH = 64
+
+
 def _expand_rows(t, B):
     """(R, n) shared rows -> (B*R, n) per-domain rows."""
     R, n = t.shape
@@ -355,10 +361,15 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
                 if trace is not None:
                     trace.relus.append((L, rows.ew, rows.shared))
                     trace.fcs.append(op)
+                # the relaxed rows buffer selects the library's two-phase
+                # step (relaxation streamed through HBM, then a plain GEMM)
+                rel = (torch.empty(M, p['n_out'], device=dev)
+                       if p['n_out'] >= _TWO_PHASE_MIN_WIDTH else None)
                 call('vc_backward_fc', ptr(rows.ew), M, R, p['n_out'],
                      ptr(lo), ptr(hi), ptr(rows.alpha), rows.alpha_row,
                      ptr(rows.beta), ptr(p['W']), ptr(p['b']), p['n_in'],
-                     ptr(out), ptr(acc), None, 1 if rows.shared else 0, st)
+                     ptr(out), ptr(acc), ptr(rel), 1 if rows.shared else 0, st)
+                del rel
                 ew_at[inp] = _Rows(out, False)
             else:
                 if not rows.shared:
@@ -621,9 +632,14 @@ def _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, want_grad, galpha,
         if i > 0:
             fn = _op_params(fcs[i], dev)
             g2 = torch.empty(M, fn['n_out'], device=dev)
-            call('vc_alpha_grad_step', ptr(g), ptr(P), M, Q, n, ptr(lo),
-                 ptr(hi), ptr(a), 1 if p_shared else 0, ptr(fn['W']),
-                 ptr(fn['b']), fn['n_out'], ptr(g2), st)
+            # slopes once per (domain, neuron), then the sweep step without
+            # a per-element division
+            ls, us, ut = (torch.empty(B, n, device=dev) for _ in range(3))
+            call('vc_relax_slopes', ptr(lo), ptr(hi), ptr(a), B * n, ptr(ls),
+                 ptr(us), ptr(ut), st)
+            call('vc_alpha_grad_step_slopes', ptr(g), ptr(P), M, Q, n,
+                 ptr(ls), ptr(us), ptr(ut), 1 if p_shared else 0,
+                 ptr(fn['W']), ptr(fn['b']), fn['n_out'], ptr(g2), st)
             g = g2
     return lb
 
