@@ -330,18 +330,39 @@ def kernel_suite(reps):
     report('a2', 'gemm_kernel (interval fc, two products)', '784->256 fc, 8,192 boxes',
            _time_launches([fn], reps), 'mfma', 2.0 * 2 * B * n_in * n_out)
 
-    # -- a7: backward through conv(32->64, 4x4, s2, p1) as a transposed conv
-    M, C_in, H, C_out, Ho, k = 64 * 9, 32, 32, 64, 16, 4
-    ew = rndn(M, C_out * Ho * Ho)
+    # -- a7: backward through the CNN's convolutions (transposed conv as
+    #    implicit GEMM by output parity class), 64 domains x 9 spec rows
+    for C_in, H, C_out, k, cs, cp in ((3, 32, 32, 3, 1, 1), (32, 32, 64, 4, 2, 1),
+                                      (64, 16, 64, 4, 2, 1)):
+        Ho = (H + 2 * cp - k) // cs + 1
+        M = 64 * 9
+        ew = rndn(M, C_out * Ho * Ho)
+        K = rndn(C_out, C_in, k, k) * (2.0 / (C_in * k * k)) ** 0.5
+        bias = rndn(C_out) * 0.01
+        out = torch.empty(M, C_in * H * H, device=dev)
+        acc = torch.zeros(M, device=dev)
+        fn = lambda: call('vc_backward_conv', ptr(ew), M, ptr(K), ptr(bias), C_out, Ho, Ho, C_in,
+                          H, H, k, k, cs, cs, cp, cp, ptr(out), ptr(acc), st)
+        report('a7', 'gemm_kernel (transposed conv, implicit GEMM) + k_conv_bias_dot',
+               f'conv {C_in}->{C_out} {k}x{k} s{cs} p{cp} ({H}x{H} in), 576 rows '
+               '(64 domains x 9)', _time_launches([fn], max(3, reps // 4)), 'mfma',
+               2.0 * M * (C_out * Ho * Ho) * (C_in * k * k))
+        del ew, out, acc
+
+    # -- a2: interval forward through the CNN's second convolution, 64 boxes
+    C_in, H, C_out, k, cs, cp, B = 32, 32, 64, 4, 2, 1, 64
+    Ho = (H + 2 * cp - k) // cs + 1
+    l = rnd(B, C_in * H * H)
+    h = l + 0.01
     K = rndn(C_out, C_in, k, k) * (2.0 / (C_in * k * k)) ** 0.5
     bias = rndn(C_out) * 0.01
-    out = torch.empty(M, C_in * H * H, device=dev)
-    acc = torch.zeros(M, device=dev)
-    fn = lambda: call('vc_backward_conv', ptr(ew), M, ptr(K), ptr(bias), C_out, Ho, Ho, C_in, H,
-                      H, k, k, 2, 2, 1, 1, ptr(out), ptr(acc), st)
-    report('a7', 'k_conv_transpose', 'conv 32->64 4x4 s2 p1 (32x32 in), 576 rows '
-           '(64 domains x 9)', _time_launches([fn], max(3, reps // 4)), 'mfma',
-           2.0 * M * (C_out * Ho * Ho) * (C_in * k * k))
+    lo, hi = torch.empty(B, C_out * Ho * Ho, device=dev), torch.empty(B, C_out * Ho * Ho,
+                                                                      device=dev)
+    fn = lambda: call('vc_ibp_conv', ptr(l), ptr(h), B, C_in, H, H, ptr(K), ptr(bias), C_out, k,
+                      k, cs, cs, cp, cp, Ho, Ho, ptr(lo), ptr(hi), st)
+    report('a2', 'gemm_kernel (interval conv, two products, implicit GEMM)',
+           f'conv {C_in}->{C_out} {k}x{k} s{cs} p{cp} ({H}x{H} in), 64 boxes',
+           _time_launches([fn], reps), 'mfma', 2.0 * 2 * B * (C_out * Ho * Ho) * (C_in * k * k))
 
 
 def main():

@@ -243,6 +243,87 @@ def test_alpha_grad_step_slopes_matches_bounds_form(gpu):
         assert bool(((cpu(got).double() - ref).abs() <= 1e-6 + 1e-5 * sc).all())
 
 
+# Convolution geometries: (C_in, H, W, C_out, k, stride, pad) -- the CNN's
+# three layers and odd shapes (kernel not a multiple of the stride, stride
+# 3, padding 0 and 2, non-square images, widths not a multiple of 4).
+CONV_GEOMS = [(3, 32, 32, 32, 3, 1, 1), (32, 32, 32, 64, 4, 2, 1), (64, 16, 16, 64, 4, 2, 1),
+              (5, 9, 7, 6, 3, 2, 1), (4, 11, 10, 3, 5, 3, 2), (2, 6, 13, 7, 2, 1, 0)]
+
+
+@pytest.mark.parametrize('geom', CONV_GEOMS)
+def test_conv_layers_against_fp64(gpu, geom):
+    """vc_ibp_conv, vc_zono_conv and vc_backward_conv (implicit-GEMM MFMA
+    kernels) against torch's conv2d / conv_transpose2d in fp64 on the same
+    fp32 inputs, within the bound tolerance of the summed magnitudes."""
+    import torch.nn.functional as F
+    C_in, H, W, C_out, k, s, p = geom
+    Ho, Wo = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    g = torch.Generator().manual_seed(sum(geom))
+    K = torch.randn(C_out, C_in, k, k, generator=g) / (C_in * k * k) ** 0.5
+    bias = torch.randn(C_out, generator=g) * 0.1
+    st = torch.cuda.current_stream().cuda_stream
+    dK, db = K.to(gpu), bias.to(gpu)
+    K64, b64 = K.double(), bias.double()
+
+    def close(got, ref, scale, what):
+        err = (cpu(got).double() - ref).abs()
+        assert bool((err <= 1e-6 + 1e-5 * scale).all()), (what, geom, float(err.max()))
+
+    # interval forward
+    B = 3
+    lo = torch.randn(B, C_in, H, W, generator=g)
+    hi = lo + torch.rand(B, C_in, H, W, generator=g)
+    glo, ghi = (torch.empty(B, C_out * Ho * Wo, device=gpu) for _ in range(2))
+    dlo, dhi = lo.to(gpu), hi.to(gpu)  # held: the call takes raw pointers
+    call('vc_ibp_conv', ptr(dlo), ptr(dhi), B, C_in, H, W, ptr(dK), ptr(db), C_out,
+         k, k, s, s, p, p, Ho, Wo, ptr(glo), ptr(ghi), st)
+    mid, rad = (lo.double() + hi.double()) / 2, (hi.double() - lo.double()) / 2
+    mc = F.conv2d(mid, K64, b64, stride=s, padding=p).reshape(B, -1)
+    rc = F.conv2d(rad, K64.abs(), stride=s, padding=p).reshape(B, -1)
+    sc = F.conv2d(mid.abs(), K64.abs(), b64.abs(), stride=s, padding=p).reshape(B, -1) + rc
+    torch.cuda.synchronize()
+    close(glo, mc - rc, sc, 'ibp lo')
+    close(ghi, mc + rc, sc, 'ibp hi')
+
+    # zonotope forward: centre and Kg generator columns (Kg not a multiple of 4)
+    Kg = 6
+    c = torch.randn(B, C_in * H * W, generator=g)
+    G = torch.randn(B, C_in * H * W, Kg, generator=g)
+    gc = torch.empty(B, C_out * Ho * Wo, device=gpu)
+    gG = torch.empty(B, C_out * Ho * Wo, Kg, device=gpu)
+    dc, dG = c.to(gpu), G.to(gpu)
+    call('vc_zono_conv', ptr(dc), ptr(dG), B, Kg, C_in, H, W, ptr(dK), ptr(db),
+         C_out, k, k, s, s, p, p, Ho, Wo, ptr(gc), ptr(gG), st)
+    cref = F.conv2d(c.double().reshape(B, C_in, H, W), K64, b64, stride=s, padding=p)
+    csc = F.conv2d(c.double().abs().reshape(B, C_in, H, W), K64.abs(), b64.abs(), stride=s,
+                   padding=p)
+    Gi = G.double().permute(0, 2, 1).reshape(B * Kg, C_in, H, W)
+    Gref = F.conv2d(Gi, K64, stride=s, padding=p).reshape(B, Kg, -1).permute(0, 2, 1)
+    Gsc = F.conv2d(Gi.abs(), K64.abs(), stride=s, padding=p).reshape(B, Kg, -1).permute(0, 2, 1)
+    torch.cuda.synchronize()
+    close(gc, cref.reshape(B, -1), csc.reshape(B, -1), 'zono centre')
+    close(gG, Gref, Gsc, 'zono generators')
+
+    # backward: transposed conv of M rows + the bias dot into acc
+    M = 5
+    ew = torch.randn(M, C_out, Ho, Wo, generator=g)
+    acc0 = torch.randn(M, generator=g)
+    oph, opw = H - ((Ho - 1) * s - 2 * p + k), W - ((Wo - 1) * s - 2 * p + k)
+    out = torch.empty(M, C_in * H * W, device=gpu)
+    acc = acc0.to(gpu)
+    dew = ew.to(gpu)
+    call('vc_backward_conv', ptr(dew), M, ptr(dK), ptr(db), C_out, Ho, Wo, C_in, H, W, k,
+         k, s, s, p, p, ptr(out), ptr(acc), st)
+    ref = F.conv_transpose2d(ew.double(), K64, stride=s, padding=p, output_padding=(oph, opw))
+    rsc = F.conv_transpose2d(ew.double().abs(), K64.abs(), stride=s, padding=p,
+                             output_padding=(oph, opw))
+    aref = acc0.double() + (ew.double() * b64.view(1, -1, 1, 1)).sum((1, 2, 3))
+    asc = acc0.double().abs() + (ew.double().abs() * b64.abs().view(1, -1, 1, 1)).sum((1, 2, 3))
+    torch.cuda.synchronize()
+    close(out, ref.reshape(M, -1), rsc.reshape(M, -1), 'conv_transpose')
+    close(acc, aref, asc, 'conv bias dot')
+
+
 # ----------------------------------------------------------------- a1
 def test_make_slopes_bit_exact(gpu):
     g = torch.Generator().manual_seed(1)

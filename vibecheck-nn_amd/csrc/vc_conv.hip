@@ -1,163 +1,367 @@
-// Convolution layers of the bound engine (NCHW, zero padding):
+// Convolution layers of the bound engine (NCHW, zero padding) as implicit
+// GEMMs on the MFMA core (vc_gemm_core.h): rows are output channels,
+// columns are (image, output pixel[, generator column]), K runs over
+// (input channel, kernel tap), and the B loader gathers the input pixels
+// of a column (zero outside the image), so no im2col copy exists.
 //   - interval forward: conv2d(mid, K) + bias -/+ conv2d(rad, |K|)
-//     (verify_zono_bnb.py:1098-1107)
-//   - zonotope forward on generator columns (verify_zono_bnb.py:3400-3425)
-//   - CROWN backward: acc += ew . bias[channel], ew <- conv_transpose2d(ew)
-//     (verify_zono_bnb.py:4568-4593)
-// Direct forms: one thread per output element.
-#include "vc_common.h"
+//     (verify_zono_bnb.py:1098-1107), both products in one launch;
+//   - zonotope forward: conv2d(c, K) + bias and every generator column
+//     convolved without bias (verify_zono_bnb.py:3400-3425);
+//   - CROWN backward: acc += ew . bias[channel] and ew <- conv_transpose2d
+//     (verify_zono_bnb.py:4568-4593).  The transposed convolution is split
+//     by output parity (y mod sh, x mod sw) into sh * sw correlations, one
+//     per batch index of the launch: output pixel (yy, xx) of class
+//     (py, px) is y = sh yy + py, and only the taps ky = ky0 + sh ty with
+//     ky0 = (py + ph) mod sh reach it, from source row yy + cy - ty with
+//     cy = (py + ph - ky0) / sh (the same along x), so no zero tap is
+//     multiplied.
+#include "vc_gemm_core.h"
 
 namespace {
 
-constexpr int NT = 256;
+using namespace vcg;
 
 struct ConvGeom {
   int C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, Ho, Wo;
 };
 
-__global__ void k_ibp_conv(const float* l, const float* h, int64_t B, ConvGeom g,
-                           const float* K, const float* bias, float* lo, float* hi) {
-  const int64_t n_out = (int64_t)g.C_out * g.Ho * g.Wo;
-  const int64_t total = B * n_out;
-  const int64_t n_in = (int64_t)g.C_in * g.H * g.W;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t b = i / n_out;
-    const int o = (int)(i % n_out);
-    const int co = o / (g.Ho * g.Wo);
-    const int yo = (o / g.Wo) % g.Ho;
-    const int xo = o % g.Wo;
-    KSum sm, sr;
-    const float* lb = l + b * n_in;
-    const float* hb = h + b * n_in;
-    for (int ci = 0; ci < g.C_in; ++ci)
-      for (int ky = 0; ky < g.kh; ++ky) {
-        const int yi = yo * g.sh - g.ph + ky;
-        if (yi < 0 || yi >= g.H) continue;
-        for (int kx = 0; kx < g.kw; ++kx) {
-          const int xi = xo * g.sw - g.pw + kx;
-          if (xi < 0 || xi >= g.W) continue;
-          const int64_t e = ((int64_t)ci * g.H + yi) * g.W + xi;
-          const float lv = lb[e], hv = hb[e];
-          const float kv = K[((co * g.C_in + ci) * g.kh + ky) * g.kw + kx];
-          sm.add(kv * ((lv + hv) / 2.f));
-          sr.add(fabsf(kv) * ((hv - lv) / 2.f));
-        }
-      }
-    const float mv = sm.value(), rv = sr.value();
-    const float mc = bias ? mv + bias[co] : mv;
-    lo[i] = mc - rv;
-    hi[i] = mc + rv;
-  }
+// Parity class bz of a transposed convolution along one dimension.
+struct TapClass {
+  int k0, c;  // first tap, source offset
+};
+__device__ __forceinline__ TapClass tap_class(int parity, int pad, int s) {
+  const int k0 = (parity + pad) % s;
+  return TapClass{k0, (parity + pad - k0) / s};
 }
 
-// Zonotope generators: G (B, n_in, K) -> G_out (B, n_out, K), each
-// generator column k of domain b convolved (no bias).
-__global__ void k_zono_conv_gen(const float* G, int64_t B, int Kg, ConvGeom g, const float* K,
-                                float* Go) {
-  const int64_t n_out = (int64_t)g.C_out * g.Ho * g.Wo;
-  const int64_t n_in = (int64_t)g.C_in * g.H * g.W;
-  const int64_t total = B * n_out * Kg;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int k = (int)(i % Kg);
-    const int64_t bo = i / Kg;
-    const int64_t b = bo / n_out;
-    const int o = (int)(bo % n_out);
-    const int co = o / (g.Ho * g.Wo);
-    const int yo = (o / g.Wo) % g.Ho;
-    const int xo = o % g.Wo;
-    KSum s;
-    for (int ci = 0; ci < g.C_in; ++ci)
-      for (int ky = 0; ky < g.kh; ++ky) {
-        const int yi = yo * g.sh - g.ph + ky;
-        if (yi < 0 || yi >= g.H) continue;
-        for (int kx = 0; kx < g.kw; ++kx) {
-          const int xi = xo * g.sw - g.pw + kx;
-          if (xi < 0 || xi >= g.W) continue;
-          const int64_t e = ((int64_t)ci * g.H + yi) * g.W + xi;
-          s.add(K[((co * g.C_in + ci) * g.kh + ky) * g.kw + kx] * G[(b * n_in + e) * Kg + k]);
+// ------------------------------------------------------------ B: gather
+// Column n = (img * npix + pix) * nk + g, pix = py * Wg + px.  Element
+// (k, n) = src[img * s_img + g + c * s_c + y * s_y + x * s_x] with
+// c = k / T, t = k % T, ty = t / Tx, tx = t % Tx, y = py * psy + oy + dsg ty,
+// x = px * psx + ox + dsg tx, zero outside [0, Hs) x [0, Ws).  TR: the
+// offsets (oy, ox) are those of the transposed-convolution parity class bz
+// (dsg = -1), else (-ph, -pw) (dsg = +1).  NS = 2 gathers two sources
+// (interval lo, hi) into (mid, rad).
+template <int NS, bool TR>
+struct LoadGather {
+  static constexpr bool kTrans = false;
+  const float *src, *src2;
+  int64_t s_img, s_c;
+  int s_y, s_x, Hs, Ws;
+  int nk, T, Tx, psy, psx, ph, pw, sh, sw, Wg;
+  int64_t per_img;  // npix * nk
+  FastDiv f_img, f_nk, f_wg, f_T, f_Tx;
+  struct Col {
+    int64_t off;
+    int yb, xb, mode, n;
+  };
+  struct Raw {
+    float x[NS][4];
+  };
+  __device__ void origin(int64_t bz, int& oy, int& ox) const {
+    if (TR) {
+      oy = tap_class((int)bz / sw, ph, sh).c;
+      ox = tap_class((int)bz % sw, pw, sw).c;
+    } else {
+      oy = -ph;
+      ox = -pw;
+    }
+  }
+  __device__ void place(int n, int oy, int ox, int64_t& off, int& yb, int& xb, int& g,
+                        int& px) const {
+    const int img = (int)f_img.div((uint32_t)n);
+    const int r = n - (int)(img * per_img);
+    const int pix = (int)f_nk.div((uint32_t)r);
+    g = r - pix * nk;
+    const int py = (int)f_wg.div((uint32_t)pix);
+    px = pix - py * Wg;
+    off = img * s_img + g;
+    yb = py * psy + oy;
+    xb = px * psx + ox;
+  }
+  __device__ Col col(int64_t bz, int n) const {
+    int oy, ox, g, px;
+    Col c;
+    origin(bz, oy, ox);
+    place(n, oy, ox, c.off, c.yb, c.xb, g, px);
+    c.n = n;
+    // 0: the quad's columns are consecutive pixels of one row (step psx);
+    // 1: consecutive generator columns of one pixel; 2: anything else
+    c.mode = (nk == 1 && px + 3 < Wg) ? 0 : ((nk > 1 && g + 3 < nk) ? 1 : 2);
+    c.mode |= (int)bz << 2;
+    return c;
+  }
+  __device__ float at(const float* base, int y, int x) const {
+    return ((unsigned)y < (unsigned)Hs && (unsigned)x < (unsigned)Ws) ? base[y * s_y + x * s_x]
+                                                                      : 0.f;
+  }
+  template <bool VEC>
+  __device__ void fetch(const Col& cl, int k, int cnt, Raw& r) const {
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r.x[s][j] = 0.f;
+    if (cnt == 0) return;
+    const int c = (int)f_T.div((uint32_t)k);
+    const int t = k - c * T;
+    const int ty = (int)f_Tx.div((uint32_t)t);
+    const int tx = t - ty * Tx;
+    const int dy = TR ? -ty : ty, dx = TR ? -tx : tx;
+    const int mode = cl.mode & 3;
+    if (mode == 2) {
+      int oy, ox;
+      origin(cl.mode >> 2, oy, ox);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (j < cnt) {
+          int64_t off;
+          int yb, xb, g, px;
+          place(cl.n + j, oy, ox, off, yb, xb, g, px);
+          r.x[0][j] = at(src + off + c * s_c, yb + dy, xb + dx);
+          if (NS == 2) r.x[NS - 1][j] = at(src2 + off + c * s_c, yb + dy, xb + dx);
         }
       }
-    Go[i] = s.value();
-  }
-}
-
-__global__ void k_conv_center(const float* c, int64_t B, ConvGeom g, const float* K,
-                              const float* bias, float* co_out) {
-  const int64_t n_out = (int64_t)g.C_out * g.Ho * g.Wo;
-  const int64_t n_in = (int64_t)g.C_in * g.H * g.W;
-  const int64_t total = B * n_out;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t b = i / n_out;
-    const int o = (int)(i % n_out);
-    const int co = o / (g.Ho * g.Wo);
-    const int yo = (o / g.Wo) % g.Ho;
-    const int xo = o % g.Wo;
-    KSum s;
-    for (int ci = 0; ci < g.C_in; ++ci)
-      for (int ky = 0; ky < g.kh; ++ky) {
-        const int yi = yo * g.sh - g.ph + ky;
-        if (yi < 0 || yi >= g.H) continue;
-        for (int kx = 0; kx < g.kw; ++kx) {
-          const int xi = xo * g.sw - g.pw + kx;
-          if (xi < 0 || xi >= g.W) continue;
-          s.add(K[((co * g.C_in + ci) * g.kh + ky) * g.kw + kx] *
-                c[b * n_in + ((int64_t)ci * g.H + yi) * g.W + xi]);
-        }
-      }
-    const float sv = s.value();
-    co_out[i] = bias ? sv + bias[co] : sv;
-  }
-}
-
-// Transposed conv: out[m, ci, yi, xi] = sum over (co, ky, kx) with
-// yi = yo*sh - ph + ky, xi = xo*sw - pw + kx of ew[m, co, yo, xo] K[co, ci, ky, kx].
-__global__ void k_conv_transpose(const float* ew, int64_t M, ConvGeom g, const float* K,
-                                 float* out) {
-  const int64_t n_out = (int64_t)g.C_out * g.Ho * g.Wo;
-  const int64_t n_in = (int64_t)g.C_in * g.H * g.W;
-  const int64_t total = M * n_in;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t m = i / n_in;
-    const int e = (int)(i % n_in);
-    const int ci = e / (g.H * g.W);
-    const int yi = (e / g.W) % g.H;
-    const int xi = e % g.W;
-    KSum s;
-    const float* em = ew + m * n_out;
-    for (int ky = 0; ky < g.kh; ++ky) {
-      const int ty = yi + g.ph - ky;
-      if (ty < 0 || ty % g.sh) continue;
-      const int yo = ty / g.sh;
-      if (yo >= g.Ho) continue;
-      for (int kx = 0; kx < g.kw; ++kx) {
-        const int tx = xi + g.pw - kx;
-        if (tx < 0 || tx % g.sw) continue;
-        const int xo = tx / g.sw;
-        if (xo >= g.Wo) continue;
-        for (int co = 0; co < g.C_out; ++co)
-          s.add(em[((int64_t)co * g.Ho + yo) * g.Wo + xo] *
-                K[((co * g.C_in + ci) * g.kh + ky) * g.kw + kx]);
+      return;
+    }
+    const int y = cl.yb + dy;
+    const float* b1 = src + cl.off + c * s_c;
+    const float* b2 = NS == 2 ? src2 + cl.off + c * s_c : nullptr;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j < cnt) {
+        const int x = cl.xb + dx + (mode == 0 ? psx * j : 0);
+        const int gj = mode == 1 ? j : 0;
+        r.x[0][j] = at(b1 + gj, y, x);
+        if (NS == 2) r.x[NS - 1][j] = at(b2 + gj, y, x);
       }
     }
-    out[i] = s.value();
+  }
+  __device__ static void finish(const Raw& r, float (*v)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (NS == 2) {
+        v[0][j] = (r.x[0][j] + r.x[NS - 1][j]) / 2.f;
+        v[NS - 1][j] = (r.x[NS - 1][j] - r.x[0][j]) / 2.f;
+      } else {
+        v[0][j] = r.x[0][j];
+      }
+    }
+  }
+};
+
+// ------------------------------------------------------------ A: weights
+// Forward: A = K viewed (C_out, C_in kh kw), rows co; with NA = 2 the
+// second operand is |K| (the interval radius product).
+template <int NA>
+struct LoadKernel {
+  static constexpr int kBK = 32;
+  static constexpr bool kSmallM = true;
+  const float* K;
+  int ld;
+  struct Row {
+    int64_t o;
+  };
+  struct Raw {
+    float x[4];
+  };
+  __device__ Row row(int64_t, int64_t m, bool) const { return Row{m * ld}; }
+  template <bool VEC>
+  __device__ void fetch(const Row& rw, int k, int n, Raw& x) const {
+    ld4<false>(K + rw.o + k, n, x.x);
+  }
+  template <bool VEC>
+  __device__ void finish(const Row&, int, int, const Raw& x, float (*v)[4], KSum&, bool) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[0][j] = x.x[j];
+      if (NA == 2) v[NA - 1][j] = fabsf(x.x[j]);
+    }
+  }
+};
+
+// Transposed, parity class bz: A[ci][(co, ty, tx)] = K[co][ci][ky0 + sh ty]
+// [kx0 + sw tx], zero for taps past the kernel (classes with fewer taps).
+struct LoadKernelT {
+  static constexpr int kBK = 32;
+  static constexpr bool kSmallM = true;
+  const float* K;
+  int C_in, kh, kw, sh, sw, ph, pw, T, Tx, Ty;
+  FastDiv f_T, f_Tx;
+  struct Row {
+    int ci, ky0, kx0;
+  };
+  struct Raw {
+    float x[4];
+  };
+  __device__ Row row(int64_t bz, int64_t m, bool) const {
+    return Row{(int)m, tap_class((int)bz / sw, ph, sh).k0, tap_class((int)bz % sw, pw, sw).k0};
+  }
+  template <bool VEC>
+  __device__ void fetch(const Row& rw, int k, int n, Raw& x) const {
+    int co = (int)f_T.div((uint32_t)k);
+    const int t = k - co * T;
+    int ty = (int)f_Tx.div((uint32_t)t);
+    int tx = t - ty * Tx;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v = 0.f;
+      const int ky = rw.ky0 + sh * ty, kx = rw.kx0 + sw * tx;
+      if (j < n && ky < kh && kx < kw) v = K[(((int64_t)co * C_in + rw.ci) * kh + ky) * kw + kx];
+      x.x[j] = v;
+      if (++tx == Tx) {
+        tx = 0;
+        if (++ty == Ty) {
+          ty = 0;
+          ++co;
+        }
+      }
+    }
+  }
+  template <bool VEC>
+  __device__ void finish(const Row&, int, int, const Raw& x, float (*v)[4], KSum&, bool) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[0][j] = x.x[j];
+  }
+};
+
+// ------------------------------------------------------------ epilogues
+// Forward outputs: column n = img * per_img + r -> out[img * o_img + m * o_c + r]
+// (r = pix * nk + g).  NA = 2: interval (lo, hi) = mid + bias -/+ rad.
+template <int NA>
+struct EpConv {
+  const float* bias;
+  float *out, *out2;
+  int64_t per_img, o_img, o_c;
+  FastDiv f_img;
+  __device__ void operator()(int64_t, int64_t m, int n, const float* c) const {
+    const int img = (int)f_img.div((uint32_t)n);
+    const int64_t r = n - img * per_img;
+    const int64_t o = img * o_img + m * o_c + r;
+    const float mc = bias ? c[0] + bias[m] : c[0];
+    if (NA == 2) {
+      out[o] = mc - c[NA - 1];
+      out2[o] = mc + c[NA - 1];
+    } else {
+      out[o] = mc;
+    }
+  }
+};
+
+// Transposed outputs of parity class bz: column n = (img, yy, xx) on the
+// class grid (Hc, Wc) -> out[img][ci = m][sh yy + py][sw xx + px], inside H x W.
+struct EpConvT {
+  float* out;
+  int H, W, Wc, sh, sw;
+  int64_t per_img, o_img;
+  FastDiv f_img, f_wc;
+  __device__ void operator()(int64_t bz, int64_t m, int n, const float* c) const {
+    const int img = (int)f_img.div((uint32_t)n);
+    const int pix = n - (int)(img * per_img);
+    const int yy = (int)f_wc.div((uint32_t)pix);
+    const int xx = pix - yy * Wc;
+    const int y = sh * yy + (int)bz / sw, x = sw * xx + (int)bz % sw;
+    if (y < H && x < W) out[img * o_img + (m * H + y) * (int64_t)W + x] = c[0];
+  }
+};
+
+// Transposed convolution onto few channels (C_in <= 4, the network's
+// input layer): an MFMA tile would hold C_in of its 64 rows, so one thread
+// takes one output pixel of one row and all CI channels.  The kernel taps
+// sit in LDS as doubles; products and sums are fp64 FMAs, rounded once.
+// Neighbouring threads read neighbouring source pixels.
+constexpr int kSmallC = 4;
+constexpr int kSmallCLds = 48 * 1024;  // bytes of LDS for the taps
+
+template <int CI>
+__global__ __launch_bounds__(NT) void k_conv_t_smallc(const float* ew, int64_t M, ConvGeom g,
+                                                      const float* K, float* out) {
+  extern __shared__ double wd[];  // [C_out][kh][kw][CI]
+  const int taps = g.C_out * g.kh * g.kw;
+  for (int i = threadIdx.x; i < taps * CI; i += NT) {
+    const int ci = i % CI, r = i / CI;
+    const int kx = r % g.kw, ky = (r / g.kw) % g.kh, co = r / (g.kw * g.kh);
+    wd[i] = (double)K[((co * g.C_in + ci) * g.kh + ky) * g.kw + kx];
+  }
+  __syncthreads();
+  const int64_t hw = (int64_t)g.H * g.W, total = M * hw;
+  const int64_t so = (int64_t)g.Ho * g.Wo;
+  for (int64_t i = blockIdx.x * (int64_t)NT + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * NT) {
+    const int64_t m = i / hw;
+    const int p = (int)(i - m * hw);
+    const int y = p / g.W, x = p - (p / g.W) * g.W;
+    double acc[CI];
+#pragma unroll
+    for (int c = 0; c < CI; ++c) acc[c] = 0.0;
+    const float* em = ew + m * g.C_out * so;
+    for (int ky = 0; ky < g.kh; ++ky) {
+      const int ty = y + g.ph - ky;
+      if (ty < 0 || ty % g.sh) continue;
+      const int oy = ty / g.sh;
+      if (oy >= g.Ho) continue;
+      for (int kx = 0; kx < g.kw; ++kx) {
+        const int tx = x + g.pw - kx;
+        if (tx < 0 || tx % g.sw) continue;
+        const int ox = tx / g.sw;
+        if (ox >= g.Wo) continue;
+        const float* e = em + oy * g.Wo + ox;
+        const double* w = wd + (ky * g.kw + kx) * CI;
+        const int wstep = g.kh * g.kw * CI;
+        int co = 0;
+        for (; co + 8 <= g.C_out; co += 8) {  // eight loads in flight
+          float v8[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v8[u] = e[(co + u) * so];
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+#pragma unroll
+            for (int c = 0; c < CI; ++c)
+              acc[c] = __builtin_fma((double)v8[u], w[(co + u) * wstep + c], acc[c]);
+        }
+        for (; co < g.C_out; ++co) {
+          const double v = (double)e[co * so];
+#pragma unroll
+          for (int c = 0; c < CI; ++c) acc[c] = __builtin_fma(v, w[co * wstep + c], acc[c]);
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CI; ++c) out[(m * g.C_in + c) * hw + p] = (float)acc[c];
   }
 }
 
-// acc[m] += sum_{co, p} ew[m, co, p] * bias[co]; one wave per row.
-__global__ void k_conv_bias_dot(const float* ew, int64_t M, int C_out, int sp,
-                                const float* bias, float* acc) {
-  const int lane = threadIdx.x & 63;
-  for (int64_t m = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6; m < M;
-       m += ((int64_t)gridDim.x * blockDim.x) >> 6) {
-    const int64_t n = (int64_t)C_out * sp;
-    KSum ks;
-    for (int64_t j = lane; j < n; j += 64) ks.add(ew[m * n + j] * bias[j / sp]);
-    const float s = wave_sum_comp(ks);
-    if (lane == 0) acc[m] += s;
+// acc[m] += sum_{co, p} ew[m, co, p] * bias[co].  One workgroup per row
+// (rows of a conv layer are tens of thousands of values long); products in
+// fp32 as the reference's (ew * bias_flat) forms them, summed in fp64,
+// reduced over the workgroup in a fixed order.
+template <bool VEC>
+__global__ __launch_bounds__(NT) void k_conv_bias_dot(const float* ew, int64_t M, int C_out,
+                                                      int sp, FastDiv f_sp, const float* bias,
+                                                      float* acc) {
+  __shared__ double red[NT / 64];
+  const int64_t n = (int64_t)C_out * sp;
+  for (int64_t m = blockIdx.x; m < M; m += gridDim.x) {
+    const float* row = ew + m * n;
+    double p = 0.0;
+    if (VEC) {
+      for (int64_t q = threadIdx.x; 4 * q < n; q += NT) {
+        const float4 v = reinterpret_cast<const float4*>(row)[q];
+        const uint32_t j = (uint32_t)(4 * q);
+        p += (double)(v.x * bias[f_sp.div(j)]);
+        p += (double)(v.y * bias[f_sp.div(j + 1)]);
+        p += (double)(v.z * bias[f_sp.div(j + 2)]);
+        p += (double)(v.w * bias[f_sp.div(j + 3)]);
+      }
+    } else {
+      for (int64_t j = threadIdx.x; j < n; j += NT)
+        p += (double)(row[j] * bias[f_sp.div((uint32_t)j)]);
+    }
+    p = wave_sum_f64(p);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = p;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      acc[m] = (float)((double)acc[m] + ((red[0] + red[1]) + (red[2] + red[3])));
+    __syncthreads();
   }
 }
 
@@ -171,6 +375,43 @@ int check_geom(const ConvGeom& g) {
   return VC_OK;
 }
 
+// Columns and K of one implicit GEMM must fit the core's int indices (and
+// the 31-bit range of FastDiv).
+constexpr int64_t kMaxDim = (int64_t(1) << 31) - 1;
+
+// The gather of a forward convolution over images of (C_in, H, W) laid out
+// with the given strides; nk generator columns per pixel.
+template <int NS>
+LoadGather<NS, false> forward_gather(const ConvGeom& g, const float* src, const float* src2,
+                                     int64_t s_img, int64_t s_c, int s_y, int s_x, int nk) {
+  LoadGather<NS, false> b{};
+  b.src = src;
+  b.src2 = src2;
+  b.s_img = s_img;
+  b.s_c = s_c;
+  b.s_y = s_y;
+  b.s_x = s_x;
+  b.Hs = g.H;
+  b.Ws = g.W;
+  b.nk = nk;
+  b.T = g.kh * g.kw;
+  b.Tx = g.kw;
+  b.psy = g.sh;
+  b.psx = g.sw;
+  b.ph = g.ph;
+  b.pw = g.pw;
+  b.sh = g.sh;
+  b.sw = g.sw;
+  b.Wg = g.Wo;
+  b.per_img = (int64_t)g.Ho * g.Wo * nk;
+  b.f_img = FastDiv::make((uint32_t)b.per_img);
+  b.f_nk = FastDiv::make((uint32_t)nk);
+  b.f_wg = FastDiv::make((uint32_t)g.Wo);
+  b.f_T = FastDiv::make((uint32_t)b.T);
+  b.f_Tx = FastDiv::make((uint32_t)b.Tx);
+  return b;
+}
+
 }  // namespace
 
 extern "C" int vc_ibp_conv(const float* l, const float* h, int64_t B, int C_in, int H, int W,
@@ -179,12 +420,14 @@ extern "C" int vc_ibp_conv(const float* l, const float* h, int64_t B, int C_in, 
                            float* hi, vc_stream_t stream) {
   ConvGeom g{C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, H_out, W_out};
   if (check_geom(g) != VC_OK || !l || !h || !kernel || !lo || !hi || B < 0) return VC_ERR_ARG;
-  const int64_t total = B * (int64_t)C_out * H_out * W_out;
-  if (total == 0) return VC_OK;
-  hipLaunchKernelGGL(k_ibp_conv, dim3(vc_blocks(total, NT)), dim3(NT), 0, (hipStream_t)stream,
-                     l, h, B, g, kernel, bias, lo, hi);
-  VC_LAUNCH_CHECK();
-  return VC_OK;
+  const int64_t npix = (int64_t)H_out * W_out, N = B * npix, Kd = (int64_t)C_in * kh * kw;
+  if (N == 0) return VC_OK;
+  if (N > kMaxDim || Kd > kMaxDim) return VC_ERR_UNSUPPORTED;
+  const int64_t n_in = (int64_t)C_in * H * W;
+  auto gb = forward_gather<2>(g, l, h, n_in, (int64_t)H * W, W, 1, 1);
+  EpConv<2> ep{bias, lo, hi, npix, (int64_t)C_out * npix, npix, FastDiv::make((uint32_t)npix)};
+  return launch_gemm<2, false>(1, C_out, (int)N, (int)Kd, LoadKernel<2>{kernel, (int)Kd}, gb, ep,
+                               nullptr, false, (hipStream_t)stream);
 }
 
 extern "C" int vc_zono_conv(const float* c, const float* G, int64_t B, int Kg, int C_in, int H,
@@ -195,15 +438,24 @@ extern "C" int vc_zono_conv(const float* c, const float* G, int64_t B, int Kg, i
   if (check_geom(g) != VC_OK || !c || !kernel || !c_out || B < 0 || Kg < 0) return VC_ERR_ARG;
   if (Kg > 0 && (!G || !G_out)) return VC_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
-  const int64_t total = B * (int64_t)C_out * H_out * W_out;
-  if (total == 0) return VC_OK;
-  hipLaunchKernelGGL(k_conv_center, dim3(vc_blocks(total, NT)), dim3(NT), 0, st, c, B, g,
-                     kernel, bias, c_out);
-  if (Kg > 0)
-    hipLaunchKernelGGL(k_zono_conv_gen, dim3(vc_blocks(total * Kg, NT)), dim3(NT), 0, st, G,
-                       B, Kg, g, kernel, G_out);
-  VC_LAUNCH_CHECK();
-  return VC_OK;
+  const int64_t npix = (int64_t)H_out * W_out, Kd = (int64_t)C_in * kh * kw;
+  const int64_t n_in = (int64_t)C_in * H * W, n_out = (int64_t)C_out * npix;
+  if (B == 0) return VC_OK;
+  if (B * npix * (Kg > 0 ? Kg : 1) > kMaxDim || Kd > kMaxDim) return VC_ERR_UNSUPPORTED;
+  {
+    auto gb = forward_gather<1>(g, c, nullptr, n_in, (int64_t)H * W, W, 1, 1);
+    EpConv<1> ep{bias, c_out, nullptr, npix, n_out, npix, FastDiv::make((uint32_t)npix)};
+    const int rc = launch_gemm<1, false>(1, C_out, (int)(B * npix), (int)Kd,
+                                         LoadKernel<1>{kernel, (int)Kd}, gb, ep, nullptr, false, st);
+    if (rc != VC_OK) return rc;
+  }
+  if (Kg == 0) return VC_OK;
+  // generator columns: element (b, ci, y, x, k) at ((b n_in + (ci H + y) W + x) Kg + k
+  auto gb = forward_gather<1>(g, G, nullptr, n_in * Kg, (int64_t)H * W * Kg, W * Kg, Kg, Kg);
+  const int64_t per = npix * Kg;
+  EpConv<1> ep{nullptr, G_out, nullptr, per, n_out * Kg, per, FastDiv::make((uint32_t)per)};
+  return launch_gemm<1, false>(1, C_out, (int)(B * per), (int)Kd, LoadKernel<1>{kernel, (int)Kd},
+                               gb, ep, nullptr, false, st);
 }
 
 extern "C" int vc_backward_conv(const float* ew_in, int64_t M, const float* kernel,
@@ -215,12 +467,64 @@ extern "C" int vc_backward_conv(const float* ew_in, int64_t M, const float* kern
   if (bias && !acc) return VC_ERR_ARG;
   if (M == 0) return VC_OK;
   hipStream_t st = (hipStream_t)stream;
-  if (bias)
-    hipLaunchKernelGGL(k_conv_bias_dot, dim3(vc_blocks(M * 64, NT)), dim3(NT), 0, st, ew_in, M,
-                       C_out, H_out * W_out, bias, acc);
-  const int64_t total = M * (int64_t)C_in * H * W;
-  hipLaunchKernelGGL(k_conv_transpose, dim3(vc_blocks(total, NT)), dim3(NT), 0, st, ew_in, M,
-                     g, kernel, ew_out);
+  const int Hc = (H + sh - 1) / sh, Wc = (W + sw - 1) / sw;
+  const int Ty = (kh + sh - 1) / sh, Tx = (kw + sw - 1) / sw;
+  const int64_t npix = (int64_t)Hc * Wc, N = M * npix, Kd = (int64_t)C_out * Ty * Tx;
+  if (N > kMaxDim || Kd > kMaxDim) return VC_ERR_UNSUPPORTED;
+  if (bias) {
+    const int sp = H_out * W_out;
+    const bool v = ((int64_t)C_out * sp) % 4 == 0 && aligned16(ew_in);
+    const dim3 grid((unsigned)(M < kMaxGrid ? M : kMaxGrid));
+    if (v)
+      hipLaunchKernelGGL(k_conv_bias_dot<true>, grid, dim3(NT), 0, st, ew_in, M, C_out, sp,
+                         FastDiv::make((uint32_t)sp), bias, acc);
+    else
+      hipLaunchKernelGGL(k_conv_bias_dot<false>, grid, dim3(NT), 0, st, ew_in, M, C_out, sp,
+                         FastDiv::make((uint32_t)sp), bias, acc);
+  }
   VC_LAUNCH_CHECK();
-  return VC_OK;
+  const size_t lds = (size_t)C_out * kh * kw * C_in * sizeof(double);
+  if (C_in <= kSmallC && lds <= (size_t)kSmallCLds) {
+    const int64_t total = M * H * W;
+    const dim3 grid((unsigned)((total + NT - 1) / NT < kMaxGrid ? (total + NT - 1) / NT : kMaxGrid));
+    switch (C_in) {
+      case 1: hipLaunchKernelGGL(k_conv_t_smallc<1>, grid, dim3(NT), lds, st, ew_in, M, g, kernel, ew_out); break;
+      case 2: hipLaunchKernelGGL(k_conv_t_smallc<2>, grid, dim3(NT), lds, st, ew_in, M, g, kernel, ew_out); break;
+      case 3: hipLaunchKernelGGL(k_conv_t_smallc<3>, grid, dim3(NT), lds, st, ew_in, M, g, kernel, ew_out); break;
+      default: hipLaunchKernelGGL(k_conv_t_smallc<4>, grid, dim3(NT), lds, st, ew_in, M, g, kernel, ew_out); break;
+    }
+    VC_LAUNCH_CHECK();
+    return VC_OK;
+  }
+  LoadGather<1, true> gb{};
+  gb.src = ew_in;
+  gb.src2 = nullptr;
+  gb.s_img = (int64_t)C_out * H_out * W_out;
+  gb.s_c = (int64_t)H_out * W_out;
+  gb.s_y = W_out;
+  gb.s_x = 1;
+  gb.Hs = H_out;
+  gb.Ws = W_out;
+  gb.nk = 1;
+  gb.T = Ty * Tx;
+  gb.Tx = Tx;
+  gb.psy = 1;
+  gb.psx = 1;
+  gb.ph = ph;
+  gb.pw = pw;
+  gb.sh = sh;
+  gb.sw = sw;
+  gb.Wg = Wc;
+  gb.per_img = npix;
+  gb.f_img = FastDiv::make((uint32_t)npix);
+  gb.f_nk = FastDiv::make(1);
+  gb.f_wg = FastDiv::make((uint32_t)Wc);
+  gb.f_T = FastDiv::make((uint32_t)gb.T);
+  gb.f_Tx = FastDiv::make((uint32_t)Tx);
+  LoadKernelT la{kernel, C_in, kh, kw, sh, sw, ph, pw, Ty * Tx, Tx, Ty,
+                 FastDiv::make((uint32_t)(Ty * Tx)), FastDiv::make((uint32_t)Tx)};
+  EpConvT ep{ew_out, H, W, Wc, sh, sw, npix, (int64_t)C_in * H * W,
+             FastDiv::make((uint32_t)npix), FastDiv::make((uint32_t)Wc)};
+  return launch_gemm<1, false>((int64_t)sh * sw, C_in, (int)N, (int)Kd, la, gb, ep, nullptr, false,
+                               st);
 }

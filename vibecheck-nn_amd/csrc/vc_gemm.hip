@@ -1,306 +1,16 @@
-// Generic fp32 MFMA GEMM with fused prologues/epilogues.
-//
-// C[m, n] = sum_k A[m, k] * B[k, n].  A workgroup of 256 threads (4 waves,
-// 2 x 2) owns a (32 FM) x (32 FN) tile; each wave owns (16 FM) x (16 FN) as
-// FM x FN blocks of v_mfma_f32_16x16x4_f32.  Three tile shapes are built:
-// 64x64, 128x64 and 128x128; the launcher picks the largest one that still
-// gives the chip several waves of workgroups.
-//
-// K runs in BK = 16 tiles through two LDS buffers: the global loads of tile
-// t+1 are issued into registers before the MFMAs of tile t, and the
-// loader's arithmetic (e.g. the ReLU relaxation of a CROWN backward row)
-// and the LDS store of tile t+1 follow them, so one barrier per tile.
-// Operands arrive as quads of 4 consecutive elements along their contiguous
-// dimension (one 16-byte load when the host found every stride and base
-// aligned).  Per-row index math (domain of a row, broadcast rows) is done
-// once per tile, not per element.
-//
-// Each K-tile is reduced by MFMA into a fresh fp32 accumulator and folded
-// into an fp64 running sum (two VALU ops per element), so the rounding
-// error does not grow with K: the result is the 16-term tile partials
-// summed exactly enough to round once at the end (the fp32 sums are at
-// least as accurate as a blocked CPU BLAS).
-//
-// Tiles are dealt so that the workgroups of one XCD (blocks b with the same
-// b mod 8) take consecutive tiles: the column tiles of one row block share
-// that XCD's L2 for the A rows.
-#include <initializer_list>
-
-#include "vc_common.h"
+// fp32 MFMA GEMMs of the fc layers: the interval forward, the zonotope
+// forward, the CROWN backward step (fused, or two-phase through relax_out),
+// and the alpha gradient sweep.  The GEMM core is vc_gemm_core.h.
+#include "vc_gemm_core.h"
 #include "vc_relax.h"
 
 namespace {
 
-constexpr int NT = 256;
-constexpr int PAD = 16;  // LDS row padding: MFMA fragment reads hit distinct banks
-
-// LDS row of element kk (0 .. BK-1) of a K-tile.  Quads deliver 4
-// consecutive k; element j of quad q is stored at row (BK/4) j + q, so the
-// quads of a row block land in different banks.  A and B use the same map;
-// the order of k inside a tile does not change the product.
-template <int BK>
-__device__ __forceinline__ int krow(int kk) { return (BK / 4) * (kk & 3) + (kk >> 2); }
-
-// p[0 .. n-1] into o[0..3] (n <= 4), zeros past n; one 16-byte load when
-// VEC and n == 4 (VEC: the host checked 16-byte alignment of every quad).
-template <bool VEC>
-__device__ __forceinline__ void ld4(const float* p, int n, float* o) {
-  if (VEC && n == 4) {
-    const float4 v = *reinterpret_cast<const float4*>(p);
-    o[0] = v.x;
-    o[1] = v.y;
-    o[2] = v.z;
-    o[3] = v.w;
-  } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o[j] = 0.f;
-      if (j < n) o[j] = p[j];
-    }
-  }
-}
-
-__device__ __forceinline__ int clamp4(int64_t v) { return v <= 0 ? 0 : (v >= 4 ? 4 : (int)v); }
-
-// Workgroup b of n (1-D grid) -> tile index: the blocks that run on one
-// XCD (same b mod 8) get one contiguous range of tiles.
-__device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t n) {
-  const int64_t q = n >> 3, rem = n & 7;
-  const int64_t x = b & 7, i = b >> 3;
-  return x * q + (x < rem ? x : rem) + i;
-}
-
-// ---------------------------------------------------------------- core
-// NA: number of A/B operand pairs (1, or 2 for the dual IBP product).
-// ACC_ROWS: the A loader also returns a per-element row contribution,
-//   summed into acc_rows[m] by the first column tile of each row block.
-// LA (A loader): Row row(bz, m, first_col_tile); Raw; fetch<VEC>(row, k, n, raw);
-//   finish(row, k, n, raw, v[NA][4], KSum&) for the quad A[m][k .. k+n-1].
-// LB (B loader): kTrans (quads along k of Bt[n][k], else along n of B[k][n]);
-//   const float* ptr(bz, k, n); finish(raw[4], v[NA][4]).
-// EP (epilogue): operator()(bz, m, n, c[NA]).
-template <int NA, bool ACC_ROWS, int FM, int FN, int BK, bool VEC, class LA, class LB, class EP>
-__global__ __launch_bounds__(NT) void gemm_kernel(int64_t M, int N, int K, int tiles_n,
-                                                   int64_t tiles_m, int64_t n_tiles, LA la,
-                                                   LB lb, EP ep, float* acc_rows) {
-  constexpr int BM = 32 * FM, BN = 32 * FN;
-  constexpr int SA = BM + PAD, SB = BN + PAD;
-  constexpr int QR = BK / 4;     // quads per row of a K-tile
-  constexpr int RP = NT / QR;    // rows covered by one pass of the workgroup
-  constexpr int QA = BM / RP;    // A quads per thread per K-tile
-  constexpr int QB = BN / RP;    // B quads per thread per K-tile
-  static_assert(QA * RP == BM && QB * RP == BN, "tile / thread mismatch");
-  constexpr bool TB = LB::kTrans;
-  __shared__ __align__(16) float As[2][NA][BK][SA];
-  __shared__ __align__(16) float Bs[2][NA][BK][SB];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
-  const int g = lane >> 4, r = lane & 15;
-  const int wm = w >> 1, wn = w & 1;
-  const int q4 = tid % QR;  // quad slot along k (A, and B when transposed)
-  const int r4 = tid / QR;  // row (A) or column (transposed B) of the quad
-
-  for (int64_t blk = blockIdx.x; blk < n_tiles; blk += gridDim.x) {
-    int64_t t = xcd_tile(blk, n_tiles);
-    const int tn = (int)(t % tiles_n);
-    t /= tiles_n;
-    const int64_t tm = t % tiles_m;
-    const int64_t bz = t / tiles_m;
-    const int64_t m0 = tm * BM;
-    const int n0 = tn * BN;
-    const bool do_rows = ACC_ROWS && tn == 0 && acc_rows != nullptr;
-
-    typename LA::Row arow[QA];
-    bool aok[QA];
-#pragma unroll
-    for (int p = 0; p < QA; ++p) {
-      const int64_t m = m0 + r4 + RP * p;
-      aok[p] = m < M;
-      arow[p] = la.row(bz, aok[p] ? m : m0, tn == 0);
-    }
-
-    double acc[NA][FM][FN][4];
-#pragma unroll
-    for (int a = 0; a < NA; ++a)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[a][i][j][e] = 0.0;
-    KSum rowpart[QA];
-
-    typename LA::Raw araw[QA];
-    int acnt[QA];
-    float braw[QB][4];
-    int bcnt[QB];
-
-    auto fetch = [&](int k0) {
-#pragma unroll
-      for (int p = 0; p < QA; ++p) {
-        const int k = k0 + 4 * q4;
-        acnt[p] = aok[p] ? clamp4((int64_t)K - k) : 0;
-        la.template fetch<VEC>(arow[p], k, acnt[p], araw[p]);
-      }
-#pragma unroll
-      for (int p = 0; p < QB; ++p) {
-        int k, n;
-        if (TB) {
-          n = n0 + r4 + RP * p;
-          k = k0 + 4 * q4;
-          bcnt[p] = n < N ? clamp4((int64_t)K - k) : 0;
-        } else {
-          const int qi = tid + NT * p;
-          k = k0 + qi / (BN / 4);
-          n = n0 + 4 * (qi % (BN / 4));
-          bcnt[p] = k < K ? clamp4((int64_t)N - n) : 0;
-        }
-        ld4<VEC>(bcnt[p] ? lb.ptr(bz, k, n) : nullptr, bcnt[p], braw[p]);
-      }
-    };
-
-    auto store = [&](int k0, int buf) {
-#pragma unroll
-      for (int p = 0; p < QA; ++p) {
-        float v[NA][4];
-        la.template finish<VEC>(arow[p], k0 + 4 * q4, acnt[p], araw[p], v, rowpart[p], do_rows);
-        const int mm = r4 + RP * p;
-#pragma unroll
-        for (int a = 0; a < NA; ++a)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) As[buf][a][QR * j + q4][mm] = v[a][j];
-      }
-#pragma unroll
-      for (int p = 0; p < QB; ++p) {
-        float v[NA][4];
-        LB::finish(braw[p], v);
-        if (TB) {
-          const int nn = r4 + RP * p;
-#pragma unroll
-          for (int a = 0; a < NA; ++a)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) Bs[buf][a][QR * j + q4][nn] = v[a][j];
-        } else {
-          const int qi = tid + NT * p;
-          const int kk = qi / (BN / 4), nn = 4 * (qi % (BN / 4));
-#pragma unroll
-          for (int a = 0; a < NA; ++a)
-            *reinterpret_cast<float4*>(&Bs[buf][a][krow<BK>(kk)][nn]) =
-                make_float4(v[a][0], v[a][1], v[a][2], v[a][3]);
-        }
-      }
-    };
-
-    fetch(0);
-    store(0, 0);
-    __syncthreads();
-    int buf = 0;
-    for (int k0 = 0; k0 < K; k0 += BK) {
-      const bool more = k0 + BK < K;
-      if (more) fetch(k0 + BK);
-#pragma unroll
-      for (int a = 0; a < NA; ++a) {
-        v4f tt[FM][FN];
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int j = 0; j < FN; ++j) tt[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < BK / 4; ++ks) {
-          float af[FM], bf[FN];
-#pragma unroll
-          for (int i = 0; i < FM; ++i) af[i] = As[buf][a][4 * ks + g][wm * 16 * FM + 16 * i + r];
-#pragma unroll
-          for (int j = 0; j < FN; ++j) bf[j] = Bs[buf][a][4 * ks + g][wn * 16 * FN + 16 * j + r];
-#pragma unroll
-          for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j) tt[i][j] = mfma16x16x4(af[i], bf[j], tt[i][j]);
-        }
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[a][i][j][e] += (double)tt[i][j][e];
-      }
-      if (more) store(k0 + BK, buf ^ 1);
-      __syncthreads();
-      buf ^= 1;
-    }
-
-    if (do_rows) {
-#pragma unroll
-      for (int p = 0; p < QA; ++p) {
-        float v = rowpart[p].value();
-#pragma unroll
-        for (int o = 1; o < QR; o <<= 1) v += __shfl_xor(v, o, 64);
-        if (q4 == 0 && aok[p]) acc_rows[m0 + r4 + RP * p] += v;
-      }
-    }
-
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t m = m0 + wm * 16 * FM + i * 16 + 4 * g + e;
-          const int n = n0 + wn * 16 * FN + j * 16 + r;
-          if (m < M && n < N) {
-            float c[NA];
-#pragma unroll
-            for (int a = 0; a < NA; ++a) c[a] = (float)acc[a][i][j][e];
-            ep(bz, m, n, c);
-          }
-        }
-  }
-}
-
-constexpr int64_t kMaxGrid = 1 << 20;  // workgroups; tiles beyond loop (a multiple of 8)
+using namespace vcg;
 
 // vc_backward_fc runs its two-phase form (relaxed rows through relax_out)
 // from this row width up; narrower rows keep the fused prologue.
 constexpr int kTwoPhaseMinWidth = 64;
-
-// One tile shape, 64x64 (FM = FN = 2), for every GEMM: measured on MI355X
-// against 128x64 and 128x128 at the workload shapes (1024-wide fc backward,
-// 256-wide spec backward, 784->256 interval fc, 1024x1024 zonotope
-// generators), the small tile wins everywhere, because it keeps 3-4 waves
-// per SIMD to cover the global-load latency.  The K-tile depth comes from
-// the A loader: 32 for plain loads (fewer barriers, the fold every 32 k),
-// 16 when the loader's per-element arithmetic holds more registers.
-template <int NA, bool ACC_ROWS, class LA, class LB, class EP>
-int launch_gemm(int64_t batch, int64_t M, int N, int K, LA la, LB lb, EP ep, float* acc_rows,
-                bool vec, hipStream_t st) {
-  if (M <= 0 || N <= 0 || batch <= 0) return VC_OK;
-  constexpr int FM = 2, FN = 2, BM = 32 * FM, BN = 32 * FN, BK = LA::kBK;
-  const int tiles_n = (N + BN - 1) / BN;
-  const int64_t tiles_m = (M + BM - 1) / BM;
-  const int64_t n_tiles = batch * tiles_m * tiles_n;
-  const int64_t grid = n_tiles < kMaxGrid ? n_tiles : kMaxGrid;
-  if (vec)
-    hipLaunchKernelGGL((gemm_kernel<NA, ACC_ROWS, FM, FN, BK, true, LA, LB, EP>),
-                       dim3((unsigned)grid), dim3(NT), 0, st, M, N, K, tiles_n, tiles_m, n_tiles,
-                       la, lb, ep, acc_rows);
-  else
-    hipLaunchKernelGGL((gemm_kernel<NA, ACC_ROWS, FM, FN, BK, false, LA, LB, EP>),
-                       dim3((unsigned)grid), dim3(NT), 0, st, M, N, K, tiles_n, tiles_m, n_tiles,
-                       la, lb, ep, acc_rows);
-  VC_LAUNCH_CHECK();
-  return VC_OK;
-}
-
-// every pointer 16-byte aligned and every stride a multiple of 4 floats
-static inline bool vec_ok(std::initializer_list<const void*> ptrs,
-                          std::initializer_list<int64_t> strides) {
-  for (const void* p : ptrs)
-    if (p && !aligned16(p)) return false;
-  for (int64_t s : strides)
-    if (s % 4) return false;
-  return true;
-}
 
 // ------------------------------------------------------------- A loaders
 struct LoadMidRad {  // A = (mid, rad) of an interval row-block
@@ -326,28 +36,6 @@ struct LoadMidRad {  // A = (mid, rad) of an interval row-block
       v[0][j] = (x.l[j] + x.h[j]) / 2.f;
       v[1][j] = (x.h[j] - x.l[j]) / 2.f;
     }
-  }
-};
-
-struct LoadRow {  // A[m][k] plain (row-major, ld)
-  static constexpr int kBK = 32;
-  const float* A;
-  int ld;
-  struct Row {
-    int64_t o;
-  };
-  struct Raw {
-    float x[4];
-  };
-  __device__ Row row(int64_t, int64_t m, bool) const { return Row{m * ld}; }
-  template <bool VEC>
-  __device__ void fetch(const Row& rw, int k, int n, Raw& x) const {
-    ld4<VEC>(A + rw.o + k, n, x.x);
-  }
-  template <bool VEC>
-  __device__ void finish(const Row&, int, int, const Raw& x, float (*v)[4], KSum&, bool) const {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[0][j] = x.x[j];
   }
 };
 
@@ -535,8 +223,20 @@ struct LoadWtAbs {  // B[k][n] = (W[n][k], |W[n][k]|), W (n_out, ld)
   static constexpr bool kTrans = true;
   const float* W;
   int ld;
-  __device__ const float* ptr(int64_t, int k, int n) const { return W + (int64_t)n * ld + k; }
-  __device__ static void finish(const float* x, float (*v)[4]) {
+  struct Col {
+    int64_t o;
+  };
+  struct Raw {
+    float x[4];
+  };
+  __device__ Col col(int64_t, int n) const { return Col{(int64_t)n * ld}; }
+  template <bool VEC>
+  __device__ void fetch(const Col& c, int k, int cnt, Raw& r) const {
+    float* o = r.x;
+    ld4<VEC>(W + c.o + k, cnt, o);
+  }
+  __device__ static void finish(const Raw& r, float (*v)[4]) {
+    const float* x = r.x;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       v[0][j] = x[j];
@@ -544,35 +244,25 @@ struct LoadWtAbs {  // B[k][n] = (W[n][k], |W[n][k]|), W (n_out, ld)
     }
   }
 };
-struct LoadWt {  // B[k][n] = W[n][k]
-  static constexpr bool kTrans = true;
-  const float* W;
-  int ld;
-  __device__ const float* ptr(int64_t, int k, int n) const { return W + (int64_t)n * ld + k; }
-  __device__ static void finish(const float* x, float (*v)[4]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[0][j] = x[j];
-  }
-};
-struct LoadW {  // B[k][n] = W[k][n]
-  static constexpr bool kTrans = false;
-  const float* W;
-  int ld;
-  __device__ const float* ptr(int64_t, int k, int n) const { return W + (int64_t)k * ld + n; }
-  __device__ static void finish(const float* x, float (*v)[4]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[0][j] = x[j];
-  }
-};
 struct LoadGen {  // B[k][n] = G[bz][k][n]
   static constexpr bool kTrans = false;
   const float* G;
   int64_t stride_b;
   int ld;
-  __device__ const float* ptr(int64_t bz, int k, int n) const {
-    return G + bz * stride_b + (int64_t)k * ld + n;
+  struct Col {
+    int64_t o;
+  };
+  struct Raw {
+    float x[4];
+  };
+  __device__ Col col(int64_t bz, int n) const { return Col{bz * stride_b + n}; }
+  template <bool VEC>
+  __device__ void fetch(const Col& c, int k, int cnt, Raw& r) const {
+    float* o = r.x;
+    ld4<VEC>(G + c.o + (int64_t)k * ld, cnt, o);
   }
-  __device__ static void finish(const float* x, float (*v)[4]) {
+  __device__ static void finish(const Raw& r, float (*v)[4]) {
+    const float* x = r.x;
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[0][j] = x[j];
   }
@@ -587,14 +277,6 @@ struct EpIbp {
     const float mc = bias ? c[0] + bias[n] : c[0];
     lo[m * ld + n] = mc - c[1];
     hi[m * ld + n] = mc + c[1];
-  }
-};
-struct EpStoreBias {
-  const float* bias;
-  float* out;
-  int ld;
-  __device__ void operator()(int64_t, int64_t m, int n, const float* c) const {
-    out[m * ld + n] = bias ? c[0] + bias[n] : c[0];
   }
 };
 struct EpGen {
