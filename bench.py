@@ -343,7 +343,9 @@ def kernel_suite(reps):
         acc = torch.zeros(M, device=dev)
         fn = lambda: call('vc_backward_conv', ptr(ew), M, ptr(K), ptr(bias), C_out, Ho, Ho, C_in,
                           H, H, k, k, cs, cs, cp, cp, ptr(out), ptr(acc), st)
-        report('a7', 'gemm_kernel (transposed conv, implicit GEMM) + k_conv_bias_dot',
+        kern = ('k_conv_t_smallc' if C_in <= 4 else
+                'gemm_kernel (transposed conv, implicit GEMM)') + ' + k_conv_bias_dot'
+        report('a7', kern,
                f'conv {C_in}->{C_out} {k}x{k} s{cs} p{cp} ({H}x{H} in), 576 rows '
                '(64 domains x 9)', _time_launches([fn], max(3, reps // 4)), 'mfma',
                2.0 * M * (C_out * Ho * Ho) * (C_in * k * k))
