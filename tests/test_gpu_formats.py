@@ -1,0 +1,48 @@
+"""Known answers on a real network through the drop-in driver (GPU).
+
+The reference's bundled ACAS-Xu example (fixtures in tests/golden/acasxu/,
+read by vibecheck_amd.onnx_net and vibecheck_amd.vnnlib): its README runs
+prop_1 to 'verified' (unsat) and finds prop_2 violated at a printed input.
+Here the input-split driver must verify prop_1, must never verify prop_2,
+and the GPU's interval forward at the witness (a zero-width box) must
+reproduce the printed output."""
+import os
+
+import pytest
+import torch
+
+from vibecheck_amd import onnx_net, vnnlib
+from vibecheck_amd import verify_graph as vg
+from vibecheck_amd import verify_zono_bnb as vz
+
+from test_formats import GOLD, NET, WITNESS_X, WITNESS_Y
+
+pytestmark = pytest.mark.gpu
+F32 = torch.float32
+SETTINGS = {'total_timeout': 60.0, 'input_split_batch_size': 4096,
+            'input_split_crown_intermediate': True,
+            'input_split_batched_clip_enabled': True}
+
+
+def test_acasxu_prop1_verified(gpu):
+    gg = onnx_net.load_onnx(NET, device=gpu, dtype=F32)
+    spec = vnnlib.load_vnnlib(os.path.join(GOLD, 'prop_1.vnnlib'))
+    verdict, details = vg._input_split_batched(None, spec, SETTINGS, gg, gpu, F32)
+    print(f'prop_1: {verdict} {details}')
+    assert verdict == 'verified', details
+
+
+def test_acasxu_prop2_never_verified_and_witness_forward(gpu):
+    gg = onnx_net.load_onnx(NET, device=gpu, dtype=F32)
+    x = torch.tensor([WITNESS_X], dtype=F32, device=gpu)
+    sb = vz._ibp_forward_graph_batched(x, x, gg, gpu, F32)
+    _, (c, _) = vz._forward_zonotope_graph_batched(x, x, gg, gpu, F32)
+    y = c.double().cpu()[0]
+    err = (y - torch.tensor(WITNESS_Y, dtype=torch.float64)).abs().max()
+    assert float(err) < 2e-8, float(err)
+    assert len(sb) == 6
+    spec = vnnlib.load_vnnlib(os.path.join(GOLD, 'prop_2.vnnlib'))
+    settings = dict(SETTINGS, input_split_batched_max_iters=12)
+    verdict, details = vg._input_split_batched(None, spec, settings, gg, gpu, F32)
+    print(f'prop_2: {verdict} {details}')
+    assert verdict != 'verified', details
