@@ -596,6 +596,42 @@ int vc_bisect(const float *xl, const float *xh, const int64_t *ax,
               float *low_xh, float *high_xl, float *high_xh,
               vc_stream_t stream);
 
+/* Split-dimension selection: the K (1..8, <= n) best input dimensions of
+ * each of B leaves, best first, into dims (B, K).  Scores in the
+ * reference's fp32 operation order (verify_graph.py:13271-13285):
+ *   mode 0: widest, w_i = xh_i - xl_i;
+ *   mode 1: SB sum, w_i * sum_q |A[b, q, i]| (q ascending);
+ *   mode 2: SB margin, max_q (max(|A[b, q, i]|, thr) * w_i / 2 + lb[b, q] * mw).
+ * A (B, Q, n) is the leaves' input linearization, lb (B, Q) their spec lower
+ * bounds (mode 2 only).  Ties go to the lower index (torch.argmax's first
+ * maximum for K = 1; for K > 1 the order of a stable descending sort, which
+ * is torch.topk's wherever the scores differ).  usable (B, nullable): the
+ * first chosen dimension is wider than 1e-12 (the bisection's test).
+ * Replaces the score and argmax / topk of verify_graph.py:13244-13291,
+ * 13348-13351. */
+int vc_branch_topk(const float *xl, const float *xh, const float *A,
+                   const float *lb, int64_t B, int Q, int n, int mode,
+                   float thr, float mw, int K, int64_t *dims,
+                   uint8_t *usable, vc_stream_t stream);
+
+/* Plan of the 2^K-way split (verify_graph.py:13392-13420): per leaf the
+ * usable dimensions among its K split dimensions dims (B, K) (width >
+ * 1e-12), children 2^K_u (0 when none is usable).  offsets (B + 1): the
+ * exclusive prefix sum of the child counts, offsets[B] the total;
+ * n_degenerate: leaves with no usable dimension.  One workgroup. */
+int vc_split_multi_plan(const float *xl, const float *xh, const int64_t *dims,
+                        int64_t B, int n, int K, int64_t *offsets,
+                        int64_t *n_degenerate, vc_stream_t stream);
+
+/* The children of that plan into out_xl / out_xh (offsets[B], n): leaf b's
+ * child combo (0 .. 2^K_u - 1) at row offsets[b] + combo, bit k of combo
+ * taking the high half (lower end = midpoint (lo + hi) / 2) of the k-th
+ * usable dimension, else the low half.  Replaces the per-leaf loop of
+ * verify_graph.py:13392-13420. */
+int vc_split_multi(const float *xl, const float *xh, const int64_t *dims,
+                   const int64_t *offsets, int64_t B, int n, int K,
+                   float *out_xl, float *out_xh, vc_stream_t stream);
+
 /* One input-split BaB round on the narrow-MLP kernels (the bound,
  * alpha, clip and split phases of verify_graph.py:12855-13382, with
  * crown intermediate bounds, the clip on and alpha-CROWN on every open leaf),

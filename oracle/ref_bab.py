@@ -4,8 +4,9 @@ Test infrastructure: see the package docstring.  Follows
 ``_input_split_batched_inner`` and ``_clip_box_by_halfspaces_batched`` of the
 reference (verify_graph.py:12363-12426, 12511-13464) for the settings this
 engine supports: CROWN or zonotope intermediate bounds, domain clipping,
-batched alpha-CROWN on unclosed leaves, widest-dimension bisection (K = 1).
-Root PGD, leaf PGD, SB branching, MILP/LP escalation are not part of it.
+batched alpha-CROWN on unclosed leaves, widest-dimension or SB (sum or
+margin score) split dimensions, bisection or the 2^K-way split on the top K
+dimensions.  Root PGD, leaf PGD, MILP/LP escalation are not part of it.
 """
 import time
 
@@ -97,6 +98,64 @@ def bisect(xl, xh, ax):
     return n_deg, (xl_u, xh_low), (xl_high, xh_u)
 
 
+def sb_scores(xl, xh, A, lb, margin=False, thr=0.01, mw=1.0):
+    """Split-dimension scores of SB branching (verify_graph.py:13255-13285):
+    widths * sum_q |A_q| (the default 'sum' form) or, with ``margin``,
+    max_q (|A_q|.clamp(thr) * widths / 2 + lb_q * mw).  xl, xh (B, n);
+    A (B, Q, n); lb (B, Q)."""
+    widths = xh - xl
+    if margin:
+        base = A.abs().clamp(min=thr) * widths.unsqueeze(1) / 2
+        base = base + lb.unsqueeze(-1) * mw
+        return base.amax(dim=1)
+    sens = A.abs().sum(dim=1)
+    return widths * sens
+
+
+def top_dims(scores, K):
+    """The K best dimensions per row, best first (verify_graph.py:13291,
+    13348-13351): argmax (first maximum) for K = 1; for K > 1 a stable
+    descending sort, i.e. torch.topk's order with ties broken by the lower
+    index."""
+    if K == 1:
+        return scores.argmax(dim=1, keepdim=True)
+    return torch.sort(scores, dim=1, descending=True, stable=True).indices[:, :K]
+
+
+def split_multi(xl, xh, dims):
+    """2^K-way split of every leaf on its K dimensions dims (B, K)
+    (verify_graph.py:13392-13420): the dimensions wider than 1e-12, in
+    order, each halved at (lo + hi) / 2; child ``combo`` takes the high
+    half of usable dimension k when bit k is set.  Leaves without a usable
+    dimension are dropped and counted.  Returns (n_degenerate, (xl, xh) of
+    the children, leaf-major)."""
+    kids_l, kids_h = [], []
+    n_deg = 0
+    for i in range(xl.shape[0]):
+        usable, mids = [], []
+        for k in range(dims.shape[1]):
+            d = int(dims[i, k])
+            if float(xh[i, d] - xl[i, d]) > 1e-12:
+                usable.append(d)
+                mids.append(float((xl[i, d] + xh[i, d]) / 2))
+        if not usable:
+            n_deg += 1
+            continue
+        for combo in range(1 << len(usable)):
+            cl, ch = xl[i].clone(), xh[i].clone()
+            for k, d in enumerate(usable):
+                if (combo >> k) & 1:
+                    cl[d] = mids[k]
+                else:
+                    ch[d] = mids[k]
+            kids_l.append(cl)
+            kids_h.append(ch)
+    n = xl.shape[1]
+    if not kids_l:
+        return n_deg, (xl.new_zeros(0, n), xh.new_zeros(0, n))
+    return n_deg, (torch.stack(kids_l), torch.stack(kids_h))
+
+
 class ChunkWorklist:
     """LIFO worklist of 2-D chunks (verify_graph.py:12695-12726)."""
 
@@ -185,14 +244,20 @@ def alpha_on_leaves(lb, xl, xh, gg, spec_ew, disj_q_idx, closed,
 
 def bab_step(xl, xh, gg, spec_ew, disj_q_idx, crown_intermediate=True,
              clip_enabled=True, alpha_iters=0, alpha_all=False, alpha_eps=0.0,
-             alpha_max_leaves=200, alpha_lr=0.25, alpha_lr_decay=0.98):
+             alpha_max_leaves=200, alpha_lr=0.25, alpha_lr_decay=0.98,
+             branch_sb=False, sb_margin=False, sb_thr=0.01, sb_mw=1.0, split_depth=1):
     """One BaB iteration on a popped batch: bound, closure, optional
-    alpha-CROWN, one clip iteration, widest-axis bisection
-    (verify_graph.py:12855-13382).
+    alpha-CROWN, one clip iteration, split (verify_graph.py:12855-13423).
+
+    The split dimension is the widest, or with ``branch_sb`` (and a clip,
+    which gives the input linearization A) the best SB score of the
+    feasible leaves' A rows and spec bounds.  ``split_depth`` K > 1 (SB
+    only) splits every leaf on its top K dimensions at once.
 
     Returns a dict with lb, closed, unclosed (indices), feasible (after
-    clip, over unclosed), xl_split/xh_split, ax, n_degenerate, low/high
-    children.
+    clip, over unclosed), xl_split/xh_split, ax, n_degenerate, the
+    children as ``chunks`` (the worklist pushes, in order) and, for
+    bisection, low/high.
     """
     lb, A, acc = bound_batch(xl, xh, gg, spec_ew, crown_intermediate,
                              clip_enabled)
@@ -204,6 +269,7 @@ def bab_step(xl, xh, gg, spec_ew, disj_q_idx, crown_intermediate=True,
     out = {'lb': lb, 'A': A, 'acc': acc, 'closed': closed,
            'unclosed': unclosed, 'n_alpha_leaves': n_al,
            'n_alpha_iters': n_ait}
+    A_s = None
     if clip_enabled and unclosed.numel() > 0 and A is not None:
         xl_u, xh_u = xl[unclosed], xh[unclosed]
         xl_c, xh_c, feas = clip_leaves(xl_u, xh_u, A[unclosed],
@@ -211,17 +277,30 @@ def bab_step(xl, xh, gg, spec_ew, disj_q_idx, crown_intermediate=True,
         fidx = feas.nonzero(as_tuple=True)[0]
         out['feasible'] = feas
         xl_s, xh_s = xl_c[fidx], xh_c[fidx]
+        A_s, lb_s = A[unclosed][fidx], lb[unclosed][fidx]
     else:
         out['feasible'] = None
         xl_s, xh_s = xl[unclosed], xh[unclosed]
     out['xl_split'], out['xh_split'] = xl_s, xh_s
     if xl_s.shape[0] > 0:
-        ax = widest_axis(xl_s, xh_s)
+        if branch_sb and A_s is not None:
+            scores = sb_scores(xl_s, xh_s, A_s, lb_s, sb_margin, sb_thr, sb_mw)
+            K = min(split_depth, xl_s.shape[1])
+            dims = top_dims(scores, K)
+        else:
+            dims = widest_axis(xl_s, xh_s).unsqueeze(1)
+        ax = dims[:, 0]
+        if dims.shape[1] > 1:
+            n_deg, kids = split_multi(xl_s, xh_s, dims)
+            out.update(ax=ax, dims=dims, n_degenerate=n_deg, chunks=[kids], low=None,
+                       high=None)
+            return out
         n_deg, low, high = bisect(xl_s, xh_s, ax)
     else:
         ax = torch.zeros(0, dtype=torch.long)
         n_deg, low, high = 0, (xl_s, xh_s), (xl_s, xh_s)
-    out.update(ax=ax, n_degenerate=n_deg, low=low, high=high)
+    out.update(ax=ax, n_degenerate=n_deg, low=low, high=high,
+               chunks=[low, high] if low[0].shape[0] > 0 else [])
     return out
 
 
@@ -229,8 +308,10 @@ def input_split_batched(xl0, xh0, gg, spec_ew, disj_q_idx, batch_size=4096,
                         max_worklist=200_000, total_timeout=60.0,
                         max_iters=None, **step_kw):
     """Worklist-driven input-split BaB (verify_graph.py:12834-13464) with an
-    optional cap on iterations.  Returns (verdict, details, trace) where
-    trace lists per-iteration dicts (B, n_closed, n_children)."""
+    optional cap on iterations.  A ``split_depth`` K > 1 applies only to a
+    popped batch smaller than batch_size (verify_graph.py:13343-13344).
+    Returns (verdict, details, trace) where trace lists per-iteration dicts
+    (B, n_closed, n_children)."""
     t0 = time.perf_counter()
     wl = ChunkWorklist(xl0, xh0)
     n_leaves = n_iters = n_open = 0
@@ -244,15 +325,16 @@ def input_split_batched(xl0, xh0, gg, spec_ew, disj_q_idx, batch_size=4096,
             break
         B = min(batch_size, wl_n)
         xl, xh = wl.pop(B)
-        st = bab_step(xl, xh, gg, spec_ew, disj_q_idx, **step_kw)
+        kw = dict(step_kw)
+        if B >= batch_size:
+            kw['split_depth'] = 1
+        st = bab_step(xl, xh, gg, spec_ew, disj_q_idx, **kw)
         n_leaves += B
         n_open += st['n_degenerate']
-        low, high = st['low'], st['high']
-        if low[0].shape[0] > 0:
-            wl.push(*low)
-            wl.push(*high)
+        for c in st['chunks']:
+            wl.push(*c)
         trace.append({'B': B, 'n_closed': int(st['closed'].sum()),
-                      'n_children': 2 * int(low[0].shape[0])})
+                      'n_children': sum(int(c[0].shape[0]) for c in st['chunks'])})
         n_iters += 1
         if wl.size() > max_worklist:
             return 'unknown', {'phase': 'batched_worklist_overflow',

@@ -46,3 +46,14 @@ def test_acasxu_prop2_never_verified_and_witness_forward(gpu):
     verdict, details = vg._input_split_batched(None, spec, settings, gg, gpu, F32)
     print(f'prop_2: {verdict} {details}')
     assert verdict != 'verified', details
+
+
+@pytest.mark.parametrize('margin,depth', [(False, 1), (True, 2)])
+def test_acasxu_prop1_verified_with_sb_branching(gpu, margin, depth):
+    gg = onnx_net.load_onnx(NET, device=gpu, dtype=F32)
+    spec = vnnlib.load_vnnlib(os.path.join(GOLD, 'prop_1.vnnlib'))
+    settings = dict(SETTINGS, input_split_batched_branch_sb=True,
+                    input_split_sb_margin_score=margin, bab_split_depth=depth)
+    verdict, details = vg._input_split_batched(None, spec, settings, gg, gpu, F32)
+    print(f'prop_1 SB (margin={margin}, K={depth}): {verdict} {details}')
+    assert verdict == 'verified', details

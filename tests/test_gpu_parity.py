@@ -913,3 +913,80 @@ def test_bab_step_parity_c0(gpu, mlp_path):
     assert torch.equal(cpu(got['ax']), ref['ax'])
     for a, b in zip(got['low'] + got['high'], ref['low'] + ref['high']):
         assert_bounds(a, b, 'C0 children')
+
+
+# ----------------------------------------------------------- SB and K > 1
+@pytest.mark.parametrize('n,Q', [(5, 4), (100, 9), (70, 1)])
+def test_branch_topk_and_multi_split_bit_exact(gpu, n, Q):
+    """vc_branch_topk (widest, SB sum, SB margin; K = 1..4) and the 2^K-way
+    split against the oracle on identical inputs: dimensions, usable flags,
+    children and degenerate counts exact.  Includes tied scores (duplicated
+    columns) and zero-width dimensions."""
+    g = torch.Generator().manual_seed(n + Q)
+    B = 300
+    xl = torch.rand(B, n, generator=g) * 2 - 1
+    xh = xl + torch.rand(B, n, generator=g)
+    A = torch.randn(B, Q, n, generator=g)
+    lb = torch.randn(B, Q, generator=g)
+    A[:, :, 1] = A[:, :, 0]                  # ties in the SB scores ...
+    xh[:, 1] = xl[:, 1] + (xh[:, 0] - xl[:, 0])
+    xh[:7] = xl[:7]                          # ... and degenerate leaves
+    xh[7:20, 0] = xl[7:20, 0]
+    st = torch.cuda.current_stream().cuda_stream
+    d = [t.to(gpu) for t in (xl, xh, A, lb)]
+    for mode in (0, 1, 2):
+        scores = (xh - xl) if mode == 0 else rbab.sb_scores(xl, xh, A, lb, mode == 2, 0.05, 0.5)
+        for K in (1, 2, 4):
+            dims = torch.empty(B, K, dtype=torch.int64, device=gpu)
+            usable = torch.empty(B, dtype=torch.uint8, device=gpu)
+            call('vc_branch_topk', *map(ptr, d), B, Q, n, mode, 0.05, 0.5, K, ptr(dims),
+                 ptr(usable), st)
+            ref = rbab.top_dims(scores, K)
+            torch.cuda.synchronize()
+            assert torch.equal(cpu(dims), ref), (mode, K)
+            w = (xh - xl).gather(1, ref[:, :1]).squeeze(1)
+            assert torch.equal(cpu(usable).bool(), w.double() > 1e-12)
+            if K == 1:
+                continue
+            plan = torch.empty(B + 2, dtype=torch.int64, device=gpu)
+            call('vc_split_multi_plan', ptr(d[0]), ptr(d[1]), ptr(dims), B, n, K, ptr(plan),
+                 ptr(plan[B + 1:]), st)
+            total, n_deg = plan[B:].tolist()
+            kl = torch.empty(total, n, device=gpu)
+            kh = torch.empty(total, n, device=gpu)
+            call('vc_split_multi', ptr(d[0]), ptr(d[1]), ptr(dims), ptr(plan), B, n, K,
+                 ptr(kl), ptr(kh), st)
+            rdeg, (rl, rh) = rbab.split_multi(xl, xh, ref)
+            torch.cuda.synchronize()
+            assert n_deg == rdeg and total == rl.shape[0], (mode, K)
+            assert torch.equal(cpu(kl), rl) and torch.equal(cpu(kh), rh)
+
+
+@pytest.mark.parametrize('margin,depth', [(False, 1), (True, 1), (False, 3)])
+def test_bab_step_sb_branching(gpu, margin, depth):
+    """bab_step with SB branching: the split dimensions are the oracle's SB
+    choice on the step's own clipped boxes, A rows and (post-alpha) bounds
+    of the feasible leaves, and the children equal the oracle's split of
+    those boxes, bit for bit."""
+    gg_c, gg_g, xl, xh = acas(gpu, 256, seed=3, scale=8.0)
+    se_c, se_g, dq = spec_pair(5, gpu)
+    table = vg.DisjunctTable(dq, gpu)
+    st = vg.bab_step(xl.to(gpu), xh.to(gpu), gg_g, se_g, table, alpha_iters=3, alpha_all=True,
+                     branch_sb=True, sb_margin=margin, split_depth=depth)
+    torch.cuda.synchronize()
+    xs, hs = cpu(st['xl_split']), cpu(st['xh_split'])
+    assert xs.shape[0] > 0
+    unc, feas = cpu(st['unclosed']), cpu(st['feasible'])
+    A_s = cpu(st['A'])[unc][feas]
+    lb_s = cpu(st['lb'])[unc][feas]
+    dims = rbab.top_dims(rbab.sb_scores(xs, hs, A_s, lb_s, margin), depth)
+    assert torch.equal(cpu(st['ax']), dims[:, 0])
+    if depth == 1:
+        n_deg, low, high = rbab.bisect(xs, hs, dims[:, 0])
+        ref_chunks = [low, high] if low[0].shape[0] else []
+    else:
+        n_deg, kids = rbab.split_multi(xs, hs, dims)
+        ref_chunks = [kids] if kids[0].shape[0] else []
+    assert st['n_degenerate'] == n_deg and len(st['chunks']) == len(ref_chunks)
+    for (a, b), (c, d) in zip(st['chunks'], ref_chunks):
+        assert torch.equal(cpu(a), c) and torch.equal(cpu(b), d)

@@ -177,3 +177,84 @@ def test_input_split_driver_closes_small_problem():
                                                    max_iters=30)
     assert verdict in ('verified', 'unknown')
     assert det['batched_n_iters'] == len(trace) >= 1
+
+
+# ----------------------------------------------------------- SB and K > 1
+def test_sb_scores_known_answer():
+    """widths (1, 2, 0.5); A rows (1, -1, 4), (2, 0.5, -2); lb (-1, -0.5).
+    sum form: (1 * 3, 2 * 1.5, 0.5 * 6) = (3, 3, 3); margin form (thr 0.6,
+    mw 1): q0 (1*1/2 - 1, 1*2/2 - 1, 4*0.5/2 - 1) = (-0.5, 0, 0),
+    q1 (2*1/2 - 0.5, 0.6*2/2 - 0.5, 2*0.5/2 - 0.5) = (0.5, 0.1, 0), max over
+    q = (0.5, 0.1, 0)."""
+    xl = _t([[0.0, 0.0, 0.0]])
+    xh = _t([[1.0, 2.0, 0.5]])
+    A = _t([[[1.0, -1.0, 4.0], [2.0, 0.5, -2.0]]])
+    lb = _t([[-1.0, -0.5]])
+    s = rbab.sb_scores(xl, xh, A, lb)
+    assert s.tolist() == [[3.0, 3.0, 3.0]]
+    m = rbab.sb_scores(xl, xh, A, lb, margin=True, thr=0.6, mw=1.0)
+    assert torch.allclose(m, _t([[0.5, 0.1, 0.0]]), rtol=0, atol=1e-15)
+    # ties: the first maximum (torch.argmax), a stable order for K > 1
+    assert rbab.top_dims(s, 1).tolist() == [[0]]
+    assert rbab.top_dims(_t([[1.0, 3.0, 3.0, 2.0]]), 1).tolist() == [[1]]
+    assert rbab.top_dims(_t([[1.0, 3.0, 3.0, 2.0]]), 3).tolist() == [[1, 2, 3]]
+
+
+def test_split_multi_partitions_each_leaf():
+    """Brute force: the children of a leaf are its 2^K_u sub-boxes (K_u =
+    dimensions wider than 1e-12 among the K), in combo-bit order, and every
+    sample of the parent box lies in exactly one child (off the split
+    planes); leaves with no usable dimension are dropped and counted."""
+    g = torch.Generator().manual_seed(3)
+    xl = torch.rand(4, 5, generator=g, dtype=DT)
+    xh = xl + torch.rand(4, 5, generator=g, dtype=DT)
+    xh[1, 2] = xl[1, 2]                      # one zero-width split dimension
+    xh[3] = xl[3]                            # a leaf with nothing to split
+    dims = torch.tensor([[4, 0, 2], [2, 1, 3], [0, 1, 2], [1, 2, 3]])
+    n_deg, (cl, ch) = rbab.split_multi(xl, xh, dims)
+    assert n_deg == 1
+    counts = [8, 4, 8]
+    assert cl.shape[0] == sum(counts)
+    row = 0
+    for b, cnt in zip(range(3), counts):
+        usable = [int(d) for d in dims[b] if float(xh[b, d] - xl[b, d]) > 1e-12]
+        assert cnt == 1 << len(usable)
+        kids_l, kids_h = cl[row:row + cnt], ch[row:row + cnt]
+        for c in range(cnt):
+            for k, d in enumerate(usable):
+                mid = (xl[b, d] + xh[b, d]) / 2
+                if (c >> k) & 1:
+                    assert kids_l[c, d] == mid and kids_h[c, d] == xh[b, d]
+                else:
+                    assert kids_l[c, d] == xl[b, d] and kids_h[c, d] == mid
+        pts = xl[b] + torch.rand(500, 5, generator=g, dtype=DT) * (xh[b] - xl[b])
+        inside = ((pts.unsqueeze(1) > kids_l) & (pts.unsqueeze(1) < kids_h)) | \
+            (kids_l == kids_h)
+        assert bool((inside.all(-1).sum(1) == 1).all())
+        row += cnt
+
+
+def test_bab_step_sb_and_multi_split():
+    """One step with SB branching and K = 3: every feasible split leaf gives
+    2^K_u children inside its clipped box, the split dimensions are the
+    top-3 SB scores of that leaf's A rows, and the driver grows the queue."""
+    gg = wk.acas_gg(dtype=DT)
+    xl, xh = wk.acas_boxes(32, seed=2, dtype=DT)
+    c, r = (xl + xh) / 2, (xh - xl) / 2
+    xl, xh = c - 8 * r, c + 8 * r
+    spec_ew, dq = _util.spec_for(5)
+    st = rbab.bab_step(xl, xh, gg, spec_ew, dq, branch_sb=True, split_depth=3)
+    xs, hs = st['xl_split'], st['xh_split']
+    assert xs.shape[0] > 0 and len(st['chunks']) == 1
+    A_s = st['A'][st['unclosed']][st['feasible']]
+    lb_s = st['lb'][st['unclosed']][st['feasible']]
+    dims = rbab.top_dims(rbab.sb_scores(xs, hs, A_s, lb_s), 3)
+    assert torch.equal(st['dims'], dims)
+    kl, kh = st['chunks'][0]
+    row = 0
+    for b in range(xs.shape[0]):
+        ku = sum(float(hs[b, d] - xs[b, d]) > 1e-12 for d in dims[b].tolist())
+        n = 1 << ku if ku else 0
+        assert bool((kl[row:row + n] >= xs[b]).all() and (kh[row:row + n] <= hs[b]).all())
+        row += n
+    assert row == kl.shape[0]

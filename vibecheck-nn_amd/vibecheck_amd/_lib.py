@@ -58,6 +58,9 @@ SIGNATURES = {
     'vc_best_update': [_P, _P, _L, _I, _P, _P],
     'vc_closure': [_P, _L, _I, _P, _P, _I, _P, _P],
     'vc_clip_box': [_P, _P, _P, _P, _L, _I, _I, _P, _P, _I, _P, _P, _P, _P],
+    'vc_branch_topk': [_P, _P, _P, _P, _L, _I, _I, _I, _F, _F, _I, _P, _P, _P],
+    'vc_split_multi_plan': [_P, _P, _P, _L, _I, _I, _P, _P, _P],
+    'vc_split_multi': [_P, _P, _P, _P, _L, _I, _I, _P, _P, _P],
     'vc_compact_workspace': [_L],
     'vc_compact': [_P, _L, _I, _P, _P, _P, _L, _P],
     'vc_scatter_max_rows': [_P, _P, _P, _L, _I, _P],

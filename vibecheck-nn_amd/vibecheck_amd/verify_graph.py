@@ -134,17 +134,46 @@ def _clip_box_by_halfspaces_batched(xl, xh, A, b):
     return _clip(xl, xh, A, b, table)
 
 
-def _split_feasible(xl, xh, feas):
-    """The feasible rows (feas) of clipped boxes, their widest axes and the
-    bisection of the usable ones, with one host read for both counts: the
-    widest axis is taken on every row, so the feasible and the split lists
-    are compacted together (verify_graph.py:13115-13121, 13291,
-    13366-13382).  Returns (xl_f, xh_f, n_degenerate, ax_f, low, high)."""
+def _split_feasible(xl, xh, feas, branch=None, K=1):
+    """The feasible rows (feas) of clipped boxes, their split dimensions and
+    children, with one host read for the counts: the split dimension is
+    taken on every row, so the feasible and the split lists are compacted
+    together (verify_graph.py:13115-13121, 13244-13423).
+
+    ``branch`` None: widest axis; else (A, lb, mode, thr, mw) for the SB
+    score (mode 1 sum, 2 margin) over the rows' A (B, Q, n) and lb (B, Q).
+    K > 1 (SB only): the 2^K-way split on each row's top K dimensions.
+    Returns (xl_f, xh_f, n_degenerate, ax_f, chunks), chunks being the
+    worklist pushes in order: [low, high] for a bisection, [children]."""
     B, n = xl.shape
     dev = xl.device
-    ax = torch.empty(B, dtype=torch.int64, device=dev)
+    K = max(1, min(int(K), n)) if branch is not None else 1
+    dims = torch.empty(B, K, dtype=torch.int64, device=dev)
     usable = torch.empty(B, dtype=torch.bool, device=dev)
-    call('vc_widest_axis', ptr(xl), ptr(xh), B, n, ptr(ax), ptr(usable), stream())
+    if branch is None:
+        call('vc_widest_axis', ptr(xl), ptr(xh), B, n, ptr(dims), ptr(usable), stream())
+    else:
+        A, lb, mode, thr, mw = branch
+        call('vc_branch_topk', ptr(xl), ptr(xh), ptr(A), ptr(lb), B, A.shape[1], n, mode,
+             float(thr), float(mw), K, ptr(dims), ptr(usable), stream())
+    if K > 1:
+        cnt = torch.empty(1, dtype=torch.int64, device=dev)
+        fidx, _ = _compact_device(feas, cnt=cnt)
+        nf = int(cnt.item())
+        fidx = fidx[:nf]
+        # the int64 dimensions travel as float pairs through the row gather
+        xl_f, xh_f, d2 = _gather_many([xl, xh, dims.view(torch.float32).view(B, 2 * K)], fidx)
+        dims_f = d2.contiguous().view(torch.int64).view(nf, K)
+        plan = torch.empty(nf + 2, dtype=torch.int64, device=dev)
+        call('vc_split_multi_plan', ptr(xl_f), ptr(xh_f), ptr(dims_f), nf, n, K, ptr(plan),
+             ptr(plan[nf + 1:]), stream())
+        total, n_deg = plan[nf:].tolist()
+        kl = torch.empty(total, n, device=dev)
+        kh = torch.empty(total, n, device=dev)
+        call('vc_split_multi', ptr(xl_f), ptr(xh_f), ptr(dims_f), ptr(plan), nf, n, K, ptr(kl),
+             ptr(kh), stream())
+        return xl_f, xh_f, n_deg, dims_f[:, 0], ([(kl, kh)] if total > 0 else [])
+    ax = dims.view(B)
     split = feas & usable
     cnts = torch.empty(2, dtype=torch.int64, device=dev)
     fidx, _ = _compact_device(feas, cnt=cnts[0:1])
@@ -161,7 +190,8 @@ def _split_feasible(xl, xh, feas):
     if nu > 0:
         call('vc_bisect', ptr(xl), ptr(xh), ptr(ax), ptr(uidx), nu, n,
              ptr(low_xl), ptr(low_xh), ptr(high_xl), ptr(high_xh), stream())
-    return xl_f, xh_f, nf - nu, ax_f, (low_xl, low_xh), (high_xl, high_xh)
+    chunks = [(low_xl, low_xh), (high_xl, high_xh)] if nu > 0 else []
+    return xl_f, xh_f, nf - nu, ax_f, chunks
 
 
 def _widest_and_bisect(xl, xh):
@@ -295,19 +325,25 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
            'xl_split': boxes[0, :nf], 'xh_split': boxes[1, :nf], 'ax': idx[1, :nf],
            'n_degenerate': n_deg, 'low': (boxes[2, :nu], boxes[3, :nu]),
            'high': (boxes[4, :nu], boxes[5, :nu])}
+    out['chunks'] = [out['low'], out['high']] if nu > 0 else []
     return out
 
 
 def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
              clip_enabled=True, alpha_iters=0, alpha_all=False, alpha_eps=0.0,
              alpha_max_leaves=200, alpha_lr=0.25, alpha_lr_decay=0.98,
-             timers=None):
-    """One BaB iteration on a popped batch (verify_graph.py:12855-13382):
+             timers=None, branch_sb=False, sb_margin=False, sb_thr=0.01, sb_mw=1.0,
+             split_depth=1):
+    """One BaB iteration on a popped batch (verify_graph.py:12855-13423):
     bound, closure, optional alpha-CROWN on unclosed leaves, one clip
-    iteration, widest-axis bisection.  Returns a dict of device tensors
-    (same keys as the oracle's bab_step)."""
+    iteration, split.  The split dimension is the widest, or with
+    ``branch_sb`` (and a clip, which gives the input linearization) the best
+    SB score (sum form, or ``sb_margin``); ``split_depth`` K > 1 (SB only)
+    splits each leaf on its top K dimensions into 2^K children.  Returns a
+    dict of device tensors (same keys as the oracle's bab_step; ``chunks``
+    are the worklist pushes in order)."""
     if (NATIVE_ROUND and timers is None and crown_intermediate and clip_enabled
-            and (alpha_iters == 0 or alpha_all)):
+            and (alpha_iters == 0 or alpha_all) and not branch_sb):
         out = _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr,
                                 alpha_lr_decay)
         if out is not None:
@@ -373,10 +409,13 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
            'unclosed': unclosed, 'n_alpha_leaves': n_al,
            'n_alpha_iters': n_ait}
     if clip_enabled and unclosed.numel() > 0 and A is not None:
-        xl_u, xh_u, A_u, acc_u = _gather_many([xl, xh, A, acc], unclosed)
+        xl_u, xh_u, A_u, acc_u, lb_u = _gather_many([xl, xh, A, acc, lb], unclosed)
         xl_c, xh_c, feas = _clip(xl_u, xh_u, A_u, acc_u, table)
         out['feasible'] = feas
-        xl_s, xh_s, n_deg, ax, low, high = _split_feasible(xl_c, xh_c, feas)
+        branch = ((A_u, lb_u, 2 if sb_margin else 1, sb_thr, sb_mw) if branch_sb
+                  else None)
+        xl_s, xh_s, n_deg, ax, chunks = _split_feasible(xl_c, xh_c, feas, branch,
+                                                        split_depth)
         if timers is not None:
             timers['clip'] = timers.get('clip', 0.0) + sync_t() - t0
             t0 = sync_t()
@@ -388,8 +427,15 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
             timers['clip'] = timers.get('clip', 0.0) + t1 - t0
             t0 = t1
         n_deg, ax, low, high = _widest_and_bisect(xl_s, xh_s)
+        chunks = [low, high] if low[0].shape[0] > 0 else []
     out['xl_split'], out['xh_split'] = xl_s, xh_s
-    out.update(ax=ax, n_degenerate=n_deg, low=low, high=high)
+    if len(chunks) == 2:
+        low, high = chunks
+    elif chunks:             # the 2^K-way split: one chunk, no low/high halves
+        low = high = None
+    else:
+        low = high = (xl_s[:0], xh_s[:0])
+    out.update(ax=ax, n_degenerate=n_deg, chunks=chunks, low=low, high=high)
     if timers is not None:
         timers['split'] = timers.get('split', 0.0) + sync_t() - t0
     return out
@@ -413,7 +459,9 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
     input_split_crown_intermediate, input_split_batched_alpha_iters,
     input_split_batched_alpha_all_leaves, input_split_batched_alpha_lr
     (extension; reference hard-codes 0.25), input_split_batched_max_iters
-    (extension: stop after that many iterations).
+    (extension: stop after that many iterations), input_split_batched_branch_sb,
+    input_split_sb_margin_score, input_split_sb_coeff_thresh,
+    input_split_sb_margin_weight, bab_split_depth.
     """
     if dtype != torch.float32:
         raise NotImplementedError('vibecheck_amd computes in fp32 only')
@@ -433,6 +481,11 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
                                'input_split_batched_alpha_boundary_eps', 0.0))
     alpha_lr = float(_setting(settings, 'input_split_batched_alpha_lr', 0.25))
     max_iters = _setting(settings, 'input_split_batched_max_iters', None)
+    branch_sb = bool(_setting(settings, 'input_split_batched_branch_sb', False))
+    sb_margin = bool(_setting(settings, 'input_split_sb_margin_score', False))
+    sb_thr = float(_setting(settings, 'input_split_sb_coeff_thresh', 0.01))
+    sb_mw = float(_setting(settings, 'input_split_sb_margin_weight', 1.0))
+    split_depth = int(_setting(settings, 'bab_split_depth', 1))
     dev = torch.device(device)
 
     xc = ((torch.as_tensor(spec.x_lo, dtype=dtype, device=dev)
@@ -462,9 +515,13 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
         B = min(batch_size, wl_n)
         xl_b, xh_b = wl.pop(B)
         try:
+            # K > 1 only grows a queue that does not fill the batch
+            # (verify_graph.py:13343-13344)
             st = bab_step(xl_b, xh_b, gg, spec_ew, table, crown_int,
                           clip_enabled, alpha_iters, alpha_all, alpha_eps,
-                          alpha_lr=alpha_lr)
+                          alpha_lr=alpha_lr, branch_sb=branch_sb, sb_margin=sb_margin,
+                          sb_thr=sb_thr, sb_mw=sb_mw,
+                          split_depth=split_depth if B < batch_size else 1)
         except torch.cuda.OutOfMemoryError:
             new_bs = max(1, batch_size // 2)
             if new_bs == batch_size:
@@ -477,10 +534,8 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
             continue
         n_leaves += B
         n_open += st['n_degenerate']
-        low, high = st['low'], st['high']
-        if low[0].shape[0] > 0:
-            wl.push(*low)
-            wl.push(*high)
+        for c in st['chunks']:
+            wl.push(*c)
         n_iters += 1
         if wl.size() > max_worklist:
             return 'unknown', {'phase': 'batched_worklist_overflow',
