@@ -632,6 +632,22 @@ int vc_split_multi(const float *xl, const float *xh, const int64_t *dims,
                    const int64_t *offsets, int64_t B, int n, int K,
                    float *out_xl, float *out_xh, vc_stream_t stream);
 
+/* Boundary band of the alpha-CROWN leaves (verify_graph.py:12938-12946):
+ * keys (B) = min over disjuncts of the max over the disjunct's queries of
+ * lb (B, Q) (disjunct table as vc_closure); cand (B) = not closed and key >
+ * neg_eps (the reference's -alpha_eps, as fp32). */
+int vc_alpha_band_keys(const float *lb, int64_t B, int Q, const int32_t *d_ptr,
+                       const int32_t *q_idx, int n_disj, const uint8_t *closed,
+                       float neg_eps, float *keys, uint8_t *cand,
+                       vc_stream_t stream);
+
+/* The k_max best of C candidates (leaves idx, ascending) by key,
+ * descending, ties in leaf order (a stable sort; the reference's argsort
+ * leaves their order open): out[0 .. min(C, k_max) - 1].  Replaces the
+ * argsort and truncation of verify_graph.py:12947-12950. */
+int vc_rank_select_desc(const float *keys, const int64_t *idx, int64_t C,
+                        int64_t k_max, int64_t *out, vc_stream_t stream);
+
 /* One input-split BaB round on the narrow-MLP kernels (the bound,
  * alpha, clip and split phases of verify_graph.py:12855-13382, with
  * crown intermediate bounds, the clip on and alpha-CROWN on every open leaf),

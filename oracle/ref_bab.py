@@ -213,6 +213,18 @@ def bound_batch(xl, xh, gg, spec_ew, crown_intermediate=True,
     return spec_backward_batched(sb, xl, xh, gg, spec_ew), None, None
 
 
+def band_select(lb, closed, disj_q_idx, eps, max_leaves):
+    """Leaves of the alpha boundary band (verify_graph.py:12938-12950):
+    unclosed with worst disjunct's best bound > -eps, in descending order of
+    that bound, at most max_leaves.  Equal bounds keep their ascending leaf
+    order (a stable sort: the reference's argsort leaves ties open)."""
+    per_disj = [lb[:, q].max(dim=1).values for q in disj_q_idx.values()]
+    worst = torch.stack(per_disj, dim=1).min(dim=1).values
+    idx = ((~closed) & (worst > -eps)).nonzero(as_tuple=True)[0]
+    order = worst[idx].argsort(descending=True, stable=True)
+    return idx[order[:max_leaves]]
+
+
 def alpha_on_leaves(lb, xl, xh, gg, spec_ew, disj_q_idx, closed,
                     alpha_iters, alpha_all, alpha_eps, alpha_max_leaves,
                     lr=0.25, lr_decay=0.98):
@@ -222,18 +234,10 @@ def alpha_on_leaves(lb, xl, xh, gg, spec_ew, disj_q_idx, closed,
     if not (alpha_iters > 0 and (alpha_all or alpha_eps > 0)
             and not bool(closed.all())):
         return lb, closed, 0, 0
-    per_disj = [lb[:, q].max(dim=1).values for q in disj_q_idx.values()]
-    worst = torch.stack(per_disj, dim=1).min(dim=1).values
-    if alpha_all:
-        sel = ~closed
-    else:
-        sel = (~closed) & (worst > -alpha_eps)
-    idx = sel.nonzero(as_tuple=True)[0]
+    idx = (~closed).nonzero(as_tuple=True)[0] if alpha_all else \
+        band_select(lb, closed, disj_q_idx, alpha_eps, alpha_max_leaves)
     if idx.numel() == 0:
         return lb, closed, 0, 0
-    if not alpha_all:
-        order = worst[idx].argsort(descending=True)
-        idx = idx[order[:alpha_max_leaves]]
     new, n_it = alpha_crown_batched(xl[idx], xh[idx], gg, spec_ew,
                                     n_iters=alpha_iters, lr=lr,
                                     lr_decay=lr_decay, return_trace=True)

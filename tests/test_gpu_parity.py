@@ -990,3 +990,43 @@ def test_bab_step_sb_branching(gpu, margin, depth):
     assert st['n_degenerate'] == n_deg and len(st['chunks']) == len(ref_chunks)
     for (a, b), (c, d) in zip(st['chunks'], ref_chunks):
         assert torch.equal(cpu(a), c) and torch.equal(cpu(b), d)
+
+
+# ------------------------------------------------- alpha boundary band
+@pytest.mark.parametrize('one_disjunct', [True, False])
+def test_alpha_band_selection_bit_exact(gpu, one_disjunct):
+    """The band's leaves (worst disjunct's best lb > -eps, unclosed, best
+    first, truncated) against the oracle on identical bounds, with ties
+    (duplicated rows) and truncation above and below the candidate count."""
+    g = torch.Generator().manual_seed(21)
+    B, Q = 3000, 4
+    lb = torch.randn(B, Q, generator=g) * 2
+    lb[100:140] = lb[0]                      # tied keys
+    lb[200:260] = torch.rand(60, Q, generator=g) + 0.1   # closed leaves
+    dq = {0: [0, 1, 2, 3]} if one_disjunct else {0: [0, 1], 1: [2], 2: [3]}
+    table = vg.DisjunctTable(dq, gpu)
+    closed_ref = rbab.closure(lb, dq)
+    lbg = lb.to(gpu)
+    closed = vg._closure(lbg, table)
+    assert torch.equal(cpu(closed), closed_ref)
+    for eps in (0.3, 3.0):
+        for k in (10, 200, 5000):
+            ref = rbab.band_select(lb, closed_ref, dq, eps, k)
+            got = vg._alpha_band(lbg, closed, table, eps, k)
+            assert torch.equal(cpu(got), ref), (eps, k)
+
+
+def test_bab_step_alpha_band_parity(gpu):
+    """A step with boundary-band alpha (eps 4, at most 40 leaves): the same
+    leaves get alpha, the same evaluation count, the best bounds within the
+    alpha tolerance and the same verdicts."""
+    gg_c, gg_g, xl, xh = acas(gpu, 512, seed=4, scale=6.0)
+    se_c, se_g, dq = spec_pair(5, gpu)
+    kw = dict(alpha_iters=6, alpha_all=False, alpha_eps=4.0, alpha_max_leaves=40,
+              alpha_lr=0.1)
+    ref = rbab.bab_step(xl, xh, gg_c, se_c, dq, **kw)
+    got = vg.bab_step(xl.to(gpu), xh.to(gpu), gg_g, se_g, vg.DisjunctTable(dq, gpu), **kw)
+    assert got['n_alpha_leaves'] == ref['n_alpha_leaves'] > 0
+    assert got['n_alpha_iters'] == ref['n_alpha_iters']
+    assert_adam_drift(got['lb'], ref['lb'], 'band alpha lb')
+    assert torch.equal(cpu(got['closed']), ref['closed'])

@@ -1,6 +1,9 @@
-// Branching of the input-split BaB beyond the widest-axis bisection
-// (verify_graph.py:13236-13423): the split-dimension scores and their top K
-// per leaf, and the 2^K-way split of a leaf on its top K dimensions.
+// Selections of the input-split BaB beyond the widest-axis bisection:
+//   - the split-dimension scores and their top K per leaf, and the 2^K-way
+//     split of a leaf on its top K dimensions (verify_graph.py:13236-13423);
+//   - the boundary band of leaves that get alpha-CROWN: unclosed leaves
+//     whose worst disjunct's best bound is above -eps, the best
+//     alpha_max_leaves of them first (verify_graph.py:12938-12950).
 #include "vc_common.h"
 
 namespace {
@@ -169,6 +172,51 @@ __global__ __launch_bounds__(NT) void k_split_multi(const float* xl, const float
   }
 }
 
+// Band keys: key[b] = min over disjuncts of (max over the disjunct's
+// queries of lb[b, q]) (the worst disjunct's best bound); cand[b] = the
+// leaf is not closed and key > neg_eps (the reference compares with
+// -alpha_eps in the tensor's fp32).
+__global__ void k_band_keys(const float* lb, int64_t B, int Q, const int32_t* dptr,
+                            const int32_t* qidx, int nd, const uint8_t* closed, float neg_eps,
+                            float* keys, uint8_t* cand) {
+  for (int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; b < B;
+       b += (int64_t)gridDim.x * blockDim.x) {
+    float worst = INFINITY;
+    for (int d = 0; d < nd; ++d) {
+      float best = -INFINITY;
+      for (int t = dptr[d]; t < dptr[d + 1]; ++t) best = fmaxf(best, lb[b * Q + qidx[t]]);
+      worst = fminf(worst, best);
+    }
+    keys[b] = worst;
+    cand[b] = !closed[b] && worst > neg_eps;
+  }
+}
+
+// Rank selection: candidate i (leaf idx[i], idx ascending) has rank =
+// #{j : key_j > key_i, or key_j == key_i and j < i}; the first k_max ranks
+// go to out[rank], so out holds the best k_max leaves in descending key
+// order, ties in leaf order.  The keys are compared through LDS tiles.
+__global__ __launch_bounds__(NT) void k_rank_select(const float* keys, const int64_t* idx,
+                                                    int64_t C, int64_t k_max, int64_t* out) {
+  __shared__ float tile[NT];
+  for (int64_t i0 = (int64_t)blockIdx.x * NT; i0 < C; i0 += (int64_t)gridDim.x * NT) {
+    const int64_t i = i0 + threadIdx.x;
+    const float ki = i < C ? keys[idx[i]] : 0.f;
+    int64_t rank = 0;
+    for (int64_t j0 = 0; j0 < C; j0 += NT) {
+      __syncthreads();
+      if (j0 + threadIdx.x < C) tile[threadIdx.x] = keys[idx[j0 + threadIdx.x]];
+      __syncthreads();
+      const int m = C - j0 < NT ? (int)(C - j0) : NT;
+      for (int t = 0; t < m; ++t) {
+        const float kj = tile[t];
+        rank += (kj > ki || (kj == ki && j0 + t < i)) ? 1 : 0;
+      }
+    }
+    if (i < C && rank < k_max) out[rank] = idx[i];
+  }
+}
+
 }  // namespace
 
 extern "C" int vc_branch_topk(const float* xl, const float* xh, const float* A, const float* lb,
@@ -204,6 +252,29 @@ extern "C" int vc_split_multi(const float* xl, const float* xh, const int64_t* d
   if (!xl || !xh || !dims || !offsets || !out_xl || !out_xh) return VC_ERR_ARG;
   hipLaunchKernelGGL(k_split_multi, dim3(vc_blocks(B, NT)), dim3(NT), 0, (hipStream_t)stream, xl,
                      xh, dims, offsets, B, n, K, out_xl, out_xh);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_alpha_band_keys(const float* lb, int64_t B, int Q, const int32_t* d_ptr,
+                                  const int32_t* q_idx, int n_disj, const uint8_t* closed,
+                                  float neg_eps, float* keys, uint8_t* cand, vc_stream_t stream) {
+  if (B < 0 || Q <= 0 || n_disj <= 0) return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  if (!lb || !d_ptr || !q_idx || !closed || !keys || !cand) return VC_ERR_ARG;
+  hipLaunchKernelGGL(k_band_keys, dim3(vc_blocks(B, NT)), dim3(NT), 0, (hipStream_t)stream, lb, B,
+                     Q, d_ptr, q_idx, n_disj, closed, neg_eps, keys, cand);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_rank_select_desc(const float* keys, const int64_t* idx, int64_t C,
+                                   int64_t k_max, int64_t* out, vc_stream_t stream) {
+  if (C < 0 || k_max < 0) return VC_ERR_ARG;
+  if (C == 0 || k_max == 0) return VC_OK;
+  if (!keys || !idx || !out) return VC_ERR_ARG;
+  hipLaunchKernelGGL(k_rank_select, dim3(vc_blocks(C, NT)), dim3(NT), 0, (hipStream_t)stream,
+                     keys, idx, C, k_max, out);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }

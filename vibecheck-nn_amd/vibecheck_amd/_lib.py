@@ -61,6 +61,8 @@ SIGNATURES = {
     'vc_branch_topk': [_P, _P, _P, _P, _L, _I, _I, _I, _F, _F, _I, _P, _P, _P],
     'vc_split_multi_plan': [_P, _P, _P, _L, _I, _I, _P, _P, _P],
     'vc_split_multi': [_P, _P, _P, _P, _L, _I, _I, _P, _P, _P],
+    'vc_alpha_band_keys': [_P, _L, _I, _P, _P, _I, _P, _F, _P, _P, _P],
+    'vc_rank_select_desc': [_P, _P, _L, _L, _P, _P],
     'vc_compact_workspace': [_L],
     'vc_compact': [_P, _L, _I, _P, _P, _P, _L, _P],
     'vc_scatter_max_rows': [_P, _P, _P, _L, _I, _P],

@@ -329,6 +329,25 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
     return out
 
 
+def _alpha_band(lb, closed, table, eps, max_leaves):
+    """The alpha-CROWN leaves of the boundary band (verify_graph.py:
+    12938-12950): unclosed leaves whose worst disjunct's best bound is above
+    -eps, best first, at most max_leaves; ties in leaf order."""
+    B, Q = lb.shape
+    dev = lb.device
+    keys = torch.empty(B, device=dev)
+    cand = torch.empty(B, dtype=torch.bool, device=dev)
+    call('vc_alpha_band_keys', ptr(lb), B, Q, ptr(table.d_ptr), ptr(table.q_idx), table.n,
+         ptr(closed), float(-eps), ptr(keys), ptr(cand), stream())
+    cidx = _compact(cand)
+    C = int(cidx.numel())
+    k = min(C, int(max_leaves))
+    sel = torch.empty(k, dtype=torch.int64, device=dev)
+    if k > 0:
+        call('vc_rank_select_desc', ptr(keys), ptr(cidx), C, k, ptr(sel), stream())
+    return sel
+
+
 def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
              clip_enabled=True, alpha_iters=0, alpha_all=False, alpha_eps=0.0,
              alpha_max_leaves=200, alpha_lr=0.25, alpha_lr_decay=0.98,
@@ -378,12 +397,11 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
         timers['bound'] = timers.get('bound', 0.0) + t1 - t0
         t0 = t1
     if alpha_iters > 0 and (alpha_all or alpha_eps > 0):
-        open_idx = _compact(closed, select_zero=True)
+        if alpha_all:
+            open_idx = _compact(closed, select_zero=True)
+        else:
+            open_idx = _alpha_band(lb, closed, table, alpha_eps, alpha_max_leaves)
         if open_idx.numel() > 0:
-            if not alpha_all:
-                raise NotImplementedError(
-                    'vibecheck_amd: boundary-band alpha selection '
-                    '(alpha_all=False) is not supported')
             # alpha starts from the zonotope bounds of the same boxes, which
             # the bound phase has already computed: gather their rows
             sb_open = None if sb is None else _gather_layers(sb, open_idx)
@@ -457,7 +475,8 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
     ``settings`` (attribute or dict): total_timeout, input_split_batch_size,
     input_split_batched_max_worklist, input_split_batched_clip_enabled,
     input_split_crown_intermediate, input_split_batched_alpha_iters,
-    input_split_batched_alpha_all_leaves, input_split_batched_alpha_lr
+    input_split_batched_alpha_all_leaves, input_split_batched_alpha_boundary_eps,
+    input_split_batched_alpha_max_leaves, input_split_batched_alpha_lr
     (extension; reference hard-codes 0.25), input_split_batched_max_iters
     (extension: stop after that many iterations), input_split_batched_branch_sb,
     input_split_sb_margin_score, input_split_sb_coeff_thresh,
@@ -479,6 +498,7 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
                               'input_split_batched_alpha_all_leaves', False))
     alpha_eps = float(_setting(settings,
                                'input_split_batched_alpha_boundary_eps', 0.0))
+    alpha_max_leaves = int(_setting(settings, 'input_split_batched_alpha_max_leaves', 200))
     alpha_lr = float(_setting(settings, 'input_split_batched_alpha_lr', 0.25))
     max_iters = _setting(settings, 'input_split_batched_max_iters', None)
     branch_sb = bool(_setting(settings, 'input_split_batched_branch_sb', False))
@@ -519,7 +539,8 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
             # (verify_graph.py:13343-13344)
             st = bab_step(xl_b, xh_b, gg, spec_ew, table, crown_int,
                           clip_enabled, alpha_iters, alpha_all, alpha_eps,
-                          alpha_lr=alpha_lr, branch_sb=branch_sb, sb_margin=sb_margin,
+                          alpha_max_leaves=alpha_max_leaves, alpha_lr=alpha_lr,
+                          branch_sb=branch_sb, sb_margin=sb_margin,
                           sb_thr=sb_thr, sb_mw=sb_mw,
                           split_depth=split_depth if B < batch_size else 1)
         except torch.cuda.OutOfMemoryError:
