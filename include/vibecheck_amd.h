@@ -230,6 +230,23 @@ int vc_alpha_grad_step_slopes(const float *gE, const float *P, int64_t M,
                               const float *bias_next, int n_next,
                               float *g_out, vc_stream_t stream);
 
+/* vc_alpha_grad_step with one alpha per backward row (the per-query alpha
+ * of the hybrid freeze / replay verifier, verify_hybrid_acasxu.py:164-318):
+ * alpha_rows (M, n), row m's lower slope active + unstable * alpha_rows[m]. */
+int vc_alpha_grad_step_rows(const float *gE, const float *P, int64_t M, int R,
+                            int n, const float *relu_lo, const float *relu_hi,
+                            const float *alpha_rows, int p_bcast,
+                            const float *W_next, const float *bias_next,
+                            int n_next, float *g_out, vc_stream_t stream);
+
+/* d lb / d alpha with one alpha per row: galpha (M, n)[m, j] = gE[m, j] *
+ * pos(P[m, j]) where neuron j of row m's domain (m / R) is unstable, else 0
+ * (P (M, n), or (R, n) shared when p_bcast).  The per-row form of
+ * vc_alpha_grad_reduce (the autograd of the per-query alpha backward). */
+int vc_alpha_grad_rows(const float *gE, const float *P, int p_bcast, int64_t M,
+                       int R, int n, const float *relu_lo, const float *relu_hi,
+                       float *galpha, vc_stream_t stream);
+
 /* d lb / d alpha for one layer: galpha[b, j] = sum over the R rows of b of
  * gE[m, j] * pos(P[m, j]), zero where the neuron is not unstable;
  * gbeta[b, j] (nullable) = sum over rows of gE[m, j] (d lb / d beta).
@@ -647,6 +664,26 @@ int vc_alpha_band_keys(const float *lb, int64_t B, int Q, const int32_t *d_ptr,
  * argsort and truncation of verify_graph.py:12947-12950. */
 int vc_rank_select_desc(const float *keys, const int64_t *idx, int64_t C,
                         int64_t k_max, int64_t *out, vc_stream_t stream);
+
+/* Layer tightening of the hybrid freeze / replay (verify_hybrid_acasxu.py:
+ * 231-235, 279-283): with sl (B, 2n) the lower bounds of the seeded rows
+ * [+I; -I], lo = max(lo, sl[:, :n]), hi = min(hi, -sl[:, n:]),
+ * lo = min(lo, hi), in place on lo, hi (B, n). */
+int vc_bound_tighten(float *lo, float *hi, const float *sl, int64_t B, int n,
+                     vc_stream_t stream);
+
+/* best = max(best, lb) over n values (a copy when init != 0), and
+ * out[0] = the sum of best in fp64 (the early-stop quantity of the freeze's
+ * Adam loops, verify_hybrid_acasxu.py:212-225, 262-272).  One workgroup. */
+int vc_best_sum(float *best, const float *lb, int64_t n, int init, double *out,
+                vc_stream_t stream);
+
+/* Replay's running best (verify_hybrid_acasxu.py:302-311): per leaf b,
+ * imp = lb[b] > best[b] (every entry when init != 0), best[b] = where(imp,
+ * lb[b], best[b]); when any entry improved, best_A[b] = A[b] (Q x n_in). */
+int vc_best_rows_with_A(float *best, const float *lb, float *best_A,
+                        const float *A, int64_t B, int Q, int n_in, int init,
+                        vc_stream_t stream);
 
 /* One input-split BaB round on the narrow-MLP kernels (the bound,
  * alpha, clip and split phases of verify_graph.py:12855-13382, with

@@ -1,0 +1,150 @@
+"""Oracle: the hybrid per-query alpha-CROWN freeze / replay restated in
+PyTorch (CPU, autograd for the alpha gradients).
+
+Test infrastructure: see the package docstring.  Follows ``_full_freeze``
+and ``_replay_batched`` of the reference (verify_hybrid_acasxu.py:164-257,
+260-318) over the oracle's own zonotope forward and batched backward.
+``early_stop_eps`` / ``lr_decay`` are the reference's fixed 1e-6 / 0.98
+made settable so that tests can run a fixed number of iterations.
+"""
+import torch
+
+from .ref_bound import make_slopes, spec_backward_batched, zono_forward_batched
+
+
+def relu_feeds(gg):
+    """{L: name of the op feeding ReLU L} (verify_hybrid_acasxu.py:175-176)."""
+    return {op['layer_idx']: op['inputs'][0] for op in gg['ops']
+            if op['type'] == 'relu' and 'layer_idx' in op}
+
+
+def tighten(lo, hi, sl):
+    """Intersection of (lo, hi) (B, n) with the seeded bounds sl (B, 2n) of
+    the rows [+I; -I] (verify_hybrid_acasxu.py:224-228)."""
+    n = lo.shape[1]
+    lo_t = torch.maximum(lo, sl[:, :n])
+    hi_t = torch.minimum(hi, -sl[:, n:])
+    return torch.minimum(lo_t, hi_t), hi_t
+
+
+def best_update_with_A(best, best_A, lb, A):
+    """The replay's per-leaf record (verify_hybrid_acasxu.py:302-312): best
+    = where(lb > best, lb, best); a leaf with any improved query takes A."""
+    if best is None:
+        return lb.clone(), A.clone()
+    imp = lb > best
+    best = torch.where(imp, lb, best)
+    best_A = best_A.clone()
+    leaf = imp.any(dim=1)
+    best_A[leaf] = A[leaf]
+    return best, best_A
+
+
+def _init_alpha(lo, hi, Q):
+    _, up_s, _, _, _, unstable = make_slopes(lo, hi)
+    a = (up_s > 0.5).to(lo.dtype) * unstable.to(lo.dtype)
+    return a.unsqueeze(1).expand(-1, Q, -1).contiguous()
+
+
+def _adam_loop(params, evaluate, n_iters, lr, lr_decay, early_stop_eps, trace=None):
+    opt = torch.optim.Adam(list(params.values()), lr=lr)
+    best = None
+    prev = -float('inf')
+    for it in range(n_iters):
+        opt.zero_grad()
+        sl = evaluate()
+        with torch.no_grad():
+            best = sl.detach().clone() if best is None else torch.maximum(best, sl.detach())
+            cur = float(best.double().sum().item())
+        (-sl.sum()).backward()
+        opt.step()
+        with torch.no_grad():
+            for a in params.values():
+                a.clamp_(0.0, 1.0)
+        if trace is not None:
+            trace.append(it)
+        if it > 0 and cur - prev < early_stop_eps:
+            break
+        prev = cur
+        for g in opt.param_groups:
+            g['lr'] *= lr_decay
+    return best
+
+
+def full_freeze(xl, xh, gg, spec_ew, n_iters_per_layer=100, n_iters_spec=100, lr=0.25,
+                lr_decay=0.98, early_stop_eps=1e-6):
+    """verify_hybrid_acasxu.py:164-257 (without the deadline): per ReLU
+    layer L, the rows [+I; -I] seeded at L's input with per-(leaf, row)
+    alphas on the layers below, initialised to CROWN's lower slopes, Adam on
+    -sum(lb) with clamp, early stop on the sum of the best, then the layer's
+    bounds intersected with the best; then the same loop on the spec rows.
+    The early stop reads the best's sum in fp64.  Returns (tight,
+    alpha_per_layer, alpha_spec, best_spec)."""
+    B = xl.shape[0]
+    dt = xl.dtype
+    with torch.no_grad():
+        sb, _ = zono_forward_batched(xl, xh, gg)
+    tight = {L: (lo.clone(), hi.clone()) for L, (lo, hi) in sb.items()}
+    order = sorted(tight)
+    feeds = relu_feeds(gg)
+    alpha_per_layer = {}
+    for L in order:
+        n = tight[L][0].shape[1]
+        Q = 2 * n
+        eye = torch.eye(n, dtype=dt)
+        seed = {feeds[L]: torch.cat([eye, -eye]).unsqueeze(0).expand(B, -1, -1)}
+        acc0 = torch.zeros(B, Q, dtype=dt)
+        alpha = {k: _init_alpha(*tight[k], Q).requires_grad_(True) for k in order if k < L}
+        if alpha:
+            best = _adam_loop(alpha, lambda: spec_backward_batched(
+                tight, xl, xh, gg, None, alpha_at_layer=alpha, seed_ew_at=seed,
+                seed_acc=acc0), n_iters_per_layer, lr, lr_decay, early_stop_eps)
+            tight[L] = tighten(tight[L][0], tight[L][1], best)
+        alpha_per_layer[L] = {k: a.detach().clone() for k, a in alpha.items()}
+    Q = len(spec_ew)
+    alpha = {L: _init_alpha(*tight[L], Q).requires_grad_(True) for L in order}
+    best = _adam_loop(alpha, lambda: spec_backward_batched(
+        tight, xl, xh, gg, spec_ew, alpha_at_layer=alpha),
+        n_iters_spec, lr, lr_decay, early_stop_eps)
+    return tight, alpha_per_layer, {k: a.detach().clone() for k, a in alpha.items()}, best
+
+
+def replay_batched(xl, xh, gg, spec_ew, alpha_layer_b, alpha_spec_b, spec_iters=10,
+                   spec_lr=0.1):
+    """verify_hybrid_acasxu.py:260-318: zonotope bounds, every layer
+    re-tightened with its frozen alphas (leading dim 1 expanded over the
+    batch, or one per leaf), then ``spec_iters`` evaluations of the spec
+    bound with Adam (no decay) on the spec alphas, warm-started from the
+    frozen ones.  Returns (best (B, Q), best_A (B, Q, n_in), tight)."""
+    B = xl.shape[0]
+    dt = xl.dtype
+    feeds = relu_feeds(gg)
+    with torch.no_grad():
+        sb, _ = zono_forward_batched(xl, xh, gg)
+        tight = {L: (lo.clone(), hi.clone()) for L, (lo, hi) in sb.items()}
+        for L in sorted(tight):
+            if not alpha_layer_b.get(L):
+                continue
+            n = tight[L][0].shape[1]
+            eye = torch.eye(n, dtype=dt)
+            seed = {feeds[L]: torch.cat([eye, -eye]).unsqueeze(0).expand(B, -1, -1)}
+            alpha = {k: a.expand(B, -1, -1).contiguous() for k, a in alpha_layer_b[L].items()}
+            sl = spec_backward_batched(tight, xl, xh, gg, None, alpha_at_layer=alpha,
+                                       seed_ew_at=seed, seed_acc=torch.zeros(B, 2 * n, dtype=dt))
+            tight[L] = tighten(tight[L][0], tight[L][1], sl)
+    alpha = {k: a.expand(B, -1, -1).contiguous().clone().requires_grad_(True)
+             for k, a in alpha_spec_b.items()}
+    opt = torch.optim.Adam(list(alpha.values()), lr=spec_lr)
+    best = best_A = None
+    for _ in range(max(1, spec_iters)):
+        opt.zero_grad()
+        sl, A, _ = spec_backward_batched(tight, xl, xh, gg, spec_ew, return_input_linear=True,
+                                         alpha_at_layer=alpha)
+        with torch.no_grad():
+            best, best_A = best_update_with_A(best, best_A, sl.detach(), A.detach())
+        (-sl.sum()).backward()
+        opt.step()
+        with torch.no_grad():
+            for a in alpha.values():
+                a.clamp_(0.0, 1.0)
+    return best, best_A, tight

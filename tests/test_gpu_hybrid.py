@@ -1,0 +1,215 @@
+"""GPU parity of the hybrid per-query alpha-CROWN freeze / replay
+(vibecheck_amd.verify_hybrid_acasxu) against the oracle
+(oracle/ref_hybrid.py), through the C-ABI library.
+
+  - the per-row alpha backward and its gradient (seeded at a ReLU's input,
+    one alpha per leaf, row and neuron) against autograd in fp64;
+  - the bookkeeping kernels bit-exact (bound intersection, running best
+    with the improving leaves' A, running best with its fp64 sum);
+  - the freeze and the replay against the oracle run on the same inputs:
+    after 1 and 2 iterations within the bound tolerance, after 10 within
+    the Adam drift criterion of free-running Adam loops;
+  - one replay over leaves of several groups (per-leaf alphas) equal to one
+    replay per group;
+  - the driver's known answers on the reference's bundled ACAS-Xu network
+    (prop_1 is unsat; prop_2 is violated, so never 'unsat').
+"""
+import os
+
+import pytest
+import torch
+
+from oracle import ref_bound as rb
+from oracle import ref_hybrid as rh
+from vibecheck_amd import onnx_net, vnnlib
+from vibecheck_amd import verify_hybrid_acasxu as vh
+from vibecheck_amd import verify_zono_bnb as vz
+from vibecheck_amd._lib import call, ptr
+
+import _util
+from test_formats import GOLD, NET
+from test_gpu_parity import acas, assert_adam_drift, assert_bounds, cpu, spec_pair
+
+pytestmark = pytest.mark.gpu
+F32 = torch.float32
+
+
+def _st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def test_per_row_alpha_gradient_matches_autograd(gpu):
+    gg_c, gg_g, xl, xh = acas(gpu, 24, seed=3, scale=4.0)
+    sb, _ = rb.zono_forward_batched(xl, xh, gg_c)
+    L = 3
+    feed = rh.relu_feeds(gg_c)[L]
+    n = sb[L][0].shape[1]
+    B, Q = xl.shape[0], 2 * n
+    g = torch.Generator().manual_seed(5)
+    alpha = {k: torch.rand(B, Q, sb[k][0].shape[1], generator=g, dtype=torch.float64)
+             for k in range(L)}
+    a_ref = {k: a.clone().requires_grad_(True) for k, a in alpha.items()}
+    sb64 = {k: (lo.double(), hi.double()) for k, (lo, hi) in sb.items()}
+    gg64 = _util.to_dev(gg_c, 'cpu', torch.float64)
+    eye = torch.eye(n, dtype=torch.float64)
+    seed = {feed: torch.cat([eye, -eye]).unsqueeze(0).expand(B, -1, -1)}
+    lb = rb.spec_backward_batched(sb64, xl.double(), xh.double(), gg64, None,
+                                  alpha_at_layer=a_ref, seed_ew_at=seed,
+                                  seed_acc=torch.zeros(B, Q, dtype=torch.float64))
+    lb.sum().backward()
+    sbg = {k: (a.to(gpu), b.to(gpu)) for k, (a, b) in sb.items()}
+    Wq, bq = vh._bound_rows(n, gpu)
+    a_g = {k: a.float().to(gpu) for k, a in alpha.items()}
+    ga = {k: torch.zeros_like(a) for k, a in a_g.items()}
+    glb = vz._alpha_backward_and_grad(sbg, xl.to(gpu), xh.to(gpu), gg_g, Wq, bq, a_g, True, ga,
+                                      seed_name=feed)
+    assert_bounds(glb, lb.detach().float(), 'per-row alpha lb', rtol=1e-4, atol=1e-5)
+    for k in alpha:
+        ref_g = a_ref[k].grad.float()
+        scale = ref_g.abs().max().clamp(min=1.0)
+        err = (cpu(ga[k]) - ref_g).abs().max() / scale
+        print(f'layer {k}: grad max err {float(err):.2e} (scale {float(scale):.2f})')
+        assert float(err) < 1e-4, (k, float(err))
+        assert float(ref_g.abs().max()) > 0
+
+
+def test_bookkeeping_kernels_bit_exact(gpu):
+    g = torch.Generator().manual_seed(2)
+    B, n, Q, n_in = 300, 37, 6, 5
+    lo = torch.randn(B, n, generator=g)
+    hi = lo + torch.rand(B, n, generator=g) * 2
+    sl = torch.randn(B, 2 * n, generator=g) * 2
+    lo_g, hi_g = lo.to(gpu), hi.to(gpu)
+    call('vc_bound_tighten', ptr(lo_g), ptr(hi_g), ptr(sl.to(gpu)), B, n, _st())
+    lo_r, hi_r = rh.tighten(lo, hi, sl)
+    assert torch.equal(cpu(lo_g), lo_r) and torch.equal(cpu(hi_g), hi_r)
+    assert bool((lo_r == hi_r).any())           # crossings occurred and were closed
+
+    best_r = best_A_r = None
+    best = torch.empty(B, Q, device=gpu)
+    best_A = torch.empty(B, Q, n_in, device=gpu)
+    for it in range(4):
+        lb = torch.randn(B, Q, generator=g)
+        lb[: B // 3] = -10.0                    # leaves that never improve
+        A = torch.randn(B, Q, n_in, generator=g)
+        lb_g, A_g = lb.to(gpu), A.to(gpu)
+        call('vc_best_rows_with_A', ptr(best), ptr(lb_g), ptr(best_A), ptr(A_g), B, Q, n_in,
+             1 if it == 0 else 0, _st())
+        best_r, best_A_r = rh.best_update_with_A(best_r, best_A_r, lb, A)
+        assert torch.equal(cpu(best), best_r) and torch.equal(cpu(best_A), best_A_r), it
+
+    bs = torch.empty(B * Q, device=gpu)
+    out = torch.empty(1, dtype=torch.float64, device=gpu)
+    ref = None
+    for it in range(3):
+        lb = torch.randn(B * Q, generator=g)
+        call('vc_best_sum', ptr(bs), ptr(lb.to(gpu)), B * Q, 1 if it == 0 else 0, ptr(out), _st())
+        ref = lb.clone() if ref is None else torch.maximum(ref, lb)
+        assert torch.equal(cpu(bs), ref)
+        s = float(ref.double().sum())
+        assert abs(float(out.item()) - s) <= 1e-12 * max(1.0, abs(s)), (float(out.item()), s)
+
+
+def _freeze_pair(gpu, B, iters, seed=4, scale=3.0, eps=-1.0):
+    gg_c, gg_g, xl, xh = acas(gpu, B, seed=seed, scale=scale)
+    se_c, se_g, _ = spec_pair(5, gpu)
+    ref = rh.full_freeze(xl, xh, gg_c, se_c, n_iters_per_layer=iters, n_iters_spec=iters,
+                         early_stop_eps=eps)
+    got = vh._full_freeze(xl.to(gpu), xh.to(gpu), gg_g, se_g, gpu, F32,
+                          n_iters_per_layer=iters, n_iters_spec=iters, early_stop_eps=eps)
+    return ref, got
+
+
+@pytest.mark.parametrize('iters', [1, 2, 10])
+def test_full_freeze_matches_oracle(gpu, iters):
+    (t_r, a_r, s_r, b_r), (t_g, a_g, s_g, b_g) = _freeze_pair(gpu, 12, iters)
+    assert set(a_g) == set(a_r) and all(set(a_g[L]) == set(a_r[L]) for L in a_r)
+    for L in sorted(t_r):
+        for j, what in ((0, 'lo'), (1, 'hi')):
+            got, ref = t_g[L][j], t_r[L][j]
+            if iters <= 2:
+                assert_bounds(got, ref, f'freeze {iters} it, layer {L} {what}',
+                              rtol=1e-4, atol=1e-5)
+            else:
+                assert_adam_drift(got, ref, f'freeze {iters} it, layer {L} {what}')
+    if iters <= 2:
+        assert_bounds(b_g, b_r, f'freeze spec best, {iters} it', rtol=1e-4, atol=1e-5)
+        # Adam's first steps move an alpha by lr * g / (|g| + eps): a full lr
+        # unless |g| is of the size of eps, where fp32 noise in g decides
+        for L in a_r:
+            for k in a_r[L]:
+                d = (cpu(a_g[L][k]) - a_r[L][k]).abs()
+                frac = float((d <= 1e-4).double().mean())
+                print(f'frozen alpha {L}/{k}: {frac:.5f} within 1e-4, max {float(d.max()):.2e}')
+                assert frac >= 0.999, (L, k, frac)
+    else:
+        assert_adam_drift(b_g, b_r, f'freeze spec best, {iters} it')
+
+
+def test_full_freeze_early_stop_reads_same_iterations(gpu):
+    """With the reference's early stop the GPU and the oracle stop after the
+    same evaluations: the frozen bounds agree to the drift criterion."""
+    (t_r, _, _, b_r), (t_g, _, _, b_g) = _freeze_pair(gpu, 8, 30, seed=6, eps=1e-6)
+    assert_adam_drift(b_g, b_r, 'freeze spec best with early stop')
+    for L in sorted(t_r):
+        assert_adam_drift(t_g[L][0], t_r[L][0], f'freeze with early stop, layer {L} lo')
+
+
+@pytest.mark.parametrize('spec_iters', [1, 2, 10])
+def test_replay_matches_oracle(gpu, spec_iters):
+    gg_c, gg_g, xl, xh = acas(gpu, 10, seed=8, scale=3.0)
+    se_c, se_g, _ = spec_pair(5, gpu)
+    _, a_layer, a_spec, _ = rh.full_freeze(xl, xh, gg_c, se_c, n_iters_per_layer=4,
+                                           n_iters_spec=4)
+    # one group's alphas (leaf 0), replayed on sub-boxes of every leaf
+    grp_l = {L: {k: a[:1] for k, a in d.items()} for L, d in a_layer.items()}
+    grp_s = {L: a[:1] for L, a in a_spec.items()}
+    c, r = (xl + xh) / 2, (xh - xl) / 2
+    sxl, sxh = c - 0.6 * r, c + 0.3 * r
+    b_r, A_r, t_r = rh.replay_batched(sxl, sxh, gg_c, se_c, grp_l, grp_s, spec_iters=spec_iters)
+    to = lambda d: {L: {k: a.to(gpu) for k, a in v.items()} for L, v in d.items()}
+    b_g, A_g, t_g = vh._replay_batched(sxl.to(gpu), sxh.to(gpu), gg_g, se_g, to(grp_l),
+                                       {L: a.to(gpu) for L, a in grp_s.items()}, gpu, F32,
+                                       spec_iters=spec_iters, return_tight=True)
+    for L in t_r:
+        assert_bounds(t_g[L][0], t_r[L][0], f'replay layer {L} lo', rtol=1e-4, atol=1e-5)
+        assert_bounds(t_g[L][1], t_r[L][1], f'replay layer {L} hi', rtol=1e-4, atol=1e-5)
+    if spec_iters <= 2:
+        assert_bounds(b_g, b_r, f'replay best, {spec_iters} it', rtol=1e-4, atol=1e-5)
+        assert_bounds(A_g, A_r, f'replay best A, {spec_iters} it', rtol=1e-4, atol=1e-5)
+    else:
+        assert_adam_drift(b_g, b_r, f'replay best, {spec_iters} it')
+
+
+def test_replay_per_leaf_groups_equal_per_group_calls(gpu):
+    gg_c, gg_g, xl, xh = acas(gpu, 6, seed=12, scale=3.0)
+    se_c, se_g, _ = spec_pair(5, gpu)
+    _, a_layer, a_spec, _ = vh._full_freeze(xl.to(gpu), xh.to(gpu), gg_g, se_g, gpu, F32,
+                                            n_iters_per_layer=5, n_iters_spec=5)
+    gid = torch.tensor([0, 3, 3, 5, 0, 1, 5, 5], dtype=torch.int64, device=gpu)
+    c, r = (xl + xh) / 2, (xh - xl) / 2
+    g = torch.Generator().manual_seed(1)
+    t = torch.rand(gid.numel(), 5, generator=g)
+    bxl = (c[gid.cpu()] - r[gid.cpu()] * t).to(gpu)
+    bxh = (c[gid.cpu()] + r[gid.cpu()] * t * 0.5).to(gpu)
+    pl, ps = vh._gather_alphas(a_layer, a_spec, gid)
+    best, A = vh._replay_batched(bxl, bxh, gg_g, se_g, pl, ps, gpu, F32)
+    for grp in gid.unique().tolist():
+        sel = (gid == grp).nonzero(as_tuple=True)[0]
+        gl = {L: {k: a[grp:grp + 1] for k, a in d.items()} for L, d in a_layer.items()}
+        gs = {L: a[grp:grp + 1] for L, a in a_spec.items()}
+        b1, A1 = vh._replay_batched(bxl[sel], bxh[sel], gg_g, se_g, gl, gs, gpu, F32)
+        assert_bounds(best[sel], b1, f'group {grp} best', rtol=1e-5, atol=1e-6)
+        assert_bounds(A[sel], A1, f'group {grp} A', rtol=1e-5, atol=1e-6)
+
+
+def test_hybrid_driver_acasxu_known_answers(gpu):
+    gg = onnx_net.load_onnx(NET, device=gpu, dtype=F32)
+    spec = vnnlib.load_vnnlib(os.path.join(GOLD, 'prop_1.vnnlib'))
+    res = vh.verify_hybrid(gg, spec, timeout=60.0)
+    print(f'prop_1 hybrid: {res}')
+    assert res['verdict'] == 'unsat', res
+    spec = vnnlib.load_vnnlib(os.path.join(GOLD, 'prop_2.vnnlib'))
+    res = vh.verify_hybrid(gg, spec, timeout=8.0, settings={'hybrid_freeze_iters': 20})
+    print(f'prop_2 hybrid: {res}')
+    assert res['verdict'] == 'unknown', res

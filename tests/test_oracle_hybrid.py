@@ -1,0 +1,160 @@
+"""Pins the CPU oracle of the hybrid freeze / replay (oracle/ref_hybrid.py).
+
+Checks: hand-computed known answers of the two bookkeeping rules; the
+identity that the freeze's first evaluation (alphas at CROWN's lower
+slopes) and the replay with those slopes reproduce the oracle's CROWN
+intermediate bounds and CROWN spec bound, which are pinned on their own;
+sampled ground truth for the optimised bounds (every sampled
+pre-activation inside the tightened layer bounds, every sampled spec value
+above the best spec bound); the optimisation never loosens a layer whose
+lower layers it did not change.  float64, CPU.
+"""
+import torch
+
+from oracle import ref_bound as rb
+from oracle import ref_hybrid as rh
+
+import _util
+
+DT = torch.float64
+
+
+def _t(v):
+    return torch.tensor(v, dtype=DT)
+
+
+def _net(widths=(3, 12, 12, 10, 3), seed=4, B=6, half=0.4):
+    gg = _util.tiny_mlp(list(widths), seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    c = torch.rand(B, widths[0], generator=g, dtype=DT) * 2 - 1
+    r = half * (0.5 + torch.rand(B, widths[0], generator=g, dtype=DT))
+    se, _ = _util.spec_for(widths[-1])
+    return gg, c - r, c + r, se
+
+
+def _pre_activations(x, gg):
+    """{L: pre-activation values feeding ReLU L} of points x (N, d)."""
+    vals, out = {}, {gg['input_name']: x}
+    for op in gg['ops']:
+        v = out[op['inputs'][0]]
+        if op['type'] == 'fc':
+            out[op['name']] = v @ op['W'].T + op['bias']
+        elif op['type'] == 'relu':
+            vals[op['layer_idx']] = v
+            out[op['name']] = v.clamp(min=0)
+        else:
+            out[op['name']] = v
+    return vals, out[gg['ops'][-1]['name']]
+
+
+def test_tighten_known_answer():
+    lo, hi = _t([[-1.0, -2.0, 0.5]]), _t([[3.0, 1.0, 2.0]])
+    # lower bounds 0 / -3 / 1.5, upper bounds -(-2)=2 / -(-0.5)=0.5 / -(-1)=1
+    sl = _t([[0.0, -3.0, 1.5, -2.0, -0.5, -1.0]])
+    lo_t, hi_t = rh.tighten(lo, hi, sl)
+    assert torch.equal(lo_t, _t([[0.0, -2.0, 1.0]]))   # 1.5 > hi 1 -> lo = hi
+    assert torch.equal(hi_t, _t([[2.0, 0.5, 1.0]]))
+
+
+def test_best_update_with_A_known_answer():
+    best, bA = rh.best_update_with_A(None, None, _t([[1.0, 2.0], [0.0, 0.0]]),
+                                     torch.zeros(2, 2, 1, dtype=DT))
+    lb = _t([[0.5, 2.5], [-1.0, 0.0]])          # leaf 0 improves query 1 only
+    A = torch.ones(2, 2, 1, dtype=DT)
+    best, bA = rh.best_update_with_A(best, bA, lb, A)
+    assert torch.equal(best, _t([[1.0, 2.5], [0.0, 0.0]]))
+    assert torch.equal(bA[0], torch.ones(2, 1, dtype=DT))   # the whole leaf's A
+    assert torch.equal(bA[1], torch.zeros(2, 1, dtype=DT))  # ties do not improve
+
+
+def test_freeze_first_evaluation_is_crown_intermediate():
+    """One iteration per layer: best = the bounds with alphas at CROWN's
+    lower slopes on the (unchanged) lower layers, i.e. the CROWN
+    intermediate bounds of every neuron unstable in some leaf."""
+    gg, xl, xh, se = _net()
+    tight, alphas, _, _ = rh.full_freeze(xl, xh, gg, se, n_iters_per_layer=1,
+                                         n_iters_spec=1)
+    ci = rb.crown_intermediate_batched(gg, xl, xh)
+    zono, _ = rb.zono_forward_batched(xl, xh, gg)
+    n_checked = 0
+    for L in sorted(tight):
+        lo, hi = tight[L]
+        u = ((zono[L][0] < 0) & (zono[L][1] > 0)).any(dim=0)
+        ok = lo <= hi
+        if L > 0:
+            assert set(alphas[L]) == set(range(L))
+            assert alphas[L][0].shape == (xl.shape[0], 2 * lo.shape[1], zono[0][0].shape[1])
+        for a, b in ((lo, ci[L][0]), (hi, ci[L][1])):
+            d = (a - b).abs()[:, u][ok[:, u]]
+            assert float(d.max()) < 1e-9, (L, float(d.max()))
+            n_checked += d.numel()
+        # stable columns: still inside the zonotope bounds
+        assert bool((lo >= zono[L][0] - 1e-12).all()) and bool((hi <= zono[L][1] + 1e-12).all())
+    assert n_checked > 50
+
+
+def test_freeze_bounds_are_sound_and_tighter():
+    gg, xl, xh, se = _net()
+    tight1, _, _, best1 = rh.full_freeze(xl, xh, gg, se, n_iters_per_layer=1, n_iters_spec=1)
+    tight, _, alpha_spec, best = rh.full_freeze(xl, xh, gg, se, n_iters_per_layer=25,
+                                                n_iters_spec=25, early_stop_eps=-1.0)
+    x = _util.sample_box(xl, xh, 4000, seed=3)
+    B, N, d = x.shape
+    pre, y = _pre_activations(x.reshape(B * N, d), gg)
+    for L, v in pre.items():
+        v = v.reshape(B, N, -1)
+        assert bool((v >= tight[L][0].unsqueeze(1) - 1e-9).all()), L
+        assert bool((v <= tight[L][1].unsqueeze(1) + 1e-9).all()), L
+    Wq = torch.stack([se[q][0] for q in sorted(se)])
+    bq = _t([se[q][1] for q in sorted(se)])
+    vals = (y @ Wq.T + bq).reshape(B, N, -1)
+    assert bool((best <= vals.min(dim=1).values + 1e-9).all())
+    # layer 1 sits on the unchanged zonotope bounds of layer 0, and the best
+    # includes the first evaluation: never looser than one iteration
+    assert bool((tight[1][0] >= tight1[1][0] - 1e-12).all())
+    assert bool((tight[1][1] <= tight1[1][1] + 1e-12).all())
+    assert float((tight[1][1] - tight[1][0]).sum()) < float((tight1[1][1] - tight1[1][0]).sum())
+    for a in alpha_spec.values():
+        assert float(a.min()) >= 0.0 and float(a.max()) <= 1.0
+
+
+def test_replay_with_crown_slopes_is_crown():
+    """Frozen alphas equal to CROWN's lower slopes on the CROWN
+    intermediate bounds: the replay's layer bounds are those bounds and its
+    one-iteration spec bound and A are the plain CROWN spec bound's."""
+    gg, xl, xh, se = _net(seed=7)
+    B = xl.shape[0]
+    ci = rb.crown_intermediate_batched(gg, xl, xh)
+    layer = {}
+    for L in sorted(ci):
+        Q = 2 * ci[L][0].shape[1]
+        layer[L] = {k: rh._init_alpha(*ci[k], Q) for k in sorted(ci) if k < L}
+    spec_a = {L: rh._init_alpha(*ci[L], len(se)) for L in ci}
+    best, bA, tight = rh.replay_batched(xl, xh, gg, se, layer, spec_a, spec_iters=1)
+    zono, _ = rb.zono_forward_batched(xl, xh, gg)
+    for L in ci:
+        u = ((zono[L][0] < 0) & (zono[L][1] > 0)).any(dim=0)
+        for a, b in ((tight[L][0], ci[L][0]), (tight[L][1], ci[L][1])):
+            assert float((a - b).abs()[:, u].max()) < 1e-9
+    lb, A, _ = rb.spec_backward_batched(tight, xl, xh, gg, se, return_input_linear=True)
+    assert float((best - lb).abs().max()) < 1e-12
+    assert float((bA - A).abs().max()) < 1e-12
+    assert best.shape == (B, len(se)) and bA.shape == (B, len(se), xl.shape[1])
+
+
+def test_replay_spec_iterations_only_improve():
+    gg, xl, xh, se = _net(seed=9)
+    _, layer, spec_a, _ = rh.full_freeze(xl, xh, gg, se, n_iters_per_layer=5, n_iters_spec=5)
+    b1, _, t1 = rh.replay_batched(xl, xh, gg, se, layer, spec_a, spec_iters=1)
+    b10, A10, t10 = rh.replay_batched(xl, xh, gg, se, layer, spec_a, spec_iters=10)
+    assert bool((b10 >= b1).all())
+    for L in t1:
+        assert torch.equal(t1[L][0], t10[L][0]) and torch.equal(t1[L][1], t10[L][1])
+    # the best spec bounds stay sound on samples
+    x = _util.sample_box(xl, xh, 2000, seed=5)
+    B, N, d = x.shape
+    _, y = _pre_activations(x.reshape(B * N, d), gg)
+    Wq = torch.stack([se[q][0] for q in sorted(se)])
+    bq = _t([se[q][1] for q in sorted(se)])
+    vals = (y @ Wq.T + bq).reshape(B, N, -1)
+    assert bool((b10 <= vals.min(dim=1).values + 1e-9).all())

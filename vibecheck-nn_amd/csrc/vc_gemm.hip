@@ -148,7 +148,8 @@ struct LoadGradRelax {
   const float *gE, *P;
   int ld, R;
   const float *lo, *hi, *alpha;
-  int p_bcast;  // P shared by all domains: row m reads P[m % R]
+  int p_bcast;    // P shared by all domains: row m reads P[m % R]
+  int alpha_row;  // alpha (M, ld), one per row (per-query alpha), else (B, ld)
   struct Row {
     int64_t mo, po, dom;
   };
@@ -175,7 +176,8 @@ struct LoadGradRelax {
       if (j < n) {
         Relax s = relax(x.lo[j], x.hi[j]);
         float ls = s.lo_s;
-        if (alpha) ls = s.active ? 1.f : (s.unstable ? alpha[rw.dom + k + j] : 0.f);
+        if (alpha)
+          ls = s.active ? 1.f : (s.unstable ? alpha[(alpha_row ? rw.mo : rw.dom) + k + j] : 0.f);
         const bool mp = x.pv[j] >= 0.f, mn = x.pv[j] <= 0.f;
         const float f = (mp ? ls : 0.f) + (mn ? s.up_s : 0.f);
         gp = x.ge[j] * f;
@@ -471,7 +473,23 @@ extern "C" int vc_alpha_grad_step(const float* gE, const float* P, int64_t M, in
   if (!gE || !P || !relu_lo || !relu_hi || !g_out || R <= 0 || n <= 0 || M < 0) return VC_ERR_ARG;
   if (M % R != 0) return VC_ERR_ARG;
   if (!W_next) return VC_ERR_UNSUPPORTED;
-  LoadGradRelax la{gE, P, n, R, relu_lo, relu_hi, alpha, p_bcast};
+  LoadGradRelax la{gE, P, n, R, relu_lo, relu_hi, alpha, p_bcast, 0};
+  const bool vec = vec_ok({gE, P, relu_lo, relu_hi, W_next}, {n});
+  return launch_gemm<1, false>(1, M, n_next, n, la, LoadWt{W_next, n},
+                               EpStoreBias{bias_next, g_out, n_next}, nullptr, vec,
+                               (hipStream_t)stream);
+}
+
+extern "C" int vc_alpha_grad_step_rows(const float* gE, const float* P, int64_t M, int R, int n,
+                                       const float* relu_lo, const float* relu_hi,
+                                       const float* alpha_rows, int p_bcast,
+                                       const float* W_next, const float* bias_next, int n_next,
+                                       float* g_out, vc_stream_t stream) {
+  if (!gE || !P || !relu_lo || !relu_hi || !alpha_rows || !g_out || R <= 0 || n <= 0 || M < 0)
+    return VC_ERR_ARG;
+  if (M % R != 0) return VC_ERR_ARG;
+  if (!W_next) return VC_ERR_UNSUPPORTED;
+  LoadGradRelax la{gE, P, n, R, relu_lo, relu_hi, alpha_rows, p_bcast, 1};
   const bool vec = vec_ok({gE, P, relu_lo, relu_hi, W_next}, {n});
   return launch_gemm<1, false>(1, M, n_next, n, la, LoadWt{W_next, n},
                                EpStoreBias{bias_next, g_out, n_next}, nullptr, vec,

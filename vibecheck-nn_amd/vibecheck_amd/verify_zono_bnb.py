@@ -588,21 +588,29 @@ def _crown_intermediate_batched(gg, xl, xh, device, dtype, chunk=2048,
 # --------------------------------------------------------------------------
 
 def _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, want_grad, galpha,
-                             beta=None, gbeta=None):
+                             beta=None, gbeta=None, seed_name=None, want_A=False):
     """One alpha-CROWN evaluation: lb (B, Q); when ``want_grad`` also fills
     ``galpha[L]`` with d(sum lb)/d alpha_L (the autograd of the reference's
     backward, torch clamp subgradients included).  ``beta`` is the signed
     ReLU-split beta {L: (B, n_L)} added at each relu's input
-    (``relu_split_beta``); ``gbeta[L]`` receives d(sum lb)/d beta_L."""
+    (``relu_split_beta``); ``gbeta[L]`` receives d(sum lb)/d beta_L.
+    ``seed_name`` (default: the output op) is the op whose output the Q
+    shared rows Wq (Q, n) seed, as ``seed_ew_at`` does; an alpha_L of shape
+    (B, Q, n_L) is one alpha per row (per-query alpha), and galpha_L then
+    has that shape too.  ``want_A``: returns (lb, A) with A (B*Q, n_in) the
+    input linearization of the rows."""
     B, n_in = xl.shape
     Q = Wq.shape[0]
     dev = xl.device
     st = stream()
     trace = BackwardTrace() if want_grad else None
-    lb, A, a_shared, _ = _backward(sb, xl, xh, gg, gg['ops'][-1]['name'], Wq,
+    seed = gg['ops'][-1]['name'] if seed_name is None else seed_name
+    lb, A, a_shared, _ = _backward(sb, xl, xh, gg, seed, Wq,
                                    True, bq, alpha, beta, trace)
+    if want_A and (A is None or a_shared):
+        raise NotImplementedError('vibecheck_amd: per-row linearization needs a relu')
     if not want_grad:
-        return lb
+        return (lb, A) if want_A else lb
     if A is None or a_shared:
         raise NotImplementedError('vibecheck_amd: alpha gradient needs a relu')
     # trace.relus: (L, P, shared) in backward order (top relu first);
@@ -624,12 +632,24 @@ def _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, want_grad, galpha,
         lo, hi = f32(sb[L][0]), f32(sb[L][1])
         n = lo.shape[1]
         a = f32(alpha[L]) if (alpha is not None and L in alpha) else None
+        per_row = a is not None and a.dim() == 3
         ga = galpha.get(L) if galpha is not None else None
         gb = gbeta.get(L) if gbeta is not None else None
+        if per_row and ga is not None:
+            call('vc_alpha_grad_rows', ptr(g), ptr(P), 1 if p_shared else 0, M, Q, n,
+                 ptr(lo), ptr(hi), ptr(ga), st)
+            ga = None
         if ga is not None or gb is not None:
             call('vc_alpha_grad_reduce', ptr(g), ptr(P), 1 if p_shared else 0,
                  B, Q, n, ptr(lo), ptr(hi), ptr(ga), ptr(gb), st)
-        if i > 0:
+        if i > 0 and per_row:
+            fn = _op_params(fcs[i], dev)
+            g2 = torch.empty(M, fn['n_out'], device=dev)
+            call('vc_alpha_grad_step_rows', ptr(g), ptr(P), M, Q, n, ptr(lo), ptr(hi),
+                 ptr(a.reshape(M, n)), 1 if p_shared else 0, ptr(fn['W']), ptr(fn['b']),
+                 fn['n_out'], ptr(g2), st)
+            g = g2
+        elif i > 0:
             fn = _op_params(fcs[i], dev)
             g2 = torch.empty(M, fn['n_out'], device=dev)
             # slopes once per (domain, neuron), then the sweep step without
@@ -641,7 +661,7 @@ def _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, want_grad, galpha,
                  ptr(ls), ptr(us), ptr(ut), 1 if p_shared else 0,
                  ptr(fn['W']), ptr(fn['b']), fn['n_out'], ptr(g2), st)
             g = g2
-    return lb
+    return (lb, A) if want_A else lb
 
 
 def _run_alpha_crown_inputsplit_batched(xl, xh, gg, spec_ew, device, dtype,
