@@ -367,6 +367,54 @@ def kernel_suite(reps):
            _time_launches([fn], reps), 'mfma', 2.0 * 2 * B * (C_out * Ho * Ho) * (C_in * k * k))
 
 
+def hybrid_replay_suite(reps=5, B=4096, spec_iters=10):
+    """The hybrid replay (zonotope bounds, frozen per-query alpha layer
+    tightening, ``spec_iters`` per-leaf spec alpha Adam iterations) on
+    B ACAS-Xu-shaped leaves, each with its own group's alphas: one JSON line
+    with the time per call, leaves/s and the algorithmic FLOP of the
+    per-row backward GEMMs of the layer tightening (2 * B * 2 n_L * n_out *
+    n_in per fc below the seeded one, Q = 2 n_L rows per leaf)."""
+    from vibecheck_amd import verify_hybrid_acasxu as vh
+    from vibecheck_amd import workloads as wk
+    from vibecheck_amd.spec import dedup_queries
+
+    dev = torch.device('cuda:0')
+    gg = wk.acas_gg(device=dev, dtype=torch.float32)
+    spec = wk.pairwise_spec(5, [0.0], [0.0], True)
+    uq, _ = dedup_queries(spec.as_linear_queries(5))
+    se = {i: (torch.tensor(w, dtype=torch.float32, device=dev), b) for i, (w, b) in enumerate(uq)}
+    xl, xh = wk.acas_boxes(32, seed=3, device=dev, dtype=torch.float32)
+    _, a_layer, a_spec, _ = vh._full_freeze(xl, xh, gg, se, dev, torch.float32,
+                                            n_iters_per_layer=20, n_iters_spec=20)
+    g = torch.Generator(device=dev).manual_seed(5)
+    gid = torch.randint(0, 32, (B,), device=dev, generator=g)
+    t = torch.rand(B, 5, device=dev, generator=g)
+    c, r = (xl + xh)[gid] / 2, (xh - xl)[gid] / 2
+    bxl, bxh = c - r * t, c + r * t
+    pl, ps = vh._gather_alphas(a_layer, a_spec, gid)
+    fcs = [op for op in gg['ops'] if op['type'] == 'fc']
+    flop = 0.0
+    for L in a_layer:
+        if a_layer[L]:
+            q = 2 * fcs[L]['W'].shape[0]
+            flop += sum(2.0 * B * q * f['W'].shape[0] * f['W'].shape[1] for f in fcs[:L])
+    fn = lambda: vh._replay_batched(bxl, bxh, gg, se, pl, ps, dev, torch.float32,
+                                    spec_iters=spec_iters)
+    fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / reps
+    print(json.dumps({
+        'row': 'f4', 'kernel': '_replay_batched (per-row alpha backward + spec alpha Adam)',
+        'workload': f'ACAS-Xu 5-50x6-5, {B} leaves of 32 groups, {spec_iters} spec iterations',
+        'ms_per_call': sec * 1e3, 'leaves_per_s': B / sec,
+        'tighten_gemm_flop': flop, 'tighten_gemm_tflops_over_call': flop / sec / 1e12}),
+        flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -378,6 +426,8 @@ def main():
                     help='only run a plain copy of MIB MiB (counter calibration)')
     ap.add_argument('--kernels', action='store_true',
                     help='only time the layer-wise kernels one at a time (one JSON line each)')
+    ap.add_argument('--hybrid', action='store_true',
+                    help='only time the hybrid replay on ACAS-Xu-shaped leaves (one JSON line)')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU only (this build has no multi-GPU path); '
@@ -388,6 +438,10 @@ def main():
         return
     if args.kernels:
         kernel_suite(max(4, args.steps * 4))
+        hybrid_replay_suite()
+        return
+    if args.hybrid:
+        hybrid_replay_suite(reps=max(1, args.steps))
         return
 
     from vibecheck_amd import _lib
