@@ -154,6 +154,8 @@ def _relaxed_rows_oracle(ew, B, R, lo, hi, alpha, alpha_row, beta):
     (6, 16, 128, 64, 1, None, False),     # rows shared by every domain
     (4, 5, 80, 50, 0, 'row', True),       # per-row alpha
     (3, 130, 1024, 33, 0, 'dom', False),  # rows of one domain over many row groups
+    (37, 9, 64, 50, 0, 'row', True),      # 64 columns: the 16-lane narrow pass, float4
+    (11, 7, 64, 64, 1, 'dom', False),     # narrow pass, shared rows, M % 16 != 0
 ])
 def test_backward_fc_two_phase(gpu, B, R, n_out, n_in, bcast, alpha_mode, with_beta):
     """vc_backward_fc with a relaxed-rows buffer (relaxation pass + plain

@@ -57,18 +57,22 @@ struct LoadRelaxRow {
     bool ro;              // this tile writes relax_out
   };
   struct Raw {
-    float x[4], lo[4], hi[4];
+    float x[4], lo[4], hi[4], a[4], b[4];
   };
   __device__ Row row(int64_t, int64_t m, bool first) const {
     const int64_t d = m / R;
     return Row{(ew_bcast ? m - d * R : m) * ld, d * ld, m * ld, first && relax_out != nullptr};
   }
+  // alpha and beta travel with the prefetched tile, so their latency hides
+  // behind the previous tile's MFMAs like the rows'
   template <bool VEC>
   __device__ void fetch(const Row& rw, int k, int n, Raw& x) const {
     ld4<VEC>(ew + rw.xo + k, n, x.x);
     if (lo) {
       ld4<VEC>(lo + rw.dom + k, n, x.lo);
       ld4<VEC>(hi + rw.dom + k, n, x.hi);
+      if (alpha) ld4<VEC>(alpha + (alpha_per_row ? rw.mo : rw.dom) + k, n, x.a);
+      if (beta) ld4<VEC>(beta + rw.dom + k, n, x.b);
     }
   }
   template <bool VEC>
@@ -81,13 +85,10 @@ struct LoadRelaxRow {
         if (lo) {
           Relax s = relax(x.lo[j], x.hi[j]);
           float ls = s.lo_s;
-          if (alpha) {
-            const float a = alpha[(alpha_per_row ? rw.mo : rw.dom) + k + j];
-            ls = s.active ? 1.f : (s.unstable ? a : 0.f);
-          }
+          if (alpha) ls = s.active ? 1.f : (s.unstable ? x.a[j] : 0.f);
           const float ep = fmaxf(e, 0.f), en = fminf(e, 0.f);
           e = ep * ls + en * s.up_s;
-          if (beta) e = e + beta[rw.dom + k + j];
+          if (beta) e = e + x.b[j];
           p = en * s.up_t;
         }
         if (bias) p += e * bias[k + j];
@@ -154,7 +155,7 @@ struct LoadGradRelax {
     int64_t mo, po, dom;
   };
   struct Raw {
-    float ge[4], pv[4], lo[4], hi[4];
+    float ge[4], pv[4], lo[4], hi[4], a[4];
   };
   __device__ Row row(int64_t, int64_t m, bool) const {
     const int64_t d = m / R;
@@ -166,6 +167,7 @@ struct LoadGradRelax {
     ld4<VEC>(P + rw.po + k, n, x.pv);
     ld4<VEC>(lo + rw.dom + k, n, x.lo);
     ld4<VEC>(hi + rw.dom + k, n, x.hi);
+    if (alpha) ld4<VEC>(alpha + (alpha_row ? rw.mo : rw.dom) + k, n, x.a);
   }
   template <bool VEC>
   __device__ void finish(const Row& rw, int k, int n, const Raw& x, float (*v)[4], KSum&,
@@ -176,8 +178,7 @@ struct LoadGradRelax {
       if (j < n) {
         Relax s = relax(x.lo[j], x.hi[j]);
         float ls = s.lo_s;
-        if (alpha)
-          ls = s.active ? 1.f : (s.unstable ? alpha[(alpha_row ? rw.mo : rw.dom) + k + j] : 0.f);
+        if (alpha) ls = s.active ? 1.f : (s.unstable ? x.a[j] : 0.f);
         const bool mp = x.pv[j] >= 0.f, mn = x.pv[j] <= 0.f;
         const float f = (mp ? ls : 0.f) + (mn ? s.up_s : 0.f);
         gp = x.ge[j] * f;
@@ -423,6 +424,68 @@ extern "C" int vc_zono_fc(const float* c, const float* G, int64_t B, int n_in, i
                                vec_ok({W, G}, {n_in, K}), st);
 }
 
+// Phase 1 for narrow rows (n <= 64): one 16-lane row of the wavefront per
+// backward row, a quad of 4 columns per lane, RN rows per workgroup pass;
+// the row's constant term is summed over its 16 lanes in fp64.  Same
+// arithmetic per element as k_relax_rows, whose quads-per-thread mapping
+// leaves 3/4 of a workgroup idle at 64 columns.  Below 64 columns the
+// fused form is faster (the relaxed rows' round trip through HBM costs more
+// than the loads' arithmetic), so the two-phase step starts at 64.
+constexpr int RN = NT / 16;
+constexpr int kNarrowMaxWidth = 64;
+
+template <bool VEC>
+__global__ __launch_bounds__(NT) void k_relax_rows_narrow(const float* ew, int64_t M, int R,
+                                                          int n, const float* lo, const float* hi,
+                                                          const float* alpha, int alpha_per_row,
+                                                          const float* beta, const float* bias,
+                                                          int ew_bcast, float* out, float* acc) {
+  const int c = 4 * (threadIdx.x & 15);
+  const int cnt = n - c < 4 ? n - c : 4;  // <= 0: the lane holds no column
+  for (int64_t m0 = (int64_t)blockIdx.x * RN; m0 < M; m0 += (int64_t)gridDim.x * RN) {
+    const int64_t mm = m0 + (threadIdx.x >> 4);
+    const int64_t m = mm < M ? mm : M - 1;  // past the end: recompute the last row, no store
+    const int64_t d = m / R;
+    const int64_t xr = ew_bcast ? m - d * R : m;
+    double p = 0.0;
+    if (cnt > 0) {
+      float x[4], l4[4], h4[4], a4[4], b4[4], bi[4], e[4];
+      ld4<VEC>(ew + xr * n + c, cnt, x);
+      ld4<VEC>(lo + d * n + c, cnt, l4);
+      ld4<VEC>(hi + d * n + c, cnt, h4);
+      if (alpha) ld4<VEC>(alpha + (alpha_per_row ? m : d) * n + c, cnt, a4);
+      if (beta) ld4<VEC>(beta + d * n + c, cnt, b4);
+      if (bias) ld4<VEC>(bias + c, cnt, bi);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        e[j] = 0.f;
+        if (j >= cnt) continue;
+        const Relax r = relax(l4[j], h4[j]);
+        const float ls = alpha ? (r.active ? 1.f : (r.unstable ? a4[j] : 0.f)) : r.lo_s;
+        const float ep = fmaxf(x[j], 0.f), en = fminf(x[j], 0.f);
+        float v = ep * ls + en * r.up_s;
+        if (beta) v = v + b4[j];
+        float pp = en * r.up_t;
+        if (bias) pp += v * bi[j];
+        p += (double)pp;
+        e[j] = v;
+      }
+      if (mm < M) {
+        float* o = out + mm * n + c;
+        if (VEC && cnt == 4) {
+          *reinterpret_cast<float4*>(o) = make_float4(e[0], e[1], e[2], e[3]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (j < cnt) o[j] = e[j];
+        }
+      }
+    }
+    p = row_sum16(p);
+    if ((threadIdx.x & 15) == 0 && mm < M) acc[mm] = (float)((double)acc[mm] + p);
+  }
+}
+
 extern "C" int vc_backward_fc(const float* ew_in, int64_t M, int R, int n_out,
                               const float* relu_lo, const float* relu_hi,
                               const float* alpha, int alpha_per_row, const float* beta,
@@ -440,6 +503,21 @@ extern "C" int vc_backward_fc(const float* ew_in, int64_t M, int R, int n_out,
     // relax_out, which the contract fills anyway), and the product runs as
     // a plain GEMM whose prologue holds no per-element arithmetic.
     const bool v1 = vec_ok({ew_in, relu_lo, relu_hi, alpha, beta, bias, relax_out}, {n_out});
+    if (n_out <= kNarrowMaxWidth) {
+      const int64_t grid = (M + RN - 1) / RN < kMaxGrid ? (M + RN - 1) / RN : kMaxGrid;
+      if (v1)
+        hipLaunchKernelGGL(k_relax_rows_narrow<true>, dim3((unsigned)grid), dim3(NT), 0, st,
+                           ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, beta,
+                           bias, ew_bcast, relax_out, acc);
+      else
+        hipLaunchKernelGGL(k_relax_rows_narrow<false>, dim3((unsigned)grid), dim3(NT), 0, st,
+                           ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, beta,
+                           bias, ew_bcast, relax_out, acc);
+      VC_LAUNCH_CHECK();
+      return launch_gemm<1, false>(1, M, n_in, n_out, LoadRow{relax_out, n_out}, LoadW{W, n_in},
+                                   EpStoreBias{nullptr, ew_out, n_in}, nullptr,
+                                   vec_ok({relax_out, W}, {n_out, n_in}), st);
+    }
     const int64_t grid = (M + RR - 1) / RR < kMaxGrid ? (M + RR - 1) / RR : kMaxGrid;
     if (v1)
       hipLaunchKernelGGL(k_relax_rows<true>, dim3((unsigned)grid), dim3(NT), 0, st, ew_in, M, R,
@@ -460,7 +538,7 @@ extern "C" int vc_backward_fc(const float* ew_in, int64_t M, int R, int n_out,
                                  vec_ok({ew_in, W}, {n_out, n_in}), st);
   LoadRelaxRow la{ew_in, n_out, R, relu_lo, relu_hi, alpha, beta, bias, alpha_per_row, relax_out,
                   ew_bcast};
-  const bool vec = vec_ok({ew_in, relu_lo, relu_hi, W}, {n_out, n_in});
+  const bool vec = vec_ok({ew_in, relu_lo, relu_hi, alpha, beta, W}, {n_out, n_in});
   return launch_gemm<1, true>(1, M, n_in, n_out, la, LoadW{W, n_in},
                               EpStoreBias{nullptr, ew_out, n_in}, acc, vec, st);
 }
@@ -474,7 +552,7 @@ extern "C" int vc_alpha_grad_step(const float* gE, const float* P, int64_t M, in
   if (M % R != 0) return VC_ERR_ARG;
   if (!W_next) return VC_ERR_UNSUPPORTED;
   LoadGradRelax la{gE, P, n, R, relu_lo, relu_hi, alpha, p_bcast, 0};
-  const bool vec = vec_ok({gE, P, relu_lo, relu_hi, W_next}, {n});
+  const bool vec = vec_ok({gE, P, relu_lo, relu_hi, alpha, W_next}, {n});
   return launch_gemm<1, false>(1, M, n_next, n, la, LoadWt{W_next, n},
                                EpStoreBias{bias_next, g_out, n_next}, nullptr, vec,
                                (hipStream_t)stream);
@@ -490,7 +568,7 @@ extern "C" int vc_alpha_grad_step_rows(const float* gE, const float* P, int64_t 
   if (M % R != 0) return VC_ERR_ARG;
   if (!W_next) return VC_ERR_UNSUPPORTED;
   LoadGradRelax la{gE, P, n, R, relu_lo, relu_hi, alpha_rows, p_bcast, 1};
-  const bool vec = vec_ok({gE, P, relu_lo, relu_hi, W_next}, {n});
+  const bool vec = vec_ok({gE, P, relu_lo, relu_hi, alpha_rows, W_next}, {n});
   return launch_gemm<1, false>(1, M, n_next, n, la, LoadWt{W_next, n},
                                EpStoreBias{bias_next, g_out, n_next}, nullptr, vec,
                                (hipStream_t)stream);
