@@ -113,9 +113,12 @@ __global__ __launch_bounds__(NT) void gemm_kernel(int64_t M, int N, int K, int t
   constexpr int SA = BM + PAD, SB = BN + PAD;
   constexpr int QR = BK / 4;     // quads per row of a K-tile
   constexpr int RP = NT / QR;    // rows covered by one pass of the workgroup
-  constexpr int QA = BM / RP;    // A quads per thread per K-tile
-  constexpr int QB = BN / RP;    // B quads per thread per K-tile
-  static_assert(QA * RP == BM && QB * RP == BN, "tile / thread mismatch");
+  // 32-row tiles with 16-deep K-tiles: one pass covers 64 rows, so only the
+  // threads of the first 32 load A (AH)
+  constexpr bool AH = BM < RP;
+  constexpr int QA = AH ? 1 : BM / RP;  // A quads per thread per K-tile
+  constexpr int QB = BN / RP;           // B quads per thread per K-tile
+  static_assert((AH ? RP == 2 * BM : QA * RP == BM) && QB * RP == BN, "tile / thread mismatch");
   constexpr bool TB = LB::kTrans;
   __shared__ __align__(16) float As[2][NA][BK][SA];
   __shared__ __align__(16) float Bs[2][NA][BK][SB];
@@ -139,10 +142,11 @@ __global__ __launch_bounds__(NT) void gemm_kernel(int64_t M, int N, int K, int t
 
     typename LA::Row arow[QA];
     bool aok[QA];
+    const bool a_in = !AH || r4 < BM;
 #pragma unroll
     for (int p = 0; p < QA; ++p) {
       const int64_t m = m0 + r4 + RP * p;
-      aok[p] = m < M;
+      aok[p] = a_in && m < M;
       arow[p] = la.row(bz, aok[p] ? m : m0, tn == 0);
     }
 
@@ -191,15 +195,18 @@ __global__ __launch_bounds__(NT) void gemm_kernel(int64_t M, int N, int K, int t
     };
 
     auto store = [&](int k0, int buf) {
+      if (a_in) {
 #pragma unroll
-      for (int p = 0; p < QA; ++p) {
-        float v[NA][4];
-        la.template finish<VEC>(arow[p], k0 + 4 * q4, acnt[p], araw[p], v, rowpart[p], do_rows);
-        const int mm = r4 + RP * p;
+        for (int p = 0; p < QA; ++p) {
+          float v[NA][4];
+          la.template finish<VEC>(arow[p], k0 + 4 * q4, acnt[p], araw[p], v, rowpart[p],
+                                  do_rows);
+          const int mm = r4 + RP * p;
 #pragma unroll
-        for (int a = 0; a < NA; ++a)
+          for (int a = 0; a < NA; ++a)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) As[buf][a][QR * j + q4][mm] = v[a][j];
+            for (int j = 0; j < 4; ++j) As[buf][a][QR * j + q4][mm] = v[a][j];
+        }
       }
 #pragma unroll
       for (int p = 0; p < QB; ++p) {
@@ -290,7 +297,9 @@ __global__ __launch_bounds__(NT) void gemm_kernel(int64_t M, int N, int K, int t
 
 constexpr int64_t kMaxGrid = 1 << 20;  // workgroups; tiles beyond loop (a multiple of 8)
 
-// Loaders opt into 32-row tiles with a static kSmallM = true.
+constexpr int64_t kFewTiles = 512;  // two 64x64 tiles per CU
+
+// Loaders opt into 32-row tiles for M <= 32 with a static kSmallM = true.
 template <class T, class = void>
 struct small_m_ok : std::false_type {};
 template <class T>
@@ -332,6 +341,10 @@ int launch_gemm(int64_t batch, int64_t M, int N, int K, LA la, LB lb, EP ep, flo
   if constexpr (small_m_ok<LA>::value) {
     if (M <= 32) return launch_fm<NA, ACC_ROWS, 1>(batch, M, N, K, la, lb, ep, acc_rows, vec, st);
   }
+  // fewer 64-row tiles than kFewTiles: 32-row tiles double the workgroups
+  // of a launch that would leave CUs without a second workgroup
+  if (batch * ((M + 63) / 64) * ((N + 63) / 64) < kFewTiles)
+    return launch_fm<NA, ACC_ROWS, 1>(batch, M, N, K, la, lb, ep, acc_rows, vec, st);
   return launch_fm<NA, ACC_ROWS, 2>(batch, M, N, K, la, lb, ep, acc_rows, vec, st);
 }
 
