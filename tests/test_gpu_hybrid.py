@@ -182,6 +182,9 @@ def test_replay_matches_oracle(gpu, spec_iters):
 
 
 def test_replay_per_leaf_groups_equal_per_group_calls(gpu):
+    """One replay over leaves of several groups, with per-leaf alpha copies
+    or reading the frozen alphas by group index, equals one replay per
+    group."""
     gg_c, gg_g, xl, xh = acas(gpu, 6, seed=12, scale=3.0)
     se_c, se_g, _ = spec_pair(5, gpu)
     _, a_layer, a_spec, _ = vh._full_freeze(xl.to(gpu), xh.to(gpu), gg_g, se_g, gpu, F32,
@@ -194,6 +197,16 @@ def test_replay_per_leaf_groups_equal_per_group_calls(gpu):
     bxh = (c[gid.cpu()] + r[gid.cpu()] * t * 0.5).to(gpu)
     pl, ps = vh._gather_alphas(a_layer, a_spec, gid)
     best, A = vh._replay_batched(bxl, bxh, gg_g, se_g, pl, ps, gpu, F32)
+    # the frozen layer alphas read through the group index: the same launches
+    # on the same values, so bit-identical to the per-leaf copies
+    bg, Ag, tg = vh._replay_batched(bxl, bxh, gg_g, se_g, a_layer, a_spec, gpu, F32, group=gid,
+                                    return_tight=True)
+    _, _, tp = vh._replay_batched(bxl, bxh, gg_g, se_g, pl, ps, gpu, F32, return_tight=True)
+    assert torch.equal(bg, best) and torch.equal(Ag, A)
+    for L in tp:
+        assert torch.equal(tg[L][0], tp[L][0]) and torch.equal(tg[L][1], tp[L][1])
+    with pytest.raises(ValueError):
+        vh._replay_batched(bxl, bxh, gg_g, se_g, a_layer, a_spec, gpu, F32, group=gid + 6)
     for grp in gid.unique().tolist():
         sel = (gid == grp).nonzero(as_tuple=True)[0]
         gl = {L: {k: a[grp:grp + 1] for k, a in d.items()} for L, d in a_layer.items()}

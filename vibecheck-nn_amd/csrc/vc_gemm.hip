@@ -52,16 +52,20 @@ struct LoadRelaxRow {
   int alpha_per_row;
   float* relax_out;
   int ew_bcast;  // rows shared by all domains: row m reads ew[m % R]
+  const int64_t* alpha_group = nullptr;  // per-row alpha of domain d's group: (G, R, ld)
   struct Row {
-    int64_t xo, dom, mo;  // offsets of the ew row, the domain's neurons, row m
-    bool ro;              // this tile writes relax_out
+    int64_t xo, dom, mo, ao;  // offsets of the ew row, the domain's neurons, row m, alpha
+    bool ro;                  // this tile writes relax_out
   };
   struct Raw {
     float x[4], lo[4], hi[4], a[4], b[4];
   };
   __device__ Row row(int64_t, int64_t m, bool first) const {
     const int64_t d = m / R;
-    return Row{(ew_bcast ? m - d * R : m) * ld, d * ld, m * ld, first && relax_out != nullptr};
+    const int64_t ao = alpha_group ? (alpha_group[d] * R + (m - d * R)) * ld
+                                   : (alpha_per_row ? m * ld : d * ld);
+    return Row{(ew_bcast ? m - d * R : m) * ld, d * ld, m * ld, ao,
+               first && relax_out != nullptr};
   }
   // alpha and beta travel with the prefetched tile, so their latency hides
   // behind the previous tile's MFMAs like the rows'
@@ -71,7 +75,7 @@ struct LoadRelaxRow {
     if (lo) {
       ld4<VEC>(lo + rw.dom + k, n, x.lo);
       ld4<VEC>(hi + rw.dom + k, n, x.hi);
-      if (alpha) ld4<VEC>(alpha + (alpha_per_row ? rw.mo : rw.dom) + k, n, x.a);
+      if (alpha) ld4<VEC>(alpha + rw.ao + k, n, x.a);
       if (beta) ld4<VEC>(beta + rw.dom + k, n, x.b);
     }
   }
@@ -304,6 +308,7 @@ template <bool VEC>
 __global__ __launch_bounds__(NT) void k_relax_rows(const float* ew, int64_t M, int R, int n,
                                                    const float* lo, const float* hi,
                                                    const float* alpha, int alpha_per_row,
+                                                   const int64_t* alpha_group,
                                                    const float* beta, const float* bias,
                                                    int ew_bcast, float* out, float* acc) {
   __shared__ double red[NT / 64][RR];
@@ -317,7 +322,7 @@ __global__ __launch_bounds__(NT) void k_relax_rows(const float* ew, int64_t M, i
       dr[k] = mr[k] / R;
       xr[k] = ew_bcast ? mr[k] - dr[k] * R : mr[k];
     }
-    const bool shared = dr[0] == dr[RR - 1] && !(alpha && alpha_per_row);
+    const bool shared = dr[0] == dr[RR - 1] && !(alpha && (alpha_per_row || alpha_group));
     double p[RR];
 #pragma unroll
     for (int k = 0; k < RR; ++k) p[k] = 0.0;
@@ -334,7 +339,11 @@ __global__ __launch_bounds__(NT) void k_relax_rows(const float* ew, int64_t M, i
         float l4[4], h4[4], a4[4], b4[4];
         ld4<VEC>(lo + dr[k] * n + c, cnt, l4);
         ld4<VEC>(hi + dr[k] * n + c, cnt, h4);
-        if (alpha) ld4<VEC>(alpha + (alpha_per_row ? mr[k] : dr[k]) * n + c, cnt, a4);
+        if (alpha) {
+          const int64_t ar = alpha_group ? alpha_group[dr[k]] * R + (mr[k] - dr[k] * R)
+                                         : (alpha_per_row ? mr[k] : dr[k]);
+          ld4<VEC>(alpha + ar * n + c, cnt, a4);
+        }
         if (beta) ld4<VEC>(beta + dr[k] * n + c, cnt, b4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -438,6 +447,7 @@ template <bool VEC>
 __global__ __launch_bounds__(NT) void k_relax_rows_narrow(const float* ew, int64_t M, int R,
                                                           int n, const float* lo, const float* hi,
                                                           const float* alpha, int alpha_per_row,
+                                                          const int64_t* alpha_group,
                                                           const float* beta, const float* bias,
                                                           int ew_bcast, float* out, float* acc) {
   const int c = 4 * (threadIdx.x & 15);
@@ -453,7 +463,11 @@ __global__ __launch_bounds__(NT) void k_relax_rows_narrow(const float* ew, int64
       ld4<VEC>(ew + xr * n + c, cnt, x);
       ld4<VEC>(lo + d * n + c, cnt, l4);
       ld4<VEC>(hi + d * n + c, cnt, h4);
-      if (alpha) ld4<VEC>(alpha + (alpha_per_row ? m : d) * n + c, cnt, a4);
+      if (alpha) {
+        const int64_t ar = alpha_group ? alpha_group[d] * R + (m - d * R)
+                                       : (alpha_per_row ? m : d);
+        ld4<VEC>(alpha + ar * n + c, cnt, a4);
+      }
       if (beta) ld4<VEC>(beta + d * n + c, cnt, b4);
       if (bias) ld4<VEC>(bias + c, cnt, bi);
 #pragma unroll
@@ -486,12 +500,13 @@ __global__ __launch_bounds__(NT) void k_relax_rows_narrow(const float* ew, int64
   }
 }
 
-extern "C" int vc_backward_fc(const float* ew_in, int64_t M, int R, int n_out,
-                              const float* relu_lo, const float* relu_hi,
-                              const float* alpha, int alpha_per_row, const float* beta,
-                              const float* W, const float* bias, int n_in, float* ew_out,
-                              float* acc, float* relax_out, int ew_bcast,
-                              vc_stream_t stream) {
+namespace {
+
+int backward_fc(const float* ew_in, int64_t M, int R, int n_out, const float* relu_lo,
+                const float* relu_hi, const float* alpha, int alpha_per_row,
+                const int64_t* alpha_group, const float* beta, const float* W,
+                const float* bias, int n_in, float* ew_out, float* acc, float* relax_out,
+                int ew_bcast, vc_stream_t stream) {
   if (!ew_in || !W || !ew_out || R <= 0 || n_out <= 0 || n_in <= 0 || M < 0) return VC_ERR_ARG;
   if ((relu_lo == nullptr) != (relu_hi == nullptr)) return VC_ERR_ARG;
   if (M % R != 0) return VC_ERR_ARG;
@@ -507,12 +522,12 @@ extern "C" int vc_backward_fc(const float* ew_in, int64_t M, int R, int n_out,
       const int64_t grid = (M + RN - 1) / RN < kMaxGrid ? (M + RN - 1) / RN : kMaxGrid;
       if (v1)
         hipLaunchKernelGGL(k_relax_rows_narrow<true>, dim3((unsigned)grid), dim3(NT), 0, st,
-                           ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, beta,
-                           bias, ew_bcast, relax_out, acc);
+                           ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group,
+                           beta, bias, ew_bcast, relax_out, acc);
       else
         hipLaunchKernelGGL(k_relax_rows_narrow<false>, dim3((unsigned)grid), dim3(NT), 0, st,
-                           ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, beta,
-                           bias, ew_bcast, relax_out, acc);
+                           ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group,
+                           beta, bias, ew_bcast, relax_out, acc);
       VC_LAUNCH_CHECK();
       return launch_gemm<1, false>(1, M, n_in, n_out, LoadRow{relax_out, n_out}, LoadW{W, n_in},
                                    EpStoreBias{nullptr, ew_out, n_in}, nullptr,
@@ -521,12 +536,12 @@ extern "C" int vc_backward_fc(const float* ew_in, int64_t M, int R, int n_out,
     const int64_t grid = (M + RR - 1) / RR < kMaxGrid ? (M + RR - 1) / RR : kMaxGrid;
     if (v1)
       hipLaunchKernelGGL(k_relax_rows<true>, dim3((unsigned)grid), dim3(NT), 0, st, ew_in, M, R,
-                         n_out, relu_lo, relu_hi, alpha, alpha_per_row, beta, bias, ew_bcast,
-                         relax_out, acc);
+                         n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group, beta, bias,
+                         ew_bcast, relax_out, acc);
     else
       hipLaunchKernelGGL(k_relax_rows<false>, dim3((unsigned)grid), dim3(NT), 0, st, ew_in, M, R,
-                         n_out, relu_lo, relu_hi, alpha, alpha_per_row, beta, bias, ew_bcast,
-                         relax_out, acc);
+                         n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group, beta, bias,
+                         ew_bcast, relax_out, acc);
     VC_LAUNCH_CHECK();
     return launch_gemm<1, false>(1, M, n_in, n_out, LoadRow{relax_out, n_out}, LoadW{W, n_in},
                                  EpStoreBias{nullptr, ew_out, n_in}, nullptr,
@@ -537,10 +552,33 @@ extern "C" int vc_backward_fc(const float* ew_in, int64_t M, int R, int n_out,
                                  EpStoreBias{nullptr, ew_out, n_in}, nullptr,
                                  vec_ok({ew_in, W}, {n_out, n_in}), st);
   LoadRelaxRow la{ew_in, n_out, R, relu_lo, relu_hi, alpha, beta, bias, alpha_per_row, relax_out,
-                  ew_bcast};
+                  ew_bcast, alpha_group};
   const bool vec = vec_ok({ew_in, relu_lo, relu_hi, alpha, beta, W}, {n_out, n_in});
   return launch_gemm<1, true>(1, M, n_in, n_out, la, LoadW{W, n_in},
                               EpStoreBias{nullptr, ew_out, n_in}, acc, vec, st);
+}
+
+}  // namespace
+
+extern "C" int vc_backward_fc(const float* ew_in, int64_t M, int R, int n_out,
+                              const float* relu_lo, const float* relu_hi,
+                              const float* alpha, int alpha_per_row, const float* beta,
+                              const float* W, const float* bias, int n_in, float* ew_out,
+                              float* acc, float* relax_out, int ew_bcast,
+                              vc_stream_t stream) {
+  return backward_fc(ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, nullptr, beta,
+                     W, bias, n_in, ew_out, acc, relax_out, ew_bcast, stream);
+}
+
+extern "C" int vc_backward_fc_grouped(const float* ew_in, int64_t M, int R, int n_out,
+                                      const float* relu_lo, const float* relu_hi,
+                                      const float* alpha_groups, const int64_t* group,
+                                      const float* W, const float* bias, int n_in,
+                                      float* ew_out, float* acc, float* relax_out, int ew_bcast,
+                                      vc_stream_t stream) {
+  if (!relu_lo || !alpha_groups || !group) return VC_ERR_ARG;
+  return backward_fc(ew_in, M, R, n_out, relu_lo, relu_hi, alpha_groups, 0, group, nullptr, W,
+                     bias, n_in, ew_out, acc, relax_out, ew_bcast, stream);
 }
 
 extern "C" int vc_alpha_grad_step(const float* gE, const float* P, int64_t M, int R, int n,

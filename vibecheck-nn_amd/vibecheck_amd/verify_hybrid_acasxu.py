@@ -25,9 +25,11 @@ HIP library (the shared backward and gradient sweep with per-row alpha,
 vc_bound_tighten, vc_best_sum, vc_best_rows_with_A, vc_adam_step); torch
 holds the device memory.  Differences from the reference, by design:
   - the replay bounds every leaf of a batch in one call, each leaf with the
-    alphas of its own group gathered into per-leaf rows (the reference calls
-    the replay once per group; the leaves' computations are independent, so
-    the bounds are the same);
+    alphas of its own group: the backward reads the frozen layer alphas
+    through the leaf's group index, and the spec alphas (which Adam then
+    moves per leaf) are gathered into per-leaf rows (the reference calls the
+    replay once per group; the leaves' computations are independent, so the
+    bounds are the same);
   - the replay's last iteration computes no gradient and takes no Adam
     step (neither reaches a returned value);
   - the early stop reads the sum of the running best accumulated in fp64
@@ -39,6 +41,8 @@ holds the device memory.  Differences from the reference, by design:
   - a box whose widest width is zero cannot be bisected: the driver
     answers 'unknown' there (the reference would bisect it into copies of
     itself until the timeout, also ending 'unknown').
+The alpha gradient sweep covers fc/ReLU chains (the ACAS-Xu networks this
+path is for); other graphs raise NotImplementedError.
 """
 import time
 
@@ -201,20 +205,33 @@ def _full_freeze(xl, xh, gg, spec_ew, device, dtype, n_iters_per_layer=100,
 
 
 def _replay_batched(xl_b, xh_b, gg, spec_ew, alpha_layer_b, alpha_spec_b,
-                    device, dtype, spec_iters=10, spec_lr=0.1, return_tight=False):
+                    device, dtype, spec_iters=10, spec_lr=0.1, return_tight=False,
+                    group=None):
     """Zonotope bounds, frozen-alpha layer tightening, per-leaf spec alpha
     Adam (verify_hybrid_acasxu.py:260-318).
 
     ``alpha_layer_b`` {L: {k: (1 or B, 2 n_L, n_k)}}, ``alpha_spec_b``
     {L: (1 or B, Q, n_L)}: one group's alphas (leading 1, expanded over the
-    batch) or per-leaf alphas (leading B).  Returns (best (B, Q), best_A
-    (B, Q, n_in)); ``return_tight`` (extension) also returns the tightened
-    layer bounds.
+    batch) or per-leaf alphas (leading B).  ``group`` (extension, (B,)
+    int64): the alphas hold G groups (leading G) and leaf b takes those of
+    group[b]; the layer alphas are then read in place by the backward
+    (vc_backward_fc_grouped), without per-leaf copies.  Returns (best (B, Q),
+    best_A (B, Q, n_in)); ``return_tight`` (extension) also returns the
+    tightened layer bounds.
     """
     vz._check_dtype(dtype)
     xl, xh = f32(xl_b).contiguous(), f32(xh_b).contiguous()
     B, n_in = xl.shape
     dev = xl.device
+    if group is not None:
+        group = group.to(device=dev, dtype=torch.int64).contiguous()
+        G = next(iter(alpha_spec_b.values())).shape[0]
+        if group.shape != (B,):
+            raise ValueError('vibecheck_amd: group must hold one index per leaf')
+        if B > 0 and not (0 <= int(group.min()) and int(group.max()) < G):
+            raise ValueError(f'vibecheck_amd: group index outside [0, {G})')
+        alpha_spec_b = {k: _gather(f32(a).reshape(G, -1), group).view(B, *a.shape[1:])
+                        for k, a in alpha_spec_b.items()}
     tight = _zono_tight(xl, xh, gg, device, dtype)
     feeds = _relu_feeds(gg)
     for L in sorted(tight):
@@ -222,7 +239,10 @@ def _replay_batched(xl_b, xh_b, gg, spec_ew, alpha_layer_b, alpha_spec_b,
             continue
         n = tight[L][0].shape[1]
         Wq, bq = _bound_rows(n, dev)
-        alpha = {k: _per_leaf(a, B) for k, a in alpha_layer_b[L].items()}
+        if group is not None:
+            alpha = {k: (f32(a).contiguous(), group) for k, a in alpha_layer_b[L].items()}
+        else:
+            alpha = {k: _per_leaf(a, B) for k, a in alpha_layer_b[L].items()}
         sl = vz._alpha_backward_and_grad(tight, xl, xh, gg, Wq, bq, alpha, False, None,
                                          seed_name=feeds[L])
         _tighten_layer(tight, L, sl)
@@ -340,10 +360,9 @@ def verify_hybrid(gg, spec, settings=None, timeout=120.0, init_leaves=32, batch=
         take = min(cur_batch, N)
         bxl, bxh, bgid = (t[N - take:].contiguous() for t in (wl_xl, wl_xh, wl_gid))
         try:
-            a_layer, a_spec = _gather_alphas(alpha_layer, alpha_spec, bgid)
-            best, _ = _replay_batched(bxl, bxh, gg, spec_ew, a_layer, a_spec, dev, dtype,
-                                      spec_iters=spec_iters, spec_lr=spec_lr)
-            del a_layer, a_spec
+            best, _ = _replay_batched(bxl, bxh, gg, spec_ew, alpha_layer, alpha_spec, dev,
+                                      dtype, spec_iters=spec_iters, spec_lr=spec_lr,
+                                      group=bgid)
         except torch.cuda.OutOfMemoryError:
             if cur_batch <= 8:
                 return {'verdict': 'unknown', 'time': time.perf_counter() - t_start,

@@ -266,9 +266,10 @@ class _Rows:
     ``ew`` is (R, n) when ``shared`` (identical for every domain, before the
     first per-domain relaxation) else (B*R, n).  ``relu`` names a relu layer
     whose relaxation is still to be applied (it is fused into the next fc).
-    ``alpha``/``beta`` belong to that pending relu.
+    ``alpha``/``beta`` belong to that pending relu; ``alpha_group`` (B,)
+    int64 makes ``alpha`` (G*R, n) the rows of each domain's group.
     """
-    __slots__ = ('ew', 'shared', 'relu', 'alpha', 'alpha_row', 'beta')
+    __slots__ = ('ew', 'shared', 'relu', 'alpha', 'alpha_row', 'beta', 'alpha_group')
 
     def __init__(self, ew, shared):
         self.ew = ew
@@ -277,6 +278,7 @@ class _Rows:
         self.alpha = None
         self.alpha_row = 0
         self.beta = None
+        self.alpha_group = None
 
 
 class BackwardTrace:
@@ -326,6 +328,9 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
         """Apply a pending relu relaxation with the standalone kernel."""
         if rows.relu is None:
             return rows
+        if rows.alpha_group is not None:
+            raise NotImplementedError(
+                'vibecheck_amd: group-indexed alpha is supported before an fc only')
         L = rows.relu
         lo, hi = tight[L]
         lo, hi = f32(lo), f32(hi)
@@ -365,10 +370,19 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
                 # step (relaxation streamed through HBM, then a plain GEMM)
                 rel = (torch.empty(M, p['n_out'], device=dev)
                        if p['n_out'] >= _TWO_PHASE_MIN_WIDTH else None)
-                call('vc_backward_fc', ptr(rows.ew), M, R, p['n_out'],
-                     ptr(lo), ptr(hi), ptr(rows.alpha), rows.alpha_row,
-                     ptr(rows.beta), ptr(p['W']), ptr(p['b']), p['n_in'],
-                     ptr(out), ptr(acc), ptr(rel), 1 if rows.shared else 0, st)
+                if rows.alpha_group is not None:
+                    if rows.beta is not None:
+                        raise NotImplementedError(
+                            'vibecheck_amd: group-indexed alpha takes no beta')
+                    call('vc_backward_fc_grouped', ptr(rows.ew), M, R, p['n_out'],
+                         ptr(lo), ptr(hi), ptr(rows.alpha), ptr(rows.alpha_group),
+                         ptr(p['W']), ptr(p['b']), p['n_in'], ptr(out), ptr(acc),
+                         ptr(rel), 1 if rows.shared else 0, st)
+                else:
+                    call('vc_backward_fc', ptr(rows.ew), M, R, p['n_out'],
+                         ptr(lo), ptr(hi), ptr(rows.alpha), rows.alpha_row,
+                         ptr(rows.beta), ptr(p['W']), ptr(p['b']), p['n_in'],
+                         ptr(out), ptr(acc), ptr(rel), 1 if rows.shared else 0, st)
                 del rel
                 ew_at[inp] = _Rows(out, False)
             else:
@@ -388,8 +402,18 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
                 L = op['layer_idx']
                 rows.relu = L
                 if alpha_at_layer is not None and L in alpha_at_layer:
-                    a = f32(alpha_at_layer[L])
-                    if a.dim() == 3:
+                    a = alpha_at_layer[L]
+                    if isinstance(a, tuple):
+                        # (alpha of each group (G, R, n), group of each domain (B,))
+                        rows.alpha = f32(a[0]).reshape(-1, a[0].shape[-1])
+                        rows.alpha_row = 0
+                        rows.alpha_group = a[1]
+                        a = None
+                    else:
+                        a = f32(a)
+                    if a is None:
+                        pass
+                    elif a.dim() == 3:
                         rows.alpha = a.reshape(B * R, -1)
                         rows.alpha_row = 1
                     else:
