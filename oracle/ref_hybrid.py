@@ -148,3 +148,86 @@ def replay_batched(xl, xh, gg, spec_ew, alpha_layer_b, alpha_spec_b, spec_iters=
             for a in alpha.values():
                 a.clamp_(0.0, 1.0)
     return best, best_A, tight
+
+
+def verify_hybrid(gg, spec, init_leaves=32, batch=4096, freeze_iters=100, spec_iters=10,
+                  spec_lr=0.1, max_rounds=None):
+    """verify_hybrid_acasxu.py:321-527 without its PGD phases (the
+    reference's ``disable_sat_finding``) and without the timeout: fan-out by
+    widest-dimension bisection to ``init_leaves`` boxes, one freeze, then a
+    LIFO worklist of (box, group) popped ``batch`` at a time, each popped
+    batch bounded by one replay per group, closed where the worst disjunct's
+    best bound is > 0, every open leaf bisected on its widest dimension
+    (children low then high, in pop order).  ``max_rounds`` (extension)
+    stops early with 'unknown'.  Returns {'verdict', 'evaluated', 'closed',
+    'bab_iters'}."""
+    dt = torch.float32
+    n_out = next(int(op['W'].shape[0]) for op in reversed(gg['ops']) if op['type'] == 'fc')
+    queries = spec.as_linear_queries(n_out)
+    spec_ew = {qi: (torch.as_tensor(w, dtype=dt).flatten(), float(b))
+               for qi, (di, w, b) in enumerate(queries)}
+    disj = {}
+    for qi, (di, _, _) in enumerate(queries):
+        disj.setdefault(di, []).append(qi)
+
+    def worst(best):
+        return torch.stack([best[:, sorted(q)].max(dim=1).values for q in disj.values()],
+                           dim=1).min(dim=1).values
+
+    def bisect(xl, xh):
+        d = int((xh - xl).argmax())
+        mid = float((xl[d] + xh[d]) / 2)
+        a_xh = xh.clone()
+        a_xh[d] = mid
+        b_xl = xl.clone()
+        b_xl[d] = mid
+        return (xl, a_xh), (b_xl, xh)
+
+    boxes = [(torch.as_tensor(spec.x_lo, dtype=dt).flatten(),
+              torch.as_tensor(spec.x_hi, dtype=dt).flatten())]
+    while len(boxes) < init_leaves:
+        new = []
+        for xl, xh in boxes:
+            new.extend(bisect(xl, xh))
+            if len(new) >= init_leaves:
+                break
+        boxes = new
+    boxes = boxes[:init_leaves]
+    xl0 = torch.stack([b[0] for b in boxes])
+    xh0 = torch.stack([b[1] for b in boxes])
+    _, a_layer, a_spec, best = full_freeze(xl0, xh0, gg, spec_ew, freeze_iters, freeze_iters)
+    w = worst(best)
+    work = [(xl0[i], xh0[i], i) for i in range(len(boxes)) if float(w[i]) <= 0]
+    evaluated = len(boxes)
+    closed = len(boxes) - len(work)
+    rounds = 0
+    while work:
+        if max_rounds is not None and rounds >= max_rounds:
+            return {'verdict': 'unknown', 'evaluated': evaluated, 'closed': closed,
+                    'bab_iters': rounds}
+        take = min(batch, len(work))
+        popped = work[-take:]
+        del work[-take:]
+        best = torch.empty(take, len(spec_ew), dtype=dt)
+        groups = {}
+        for j, (_, _, gid) in enumerate(popped):
+            groups.setdefault(gid, []).append(j)
+        for gid, idx in groups.items():
+            layer = {L: {k: a[gid:gid + 1] for k, a in d.items()} for L, d in a_layer.items()}
+            spec_a = {L: a[gid:gid + 1] for L, a in a_spec.items()}
+            b, _, _ = replay_batched(torch.stack([popped[j][0] for j in idx]),
+                                     torch.stack([popped[j][1] for j in idx]), gg, spec_ew,
+                                     layer, spec_a, spec_iters, spec_lr)
+            best[idx] = b
+        evaluated += take
+        w = worst(best)
+        for j in range(take):
+            if float(w[j]) > 0:
+                closed += 1
+                continue
+            xl, xh, gid = popped[j]
+            lo_c, hi_c = bisect(xl, xh)
+            work.append((lo_c[0], lo_c[1], gid))
+            work.append((hi_c[0], hi_c[1], gid))
+        rounds += 1
+    return {'verdict': 'unsat', 'evaluated': evaluated, 'closed': closed, 'bab_iters': rounds}

@@ -222,6 +222,11 @@ def test_hybrid_driver_acasxu_known_answers(gpu):
     res = vh.verify_hybrid(gg, spec, timeout=60.0)
     print(f'prop_1 hybrid: {res}')
     assert res['verdict'] == 'unsat', res
+    # the oracle's driver on the CPU takes the same leaves: same counts
+    ref = rh.verify_hybrid(onnx_net.load_onnx(NET, dtype=F32), spec)
+    print(f'prop_1 oracle hybrid: {ref}')
+    assert (res['evaluated'], res['closed'], res['bab_iters']) == \
+        (ref['evaluated'], ref['closed'], ref['bab_iters'])
     spec = vnnlib.load_vnnlib(os.path.join(GOLD, 'prop_2.vnnlib'))
     res = vh.verify_hybrid(gg, spec, timeout=8.0, settings={'hybrid_freeze_iters': 20})
     print(f'prop_2 hybrid: {res}')

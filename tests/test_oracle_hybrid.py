@@ -158,3 +158,22 @@ def test_replay_spec_iterations_only_improve():
     bq = _t([se[q][1] for q in sorted(se)])
     vals = (y @ Wq.T + bq).reshape(B, N, -1)
     assert bool((b10 <= vals.min(dim=1).values + 1e-9).all())
+
+
+def test_oracle_hybrid_driver_acasxu_prop1_unsat():
+    """Known answer of the reference's bundled example: prop_1 of its
+    ACAS-Xu network is unsat (README), and the hybrid driver proves it."""
+    import os
+    from vibecheck_amd import onnx_net, vnnlib
+    from test_formats import GOLD, NET
+    gg = onnx_net.load_onnx(NET, dtype=torch.float32)
+    spec = vnnlib.load_vnnlib(os.path.join(GOLD, 'prop_1.vnnlib'))
+    res = rh.verify_hybrid(gg, spec)
+    print(res)
+    assert res['verdict'] == 'unsat'
+    # the o init leaves the freeze left open are evaluated twice (freeze and
+    # replay); every replayed leaf is closed or split into two replayed
+    # children: closed = 32 + splits, evaluated = 32 + o + 2 splits
+    o = res['evaluated'] - 32 - 2 * (res['closed'] - 32)
+    assert 0 <= o <= 32, res
+    assert res['bab_iters'] >= 1
