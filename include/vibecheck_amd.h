@@ -246,12 +246,15 @@ int vc_alpha_grad_step_slopes(const float *gE, const float *P, int64_t M,
 
 /* vc_alpha_grad_step with one alpha per backward row (the per-query alpha
  * of the hybrid freeze / replay verifier, verify_hybrid_acasxu.py:164-318):
- * alpha_rows (M, n), row m's lower slope active + unstable * alpha_rows[m]. */
+ * alpha_rows (M, n), row m's lower slope active + unstable * alpha_rows[m].
+ * galpha_rows (M, n), if not NULL, also receives d lb / d alpha_rows (what
+ * vc_alpha_grad_rows computes), from the same loads. */
 int vc_alpha_grad_step_rows(const float *gE, const float *P, int64_t M, int R,
                             int n, const float *relu_lo, const float *relu_hi,
                             const float *alpha_rows, int p_bcast,
                             const float *W_next, const float *bias_next,
-                            int n_next, float *g_out, vc_stream_t stream);
+                            int n_next, float *g_out, float *galpha_rows,
+                            vc_stream_t stream);
 
 /* d lb / d alpha with one alpha per row: galpha (M, n)[m, j] = gE[m, j] *
  * pos(P[m, j]) where neuron j of row m's domain (m / R) is unstable, else 0

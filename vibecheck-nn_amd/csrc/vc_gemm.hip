@@ -155,15 +155,17 @@ struct LoadGradRelax {
   const float *lo, *hi, *alpha;
   int p_bcast;    // P shared by all domains: row m reads P[m % R]
   int alpha_row;  // alpha (M, ld), one per row (per-query alpha), else (B, ld)
+  float* galpha_rows = nullptr;  // d lb / d alpha per row (M, ld), written by column tile 0
   struct Row {
     int64_t mo, po, dom;
+    bool go;  // this tile writes galpha_rows
   };
   struct Raw {
     float ge[4], pv[4], lo[4], hi[4], a[4];
   };
-  __device__ Row row(int64_t, int64_t m, bool) const {
+  __device__ Row row(int64_t, int64_t m, bool first) const {
     const int64_t d = m / R;
-    return Row{m * ld, (p_bcast ? m - d * R : m) * ld, d * ld};
+    return Row{m * ld, (p_bcast ? m - d * R : m) * ld, d * ld, first && galpha_rows != nullptr};
   }
   template <bool VEC>
   __device__ void fetch(const Row& rw, int k, int n, Raw& x) const {
@@ -183,6 +185,7 @@ struct LoadGradRelax {
         Relax s = relax(x.lo[j], x.hi[j]);
         float ls = s.lo_s;
         if (alpha) ls = s.active ? 1.f : (s.unstable ? x.a[j] : 0.f);
+        if (rw.go) galpha_rows[rw.mo + k + j] = s.unstable ? x.ge[j] * fmaxf(x.pv[j], 0.f) : 0.f;
         const bool mp = x.pv[j] >= 0.f, mn = x.pv[j] <= 0.f;
         const float f = (mp ? ls : 0.f) + (mn ? s.up_s : 0.f);
         gp = x.ge[j] * f;
@@ -600,12 +603,13 @@ extern "C" int vc_alpha_grad_step_rows(const float* gE, const float* P, int64_t 
                                        const float* relu_lo, const float* relu_hi,
                                        const float* alpha_rows, int p_bcast,
                                        const float* W_next, const float* bias_next, int n_next,
-                                       float* g_out, vc_stream_t stream) {
+                                       float* g_out, float* galpha_rows,
+                                       vc_stream_t stream) {
   if (!gE || !P || !relu_lo || !relu_hi || !alpha_rows || !g_out || R <= 0 || n <= 0 || M < 0)
     return VC_ERR_ARG;
   if (M % R != 0) return VC_ERR_ARG;
   if (!W_next) return VC_ERR_UNSUPPORTED;
-  LoadGradRelax la{gE, P, n, R, relu_lo, relu_hi, alpha_rows, p_bcast, 1};
+  LoadGradRelax la{gE, P, n, R, relu_lo, relu_hi, alpha_rows, p_bcast, 1, galpha_rows};
   const bool vec = vec_ok({gE, P, relu_lo, relu_hi, alpha_rows, W_next}, {n});
   return launch_gemm<1, false>(1, M, n_next, n, la, LoadWt{W_next, n},
                                EpStoreBias{bias_next, g_out, n_next}, nullptr, vec,

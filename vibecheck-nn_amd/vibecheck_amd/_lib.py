@@ -65,7 +65,7 @@ SIGNATURES = {
     'vc_split_multi': [_P, _P, _P, _P, _L, _I, _I, _P, _P, _P],
     'vc_alpha_band_keys': [_P, _L, _I, _P, _P, _I, _P, _F, _P, _P, _P],
     'vc_rank_select_desc': [_P, _P, _L, _L, _P, _P],
-    'vc_alpha_grad_step_rows': [_P, _P, _L, _I, _I, _P, _P, _P, _I, _P, _P, _I, _P, _P],
+    'vc_alpha_grad_step_rows': [_P, _P, _L, _I, _I, _P, _P, _P, _I, _P, _P, _I, _P, _P, _P],
     'vc_alpha_grad_rows': [_P, _P, _I, _L, _I, _I, _P, _P, _P, _P],
     'vc_bound_tighten': [_P, _P, _P, _L, _I, _P],
     'vc_best_sum': [_P, _P, _L, _I, _P, _P],

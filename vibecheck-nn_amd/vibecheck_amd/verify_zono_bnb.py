@@ -660,9 +660,13 @@ def _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, want_grad, galpha,
         ga = galpha.get(L) if galpha is not None else None
         gb = gbeta.get(L) if gbeta is not None else None
         if per_row and ga is not None:
-            call('vc_alpha_grad_rows', ptr(g), ptr(P), 1 if p_shared else 0, M, Q, n,
-                 ptr(lo), ptr(hi), ptr(ga), st)
+            if i == 0:  # above the input: no gradient step to fuse it into
+                call('vc_alpha_grad_rows', ptr(g), ptr(P), 1 if p_shared else 0, M, Q, n,
+                     ptr(lo), ptr(hi), ptr(ga), st)
+            ga_rows = ga
             ga = None
+        else:
+            ga_rows = None
         if ga is not None or gb is not None:
             call('vc_alpha_grad_reduce', ptr(g), ptr(P), 1 if p_shared else 0,
                  B, Q, n, ptr(lo), ptr(hi), ptr(ga), ptr(gb), st)
@@ -671,7 +675,7 @@ def _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, want_grad, galpha,
             g2 = torch.empty(M, fn['n_out'], device=dev)
             call('vc_alpha_grad_step_rows', ptr(g), ptr(P), M, Q, n, ptr(lo), ptr(hi),
                  ptr(a.reshape(M, n)), 1 if p_shared else 0, ptr(fn['W']), ptr(fn['b']),
-                 fn['n_out'], ptr(g2), st)
+                 fn['n_out'], ptr(g2), ptr(ga_rows), st)
             g = g2
         elif i > 0:
             fn = _op_params(fcs[i], dev)
