@@ -44,7 +44,7 @@ struct LoadMidRad {  // A = (mid, rad) of an interval row-block
 // (+ beta); row part en * up_t (+ e * bias[k]); lo_s from the alpha
 // override when given (active -> 1, unstable -> alpha, dead -> 0).
 struct LoadRelaxRow {
-  static constexpr int kBK = 16;
+  static constexpr int kBK = 16;  // 32 measured slower at every shape (more live registers)
   const float* ew;
   int ld;  // n_out
   int R;
