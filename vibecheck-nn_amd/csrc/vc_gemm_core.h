@@ -297,7 +297,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(int64_t M, int N, int K, int t
 
 constexpr int64_t kMaxGrid = 1 << 20;  // workgroups; tiles beyond loop (a multiple of 8)
 
-constexpr int64_t kFewTiles = 512;  // two 64x64 tiles per CU
+constexpr int64_t kFewTiles = 512;  // two 64x64 tiles per CU (2048 measured: mixed, mostly slower)
 
 // Loaders opt into 32-row tiles for M <= 32 with a static kSmallM = true.
 template <class T, class = void>
