@@ -149,7 +149,9 @@ def _tighten_layer(tight, L, sl):
 
 
 def _zono_tight(xl, xh, gg, device, dtype):
-    sb, _ = vz._forward_zonotope_graph_batched(xl, xh, gg, device, dtype)
+    """Zonotope pre-activation bounds, writable copies: only the bounds are
+    needed, so narrow MLPs take the bounds-only whole-network kernel."""
+    sb = vz._zono_sb(gg, xl, xh, device, dtype)
     return {L: (f32(lo).clone(), f32(hi).clone()) for L, (lo, hi) in sb.items()}
 
 
