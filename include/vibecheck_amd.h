@@ -526,7 +526,10 @@ int vc_mlp_alpha_iter(const int32_t *dims, int n_relu, const float *frag_bwd,
  * biases carried by the MFMA in both directions.  init != 0 (the first
  * iteration): alpha starts at (up_s > 0.5) * unstable and the Adam state at
  * zero, whatever the arrays hold.  ctl (nullable): the loop state of
- * vc_alpha_control; the call does nothing once it says stopped.
+ * vc_alpha_control; the call does nothing once it says stopped.  grad
+ * (nullable; else per-layer (B, dims[l+1]) device arrays): the iteration's
+ * d(sum_q lb_q)/d alpha, the gradient its Adam step took with the opposite
+ * sign (torch minimises -sum lb), 0 off the unstable set.
  * Replaces one iteration of _run_alpha_crown_inputsplit_batched
  * (verify_zono_bnb.py:5248-5266). */
 int vc_mlp_tiled_alpha_iter(const int32_t *dims, int n_relu, const float *frag,
@@ -534,7 +537,7 @@ int vc_mlp_tiled_alpha_iter(const int32_t *dims, int n_relu, const float *frag,
                             const float *xh, const float *const *lo,
                             const float *const *hi, float *const *alpha,
                             float *const *exp_avg, float *const *exp_avg_sq,
-                            int Q, const float *spec_rows,
+                            float *const *grad, int Q, const float *spec_rows,
                             const float *spec_acc, float *lb_out, double b1,
                             double b2, double eps, double step_size,
                             double bc2_sqrt, int init, const float *ctl,
@@ -584,6 +587,14 @@ int vc_clip_box(const float *xl, const float *xh, const float *A,
                 const float *b, int64_t B, int Q, int n, const int32_t *d_ptr,
                 const int32_t *q_idx, int n_disj, float *xl_out,
                 float *xh_out, uint8_t *feasible, vc_stream_t stream);
+
+/* flag[0] = 1 if the new boxes are tighter anywhere than the old ones
+ * (xl_new > xl_old or xh_new < xh_old over the n entries), else 0: the stop
+ * test of the clip loop, `((xl_new > xl_c) | (xh_new < xh_c)).any()`
+ * (verify_graph.py:13036-13081, stop test at 13078). */
+int vc_box_shrunk(const float *xl_old, const float *xh_old,
+                  const float *xl_new, const float *xh_new, int64_t n,
+                  int32_t *flag, vc_stream_t stream);
 
 /* Ascending stream compaction: idx_out[0..count) = positions of non-zero
  * flags (of zero flags when select_zero != 0); count_out[0] = count.

@@ -74,6 +74,20 @@ def clip_leaves(xl, xh, A, b, disj_q_idx):
     return xl_n, xh_n, feas
 
 
+def clip_iterated(xl, xh, A, b, disj_q_idx, clip_iters=1):
+    """The clip loop (verify_graph.py:13036-13081): clip_leaves with the same
+    halfspaces until no box of the batch shrinks, at most clip_iters times;
+    the feasibility is the last iteration's."""
+    xl_c, xh_c, feas = xl, xh, None
+    for _ in range(max(1, int(clip_iters))):
+        xl_n, xh_n, feas = clip_leaves(xl_c, xh_c, A, b, disj_q_idx)
+        shrunk = bool(((xl_n > xl_c) | (xh_n < xh_c)).any())
+        xl_c, xh_c = xl_n, xh_n
+        if not shrunk:
+            break
+    return xl_c, xh_c, feas
+
+
 def widest_axis(xl, xh):
     """First index of the maximum width (verify_graph.py:13291)."""
     return (xh - xl).argmax(dim=1)
@@ -249,9 +263,11 @@ def alpha_on_leaves(lb, xl, xh, gg, spec_ew, disj_q_idx, closed,
 def bab_step(xl, xh, gg, spec_ew, disj_q_idx, crown_intermediate=True,
              clip_enabled=True, alpha_iters=0, alpha_all=False, alpha_eps=0.0,
              alpha_max_leaves=200, alpha_lr=0.25, alpha_lr_decay=0.98,
-             branch_sb=False, sb_margin=False, sb_thr=0.01, sb_mw=1.0, split_depth=1):
+             branch_sb=False, sb_margin=False, sb_thr=0.01, sb_mw=1.0, split_depth=1,
+             clip_iters=1):
     """One BaB iteration on a popped batch: bound, closure, optional
-    alpha-CROWN, one clip iteration, split (verify_graph.py:12855-13423).
+    alpha-CROWN, the clip (repeated while a box shrinks, at most
+    ``clip_iters`` times), split (verify_graph.py:12855-13423).
 
     The split dimension is the widest, or with ``branch_sb`` (and a clip,
     which gives the input linearization A) the best SB score of the
@@ -259,25 +275,28 @@ def bab_step(xl, xh, gg, spec_ew, disj_q_idx, crown_intermediate=True,
     only) splits every leaf on its top K dimensions at once.
 
     Returns a dict with lb, closed, unclosed (indices), feasible (after
-    clip, over unclosed), xl_split/xh_split, ax, n_degenerate, the
+    clip, over unclosed), xl_split/xh_split, ax, n_degenerate, crown_lb /
+    crown_closed (the bound and closure before alpha-CROWN), the
     children as ``chunks`` (the worklist pushes, in order) and, for
     bisection, low/high.
     """
     lb, A, acc = bound_batch(xl, xh, gg, spec_ew, crown_intermediate,
                              clip_enabled)
     closed = closure(lb, disj_q_idx)
+    crown_lb, crown_closed = lb, closed
     lb, closed, n_al, n_ait = alpha_on_leaves(
         lb, xl, xh, gg, spec_ew, disj_q_idx, closed, alpha_iters, alpha_all,
         alpha_eps, alpha_max_leaves, alpha_lr, alpha_lr_decay)
     unclosed = (~closed).nonzero(as_tuple=True)[0]
     out = {'lb': lb, 'A': A, 'acc': acc, 'closed': closed,
            'unclosed': unclosed, 'n_alpha_leaves': n_al,
-           'n_alpha_iters': n_ait}
+           'n_alpha_iters': n_ait, 'crown_lb': crown_lb,
+           'crown_closed': crown_closed}
     A_s = None
     if clip_enabled and unclosed.numel() > 0 and A is not None:
         xl_u, xh_u = xl[unclosed], xh[unclosed]
-        xl_c, xh_c, feas = clip_leaves(xl_u, xh_u, A[unclosed],
-                                       acc[unclosed], disj_q_idx)
+        xl_c, xh_c, feas = clip_iterated(xl_u, xh_u, A[unclosed], acc[unclosed],
+                                         disj_q_idx, clip_iters)
         fidx = feas.nonzero(as_tuple=True)[0]
         out['feasible'] = feas
         xl_s, xh_s = xl_c[fidx], xh_c[fidx]

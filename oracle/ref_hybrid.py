@@ -55,7 +55,9 @@ def _adam_loop(params, evaluate, n_iters, lr, lr_decay, early_stop_eps, trace=No
         sl = evaluate()
         with torch.no_grad():
             best = sl.detach().clone() if best is None else torch.maximum(best, sl.detach())
-            cur = float(best.double().sum().item())
+            # fp32, torch's own sum, as the reference reads it
+            # (verify_hybrid_acasxu.py:210, 246)
+            cur = float(best.sum().item())
         (-sl.sum()).backward()
         opt.step()
         with torch.no_grad():

@@ -53,3 +53,20 @@ def rel_err_ok(a, b, rtol=1e-5, atol=1e-6):
     a = a.detach().double().cpu()
     b = b.detach().double().cpu()
     return (a - b).abs() <= atol + rtol * b.abs()
+
+
+def clip_tolerance(A, acc, xl, xh, rtol=1e-5, atol=1e-6):
+    """Per (row, dimension) tolerance of a clipped box coordinate: the clip
+    threshold (-b_q - sum_{j != i} A_qj x_j) / A_qi carries the rounding of
+    its numerator, atol + rtol (|b_q| + sum_j |A_qj| max(|xl_j|, |xh_j|)),
+    divided by |A_qi|; the largest over the halfspaces that can cut
+    dimension i (|A_qi| > 1e-12), capped by the box width, plus the plain
+    tolerance of the coordinate.  A (R, Q, n), acc (R, Q), xl, xh (R, n):
+    the rows' halfspaces and unclipped boxes."""
+    A, acc, xl, xh = (t.detach().double().cpu() for t in (A, acc, xl, xh))
+    xm = torch.maximum(xl.abs(), xh.abs())
+    scale = acc.abs() + (A.abs() * xm.unsqueeze(1)).sum(-1)
+    cut = A.abs() > 1e-12
+    per = torch.where(cut, (atol + rtol * scale).unsqueeze(-1) / A.abs().clamp(min=1e-30),
+                      torch.zeros_like(A))
+    return torch.minimum(per.amax(1), xh - xl) + atol + rtol * xm

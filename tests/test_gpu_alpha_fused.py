@@ -1,0 +1,203 @@
+"""The fused alpha-CROWN kernels of the bench path (k_alpha_quad for batches
+of at most 4 x CUs domains, k_alpha_tiled above) held to the oracle one
+iteration at a time.
+
+Each iteration is teacher-forced: the kernel starts from the oracle's own
+alpha and torch.optim.Adam state (exp_avg, exp_avg_sq) at that iteration
+and runs one iteration through the C ABI (vc_mlp_tiled_alpha_iter):
+  - its spec bound lb against the oracle's lb of the same alpha
+    (|gpu - ref32| <= 1e-6 + 1e-5 |ref32|; entries that pass only relative
+    to their concretization scale, or only by being at least as close to the
+    fp64 oracle, are counted and bounded);
+  - its gradient d(sum lb)/d alpha against fp64 autograd of the same state;
+  - its Adam update against torch.optim.Adam applied to the kernel's own
+    gradient from the same state, followed by the clamp to [0, 1]
+    (verify_zono_bnb.py:5248-5287): within 4 ulps (see N_ULP), with the
+    count of entries that differ at all printed.
+The oracle then takes its own step, and the next iteration starts from it.
+"""
+import ctypes
+
+import pytest
+import torch
+
+from oracle import ref_bound as rb
+from vibecheck_amd import _lib
+from vibecheck_amd import mlp_fused as mf
+from vibecheck_amd import verify_zono_bnb as vz
+from vibecheck_amd import workloads as wk
+from vibecheck_amd._lib import call, host_array, ptr, stream
+
+import _util
+
+pytestmark = pytest.mark.gpu
+F32 = torch.float32
+B1, B2, EPS = 0.9, 0.999, 1e-8
+LR, DECAY = 0.1, 0.98
+# torch's CPU Adam rounds differently on different host CPUs (its vectorised
+# kernels are chosen per instruction set): on one host the kernel matches it
+# bit for bit, on another an update differs by 3 ulps.  The bar is 4 ulps;
+# the test prints how many entries differ at all.
+N_ULP = 4
+
+
+def _spec_scale(A, acc, xl, xh):
+    xm = torch.maximum(xl.double().abs(), xh.double().abs())
+    return acc.double().abs() + (A.double().abs() * xm.unsqueeze(1)).sum(-1)
+
+
+def _bounds_with_counts(got, ref, ref64, scale, rtol=1e-5, atol=1e-6):
+    """Entries outside |gpu - ref| <= atol + rtol |ref| that pass relative to
+    their scale, or by being at least as close to fp64 as the oracle; the
+    counts of both kinds, and the number failing everything."""
+    g = got.detach().double().cpu()
+    r = ref.detach().double()
+    ok = (g - r).abs() <= atol + rtol * r.abs()
+    by_scale = ~ok & ((g - r).abs() <= atol + rtol * torch.maximum(r.abs(), scale))
+    ok2 = ok | by_scale
+    by64 = ~ok2 & ((g - ref64).abs() <= (r - ref64).abs())
+    bad = ~(ok2 | by64)
+    return int(by_scale.sum()), int(by64.sum()), int(bad.sum())
+
+
+def _ulps(got, ref, old):
+    """|got - ref| in fp32 ulps of the larger of |ref| and |old| (an update
+    that cancels most of the old value keeps the absolute rounding of its
+    terms)."""
+    mag = torch.maximum(ref.abs(), old.abs())
+    ulp = torch.nextafter(mag, torch.tensor(float('inf'))) - mag
+    return ((got - ref).abs() / ulp.clamp(min=float(torch.finfo(torch.float32).tiny)))
+
+
+@pytest.mark.parametrize('B', [384, 2048])
+def test_fused_alpha_step_map_teacher_forced(gpu, B):
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    kernel = 'k_alpha_quad' if B <= 4 * n_cu else 'k_alpha_tiled'
+    print(f'B={B}: {kernel}', flush=True)
+    gg_c = wk.acas_gg(dtype=F32)
+    gg_g = wk.acas_gg(device=gpu, dtype=F32)
+    xl, xh = wk.acas_boxes(B, seed=21, dtype=F32)
+    c, r = (xl + xh) / 2, (xh - xl) / 2
+    xl, xh = c - 4 * r, c + 4 * r            # wider boxes: many unstable neurons
+    spec, _ = _util.spec_for(5, dtype=F32)
+    with torch.no_grad():
+        sb, _ = rb.zono_forward_batched(xl, xh, gg_c)
+    Ls = sorted(sb)
+    alpha = {}
+    for L in Ls:
+        _, up_s, _, _, _, un = rb.make_slopes(*sb[L])
+        alpha[L] = ((up_s > 0.5).to(F32) * un.to(F32)).requires_grad_(True)
+    opt = torch.optim.Adam([alpha[L] for L in Ls], lr=LR)
+    n_un = sum(int(rb.make_slopes(*sb[L])[5].sum()) for L in Ls)
+    assert n_un > 10 * B, n_un
+
+    plan = mf.plan_for(gg_g, gpu)
+    assert plan is not None and plan.tfrag is not None
+    se_g = {q: (w.to(gpu), b) for q, (w, b) in spec.items()}
+    Wq, bq = vz._spec_rows(se_g, gpu)
+    S, acc0 = mf.fold_spec(plan, Wq, bq)
+    Q = S.shape[0]
+    xl_g, xh_g = xl.to(gpu), xh.to(gpu)
+    lo_g = [sb[L][0].to(gpu).contiguous() for L in Ls]
+    hi_g = [sb[L][1].to(gpu).contiguous() for L in Ls]
+    gg64 = _util.to_dev(gg_c, 'cpu', torch.float64)
+    sb64 = {L: (lo.double(), hi.double()) for L, (lo, hi) in sb.items()}
+    spec64 = {q: (w.double(), b) for q, (w, b) in spec.items()}
+    lr_t = LR
+    totals = [0, 0]
+    hist = {}
+    for it in range(6):
+        step = it + 1
+        # the oracle's state before this iteration
+        a0 = {L: alpha[L].detach().clone() for L in Ls}
+        st = opt.state
+        m0 = {L: (st[alpha[L]]['exp_avg'].clone() if alpha[L] in st
+                  else torch.zeros_like(a0[L])) for L in Ls}
+        v0 = {L: (st[alpha[L]]['exp_avg_sq'].clone() if alpha[L] in st
+                  else torch.zeros_like(a0[L])) for L in Ls}
+        # one kernel iteration from that state (the first from its own init)
+        ag = [a0[L].to(gpu).contiguous() for L in Ls]
+        mg = [m0[L].to(gpu).contiguous() for L in Ls]
+        vg_ = [v0[L].to(gpu).contiguous() for L in Ls]
+        gg_out = [torch.full_like(t, float('nan')) for t in ag]
+        lb_g = torch.empty(B, Q, device=gpu)
+        keep = [host_array(ctypes.c_void_p, [ptr(t) for t in ts])
+                for ts in (lo_g, hi_g, ag, mg, vg_, gg_out)]
+        call('vc_mlp_tiled_alpha_iter', plan.dims_p, plan.n, ptr(plan.tfrag),
+             ptr(plan.bias_cat), B, ptr(xl_g), ptr(xh_g), *[k[1] for k in keep], Q, ptr(S),
+             ptr(acc0), ptr(lb_g), B1, B2, EPS, lr_t / (1 - B1 ** step),
+             (1 - B2 ** step) ** 0.5, 1 if it == 0 else 0, None, stream())
+        torch.cuda.synchronize()
+        # the oracle's bound and gradient of the same state
+        opt.zero_grad()
+        lb, A, acc = rb.spec_backward_batched(sb, xl, xh, gg_c, spec, alpha_at_layer=alpha,
+                                              return_input_linear=True)
+        (-lb.sum()).backward()
+        a64 = {L: a0[L].double().requires_grad_(True) for L in Ls}
+        lb64 = rb.spec_backward_batched(sb64, xl.double(), xh.double(), gg64, spec64,
+                                        alpha_at_layer=a64)
+        lb64.sum().backward()
+        n_sc, n_64, n_bad = _bounds_with_counts(lb_g, lb.detach(), lb64.detach(),
+                                                _spec_scale(A.detach(), acc.detach(), xl, xh))
+        print(f'it {it}: lb escapes: {n_sc} by scale, {n_64} by fp64, {n_bad} outside',
+              flush=True)
+        assert n_bad == 0, (it, n_bad)
+        totals[0] += n_sc
+        totals[1] += n_64
+        # gradient against fp64 autograd: within 1e-5 of the layer's largest
+        for k, L in enumerate(Ls):
+            g = gg_out[k].cpu()
+            assert not bool(torch.isnan(g).any()), (it, L)
+            r64 = a64[L].grad
+            scale = float(r64.abs().max().clamp(min=1e-30))
+            err = float((g.double() - r64).abs().max()) / scale
+            assert err < 1e-5, (it, L, err)
+            # stable neurons carry no gradient
+            un = rb.make_slopes(*sb[L])[5]
+            assert bool((g[~un] == 0).all()), (it, L)
+        # torch.optim.Adam on the kernel's gradient, from the same state
+        for k, L in enumerate(Ls):
+            p = a0[L].clone().requires_grad_(True)
+            o2 = torch.optim.Adam([p], lr=lr_t)
+            if it > 0:
+                o2.state[p] = {'step': torch.tensor(float(it)), 'exp_avg': m0[L].clone(),
+                               'exp_avg_sq': v0[L].clone()}
+            p.grad = -gg_out[k].cpu()
+            o2.step()
+            with torch.no_grad():
+                p.clamp_(0.0, 1.0)
+            m_ref, v_ref = o2.state[p]['exp_avg'], o2.state[p]['exp_avg_sq']
+            for what, got, ref, old in (('alpha', ag[k], p.detach(), a0[L]),
+                                        ('exp_avg', mg[k], m_ref, m0[L]),
+                                        ('exp_avg_sq', vg_[k], v_ref, v0[L])):
+                u = _ulps(got.cpu(), ref, old)
+                for b in (0, 1, 2, 4):
+                    hist[(what, b)] = hist.get((what, b), 0) + int((u > b).sum())
+                hist[(what, 'n')] = hist.get((what, 'n'), 0) + u.numel()
+                ok = u <= N_ULP
+                if not bool(ok.all()):
+                    bad = (~ok).nonzero(as_tuple=True)
+                    rows = [(float(got.cpu()[i]), float(ref[i]), float(old[i]), float(m0[L][i]),
+                             float(v0[L][i]), float(gg_out[k].cpu()[i]), float(mg[k].cpu()[i]),
+                             float(m_ref[i]), float(vg_[k].cpu()[i]), float(v_ref[i]))
+                            for i in zip(*bad)][:4]
+                    raise AssertionError(f'{(it, L, what)}: {int((~ok).sum())} beyond {N_ULP} ulps; '
+                                         f'(got, ref, old, m0, v0, g, m_gpu, m_ref, v_gpu, '
+                                         f'v_ref): {rows}')
+        # the oracle's own step; the next iteration starts from it
+        opt.step()
+        with torch.no_grad():
+            for L in Ls:
+                alpha[L].clamp_(0.0, 1.0)
+        lr_t *= DECAY
+        for gpar in opt.param_groups:
+            gpar['lr'] *= DECAY
+    for what in ('alpha', 'exp_avg', 'exp_avg_sq'):
+        n = hist[(what, 'n')]
+        print(f'{what}: of {n} entries, {hist[(what, 0)]} differ from torch, '
+              f'{hist[(what, 1)]} by more than 1 ulp, {hist[(what, 2)]} by more than 2, '
+              f'{hist[(what, 4)]} by more than 4')
+    # escapes stay rare: at most 0.1% of the checked bounds
+    n_checked = 6 * B * Q
+    print(f'{kernel}: {totals[0]} scale escapes, {totals[1]} fp64 escapes of {n_checked}')
+    assert totals[0] + totals[1] <= n_checked // 1000, totals

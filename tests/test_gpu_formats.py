@@ -11,7 +11,9 @@ import os
 import pytest
 import torch
 
+from oracle import ref_bab as rbab
 from vibecheck_amd import onnx_net, vnnlib
+from vibecheck_amd.spec import dedup_queries
 from vibecheck_amd import verify_graph as vg
 from vibecheck_amd import verify_zono_bnb as vz
 
@@ -25,11 +27,22 @@ SETTINGS = {'total_timeout': 60.0, 'input_split_batch_size': 4096,
 
 
 def test_acasxu_prop1_verified(gpu):
+    """prop_1 verified, popping the same leaves as the oracle's driver on the
+    CPU: the same leaf and iteration counts."""
     gg = onnx_net.load_onnx(NET, device=gpu, dtype=F32)
     spec = vnnlib.load_vnnlib(os.path.join(GOLD, 'prop_1.vnnlib'))
     verdict, details = vg._input_split_batched(None, spec, SETTINGS, gg, gpu, F32)
     print(f'prop_1: {verdict} {details}')
     assert verdict == 'verified', details
+    uq, dq = dedup_queries(spec.as_linear_queries(5))
+    se = {i: (torch.tensor(w, dtype=F32), b) for i, (w, b) in enumerate(uq)}
+    v_r, d_r, _ = rbab.input_split_batched(
+        torch.tensor(spec.x_lo, dtype=F32), torch.tensor(spec.x_hi, dtype=F32),
+        onnx_net.load_onnx(NET, dtype=F32), se, dq, batch_size=4096,
+        crown_intermediate=True, clip_enabled=True)
+    assert v_r == 'verified'
+    assert (details['batched_n_leaves'], details['batched_n_iters']) == \
+        (d_r['batched_n_leaves'], d_r['batched_n_iters']), (details, d_r)
 
 
 def test_acasxu_prop2_never_verified_and_witness_forward(gpu):

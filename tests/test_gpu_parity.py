@@ -380,6 +380,13 @@ def test_zono_parity_acas(gpu):
     assert gG.shape == rG.shape
     assert_bounds(gc, rc, 'zono centre')
     assert_bounds(gG.abs().sum(-1), rG.abs().sum(-1), 'zono radius')
+    # the generator matrix element by element: the input generators, then per
+    # ReLU one column per unstable neuron in rank order, zero-padded to the
+    # batch maximum (verify_zono_bnb.py:3190-3210); each entry against the
+    # radius of its row
+    rad = rG.abs().sum(-1, keepdim=True).double().expand_as(rG)
+    assert_bounds(gG, rG, 'zono generators', scale=rad)
+    assert torch.equal(cpu(gG) == 0, rG == 0)
 
 
 # ----------------------------------------------------------------- a5-a8

@@ -125,9 +125,83 @@ def test_worklist_lifo_chunks():
     assert not wl
 
 
-def test_compaction_ascending():
-    closed = torch.tensor([True, False, False, True, False])
-    assert (~closed).nonzero(as_tuple=True)[0].tolist() == [1, 2, 4]
+def test_step_compaction_order_and_clipped_rows():
+    """bab_step's leaf bookkeeping against a per-leaf brute force on a C0
+    batch: ``unclosed`` lists exactly the open leaves in ascending order,
+    ``feasible`` and the split rows follow that order (each row the clip of
+    its own leaf alone), and the low/high children pair up row by row.  A
+    descending or closed-leaf compaction, or a clip over the wrong rows,
+    fails here."""
+    gg = wk.acas_gg(dtype=DT)
+    xl, xh = wk.acas_boxes(48, seed=4, dtype=DT)
+    c, r = (xl + xh) / 2, (xh - xl) / 2
+    xl, xh = c - 6 * r, c + 6 * r                 # wide enough to leave some open
+    spec_ew, dq = _util.spec_for(5)
+    st = rbab.bab_step(xl, xh, gg, spec_ew, dq)
+    closed = st['closed']
+    want = [i for i in range(48) if not bool(closed[i])]
+    assert 0 < len(want) < 48
+    assert st['unclosed'].tolist() == want
+    rows_l, rows_h, feas = [], [], []
+    for i in want:
+        l1, h1, f1 = rbab.clip_box_by_halfspaces_batched(
+            xl[i:i + 1], xh[i:i + 1], st['A'][i:i + 1], st['acc'][i:i + 1])
+        feas.append(bool(f1[0]))
+        if f1[0]:
+            rows_l.append(l1[0])
+            rows_h.append(h1[0])
+    assert st['feasible'].tolist() == feas
+    assert torch.equal(st['xl_split'], torch.stack(rows_l))
+    assert torch.equal(st['xh_split'], torch.stack(rows_h))
+    (lxl, lxh), (hxl, hxh) = st['low'], st['high']
+    assert torch.equal(lxl, st['xl_split']) and torch.equal(hxh, st['xh_split'])
+    for k in range(lxl.shape[0]):
+        a = int(st['ax'][k])
+        assert lxh[k, a] == hxl[k, a]
+
+
+def test_band_select_hand_computed():
+    """Boundary-band alpha leaves (verify_graph.py:12938-12950): worst
+    disjunct's best bound > -eps, unclosed only, best first, ties in leaf
+    order, truncated to max_leaves."""
+    lb = _t([[-0.1, -0.3, -0.2],     # d0 -0.1, d1 -0.2 -> worst -0.2
+             [-0.6, -0.7, 0.1],      # worst -0.6: outside the band
+             [-0.4, -0.05, -0.2],    # d0 -0.05, d1 -0.2 -> -0.2 (tie with leaf 0)
+             [0.3, -1.0, -0.01],     # d0 0.3, d1 -0.01 -> -0.01 (best)
+             [0.2, 0.1, 0.3],        # closed
+             [-0.45, -0.5, -0.3],    # -0.45
+             [-0.5, -0.9, -0.5]])    # exactly -eps: outside (strict)
+    dq = {0: [0, 1], 1: [2]}
+    closed = rbab.closure(lb, dq)
+    assert closed.tolist() == [False, False, False, False, True, False, False]
+    assert rbab.band_select(lb, closed, dq, 0.5, 200).tolist() == [3, 0, 2, 5]
+    assert rbab.band_select(lb, closed, dq, 0.5, 3).tolist() == [3, 0, 2]
+    assert rbab.band_select(lb, closed, dq, 0.5, 2).tolist() == [3, 0]
+    assert rbab.band_select(lb, closed, dq, 0.7, 200).tolist() == [3, 0, 2, 5, 6, 1]
+    assert rbab.band_select(lb, closed, dq, 0.005, 200).tolist() == []
+
+
+def test_clip_loop_repeats_until_nothing_shrinks():
+    """x0 - x1 <= 0 and x1 - 0.3 <= 0 on [0, 1]^2: the first clip gives
+    x1 <= 0.3 but keeps x0 <= 1; the second, on the smaller box, gives
+    x0 <= 0.3; the third changes nothing and ends the loop
+    (verify_graph.py:13036-13081)."""
+    xl, xh = _t([[0.0, 0.0]]), _t([[1.0, 1.0]])
+    A = _t([[[1.0, -1.0], [0.0, 1.0]]])
+    b = _t([[0.0, -0.3]])
+    dq = {0: [0, 1]}
+    l1, h1, f1 = rbab.clip_iterated(xl, xh, A, b, dq, 1)
+    torch.testing.assert_close(h1, _t([[1.0, 0.3]]))
+    l2, h2, f2 = rbab.clip_iterated(xl, xh, A, b, dq, 2)
+    torch.testing.assert_close(h2, _t([[0.3, 0.3]]))
+    l9, h9, f9 = rbab.clip_iterated(xl, xh, A, b, dq, 9)
+    torch.testing.assert_close(h9, _t([[0.3, 0.3]]))
+    assert bool(f1[0] and f2[0] and f9[0])
+    torch.testing.assert_close(l9, xl)
+    # an emptied box stays infeasible on later iterations
+    b_e = _t([[0.0, 0.1]])                      # x1 <= -0.1: empty on x1 >= 0
+    _, _, fe = rbab.clip_iterated(xl, xh, A, b_e, dq, 5)
+    assert not bool(fe[0])
 
 
 def test_spec_queries_and_dedup():
@@ -166,17 +240,54 @@ def test_bab_step_sound_split_of_unclosed_only():
     assert bool((lxh >= lxl).all() and (hxh >= hxl).all())
 
 
-def test_input_split_driver_closes_small_problem():
-    gg = wk.acas_gg(dtype=torch.float32)
-    spec = wk.acas_spec([0.1, 0.1, 0.1, 0.1, 0.1], [0.14, 0.14, 0.14, 0.14, 0.14])
-    uq, dq = dedup_queries(spec.as_linear_queries(5))
-    spec_ew = {i: (torch.tensor(w, dtype=torch.float32), b) for i, (w, b) in enumerate(uq)}
-    xl0 = torch.tensor(spec.x_lo, dtype=torch.float32)
-    xh0 = torch.tensor(spec.x_hi, dtype=torch.float32)
-    verdict, det, trace = rbab.input_split_batched(xl0, xh0, gg, spec_ew, dq,
-                                                   max_iters=30)
-    assert verdict in ('verified', 'unknown')
-    assert det['batched_n_iters'] == len(trace) >= 1
+def test_input_split_driver_known_answers():
+    """The oracle's driver on the reference's bundled ACAS-Xu example
+    (README.md:42-80): prop_1 is unsat -- verified, here after 253 leaves in
+    11 iterations (the counts the GPU driver must reproduce); prop_2 is
+    violated and is never verified; a box around a point where the spec
+    holds strictly closes at the root."""
+    import os
+    from vibecheck_amd import onnx_net, vnnlib
+    from test_formats import GOLD, NET
+    gg = onnx_net.load_onnx(NET, dtype=torch.float32)
+
+    def run(spec, **kw):
+        uq, dq = dedup_queries(spec.as_linear_queries(5))
+        se = {i: (torch.tensor(w, dtype=torch.float32), b) for i, (w, b) in enumerate(uq)}
+        return rbab.input_split_batched(torch.tensor(spec.x_lo, dtype=torch.float32),
+                                        torch.tensor(spec.x_hi, dtype=torch.float32), gg,
+                                        se, dq, **kw)
+    p1 = vnnlib.load_vnnlib(os.path.join(GOLD, 'prop_1.vnnlib'))
+    verdict, det, trace = run(p1)
+    assert verdict == 'verified', det
+    assert (det['batched_n_leaves'], det['batched_n_iters']) == (253, 11), det
+    assert sum(t['B'] for t in trace) == 253 and trace[0]['B'] == 1
+    # every popped leaf is closed or split: children = 2 (B - closed)
+    assert all(t['n_children'] == 2 * (t['B'] - t['n_closed']) for t in trace)
+    p2 = vnnlib.load_vnnlib(os.path.join(GOLD, 'prop_2.vnnlib'))
+    verdict, det, _ = run(p2, max_iters=12)
+    assert verdict == 'unknown', det
+    # a tiny box around a point whose spec margin (the largest query value,
+    # one disjunct: any query > 0 closes) is clearly positive closes at the
+    # root
+    gg64 = wk.acas_gg(dtype=DT)
+    gg32 = wk.acas_gg(dtype=torch.float32)
+    se64, _ = _util.spec_for(5)
+    Wq = torch.stack([se64[q][0] for q in sorted(se64)])
+    g = torch.Generator().manual_seed(11)
+    pts = torch.rand(400, 5, generator=g, dtype=DT) * 2 - 1
+    margins = torch.stack([(Wq @ rb.point_forward(p, gg64)[0].reshape(-1)).max() for p in pts])
+    for k, want in ((int(margins.argmax()), 'verified'),):
+        assert float(margins[k]) > 1e-2, float(margins[k])
+        spec = wk.acas_spec((pts[k] - 1e-4).tolist(), (pts[k] + 1e-4).tolist())
+        uq, dq = dedup_queries(spec.as_linear_queries(5))
+        se = {i: (torch.tensor(w, dtype=torch.float32), b) for i, (w, b) in enumerate(uq)}
+        v, det, _ = rbab.input_split_batched(torch.tensor(spec.x_lo, dtype=torch.float32),
+                                             torch.tensor(spec.x_hi, dtype=torch.float32),
+                                             gg32, se, dq, max_iters=6)
+        assert v == want, (float(margins[k]), det)
+        if want == 'verified':
+            assert det['batched_n_iters'] == 1 and det['batched_n_leaves'] == 1
 
 
 # ----------------------------------------------------------- SB and K > 1

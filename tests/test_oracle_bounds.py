@@ -185,6 +185,30 @@ def test_zono_hand_computed_two_dims():
     torch.testing.assert_close(sb[1][1], _t([[8.0 / 3.0]]))
 
 
+def test_zono_generator_layout_rank_and_padding():
+    """The new generator columns of a ReLU (verify_zono_bnb.py:3190-3210):
+    one per unstable neuron, in neuron order (the cumulative-count rank),
+    padded with zero columns to the batch's largest unstable count.
+    z = [x, x + 0.5, x - 0.5]; domain 0: x in [-1, 1], all three unstable;
+    domain 1: x in [-0.1, 0.3], only neuron 0 unstable (1 active, 2 dead).
+    An identity fc after the ReLU keeps G as the ReLU leaves it."""
+    gg = _chain([[[1.0], [1.0], [1.0]], [[1.0, 0.0, 0.0], [0.0, 1.0, 0.0], [0.0, 0.0, 1.0]]],
+                [[0.0, 0.5, -0.5], [0.0, 0.0, 0.0]])
+    _, (c, G) = rb.zono_forward_batched(_t([[-1.0], [-0.1]]), _t([[1.0], [0.3]]), gg)
+    assert G.shape == (2, 3, 4)
+    # domain 0: lam = (1/2, 3/4, 1/4), mu = (1/4, 3/16, 3/16)
+    torch.testing.assert_close(c[0], _t([0.25, 0.5625, 0.0625]))
+    torch.testing.assert_close(G[0], _t([[0.5, 0.25, 0.0, 0.0],
+                                         [0.75, 0.0, 0.1875, 0.0],
+                                         [0.25, 0.0, 0.0, 0.1875]]))
+    # domain 1: centre 0.1, radius 0.2; neuron 0 on [-0.1, 0.3]: lam = 3/4,
+    # mu = 0.0375 in column 0 of the new block, columns 1 and 2 padding
+    torch.testing.assert_close(c[1], _t([0.1125, 0.6, 0.0]))
+    torch.testing.assert_close(G[1], _t([[0.15, 0.0375, 0.0, 0.0],
+                                         [0.2, 0.0, 0.0, 0.0],
+                                         [0.0, 0.0, 0.0, 0.0]]))
+
+
 def test_zono_contains_samples_and_matches_ibp_at_first_layer():
     gg = wk.acas_gg(dtype=DT)
     xl, xh = wk.acas_boxes(16, seed=5, dtype=DT)

@@ -984,6 +984,23 @@ __global__ void k_widest(const float* xl, const float* xh, int64_t B, int n, int
   }
 }
 
+// One workgroup: flag[0] = 1 if any entry of the new box is tighter than the
+// old one (xl_new > xl_old or xh_new < xh_old), else 0.  The workgroup owns the
+// whole flag, so nothing has to be cleared before the launch.
+__global__ __launch_bounds__(1024) void k_box_shrunk(const float* xl_o, const float* xh_o,
+                                                     const float* xl_n, const float* xh_n,
+                                                     int64_t n, int32_t* flag) {
+  __shared__ int any;
+  if (threadIdx.x == 0) any = 0;
+  __syncthreads();
+  int mine = 0;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x)
+    mine |= (xl_n[i] > xl_o[i]) | (xh_n[i] < xh_o[i]);
+  if (__any(mine) && (threadIdx.x & 63) == 0) any = 1;
+  __syncthreads();
+  if (threadIdx.x == 0) flag[0] = any;
+}
+
 __global__ void k_bisect(const float* xl, const float* xh, const int64_t* ax,
                          const int64_t* uidx, int64_t nu, int n, float* lxl, float* lxh,
                          float* hxl, float* hxh) {
@@ -1389,6 +1406,17 @@ extern "C" int vc_widest_axis(const float* xl, const float* xh, int64_t B, int n
   if (B == 0) return VC_OK;
   hipLaunchKernelGGL(k_widest, dim3(vc_blocks(B, NT)), dim3(NT), 0, (hipStream_t)stream, xl,
                      xh, B, n, ax, usable);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_box_shrunk(const float* xl_old, const float* xh_old, const float* xl_new,
+                             const float* xh_new, int64_t n, int32_t* flag,
+                             vc_stream_t stream) {
+  if (!flag || n < 0 || (n > 0 && (!xl_old || !xh_old || !xl_new || !xh_new)))
+    return VC_ERR_ARG;
+  hipLaunchKernelGGL(k_box_shrunk, dim3(1), dim3(1024), 0, (hipStream_t)stream, xl_old, xh_old,
+                     xl_new, xh_new, n, flag);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }

@@ -44,7 +44,9 @@ __global__ void k_bound_tighten(float* lo, float* hi, const float* sl, int64_t B
   }
 }
 
-// best = max(best, lb) (a copy when init), out[0] = sum of best in fp64.
+// best = max(best, lb) (a copy when init), out[0] = the sum of best, accumulated
+// in fp64 and rounded once to fp32: the correctly rounded value of the fp32
+// sum the reference's early stop reads (verify_hybrid_acasxu.py:210, 246).
 __global__ __launch_bounds__(1024) void k_best_sum(float* best, const float* lb, int64_t n,
                                                    int init, double* out) {
   __shared__ double part[16];
@@ -60,7 +62,7 @@ __global__ __launch_bounds__(1024) void k_best_sum(float* best, const float* lb,
   if (threadIdx.x == 0) {
     double t = 0.0;
     for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += part[w];
-    *out = t;
+    *out = (double)(float)t;
   }
 }
 

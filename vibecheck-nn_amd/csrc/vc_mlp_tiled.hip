@@ -645,6 +645,7 @@ struct TAlphaArgs {
   float* alpha[MAXL];
   float* m1[MAXL];
   float* m2[MAXL];
+  float* grad[MAXL];  // nullable: d(sum lb)/d alpha of the iteration (0 off the unstable set)
 };
 
 // Set element j (runtime, < 16 MT) of a D-layout block to v in the lanes of
@@ -772,7 +773,7 @@ __device__ __forceinline__ double alpha_pass(const TGeom& G, const AlphaLds& w, 
                                              const float4* frh, const float* sbias, int Q,
                                              const float* spec_rows, const float* spec_acc,
                                              const AdamConst& adam, bool keep_ls, int lane,
-                                             int g, int r) {
+                                             int g, int r, const TAlphaArgs& aa, int64_t dom) {
   const int n = G.n, d0 = G.d[0], dN = G.d[n];
   const bool live = r < Q;
   float* ssl = w.ssl;
@@ -872,7 +873,8 @@ __device__ __forceinline__ double alpha_pass(const TGeom& G, const AlphaLds& w, 
     {
       float* sa = sad + l * 3 * FW;
       const int j = lane;
-      if (j < dW && sl[3 * FW + j] != 0.f) {
+      const bool un = j < dW && sl[3 * FW + j] != 0.f;
+      if (un) {
         float mi = sa[FW + j], vi = sa[2 * FW + j];
         float pa = adam_update(sa[j], -sga[j], mi, vi, adam);
         pa = fminf(fmaxf(pa, 0.f), 1.f);
@@ -881,6 +883,7 @@ __device__ __forceinline__ double alpha_pass(const TGeom& G, const AlphaLds& w, 
         sa[j] = pa;
         if (keep_ls) sl[j] = pa;  // unstable: ls_eff = alpha
       }
+      if (aa.grad[l] && j < dW) aa.grad[l][dom * dW + j] = un ? sga[j] : 0.f;
     }
     __threadfence_block();
     if (l + 1 < n) {
@@ -939,7 +942,7 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
     alpha_load<KS>(G, aa, xl, xh, dom, init, w, lane);
     __threadfence_block();
     const double lbd = alpha_pass<MT, KS, BROW>(G, w, fr0, frh, sbias, Q, spec_rows, spec_acc,
-                                                adam, false, lane, g, r);
+                                                adam, false, lane, g, r, aa, dom);
     if (g == 0 && r < Q) lb_out[dom * Q + r] = (float)lbd;
     alpha_store(G, aa, dom, w, lane);
     __threadfence_block();
@@ -1188,7 +1191,8 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
       if (has && lane < 16) {
         float* sa = sad + l * 3 * FW;
         const int j = 16 * w + lane;
-        if (j < dW && sl[3 * FW + j] != 0.f) {
+        const bool un = j < dW && sl[3 * FW + j] != 0.f;
+        if (un) {
           float mi = sa[FW + j], vi = sa[2 * FW + j];
           float pa = adam_update(sa[j], -sga[j], mi, vi, adam);
           pa = fminf(fmaxf(pa, 0.f), 1.f);
@@ -1197,6 +1201,8 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
           sa[j] = pa;
           sl[j] = pa;  // unstable: the next iteration's lower slope is alpha
         }
+        // the last iteration of the launch leaves its gradient
+        if (aa.grad[l] && j < dW && t_it == ac.n - 1) aa.grad[l][dom * dW + j] = un ? sga[j] : 0.f;
       }
       if (l + 1 < n) {
         // with the bias row, a constant 1 at index d_{l+1} picks up b_{l+1}
@@ -1879,7 +1885,7 @@ struct AlphaLaunch {
 int alpha_prepare(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
                   int64_t B, const float* xl, const float* xh, const float* const* lo,
                   const float* const* hi, float* const* alpha, float* const* exp_avg,
-                  float* const* exp_avg_sq, int Q, const float* spec_rows,
+                  float* const* exp_avg_sq, float* const* grad, int Q, const float* spec_rows,
                   const float* spec_acc, const float* lb_out, AlphaLaunch& L) {
   TGeom& G = L.G;
   int rc = tiled_geom(dims, n_relu, G);
@@ -1895,8 +1901,10 @@ int alpha_prepare(const int32_t* dims, int n_relu, const float* frag, const floa
     L.aa.alpha[l] = in ? alpha[l] : nullptr;
     L.aa.m1[l] = in ? exp_avg[l] : nullptr;
     L.aa.m2[l] = in ? exp_avg_sq[l] : nullptr;
+    L.aa.grad[l] = (in && grad) ? grad[l] : nullptr;
     if (in && (!L.aa.lo[l] || !L.aa.hi[l] || !L.aa.alpha[l] || !L.aa.m1[l] || !L.aa.m2[l]))
       return VC_ERR_ARG;
+    if (in && grad && !L.aa.grad[l]) return VC_ERR_ARG;
   }
   const size_t fixed = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float);
   // small batches: every domain in flight at once, MT wavefronts each
@@ -1981,14 +1989,14 @@ extern "C" int vc_mlp_tiled_alpha_iter(const int32_t* dims, int n_relu, const fl
                                        const float* bias_cat, int64_t B, const float* xl,
                                        const float* xh, const float* const* lo,
                                        const float* const* hi, float* const* alpha,
-                                       float* const* exp_avg, float* const* exp_avg_sq, int Q,
-                                       const float* spec_rows, const float* spec_acc,
-                                       float* lb_out, double b1, double b2, double eps,
-                                       double step_size, double bc2_sqrt, int init,
+                                       float* const* exp_avg, float* const* exp_avg_sq,
+                                       float* const* grad, int Q, const float* spec_rows,
+                                       const float* spec_acc, float* lb_out, double b1, double b2,
+                                       double eps, double step_size, double bc2_sqrt, int init,
                                        const float* ctl, vc_stream_t stream) {
   AlphaLaunch L;
   int rc = alpha_prepare(dims, n_relu, frag, bias_cat, B, xl, xh, lo, hi, alpha, exp_avg,
-                         exp_avg_sq, Q, spec_rows, spec_acc, lb_out, L);
+                         exp_avg_sq, grad, Q, spec_rows, spec_acc, lb_out, L);
   if (rc != VC_OK) return rc;
   if (B == 0) return VC_OK;
   AdamChunk ac;
@@ -2023,7 +2031,7 @@ extern "C" int vc_mlp_tiled_alpha_run(const int32_t* dims, int n_relu, const flo
   if (B < 0) return VC_ERR_ARG;
   AlphaLaunch L;
   int rc = alpha_prepare(dims, n_relu, frag, bias_cat, B, xl, xh, lo, hi, alpha, exp_avg,
-                         exp_avg_sq, Q, spec_rows, spec_acc, lb_out, L);
+                         exp_avg_sq, nullptr, Q, spec_rows, spec_acc, lb_out, L);
   if (rc != VC_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(k_alpha_ctl_init, dim3(1), dim3(64), 0, st, ctl);

@@ -58,6 +58,7 @@ SIGNATURES = {
     'vc_split_beta_sign': [_P, _P, _L, _P, _P],
     'vc_split_clamps': [_P, _P, _P, _L, _I, _L, _I, _P, _P, _P, _P],
     'vc_best_update': [_P, _P, _L, _I, _P, _P],
+    'vc_box_shrunk': [_P, _P, _P, _P, _L, _P, _P],
     'vc_closure': [_P, _L, _I, _P, _P, _I, _P, _P],
     'vc_clip_box': [_P, _P, _P, _P, _L, _I, _I, _P, _P, _I, _P, _P, _P, _P],
     'vc_branch_topk': [_P, _P, _P, _P, _L, _I, _I, _I, _F, _F, _I, _P, _P, _P],
@@ -86,7 +87,7 @@ SIGNATURES = {
     'vc_mlp_tiled_pack': [_P, _P, _P, _I, _P, _P],
     'vc_mlp_tiled_crown': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I,
                            _I, _P, _P, _P, _P, _P, _P, _P, _P],
-    'vc_mlp_tiled_alpha_iter': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
+    'vc_mlp_tiled_alpha_iter': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _I,
                                 _P, _P, _P, _D, _D, _D, _D, _D, _I, _P, _P],
     'vc_mlp_tiled_alpha_run': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
                                _P, _P, _P, _P, _D, _D, _D, _D, _D, _I, _D, _P, _P, _P],

@@ -6,8 +6,9 @@ names and signatures (verify_graph.py of the reference).
 zonotope intermediate bounds, domain clipping, batched alpha-CROWN on
 unclosed leaves, widest-dimension bisection.  Closure, clipping,
 compaction, branching and bisection run as HIP kernels; the worklist is a
-LIFO list of device-resident 2-D chunks.  Root/leaf PGD, SB branching and
-LP/MILP escalation are not part of this engine.
+LIFO list of device-resident 2-D chunks.  SB branching and 2^K-way splits
+are supported; root/leaf PGD and LP/MILP escalation are not part of this
+engine.
 """
 import ctypes
 import time
@@ -123,6 +124,27 @@ def _clip(xl, xh, A, b, table):
              ptr(b.contiguous()), B, Q, n, ptr(table.d_ptr), ptr(table.q_idx),
              table.n, ptr(xl_o), ptr(xh_o), ptr(feas), stream())
     return xl_o, xh_o, feas
+
+
+def _clip_iterated(xl, xh, A, b, table, clip_iters):
+    """Clip until no box shrinks, at most clip_iters times, with the same
+    halfspaces (verify_graph.py:13036-13081): the stop test is over the
+    whole batch (one host read per iteration, as the reference's
+    ``.any().item()``); feasibility is the last iteration's."""
+    xl_c, xh_c = xl, xh
+    feas = None
+    flag = torch.empty(1, dtype=torch.int32, device=xl.device) if clip_iters > 1 else None
+    for it in range(max(1, int(clip_iters))):
+        xl_n, xh_n, feas = _clip(xl_c, xh_c, A, b, table)
+        if it + 1 >= clip_iters:
+            xl_c, xh_c = xl_n, xh_n
+            break
+        call('vc_box_shrunk', ptr(xl_c), ptr(xh_c), ptr(xl_n), ptr(xh_n), xl_c.numel(),
+             ptr(flag), stream())
+        xl_c, xh_c = xl_n, xh_n
+        if int(flag.item()) == 0:
+            break
+    return xl_c, xh_c, feas
 
 
 def _clip_box_by_halfspaces_batched(xl, xh, A, b):
@@ -352,17 +374,19 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
              clip_enabled=True, alpha_iters=0, alpha_all=False, alpha_eps=0.0,
              alpha_max_leaves=200, alpha_lr=0.25, alpha_lr_decay=0.98,
              timers=None, branch_sb=False, sb_margin=False, sb_thr=0.01, sb_mw=1.0,
-             split_depth=1):
+             split_depth=1, clip_iters=1):
     """One BaB iteration on a popped batch (verify_graph.py:12855-13423):
-    bound, closure, optional alpha-CROWN on unclosed leaves, one clip
-    iteration, split.  The split dimension is the widest, or with
+    bound, closure, optional alpha-CROWN on unclosed leaves (opportunistic:
+    a RuntimeError or OOM inside it keeps the bound it had, as at
+    verify_graph.py:12962-12969), the clip (repeated while any box shrinks,
+    at most ``clip_iters`` times), split.  The split dimension is the widest, or with
     ``branch_sb`` (and a clip, which gives the input linearization) the best
     SB score (sum form, or ``sb_margin``); ``split_depth`` K > 1 (SB only)
     splits each leaf on its top K dimensions into 2^K children.  Returns a
     dict of device tensors (same keys as the oracle's bab_step; ``chunks``
     are the worklist pushes in order)."""
     if (NATIVE_ROUND and timers is None and crown_intermediate and clip_enabled
-            and (alpha_iters == 0 or alpha_all) and not branch_sb):
+            and (alpha_iters == 0 or alpha_all) and not branch_sb and clip_iters == 1):
         out = _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr,
                                 alpha_lr_decay)
         if out is not None:
@@ -406,15 +430,23 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
             # the bound phase has already computed: gather their rows
             sb_open = None if sb is None else _gather_layers(sb, open_idx)
             xl_o, xh_o = _gather_many([xl, xh], open_idx)
-            new, n_ait = _run_alpha_crown_inputsplit_batched(
-                xl_o, xh_o, gg, spec_ew,
-                dev, dt, n_iters=alpha_iters, lr=alpha_lr,
-                lr_decay=alpha_lr_decay, sb=sb_open, return_trace=True,
-                lazy_trace=True)
+            try:
+                new, n_ait = _run_alpha_crown_inputsplit_batched(
+                    xl_o, xh_o, gg, spec_ew,
+                    dev, dt, n_iters=alpha_iters, lr=alpha_lr,
+                    lr_decay=alpha_lr_decay, sb=sb_open, return_trace=True,
+                    lazy_trace=True)
+            except RuntimeError:
+                # torch.cuda.OutOfMemoryError and NotImplementedError are
+                # RuntimeErrors: alpha-CROWN only tightens, the step goes on
+                # with the bound it has (verify_graph.py:12962-12969)
+                new = None
+                n_ait = 0
             n_al = int(open_idx.numel())
-            call('vc_scatter_max_rows', ptr(lb), ptr(open_idx),
-                 ptr(new.contiguous()), n_al, lb.shape[1], stream())
-            closed = _closure(lb, table)
+            if new is not None:
+                call('vc_scatter_max_rows', ptr(lb), ptr(open_idx),
+                     ptr(new.contiguous()), n_al, lb.shape[1], stream())
+                closed = _closure(lb, table)
     if timers is not None:
         t1 = sync_t()
         timers['alpha'] = timers.get('alpha', 0.0) + t1 - t0
@@ -428,7 +460,7 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
            'n_alpha_iters': n_ait}
     if clip_enabled and unclosed.numel() > 0 and A is not None:
         xl_u, xh_u, A_u, acc_u, lb_u = _gather_many([xl, xh, A, acc, lb], unclosed)
-        xl_c, xh_c, feas = _clip(xl_u, xh_u, A_u, acc_u, table)
+        xl_c, xh_c, feas = _clip_iterated(xl_u, xh_u, A_u, acc_u, table, clip_iters)
         out['feasible'] = feas
         branch = ((A_u, lb_u, 2 if sb_margin else 1, sb_thr, sb_mw) if branch_sb
                   else None)
@@ -480,7 +512,13 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
     (extension; reference hard-codes 0.25), input_split_batched_max_iters
     (extension: stop after that many iterations), input_split_batched_branch_sb,
     input_split_sb_margin_score, input_split_sb_coeff_thresh,
-    input_split_sb_margin_weight, bab_split_depth.
+    input_split_sb_margin_weight, bab_split_depth, input_split_batched_clip_iters,
+    raise_on_oom.
+
+    A RuntimeError in a step (torch.cuda.OutOfMemoryError included) halves
+    the batch size and pushes the popped batch back; at batch size 1 a real
+    OOM is re-raised (unless raise_on_oom is off) and anything else ends the
+    run 'unknown' / batched_oom (verify_graph.py:12872-12897).
     """
     if dtype != torch.float32:
         raise NotImplementedError('vibecheck_amd computes in fp32 only')
@@ -506,6 +544,7 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
     sb_thr = float(_setting(settings, 'input_split_sb_coeff_thresh', 0.01))
     sb_mw = float(_setting(settings, 'input_split_sb_margin_weight', 1.0))
     split_depth = int(_setting(settings, 'bab_split_depth', 1))
+    clip_iters = int(_setting(settings, 'input_split_batched_clip_iters', 1))
     dev = torch.device(device)
 
     xc = ((torch.as_tensor(spec.x_lo, dtype=dtype, device=dev)
@@ -542,11 +581,16 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
                           alpha_max_leaves=alpha_max_leaves, alpha_lr=alpha_lr,
                           branch_sb=branch_sb, sb_margin=sb_margin,
                           sb_thr=sb_thr, sb_mw=sb_mw,
-                          split_depth=split_depth if B < batch_size else 1)
-        except torch.cuda.OutOfMemoryError:
+                          split_depth=split_depth if B < batch_size else 1,
+                          clip_iters=clip_iters)
+        except RuntimeError as e:
+            # torch.cuda.OutOfMemoryError is a RuntimeError
+            if torch.cuda.is_available():
+                torch.cuda.empty_cache()
             new_bs = max(1, batch_size // 2)
             if new_bs == batch_size:
-                if bool(_setting(settings, 'raise_on_oom', True)):
+                if (isinstance(e, torch.cuda.OutOfMemoryError)
+                        and bool(_setting(settings, 'raise_on_oom', True))):
                     raise
                 return 'unknown', {'phase': 'batched_oom',
                                    'batch_size': batch_size}

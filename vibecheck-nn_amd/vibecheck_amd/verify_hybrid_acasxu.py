@@ -33,8 +33,10 @@ holds the device memory.  Differences from the reference, by design:
   - the replay's last iteration computes no gradient and takes no Adam
     step (neither reaches a returned value);
   - the early stop reads the sum of the running best accumulated in fp64
-    (the reference sums fp32 in torch's order; the two read the same stop
-    unless the improvement lies within the fp32 sum's rounding);
+    and rounded once to fp32 (the reference sums in fp32 in torch's order,
+    which lies within a few fp32 ulps of that value; both see the sum at
+    fp32 resolution, so they stop alike unless an improvement is within
+    those few ulps);
   - the sign-gradient PGD attacks (verify_hybrid_acasxu.py:39-161) are not
     part of this module: ``verify_hybrid`` runs as the reference does with
     ``disable_sat_finding``, so its verdicts are 'unsat' and 'unknown';
