@@ -487,6 +487,29 @@ int vc_mlp_tiled_crown(const int32_t *dims, int n_relu, const float *frag,
                        float *lb_out, float *A_out, float *acc_out,
                        uint64_t *seed_rows, int32_t *queue, vc_stream_t stream);
 
+/* No counterpart in the reference: vc_mlp_tiled_crown for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).  Same arguments, kernels and
+ * results as vc_unstable_union_layers + vc_union_compact +
+ * vc_mlp_tiled_crown (seed_rows off), but the union flags, its index lists
+ * and the domain queue's counter live in a static 8 KiB device array, one
+ * per GPU, held until the process ends; the call allocates nothing.  The
+ * caller passes the inputs and outputs only.  Limit: the ReLU widths may
+ * sum to at most 1024 (VC_ERR_UNSUPPORTED beyond).  Calls that overlap on
+ * one GPU (two host threads, or two streams) share the array and race:
+ * serialise them.  Any batch size B.  The GPU is the one running `stream`
+ * (the current device for the null stream). */
+int vc_mlp_tiled_crown_noalloc(const int32_t *dims, int n_relu,
+                               const float *frag, const float *bias_cat,
+                               int64_t B, const float *xl, const float *xh,
+                               const float *const *lo_in,
+                               const float *const *hi_in,
+                               float *const *lo_out, float *const *hi_out,
+                               int do_crown, int per_domain, int Q,
+                               const float *spec_rows, const float *spec_acc,
+                               float *lb_out, float *A_out, float *acc_out,
+                               vc_stream_t stream);
+
 /* The neurons unstable in any domain, per layer, for the CROWN seeding of
  * _crown_intermediate_batched (verify_zono_bnb.py:4123): flags (sum of
  * widths, uint8) = 1 where some domain has lo < 0 < hi, for n_layers

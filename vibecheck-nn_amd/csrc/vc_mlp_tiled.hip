@@ -1869,6 +1869,95 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
   return VC_OK;
 }
 
+// ------------------------------------------- CROWN without allocation
+// vc_mlp_tiled_crown_noalloc keeps the union of unstable neurons (flags,
+// index lists, counts) and the domain queue's counter in `scratch`, one copy
+// per GPU for the life of the process.  Host code never uses the array's
+// name as an address: each device's address comes from hipGetSymbolAddress
+// with that device current, once, and is kept in g_scratch_dev.
+namespace {
+constexpr int kScratchNeurons = MAXL * FW;                 // union flags and indices
+constexpr size_t kScratchFlags = 0;                        // uint8 [kScratchNeurons]
+constexpr size_t kScratchIdx = kScratchNeurons;            // int32 [kScratchNeurons]
+constexpr size_t kScratchMeta = kScratchIdx + 4 * kScratchNeurons;  // int32 [2 MAXL]
+constexpr size_t kScratchQueue = kScratchMeta + 4 * 2 * MAXL;       // int32 [2]
+constexpr size_t kScratchBytes = 8192;
+static_assert(kScratchQueue + 8 <= kScratchBytes, "scratch layout");
+static_assert(kScratchIdx % 4 == 0 && kScratchMeta % 4 == 0 && kScratchQueue % 4 == 0,
+              "scratch alignment");
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_dev[kMaxDevices] = {};
+
+// The device address of `scratch` on the GPU that runs `stream`, looked up
+// once per device with that device current.
+int scratch_on(hipStream_t stream, unsigned char** out) {
+  int dev = -1;
+  if (stream) {
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess) return VC_ERR_ARG;
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return VC_ERR_LAUNCH;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return VC_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return VC_ERR_LAUNCH;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return VC_ERR_LAUNCH;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev && hipSetDevice(cur) != hipSuccess) return VC_ERR_LAUNCH;
+    if (e != hipSuccess || !p) return VC_ERR_LAUNCH;
+    g_scratch_dev[dev] = static_cast<unsigned char*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return VC_OK;
+}
+}  // namespace
+
+extern "C" int vc_mlp_tiled_crown_noalloc(const int32_t* dims, int n_relu, const float* frag,
+                                          const float* bias_cat, int64_t B, const float* xl,
+                                          const float* xh, const float* const* lo_in,
+                                          const float* const* hi_in, float* const* lo_out,
+                                          float* const* hi_out, int do_crown, int per_domain,
+                                          int Q, const float* spec_rows, const float* spec_acc,
+                                          float* lb_out, float* A_out, float* acc_out,
+                                          vc_stream_t stream) {
+  if (!dims || n_relu < 1 || n_relu > MAXL) return VC_ERR_UNSUPPORTED;
+  int32_t widths[MAXL];
+  int total = 0;
+  for (int l = 0; l < n_relu; ++l) {
+    widths[l] = dims[l + 1];
+    if (widths[l] <= 0) return VC_ERR_ARG;
+    total += widths[l];
+  }
+  // the union lists live in `scratch`: nets beyond its size are refused
+  if (total > kScratchNeurons) return VC_ERR_UNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  unsigned char* sp = nullptr;
+  int rc = scratch_on(st, &sp);
+  if (rc != VC_OK) return rc;
+  uint8_t* flags = sp + kScratchFlags;
+  int32_t* idx = reinterpret_cast<int32_t*>(sp + kScratchIdx);
+  int32_t* meta = reinterpret_cast<int32_t*>(sp + kScratchMeta);
+  int32_t* queue = reinterpret_cast<int32_t*>(sp + kScratchQueue);
+  if (do_crown && B > 0) {
+    // the flags are cleared by a fill kernel inside, the lists written whole
+    rc = vc_unstable_union_layers(lo_in, hi_in, widths, n_relu, B, flags, stream);
+    if (rc != VC_OK) return rc;
+    rc = vc_union_compact(flags, widths, n_relu, idx, meta, stream);
+    if (rc != VC_OK) return rc;
+  }
+  // the queue counter is reset by a kernel before the CROWN launch
+  return vc_mlp_tiled_crown(dims, n_relu, frag, bias_cat, B, xl, xh, lo_in, hi_in, lo_out,
+                            hi_out, do_crown ? idx : nullptr, do_crown ? meta : nullptr,
+                            do_crown, per_domain, Q, spec_rows, spec_acc, lb_out, A_out,
+                            acc_out, nullptr, queue, stream);
+}
+
 namespace {
 // One alpha-CROWN iteration's launch, prepared once per batch: the kernel
 // (4 wavefronts per domain for batches that fit at once, else one), its

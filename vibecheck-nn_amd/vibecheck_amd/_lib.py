@@ -92,6 +92,8 @@ SIGNATURES = {
     'vc_mlp_tiled_alpha_run': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
                                _P, _P, _P, _P, _D, _D, _D, _D, _D, _I, _D, _P, _P, _P],
     'vc_mlp_tiled_crown_mode': [_L],
+    'vc_mlp_tiled_crown_noalloc': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _I, _I, _I,
+                                   _P, _P, _P, _P, _P, _P],
     'vc_unstable_union_layers': [_P, _P, _P, _I, _L, _P, _P],
     'vc_union_compact': [_P, _P, _I, _P, _P, _P],
     'vc_gather_rows_multi': [_P, _P, _P, _I, _P, _L, _P],
