@@ -7,11 +7,22 @@ alpha-CROWN (20 Adam iterations, lr 0.1, decay 0.98) on every unclosed
 leaf, one halfspace clip, widest-dimension bisection; the children are the
 next round's batch.  value = domains bounded / wall time of the step.
 
-Prints one JSON line (rank 0).  Extra keys: roofline (dominant kernel,
-measured with HIP events on the launch stream), cpu_baseline (CPU oracle on
-a bounded sample of the same workload), alpha_iters_per_s, rounds.
+Prints one JSON line.  Extra keys:
+  roofline     the dominant kernel (k_crown_tiled), timed with HIP events on
+               its launch stream inside the timed region; traffic from the
+               committed rocprofv3 counter summary of the same source;
+  secondary    the step's other kernels on the step's own batches, each
+               launch timed alone (zonotope bounds, small-batch CROWN, one
+               alpha iteration at the open leaves and at 65,536 domains);
+  alpha        alpha-CROWN's own iterations/s and domain-iterations/s;
+  rounds       per round: batch, closed, alpha leaves and iterations, and the
+               domains whose spec bound lies within the bound tolerance of 0;
+  cpu_baseline the oracle on the same 3-round step (all host threads), and
+               a labelled 1-thread sample.
+--config c0|c2|c3|c4 prints the line of another configuration instead.
 """
 import argparse
+import gc
 import json
 import os
 import statistics
@@ -33,8 +44,9 @@ HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK = 157.3
 
 
-def run_rounds(gg, xl, xh, spec_ew, table, timers=None):
-    """Three BaB rounds; returns per-round stats."""
+def run_rounds(gg, xl, xh, spec_ew, table, timers=None, keep=None):
+    """Three BaB rounds; returns per-round stats.  ``keep`` (a list): each
+    round's batch and step outputs are appended to it."""
     from vibecheck_amd import verify_graph as vg
     stats = []
     for _ in range(N_ROUNDS):
@@ -45,6 +57,8 @@ def run_rounds(gg, xl, xh, spec_ew, table, timers=None):
         st = vg.bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
                          clip_enabled=True, alpha_iters=ALPHA_ITERS, alpha_all=True,
                          alpha_lr=ALPHA_LR, timers=timers)
+        if keep is not None:
+            keep.append((xl, xh, st))
         (lxl, lxh), (hxl, hxh) = st['low'], st['high']
         # next batch = the LIFO pop of [low chunk, high chunk]: high first
         xl = torch.cat([hxl, lxl], 0)
@@ -55,45 +69,260 @@ def run_rounds(gg, xl, xh, spec_ew, table, timers=None):
     return stats
 
 
-def cpu_baseline(sample_B=2048, reps=3):
-    """Oracle (op-for-op torch CPU restatement) on one BaB round of a
-    sample_B-box slice of the same workload, all host threads."""
+def near_zero(lb, A, acc, xl, xh, rtol=1e-5, atol=1e-6):
+    """Domains with a spec bound inside the bound tolerance of 0, |lb| <=
+    atol + rtol * scale, scale = |acc| + sum_i |A_i| max(|xl_i|, |xh_i|): the
+    domains whose verdict fp32 rounding could flip (closure is lb > 0)."""
+    xm = torch.maximum(xl.abs(), xh.abs()).double()
+    scale = acc.double().abs() + (A.double().abs() * xm.unsqueeze(1)).sum(-1)
+    return int(((lb.double().abs() <= atol + rtol * scale).any(1)).sum())
+
+
+def _events():
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def _timed(fn, reps=5):
+    """Average seconds per call of fn with HIP events on the current stream
+    (after one untimed call)."""
+    fn()
+    torch.cuda.synchronize()
+    s, e = _events()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / 1e3 / reps
+
+
+def _roof(kernel, workload, sec, flop=None, nbytes=None, launches=1):
+    if flop is not None:
+        ach = flop / sec / 1e12
+        return {'kernel': kernel, 'workload': workload, 'bound': 'mfma', 'achieved': ach,
+                'peak': FP32_MFMA_PEAK, 'unit': 'TFLOP/s', 'frac': ach / FP32_MFMA_PEAK,
+                'flop_per_launch': flop / launches, 'avg_launch_us': 1e6 * sec / launches}
+    ach = nbytes / sec / 1e9
+    return {'kernel': kernel, 'workload': workload, 'bound': 'hbm', 'achieved': ach,
+            'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': ach / HBM_PEAK_GBS,
+            'bytes_per_launch': nbytes / launches, 'avg_launch_us': 1e6 * sec / launches}
+
+
+def secondary_c1(gg, se, kept):
+    """Rooflines of the step's other kernels on the step's own batches, each
+    launch timed alone with HIP events (outside the timed step), plus
+    alpha-CROWN's own rates: its loop on round 1's open leaves (as the step
+    runs it), and on all 65,536 domains (the configuration's batch)."""
+    from vibecheck_amd import _lib
+    from vibecheck_amd import mlp_fused as mf
+    from vibecheck_amd import verify_graph as vg
+    from vibecheck_amd import verify_zono_bnb as vz
+    import ctypes
+    dev = torch.device('cuda:0')
+    plan = mf.plan_for(gg, dev)
+    dims = plan.dims
+    n = plan.n
+    Wq, bq = vz._spec_rows(se, dev)
+    S, acc0 = mf.fold_spec(plan, Wq, bq)
+    Q = S.shape[0]
+    out = []
+    # -- k_zono_tiled (+ the wide pass) on round 1's 65,536 boxes:
+    #    sum_l 2 d_{l+1} d_l K_l per domain, K_l = 1 + n_in + unstable below l
+    xl1, xh1, _ = kept[0]
+    sb = vz._zono_sb(gg, xl1, xh1, dev, torch.float32)
+    unst = torch.stack([((sb[L][0] < 0) & (sb[L][1] > 0)).sum(1) for L in range(n)], 1).double()
+    below = torch.cat([torch.zeros_like(unst[:, :1]), unst.cumsum(1)[:, :-1]], 1)
+    K = 1 + dims[0] + below
+    w = torch.tensor([2.0 * dims[l + 1] * dims[l] for l in range(n)], device=dev,
+                     dtype=torch.float64)
+    zflop = float((K * w).sum())
+    _lib.timing_begin(['vc_mlp_tiled_zono_bounds', 'vc_mlp_tiled_zono_wide'])
+    for _ in range(5):
+        mf.zono_bounds(plan, xl1, xh1, None)
+    kt = _lib.timing_end()
+    sec = kt['vc_mlp_tiled_zono_bounds']['seconds'] + kt['vc_mlp_tiled_zono_wide']['seconds']
+    out.append(_roof('k_zono_tiled + k_zono_wide_tiled (vc_mlp_tiled_zono_bounds, '
+                     '_zono_wide)', '65,536 ACAS boxes (round 1)', sec, flop=5 * zflop,
+                     launches=5))
+    # -- k_crown_dom on round 2's batch (small-batch kernel): spec rows +
+    #    each domain's own seeded rows (counted by the kernel)
+    xl2, xh2, _ = kept[1]
+    B2 = xl2.shape[0]
+    sb2 = vz._zono_sb(gg, xl2, xh2, dev, torch.float32)
+    seeded = torch.zeros(8, 16, dtype=torch.int64, device=dev)
+    mf.SEED_COUNTER, mf.SEED_ROW = seeded, 0
+    _lib.timing_begin(['vc_mlp_tiled_crown'])
+    for _ in range(5):
+        mf.crown(plan, xl2, xh2, sb2, True, spec=(Wq, bq), want_linear=True, per_domain=True)
+    kt = _lib.timing_end()
+    mf.SEED_COUNTER = None
+    rows = seeded.tolist()
+    lst = kt['vc_mlp_tiled_crown']['per_launch']
+    cflop = sum(f + _lib.seed_flops([dims[0]] + dims[1:n + 1], rows[k])
+                for k, (_, f, _) in enumerate(lst))
+    kern = 'k_crown_dom' if _lib.load().vc_mlp_tiled_crown_mode(B2) == 1 else 'k_crown_tiled'
+    out.append(_roof(f'{kern} (vc_mlp_tiled_crown)', f'{B2} boxes (round 2)',
+                     sum(x[0] for x in lst), flop=cflop, launches=len(lst)))
+    # -- one alpha iteration launch (vc_mlp_tiled_alpha_iter) at the open
+    #    leaves of round 1 (small-batch kernel) and at 65,536 domains:
+    #    2 Q sum_l 2 d_l d_{l+1} per domain (spec backward + gradient sweep)
+    aflop_dom = 2.0 * Q * sum(2.0 * dims[l] * dims[l + 1] for l in range(n))
+    st0 = vg.bab_step(xl1, xh1, gg, se, vg.DisjunctTable({0: list(range(Q))}, dev),
+                      alpha_iters=0)
+    open_idx = (~st0['closed']).nonzero(as_tuple=True)[0]
+    xlo, xho = xl1[open_idx].contiguous(), xh1[open_idx].contiguous()
+    sbo = {L: (a[open_idx].contiguous(), b[open_idx].contiguous()) for L, (a, b) in sb.items()}
+    rates = {}
+    for what, (xa, xb, sba) in (('open', (xlo, xho, sbo)), ('all', (xl1, xh1, sb))):
+        B = xa.shape[0]
+        lo = [sba[L][0] for L in range(n)]
+        hi = [sba[L][1] for L in range(n)]
+        st = [torch.zeros(B, dims[L + 1], device=dev) for L in range(n) for _ in range(3)]
+        lb = torch.empty(B, Q, device=dev)
+        keep = [_lib.host_array(ctypes.c_void_p, [_lib.ptr(t) for t in ts])
+                for ts in (lo, hi, st[0::3], st[1::3], st[2::3])]
+
+        def it():
+            _lib.call('vc_mlp_tiled_alpha_iter', plan.dims_p, n, _lib.ptr(plan.tfrag),
+                      _lib.ptr(plan.bias_cat), B, _lib.ptr(xa), _lib.ptr(xb),
+                      *[k[1] for k in keep[:5]], None, Q, _lib.ptr(S), _lib.ptr(acc0),
+                      _lib.ptr(lb), 0.9, 0.999, 1e-8, ALPHA_LR / 0.1, 0.0316, 1, None,
+                      _lib.stream())
+        sec = _timed(it, 10)
+        n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+        kern = 'k_alpha_quad' if B <= 4 * n_cu else 'k_alpha_tiled'
+        out.append(_roof(f'{kern} (vc_mlp_tiled_alpha_iter, one iteration)',
+                         f'{B} domains ({"round 1 open leaves" if what == "open" else "all"})',
+                         sec, flop=aflop_dom * B))
+        # the whole alpha loop as the step runs it (20 iterations at most,
+        # the reference's early stop): evaluated iterations per second
+        res = {}
+
+        def loop():
+            best, n_it = vz._run_alpha_crown_inputsplit_batched(
+                xa, xb, gg, se, dev, torch.float32, n_iters=ALPHA_ITERS, lr=ALPHA_LR,
+                sb=sba, return_trace=True)
+            res['n'] = n_it
+        sec_loop = _timed(loop, 3)
+        rates[what] = {'domains': B, 'iters': res['n'], 'ms': 1e3 * sec_loop,
+                       'iters_per_s': res['n'] / sec_loop,
+                       'domain_iters_per_s': B * res['n'] / sec_loop}
+    return out, rates
+
+
+def cpu_info():
+    """The host's CPU model and the threads torch uses (OMP_NUM_THREADS when
+    set: the GPU box's share of its host)."""
+    model = None
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    model = line.split(':', 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {'model': model, 'nproc': os.cpu_count(), 'threads': torch.get_num_threads()}
+
+
+def _median_time(fn, warm, reps):
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), ts
+
+
+def _cpu_line(units, fn, warm, reps, sample, threads=None, units_1=None, fn_1=None, reps_1=1,
+              sample_1=None):
+    """cpu_baseline: the oracle (the op-for-op torch CPU restatement of the
+    reference) timed with perf_counter, median of ``reps`` after ``warm``
+    warm-ups, on ``threads`` threads; optionally a 1-thread run of fn_1."""
+    n_thr = threads or torch.get_num_threads()
+    torch.set_num_threads(n_thr)
+    t, ts = _median_time(fn, warm, reps)
+    out = {'value': units / t, 'unit': 'domains/s', 'cores': n_thr, 'kind': 'port',
+           'sample': sample, 'seconds': ts, 'cpu': cpu_info()}
+    if fn_1 is not None:
+        torch.set_num_threads(1)
+        t1, ts1 = _median_time(fn_1, 0, reps_1)
+        out['one_thread'] = {'value': units_1 / t1, 'unit': 'domains/s', 'cores': 1,
+                             'sample': sample_1, 'seconds': ts1}
+        torch.set_num_threads(n_thr)
+    return out
+
+
+def cpu_baseline_c1(reps=1):
+    """The oracle on the benchmark's own step: the three BaB rounds from the
+    65,536 seeded boxes (each round's children are the next round's batch),
+    after a warm-up round on a 2,048-box slice.  The oracle's per-domain
+    cost grows with the batch (its union-seeded CROWN tensors of B x 100 x
+    50 floats), so a smaller sample would flatter it.  The 1-thread figure
+    is round 1 on the 2,048-box slice (labelled)."""
     from oracle import ref_bab
     from vibecheck_amd import workloads as wk
     from vibecheck_amd.spec import dedup_queries
-    cores = os.cpu_count() or 1
-    torch.set_num_threads(cores)
     gg = wk.acas_gg(dtype=torch.float32)
-    xl, xh = wk.acas_boxes(N_DOMAINS, seed=1)
-    xl, xh = xl[:sample_B].contiguous(), xh[:sample_B].contiguous()
+    xl0, xh0 = wk.acas_boxes(N_DOMAINS, seed=1)
     uq, dq = dedup_queries(wk.acas_spec().as_linear_queries(5))
     se = {i: (torch.tensor(w, dtype=torch.float32), b) for i, (w, b) in enumerate(uq)}
-    ts = []
-    for r in range(reps + 1):
-        t0 = time.perf_counter()
-        ref_bab.bab_step(xl, xh, gg, se, dq, crown_intermediate=True, clip_enabled=True,
-                         alpha_iters=ALPHA_ITERS, alpha_all=True, alpha_lr=ALPHA_LR)
-        if r > 0:
-            ts.append(time.perf_counter() - t0)
-    t = statistics.median(ts)
-    return {'value': sample_B / t, 'unit': 'domains/s', 'cores': cores, 'kind': 'port',
-            'sample': f'one BaB round (CROWN-intermediate, spec bound, alpha 20 it, clip, '
-                      f'split) on the first {sample_B} of the 65,536 boxes, median of {reps}'}
+    kw = dict(crown_intermediate=True, clip_enabled=True, alpha_iters=ALPHA_ITERS,
+              alpha_all=True, alpha_lr=ALPHA_LR)
+    count = [0]
+
+    def step():
+        xl, xh = xl0, xh0
+        count[0] = 0
+        for r in range(N_ROUNDS):
+            count[0] += xl.shape[0]
+            t0 = time.perf_counter()
+            st = ref_bab.bab_step(xl, xh, gg, se, dq, **kw)
+            print(f'cpu_baseline: oracle round {r + 1} on {xl.shape[0]} boxes, '
+                  f'{time.perf_counter() - t0:.1f} s', file=sys.stderr, flush=True)
+            (lxl, lxh), (hxl, hxh) = st['low'], st['high']
+            xl, xh = torch.cat([hxl, lxl], 0), torch.cat([hxh, lxh], 0)
+
+    def slice_round():
+        ref_bab.bab_step(xl0[:2048].contiguous(), xh0[:2048].contiguous(), gg, se, dq, **kw)
+    slice_round()
+    out = _cpu_line(67082, step, 0, reps,
+                    f'the benchmark step itself: 3 BaB rounds from the 65,536 boxes '
+                    f'(CROWN intermediate, alpha 20 it, clip, split), median of {reps} after a '
+                    f'warm-up round on 2,048 boxes',
+                    units_1=2048, fn_1=slice_round, reps_1=3,
+                    sample_1='round 1 on the first 2,048 boxes, median of 3 (cheaper per '
+                             'domain than the full batch)')
+    out['value'] = count[0] / statistics.median(out['seconds'])
+    return out
 
 
 def measured_traffic(kernel):
     """HBM bytes per launch of the dominant kernel on this workload, from the
     committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (each counter scaled
-    by what it reads for a plain copy of known size); None when absent."""
+    by what it reads for a plain copy of known size).  The summary records
+    the sha256 of the kernel's source file it measured; a summary of an older
+    source gives None (and the reason)."""
+    import hashlib
     path = os.path.join(ROOT, 'profiles', f'{kernel}_acas_65536_traffic.md')
+    src = os.path.join(ROOT, 'vibecheck-nn_amd', 'csrc', 'vc_mlp_tiled.hip')
     try:
+        with open(src, 'rb') as f:
+            cur = hashlib.sha256(f.read()).hexdigest()
+        val = sha = None
         with open(path) as f:
             for line in f:
                 if line.startswith('traffic_bytes_per_launch:'):
-                    return float(line.split(':', 1)[1])
+                    val = float(line.split(':', 1)[1])
+                elif line.startswith('source_sha256:'):
+                    sha = line.split(':', 1)[1].strip()
     except OSError:
-        pass
-    return None
+        return None, 'no traffic summary'
+    if sha != cur:
+        return None, 'traffic summary measured an older vc_mlp_tiled.hip'
+    return val, 'rocprofv3 FETCH_SIZE + WRITE_SIZE of this source (sha256 matches)'
 
 
 def copy_probe(mib):
@@ -422,13 +651,238 @@ def hybrid_replay_suite(reps=5, B=4096, spec_iters=10):
         flush=True)
 
 
+# Algorithmic FLOP per launch of the layer-wise MFMA entry points, from
+# their arguments (the per-config bench lines time them with HIP events).
+LAYERWISE_MFMA = {
+    # 2 M n_out n_in
+    'vc_backward_fc': lambda a: 2.0 * a[1] * a[3] * a[11],
+    # 2 M (C_out H_out W_out)(C_in kh kw)
+    'vc_backward_conv': lambda a: 2.0 * a[1] * a[4] * a[5] * a[6] * a[7] * a[10] * a[11],
+    # 2 M n n_next
+    'vc_alpha_grad_step_slopes': lambda a: 2.0 * a[2] * a[4] * a[11],
+    'vc_alpha_grad_step': lambda a: 2.0 * a[2] * a[4] * a[11],
+    # mid W^T and rad |W|^T: 4 B n_in n_out
+    'vc_ibp_fc': lambda a: 4.0 * a[2] * a[3] * a[6],
+    # 4 B (C_out H_out W_out)(C_in kh kw)
+    'vc_ibp_conv': lambda a: 4.0 * a[2] * a[8] * a[15] * a[16] * a[3] * a[9] * a[10],
+}
+
+
+def layerwise_roofline(step, reps):
+    """Run ``step`` with HIP events around every layer-wise MFMA entry
+    point: per entry its time per step, algorithmic TFLOP/s and fraction of
+    the fp32 MFMA peak; the roofline is the entry with the most time."""
+    from vibecheck_amd import _lib
+    for name, f in LAYERWISE_MFMA.items():
+        _lib._FLOPS[name] = f
+    _lib.timing_begin(list(LAYERWISE_MFMA))
+    for _ in range(reps):
+        step()
+    kt = _lib.timing_end()
+    rows = []
+    for name, k in kt.items():
+        if k['launches'] and k['seconds'] > 0:
+            ach = k['flops'] / k['seconds'] / 1e12
+            rows.append({'entry': name, 'ms_per_step': 1e3 * k['seconds'] / reps,
+                         'launches_per_step': k['launches'] / reps, 'achieved': ach,
+                         'frac': ach / FP32_MFMA_PEAK})
+    rows.sort(key=lambda r: -r['ms_per_step'])
+    return rows
+
+
+def run_config(cfg, steps, warmup, cpu):
+    """One JSON line for a non-headline configuration: value = domains
+    bounded per second of the configuration's step (below), the roofline of
+    its dominant kernel, the CPU oracle on the same step (full batch or a
+    stated sample)."""
+    from oracle import ref_bab, ref_bound as rb
+    from vibecheck_amd import _lib
+    from vibecheck_amd import mlp_fused as mf
+    from vibecheck_amd import verify_graph as vg
+    from vibecheck_amd import verify_milp as vm
+    from vibecheck_amd import verify_zono_bnb as vz
+    from vibecheck_amd import workloads as wk
+    from vibecheck_amd.spec import dedup_queries
+    dev = torch.device('cuda:0')
+    F = torch.float32
+    _lib.load()
+
+    def specs(n_out, one):
+        spec = wk.pairwise_spec(n_out, [0.0], [0.0], one)
+        uq, dq = dedup_queries(spec.as_linear_queries(n_out))
+        c = {i: (torch.tensor(w, dtype=F), b) for i, (w, b) in enumerate(uq)}
+        return c, {k: (w.to(dev), b) for k, (w, b) in c.items()}, dq
+
+    line = {'unit': 'domains/s', 'n_gpus': 1, 'steps': steps, 'warmup': warmup,
+            'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32',
+            'data': 'synthetic (seeded boxes and Kaiming-normal weights)'}
+    if cfg == 'c0':
+        gg = wk.acas_gg(device=dev, dtype=F)
+        ggc = wk.acas_gg(dtype=F)
+        xlc, xhc = wk.acas_boxes(4096, seed=1)
+        xl, xh = xlc.to(dev), xhc.to(dev)
+        sec_c, se, dq = specs(5, True)
+        table = vg.DisjunctTable(dq, dev)
+        B = 4096
+
+        def step():
+            vg.bab_step(xl, xh, gg, se, table, crown_intermediate=True, clip_enabled=True,
+                        alpha_iters=0)
+        line.update(metric='CROWN-bounded domains/sec at 1 GPU (5-50x6-5 MLP, 4,096 domains, '
+                           'one BaB step)',
+                    config={'workload': '5-50x6-5 ReLU MLP, 4,096 input boxes, one BaB step: '
+                                        'CROWN intermediate + spec bound + clip + widest split',
+                            'domains_per_step': B})
+        cpu_fn = lambda: ref_bab.bab_step(xlc, xhc, ggc, sec_c, dq)
+        cpu_kw = dict(units=B, warm=1, reps=5, sample='the full step (4,096 boxes)',
+                      units_1=1024, reps_1=3, sample_1='the step on the first 1,024 boxes',
+                      fn_1=lambda: ref_bab.bab_step(xlc[:1024], xhc[:1024], ggc, sec_c, dq))
+    elif cfg == 'c2':
+        gg = wk.mnist_mlp_gg(device=dev, dtype=F)
+        ggc = wk.mnist_mlp_gg(dtype=F)
+        xlc, xhc = wk.mnist_mlp_boxes(512)
+        xl, xh = xlc.to(dev), xhc.to(dev)
+        sec_c, se, _ = specs(10, False)
+        B = 512
+
+        def step():
+            sb = vz._crown_intermediate_batched(gg, xl, xh, dev, F)
+            vz._run_alpha_crown_inputsplit_batched(xl, xh, gg, se, dev, F, n_iters=10,
+                                                   lr=0.25, sb=sb)
+
+        def cpu_step(n):
+            sbc = rb.crown_intermediate_batched(ggc, xlc[:n], xhc[:n])
+            rb.alpha_crown_batched(xlc[:n], xhc[:n], ggc, sec_c, n_iters=10, lr=0.25, sb=sbc)
+        line.update(metric='CROWN-bounded domains/sec at 1 GPU (784-1024x4-10 MLP, 512 '
+                           'domains, CROWN intermediate + alpha-CROWN 10 it)',
+                    config={'workload': '784-[1024]x4-10 ReLU MLP, 512 L-inf boxes eps 0.02: '
+                                        'CROWN intermediate bounds for every ReLU layer, '
+                                        'then 10 alpha-CROWN iterations (lr 0.25)',
+                            'domains_per_step': B})
+        cpu_kw = dict(units=16, warm=1, reps=5,
+                      sample='the step on the first 16 of the 512 boxes (the oracle seeds '
+                             'the union of those 16 boxes\' unstable neurons, fewer rows per '
+                             'domain than the GPU\'s 512-box union)',
+                      units_1=4, reps_1=1, sample_1='the step on the first 4 boxes',
+                      fn_1=lambda: cpu_step(4))
+        cpu_fn = lambda: cpu_step(16)
+    elif cfg == 'c3':
+        gg = wk.cifar_cnn_gg(device=dev, dtype=F)
+        ggc = wk.cifar_cnn_gg(dtype=F)
+        xlc, xhc = wk.cifar_cnn_boxes(64)
+        xl, xh = xlc.to(dev), xhc.to(dev)
+        sec_c, se, _ = specs(10, False)
+        B = 64
+
+        def step():
+            ibp = vz._ibp_forward_graph_batched(xl, xh, gg, dev, F)
+            sb = vz._crown_intermediate_batched(gg, xl, xh, dev, F, sb=ibp)
+            vz._spec_backward_graph_batched(sb, xl, xh, gg, se, dev, F)
+
+        def cpu_step(n):
+            ibp = rb.ibp_forward_batched(xlc[:n], xhc[:n], ggc)
+            sbc = rb.crown_intermediate_batched(ggc, xlc[:n], xhc[:n], sb=ibp)
+            rb.spec_backward_batched(sbc, xlc[:n], xhc[:n], ggc, sec_c)
+        line.update(metric='CROWN-bounded domains/sec at 1 GPU (3x32x32 CNN, 64 domains, '
+                           'CROWN with intermediate bounds)',
+                    config={'workload': 'CNN conv 3-32 3x3, 32-64 4x4 s2, 64-64 4x4 s2, fc '
+                                        '4096-512-10; 64 L-inf boxes eps 2/255: IBP, CROWN '
+                                        'intermediate bounds (IBP-seeded), spec bound',
+                            'domains_per_step': B})
+        cpu_fn = lambda: cpu_step(1)
+        cpu_kw = dict(units=1, warm=1, reps=3, sample='the step on the first of the 64 boxes')
+    elif cfg == 'c4':
+        widths = wk.DEEP_MLP_WIDTHS
+        Ws, bs = wk.mlp_params(widths, seed=0)
+        gg = wk.mlp_gg(Ws, bs, device=dev, dtype=F)
+        ggc = wk.mlp_gg(Ws, bs, dtype=F)
+        x_l, x_h = wk.linf_boxes(1, 784, 0.03, seed=1, dtype=F)
+        root_c = {L: (lo[0], hi[0]) for L, (lo, hi) in
+                  rb.ibp_forward_batched(x_l, x_h, ggc).items()}
+        root = {L: (a.to(dev), b.to(dev)) for L, (a, b) in root_c.items()}
+        un = [(L, int(j)) for L in sorted(root_c)
+              for j in ((root_c[L][0] < 0) & (root_c[L][1] > 0)).nonzero().flatten().tolist()]
+        layer, neuron, side = wk.relu_split_domains(un, n_domains=8192, n_splits=8, seed=2)
+        cl, _ = vm._split_clamps_batched(layer.to(dev), neuron.to(dev), side.to(dev),
+                                         widths[1:-1], dev)
+        sec_c, se, _ = specs(10, False)
+        xl, xh = x_l[0].to(dev), x_h[0].to(dev)
+        B = 8192
+
+        def step():
+            vm._ibp_crown_bab_bound(gg, xl, xh, root, cl, se, dev, F, alpha_iters=10, lr=0.25)
+
+        def cpu_step(n):
+            clamps = wk.relu_clamps_from_splits(layer[:n], neuron[:n], side[:n], widths[1:-1])
+            xlb, xhb = x_l.expand(n, -1).clone(), x_h.expand(n, -1).clone()
+            sbc = rb.split_domain_bounds(xlb, xhb, ggc, root_c, clamps)
+            rb.beta_crown_bound(sbc, xlb, xhb, ggc, sec_c, rb.beta_signs_from_clamps(clamps),
+                                n_iters=10, lr=0.25)
+        line.update(metric='CROWN-bounded domains/sec at 1 GPU (784-256x6-10 MLP, 8,192 '
+                           'ReLU-split subdomains, alpha/beta 10 it)',
+                    config={'workload': '784-[256]x6-10 ReLU MLP, one L-inf box eps 0.03 split '
+                                        'into 8,192 subdomains of 8 ReLU splits: IBP with the '
+                                        'split clamps, joint alpha/beta-CROWN 10 Adam '
+                                        'iterations (lr 0.25)',
+                            'domains_per_step': B})
+        cpu_fn = lambda: cpu_step(8192)
+        cpu_kw = dict(units=8192, warm=1, reps=3, sample='the full step (8,192 subdomains)',
+                      units_1=1024, reps_1=1, sample_1='the step on the first 1,024 subdomains',
+                      fn_1=lambda: cpu_step(1024))
+    else:
+        raise SystemExit(f'unknown config {cfg}')
+    # setup objects to the permanent generation (see main)
+    gc.collect()
+    gc.freeze()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    per_step = (time.perf_counter() - t0) / steps
+    line.update(value=B / per_step, ms_per_step=1e3 * per_step)
+    if cfg == 'c0':
+        seeded = torch.zeros(steps + 4, 16, dtype=torch.int64, device=dev)
+        mf.SEED_COUNTER, mf.SEED_ROW = seeded, 0
+        _lib.timing_begin(['vc_mlp_tiled_crown'])
+        for _ in range(steps):
+            step()
+        kt = _lib.timing_end()
+        mf.SEED_COUNTER = None
+        lst = kt['vc_mlp_tiled_crown']['per_launch']
+        dims = mf.plan_for(gg, dev).dims
+        flop = sum(f + _lib.seed_flops(dims, seeded.tolist()[k]) for k, (_, f, _) in
+                   enumerate(lst))
+        sec = sum(x[0] for x in lst)
+        line['roofline'] = _roof('k_crown_tiled (vc_mlp_tiled_crown)', '4,096 boxes', sec,
+                                 flop=flop, launches=len(lst))
+        line['roofline'].update(traffic=None, share_of_step=sec / steps / per_step)
+    else:
+        rows = layerwise_roofline(step, steps)
+        top = rows[0]
+        line['roofline'] = {'kernel': f'{top["entry"]} (MFMA GEMM core)', 'bound': 'mfma',
+                            'achieved': top['achieved'], 'peak': FP32_MFMA_PEAK,
+                            'unit': 'TFLOP/s', 'frac': top['frac'], 'traffic': None,
+                            'share_of_step': top['ms_per_step'] / (1e3 * per_step)}
+        line['mfma_entries'] = rows
+    if cpu:
+        line['cpu_baseline'] = _cpu_line(fn=cpu_fn, **cpu_kw)
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=5)
     ap.add_argument('--warmup', type=int, default=2)
+    ap.add_argument('--config', default='c1', choices=['c0', 'c1', 'c2', 'c3', 'c4'],
+                    help='c1 (default): the headline 65,536-box ACAS step; the others print '
+                         'their own line')
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--cpu-sample', type=int, default=2048)
+    ap.add_argument('--cpu-reps', type=int, default=1,
+                    help='timed CPU runs of the headline step (median)')
     ap.add_argument('--copy-probe', type=int, default=0, metavar='MIB',
                     help='only run a plain copy of MIB MiB (counter calibration)')
     ap.add_argument('--kernels', action='store_true',
@@ -450,6 +904,10 @@ def main():
     if args.hybrid:
         hybrid_replay_suite(reps=max(1, args.steps))
         return
+    if args.config != 'c1':
+        print(json.dumps(run_config(args.config, args.steps, args.warmup,
+                                    not args.no_cpu_baseline)), flush=True)
+        return
 
     from vibecheck_amd import _lib
     from vibecheck_amd import mlp_fused as mf
@@ -466,15 +924,26 @@ def main():
     se = {i: (torch.tensor(w, dtype=torch.float32, device=dev), b) for i, (w, b) in enumerate(uq)}
     table = vg.DisjunctTable(dq, dev)
 
-    for _ in range(args.warmup):
-        run_rounds(gg, xl0, xh0, se, table)
-    torch.cuda.synchronize()
-
+    # The objects of torch's and this setup's imports go to the permanent
+    # generation: otherwise the collector's first full pass over them (~45 ms,
+    # about 1.5 s after start) can land inside the timed steps.  The
+    # collector stays on.
+    gc.collect()
+    gc.freeze()
     # The shape-specialised CROWN kernels count the neurons they seed per
     # layer (one atomic per wavefront per layer), one counter row per call:
-    # the work of the seeded rows depends on each domain's bounds.
-    seeded = torch.zeros(args.steps * N_ROUNDS + 8, 16, dtype=torch.int64, device=dev)
+    # the work of the seeded rows depends on each domain's bounds.  The
+    # warm-up runs with the same counters and HIP events as the timed steps.
+    seeded = torch.zeros(max(args.steps, args.warmup) * N_ROUNDS + 8, 16, dtype=torch.int64,
+                         device=dev)
     mf.SEED_COUNTER, mf.SEED_ROW = seeded, 0
+    _lib.timing_begin(['vc_mlp_crown', 'vc_mlp_tiled_crown'])
+    for _ in range(max(1, args.warmup)):
+        run_rounds(gg, xl0, xh0, se, table)
+    _lib.timing_end()
+    seeded.zero_()
+    mf.SEED_ROW = 0
+    torch.cuda.synchronize()
     _lib.timing_begin(['vc_mlp_crown', 'vc_mlp_tiled_crown'])
     t0 = time.perf_counter()
     stats = None
@@ -498,11 +967,18 @@ def main():
 
     per_step = wall / args.steps
     domains = sum(s['B'] for s in stats)
-    alpha_iters = sum(s['alpha_iters'] for s in stats)
     entry = max(kt, key=lambda n: kt[n]['launches'])
     k = kt[entry]
     kernel = {'vc_mlp_crown': 'k_mlp_crown', 'vc_mlp_tiled_crown': 'k_crown_tiled'}[entry]
     achieved = k['flops'] / k['seconds'] / 1e12 if k['seconds'] > 0 else 0.0
+    traffic, traffic_note = measured_traffic(kernel)
+
+    # outside the timed region: the rounds' outputs once more, for the
+    # domains inside the zero band and the other kernels' rooflines
+    kept = []
+    run_rounds(gg, xl0, xh0, se, table, keep=kept)
+    nz = [near_zero(st['lb'], st['A'], st['acc'], xl, xh) for xl, xh, st in kept]
+    secondary, alpha_rates = secondary_c1(gg, se, kept)
     out = {
         'metric': 'CROWN-bounded domains/sec at 1 GPU (5-50x6-5 MLP, 65,536 domains)',
         'value': domains / per_step, 'unit': 'domains/s', 'n_gpus': 1,
@@ -512,19 +988,22 @@ def main():
         'config': {'workload': '5-50x6-5 ReLU MLP, 65,536 input boxes, 3 BaB rounds, '
                                'CROWN intermediate + alpha-CROWN 20 it lr 0.1 + clip + '
                                'widest split', 'domains_per_step': domains},
-        'alpha_iters_per_s': alpha_iters / per_step,
-        'rounds': stats,
+        'alpha_iters_per_s': alpha_rates['open']['iters_per_s'],
+        'alpha': {'step_open_leaves': alpha_rates['open'], 'all_65536': alpha_rates['all']},
+        'rounds': [dict(s, near_zero=z) for s, z in zip(stats, nz)],
         'roofline': {'kernel': f'{kernel} ({entry}: CROWN intermediate bounds + spec '
                                'backward, whole network per wavefront, fp32 MFMA)',
                      'bound': 'mfma', 'achieved': achieved, 'peak': FP32_MFMA_PEAK,
                      'unit': 'TFLOP/s', 'frac': achieved / FP32_MFMA_PEAK,
-                     'traffic': measured_traffic(kernel),
+                     'traffic': traffic,
                      'traffic_unit': 'bytes per launch (HBM, rocprofv3 FETCH_SIZE + WRITE_SIZE)',
+                     'traffic_note': traffic_note,
                      'launches_per_step': k['launches'] / args.steps,
                      'avg_launch_us': 1e6 * k['seconds'] / max(1, k['launches'])},
+        'secondary': secondary,
     }
     if not args.no_cpu_baseline:
-        out['cpu_baseline'] = cpu_baseline(args.cpu_sample)
+        out['cpu_baseline'] = cpu_baseline_c1(args.cpu_reps)
     print(json.dumps(out), flush=True)
 
 
