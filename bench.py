@@ -8,9 +8,12 @@ leaf, one halfspace clip, widest-dimension bisection; the children are the
 next round's batch.  value = domains bounded / wall time of the step.
 
 Prints one JSON line.  Extra keys:
-  roofline     the dominant kernel (k_crown_tiled), timed with HIP events on
-               its launch stream inside the timed region; traffic from the
-               committed rocprofv3 counter summary of the same source;
+  roofline     the dominant kernel work, the CROWN pass of the 65,536-box
+               round (vc_mlp_crown_rows: per ReLU layer one k_crown_rows
+               launch over the packed rows plus its k_rows_cut, then
+               k_spec_rows), timed with HIP events on its launch stream
+               inside the timed region; traffic from the committed
+               rocprofv3 counter summary of the same source;
   secondary    the step's other kernels on the step's own batches, each
                launch timed alone (zonotope bounds, small-batch CROWN, one
                alpha iteration at the open leaves and at 65,536 domains);
@@ -42,6 +45,26 @@ ALPHA_ITERS = 20
 ALPHA_LR = 0.1
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK = 157.3
+
+# The CROWN pass's entry points as timed: vc_mlp_tiled_crown (also the name
+# the native round files its CROWN pass under, whichever form runs) and the
+# layer-synchronous form called directly.
+CROWN_ENTRIES = ['vc_mlp_tiled_crown', 'vc_mlp_crown_rows']
+
+
+def _crown_launches(kt):
+    """The timed CROWN passes, in call order within each entry point (a
+    workload calls one of them)."""
+    return [x for n in CROWN_ENTRIES for x in kt.get(n, {}).get('per_launch', [])]
+
+
+def crown_kernel_name(B):
+    """The kernels that run the CROWN pass of a B-box batch."""
+    from vibecheck_amd import _lib
+    if _lib.load().vc_mlp_tiled_crown_mode(B) == 1:
+        return 'k_crown_dom (vc_mlp_tiled_crown)'
+    return ('CROWN rows pass (vc_mlp_crown_rows: k_rows_mask, k_rows_scan1/2, k_rows_write, '
+            'per ReLU layer k_crown_rows + k_rows_cut, k_spec_rows)')
 
 
 def run_rounds(gg, xl, xh, spec_ew, table, timers=None, keep=None):
@@ -151,17 +174,15 @@ def secondary_c1(gg, se, kept):
     sb2 = vz._zono_sb(gg, xl2, xh2, dev, torch.float32)
     seeded = torch.zeros(8, 16, dtype=torch.int64, device=dev)
     mf.SEED_COUNTER, mf.SEED_ROW = seeded, 0
-    _lib.timing_begin(['vc_mlp_tiled_crown'])
+    _lib.timing_begin(CROWN_ENTRIES)
     for _ in range(5):
         mf.crown(plan, xl2, xh2, sb2, True, spec=(Wq, bq), want_linear=True, per_domain=True)
-    kt = _lib.timing_end()
+    lst = _crown_launches(_lib.timing_end())
     mf.SEED_COUNTER = None
     rows = seeded.tolist()
-    lst = kt['vc_mlp_tiled_crown']['per_launch']
     cflop = sum(f + _lib.seed_flops([dims[0]] + dims[1:n + 1], rows[k])
                 for k, (_, f, _) in enumerate(lst))
-    kern = 'k_crown_dom' if _lib.load().vc_mlp_tiled_crown_mode(B2) == 1 else 'k_crown_tiled'
-    out.append(_roof(f'{kern} (vc_mlp_tiled_crown)', f'{B2} boxes (round 2)',
+    out.append(_roof(crown_kernel_name(B2), f'{B2} boxes (round 2)',
                      sum(x[0] for x in lst), flop=cflop, launches=len(lst)))
     # -- one alpha iteration launch (vc_mlp_tiled_alpha_iter) at the open
     #    leaves of round 1 (small-batch kernel) and at 65,536 domains:
@@ -846,17 +867,16 @@ def run_config(cfg, steps, warmup, cpu):
     if cfg == 'c0':
         seeded = torch.zeros(steps + 4, 16, dtype=torch.int64, device=dev)
         mf.SEED_COUNTER, mf.SEED_ROW = seeded, 0
-        _lib.timing_begin(['vc_mlp_tiled_crown'])
+        _lib.timing_begin(CROWN_ENTRIES)
         for _ in range(steps):
             step()
-        kt = _lib.timing_end()
+        lst = _crown_launches(_lib.timing_end())
         mf.SEED_COUNTER = None
-        lst = kt['vc_mlp_tiled_crown']['per_launch']
         dims = mf.plan_for(gg, dev).dims
         flop = sum(f + _lib.seed_flops(dims, seeded.tolist()[k]) for k, (_, f, _) in
                    enumerate(lst))
         sec = sum(x[0] for x in lst)
-        line['roofline'] = _roof('k_crown_tiled (vc_mlp_tiled_crown)', '4,096 boxes', sec,
+        line['roofline'] = _roof(crown_kernel_name(B), f'{B:,} boxes', sec,
                                  flop=flop, launches=len(lst))
         line['roofline'].update(traffic=None, share_of_step=sec / steps / per_step)
     else:
@@ -954,8 +974,8 @@ def main():
     kt = _lib.timing_end()
     mf.SEED_COUNTER = None
     if kt.get('vc_mlp_tiled_crown', {}).get('launches'):
-        # the dominant kernel is k_crown_tiled, the one-wavefront-per-domain
-        # kernel of the large batches; the small rounds run k_crown_dom
+        # the dominant work is the CROWN pass of the large batch (the
+        # layer-synchronous rows form); the small rounds run k_crown_dom
         lib = _lib.load()
         dims = [op['W'].shape[1] for op in gg['ops'] if op['type'] == 'fc']
         rows = seeded.tolist()
@@ -969,7 +989,7 @@ def main():
     domains = sum(s['B'] for s in stats)
     entry = max(kt, key=lambda n: kt[n]['launches'])
     k = kt[entry]
-    kernel = {'vc_mlp_crown': 'k_mlp_crown', 'vc_mlp_tiled_crown': 'k_crown_tiled'}[entry]
+    kernel = {'vc_mlp_crown': 'k_mlp_crown', 'vc_mlp_tiled_crown': 'crown_rows_pass'}[entry]
     achieved = k['flops'] / k['seconds'] / 1e12 if k['seconds'] > 0 else 0.0
     traffic, traffic_note = measured_traffic(kernel)
 
@@ -991,8 +1011,9 @@ def main():
         'alpha_iters_per_s': alpha_rates['open']['iters_per_s'],
         'alpha': {'step_open_leaves': alpha_rates['open'], 'all_65536': alpha_rates['all']},
         'rounds': [dict(s, near_zero=z) for s, z in zip(stats, nz)],
-        'roofline': {'kernel': f'{kernel} ({entry}: CROWN intermediate bounds + spec '
-                               'backward, whole network per wavefront, fp32 MFMA)',
+        'roofline': {'kernel': (crown_kernel_name(N_DOMAINS) if entry == 'vc_mlp_tiled_crown'
+                                else 'k_mlp_crown (vc_mlp_crown)')
+                               + ': CROWN intermediate bounds + spec backward, fp32 MFMA',
                      'bound': 'mfma', 'achieved': achieved, 'peak': FP32_MFMA_PEAK,
                      'unit': 'TFLOP/s', 'frac': achieved / FP32_MFMA_PEAK,
                      'traffic': traffic,

@@ -487,6 +487,29 @@ int vc_mlp_tiled_crown(const int32_t *dims, int n_relu, const float *frag,
                        float *lb_out, float *A_out, float *acc_out,
                        uint64_t *seed_rows, int32_t *queue, vc_stream_t stream);
 
+/* vc_mlp_tiled_crown with the work laid out by layer (same arguments and
+ * results, bit for bit; seed_rows as there; queue not needed): the seeded
+ * rows of one layer of every domain are packed into full 16-row MFMA tiles
+ * and the spec rows of 16 / Q domains share a tile, where
+ * vc_mlp_tiled_crown gives every domain tiles of its own.  Each row reads
+ * its domain's slopes of the layers below from a slope buffer in `work`
+ * (vc_mlp_crown_rows_workspace(dims, n_relu, B) bytes: masks, row offsets,
+ * row lists and bounds of one layer, and the slopes of every layer, 512 B
+ * per domain and layer).  lo_out/hi_out: nullable (both or neither).
+ * B < 2^25.  Replaces _crown_intermediate_batched + the spec backward
+ * (verify_zono_bnb.py:4077-4147, 4270-4453, 5117-5134) for narrow MLPs. */
+int64_t vc_mlp_crown_rows_workspace(const int32_t *dims, int n_relu, int64_t B);
+int vc_mlp_crown_rows(const int32_t *dims, int n_relu, const float *frag,
+                      const float *bias_cat, int64_t B, const float *xl,
+                      const float *xh, const float *const *lo_in,
+                      const float *const *hi_in, float *const *lo_out,
+                      float *const *hi_out, const int32_t *idx_all,
+                      const int32_t *idx_meta, int do_crown, int per_domain,
+                      int Q, const float *spec_rows, const float *spec_acc,
+                      float *lb_out, float *A_out, float *acc_out,
+                      uint64_t *seed_rows, void *work, int64_t work_bytes,
+                      vc_stream_t stream);
+
 /* No counterpart in the reference: vc_mlp_tiled_crown for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid allocation).  Same arguments, kernels and

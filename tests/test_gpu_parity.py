@@ -587,6 +587,54 @@ def test_crown_small_batch_kernel_matches_throughput_kernel(gpu, n_small):
         assert torch.equal(st[L][1], bt[L][1][:n_small])
 
 
+def _rows_case(gpu, net, B, scale):
+    if net == 'acas':
+        gg = wk.acas_gg(device=gpu, dtype=F32)
+        xl, xh = wk.acas_boxes(B, seed=1, device=gpu, dtype=F32)
+        n_out = 5
+    else:
+        gg = _util.tiny_mlp(net, seed=3, dtype=F32, device=gpu)
+        xl, xh = wk.linf_boxes(B, net[0], 0.05, seed=2, device=gpu, dtype=F32)
+        n_out = net[-1]
+    c, r = (xl + xh) / 2, (xh - xl) / 2
+    return gg, (c - scale * r).contiguous(), (c + scale * r).contiguous(), n_out
+
+
+@pytest.mark.parametrize('net,B,scale', [
+    ('acas', 65536, 1.0), ('acas', 20011, 3.0), ('acas', 1031, 2.0),
+    ([5, 64, 64, 64, 5], 4099, 2.0), ([3, 12, 12, 2], 3000, 2.0),
+    ([7, 30, 30, 30, 3], 5000, 2.0), ([4, 44, 44, 4], 2500, 2.0)])
+def test_crown_rows_layout_bit_exact(gpu, monkeypatch, net, B, scale):
+    """Batches above 4 x CUs run the layer-synchronous CROWN (rows of all
+    domains packed into full tiles, one launch per layer) instead of one
+    wavefront per domain.  Both give bit-identical spec bounds, A, acc and
+    CROWN bounds, with per-domain and union seeding and without the CROWN
+    pass (spec backward only).  Nets cover every tile shape: 16, 32, 48 and
+    64 neurons, with and without a spare bias column."""
+    from vibecheck_amd import _lib, mlp_fused as mf
+    assert _lib.load().vc_mlp_tiled_crown_mode(B) == 0, 'batch too small for the rows path'
+    gg, xl, xh, n_out = _rows_case(gpu, net, B, scale)
+    plan = mf.plan_for(gg, gpu)
+    assert plan is not None and mf._tiled(plan)
+    se_c, _ = _util.spec_for(n_out, dtype=F32)
+    se = {k: (w.to(gpu), b) for k, (w, b) in se_c.items()}
+    Wq, bq = vz._spec_rows(se, gpu)
+    sb = vz._zono_sb(gg, xl, xh, gpu, F32)
+    for do_crown, per_domain in ((True, True), (True, False), (False, False)):
+        out = {}
+        for rows in (False, True):
+            monkeypatch.setattr(mf, 'ROWS', rows)
+            out[rows] = mf.crown(plan, xl, xh, sb, do_crown, spec=(Wq, bq), want_linear=True,
+                                 per_domain=per_domain)
+        (tt, *lin_t), (tr, *lin_r) = out[False], out[True]
+        for nm, a, b in zip(('lb', 'A', 'acc'), lin_r, lin_t):
+            assert torch.equal(a, b), (nm, do_crown, per_domain, int((a != b).sum()))
+        if do_crown:
+            for L in tt:
+                for k in (0, 1):
+                    assert torch.equal(tr[L][k], tt[L][k]), (L, k, per_domain)
+
+
 def test_crown_intermediate_parity_mlp_chunked(gpu):
     gg_c = wk.deep_mlp_gg(dtype=F32)
     gg_g = wk.deep_mlp_gg(device=gpu, dtype=F32)

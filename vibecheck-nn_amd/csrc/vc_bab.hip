@@ -52,6 +52,8 @@ struct RoundBufs {
   int32_t* uidx;                     // union lists (sum d)
   int32_t* umeta;                    // union counts and offsets (2 n)
   int32_t* queue;                    // work counters [2]
+  void* rws;                         // layer-synchronous CROWN workspace (large B)
+  int64_t rws_bytes;
   // alpha on the open leaves (sized for B)
   float *a_lo[MAXL], *a_hi[MAXL];
   float *a_xl, *a_xh, *a_state, *a_lb, *a_best, *a_ctl;
@@ -63,14 +65,18 @@ struct RoundBufs {
 
 void carve(Carve& c, RoundBufs& r, const int32_t* dims, int n, int64_t B, int Q) {
   const int n_in = dims[0];
+  // batches above 4 x CUs take the layer-synchronous CROWN, which needs no
+  // buffers for the CROWN bounds
+  r.rws_bytes = vc_mlp_tiled_crown_mode(B) == 0 ? vc_mlp_crown_rows_workspace(dims, n, B) : 0;
+  if (r.rws_bytes < 0) r.rws_bytes = 0;
   int sumd = 0;
   for (int l = 0; l < n; ++l) {
     const int d = dims[l + 1];
     sumd += d;
     r.sb_lo[l] = c.take<float>(B * d);
     r.sb_hi[l] = c.take<float>(B * d);
-    r.t_lo[l] = c.take<float>(B * d);
-    r.t_hi[l] = c.take<float>(B * d);
+    r.t_lo[l] = r.rws_bytes > 0 ? nullptr : c.take<float>(B * d);
+    r.t_hi[l] = r.rws_bytes > 0 ? nullptr : c.take<float>(B * d);
     r.a_lo[l] = c.take<float>(B * d);
     r.a_hi[l] = c.take<float>(B * d);
   }
@@ -84,6 +90,7 @@ void carve(Carve& c, RoundBufs& r, const int32_t* dims, int n, int64_t B, int Q)
   r.uidx = c.take<int32_t>(sumd);
   r.umeta = c.take<int32_t>(2 * n);
   r.queue = c.take<int32_t>(2);
+  r.rws = r.rws_bytes > 0 ? c.take<char>(r.rws_bytes) : nullptr;
   r.a_xl = c.take<float>(B * n_in);
   r.a_xh = c.take<float>(B * n_in);
   r.a_state = c.take<float>(3 * (int64_t)sumd * B);
@@ -210,9 +217,16 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
   VC_TRY(vc_unstable_union_layers(r.sb_lo, r.sb_hi, widths, n, B, r.uflags, stream));
   VC_TRY(vc_union_compact(r.uflags, widths, n, r.uidx, r.umeta, stream));
   if (crown_ev0 && hipEventRecord((hipEvent_t)crown_ev0, st) != hipSuccess) return VC_ERR_LAUNCH;
-  VC_TRY(vc_mlp_tiled_crown(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.t_lo,
-                            r.t_hi, r.uidx, r.umeta, 1, 1, Q, spec_rows, spec_acc, lb, A, acc,
-                            seed_rows, r.queue, stream));
+  // the round reads only the spec bound of the CROWN pass (alpha restarts
+  // from the zonotope bounds): the rows form writes no CROWN bounds
+  if (r.rws)
+    VC_TRY(vc_mlp_crown_rows(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, nullptr,
+                             nullptr, r.uidx, r.umeta, 1, 1, Q, spec_rows, spec_acc, lb, A, acc,
+                             seed_rows, r.rws, r.rws_bytes, stream));
+  else
+    VC_TRY(vc_mlp_tiled_crown(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.t_lo,
+                              r.t_hi, r.uidx, r.umeta, 1, 1, Q, spec_rows, spec_acc, lb, A,
+                              acc, seed_rows, r.queue, stream));
   if (crown_ev1 && hipEventRecord((hipEvent_t)crown_ev1, st) != hipSuccess) return VC_ERR_LAUNCH;
   VC_TRY(vc_closure(lb, B, Q, d_ptr, q_idx, n_disj, closed, stream));
 

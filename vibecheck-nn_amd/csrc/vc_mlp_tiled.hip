@@ -196,15 +196,24 @@ __device__ __forceinline__ void fc_hidden(const float4* fr, int lane, int g, int
       for (int p = 0; p < NP; ++p) o[p][mt] = mfma16x16x4(a[mt], F[p][ks >> 2][ks & 3], o[p][mt]);
   }
   if (BROW) {
-    const int mtb = mb >> 4, ib = mb & 3;
+    // the bias row's entry: (M-tile, component) is the same for every lane,
+    // so a scalar branch picks it
     const bool mine = g == ((mb & 15) >> 2);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       float v = 0.f;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v = (mt == mtb && i == ib) ? o[p][mt][i] : v;
+      switch (((mb >> 4) << 2) | (mb & 3)) {
+#define VC_BROW_CASE(C)                                   \
+  case C:                                                 \
+    if ((C >> 2) < MT) v = o[p][(C >> 2) < MT ? (C >> 2) : 0][C & 3]; \
+    break;
+        VC_BROW_CASE(0) VC_BROW_CASE(1) VC_BROW_CASE(2) VC_BROW_CASE(3)
+        VC_BROW_CASE(4) VC_BROW_CASE(5) VC_BROW_CASE(6) VC_BROW_CASE(7)
+        VC_BROW_CASE(8) VC_BROW_CASE(9) VC_BROW_CASE(10) VC_BROW_CASE(11)
+        VC_BROW_CASE(12) VC_BROW_CASE(13) VC_BROW_CASE(14) VC_BROW_CASE(15)
+#undef VC_BROW_CASE
+        default: break;
+      }
       if (mine) acc[p] += (double)v;
     }
   }
@@ -1866,6 +1875,668 @@ extern "C" int vc_mlp_tiled_crown(const int32_t* dims, int n_relu, const float* 
   }
 #undef VC_TILED_CASE
   VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+// ------------------------------- layer-synchronous CROWN over packed rows
+// vc_mlp_crown_rows computes what vc_mlp_tiled_crown computes, with the
+// work laid out by layer instead of by domain.  k_crown_tiled gives each
+// domain its own 16-row tiles, so a layer's 2 m seeded rows fill
+// ceil(2 m / 16) tiles (about half full at the ACAS-Xu shape) and the Q = 4
+// spec rows a quarter of one.  Here the seeded rows of layer L of every
+// domain are packed densely into one row list and chained through
+// fc_{L-1} .. fc_0 in full tiles; each row reads its own domain's slopes of
+// the layers below, which earlier launches left in a per-layer slope buffer,
+// and the spec rows of 16 / Q domains share a tile.  Every row is computed
+// with the operations of k_crown_tiled in the same order (an MFMA output
+// column depends only on its own B column), so the results are the same
+// bit for bit.  Launch order per call:
+//   k_rows_mask      per domain and layer: the seeded neurons (the union,
+//                    per domain filtered as in k_crown_tiled) as a 64-bit mask
+//   k_rows_scan1/2   per layer, the rows' offsets (exclusive scan of 2 m)
+//   per layer L:
+//     k_crown_rows   the rows' bounds: start +-W_L[j], relax and fc down to
+//                    the input, concretize over the row's box
+//     k_rows_cut     per domain: intersect the bounds, the slopes of layer L,
+//                    and layer L + 1's row codes (domain, sign, neuron; layer
+//                    0's by k_rows_write)
+//   k_spec_rows      the spec rows of every domain, B Q rows in full tiles
+namespace {
+
+constexpr int RNW = 8;        // waves per workgroup of the row-chain kernels
+constexpr int RSCAN = 1024;   // domains per block of the offset scan
+constexpr int SLW = 2 * FW;   // floats per (layer, domain) of the slope buffer
+
+// A row: domain << 7 | negated << 6 | neuron.
+__device__ __forceinline__ uint32_t row_code(int64_t d, int neg, int j) {
+  return ((uint32_t)d << 7) | ((uint32_t)neg << 6) | (uint32_t)j;
+}
+
+// fc0_concretize for rows of different domains: the box values of the
+// lane's first-M-tile inputs (m = 4 g + i) come preloaded in registers,
+// further M-tiles (more than 16 inputs) read them from dxl / dxh.
+template <int KS, bool BROW>
+__device__ __forceinline__ void fc0_concretize_pr(const float* fr0, int mt0, int d0, int lane,
+                                                  int g, int r, const float (&bxl)[4],
+                                                  const float (&bxh)[4], const float* dxl,
+                                                  const float* dxh, const v4f (&F)[TNP][4],
+                                                  double (&acc)[TNP], double (&cz)[TNP],
+                                                  float* A_rows, int n_live) {
+  for (int mt = 0; mt < mt0; ++mt) {
+    v4f o = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      o = mfma16x16x4(fr0[(mt * KS + ks) * 64 + swz(lane, ks)], F[0][ks >> 2][ks & 3], o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * mt + 4 * g + i;
+      const bool in = m < d0;
+      const float xlv = in ? (mt == 0 ? bxl[i] : dxl[m]) : 0.f;
+      const float xhv = in ? (mt == 0 ? bxh[i] : dxh[m]) : 0.f;
+      const float v = o[i];
+      if (in) {
+        cz[0] += (double)(fmaxf(v, 0.f) * xlv);
+        cz[0] += (double)(fminf(v, 0.f) * xhv);
+        if (A_rows && r < n_live) A_rows[(int64_t)r * d0 + m] = v;
+      } else if (BROW && m == d0) {
+        acc[0] += (double)v;
+      }
+    }
+  }
+}
+
+// The box values a lane's concretization reads first: inputs 4 g + i.
+__device__ __forceinline__ void box_load(const float* dxl, const float* dxh, int d0, int g,
+                                         float (&bxl)[4], float (&bxh)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = 4 * g + i;
+    bxl[i] = m < d0 ? dxl[m] : 0.f;
+    bxh[i] = m < d0 ? dxh[m] : 0.f;
+  }
+}
+
+// The slopes of one relu for rows of different domains: each lane's row
+// reads those of its own domain from the slope buffer (cb: that domain's
+// entry for the layer: [0, FW) lo_s folded into the sign of up_s, [FW, 2 FW)
+// up_t), the 4 K-steps of a 16-neuron tile per float4.  lo_s is 0 or 1 and
+// up_s > 0 wherever lo_s = 1, so the sign carries it.
+struct RowSlopes {
+  float4 c[4], u[4];
+};
+
+template <int KS>
+__device__ __forceinline__ void slopes_load(const float* cb, int g, RowSlopes& s) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (4 * t >= KS) break;
+    s.c[t] = *reinterpret_cast<const float4*>(cb + 16 * t + 4 * g);
+    s.u[t] = *reinterpret_cast<const float4*>(cb + FW + 16 * t + 4 * g);
+  }
+}
+
+// The relaxation with per-row slopes: relax_rows with the decoded values
+// (equal to make_slopes').
+template <int KS, bool BROW>
+__device__ __forceinline__ void relax_rows_pr(const RowSlopes& s, const float* bl, int g,
+                                              v4f (&F)[TNP][4], double (&acc)[TNP]) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (4 * t >= KS) break;
+    const float cs[4] = {s.c[t].x, s.c[t].y, s.c[t].z, s.c[t].w};
+    const float us4[4] = {s.u[t].x, s.u[t].y, s.u[t].z, s.u[t].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (4 * t + i >= KS) break;
+      const int j = 16 * t + 4 * g + i;
+      const float us = fabsf(cs[i]);
+      const float ls = cs[i] < 0.f ? 1.f : 0.f;
+      const float ut = us4[i];
+      const float bj = BROW ? 0.f : bl[j];
+      const float x = F[0][t][i];
+      const bool ng = x < 0.f;
+      const float e = x * (ng ? us : ls);
+      const float en = ng ? x : 0.f;
+      acc[0] += (double)(en * ut);
+      if (!BROW) acc[0] += (double)(e * bj);
+      F[0][t][i] = e;
+    }
+  }
+}
+
+// Rows at relu Ltop's output through relax + fc_l for l = Ltop .. 1, then
+// relu 0 and fc_0 with the concretization (chain_to_input, per-row slopes).
+// The slopes of the next relu are requested before each fc's MFMAs.
+template <int MT, int KS, bool BROW>
+__device__ __forceinline__ void chain_rows(const TGeom& G, int Ltop, const float* fr0,
+                                           const float4* frh, const float* slp, int64_t B,
+                                           int64_t d, const float* sbias, int lane, int g, int r,
+                                           const float* dxl, const float* dxh, v4f (&F)[TNP][4],
+                                           double (&acc)[TNP], double (&cz)[TNP], float* A_rows,
+                                           int n_live) {
+  // the first slopes and the box requested together (one round trip)
+  RowSlopes s;
+  slopes_load<KS>(slp + ((int64_t)Ltop * B + d) * SLW, g, s);
+  float bxl[4], bxh[4];
+  box_load(dxl, dxh, G.d[0], g, bxl, bxh);
+  for (int l = Ltop; l >= 1; --l) {
+    relax_rows_pr<KS, BROW>(s, sbias + l * FW, g, F, acc);
+    slopes_load<KS>(slp + ((int64_t)(l - 1) * B + d) * SLW, g, s);
+    fc_hidden<MT, KS, 1, BROW>(frh + (l - 1) * KS * 64, lane, g, G.d[l], F, acc);
+  }
+  relax_rows_pr<KS, BROW>(s, sbias, g, F, acc);
+  fc0_concretize_pr<KS, BROW>(fr0, G.mt0, G.d[0], lane, g, r, bxl, bxh, dxl, dxh, F, acc, cz,
+                              A_rows, n_live);
+}
+
+struct RowsLayers {
+  const float* lo[MAXL];
+  const float* hi[MAXL];
+  float* lo_out[MAXL];
+  float* hi_out[MAXL];
+};
+
+// One wavefront per domain: for every layer, the union neurons it seeds
+// (per_domain: only those with lo < 0 and hi > -1e-7 in this domain, the
+// filter of k_crown_tiled) as a bit mask, and 2 m rows.  The union lists
+// (idx_all, idx_meta of vc_union_compact) become per-layer masks in LDS.
+__global__ __launch_bounds__(256) void k_rows_mask(TGeom G, int64_t B, RowsLayers rl,
+                                                   const int32_t* __restrict__ idx_all,
+                                                   const int32_t* __restrict__ idx_meta,
+                                                   int per_domain, uint64_t* __restrict__ masks,
+                                                   int32_t* __restrict__ cnt,
+                                                   unsigned long long* __restrict__ seed_rows) {
+  __shared__ uint64_t umask[MAXL];
+  __shared__ int scnt[MAXL];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int n = G.n;
+  if (wv == 0) {
+    for (int L = 0; L < n; ++L) {
+      // bit j of the union mask for every listed neuron j (an OR over the wave)
+      const int c = min(idx_meta[L], G.d[L + 1]);
+      const int j = lane < c ? idx_all[idx_meta[n + L] + lane] : 0;
+      unsigned long long v = (lane < c && j >= 0 && j < FW) ? (1ull << j) : 0ull;
+      for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
+      if (lane == 0) umask[L] = v;
+    }
+    if (lane < MAXL) scnt[lane] = 0;
+  }
+  __syncthreads();
+  for (int64_t d = (int64_t)blockIdx.x * 4 + wv; d < B; d += (int64_t)gridDim.x * 4) {
+    // every layer's bounds requested before any is used
+    float lo[MAXL], hi[MAXL];
+#pragma unroll
+    for (int L = 0; L < MAXL; ++L) {
+      const int dW = L < n ? G.d[L + 1] : 0;
+      const bool rd = per_domain && lane < dW;
+      lo[L] = rd ? rl.lo[L][d * dW + lane] : 0.f;
+      hi[L] = rd ? rl.hi[L][d * dW + lane] : 0.f;
+    }
+#pragma unroll
+    for (int L = 0; L < MAXL; ++L) {
+      if (L >= n) break;
+      const int dW = G.d[L + 1];
+      const bool inu = lane < dW && ((umask[L] >> lane) & 1ull);
+      const bool keep = inu && (!per_domain || (lo[L] < 0.f && hi[L] > -1e-7f));
+      const uint64_t m = __ballot(keep);
+      if (lane == 0) {
+        masks[(int64_t)L * B + d] = m;
+        cnt[(int64_t)L * B + d] = 2 * __popcll(m);
+        if (seed_rows && m) atomicAdd(&scnt[L], __popcll(m));
+      }
+    }
+  }
+  __syncthreads();
+  if (seed_rows && threadIdx.x < n && scnt[threadIdx.x])
+    atomicAdd(seed_rows + threadIdx.x, (unsigned long long)scnt[threadIdx.x]);
+}
+
+// Exclusive scan of the row counts, per layer (blockIdx.y): within blocks
+// of RSCAN domains (offsets local to the block), block totals to bsum.
+__global__ __launch_bounds__(RSCAN) void k_rows_scan1(const int32_t* __restrict__ cnt, int64_t B,
+                                                      int32_t* __restrict__ off,
+                                                      int32_t* __restrict__ bsum, int nblk) {
+  __shared__ int wsum[RSCAN / 64];
+  const int L = blockIdx.y;
+  const int64_t i = (int64_t)blockIdx.x * RSCAN + threadIdx.x;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int v = i < B ? cnt[(int64_t)L * B + i] : 0;
+  int x = v;  // inclusive scan within the wave
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[wv] = x;
+  __syncthreads();
+  if (wv == 0) {
+    int w = lane < RSCAN / 64 ? wsum[lane] : 0;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(w, o, 64);
+      if (lane >= o) w += y;
+    }
+    if (lane < RSCAN / 64) wsum[lane] = w;  // inclusive wave prefix
+  }
+  __syncthreads();
+  const int base = wv > 0 ? wsum[wv - 1] : 0;
+  if (i < B) off[(int64_t)L * B + i] = base + x - v;
+  if (threadIdx.x == RSCAN - 1) bsum[L * nblk + blockIdx.x] = wsum[RSCAN / 64 - 1];
+}
+
+// Per layer (blockIdx.x): exclusive scan of the block totals in place, the
+// layer's row total to tot[L].
+__global__ __launch_bounds__(1024) void k_rows_scan2(int32_t* __restrict__ bsum, int nblk,
+                                                     int32_t* __restrict__ tot) {
+  __shared__ int wsum[16];
+  __shared__ int carry;
+  const int L = blockIdx.x;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int c0 = 0; c0 < nblk; c0 += 1024) {
+    const int k = c0 + threadIdx.x;
+    const int v = k < nblk ? bsum[L * nblk + k] : 0;
+    int x = v;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wsum[wv] = x;
+    __syncthreads();
+    if (wv == 0) {
+      int w = lane < 16 ? wsum[lane] : 0;
+      for (int o = 1; o < 16; o <<= 1) {
+        const int y = __shfl_up(w, o, 64);
+        if (lane >= o) w += y;
+      }
+      if (lane < 16) wsum[lane] = w;
+    }
+    __syncthreads();
+    const int base = carry + (wv > 0 ? wsum[wv - 1] : 0);
+    if (k < nblk) bsum[L * nblk + k] = base + x - v;
+    __syncthreads();
+    if (threadIdx.x == 0) carry += wsum[15];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) tot[L] = carry;
+}
+
+// The row codes of layer L: domain d's rows start at its offset, the m
+// "+" rows (neurons in increasing order) then the m "-" rows.
+__global__ __launch_bounds__(256) void k_rows_write(int64_t B, int L,
+                                                    const uint64_t* __restrict__ masks,
+                                                    const int32_t* __restrict__ off,
+                                                    const int32_t* __restrict__ bsum, int nblk,
+                                                    uint32_t* __restrict__ rows) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int64_t d = (int64_t)blockIdx.x * 4 + wv; d < B; d += (int64_t)gridDim.x * 4) {
+    const uint64_t m = masks[(int64_t)L * B + d];
+    if (!m) continue;
+    const int cnt = __popcll(m);
+    const int64_t base = (int64_t)off[(int64_t)L * B + d] + bsum[L * nblk + (int)(d / RSCAN)];
+    if ((m >> lane) & 1ull) {
+      const int q = __popcll(m & ((1ull << lane) - 1ull));
+      rows[base + q] = row_code(d, 0, lane);
+      rows[base + cnt + q] = row_code(d, 1, lane);
+    }
+  }
+}
+
+// The bounds of layer L's rows (chains of full 16-row tiles): each
+// workgroup takes a contiguous run of tiles, its wavefronts alternate.
+template <int MT, int KS, bool BROW>
+__global__ __launch_bounds__(RNW * 64, 4) void k_crown_rows(
+    TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
+    const float* __restrict__ xl, const float* __restrict__ xh, int L,
+    const uint32_t* __restrict__ rows, const int32_t* __restrict__ tot,
+    const float* __restrict__ slp, float* __restrict__ slb) {
+  extern __shared__ float smem[];
+  float* sfrag = smem;
+  float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int n = G.n, d0 = G.d[0];
+  vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
+  for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
+    const int l = k / FW, j = k % FW;
+    sbias[k] = j < G.d[l + 1] ? gbias[G.boff[l] + j] : 0.f;
+  }
+  __syncthreads();
+  const float* fr0 = sfrag;
+  const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
+  const int64_t R = tot[L];
+  const int64_t ntiles = (R + 15) / 16;
+  const int64_t per = (ntiles + gridDim.x - 1) / gridDim.x;
+  const int64_t t0 = (int64_t)blockIdx.x * per;
+  const int64_t t1 = t0 + per < ntiles ? t0 + per : ntiles;
+  // each tile's row code is requested one tile ahead
+  uint32_t code_next = 0u;
+  if (t0 + wv < t1 && (t0 + wv) * 16 + r < R) code_next = rows[(t0 + wv) * 16 + r];
+  for (int64_t tile = t0 + wv; tile < t1; tile += RNW) {
+    const int64_t row = tile * 16 + r;
+    const bool live = row < R;
+    const uint32_t code = live ? code_next : 0u;
+    {
+      const int64_t nrow = (tile + RNW) * 16 + r;
+      code_next = (tile + RNW < t1 && nrow < R) ? rows[nrow] : 0u;
+    }
+    const int64_t d = (int64_t)(code >> 7);
+    const int j = (int)(code & 63u);
+    const float sg = (code >> 6) & 1u ? -1.f : 1.f;
+    const float* dxl = xl + d * d0;
+    const float* dxh = xh + d * d0;
+    const int ksj = 4 * (j >> 4) + (j & 3), gj = (j & 15) >> 2;
+    v4f F[TNP][4];
+    double acc[TNP], cz[TNP];
+    acc[0] = (live && g == 0) ? (double)(sg * sbias[L * FW + j]) : 0.0;
+    cz[0] = 0.0;
+    if (L > 0) {
+      const float4* fl = frh + (L - 1) * KS * 64 + ksj * 64;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 w = live ? fl[swz(16 * gj + 4 * g + i, ksj)] : float4{0.f, 0.f, 0.f, 0.f};
+        F[0][0][i] = sg * w.x;
+        F[0][1][i] = sg * w.y;
+        F[0][2][i] = sg * w.z;
+        F[0][3][i] = sg * w.w;
+      }
+      chain_rows<MT, KS, BROW>(G, L - 1, fr0, frh, slp, B, d, sbias, lane, g, r, dxl, dxh, F,
+                               acc, cz, nullptr, 0);
+    } else if (live) {
+      // seeded at relu 0: the row is +-W_0[j] over the inputs
+      for (int mt = 0; mt < G.mt0; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int mi = 16 * mt + 4 * g + i;
+          if (mi < d0) {
+            const float v = sg * fr0[(mt * KS + ksj) * 64 + swz(16 * gj + 4 * g + i, ksj)];
+            cz[0] += (double)(fmaxf(v, 0.f) * dxl[mi]);
+            cz[0] += (double)(fminf(v, 0.f) * dxh[mi]);
+          }
+        }
+    }
+    const double lbd = group_sum4_d(acc[0] + cz[0]);
+    if (g == 0 && live) slb[row] = (float)lbd;
+  }
+}
+
+// Layer L's final bounds of every domain (lane j holds neuron j; two
+// domains per wavefront, their loads issued together): lo = max(lo, lb+),
+// hi = max(min(hi, -lb-), lo) for the seeded neurons, then the slopes of
+// make_slopes into the slope buffer and the bounds to lo_out / hi_out when
+// given; and, with wnext, layer L + 1's row codes (k_rows_write's).
+// masks null: no seeds (the slopes of the given bounds).
+__global__ __launch_bounds__(256) void k_rows_cut(TGeom G, int64_t B, int L, RowsLayers rl,
+                                                  const uint64_t* __restrict__ masks,
+                                                  const int32_t* __restrict__ off,
+                                                  const int32_t* __restrict__ bsum, int nblk,
+                                                  const float* __restrict__ slb,
+                                                  float* __restrict__ slp, int wnext,
+                                                  uint32_t* __restrict__ rows) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int dW = G.d[L + 1];
+  const bool in = lane < dW;
+  for (int64_t d0 = ((int64_t)blockIdx.x * 4 + wv) * 2; d0 < B; d0 += (int64_t)gridDim.x * 8) {
+    float lo[2], hi[2];
+    uint64_t m[2], mn[2];
+    int64_t base[2], bn[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int64_t d = d0 + k;
+      const bool v = d < B;
+      lo[k] = (v && in) ? rl.lo[L][d * dW + lane] : 0.f;
+      hi[k] = (v && in) ? rl.hi[L][d * dW + lane] : 0.f;
+      m[k] = (v && masks) ? masks[(int64_t)L * B + d] : 0ull;
+      base[k] = (v && masks)
+                    ? (int64_t)off[(int64_t)L * B + d] + bsum[L * nblk + (int)(d / RSCAN)]
+                    : 0;
+      mn[k] = (v && wnext) ? masks[(int64_t)(L + 1) * B + d] : 0ull;
+      bn[k] = (v && wnext) ? (int64_t)off[(int64_t)(L + 1) * B + d] +
+                                 bsum[(L + 1) * nblk + (int)(d / RSCAN)]
+                           : 0;
+    }
+    float sp[2], sn[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const bool seeded = in && ((m[k] >> lane) & 1ull);
+      const int cnt = __popcll(m[k]);
+      const int q = __popcll(m[k] & ((1ull << lane) - 1ull));
+      sp[k] = seeded ? slb[base[k] + q] : 0.f;
+      sn[k] = seeded ? slb[base[k] + cnt + q] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int64_t d = d0 + k;
+      if (d >= B) break;
+      float l = lo[k], h = hi[k];
+      if (in && ((m[k] >> lane) & 1ull)) {
+        const float lc = fmaxf(l, sp[k]);
+        const float hc = fmaxf(fminf(h, -sn[k]), lc);
+        l = lc;
+        h = hc;
+      }
+      if (in && rl.lo_out[L]) {
+        rl.lo_out[L][d * dW + lane] = l;
+        rl.hi_out[L][d * dW + lane] = h;
+      }
+      float code = 0.f, ut = 0.f;
+      if (in) {
+        const Relax s = relax(l, h);
+        code = s.lo_s != 0.f ? -s.up_s : s.up_s;
+        ut = s.up_t;
+      }
+      float* e = slp + ((int64_t)L * B + d) * SLW;
+      e[lane] = code;
+      e[FW + lane] = ut;
+      if (wnext && ((mn[k] >> lane) & 1ull)) {
+        const int cnt = __popcll(mn[k]);
+        const int q = __popcll(mn[k] & ((1ull << lane) - 1ull));
+        rows[bn[k] + q] = row_code(d, 0, lane);
+        rows[bn[k] + cnt + q] = row_code(d, 1, lane);
+      }
+    }
+  }
+}
+
+// The spec rows of every domain (row d Q + q: domain d, spec row q) through
+// relu n-1 .. relu 0 in full tiles; lb, acc and the input coefficients out.
+template <int MT, int KS, bool BROW>
+__global__ __launch_bounds__(RNW * 64, 4) void k_spec_rows(
+    TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
+    const float* __restrict__ xl, const float* __restrict__ xh, int Q,
+    const float* __restrict__ spec_rows, const float* __restrict__ spec_acc,
+    const float* __restrict__ slp, float* __restrict__ lb_out, float* __restrict__ A_out,
+    float* __restrict__ acc_out) {
+  extern __shared__ float smem[];
+  float* sfrag = smem;
+  float* sbias = smem + G.nfloats;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int n = G.n, d0 = G.d[0], dN = G.d[n];
+  vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
+  for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
+    const int l = k / FW, j = k % FW;
+    sbias[k] = j < G.d[l + 1] ? gbias[G.boff[l] + j] : 0.f;
+  }
+  __syncthreads();
+  const float* fr0 = sfrag;
+  const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
+  const int64_t R = B * Q;
+  const int64_t ntiles = (R + 15) / 16;
+  const int64_t per = (ntiles + gridDim.x - 1) / gridDim.x;
+  const int64_t t0 = (int64_t)blockIdx.x * per;
+  const int64_t t1 = t0 + per < ntiles ? t0 + per : ntiles;
+  for (int64_t tile = t0 + wv; tile < t1; tile += RNW) {
+    const int64_t row = tile * 16 + r;
+    const bool live = row < R;
+    const int64_t d = live ? row / Q : 0;
+    const int q = live ? (int)(row - d * Q) : 0;
+    const float* dxl = xl + d * d0;
+    const float* dxh = xh + d * d0;
+    v4f F[TNP][4];
+    double acc[TNP], cz[TNP];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int k = 16 * t + 4 * g + i;
+        F[0][t][i] = (live && k < dN) ? spec_rows[q * dN + k] : 0.f;
+      }
+    acc[0] = (live && g == 0) ? (double)spec_acc[q] : 0.0;
+    cz[0] = 0.0;
+    float* A_rows = A_out ? A_out + tile * 16 * d0 : nullptr;
+    chain_rows<MT, KS, BROW>(G, n - 1, fr0, frh, slp, B, d, sbias, lane, g, r, dxl, dxh, F, acc,
+                             cz, A_rows, (int)(R - tile * 16 < 16 ? R - tile * 16 : 16));
+    const double a = group_sum4_d(acc[0]);
+    const double lbd = a + group_sum4_d(cz[0]);
+    if (g == 0 && live) {
+      lb_out[row] = (float)lbd;
+      if (acc_out) acc_out[row] = (float)a;
+    }
+  }
+}
+
+template <int V>
+const void* crown_rows_fn() {
+  return reinterpret_cast<const void*>(
+      &k_crown_rows<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
+}
+
+template <int V>
+const void* spec_rows_fn() {
+  return reinterpret_cast<const void*>(
+      &k_spec_rows<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
+}
+
+// The workspace of vc_mlp_crown_rows, carved in order (256-byte aligned).
+struct RowsWork {
+  uint64_t* masks;  // [n][B]
+  int32_t* cnt;     // [n][B]
+  int32_t* off;     // [n][B]
+  int32_t* bsum;    // [n][nblk]
+  int32_t* tot;     // [n]
+  uint32_t* rows;   // [B * 2 * max width]
+  float* slb;       // [B * 2 * max width]
+  float* slp;       // [n][B][2 FW]
+  size_t bytes;
+};
+
+RowsWork rows_carve(char* base, int n, int maxw, int64_t B) {
+  RowsWork w{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + o : nullptr;
+    o += (bytes + 255) & ~(size_t)255;
+    return p;
+  };
+  const int nblk = (int)((B + RSCAN - 1) / RSCAN);
+  w.masks = reinterpret_cast<uint64_t*>(take(sizeof(uint64_t) * n * B));
+  w.cnt = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * n * B));
+  w.off = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * n * B));
+  w.bsum = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * n * (size_t)nblk));
+  w.tot = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * n));
+  w.rows = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * B * 2 * (size_t)maxw));
+  w.slb = reinterpret_cast<float*>(take(sizeof(float) * B * 2 * (size_t)maxw));
+  w.slp = reinterpret_cast<float*>(take(sizeof(float) * n * B * (size_t)SLW));
+  w.bytes = o;
+  return w;
+}
+
+}  // namespace
+
+extern "C" int64_t vc_mlp_crown_rows_workspace(const int32_t* dims, int n_relu, int64_t B) {
+  TGeom G;
+  const int rc = tiled_geom(dims, n_relu, G);
+  if (rc != VC_OK) return -rc;
+  if (B < 0) return -VC_ERR_ARG;
+  int maxw = 1;
+  for (int l = 1; l <= n_relu; ++l) maxw = G.d[l] > maxw ? G.d[l] : maxw;
+  return (int64_t)rows_carve(nullptr, n_relu, maxw, B).bytes;
+}
+
+extern "C" int vc_mlp_crown_rows(const int32_t* dims, int n_relu, const float* frag,
+                                 const float* bias_cat, int64_t B, const float* xl,
+                                 const float* xh, const float* const* lo_in,
+                                 const float* const* hi_in, float* const* lo_out,
+                                 float* const* hi_out, const int32_t* idx_all,
+                                 const int32_t* idx_meta, int do_crown, int per_domain, int Q,
+                                 const float* spec_rows, const float* spec_acc, float* lb_out,
+                                 float* A_out, float* acc_out, uint64_t* seed_rows, void* work,
+                                 int64_t work_bytes, vc_stream_t stream) {
+  TGeom G;
+  int rc = tiled_geom(dims, n_relu, G);
+  if (rc != VC_OK) return rc;
+  if (!frag || !bias_cat || !xl || !xh || !lo_in || !hi_in || B < 0) return VC_ERR_ARG;
+  if (Q < 0 || Q > TQMAX) return VC_ERR_UNSUPPORTED;
+  if (Q > 0 && (!spec_rows || !spec_acc || !lb_out)) return VC_ERR_ARG;
+  if (do_crown && (!idx_all || !idx_meta)) return VC_ERR_ARG;
+  // row offsets are int32 (up to 2 x 64 rows per domain and layer), and row
+  // codes carry the domain in 25 bits
+  if (B >= ((int64_t)1 << 24)) return VC_ERR_UNSUPPORTED;
+  int maxw = 1;
+  for (int l = 1; l <= n_relu; ++l) maxw = G.d[l] > maxw ? G.d[l] : maxw;
+  RowsWork w = rows_carve(reinterpret_cast<char*>(work), n_relu, maxw, B);
+  if (!work || work_bytes < (int64_t)w.bytes) return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  RowsLayers rl{};
+  for (int l = 0; l < n_relu; ++l) {
+    rl.lo[l] = lo_in[l];
+    rl.hi[l] = hi_in[l];
+    rl.lo_out[l] = lo_out ? lo_out[l] : nullptr;
+    rl.hi_out[l] = hi_out ? hi_out[l] : nullptr;
+    if (!rl.lo[l] || !rl.hi[l] || (rl.lo_out[l] == nullptr) != (rl.hi_out[l] == nullptr))
+      return VC_ERR_ARG;
+  }
+  const void* fc = nullptr;
+  const void* fs = nullptr;
+  switch (G.variant) {
+    case 0: fc = crown_rows_fn<0>(); fs = spec_rows_fn<0>(); break;
+    case 1: fc = crown_rows_fn<1>(); fs = spec_rows_fn<1>(); break;
+    case 2: fc = crown_rows_fn<2>(); fs = spec_rows_fn<2>(); break;
+    case 3: fc = crown_rows_fn<3>(); fs = spec_rows_fn<3>(); break;
+    case 4: fc = crown_rows_fn<4>(); fs = spec_rows_fn<4>(); break;
+    case 5: fc = crown_rows_fn<5>(); fs = spec_rows_fn<5>(); break;
+    default: return VC_ERR_UNSUPPORTED;
+  }
+  const size_t lds = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float);
+  if (lds > 160 * 1024 || !vcm::allow_max_lds(fc) || !vcm::allow_max_lds(fs))
+    return VC_ERR_UNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  const int cus = vcm::cu_count();
+  const int per_cu = std::max(1, std::min(2, (int)((160 * 1024) / lds)));
+  const dim3 gchain((unsigned)(cus * per_cu)), bchain(RNW * 64);
+  const dim3 gdom((unsigned)std::min<int64_t>((B + 3) / 4, 65536)), bdom(256);
+  const int nblk = (int)((B + RSCAN - 1) / RSCAN);
+  if (do_crown) {
+    hipLaunchKernelGGL(k_rows_mask, gdom, bdom, 0, st, G, B, rl, idx_all, idx_meta, per_domain,
+                       w.masks, w.cnt, reinterpret_cast<unsigned long long*>(seed_rows));
+    hipLaunchKernelGGL(k_rows_scan1, dim3((unsigned)nblk, (unsigned)n_relu), dim3(RSCAN), 0, st,
+                       w.cnt, B, w.off, w.bsum, nblk);
+    hipLaunchKernelGGL(k_rows_scan2, dim3((unsigned)n_relu), dim3(1024), 0, st, w.bsum, nblk,
+                       w.tot);
+  }
+  // layer 0's rows; every later layer's are written by the previous cut
+  if (do_crown)
+    hipLaunchKernelGGL(k_rows_write, gdom, bdom, 0, st, B, 0, w.masks, w.off, w.bsum, nblk,
+                       w.rows);
+  const dim3 gcut((unsigned)std::min<int64_t>((B + 7) / 8, 65536));
+  for (int L = 0; L < n_relu; ++L) {
+    if (do_crown) {
+      void* args[] = {&G, (void*)&frag, (void*)&bias_cat, &B, (void*)&xl, (void*)&xh, &L,
+                      (void*)&w.rows, (void*)&w.tot, (void*)&w.slp, (void*)&w.slb};
+      if (hipLaunchKernel(fc, gchain, bchain, args, lds, st) != hipSuccess) return VC_ERR_LAUNCH;
+    }
+    const int wnext = do_crown && L + 1 < n_relu ? 1 : 0;
+    hipLaunchKernelGGL(k_rows_cut, gcut, bdom, 0, st, G, B, L, rl,
+                       do_crown ? w.masks : (const uint64_t*)nullptr, w.off, w.bsum, nblk,
+                       w.slb, w.slp, wnext, w.rows);
+  }
+  VC_LAUNCH_CHECK();
+  if (Q > 0) {
+    void* args[] = {&G, (void*)&frag, (void*)&bias_cat, &B, (void*)&xl, (void*)&xh, &Q,
+                    (void*)&spec_rows, (void*)&spec_acc, (void*)&w.slp, (void*)&lb_out,
+                    (void*)&A_out, (void*)&acc_out};
+    if (hipLaunchKernel(fs, gchain, bchain, args, lds, st) != hipSuccess) return VC_ERR_LAUNCH;
+  }
   return VC_OK;
 }
 

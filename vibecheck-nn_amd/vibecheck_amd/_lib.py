@@ -92,6 +92,9 @@ SIGNATURES = {
     'vc_mlp_tiled_alpha_run': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _I,
                                _P, _P, _P, _P, _D, _D, _D, _D, _D, _I, _D, _P, _P, _P],
     'vc_mlp_tiled_crown_mode': [_L],
+    'vc_mlp_crown_rows_workspace': [_P, _I, _L],
+    'vc_mlp_crown_rows': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
+                          _P, _P, _P, _P, _P, _P, _P, _L, _P],
     'vc_mlp_tiled_crown_noalloc': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _I, _I, _I,
                                    _P, _P, _P, _P, _P, _P],
     'vc_unstable_union_layers': [_P, _P, _P, _I, _L, _P, _P],
@@ -109,6 +112,7 @@ SIGNATURES = {
     'vc_bisect': [_P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P],
 }
 _RESTYPE = {'vc_compact_workspace': ctypes.c_int64,
+            'vc_mlp_crown_rows_workspace': ctypes.c_int64,
             'vc_mlp_bab_round_workspace': ctypes.c_int64,
             'vc_mlp_frag_floats': ctypes.c_int64,
             'vc_mlp_tiled_floats': ctypes.c_int64}
@@ -202,6 +206,7 @@ _FLOPS = {
     'vc_backward_fc': lambda a: 2.0 * a[1] * a[3] * a[11],
     'vc_mlp_crown': _flops_mlp_crown,
     'vc_mlp_tiled_crown': _flops_tiled_spec,
+    'vc_mlp_crown_rows': _flops_tiled_spec,
 }
 
 _timing = None

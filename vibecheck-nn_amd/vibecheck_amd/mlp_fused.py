@@ -22,6 +22,11 @@ PLAN_KEY = '_vc_amd_mlp_plan'
 # has an instantiation; switching this off runs vc_mlp_crown.
 TILED = True
 
+# Batches above 4 x CUs run the layer-synchronous form (vc_mlp_crown_rows:
+# rows of every domain packed into full tiles) instead of one wavefront per
+# domain; both give the same results bit for bit.
+ROWS = True
+
 # When set to a zeroed device int64 tensor (calls, MAX_L), the k-th call of
 # the shape-specialised CROWN kernel adds its seeded neurons per layer to
 # row k (work accounting; SEED_ROW is the next row).
@@ -393,10 +398,19 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False, per_domain=F
             global SEED_ROW
             seeds = SEED_COUNTER[SEED_ROW]
             SEED_ROW += 1
-        call('vc_mlp_tiled_crown', plan.dims_p, plan.n, ptr(plan.tfrag), ptr(plan.bias_cat), B,
-             ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
-             1 if do_crown else 0, 1 if per_domain else 0, Q, ptr(S), ptr(acc0), ptr(lb),
-             ptr(A), ptr(acc), ptr(seeds), plan.queue.data_ptr(), stream())
+        lib = _lib.load()
+        if ROWS and lib.vc_mlp_tiled_crown_mode(B) == 0:
+            nws = int(lib.vc_mlp_crown_rows_workspace(plan.dims_p, plan.n, B))
+            ws = torch.empty(max(nws, 8), dtype=torch.uint8, device=dev)
+            call('vc_mlp_crown_rows', plan.dims_p, plan.n, ptr(plan.tfrag), ptr(plan.bias_cat),
+                 B, ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
+                 1 if do_crown else 0, 1 if per_domain else 0, Q, ptr(S), ptr(acc0), ptr(lb),
+                 ptr(A), ptr(acc), ptr(seeds), ptr(ws), nws, stream())
+        else:
+            call('vc_mlp_tiled_crown', plan.dims_p, plan.n, ptr(plan.tfrag), ptr(plan.bias_cat),
+                 B, ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
+                 1 if do_crown else 0, 1 if per_domain else 0, Q, ptr(S), ptr(acc0), ptr(lb),
+                 ptr(A), ptr(acc), ptr(seeds), plan.queue.data_ptr(), stream())
     else:
         call('vc_mlp_crown', plan.dims_p, plan.n, ptr(plan.frag[0]), ptr(plan.bias_cat), B,
              ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
