@@ -901,6 +901,10 @@ def main():
                     help='c1 (default): the headline 65,536-box ACAS step; the others print '
                          'their own line')
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--no-secondary', action='store_true',
+                    help='after the timed steps, skip the extra pass over the rounds '
+                         '(near-zero counts, secondary rooflines, alpha rates): a profile '
+                         'of the run then holds the warm-up and timed steps only')
     ap.add_argument('--cpu-reps', type=int, default=1,
                     help='timed CPU runs of the headline step (median)')
     ap.add_argument('--copy-probe', type=int, default=0, metavar='MIB',
@@ -995,10 +999,12 @@ def main():
 
     # outside the timed region: the rounds' outputs once more, for the
     # domains inside the zero band and the other kernels' rooflines
-    kept = []
-    run_rounds(gg, xl0, xh0, se, table, keep=kept)
-    nz = [near_zero(st['lb'], st['A'], st['acc'], xl, xh) for xl, xh, st in kept]
-    secondary, alpha_rates = secondary_c1(gg, se, kept)
+    nz, secondary, alpha_rates = [None] * len(stats), None, None
+    if not args.no_secondary:
+        kept = []
+        run_rounds(gg, xl0, xh0, se, table, keep=kept)
+        nz = [near_zero(st['lb'], st['A'], st['acc'], xl, xh) for xl, xh, st in kept]
+        secondary, alpha_rates = secondary_c1(gg, se, kept)
     out = {
         'metric': 'CROWN-bounded domains/sec at 1 GPU (5-50x6-5 MLP, 65,536 domains)',
         'value': domains / per_step, 'unit': 'domains/s', 'n_gpus': 1,
@@ -1008,8 +1014,9 @@ def main():
         'config': {'workload': '5-50x6-5 ReLU MLP, 65,536 input boxes, 3 BaB rounds, '
                                'CROWN intermediate + alpha-CROWN 20 it lr 0.1 + clip + '
                                'widest split', 'domains_per_step': domains},
-        'alpha_iters_per_s': alpha_rates['open']['iters_per_s'],
-        'alpha': {'step_open_leaves': alpha_rates['open'], 'all_65536': alpha_rates['all']},
+        'alpha_iters_per_s': alpha_rates['open']['iters_per_s'] if alpha_rates else None,
+        'alpha': ({'step_open_leaves': alpha_rates['open'], 'all_65536': alpha_rates['all']}
+                  if alpha_rates else None),
         'rounds': [dict(s, near_zero=z) for s, z in zip(stats, nz)],
         'roofline': {'kernel': (crown_kernel_name(N_DOMAINS) if entry == 'vc_mlp_tiled_crown'
                                 else 'k_mlp_crown (vc_mlp_crown)')

@@ -496,8 +496,12 @@ int vc_mlp_tiled_crown(const int32_t *dims, int n_relu, const float *frag,
  * (vc_mlp_crown_rows_workspace(dims, n_relu, B) bytes: masks, row offsets,
  * row lists and bounds of one layer, and the slopes of every layer, 512 B
  * per domain and layer).  lo_out/hi_out: nullable (both or neither).
- * B < 2^25.  Replaces _crown_intermediate_batched + the spec backward
- * (verify_zono_bnb.py:4077-4147, 4270-4453, 5117-5134) for narrow MLPs. */
+ * idx_all/idx_meta: the union lists of vc_union_compact, or null: then the
+ * union of the neurons unstable in some domain (lo < 0 < hi) is formed here,
+ * in the same pass over the bounds that builds the per-domain seed masks
+ * (the same union, so the same results).  B < 2^24.  Replaces
+ * _crown_intermediate_batched + the spec backward (verify_zono_bnb.py:
+ * 4077-4147, 4270-4453, 5117-5134) for narrow MLPs. */
 int64_t vc_mlp_crown_rows_workspace(const int32_t *dims, int n_relu, int64_t B);
 int vc_mlp_crown_rows(const int32_t *dims, int n_relu, const float *frag,
                       const float *bias_cat, int64_t B, const float *xl,

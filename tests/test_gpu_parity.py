@@ -609,8 +609,10 @@ def test_crown_rows_layout_bit_exact(gpu, monkeypatch, net, B, scale):
     domains packed into full tiles, one launch per layer) instead of one
     wavefront per domain.  Both give bit-identical spec bounds, A, acc and
     CROWN bounds, with per-domain and union seeding and without the CROWN
-    pass (spec backward only).  Nets cover every tile shape: 16, 32, 48 and
-    64 neurons, with and without a spare bias column."""
+    pass (spec backward only), whether the rows form builds the union of
+    unstable neurons in its own mask pass or is given the union lists.  Nets
+    cover every tile shape: 16, 32, 48 and 64 neurons, with and without a
+    spare bias column."""
     from vibecheck_amd import _lib, mlp_fused as mf
     assert _lib.load().vc_mlp_tiled_crown_mode(B) == 0, 'batch too small for the rows path'
     gg, xl, xh, n_out = _rows_case(gpu, net, B, scale)
@@ -622,17 +624,23 @@ def test_crown_rows_layout_bit_exact(gpu, monkeypatch, net, B, scale):
     sb = vz._zono_sb(gg, xl, xh, gpu, F32)
     for do_crown, per_domain in ((True, True), (True, False), (False, False)):
         out = {}
-        for rows in (False, True):
+        # tiled; rows with the union formed in its mask pass; rows given the
+        # union lists
+        for key, rows, own in (('tiled', False, True), ('own', True, True),
+                               ('lists', True, False)):
             monkeypatch.setattr(mf, 'ROWS', rows)
-            out[rows] = mf.crown(plan, xl, xh, sb, do_crown, spec=(Wq, bq), want_linear=True,
-                                 per_domain=per_domain)
-        (tt, *lin_t), (tr, *lin_r) = out[False], out[True]
-        for nm, a, b in zip(('lb', 'A', 'acc'), lin_r, lin_t):
-            assert torch.equal(a, b), (nm, do_crown, per_domain, int((a != b).sum()))
-        if do_crown:
-            for L in tt:
-                for k in (0, 1):
-                    assert torch.equal(tr[L][k], tt[L][k]), (L, k, per_domain)
+            monkeypatch.setattr(mf, 'ROWS_OWN_UNION', own)
+            out[key] = mf.crown(plan, xl, xh, sb, do_crown, spec=(Wq, bq), want_linear=True,
+                                per_domain=per_domain)
+        tt, *lin_t = out['tiled']
+        for key in ('own', 'lists'):
+            tr, *lin_r = out[key]
+            for nm, a, b in zip(('lb', 'A', 'acc'), lin_r, lin_t):
+                assert torch.equal(a, b), (key, nm, do_crown, per_domain, int((a != b).sum()))
+            if do_crown:
+                for L in tt:
+                    for k in (0, 1):
+                        assert torch.equal(tr[L][k], tt[L][k]), (key, L, k, per_domain)
 
 
 def test_crown_intermediate_parity_mlp_chunked(gpu):

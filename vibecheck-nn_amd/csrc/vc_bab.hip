@@ -214,14 +214,17 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
   VC_TRY(vc_compact(r.ovf, B, 0, r.idx, r.cnt, r.cws, r.cws_bytes, stream));
   VC_TRY(vc_mlp_tiled_zono_wide(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
                                 r.idx, r.cnt, stream));
-  VC_TRY(vc_unstable_union_layers(r.sb_lo, r.sb_hi, widths, n, B, r.uflags, stream));
-  VC_TRY(vc_union_compact(r.uflags, widths, n, r.uidx, r.umeta, stream));
+  // the rows form builds the union in its own pass over the bounds
+  if (!r.rws) {
+    VC_TRY(vc_unstable_union_layers(r.sb_lo, r.sb_hi, widths, n, B, r.uflags, stream));
+    VC_TRY(vc_union_compact(r.uflags, widths, n, r.uidx, r.umeta, stream));
+  }
   if (crown_ev0 && hipEventRecord((hipEvent_t)crown_ev0, st) != hipSuccess) return VC_ERR_LAUNCH;
   // the round reads only the spec bound of the CROWN pass (alpha restarts
   // from the zonotope bounds): the rows form writes no CROWN bounds
   if (r.rws)
     VC_TRY(vc_mlp_crown_rows(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, nullptr,
-                             nullptr, r.uidx, r.umeta, 1, 1, Q, spec_rows, spec_acc, lb, A, acc,
+                             nullptr, nullptr, nullptr, 1, 1, Q, spec_rows, spec_acc, lb, A, acc,
                              seed_rows, r.rws, r.rws_bytes, stream));
   else
     VC_TRY(vc_mlp_tiled_crown(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.t_lo,

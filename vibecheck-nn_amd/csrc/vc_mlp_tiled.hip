@@ -2036,71 +2036,105 @@ struct RowsLayers {
   float* hi_out[MAXL];
 };
 
-// One wavefront per domain: for every layer, the union neurons it seeds
-// (per_domain: only those with lo < 0 and hi > -1e-7 in this domain, the
-// filter of k_crown_tiled) as a bit mask, and 2 m rows.  The union lists
-// (idx_all, idx_meta of vc_union_compact) become per-layer masks in LDS.
-__global__ __launch_bounds__(256) void k_rows_mask(TGeom G, int64_t B, RowsLayers rl,
-                                                   const int32_t* __restrict__ idx_all,
+// The union of unstable neurons per layer as a bit mask, umask[L]: from
+// the caller's lists (idx_all, idx_meta of vc_union_compact), or, with no
+// lists, cleared here for k_rows_mask to OR into.  One wavefront.
+__global__ __launch_bounds__(64) void k_rows_union(TGeom G, const int32_t* __restrict__ idx_all,
                                                    const int32_t* __restrict__ idx_meta,
-                                                   int per_domain, uint64_t* __restrict__ masks,
-                                                   int32_t* __restrict__ cnt,
-                                                   unsigned long long* __restrict__ seed_rows) {
-  __shared__ uint64_t umask[MAXL];
-  __shared__ int scnt[MAXL];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+                                                   unsigned long long* __restrict__ umask) {
+  const int lane = threadIdx.x;
   const int n = G.n;
-  if (wv == 0) {
-    for (int L = 0; L < n; ++L) {
-      // bit j of the union mask for every listed neuron j (an OR over the wave)
+  for (int L = 0; L < n; ++L) {
+    unsigned long long v = 0ull;
+    if (idx_all) {
+      // bit j for every listed neuron j (an OR over the wave)
       const int c = min(idx_meta[L], G.d[L + 1]);
       const int j = lane < c ? idx_all[idx_meta[n + L] + lane] : 0;
-      unsigned long long v = (lane < c && j >= 0 && j < FW) ? (1ull << j) : 0ull;
+      v = (lane < c && j >= 0 && j < FW) ? (1ull << j) : 0ull;
       for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
-      if (lane == 0) umask[L] = v;
     }
-    if (lane < MAXL) scnt[lane] = 0;
+    if (lane == 0) umask[L] = v;
   }
+}
+
+// Per domain and layer, the neurons this domain would seed (per_domain:
+// lo < 0 and hi > -1e-7, the filter of k_crown_tiled; else every neuron)
+// as a bit mask, before the union is applied (k_rows_scan1 does that).
+// With want_union, the neurons unstable here (lo < 0 < hi) are ORed into
+// umask: per wavefront over its domains, per workgroup through LDS, then
+// one atomic per workgroup and layer.  Persistent: each wavefront takes two
+// domains at a time, all their loads issued before any is used (NL >= n
+// layers' worth of registers).
+template <int NL>
+__global__ __launch_bounds__(256) void k_rows_mask(TGeom G, int64_t B, RowsLayers rl,
+                                                   int per_domain, int want_union,
+                                                   uint64_t* __restrict__ masks,
+                                                   unsigned long long* __restrict__ umask) {
+  __shared__ unsigned long long wu[MAXL];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int n = G.n;
+  if (threadIdx.x < MAXL) wu[threadIdx.x] = 0ull;
   __syncthreads();
-  for (int64_t d = (int64_t)blockIdx.x * 4 + wv; d < B; d += (int64_t)gridDim.x * 4) {
-    // every layer's bounds requested before any is used
-    float lo[MAXL], hi[MAXL];
+  const bool need = per_domain || want_union;
+  uint64_t un[NL];
 #pragma unroll
-    for (int L = 0; L < MAXL; ++L) {
-      const int dW = L < n ? G.d[L + 1] : 0;
-      const bool rd = per_domain && lane < dW;
-      lo[L] = rd ? rl.lo[L][d * dW + lane] : 0.f;
-      hi[L] = rd ? rl.hi[L][d * dW + lane] : 0.f;
+  for (int L = 0; L < NL; ++L) un[L] = 0ull;
+  const int64_t stride = (int64_t)gridDim.x * 8;
+  for (int64_t d0 = ((int64_t)blockIdx.x * 4 + wv) * 2; d0 < B; d0 += stride) {
+    float lo[2][NL], hi[2][NL];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int64_t d = d0 + k;
+#pragma unroll
+      for (int L = 0; L < NL; ++L) {
+        const int dW = L < n ? G.d[L + 1] : 0;
+        const bool rd = need && d < B && lane < dW;
+        lo[k][L] = rd ? rl.lo[L][d * dW + lane] : 0.f;
+        hi[k][L] = rd ? rl.hi[L][d * dW + lane] : 0.f;
+      }
     }
 #pragma unroll
-    for (int L = 0; L < MAXL; ++L) {
-      if (L >= n) break;
-      const int dW = G.d[L + 1];
-      const bool inu = lane < dW && ((umask[L] >> lane) & 1ull);
-      const bool keep = inu && (!per_domain || (lo[L] < 0.f && hi[L] > -1e-7f));
-      const uint64_t m = __ballot(keep);
-      if (lane == 0) {
-        masks[(int64_t)L * B + d] = m;
-        cnt[(int64_t)L * B + d] = 2 * __popcll(m);
-        if (seed_rows && m) atomicAdd(&scnt[L], __popcll(m));
+    for (int k = 0; k < 2; ++k) {
+      const int64_t d = d0 + k;
+      if (d >= B) break;
+#pragma unroll
+      for (int L = 0; L < NL; ++L) {
+        if (L >= n) break;
+        const bool in = lane < G.d[L + 1];
+        const bool keep = in && (!per_domain || (lo[k][L] < 0.f && hi[k][L] > -1e-7f));
+        const uint64_t m = __ballot(keep);
+        un[L] |= __ballot(in && lo[k][L] < 0.f && hi[k][L] > 0.f);
+        if (lane == 0) masks[(int64_t)L * B + d] = m;
       }
     }
   }
-  __syncthreads();
-  if (seed_rows && threadIdx.x < n && scnt[threadIdx.x])
-    atomicAdd(seed_rows + threadIdx.x, (unsigned long long)scnt[threadIdx.x]);
+  if (want_union) {
+    if (lane == 0)
+      for (int L = 0; L < n; ++L)
+        if (un[L]) atomicOr(&wu[L], (unsigned long long)un[L]);
+    __syncthreads();
+    if (threadIdx.x < n && wu[threadIdx.x]) atomicOr(umask + threadIdx.x, wu[threadIdx.x]);
+  }
 }
 
-// Exclusive scan of the row counts, per layer (blockIdx.y): within blocks
-// of RSCAN domains (offsets local to the block), block totals to bsum.
-__global__ __launch_bounds__(RSCAN) void k_rows_scan1(const int32_t* __restrict__ cnt, int64_t B,
-                                                      int32_t* __restrict__ off,
+// Per layer (blockIdx.y), within blocks of RSCAN domains: the seeded
+// neurons m = mask & umask[L] (written back to masks), and the exclusive
+// scan of the row counts 2 |m| (offsets local to the block), block totals
+// to bsum.
+__global__ __launch_bounds__(RSCAN) void k_rows_scan1(uint64_t* __restrict__ masks,
+                                                      const unsigned long long* __restrict__ umask,
+                                                      int64_t B, int32_t* __restrict__ off,
                                                       int32_t* __restrict__ bsum, int nblk) {
   __shared__ int wsum[RSCAN / 64];
   const int L = blockIdx.y;
   const int64_t i = (int64_t)blockIdx.x * RSCAN + threadIdx.x;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int v = i < B ? cnt[(int64_t)L * B + i] : 0;
+  int v = 0;
+  if (i < B) {
+    const uint64_t m = masks[(int64_t)L * B + i] & (uint64_t)umask[L];
+    masks[(int64_t)L * B + i] = m;
+    v = 2 * __popcll(m);
+  }
   int x = v;  // inclusive scan within the wave
   for (int o = 1; o < 64; o <<= 1) {
     const int y = __shfl_up(x, o, 64);
@@ -2123,9 +2157,11 @@ __global__ __launch_bounds__(RSCAN) void k_rows_scan1(const int32_t* __restrict_
 }
 
 // Per layer (blockIdx.x): exclusive scan of the block totals in place, the
-// layer's row total to tot[L].
+// layer's row total to tot[L] and, when counted, its seeded neurons (half
+// the rows) added to seed_rows[L].
 __global__ __launch_bounds__(1024) void k_rows_scan2(int32_t* __restrict__ bsum, int nblk,
-                                                     int32_t* __restrict__ tot) {
+                                                     int32_t* __restrict__ tot,
+                                                     unsigned long long* __restrict__ seed_rows) {
   __shared__ int wsum[16];
   __shared__ int carry;
   const int L = blockIdx.x;
@@ -2157,7 +2193,10 @@ __global__ __launch_bounds__(1024) void k_rows_scan2(int32_t* __restrict__ bsum,
     if (threadIdx.x == 0) carry += wsum[15];
     __syncthreads();
   }
-  if (threadIdx.x == 0) tot[L] = carry;
+  if (threadIdx.x == 0) {
+    tot[L] = carry;
+    if (seed_rows) atomicAdd(seed_rows + L, (unsigned long long)(carry / 2));
+  }
 }
 
 // The row codes of layer L: domain d's rows start at its offset, the m
@@ -2410,7 +2449,7 @@ const void* spec_rows_fn() {
 // The workspace of vc_mlp_crown_rows, carved in order (256-byte aligned).
 struct RowsWork {
   uint64_t* masks;  // [n][B]
-  int32_t* cnt;     // [n][B]
+  unsigned long long* umask;  // [MAXL]
   int32_t* off;     // [n][B]
   int32_t* bsum;    // [n][nblk]
   int32_t* tot;     // [n]
@@ -2430,7 +2469,7 @@ RowsWork rows_carve(char* base, int n, int maxw, int64_t B) {
   };
   const int nblk = (int)((B + RSCAN - 1) / RSCAN);
   w.masks = reinterpret_cast<uint64_t*>(take(sizeof(uint64_t) * n * B));
-  w.cnt = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * n * B));
+  w.umask = reinterpret_cast<unsigned long long*>(take(sizeof(unsigned long long) * MAXL));
   w.off = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * n * B));
   w.bsum = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * n * (size_t)nblk));
   w.tot = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * n));
@@ -2468,7 +2507,7 @@ extern "C" int vc_mlp_crown_rows(const int32_t* dims, int n_relu, const float* f
   if (!frag || !bias_cat || !xl || !xh || !lo_in || !hi_in || B < 0) return VC_ERR_ARG;
   if (Q < 0 || Q > TQMAX) return VC_ERR_UNSUPPORTED;
   if (Q > 0 && (!spec_rows || !spec_acc || !lb_out)) return VC_ERR_ARG;
-  if (do_crown && (!idx_all || !idx_meta)) return VC_ERR_ARG;
+  if (idx_all && !idx_meta) return VC_ERR_ARG;
   // row offsets are int32 (up to 2 x 64 rows per domain and layer), and row
   // codes carry the domain in 25 bits
   if (B >= ((int64_t)1 << 24)) return VC_ERR_UNSUPPORTED;
@@ -2506,13 +2545,20 @@ extern "C" int vc_mlp_crown_rows(const int32_t* dims, int n_relu, const float* f
   const dim3 gchain((unsigned)(cus * per_cu)), bchain(RNW * 64);
   const dim3 gdom((unsigned)std::min<int64_t>((B + 3) / 4, 65536)), bdom(256);
   const int nblk = (int)((B + RSCAN - 1) / RSCAN);
+  // the mask pass: persistent, 8 domains per workgroup per sweep
+  const dim3 gmask((unsigned)std::max<int64_t>(1, std::min<int64_t>((B + 7) / 8, (int64_t)cus * 8)));
   if (do_crown) {
-    hipLaunchKernelGGL(k_rows_mask, gdom, bdom, 0, st, G, B, rl, idx_all, idx_meta, per_domain,
-                       w.masks, w.cnt, reinterpret_cast<unsigned long long*>(seed_rows));
+    hipLaunchKernelGGL(k_rows_union, dim3(1), dim3(64), 0, st, G, idx_all, idx_meta, w.umask);
+    if (n_relu <= 8)
+      hipLaunchKernelGGL(k_rows_mask<8>, gmask, bdom, 0, st, G, B, rl, per_domain,
+                         idx_all ? 0 : 1, w.masks, w.umask);
+    else
+      hipLaunchKernelGGL(k_rows_mask<MAXL>, gmask, bdom, 0, st, G, B, rl, per_domain,
+                         idx_all ? 0 : 1, w.masks, w.umask);
     hipLaunchKernelGGL(k_rows_scan1, dim3((unsigned)nblk, (unsigned)n_relu), dim3(RSCAN), 0, st,
-                       w.cnt, B, w.off, w.bsum, nblk);
+                       w.masks, w.umask, B, w.off, w.bsum, nblk);
     hipLaunchKernelGGL(k_rows_scan2, dim3((unsigned)n_relu), dim3(1024), 0, st, w.bsum, nblk,
-                       w.tot);
+                       w.tot, reinterpret_cast<unsigned long long*>(seed_rows));
   }
   // layer 0's rows; every later layer's are written by the previous cut
   if (do_crown)

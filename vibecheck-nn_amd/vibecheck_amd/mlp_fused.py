@@ -27,6 +27,11 @@ TILED = True
 # domain; both give the same results bit for bit.
 ROWS = True
 
+# The rows form builds the union of unstable neurons itself (in its seed-mask
+# pass over the bounds); switching this off hands it the union lists of
+# vc_unstable_union_layers + vc_union_compact instead (same results).
+ROWS_OWN_UNION = True
+
 # When set to a zeroed device int64 tensor (calls, MAX_L), the k-th call of
 # the shape-specialised CROWN kernel adds its seeded neurons per layer to
 # row k (work accounting; SEED_ROW is the next row).
@@ -361,8 +366,12 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False, per_domain=F
     idx_t = None
     cnt_p = None
     tiled = _tiled(plan)
+    lib = _lib.load()
+    rows = tiled and ROWS and lib.vc_mlp_tiled_crown_mode(B) == 0
     if do_crown:
-        if tiled:
+        if rows and ROWS_OWN_UNION:
+            pass  # the rows form builds the union in its own pass over the bounds
+        elif tiled:
             # union of the unstable sets and its index lists, on the device
             nw = sum(plan.dims[1:])
             flags = torch.empty(nw, dtype=torch.uint8, device=dev)
@@ -398,8 +407,7 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False, per_domain=F
             global SEED_ROW
             seeds = SEED_COUNTER[SEED_ROW]
             SEED_ROW += 1
-        lib = _lib.load()
-        if ROWS and lib.vc_mlp_tiled_crown_mode(B) == 0:
+        if rows:
             nws = int(lib.vc_mlp_crown_rows_workspace(plan.dims_p, plan.n, B))
             ws = torch.empty(max(nws, 8), dtype=torch.uint8, device=dev)
             call('vc_mlp_crown_rows', plan.dims_p, plan.n, ptr(plan.tfrag), ptr(plan.bias_cat),
