@@ -864,6 +864,30 @@ def run_config(cfg, steps, warmup, cpu):
     torch.cuda.synchronize()
     per_step = (time.perf_counter() - t0) / steps
     line.update(value=B / per_step, ms_per_step=1e3 * per_step)
+    # alpha's own rates at the configuration's batch (outside the timed step)
+    if cfg == 'c2':
+        sb = vz._crown_intermediate_batched(gg, xl, xh, dev, F)
+        res = {}
+
+        def alpha_only():
+            _, res['n'] = vz._run_alpha_crown_inputsplit_batched(
+                xl, xh, gg, se, dev, F, n_iters=10, lr=0.25, sb=sb, return_trace=True)
+        sec = _timed(alpha_only, 3)
+        line['alpha'] = {'domains': B, 'iters': int(res['n']), 'ms': 1e3 * sec,
+                         'iters_per_s': res['n'] / sec, 'domain_iters_per_s': B * res['n'] / sec,
+                         'sample': 'the alpha-CROWN loop alone from the step\'s CROWN bounds'}
+    elif cfg == 'c4':
+        res = {}
+
+        def ab_only():
+            _, res['n'] = vm._ibp_crown_bab_bound(gg, xl, xh, root, cl, se, dev, F,
+                                                  alpha_iters=10, lr=0.25, return_trace=True)
+        sec = _timed(ab_only, 3)
+        line['alpha_beta'] = {'domains': B, 'iters': int(res['n']), 'ms': 1e3 * sec,
+                              'iters_per_s': res['n'] / sec,
+                              'domain_iters_per_s': B * res['n'] / sec,
+                              'sample': 'the whole bound call: IBP with the split clamps, '
+                                        'then the joint alpha/beta iterations'}
     if cfg == 'c0':
         seeded = torch.zeros(steps + 4, 16, dtype=torch.int64, device=dev)
         mf.SEED_COUNTER, mf.SEED_ROW = seeded, 0

@@ -22,3 +22,21 @@ def gpu():
     from vibecheck_amd import _lib
     _lib.load()
     return torch.device('cuda:0')
+
+
+def pytest_terminal_summary(terminalreporter):
+    """The escape counts of the GPU bound comparisons (entries within the
+    tolerance only relative to their scale, or only as close to fp64 as the
+    fp32 oracle), summed over the run."""
+    mod = sys.modules.get('test_gpu_parity')
+    esc = getattr(mod, 'ESCAPES', None)
+    if not esc:
+        return
+    n = sum(e[3] for e in esc)
+    n_sc = sum(e[1] for e in esc)
+    n_64 = sum(e[2] for e in esc)
+    worst = max(esc, key=lambda e: (e[1] + e[2]) / max(1, e[3]))
+    terminalreporter.write_line(
+        f'bound comparisons: {len(esc)} calls, {n} entries; escapes: {n_sc} by scale, '
+        f'{n_64} by fp64 ({100.0 * (n_sc + n_64) / max(1, n):.4f}%); worst call '
+        f'{worst[0]!r}: {worst[1] + worst[2]} of {worst[3]}')
