@@ -122,6 +122,50 @@ int vc_zono_relu_apply(const float *c, const float *G, const float *lo,
                        int K, int K_new, float *c_out, float *G_out,
                        vc_stream_t stream);
 
+/* ---- add / sub / mul ops (constant and residual merge) --------------- */
+
+/* out = x + v (mode 0), x - v (mode 1) or x * v (mode 2), elementwise over
+ * x of outer x n x inner floats; element i of the n is (t / inner) % n and
+ * its constant v[i] (nv == n) or v[0] (nv == 1).  inner = 1 for (B, n)
+ * rows, K for (B, n, K) generators.  Replaces the constant add and sub of
+ * the interval forward (verify_zono_bnb.py:1136-1143), the zonotope's add
+ * and sub of the centre (3235-3265) and mul of centre and generators
+ * (3501-3536), and the backward's mul, ew * scale (4686-4712). */
+int vc_affine_ew(const float *x, int64_t outer, int n, int64_t inner,
+                 const float *v, int nv, int mode, float *out,
+                 vc_stream_t stream);
+
+/* Interval times a constant (B, n): lo = min(s l, s h), hi = max(s l, s h)
+ * with torch.minimum / torch.maximum's NaN and tie rules; s scalar
+ * (ns == 1) or per element (ns == n).  Replaces the mul branch of
+ * _ibp_forward_graph_batched (verify_zono_bnb.py:1144-1148). */
+int vc_interval_mul(const float *l, const float *h, int64_t B, int n,
+                    const float *s, int ns, float *lo, float *hi,
+                    vc_stream_t stream);
+
+/* out = a + b over total floats: a residual merge's interval bounds and
+ * zonotope centre (verify_zono_bnb.py:1133-1135, 3213-3234), and the sum
+ * of backward rows arriving at a fork point from two consumers
+ * (ew_at[inp] + ew, verify_zono_bnb.py:4462-4469). */
+int vc_add_ew(const float *a, const float *b, int64_t total, float *out,
+              vc_stream_t stream);
+
+/* Generators of a residual merge, rows = B * n: Gout (rows, Ka + Kb -
+ * shared) = [Ga[:, :shared] + Gb[:, :shared] | Ga[:, shared:] |
+ * Gb[:, shared:]]; `shared` is the generator count at the branches' fork
+ * point (_find_shared_gens_count).  Replaces verify_zono_bnb.py:3213-3234. */
+int vc_zono_merge(const float *Ga, int Ka, const float *Gb, int Kb, int shared,
+                  int64_t rows, float *Gout, vc_stream_t stream);
+
+/* acc[m] += sign * sum_i ew[row, i] v[i] over M rows of n (row = m, or
+ * m % R when shared: rows common to every domain), the products in fp32
+ * summed in fp64: the constant add's (sign 1) and sub's (sign -1)
+ * contribution to the backward's constant term.  Replaces
+ * verify_zono_bnb.py:4469-4504 and 4506-4518. */
+int vc_rows_bias_dot(const float *ew, int64_t M, int R, int n, int shared,
+                     const float *v, int nv, float sign, float *acc,
+                     vc_stream_t stream);
+
 /* ---- CROWN backward -------------------------------------------------- */
 
 /* One backward step through [relu ->] fc, fused.

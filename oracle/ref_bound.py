@@ -2,9 +2,12 @@
 
 Test infrastructure: see the package docstring.  Each function follows the
 reference function named in its docstring (paths relative to
-src/vibecheck/ of the reference).  Supported ops: fc, relu, conv, reshape --
-the op set of the Linear/Conv/ReLU networks this engine targets.  Anything
-else raises NotImplementedError, as the reference does for unsupported ops.
+src/vibecheck/ of the reference).  Supported ops: fc, relu, conv, reshape,
+and add (a constant, or the residual merge of two live inputs), sub and mul
+by constants -- the op set of the Linear/Conv/ReLU networks this engine
+targets, with the affine ops the reference's ONNX reader emits around them.
+Anything else raises NotImplementedError, as the reference does for
+unsupported ops.
 """
 import torch
 import torch.nn.functional as F
@@ -34,6 +37,67 @@ def _unsupported(fn, op):
         f'{fn}: unsupported op {op["type"]!r} at {op["name"]!r}')
 
 
+def _const(op, key, n, dt):
+    """An add/sub 'bias' or a mul 'scale' as a flat tensor broadcastable
+    against n values: the float64 constant rounded to dt, one value or n;
+    otherwise a per-channel scale (in_shapes_nd (C, H, W),
+    verify_zono_bnb.py:3523-3534) or a trailing-dimension vector
+    (out_shape_nd, :3240-3251, :4490-4503) spelled out to n values."""
+    v = op.get(key)
+    if v is None:
+        return None
+    t = torch.as_tensor(v, dtype=dt).reshape(-1)
+    if t.numel() in (1, n):
+        return t
+    shp_in = (op.get('in_shapes_nd') or [None])[0]
+    shp_out = op.get('out_shape_nd')
+    if key == 'scale' and shp_in is not None and len(shp_in) == 3 and shp_in[0] == t.numel():
+        C, H, W = shp_in
+        return t.view(C, 1, 1).expand(C, H, W).reshape(-1)
+    if shp_out is not None and shp_out[-1] == t.numel():
+        return t.reshape(*([1] * (len(shp_out) - 1)), -1).expand(*shp_out).reshape(-1)
+    raise ValueError(f'{op["name"]}: {key} does not broadcast to {n} values')
+
+
+def fork_points(gg):
+    """Names consumed by more than one op (network.py:1713's 'fork_points'),
+    from the gg when present."""
+    if gg.get('fork_points') is not None:
+        return gg['fork_points']
+    cnt = {}
+    for op in gg['ops']:
+        for i in op['inputs']:
+            cnt[i] = cnt.get(i, 0) + 1
+    return {k for k, c in cnt.items() if c > 1}
+
+
+def shared_gens_count(name_a, name_b, gg, gen_count):
+    """_find_shared_gens_count (verify_zono_bnb.py:2387-2428): walk name_a's
+    ancestors depth-first (a stack, each node's inputs pushed in order); the
+    first one that is an ancestor of name_b and a fork point gives its
+    generator count; none: the input's."""
+    forks = fork_points(gg)
+    pred = {op['name']: op['inputs'] for op in gg['ops']}
+
+    def walk(name):
+        out, stack, seen = [], [name], set()
+        while stack:
+            x = stack.pop()
+            if x in seen:
+                continue
+            seen.add(x)
+            out.append(x)
+            for i in pred.get(x, []):
+                stack.append(i)
+        return out
+
+    in_b = set(walk(name_b))
+    for x in walk(name_a):
+        if x in in_b and x in forks:
+            return gen_count.get(x, 0)
+    return gen_count.get(gg['input_name'], 0)
+
+
 def point_forward(x, gg):
     """Concrete forward of a batch of points x (P, n_in).
 
@@ -59,6 +123,14 @@ def point_forward(x, gg):
             act[op['name']] = a.clamp(min=0)
         elif t == 'reshape':
             act[op['name']] = a
+        elif t == 'add' and op.get('is_merge'):
+            act[op['name']] = a + act[op['inputs'][1]]
+        elif t == 'add':
+            act[op['name']] = a + _const(op, 'bias', a.shape[1], a.dtype)
+        elif t == 'sub':
+            act[op['name']] = a - _const(op, 'bias', a.shape[1], a.dtype)
+        elif t == 'mul':
+            act[op['name']] = a * _const(op, 'scale', a.shape[1], a.dtype)
         else:
             _unsupported('point_forward', op)
     return act[gg['ops'][-1]['name']], pre
@@ -109,6 +181,19 @@ def ibp_forward_batched(xl, xh, gg, relu_clamps=None, root_sb=None):
             lo[name], hi[name] = l.clamp(min=0), h.clamp(min=0)
         elif t == 'reshape':
             lo[name], hi[name] = l, h
+        elif t == 'add' and op.get('is_merge'):
+            # verify_zono_bnb.py:1133-1135
+            lo[name] = l + lo[op['inputs'][1]]
+            hi[name] = h + hi[op['inputs'][1]]
+        elif t in ('add', 'sub'):
+            # verify_zono_bnb.py:1136-1143
+            b = _const(op, 'bias', l.shape[1], l.dtype)
+            lo[name], hi[name] = (l + b, h + b) if t == 'add' else (l - b, h - b)
+        elif t == 'mul':
+            # verify_zono_bnb.py:1144-1148
+            sc = _const(op, 'scale', l.shape[1], l.dtype)
+            p, q = sc * l, sc * h
+            lo[name], hi[name] = torch.minimum(p, q), torch.maximum(p, q)
         else:
             _unsupported('ibp_forward_batched', op)
     return sb
@@ -137,12 +222,34 @@ def zono_forward_batched(xl, xh, gg):
         G = torch.zeros(B, n_in, K, dtype=dt)
         G[:, vidx, torch.arange(K)] = radii[:, vidx]
     state = {gg['input_name']: (c, G)}
+    gen_count = {gg['input_name']: K}
     sb = {}
     for op in gg['ops']:
         t = op['type']
         name = op['name']
         c_in, G_in = state[op['inputs'][0]]
-        if t == 'fc':
+        if t == 'add' and op.get('is_merge'):
+            # verify_zono_bnb.py:3213-3234: shared columns summed, then a's
+            # own columns, then b's
+            c_b, G_b = state[op['inputs'][1]]
+            sh = shared_gens_count(op['inputs'][0], op['inputs'][1], gg, gen_count)
+            Ka, Kb = G_in.shape[2], G_b.shape[2]
+            assert 0 <= sh <= Ka and 0 <= sh <= Kb
+            G_out = torch.cat([G_in[:, :, :sh] + G_b[:, :, :sh], G_in[:, :, sh:],
+                               G_b[:, :, sh:]], dim=2)
+            state[name] = (c_in + c_b, G_out)
+        elif t in ('add', 'sub'):
+            # verify_zono_bnb.py:3235-3265: the centre moves
+            b = _const(op, 'bias', c_in.shape[1], dt)
+            if b is not None:
+                c_in = c_in + b if t == 'add' else c_in - b
+            state[name] = (c_in, G_in)
+        elif t == 'mul':
+            # verify_zono_bnb.py:3501-3536
+            sc = _const(op, 'scale', c_in.shape[1], dt)
+            state[name] = (c_in * sc, G_in * sc.reshape(1, -1, 1)
+                           if sc.numel() > 1 else G_in * sc)
+        elif t == 'fc':
             W = op['W']
             state[name] = (c_in @ W.T + op['bias'],
                            torch.einsum('oi,bik->bok', W, G_in))
@@ -192,6 +299,7 @@ def zono_forward_batched(xl, xh, gg):
             state[name] = (c_in, G_in)
         else:
             _unsupported('zono_forward_batched', op)
+        gen_count[name] = state[name][1].shape[2]
     return sb, state[gg['ops'][-1]['name']]
 
 
@@ -275,6 +383,20 @@ def spec_backward_batched(tight, xl, xh, gg, spec_ew=None,
         elif t == 'reshape':
             prev = ew_at.get(op['inputs'][0])
             ew_at[op['inputs'][0]] = ew.clone() if prev is None else prev + ew
+        elif t == 'add' and op.get('is_merge'):
+            # verify_zono_bnb.py:4462-4469: to both inputs, no constant
+            for i in op['inputs']:
+                _put(i, ew.clone())
+        elif t in ('add', 'sub'):
+            # verify_zono_bnb.py:4470-4518: acc +/-= (ew * bias).sum
+            b = _const(op, 'bias', ew.shape[-1], dt)
+            if b is not None:
+                term = (ew * b).sum(dim=-1)
+                acc = acc + term if t == 'add' else acc - term
+            _put(op['inputs'][0], ew.clone())
+        elif t == 'mul':
+            # verify_zono_bnb.py:4686-4712
+            _put(op['inputs'][0], ew * _const(op, 'scale', ew.shape[-1], dt))
         else:
             _unsupported('spec_backward_batched', op)
 

@@ -526,3 +526,162 @@ def test_alpha_early_stop_on_global_max():
     spec = {0: (_t([-1.0]), 0.0)}
     _, n = rb.alpha_crown_batched(xl, xh, gg, spec, n_iters=20, return_trace=True)
     assert n == 2
+
+
+# ---------------------------------------------------------------- add / sub / mul
+def _affine_gg(ops, n_in):
+    return wk._finish(ops, n_in, (1, n_in))
+
+
+def _fc(name, inp, W, b):
+    return {'name': name, 'type': 'fc', 'inputs': [inp], 'W': _t(W), 'bias': _t(b)}
+
+
+def test_affine_ops_hand_computed():
+    """x in [1, 3]; z = (-2 x + 5) - 0.5 = -2 x + 4.5 in [-1.5, 2.5]; y =
+    relu(z).  IBP and the zonotope give [-1.5, 2.5] (the zonotope: c = 2,
+    G = 1, then -4 / -2, +5, -0.5).  The CROWN bound of y uses the lower
+    slope 1 (2.5 > 1.5): y >= z = -2 x + 4.5, so A = -2, acc = 4.5,
+    lb = -1.5; of -y the upper line 0.625 z + 0.9375: A = 1.25,
+    acc = -3.75, lb = -2.5 = -max y (verify_zono_bnb.py:1136-1148,
+    3235-3265, 3501-3536, 4470-4518, 4686-4712)."""
+    ops = [{'name': 'm', 'type': 'mul', 'inputs': [wk.INPUT_NAME], 'scale': np.array([-2.0])},
+           {'name': 'a', 'type': 'add', 'inputs': ['m'], 'is_merge': False,
+            'bias': np.array([5.0])},
+           {'name': 's', 'type': 'sub', 'inputs': ['a'], 'bias': np.array([0.5])},
+           {'name': 'r', 'type': 'relu', 'inputs': ['s'], 'layer_idx': 0},
+           _fc('f', 'r', [[1.0]], [0.0])]
+    gg = _affine_gg(ops, 1)
+    xl, xh = _t([[1.0]]), _t([[3.0]])
+    sb = rb.ibp_forward_batched(xl, xh, gg)
+    assert torch.equal(sb[0][0], _t([[-1.5]])) and torch.equal(sb[0][1], _t([[2.5]]))
+    sbz, (c, G) = rb.zono_forward_batched(xl, xh, gg)
+    assert torch.equal(sbz[0][0], _t([[-1.5]])) and torch.equal(sbz[0][1], _t([[2.5]]))
+    spec = {0: (_t([1.0]), 0.0), 1: (_t([-1.0]), 0.0)}
+    lb, A, acc = rb.spec_backward_batched(sb, xl, xh, gg, spec, return_input_linear=True)
+    torch.testing.assert_close(lb, _t([[-1.5, -2.5]]))
+    torch.testing.assert_close(A, _t([[[-2.0], [1.25]]]))
+    torch.testing.assert_close(acc, _t([[4.5, -3.75]]))
+
+
+def test_residual_merge_shares_the_fork_generators():
+    """z = x + (-1) x over x in [-1, 1]: the input is the fork point, so the
+    merge's one generator column is shared and cancels (zonotope [0, 0]);
+    interval arithmetic cannot see it ([-2, 2]); the CROWN rows reaching
+    the input from both branches sum to 0 (A = 0, lb = 0).  A merge that
+    took no shared column, or a backward that kept one branch, fails
+    (verify_zono_bnb.py:2387-2428, 3213-3234, 1133-1135, 4462-4469)."""
+    ops = [{'name': 'ra', 'type': 'reshape', 'inputs': [wk.INPUT_NAME]},
+           {'name': 'nb', 'type': 'mul', 'inputs': [wk.INPUT_NAME], 'scale': np.array([-1.0])},
+           {'name': 'z', 'type': 'add', 'inputs': ['ra', 'nb'], 'is_merge': True, 'bias': None},
+           {'name': 'r', 'type': 'relu', 'inputs': ['z'], 'layer_idx': 0},
+           _fc('f', 'r', [[1.0]], [0.0])]
+    gg = _affine_gg(ops, 1)
+    assert wk.INPUT_NAME in gg['fork_points']
+    xl, xh = _t([[-1.0]]), _t([[1.0]])
+    sb = rb.ibp_forward_batched(xl, xh, gg)
+    assert torch.equal(sb[0][0], _t([[-2.0]])) and torch.equal(sb[0][1], _t([[2.0]]))
+    sbz, _ = rb.zono_forward_batched(xl, xh, gg)
+    assert torch.equal(sbz[0][0], _t([[0.0]])) and torch.equal(sbz[0][1], _t([[0.0]]))
+    seed = {'z': _t([[[1.0], [-1.0]]])}
+    lb, A, acc = rb.spec_backward_batched(sbz, xl, xh, gg, None, return_input_linear=True,
+                                          seed_ew_at=seed, seed_acc=_t([[0.0, 0.0]]))
+    assert torch.equal(A, _t([[[0.0], [0.0]]])) and torch.equal(lb, _t([[0.0, 0.0]]))
+
+
+def test_merge_shared_count_at_a_deeper_fork():
+    """A fork after a ReLU: both branches carry the ReLU's new generator
+    columns as the shared prefix.  _find_shared_gens_count returns the
+    fork's count, and the merge's width is K_a + K_b - shared."""
+    gg = wk.residual_mlp_gg(3, 6, 2, seed=4, dtype=DT, n_blocks=1)
+    xl, xh = _box(3, 5, 0.3, seed=2)
+    # the generator counts the forward records, op by op
+    counts = {}
+    orig = rb.shared_gens_count
+
+    def spy(a, b, gg_, gc):
+        counts.update(gc)
+        return orig(a, b, gg_, gc)
+    rb.shared_gens_count = spy
+    try:
+        _, (c, G) = rb.zono_forward_batched(xl, xh, gg)
+    finally:
+        rb.shared_gens_count = orig
+    assert orig('b0_fb', 'relu0', gg, counts) == counts['relu0'] > counts[wk.INPUT_NAME]
+    # the block's merge: a = b0_fb (relu0's columns, then b0_ra's), b = relu0
+    # (exactly the shared ones): the fast path, K_out = K_a
+    assert counts['b0_fb'] >= counts['relu0']
+
+
+def test_affine_ops_equal_the_folded_network():
+    """Input normalisation ((x - m) / s), a constant add after a hidden fc
+    and a scalar mul by -1 before the last fc, against the same network
+    with the constants folded into the fc weights and biases: IBP, the
+    zonotope, CROWN intermediate bounds and the spec bound agree to fp64
+    rounding.  A wrong sign of sub or mul, or a constant left out of the
+    backward's acc, fails here."""
+    g = torch.Generator().manual_seed(9)
+    n_in, h, n_out = 4, 7, 3
+    W0, b0 = torch.randn(h, n_in, generator=g, dtype=DT), torch.randn(h, generator=g, dtype=DT)
+    W1, b1 = torch.randn(h, h, generator=g, dtype=DT), torch.randn(h, generator=g, dtype=DT)
+    W2, b2 = torch.randn(n_out, h, generator=g, dtype=DT), torch.randn(n_out, generator=g, dtype=DT)
+    m = torch.rand(n_in, generator=g, dtype=DT) - 0.5
+    s = 0.5 + torch.rand(n_in, generator=g, dtype=DT)
+    cst = torch.randn(h, generator=g, dtype=DT) * 0.3
+    ops = [{'name': 'ns', 'type': 'sub', 'inputs': [wk.INPUT_NAME], 'bias': m.numpy()},
+           {'name': 'nm', 'type': 'mul', 'inputs': ['ns'], 'scale': (1.0 / s).numpy()},
+           {'name': 'f0', 'type': 'fc', 'inputs': ['nm'], 'W': W0, 'bias': b0},
+           {'name': 'r0', 'type': 'relu', 'inputs': ['f0'], 'layer_idx': 0},
+           {'name': 'f1', 'type': 'fc', 'inputs': ['r0'], 'W': W1, 'bias': b1},
+           {'name': 'c1', 'type': 'add', 'inputs': ['f1'], 'is_merge': False,
+            'bias': cst.numpy()},
+           {'name': 'r1', 'type': 'relu', 'inputs': ['c1'], 'layer_idx': 1},
+           {'name': 'ng', 'type': 'mul', 'inputs': ['r1'], 'scale': np.array([-1.0])},
+           {'name': 'f2', 'type': 'fc', 'inputs': ['ng'], 'W': W2, 'bias': b2}]
+    gg = _affine_gg(ops, n_in)
+    Wf0 = W0 / s
+    folded = wk.mlp_gg([Wf0, W1, -W2], [b0 - Wf0 @ m, b1 + cst, b2], dtype=DT)
+    xl, xh = _box(n_in, 6, 0.4, seed=5)
+    for f in (lambda g_: rb.ibp_forward_batched(xl, xh, g_),
+              lambda g_: rb.zono_forward_batched(xl, xh, g_)[0],
+              lambda g_: rb.crown_intermediate_batched(g_, xl, xh)):
+        a, b = f(gg), f(folded)
+        for L in a:
+            for k in (0, 1):
+                torch.testing.assert_close(a[L][k], b[L][k], rtol=1e-10, atol=1e-10)
+    spec, _ = _util.spec_for(n_out)
+    t = rb.crown_intermediate_batched(gg, xl, xh)
+    la, Aa, ca = rb.spec_backward_batched(t, xl, xh, gg, spec, return_input_linear=True)
+    lb_, Ab, cb = rb.spec_backward_batched(t, xl, xh, folded, spec, return_input_linear=True)
+    torch.testing.assert_close(la, lb_, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(Aa, Ab, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(ca, cb, rtol=1e-10, atol=1e-10)
+
+
+def test_residual_net_bounds_contain_samples():
+    """The residual MLP (normalisation constants, two skip blocks, offset,
+    negation, output offset): every pre-activation sample lies inside the
+    IBP, zonotope and CROWN bounds, CROWN is at least as tight as the
+    zonotope, and the spec bound's linear form A x + acc lies below the
+    spec value at every sample."""
+    gg = wk.residual_mlp_gg(5, 10, 4, seed=3, dtype=DT)
+    xl, xh = _box(5, 3, 0.2, seed=6)
+    ibp = rb.ibp_forward_batched(xl, xh, gg)
+    zono, _ = rb.zono_forward_batched(xl, xh, gg)
+    crown = rb.crown_intermediate_batched(gg, xl, xh)
+    spec, _ = _util.spec_for(4)
+    lb, A, acc = rb.spec_backward_batched(crown, xl, xh, gg, spec, return_input_linear=True)
+    X = _util.sample_box(xl, xh, 400, seed=7)
+    Wq = torch.stack([spec[q][0] for q in sorted(spec)])
+    for b in range(xl.shape[0]):
+        y, pre = rb.point_forward(X[b], gg)
+        for L in crown:
+            for bounds in (ibp, zono, crown):
+                assert bool((pre[L] >= bounds[L][0][b] - 1e-9).all())
+                assert bool((pre[L] <= bounds[L][1][b] + 1e-9).all())
+            assert bool((crown[L][1][b] - crown[L][0][b] <= zono[L][1][b] - zono[L][0][b]
+                         + 1e-12).all())
+        val = y @ Wq.T
+        lin = X[b] @ A[b].T + acc[b]
+        assert bool((lin <= val + 1e-9).all())
+        assert bool((lb[b] <= val.min(0).values + 1e-9).all())

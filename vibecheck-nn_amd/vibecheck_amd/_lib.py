@@ -30,6 +30,11 @@ SIGNATURES = {
                     _I, _I, _I, _P, _P, _P],
     'vc_ibp_relu': [_P, _P, _L, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     'vc_zono_input': [_P, _P, _L, _I, _P, _I, _P, _P, _P],
+    'vc_affine_ew': [_P, _L, _I, _L, _P, _I, _I, _P, _P],
+    'vc_interval_mul': [_P, _P, _L, _I, _P, _I, _P, _P, _P],
+    'vc_add_ew': [_P, _P, _L, _P, _P],
+    'vc_zono_merge': [_P, _I, _P, _I, _I, _L, _P, _P],
+    'vc_rows_bias_dot': [_P, _L, _I, _I, _I, _P, _I, _F, _P, _P],
     'vc_zono_fc': [_P, _P, _L, _I, _I, _P, _P, _I, _P, _P, _P],
     'vc_zono_conv': [_P, _P, _L, _I, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I,
                      _I, _I, _I, _I, _P, _P, _P],

@@ -2,7 +2,8 @@
 function names and signatures (verify_zono_bnb.py of the reference).
 
 Every function takes the reference's ``gg`` dict (fc / relu / conv /
-reshape ops) and fp32 GPU tensors, computes with the kernels of
+reshape ops, and the constant add / sub / mul and residual-merge add ops)
+and fp32 GPU tensors, computes with the kernels of
 libvibecheck_amd.so, and returns new tensors.  Unsupported ops raise
 NotImplementedError, fp64 raises NotImplementedError, CPU tensors raise
 RuntimeError: there is no other compute path.
@@ -99,6 +100,83 @@ def _unsupported(fn, op):
 
 
 # --------------------------------------------------------------------------
+# add / sub / mul: their constants, and residual merges
+# --------------------------------------------------------------------------
+
+def _op_const(op, key, device, n):
+    """An add/sub op's 'bias' or a mul op's 'scale' as an fp32 device
+    vector of n values, or of one value for a scalar (None when the op has
+    none).  The reference converts the float64 constant with
+    torch.as_tensor(..., dtype=float32) and broadcasts it against the n
+    values: a vector of the trailing N-D dimension repeats along the
+    leading ones (out_shape_nd, verify_zono_bnb.py:3240-3251, 4490-4503);
+    a mul's per-channel vector repeats over each channel's H x W
+    (in_shapes_nd, :3523-3534, :4702-4708).  Cached on the op."""
+    cached = op.get('_vc_amd_' + key)
+    if cached is not None and cached[0] == (str(device), n):
+        return cached[1]
+    v = op.get(key)
+    if v is None:
+        return None
+    t = torch.as_tensor(v, dtype=torch.float32).reshape(-1).cpu()
+    k = t.numel()
+    if k not in (1, n):
+        shp_in = (op.get('in_shapes_nd') or [None])[0]
+        shp_out = op.get('out_shape_nd')
+        if (key == 'scale' and shp_in is not None and len(shp_in) == 3
+                and int(shp_in[0]) == k and k * int(shp_in[1]) * int(shp_in[2]) == n):
+            t = t.repeat_interleave(int(shp_in[1]) * int(shp_in[2]))
+        elif shp_out is not None and len(shp_out) >= 1 and int(shp_out[-1]) == k and n % k == 0:
+            t = t.repeat(n // k)
+        else:
+            raise ValueError(f'{op["type"]} {op["name"]!r}: {key} of {k} values does not '
+                             f'broadcast to {n}')
+    t = t.to(device).contiguous()
+    op['_vc_amd_' + key] = ((str(device), n), t)
+    return t
+
+
+def _fork_points(gg):
+    """The names consumed by more than one op (the gg's 'fork_points',
+    network.py:1713; derived from the ops when the dict has none)."""
+    fp = gg.get('fork_points')
+    if fp is not None:
+        return fp
+    uses = {}
+    for op in gg['ops']:
+        for i in op['inputs']:
+            uses[i] = uses.get(i, 0) + 1
+    return {k for k, v in uses.items() if v > 1}
+
+
+def _shared_gens(name_a, name_b, gg, gen_count):
+    """Generator columns two merging branches share: the count at the first
+    fork point among name_a's ancestors (depth-first from name_a, inputs
+    pushed in order) that is also an ancestor of name_b, else at the input.
+    The reference's _find_shared_gens_count (verify_zono_bnb.py:2387-2428);
+    column k of every descendant of a fork is that fork's k-th noise."""
+    forks = _fork_points(gg)
+    pred = {op['name']: op['inputs'] for op in gg['ops']}
+
+    def ancestors(name):
+        order, stack, seen = [], [name], set()
+        while stack:
+            x = stack.pop()
+            if x in seen:
+                continue
+            seen.add(x)
+            order.append(x)
+            stack.extend(pred.get(x, ()))
+        return order
+
+    anc_b = set(ancestors(name_b))
+    for a in ancestors(name_a):
+        if a in anc_b and a in forks:
+            return gen_count.get(a, 0)
+    return gen_count.get(gg['input_name'], 0)
+
+
+# --------------------------------------------------------------------------
 # a1: ReLU relaxation
 # --------------------------------------------------------------------------
 
@@ -178,6 +256,34 @@ def _ibp_forward_graph_batched(xl, xh, gg, device, dtype, relu_clamps=None,
             lo[name], hi[name] = pl, ph_
         elif t == 'reshape':
             lo[name], hi[name] = l, h
+        elif t == 'add' and op.get('is_merge'):
+            # residual merge (verify_zono_bnb.py:1133-1135)
+            l2, h2 = lo[op['inputs'][1]], hi[op['inputs'][1]]
+            lo_o, hi_o = torch.empty_like(l), torch.empty_like(h)
+            call('vc_add_ew', ptr(l), ptr(l2), l.numel(), ptr(lo_o), st)
+            call('vc_add_ew', ptr(h), ptr(h2), h.numel(), ptr(hi_o), st)
+            lo[name], hi[name] = lo_o, hi_o
+        elif t in ('add', 'sub'):
+            # constant shift (verify_zono_bnb.py:1136-1143)
+            n = l.shape[1]
+            b = _op_const(op, 'bias', dev, n)
+            if b is None:
+                raise ValueError(f'{t} {name!r}: no constant')
+            mode = 0 if t == 'add' else 1
+            lo_o, hi_o = torch.empty_like(l), torch.empty_like(h)
+            call('vc_affine_ew', ptr(l), B, n, 1, ptr(b), b.numel(), mode, ptr(lo_o), st)
+            call('vc_affine_ew', ptr(h), B, n, 1, ptr(b), b.numel(), mode, ptr(hi_o), st)
+            lo[name], hi[name] = lo_o, hi_o
+        elif t == 'mul':
+            # constant scale (verify_zono_bnb.py:1144-1148)
+            n = l.shape[1]
+            s = _op_const(op, 'scale', dev, n)
+            if s is None:
+                raise ValueError(f'mul {name!r}: no scale')
+            lo_o, hi_o = torch.empty_like(l), torch.empty_like(h)
+            call('vc_interval_mul', ptr(l), ptr(h), B, n, ptr(s), s.numel(), ptr(lo_o),
+                 ptr(hi_o), st)
+            lo[name], hi[name] = lo_o, hi_o
         else:
             raise NotImplementedError(
                 f'_ibp_forward_graph_batched: unsupported op {t!r} at '
@@ -191,8 +297,10 @@ def _ibp_forward_graph_batched(xl, xh, gg, device, dtype, relu_clamps=None,
 
 def _forward_zonotope_graph_batched(xl, xh, gg, device, dtype):
     """Batched zonotope forward (verify_zono_bnb.py:3079-4075, fc/relu/conv/
-    reshape).  Returns (sb, (c, G)); G is (B, n, K) with the new generator
-    columns of each ReLU padded to the batch maximum, as in the reference.
+    reshape/add/sub/mul).  Returns (sb, (c, G)); G is (B, n, K) with the new
+    generator columns of each ReLU padded to the batch maximum, as in the
+    reference; a residual merge sums the generator columns the two branches
+    share from their fork point and appends each branch's own.
     (The (c, G) output needs the layer-wise kernels; bound-only callers use
     the fused kernel through _zono_sb.)
     """
@@ -210,13 +318,48 @@ def _forward_zonotope_graph_batched(xl, xh, gg, device, dtype):
     call('vc_zono_input', ptr(xl), ptr(xh), B, n_in, ptr(vidx), K, ptr(c),
          ptr(G), st)
     state = {gg['input_name']: (c, G)}
+    gen_count = {gg['input_name']: K}
     sb = {}
     for op in gg['ops']:
         t = op['type']
         name = op['name']
         c_in, G_in = state[op['inputs'][0]]
         Kc = G_in.shape[2]
-        if t == 'fc':
+        n = c_in.shape[1]
+        if t == 'add' and op.get('is_merge'):
+            # residual merge: the fork point's generators are shared
+            # (verify_zono_bnb.py:3213-3234)
+            c_b, G_b = state[op['inputs'][1]]
+            Kb = G_b.shape[2]
+            shared = _shared_gens(op['inputs'][0], op['inputs'][1], gg, gen_count)
+            if not (0 <= shared <= Kc and shared <= Kb):
+                raise ValueError(f'add {name!r}: {shared} shared generators of {Kc} and {Kb}')
+            c_o = torch.empty_like(c_in)
+            call('vc_add_ew', ptr(c_in), ptr(c_b), c_in.numel(), ptr(c_o), st)
+            G_o = torch.empty(B, n, Kc + Kb - shared, device=dev)
+            call('vc_zono_merge', ptr(G_in), Kc, ptr(G_b), Kb, shared, B * n, ptr(G_o), st)
+            state[name] = (c_o, G_o)
+        elif t in ('add', 'sub'):
+            # constant shift of the centre (verify_zono_bnb.py:3235-3265)
+            b = _op_const(op, 'bias', dev, n)
+            c_o = c_in
+            if b is not None:
+                c_o = torch.empty_like(c_in)
+                call('vc_affine_ew', ptr(c_in), B, n, 1, ptr(b), b.numel(),
+                     0 if t == 'add' else 1, ptr(c_o), st)
+            state[name] = (c_o, G_in)
+        elif t == 'mul':
+            # constant scale of centre and generators (verify_zono_bnb.py:3501-3536)
+            s = _op_const(op, 'scale', dev, n)
+            if s is None:
+                raise ValueError(f'mul {name!r}: no scale')
+            c_o = torch.empty_like(c_in)
+            call('vc_affine_ew', ptr(c_in), B, n, 1, ptr(s), s.numel(), 2, ptr(c_o), st)
+            G_o = torch.empty_like(G_in)
+            if Kc > 0:
+                call('vc_affine_ew', ptr(G_in), B, n, Kc, ptr(s), s.numel(), 2, ptr(G_o), st)
+            state[name] = (c_o, G_o)
+        elif t == 'fc':
             p = _op_params(op, dev)
             c_o = torch.empty(B, p['n_out'], device=dev)
             G_o = torch.empty(B, p['n_out'], Kc, device=dev)
@@ -252,6 +395,7 @@ def _forward_zonotope_graph_batched(xl, xh, gg, device, dtype):
             state[name] = (c_in, G_in)
         else:
             raise ValueError(f'batched zono forward: unknown op type {t!r}')
+        gen_count[name] = state[name][1].shape[2]
     _forward_zonotope_graph_batched.last_bilinear_op_bounds = {}
     return sb, state[gg['ops'][-1]['name']]
 
@@ -283,11 +427,13 @@ class _Rows:
 
 class BackwardTrace:
     """Per-relu stored pre-relaxation rows of one backward, for the alpha
-    gradient sweep: entries (L, P, p_shared) in backward order."""
+    gradient sweep: entries (L, P, p_shared) in backward order.  ``other``
+    names an op the sweep does not replay (add, sub, mul, a fan-in)."""
 
     def __init__(self):
         self.relus = []
         self.fcs = []
+        self.other = None
 
 
 # vc_backward_fc runs as relaxation pass + plain MFMA GEMM from this row
@@ -324,6 +470,38 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
             acc = acc.unsqueeze(0).expand(B, R).reshape(B * R).contiguous()
             acc_shared = False
 
+    def combine(a, b):
+        """Rows reaching one node from two consumers, summed (ew_at[inp] +
+        ew, verify_zono_bnb.py:4462-4469)."""
+        a, b = materialize(a), materialize(b)
+        if a.shared and b.shared:
+            out = torch.empty_like(a.ew)
+            call('vc_add_ew', ptr(a.ew), ptr(b.ew), a.ew.numel(), ptr(out), st)
+            return _Rows(out, True)
+        per_domain_acc()
+        ea = _expand_rows(a.ew, B) if a.shared else a.ew
+        eb = _expand_rows(b.ew, B) if b.shared else b.ew
+        out = torch.empty_like(ea)
+        call('vc_add_ew', ptr(ea), ptr(eb), ea.numel(), ptr(out), st)
+        return _Rows(out, False)
+
+    def put(inp, rows):
+        prev = ew_at.get(inp)
+        if prev is not None and trace is not None:
+            trace.other = trace.other or 'fan-in'
+        ew_at[inp] = rows if prev is None else combine(prev, rows)
+
+    def bias_dot(rows, v, sign):
+        """acc += sign * rows . v (the constant of an add or sub)."""
+        n = rows.ew.shape[1]
+        if rows.shared and acc_shared:
+            call('vc_rows_bias_dot', ptr(rows.ew), R, R, n, 1, ptr(v), v.numel(), sign,
+                 ptr(acc), st)
+        else:
+            per_domain_acc()
+            call('vc_rows_bias_dot', ptr(rows.ew), B * R, R, n, 1 if rows.shared else 0,
+                 ptr(v), v.numel(), sign, ptr(acc), st)
+
     def materialize(rows):
         """Apply a pending relu relaxation with the standalone kernel."""
         if rows.relu is None:
@@ -352,10 +530,32 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
         rows = ew_at.pop(name)
         t = op['type']
         inp = op['inputs'][0]
-        if inp in ew_at:
-            raise NotImplementedError(
-                'vibecheck_amd: fan-in (skip connections) is not supported')
-        if t == 'fc':
+        if t in ('add', 'sub', 'mul') and trace is not None:
+            trace.other = trace.other or t
+        if t == 'add' and op.get('is_merge'):
+            # the rows flow to both branches unchanged (verify_zono_bnb.py:4462-4469)
+            rows = materialize(rows)
+            for i in op['inputs']:
+                put(i, _Rows(rows.ew, rows.shared))
+        elif t in ('add', 'sub'):
+            # constant shift: acc +/-= rows . bias, rows unchanged
+            # (verify_zono_bnb.py:4470-4518)
+            rows = materialize(rows)
+            b = _op_const(op, 'bias', dev, rows.ew.shape[1])
+            if b is not None:
+                bias_dot(rows, b, 1.0 if t == 'add' else -1.0)
+            put(inp, rows)
+        elif t == 'mul':
+            # constant scale: rows * scale (verify_zono_bnb.py:4686-4712)
+            rows = materialize(rows)
+            s = _op_const(op, 'scale', dev, rows.ew.shape[1])
+            if s is None:
+                raise ValueError(f'mul {name!r}: no scale')
+            out = torch.empty_like(rows.ew)
+            call('vc_affine_ew', ptr(rows.ew), rows.ew.shape[0], rows.ew.shape[1], 1, ptr(s),
+                 s.numel(), 2, ptr(out), st)
+            put(inp, _Rows(out, rows.shared))
+        elif t == 'fc':
             p = _op_params(op, dev)
             if rows.relu is not None:
                 L = rows.relu
@@ -384,7 +584,7 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
                          ptr(rows.beta), ptr(p['W']), ptr(p['b']), p['n_in'],
                          ptr(out), ptr(acc), ptr(rel), 1 if rows.shared else 0, st)
                 del rel
-                ew_at[inp] = _Rows(out, False)
+                put(inp, _Rows(out, False))
             else:
                 if not rows.shared:
                     per_domain_acc()
@@ -395,7 +595,7 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
                 call('vc_backward_fc', ptr(rows.ew), M, R, p['n_out'], None,
                      None, None, 0, None, ptr(p['W']), ptr(p['b']),
                      p['n_in'], ptr(out), ptr(acc), None, 0, st)
-                ew_at[inp] = _Rows(out, rows.shared)
+                put(inp, _Rows(out, rows.shared))
         elif t == 'relu':
             if 'layer_idx' in op:
                 rows = materialize(rows)
@@ -421,7 +621,7 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
                         rows.alpha_row = 0
                 if relu_split_beta is not None and L in relu_split_beta:
                     rows.beta = f32(relu_split_beta[L])
-            ew_at[inp] = rows
+            put(inp, rows)
         elif t == 'conv':
             rows = materialize(rows)
             p = _op_params(op, dev)
@@ -433,9 +633,9 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
             call('vc_backward_conv', ptr(rows.ew), M, ptr(p['K']),
                  ptr(p['b']), C_out, Ho, Wo, C_in, H, W, kh, kw, sh, sw, ph,
                  pw, ptr(out), ptr(acc), st)
-            ew_at[inp] = _Rows(out, rows.shared)
+            put(inp, _Rows(out, rows.shared))
         elif t == 'reshape':
-            ew_at[inp] = rows
+            put(inp, rows)
         else:
             raise ValueError(f'batched spec backward: unknown op {t!r}')
 
@@ -637,6 +837,9 @@ def _alpha_backward_and_grad(sb, xl, xh, gg, Wq, bq, alpha, want_grad, galpha,
         return (lb, A) if want_A else lb
     if A is None or a_shared:
         raise NotImplementedError('vibecheck_amd: alpha gradient needs a relu')
+    if trace.other is not None:
+        raise NotImplementedError(
+            f'vibecheck_amd: alpha-CROWN gradient supports fc/relu chains (found {trace.other})')
     # trace.relus: (L, P, shared) in backward order (top relu first);
     # trace.fcs: fc ops in backward order.  Sequential fc/relu nets only:
     # fcs[i] sits below relus[i-1] ... check the chain shape.

@@ -14,6 +14,8 @@ zero biases.
 """
 import math
 
+import numpy as np
+
 import torch
 
 from .spec import Conjunct, PairwiseConstraint, VNNSpec
@@ -62,6 +64,50 @@ def mlp_gg(weights, biases, device='cpu', dtype=torch.float32):
                         'layer_idx': i})
             prev = f'relu{i}'
     n_in = int(weights[0].shape[1])
+    return _finish(ops, n_in, (1, n_in))
+
+
+def residual_mlp_gg(n_in, width, n_out, seed=0, device='cpu', dtype=torch.float32,
+                    n_blocks=2):
+    """A residual ReLU MLP in the op form the reference's ONNX reader emits
+    (network.py:1925-2150): input normalisation as sub (mean) then mul
+    (1 / std) constants, fc0 -> relu, then ``n_blocks`` blocks
+    y = relu(fc_b(relu(fc_a(x))) + x) whose skip is an 'add' with
+    is_merge (x is a fork point), a constant 'add' offset and a scalar
+    'mul' by -1 before the head's last fc, which ends in a constant 'add'.
+    Kaiming-normal weights, biases N(0, 0.1^2), seeded."""
+    g = _gen(seed)
+
+    def fc(name, inp, n_o, n_i):
+        W = torch.randn(n_o, n_i, generator=g, dtype=torch.float64) * (2.0 / n_i) ** 0.5
+        b = torch.randn(n_o, generator=g, dtype=torch.float64) * 0.1
+        return _fc_op(name, inp, W.float(), b.float(), device, dtype)
+
+    mean = (torch.rand(n_in, generator=g, dtype=torch.float64) - 0.5).numpy()
+    std = (0.5 + torch.rand(n_in, generator=g, dtype=torch.float64)).numpy()
+    ops = [{'name': 'norm_sub', 'type': 'sub', 'inputs': [INPUT_NAME], 'bias': mean},
+           {'name': 'norm_mul', 'type': 'mul', 'inputs': ['norm_sub'], 'scale': 1.0 / std},
+           fc('fc0', 'norm_mul', width, n_in),
+           {'name': 'relu0', 'type': 'relu', 'inputs': ['fc0'], 'layer_idx': 0}]
+    prev, L = 'relu0', 1
+    for k in range(n_blocks):
+        ops.append(fc(f'b{k}_fa', prev, width, width))
+        ops.append({'name': f'b{k}_ra', 'type': 'relu', 'inputs': [f'b{k}_fa'],
+                    'layer_idx': L})
+        ops.append(fc(f'b{k}_fb', f'b{k}_ra', width, width))
+        ops.append({'name': f'b{k}_add', 'type': 'add', 'inputs': [f'b{k}_fb', prev],
+                    'is_merge': True, 'bias': None})
+        ops.append({'name': f'b{k}_rb', 'type': 'relu', 'inputs': [f'b{k}_add'],
+                    'layer_idx': L + 1})
+        prev, L = f'b{k}_rb', L + 2
+    off = (torch.rand(width, generator=g, dtype=torch.float64) * 0.2 - 0.1).numpy()
+    ops.append({'name': 'head_off', 'type': 'add', 'inputs': [prev], 'is_merge': False,
+                'bias': off})
+    ops.append({'name': 'head_neg', 'type': 'mul', 'inputs': ['head_off'],
+                'scale': np.array([-1.0])})
+    ops.append(fc('head', 'head_neg', n_out, width))
+    ops.append({'name': 'out', 'type': 'add', 'inputs': ['head'], 'is_merge': False,
+                'bias': (torch.rand(n_out, generator=g, dtype=torch.float64) - 0.5).numpy()})
     return _finish(ops, n_in, (1, n_in))
 
 
