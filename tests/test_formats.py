@@ -226,3 +226,47 @@ def test_onnx_refuses_what_it_cannot_represent():
     with pytest.raises(NotImplementedError):
         onnx_net.onnx_to_gg(_model(nodes, dict(m=np.full((1, 1, 1, 1), 0.5), K=K),
                                    [1, 1, 4, 4]))
+
+
+def test_onnx_synthetic_residual_and_affine_ops():
+    """A residual MLP written as ONNX: Gemm -> Relu (r1) -> Gemm -> Add with
+    r1 (a merge of two computed tensors) -> Relu -> Mul by a constant ->
+    Sub a constant -> (const - x) -> Div by a constant -> MatMul.  The
+    reader emits the reference's op forms (merge add; mul, sub, mul(-1) +
+    add, mul(1/c)); the oracle's point forward of the gg equals numpy's."""
+    rng = np.random.default_rng(11)
+    W1 = rng.standard_normal((6, 4)).astype(np.float32)   # Gemm B, transB
+    c1 = rng.standard_normal(6).astype(np.float32)
+    W2 = rng.standard_normal((6, 6)).astype(np.float32)
+    c2 = rng.standard_normal(6).astype(np.float32)
+    sc = (rng.random(6) + 0.5).astype(np.float32)
+    sh = rng.standard_normal(6).astype(np.float32)
+    k0 = rng.standard_normal(6).astype(np.float32)
+    dv = (rng.random(6) + 1.0).astype(np.float32)
+    W3 = rng.standard_normal((6, 3)).astype(np.float32)   # MatMul weight
+    nodes = [_node('Gemm', ['input', 'W1', 'c1'], ['t1'], transB=1),
+             _node('Relu', ['t1'], ['r1']),
+             _node('Gemm', ['r1', 'W2', 'c2'], ['t2'], transB=1),
+             _node('Add', ['t2', 'r1'], ['t3']),
+             _node('Relu', ['t3'], ['r2']),
+             _node('Mul', ['r2', 'sc'], ['t4']),
+             _node('Sub', ['t4', 'sh'], ['t5']),
+             _node('Sub', ['k0', 't5'], ['t6']),
+             _node('Div', ['t6', 'dv'], ['t7']),
+             _node('MatMul', ['t7', 'W3'], ['out'])]
+    data = _model(nodes, dict(W1=W1, c1=c1, W2=W2, c2=c2, sc=sc, sh=sh, k0=k0, dv=dv, W3=W3),
+                  [1, 4])
+    gg = onnx_net.onnx_to_gg(data, dtype=torch.float64)
+    types = [(op['type'], op.get('is_merge')) for op in gg['ops']]
+    assert types == [('fc', None), ('relu', None), ('fc', None), ('add', True),
+                     ('relu', None), ('mul', None), ('sub', None), ('mul', None),
+                     ('add', False), ('mul', None), ('fc', None)]
+    assert gg['ops'][1]['name'] in gg['fork_points']
+    x = rng.random((5, 4))
+    f = lambda a: a.astype(np.float64)
+    r1 = np.maximum(x @ f(W1).T + f(c1), 0)
+    r2 = np.maximum(r1 @ f(W2).T + f(c2) + r1, 0)
+    t7 = (f(k0) - (r2 * f(sc) - f(sh))) / f(dv)
+    ref = t7 @ f(W3)
+    got, _ = rb.point_forward(torch.tensor(x), gg)
+    assert np.allclose(got.numpy(), ref, rtol=1e-9, atol=1e-9)

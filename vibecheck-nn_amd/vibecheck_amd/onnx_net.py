@@ -23,6 +23,12 @@ input (input normalisation) is folded into the first fc or conv: an
 all-zero offset or unit scale is dropped exactly, anything else changes
 that layer's weights and bias (computed in float64, then rounded once).  A
 conv takes per-channel transforms only, and no offset when it pads.
+Elsewhere in the graph an Add of two computed tensors becomes a residual
+merge ('add' with is_merge), and an Add / Sub / Mul / Div of a computed
+tensor and a constant becomes an 'add' / 'sub' / 'mul' op with the
+constant spelled out over the tensor's values (const - x as a negation
+then an add; x / c as a mul by 1 / c), the op forms of the reference's
+reader (network.py:1925-1946, 2020-2053, 2100-2150).
 Any other op raises NotImplementedError, as the reference does for ops it
 cannot bound.
 """
@@ -338,6 +344,38 @@ def onnx_to_gg(data, device='cpu', dtype=torch.float32):
                         'stride': (st[0], st[1]), 'padding': (pads[0], pads[1]),
                         'output_padding': (oph, opw), 'n_out': C_out * Ho * Wo})
             val[outs[0]] = ('op', r, [C_out, Ho, Wo])
+        elif op_type == 'Add' and xs[0] and xs[1] and xs[0][0] != 'const' \
+                and xs[1][0] != 'const':
+            # two live inputs: a residual merge (network.py:2020-2053)
+            (na, sa), (nb, sb_) = src(xs[0]), src(xs[1])
+            if int(np.prod(sa)) != int(np.prod(sb_)):
+                raise NotImplementedError('onnx: Add of differently shaped tensors')
+            r = add_op({'type': 'add', 'inputs': [na, nb], 'is_merge': True, 'bias': None})
+            val[outs[0]] = ('op', r, sa)
+        elif op_type in ('Add', 'Sub', 'Mul', 'Div') and xs[0] and xs[1] \
+                and (xs[0][0] == 'const') != (xs[1][0] == 'const'):
+            # a computed tensor and a constant (network.py:1925-1946,
+            # 2100-2150): the constant spelled out over the tensor's values
+            live_first = xs[1][0] == 'const'
+            name, shape = src(xs[0] if live_first else xs[1])
+            c = np.asarray((xs[1] if live_first else xs[0])[1], dtype=np.float64)
+            flat = np.ascontiguousarray(np.broadcast_to(c, shape)).reshape(-1) \
+                if c.size != 1 else c.reshape(-1)
+            if op_type == 'Add':
+                r = add_op({'type': 'add', 'inputs': [name], 'is_merge': False, 'bias': flat})
+            elif op_type == 'Sub' and live_first:
+                r = add_op({'type': 'sub', 'inputs': [name], 'bias': flat})
+            elif op_type == 'Sub':
+                # const - x: negate, then add the constant
+                m = add_op({'type': 'mul', 'inputs': [name], 'scale': np.array([-1.0])})
+                r = add_op({'type': 'add', 'inputs': [m], 'is_merge': False, 'bias': flat})
+            elif op_type == 'Mul':
+                r = add_op({'type': 'mul', 'inputs': [name], 'scale': flat})
+            elif live_first:
+                r = add_op({'type': 'mul', 'inputs': [name], 'scale': 1.0 / flat})
+            else:
+                raise NotImplementedError('onnx: Div of a constant by a tensor')
+            val[outs[0]] = ('op', r, shape)
         else:
             raise NotImplementedError(f'onnx: unsupported op {op_type!r}')
 
