@@ -453,7 +453,7 @@ def kernel_suite(reps):
             sets.append((A, acc, xl, xl + 0.05, torch.empty(M, device=dev)))
         fns = [lambda s=s: call('vc_concretize', ptr(s[0]), ptr(s[1]), ptr(s[2]), ptr(s[3]),
                                 M, R, n_in, 0, ptr(s[4]), st) for s in sets]
-        kern = 'k_concretize_thread' if n_in <= 32 else 'k_concretize_wave'
+        kern = 'k_concretize_tile' if n_in <= 32 else 'k_concretize_wave'
         report('a8', kern, what, _time_launches(fns, reps), 'hbm', per)
         del sets, fns
 

@@ -870,6 +870,38 @@ def test_relaxation_kernels_rows_and_domains(gpu, n, alpha_mode, with_beta):
                   scale=acc0.double().abs() + terms.abs().sum(-1))
 
 
+@pytest.mark.parametrize('n,R,B', [(5, 4, 3000), (13, 3, 777), (32, 1, 1000), (7, 300, 9),
+                                   (1, 1, 257)])
+def test_concretize_tiled_matches_thread_form(gpu, n, R, B):
+    """Narrow inputs: the LDS-tiled concretization (16-byte aligned A) and
+    the one-thread-per-row form (taken for an unaligned A) give the same
+    bits; both equal lb = acc + pos(A) xl + neg(A) xh within fp32 of the
+    fp64 value (verify_zono_bnb.py:5117-5134)."""
+    M = B * R
+    g = torch.Generator().manual_seed(n * 1000 + R)
+    A = torch.randn(M, n, generator=g)
+    acc = torch.randn(M, generator=g)
+    xl = torch.rand(B, n, generator=g) * 2 - 1
+    xh = xl + torch.rand(B, n, generator=g)
+    Ag, accg, xlg, xhg = (t.to(gpu).contiguous() for t in (A, acc, xl, xh))
+    buf = torch.empty(M * n + 1, device=gpu)
+    buf[1:] = Ag.reshape(-1)
+    A_un = buf[1:].view(M, n)
+    assert A_un.data_ptr() % 16 != 0 and Ag.data_ptr() % 16 == 0
+    out = {}
+    for k, a in (('tile', Ag), ('thread', A_un)):
+        lb = torch.empty(M, device=gpu)
+        call('vc_concretize', ptr(a), ptr(accg), ptr(xlg), ptr(xhg), M, R, n, 0, ptr(lb),
+             _lib_stream())
+        out[k] = lb.cpu()
+    assert torch.equal(out['tile'], out['thread'])
+    d = torch.arange(M) // R
+    ref = (acc.double() + (A.double().clamp(min=0) * xl.double()[d]).sum(1)
+           + (A.double().clamp(max=0) * xh.double()[d]).sum(1))
+    scale = acc.double().abs() + (A.double().abs() * torch.maximum(xl.abs(), xh.abs()).double()[d]).sum(1)
+    assert bool(((out['tile'].double() - ref).abs() <= 1e-6 * scale + 1e-7).all())
+
+
 def test_row_kernels_beyond_grid_cap(gpu):
     """The one-wavefront-per-row kernels cover every row when there are more
     rows than one launch has wavefronts (1,048,576 workgroups x 4 waves =

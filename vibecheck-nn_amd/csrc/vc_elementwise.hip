@@ -1,6 +1,8 @@
 // Elementwise, reduction and integer/indexing kernels: ReLU relaxation,
 // IBP relu, concretization, CROWN intersection, alpha-CROWN reductions and
 // Adam, closure, halfspace clipping, compaction, widest-axis bisection.
+#include <algorithm>
+
 #include "vc_common.h"
 #include "vc_relax.h"
 
@@ -164,6 +166,56 @@ __global__ __launch_bounds__(CT) void k_concretize_thread(const float* A, int a_
     const float* a = A + (a_bcast ? m % R : m) * (int64_t)n;
     double s = 0.0;
     for (int i = 0; i < n; ++i) s += conc_term(a[i], xl[d * n + i], xh[d * n + i]);
+    lb[m] = (float)((double)acc[m] + s);
+  }
+}
+
+// Narrow inputs, A per row: each workgroup takes CT consecutive rows.  Its
+// rows of A (CT x n floats, contiguous) and its domains' boxes (contiguous
+// too) are staged into LDS with float4 loads that cover the whole span
+// (a row of 5 floats is not 16-byte aligned, so per-thread loads would
+// touch every cache line once per input); each thread then sums its row
+// from LDS in k_concretize_thread's order, so the results are the same.
+__global__ __launch_bounds__(CT) void k_concretize_tile(const float* __restrict__ A,
+                                                        const float* __restrict__ acc,
+                                                        const float* __restrict__ xl,
+                                                        const float* __restrict__ xh,
+                                                        int64_t M, int R, int n,
+                                                        float* __restrict__ lb) {
+  extern __shared__ float csm[];
+  const int64_t m0 = (int64_t)blockIdx.x * CT;
+  const int rows = (int)min((int64_t)CT, M - m0);
+  const int64_t d0 = m0 / R;
+  const int nd = (int)((m0 + rows - 1) / R - d0 + 1);  // domains of this tile
+  float* sa = csm;                                      // [CT * n]
+  float* sl = sa + CT * n;                              // [nd * n]
+  float* sh = sl + ((nd * n + 3) & ~3);                 // [nd * n]
+  // A's span [m0 n, (m0 + rows) n): 16-byte aligned at m0 n (CT n is a
+  // multiple of 4) when A is
+  {
+    const float* src = A + m0 * n;
+    const int cnt = rows * n;
+    const int c4 = cnt >> 2;
+    for (int k = threadIdx.x; k < c4; k += CT)
+      *reinterpret_cast<float4*>(sa + 4 * k) = reinterpret_cast<const float4*>(src)[k];
+    for (int k = 4 * c4 + threadIdx.x; k < cnt; k += CT) sa[k] = src[k];
+  }
+  // the boxes' span [d0 n, (d0 + nd) n): any alignment, scalar loads
+  {
+    const int cnt = nd * n;
+    for (int k = threadIdx.x; k < cnt; k += CT) {
+      sl[k] = xl[d0 * n + k];
+      sh[k] = xh[d0 * n + k];
+    }
+  }
+  __syncthreads();
+  const int r = threadIdx.x;
+  if (r < rows) {
+    const int64_t m = m0 + r;
+    const int dl = (int)(m / R - d0);
+    const float* a = sa + r * n;
+    double s = 0.0;
+    for (int i = 0; i < n; ++i) s += conc_term(a[i], sl[dl * n + i], sh[dl * n + i]);
     lb[m] = (float)((double)acc[m] + s);
   }
 }
@@ -1085,7 +1137,17 @@ extern "C" int vc_concretize(const float* A, const float* acc, const float* xl,
   if (!A || !acc || !xl || !xh || !lb || R <= 0 || n_in <= 0 || M < 0 || M % R) return VC_ERR_ARG;
   if (M == 0) return VC_OK;
   hipStream_t st = (hipStream_t)stream;
-  if (n_in <= CT_MAXN) {
+  // LDS of the tiled form: CT rows of A, and the boxes of at most
+  // (CT - 1) / R + 2 domains (a tile's rows straddle domain boundaries)
+  const int nd_max = (int)(R >= CT ? 2 : std::min(CT, (CT - 1) / R + 2));
+  const size_t lds_tile =
+      sizeof(float) * ((size_t)CT * n_in + 2 * (((size_t)nd_max * n_in + 3) & ~(size_t)3));
+  if (n_in <= CT_MAXN && !a_bcast && aligned16(A) && lds_tile <= 64 * 1024 &&
+      (M + CT - 1) / CT <= 0x7fffffff) {
+    const size_t lds = lds_tile;
+    hipLaunchKernelGGL(k_concretize_tile, dim3((unsigned)((M + CT - 1) / CT)), dim3(CT), lds, st,
+                       A, acc, xl, xh, M, R, n_in, lb);
+  } else if (n_in <= CT_MAXN) {
     hipLaunchKernelGGL(k_concretize_thread, dim3(vc_blocks(M, CT)), dim3(CT), 0, st, A, a_bcast,
                        acc, xl, xh, M, R, n_in, lb);
   } else if (n_in % 4 == 0 && aligned16(A) && aligned16(xl) && aligned16(xh)) {
