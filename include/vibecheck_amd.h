@@ -195,17 +195,27 @@ int vc_backward_fc(const float *ew_in, int64_t M, int R, int n_out,
 
 /* vc_backward_fc with the per-row alpha of a group: alpha_groups (G, R,
  * n_out) holds one alpha per (group, row, neuron) and domain d reads the
- * rows of group group[d] (B int64, each in [0, G): the caller guarantees
- * it).  No beta.  The hybrid replay's frozen layer alphas, shared by every
- * leaf of a group, bound without a per-leaf copy: replaces the
- * alpha_b = a.expand(B, -1, -1) of verify_hybrid_acasxu.py:286-287 with
- * the backward of verify_zono_bnb.py:4409-4453 that reads it. */
+ * rows of group group[d] (B int64; n_groups = G).  An index outside
+ * [0, G) reads group 0 instead of memory past the buffer; callers that do
+ * not build the indices themselves pass them through vc_group_clamp first,
+ * which reports such indices.  No beta.  The hybrid replay's frozen layer
+ * alphas, shared by every leaf of a group, bound without a per-leaf copy:
+ * replaces the alpha_b = a.expand(B, -1, -1) of verify_hybrid_acasxu.py:
+ * 286-287 with the backward of verify_zono_bnb.py:4409-4453 that reads it. */
 int vc_backward_fc_grouped(const float *ew_in, int64_t M, int R, int n_out,
                            const float *relu_lo, const float *relu_hi,
                            const float *alpha_groups, const int64_t *group,
-                           const float *W, const float *bias, int n_in,
+                           int64_t n_groups, const float *W, const float *bias, int n_in,
                            float *ew_out, float *acc, float *relax_out, int ew_bcast,
                            vc_stream_t stream);
+
+/* Group indices made safe to read by: out[b] = group[b] when it lies in
+ * [0, n_groups), else 0, and *bad = 1 if any did not (the caller zeroes
+ * *bad beforehand and reads it at its next synchronisation).  The hybrid
+ * replay's check of the leaves' group indices (verify_hybrid_acasxu.py:
+ * 286-287 indexes the group alphas by them). */
+int vc_group_clamp(const int64_t *group, int64_t B, int64_t n_groups, int64_t *out,
+                   int32_t *bad, vc_stream_t stream);
 
 /* Slopes of a relu layer for the backward, elementwise over n (= B * n_L)
  * pre-activation bounds: lo_s = active + unstable * alpha when alpha (same

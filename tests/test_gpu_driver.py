@@ -121,3 +121,45 @@ def test_bab_step_clip_iters_parity(gpu):
     for k in ('xl_split', 'xh_split'):
         err = (got[k].cpu().double() - ref[k].double()).abs()
         assert bool((err <= tol).all()), (k, int((err > tol).sum()))
+
+
+def test_native_rounds_from_two_host_threads(gpu):
+    """Two host threads run BaB rounds at once, each on its own stream: the
+    counts the native round polls and alpha's stop word are per thread, and
+    the domain-queue counters per call, so each thread's round equals the
+    same round run alone."""
+    import threading
+    gg = wk.acas_gg(device=gpu, dtype=F32)
+    se_c, dq = _util.spec_for(5, dtype=F32)
+    se = {k: (w.to(gpu), b) for k, (w, b) in se_c.items()}
+    batches = []
+    for seed in (11, 12):
+        xl, xh = wk.acas_boxes(3000, seed=seed, device=gpu, dtype=F32)
+        c, r = (xl + xh) / 2, (xh - xl) / 2
+        batches.append(((c - 3 * r).contiguous(), (c + 3 * r).contiguous()))
+    kw = dict(alpha_iters=8, alpha_all=True, alpha_lr=0.1)
+    alone = [vg.bab_step(xl, xh, gg, se, vg.DisjunctTable(dq, gpu), **kw)
+             for xl, xh in batches]
+    got = [None, None]
+    errors = []
+
+    def run(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for _ in range(3):
+                    got[i] = vg.bab_step(*batches[i], gg, se, vg.DisjunctTable(dq, gpu), **kw)
+            s.synchronize()
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+    ts = [threading.Thread(target=run, args=(i,)) for i in (0, 1)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=120)
+    assert not errors, errors
+    for a, b in zip(alone, got):
+        assert b is not None
+        assert torch.equal(a['closed'], b['closed']) and torch.equal(a['lb'], b['lb'])
+        assert torch.equal(a['unclosed'], b['unclosed'])
+        assert a['n_alpha_iters'] == b['n_alpha_iters']

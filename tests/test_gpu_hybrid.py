@@ -213,6 +213,16 @@ def test_replay_per_leaf_groups_equal_per_group_calls(gpu):
         assert torch.equal(tg[L][0], tp[L][0]) and torch.equal(tg[L][1], tp[L][1])
     with pytest.raises(ValueError):
         vh._replay_batched(bxl, bxh, gg_g, se_g, a_layer, a_spec, gpu, F32, group=gid + 6)
+    # without the host check an index outside [0, G) reads group 0 (the
+    # library clamps every read), so the result equals that of passing 0
+    bad_gid, zero_gid = gid.clone(), gid.clone()
+    bad_gid[::3] = 999
+    zero_gid[::3] = 0
+    b_bad, A_bad = vh._replay_batched(bxl, bxh, gg_g, se_g, a_layer, a_spec, gpu, F32,
+                                      group=bad_gid, check_groups=False)
+    b_0, A_0 = vh._replay_batched(bxl, bxh, gg_g, se_g, a_layer, a_spec, gpu, F32,
+                                  group=zero_gid)
+    assert torch.equal(b_bad, b_0) and torch.equal(A_bad, A_0)
     for grp in gid.unique().tolist():
         sel = (gid == grp).nonzero(as_tuple=True)[0]
         gl = {L: {k: a[grp:grp + 1] for k, a in d.items()} for L, d in a_layer.items()}

@@ -39,6 +39,13 @@ struct LoadMidRad {  // A = (mid, rad) of an interval row-block
   }
 };
 
+// The group of domain d, read in range: an index outside [0, n_groups)
+// reads group 0 (vc_group_clamp reports such indices to the caller).
+__device__ __forceinline__ int64_t safe_group(const int64_t* group, int64_t n_groups, int64_t d) {
+  const int64_t g = group[d];
+  return (uint64_t)g < (uint64_t)n_groups ? g : 0;
+}
+
 // CROWN backward: relaxation of ew rows at a relu, then the fc product.
 // Per element: ep = max(x, 0), en = min(x, 0); e = ep * lo_s + en * up_s
 // (+ beta); row part en * up_t (+ e * bias[k]); lo_s from the alpha
@@ -53,6 +60,7 @@ struct LoadRelaxRow {
   float* relax_out;
   int ew_bcast;  // rows shared by all domains: row m reads ew[m % R]
   const int64_t* alpha_group = nullptr;  // per-row alpha of domain d's group: (G, R, ld)
+  int64_t n_groups = 0;                   // G: an index outside [0, G) reads group 0
   struct Row {
     int64_t xo, dom, mo, ao;  // offsets of the ew row, the domain's neurons, row m, alpha
     bool ro;                  // this tile writes relax_out
@@ -62,7 +70,7 @@ struct LoadRelaxRow {
   };
   __device__ Row row(int64_t, int64_t m, bool first) const {
     const int64_t d = m / R;
-    const int64_t ao = alpha_group ? (alpha_group[d] * R + (m - d * R)) * ld
+    const int64_t ao = alpha_group ? (safe_group(alpha_group, n_groups, d) * R + (m - d * R)) * ld
                                    : (alpha_per_row ? m * ld : d * ld);
     return Row{(ew_bcast ? m - d * R : m) * ld, d * ld, m * ld, ao,
                first && relax_out != nullptr};
@@ -311,7 +319,7 @@ template <bool VEC>
 __global__ __launch_bounds__(NT) void k_relax_rows(const float* ew, int64_t M, int R, int n,
                                                    const float* lo, const float* hi,
                                                    const float* alpha, int alpha_per_row,
-                                                   const int64_t* alpha_group,
+                                                   const int64_t* alpha_group, int64_t n_groups,
                                                    const float* beta, const float* bias,
                                                    int ew_bcast, float* out, float* acc) {
   __shared__ double red[NT / 64][RR];
@@ -343,8 +351,9 @@ __global__ __launch_bounds__(NT) void k_relax_rows(const float* ew, int64_t M, i
         ld4<VEC>(lo + dr[k] * n + c, cnt, l4);
         ld4<VEC>(hi + dr[k] * n + c, cnt, h4);
         if (alpha) {
-          const int64_t ar = alpha_group ? alpha_group[dr[k]] * R + (mr[k] - dr[k] * R)
-                                         : (alpha_per_row ? mr[k] : dr[k]);
+          const int64_t ar = alpha_group
+                                 ? safe_group(alpha_group, n_groups, dr[k]) * R + (mr[k] - dr[k] * R)
+                                 : (alpha_per_row ? mr[k] : dr[k]);
           ld4<VEC>(alpha + ar * n + c, cnt, a4);
         }
         if (beta) ld4<VEC>(beta + dr[k] * n + c, cnt, b4);
@@ -451,6 +460,7 @@ __global__ __launch_bounds__(NT) void k_relax_rows_narrow(const float* ew, int64
                                                           int n, const float* lo, const float* hi,
                                                           const float* alpha, int alpha_per_row,
                                                           const int64_t* alpha_group,
+                                                          int64_t n_groups,
                                                           const float* beta, const float* bias,
                                                           int ew_bcast, float* out, float* acc) {
   const int c = 4 * (threadIdx.x & 15);
@@ -467,7 +477,7 @@ __global__ __launch_bounds__(NT) void k_relax_rows_narrow(const float* ew, int64
       ld4<VEC>(lo + d * n + c, cnt, l4);
       ld4<VEC>(hi + d * n + c, cnt, h4);
       if (alpha) {
-        const int64_t ar = alpha_group ? alpha_group[d] * R + (m - d * R)
+        const int64_t ar = alpha_group ? safe_group(alpha_group, n_groups, d) * R + (m - d * R)
                                        : (alpha_per_row ? m : d);
         ld4<VEC>(alpha + ar * n + c, cnt, a4);
       }
@@ -507,7 +517,7 @@ namespace {
 
 int backward_fc(const float* ew_in, int64_t M, int R, int n_out, const float* relu_lo,
                 const float* relu_hi, const float* alpha, int alpha_per_row,
-                const int64_t* alpha_group, const float* beta, const float* W,
+                const int64_t* alpha_group, int64_t n_groups, const float* beta, const float* W,
                 const float* bias, int n_in, float* ew_out, float* acc, float* relax_out,
                 int ew_bcast, vc_stream_t stream) {
   if (!ew_in || !W || !ew_out || R <= 0 || n_out <= 0 || n_in <= 0 || M < 0) return VC_ERR_ARG;
@@ -525,11 +535,11 @@ int backward_fc(const float* ew_in, int64_t M, int R, int n_out, const float* re
       const int64_t grid = (M + RN - 1) / RN < kMaxGrid ? (M + RN - 1) / RN : kMaxGrid;
       if (v1)
         hipLaunchKernelGGL(k_relax_rows_narrow<true>, dim3((unsigned)grid), dim3(NT), 0, st,
-                           ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group,
+                           ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group, n_groups,
                            beta, bias, ew_bcast, relax_out, acc);
       else
         hipLaunchKernelGGL(k_relax_rows_narrow<false>, dim3((unsigned)grid), dim3(NT), 0, st,
-                           ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group,
+                           ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group, n_groups,
                            beta, bias, ew_bcast, relax_out, acc);
       VC_LAUNCH_CHECK();
       return launch_gemm<1, false>(1, M, n_in, n_out, LoadRow{relax_out, n_out}, LoadW{W, n_in},
@@ -539,11 +549,11 @@ int backward_fc(const float* ew_in, int64_t M, int R, int n_out, const float* re
     const int64_t grid = (M + RR - 1) / RR < kMaxGrid ? (M + RR - 1) / RR : kMaxGrid;
     if (v1)
       hipLaunchKernelGGL(k_relax_rows<true>, dim3((unsigned)grid), dim3(NT), 0, st, ew_in, M, R,
-                         n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group, beta, bias,
+                         n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group, n_groups, beta, bias,
                          ew_bcast, relax_out, acc);
     else
       hipLaunchKernelGGL(k_relax_rows<false>, dim3((unsigned)grid), dim3(NT), 0, st, ew_in, M, R,
-                         n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group, beta, bias,
+                         n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group, n_groups, beta, bias,
                          ew_bcast, relax_out, acc);
     VC_LAUNCH_CHECK();
     return launch_gemm<1, false>(1, M, n_in, n_out, LoadRow{relax_out, n_out}, LoadW{W, n_in},
@@ -555,7 +565,7 @@ int backward_fc(const float* ew_in, int64_t M, int R, int n_out, const float* re
                                  EpStoreBias{nullptr, ew_out, n_in}, nullptr,
                                  vec_ok({ew_in, W}, {n_out, n_in}), st);
   LoadRelaxRow la{ew_in, n_out, R, relu_lo, relu_hi, alpha, beta, bias, alpha_per_row, relax_out,
-                  ew_bcast, alpha_group};
+                  ew_bcast, alpha_group, n_groups};
   const bool vec = vec_ok({ew_in, relu_lo, relu_hi, alpha, beta, W}, {n_out, n_in});
   return launch_gemm<1, true>(1, M, n_in, n_out, la, LoadW{W, n_in},
                               EpStoreBias{nullptr, ew_out, n_in}, acc, vec, st);
@@ -569,19 +579,19 @@ extern "C" int vc_backward_fc(const float* ew_in, int64_t M, int R, int n_out,
                               const float* W, const float* bias, int n_in, float* ew_out,
                               float* acc, float* relax_out, int ew_bcast,
                               vc_stream_t stream) {
-  return backward_fc(ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, nullptr, beta,
+  return backward_fc(ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, nullptr, 0, beta,
                      W, bias, n_in, ew_out, acc, relax_out, ew_bcast, stream);
 }
 
 extern "C" int vc_backward_fc_grouped(const float* ew_in, int64_t M, int R, int n_out,
                                       const float* relu_lo, const float* relu_hi,
                                       const float* alpha_groups, const int64_t* group,
-                                      const float* W, const float* bias, int n_in,
-                                      float* ew_out, float* acc, float* relax_out, int ew_bcast,
-                                      vc_stream_t stream) {
-  if (!relu_lo || !alpha_groups || !group) return VC_ERR_ARG;
-  return backward_fc(ew_in, M, R, n_out, relu_lo, relu_hi, alpha_groups, 0, group, nullptr, W,
-                     bias, n_in, ew_out, acc, relax_out, ew_bcast, stream);
+                                      int64_t n_groups, const float* W, const float* bias,
+                                      int n_in, float* ew_out, float* acc, float* relax_out,
+                                      int ew_bcast, vc_stream_t stream) {
+  if (!relu_lo || !alpha_groups || !group || n_groups < 1) return VC_ERR_ARG;
+  return backward_fc(ew_in, M, R, n_out, relu_lo, relu_hi, alpha_groups, 0, group, n_groups,
+                     nullptr, W, bias, n_in, ew_out, acc, relax_out, ew_bcast, stream);
 }
 
 extern "C" int vc_alpha_grad_step(const float* gE, const float* P, int64_t M, int R, int n,

@@ -89,6 +89,19 @@ __global__ __launch_bounds__(NT) void k_best_rows_A(float* best, const float* lb
   }
 }
 
+// out[b] = group[b] when it lies in [0, n_groups), else 0 and *bad = 1
+// (written only by a thread that found a bad index).
+__global__ void k_group_clamp(const int64_t* __restrict__ group, int64_t B, int64_t n_groups,
+                              int64_t* __restrict__ out, int32_t* __restrict__ bad) {
+  for (int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; b < B;
+       b += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t g = group[b];
+    const bool ok = (uint64_t)g < (uint64_t)n_groups;
+    out[b] = ok ? g : 0;
+    if (!ok) *bad = 1;
+  }
+}
+
 }  // namespace
 
 extern "C" int vc_alpha_grad_rows(const float* gE, const float* P, int p_bcast, int64_t M, int R,
@@ -110,6 +123,16 @@ extern "C" int vc_bound_tighten(float* lo, float* hi, const float* sl, int64_t B
   if (!lo || !hi || !sl) return VC_ERR_ARG;
   hipLaunchKernelGGL(k_bound_tighten, dim3(vc_blocks(B * n, NT)), dim3(NT), 0,
                      (hipStream_t)stream, lo, hi, sl, B, n);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_group_clamp(const int64_t* group, int64_t B, int64_t n_groups, int64_t* out,
+                              int32_t* bad, vc_stream_t stream) {
+  if (!group || !out || !bad || B < 0 || n_groups < 1) return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  hipLaunchKernelGGL(k_group_clamp, dim3(vc_blocks(B, 256)), dim3(256), 0, (hipStream_t)stream,
+                     group, B, n_groups, out, bad);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }

@@ -42,8 +42,9 @@ SIGNATURES = {
     'vc_zono_relu_apply': [_P, _P, _P, _P, _P, _L, _I, _I, _I, _P, _P, _P],
     'vc_backward_fc': [_P, _L, _I, _I, _P, _P, _P, _I, _P, _P, _P, _I, _P,
                        _P, _P, _I, _P],
-    'vc_backward_fc_grouped': [_P, _L, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P,
+    'vc_backward_fc_grouped': [_P, _L, _I, _I, _P, _P, _P, _P, _L, _P, _P, _I, _P, _P, _P,
                                _I, _P],
+    'vc_group_clamp': [_P, _L, _L, _P, _P, _P],
     'vc_backward_relu': [_P, _L, _I, _I, _P, _P, _P, _I, _P, _P, _P, _P],
     'vc_relax_slopes': [_P, _P, _P, _L, _P, _P, _P, _P],
     'vc_alpha_grad_step_slopes': [_P, _P, _L, _I, _I, _P, _P, _P, _I, _P, _P,

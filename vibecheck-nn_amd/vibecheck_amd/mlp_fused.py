@@ -8,6 +8,7 @@ spec backward run as one wavefront per domain (vc_mlp_* entry points);
 other nets use the layer-wise kernels.
 """
 import ctypes
+import threading
 
 import torch
 
@@ -74,9 +75,6 @@ class MlpPlan:
             self.frag[fwd] = buf
         # fragments of the shape-specialised CROWN kernel (None: no instantiation)
         self.tfrag = None
-        # work counters of the shape-specialised CROWN and zonotope kernels
-        # (reset by each call; calls on one plan are ordered on one stream)
-        self.queue = torch.zeros(2, dtype=torch.int32, device=device)
         nt = int(lib.vc_mlp_tiled_floats(self.dims_p, self.n))
         if nt > 0:
             bp_arr, bp = host_array(ctypes.c_void_p, [ptr(b) for b in self.bs])
@@ -148,8 +146,11 @@ def zono_bounds(plan, xl, xh, fallback):
         # compacted on the device
         ovf = torch.empty(B, dtype=torch.uint8, device=dev)
         args = (B, ptr(xl), ptr(xh), lo_p, hi_p, ptr(ovf))
+        # the domain queue's counter, per call (the library resets it on the
+        # stream), so calls from several host threads never share one
+        queue = torch.empty(1, dtype=torch.int32, device=dev)
         call('vc_mlp_tiled_zono_bounds', plan.dims_p, plan.n, ptr(plan.tfrag),
-             ptr(plan.bias_cat), *args, plan.queue[1:].data_ptr(), stream())
+             ptr(plan.bias_cat), *args, ptr(queue), stream())
         lst, cnt = _compact_device(ovf)
         call('vc_mlp_tiled_zono_wide', plan.dims_p, plan.n, ptr(plan.tfrag),
              ptr(plan.bias_cat), *args, ptr(lst), ptr(cnt), stream())
@@ -234,29 +235,29 @@ def alpha_supported(plan, Q):
     return _tiled(plan) or plan.n <= ALPHA_MAX_L
 
 
-_STOP_WORD = None
+# Pinned host words the library's kernels store into and the host polls:
+# one set per host thread, so rounds and alpha loops run from different
+# threads (on their own streams) never read each other's words.
+_HOST_WORDS = threading.local()
 
 
 def _stop_word():
     """A pinned host int32 the alpha loop's control kernel sets when the loop
-    stops, so that the host stops enqueueing iterations (one per process;
-    each alpha loop ends with a host read, so it is free again)."""
-    global _STOP_WORD
-    if _STOP_WORD is None:
-        _STOP_WORD = torch.zeros(1, dtype=torch.int32, pin_memory=True)
-    return _STOP_WORD
-
-
-_PINNED_WORDS = None
+    stops, so that the host stops enqueueing iterations (one per host
+    thread; each alpha loop ends with a host read, so it is free again)."""
+    w = getattr(_HOST_WORDS, 'stop', None)
+    if w is None:
+        w = _HOST_WORDS.stop = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    return w
 
 
 def _pinned_words():
     """Pinned host int64 words the native BaB round's counts are stored in
-    (one set per process; each round ends with them read)."""
-    global _PINNED_WORDS
-    if _PINNED_WORDS is None:
-        _PINNED_WORDS = torch.zeros(4, dtype=torch.int64, pin_memory=True)
-    return _PINNED_WORDS
+    (one set per host thread; each round ends with them read)."""
+    w = getattr(_HOST_WORDS, 'counts', None)
+    if w is None:
+        w = _HOST_WORDS.counts = torch.zeros(4, dtype=torch.int64, pin_memory=True)
+    return w
 
 
 def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps, lazy=False):
@@ -418,7 +419,8 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False, per_domain=F
             call('vc_mlp_tiled_crown', plan.dims_p, plan.n, ptr(plan.tfrag), ptr(plan.bias_cat),
                  B, ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,
                  1 if do_crown else 0, 1 if per_domain else 0, Q, ptr(S), ptr(acc0), ptr(lb),
-                 ptr(A), ptr(acc), ptr(seeds), plan.queue.data_ptr(), stream())
+                 ptr(A), ptr(acc), ptr(seeds),
+                 ptr(torch.empty(2, dtype=torch.int32, device=dev)), stream())
     else:
         call('vc_mlp_crown', plan.dims_p, plan.n, ptr(plan.frag[0]), ptr(plan.bias_cat), B,
              ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,

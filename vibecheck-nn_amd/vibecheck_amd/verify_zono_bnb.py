@@ -413,7 +413,8 @@ class _Rows:
     ``alpha``/``beta`` belong to that pending relu; ``alpha_group`` (B,)
     int64 makes ``alpha`` (G*R, n) the rows of each domain's group.
     """
-    __slots__ = ('ew', 'shared', 'relu', 'alpha', 'alpha_row', 'beta', 'alpha_group')
+    __slots__ = ('ew', 'shared', 'relu', 'alpha', 'alpha_row', 'beta', 'alpha_group',
+                 'n_groups')
 
     def __init__(self, ew, shared):
         self.ew = ew
@@ -423,6 +424,7 @@ class _Rows:
         self.alpha_row = 0
         self.beta = None
         self.alpha_group = None
+        self.n_groups = 0
 
 
 class BackwardTrace:
@@ -576,7 +578,7 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
                             'vibecheck_amd: group-indexed alpha takes no beta')
                     call('vc_backward_fc_grouped', ptr(rows.ew), M, R, p['n_out'],
                          ptr(lo), ptr(hi), ptr(rows.alpha), ptr(rows.alpha_group),
-                         ptr(p['W']), ptr(p['b']), p['n_in'], ptr(out), ptr(acc),
+                         rows.n_groups, ptr(p['W']), ptr(p['b']), p['n_in'], ptr(out), ptr(acc),
                          ptr(rel), 1 if rows.shared else 0, st)
                 else:
                     call('vc_backward_fc', ptr(rows.ew), M, R, p['n_out'],
@@ -608,6 +610,7 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
                         rows.alpha = f32(a[0]).reshape(-1, a[0].shape[-1])
                         rows.alpha_row = 0
                         rows.alpha_group = a[1]
+                        rows.n_groups = int(a[0].shape[0])
                         a = None
                     else:
                         a = f32(a)
