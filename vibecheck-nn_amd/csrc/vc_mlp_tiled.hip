@@ -186,6 +186,10 @@ __device__ __forceinline__ void fc_hidden(const float4* fr, int lane, int g, int
   for (int p = 0; p < NP; ++p)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) o[p][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  // the MFMA block at raised wave priority: a wavefront ready to issue its
+  // MFMAs wins the arbitration, and the other wavefronts' relaxation VALU
+  // work fills the matrix unit's gaps (2% faster on the CROWN rows pass)
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const float4 a4 = fr[ks * 64 + swz(lane, ks)];
@@ -195,6 +199,7 @@ __device__ __forceinline__ void fc_hidden(const float4* fr, int lane, int g, int
 #pragma unroll
       for (int p = 0; p < NP; ++p) o[p][mt] = mfma16x16x4(a[mt], F[p][ks >> 2][ks & 3], o[p][mt]);
   }
+  __builtin_amdgcn_s_setprio(0);
   if (BROW) {
     // the bias row's entry: (M-tile, component) is the same for every lane,
     // so a scalar branch picks it
@@ -1924,9 +1929,11 @@ __device__ __forceinline__ void fc0_concretize_pr(const float* fr0, int mt0, int
                                                   float* A_rows, int n_live) {
   for (int mt = 0; mt < mt0; ++mt) {
     v4f o = v4f{0.f, 0.f, 0.f, 0.f};
+    __builtin_amdgcn_s_setprio(1);  // as in fc_hidden
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       o = mfma16x16x4(fr0[(mt * KS + ks) * 64 + swz(lane, ks)], F[0][ks >> 2][ks & 3], o);
+    __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = 16 * mt + 4 * g + i;
