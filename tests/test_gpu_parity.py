@@ -902,6 +902,28 @@ def test_concretize_tiled_matches_thread_form(gpu, n, R, B):
     assert bool(((out['tile'].double() - ref).abs() <= 1e-6 * scale + 1e-7).all())
 
 
+@pytest.mark.parametrize('n', [1, 15, 16, 17, 1000, 16383, 16384, 16385, 65536, 131072,
+                               131073, 300001])
+def test_compaction_against_nonzero(gpu, n):
+    """vc_compact (one workgroup up to 2^17 flags, three launches above)
+    against torch.nonzero on the host: the ascending positions of the set
+    flags, and of the clear ones with select_zero, for 16-byte aligned and
+    unaligned flag arrays (verify_graph.py:12986, 13115)."""
+    from vibecheck_amd import verify_graph as vg
+    g = torch.Generator().manual_seed(n)
+    f = torch.rand(n + 1, generator=g) < 0.37
+    for fl in (f[:n], f[1:]):
+        ref_flags = fl.clone()
+        fg = fl.to(gpu)
+        if fl is f[1:]:
+            fg = f.to(gpu)[1:]
+            assert fg.data_ptr() % 16 != 0
+        for zero in (False, True):
+            got = vg._compact(fg, select_zero=zero).cpu()
+            ref = (~ref_flags if zero else ref_flags).nonzero(as_tuple=True)[0]
+            assert torch.equal(got, ref), (n, zero)
+
+
 def test_row_kernels_beyond_grid_cap(gpu):
     """The one-wavefront-per-row kernels cover every row when there are more
     rows than one launch has wavefronts (1,048,576 workgroups x 4 waves =

@@ -975,6 +975,60 @@ __global__ void k_compact_write(const uint8_t* f, int64_t n, int zero, const int
     if (sel_hit(f, base + e, n, zero)) idx[o++] = base + e;
 }
 
+// Compaction of up to C1N flags in one launch: one workgroup sweeps the
+// flags in passes of C1T x C1P, each thread C1P consecutive flags (one
+// 16-byte load when VEC), a workgroup scan per pass and a running carry.
+// The same ascending indices as the three-launch form, without its two
+// extra launches (the round's compactions are of 65,536 flags or fewer).
+constexpr int C1T = 1024, C1P = 16;
+constexpr int64_t C1N = (int64_t)1 << 17;
+
+template <bool VEC>
+__global__ __launch_bounds__(C1T) void k_compact_single(const uint8_t* __restrict__ f, int64_t n,
+                                                         int zero, int64_t* __restrict__ idx,
+                                                         int64_t* __restrict__ count_out) {
+  __shared__ int wsum[C1T / 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int64_t carry = 0;
+  for (int64_t c0 = 0; c0 < n; c0 += (int64_t)C1T * C1P) {
+    const int64_t base = c0 + (int64_t)threadIdx.x * C1P;
+    uint32_t bits = 0;
+    if (VEC && base + C1P <= n) {
+      const uint4 v = *reinterpret_cast<const uint4*>(f + base);
+      const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < C1P; ++e) {
+        const bool set = ((wd[e >> 2] >> (8 * (e & 3))) & 0xffu) != 0;
+        if (set != (zero != 0)) bits |= 1u << e;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < C1P; ++e)
+        if (sel_hit(f, base + e, n, zero)) bits |= 1u << e;
+    }
+    const int c = __popc(bits);
+    int x = c;  // inclusive scan within the wave
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wsum[w] = x;
+    __syncthreads();
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < C1T / 64; ++i) {
+      if (i < w) off += wsum[i];
+      tot += wsum[i];
+    }
+    int64_t o = carry + off + x - c;
+    for (int e = 0; e < C1P; ++e)
+      if ((bits >> e) & 1u) idx[o++] = base + e;
+    carry += tot;
+    __syncthreads();  // wsum is rewritten by the next pass
+  }
+  if (threadIdx.x == 0) count_out[0] = carry;
+}
+
 // rows[idx[r]] = max(rows[idx[r]], src[r]) over rows of q floats.
 __global__ void k_scatter_max_rows(float* rows, const int64_t* idx, const float* src, int64_t nr,
                                    int q) {
@@ -1432,6 +1486,16 @@ extern "C" int vc_compact(const uint8_t* flags, int64_t n, int select_zero, int6
   int64_t nb = (n + CCH - 1) / CCH;
   if (nb < 1) nb = 1;
   if (nb > 2147483647LL) return VC_ERR_ARG;
+  if (n <= C1N) {
+    if (aligned16(flags))
+      hipLaunchKernelGGL(k_compact_single<true>, dim3(1), dim3(C1T), 0, st, flags, n, select_zero,
+                         idx_out, count_out);
+    else
+      hipLaunchKernelGGL(k_compact_single<false>, dim3(1), dim3(C1T), 0, st, flags, n,
+                         select_zero, idx_out, count_out);
+    VC_LAUNCH_CHECK();
+    return VC_OK;
+  }
   int64_t* bc = (int64_t*)workspace;
   hipLaunchKernelGGL(k_compact_count, dim3((unsigned)nb), dim3(NT), 0, st, flags, n, select_zero,
                      bc);
