@@ -389,7 +389,7 @@ def kernel_suite(reps):
     kernels) per launch, the average launch time and the fraction of the
     MI355X peak.  A plain device copy gives the achievable HBM rate."""
     from vibecheck_amd import _lib
-    from vibecheck_amd._lib import call, ptr, stream
+    from vibecheck_amd._lib import call, load, ptr, stream
 
     dev = torch.device('cuda:0')
     _lib.load()
@@ -591,15 +591,26 @@ def kernel_suite(reps):
         bias = rndn(C_out) * 0.01
         out = torch.empty(M, C_in * H * H, device=dev)
         acc = torch.zeros(M, device=dev)
-        fn = lambda: call('vc_backward_conv', ptr(ew), M, ptr(K), ptr(bias), C_out, Ho, Ho, C_in,
-                          H, H, k, k, cs, cs, cp, cp, ptr(out), ptr(acc), st)
-        kern = ('k_conv_t_smallc' if C_in <= 4 else
-                'gemm_kernel (transposed conv, implicit GEMM)') + ' + k_conv_bias_dot'
-        report('a7', kern,
-               f'conv {C_in}->{C_out} {k}x{k} s{cs} p{cp} ({H}x{H} in), 576 rows '
-               '(64 domains x 9)', _time_launches([fn], max(3, reps // 4)), 'mfma',
-               2.0 * M * (C_out * Ho * Ho) * (C_in * k * k))
-        del ew, out, acc
+        KT = torch.empty(load().vc_conv_t_pack_floats(C_out, C_in, k, k, cs, cs), device=dev)
+        call('vc_conv_t_pack', ptr(K), C_out, C_in, k, k, cs, cs, cp, cp, ptr(KT), st)
+        fn = lambda: call('vc_backward_conv_packed', ptr(ew), M, ptr(K), ptr(KT), ptr(bias),
+                          C_out, Ho, Ho, C_in, H, H, k, k, cs, cs, cp, cp, ptr(out), ptr(acc),
+                          st)
+        work = f'conv {C_in}->{C_out} {k}x{k} s{cs} p{cp} ({H}x{H} in), 576 rows (64 domains x 9)'
+        flop = 2.0 * M * (C_out * Ho * Ho) * (C_in * k * k)
+        if C_in <= 4:
+            report('a7', 'k_conv_t_smallc + k_conv_bias_dot', work,
+                   _time_launches([fn], max(3, reps // 4)), 'mfma', flop)
+        else:
+            report('a7', 'gemm_kernel<LoadPackedT> (transposed conv, packed taps) + '
+                   'k_conv_bias_dot', work, _time_launches([fn], max(3, reps // 4)), 'mfma',
+                   flop)
+            fn = lambda: call('vc_backward_conv', ptr(ew), M, ptr(K), ptr(bias), C_out, Ho, Ho,
+                              C_in, H, H, k, k, cs, cs, cp, cp, ptr(out), ptr(acc), st)
+            report('a7', 'gemm_kernel<LoadKernelT> (transposed conv, taps from the kernel) + '
+                   'k_conv_bias_dot', work, _time_launches([fn], max(3, reps // 4)), 'mfma',
+                   flop)
+        del ew, out, acc, KT
 
     # -- a2: interval forward through the CNN's second convolution, 64 boxes
     C_in, H, C_out, k, cs, cp, B = 32, 32, 64, 4, 2, 1, 64
@@ -679,6 +690,7 @@ LAYERWISE_MFMA = {
     'vc_backward_fc': lambda a: 2.0 * a[1] * a[3] * a[11],
     # 2 M (C_out H_out W_out)(C_in kh kw)
     'vc_backward_conv': lambda a: 2.0 * a[1] * a[4] * a[5] * a[6] * a[7] * a[10] * a[11],
+    'vc_backward_conv_packed': lambda a: 2.0 * a[1] * a[5] * a[6] * a[7] * a[8] * a[11] * a[12],
     # 2 M n n_next
     'vc_alpha_grad_step_slopes': lambda a: 2.0 * a[2] * a[4] * a[11],
     'vc_alpha_grad_step': lambda a: 2.0 * a[2] * a[4] * a[11],

@@ -244,6 +244,28 @@ int vc_backward_conv(const float *ew_in, int64_t M, const float *kernel,
                      int ph, int pw, float *ew_out, float *acc,
                      vc_stream_t stream);
 
+/* The taps of the transposed convolution packed once per kernel for
+ * vc_backward_conv_packed: for each of the sh * sw output-parity classes,
+ * C_in rows of C_out * ceil(kh / sh) * ceil(kw / sw) taps (zero past the
+ * kernel), rows padded to a multiple of 4 floats; vc_conv_t_pack_floats
+ * gives the size.  The reference has no counterpart (it calls
+ * conv_transpose2d, verify_zono_bnb.py:4568-4593): the packing is this
+ * build's weight cache, like the reference's cached op tensors
+ * (verify_zono_bnb.py:4482-4486). */
+int64_t vc_conv_t_pack_floats(int C_out, int C_in, int kh, int kw, int sh, int sw);
+int vc_conv_t_pack(const float *kernel, int C_out, int C_in, int kh, int kw, int sh,
+                   int sw, int ph, int pw, float *out, vc_stream_t stream);
+
+/* vc_backward_conv reading the packed taps (16-byte aligned, from
+ * vc_conv_t_pack of the same kernel and geometry) instead of deriving each
+ * tap from the kernel in every K-tile: the same values in the same order,
+ * so the same results bit for bit.  kernel is still read when C_in <= 4
+ * (that form takes no packing).  Replaces verify_zono_bnb.py:4568-4593. */
+int vc_backward_conv_packed(const float *ew_in, int64_t M, const float *kernel,
+                            const float *packed, const float *bias, int C_out, int H_out,
+                            int W_out, int C_in, int H, int W, int kh, int kw, int sh, int sw,
+                            int ph, int pw, float *ew_out, float *acc, vc_stream_t stream);
+
 /* Concretization over the input boxes:
  *   lb[m] = acc[m] + sum_i pos(A[m,i]) xl[b,i] + neg(A[m,i]) xh[b,i].
  * A (M, n_in), acc/lb (M), xl/xh (B, n_in), M = B * R.  With a_bcast != 0,

@@ -19,7 +19,7 @@ from oracle import ref_bound as rb
 from vibecheck_amd import verify_graph as vg
 from vibecheck_amd import verify_zono_bnb as vz
 from vibecheck_amd import workloads as wk
-from vibecheck_amd._lib import call, ptr
+from vibecheck_amd._lib import call, load, ptr
 from vibecheck_amd._lib import stream as _lib_stream
 
 import _util
@@ -340,6 +340,23 @@ def test_conv_layers_against_fp64(gpu, geom):
     torch.cuda.synchronize()
     close(out, ref.reshape(M, -1), rsc.reshape(M, -1), 'conv_transpose')
     close(acc, aref, asc, 'conv bias dot')
+
+    # the packed-tap form: the same values in the same order, so the same
+    # bits; a packing at an address not 16-byte aligned takes the unpacked
+    # loader (same bits again)
+    n_pack = load().vc_conv_t_pack_floats(C_out, C_in, k, k, s, s)
+    Ty, Tx = -(-k // s), -(-k // s)
+    assert n_pack == s * s * C_in * ((C_out * Ty * Tx + 3) // 4 * 4)
+    KT = torch.full((n_pack + 1,), float('nan'), device=gpu)
+    for base in (KT[:n_pack], KT[1:]):
+        call('vc_conv_t_pack', ptr(dK), C_out, C_in, k, k, s, s, p, p, ptr(base), st)
+        out2 = torch.empty_like(out)
+        acc2 = acc0.to(gpu)
+        call('vc_backward_conv_packed', ptr(dew), M, ptr(dK), ptr(base), ptr(db), C_out, Ho, Wo,
+             C_in, H, W, k, k, s, s, p, p, ptr(out2), ptr(acc2), st)
+        torch.cuda.synchronize()
+        assert torch.equal(out2, out) and torch.equal(acc2, acc), (geom, base.data_ptr() % 16)
+        assert not bool(base.isnan().any())
 
 
 # ----------------------------------------------------------------- a1

@@ -224,6 +224,60 @@ struct LoadKernelT {
   }
 };
 
+// Pre-packed transposed taps (vc_conv_t_pack): class bz's A rows at
+// A + bz * cs, row ci at ci * ld, so the loader does no tap arithmetic.
+// The same values in the same k order as LoadKernelT, the same K-tiles.
+struct LoadPackedT {
+  static constexpr int kBK = 32;
+  static constexpr bool kSmallM = true;
+  const float* A;
+  int64_t cs;  // floats per parity class
+  int ld;      // floats per row (Kd rounded up to 4)
+  struct Row {
+    int64_t o;
+  };
+  struct Raw {
+    float x[4];
+  };
+  __device__ Row row(int64_t bz, int64_t m, bool) const { return Row{bz * cs + m * ld}; }
+  template <bool VEC>
+  __device__ void fetch(const Row& rw, int k, int n, Raw& x) const {
+    // rows are 16-byte aligned (ld a multiple of 4, A from the allocator)
+    ld4<true>(A + rw.o + k, n, x.x);
+  }
+  template <bool VEC>
+  __device__ void finish(const Row&, int, int, const Raw& x, float (*v)[4], KSum&, bool) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[0][j] = x.x[j];
+  }
+};
+
+// A[bz][ci][(co, ty, tx)] = K[co][ci][ky0 + sh ty][kx0 + sw tx] for every
+// parity class bz (LoadKernelT's values), zero past the kernel and in the
+// row padding.
+__global__ void k_conv_t_pack(const float* __restrict__ K, ConvGeom g, int Ty, int Tx, int ld,
+                              float* __restrict__ out) {
+  const int classes = g.sh * g.sw;
+  const int64_t total = (int64_t)classes * g.C_in * ld;
+  const int Kd = g.C_out * Ty * Tx;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int k = (int)(t % ld);
+    const int64_t rest = t / ld;
+    const int ci = (int)(rest % g.C_in);
+    const int bz = (int)(rest / g.C_in);
+    float v = 0.f;
+    if (k < Kd) {
+      const int co = k / (Ty * Tx), tt = k % (Ty * Tx);
+      const int ty = tt / Tx, tx = tt % Tx;
+      const int ky = tap_class(bz / g.sw, g.ph, g.sh).k0 + g.sh * ty;
+      const int kx = tap_class(bz % g.sw, g.pw, g.sw).k0 + g.sw * tx;
+      if (ky < g.kh && kx < g.kw) v = K[(((int64_t)co * g.C_in + ci) * g.kh + ky) * g.kw + kx];
+    }
+    out[t] = v;
+  }
+}
+
 // ------------------------------------------------------------ epilogues
 // Forward outputs: column n = img * per_img + r -> out[img * o_img + m * o_c + r]
 // (r = pix * nk + g).  NA = 2: interval (lo, hi) = mid + bias -/+ rad.
@@ -458,10 +512,18 @@ extern "C" int vc_zono_conv(const float* c, const float* G, int64_t B, int Kg, i
                                gb, ep, nullptr, false, st);
 }
 
-extern "C" int vc_backward_conv(const float* ew_in, int64_t M, const float* kernel,
-                                const float* bias, int C_out, int H_out, int W_out, int C_in,
-                                int H, int W, int kh, int kw, int sh, int sw, int ph, int pw,
-                                float* ew_out, float* acc, vc_stream_t stream) {
+namespace {
+
+// Row length of the packed transposed taps: C_out Ty Tx rounded up to 4.
+int conv_t_ld(int C_out, int kh, int kw, int sh, int sw) {
+  const int Ty = (kh + sh - 1) / sh, Tx = (kw + sw - 1) / sw;
+  return (C_out * Ty * Tx + 3) & ~3;
+}
+
+int backward_conv(const float* ew_in, int64_t M, const float* kernel, const float* packed,
+                  const float* bias, int C_out, int H_out, int W_out, int C_in, int H, int W,
+                  int kh, int kw, int sh, int sw, int ph, int pw, float* ew_out, float* acc,
+                  vc_stream_t stream) {
   ConvGeom g{C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, H_out, W_out};
   if (check_geom(g) != VC_OK || !ew_in || !kernel || !ew_out || M < 0) return VC_ERR_ARG;
   if (bias && !acc) return VC_ERR_ARG;
@@ -521,10 +583,56 @@ extern "C" int vc_backward_conv(const float* ew_in, int64_t M, const float* kern
   gb.f_wg = FastDiv::make((uint32_t)Wc);
   gb.f_T = FastDiv::make((uint32_t)gb.T);
   gb.f_Tx = FastDiv::make((uint32_t)Tx);
-  LoadKernelT la{kernel, C_in, kh, kw, sh, sw, ph, pw, Ty * Tx, Tx, Ty,
-                 FastDiv::make((uint32_t)(Ty * Tx)), FastDiv::make((uint32_t)Tx)};
   EpConvT ep{ew_out, H, W, Wc, sh, sw, npix, (int64_t)C_in * H * W,
              FastDiv::make((uint32_t)npix), FastDiv::make((uint32_t)Wc)};
+  if (packed && aligned16(packed)) {
+    const int ld = conv_t_ld(C_out, kh, kw, sh, sw);
+    LoadPackedT la{packed, (int64_t)C_in * ld, ld};
+    return launch_gemm<1, false>((int64_t)sh * sw, C_in, (int)N, (int)Kd, la, gb, ep, nullptr,
+                                 false, st);
+  }
+  LoadKernelT la{kernel, C_in, kh, kw, sh, sw, ph, pw, Ty * Tx, Tx, Ty,
+                 FastDiv::make((uint32_t)(Ty * Tx)), FastDiv::make((uint32_t)Tx)};
   return launch_gemm<1, false>((int64_t)sh * sw, C_in, (int)N, (int)Kd, la, gb, ep, nullptr, false,
                                st);
+}
+
+}  // namespace
+
+extern "C" int vc_backward_conv(const float* ew_in, int64_t M, const float* kernel,
+                                const float* bias, int C_out, int H_out, int W_out, int C_in,
+                                int H, int W, int kh, int kw, int sh, int sw, int ph, int pw,
+                                float* ew_out, float* acc, vc_stream_t stream) {
+  return backward_conv(ew_in, M, kernel, nullptr, bias, C_out, H_out, W_out, C_in, H, W, kh, kw,
+                       sh, sw, ph, pw, ew_out, acc, stream);
+}
+
+extern "C" int64_t vc_conv_t_pack_floats(int C_out, int C_in, int kh, int kw, int sh, int sw) {
+  if (C_out <= 0 || C_in <= 0 || kh <= 0 || kw <= 0 || sh <= 0 || sw <= 0) return -VC_ERR_ARG;
+  return (int64_t)sh * sw * C_in * conv_t_ld(C_out, kh, kw, sh, sw);
+}
+
+extern "C" int vc_conv_t_pack(const float* kernel, int C_out, int C_in, int kh, int kw, int sh,
+                              int sw, int ph, int pw, float* out, vc_stream_t stream) {
+  if (!kernel || !out || C_out <= 0 || C_in <= 0 || kh <= 0 || kw <= 0 || sh <= 0 || sw <= 0 ||
+      ph < 0 || pw < 0)
+    return VC_ERR_ARG;
+  ConvGeom g{C_in, 1, 1, C_out, kh, kw, sh, sw, ph, pw, 1, 1};
+  const int Ty = (kh + sh - 1) / sh, Tx = (kw + sw - 1) / sw;
+  const int ld = conv_t_ld(C_out, kh, kw, sh, sw);
+  const int64_t total = (int64_t)sh * sw * C_in * ld;
+  hipLaunchKernelGGL(k_conv_t_pack, dim3(vc_blocks(total, NT)), dim3(NT), 0, (hipStream_t)stream,
+                     kernel, g, Ty, Tx, ld, out);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+extern "C" int vc_backward_conv_packed(const float* ew_in, int64_t M, const float* kernel,
+                                       const float* packed, const float* bias, int C_out,
+                                       int H_out, int W_out, int C_in, int H, int W, int kh,
+                                       int kw, int sh, int sw, int ph, int pw, float* ew_out,
+                                       float* acc, vc_stream_t stream) {
+  if (!packed) return VC_ERR_ARG;
+  return backward_conv(ew_in, M, kernel, packed, bias, C_out, H_out, W_out, C_in, H, W, kh, kw,
+                       sh, sw, ph, pw, ew_out, acc, stream);
 }

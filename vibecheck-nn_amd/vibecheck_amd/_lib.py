@@ -51,6 +51,10 @@ SIGNATURES = {
                                   _I, _P, _P],
     'vc_backward_conv': [_P, _L, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                          _I, _I, _I, _P, _P, _P],
+    'vc_conv_t_pack_floats': [_I, _I, _I, _I, _I, _I],
+    'vc_conv_t_pack': [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P],
+    'vc_backward_conv_packed': [_P, _L, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I,
+                                _I, _I, _I, _P, _P, _P],
     'vc_concretize': [_P, _P, _P, _P, _L, _I, _I, _I, _P, _P],
     'vc_crown_intersect': [_P, _P, _I, _L, _I, _P, _P, _P],
     'vc_unstable_union': [_P, _P, _L, _I, _P, _P],
@@ -118,6 +122,7 @@ SIGNATURES = {
     'vc_bisect': [_P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P],
 }
 _RESTYPE = {'vc_compact_workspace': ctypes.c_int64,
+            'vc_conv_t_pack_floats': ctypes.c_int64,
             'vc_mlp_crown_rows_workspace': ctypes.c_int64,
             'vc_mlp_bab_round_workspace': ctypes.c_int64,
             'vc_mlp_frag_floats': ctypes.c_int64,

@@ -86,6 +86,23 @@ def _op_params(op, device):
     return p
 
 
+def _conv_t_taps(p, st):
+    """The conv kernel's transposed taps packed per output-parity class
+    (vc_conv_t_pack), made on first use by a backward pass and cached with
+    the op's other device tensors."""
+    packed = p.get('KT')
+    if packed is None:
+        C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, Ho, Wo = p['geom']
+        n = _lib.load().vc_conv_t_pack_floats(C_out, C_in, kh, kw, sh, sw)
+        if n < 0:
+            raise RuntimeError(f'vc_conv_t_pack_floats: bad geometry {p["geom"]}')
+        packed = torch.empty(n, device=p['K'].device)
+        call('vc_conv_t_pack', ptr(p['K']), C_out, C_in, kh, kw, sh, sw, ph, pw,
+             ptr(packed), st)
+        p['KT'] = packed
+    return packed
+
+
 def _pair(v):
     if isinstance(v, int):
         return v, v
@@ -633,9 +650,9 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
                 per_domain_acc()
             M = R if rows.shared else B * R
             out = torch.empty(M, p['n_in'], device=dev)
-            call('vc_backward_conv', ptr(rows.ew), M, ptr(p['K']),
-                 ptr(p['b']), C_out, Ho, Wo, C_in, H, W, kh, kw, sh, sw, ph,
-                 pw, ptr(out), ptr(acc), st)
+            call('vc_backward_conv_packed', ptr(rows.ew), M, ptr(p['K']),
+                 ptr(_conv_t_taps(p, st)), ptr(p['b']), C_out, Ho, Wo, C_in, H, W,
+                 kh, kw, sh, sw, ph, pw, ptr(out), ptr(acc), st)
             put(inp, _Rows(out, rows.shared))
         elif t == 'reshape':
             put(inp, rows)
