@@ -599,7 +599,7 @@ def kernel_suite(reps):
         work = f'conv {C_in}->{C_out} {k}x{k} s{cs} p{cp} ({H}x{H} in), 576 rows (64 domains x 9)'
         flop = 2.0 * M * (C_out * Ho * Ho) * (C_in * k * k)
         if C_in <= 4:
-            report('a7', 'k_conv_t_smallc + k_conv_bias_dot', work,
+            report('a7', 'k_conv_t_fold (MFMA GEMM + fold, bias dot fused)', work,
                    _time_launches([fn], max(3, reps // 4)), 'mfma', flop)
         else:
             report('a7', 'gemm_kernel<LoadPackedT> (transposed conv, packed taps) + '
@@ -611,6 +611,31 @@ def kernel_suite(reps):
                    'k_conv_bias_dot', work, _time_launches([fn], max(3, reps // 4)), 'mfma',
                    flop)
         del ew, out, acc, KT
+
+    # -- a6+a7: the relu relaxation fused into the first layer's conv
+    #    backward, rows shared by the domains until that relu (the CROWN
+    #    intermediate-bound chunks of the CNN): 64 domains x 512 rows
+    C_in, H, C_out, k, cs, cp = 3, 32, 32, 3, 1, 1
+    Ho, B, R = H, 64, 512
+    n = C_out * Ho * Ho
+    M = B * R
+    x = rndn(R, n)
+    lo = rndn(B, n)
+    hi = lo + rnd(B, n) * 2
+    ls, us, ut = (torch.empty(B, n, device=dev) for _ in range(3))
+    call('vc_relax_slopes', ptr(lo), ptr(hi), None, B * n, ptr(ls), ptr(us), ptr(ut), st)
+    K = rndn(C_out, C_in, k, k) * (2.0 / (C_in * k * k)) ** 0.5
+    bias = rndn(C_out) * 0.01
+    out = torch.empty(M, C_in * H * H, device=dev)
+    acc = torch.zeros(M, device=dev)
+    fn = lambda: call('vc_backward_relu_conv', ptr(x), M, R, 1, ptr(ls), ptr(us), ptr(ut), None,
+                      ptr(K), ptr(bias), C_out, Ho, Ho, C_in, H, H, k, k, cs, cs, cp, cp,
+                      ptr(out), ptr(acc), st)
+    report('a7', 'k_conv_t_fold<relu> (relu relaxation + MFMA GEMM + fold + bias dot)',
+           f'relu + conv {C_in}->{C_out} {k}x{k} s{cs} p{cp} ({H}x{H} in), {M:,} rows '
+           f'({B} domains x {R} shared rows)', _time_launches([fn], max(3, reps // 4)), 'mfma',
+           2.0 * M * n * (C_in * k * k))
+    del x, lo, hi, ls, us, ut, out, acc
 
     # -- a2: interval forward through the CNN's second convolution, 64 boxes
     C_in, H, C_out, k, cs, cp, B = 32, 32, 64, 4, 2, 1, 64
@@ -691,6 +716,7 @@ LAYERWISE_MFMA = {
     # 2 M (C_out H_out W_out)(C_in kh kw)
     'vc_backward_conv': lambda a: 2.0 * a[1] * a[4] * a[5] * a[6] * a[7] * a[10] * a[11],
     'vc_backward_conv_packed': lambda a: 2.0 * a[1] * a[5] * a[6] * a[7] * a[8] * a[11] * a[12],
+    'vc_backward_relu_conv': lambda a: 2.0 * a[1] * a[10] * a[11] * a[12] * a[13] * a[16] * a[17],
     # 2 M n n_next
     'vc_alpha_grad_step_slopes': lambda a: 2.0 * a[2] * a[4] * a[11],
     'vc_alpha_grad_step': lambda a: 2.0 * a[2] * a[4] * a[11],

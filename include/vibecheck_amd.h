@@ -266,6 +266,29 @@ int vc_backward_conv_packed(const float *ew_in, int64_t M, const float *kernel,
                             int W_out, int C_in, int H, int W, int kh, int kw, int sh, int sw,
                             int ph, int pw, float *ew_out, float *acc, vc_stream_t stream);
 
+/* The relu backward step fused into the following conv backward, for
+ * convolutions onto few values per tap set (C_in <= 4, C_in kh kw <= 32,
+ * C_out <= 64: the network's input layer; vc_backward_relu_conv_ok says
+ * whether a geometry qualifies, else VC_ERR_UNSUPPORTED and the caller
+ * takes vc_backward_relu + vc_backward_conv).  Row m = d * R + s of the
+ * M = B * R rows out is relaxed with domain d's slopes (lo_s, up_s, up_t
+ * from vc_relax_slopes, (B, C_out * H_out * W_out); beta the same shape or
+ * NULL) from input row s (ew_shared: ew_in holds the R rows every domain
+ * shares) or m, then transposed-convolved:
+ *   e = pos(x) lo_s + neg(x) up_s [+ beta];  acc[m] += neg(x) . up_t;
+ *   acc[m] += e . bias[channel];  ew_out[m] = conv_transpose2d(e).
+ * The same arithmetic as the two separate calls: ew_out is bit-identical,
+ * and acc differs from theirs only by the order of its fp64 sums.
+ * Replaces verify_zono_bnb.py:4409-4453 followed by 4568-4593. */
+int vc_backward_relu_conv_ok(int C_out, int H_out, int W_out, int C_in, int H, int W,
+                             int kh, int kw, int sh, int sw, int ph, int pw);
+int vc_backward_relu_conv(const float *ew_in, int64_t M, int64_t R, int ew_shared,
+                          const float *lo_s, const float *up_s, const float *up_t,
+                          const float *beta, const float *kernel, const float *bias,
+                          int C_out, int H_out, int W_out, int C_in, int H, int W,
+                          int kh, int kw, int sh, int sw, int ph, int pw,
+                          float *ew_out, float *acc, vc_stream_t stream);
+
 /* Concretization over the input boxes:
  *   lb[m] = acc[m] + sum_i pos(A[m,i]) xl[b,i] + neg(A[m,i]) xh[b,i].
  * A (M, n_in), acc/lb (M), xl/xh (B, n_in), M = B * R.  With a_bcast != 0,

@@ -16,6 +16,7 @@
 //     cy = (py + ph - ky0) / sh (the same along x), so no zero tap is
 //     multiplied.
 #include "vc_gemm_core.h"
+#include "vc_mlp_common.h"
 
 namespace {
 
@@ -384,6 +385,283 @@ __global__ __launch_bounds__(NT) void k_conv_t_smallc(const float* ew, int64_t M
   }
 }
 
+// Transposed convolution onto few values per tap set (C_in kh kw <= 32, the
+// network's input layer) as a GEMM and a fold.  Per image, first
+//   Y[(ci, ky, kx), q] = sum_co K[co, ci, ky, kx] e[co, q]
+// over the source pixels q on the MFMA (M = C_in kh kw in MT tiles of 16
+// rows, K = C_out, N = source pixels), then
+//   out[ci, y, x] = sum of Y[(ci, ky, kx), (qy, qx)] over the taps with
+//   sh qy = y + ph - ky and sw qx = x + pw - kx inside the source image,
+// the tap sum in fp64, rounded once (each Y value is an fp32 MFMA sum over
+// C_out <= 64 products).  Each source value is loaded once, so the conv
+// bias dot (acc += e . bias[co], as k_conv_bias_dot) and, in the fused
+// form, the ReLU relaxation that produces e from the rows x above the
+// ReLU (e = pos(x) lo_s + neg(x) up_s [+ beta], acc += neg(x) up_t, the
+// arithmetic of the relu backward) ride on that load.
+// A workgroup takes one image at a time: source rows in bands of BS whose
+// Y go to an LDS ring of RS >= BS + (kh - 1) / sh rows; after each band the
+// output rows whose taps all lie in the ring are folded and stored.  A
+// wave's 64 source pixels per pass are c0 + 4 r + j (lane column r of
+// N-tile j), so a lane's four consecutive pixels are one 16-byte load.
+constexpr int kFoldNT = 256;
+constexpr int kFoldMaxMF = 32;
+constexpr int kFoldMaxCout = 64;
+constexpr int kFoldMaxLds = 64 * 1024;
+
+struct FoldArgs {
+  const float* ew;  // R rows (shared) or M rows of C_out Ho Wo
+  int64_t M, R, B;  // rows out, rows per domain, domains (M / R)
+  int shared;
+  const float *ls, *us, *ut, *beta;  // (B, C_out Ho Wo) slopes and beta, or null
+  const float* K;                    // (C_out, C_in, kh, kw)
+  const float* bias;                 // (C_out) or null
+  float* out;                        // (M, C_in H W)
+  float* acc;                        // (M)
+  int C_out, Ho, Wo, C_in, H, W, kh, kw, sh, sw, ph, pw;
+  int MF, nks, BS, RS;
+  int hl, hr;  // zero columns left and right of each Y ring row
+  int DB, SB;  // image tile (shared rows): domains x rows
+  FastDiv f_W, f_Wo, f_RS, f_sh, f_sw;
+};
+
+__device__ __forceinline__ float pos_of(float a) { return a < 0.f ? 0.f : a; }
+__device__ __forceinline__ float neg_of(float a) { return a > 0.f ? 0.f : a; }
+
+// One K-step's operands of a lane: its quad of source values (channel
+// co = 4 ks + gq, pixels pq .. pq + 3) and, fused, their slopes and beta.
+// The bases are uniform over the workgroup, the offsets 32-bit.
+struct FoldLd {
+  float x[4], l[4], u[4], t[4], b[4];
+};
+
+struct FoldSrc {
+  const float *x, *l, *u, *t, *b;  // the image's row and its domain's slopes (b may be null)
+};
+
+template <bool RELU, bool VEC>
+__device__ __forceinline__ void fold_load(const FoldSrc& sp, int C_out, int HoWo, int pq,
+                                          int p_hi, int ks, int gq, FoldLd& d) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) d.x[j] = d.l[j] = d.u[j] = d.t[j] = d.b[j] = 0.f;
+  const int co = 4 * ks + gq;
+  if (co >= C_out) return;
+  const uint32_t off = (uint32_t)(co * HoWo + pq);
+  if (VEC) {
+    if (pq >= p_hi) return;  // p_hi and pq are multiples of 4: the whole quad
+    const float4 v = *reinterpret_cast<const float4*>(sp.x + off);
+    d.x[0] = v.x, d.x[1] = v.y, d.x[2] = v.z, d.x[3] = v.w;
+    if (RELU) {
+      const float4 lv = *reinterpret_cast<const float4*>(sp.l + off);
+      const float4 uv = *reinterpret_cast<const float4*>(sp.u + off);
+      const float4 tv = *reinterpret_cast<const float4*>(sp.t + off);
+      d.l[0] = lv.x, d.l[1] = lv.y, d.l[2] = lv.z, d.l[3] = lv.w;
+      d.u[0] = uv.x, d.u[1] = uv.y, d.u[2] = uv.z, d.u[3] = uv.w;
+      d.t[0] = tv.x, d.t[1] = tv.y, d.t[2] = tv.z, d.t[3] = tv.w;
+      if (sp.b) {
+        const float4 bv = *reinterpret_cast<const float4*>(sp.b + off);
+        d.b[0] = bv.x, d.b[1] = bv.y, d.b[2] = bv.z, d.b[3] = bv.w;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (pq + j < p_hi) {
+        d.x[j] = sp.x[off + j];
+        if (RELU) {
+          d.l[j] = sp.l[off + j];
+          d.u[j] = sp.u[off + j];
+          d.t[j] = sp.t[off + j];
+          if (sp.b) d.b[j] = sp.b[off + j];
+        }
+      }
+  }
+}
+
+// The K-step: relax (fused form), the bias dot, MT x 4 MFMAs.  Elements
+// outside the image or channel range hold zeros and add nothing.
+template <int MT, bool RELU>
+__device__ __forceinline__ void fold_use(const float* As, const float* Bsh, bool has_beta,
+                                         bool has_bias, int lane, int ks, int gq, FoldLd& d,
+                                         v4f (*yt)[4], double& p_relu, double& p_bias) {
+  if (RELU) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float ep = pos_of(d.x[j]), en = neg_of(d.x[j]);
+      float e = ep * d.l[j] + en * d.u[j];
+      if (has_beta) e = e + d.b[j];
+      p_relu += (double)(en * d.t[j]);
+      d.x[j] = e;
+    }
+  }
+  if (has_bias) {
+    const float bc = Bsh[4 * ks + gq];  // zero past C_out
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p_bias += (double)(d.x[j] * bc);
+  }
+  float af[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) af[mt] = As[(ks * MT + mt) * 64 + lane];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) yt[mt][j] = mfma16x16x4(af[mt], d.x[j], yt[mt][j]);
+}
+
+// The Y ring: for each m, RS rows of Wp = hl + Wo + hr columns (source
+// column qx at hl + qx, hl = Tx - 1 zero columns on the left, hr on the
+// right: every column a fold reads exists) and one zero row (slot RS), the
+// target of every tap outside the kernel or the source rows.  Zeroed once;
+// Y stores write only the interior.
+template <int MT, bool RELU, bool VEC>
+__global__ __launch_bounds__(kFoldNT) void k_conv_t_fold(FoldArgs a) {
+  extern __shared__ __align__(16) float lds[];
+  __shared__ double red[2][kFoldNT / 64];
+  float* As = lds;                    // [nks][MT][64]: lane l's A value of K-step ks, tile mt
+  float* Bsh = As + a.nks * MT * 64;  // [4 nks]: the bias, zero past C_out
+  float* Yr = Bsh + a.nks * 4;        // [MF][RS + 1][Wp]
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int gq = lane >> 4, r = lane & 15;
+  const int HoWo = a.Ho * a.Wo;
+  const int64_t n_e = (int64_t)a.C_out * HoWo;
+  const int64_t n_o = (int64_t)a.C_in * a.H * a.W;
+  const int Wp = a.hl + a.Wo + a.hr;
+  const int ringsz = (a.RS + 1) * Wp;
+  const int kk = a.kh * a.kw;
+  const int Ty = (a.kh + a.sh - 1) / a.sh, Tx = (a.kw + a.sw - 1) / a.sw;
+  // A[m][co] = K[co][ci][ky][kx] with m = (ci kh + ky) kw + kx, i.e. K[co MF + m]
+  for (int i = tid; i < a.nks * MT * 64; i += kFoldNT) {
+    const int l = i & 63, mt = (i >> 6) % MT, ks = (i >> 6) / MT;
+    const int co = 4 * ks + (l >> 4), m = 16 * mt + (l & 15);
+    As[i] = (co < a.C_out && m < a.MF) ? a.K[(int64_t)co * a.MF + m] : 0.f;
+  }
+  for (int i = tid; i < a.nks * 4; i += kFoldNT) Bsh[i] = (a.bias && i < a.C_out) ? a.bias[i] : 0.f;
+  for (int i = tid; i < a.MF * ringsz; i += kFoldNT) Yr[i] = 0.f;
+  __syncthreads();
+  // Shared source rows: the images run in tiles of DB domains x SB rows,
+  // about the images in flight on one XCD, so that its L2 serves both the
+  // DB domains' slopes and the SB rows to the whole tile (ragged tiles skip
+  // their missing images).  Per-domain rows run in row order.
+  const int64_t tile = a.shared ? (int64_t)a.DB * a.SB : 1;
+  const int64_t ndb = a.shared ? (a.B + a.DB - 1) / a.DB : 1;
+  const int64_t total = a.shared ? ndb * ((a.R + a.SB - 1) / a.SB) * tile : a.M;
+  for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
+    const int64_t w = xcd_tile(t, total);
+    int64_t m, src;
+    if (a.shared) {
+      const int64_t tl = w / tile, in = w - tl * tile;
+      const int64_t sb = tl / ndb;
+      const int64_t b = (tl - sb * ndb) * a.DB + in % a.DB, s = sb * a.SB + in / a.DB;
+      if (b >= a.B || s >= a.R) continue;
+      m = b * a.R + s;
+      src = s;
+    } else {
+      m = w;
+      src = w;
+    }
+    FoldSrc sp;
+    sp.x = a.ew + src * n_e;
+    if (RELU) {
+      const int64_t so = (m / a.R) * n_e;
+      sp.l = a.ls + so;
+      sp.u = a.us + so;
+      sp.t = a.ut + so;
+      sp.b = a.beta ? a.beta + so : nullptr;
+    } else {
+      sp.l = sp.u = sp.t = sp.b = nullptr;
+    }
+    float* orow = a.out + m * n_o;
+    double p_relu = 0.0, p_bias = 0.0;
+    int yo = 0;
+    for (int q0 = 0; q0 < a.Ho; q0 += a.BS) {
+      const int qe = min(a.Ho, q0 + a.BS);
+      const int p_hi = qe * a.Wo;
+      for (int c0 = q0 * a.Wo + 64 * wv; c0 < p_hi; c0 += kFoldNT) {
+        const int pq = c0 + 4 * r;
+        v4f yt[MT][4];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) yt[mt][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int ks = 0; ks < a.nks; ++ks) {
+          FoldLd d;
+          fold_load<RELU, VEC>(sp, a.C_out, HoWo, pq, p_hi, ks, gq, d);
+          fold_use<MT, RELU>(As, Bsh, sp.b != nullptr, a.bias != nullptr, lane, ks, gq, d, yt,
+                             p_relu, p_bias);
+        }
+        // lane (gq, r) holds Y[16 mt + 4 gq + e][pq + j] in yt[mt][j][e]
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int p = pq + j;
+          if (p < p_hi) {
+            const int qy = (int)a.f_Wo.div((uint32_t)p), qx = p - qy * a.Wo;
+            const int slot = qy - (int)a.f_RS.div((uint32_t)qy) * a.RS;
+            float* yp = Yr + slot * Wp + a.hl + qx;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int mm = 16 * mt + 4 * gq + e;
+                if (mm < a.MF) yp[mm * ringsz] = yt[mt][j][e];
+              }
+          }
+        }
+      }
+      __syncthreads();
+      // output rows y < sh qe - ph take taps from source rows < qe only
+      int ye = qe == a.Ho ? a.H : min(a.H, a.sh * qe - a.ph);
+      if (ye < yo) ye = yo;
+      const int cnt = (ye - yo) * a.W;
+      for (int i = tid; i < cnt; i += kFoldNT) {
+        const int dy = (int)a.f_W.div((uint32_t)i), x = i - dy * a.W, y = yo + dy;
+        const int ty0 = y + a.ph, tx0 = x + a.pw;
+        const int qy0 = (int)a.f_sh.div((uint32_t)ty0), ky0 = ty0 - qy0 * a.sh;
+        const int qx0 = (int)a.f_sw.div((uint32_t)tx0), kx0 = tx0 - qx0 * a.sw;
+        double sum[kSmallC];
+#pragma unroll
+        for (int c = 0; c < kSmallC; ++c) sum[c] = 0.0;
+        for (int ty = 0; ty < Ty; ++ty) {
+          const int ky = ky0 + a.sh * ty, qy = qy0 - ty;
+          const bool vy = ky < a.kh && qy >= 0 && qy < a.Ho;
+          const int row = vy ? (qy - (int)a.f_RS.div((uint32_t)qy) * a.RS) : a.RS;
+          const int kyc = vy ? ky : 0;
+          for (int tx = 0; tx < Tx; ++tx) {
+            const int kx = kx0 + a.sw * tx;
+            const bool v = vy && kx < a.kw;
+            const int off = (kyc * a.kw + (v ? kx : 0)) * ringsz + (v ? row : a.RS) * Wp + a.hl +
+                            qx0 - tx;
+#pragma unroll
+            for (int c = 0; c < kSmallC; ++c)
+              if (c < a.C_in) sum[c] += (double)Yr[c * kk * ringsz + off];
+          }
+        }
+        float* op = orow + (int64_t)y * a.W + x;
+#pragma unroll
+        for (int c = 0; c < kSmallC; ++c)
+          if (c < a.C_in) op[(int64_t)c * a.H * a.W] = (float)sum[c];
+      }
+      yo = ye;
+      __syncthreads();
+    }
+    if (RELU || a.bias) {
+      // the relu's intercepts, then the bias dot, each rounded into acc as
+      // the two separate steps round them
+      p_relu = wave_sum_f64(p_relu);
+      p_bias = wave_sum_f64(p_bias);
+      if (lane == 0) {
+        red[0][wv] = p_relu;
+        red[1][wv] = p_bias;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        float v = a.acc[m];
+        if (RELU) v = (float)((double)v + ((red[0][0] + red[0][1]) + (red[0][2] + red[0][3])));
+        if (a.bias) v = (float)((double)v + ((red[1][0] + red[1][1]) + (red[1][2] + red[1][3])));
+        a.acc[m] = v;
+      }
+    }
+  }
+}
+
 // acc[m] += sum_{co, p} ew[m, co, p] * bias[co].  One workgroup per row
 // (rows of a conv layer are tens of thousands of values long); products in
 // fp32 as the reference's (ew * bias_flat) forms them, summed in fp64,
@@ -514,6 +792,88 @@ extern "C" int vc_zono_conv(const float* c, const float* G, int64_t B, int Kg, i
 
 namespace {
 
+// Band and ring sizes of k_conv_t_fold for a geometry, or false when the
+// geometry is outside its limits.  Bands of about 256 source pixels (one
+// pass of the four waves), halved until the LDS fits.
+struct FoldPlan {
+  int MT, nks, BS, RS, hl, hr;
+  size_t lds;
+};
+
+bool fold_plan(int C_out, int Ho, int Wo, int C_in, int W, int kh, int kw, int sh, int sw,
+               int pw, FoldPlan& f) {
+  const int64_t MF = (int64_t)C_in * kh * kw;
+  if (MF > kFoldMaxMF || C_out > kFoldMaxCout || C_in > kSmallC) return false;
+  f.MT = MF > 16 ? 2 : 1;
+  f.nks = (C_out + 3) / 4;
+  f.hl = (kw + sw - 1) / sw - 1;
+  f.hr = (W - 1 + pw) / sw - (Wo - 1);
+  if (f.hr < 0) f.hr = 0;
+  f.BS = Wo >= 256 ? 1 : 256 / Wo;
+  if (f.BS > Ho) f.BS = Ho;
+  for (;;) {
+    f.RS = f.BS + (kh - 1) / sh;
+    f.lds = ((size_t)f.nks * (f.MT * 64 + 4) +
+             (size_t)MF * (f.RS + 1) * (f.hl + Wo + f.hr)) * sizeof(float);
+    if (f.lds <= (size_t)kFoldMaxLds) return true;
+    if (f.BS == 1) return false;
+    f.BS /= 2;
+  }
+}
+
+template <int MT, bool RELU>
+void launch_fold_vec(const FoldArgs& a, bool vec, dim3 grid, size_t lds, hipStream_t st) {
+  if (vec)
+    hipLaunchKernelGGL((k_conv_t_fold<MT, RELU, true>), grid, dim3(kFoldNT), lds, st, a);
+  else
+    hipLaunchKernelGGL((k_conv_t_fold<MT, RELU, false>), grid, dim3(kFoldNT), lds, st, a);
+}
+
+// One image per workgroup at a time, as many workgroups as fit the CUs
+// (a multiple of 8, so each keeps its XCD across images).
+int launch_fold(FoldArgs a, const FoldPlan& f, hipStream_t st) {
+  a.MF = a.C_in * a.kh * a.kw;
+  a.nks = f.nks;
+  a.BS = f.BS;
+  a.RS = f.RS;
+  a.hl = f.hl;
+  a.hr = f.hr;
+  a.f_W = FastDiv::make((uint32_t)a.W);
+  a.f_Wo = FastDiv::make((uint32_t)a.Wo);
+  a.f_RS = FastDiv::make((uint32_t)a.RS);
+  a.f_sh = FastDiv::make((uint32_t)a.sh);
+  a.f_sw = FastDiv::make((uint32_t)a.sw);
+  const bool relu = a.ls != nullptr;
+  bool vec = a.Wo % 4 == 0 && aligned16(a.ew);
+  if (relu) vec = vec && aligned16(a.ls) && aligned16(a.us) && aligned16(a.ut) &&
+                  (!a.beta || aligned16(a.beta));
+  int per_cu = (int)((160 * 1024) / (f.lds + 2 * (kFoldNT / 64) * sizeof(double)));
+  if (per_cu > 8) per_cu = 8;
+  if (per_cu < 1) per_cu = 1;
+  int64_t grid = (int64_t)vcm::cu_count() * per_cu;
+  grid -= grid % 8;
+  // a tile is about one XCD's images in flight
+  const int64_t flight = grid / 8 > 1 ? grid / 8 : 1;
+  a.DB = (int)(a.B < 8 ? a.B : 8);
+  a.SB = (int)((flight + a.DB - 1) / a.DB);
+  if (a.SB > a.R) a.SB = (int)a.R;
+  if (grid > a.M) grid = a.M;
+  const dim3 g((unsigned)grid);
+  if (f.MT == 1) {
+    if (relu)
+      launch_fold_vec<1, true>(a, vec, g, f.lds, st);
+    else
+      launch_fold_vec<1, false>(a, vec, g, f.lds, st);
+  } else {
+    if (relu)
+      launch_fold_vec<2, true>(a, vec, g, f.lds, st);
+    else
+      launch_fold_vec<2, false>(a, vec, g, f.lds, st);
+  }
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
 // Row length of the packed transposed taps: C_out Ty Tx rounded up to 4.
 int conv_t_ld(int C_out, int kh, int kw, int sh, int sw) {
   const int Ty = (kh + sh - 1) / sh, Tx = (kw + sw - 1) / sw;
@@ -533,6 +893,22 @@ int backward_conv(const float* ew_in, int64_t M, const float* kernel, const floa
   const int Ty = (kh + sh - 1) / sh, Tx = (kw + sw - 1) / sw;
   const int64_t npix = (int64_t)Hc * Wc, N = M * npix, Kd = (int64_t)C_out * Ty * Tx;
   if (N > kMaxDim || Kd > kMaxDim) return VC_ERR_UNSUPPORTED;
+  FoldPlan fp;
+  if (fold_plan(C_out, H_out, W_out, C_in, W, kh, kw, sh, sw, pw, fp)) {
+    FoldArgs a{};
+    a.ew = ew_in;
+    a.M = M;
+    a.R = 1;
+    a.B = M;
+    a.shared = 0;
+    a.K = kernel;
+    a.bias = bias;
+    a.out = ew_out;
+    a.acc = acc;
+    a.C_out = C_out, a.Ho = H_out, a.Wo = W_out, a.C_in = C_in, a.H = H, a.W = W;
+    a.kh = kh, a.kw = kw, a.sh = sh, a.sw = sw, a.ph = ph, a.pw = pw;
+    return launch_fold(a, fp, st);
+  }
   if (bias) {
     const int sp = H_out * W_out;
     const bool v = ((int64_t)C_out * sp) % 4 == 0 && aligned16(ew_in);
@@ -635,4 +1011,45 @@ extern "C" int vc_backward_conv_packed(const float* ew_in, int64_t M, const floa
   if (!packed) return VC_ERR_ARG;
   return backward_conv(ew_in, M, kernel, packed, bias, C_out, H_out, W_out, C_in, H, W, kh, kw,
                        sh, sw, ph, pw, ew_out, acc, stream);
+}
+
+extern "C" int vc_backward_relu_conv_ok(int C_out, int H_out, int W_out, int C_in, int H, int W,
+                                        int kh, int kw, int sh, int sw, int ph, int pw) {
+  ConvGeom g{C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, H_out, W_out};
+  if (check_geom(g) != VC_OK) return 0;
+  FoldPlan fp;
+  return fold_plan(C_out, H_out, W_out, C_in, W, kh, kw, sh, sw, pw, fp) ? 1 : 0;
+}
+
+extern "C" int vc_backward_relu_conv(const float* ew_in, int64_t M, int64_t R, int ew_shared,
+                                     const float* lo_s, const float* up_s, const float* up_t,
+                                     const float* beta, const float* kernel, const float* bias,
+                                     int C_out, int H_out, int W_out, int C_in, int H, int W,
+                                     int kh, int kw, int sh, int sw, int ph, int pw,
+                                     float* ew_out, float* acc, vc_stream_t stream) {
+  ConvGeom g{C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, H_out, W_out};
+  if (check_geom(g) != VC_OK || !ew_in || !kernel || !ew_out || !acc || !lo_s || !up_s ||
+      !up_t || M < 0 || R <= 0 || M % R)
+    return VC_ERR_ARG;
+  FoldPlan fp;
+  if (!fold_plan(C_out, H_out, W_out, C_in, W, kh, kw, sh, sw, pw, fp)) return VC_ERR_UNSUPPORTED;
+  if ((int64_t)C_out * H_out * W_out > kMaxDim) return VC_ERR_UNSUPPORTED;
+  if (M == 0) return VC_OK;
+  FoldArgs a{};
+  a.ew = ew_in;
+  a.M = M;
+  a.R = R;
+  a.B = M / R;
+  a.shared = ew_shared ? 1 : 0;
+  a.ls = lo_s;
+  a.us = up_s;
+  a.ut = up_t;
+  a.beta = beta;
+  a.K = kernel;
+  a.bias = bias;
+  a.out = ew_out;
+  a.acc = acc;
+  a.C_out = C_out, a.Ho = H_out, a.Wo = W_out, a.C_in = C_in, a.H = H, a.W = W;
+  a.kh = kh, a.kw = kw, a.sh = sh, a.sw = sw, a.ph = ph, a.pw = pw;
+  return launch_fold(a, fp, (hipStream_t)stream);
 }

@@ -52,6 +52,9 @@ SIGNATURES = {
     'vc_backward_conv': [_P, _L, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                          _I, _I, _I, _P, _P, _P],
     'vc_conv_t_pack_floats': [_I, _I, _I, _I, _I, _I],
+    'vc_backward_relu_conv_ok': [_I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I],
+    'vc_backward_relu_conv': [_P, _L, _L, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                              _I, _I, _I, _I, _I, _I, _P, _P, _P],
     'vc_conv_t_pack': [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P],
     'vc_backward_conv_packed': [_P, _L, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                                 _I, _I, _I, _P, _P, _P],

@@ -21,6 +21,9 @@ __all__ = ['_make_slopes', '_ibp_forward_graph_batched',
 # Use the whole-network kernels for narrow fc/ReLU chains (<= 64 wide).
 # Switching this off routes those nets through the layer-wise kernels.
 FUSED_MLP = True
+# Fuse a relu relaxation into the conv backward after it where the conv
+# qualifies (vc_backward_relu_conv); off: the relu is applied on its own.
+FUSED_RELU_CONV = True
 
 
 def _plan(gg, dev):
@@ -542,6 +545,36 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
              ptr(acc), st)
         return _Rows(out, False)
 
+    def relu_conv(rows, op, p):
+        """The pending relu relaxation fused into the conv backward that
+        follows it (vc_backward_relu_conv), or None when the geometry or
+        the relaxation's form is outside the fused kernel."""
+        if rows.alpha_group is not None or (rows.alpha is not None and rows.alpha_row):
+            return None
+        ok = p.get('relu_conv_ok')
+        if ok is None:
+            C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, Ho, Wo = p['geom']
+            ok = bool(_lib.load().vc_backward_relu_conv_ok(C_out, Ho, Wo, C_in, H, W, kh, kw,
+                                                           sh, sw, ph, pw))
+            p['relu_conv_ok'] = ok
+        if not ok:
+            return None
+        L = rows.relu
+        lo, hi = f32(tight[L][0]), f32(tight[L][1])
+        n = lo.shape[1]
+        per_domain_acc()
+        if trace is not None:
+            trace.relus.append((L, rows.ew, rows.shared))
+        ls, us, ut = (torch.empty(B, n, device=dev) for _ in range(3))
+        call('vc_relax_slopes', ptr(lo), ptr(hi), ptr(rows.alpha), B * n, ptr(ls), ptr(us),
+             ptr(ut), st)
+        C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, Ho, Wo = p['geom']
+        out = torch.empty(B * R, p['n_in'], device=dev)
+        call('vc_backward_relu_conv', ptr(rows.ew), B * R, R, 1 if rows.shared else 0, ptr(ls),
+             ptr(us), ptr(ut), ptr(rows.beta), ptr(p['K']), ptr(p['b']), C_out, Ho, Wo, C_in,
+             H, W, kh, kw, sh, sw, ph, pw, ptr(out), ptr(acc), st)
+        return out
+
     for op in reversed(ops):
         name = op['name']
         if name not in ew_at:
@@ -643,8 +676,13 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
                     rows.beta = f32(relu_split_beta[L])
             put(inp, rows)
         elif t == 'conv':
-            rows = materialize(rows)
             p = _op_params(op, dev)
+            if rows.relu is not None and FUSED_RELU_CONV:
+                out = relu_conv(rows, op, p)
+                if out is not None:
+                    put(inp, _Rows(out, False))
+                    continue
+            rows = materialize(rows)
             C_in, H, W, C_out, kh, kw, sh, sw, ph, pw, Ho, Wo = p['geom']
             if not rows.shared:
                 per_domain_acc()
