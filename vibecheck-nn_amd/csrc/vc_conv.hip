@@ -421,7 +421,9 @@ struct FoldArgs {
   int MF, nks, BS, RS;
   int hl, hr;  // zero columns left and right of each Y ring row
   int DB, SB;  // image tile (shared rows): domains x rows
-  FastDiv f_W, f_Wo, f_RS, f_sh, f_sw;
+  int ndb;     // tiles along the domains
+  int64_t total;  // image slots (M, or whole tiles)
+  FastDiv f_W, f_Wo, f_RS, f_sh, f_sw, f_R, f_DB, f_ndb, f_tile;
 };
 
 __device__ __forceinline__ float pos_of(float a) { return a < 0.f ? 0.f : a; }
@@ -440,14 +442,17 @@ struct FoldSrc {
 
 template <bool RELU, bool VEC>
 __device__ __forceinline__ void fold_load(const FoldSrc& sp, int C_out, int HoWo, int pq,
-                                          int p_hi, int ks, int gq, FoldLd& d) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) d.x[j] = d.l[j] = d.u[j] = d.t[j] = d.b[j] = 0.f;
+                                          int p_hi, int ks, int gq, bool full, FoldLd& d) {
   const int co = 4 * ks + gq;
-  if (co >= C_out) return;
   const uint32_t off = (uint32_t)(co * HoWo + pq);
+  // full: every lane of the wave in range (uniform), no zero fills
+  if (!full) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d.x[j] = d.l[j] = d.u[j] = d.t[j] = d.b[j] = 0.f;
+    if (co >= C_out) return;
+  }
   if (VEC) {
-    if (pq >= p_hi) return;  // p_hi and pq are multiples of 4: the whole quad
+    if (!full && pq >= p_hi) return;  // p_hi and pq are multiples of 4: the whole quad
     const float4 v = *reinterpret_cast<const float4*>(sp.x + off);
     d.x[0] = v.x, d.x[1] = v.y, d.x[2] = v.z, d.x[3] = v.w;
     if (RELU) {
@@ -460,6 +465,9 @@ __device__ __forceinline__ void fold_load(const FoldSrc& sp, int C_out, int HoWo
       if (sp.b) {
         const float4 bv = *reinterpret_cast<const float4*>(sp.b + off);
         d.b[0] = bv.x, d.b[1] = bv.y, d.b[2] = bv.z, d.b[3] = bv.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) d.b[j] = 0.f;
       }
     }
   } else {
@@ -486,10 +494,12 @@ __device__ __forceinline__ void fold_use(const float* As, const float* Bsh, bool
   if (RELU) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float ep = pos_of(d.x[j]), en = neg_of(d.x[j]);
-      float e = ep * d.l[j] + en * d.u[j];
+      // pos(x) lo_s + neg(x) up_s with one of the two parts zero: the
+      // nonzero product itself (the same value; a zero may differ in sign)
+      const float x = d.x[j];
+      float e = x * (x < 0.f ? d.u[j] : d.l[j]);
       if (has_beta) e = e + d.b[j];
-      p_relu += (double)(en * d.t[j]);
+      p_relu += (double)(neg_of(x) * d.t[j]);
       d.x[j] = e;
     }
   }
@@ -541,18 +551,16 @@ __global__ __launch_bounds__(kFoldNT) void k_conv_t_fold(FoldArgs a) {
   // about the images in flight on one XCD, so that its L2 serves both the
   // DB domains' slopes and the SB rows to the whole tile (ragged tiles skip
   // their missing images).  Per-domain rows run in row order.
-  const int64_t tile = a.shared ? (int64_t)a.DB * a.SB : 1;
-  const int64_t ndb = a.shared ? (a.B + a.DB - 1) / a.DB : 1;
-  const int64_t total = a.shared ? ndb * ((a.R + a.SB - 1) / a.SB) * tile : a.M;
-  for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
-    const int64_t w = xcd_tile(t, total);
+  // (image counts below 2^31: 32-bit index arithmetic)
+  for (int64_t t = blockIdx.x; t < a.total; t += gridDim.x) {
+    const uint32_t w = (uint32_t)xcd_tile(t, a.total);
     int64_t m, src;
     if (a.shared) {
-      const int64_t tl = w / tile, in = w - tl * tile;
-      const int64_t sb = tl / ndb;
-      const int64_t b = (tl - sb * ndb) * a.DB + in % a.DB, s = sb * a.SB + in / a.DB;
-      if (b >= a.B || s >= a.R) continue;
-      m = b * a.R + s;
+      const uint32_t tl = a.f_tile.div(w), in = w - tl * a.DB * a.SB;
+      const uint32_t sb = a.f_ndb.div(tl), ib = a.f_DB.div(in);
+      const uint32_t b = (tl - sb * a.ndb) * a.DB + (in - ib * a.DB), s = sb * a.SB + ib;
+      if (b >= (uint32_t)a.B || s >= (uint32_t)a.R) continue;
+      m = (int64_t)b * a.R + s;
       src = s;
     } else {
       m = w;
@@ -561,7 +569,7 @@ __global__ __launch_bounds__(kFoldNT) void k_conv_t_fold(FoldArgs a) {
     FoldSrc sp;
     sp.x = a.ew + src * n_e;
     if (RELU) {
-      const int64_t so = (m / a.R) * n_e;
+      const int64_t so = (int64_t)a.f_R.div((uint32_t)m) * n_e;
       sp.l = a.ls + so;
       sp.u = a.us + so;
       sp.t = a.ut + so;
@@ -582,18 +590,22 @@ __global__ __launch_bounds__(kFoldNT) void k_conv_t_fold(FoldArgs a) {
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int j = 0; j < 4; ++j) yt[mt][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        const bool full_px = VEC && c0 + 63 < p_hi;
         for (int ks = 0; ks < a.nks; ++ks) {
           FoldLd d;
-          fold_load<RELU, VEC>(sp, a.C_out, HoWo, pq, p_hi, ks, gq, d);
+          fold_load<RELU, VEC>(sp, a.C_out, HoWo, pq, p_hi, ks, gq, full_px && 4 * ks + 3 < a.C_out,
+                               d);
           fold_use<MT, RELU>(As, Bsh, sp.b != nullptr, a.bias != nullptr, lane, ks, gq, d, yt,
                              p_relu, p_bias);
         }
-        // lane (gq, r) holds Y[16 mt + 4 gq + e][pq + j] in yt[mt][j][e]
+        // lane (gq, r) holds Y[16 mt + 4 gq + e][pq + j] in yt[mt][j][e]; with
+        // Wo a multiple of 4 (VEC) the quad lies in one source row
+        const int qyq = (int)a.f_Wo.div((uint32_t)pq);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int p = pq + j;
           if (p < p_hi) {
-            const int qy = (int)a.f_Wo.div((uint32_t)p), qx = p - qy * a.Wo;
+            const int qy = VEC ? qyq : (int)a.f_Wo.div((uint32_t)p), qx = p - qy * a.Wo;
             const int slot = qy - (int)a.f_RS.div((uint32_t)qy) * a.RS;
             float* yp = Yr + slot * Wp + a.hl + qx;
 #pragma unroll
@@ -857,6 +869,13 @@ int launch_fold(FoldArgs a, const FoldPlan& f, hipStream_t st) {
   a.DB = (int)(a.B < 8 ? a.B : 8);
   a.SB = (int)((flight + a.DB - 1) / a.DB);
   if (a.SB > a.R) a.SB = (int)a.R;
+  a.ndb = (int)((a.B + a.DB - 1) / a.DB);
+  a.total = a.shared ? (int64_t)a.ndb * ((a.R + a.SB - 1) / a.SB) * a.DB * a.SB : a.M;
+  if (a.total >= (int64_t(1) << 31)) return VC_ERR_UNSUPPORTED;
+  a.f_R = FastDiv::make((uint32_t)a.R);
+  a.f_DB = FastDiv::make((uint32_t)a.DB);
+  a.f_ndb = FastDiv::make((uint32_t)a.ndb);
+  a.f_tile = FastDiv::make((uint32_t)(a.DB * a.SB));
   if (grid > a.M) grid = a.M;
   const dim3 g((unsigned)grid);
   if (f.MT == 1) {
