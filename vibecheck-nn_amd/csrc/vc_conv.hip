@@ -43,7 +43,10 @@ __device__ __forceinline__ TapClass tap_class(int parity, int pad, int s) {
 // offsets (oy, ox) are those of the transposed-convolution parity class bz
 // (dsg = -1), else (-ph, -pw) (dsg = +1).  NS = 2 gathers two sources
 // (interval lo, hi) into (mid, rad).
-template <int NS, bool TR>
+// ROWQ: every quad of columns is four consecutive pixels of one row (the
+// host checked the grid width and pixel count are multiples of 4, nk = 1),
+// so only the row path is compiled.
+template <int NS, bool TR, bool ROWQ = false>
 struct LoadGather {
   static constexpr bool kTrans = false;
   const float *src, *src2;
@@ -108,7 +111,7 @@ struct LoadGather {
     const int ty = (int)f_Tx.div((uint32_t)t);
     const int tx = t - ty * Tx;
     const int dy = TR ? -ty : ty, dx = TR ? -tx : tx;
-    const int mode = cl.mode & 3;
+    const int mode = ROWQ ? 0 : (cl.mode & 3);
     if (mode == 2) {
       int oy, ox;
       origin(cl.mode >> 2, oy, ox);
@@ -127,6 +130,23 @@ struct LoadGather {
     const int y = cl.yb + dy;
     const float* b1 = src + cl.off + c * s_c;
     const float* b2 = NS == 2 ? src2 + cl.off + c * s_c : nullptr;
+    if (TR && NS == 1 && mode == 0 && cnt == 4) {
+      // the transposed conv's rows are contiguous (unit pixel steps): a
+      // quad inside the image is four consecutive floats, one 16-byte load
+      // when aligned, else four loads without bounds checks
+      const int x0 = cl.xb + dx;
+      if ((unsigned)y < (unsigned)Hs && x0 >= 0 && x0 + 3 < Ws) {
+        const float* p = b1 + y * s_y + x0;
+        if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+          const float4 v = *reinterpret_cast<const float4*>(p);
+          r.x[0][0] = v.x, r.x[0][1] = v.y, r.x[0][2] = v.z, r.x[0][3] = v.w;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) r.x[0][j] = p[j];
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (j < cnt) {
@@ -953,43 +973,48 @@ int backward_conv(const float* ew_in, int64_t M, const float* kernel, const floa
     VC_LAUNCH_CHECK();
     return VC_OK;
   }
-  LoadGather<1, true> gb{};
-  gb.src = ew_in;
-  gb.src2 = nullptr;
-  gb.s_img = (int64_t)C_out * H_out * W_out;
-  gb.s_c = (int64_t)H_out * W_out;
-  gb.s_y = W_out;
-  gb.s_x = 1;
-  gb.Hs = H_out;
-  gb.Ws = W_out;
-  gb.nk = 1;
-  gb.T = Ty * Tx;
-  gb.Tx = Tx;
-  gb.psy = 1;
-  gb.psx = 1;
-  gb.ph = ph;
-  gb.pw = pw;
-  gb.sh = sh;
-  gb.sw = sw;
-  gb.Wg = Wc;
-  gb.per_img = npix;
-  gb.f_img = FastDiv::make((uint32_t)npix);
-  gb.f_nk = FastDiv::make(1);
-  gb.f_wg = FastDiv::make((uint32_t)Wc);
-  gb.f_T = FastDiv::make((uint32_t)gb.T);
-  gb.f_Tx = FastDiv::make((uint32_t)Tx);
-  EpConvT ep{ew_out, H, W, Wc, sh, sw, npix, (int64_t)C_in * H * W,
-             FastDiv::make((uint32_t)npix), FastDiv::make((uint32_t)Wc)};
-  if (packed && aligned16(packed)) {
-    const int ld = conv_t_ld(C_out, kh, kw, sh, sw);
-    LoadPackedT la{packed, (int64_t)C_in * ld, ld};
+  auto run = [&](auto gb) {
+    gb.src = ew_in;
+    gb.src2 = nullptr;
+    gb.s_img = (int64_t)C_out * H_out * W_out;
+    gb.s_c = (int64_t)H_out * W_out;
+    gb.s_y = W_out;
+    gb.s_x = 1;
+    gb.Hs = H_out;
+    gb.Ws = W_out;
+    gb.nk = 1;
+    gb.T = Ty * Tx;
+    gb.Tx = Tx;
+    gb.psy = 1;
+    gb.psx = 1;
+    gb.ph = ph;
+    gb.pw = pw;
+    gb.sh = sh;
+    gb.sw = sw;
+    gb.Wg = Wc;
+    gb.per_img = npix;
+    gb.f_img = FastDiv::make((uint32_t)npix);
+    gb.f_nk = FastDiv::make(1);
+    gb.f_wg = FastDiv::make((uint32_t)Wc);
+    gb.f_T = FastDiv::make((uint32_t)gb.T);
+    gb.f_Tx = FastDiv::make((uint32_t)Tx);
+    EpConvT ep{ew_out, H, W, Wc, sh, sw, npix, (int64_t)C_in * H * W,
+               FastDiv::make((uint32_t)npix), FastDiv::make((uint32_t)Wc)};
+    if (packed && aligned16(packed)) {
+      const int ld = conv_t_ld(C_out, kh, kw, sh, sw);
+      LoadPackedT la{packed, (int64_t)C_in * ld, ld};
+      return launch_gemm<1, false>((int64_t)sh * sw, C_in, (int)N, (int)Kd, la, gb, ep, nullptr,
+                                   false, st);
+    }
+    LoadKernelT la{kernel, C_in, kh, kw, sh, sw, ph, pw, Ty * Tx, Tx, Ty,
+                   FastDiv::make((uint32_t)(Ty * Tx)), FastDiv::make((uint32_t)Tx)};
     return launch_gemm<1, false>((int64_t)sh * sw, C_in, (int)N, (int)Kd, la, gb, ep, nullptr,
                                  false, st);
-  }
-  LoadKernelT la{kernel, C_in, kh, kw, sh, sw, ph, pw, Ty * Tx, Tx, Ty,
-                 FastDiv::make((uint32_t)(Ty * Tx)), FastDiv::make((uint32_t)Tx)};
-  return launch_gemm<1, false>((int64_t)sh * sw, C_in, (int)N, (int)Kd, la, gb, ep, nullptr, false,
-                               st);
+  };
+  // quads of 4 columns start at multiples of 4; with the class grid's width
+  // and pixel count multiples of 4 each lies in one source row
+  if (Wc % 4 == 0 && npix % 4 == 0) return run(LoadGather<1, true, true>{});
+  return run(LoadGather<1, true, false>{});
 }
 
 }  // namespace
