@@ -460,65 +460,64 @@ struct FoldSrc {
   const float *x, *l, *u, *t, *b;  // the image's row and its domain's slopes (b may be null)
 };
 
-template <bool RELU, bool VEC>
+// FULL: every lane of the wave in range (a uniform fact of the chunk and the
+// channel count): no masks, no zero fills.  RL: 0 plain, 1 relu, 2 relu +
+// beta.
+template <int RL, bool VEC, bool FULL>
 __device__ __forceinline__ void fold_load(const FoldSrc& sp, int C_out, int HoWo, int pq,
-                                          int p_hi, int ks, int gq, bool full, FoldLd& d) {
+                                          int p_hi, int ks, int gq, FoldLd& d) {
   const int co = 4 * ks + gq;
   const uint32_t off = (uint32_t)(co * HoWo + pq);
-  // full: every lane of the wave in range (uniform), no zero fills
-  if (!full) {
+  if (!FULL) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) d.x[j] = d.l[j] = d.u[j] = d.t[j] = d.b[j] = 0.f;
     if (co >= C_out) return;
   }
   if (VEC) {
-    if (!full && pq >= p_hi) return;  // p_hi and pq are multiples of 4: the whole quad
+    if (!FULL && pq >= p_hi) return;  // p_hi and pq are multiples of 4: the whole quad
     const float4 v = *reinterpret_cast<const float4*>(sp.x + off);
     d.x[0] = v.x, d.x[1] = v.y, d.x[2] = v.z, d.x[3] = v.w;
-    if (RELU) {
+    if (RL > 0) {
       const float4 lv = *reinterpret_cast<const float4*>(sp.l + off);
       const float4 uv = *reinterpret_cast<const float4*>(sp.u + off);
       const float4 tv = *reinterpret_cast<const float4*>(sp.t + off);
       d.l[0] = lv.x, d.l[1] = lv.y, d.l[2] = lv.z, d.l[3] = lv.w;
       d.u[0] = uv.x, d.u[1] = uv.y, d.u[2] = uv.z, d.u[3] = uv.w;
       d.t[0] = tv.x, d.t[1] = tv.y, d.t[2] = tv.z, d.t[3] = tv.w;
-      if (sp.b) {
-        const float4 bv = *reinterpret_cast<const float4*>(sp.b + off);
-        d.b[0] = bv.x, d.b[1] = bv.y, d.b[2] = bv.z, d.b[3] = bv.w;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) d.b[j] = 0.f;
-      }
+    }
+    if (RL == 2) {
+      const float4 bv = *reinterpret_cast<const float4*>(sp.b + off);
+      d.b[0] = bv.x, d.b[1] = bv.y, d.b[2] = bv.z, d.b[3] = bv.w;
     }
   } else {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (pq + j < p_hi) {
         d.x[j] = sp.x[off + j];
-        if (RELU) {
+        if (RL > 0) {
           d.l[j] = sp.l[off + j];
           d.u[j] = sp.u[off + j];
           d.t[j] = sp.t[off + j];
-          if (sp.b) d.b[j] = sp.b[off + j];
         }
+        if (RL == 2) d.b[j] = sp.b[off + j];
       }
   }
 }
 
 // The K-step: relax (fused form), the bias dot, MT x 4 MFMAs.  Elements
 // outside the image or channel range hold zeros and add nothing.
-template <int MT, bool RELU>
-__device__ __forceinline__ void fold_use(const float* As, const float* Bsh, bool has_beta,
-                                         bool has_bias, int lane, int ks, int gq, FoldLd& d,
-                                         v4f (*yt)[4], double& p_relu, double& p_bias) {
-  if (RELU) {
+template <int MT, int RL>
+__device__ __forceinline__ void fold_use(const float* As, const float* Bsh, bool has_bias,
+                                         int lane, int ks, int gq, FoldLd& d, v4f (*yt)[4],
+                                         double& p_relu, double& p_bias) {
+  if (RL > 0) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       // pos(x) lo_s + neg(x) up_s with one of the two parts zero: the
       // nonzero product itself (the same value; a zero may differ in sign)
       const float x = d.x[j];
       float e = x * (x < 0.f ? d.u[j] : d.l[j]);
-      if (has_beta) e = e + d.b[j];
+      if (RL == 2) e = e + d.b[j];
       p_relu += (double)(neg_of(x) * d.t[j]);
       d.x[j] = e;
     }
@@ -542,8 +541,9 @@ __device__ __forceinline__ void fold_use(const float* As, const float* Bsh, bool
 // right: every column a fold reads exists) and one zero row (slot RS), the
 // target of every tap outside the kernel or the source rows.  Zeroed once;
 // Y stores write only the interior.
-template <int MT, bool RELU, bool VEC>
+template <int MT, int RL, bool VEC>
 __global__ __launch_bounds__(kFoldNT) void k_conv_t_fold(FoldArgs a) {
+  constexpr bool RELU = RL > 0;
   extern __shared__ __align__(16) float lds[];
   __shared__ double red[2][kFoldNT / 64];
   float* As = lds;                    // [nks][MT][64]: lane l's A value of K-step ks, tile mt
@@ -610,13 +610,18 @@ __global__ __launch_bounds__(kFoldNT) void k_conv_t_fold(FoldArgs a) {
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int j = 0; j < 4; ++j) yt[mt][j] = v4f{0.f, 0.f, 0.f, 0.f};
-        const bool full_px = VEC && c0 + 63 < p_hi;
-        for (int ks = 0; ks < a.nks; ++ks) {
-          FoldLd d;
-          fold_load<RELU, VEC>(sp, a.C_out, HoWo, pq, p_hi, ks, gq, full_px && 4 * ks + 3 < a.C_out,
-                               d);
-          fold_use<MT, RELU>(As, Bsh, sp.b != nullptr, a.bias != nullptr, lane, ks, gq, d, yt,
-                             p_relu, p_bias);
+        if (VEC && c0 + 63 < p_hi && (a.C_out & 3) == 0) {
+          for (int ks = 0; ks < a.nks; ++ks) {
+            FoldLd d;
+            fold_load<RL, VEC, true>(sp, a.C_out, HoWo, pq, p_hi, ks, gq, d);
+            fold_use<MT, RL>(As, Bsh, a.bias != nullptr, lane, ks, gq, d, yt, p_relu, p_bias);
+          }
+        } else {
+          for (int ks = 0; ks < a.nks; ++ks) {
+            FoldLd d;
+            fold_load<RL, VEC, false>(sp, a.C_out, HoWo, pq, p_hi, ks, gq, d);
+            fold_use<MT, RL>(As, Bsh, a.bias != nullptr, lane, ks, gq, d, yt, p_relu, p_bias);
+          }
         }
         // lane (gq, r) holds Y[16 mt + 4 gq + e][pq + j] in yt[mt][j][e]; with
         // Wo a multiple of 4 (VEC) the quad lies in one source row
@@ -853,12 +858,22 @@ bool fold_plan(int C_out, int Ho, int Wo, int C_in, int W, int kh, int kw, int s
   }
 }
 
-template <int MT, bool RELU>
+template <int MT, int RL>
 void launch_fold_vec(const FoldArgs& a, bool vec, dim3 grid, size_t lds, hipStream_t st) {
   if (vec)
-    hipLaunchKernelGGL((k_conv_t_fold<MT, RELU, true>), grid, dim3(kFoldNT), lds, st, a);
+    hipLaunchKernelGGL((k_conv_t_fold<MT, RL, true>), grid, dim3(kFoldNT), lds, st, a);
   else
-    hipLaunchKernelGGL((k_conv_t_fold<MT, RELU, false>), grid, dim3(kFoldNT), lds, st, a);
+    hipLaunchKernelGGL((k_conv_t_fold<MT, RL, false>), grid, dim3(kFoldNT), lds, st, a);
+}
+
+template <int MT>
+void launch_fold_rl(const FoldArgs& a, bool vec, dim3 grid, size_t lds, hipStream_t st) {
+  if (!a.ls)
+    launch_fold_vec<MT, 0>(a, vec, grid, lds, st);
+  else if (!a.beta)
+    launch_fold_vec<MT, 1>(a, vec, grid, lds, st);
+  else
+    launch_fold_vec<MT, 2>(a, vec, grid, lds, st);
 }
 
 // One image per workgroup at a time, as many workgroups as fit the CUs
@@ -898,17 +913,10 @@ int launch_fold(FoldArgs a, const FoldPlan& f, hipStream_t st) {
   a.f_tile = FastDiv::make((uint32_t)(a.DB * a.SB));
   if (grid > a.M) grid = a.M;
   const dim3 g((unsigned)grid);
-  if (f.MT == 1) {
-    if (relu)
-      launch_fold_vec<1, true>(a, vec, g, f.lds, st);
-    else
-      launch_fold_vec<1, false>(a, vec, g, f.lds, st);
-  } else {
-    if (relu)
-      launch_fold_vec<2, true>(a, vec, g, f.lds, st);
-    else
-      launch_fold_vec<2, false>(a, vec, g, f.lds, st);
-  }
+  if (f.MT == 1)
+    launch_fold_rl<1>(a, vec, g, f.lds, st);
+  else
+    launch_fold_rl<2>(a, vec, g, f.lds, st);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }
