@@ -611,10 +611,15 @@ __global__ __launch_bounds__(kFoldNT) void k_conv_t_fold(FoldArgs a) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) yt[mt][j] = v4f{0.f, 0.f, 0.f, 0.f};
         if (VEC && c0 + 63 < p_hi && (a.C_out & 3) == 0) {
+          // the next K-step's loads in flight during this one's arithmetic
+          // (the last step reloads itself: always in range)
+          FoldLd cur;
+          fold_load<RL, VEC, true>(sp, a.C_out, HoWo, pq, p_hi, 0, gq, cur);
           for (int ks = 0; ks < a.nks; ++ks) {
-            FoldLd d;
-            fold_load<RL, VEC, true>(sp, a.C_out, HoWo, pq, p_hi, ks, gq, d);
-            fold_use<MT, RL>(As, Bsh, a.bias != nullptr, lane, ks, gq, d, yt, p_relu, p_bias);
+            FoldLd nxt;
+            fold_load<RL, VEC, true>(sp, a.C_out, HoWo, pq, p_hi, min(ks + 1, a.nks - 1), gq, nxt);
+            fold_use<MT, RL>(As, Bsh, a.bias != nullptr, lane, ks, gq, cur, yt, p_relu, p_bias);
+            cur = nxt;
           }
         } else {
           for (int ks = 0; ks < a.nks; ++ks) {
