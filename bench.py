@@ -424,6 +424,14 @@ def kernel_suite(reps):
     sec = _time_launches([lambda: dst.copy_(src)], reps)
     report('-', 'device copy (torch copy_)', '1 GiB read + 1 GiB write', sec, 'hbm', 2.0 * n * 4)
     del src, dst
+    # -- achievable at the narrow kernels' sizes (tens of MB per launch, where
+    #    launch and drain take a larger share): 40 MiB copies, sets rotated
+    #    past the 256 MB cache like the rows below
+    n = (40 << 20) // 4
+    sets = [(rnd(n), torch.empty(n, device=dev)) for _ in range(_n_sets(8 * n))]
+    sec = _time_launches([lambda s=s: s[1].copy_(s[0]) for s in sets], reps)
+    report('-', 'device copy (torch copy_)', '40 MiB read + 40 MiB write', sec, 'hbm', 2.0 * n * 4)
+    del sets
 
     # -- a1: slopes of every (domain, neuron), 524,288 x 50
     n = 524288 * 50

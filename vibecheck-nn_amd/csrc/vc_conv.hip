@@ -946,7 +946,7 @@ int backward_conv(const float* ew_in, int64_t M, const float* kernel, const floa
   const int64_t npix = (int64_t)Hc * Wc, N = M * npix, Kd = (int64_t)C_out * Ty * Tx;
   if (N > kMaxDim || Kd > kMaxDim) return VC_ERR_UNSUPPORTED;
   FoldPlan fp;
-  if (fold_plan(C_out, H_out, W_out, C_in, W, kh, kw, sh, sw, pw, fp)) {
+  if (M < (int64_t(1) << 31) && fold_plan(C_out, H_out, W_out, C_in, W, kh, kw, sh, sw, pw, fp)) {
     FoldArgs a{};
     a.ew = ew_in;
     a.M = M;
