@@ -406,7 +406,9 @@ __global__ __launch_bounds__(NT) void k_conv_t_smallc(const float* ew, int64_t M
 }
 
 // Transposed convolution onto few values per tap set (C_in kh kw <= 32, the
-// network's input layer) as a GEMM and a fold.  Per image, first
+// network's input layer) as a GEMM and a fold (the conv branch of the
+// backward, verify_zono_bnb.py:4568-4593, and in the fused form the relu
+// branch before it, :4409-4453).  Per image, first
 //   Y[(ci, ky, kx), q] = sum_co K[co, ci, ky, kx] e[co, q]
 // over the source pixels q on the MFMA (M = C_in kh kw in MT tiles of 16
 // rows, K = C_out, N = source pixels), then
@@ -446,7 +448,6 @@ struct FoldArgs {
   FastDiv f_W, f_Wo, f_RS, f_sh, f_sw, f_R, f_DB, f_ndb, f_tile;
 };
 
-__device__ __forceinline__ float pos_of(float a) { return a < 0.f ? 0.f : a; }
 __device__ __forceinline__ float neg_of(float a) { return a > 0.f ? 0.f : a; }
 
 // One K-step's operands of a lane: its quad of source values (channel
