@@ -1548,6 +1548,9 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
   float* sbias = smem + G.nfloats;                                // [n][FW]
   double* sred = reinterpret_cast<double*>(sbias + G.n * FW);     // [ZWW][FW]
   float* scen = reinterpret_cast<float*>(sred + ZWW * FW);        // centre column [FW]
+  float* slam = scen + FW;                                        // lambda [FW]
+  float* smu = slam + FW;                                         // mu [FW]
+  unsigned long long* sumask = reinterpret_cast<unsigned long long*>(smu + FW);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int n = G.n, d0 = G.d[0];
@@ -1655,39 +1658,45 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
         __syncthreads();
         const int dM = G.d[l + 1];
         const bool last = l == n - 1;
+        // wave 0, lane j: neuron j's radius (the waves' partials in a fixed
+        // order), bounds, lambda and mu, and the unstable set as one mask;
+        // the other waves read them back (one reduction, not one per wave)
+        if (wv == 0) {
+          const int j = lane;
+          double sd = sred[j];
+#pragma unroll
+          for (int w2 = 1; w2 < ZWW; ++w2) sd += sred[w2 * FW + j];
+          const float rad = (float)sd;
+          const float c = scen[j];
+          const float lo = c - rad, hi = c + rad;
+          const bool valid = j < dM;
+          const bool ust = valid && lo < 0.f && hi > 0.f;
+          const bool dead = hi <= 0.f;
+          if (valid) {
+            out.lo[l][dom * dM + j] = lo;
+            out.hi[l][dom * dM + j] = hi;
+          }
+          slam[j] = ust ? hi / (hi - lo) : (dead ? 0.f : 1.f);
+          smu[j] = ust ? (-hi * lo) / (2.f * (hi - lo)) : 0.f;
+          const uint64_t um = __ballot(ust);
+          if (lane == 0) *sumask = um;
+        }
+        __syncthreads();  // sred / scen are rewritten by the next layer after this
+        const uint64_t umask = *sumask;
         float mu[MT][4];
-        uint64_t umask = 0;
 #pragma unroll
         for (int t = 0; t < MT; ++t)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int j = 16 * t + 4 * g + i;
-            double sd = sred[j];
-#pragma unroll
-            for (int w2 = 1; w2 < ZWW; ++w2) sd += sred[w2 * FW + j];
-            const float rad = (float)sd;
-            const float c = scen[j];
-            const float lo = c - rad, hi = c + rad;
-            const bool valid = j < dM;
-            const bool ust = valid && lo < 0.f && hi > 0.f;
-            const bool dead = hi <= 0.f;
-            if (valid && centre) {
-              out.lo[l][dom * dM + j] = lo;
-              out.hi[l][dom * dM + j] = hi;
-            }
-            const float lam = ust ? hi / (hi - lo) : (dead ? 0.f : 1.f);
-            mu[t][i] = ust ? (-hi * lo) / (2.f * (hi - lo)) : 0.f;
+            const float lam = slam[j];
+            mu[t][i] = smu[j];
             if (!last) {
 #pragma unroll
               for (int q = 0; q < ZWT; ++q)
                 Z[q][t][i] = (q == 0 && centre) ? lam * Z[q][t][i] + mu[t][i] : Z[q][t][i] * lam;
             }
-            const uint64_t bal2 = __ballot(ust && r == 0);
-#pragma unroll
-            for (int gg = 0; gg < 4; ++gg)
-              if ((bal2 >> (16 * gg)) & 1ull) umask |= 1ull << (16 * t + 4 * gg + i);
           }
-        __syncthreads();  // sred / scen are rewritten by the next layer
         const int cnt = __popcll(umask);
         if (last) break;
         if (Kc + cnt > cap) {
@@ -2957,7 +2966,8 @@ extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const flo
     if (l < n_relu && (!za.lo[l] || !za.hi[l])) return VC_ERR_ARG;
   }
   const size_t lds = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float) +
-                     (size_t)ZWW * FW * sizeof(double) + (size_t)FW * sizeof(float);
+                     (size_t)ZWW * FW * sizeof(double) + (size_t)3 * FW * sizeof(float) +
+                     sizeof(unsigned long long);
   if (lds > 160 * 1024 - 2048) return VC_ERR_UNSUPPORTED;
   const void* fn = nullptr;
   switch (G.variant) {
