@@ -52,6 +52,13 @@ FP32_MFMA_PEAK = 157.3
 CROWN_ENTRIES = ['vc_mlp_tiled_crown', 'vc_mlp_crown_rows']
 
 
+def _seed_row(k, args):
+    """The seed-counter row of the k-th timed CROWN launch: the native round
+    files its row with the launch (rounds it does not time still take one);
+    launches timed through the entry point take one row each, in order."""
+    return args[5] if len(args) > 5 and args[5] is not None else k
+
+
 def _crown_launches(kt):
     """The timed CROWN passes, in call order within each entry point (a
     workload calls one of them)."""
@@ -943,8 +950,8 @@ def run_config(cfg, steps, warmup, cpu):
         lst = _crown_launches(_lib.timing_end())
         mf.SEED_COUNTER = None
         dims = mf.plan_for(gg, dev).dims
-        flop = sum(f + _lib.seed_flops(dims, seeded.tolist()[k]) for k, (_, f, _) in
-                   enumerate(lst))
+        flop = sum(f + _lib.seed_flops(dims, seeded.tolist()[_seed_row(k, a)])
+                   for k, (_, f, a) in enumerate(lst))
         sec = sum(x[0] for x in lst)
         line['roofline'] = _roof(crown_kernel_name(B), f'{B:,} boxes', sec,
                                  flop=flop, launches=len(lst))
@@ -1031,14 +1038,18 @@ def main():
     seeded = torch.zeros(max(args.steps, args.warmup) * N_ROUNDS + 8, 16, dtype=torch.int64,
                          device=dev)
     mf.SEED_COUNTER, mf.SEED_ROW = seeded, 0
-    _lib.timing_begin(['vc_mlp_crown', 'vc_mlp_tiled_crown'])
+    # only the large round's CROWN pass is the roofline's unit: the small
+    # rounds' launches are not bracketed by events
+    lib = _lib.load()
+    when = {'vc_mlp_tiled_crown': lambda b: lib.vc_mlp_tiled_crown_mode(b) == 0}
+    _lib.timing_begin(['vc_mlp_crown', 'vc_mlp_tiled_crown'], when=when)
     for _ in range(max(1, args.warmup)):
         run_rounds(gg, xl0, xh0, se, table)
     _lib.timing_end()
     seeded.zero_()
     mf.SEED_ROW = 0
     torch.cuda.synchronize()
-    _lib.timing_begin(['vc_mlp_crown', 'vc_mlp_tiled_crown'])
+    _lib.timing_begin(['vc_mlp_crown', 'vc_mlp_tiled_crown'], when=when)
     t0 = time.perf_counter()
     stats = None
     for _ in range(args.steps):
@@ -1050,10 +1061,9 @@ def main():
     if kt.get('vc_mlp_tiled_crown', {}).get('launches'):
         # the dominant work is the CROWN pass of the large batch (the
         # layer-synchronous rows form); the small rounds run k_crown_dom
-        lib = _lib.load()
         dims = [op['W'].shape[1] for op in gg['ops'] if op['type'] == 'fc']
         rows = seeded.tolist()
-        sel = [(sec, fl + _lib.seed_flops(dims, rows[k]))
+        sel = [(sec, fl + _lib.seed_flops(dims, rows[_seed_row(k, a)]))
                for k, (sec, fl, a) in enumerate(kt['vc_mlp_tiled_crown']['per_launch'])
                if lib.vc_mlp_tiled_crown_mode(a[4]) == 0]
         kt = {'vc_mlp_tiled_crown': {'launches': len(sel), 'seconds': sum(x[0] for x in sel),

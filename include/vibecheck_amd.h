@@ -703,9 +703,12 @@ int vc_mlp_tiled_alpha_iter(const int32_t *dims, int n_relu, const float *frag,
  * here and ends as vc_alpha_control leaves it (ctl[2] = evaluated
  * iterations); best (B, Q) = the best bound per spec row.  Torch Adam's
  * schedule: step size lr_t / (1 - b1^t), bias correction (1 - b2^t)^0.5,
- * lr_{t+1} = lr_t * lr_decay.  stop_host (nullable, pinned host memory,
- * zero on entry): vc_alpha_control sets it when the loop stops, and the
- * iterations not yet enqueued then are skipped (they would do nothing). */
+ * lr_{t+1} = lr_t * lr_decay.  stop_host (nullable; two int32 words of
+ * pinned host memory, zero on entry): the control sets word 0 when the
+ * loop stops and stores in word 1 how many iterations it has taken; the
+ * host keeps one chunk of iterations enqueued beyond the controls it has
+ * seen (a bounded wait) and skips the chunks after a stop, which would do
+ * nothing. */
 int vc_mlp_tiled_alpha_run(const int32_t *dims, int n_relu, const float *frag,
                            const float *bias_cat, int64_t B, const float *xl,
                            const float *xh, const float *const *lo,

@@ -264,7 +264,10 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
         m2[l] = r.a_state + 2 * (int64_t)sumd * n_open + off;
         off += sz;
       }
-      if (stop_host) *reinterpret_cast<volatile int32_t*>(stop_host) = 0;
+      if (stop_host) {
+        reinterpret_cast<volatile int32_t*>(stop_host)[0] = 0;
+        reinterpret_cast<volatile int32_t*>(stop_host)[1] = 0;
+      }
       VC_TRY(vc_mlp_tiled_alpha_run(dims, n, frag, bias_cat, n_open, r.a_xl, r.a_xh, r.a_lo,
                                     r.a_hi, alpha, m1, m2, Q, spec_rows, spec_acc, r.a_lb,
                                     r.a_best, 0.9, 0.999, 1e-8, alpha_lr, alpha_lr_decay,

@@ -82,7 +82,9 @@ struct AdamChunk {
 };
 
 // vc_alpha_control over n_it consecutive iterations (lbs: n_it x n),
-// stopping at the first stop (vc_elementwise.hip).
+// stopping at the first stop (vc_elementwise.hip).  stop_host (nullable):
+// two pinned words, [0] set at a stop, [1] = it0 + n_it once all n_it
+// iterations have been taken.
 int alpha_control_chunk(float* best, const float* lbs, int64_t n, int it0, int n_it, double eps,
                         float* ctl, int32_t* stop_host, hipStream_t stream);
 

@@ -590,8 +590,12 @@ __global__ void k_split_clamps(const int64_t* layer, const int64_t* neuron, cons
 // it0 + n_it - 1 whose bounds are lbs[t] (n each), in order, up to the
 // first stop (the later ones are discarded): best update, global max, the
 // reference's two stop tests.
+// stop_host (a pinned host word, nullable) is set to 1 at a stop; progress
+// (pinned, nullable) to it0 + n_it once the launch has taken every one of
+// its iterations without a stop.
 __global__ void k_alpha_control(float* best, const float* lbs, int64_t n, int it0, int n_it,
-                                double eps, float* ctl, int32_t* stop_host) {
+                                double eps, float* ctl, int32_t* stop_host,
+                                int32_t* progress) {
   __shared__ float smax[16];
   __shared__ int sneg[16];
   __shared__ int s_stop;
@@ -641,6 +645,8 @@ __global__ void k_alpha_control(float* best, const float* lbs, int64_t n, int it
     __syncthreads();
     if (s_stop) return;
   }
+  if (threadIdx.x == 0 && progress)
+    __hip_atomic_store(progress, it0 + n_it, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 __global__ void k_best_update(float* best, const float* lb, int64_t n, int init, float* out2) {
@@ -1412,7 +1418,7 @@ int alpha_control_chunk(float* best, const float* lbs, int64_t n, int it0, int n
                         float* ctl, int32_t* stop_host, hipStream_t stream) {
   if (!best || !lbs || !ctl || n <= 0 || it0 < 0 || n_it < 1) return VC_ERR_ARG;
   hipLaunchKernelGGL(k_alpha_control, dim3(1), dim3(1024), 0, stream, best, lbs, n, it0, n_it,
-                     eps, ctl, stop_host);
+                     eps, ctl, stop_host, stop_host ? stop_host + 1 : nullptr);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }
@@ -1421,7 +1427,7 @@ extern "C" int vc_alpha_control(float* best, const float* lb, int64_t n, int it,
                                 float* ctl, int32_t* stop_host, vc_stream_t stream) {
   if (!best || !lb || !ctl || n <= 0 || it < 0) return VC_ERR_ARG;
   hipLaunchKernelGGL(k_alpha_control, dim3(1), dim3(1024), 0, (hipStream_t)stream, best, lb, n,
-                     it, 1, eps, ctl, stop_host);
+                     it, 1, eps, ctl, stop_host, nullptr);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }

@@ -2866,11 +2866,17 @@ extern "C" int vc_mlp_tiled_alpha_run(const int32_t* dims, int n_relu, const flo
   // The small-batch kernel runs up to VC_ALPHA_CHUNK iterations per launch
   // on its LDS state; the control replays the stop tests over them in
   // order and discards the ones after a stop.
+  // With stop_host, one chunk is kept in flight ahead of the control the
+  // host has seen: before chunk k the host waits (bounded) for chunk k - 2's
+  // control, so a stop costs at most one enqueued chunk that does nothing.
   volatile int32_t* sh = stop_host;
   const int K = L.quad ? VC_ALPHA_CHUNK : 1;
   double cur_lr = lr;
-  for (int it0 = 0; it0 < n_iters; it0 += K) {
-    if (sh && *sh != 0) break;
+  for (int it0 = 0, k = 0; it0 < n_iters; it0 += K, ++k) {
+    if (sh && k >= 2)
+      for (long spin = 0; spin < (1l << 24) && sh[0] == 0 && sh[1] < it0 - K; ++spin) {
+      }
+    if (sh && sh[0] != 0) break;
     AdamChunk ac;
     ac.n = std::min(K, n_iters - it0);
     for (int t = 0; t < ac.n; ++t) {

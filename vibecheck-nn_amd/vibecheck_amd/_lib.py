@@ -224,13 +224,21 @@ _FLOPS = {
 }
 
 _timing = None
+_timing_when = {}
+# Event pairs of earlier timing sessions, reused: creating a HIP event costs
+# tens of microseconds of host time, which inside a timed region is time
+# the GPU can spend idle.
+_EV_FREE = []
 
 
-def timing_begin(names):
+def timing_begin(names, when=None):
     """Record HIP events around every call of the named entry points (on the
-    current stream, which is the launch stream)."""
-    global _timing
+    current stream, which is the launch stream).  ``when``: {name:
+    predicate(batch)}; a launch timed through timing_events on a batch the
+    predicate rejects is not recorded."""
+    global _timing, _timing_when
     _timing = {n: [] for n in names}
+    _timing_when = dict(when or {})
 
 
 def timing_end():
@@ -242,21 +250,32 @@ def timing_end():
     out = {}
     for n, lst in (rec or {}).items():
         per = [(s.elapsed_time(e) / 1e3, f, a) for s, e, f, a in lst]
+        _EV_FREE.extend((s, e) for s, e, _, _ in lst)
         out[n] = {'launches': len(per), 'seconds': sum(p[0] for p in per),
                   'flops': sum(p[1] for p in per), 'per_launch': per}
     return out
 
 
-def timing_events(name):
-    """A recorded (start, end) event pair for a launch of `name` made inside
-    another entry point, when `name` is being timed (else None)."""
-    if _timing is None or name not in _timing:
-        return None
+def _event_pair():
+    if _EV_FREE:
+        return _EV_FREE.pop()
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
-    s.record()  # creates the events; the entry point records them again
+    s.record()  # creates the events; their user records them again
     e.record()
     return s, e
+
+
+def timing_events(name, batch=None):
+    """A recorded (start, end) event pair for a launch of `name` made inside
+    another entry point, when `name` is being timed on this batch (else
+    None)."""
+    if _timing is None or name not in _timing:
+        return None
+    w = _timing_when.get(name)
+    if w is not None and batch is not None and not w(batch):
+        return None
+    return _event_pair()
 
 
 def timing_add(name, events, flops, args):
@@ -267,8 +286,7 @@ def timing_add(name, events, flops, args):
 def call(name, *args):
     lib = load()
     if _timing is not None and name in _timing:
-        s = torch.cuda.Event(enable_timing=True)
-        e = torch.cuda.Event(enable_timing=True)
+        s, e = _event_pair()
         s.record()
         rc = getattr(lib, name)(*args)
         e.record()

@@ -242,12 +242,13 @@ _HOST_WORDS = threading.local()
 
 
 def _stop_word():
-    """A pinned host int32 the alpha loop's control kernel sets when the loop
-    stops, so that the host stops enqueueing iterations (one per host
-    thread; each alpha loop ends with a host read, so it is free again)."""
+    """Two pinned host int32 words the alpha loop's control kernel stores
+    into (stopped; iterations taken), so that the host stops enqueueing
+    iterations (one pair per host thread; each alpha loop ends with a host
+    read, so it is free again)."""
     w = getattr(_HOST_WORDS, 'stop', None)
     if w is None:
-        w = _HOST_WORDS.stop = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        w = _HOST_WORDS.stop = torch.zeros(2, dtype=torch.int32, pin_memory=True)
     return w
 
 
@@ -309,7 +310,7 @@ def alpha_crown(plan, xl, xh, sb, Wq, bq, n_iters, lr, lr_decay, early_stop_eps,
             raise ValueError('alpha_crown: n_iters must be >= 1')
         ctl = torch.empty(4, device=dev)
         stop = _stop_word()
-        stop[0] = 0
+        stop.zero_()
         call('vc_mlp_tiled_alpha_run', plan.dims_p, plan.n, ptr(plan.tfrag),
              ptr(plan.bias_cat), B, ptr(xl), ptr(xh), *ptrs, Q, ptr(S), ptr(acc0), ptr(lb),
              ptr(best), b1, b2, eps, cur_lr, float(lr_decay), int(n_iters),

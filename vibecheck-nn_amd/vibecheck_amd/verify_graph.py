@@ -308,45 +308,59 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
     S, acc0 = mlp_fused.fold_spec(plan, Wq, bq)
     xl, xh = f32(xl), f32(xh)
     B, n_in = xl.shape
-    # the float outputs in one allocation: lb, acc, A, then 6 box arrays
+    # Between two rounds the GPU waits on this host code (each round ends
+    # with the children's count read back), so the outputs are one
+    # allocation addressed by offsets, and their views are made after the
+    # call: floats (lb, acc, A, 6 box arrays), then int64 indices [2, Bm],
+    # then flags [2, Bm], each 256-byte aligned.
     Bm = max(B, 1)
-    flt = torch.empty(Bm * (2 * Q + Q * n_in + 6 * n_in), device=dev)
-    lb = flt[:B * Q].view(B, Q)
-    acc = flt[Bm * Q:Bm * Q + B * Q].view(B, Q)
-    A = flt[2 * Bm * Q:2 * Bm * Q + B * Q * n_in].view(B, Q, n_in)
-    boxes = flt[Bm * (2 * Q + Q * n_in):].view(6, Bm, n_in)
-    flags = torch.empty(2, Bm, dtype=torch.bool, device=dev)
-    closed, feas = flags[0, :B], flags[1]
-    idx = torch.empty(2, Bm, dtype=torch.int64, device=dev)
+    nflt = Bm * (2 * Q + Q * n_in + 6 * n_in)
+    o_idx = (4 * nflt + 255) & ~255
+    o_flg = (o_idx + 16 * Bm + 255) & ~255
+    buf = torch.empty(o_flg + 2 * Bm, dtype=torch.uint8, device=dev)
+    p = buf.data_ptr()
+    p_box = p + 4 * Bm * (2 * Q + Q * n_in)
+    nb = 4 * Bm * n_in
     lib = _lib.load()
     nws = int(lib.vc_mlp_bab_round_workspace(plan.dims_p, plan.n, B, Q))
     ws = torch.empty(max(nws, 8), dtype=torch.uint8, device=dev)
     counts = (ctypes.c_int64 * 6)()
-    stop = mlp_fused._stop_word()
     # work accounting and timing of the CROWN launch, as mlp_fused.crown does
-    seeds = None
+    seeds = seed_row = None
     if mlp_fused.SEED_COUNTER is not None:
-        seeds = mlp_fused.SEED_COUNTER[mlp_fused.SEED_ROW]
+        seed_row = mlp_fused.SEED_ROW
+        seeds = mlp_fused.SEED_COUNTER[seed_row]
         mlp_fused.SEED_ROW += 1
-    ev = _lib.timing_events('vc_mlp_tiled_crown')
-    call('vc_mlp_bab_round', plan.dims_p, plan.n, ptr(plan.tfrag), ptr(plan.bias_cat), Q,
-         ptr(S), ptr(acc0), ptr(table.d_ptr), ptr(table.q_idx), table.n, B, ptr(xl), ptr(xh),
-         int(alpha_iters), float(alpha_lr), float(alpha_lr_decay), 1e-6, ptr(lb), ptr(A),
-         ptr(acc), ptr(closed), ptr(idx[0]), ptr(feas), ptr(boxes[0]), ptr(boxes[1]),
-         ptr(idx[1]), ptr(boxes[2]), ptr(boxes[3]), ptr(boxes[4]), ptr(boxes[5]), ptr(seeds),
-         ev[0].cuda_event if ev else None, ev[1].cuda_event if ev else None, ptr(ws),
-         nws, stop.data_ptr(), mlp_fused._pinned_words().data_ptr(), ctypes.addressof(counts),
-         stream())
+    ev = _lib.timing_events('vc_mlp_tiled_crown', B)
+    call('vc_mlp_bab_round', plan.dims_p, plan.n, plan.tfrag.data_ptr(),
+         plan.bias_cat.data_ptr(), Q, S.data_ptr(), acc0.data_ptr(), ptr(table.d_ptr),
+         ptr(table.q_idx), table.n, B, ptr(xl), ptr(xh), int(alpha_iters),
+         float(alpha_lr), float(alpha_lr_decay), 1e-6, p, p + 8 * Bm * Q, p + 4 * Bm * Q,
+         p + o_flg, p + o_idx, p + o_flg + Bm, p_box, p_box + nb, p + o_idx + 8 * Bm,
+         p_box + 2 * nb, p_box + 3 * nb, p_box + 4 * nb, p_box + 5 * nb, ptr(seeds),
+         ev[0].cuda_event if ev else None, ev[1].cuda_event if ev else None, ws.data_ptr(),
+         nws, mlp_fused._stop_word().data_ptr(), mlp_fused._pinned_words().data_ptr(),
+         ctypes.addressof(counts), stream())
     if ev:
         spec = _lib.mlp_crown_flops(plan.dims, plan.n, B, [0] * plan.n, 0, Q)
-        _lib.timing_add('vc_mlp_tiled_crown', ev, spec, (None, None, None, None, B))
+        _lib.timing_add('vc_mlp_tiled_crown', ev, spec, (None, None, None, None, B, seed_row))
     n_open, n_eval, n_unc, nf, nu, n_deg = (int(c) for c in counts)
-    out = {'lb': lb, 'A': A, 'acc': acc, 'closed': closed, 'unclosed': idx[0, :n_unc],
+    # the views by absolute storage offsets (in elements of each dtype)
+    fl = buf[:4 * nflt].view(torch.float32)
+    i64 = buf[o_idx:o_idx + 16 * Bm].view(torch.int64)
+    bl = buf[o_flg:].view(torch.bool)
+    ast = torch.as_strided
+    bo, nb, oi, r = Bm * (2 * Q + Q * n_in), Bm * n_in, o_idx // 8, (n_in, 1)
+    out = {'lb': ast(fl, (B, Q), (Q, 1), 0),
+           'A': ast(fl, (B, Q, n_in), (Q * n_in, n_in, 1), 2 * Bm * Q),
+           'acc': ast(fl, (B, Q), (Q, 1), Bm * Q),
+           'closed': ast(bl, (B,), (1,), o_flg), 'unclosed': ast(i64, (n_unc,), (1,), oi),
            'n_alpha_leaves': n_open, 'n_alpha_iters': n_eval,
-           'feasible': feas[:n_unc] if n_unc > 0 else None,
-           'xl_split': boxes[0, :nf], 'xh_split': boxes[1, :nf], 'ax': idx[1, :nf],
-           'n_degenerate': n_deg, 'low': (boxes[2, :nu], boxes[3, :nu]),
-           'high': (boxes[4, :nu], boxes[5, :nu])}
+           'feasible': ast(bl, (n_unc,), (1,), o_flg + Bm) if n_unc > 0 else None,
+           'xl_split': ast(fl, (nf, n_in), r, bo), 'xh_split': ast(fl, (nf, n_in), r, bo + nb),
+           'ax': ast(i64, (nf,), (1,), oi + Bm), 'n_degenerate': n_deg,
+           'low': (ast(fl, (nu, n_in), r, bo + 2 * nb), ast(fl, (nu, n_in), r, bo + 3 * nb)),
+           'high': (ast(fl, (nu, n_in), r, bo + 4 * nb), ast(fl, (nu, n_in), r, bo + 5 * nb))}
     out['chunks'] = [out['low'], out['high']] if nu > 0 else []
     return out
 
