@@ -976,9 +976,9 @@ constexpr int AQD = 4;  // domains per workgroup at most
 
 __host__ __device__ inline int alpha_quad_floats(int n, int KS, int Q, int MT) {
   // slopes [n][4][FW], Adam state [n][3][FW], P_l [n][KS][4][Q], d lb / d
-  // alpha [FW], box [2 FW], exchange [2][MT][4][Q][4], row sums [MT + 1][16]
-  // doubles
-  const int f = n * 7 * FW + n * KS * 4 * Q + 3 * FW + 2 * MT * 16 * Q + 2 * (MT + 1) * 16;
+  // alpha [n][FW], box [2 FW], exchange [2][MT][4][Q][4], row sums
+  // [MT + 1][16] doubles
+  const int f = n * 8 * FW + n * KS * 4 * Q + 2 * FW + 2 * MT * 16 * Q + 2 * (MT + 1) * 16;
   return (f + 3) & ~3;
 }
 
@@ -1018,8 +1018,8 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
   float* ssl = sbias + n * FW + qd * alpha_quad_floats(n, KS, Q, MT);  // [l][ls, us, ut, un][FW]
   float* sad = ssl + n * 4 * FW;                                        // [l][alpha, m, v][FW]
   float* sP = sad + n * 3 * FW;                                         // [l][ks][g][r < Q]
-  float* sga = sP + n * KS * 4 * Q;                                     // [FW]
-  float* sx = sga + FW;                                                 // xl, xh [FW]
+  float* sga = sP + n * KS * 4 * Q;                                     // [n][FW]
+  float* sx = sga + n * FW;                                             // xl, xh [FW]
   float* xch = sx + 2 * FW;                                             // [2][MT][4][Q][4]
   double* sacc = reinterpret_cast<double*>(xch + 2 * MT * 16 * Q);      // [MT + 1][16]
   vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
@@ -1176,7 +1176,8 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
       for (int u = 0; u < MT; ++u) t += sacc[u * 16 + r];
       lb_out[(int64_t)t_it * B * Q + dom * Q + r] = (float)(t + sacc[MT * 16 + r]);
     }
-    // ---- forward gradient sweep with the Adam update, owned neurons
+    // ---- forward gradient sweep, owned neurons; the Adam update of every
+    // layer follows it (it changes only the next iteration's slopes)
     for (int l = 0; l < n; ++l) {
       const int dW = G.d[l + 1];
       float* sl = ssl + l * 4 * FW;
@@ -1194,29 +1195,12 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
           const float pv = (has && live) ? pl[(ks * 4 + g) * Q + r] : 0.f;
           const float ge = GEw[i];
           const float s = row_sum16(ge * fmaxf(pv, 0.f));
-          if (r == 0) sga[j] = s;
+          if (r == 0) sga[l * FW + j] = s;
           const bool mp = pv >= 0.f, mn = pv <= 0.f;
           float gp = ge * ((mp ? sl[j] : 0.f) + (mn ? sl[FW + j] : 0.f));
           if (mn) gp = gp + sl[2 * FW + j];
           GEw[i] = live ? gp : 0.f;
         }
-      }
-      __threadfence_block();
-      if (has && lane < 16) {
-        float* sa = sad + l * 3 * FW;
-        const int j = 16 * w + lane;
-        const bool un = j < dW && sl[3 * FW + j] != 0.f;
-        if (un) {
-          float mi = sa[FW + j], vi = sa[2 * FW + j];
-          float pa = adam_update(sa[j], -sga[j], mi, vi, adam);
-          pa = fminf(fmaxf(pa, 0.f), 1.f);
-          sa[FW + j] = mi;
-          sa[2 * FW + j] = vi;
-          sa[j] = pa;
-          sl[j] = pa;  // unstable: the next iteration's lower slope is alpha
-        }
-        // the last iteration of the launch leaves its gradient
-        if (aa.grad[l] && j < dW && t_it == ac.n - 1) aa.grad[l][dom * dW + j] = un ? sga[j] : 0.f;
       }
       if (l + 1 < n) {
         // with the bias row, a constant 1 at index d_{l+1} picks up b_{l+1}
@@ -1240,6 +1224,30 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
         GEw = o;
       }
     }
+    // ---- Adam on the owned neurons of every layer, all lanes
+    __threadfence_block();
+    if (has) {
+      for (int k = lane; k < n * 16; k += 64) {
+        const int l = k >> 4, j = 16 * w + (k & 15);
+        const int dW = G.d[l + 1];
+        float* sl = ssl + l * 4 * FW;
+        float* sa = sad + l * 3 * FW;
+        const float gs = sga[l * FW + j];
+        const bool un = j < dW && sl[3 * FW + j] != 0.f;
+        if (un) {
+          float mi = sa[FW + j], vi = sa[2 * FW + j];
+          float pa = adam_update(sa[j], -gs, mi, vi, adam);
+          pa = fminf(fmaxf(pa, 0.f), 1.f);
+          sa[FW + j] = mi;
+          sa[2 * FW + j] = vi;
+          sa[j] = pa;
+          sl[j] = pa;  // unstable: the next iteration's lower slope is alpha
+        }
+        // the last iteration of the launch leaves its gradient
+        if (aa.grad[l] && j < dW && t_it == ac.n - 1) aa.grad[l][dom * dW + j] = un ? gs : 0.f;
+      }
+    }
+    __threadfence_block();
     }  // iterations
     // ---- the owned neurons' Adam state back (the wave's own LDS writes)
     __threadfence_block();
