@@ -70,8 +70,9 @@ def crown_kernel_name(B):
     from vibecheck_amd import _lib
     if _lib.load().vc_mlp_tiled_crown_mode(B) == 1:
         return 'k_crown_dom (vc_mlp_tiled_crown)'
-    return ('CROWN rows pass (vc_mlp_crown_rows: k_rows_mask, k_rows_scan1/2, k_rows_write, '
-            'per ReLU layer k_crown_rows + k_rows_cut, k_spec_rows)')
+    return ('CROWN rows pass (vc_mlp_crown_rows: k_rows_scan1/2, k_rows_write, per ReLU '
+            'layer k_crown_rows + k_rows_cut, k_spec_rows; in the native round the seed '
+            'masks come from the zonotope passes)')
 
 
 def run_rounds(gg, xl, xh, spec_ew, table, timers=None, keep=None):

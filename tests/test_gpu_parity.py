@@ -1021,8 +1021,19 @@ def test_split_and_compaction_bit_exact(gpu):
 def test_bab_round_native_matches_python_round(gpu, alpha_iters):
     """The round as one native call (vc_mlp_bab_round) runs the same entry
     points in the same order as bab_step's Python round: every output equal
-    bit for bit, every count equal."""
+    bit for bit, every count equal.  The native round takes the CROWN rows
+    pass's seed masks and union from its zonotope passes, the Python round
+    computes them in the rows pass (k_rows_mask); the batch has domains that
+    overflow the one-wavefront zonotope pass, whose masks the wide pass
+    writes."""
     gg_c, gg_g, xl, xh = acas(gpu, 4096, seed=23, scale=2.0)
+    # generator columns per domain at the last append (oracle bounds):
+    # 1 + inputs + unstable neurons of every relu but the last
+    sb, _ = rb.zono_forward_batched(xl, xh, gg_c)
+    cols = torch.full((xl.shape[0],), 1 + xl.shape[1])
+    for L in sorted(sb)[:-1]:
+        cols = cols + ((sb[L][0] < 0) & (sb[L][1] > 0)).sum(1)
+    assert int((cols > 128).sum()) > 0
     _, se_g, dq = spec_pair(5, gpu)
     table = vg.DisjunctTable(dq, gpu)
     xl, xh = xl.to(gpu), xh.to(gpu)

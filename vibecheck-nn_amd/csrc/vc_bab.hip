@@ -208,12 +208,25 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
   int32_t widths[MAXL];
   for (int l = 0; l < n; ++l) widths[l] = dims[l + 1];
 
-  // ---- bound phase: zonotope, union of the unstable neurons, CROWN + spec
-  VC_TRY(vc_mlp_tiled_zono_bounds(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
-                                  r.queue + 1, stream));
+  // ---- bound phase: zonotope, union of the unstable neurons, CROWN + spec.
+  // For the rows form the zonotope passes also leave its per-domain seed
+  // masks and the union in its workspace (same bounds, no second pass over
+  // them).
+  if (r.rws) {
+    VC_TRY(vcm::zono_bounds_masked(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
+                                   r.queue + 1, r.rws, st));
+  } else {
+    VC_TRY(vc_mlp_tiled_zono_bounds(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi,
+                                    r.ovf, r.queue + 1, stream));
+  }
   VC_TRY(vc_compact(r.ovf, B, 0, r.idx, r.cnt, r.cws, r.cws_bytes, stream));
-  VC_TRY(vc_mlp_tiled_zono_wide(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
-                                r.idx, r.cnt, stream));
+  if (r.rws) {
+    VC_TRY(vcm::zono_wide_masked(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
+                                 r.idx, r.cnt, r.rws, st));
+  } else {
+    VC_TRY(vc_mlp_tiled_zono_wide(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
+                                  r.idx, r.cnt, stream));
+  }
   // the rows form builds the union in its own pass over the bounds
   if (!r.rws) {
     VC_TRY(vc_unstable_union_layers(r.sb_lo, r.sb_hi, widths, n, B, r.uflags, stream));
@@ -223,9 +236,9 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
   // the round reads only the spec bound of the CROWN pass (alpha restarts
   // from the zonotope bounds): the rows form writes no CROWN bounds
   if (r.rws)
-    VC_TRY(vc_mlp_crown_rows(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, nullptr,
-                             nullptr, nullptr, nullptr, 1, 1, Q, spec_rows, spec_acc, lb, A, acc,
-                             seed_rows, r.rws, r.rws_bytes, stream));
+    VC_TRY(vcm::crown_rows_premasked(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, Q,
+                                     spec_rows, spec_acc, lb, A, acc, seed_rows, r.rws,
+                                     r.rws_bytes, st));
   else
     VC_TRY(vc_mlp_tiled_crown(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.t_lo,
                               r.t_hi, r.uidx, r.umeta, 1, 1, Q, spec_rows, spec_acc, lb, A,

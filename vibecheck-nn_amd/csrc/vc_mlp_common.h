@@ -47,6 +47,26 @@ __device__ __forceinline__ int queue_take(int* q, int lane) {
 __device__ __forceinline__ int64_t queue_bcast(int t) { return (int64_t)__shfl(t, 0, 64); }
 
 
+// The input-split round's bound phase with the CROWN rows pass's per-domain
+// seed masks and union of unstable sets written by the zonotope passes
+// (vc_mlp_tiled.hip): rows_work is the vc_mlp_crown_rows workspace of the
+// same B that crown_rows_premasked then runs in (per_domain, no index
+// lists, no CROWN bounds out), skipping its own pass over the bounds.
+int zono_bounds_masked(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+                       int64_t B, const float* xl, const float* xh, float* const* lo_out,
+                       float* const* hi_out, uint8_t* overflow, int32_t* queue, void* rows_work,
+                       hipStream_t st);
+int zono_wide_masked(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+                     int64_t B, const float* xl, const float* xh, float* const* lo_out,
+                     float* const* hi_out, uint8_t* overflow, const int64_t* list,
+                     const int64_t* n_list, void* rows_work, hipStream_t st);
+int crown_rows_premasked(const int32_t* dims, int n_relu, const float* frag,
+                         const float* bias_cat, int64_t B, const float* xl, const float* xh,
+                         const float* const* lo_in, const float* const* hi_in, int Q,
+                         const float* spec_rows, const float* spec_acc, float* lb_out,
+                         float* A_out, float* acc_out, uint64_t* seed_rows, void* work,
+                         int64_t work_bytes, hipStream_t st);
+
 // Compute units of the current device (read once per device).
 inline int cu_count() {
   static int cached[64] = {0};

@@ -1297,6 +1297,15 @@ struct TZonoArgs {
   float* hi[MAXL];
 };
 
+// Optional outputs of the zonotope passes for the CROWN rows pass (its
+// k_rows_mask over the same bounds): per layer and domain the seed filter
+// lo < 0, hi > -1e-7 as a mask ([n][B]), and the union of the unstable sets
+// (lo < 0 < hi) ORed into umask[n], which the caller clears.
+struct ZonoMasks {
+  uint64_t* masks;
+  unsigned long long* umask;
+};
+
 // fc_0 on the input block for NP column tiles, tile p starting at column
 // base + p * step: column 0 = centre (and the constant 1 of the bias row),
 // column 1 + k = radius k.
@@ -1347,13 +1356,18 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
                                                          int64_t B, const float* __restrict__ xl,
                                                          const float* __restrict__ xh,
                                                          TZonoArgs out, uint8_t* overflow,
-                                                         int* queue) {
+                                                         int* queue, ZonoMasks zm) {
   extern __shared__ float smem[];
+  // with zm.masks: this wave's unstable sets of the current domain, and the
+  // workgroup's union of them over its domains that did not overflow
+  __shared__ unsigned long long s_dun[ZNW][MAXL];
+  __shared__ unsigned long long s_wun[MAXL];
   float* sfrag = smem;
   float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int n = G.n, d0 = G.d[0];
+  if (threadIdx.x < MAXL) s_wun[threadIdx.x] = 0ull;
   vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
   for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
     const int l = k / FW, j = k % FW;
@@ -1492,6 +1506,15 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
         out.hi[l][dom * dM + j] = hi;
       }
       const uint64_t umask = __ballot(ust);
+      if (zm.masks) {
+        // the neurons the CROWN rows pass seeds for this domain (lo < 0,
+        // hi > -1e-7: the filter of k_rows_mask) and its unstable set
+        const uint64_t km = __ballot(valid && lo < 0.f && hi > -1e-7f);
+        if (lane == 0) {
+          zm.masks[(int64_t)l * B + dom] = km;
+          s_dun[wv][l] = umask;
+        }
+      }
       const int cnt = __popcll(umask);
       if (l == n - 1) break;  // the last relu's output is not propagated
       if (Kc + cnt > 16 * ZT) {
@@ -1526,7 +1549,13 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
       Kc += cnt;
     }
     if (lane == 0) overflow[dom] = ovf ? 1 : 0;
+    // an overflowing domain's sets come from the wide pass, over its bounds
+    if (zm.masks && !ovf && lane < n) atomicOr(&s_wun[lane], s_dun[wv][lane]);
     dom = (queue && B > nwaves) ? nwaves + vcm::queue_bcast(tnext) : dom + nwaves;
+  }
+  if (zm.masks) {
+    __syncthreads();
+    if (threadIdx.x < n && s_wun[threadIdx.x]) atomicOr(zm.umask + threadIdx.x, s_wun[threadIdx.x]);
   }
 }
 
@@ -1550,8 +1579,10 @@ template <int MT, int KS, bool BROW>
 __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
     TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
     const float* __restrict__ xl, const float* __restrict__ xh, TZonoArgs out,
-    uint8_t* overflow, const int64_t* __restrict__ list, const int64_t* __restrict__ n_list) {
+    uint8_t* overflow, const int64_t* __restrict__ list, const int64_t* __restrict__ n_list,
+    ZonoMasks zm) {
   extern __shared__ float smem[];
+  __shared__ unsigned long long s_wun[MAXL];  // with zm.masks: the union over this workgroup's domains
   float* sfrag = smem;
   float* sbias = smem + G.nfloats;                                // [n][FW]
   double* sred = reinterpret_cast<double*>(sbias + G.n * FW);     // [ZWW][FW]
@@ -1567,6 +1598,7 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
   // spread evenly whatever their positions; idle workgroups leave at once
   const int64_t nflag = *n_list;
   if ((int64_t)blockIdx.x >= nflag) return;
+  if (threadIdx.x < MAXL) s_wun[threadIdx.x] = 0ull;
   vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
   for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
     const int l = k / FW, j = k % FW;
@@ -1688,6 +1720,13 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
           smu[j] = ust ? (-hi * lo) / (2.f * (hi - lo)) : 0.f;
           const uint64_t um = __ballot(ust);
           if (lane == 0) *sumask = um;
+          if (zm.masks) {
+            const uint64_t km = __ballot(valid && lo < 0.f && hi > -1e-7f);
+            if (lane == 0) {
+              zm.masks[(int64_t)l * B + dom] = km;
+              s_wun[l] |= um;
+            }
+          }
         }
         __syncthreads();  // sred / scen are rewritten by the next layer after this
         const uint64_t umask = *sumask;
@@ -1731,6 +1770,10 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
       }
       if (threadIdx.x == 0) overflow[dom] = ovf ? 1 : 0;
     }
+  }
+  if (zm.masks) {
+    __syncthreads();
+    if (threadIdx.x < n && s_wun[threadIdx.x]) atomicOr(zm.umask + threadIdx.x, s_wun[threadIdx.x]);
   }
 }
 
@@ -2516,15 +2559,19 @@ extern "C" int64_t vc_mlp_crown_rows_workspace(const int32_t* dims, int n_relu, 
   return (int64_t)rows_carve(nullptr, n_relu, maxw, B).bytes;
 }
 
-extern "C" int vc_mlp_crown_rows(const int32_t* dims, int n_relu, const float* frag,
-                                 const float* bias_cat, int64_t B, const float* xl,
-                                 const float* xh, const float* const* lo_in,
-                                 const float* const* hi_in, float* const* lo_out,
-                                 float* const* hi_out, const int32_t* idx_all,
-                                 const int32_t* idx_meta, int do_crown, int per_domain, int Q,
-                                 const float* spec_rows, const float* spec_acc, float* lb_out,
-                                 float* A_out, float* acc_out, uint64_t* seed_rows, void* work,
-                                 int64_t work_bytes, vc_stream_t stream) {
+namespace {
+// premasked: the seed masks and the union of the unstable sets are already
+// in the workspace (written by the zonotope passes over the same bounds,
+// vcm::zono_bounds_masked), so k_rows_union and k_rows_mask are skipped;
+// only with do_crown, per_domain and no index lists.
+int crown_rows_run(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+                   int64_t B, const float* xl, const float* xh, const float* const* lo_in,
+                   const float* const* hi_in, float* const* lo_out, float* const* hi_out,
+                   const int32_t* idx_all, const int32_t* idx_meta, int do_crown, int per_domain,
+                   int Q, const float* spec_rows, const float* spec_acc, float* lb_out,
+                   float* A_out, float* acc_out, uint64_t* seed_rows, void* work,
+                   int64_t work_bytes, bool premasked, vc_stream_t stream) {
+  if (premasked && (!do_crown || !per_domain || idx_all)) return VC_ERR_ARG;
   TGeom G;
   int rc = tiled_geom(dims, n_relu, G);
   if (rc != VC_OK) return rc;
@@ -2572,13 +2619,15 @@ extern "C" int vc_mlp_crown_rows(const int32_t* dims, int n_relu, const float* f
   // the mask pass: persistent, 8 domains per workgroup per sweep
   const dim3 gmask((unsigned)std::max<int64_t>(1, std::min<int64_t>((B + 7) / 8, (int64_t)cus * 8)));
   if (do_crown) {
-    hipLaunchKernelGGL(k_rows_union, dim3(1), dim3(64), 0, st, G, idx_all, idx_meta, w.umask);
-    if (n_relu <= 8)
-      hipLaunchKernelGGL(k_rows_mask<8>, gmask, bdom, 0, st, G, B, rl, per_domain,
-                         idx_all ? 0 : 1, w.masks, w.umask);
-    else
-      hipLaunchKernelGGL(k_rows_mask<MAXL>, gmask, bdom, 0, st, G, B, rl, per_domain,
-                         idx_all ? 0 : 1, w.masks, w.umask);
+    if (!premasked) {
+      hipLaunchKernelGGL(k_rows_union, dim3(1), dim3(64), 0, st, G, idx_all, idx_meta, w.umask);
+      if (n_relu <= 8)
+        hipLaunchKernelGGL(k_rows_mask<8>, gmask, bdom, 0, st, G, B, rl, per_domain,
+                           idx_all ? 0 : 1, w.masks, w.umask);
+      else
+        hipLaunchKernelGGL(k_rows_mask<MAXL>, gmask, bdom, 0, st, G, B, rl, per_domain,
+                           idx_all ? 0 : 1, w.masks, w.umask);
+    }
     hipLaunchKernelGGL(k_rows_scan1, dim3((unsigned)nblk, (unsigned)n_relu), dim3(RSCAN), 0, st,
                        w.masks, w.umask, B, w.off, w.bsum, nblk);
     hipLaunchKernelGGL(k_rows_scan2, dim3((unsigned)n_relu), dim3(1024), 0, st, w.bsum, nblk,
@@ -2608,6 +2657,22 @@ extern "C" int vc_mlp_crown_rows(const int32_t* dims, int n_relu, const float* f
     if (hipLaunchKernel(fs, gchain, bchain, args, lds, st) != hipSuccess) return VC_ERR_LAUNCH;
   }
   return VC_OK;
+}
+
+}  // namespace
+
+extern "C" int vc_mlp_crown_rows(const int32_t* dims, int n_relu, const float* frag,
+                                 const float* bias_cat, int64_t B, const float* xl,
+                                 const float* xh, const float* const* lo_in,
+                                 const float* const* hi_in, float* const* lo_out,
+                                 float* const* hi_out, const int32_t* idx_all,
+                                 const int32_t* idx_meta, int do_crown, int per_domain, int Q,
+                                 const float* spec_rows, const float* spec_acc, float* lb_out,
+                                 float* A_out, float* acc_out, uint64_t* seed_rows, void* work,
+                                 int64_t work_bytes, vc_stream_t stream) {
+  return crown_rows_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_in, hi_in, lo_out, hi_out,
+                        idx_all, idx_meta, do_crown, per_domain, Q, spec_rows, spec_acc, lb_out,
+                        A_out, acc_out, seed_rows, work, work_bytes, false, stream);
 }
 
 // ------------------------------------------- CROWN without allocation
@@ -2903,11 +2968,11 @@ extern "C" int vc_mlp_tiled_alpha_run(const int32_t* dims, int n_relu, const flo
   return VC_OK;
 }
 
-extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const float* frag,
-                                        const float* bias_cat, int64_t B, const float* xl,
-                                        const float* xh, float* const* lo_out,
-                                        float* const* hi_out, uint8_t* overflow,
-                                        int32_t* queue, vc_stream_t stream) {
+namespace {
+int zono_bounds_run(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+                    int64_t B, const float* xl, const float* xh, float* const* lo_out,
+                    float* const* hi_out, uint8_t* overflow, int32_t* queue, ZonoMasks zm,
+                    vc_stream_t stream) {
   TGeom G;
   int rc = tiled_geom(dims, n_relu, G);
   if (rc != VC_OK) return rc;
@@ -2920,7 +2985,9 @@ extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const f
     za.hi[l] = l < n_relu ? hi_out[l] : nullptr;
     if (l < n_relu && (!za.lo[l] || !za.hi[l])) return VC_ERR_ARG;
   }
-  const size_t base = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float);
+  // the kernel's static LDS (the mask pass's union staging) comes first
+  const size_t base = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float) +
+                      sizeof(unsigned long long) * (ZNW + 1) * MAXL;
   const size_t scr = (size_t)ZSCR * sizeof(float);
   if (base + scr > 160 * 1024) return VC_ERR_UNSUPPORTED;
   const int nw = (int)std::min<size_t>(ZNW, (160 * 1024 - base) / scr);
@@ -2943,8 +3010,8 @@ extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const f
   case V:                                                                                    \
     hipLaunchKernelGGL((k_zono_tiled<kVariants[V].MT, kVariants[V].KS,                       \
                                      kVariants[V].brow != 0>),                               \
-                       grid, block, lds, st, G, frag, bias_cat, B, xl, xh, za, overflow,     \
-                       queue);                                                               \
+                       grid, block, lds - sizeof(unsigned long long) * (ZNW + 1) * MAXL, st, \
+                       G, frag, bias_cat, B, xl, xh, za, overflow, queue, zm);               \
     break;
   switch (G.variant) {
     VC_TZONO_CASE(0)
@@ -2960,12 +3027,10 @@ extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const f
   return VC_OK;
 }
 
-extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const float* frag,
-                                      const float* bias_cat, int64_t B, const float* xl,
-                                      const float* xh, float* const* lo_out,
-                                      float* const* hi_out, uint8_t* overflow,
-                                      const int64_t* list, const int64_t* n_list,
-                                      vc_stream_t stream) {
+int zono_wide_run(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+                  int64_t B, const float* xl, const float* xh, float* const* lo_out,
+                  float* const* hi_out, uint8_t* overflow, const int64_t* list,
+                  const int64_t* n_list, ZonoMasks zm, vc_stream_t stream) {
   TGeom G;
   int rc = tiled_geom(dims, n_relu, G);
   if (rc != VC_OK) return rc;
@@ -3002,7 +3067,7 @@ extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const flo
     hipLaunchKernelGGL((k_zono_wide_tiled<kVariants[V].MT, kVariants[V].KS,                  \
                                           kVariants[V].brow != 0>),                          \
                        dim3((unsigned)gw), dim3(ZWW * 64), lds, st, G, frag, bias_cat, B, xl, \
-                       xh, za, overflow, list, n_list);                                      \
+                       xh, za, overflow, list, n_list, zm);                                  \
     break;
   switch (G.variant) {
     VC_TWIDE_CASE(0)
@@ -3017,3 +3082,81 @@ extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const flo
   VC_LAUNCH_CHECK();
   return VC_OK;
 }
+}  // namespace
+
+extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const float* frag,
+                                        const float* bias_cat, int64_t B, const float* xl,
+                                        const float* xh, float* const* lo_out,
+                                        float* const* hi_out, uint8_t* overflow,
+                                        int32_t* queue, vc_stream_t stream) {
+  return zono_bounds_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow,
+                         queue, ZonoMasks{nullptr, nullptr}, stream);
+}
+
+extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const float* frag,
+                                      const float* bias_cat, int64_t B, const float* xl,
+                                      const float* xh, float* const* lo_out,
+                                      float* const* hi_out, uint8_t* overflow,
+                                      const int64_t* list, const int64_t* n_list,
+                                      vc_stream_t stream) {
+  return zono_wide_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow, list,
+                       n_list, ZonoMasks{nullptr, nullptr}, stream);
+}
+
+// ------------------------------------- the round's masked bound phase
+namespace vcm {
+
+namespace {
+// The seed masks and the union slots inside a vc_mlp_crown_rows workspace
+// for B domains (rows_carve's first two regions).
+bool rows_mask_slots(const int32_t* dims, int n_relu, int64_t B, void* rows_work,
+                     ZonoMasks& zm) {
+  TGeom G;
+  if (!rows_work || tiled_geom(dims, n_relu, G) != VC_OK) return false;
+  int maxw = 1;
+  for (int l = 1; l <= n_relu; ++l) maxw = G.d[l] > maxw ? G.d[l] : maxw;
+  const RowsWork w = rows_carve(reinterpret_cast<char*>(rows_work), n_relu, maxw, B);
+  zm.masks = w.masks;
+  zm.umask = w.umask;
+  return true;
+}
+}  // namespace
+
+int zono_bounds_masked(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+                       int64_t B, const float* xl, const float* xh, float* const* lo_out,
+                       float* const* hi_out, uint8_t* overflow, int32_t* queue, void* rows_work,
+                       hipStream_t st) {
+  ZonoMasks zm{nullptr, nullptr};
+  if (!rows_mask_slots(dims, n_relu, B, rows_work, zm)) return VC_ERR_ARG;
+  TGeom G;
+  const int rc = tiled_geom(dims, n_relu, G);
+  if (rc != VC_OK) return rc;
+  // the union starts empty (k_rows_union without index lists clears it)
+  hipLaunchKernelGGL(k_rows_union, dim3(1), dim3(64), 0, st, G, nullptr, nullptr, zm.umask);
+  VC_LAUNCH_CHECK();
+  return zono_bounds_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow,
+                         queue, zm, st);
+}
+
+int zono_wide_masked(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+                     int64_t B, const float* xl, const float* xh, float* const* lo_out,
+                     float* const* hi_out, uint8_t* overflow, const int64_t* list,
+                     const int64_t* n_list, void* rows_work, hipStream_t st) {
+  ZonoMasks zm{nullptr, nullptr};
+  if (!rows_mask_slots(dims, n_relu, B, rows_work, zm)) return VC_ERR_ARG;
+  return zono_wide_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow, list,
+                       n_list, zm, st);
+}
+
+int crown_rows_premasked(const int32_t* dims, int n_relu, const float* frag,
+                         const float* bias_cat, int64_t B, const float* xl, const float* xh,
+                         const float* const* lo_in, const float* const* hi_in, int Q,
+                         const float* spec_rows, const float* spec_acc, float* lb_out,
+                         float* A_out, float* acc_out, uint64_t* seed_rows, void* work,
+                         int64_t work_bytes, hipStream_t st) {
+  return crown_rows_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_in, hi_in, nullptr, nullptr,
+                        nullptr, nullptr, 1, 1, Q, spec_rows, spec_acc, lb_out, A_out, acc_out,
+                        seed_rows, work, work_bytes, true, (vc_stream_t)st);
+}
+
+}  // namespace vcm
