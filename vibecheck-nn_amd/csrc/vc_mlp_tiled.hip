@@ -1290,7 +1290,11 @@ const void* alpha_fn() {
 // constant 1 in the centre column at the bias row.
 constexpr int ZNW = 8;  // waves per workgroup (fewer when the LDS scratch does not fit)
 constexpr int ZT = 8;   // column tiles per wave: 128 columns, centre included
-constexpr int ZSCR = 20 * FW;  // relu scratch floats per wave
+// The |G| partials' rows are ZPS floats apart: lane (g, r) writes row r at
+// column 16 t + 4 g, so a row stride of FW would put the 16 rows of a
+// quarter-wave on the same four banks; FW + 4 spreads them over all 64.
+constexpr int ZPS = FW + 4;
+constexpr int ZSCR = 16 * ZPS + 4 * FW;  // relu scratch floats per wave
 
 struct TZonoArgs {
   float* lo[MAXL];
@@ -1376,10 +1380,10 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
   __syncthreads();
   const float* fr0 = sfrag;
   const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
-  // this wave's relu scratch: |G| partials [16 lanes][FW], centre, lambda,
+  // this wave's relu scratch: |G| partials [16 lanes][ZPS], centre, lambda,
   // mu, new-column index [FW] each
   float* zpart = sbias + n * FW + wv * ZSCR;
-  float* zcen = zpart + 16 * FW;
+  float* zcen = zpart + 16 * ZPS;
   float* zlam = zcen + FW;
   float* zmu = zlam + FW;
   int* zcol = reinterpret_cast<int*>(zmu + FW);
@@ -1483,7 +1487,7 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
           }
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-          *reinterpret_cast<float4*>(zpart + r * FW + 16 * t + 4 * g) =
+          *reinterpret_cast<float4*>(zpart + r * ZPS + 16 * t + 4 * g) =
               make_float4(ps[t][0], ps[t][1], ps[t][2], ps[t][3]);
           if (r == 0)
             *reinterpret_cast<float4*>(zcen + 16 * t + 4 * g) =
@@ -1494,7 +1498,7 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
       const int j = lane;
       double sd = 0.0;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) sd += (double)zpart[q * FW + j];
+      for (int q = 0; q < 16; ++q) sd += (double)zpart[q * ZPS + j];
       const float rad = (float)sd;
       const float c = zcen[j];
       const float lo = c - rad, hi = c + rad;
