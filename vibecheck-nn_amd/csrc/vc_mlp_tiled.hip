@@ -683,7 +683,8 @@ __device__ __forceinline__ void set_elem(v4f (&X)[4], int j, int g, float v) {
 // independent accumulators, interleaved.
 template <int MT, int KS, int NX, int NT>
 __device__ __forceinline__ void fc_forward(const float4* fr, int lane, int g, int r,
-                                           const v4f (&X)[NT][4], int x0, v4f (&out)[NX][4]) {
+                                           const v4f (&X)[NT][4], int x0, v4f (&out)[NX][4],
+                                           int kmax = 1 << 30) {
 #pragma unroll
   for (int x = 0; x < NX; ++x)
 #pragma unroll
@@ -702,12 +703,16 @@ __device__ __forceinline__ void fc_forward(const float4* fr, int lane, int g, in
       a[mo][3] = q.w;
     }
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+    for (int t = 0; t < MT; ++t) {
+      // K-step (t, i) contracts inputs 16 t + 4 g + i: past the last live
+      // one (kmax, the bias row included) every product is zero
+      if (t == MT - 1 && 16 * t + i >= kmax) continue;
 #pragma unroll
       for (int mo = 0; mo < MT; ++mo)
 #pragma unroll
         for (int x = 0; x < NX; ++x)
           out[x][mo] = mfma16x16x4(a[mo][t], X[x0 + x][t][i], out[x][mo]);
+    }
   }
 }
 
@@ -1219,7 +1224,12 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
                                      : float4{0.f, 0.f, 0.f, 0.f};
           const float a[4] = {q4.x, q4.y, q4.z, q4.w};
 #pragma unroll
-          for (int t = 0; t < MT; ++t) o = mfma16x16x4(a[t], X[t][i], o);
+          for (int t = 0; t < MT; ++t) {
+            // inputs 16 t + 4 g + i past the last live one (bias row
+            // included) contribute zeros
+            if (t == MT - 1 && 16 * t + i >= dW + (BROW ? 1 : 0)) continue;
+            o = mfma16x16x4(a[t], X[t][i], o);
+          }
         }
         GEw = o;
       }
@@ -1442,7 +1452,7 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
         for (int nt0 = 0; nt0 < ZT; nt0 += 2) {
           if (16 * (nt0 + 1) < Kc) {
             v4f o[2][4];
-            fc_forward<MT, KS, 2, ZT>(fr, lane, g, r, Z, nt0, o);
+            fc_forward<MT, KS, 2, ZT>(fr, lane, g, r, Z, nt0, o, G.d[l] + (BROW ? 1 : 0));
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
               Z[nt0][mt] = o[0][mt];
@@ -1451,7 +1461,7 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
           } else if (16 * nt0 < Kc) {
             // tile nt0 + 1 holds no generator (zeros stay zeros)
             v4f o[1][4];
-            fc_forward<MT, KS, 1, ZT>(fr, lane, g, r, Z, nt0, o);
+            fc_forward<MT, KS, 1, ZT>(fr, lane, g, r, Z, nt0, o, G.d[l] + (BROW ? 1 : 0));
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) Z[nt0][mt] = o[0][mt];
           }
@@ -1664,7 +1674,7 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
           for (int q0 = 0; q0 < ZWT; q0 += 2) {
             if (16 * (ZWW * (q0 + 1) + wv) < Kc) {
               v4f o[2][4];
-              fc_forward<MT, KS, 2, ZWT>(fr, lane, g, r, Z, q0, o);
+              fc_forward<MT, KS, 2, ZWT>(fr, lane, g, r, Z, q0, o, G.d[l] + (BROW ? 1 : 0));
 #pragma unroll
               for (int mt = 0; mt < 4; ++mt) {
                 Z[q0][mt] = o[0][mt];
@@ -1672,7 +1682,7 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
               }
             } else if (16 * (ZWW * q0 + wv) < Kc) {
               v4f o[1][4];
-              fc_forward<MT, KS, 1, ZWT>(fr, lane, g, r, Z, q0, o);
+              fc_forward<MT, KS, 1, ZWT>(fr, lane, g, r, Z, q0, o, G.d[l] + (BROW ? 1 : 0));
 #pragma unroll
               for (int mt = 0; mt < 4; ++mt) Z[q0][mt] = o[0][mt];
             }
