@@ -52,10 +52,13 @@ __device__ __forceinline__ int64_t queue_bcast(int t) { return (int64_t)__shfl(t
 // (vc_mlp_tiled.hip): rows_work is the vc_mlp_crown_rows workspace of the
 // same B that crown_rows_premasked then runs in (per_domain, no index
 // lists, no CROWN bounds out), skipping its own pass over the bounds.
+// ovf_list / ovf_count (nullable together): the domains the one-wavefront
+// pass leaves to the wide pass, appended in no particular order, and their
+// count (the wide pass's list, with no compaction of the flags).
 int zono_bounds_masked(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
                        int64_t B, const float* xl, const float* xh, float* const* lo_out,
                        float* const* hi_out, uint8_t* overflow, int32_t* queue, void* rows_work,
-                       hipStream_t st);
+                       int64_t* ovf_list, int64_t* ovf_count, hipStream_t st);
 int zono_wide_masked(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
                      int64_t B, const float* xl, const float* xh, float* const* lo_out,
                      float* const* hi_out, uint8_t* overflow, const int64_t* list,

@@ -1315,9 +1315,15 @@ struct TZonoArgs {
 // k_rows_mask over the same bounds): per layer and domain the seed filter
 // lo < 0, hi > -1e-7 as a mask ([n][B]), and the union of the unstable sets
 // (lo < 0 < hi) ORed into umask[n], which the caller clears.
+// With ovf_list, the one-wavefront pass also appends every domain it
+// leaves to the wide pass to ovf_list (in no particular order: the wide pass
+// takes each domain on its own) and counts them in *ovf_count, which the
+// caller clears; the wide pass then needs no compaction of the flags.
 struct ZonoMasks {
   uint64_t* masks;
   unsigned long long* umask;
+  int64_t* ovf_list;
+  unsigned long long* ovf_count;
 };
 
 // fc_0 on the input block for NP column tiles, tile p starting at column
@@ -1562,7 +1568,10 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
         }
       Kc += cnt;
     }
-    if (lane == 0) overflow[dom] = ovf ? 1 : 0;
+    if (lane == 0) {
+      overflow[dom] = ovf ? 1 : 0;
+      if (ovf && zm.ovf_list) zm.ovf_list[atomicAdd(zm.ovf_count, 1ull)] = dom;
+    }
     // an overflowing domain's sets come from the wide pass, over its bounds
     if (zm.masks && !ovf && lane < n) atomicOr(&s_wun[lane], s_dun[wv][lane]);
     dom = (queue && B > nwaves) ? nwaves + vcm::queue_bcast(tnext) : dom + nwaves;
@@ -3104,7 +3113,7 @@ extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const f
                                         float* const* hi_out, uint8_t* overflow,
                                         int32_t* queue, vc_stream_t stream) {
   return zono_bounds_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow,
-                         queue, ZonoMasks{nullptr, nullptr}, stream);
+                         queue, ZonoMasks{nullptr, nullptr, nullptr, nullptr}, stream);
 }
 
 extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const float* frag,
@@ -3114,13 +3123,18 @@ extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const flo
                                       const int64_t* list, const int64_t* n_list,
                                       vc_stream_t stream) {
   return zono_wide_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow, list,
-                       n_list, ZonoMasks{nullptr, nullptr}, stream);
+                       n_list, ZonoMasks{nullptr, nullptr, nullptr, nullptr}, stream);
 }
 
 // ------------------------------------- the round's masked bound phase
 namespace vcm {
 
 namespace {
+__global__ void k_masked_init(unsigned long long* umask, int n, unsigned long long* cnt) {
+  if (threadIdx.x < n) umask[threadIdx.x] = 0ull;
+  if (threadIdx.x == 0 && cnt) *cnt = 0ull;
+}
+
 // The seed masks and the union slots inside a vc_mlp_crown_rows workspace
 // for B domains (rows_carve's first two regions).
 bool rows_mask_slots(const int32_t* dims, int n_relu, int64_t B, void* rows_work,
@@ -3139,14 +3153,14 @@ bool rows_mask_slots(const int32_t* dims, int n_relu, int64_t B, void* rows_work
 int zono_bounds_masked(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
                        int64_t B, const float* xl, const float* xh, float* const* lo_out,
                        float* const* hi_out, uint8_t* overflow, int32_t* queue, void* rows_work,
-                       hipStream_t st) {
-  ZonoMasks zm{nullptr, nullptr};
+                       int64_t* ovf_list, int64_t* ovf_count, hipStream_t st) {
+  ZonoMasks zm{nullptr, nullptr, nullptr, nullptr};
   if (!rows_mask_slots(dims, n_relu, B, rows_work, zm)) return VC_ERR_ARG;
-  TGeom G;
-  const int rc = tiled_geom(dims, n_relu, G);
-  if (rc != VC_OK) return rc;
-  // the union starts empty (k_rows_union without index lists clears it)
-  hipLaunchKernelGGL(k_rows_union, dim3(1), dim3(64), 0, st, G, nullptr, nullptr, zm.umask);
+  if ((ovf_list == nullptr) != (ovf_count == nullptr) || n_relu > MAXL) return VC_ERR_ARG;
+  zm.ovf_list = ovf_list;
+  zm.ovf_count = reinterpret_cast<unsigned long long*>(ovf_count);
+  // the union starts empty, and so does the overflow list
+  hipLaunchKernelGGL(k_masked_init, dim3(1), dim3(64), 0, st, zm.umask, n_relu, zm.ovf_count);
   VC_LAUNCH_CHECK();
   return zono_bounds_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow,
                          queue, zm, st);
@@ -3156,7 +3170,7 @@ int zono_wide_masked(const int32_t* dims, int n_relu, const float* frag, const f
                      int64_t B, const float* xl, const float* xh, float* const* lo_out,
                      float* const* hi_out, uint8_t* overflow, const int64_t* list,
                      const int64_t* n_list, void* rows_work, hipStream_t st) {
-  ZonoMasks zm{nullptr, nullptr};
+  ZonoMasks zm{nullptr, nullptr, nullptr, nullptr};
   if (!rows_mask_slots(dims, n_relu, B, rows_work, zm)) return VC_ERR_ARG;
   return zono_wide_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow, list,
                        n_list, zm, st);
