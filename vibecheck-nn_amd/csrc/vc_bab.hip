@@ -217,9 +217,8 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
     VC_TRY(vcm::zono_bounds_masked(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
                                    r.queue + 1, r.rws, r.idx, r.cnt, st));
   } else {
-    VC_TRY(vc_mlp_tiled_zono_bounds(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi,
-                                    r.ovf, r.queue + 1, stream));
-    VC_TRY(vc_compact(r.ovf, B, 0, r.idx, r.cnt, r.cws, r.cws_bytes, stream));
+    VC_TRY(vcm::zono_bounds_listed(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
+                                   r.queue + 1, r.idx, r.cnt, st));
   }
   if (r.rws) {
     VC_TRY(vcm::zono_wide_masked(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,

@@ -59,6 +59,11 @@ int zono_bounds_masked(const int32_t* dims, int n_relu, const float* frag, const
                        int64_t B, const float* xl, const float* xh, float* const* lo_out,
                        float* const* hi_out, uint8_t* overflow, int32_t* queue, void* rows_work,
                        int64_t* ovf_list, int64_t* ovf_count, hipStream_t st);
+// The one-wavefront zonotope pass with only the overflow list.
+int zono_bounds_listed(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+                       int64_t B, const float* xl, const float* xh, float* const* lo_out,
+                       float* const* hi_out, uint8_t* overflow, int32_t* queue,
+                       int64_t* ovf_list, int64_t* ovf_count, hipStream_t st);
 int zono_wide_masked(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
                      int64_t B, const float* xl, const float* xh, float* const* lo_out,
                      float* const* hi_out, uint8_t* overflow, const int64_t* list,

@@ -36,6 +36,15 @@ __global__ void k_queue_reset(int* q) {
   if (threadIdx.x == 0) *q = 0;
 }
 
+// k_queue_reset for the zonotope pass, which also clears the union of
+// unstable sets (umask[n], nullable) and the overflow count (nullable) that
+// it accumulates.
+__global__ void k_zono_init(int* q, unsigned long long* umask, int n, unsigned long long* cnt) {
+  if (threadIdx.x == 0 && q) *q = 0;
+  if (umask && threadIdx.x < n) umask[threadIdx.x] = 0ull;
+  if (threadIdx.x == 0 && cnt) *cnt = 0ull;
+}
+
 constexpr int TNW = 12;  // waves per workgroup, one domain each (3 per SIMD)
 constexpr int TNP = 1;   // 16-row N-tiles chained together per wave
 constexpr int TQMAX = 64;  // spec rows per call (taken 16 at a time)
@@ -3028,7 +3037,9 @@ int zono_bounds_run(const int32_t* dims, int n_relu, const float* frag, const fl
   if (!vcm::allow_max_lds(fn)) return VC_ERR_UNSUPPORTED;
   const dim3 grid(vcm::persistent_grid(B, lds, nw)), block(nw * 64);
   hipStream_t st = (hipStream_t)stream;
-  if (queue) hipLaunchKernelGGL(k_queue_reset, dim3(1), dim3(64), 0, st, queue);
+  if (queue || zm.umask || zm.ovf_count)
+    hipLaunchKernelGGL(k_zono_init, dim3(1), dim3(64), 0, st, queue, zm.umask, n_relu,
+                       zm.ovf_count);
 #define VC_TZONO_CASE(V)                                                                     \
   case V:                                                                                    \
     hipLaunchKernelGGL((k_zono_tiled<kVariants[V].MT, kVariants[V].KS,                       \
@@ -3130,11 +3141,6 @@ extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const flo
 namespace vcm {
 
 namespace {
-__global__ void k_masked_init(unsigned long long* umask, int n, unsigned long long* cnt) {
-  if (threadIdx.x < n) umask[threadIdx.x] = 0ull;
-  if (threadIdx.x == 0 && cnt) *cnt = 0ull;
-}
-
 // The seed masks and the union slots inside a vc_mlp_crown_rows workspace
 // for B domains (rows_carve's first two regions).
 bool rows_mask_slots(const int32_t* dims, int n_relu, int64_t B, void* rows_work,
@@ -3159,9 +3165,16 @@ int zono_bounds_masked(const int32_t* dims, int n_relu, const float* frag, const
   if ((ovf_list == nullptr) != (ovf_count == nullptr) || n_relu > MAXL) return VC_ERR_ARG;
   zm.ovf_list = ovf_list;
   zm.ovf_count = reinterpret_cast<unsigned long long*>(ovf_count);
-  // the union starts empty, and so does the overflow list
-  hipLaunchKernelGGL(k_masked_init, dim3(1), dim3(64), 0, st, zm.umask, n_relu, zm.ovf_count);
-  VC_LAUNCH_CHECK();
+  return zono_bounds_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow,
+                         queue, zm, st);
+}
+
+int zono_bounds_listed(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+                       int64_t B, const float* xl, const float* xh, float* const* lo_out,
+                       float* const* hi_out, uint8_t* overflow, int32_t* queue,
+                       int64_t* ovf_list, int64_t* ovf_count, hipStream_t st) {
+  if (!ovf_list || !ovf_count) return VC_ERR_ARG;
+  ZonoMasks zm{nullptr, nullptr, ovf_list, reinterpret_cast<unsigned long long*>(ovf_count)};
   return zono_bounds_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow,
                          queue, zm, st);
 }
