@@ -1017,16 +1017,18 @@ def test_split_and_compaction_bit_exact(gpu):
     assert torch.equal(cpu(vg._closure(lb.to(gpu), tab)), rbab.closure(lb, {0: [0, 1, 2, 3]}))
 
 
-@pytest.mark.parametrize('alpha_iters', [0, 20])
-def test_bab_round_native_matches_python_round(gpu, alpha_iters):
+@pytest.mark.parametrize('B,alpha_iters', [(4096, 0), (4096, 20), (600, 20)])
+def test_bab_round_native_matches_python_round(gpu, B, alpha_iters):
     """The round as one native call (vc_mlp_bab_round) runs the same entry
     points in the same order as bab_step's Python round: every output equal
     bit for bit, every count equal.  The native round takes the CROWN rows
     pass's seed masks and union from its zonotope passes, the Python round
-    computes them in the rows pass (k_rows_mask); the batch has domains that
-    overflow the one-wavefront zonotope pass, whose masks the wide pass
-    writes."""
-    gg_c, gg_g, xl, xh = acas(gpu, 4096, seed=23, scale=2.0)
+    computes them in the rows pass (k_rows_mask); at 600 boxes (the
+    small-batch CROWN) the native round takes the union from the zonotope
+    passes, the Python round from vc_unstable_union_layers.  The batches
+    have domains that overflow the one-wavefront zonotope pass, whose masks
+    and sets the wide pass provides."""
+    gg_c, gg_g, xl, xh = acas(gpu, B, seed=23, scale=2.0)
     # generator columns per domain at the last append (oracle bounds):
     # 1 + inputs + unstable neurons of every relu but the last
     sb, _ = rb.zono_forward_batched(xl, xh, gg_c)

@@ -48,9 +48,9 @@ struct RoundBufs {
   int64_t* cnt;                      // counts [4]
   void* cws;                         // compaction workspace
   int64_t cws_bytes;
-  uint8_t* uflags;                   // union flags (sum d)
   int32_t* uidx;                     // union lists (sum d)
   int32_t* umeta;                    // union counts and offsets (2 n)
+  unsigned long long* umask;         // union as bit masks [MAXL]
   int32_t* queue;                    // work counters [2]
   void* rws;                         // layer-synchronous CROWN workspace (large B)
   int64_t rws_bytes;
@@ -86,9 +86,9 @@ void carve(Carve& c, RoundBufs& r, const int32_t* dims, int n, int64_t B, int Q)
   r.cnt = c.take<int64_t>(4);
   r.cws_bytes = vc_compact_workspace(B);
   r.cws = c.take<char>(r.cws_bytes);
-  r.uflags = c.take<uint8_t>(sumd);
   r.uidx = c.take<int32_t>(sumd);
   r.umeta = c.take<int32_t>(2 * n);
+  r.umask = c.take<unsigned long long>(MAXL);
   r.queue = c.take<int32_t>(2);
   r.rws = r.rws_bytes > 0 ? c.take<char>(r.rws_bytes) : nullptr;
   r.a_xl = c.take<float>(B * n_in);
@@ -205,32 +205,23 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
   Carve c{reinterpret_cast<char*>(work), 0};
   RoundBufs r;
   carve(c, r, dims, n, B, Q);
-  int32_t widths[MAXL];
-  for (int l = 0; l < n; ++l) widths[l] = dims[l + 1];
 
   // ---- bound phase: zonotope, union of the unstable neurons, CROWN + spec.
-  // For the rows form the zonotope passes also leave its per-domain seed
-  // masks and the union in its workspace (same bounds, no second pass over
-  // them).
+  // The zonotope passes leave the union of the unstable sets (same bounds,
+  // no second pass over them), and for the rows form its per-domain seed
+  // masks in its workspace; the one-wavefront pass lists its overflowing
+  // domains itself.
   if (r.rws) {
-    // the one-wavefront pass lists its overflowing domains itself
     VC_TRY(vcm::zono_bounds_masked(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
                                    r.queue + 1, r.rws, r.idx, r.cnt, st));
-  } else {
-    VC_TRY(vcm::zono_bounds_listed(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
-                                   r.queue + 1, r.idx, r.cnt, st));
-  }
-  if (r.rws) {
     VC_TRY(vcm::zono_wide_masked(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
                                  r.idx, r.cnt, r.rws, st));
   } else {
-    VC_TRY(vc_mlp_tiled_zono_wide(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
-                                  r.idx, r.cnt, stream));
-  }
-  // the rows form builds the union in its own pass over the bounds
-  if (!r.rws) {
-    VC_TRY(vc_unstable_union_layers(r.sb_lo, r.sb_hi, widths, n, B, r.uflags, stream));
-    VC_TRY(vc_union_compact(r.uflags, widths, n, r.uidx, r.umeta, stream));
+    VC_TRY(vcm::zono_bounds_listed(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
+                                   r.queue + 1, r.idx, r.cnt, r.umask, st));
+    VC_TRY(vcm::zono_wide_union(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
+                                r.idx, r.cnt, r.umask, st));
+    VC_TRY(vcm::union_lists(dims, n, r.umask, r.uidx, r.umeta, st));
   }
   if (crown_ev0 && hipEventRecord((hipEvent_t)crown_ev0, st) != hipSuccess) return VC_ERR_LAUNCH;
   // the round reads only the spec bound of the CROWN pass (alpha restarts

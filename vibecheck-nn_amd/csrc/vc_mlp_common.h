@@ -59,11 +59,20 @@ int zono_bounds_masked(const int32_t* dims, int n_relu, const float* frag, const
                        int64_t B, const float* xl, const float* xh, float* const* lo_out,
                        float* const* hi_out, uint8_t* overflow, int32_t* queue, void* rows_work,
                        int64_t* ovf_list, int64_t* ovf_count, hipStream_t st);
-// The one-wavefront zonotope pass with only the overflow list.
+// The zonotope passes with the overflow list and (umask, nullable) the
+// union of the unstable sets as bit masks [n_relu], without seed masks; and
+// union_lists: vc_union_compact's index lists from that union.
 int zono_bounds_listed(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
                        int64_t B, const float* xl, const float* xh, float* const* lo_out,
                        float* const* hi_out, uint8_t* overflow, int32_t* queue,
-                       int64_t* ovf_list, int64_t* ovf_count, hipStream_t st);
+                       int64_t* ovf_list, int64_t* ovf_count, unsigned long long* umask,
+                       hipStream_t st);
+int zono_wide_union(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+                    int64_t B, const float* xl, const float* xh, float* const* lo_out,
+                    float* const* hi_out, uint8_t* overflow, const int64_t* list,
+                    const int64_t* n_list, unsigned long long* umask, hipStream_t st);
+int union_lists(const int32_t* dims, int n_relu, const unsigned long long* umask, int32_t* idx,
+                int32_t* meta, hipStream_t st);
 int zono_wide_masked(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
                      int64_t B, const float* xl, const float* xh, float* const* lo_out,
                      float* const* hi_out, uint8_t* overflow, const int64_t* list,

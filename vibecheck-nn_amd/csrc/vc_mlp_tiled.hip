@@ -1320,10 +1320,11 @@ struct TZonoArgs {
   float* hi[MAXL];
 };
 
-// Optional outputs of the zonotope passes for the CROWN rows pass (its
-// k_rows_mask over the same bounds): per layer and domain the seed filter
-// lo < 0, hi > -1e-7 as a mask ([n][B]), and the union of the unstable sets
-// (lo < 0 < hi) ORed into umask[n], which the caller clears.
+// Optional outputs of the zonotope passes for the CROWN passes (the rows
+// pass's k_rows_mask, the union of vc_unstable_union_layers, over the same
+// bounds): per layer and domain the seed filter lo < 0, hi > -1e-7 as a
+// mask ([n][B], masks), and the union of the unstable sets (lo < 0 < hi)
+// ORed into umask[n], which the one-wavefront pass's launch clears.
 // With ovf_list, the one-wavefront pass also appends every domain it
 // leaves to the wide pass to ovf_list (in no particular order: the wide pass
 // takes each domain on its own) and counts them in *ovf_count, which the
@@ -1537,13 +1538,11 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
       const uint64_t umask = __ballot(ust);
       if (zm.masks) {
         // the neurons the CROWN rows pass seeds for this domain (lo < 0,
-        // hi > -1e-7: the filter of k_rows_mask) and its unstable set
+        // hi > -1e-7: the filter of k_rows_mask)
         const uint64_t km = __ballot(valid && lo < 0.f && hi > -1e-7f);
-        if (lane == 0) {
-          zm.masks[(int64_t)l * B + dom] = km;
-          s_dun[wv][l] = umask;
-        }
+        if (lane == 0) zm.masks[(int64_t)l * B + dom] = km;
       }
+      if (zm.umask && lane == 0) s_dun[wv][l] = umask;  // its unstable set
       const int cnt = __popcll(umask);
       if (l == n - 1) break;  // the last relu's output is not propagated
       if (Kc + cnt > 16 * ZT) {
@@ -1582,10 +1581,10 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
       if (ovf && zm.ovf_list) zm.ovf_list[atomicAdd(zm.ovf_count, 1ull)] = dom;
     }
     // an overflowing domain's sets come from the wide pass, over its bounds
-    if (zm.masks && !ovf && lane < n) atomicOr(&s_wun[lane], s_dun[wv][lane]);
+    if (zm.umask && !ovf && lane < n) atomicOr(&s_wun[lane], s_dun[wv][lane]);
     dom = (queue && B > nwaves) ? nwaves + vcm::queue_bcast(tnext) : dom + nwaves;
   }
-  if (zm.masks) {
+  if (zm.umask) {
     __syncthreads();
     if (threadIdx.x < n && s_wun[threadIdx.x]) atomicOr(zm.umask + threadIdx.x, s_wun[threadIdx.x]);
   }
@@ -1754,11 +1753,9 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
           if (lane == 0) *sumask = um;
           if (zm.masks) {
             const uint64_t km = __ballot(valid && lo < 0.f && hi > -1e-7f);
-            if (lane == 0) {
-              zm.masks[(int64_t)l * B + dom] = km;
-              s_wun[l] |= um;
-            }
+            if (lane == 0) zm.masks[(int64_t)l * B + dom] = km;
           }
+          if (zm.umask && lane == 0) s_wun[l] |= um;
         }
         __syncthreads();  // sred / scen are rewritten by the next layer after this
         const uint64_t umask = *sumask;
@@ -1803,7 +1800,7 @@ __global__ __launch_bounds__(ZWW * 64) void k_zono_wide_tiled(
       if (threadIdx.x == 0) overflow[dom] = ovf ? 1 : 0;
     }
   }
-  if (zm.masks) {
+  if (zm.umask) {
     __syncthreads();
     if (threadIdx.x < n && s_wun[threadIdx.x]) atomicOr(zm.umask + threadIdx.x, s_wun[threadIdx.x]);
   }
@@ -3172,11 +3169,49 @@ int zono_bounds_masked(const int32_t* dims, int n_relu, const float* frag, const
 int zono_bounds_listed(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
                        int64_t B, const float* xl, const float* xh, float* const* lo_out,
                        float* const* hi_out, uint8_t* overflow, int32_t* queue,
-                       int64_t* ovf_list, int64_t* ovf_count, hipStream_t st) {
-  if (!ovf_list || !ovf_count) return VC_ERR_ARG;
-  ZonoMasks zm{nullptr, nullptr, ovf_list, reinterpret_cast<unsigned long long*>(ovf_count)};
+                       int64_t* ovf_list, int64_t* ovf_count, unsigned long long* umask,
+                       hipStream_t st) {
+  if (!ovf_list || !ovf_count || n_relu > MAXL) return VC_ERR_ARG;
+  ZonoMasks zm{nullptr, umask, ovf_list, reinterpret_cast<unsigned long long*>(ovf_count)};
   return zono_bounds_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow,
                          queue, zm, st);
+}
+
+int zono_wide_union(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+                    int64_t B, const float* xl, const float* xh, float* const* lo_out,
+                    float* const* hi_out, uint8_t* overflow, const int64_t* list,
+                    const int64_t* n_list, unsigned long long* umask, hipStream_t st) {
+  return zono_wide_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow, list,
+                       n_list, ZonoMasks{nullptr, umask, nullptr, nullptr}, st);
+}
+
+namespace {
+// vc_union_compact's index lists from the union as bit masks: one
+// wavefront per layer, ascending neuron order.
+__global__ void k_union_lists(const unsigned long long* __restrict__ umask, TGeom G,
+                              int32_t* __restrict__ idx, int32_t* __restrict__ meta) {
+  const int L = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = G.n;
+  if (L >= n) return;
+  int off = 0;
+  for (int k = 0; k < L; ++k) off += __popcll(umask[k]);
+  const uint64_t m = umask[L];
+  if ((m >> lane) & 1ull) idx[off + __popcll(m & ((1ull << lane) - 1ull))] = lane;
+  if (lane == 0) {
+    meta[L] = __popcll(m);
+    meta[n + L] = off;
+  }
+}
+}  // namespace
+
+int union_lists(const int32_t* dims, int n_relu, const unsigned long long* umask, int32_t* idx,
+                int32_t* meta, hipStream_t st) {
+  TGeom G;
+  const int rc = tiled_geom(dims, n_relu, G);
+  if (rc != VC_OK) return rc;
+  hipLaunchKernelGGL(k_union_lists, dim3(1), dim3(64 * n_relu), 0, st, umask, G, idx, meta);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
 }
 
 int zono_wide_masked(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
