@@ -18,13 +18,6 @@ namespace {
 
 using vcm::MAXL;
 
-__global__ void k_and_u8(const uint8_t* __restrict__ a, const uint8_t* __restrict__ b, int64_t n,
-                         uint8_t* __restrict__ out) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    out[i] = (a[i] != 0 && b[i] != 0) ? 1 : 0;
-}
-
 // Bump allocation of the round's buffers from the caller's workspace (or,
 // with base == nullptr, the size of that layout).
 struct Carve {
@@ -113,33 +106,45 @@ __global__ void k_ctl_count(const float* __restrict__ ctl, int64_t* out) {
   if (threadIdx.x == 0) *out = (int64_t)ctl[2];
 }
 
-// Device counts to pinned host words, stored by the GPU (system scope).
-__global__ void k_counts_to_host(const int64_t* __restrict__ dev, int k, int64_t* host) {
+// Device counts to pinned host words, stored by the GPU (system scope);
+// with ctl, word k is the alpha loop's evaluated iterations (ctl[2]).
+__global__ void k_counts_to_host(const int64_t* __restrict__ dev, int k, int64_t* host,
+                                 const float* __restrict__ ctl) {
   if (threadIdx.x < k)
     __hip_atomic_store(host + threadIdx.x, dev[threadIdx.x], __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_SYSTEM);
+  if (ctl && threadIdx.x == k)
+    __hip_atomic_store(host + k, (int64_t)ctl[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // k counts from the device once every launch before them has run.  With
 // pinned host words the GPU stores them there and the host polls (no copy,
 // no wake-up latency); the poll is bounded, then the stream is synchronised
 // and the counts are read from device memory.
-int read_counts(const int64_t* dev, int k, int64_t* host, int64_t* pinned, hipStream_t st) {
+// With ctl, one more count follows the k: the alpha loop's evaluated
+// iterations (host[k]; dev[k] is then scratch for the fallback).
+int read_counts(const int64_t* dev, int k, int64_t* host, int64_t* pinned, hipStream_t st,
+                const float* ctl = nullptr) {
+  const int kk = ctl ? k + 1 : k;
   if (pinned) {
     volatile int64_t* pw = pinned;
-    for (int i = 0; i < k; ++i) pw[i] = -1;
-    hipLaunchKernelGGL(k_counts_to_host, dim3(1), dim3(64), 0, st, dev, k, pinned);
+    for (int i = 0; i < kk; ++i) pw[i] = -1;
+    hipLaunchKernelGGL(k_counts_to_host, dim3(1), dim3(64), 0, st, dev, k, pinned, ctl);
     if (hipGetLastError() != hipSuccess) return VC_ERR_LAUNCH;
     for (long spin = 0; spin < (1l << 26); ++spin) {
       bool ready = true;
-      for (int i = 0; i < k; ++i) ready = ready && pw[i] >= 0;
+      for (int i = 0; i < kk; ++i) ready = ready && pw[i] >= 0;
       if (ready) {
-        for (int i = 0; i < k; ++i) host[i] = pw[i];
+        for (int i = 0; i < kk; ++i) host[i] = pw[i];
         return VC_OK;
       }
     }
   }
-  if (hipMemcpyAsync(host, dev, sizeof(int64_t) * k, hipMemcpyDeviceToHost, st) != hipSuccess)
+  if (ctl) {
+    hipLaunchKernelGGL(k_ctl_count, dim3(1), dim3(64), 0, st, ctl, const_cast<int64_t*>(dev) + k);
+    if (hipGetLastError() != hipSuccess) return VC_ERR_LAUNCH;
+  }
+  if (hipMemcpyAsync(host, dev, sizeof(int64_t) * kk, hipMemcpyDeviceToHost, st) != hipSuccess)
     return VC_ERR_LAUNCH;
   return hipStreamSynchronize(st) == hipSuccess ? VC_OK : VC_ERR_LAUNCH;
 }
@@ -276,8 +281,9 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
                                     r.a_hi, alpha, m1, m2, Q, spec_rows, spec_acc, r.a_lb,
                                     r.a_best, 0.9, 0.999, 1e-8, alpha_lr, alpha_lr_decay,
                                     alpha_iters, alpha_early_stop, r.a_ctl, stop_host, stream));
-      VC_TRY(vc_scatter_max_rows(lb, r.idx, r.a_best, n_open, Q, stream));
-      VC_TRY(vc_closure(lb, B, Q, d_ptr, q_idx, n_disj, closed, stream));
+      // the open leaves are distinct rows (a compaction's output)
+      VC_TRY(vcm::scatter_max_close(lb, r.idx, r.a_best, n_open, Q, d_ptr, q_idx, n_disj, closed,
+                                    st));
     }
   }
 
@@ -285,10 +291,8 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
   VC_TRY(vc_compact(closed, B, 1, unclosed, r.cnt, r.cws, r.cws_bytes, stream));
   int64_t n_unc = 0;
   if (n_open > 0) {
-    hipLaunchKernelGGL(k_ctl_count, dim3(1), dim3(64), 0, st, r.a_ctl, r.cnt + 1);
-    VC_LAUNCH_CHECK();
     int64_t two[2];
-    VC_TRY(read_counts(r.cnt, 2, two, pinned, st));
+    VC_TRY(read_counts(r.cnt, 1, two, pinned, st, r.a_ctl));
     n_unc = two[0];
     n_eval = two[1];
   } else {
@@ -305,11 +309,9 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
     VC_TRY(vc_clip_box(r.u_xl, r.u_xh, r.u_A, r.u_acc, n_unc, Q, n_in, d_ptr, q_idx, n_disj,
                        r.c_xl, r.c_xh, feasible, stream));
     VC_TRY(vc_widest_axis(r.c_xl, r.c_xh, n_unc, n_in, r.ax_u, r.usable, stream));
-    hipLaunchKernelGGL(k_and_u8, dim3((unsigned)std::min<int64_t>((n_unc + 255) / 256, 4096)),
-                       dim3(256), 0, st, feasible, r.usable, n_unc, r.split);
-    VC_LAUNCH_CHECK();
-    VC_TRY(vc_compact(feasible, n_unc, 0, r.idx, r.cnt, r.cws, r.cws_bytes, stream));
-    VC_TRY(vc_compact(r.split, n_unc, 0, r.idx2, r.cnt + 1, r.cws, r.cws_bytes, stream));
+    // the feasible leaves, and the feasible ones with a usable split axis
+    VC_TRY(vcm::compact_feasible_split(feasible, r.usable, n_unc, r.idx, r.cnt, r.idx2,
+                                       r.cnt + 1, r.split, r.cws, r.cws_bytes, st));
     int64_t two[2];
     VC_TRY(read_counts(r.cnt, 2, two, pinned, st));
     nf = two[0];

@@ -698,6 +698,27 @@ __global__ void k_closure(const float* lb, int64_t B, int Q, const int32_t* dptr
   }
 }
 
+// The open rows' bounds raised to alpha's best (rows[idx[r]] = max(rows,
+// src[r]), as k_scatter_max_rows) and their closure recomputed (as
+// k_closure; the other rows' bounds, and so their closure, are unchanged).
+__global__ void k_scatter_max_close(float* lb, const int64_t* idx, const float* src, int64_t nr,
+                                    int Q, const int32_t* dptr, const int32_t* qidx, int nd,
+                                    uint8_t* closed) {
+  for (int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; r < nr;
+       r += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = idx[r];
+    float* row = lb + b * Q;
+    for (int q = 0; q < Q; ++q) row[q] = fmaxf(row[q], src[r * Q + q]);
+    bool all = true;
+    for (int d = 0; d < nd; ++d) {
+      bool any = false;
+      for (int t = dptr[d]; t < dptr[d + 1]; ++t) any |= row[qidx[t]] > 0.f;
+      all &= any;
+    }
+    closed[b] = all;
+  }
+}
+
 // One thread per domain.  For each disjunct D: total_q = pos(A_q).xl +
 // neg(A_q).xh; per dim i the projection threshold
 // thr = (-b_q - (total_q - contrib_qi)) / A_qi; xh' = min(xh, min over
@@ -1033,6 +1054,61 @@ __global__ __launch_bounds__(C1T) void k_compact_single(const uint8_t* __restric
     __syncthreads();  // wsum is rewritten by the next pass
   }
   if (threadIdx.x == 0) count_out[0] = carry;
+}
+
+__global__ void k_and_flags(const uint8_t* __restrict__ a, const uint8_t* __restrict__ b,
+                            int64_t n, uint8_t* __restrict__ out) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = (a[i] != 0 && b[i] != 0) ? 1 : 0;
+}
+
+// Two compactions of n flags in one launch, one workgroup each (n <= C1N):
+// job j selects i where a_j[i] != 0 and (b_j null or b_j[i] != 0), in the
+// ascending order of k_compact_single.
+struct Compact2 {
+  const uint8_t* a[2];
+  const uint8_t* b[2];
+  int64_t* idx[2];
+  int64_t* count[2];
+};
+
+__global__ __launch_bounds__(C1T) void k_compact_pair(Compact2 jobs, int64_t n) {
+  __shared__ int wsum[C1T / 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint8_t* fa = jobs.a[blockIdx.x];
+  const uint8_t* fb = jobs.b[blockIdx.x];
+  int64_t* idx = jobs.idx[blockIdx.x];
+  int64_t carry = 0;
+  for (int64_t c0 = 0; c0 < n; c0 += (int64_t)C1T * C1P) {
+    const int64_t base = c0 + (int64_t)threadIdx.x * C1P;
+    uint32_t bits = 0;
+#pragma unroll
+    for (int e = 0; e < C1P; ++e) {
+      const int64_t i = base + e;
+      if (i < n && fa[i] != 0 && (fb == nullptr || fb[i] != 0)) bits |= 1u << e;
+    }
+    const int c = __popc(bits);
+    int x = c;  // inclusive scan within the wave
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wsum[w] = x;
+    __syncthreads();
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < C1T / 64; ++i) {
+      if (i < w) off += wsum[i];
+      tot += wsum[i];
+    }
+    int64_t o = carry + off + x - c;
+    for (int e = 0; e < C1P; ++e)
+      if ((bits >> e) & 1u) idx[o++] = base + e;
+    carry += tot;
+    __syncthreads();  // wsum is rewritten by the next pass
+  }
+  if (threadIdx.x == 0) jobs.count[blockIdx.x][0] = carry;
 }
 
 // rows[idx[r]] = max(rows[idx[r]], src[r]) over rows of q floats.
@@ -1482,6 +1558,44 @@ extern "C" int vc_scatter_max_rows(float* rows, const int64_t* idx, const float*
   VC_LAUNCH_CHECK();
   return VC_OK;
 }
+
+namespace vcm {
+// vc_scatter_max_rows followed by vc_closure over all B rows, for distinct
+// idx: only the scattered rows change, so only their closure is redone.
+int scatter_max_close(float* lb, const int64_t* idx, const float* src, int64_t nr, int Q,
+                      const int32_t* d_ptr, const int32_t* q_idx, int n_disj, uint8_t* closed,
+                      hipStream_t st) {
+  if (!lb || !idx || !src || !d_ptr || !q_idx || !closed || nr < 0 || Q <= 0 || n_disj < 0)
+    return VC_ERR_ARG;
+  if (nr == 0) return VC_OK;
+  hipLaunchKernelGGL(k_scatter_max_close, dim3(vc_blocks(nr, NT)), dim3(NT), 0, st, lb, idx, src,
+                     nr, Q, d_ptr, q_idx, n_disj, closed);
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
+// The feasible rows and the rows that are feasible and splittable, compacted
+// together (the input-split round): idx_f / cnt_f over feasible, idx_s /
+// cnt_s over feasible AND usable; two vc_compact calls above C1N flags.
+int compact_feasible_split(const uint8_t* feasible, const uint8_t* usable, int64_t n,
+                           int64_t* idx_f, int64_t* cnt_f, int64_t* idx_s, int64_t* cnt_s,
+                           uint8_t* split_tmp, void* ws, int64_t ws_bytes, hipStream_t st) {
+  if (!feasible || !usable || !idx_f || !cnt_f || !idx_s || !cnt_s || n < 0) return VC_ERR_ARG;
+  if (n <= C1N) {
+    Compact2 jobs{{feasible, feasible}, {nullptr, usable}, {idx_f, idx_s}, {cnt_f, cnt_s}};
+    hipLaunchKernelGGL(k_compact_pair, dim3(2), dim3(C1T), 0, st, jobs, n);
+    VC_LAUNCH_CHECK();
+    return VC_OK;
+  }
+  if (!split_tmp) return VC_ERR_ARG;
+  hipLaunchKernelGGL(k_and_flags, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 4096)),
+                     dim3(256), 0, st, feasible, usable, n, split_tmp);
+  VC_LAUNCH_CHECK();
+  int rc = vc_compact(feasible, n, 0, idx_f, cnt_f, ws, ws_bytes, (vc_stream_t)st);
+  if (rc != VC_OK) return rc;
+  return vc_compact(split_tmp, n, 0, idx_s, cnt_s, ws, ws_bytes, (vc_stream_t)st);
+}
+}  // namespace vcm
 
 extern "C" int vc_compact(const uint8_t* flags, int64_t n, int select_zero, int64_t* idx_out,
                           int64_t* count_out, void* workspace, int64_t ws_bytes,

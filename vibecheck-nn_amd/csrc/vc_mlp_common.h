@@ -84,6 +84,20 @@ int crown_rows_premasked(const int32_t* dims, int n_relu, const float* frag,
                          float* A_out, float* acc_out, uint64_t* seed_rows, void* work,
                          int64_t work_bytes, hipStream_t st);
 
+// vc_scatter_max_rows then vc_closure, for distinct rows idx: one launch
+// that redoes the closure of the scattered rows only (vc_elementwise.hip).
+int scatter_max_close(float* lb, const int64_t* idx, const float* src, int64_t nr, int Q,
+                      const int32_t* d_ptr, const int32_t* q_idx, int n_disj, uint8_t* closed,
+                      hipStream_t st);
+
+// The input-split round's two compactions after the clip (vc_elementwise.hip):
+// the feasible rows (idx_f, cnt_f) and the feasible rows with a usable split
+// axis (idx_s, cnt_s), in one launch up to 2^17 rows; split_tmp (n bytes)
+// is used above that.
+int compact_feasible_split(const uint8_t* feasible, const uint8_t* usable, int64_t n,
+                           int64_t* idx_f, int64_t* cnt_f, int64_t* idx_s, int64_t* cnt_s,
+                           uint8_t* split_tmp, void* ws, int64_t ws_bytes, hipStream_t st);
+
 // Compute units of the current device (read once per device).
 inline int cu_count() {
   static int cached[64] = {0};
