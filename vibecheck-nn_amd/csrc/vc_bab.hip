@@ -218,12 +218,12 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
   // domains itself.
   if (r.rws) {
     VC_TRY(vcm::zono_bounds_masked(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
-                                   r.queue + 1, r.rws, r.idx, r.cnt, st));
+                                   r.queue + 1, r.rws, r.idx, r.cnt, r.cnt + 3, st));
     VC_TRY(vcm::zono_wide_masked(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
                                  r.idx, r.cnt, r.rws, st));
   } else {
     VC_TRY(vcm::zono_bounds_listed(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
-                                   r.queue + 1, r.idx, r.cnt, r.umask, st));
+                                   r.queue + 1, r.idx, r.cnt, r.umask, r.cnt + 3, st));
     VC_TRY(vcm::zono_wide_union(dims, n, frag, bias_cat, B, xl, xh, r.sb_lo, r.sb_hi, r.ovf,
                                 r.idx, r.cnt, r.umask, st));
     VC_TRY(vcm::union_lists(dims, n, r.umask, r.uidx, r.umeta, st));
@@ -240,13 +240,18 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
                               r.t_hi, r.uidx, r.umeta, 1, 1, Q, spec_rows, spec_acc, lb, A,
                               acc, seed_rows, r.queue, stream));
   if (crown_ev1 && hipEventRecord((hipEvent_t)crown_ev1, st) != hipSuccess) return VC_ERR_LAUNCH;
-  VC_TRY(vc_closure(lb, B, Q, d_ptr, q_idx, n_disj, closed, stream));
+  // with alpha, the closure also lists the open leaves (their order is
+  // immaterial: each leaf's alpha is its own, and their bounds go back by
+  // index), counted in cnt[3], which the zonotope pass's init cleared
+  if (alpha_iters > 0)
+    VC_TRY(vcm::closure_open(lb, B, Q, d_ptr, q_idx, n_disj, closed, r.idx, r.cnt + 3, st));
+  else
+    VC_TRY(vc_closure(lb, B, Q, d_ptr, q_idx, n_disj, closed, stream));
 
   // ---- alpha-CROWN on the open leaves, from their zonotope bounds
   int64_t n_open = 0, n_eval = 0;
   if (alpha_iters > 0) {
-    VC_TRY(vc_compact(closed, B, 1, r.idx, r.cnt, r.cws, r.cws_bytes, stream));
-    VC_TRY(read_counts(r.cnt, 1, &n_open, pinned, st));
+    VC_TRY(read_counts(r.cnt + 3, 1, &n_open, pinned, st));
     if (n_open > 0) {
       const float* gin[2 * MAXL + 2];
       float* gout[2 * MAXL + 2];

@@ -698,6 +698,33 @@ __global__ void k_closure(const float* lb, int64_t B, int Q, const int32_t* dptr
   }
 }
 
+// k_closure that also lists the rows left open (in no particular order:
+// one atomic per wavefront), counted in *open_cnt, which the caller clears.
+__global__ void k_closure_open(const float* lb, int64_t B, int Q, const int32_t* dptr,
+                               const int32_t* qidx, int nd, uint8_t* closed, int64_t* open_idx,
+                               unsigned long long* open_cnt) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t b0 = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) & ~(int64_t)63; b0 < B;
+       b0 += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = b0 + lane;
+    bool all = true;
+    if (b < B) {
+      for (int d = 0; d < nd; ++d) {
+        bool any = false;
+        for (int t = dptr[d]; t < dptr[d + 1]; ++t) any |= lb[b * Q + qidx[t]] > 0.f;
+        all &= any;
+      }
+      closed[b] = all;
+    }
+    const uint64_t open = __ballot(b < B && !all);
+    unsigned long long base = 0;
+    if (lane == 0 && open) base = atomicAdd(open_cnt, (unsigned long long)__popcll(open));
+    base = __shfl(base, 0, 64);
+    if ((open >> lane) & 1ull)
+      open_idx[base + __popcll(open & ((1ull << lane) - 1ull))] = b;
+  }
+}
+
 // The open rows' bounds raised to alpha's best (rows[idx[r]] = max(rows,
 // src[r]), as k_scatter_max_rows) and their closure recomputed (as
 // k_closure; the other rows' bounds, and so their closure, are unchanged).
@@ -1560,6 +1587,22 @@ extern "C" int vc_scatter_max_rows(float* rows, const int64_t* idx, const float*
 }
 
 namespace vcm {
+// vc_closure that also lists the open rows (any order) and counts them in
+// *open_cnt (cleared by the caller on the stream beforehand).
+int closure_open(const float* lb, int64_t B, int Q, const int32_t* d_ptr, const int32_t* q_idx,
+                 int n_disj, uint8_t* closed, int64_t* open_idx, int64_t* open_cnt,
+                 hipStream_t st) {
+  if (!lb || !d_ptr || !q_idx || !closed || !open_idx || !open_cnt || B < 0 || Q <= 0 ||
+      n_disj < 0)
+    return VC_ERR_ARG;
+  if (B == 0) return VC_OK;
+  hipLaunchKernelGGL(k_closure_open, dim3(vc_blocks(B, NT)), dim3(NT), 0, st, lb, B, Q, d_ptr,
+                     q_idx, n_disj, closed, open_idx,
+                     reinterpret_cast<unsigned long long*>(open_cnt));
+  VC_LAUNCH_CHECK();
+  return VC_OK;
+}
+
 // vc_scatter_max_rows followed by vc_closure over all B rows, for distinct
 // idx: only the scattered rows change, so only their closure is redone.
 int scatter_max_close(float* lb, const int64_t* idx, const float* src, int64_t nr, int Q,

@@ -55,10 +55,12 @@ __device__ __forceinline__ int64_t queue_bcast(int t) { return (int64_t)__shfl(t
 // ovf_list / ovf_count (nullable together): the domains the one-wavefront
 // pass leaves to the wide pass, appended in no particular order, and their
 // count (the wide pass's list, with no compaction of the flags).
+// clear_count (nullable): a counter cleared by the pass's init launch.
 int zono_bounds_masked(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
                        int64_t B, const float* xl, const float* xh, float* const* lo_out,
                        float* const* hi_out, uint8_t* overflow, int32_t* queue, void* rows_work,
-                       int64_t* ovf_list, int64_t* ovf_count, hipStream_t st);
+                       int64_t* ovf_list, int64_t* ovf_count, int64_t* clear_count,
+                       hipStream_t st);
 // The zonotope passes with the overflow list and (umask, nullable) the
 // union of the unstable sets as bit masks [n_relu], without seed masks; and
 // union_lists: vc_union_compact's index lists from that union.
@@ -66,7 +68,7 @@ int zono_bounds_listed(const int32_t* dims, int n_relu, const float* frag, const
                        int64_t B, const float* xl, const float* xh, float* const* lo_out,
                        float* const* hi_out, uint8_t* overflow, int32_t* queue,
                        int64_t* ovf_list, int64_t* ovf_count, unsigned long long* umask,
-                       hipStream_t st);
+                       int64_t* clear_count, hipStream_t st);
 int zono_wide_union(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
                     int64_t B, const float* xl, const float* xh, float* const* lo_out,
                     float* const* hi_out, uint8_t* overflow, const int64_t* list,
@@ -83,6 +85,12 @@ int crown_rows_premasked(const int32_t* dims, int n_relu, const float* frag,
                          const float* spec_rows, const float* spec_acc, float* lb_out,
                          float* A_out, float* acc_out, uint64_t* seed_rows, void* work,
                          int64_t work_bytes, hipStream_t st);
+
+// vc_closure that also lists the open rows, in no particular order, and
+// counts them in *open_cnt, which the caller clears (vc_elementwise.hip).
+int closure_open(const float* lb, int64_t B, int Q, const int32_t* d_ptr, const int32_t* q_idx,
+                 int n_disj, uint8_t* closed, int64_t* open_idx, int64_t* open_cnt,
+                 hipStream_t st);
 
 // vc_scatter_max_rows then vc_closure, for distinct rows idx: one launch
 // that redoes the closure of the scattered rows only (vc_elementwise.hip).

@@ -39,10 +39,12 @@ __global__ void k_queue_reset(int* q) {
 // k_queue_reset for the zonotope pass, which also clears the union of
 // unstable sets (umask[n], nullable) and the overflow count (nullable) that
 // it accumulates.
-__global__ void k_zono_init(int* q, unsigned long long* umask, int n, unsigned long long* cnt) {
+__global__ void k_zono_init(int* q, unsigned long long* umask, int n, unsigned long long* cnt,
+                            unsigned long long* cnt2) {
   if (threadIdx.x == 0 && q) *q = 0;
   if (umask && threadIdx.x < n) umask[threadIdx.x] = 0ull;
   if (threadIdx.x == 0 && cnt) *cnt = 0ull;
+  if (threadIdx.x == 0 && cnt2) *cnt2 = 0ull;
 }
 
 constexpr int TNW = 12;  // waves per workgroup, one domain each (3 per SIMD)
@@ -1329,11 +1331,14 @@ struct TZonoArgs {
 // leaves to the wide pass to ovf_list (in no particular order: the wide pass
 // takes each domain on its own) and counts them in *ovf_count, which the
 // caller clears; the wide pass then needs no compaction of the flags.
+// clear_count (nullable): a counter of the caller's that the pass's init
+// launch also clears (the round's list of open leaves).
 struct ZonoMasks {
   uint64_t* masks;
   unsigned long long* umask;
   int64_t* ovf_list;
   unsigned long long* ovf_count;
+  unsigned long long* clear_count;
 };
 
 // fc_0 on the input block for NP column tiles, tile p starting at column
@@ -3034,9 +3039,9 @@ int zono_bounds_run(const int32_t* dims, int n_relu, const float* frag, const fl
   if (!vcm::allow_max_lds(fn)) return VC_ERR_UNSUPPORTED;
   const dim3 grid(vcm::persistent_grid(B, lds, nw)), block(nw * 64);
   hipStream_t st = (hipStream_t)stream;
-  if (queue || zm.umask || zm.ovf_count)
+  if (queue || zm.umask || zm.ovf_count || zm.clear_count)
     hipLaunchKernelGGL(k_zono_init, dim3(1), dim3(64), 0, st, queue, zm.umask, n_relu,
-                       zm.ovf_count);
+                       zm.ovf_count, zm.clear_count);
 #define VC_TZONO_CASE(V)                                                                     \
   case V:                                                                                    \
     hipLaunchKernelGGL((k_zono_tiled<kVariants[V].MT, kVariants[V].KS,                       \
@@ -3121,7 +3126,7 @@ extern "C" int vc_mlp_tiled_zono_bounds(const int32_t* dims, int n_relu, const f
                                         float* const* hi_out, uint8_t* overflow,
                                         int32_t* queue, vc_stream_t stream) {
   return zono_bounds_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow,
-                         queue, ZonoMasks{nullptr, nullptr, nullptr, nullptr}, stream);
+                         queue, ZonoMasks{nullptr, nullptr, nullptr, nullptr, nullptr}, stream);
 }
 
 extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const float* frag,
@@ -3131,7 +3136,7 @@ extern "C" int vc_mlp_tiled_zono_wide(const int32_t* dims, int n_relu, const flo
                                       const int64_t* list, const int64_t* n_list,
                                       vc_stream_t stream) {
   return zono_wide_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow, list,
-                       n_list, ZonoMasks{nullptr, nullptr, nullptr, nullptr}, stream);
+                       n_list, ZonoMasks{nullptr, nullptr, nullptr, nullptr, nullptr}, stream);
 }
 
 // ------------------------------------- the round's masked bound phase
@@ -3156,8 +3161,10 @@ bool rows_mask_slots(const int32_t* dims, int n_relu, int64_t B, void* rows_work
 int zono_bounds_masked(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
                        int64_t B, const float* xl, const float* xh, float* const* lo_out,
                        float* const* hi_out, uint8_t* overflow, int32_t* queue, void* rows_work,
-                       int64_t* ovf_list, int64_t* ovf_count, hipStream_t st) {
-  ZonoMasks zm{nullptr, nullptr, nullptr, nullptr};
+                       int64_t* ovf_list, int64_t* ovf_count, int64_t* clear_count,
+                       hipStream_t st) {
+  ZonoMasks zm{nullptr, nullptr, nullptr, nullptr,
+               reinterpret_cast<unsigned long long*>(clear_count)};
   if (!rows_mask_slots(dims, n_relu, B, rows_work, zm)) return VC_ERR_ARG;
   if ((ovf_list == nullptr) != (ovf_count == nullptr) || n_relu > MAXL) return VC_ERR_ARG;
   zm.ovf_list = ovf_list;
@@ -3170,9 +3177,10 @@ int zono_bounds_listed(const int32_t* dims, int n_relu, const float* frag, const
                        int64_t B, const float* xl, const float* xh, float* const* lo_out,
                        float* const* hi_out, uint8_t* overflow, int32_t* queue,
                        int64_t* ovf_list, int64_t* ovf_count, unsigned long long* umask,
-                       hipStream_t st) {
+                       int64_t* clear_count, hipStream_t st) {
   if (!ovf_list || !ovf_count || n_relu > MAXL) return VC_ERR_ARG;
-  ZonoMasks zm{nullptr, umask, ovf_list, reinterpret_cast<unsigned long long*>(ovf_count)};
+  ZonoMasks zm{nullptr, umask, ovf_list, reinterpret_cast<unsigned long long*>(ovf_count),
+               reinterpret_cast<unsigned long long*>(clear_count)};
   return zono_bounds_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow,
                          queue, zm, st);
 }
@@ -3182,7 +3190,7 @@ int zono_wide_union(const int32_t* dims, int n_relu, const float* frag, const fl
                     float* const* hi_out, uint8_t* overflow, const int64_t* list,
                     const int64_t* n_list, unsigned long long* umask, hipStream_t st) {
   return zono_wide_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow, list,
-                       n_list, ZonoMasks{nullptr, umask, nullptr, nullptr}, st);
+                       n_list, ZonoMasks{nullptr, umask, nullptr, nullptr, nullptr}, st);
 }
 
 namespace {
@@ -3218,7 +3226,7 @@ int zono_wide_masked(const int32_t* dims, int n_relu, const float* frag, const f
                      int64_t B, const float* xl, const float* xh, float* const* lo_out,
                      float* const* hi_out, uint8_t* overflow, const int64_t* list,
                      const int64_t* n_list, void* rows_work, hipStream_t st) {
-  ZonoMasks zm{nullptr, nullptr, nullptr, nullptr};
+  ZonoMasks zm{nullptr, nullptr, nullptr, nullptr, nullptr};
   if (!rows_mask_slots(dims, n_relu, B, rows_work, zm)) return VC_ERR_ARG;
   return zono_wide_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo_out, hi_out, overflow, list,
                        n_list, zm, st);
