@@ -3024,7 +3024,12 @@ int zono_bounds_run(const int32_t* dims, int n_relu, const float* frag, const fl
                       sizeof(unsigned long long) * (ZNW + 1) * MAXL;
   const size_t scr = (size_t)ZSCR * sizeof(float);
   if (base + scr > 160 * 1024) return VC_ERR_UNSUPPORTED;
-  const int nw = (int)std::min<size_t>(ZNW, (160 * 1024 - base) / scr);
+  // small batches: fewer wavefronts per workgroup, so that the domains
+  // spread over every CU (one wavefront per SIMD) instead of sharing the
+  // matrix cores of a few (each domain's arithmetic is the same)
+  const int64_t per_cu_dom = (B + vcm::cu_count() - 1) / vcm::cu_count();
+  const int nw = (int)std::min<int64_t>(std::min<size_t>(ZNW, (160 * 1024 - base) / scr),
+                                        std::max<int64_t>(1, per_cu_dom));
   const size_t lds = base + (size_t)nw * scr;
   const void* fn = nullptr;
   switch (G.variant) {
