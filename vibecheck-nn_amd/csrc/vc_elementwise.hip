@@ -860,11 +860,24 @@ __global__ __launch_bounds__(64) void k_clip_reg(const float* xl, const float* x
   for (int64_t b0 = (int64_t)blockIdx.x * 64; b0 < B; b0 += (int64_t)gridDim.x * 64) {
     const int nb = (int)min((int64_t)64, B - b0);
     // record r = [A row (Q n) | b row (Q)]; i = r w + c, c < w: the float
-    // quotient is at least 0.5 / w from an integer, far above its rounding
-    for (int i = t; i < nb * w; i += 64) {
-      const int r = (int)((i + 0.5f) * invw);
-      const int c = i - r * w;
-      rec[r * rs + c] = c < qn ? A[(b0 + r) * qn + c] : bv[(b0 + r) * Q + (c - qn)];
+    // quotient is at least 0.5 / w from an integer, far above its rounding.
+    // Eight loads in flight per thread before their stores (a batch of
+    // small domains is otherwise one load latency per element).
+    for (int i0 = t; i0 < nb * w; i0 += 64 * 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int i = i0 + 64 * k;
+        const int r = (int)((i + 0.5f) * invw);
+        const int c = i - r * w;
+        v[k] = i < nb * w ? (c < qn ? A[(b0 + r) * qn + c] : bv[(b0 + r) * Q + (c - qn)]) : 0.f;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int i = i0 + 64 * k;
+        const int r = (int)((i + 0.5f) * invw);
+        if (i < nb * w) rec[r * rs + i - r * w] = v[k];
+      }
     }
     __syncthreads();
     if (t < nb) {
