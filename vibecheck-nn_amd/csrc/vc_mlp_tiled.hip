@@ -700,6 +700,8 @@ __device__ __forceinline__ void fc_forward(const float4* fr, int lane, int g, in
   for (int x = 0; x < NX; ++x)
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) out[x][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  // the MFMA block at raised wave priority, as in fc_hidden
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float a[MT][4];
@@ -725,6 +727,7 @@ __device__ __forceinline__ void fc_forward(const float4* fr, int lane, int g, in
           out[x][mo] = mfma16x16x4(a[mo][t], X[x0 + x][t][i], out[x][mo]);
     }
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // Per-wave LDS of the alpha kernels: slopes [l][ls_eff, us, ut, unstable][FW],
