@@ -369,3 +369,170 @@ def test_bab_step_sb_and_multi_split():
         assert bool((kl[row:row + n] >= xs[b]).all() and (kh[row:row + n] <= hs[b]).all())
         row += n
     assert row == kl.shape[0]
+
+
+# --------------------------------------------------- alpha on the BaB leaves
+def _one_neuron_net():
+    """x -> z = x -> h = relu(z) -> (y0, y1) = (h + 0.1, h - 10), in fp64.
+
+    On a box [l, u] with l < 0 < u, CROWN's lower relaxation h >= alpha z
+    gives lb(y0) = alpha l + 0.1 and lb(y1) = alpha l - 10 (alpha in [0, 1]);
+    the adaptive slope is alpha = 1 iff u > -l.  The exact minimum of y0 is
+    0.1, reached by alpha = 0, and alpha-CROWN's Adam walks alpha down from 1
+    by lr_t each step (a constant gradient makes every Adam step lr_t, to
+    1e-8 relative), clamped at 0."""
+    gg = wk.mlp_gg([_t([[1.0]]), _t([[1.0], [1.0]])], [_t([0.0]), _t([0.1, -10.0])],
+                   dtype=DT)
+    se2 = {0: (_t([1.0, 0.0]), 0.0), 1: (_t([0.0, 1.0]), 0.0)}
+    se1 = {0: (_t([1.0, 0.0]), 0.0)}
+    # leaves: A [-0.5, 1] open (lb0 -0.4); B [-1, 0.5] closed (alpha 0: 0.1);
+    # C [0.2, 0.3] stable, closed (0.3); D [-0.05, 1] closed (0.05, alpha 1);
+    # E [-2, 3] open (-1.9)
+    xl = _t([[-0.5], [-1.0], [0.2], [-0.05], [-2.0]])
+    xh = _t([[1.0], [0.5], [0.3], [1.0], [3.0]])
+    return gg, se1, se2, xl, xh
+
+
+def _alpha_walk(n, g):
+    """alpha after n Adam steps from 1 at lr 0.25, decay 0.98, clamped at 0,
+    under a constant gradient of magnitude g: Adam's bias-corrected moments
+    are g and g^2, so each step is lr_t g / (g + 1e-8)."""
+    a = 1.0
+    for t in range(n):
+        a = max(0.0, a - 0.25 * 0.98 ** t * g / (g + 1e-8))
+    return a
+
+
+def test_alpha_on_leaves_closed_form():
+    """``alpha_on_leaves`` (verify_graph.py:12927-12975) on the one-neuron
+    net, every number by hand.  alpha_all runs on the CROWN-open leaves A, E
+    only; the closed leaves' bounds stay bit for bit (alpha on D would raise
+    its 0.05 to 0.1); the open leaves' bounds are max(CROWN, alpha) entry by
+    entry (a min merge keeps -0.4); the closure is recomputed from the merged
+    bound (a stale one leaves A, E open); the iteration count is the loop's
+    own: the global max of the best bound stops improving (it stays 0.1
+    once alpha is clamped at 0) after 7 evaluations."""
+    gg, _, se2, xl, xh = _one_neuron_net()
+    dq = {0: [0, 1]}
+    lb, _, _ = rbab.bound_batch(xl, xh, gg, se2)
+    torch.testing.assert_close(lb, _t([[-0.4, -10.5], [0.1, -10.0], [0.3, -9.8],
+                                       [0.05, -10.05], [-1.9, -12.0]]), rtol=0, atol=1e-12)
+    closed = rbab.closure(lb, dq)
+    assert closed.tolist() == [False, True, True, True, False]
+    lb_in = lb.clone()
+    out, cl, n_l, n_it = rbab.alpha_on_leaves(lb, xl, xh, gg, se2, dq, closed, 20,
+                                              True, 0.0, 200)
+    assert torch.equal(lb, lb_in)                       # input not mutated
+    assert (n_l, n_it) == (2, 7)
+    for i in (1, 2, 3):
+        assert torch.equal(out[i], lb[i])
+    # alpha reaches 0 after 5 steps: best y0 = 0.1, best y1 = -10
+    torch.testing.assert_close(out[[0, 4]], _t([[0.1, -10.0], [0.1, -10.0]]),
+                               rtol=0, atol=1e-9)
+    assert cl.tolist() == [True] * 5
+    # the count alone, from the alpha loop on the two open leaves
+    _, n = rb.alpha_crown_batched(xl[[0, 4]], xh[[0, 4]], gg, se2, n_iters=20,
+                                  return_trace=True)
+    assert n == 7
+    # an iteration budget below the stop: 3 evaluations, alpha 1, 0.75, 0.505
+    out3, cl3, _, n3 = rbab.alpha_on_leaves(lb, xl, xh, gg, se2, dq, closed, 3,
+                                            True, 0.0, 200)
+    # (gradient of -(lb0 + lb1) in alpha: -2 l, so 1 for A and 4 for E)
+    aA, aE = _alpha_walk(2, 1.0), _alpha_walk(2, 4.0)
+    assert n3 == 3 and abs(aA - 0.505) < 1e-7 and abs(aE - 0.505) < 1e-7
+    torch.testing.assert_close(out3[[0, 4]], _t([[-0.5 * aA + 0.1, -0.5 * aA - 10],
+                                                 [-2 * aE + 0.1, -2 * aE - 10]]),
+                               rtol=0, atol=1e-12)
+    assert cl3.tolist() == [False, True, True, True, False]
+
+
+def test_alpha_on_leaves_all_positive_stop():
+    """With the single query y0 the loop stops on every best bound > 0
+    (verify_zono_bnb.py:5258-5259) at the 5th evaluation, where alpha =
+    1 - 0.25 (1 + 0.98 + 0.98^2 + 0.98^3) = 0.029602 gives y0 bounds
+    0.085199 (A) and 0.040796 (E): the bound of the evaluation that stopped
+    the loop, not the 0.1 that further steps would reach."""
+    gg, se1, _, xl, xh = _one_neuron_net()
+    dq = {0: [0]}
+    lb, _, _ = rbab.bound_batch(xl, xh, gg, se1)
+    closed = rbab.closure(lb, dq)
+    out, cl, n_l, n_it = rbab.alpha_on_leaves(lb, xl, xh, gg, se1, dq, closed, 20,
+                                              True, 0.0, 200)
+    # (gradient of -lb0 in alpha: -l, so 0.5 for A and 2 for E)
+    aA, aE = _alpha_walk(4, 0.5), _alpha_walk(4, 2.0)
+    assert abs(aA - 0.029602) < 1e-7 and abs(aE - 0.029602) < 1e-7
+    assert (n_l, n_it) == (2, 5)
+    torch.testing.assert_close(out[[0, 4], 0], _t([-0.5 * aA + 0.1, -2 * aE + 0.1]),
+                               rtol=0, atol=1e-12)
+    assert cl.tolist() == [True] * 5
+
+
+def test_alpha_on_leaves_band_and_multi_disjunct():
+    """Band selection (alpha_all off): eps 1 takes A (worst -0.4) and not E
+    (-1.9); eps 3 with max_leaves 1 takes the best, A.  With two one-query
+    disjuncts no leaf ever closes (y1 < 0), alpha_all takes all five, and the
+    loop stops at its 2nd evaluation, because leaf C's constant 0.3 holds
+    the global max (a per-leaf stop would run on); D rises to
+    -0.75 * 0.05 + 0.1 = 0.0625."""
+    gg, _, se2, xl, xh = _one_neuron_net()
+    dq = {0: [0, 1]}
+    lb, _, _ = rbab.bound_batch(xl, xh, gg, se2)
+    closed = rbab.closure(lb, dq)
+    for eps, mx in ((1.0, 200), (3.0, 1)):
+        out, cl, n_l, n_it = rbab.alpha_on_leaves(lb, xl, xh, gg, se2, dq, closed, 20,
+                                                  False, eps, mx)
+        assert (n_l, n_it) == (1, 7)
+        torch.testing.assert_close(out[0], _t([0.1, -10.0]), rtol=0, atol=1e-9)
+        assert torch.equal(out[1:], lb[1:])
+        assert cl.tolist() == [True, True, True, True, False]
+    # nothing in the band: no alpha, nothing changes
+    out, cl, n_l, n_it = rbab.alpha_on_leaves(lb, xl, xh, gg, se2, dq, closed, 20,
+                                              False, 0.3, 200)
+    assert (n_l, n_it) == (0, 0) and torch.equal(out, lb)
+    # off: zero iterations, or neither alpha_all nor a band
+    for it, al, eps in ((0, True, 0.0), (20, False, 0.0)):
+        assert rbab.alpha_on_leaves(lb, xl, xh, gg, se2, dq, closed, it, al, eps,
+                                    200)[2:] == (0, 0)
+    dq2 = {0: [0], 1: [1]}
+    closed2 = rbab.closure(lb, dq2)
+    assert closed2.tolist() == [False] * 5
+    out, cl, n_l, n_it = rbab.alpha_on_leaves(lb, xl, xh, gg, se2, dq2, closed2, 20,
+                                              True, 0.0, 200)
+    assert (n_l, n_it) == (5, 2)
+    # one step each: alpha 0.75 to 1e-8 relative (gradients 1, 0.1, 4)
+    want = lb.clone()
+    for i, l in ((0, -0.5), (3, -0.05), (4, -2.0)):
+        a = _alpha_walk(1, -2 * l)
+        assert abs(a - 0.75) < 1e-7
+        want[i] = _t([a * l + 0.1, a * l - 10])
+    torch.testing.assert_close(want[[0, 3, 4]], _t([[-0.275, -10.375], [0.0625, -10.0375],
+                                                    [-1.4, -11.5]]), rtol=0, atol=1e-7)
+    torch.testing.assert_close(out, want, rtol=0, atol=1e-12)
+    assert cl.tolist() == [False] * 5
+
+
+def test_bab_step_alpha_branch():
+    """bab_step with alpha (verify_graph.py:12927-12986): ``crown_lb`` /
+    ``crown_closed`` are the bound phase's, ``lb`` / ``closed`` the merged
+    ones, ``unclosed`` lists the leaves still open after alpha, and the clip
+    of that leaf uses the CROWN pass's linear bound: E = [-2, 3] with
+    y0 >= x + 0.1 and y1 >= x - 10 (one disjunct: both <= 0 on the clip)
+    clips to [-2, -0.1] and bisects at -1.05."""
+    gg, _, se2, xl, xh = _one_neuron_net()
+    dq = {0: [0, 1]}
+    st = rbab.bab_step(xl, xh, gg, se2, dq, alpha_iters=20, alpha_eps=1.0)
+    st0 = rbab.bab_step(xl, xh, gg, se2, dq)
+    assert torch.equal(st['crown_lb'], st0['lb'])
+    assert torch.equal(st['crown_closed'], st0['closed'])
+    assert (st['n_alpha_leaves'], st['n_alpha_iters']) == (1, 7)
+    assert st['closed'].tolist() == [True, True, True, True, False]
+    assert st['unclosed'].tolist() == [4] and st0['unclosed'].tolist() == [0, 4]
+    torch.testing.assert_close(st['lb'][0], _t([0.1, -10.0]), rtol=0, atol=1e-9)
+    assert st['feasible'].tolist() == [True]
+    torch.testing.assert_close(st['xl_split'], _t([[-2.0]]), rtol=0, atol=1e-12)
+    torch.testing.assert_close(st['xh_split'], _t([[-0.1]]), rtol=0, atol=1e-12)
+    (lxl, lxh), (hxl, hxh) = st['low'], st['high']
+    torch.testing.assert_close(lxh, _t([[-1.05]]), rtol=0, atol=1e-12)
+    assert torch.equal(lxh, hxl) and torch.equal(lxl, st['xl_split'])
+    stall = rbab.bab_step(xl, xh, gg, se2, dq, alpha_iters=20, alpha_all=True)
+    assert stall['unclosed'].numel() == 0 and stall['chunks'] == []
