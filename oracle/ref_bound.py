@@ -9,6 +9,7 @@ targets, with the affine ops the reference's ONNX reader emits around them.
 Anything else raises NotImplementedError, as the reference does for
 unsupported ops.
 """
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -98,6 +99,17 @@ def shared_gens_count(name_a, name_b, gg, gen_count):
     return gen_count.get(gg['input_name'], 0)
 
 
+def _fc_nd(op, width):
+    """The prefix of an fc in the N-D batched MatMul form, or None: an
+    in_shapes_nd of two or more dims whose last is W.shape[1] and whose
+    product is the input width (verify_zono_bnb.py:3145-3152)."""
+    shp = (op.get('in_shapes_nd') or [None])[0]
+    if (shp is not None and len(shp) >= 2 and op['W'].shape[1] == shp[-1]
+            and width == int(np.prod(shp))):
+        return tuple(int(s) for s in shp[:-1])
+    return None
+
+
 def point_forward(x, gg):
     """Concrete forward of a batch of points x (P, n_in).
 
@@ -111,7 +123,12 @@ def point_forward(x, gg):
         a = act[op['inputs'][0]]
         t = op['type']
         if t == 'fc':
-            act[op['name']] = a @ op['W'].T + op['bias']
+            pre_nd = _fc_nd(op, a.shape[-1])
+            if pre_nd is not None:
+                y = a.reshape(*a.shape[:-1], *pre_nd, op['W'].shape[1]) @ op['W'].T + op['bias']
+                act[op['name']] = y.reshape(*a.shape[:-1], -1)
+            else:
+                act[op['name']] = a @ op['W'].T + op['bias']
         elif t == 'conv':
             y = F.conv2d(a.reshape(P, *op['in_shape']), op['kernel'],
                          op['bias'], stride=op['stride'],
@@ -251,8 +268,19 @@ def zono_forward_batched(xl, xh, gg):
                            if sc.numel() > 1 else G_in * sc)
         elif t == 'fc':
             W = op['W']
-            state[name] = (c_in @ W.T + op['bias'],
-                           torch.einsum('oi,bik->bok', W, G_in))
+            pre_nd = _fc_nd(op, c_in.shape[1])
+            if pre_nd is not None:
+                # N-D batched MatMul (verify_zono_bnb.py:3145-3168)
+                Kc = G_in.shape[2]
+                c_o = F.linear(c_in.reshape(B, *pre_nd, W.shape[1]), W,
+                               op['bias']).reshape(B, -1)
+                G_o = torch.einsum('...ik,oi->...ok',
+                                   G_in.reshape(B, *pre_nd, W.shape[1], Kc),
+                                   W).reshape(B, -1, Kc)
+                state[name] = (c_o, G_o)
+            else:
+                state[name] = (c_in @ W.T + op['bias'],
+                               torch.einsum('oi,bik->bok', W, G_in))
         elif t == 'conv':
             shp = op['in_shape']
             c_out = F.conv2d(c_in.reshape(B, *shp), op['kernel'],
@@ -346,8 +374,20 @@ def spec_backward_batched(tight, xl, xh, gg, spec_ew=None,
         ew = ew_at[name]
         t = op['type']
         if t == 'fc':
-            acc = acc + ew @ op['bias']
-            _put(op['inputs'][0], ew @ op['W'])
+            shp_in = (op.get('in_shapes_nd') or [None])[0]
+            shp_out = op.get('out_shape_nd')
+            if (shp_in is not None and len(shp_in) >= 2
+                    and op['W'].shape[1] == shp_in[-1]
+                    and shp_out is not None and len(shp_out) >= 2):
+                # N-D batched MatMul (verify_zono_bnb.py:4382-4401)
+                n_p = int(np.prod(shp_out[:-1]))
+                ew_nd = ew.reshape(*ew.shape[:-1], n_p, int(shp_out[-1]))
+                acc = acc + (ew_nd * op['bias']).sum(dim=(-2, -1))
+                back = ew_nd @ op['W']
+                _put(op['inputs'][0], back.reshape(*back.shape[:-2], -1))
+            else:
+                acc = acc + ew @ op['bias']
+                _put(op['inputs'][0], ew @ op['W'])
         elif t == 'relu':
             if 'layer_idx' in op:
                 L = op['layer_idx']

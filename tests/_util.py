@@ -70,3 +70,44 @@ def clip_tolerance(A, acc, xl, xh, rtol=1e-5, atol=1e-6):
     per = torch.where(cut, (atol + rtol * scale).unsqueeze(-1) / A.abs().clamp(min=1e-30),
                       torch.zeros_like(A))
     return torch.minimum(per.amax(1), xh - xl) + atol + rtol * xm
+
+
+def nd_mlp_gg(seed=0, dtype=torch.float64, device='cpu', out_nd=True):
+    """An fc in the N-D batched MatMul form (ONNX MatMul on a (3, 7) input,
+    W (16, 7): output (3, 16)), relu, flatten, fc 48 -> 6, relu, fc 6 -> 3.
+    ``out_nd`` False drops the first fc's out_shape_nd."""
+    g = torch.Generator().manual_seed(seed)
+    W0 = torch.randn(16, 7, generator=g, dtype=torch.float64) * (2 / 7) ** 0.5
+    b0 = torch.randn(16, generator=g, dtype=torch.float64) * 0.1
+    W1 = torch.randn(6, 48, generator=g, dtype=torch.float64) * (2 / 48) ** 0.5
+    b1 = torch.randn(6, generator=g, dtype=torch.float64) * 0.1
+    W2 = torch.randn(3, 6, generator=g, dtype=torch.float64) * (2 / 6) ** 0.5
+    b2 = torch.randn(3, generator=g, dtype=torch.float64) * 0.1
+    cv = dict(device=device, dtype=dtype)
+    fc0 = {'name': 'fc0', 'type': 'fc', 'inputs': ['input'], 'W': W0.to(**cv),
+           'bias': b0.to(**cv), 'in_shapes_nd': [(3, 7)]}
+    if out_nd:
+        fc0['out_shape_nd'] = (3, 16)
+    ops = [fc0,
+           {'name': 'relu0', 'type': 'relu', 'inputs': ['fc0'], 'layer_idx': 0},
+           {'name': 'flat', 'type': 'reshape', 'inputs': ['relu0']},
+           {'name': 'fc1', 'type': 'fc', 'inputs': ['flat'], 'W': W1.to(**cv),
+            'bias': b1.to(**cv)},
+           {'name': 'relu1', 'type': 'relu', 'inputs': ['fc1'], 'layer_idx': 1},
+           {'name': 'fc2', 'type': 'fc', 'inputs': ['relu1'], 'W': W2.to(**cv),
+            'bias': b2.to(**cv)}]
+    return {'ops': ops, 'relu_names': ['relu0', 'relu1'], 'fork_points': set(),
+            'n_relu': 2, 'input_name': 'input', 'input_n': 21, 'input_shape': (1, 3, 7)}
+
+
+def nd_as_block_diag(gg):
+    """The same net with the N-D fc written as a plain fc of the
+    block-diagonal kron(I_3, W0) and bias repeated 3 times."""
+    import copy
+    out = copy.copy(gg)
+    ops = [dict(op) for op in gg['ops']]
+    W0, b0 = ops[0]['W'], ops[0]['bias']
+    ops[0] = {'name': 'fc0', 'type': 'fc', 'inputs': ['input'],
+              'W': torch.block_diag(W0, W0, W0), 'bias': b0.repeat(3)}
+    out['ops'] = ops
+    return out

@@ -685,3 +685,114 @@ def test_residual_net_bounds_contain_samples():
         lin = X[b] @ A[b].T + acc[b]
         assert bool((lin <= val + 1e-9).all())
         assert bool((lb[b] <= val.min(0).values + 1e-9).all())
+
+
+# ------------------------------------------------ N-D batched MatMul fc
+def _nd_boxes(B, seed):
+    g = torch.Generator().manual_seed(seed)
+    c = torch.rand(B, 21, generator=g, dtype=DT) * 2 - 1
+    r = torch.rand(B, 21, generator=g, dtype=DT) * 0.2 + 0.01
+    return c - r, c + r
+
+
+def test_nd_fc_equals_block_diagonal_fc():
+    """An fc in the N-D MatMul form (W (16, 7) on a (3, 7) input,
+    verify_zono_bnb.py:3145-3168 and 4382-4401) is the plain fc of the
+    block-diagonal kron(I_3, W) with the bias repeated: point forward,
+    zonotope bounds, generators, CROWN-intermediate bounds and the spec
+    bound with its linear form all agree.  A slice order that takes the
+    prefix as the inner dim, or a bias summed once instead of per slice,
+    fails here."""
+    gg = _util.nd_mlp_gg(seed=1)
+    gb = _util.nd_as_block_diag(gg)
+    xl, xh = _nd_boxes(16, 2)
+    pts = _util.sample_box(xl, xh, 50, seed=3).reshape(-1, 21)
+    y_nd, pre_nd = rb.point_forward(pts, gg)
+    y_bd, pre_bd = rb.point_forward(pts, gb)
+    torch.testing.assert_close(y_nd, y_bd, rtol=0, atol=1e-12)
+    torch.testing.assert_close(pre_nd[0], pre_bd[0], rtol=0, atol=1e-12)
+    sb_nd, (c_nd, G_nd) = rb.zono_forward_batched(xl, xh, gg)
+    sb_bd, (c_bd, G_bd) = rb.zono_forward_batched(xl, xh, gb)
+    for L in sb_bd:
+        for a, b in zip(sb_nd[L], sb_bd[L]):
+            torch.testing.assert_close(a, b, rtol=0, atol=1e-12)
+    torch.testing.assert_close(G_nd, G_bd, rtol=0, atol=1e-12)
+    t_nd = rb.crown_intermediate_batched(gg, xl, xh)
+    t_bd = rb.crown_intermediate_batched(gb, xl, xh)
+    spec_ew, _ = _util.spec_for(3)
+    lb_nd, A_nd, acc_nd = rb.spec_backward_batched(t_nd, xl, xh, gg, spec_ew,
+                                                   return_input_linear=True)
+    lb_bd, A_bd, acc_bd = rb.spec_backward_batched(t_bd, xl, xh, gb, spec_ew,
+                                                   return_input_linear=True)
+    for L in t_bd:
+        for a, b in zip(t_nd[L], t_bd[L]):
+            torch.testing.assert_close(a, b, rtol=0, atol=1e-10)
+    torch.testing.assert_close(lb_nd, lb_bd, rtol=0, atol=1e-10)
+    torch.testing.assert_close(A_nd, A_bd, rtol=0, atol=1e-10)
+    torch.testing.assert_close(acc_nd, acc_bd, rtol=0, atol=1e-10)
+    # and the bounds contain the sampled outputs
+    Wq = torch.stack([spec_ew[q][0] for q in sorted(spec_ew)])
+    val = (y_nd @ Wq.T).reshape(16, 50, -1)
+    assert bool((val >= lb_nd.unsqueeze(1) - 1e-9).all())
+    for L, (lo, hi) in t_nd.items():
+        p = pre_nd[L].reshape(16, 50, -1)
+        assert bool((p >= lo.unsqueeze(1) - 1e-9).all() and (p <= hi.unsqueeze(1) + 1e-9).all())
+
+
+def test_nd_fc_interval_forward_has_no_nd_form():
+    """The reference's interval fc is mid @ W.T (verify_zono_bnb.py:
+    1108-1113): an N-D fc fails there with torch's shape error, and so
+    does the oracle."""
+    gg = _util.nd_mlp_gg(seed=1)
+    xl, xh = _nd_boxes(4, 2)
+    with pytest.raises(RuntimeError):
+        rb.ibp_forward_batched(xl, xh, gg)
+
+
+def test_validate_gg_widths_and_mismatches():
+    """The drop-in checks every node's width before any launch
+    (vibecheck_amd.verify_zono_bnb.validate_gg, shapes only, no device):
+    the N-D fc form gives 3 x 16; an input, fc, conv or merge width that
+    does not chain raises ValueError (the kernels would otherwise read a
+    wider tensor as rows of W.shape[1]); an unknown op raises
+    NotImplementedError."""
+    import copy
+    from vibecheck_amd.verify_zono_bnb import validate_gg
+    gg = _util.nd_mlp_gg(seed=1)
+    w = validate_gg(gg)
+    assert w == {'input': 21, 'fc0': 48, 'relu0': 48, 'flat': 48, 'fc1': 6,
+                 'relu1': 6, 'fc2': 3}
+    with pytest.raises(ValueError):
+        validate_gg(gg, n_in=20)
+    bad = copy.deepcopy(gg)
+    bad['ops'][0]['in_shapes_nd'] = [(7, 3)]           # last dim is not W's 7
+    with pytest.raises(ValueError):
+        validate_gg(bad)
+    bad = copy.deepcopy(gg)
+    del bad['ops'][0]['in_shapes_nd']                   # 21 values read as rows of 7
+    with pytest.raises(ValueError):
+        validate_gg(bad)
+    bad = copy.deepcopy(gg)
+    bad['ops'][3]['W'] = torch.zeros(6, 47, dtype=DT)
+    with pytest.raises(ValueError):
+        validate_gg(bad)
+    assert validate_gg(wk.acas_gg(dtype=DT))['fc6'] == 5
+    cnn = _util.tiny_cnn()
+    wc = validate_gg(cnn)
+    assert wc[cnn['ops'][-1]['name']] == 2
+    bad = copy.deepcopy(cnn)
+    conv = next(op for op in bad['ops'] if op['type'] == 'conv')
+    conv['in_shape'] = (2, 6, 5)
+    with pytest.raises(ValueError):
+        validate_gg(bad)
+    res = wk.residual_mlp_gg(4, 8, 3, seed=0, dtype=DT)
+    validate_gg(res)
+    bad = copy.deepcopy(res)
+    merge = next(op for op in bad['ops'] if op['type'] == 'add' and op.get('is_merge'))
+    merge['inputs'] = [merge['inputs'][0], bad['input_name']]
+    with pytest.raises(ValueError):
+        validate_gg(bad)
+    bad = copy.deepcopy(gg)
+    bad['ops'][2]['type'] = 'softmax'
+    with pytest.raises(NotImplementedError):
+        validate_gg(bad)

@@ -89,6 +89,97 @@ def _op_params(op, device):
     return p
 
 
+def _prod(shape):
+    n = 1
+    for s in shape:
+        n *= int(s)
+    return n
+
+
+def _fc_form(op, width):
+    """How an fc reads a node of ``width`` values per domain: (P, nd_out).
+
+    P = 1 is the plain form, width == W.shape[1].  The N-D batched MatMul
+    form (an ONNX MatMul on a (prefix..., n_in) input,
+    verify_zono_bnb.py:3145-3168 and 4382-4401) has in_shapes_nd[0] with
+    two or more dims, W.shape[1] equal to its last and width equal to its
+    product: W applies to each of the P = prod(prefix) slices of n_in
+    values, and the output holds P slices of W.shape[0].  nd_out tells
+    whether the op also carries the out_shape_nd the reference's backward
+    needs for that form (two or more dims).  Any other width raises
+    ValueError: the kernels would read a wider tensor as rows of
+    W.shape[1]."""
+    n_out, n_in = (int(s) for s in op['W'].shape)
+    shp = (op.get('in_shapes_nd') or [None])[0]
+    if shp is not None and len(shp) >= 2 and int(shp[-1]) == n_in \
+            and width == _prod(shp):
+        P = _prod(shp[:-1])
+        shp_o = op.get('out_shape_nd')
+        nd_out = shp_o is not None and len(shp_o) >= 2 and _prod(shp_o) == P * n_out
+        return P, nd_out
+    if width == n_in:
+        return 1, True
+    raise ValueError(f'fc {op["name"]!r}: input of {width} values per domain, but W is '
+                     f'{n_out}x{n_in} and in_shapes_nd is {shp}')
+
+
+def validate_gg(gg, n_in=None):
+    """The width of every node of ``gg``, checked op by op from the input's
+    (``n_in``, else gg['input_n'], else the product of gg['input_shape']
+    past the batch dim) before any launch, with the ops' shapes only (no
+    device tensors): an fc reads W.shape[1] values or the N-D MatMul form
+    (_fc_form); a conv reads prod(in_shape) and writes prod(out_shape); a
+    residual merge adds two nodes of one width; relu, reshape and the
+    constant add / sub / mul keep the width.  Raises ValueError on the
+    first mismatch, NotImplementedError on an op type outside
+    fc / conv / relu / reshape / add / sub / mul.  Returns {name: width}."""
+    if n_in is None:
+        n_in = gg.get('input_n')
+        if n_in is None:
+            shp = gg.get('input_shape')
+            if shp is None:
+                raise ValueError('gg has neither input_n nor input_shape')
+            n_in = _prod(shp[1:]) if len(shp) > 1 else _prod(shp)
+    width = {gg['input_name']: int(n_in)}
+    for op in gg['ops']:
+        t, name = op['type'], op['name']
+        for i in op['inputs']:
+            if i not in width:
+                raise ValueError(f'{t} {name!r}: input {i!r} is not computed before it')
+        w = width[op['inputs'][0]]
+        if t == 'fc':
+            P, _ = _fc_form(op, w)
+            width[name] = P * int(op['W'].shape[0])
+        elif t == 'conv':
+            want = _prod(op['in_shape'])
+            if w != want:
+                raise ValueError(f'conv {name!r}: input of {w} values per domain, '
+                                 f'in_shape {tuple(op["in_shape"])} holds {want}')
+            width[name] = _prod(op['out_shape'])
+        elif t == 'add' and op.get('is_merge'):
+            w2 = width[op['inputs'][1]]
+            if w2 != w:
+                raise ValueError(f'add {name!r}: merges widths {w} and {w2}')
+            width[name] = w
+        elif t in ('relu', 'reshape', 'add', 'sub', 'mul'):
+            width[name] = w
+        else:
+            _unsupported('validate_gg', op)
+    return width
+
+
+def _widths(gg, n_in):
+    """validate_gg for a call on inputs of n_in values per domain, cached on
+    the gg for its op list and input width."""
+    key = (id(gg['ops']), len(gg['ops']), int(n_in))
+    hit = gg.get('_vc_amd_widths')
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    w = validate_gg(gg, n_in)
+    gg['_vc_amd_widths'] = (key, w)
+    return w
+
+
 def _conv_t_taps(p, st):
     """The conv kernel's transposed taps packed per output-parity class
     (vc_conv_t_pack), made on first use by a backward pass and cached with
@@ -231,6 +322,7 @@ def _ibp_forward_graph_batched(xl, xh, gg, device, dtype, relu_clamps=None,
     xl, xh = f32(xl), f32(xh)
     B = xl.shape[0]
     dev = xl.device
+    widths = _widths(gg, xl.shape[1])
     lo = {gg['input_name']: xl}
     hi = {gg['input_name']: xh}
     sb = {}
@@ -240,6 +332,12 @@ def _ibp_forward_graph_batched(xl, xh, gg, device, dtype, relu_clamps=None,
         name = op['name']
         l, h = lo[op['inputs'][0]], hi[op['inputs'][0]]
         if t == 'fc':
+            if _fc_form(op, widths[op['inputs'][0]])[0] > 1:
+                # the reference's interval fc is mid @ W.T (verify_zono_bnb.py:
+                # 1108-1113), which has no N-D MatMul form
+                raise NotImplementedError(
+                    f'_ibp_forward_graph_batched: fc {name!r} is an N-D batched MatMul, '
+                    f'which the interval forward does not take')
             p = _op_params(op, dev)
             lo_o = torch.empty(B, p['n_out'], device=dev)
             hi_o = torch.empty_like(lo_o)
@@ -329,6 +427,7 @@ def _forward_zonotope_graph_batched(xl, xh, gg, device, dtype):
     B, n_in = xl.shape
     dev = xl.device
     st = stream()
+    widths = _widths(gg, n_in)
     varying = ((xh - xl) / 2).abs().amax(dim=0) > 0 if B > 0 else \
         torch.zeros(n_in, dtype=torch.bool, device=dev)
     vidx = varying.nonzero(as_tuple=True)[0].to(torch.int32).contiguous()
@@ -381,9 +480,13 @@ def _forward_zonotope_graph_batched(xl, xh, gg, device, dtype):
             state[name] = (c_o, G_o)
         elif t == 'fc':
             p = _op_params(op, dev)
-            c_o = torch.empty(B, p['n_out'], device=dev)
-            G_o = torch.empty(B, p['n_out'], Kc, device=dev)
-            call('vc_zono_fc', ptr(c_in), ptr(G_in), B, p['n_in'], Kc,
+            # the N-D MatMul form (verify_zono_bnb.py:3145-3168) applies W to
+            # each of P slices: (B, P * n_in) centres and (B, P * n_in, K)
+            # generators are (B * P, n_in) and (B * P, n_in, K) as they lie
+            P, _ = _fc_form(op, widths[op['inputs'][0]])
+            c_o = torch.empty(B, P * p['n_out'], device=dev)
+            G_o = torch.empty(B, P * p['n_out'], Kc, device=dev)
+            call('vc_zono_fc', ptr(c_in), ptr(G_in), B * P, p['n_in'], Kc,
                  ptr(p['W']), ptr(p['b']), p['n_out'], ptr(c_o), ptr(G_o), st)
             state[name] = (c_o, G_o)
         elif t == 'conv':
@@ -480,6 +583,7 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
     B, n_in = xl.shape
     dev = xl.device
     st = stream()
+    widths = _widths(gg, n_in)
     R = seed.shape[0] if seed_shared else seed.shape[0] // max(B, 1)
     acc = acc0.clone()
     acc_shared = seed_shared
@@ -606,6 +710,30 @@ def _backward(tight, xl, xh, gg, seed_name, seed, seed_shared, acc0,
             out = torch.empty_like(rows.ew)
             call('vc_affine_ew', ptr(rows.ew), rows.ew.shape[0], rows.ew.shape[1], 1, ptr(s),
                  s.numel(), 2, ptr(out), st)
+            put(inp, _Rows(out, rows.shared))
+        elif t == 'fc' and _fc_form(op, widths[inp])[0] > 1:
+            # N-D batched MatMul (verify_zono_bnb.py:4382-4401): acc += the
+            # rows . bias repeated over the P slices, then each row's P
+            # slices of n_out times W, as (M * P, n_out) rows
+            P, nd_out = _fc_form(op, widths[inp])
+            if not nd_out:
+                raise NotImplementedError(
+                    f'batched spec backward: fc {name!r} is an N-D batched MatMul '
+                    f'without out_shape_nd')
+            if trace is not None:
+                trace.other = trace.other or 'N-D fc'
+            p = _op_params(op, dev)
+            rows = materialize(rows)
+            if p['b'] is not None:
+                key = ('b_rep', P)
+                if key not in p:
+                    p[key] = p['b'].repeat(P).contiguous()
+                bias_dot(rows, p[key], 1.0)
+            M = rows.ew.shape[0]
+            out = torch.empty(M, P * p['n_in'], device=dev)
+            call('vc_backward_fc', ptr(rows.ew), M * P, R * P, p['n_out'], None,
+                 None, None, 0, None, ptr(p['W']), None, p['n_in'], ptr(out), None,
+                 None, 0, st)
             put(inp, _Rows(out, rows.shared))
         elif t == 'fc':
             p = _op_params(op, dev)
@@ -757,6 +885,7 @@ def _spec_backward_graph_batched(tight, xl, xh, gg, spec_ew, device, dtype,
             'vibecheck_amd: bilinear / reciprocal relaxations are not '
             'supported (Linear/Conv/ReLU networks only)')
     xl, xh = f32(xl), f32(xh)
+    _widths(gg, xl.shape[1])
     B, n_in = xl.shape
     dev = xl.device
     plan = _plan(gg, dev)
@@ -822,6 +951,7 @@ def _crown_intermediate_batched(gg, xl, xh, device, dtype, chunk=2048,
     """
     _check_dtype(dtype)
     xl, xh = f32(xl), f32(xh)
+    _widths(gg, xl.shape[1])
     dev = xl.device
     if sb is None:
         sb = _zono_sb(gg, xl, xh, device, dtype)
@@ -972,6 +1102,7 @@ def _run_alpha_crown_inputsplit_batched(xl, xh, gg, spec_ew, device, dtype,
     """
     _check_dtype(dtype)
     xl, xh = f32(xl), f32(xh)
+    _widths(gg, xl.shape[1])
     B = xl.shape[0]
     dev = xl.device
     st = stream()
