@@ -598,7 +598,8 @@ int vc_mlp_tiled_crown(const int32_t *dims, int n_relu, const float *frag,
  * idx_all/idx_meta: the union lists of vc_union_compact, or null: then the
  * union of the neurons unstable in some domain (lo < 0 < hi) is formed here,
  * in the same pass over the bounds that builds the per-domain seed masks
- * (the same union, so the same results).  B < 2^24.  Replaces
+ * (the same union, so the same results).  B < 2^24; the workspace size is
+ * -VC_ERR_UNSUPPORTED past it, and callers then take vc_mlp_tiled_crown.  Replaces
  * _crown_intermediate_batched + the spec backward (verify_zono_bnb.py:
  * 4077-4147, 4270-4453, 5117-5134) for narrow MLPs. */
 int64_t vc_mlp_crown_rows_workspace(const int32_t *dims, int n_relu, int64_t B);
@@ -881,13 +882,27 @@ int vc_best_rows_with_A(float *best, const float *lb, float *best_A,
  * vc_mlp_bab_round_workspace(dims, n_relu, B, Q) bytes of device memory;
  * stop_host: as for vc_mlp_tiled_alpha_run.  seed_rows (nullable): as for
  * vc_mlp_tiled_crown; crown_ev0/crown_ev1 (nullable hipEvent_t): recorded
- * on `stream` around the vc_mlp_tiled_crown call (its timing).  pinned
- * (nullable, pinned host memory, >= 2 int64): the GPU stores each count
- * there and the host polls it (bounded, then a stream synchronisation)
- * instead of a device-to-host copy and a synchronisation.  VC_ERR_UNSUPPORTED when the
- * net can have more zonotope generators than VC_ZONO_WIDE_COLS.
- * Replaces one iteration of _input_split_batched_inner's loop body
- * (verify_graph.py:12855-13382), as bab_step restates it. */
+ * on `stream` around the vc_mlp_tiled_crown call (its timing).  phase_ev
+ * (nullable, 5 hipEvent_t): recorded on `stream` at the round's start and
+ * at the end of its bound (zonotope, CROWN, closure), alpha (with the
+ * closure of the raised rows), clip (unclosed compaction, clip, widest
+ * axis, feasible compaction and gather) and split (bisection) phases: the
+ * driver's per-phase profile without a synchronisation per phase
+ * (verify_graph.py:12814-12833, 12984-12985, 13227-13228, 13430-13433).
+ * clip_widths (nullable, device double[2], zeroed by the caller):
+ * += the sums of max(xh - xl, 0) over the unclosed leaves before and after
+ * the clip (the profile's shrink ratio, verify_graph.py:13108-13113).
+ * pinned (nullable, pinned host memory, >= 2 int64): the GPU stores each
+ * count there and the host polls it (bounded, then a stream
+ * synchronisation) instead of a device-to-host copy and a
+ * synchronisation.  fail_phase (nullable host int32): -1 on success, else
+ * the phase whose step returned the error (0 bound, 1 alpha, 2 clip,
+ * 3 split): the driver halves the batch only on the bound phase's errors
+ * (verify_graph.py:12853-12897), and alpha's keep the CROWN bound
+ * (:12962-12969).  VC_ERR_UNSUPPORTED when the net can have more zonotope
+ * generators than VC_ZONO_WIDE_COLS.  Replaces one iteration of
+ * _input_split_batched_inner's loop body (verify_graph.py:12855-13382),
+ * as bab_step restates it. */
 int64_t vc_mlp_bab_round_workspace(const int32_t *dims, int n_relu, int64_t B,
                                    int Q);
 int vc_mlp_bab_round(const int32_t *dims, int n_relu, const float *frag,
@@ -901,8 +916,9 @@ int vc_mlp_bab_round(const int32_t *dims, int n_relu, const float *frag,
                      float *xl_split, float *xh_split, int64_t *ax,
                      float *low_xl, float *low_xh, float *high_xl,
                      float *high_xh, uint64_t *seed_rows, void *crown_ev0,
-                     void *crown_ev1, void *work, int64_t work_bytes,
-                     int32_t *stop_host, int64_t *pinned, int64_t *counts,
+                     void *crown_ev1, void *const *phase_ev, double *clip_widths,
+                     void *work, int64_t work_bytes, int32_t *stop_host,
+                     int64_t *pinned, int64_t *counts, int32_t *fail_phase,
                      vc_stream_t stream);
 
 #ifdef __cplusplus

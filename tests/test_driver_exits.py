@@ -129,3 +129,20 @@ def test_clip_iters_setting_reaches_the_step(driver):
     assert calls == [(1, 4)]
     _, _, calls = driver(lambda k, B: 'close')
     assert calls == [(1, 1)]
+
+
+def test_errors_after_the_bound_phase_propagate(driver):
+    """The reference's try covers the bound phase only (verify_graph.py:
+    12853-12897): a clip- or split-phase error (the step tags it with
+    vc_phase) ends the run with that error instead of halving the batch."""
+    for phase in ('clip', 'split'):
+        err = vg._tag_phase(RuntimeError('clip kernel failed'), phase)
+        assert err.vc_phase == phase
+        with pytest.raises(RuntimeError, match='clip kernel failed'):
+            driver(lambda k, B: err)
+    # an error tagged once keeps its first phase
+    err = vg._tag_phase(vg._tag_phase(RuntimeError('x'), 'split'), 'clip')
+    assert err.vc_phase == 'split'
+    # untagged (bound phase): halves as before
+    verdict, det, calls = driver(lambda k, B: RuntimeError('bound'), input_split_batch_size=4)
+    assert verdict == 'unknown' and len(calls) == 3

@@ -270,3 +270,31 @@ def test_onnx_synthetic_residual_and_affine_ops():
     ref = t7 @ f(W3)
     got, _ = rb.point_forward(torch.tensor(x), gg)
     assert np.allclose(got.numpy(), ref, rtol=1e-9, atol=1e-9)
+
+
+def test_onnx_constant_with_a_batch_axis():
+    """A per-channel constant exported with a leading batch axis, (1, C, 1,
+    1), against a computed (C, H, W) tensor is read as the channel vector
+    (the exporter's batch axis dropped); one that does not broadcast is
+    refused with NotImplementedError, not a numpy ValueError."""
+    rng = np.random.default_rng(3)
+    K = rng.standard_normal((3, 2, 3, 3)).astype(np.float32)
+    cb = rng.standard_normal((1, 3, 1, 1)).astype(np.float32)
+    G = rng.standard_normal((2, 3 * 9)).astype(np.float32)
+
+    def model(c):
+        nodes = [_node('Conv', ['input', 'K'], ['t1'], pads=[1, 1, 1, 1], kernel_shape=[3, 3]),
+                 _node('Add', ['t1', 'cb'], ['t2']), _node('Relu', ['t2'], ['t3']),
+                 _node('Flatten', ['t3'], ['t4'], axis=1),
+                 _node('Gemm', ['t4', 'G'], ['out'], transB=1)]
+        return _model(nodes, dict(K=K, cb=c, G=G), [1, 2, 3, 3])
+
+    gg = onnx_net.onnx_to_gg(model(cb), dtype=torch.float64)
+    x = rng.random((1, 2, 3, 3))
+    h = np.maximum(_np_conv(x[0], K.astype(np.float64), np.zeros(3), 1, 1)
+                   + cb[0].astype(np.float64), 0)
+    ref = h.reshape(-1) @ G.T.astype(np.float64)
+    got, _ = rb.point_forward(torch.tensor(x.reshape(1, -1)), gg)
+    assert np.allclose(got.numpy()[0], ref, rtol=1e-9, atol=1e-9)
+    with pytest.raises(NotImplementedError):
+        onnx_net.onnx_to_gg(model(np.ones((1, 4, 1, 1), dtype=np.float32)))

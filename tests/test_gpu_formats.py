@@ -70,3 +70,41 @@ def test_acasxu_prop1_verified_with_sb_branching(gpu, margin, depth):
     verdict, details = vg._input_split_batched(None, spec, settings, gg, gpu, F32)
     print(f'prop_1 SB (margin={margin}, K={depth}): {verdict} {details}')
     assert verdict == 'verified', details
+
+
+@pytest.mark.parametrize('native', [True, False])
+def test_acasxu_prop1_phase_timing(gpu, monkeypatch, native, capsys):
+    """The driver's per-phase profile (input_split_batched_phase_timing,
+    verify_graph.py:12814-12833, 13436-13450) from the native round's own
+    HIP events, and from the Python round's: the run pops the same leaves as
+    without it; every popped leaf is closed by the bound, closed by the
+    clip, or split in two, so with 253 leaves from one root (126 splits)
+    the two closure counts sum to 127, and the bound's closures are the
+    oracle driver's per-iteration closures summed; the phase times are
+    positive and within the run's wall time; the clip's width ratio is in
+    [0, 1]."""
+    monkeypatch.setattr(vg, 'NATIVE_ROUND', native)
+    gg = onnx_net.load_onnx(NET, device=gpu, dtype=F32)
+    spec = vnnlib.load_vnnlib(os.path.join(GOLD, 'prop_1.vnnlib'))
+    settings = dict(SETTINGS, input_split_batched_phase_timing=True)
+    verdict, details = vg._input_split_batched(None, spec, settings, gg, gpu, F32)
+    out = capsys.readouterr().out
+    assert '[vc-phase] BAB total=' in out and '[vc-phase] closures: crown=' in out
+    assert verdict == 'verified', details
+    assert (details['batched_n_leaves'], details['batched_n_iters']) == (253, 11)
+    pt = details['phase_timing']
+    print(pt)
+    assert pt['crown_closed'] + pt['clip_closed'] == 127
+    uq, dq = dedup_queries(spec.as_linear_queries(5))
+    se = {i: (torch.tensor(w, dtype=F32), b) for i, (w, b) in enumerate(uq)}
+    _, _, trace = rbab.input_split_batched(
+        torch.tensor(spec.x_lo, dtype=F32), torch.tensor(spec.x_hi, dtype=F32),
+        onnx_net.load_onnx(NET, dtype=F32), se, dq, batch_size=4096)
+    assert pt['crown_closed'] == sum(t['n_closed'] for t in trace)
+    for k in ('bound', 'clip', 'split'):
+        assert 0.0 < pt[k] < pt['total'], (k, pt)
+    assert 0.0 <= pt['alpha'] <= pt['bound']
+    assert pt['bound'] + pt['clip'] + pt['split'] <= pt['total']
+    if native:
+        assert pt['clip_shrink_n'] >= 1
+        assert 0.0 <= pt['clip_shrink_sum'] / pt['clip_shrink_n'] <= 1.0

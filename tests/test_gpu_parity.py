@@ -1036,9 +1036,12 @@ def test_bab_round_native_matches_python_round(gpu, B, alpha_iters):
     for L in sorted(sb)[:-1]:
         cols = cols + ((sb[L][0] < 0) & (sb[L][1] > 0)).sum(1)
     assert int((cols > 128).sum()) > 0
-    _, se_g, dq = spec_pair(5, gpu)
+    _native_round_vs_python(gpu, gg_g, xl.to(gpu), xh.to(gpu), 5, alpha_iters)
+
+
+def _native_round_vs_python(gpu, gg_g, xl, xh, n_out, alpha_iters):
+    _, se_g, dq = spec_pair(n_out, gpu)
     table = vg.DisjunctTable(dq, gpu)
-    xl, xh = xl.to(gpu), xh.to(gpu)
     res = {}
     old = vg.NATIVE_ROUND
     try:
@@ -1061,6 +1064,24 @@ def test_bab_round_native_matches_python_round(gpu, B, alpha_iters):
         assert torch.equal(a['feasible'], b['feasible'])
     for x, y in zip(a['low'] + a['high'], b['low'] + b['high']):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize('net', [[5, 64, 64, 64, 5], [3, 12, 12, 2], [7, 30, 30, 30, 3],
+                                 [4, 44, 44, 4]])
+@pytest.mark.parametrize('B,alpha_iters', [(1500, 0), (1500, 10), (500, 10)])
+def test_bab_round_native_matches_python_round_nets(gpu, net, B, alpha_iters):
+    """The native round against the Python round on nets of every tile
+    shape (16, 32, 48 and 64 neurons; 64 leaves no spare bias row), at a
+    batch above 4 x CUs (the rows pass, its seed masks and union from the
+    zonotope passes) and below (k_crown_dom with the union from the
+    zonotope passes), with and without alpha: every output equal bit for
+    bit, every count equal."""
+    from vibecheck_amd import _lib, mlp_fused as mf
+    gg, xl, xh, n_out = _rows_case(gpu, net, B, 2.0)
+    plan = mf.plan_for(gg, gpu)
+    assert plan is not None and mf._tiled(plan)
+    assert (_lib.load().vc_mlp_tiled_crown_mode(B) == 0) == (B > 1024)
+    _native_round_vs_python(gpu, gg, xl, xh, n_out, alpha_iters)
 
 
 def test_bab_step_parity_c0(gpu, mlp_path):

@@ -76,10 +76,13 @@ def test_crown_noalloc_matches_allocating_path(gpu, per_domain):
 
 
 def test_crown_noalloc_refuses_nets_beyond_its_scratch(gpu):
-    # 17 ReLU layers of 64: more than the 1024 union entries the array holds
-    dims = host_array(ctypes.c_int32, [5] + [64] * 17)
+    """Both refusals come before any pointer is read or kernel launched:
+    17 ReLU layers exceed the layer limit (16); 16 layers of 65 neurons
+    (1,040 union entries) exceed the 1,024 (16 x 64) the array holds."""
     from vibecheck_amd import _lib
-    rc = _lib.load().vc_mlp_tiled_crown_noalloc(
-        dims[1], 17, None, None, 1, None, None, None, None, None, None, 1, 0, 4, None, None,
-        None, None, None, None)
-    assert rc == _lib.VC_ERR_UNSUPPORTED
+    for widths in ([64] * 17, [65] * 16):
+        dims = host_array(ctypes.c_int32, [5] + widths)
+        rc = _lib.load().vc_mlp_tiled_crown_noalloc(
+            dims[1], len(widths), None, None, 1, None, None, None, None, None, None, 1, 0, 4,
+            None, None, None, None, None, None)
+        assert rc == _lib.VC_ERR_UNSUPPORTED, widths

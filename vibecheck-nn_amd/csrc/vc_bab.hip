@@ -149,6 +149,28 @@ int read_counts(const int64_t* dev, int k, int64_t* host, int64_t* pinned, hipSt
   return hipStreamSynchronize(st) == hipSuccess ? VC_OK : VC_ERR_LAUNCH;
 }
 
+// Clip shrink accounting of the phase timer: w[0] += sum of max(xh - xl, 0)
+// over the n values before the clip, w[1] += the same after it.  Double
+// atomics per wavefront (any order: a profiling ratio, not a bound).
+__global__ void k_clip_widths(const float* __restrict__ xl, const float* __restrict__ xh,
+                              const float* __restrict__ cl, const float* __restrict__ ch,
+                              int64_t n, double* w) {
+  double a = 0.0, b = 0.0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    a += (double)fmaxf(xh[i] - xl[i], 0.0f);
+    b += (double)fmaxf(ch[i] - cl[i], 0.0f);
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    a += __shfl_down(a, o, 64);
+    b += __shfl_down(b, o, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicAdd(w, a);
+    atomicAdd(w + 1, b);
+  }
+}
+
 // vc_gather_rows_multi in launches of at most 32 arrays.
 int gather(const float* const* in, float* const* out, const int32_t* cols, int n_arrays,
            const int64_t* idx, int64_t n_rows, vc_stream_t stream) {
@@ -177,18 +199,29 @@ extern "C" int64_t vc_mlp_bab_round_workspace(const int32_t* dims, int n_relu, i
   return (int64_t)c.used;
 }
 
-extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* frag,
-                                const float* bias_cat, int Q, const float* spec_rows,
-                                const float* spec_acc, const int32_t* d_ptr,
-                                const int32_t* q_idx, int n_disj, int64_t B, const float* xl,
-                                const float* xh, int alpha_iters, double alpha_lr,
-                                double alpha_lr_decay, double alpha_early_stop, float* lb,
-                                float* A, float* acc, uint8_t* closed, int64_t* unclosed,
-                                uint8_t* feasible, float* xl_split, float* xh_split, int64_t* ax,
-                                float* low_xl, float* low_xh, float* high_xl, float* high_xh,
-                                uint64_t* seed_rows, void* crown_ev0, void* crown_ev1,
-                                void* work, int64_t work_bytes, int32_t* stop_host,
-                                int64_t* pinned, int64_t* counts, vc_stream_t stream) {
+namespace {
+
+// The round's phases, in the order the phase timer's events close them.
+enum RoundPhase { PH_BOUND = 0, PH_ALPHA = 1, PH_CLIP = 2, PH_SPLIT = 3 };
+
+// Records phase event k (0: round start; 1..4: end of bound, alpha, clip,
+// split) when the caller asked for them.
+int mark(void* const* phase_ev, int k, hipStream_t st) {
+  if (!phase_ev) return VC_OK;
+  return hipEventRecord((hipEvent_t)phase_ev[k], st) == hipSuccess ? VC_OK : VC_ERR_LAUNCH;
+}
+
+int bab_round(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat, int Q,
+              const float* spec_rows, const float* spec_acc, const int32_t* d_ptr,
+              const int32_t* q_idx, int n_disj, int64_t B, const float* xl, const float* xh,
+              int alpha_iters, double alpha_lr, double alpha_lr_decay, double alpha_early_stop,
+              float* lb, float* A, float* acc, uint8_t* closed, int64_t* unclosed,
+              uint8_t* feasible, float* xl_split, float* xh_split, int64_t* ax, float* low_xl,
+              float* low_xh, float* high_xl, float* high_xh, uint64_t* seed_rows,
+              void* crown_ev0, void* crown_ev1, void* const* phase_ev, double* clip_widths,
+              void* work, int64_t work_bytes, int32_t* stop_host, int64_t* pinned,
+              int64_t* counts, int& phase, vc_stream_t stream) {
+  phase = PH_BOUND;
   if (!dims || !frag || !bias_cat || !spec_rows || !spec_acc || !d_ptr || !q_idx || !xl ||
       !xh || !lb || !A || !acc || !closed || !unclosed || !feasible || !xl_split ||
       !xh_split || !ax || !low_xl || !low_xh || !high_xl || !high_xh || !work || !counts)
@@ -205,8 +238,12 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
   for (int l = 0; l < n; ++l) max_cols += dims[l];
   if (max_cols > VC_ZONO_WIDE_COLS) return VC_ERR_UNSUPPORTED;
   for (int k = 0; k < 6; ++k) counts[k] = 0;
-  if (B == 0) return VC_OK;
   hipStream_t st = (hipStream_t)stream;
+  VC_TRY(mark(phase_ev, 0, st));
+  if (B == 0) {
+    for (int k = 1; k <= 4; ++k) VC_TRY(mark(phase_ev, k, st));
+    return VC_OK;
+  }
   Carve c{reinterpret_cast<char*>(work), 0};
   RoundBufs r;
   carve(c, r, dims, n, B, Q);
@@ -247,8 +284,10 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
     VC_TRY(vcm::closure_open(lb, B, Q, d_ptr, q_idx, n_disj, closed, r.idx, r.cnt + 3, st));
   else
     VC_TRY(vc_closure(lb, B, Q, d_ptr, q_idx, n_disj, closed, stream));
+  VC_TRY(mark(phase_ev, 1, st));
 
   // ---- alpha-CROWN on the open leaves, from their zonotope bounds
+  phase = PH_ALPHA;
   int64_t n_open = 0, n_eval = 0;
   if (alpha_iters > 0) {
     VC_TRY(read_counts(r.cnt + 3, 1, &n_open, pinned, st));
@@ -292,7 +331,10 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
     }
   }
 
+  VC_TRY(mark(phase_ev, 2, st));
+
   // ---- the unclosed leaves (and alpha's evaluation count with them)
+  phase = PH_CLIP;
   VC_TRY(vc_compact(closed, B, 1, unclosed, r.cnt, r.cws, r.cws_bytes, stream));
   int64_t n_unc = 0;
   if (n_open > 0) {
@@ -313,6 +355,13 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
     VC_TRY(gather(gin, gout, gcols, 4, unclosed, n_unc, stream));
     VC_TRY(vc_clip_box(r.u_xl, r.u_xh, r.u_A, r.u_acc, n_unc, Q, n_in, d_ptr, q_idx, n_disj,
                        r.c_xl, r.c_xh, feasible, stream));
+    if (clip_widths) {
+      const int64_t nv = n_unc * n_in;
+      const int blocks = (int)std::min<int64_t>((nv + 255) / 256, 1024);
+      hipLaunchKernelGGL(k_clip_widths, dim3(blocks), dim3(256), 0, st, r.u_xl, r.u_xh, r.c_xl,
+                         r.c_xh, nv, clip_widths);
+      if (hipGetLastError() != hipSuccess) return VC_ERR_LAUNCH;
+    }
     VC_TRY(vc_widest_axis(r.c_xl, r.c_xh, n_unc, n_in, r.ax_u, r.usable, stream));
     // the feasible leaves, and the feasible ones with a usable split axis
     VC_TRY(vcm::compact_feasible_split(feasible, r.usable, n_unc, r.idx, r.cnt, r.idx2,
@@ -328,10 +377,13 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
       const int32_t fcols[3] = {n_in, n_in, 2};
       VC_TRY(gather(fin, fout, fcols, 3, r.idx, nf, stream));
     }
-    if (nu > 0)
-      VC_TRY(vc_bisect(r.c_xl, r.c_xh, r.ax_u, r.idx2, nu, n_in, low_xl, low_xh, high_xl,
-                       high_xh, stream));
   }
+  VC_TRY(mark(phase_ev, 3, st));
+  phase = PH_SPLIT;
+  if (nu > 0)
+    VC_TRY(vc_bisect(r.c_xl, r.c_xh, r.ax_u, r.idx2, nu, n_in, low_xl, low_xh, high_xl,
+                     high_xh, stream));
+  VC_TRY(mark(phase_ev, 4, st));
   counts[0] = n_open;
   counts[1] = n_eval;
   counts[2] = n_unc;
@@ -339,4 +391,30 @@ extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* fr
   counts[4] = nu;
   counts[5] = nf - nu;
   return VC_OK;
+}
+
+}  // namespace
+
+extern "C" int vc_mlp_bab_round(const int32_t* dims, int n_relu, const float* frag,
+                                const float* bias_cat, int Q, const float* spec_rows,
+                                const float* spec_acc, const int32_t* d_ptr,
+                                const int32_t* q_idx, int n_disj, int64_t B, const float* xl,
+                                const float* xh, int alpha_iters, double alpha_lr,
+                                double alpha_lr_decay, double alpha_early_stop, float* lb,
+                                float* A, float* acc, uint8_t* closed, int64_t* unclosed,
+                                uint8_t* feasible, float* xl_split, float* xh_split, int64_t* ax,
+                                float* low_xl, float* low_xh, float* high_xl, float* high_xh,
+                                uint64_t* seed_rows, void* crown_ev0, void* crown_ev1,
+                                void* const* phase_ev, double* clip_widths, void* work,
+                                int64_t work_bytes, int32_t* stop_host, int64_t* pinned,
+                                int64_t* counts, int32_t* fail_phase, vc_stream_t stream) {
+  int phase = PH_BOUND;
+  const int rc = bab_round(dims, n_relu, frag, bias_cat, Q, spec_rows, spec_acc, d_ptr, q_idx,
+                           n_disj, B, xl, xh, alpha_iters, alpha_lr, alpha_lr_decay,
+                           alpha_early_stop, lb, A, acc, closed, unclosed, feasible, xl_split,
+                           xh_split, ax, low_xl, low_xh, high_xl, high_xh, seed_rows,
+                           crown_ev0, crown_ev1, phase_ev, clip_widths, work, work_bytes,
+                           stop_host, pinned, counts, phase, stream);
+  if (fail_phase) *fail_phase = rc == VC_OK ? -1 : phase;
+  return rc;
 }

@@ -2591,6 +2591,10 @@ extern "C" int64_t vc_mlp_crown_rows_workspace(const int32_t* dims, int n_relu, 
   const int rc = tiled_geom(dims, n_relu, G);
   if (rc != VC_OK) return -rc;
   if (B < 0) return -VC_ERR_ARG;
+  // the batch limit of crown_rows_run (int32 row offsets, 25-bit domain in
+  // the row codes): callers that size a workspace here fall back to the
+  // one-wavefront-per-domain CROWN instead
+  if (B >= ((int64_t)1 << 24)) return -VC_ERR_UNSUPPORTED;
   int maxw = 1;
   for (int l = 1; l <= n_relu; ++l) maxw = G.d[l] > maxw ? G.d[l] : maxw;
   return (int64_t)rows_carve(nullptr, n_relu, maxw, B).bytes;

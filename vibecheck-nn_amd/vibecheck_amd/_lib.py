@@ -120,7 +120,7 @@ SIGNATURES = {
     'vc_mlp_bab_round_workspace': [_P, _I, _L, _I],
     'vc_mlp_bab_round': [_P, _I, _P, _P, _I, _P, _P, _P, _P, _I, _L, _P, _P, _I, _D, _D, _D,
                          _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                         _L, _P, _P, _P, _P],
+                         _P, _P, _L, _P, _P, _P, _P, _P],
     'vc_widest_axis': [_P, _P, _L, _I, _P, _P, _P],
     'vc_bisect': [_P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P],
 }

@@ -105,6 +105,13 @@ def _eligible(gg):
     ops = gg['ops']
     if len(ops) < 3 or len(ops) % 2 == 0:
         return False
+    # widths chained op by op (ValueError on a mismatch); the N-D MatMul
+    # form of an fc is left to the layer-wise kernels
+    from .verify_zono_bnb import _fc_form, validate_gg
+    widths = validate_gg(gg)
+    if any(op['type'] == 'fc' and _fc_form(op, widths[op['inputs'][0]])[0] > 1
+           for op in ops):
+        return False
     prev = gg['input_name']
     n_relu = 0
     for k, op in enumerate(ops):
@@ -370,6 +377,9 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False, per_domain=F
     tiled = _tiled(plan)
     lib = _lib.load()
     rows = tiled and ROWS and lib.vc_mlp_tiled_crown_mode(B) == 0
+    # the rows form's workspace size is negative past its batch limit
+    nws = int(lib.vc_mlp_crown_rows_workspace(plan.dims_p, plan.n, B)) if rows else 0
+    rows = rows and nws >= 0
     if do_crown:
         if rows and ROWS_OWN_UNION:
             pass  # the rows form builds the union in its own pass over the bounds
@@ -410,7 +420,6 @@ def crown(plan, xl, xh, sb, do_crown, spec=None, want_linear=False, per_domain=F
             seeds = SEED_COUNTER[SEED_ROW]
             SEED_ROW += 1
         if rows:
-            nws = int(lib.vc_mlp_crown_rows_workspace(plan.dims_p, plan.n, B))
             ws = torch.empty(max(nws, 8), dtype=torch.uint8, device=dev)
             call('vc_mlp_crown_rows', plan.dims_p, plan.n, ptr(plan.tfrag), ptr(plan.bias_cat),
                  B, ptr(xl), ptr(xh), lin_p, hin_p, lout_p, hout_p, ptr(idx_t), cnt_p,

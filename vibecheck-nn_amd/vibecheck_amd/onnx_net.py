@@ -194,6 +194,22 @@ def read_model(data):
 
 
 # ---------------------------------------------------------------- gg build
+def _broadcast_const(c, shape):
+    """An elementwise constant spelled out over a tensor of ``shape`` (the
+    batch dim excluded), flattened.  Leading size-1 axes beyond the
+    tensor's rank are the exporter's batch axis, e.g. (1, C, 1, 1) against
+    (C, H, W), and are dropped first; any other shape that numpy does not
+    broadcast raises NotImplementedError."""
+    c = np.asarray(c, dtype=np.float64)
+    while c.ndim > len(shape) and c.shape[0] == 1:
+        c = c[0]
+    try:
+        return np.ascontiguousarray(np.broadcast_to(c, tuple(shape))).reshape(-1)
+    except ValueError:
+        raise NotImplementedError(f'onnx: constant of shape {c.shape} against a tensor '
+                                  f'of shape {tuple(shape)}') from None
+
+
 class _InputAffine:
     """The network input after elementwise constant ops: s * x + o."""
 
@@ -204,7 +220,7 @@ class _InputAffine:
         self.o = np.zeros(n)
 
     def apply(self, op, c):
-        c = np.broadcast_to(np.asarray(c, dtype=np.float64), self.shape).reshape(-1)
+        c = _broadcast_const(c, self.shape)
         if op == 'Sub':
             self.o = self.o - c
         elif op == 'Add':
@@ -359,8 +375,7 @@ def onnx_to_gg(data, device='cpu', dtype=torch.float32):
             live_first = xs[1][0] == 'const'
             name, shape = src(xs[0] if live_first else xs[1])
             c = np.asarray((xs[1] if live_first else xs[0])[1], dtype=np.float64)
-            flat = np.ascontiguousarray(np.broadcast_to(c, shape)).reshape(-1) \
-                if c.size != 1 else c.reshape(-1)
+            flat = _broadcast_const(c, shape) if c.size != 1 else c.reshape(-1)
             if op_type == 'Add':
                 r = add_op({'type': 'add', 'inputs': [name], 'is_merge': False, 'bias': flat})
             elif op_type == 'Sub' and live_first:

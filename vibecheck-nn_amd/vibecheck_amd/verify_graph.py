@@ -11,6 +11,7 @@ are supported; root/leaf PGD and LP/MILP escalation are not part of this
 engine.
 """
 import ctypes
+import os
 import time
 
 import torch
@@ -21,7 +22,7 @@ from .spec import dedup_queries
 from .verify_zono_bnb import (_bound_crown_spec,
                               _forward_zonotope_graph_batched,
                               _run_alpha_crown_inputsplit_batched,
-                              _spec_backward_graph_batched, _zono_sb)
+                              _spec_backward_graph_batched, _widths, _zono_sb)
 
 __all__ = ['_clip_box_by_halfspaces_batched', '_input_split_batched',
            'DisjunctTable', 'bab_step', 'ChunkWorklist']
@@ -287,7 +288,96 @@ class ChunkWorklist:
 NATIVE_ROUND = True
 
 
-def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_lr_decay):
+class PhaseTimer:
+    """The driver's per-phase profile (verify_graph.py:12814-12833,
+    13430-13450): bound (alpha-CROWN included, as in the reference), clip
+    and split time per BaB iteration, the closures by the bound (CROWN and
+    alpha) and by the clip, and the clip's mean after/before ratio of the
+    summed box widths.  Times come from HIP events recorded on the launch
+    stream at the phase boundaries (five per round; the native round
+    records them itself), read once by ``report``: no synchronisation per
+    phase, so the profiled run keeps the native round and its timing.
+    alpha's own share of the bound time is reported beside it."""
+
+    def __init__(self, device):
+        self.device = torch.device(device)
+        self.t0 = time.perf_counter()
+        self.rounds = []        # (5 events, widths tensor or None)
+        self.crown_closed = 0
+        self.clip_closed = 0
+
+    def begin(self, clip):
+        """Events and clip-width accumulator of one round."""
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        for e in ev:
+            e.record()      # creates the HIP event; the round records it again
+        w = torch.zeros(2, dtype=torch.float64, device=self.device) if clip else None
+        self.rounds.append((ev, w))
+        return ev, w
+
+    def closures(self, B, n_unclosed, n_feasible):
+        self.crown_closed += B - n_unclosed
+        if n_feasible is not None:
+            self.clip_closed += n_unclosed - n_feasible
+
+    def totals(self):
+        """{'bound', 'alpha', 'clip', 'split'} seconds, and the shrink
+        ratio's sum and count (synchronises once)."""
+        torch.cuda.synchronize(self.device)
+        t = {'bound': 0.0, 'alpha': 0.0, 'clip': 0.0, 'split': 0.0,
+             'clip_shrink_sum': 0.0, 'clip_shrink_n': 0}
+        for ev, w in self.rounds:
+            try:
+                d = [ev[k].elapsed_time(ev[k + 1]) * 1e-3 for k in range(4)]
+            except RuntimeError:
+                continue        # a round that ended in an error
+            t['bound'] += d[0] + d[1]
+            t['alpha'] += d[1]
+            t['clip'] += d[2]
+            t['split'] += d[3]
+            if w is not None:
+                wb, wa = (float(v) for v in w.cpu())
+                if wb > 0.0 or wa > 0.0:
+                    t['clip_shrink_sum'] += wa / max(wb, 1e-12)
+                    t['clip_shrink_n'] += 1
+        return t
+
+    def report(self, n_iters, n_leaves):
+        """Prints the reference's two profile lines (verify_graph.py:
+        13436-13450) and returns the totals."""
+        t = self.totals()
+        tot = max(time.perf_counter() - self.t0, 1e-12)
+        acct = t['bound'] + t['clip'] + t['split']
+        shrink = (t['clip_shrink_sum'] / t['clip_shrink_n'] if t['clip_shrink_n']
+                  else float('nan'))
+        print(f"[vc-phase] BAB total={tot:.2f}s | "
+              f"bound={t['bound']:.2f}s ({100 * t['bound'] / tot:.0f}%) "
+              f"clip={t['clip']:.2f}s ({100 * t['clip'] / tot:.0f}%) "
+              f"split={t['split']:.2f}s ({100 * t['split'] / tot:.0f}%) "
+              f"other={tot - acct:.2f}s ({100 * (tot - acct) / tot:.0f}%) | "
+              f"iters={n_iters} leaves={n_leaves} | alpha={t['alpha']:.3f}s of bound",
+              flush=True)
+        print(f"[vc-phase] closures: crown={self.crown_closed} clip={self.clip_closed} | "
+              f"clip avg post/pre box-width ratio={shrink:.4f} (1.0=no shrink) over "
+              f"{t['clip_shrink_n']} clip-iters", flush=True)
+        t.update(total=tot, crown_closed=self.crown_closed, clip_closed=self.clip_closed)
+        return t
+
+
+def _tag_phase(e, phase):
+    """Marks an error raised after the bound phase, which the driver does not
+    take for an OOM of the batch (the reference's try covers the bound
+    phase only, verify_graph.py:12853-12897)."""
+    if not hasattr(e, 'vc_phase'):
+        try:
+            e.vc_phase = phase
+        except AttributeError:
+            pass
+    return e
+
+
+def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_lr_decay,
+                      phase_timer=None):
     """bab_step's round (crown intermediate bounds, clip, alpha-CROWN on
     every open leaf) as one call of the native round orchestration, for
     nets with the shape-specialised kernels; None where it does not apply.
@@ -332,19 +422,39 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
         seeds = mlp_fused.SEED_COUNTER[seed_row]
         mlp_fused.SEED_ROW += 1
     ev = _lib.timing_events('vc_mlp_tiled_crown', B)
-    call('vc_mlp_bab_round', plan.dims_p, plan.n, plan.tfrag.data_ptr(),
-         plan.bias_cat.data_ptr(), Q, S.data_ptr(), acc0.data_ptr(), ptr(table.d_ptr),
-         ptr(table.q_idx), table.n, B, ptr(xl), ptr(xh), int(alpha_iters),
-         float(alpha_lr), float(alpha_lr_decay), 1e-6, p, p + 8 * Bm * Q, p + 4 * Bm * Q,
-         p + o_flg, p + o_idx, p + o_flg + Bm, p_box, p_box + nb, p + o_idx + 8 * Bm,
-         p_box + 2 * nb, p_box + 3 * nb, p_box + 4 * nb, p_box + 5 * nb, ptr(seeds),
-         ev[0].cuda_event if ev else None, ev[1].cuda_event if ev else None, ws.data_ptr(),
-         nws, mlp_fused._stop_word().data_ptr(), mlp_fused._pinned_words().data_ptr(),
-         ctypes.addressof(counts), stream())
+    pev_arr = pev_p = widths = None
+    if phase_timer is not None:
+        pev, widths = phase_timer.begin(clip=True)
+        pev_arr, pev_p = host_array(ctypes.c_void_p, [e.cuda_event for e in pev])
+    fail = ctypes.c_int32(-1)
+    try:
+        call('vc_mlp_bab_round', plan.dims_p, plan.n, plan.tfrag.data_ptr(),
+             plan.bias_cat.data_ptr(), Q, S.data_ptr(), acc0.data_ptr(), ptr(table.d_ptr),
+             ptr(table.q_idx), table.n, B, ptr(xl), ptr(xh), int(alpha_iters),
+             float(alpha_lr), float(alpha_lr_decay), 1e-6, p, p + 8 * Bm * Q, p + 4 * Bm * Q,
+             p + o_flg, p + o_idx, p + o_flg + Bm, p_box, p_box + nb, p + o_idx + 8 * Bm,
+             p_box + 2 * nb, p_box + 3 * nb, p_box + 4 * nb, p_box + 5 * nb, ptr(seeds),
+             ev[0].cuda_event if ev else None, ev[1].cuda_event if ev else None, pev_p,
+             ptr(widths), ws.data_ptr(), nws, mlp_fused._stop_word().data_ptr(),
+             mlp_fused._pinned_words().data_ptr(), ctypes.addressof(counts),
+             ctypes.addressof(fail), stream())
+    except RuntimeError as e:
+        if phase_timer is not None:
+            phase_timer.rounds.pop()
+        if fail.value == 1:
+            # alpha failed: the Python round redoes the step and keeps the
+            # CROWN bound there (verify_graph.py:12962-12969)
+            return None
+        if fail.value >= 2:
+            raise _tag_phase(e, 'clip' if fail.value == 2 else 'split')
+        raise
+    del pev_arr
     if ev:
         spec = _lib.mlp_crown_flops(plan.dims, plan.n, B, [0] * plan.n, 0, Q)
         _lib.timing_add('vc_mlp_tiled_crown', ev, spec, (None, None, None, None, B, seed_row))
     n_open, n_eval, n_unc, nf, nu, n_deg = (int(c) for c in counts)
+    if phase_timer is not None:
+        phase_timer.closures(B, n_unc, nf)
     # the views by absolute storage offsets (in elements of each dtype)
     fl = buf[:4 * nflt].view(torch.float32)
     i64 = buf[o_idx:o_idx + 16 * Bm].view(torch.int64)
@@ -388,7 +498,7 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
              clip_enabled=True, alpha_iters=0, alpha_all=False, alpha_eps=0.0,
              alpha_max_leaves=200, alpha_lr=0.25, alpha_lr_decay=0.98,
              timers=None, branch_sb=False, sb_margin=False, sb_thr=0.01, sb_mw=1.0,
-             split_depth=1, clip_iters=1):
+             split_depth=1, clip_iters=1, phase_timer=None):
     """One BaB iteration on a popped batch (verify_graph.py:12855-13423):
     bound, closure, optional alpha-CROWN on unclosed leaves (opportunistic:
     a RuntimeError or OOM inside it keeps the bound it had, as at
@@ -398,13 +508,20 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
     SB score (sum form, or ``sb_margin``); ``split_depth`` K > 1 (SB only)
     splits each leaf on its top K dimensions into 2^K children.  Returns a
     dict of device tensors (same keys as the oracle's bab_step; ``chunks``
-    are the worklist pushes in order)."""
+    are the worklist pushes in order).  ``phase_timer`` (a PhaseTimer)
+    records the round's phase events.  An error after the bound phase
+    carries ``vc_phase`` ('clip' or 'split')."""
+    _widths(gg, xl.shape[1])
     if (NATIVE_ROUND and timers is None and crown_intermediate and clip_enabled
             and (alpha_iters == 0 or alpha_all) and not branch_sb and clip_iters == 1):
         out = _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr,
-                                alpha_lr_decay)
+                                alpha_lr_decay, phase_timer)
         if out is not None:
             return out
+    pev = pw = None
+    if phase_timer is not None:
+        pev, pw = phase_timer.begin(clip=False)
+        pev[0].record()
     dev = xl.device
     dt = torch.float32
     sync_t = (lambda: (torch.cuda.synchronize(), time.perf_counter())[1]) \
@@ -429,6 +546,8 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
             lb = _spec_backward_graph_batched(sb, xl, xh, gg, spec_ew, dev, dt)
     lb = lb.contiguous()
     closed = _closure(lb, table)
+    if pev is not None:
+        pev[1].record()
     n_al = n_ait = 0
     if timers is not None:
         t1 = sync_t()
@@ -461,10 +580,26 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
                 call('vc_scatter_max_rows', ptr(lb), ptr(open_idx),
                      ptr(new.contiguous()), n_al, lb.shape[1], stream())
                 closed = _closure(lb, table)
+    if pev is not None:
+        pev[2].record()
     if timers is not None:
         t1 = sync_t()
         timers['alpha'] = timers.get('alpha', 0.0) + t1 - t0
         t0 = t1
+    try:
+        return _round_tail(xl, xh, lb, A, acc, closed, n_al, n_ait, table, clip_enabled,
+                           clip_iters, branch_sb, sb_margin, sb_thr, sb_mw, split_depth,
+                           timers, sync_t, t0 if timers is not None else None, pev,
+                           phase_timer)
+    except RuntimeError as e:
+        raise _tag_phase(e, 'clip')
+
+
+def _round_tail(xl, xh, lb, A, acc, closed, n_al, n_ait, table, clip_enabled, clip_iters,
+                branch_sb, sb_margin, sb_thr, sb_mw, split_depth, timers, sync_t, t0, pev,
+                phase_timer):
+    """bab_step after the bound and alpha phases: the unclosed leaves, the
+    clip and the split."""
     unclosed = _compact(closed, select_zero=True)
     # the alpha loop's evaluation count was copied to the host in stream
     # order: the compaction's read above has waited for it
@@ -475,6 +610,8 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
     if clip_enabled and unclosed.numel() > 0 and A is not None:
         xl_u, xh_u, A_u, acc_u, lb_u = _gather_many([xl, xh, A, acc, lb], unclosed)
         xl_c, xh_c, feas = _clip_iterated(xl_u, xh_u, A_u, acc_u, table, clip_iters)
+        if pev is not None:
+            pev[3].record()
         out['feasible'] = feas
         branch = ((A_u, lb_u, 2 if sb_margin else 1, sb_thr, sb_mw) if branch_sb
                   else None)
@@ -486,6 +623,8 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
     else:
         out['feasible'] = None
         xl_s, xh_s = _gather_many([xl, xh], unclosed)
+        if pev is not None:
+            pev[3].record()
         if timers is not None:
             t1 = sync_t()
             timers['clip'] = timers.get('clip', 0.0) + t1 - t0
@@ -500,6 +639,10 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
     else:
         low = high = (xl_s[:0], xh_s[:0])
     out.update(ax=ax, n_degenerate=n_deg, chunks=chunks, low=low, high=high)
+    if pev is not None:
+        pev[4].record()
+        phase_timer.closures(xl.shape[0], int(unclosed.numel()),
+                             int(xl_s.shape[0]) if out['feasible'] is not None else None)
     if timers is not None:
         timers['split'] = timers.get('split', 0.0) + sync_t() - t0
     return out
@@ -529,10 +672,17 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
     input_split_sb_margin_weight, bab_split_depth, input_split_batched_clip_iters,
     raise_on_oom.
 
-    A RuntimeError in a step (torch.cuda.OutOfMemoryError included) halves
-    the batch size and pushes the popped batch back; at batch size 1 a real
-    OOM is re-raised (unless raise_on_oom is off) and anything else ends the
-    run 'unknown' / batched_oom (verify_graph.py:12872-12897).
+    A RuntimeError in a step's bound phase (torch.cuda.OutOfMemoryError
+    included) halves the batch size and pushes the popped batch back; at
+    batch size 1 a real OOM is re-raised (unless raise_on_oom is off) and
+    anything else ends the run 'unknown' / batched_oom
+    (verify_graph.py:12872-12897).  Errors of the clip and split phases
+    propagate, as the reference's try covers the bound phase only.
+
+    With input_split_batched_phase_timing (or VC_PHASE_TIMING=1 in the
+    environment) the run prints the reference's per-phase profile
+    (verify_graph.py:12814-12833, 13436-13450) and returns it in the
+    details under 'phase_timing'.
     """
     if dtype != torch.float32:
         raise NotImplementedError('vibecheck_amd computes in fp32 only')
@@ -578,6 +728,16 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
     xh0 = torch.as_tensor(spec.x_hi, dtype=dtype, device=dev).flatten()
     wl = ChunkWorklist(xl0, xh0)
     n_leaves = n_iters = n_open = 0
+    pt = None
+    if (bool(_setting(settings, 'input_split_batched_phase_timing', False))
+            or os.environ.get('VC_PHASE_TIMING', '') == '1'):
+        pt = PhaseTimer(dev)
+
+    def done(verdict, details):
+        if pt is not None:
+            details['phase_timing'] = pt.report(n_iters, n_leaves)
+        return verdict, details
+
     while wl:
         if max_iters is not None and n_iters >= int(max_iters):
             break
@@ -596,9 +756,12 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
                           branch_sb=branch_sb, sb_margin=sb_margin,
                           sb_thr=sb_thr, sb_mw=sb_mw,
                           split_depth=split_depth if B < batch_size else 1,
-                          clip_iters=clip_iters)
+                          clip_iters=clip_iters, phase_timer=pt)
         except RuntimeError as e:
-            # torch.cuda.OutOfMemoryError is a RuntimeError
+            # torch.cuda.OutOfMemoryError is a RuntimeError; only the bound
+            # phase's errors halve the batch
+            if getattr(e, 'vc_phase', 'bound') != 'bound':
+                raise
             if torch.cuda.is_available():
                 torch.cuda.empty_cache()
             new_bs = max(1, batch_size // 2)
@@ -606,8 +769,8 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
                 if (isinstance(e, torch.cuda.OutOfMemoryError)
                         and bool(_setting(settings, 'raise_on_oom', True))):
                     raise
-                return 'unknown', {'phase': 'batched_oom',
-                                   'batch_size': batch_size}
+                return done('unknown', {'phase': 'batched_oom',
+                                        'batch_size': batch_size})
             wl.push(xl_b, xh_b)
             batch_size = new_bs
             continue
@@ -617,18 +780,18 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
             wl.push(*c)
         n_iters += 1
         if wl.size() > max_worklist:
-            return 'unknown', {'phase': 'batched_worklist_overflow',
-                               'batched_n_leaves': n_leaves,
-                               'batched_n_iters': n_iters,
-                               'worklist_size': wl.size()}
+            return done('unknown', {'phase': 'batched_worklist_overflow',
+                                    'batched_n_leaves': n_leaves,
+                                    'batched_n_iters': n_iters,
+                                    'worklist_size': wl.size()})
     if not wl and n_open == 0:
-        return 'verified', {'phase': 'batched_verified',
+        return done('verified', {'phase': 'batched_verified',
+                                 'batched_n_leaves': n_leaves,
+                                 'batched_n_iters': n_iters,
+                                 'batched_batch_size': batch_size})
+    return done('unknown', {'phase': 'batched_timeout',
                             'batched_n_leaves': n_leaves,
                             'batched_n_iters': n_iters,
-                            'batched_batch_size': batch_size}
-    return 'unknown', {'phase': 'batched_timeout',
-                       'batched_n_leaves': n_leaves,
-                       'batched_n_iters': n_iters,
-                       'batched_worklist_left': wl.size(),
-                       'batched_open_degenerate': n_open,
-                       'batched_batch_size': batch_size}
+                            'batched_worklist_left': wl.size(),
+                            'batched_open_degenerate': n_open,
+                            'batched_batch_size': batch_size})
