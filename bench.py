@@ -20,8 +20,14 @@ Prints one JSON line.  Extra keys:
   alpha        alpha-CROWN's own iterations/s and domain-iterations/s;
   rounds       per round: batch, closed, alpha leaves and iterations, and the
                domains whose spec bound lies within the bound tolerance of 0;
-  cpu_baseline the oracle on the same 3-round step (all host threads), and
-               a labelled 1-thread sample.
+  cpu_baseline the oracle on the same 3-round step (all host threads,
+               median of 3), and round 1 of it on all 65,536 boxes at one
+               thread;
+  configs      the other configurations' lines (C0: 4,096 ACAS boxes, one
+               BaB step; C2: 784-1024x4-10 MLP, 512 boxes, CROWN + alpha 10
+               it; C3: CIFAR CNN, 64 boxes; C4: 784-256x6-10 MLP, 8,192
+               ReLU-split subdomains, alpha/beta 10 it), each with its
+               roofline and CPU line (--no-configs skips them).
 --config c0|c2|c3|c4 prints the line of another configuration instead.
 """
 import argparse
@@ -284,13 +290,14 @@ def _cpu_line(units, fn, warm, reps, sample, threads=None, units_1=None, fn_1=No
     return out
 
 
-def cpu_baseline_c1(reps=1):
+def cpu_baseline_c1(reps=3):
     """The oracle on the benchmark's own step: the three BaB rounds from the
     65,536 seeded boxes (each round's children are the next round's batch),
-    after a warm-up round on a 2,048-box slice.  The oracle's per-domain
-    cost grows with the batch (its union-seeded CROWN tensors of B x 100 x
-    50 floats), so a smaller sample would flatter it.  The 1-thread figure
-    is round 1 on the 2,048-box slice (labelled)."""
+    median of ``reps`` after a warm-up round on a 2,048-box slice.  The
+    oracle's per-domain cost grows with the batch (its union-seeded CROWN
+    tensors of B x 100 x 50 floats), so a smaller sample would flatter it.
+    The 1-thread figure (the reference's own BLAS default) is round 1 on all
+    65,536 boxes, one run."""
     from oracle import ref_bab
     from vibecheck_amd import workloads as wk
     from vibecheck_amd.spec import dedup_queries
@@ -316,14 +323,20 @@ def cpu_baseline_c1(reps=1):
 
     def slice_round():
         ref_bab.bab_step(xl0[:2048].contiguous(), xh0[:2048].contiguous(), gg, se, dq, **kw)
+
+    def round_one():
+        t0 = time.perf_counter()
+        ref_bab.bab_step(xl0, xh0, gg, se, dq, **kw)
+        print(f'cpu_baseline: oracle round 1 on {N_DOMAINS} boxes, 1 thread, '
+              f'{time.perf_counter() - t0:.1f} s', file=sys.stderr, flush=True)
     slice_round()
     out = _cpu_line(67082, step, 0, reps,
                     f'the benchmark step itself: 3 BaB rounds from the 65,536 boxes '
                     f'(CROWN intermediate, alpha 20 it, clip, split), median of {reps} after a '
                     f'warm-up round on 2,048 boxes',
-                    units_1=2048, fn_1=slice_round, reps_1=3,
-                    sample_1='round 1 on the first 2,048 boxes, median of 3 (cheaper per '
-                             'domain than the full batch)')
+                    units_1=N_DOMAINS, fn_1=round_one, reps_1=1,
+                    sample_1='round 1 of the step on all 65,536 boxes (CROWN intermediate, '
+                             'alpha 20 it on the open leaves, clip, split), one run')
     out['value'] = count[0] / statistics.median(out['seconds'])
     return out
 
@@ -983,8 +996,11 @@ def main():
                     help='after the timed steps, skip the extra pass over the rounds '
                          '(near-zero counts, secondary rooflines, alpha rates): a profile '
                          'of the run then holds the warm-up and timed steps only')
-    ap.add_argument('--cpu-reps', type=int, default=1,
+    ap.add_argument('--cpu-reps', type=int, default=3,
                     help='timed CPU runs of the headline step (median)')
+    ap.add_argument('--no-configs', action='store_true',
+                    help='skip the other configurations (C0, C2, C3, C4), which the default '
+                         'run carries under "configs", each with its roofline and CPU line')
     ap.add_argument('--copy-probe', type=int, default=0, metavar='MIB',
                     help='only run a plain copy of MIB MiB (counter calibration)')
     ap.add_argument('--kernels', action='store_true',
@@ -1113,6 +1129,13 @@ def main():
     }
     if not args.no_cpu_baseline:
         out['cpu_baseline'] = cpu_baseline_c1(args.cpu_reps)
+    if not args.no_configs:
+        # the parity-test configurations, each one line as with --config
+        out['configs'] = {}
+        for cfg in ('c0', 'c2', 'c3', 'c4'):
+            print(f'bench: configuration {cfg}', file=sys.stderr, flush=True)
+            out['configs'][cfg] = run_config(cfg, args.steps, args.warmup,
+                                             not args.no_cpu_baseline)
     print(json.dumps(out), flush=True)
 
 

@@ -17,6 +17,12 @@ Per round the file holds (prefix r<k>_):
   near0             packed flags: some spec row's CROWN bound within the
                     bound tolerance of 0, |lb| <= 1e-6 + 1e-5 scale with
                     scale = |acc| + sum_i |A_i| max(|xl_i|, |xh_i|)
+  crown_lb          the CROWN pass's spec bounds of every box, (B, Q)
+  sub               a seeded subset of at most 4,096 boxes, int32 ascending
+  sub_A, sub_acc    the CROWN pass's input linearization on those boxes,
+                    (n, Q, 5) and (n, Q)
+  sub_A64           the same A from the oracle in fp64 on the same (fp32)
+                    boxes, (n, Q, 5) float64
   alpha_idx         the alpha-CROWN leaves (CROWN-unclosed), int32
   alpha_lb          their bounds after the max-merge with alpha, (n, Q)
   alpha_scale       the scale above for those rows, (n, Q)
@@ -50,7 +56,9 @@ N_ROUNDS = 3
 ALPHA_ITERS = 20
 ALPHA_LR = 0.1
 RTOL, ATOL = 1e-5, 1e-6
-OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'c1_rounds.npz')
+N_SUB = 4096
+OUT = os.environ.get('C1_ROUNDS_OUT') or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                     'c1_rounds.npz')
 
 
 def spec_scale(A, acc, xl, xh):
@@ -64,6 +72,8 @@ def main():
     xl, xh = wk.acas_boxes(N_DOMAINS, seed=1)
     uq, dq = dedup_queries(wk.acas_spec().as_linear_queries(5))
     se = {i: (torch.tensor(w, dtype=torch.float32), b) for i, (w, b) in enumerate(uq)}
+    gg64 = wk.acas_gg(dtype=torch.float64)
+    se64 = {i: (torch.tensor(w, dtype=torch.float64), b) for i, (w, b) in enumerate(uq)}
     out = {'n_rounds': np.int64(N_ROUNDS)}
     for r in range(N_ROUNDS):
         t0 = time.perf_counter()
@@ -79,6 +89,15 @@ def main():
         out[p + 'closed'] = np.packbits(st['closed'].numpy())
         out[p + 'crown_closed'] = np.packbits(crown_closed.numpy())
         out[p + 'near0'] = np.packbits(near0.numpy())
+        out[p + 'crown_lb'] = lb_c.numpy().astype(np.float32)
+        g = torch.Generator().manual_seed(100 + r)
+        sub = (torch.randperm(B, generator=g)[:N_SUB].sort().values if B > N_SUB
+               else torch.arange(B))
+        out[p + 'sub'] = sub.numpy().astype(np.int32)
+        out[p + 'sub_A'] = st['A'][sub].numpy().astype(np.float32)
+        out[p + 'sub_acc'] = st['acc'][sub].numpy().astype(np.float32)
+        _, A64, _ = ref_bab.bound_batch(xl[sub].double(), xh[sub].double(), gg64, se64)
+        out[p + 'sub_A64'] = A64.numpy()
         out[p + 'alpha_idx'] = aidx.numpy().astype(np.int32)
         out[p + 'alpha_lb'] = st['lb'][aidx].numpy().astype(np.float32)
         out[p + 'alpha_scale'] = scale[aidx].numpy().astype(np.float32)

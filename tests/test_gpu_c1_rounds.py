@@ -6,24 +6,40 @@ unclosed leaf, widest-dimension bisection), as bench.py runs them.
 The oracle's rounds are kept in tests/golden/c1_rounds.npz (written by
 tests/golden/make_c1_rounds.py; the oracle needs minutes per round).  Every
 round runs on the oracle's own boxes (round 1: the seeded boxes; then the
-oracle's children), so each round is compared on identical inputs.
+oracle's children), so each round is compared on identical inputs, and
+every comparison runs every time:
 
-Exact: the CROWN closure, the alpha-CROWN leaf set and its iteration count
-(the reference's global early stop), the closure after alpha, the unclosed
-leaves, their clip feasibility and split dimensions.  The one allowed
-exception is a domain inside the bound tolerance of 0 (a spec bound within
-1e-6 + 1e-5 scale of 0, scale the magnitude of its concretization terms),
-where fp32 rounding decides the sign; such domains are counted and printed.
-Clipped boxes and children: each coordinate within the bound tolerance
-carried through its clip threshold (the rounding of the threshold's
-numerator over |A_qi|)."""
+  - the CROWN pass's spec bound of every box, and its input linearization
+    A, acc on a seeded subset of 4,096 boxes: within 1e-5 relative /
+    1e-6 absolute, or, for at most 0.2% of the entries (counted), relative
+    to the magnitude of the concretization terms (values small because
+    large terms cancel; for A the row's L1 norm) or within twice the fp32
+    oracle's own distance from the fp64 oracle on the same domain;
+  - the CROWN closure: exact except inside the bound tolerance of 0 (a
+    spec bound within 1e-6 + 1e-5 scale of 0), where fp32 rounding decides
+    the sign; such flips are counted;
+  - the alpha-CROWN leaves: the GPU's are the oracle's up to those flips;
+    alpha is also run on exactly the oracle's leaves, so its iteration
+    count (the reference's global early stop) is compared exactly and its
+    bounds with 99% of the entries within 1e-5 relative and all within
+    1e-4, whether or not a flip changed the round's own leaf set;
+  - the closure after alpha, exact off the zero band;
+  - over the leaves open on both sides: their clip feasibility and split
+    dimensions exactly, their clipped boxes and children within the bound
+    tolerance carried through the clip threshold (the rounding of the
+    threshold's numerator over |A_qi|).
+
+The counts (flips, escapes, and alpha entries between 1e-5 and 1e-4
+relative) go to the terminal summary (C1_STATS)."""
 import os
 
 import numpy as np
 import pytest
 import torch
 
+from oracle import ref_bab as rbab
 from vibecheck_amd import verify_graph as vg
+from vibecheck_amd import verify_zono_bnb as vz
 from vibecheck_amd import workloads as wk
 from vibecheck_amd.spec import dedup_queries
 
@@ -33,6 +49,13 @@ pytestmark = pytest.mark.gpu
 FIX = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden', 'c1_rounds.npz')
 N_DOMAINS = 65536
 RTOL, ATOL = 1e-5, 1e-6
+# at most this fraction of a comparison's entries may pass only relative to
+# their scale
+ESC_FRAC = 0.002
+# per round: (B, crown flips, final flips, crown lb escapes, A escapes, alpha leaves,
+# alpha entries within 1e-5, between 1e-5 and 1e-4, above 1e-4, both-open
+# leaves compared)
+C1_STATS = []
 
 
 def _bits(a, n):
@@ -40,9 +63,58 @@ def _bits(a, n):
 
 
 def _close(got, ref, tol, what):
-    err = (got.double() - torch.from_numpy(ref).double()).abs()
+    err = (got.double() - ref.double()).abs()
     ok = err <= tol
     assert bool(ok.all()), (what, int((~ok).sum()), float((err - tol).max()))
+
+
+def _spec_scale(A, acc, xl, xh):
+    """|acc| + sum_i |A_i| max(|xl_i|, |xh_i|) per (domain, query)."""
+    xm = torch.maximum(xl.double().abs(), xh.double().abs())
+    return acc.double().abs() + (A.double().abs() * xm.unsqueeze(1)).sum(-1)
+
+
+def _bounds(got, ref, scale, what, ref64=None):
+    """|got - ref| <= 1e-6 + 1e-5 |ref|, or, for at most ESC_FRAC of the
+    entries, <= 1e-6 + 1e-5 max(|ref|, scale), or (with ref64, the oracle
+    in fp64, rows = domains) no farther from ref64 than twice the fp32
+    oracle's own largest distance from it on the same domain: an entry of
+    A sums products some 10^4 times its size (the absolute backward with
+    the domain's slopes, on these boxes), so fp32 reduction order alone
+    moves it by ~1e-5 relative, as the fp32 oracle's own error shows.
+    Returns the escapes."""
+    got, ref = got.double(), ref.double()
+    err = (got - ref).abs()
+    ok = err <= ATOL + RTOL * ref.abs()
+    ok2 = ok
+    if scale is not None:
+        ok2 = ok2 | (err <= ATOL + RTOL * torch.maximum(ref.abs(), scale.double()))
+    if ref64 is not None:
+        r64 = ref64.double()
+        noise = (ref - r64).abs().reshape(r64.shape[0], -1).amax(1)
+        noise = noise.reshape(-1, *([1] * (r64.dim() - 1)))
+        ok2 = ok2 | ((got - r64).abs() <= 2.0 * noise)
+    if not bool(ok2.all()):
+        bad = (~ok2).nonzero()[:8].tolist()
+        detail = [(b, float(got[tuple(b)]), float(ref[tuple(b)]),
+                   None if ref64 is None else float(ref64[tuple(b)])) for b in bad]
+        raise AssertionError(f'{what}: {int((~ok2).sum())} entries outside tolerance, worst '
+                             f'{float(err.max()):.3e}; (index, gpu, oracle, fp64): {detail}')
+    esc = int((ok2 & ~ok).sum())
+    assert esc <= max(8, ESC_FRAC * ok.numel()), (what, esc, ok.numel())
+    return esc
+
+
+def _rows_by_leaf(leaves, feasible):
+    """leaf -> row of the feasible leaves' arrays (the rows follow the
+    unclosed leaves in order, feasible ones only)."""
+    out = {}
+    row = 0
+    for leaf, f in zip(leaves.tolist(), feasible.tolist()):
+        if f:
+            out[leaf] = row
+            row += 1
+    return out
 
 
 def test_c1_three_rounds_match_oracle(gpu):
@@ -52,7 +124,6 @@ def test_c1_three_rounds_match_oracle(gpu):
     se = {i: (torch.tensor(w, dtype=torch.float32, device=gpu), b) for i, (w, b) in enumerate(uq)}
     table = vg.DisjunctTable(dq, gpu)
     xl, xh = wk.acas_boxes(N_DOMAINS, seed=1)
-    n_excused = 0
     for r in range(int(fx['n_rounds'])):
         p = f'r{r}_'
         B = int(fx[p + 'B'])
@@ -61,6 +132,17 @@ def test_c1_three_rounds_match_oracle(gpu):
         near0 = _bits(fx[p + 'near0'], B)
         # the CROWN bound alone (alpha off), then the round as benchmarked
         st0 = vg.bab_step(xl_g, xh_g, gg, se, table, alpha_iters=0)
+        lb0, A0, acc0 = st0['lb'].cpu(), st0['A'].cpu(), st0['acc'].cpu()
+        scale = _spec_scale(A0, acc0, xl, xh)
+        esc = _bounds(lb0, torch.from_numpy(fx[p + 'crown_lb']), scale, f'r{r} crown lb')
+        sub = torch.from_numpy(fx[p + 'sub']).long()
+        ref_acc = torch.from_numpy(fx[p + 'sub_acc'])
+        _bounds(acc0[sub], ref_acc, scale[sub], f'r{r} crown acc')
+        ref_A = torch.from_numpy(fx[p + 'sub_A'])
+        # an entry of A moves the bound by its error times the box, so its
+        # scale is its row's L1 norm (the bound's scale sums |A_i| |x_i|)
+        esc_A = _bounds(A0[sub], ref_A, ref_A.abs().sum(-1, keepdim=True).expand_as(ref_A),
+                        f'r{r} crown A', ref64=torch.from_numpy(fx[p + 'sub_A64']))
         crown_closed = st0['closed'].cpu()
         st = vg.bab_step(xl_g, xh_g, gg, se, table, alpha_iters=20, alpha_all=True,
                          alpha_lr=0.1)
@@ -68,55 +150,85 @@ def test_c1_three_rounds_match_oracle(gpu):
         ref_crown = _bits(fx[p + 'crown_closed'], B)
         ref_closed = _bits(fx[p + 'closed'], B)
         d_crown = crown_closed != ref_crown
-        d_closed = closed != ref_closed
-        print(f'round {r}: B={B} closed gpu={int(closed.sum())} oracle={int(ref_closed.sum())} '
-              f'near-zero={int(near0.sum())} crown closure differs on {int(d_crown.sum())}, '
-              f'final on {int(d_closed.sum())}', flush=True)
         assert not bool((d_crown & ~near0).any()), 'CROWN closure differs off the zero band'
-        n_excused += int(d_crown.sum())
+
+        # alpha: the round's leaves are the CROWN-open ones, the oracle's up
+        # to the flips; alpha on exactly the oracle's leaves for the count
         aidx = torch.from_numpy(fx[p + 'alpha_idx']).long()
-        if not bool(d_crown.any()):
-            # identical alpha leaves: the loop's iteration count is exact and
-            # its verdicts match except inside the zero band
-            assert st['n_alpha_leaves'] == aidx.numel()
-            assert st['n_alpha_iters'] == int(fx[p + 'n_alpha_iters']), \
-                (st['n_alpha_iters'], int(fx[p + 'n_alpha_iters']))
-            lb_a = st['lb'][aidx.to(gpu)].cpu().double()
-            ref_a = torch.from_numpy(fx[p + 'alpha_lb']).double()
-            sc_a = torch.from_numpy(fx[p + 'alpha_scale']).double()
-            band = ((ref_a.abs() <= ATOL + RTOL * sc_a).any(1))
-            near0[aidx[band]] = True
-            # the bound after 20 Adam steps: Adam turns fp32 noise in
-            # near-zero gradient components into +-lr steps, so the bound
-            # drifts: 99% within 1e-4 relative, all within 1e-3
-            err = (lb_a - ref_a).abs() / torch.maximum(ref_a.abs(), sc_a).clamp(min=1e-30)
-            assert float((err <= 1e-4).double().mean()) >= 0.99, float(err.max())
-            assert float(err.max()) <= 1e-3, float(err.max())
-        assert not bool((d_closed & ~near0).any()), 'closure differs off the zero band'
-        n_excused += int(d_closed.sum())
-        # the unclosed leaves, their feasibility and split dimensions: over
-        # the leaves open on both sides
-        unc = st['unclosed'].cpu()
-        ref_unc = torch.from_numpy(fx[p + 'unclosed']).long()
+        mine = (~crown_closed).nonzero(as_tuple=True)[0]
+        sym = set(mine.tolist()) ^ set(aidx.tolist())
+        assert sym <= set(d_crown.nonzero(as_tuple=True)[0].tolist())
+        assert st['n_alpha_leaves'] == mine.numel()
+        a_i = aidx.to(gpu)
+        best, n_it = vz._run_alpha_crown_inputsplit_batched(
+            xl_g[a_i], xh_g[a_i], gg, se, gpu, torch.float32, n_iters=20, lr=0.1,
+            lr_decay=0.98, return_trace=True)
+        assert n_it == int(fx[p + 'n_alpha_iters']), (n_it, int(fx[p + 'n_alpha_iters']))
+        if not sym:
+            assert st['n_alpha_iters'] == n_it
+        lb_a = torch.maximum(lb0[aidx], best.cpu()).double()
+        ref_a = torch.from_numpy(fx[p + 'alpha_lb']).double()
+        sc_a = torch.from_numpy(fx[p + 'alpha_scale']).double()
+        band = ((ref_a.abs() <= ATOL + RTOL * sc_a).any(1))
+        near0[aidx[band]] = True
+        # the bound after up to 20 Adam steps: Adam turns fp32 noise in
+        # near-zero gradient components into +-lr steps, which could let the
+        # bound drift; on this workload 99% stay within 1e-5 relative (in
+        # practice all of them) and every one within 1e-4
+        err = (lb_a - ref_a).abs() / torch.maximum(ref_a.abs(), sc_a).clamp(min=1e-30)
+        n_tight = int((err <= 1e-5).sum())
+        n_mid = int(((err > 1e-5) & (err <= 1e-4)).sum())
+        n_far = int((err > 1e-4).sum())
+        print(f'round {r}: alpha on {aidx.numel()} leaves, {n_it} iterations; entries within '
+              f'1e-5: {n_tight}, 1e-5..1e-4: {n_mid}, beyond: {n_far} '
+              f'(max {float(err.max()) if err.numel() else 0.0:.2e})', flush=True)
+        if err.numel():
+            assert float((err <= 1e-5).double().mean()) >= 0.99, float(err.max())
+            assert float(err.max()) <= 1e-4, float(err.max())
+        # the closure after alpha on the oracle's leaves, every time; the
+        # round's own when its alpha ran on the same leaves
+        lb_tf = lb0.clone()
+        lb_tf[aidx] = lb_a.float()
+        d_tf = rbab.closure(lb_tf, dq) != ref_closed
+        assert not bool((d_tf & ~near0).any()), 'closure after alpha differs off the zero band'
+        d_closed = closed != ref_closed
+        if not sym:
+            assert not bool((d_closed & ~near0).any()), 'closure differs off the zero band'
+
+        # over the leaves open on both sides: feasibility, split axes,
+        # clipped boxes and children
+        unc, ref_unc = st['unclosed'].cpu(), torch.from_numpy(fx[p + 'unclosed']).long()
+        assert set(unc.tolist()) ^ set(ref_unc.tolist()) <= set(
+            d_closed.nonzero(as_tuple=True)[0].tolist())
         feas = st['feasible'].cpu()
         ref_feas = torch.from_numpy(fx[p + 'feasible'])
-        if not bool(d_closed.any()):
-            assert torch.equal(unc, ref_unc)
-            assert torch.equal(feas, ref_feas)
-            ax = st['ax'].cpu()
-            assert torch.equal(ax, torch.from_numpy(fx[p + 'ax']).long())
-            # the feasible leaves' rows, their tolerance from their own bound
-            fidx = unc[feas]
-            tol = _util.clip_tolerance(st['A'][fidx.to(gpu)], st['acc'][fidx.to(gpu)],
-                                       xl[fidx], xh[fidx])
-            _close(st['xl_split'].cpu(), fx[p + 'xl_split'], tol, 'clipped xl')
-            _close(st['xh_split'].cpu(), fx[p + 'xh_split'], tol, 'clipped xh')
-            assert st['n_degenerate'] == 0
-            (lxl, lxh), (hxl, hxh) = st['low'], st['high']
-            for got, key in ((lxl, 'low_xl'), (lxh, 'low_xh'), (hxl, 'high_xl'),
-                             (hxh, 'high_xh')):
-                _close(got.cpu(), fx[p + key], tol, key)
+        f_mine = dict(zip(unc.tolist(), feas.tolist()))
+        f_ref = dict(zip(ref_unc.tolist(), ref_feas.tolist()))
+        both = sorted(set(f_mine) & set(f_ref))
+        assert all(f_mine[k] == f_ref[k] for k in both)
+        row_m = _rows_by_leaf(unc, feas)
+        row_r = _rows_by_leaf(ref_unc, ref_feas)
+        fb = [k for k in both if f_mine[k]]
+        im = torch.tensor([row_m[k] for k in fb], dtype=torch.long)
+        ir = torch.tensor([row_r[k] for k in fb], dtype=torch.long)
+        assert st['n_degenerate'] == 0
+        assert torch.equal(st['ax'].cpu()[im], torch.from_numpy(fx[p + 'ax']).long()[ir])
+        leaves = torch.tensor(fb, dtype=torch.long)
+        tol = _util.clip_tolerance(A0[leaves], acc0[leaves], xl[leaves], xh[leaves])
+        _close(st['xl_split'].cpu()[im], torch.from_numpy(fx[p + 'xl_split'])[ir], tol,
+               'clipped xl')
+        _close(st['xh_split'].cpu()[im], torch.from_numpy(fx[p + 'xh_split'])[ir], tol,
+               'clipped xh')
+        (lxl, lxh), (hxl, hxh) = st['low'], st['high']
+        for got, key in ((lxl, 'low_xl'), (lxh, 'low_xh'), (hxl, 'high_xl'),
+                         (hxh, 'high_xh')):
+            _close(got.cpu()[im], torch.from_numpy(fx[p + key])[ir], tol, key)
+        C1_STATS.append((B, int(d_crown.sum()), int(d_closed.sum()), esc, esc_A, aidx.numel(),
+                         n_tight, n_mid, n_far, len(fb)))
+        print(f'round {r}: B={B} closed gpu={int(closed.sum())} oracle={int(ref_closed.sum())} '
+              f'near-zero={int(near0.sum())} crown closure flips {int(d_crown.sum())}, '
+              f'final flips {int(d_closed.sum())}, crown lb escapes {esc}; '
+              f'{len(fb)} feasible leaves open on both sides compared', flush=True)
         # the next round starts from the oracle's children, high chunk first
         xl = torch.cat([torch.from_numpy(fx[p + 'high_xl']), torch.from_numpy(fx[p + 'low_xl'])])
         xh = torch.cat([torch.from_numpy(fx[p + 'high_xh']), torch.from_numpy(fx[p + 'low_xh'])])
-    print(f'domains excused by the zero band over all rounds: {n_excused}', flush=True)
