@@ -13,8 +13,8 @@ every comparison runs every time:
     A, acc on a seeded subset of 4,096 boxes: within 1e-5 relative /
     1e-6 absolute, or, for at most 0.2% of the entries (counted), relative
     to the magnitude of the concretization terms (values small because
-    large terms cancel; for A the row's L1 norm) or within twice the fp32
-    oracle's own distance from the fp64 oracle on the same domain;
+    large terms cancel; for A the row's L1 norm) or within four times the
+    fp32 oracle's own distance from the fp64 oracle on the same domain;
   - the CROWN closure: exact except inside the bound tolerance of 0 (a
     spec bound within 1e-6 + 1e-5 scale of 0), where fp32 rounding decides
     the sign; such flips are counted;
@@ -77,12 +77,14 @@ def _spec_scale(A, acc, xl, xh):
 def _bounds(got, ref, scale, what, ref64=None):
     """|got - ref| <= 1e-6 + 1e-5 |ref|, or, for at most ESC_FRAC of the
     entries, <= 1e-6 + 1e-5 max(|ref|, scale), or (with ref64, the oracle
-    in fp64, rows = domains) no farther from ref64 than twice the fp32
+    in fp64, rows = domains) no farther from ref64 than four times the fp32
     oracle's own largest distance from it on the same domain: an entry of
     A sums products some 10^4 times its size (the absolute backward with
-    the domain's slopes, on these boxes), so fp32 reduction order alone
-    moves it by ~1e-5 relative, as the fp32 oracle's own error shows.
-    Returns the escapes."""
+    the domain's slopes, on these boxes), and a domain with an intermediate
+    bound near a relu's threshold carries that rounding into its slopes,
+    so fp32 computations in different orders scatter around the exact
+    value by the domain's conditioning, of which the fp32 oracle's own
+    distance is one sample.  Returns the escapes."""
     got, ref = got.double(), ref.double()
     err = (got - ref).abs()
     ok = err <= ATOL + RTOL * ref.abs()
@@ -93,7 +95,7 @@ def _bounds(got, ref, scale, what, ref64=None):
         r64 = ref64.double()
         noise = (ref - r64).abs().reshape(r64.shape[0], -1).amax(1)
         noise = noise.reshape(-1, *([1] * (r64.dim() - 1)))
-        ok2 = ok2 | ((got - r64).abs() <= 2.0 * noise)
+        ok2 = ok2 | ((got - r64).abs() <= 4.0 * noise)
     if not bool(ok2.all()):
         bad = (~ok2).nonzero()[:8].tolist()
         detail = [(b, float(got[tuple(b)]), float(ref[tuple(b)]),

@@ -46,6 +46,16 @@ __device__ __forceinline__ int queue_take(int* q, int lane) {
 }
 __device__ __forceinline__ int64_t queue_bcast(int t) { return (int64_t)__shfl(t, 0, 64); }
 
+// Orders a wavefront's own LDS writes before its later LDS reads of them,
+// for LDS that no other wavefront touches: a wavefront's LDS instructions
+// execute in issue order, so keeping the compiler from reordering them is
+// all that is needed.  A wavefront-scope fence does that and emits no
+// wait; __threadfence_block() (workgroup scope) also waits for the wave's
+// outstanding global stores (s_waitcnt vmcnt(0)) at every use.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
 
 // The input-split round's bound phase with the CROWN rows pass's per-domain
 // seed masks and union of unstable sets written by the zonotope passes

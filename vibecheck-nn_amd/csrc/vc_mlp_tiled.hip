@@ -730,6 +730,98 @@ __device__ __forceinline__ void fc_forward(const float4* fr, int lane, int g, in
   __builtin_amdgcn_s_setprio(0);
 }
 
+// fc_l's forward product for a uniform hidden width d = 16 (MT - 1) + MR,
+// 1 <= MR <= 3, with the bias row in the padding: output rows below
+// 16 (MT - 1) by MFMA over the full input tiles t < MT - 1 only; the last
+// MR inputs and the bias row (in lanes of group 0 of input tile MT - 1)
+// as a rank-(MR + 1) VALU update of those rows; the last MR output rows as
+// VALU dot products over every input, reduced across the four lane groups.
+// That leaves out one output tile and the input tile's K-steps, which hold
+// 2-3 live values of 16 (a 50-wide layer: 36 MFMAs per column tile instead
+// of 60).  wk: W_l[o][16 (MT - 1) + kk] for o < 16 (MT - 1), kk <= MR (the
+// bias column at kk == MR), 4 per row; wm: W_l[16 (MT - 1) + m][k] for
+// m < MR, k < 64 (bias at k = d, zeros past it).
+template <int MT, int KS, int NX, int NT, int MR>
+__device__ __forceinline__ void fc_forward_rem(const float4* fr, const float* wk, const float* wm,
+                                               int lane, int g, int r, const v4f (&X)[NT][4],
+                                               int x0, v4f (&out)[NX][4]) {
+  static_assert(MR >= 1 && MR <= 3 && MT >= 2, "remainder form");
+  constexpr int MF = MT - 1;
+#pragma unroll
+  for (int x = 0; x < NX; ++x)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) out[x][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float a[MF][4];
+#pragma unroll
+    for (int mo = 0; mo < MF; ++mo) {
+      const int ksf = 4 * mo + (r & 3);
+      const float4 q = fr[ksf * 64 + swz(16 * (r >> 2) + 4 * g + i, ksf)];
+      a[mo][0] = q.x;
+      a[mo][1] = q.y;
+      a[mo][2] = q.z;
+      a[mo][3] = q.w;
+    }
+#pragma unroll
+    for (int t = 0; t < MF; ++t)
+#pragma unroll
+      for (int mo = 0; mo < MF; ++mo)
+#pragma unroll
+        for (int x = 0; x < NX; ++x)
+          out[x][mo] = mfma16x16x4(a[mo][t], X[x0 + x][t][i], out[x][mo]);
+  }
+  __builtin_amdgcn_s_setprio(0);
+  // the remainder inputs of each column, from its lane in group 0
+  float zb[NX][MR + 1];
+#pragma unroll
+  for (int x = 0; x < NX; ++x)
+#pragma unroll
+    for (int kk = 0; kk <= MR; ++kk) zb[x][kk] = __shfl(X[x0 + x][MF][kk], r, 64);
+#pragma unroll
+  for (int mo = 0; mo < MF; ++mo)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 w = *reinterpret_cast<const float4*>(wk + 4 * (16 * mo + 4 * g + i));
+      const float w4[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int x = 0; x < NX; ++x) {
+        float acc = out[x][mo][i];
+#pragma unroll
+        for (int kk = 0; kk <= MR; ++kk) acc = __builtin_fmaf(w4[kk], zb[x][kk], acc);
+        out[x][mo][i] = acc;
+      }
+    }
+  // the last MR output rows
+  float rem[NX][MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    float s[NX];
+#pragma unroll
+    for (int x = 0; x < NX; ++x) s[x] = 0.f;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const float4 w = *reinterpret_cast<const float4*>(wm + 64 * m + 16 * t + 4 * g);
+      const float w4[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int x = 0; x < NX; ++x) s[x] = __builtin_fmaf(w4[i], X[x0 + x][t][i], s[x]);
+    }
+#pragma unroll
+    for (int x = 0; x < NX; ++x) {
+      s[x] += __shfl_xor(s[x], 16, 64);
+      s[x] += __shfl_xor(s[x], 32, 64);
+      rem[x][m] = s[x];
+    }
+  }
+#pragma unroll
+  for (int x = 0; x < NX; ++x)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[x][MF][i] = (g == 0 && i < MR) ? rem[x][i < MR ? i : 0] : 0.f;
+}
+
 // Per-wave LDS of the alpha kernels: slopes [l][ls_eff, us, ut, unstable][FW],
 // Adam state [l][alpha, m, v][FW], the pre-relaxation rows P_l
 // [l][ks][g][r < Q], d lb / d alpha of one layer [FW], the box [2 FW].
@@ -1388,7 +1480,25 @@ __device__ __forceinline__ void zono_input_tiles(const TGeom& G, const float* fr
   }
 }
 
-template <int MT, int KS, bool BROW>
+// LDS floats of the remainder form's weight tables (fc_forward_rem) for
+// n relu layers: wk [n - 1][48][4] and wm [n - 1][MR][64].
+__host__ __device__ constexpr int zono_rem_floats(int n, int MT, int MR) {
+  return MR > 0 ? (n - 1) * (16 * (MT - 1) * 4 + MR * 64) : 0;
+}
+
+// W_l[o][k] (l >= 1; k = d_l is the bias) from fc_l's tiled backward
+// fragments: A[m][k'] = W[k'][m] sits at K-step 4 (k' / 16) + k' % 4, lane
+// 16 ((k' % 16) / 4) + m % 16, component m / 16.
+template <int KS>
+__device__ __forceinline__ float frag_weight(const float* frh_l, int o, int k) {
+  const int ks = 4 * (o >> 4) + (o & 3);
+  const int ln = 16 * ((o & 15) >> 2) + (k & 15);
+  return frh_l[(ks * 64 + swz(ln, ks)) * 4 + (k >> 4)];
+}
+
+// MR > 0: every hidden layer is 16 (MT - 1) + MR wide and fc_l runs in the
+// remainder form (fc_forward_rem); MR = 0: fc_forward over all tiles.
+template <int MT, int KS, bool BROW, int MR>
 __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* __restrict__ gfrag,
                                                          const float* __restrict__ gbias,
                                                          int64_t B, const float* __restrict__ xl,
@@ -1411,12 +1521,29 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
     const int l = k / FW, j = k % FW;
     sbias[k] = j < G.d[l + 1] ? gbias[G.boff[l] + j] : 0.f;
   }
+  // the remainder form's tables, after the fragments they are read from
+  float* swk = sbias + n * FW;
+  constexpr int MF16 = 16 * (MT - 1);
+  float* swm = swk + (n - 1) * MF16 * 4;
+  if (MR > 0) {
+    __syncthreads();
+    const int d = MF16 + MR;
+    for (int e = threadIdx.x; e < (n - 1) * MF16 * 4; e += blockDim.x) {
+      const int l = 1 + e / (MF16 * 4), o = (e / 4) % MF16, kk = e & 3;
+      swk[e] = kk <= MR ? frag_weight<KS>(sfrag + G.offh + (l - 1) * KS * 256, o, MF16 + kk)
+                        : 0.f;
+    }
+    for (int e = threadIdx.x; e < (n - 1) * MR * 64; e += blockDim.x) {
+      const int l = 1 + e / (MR * 64), m = (e / 64) % (MR > 0 ? MR : 1), k = e & 63;
+      swm[e] = k <= d ? frag_weight<KS>(sfrag + G.offh + (l - 1) * KS * 256, MF16 + m, k) : 0.f;
+    }
+  }
   __syncthreads();
   const float* fr0 = sfrag;
   const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
   // this wave's relu scratch: |G| partials [16 lanes][ZPS], centre, lambda,
   // mu, new-column index [FW] each
-  float* zpart = sbias + n * FW + wv * ZSCR;
+  float* zpart = sbias + n * FW + zono_rem_floats(n, MT, MR) + wv * ZSCR;
   float* zcen = zpart + 16 * ZPS;
   float* zlam = zcen + FW;
   float* zmu = zlam + FW;
@@ -1472,11 +1599,16 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
         // fc_l on the used column tiles; the centre column picks up b_l
         if (BROW && r == 0) set_elem<MT>(Z[0], G.d[l], g, 1.f);
         const float4* fr = frh + (l - 1) * KS * 64;
+        const float* wk = swk + (l - 1) * MF16 * 4;
+        const float* wm = swm + (l - 1) * (MR > 0 ? MR : 1) * 64;
 #pragma unroll
         for (int nt0 = 0; nt0 < ZT; nt0 += 2) {
           if (16 * (nt0 + 1) < Kc) {
             v4f o[2][4];
-            fc_forward<MT, KS, 2, ZT>(fr, lane, g, r, Z, nt0, o, G.d[l] + (BROW ? 1 : 0));
+            if constexpr (MR > 0)
+              fc_forward_rem<MT, KS, 2, ZT, MR>(fr, wk, wm, lane, g, r, Z, nt0, o);
+            else
+              fc_forward<MT, KS, 2, ZT>(fr, lane, g, r, Z, nt0, o, G.d[l] + (BROW ? 1 : 0));
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
               Z[nt0][mt] = o[0][mt];
@@ -1485,7 +1617,10 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
           } else if (16 * nt0 < Kc) {
             // tile nt0 + 1 holds no generator (zeros stay zeros)
             v4f o[1][4];
-            fc_forward<MT, KS, 1, ZT>(fr, lane, g, r, Z, nt0, o, G.d[l] + (BROW ? 1 : 0));
+            if constexpr (MR > 0)
+              fc_forward_rem<MT, KS, 1, ZT, MR>(fr, wk, wm, lane, g, r, Z, nt0, o);
+            else
+              fc_forward<MT, KS, 1, ZT>(fr, lane, g, r, Z, nt0, o, G.d[l] + (BROW ? 1 : 0));
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) Z[nt0][mt] = o[0][mt];
           }
@@ -1528,7 +1663,7 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
                 make_float4(Z[0][t][0], Z[0][t][1], Z[0][t][2], Z[0][t][3]);
         }
       }
-      __threadfence_block();
+      vcm::wave_lds_fence();
       const int j = lane;
       double sd = 0.0;
 #pragma unroll
@@ -1560,7 +1695,7 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
       zlam[j] = ust ? hi / (hi - lo) : (dead ? 0.f : 1.f);
       zmu[j] = ust ? (-hi * lo) / (2.f * (hi - lo)) : 0.f;
       zcol[j] = ust ? Kc + __popcll(umask & ((1ull << j) - 1ull)) : -1;
-      __threadfence_block();
+      vcm::wave_lds_fence();
       // scale each row by lambda (centre: lambda c + mu) and put mu in the
       // row's new column; tiles from Kc + cnt on stay zero
 #pragma unroll
@@ -1598,10 +1733,26 @@ __global__ __launch_bounds__(ZNW * 64) void k_zono_tiled(TGeom G, const float* _
   }
 }
 
-template <int V>
+template <int V, int MR>
 const void* zono_fn() {
   return reinterpret_cast<const void*>(
-      &k_zono_tiled<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
+      &k_zono_tiled<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0, MR>);
+}
+
+// The remainder form's MR for a geometry, 0 when it does not apply: the
+// 49- and 50-wide hidden layers of the (4, 14, bias row) variant, every
+// hidden layer the same width.
+constexpr int kRemVariant = 3;
+static_assert(kVariants[kRemVariant].MT == 4 && kVariants[kRemVariant].KS == 14 &&
+                  kVariants[kRemVariant].brow == 1,
+              "remainder variant");
+int zono_rem(const TGeom& G) {
+  if (G.variant != kRemVariant || G.n < 2) return 0;
+  const int d = G.d[1];
+  for (int l = 2; l <= G.n; ++l)
+    if (G.d[l] != d) return 0;
+  const int mr = d - 16 * (kVariants[kRemVariant].MT - 1);
+  return mr >= 1 && mr <= 2 ? mr : 0;
 }
 
 // Second zonotope pass over the domains flagged by the first: one
@@ -3026,9 +3177,12 @@ int zono_bounds_run(const int32_t* dims, int n_relu, const float* frag, const fl
     za.hi[l] = l < n_relu ? hi_out[l] : nullptr;
     if (l < n_relu && (!za.lo[l] || !za.hi[l])) return VC_ERR_ARG;
   }
+  const int mr = zono_rem(G);
   // the kernel's static LDS (the mask pass's union staging) comes first
-  const size_t base = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float) +
-                      sizeof(unsigned long long) * (ZNW + 1) * MAXL;
+  const size_t base =
+      ((size_t)G.nfloats + (size_t)n_relu * FW + (size_t)zono_rem_floats(n_relu, G.MT, mr)) *
+          sizeof(float) +
+      sizeof(unsigned long long) * (ZNW + 1) * MAXL;
   const size_t scr = (size_t)ZSCR * sizeof(float);
   if (base + scr > 160 * 1024) return VC_ERR_UNSUPPORTED;
   // small batches: fewer wavefronts per workgroup, so that the domains
@@ -3039,13 +3193,15 @@ int zono_bounds_run(const int32_t* dims, int n_relu, const float* frag, const fl
                                         std::max<int64_t>(1, per_cu_dom));
   const size_t lds = base + (size_t)nw * scr;
   const void* fn = nullptr;
-  switch (G.variant) {
-    case 0: fn = zono_fn<0>(); break;
-    case 1: fn = zono_fn<1>(); break;
-    case 2: fn = zono_fn<2>(); break;
-    case 3: fn = zono_fn<3>(); break;
-    case 4: fn = zono_fn<4>(); break;
-    case 5: fn = zono_fn<5>(); break;
+  switch (G.variant * 4 + mr) {
+    case 0: fn = zono_fn<0, 0>(); break;
+    case 4: fn = zono_fn<1, 0>(); break;
+    case 8: fn = zono_fn<2, 0>(); break;
+    case 12: fn = zono_fn<3, 0>(); break;
+    case 13: fn = zono_fn<3, 1>(); break;
+    case 14: fn = zono_fn<3, 2>(); break;
+    case 16: fn = zono_fn<4, 0>(); break;
+    case 20: fn = zono_fn<5, 0>(); break;
     default: return VC_ERR_UNSUPPORTED;
   }
   if (!vcm::allow_max_lds(fn)) return VC_ERR_UNSUPPORTED;
@@ -3054,20 +3210,22 @@ int zono_bounds_run(const int32_t* dims, int n_relu, const float* frag, const fl
   if (queue || zm.umask || zm.ovf_count || zm.clear_count)
     hipLaunchKernelGGL(k_zono_init, dim3(1), dim3(64), 0, st, queue, zm.umask, n_relu,
                        zm.ovf_count, zm.clear_count);
-#define VC_TZONO_CASE(V)                                                                     \
-  case V:                                                                                    \
+#define VC_TZONO_CASE(V, MR)                                                                 \
+  case V * 4 + MR:                                                                           \
     hipLaunchKernelGGL((k_zono_tiled<kVariants[V].MT, kVariants[V].KS,                       \
-                                     kVariants[V].brow != 0>),                               \
+                                     kVariants[V].brow != 0, MR>),                           \
                        grid, block, lds - sizeof(unsigned long long) * (ZNW + 1) * MAXL, st, \
                        G, frag, bias_cat, B, xl, xh, za, overflow, queue, zm);               \
     break;
-  switch (G.variant) {
-    VC_TZONO_CASE(0)
-    VC_TZONO_CASE(1)
-    VC_TZONO_CASE(2)
-    VC_TZONO_CASE(3)
-    VC_TZONO_CASE(4)
-    VC_TZONO_CASE(5)
+  switch (G.variant * 4 + mr) {
+    VC_TZONO_CASE(0, 0)
+    VC_TZONO_CASE(1, 0)
+    VC_TZONO_CASE(2, 0)
+    VC_TZONO_CASE(3, 0)
+    VC_TZONO_CASE(3, 1)
+    VC_TZONO_CASE(3, 2)
+    VC_TZONO_CASE(4, 0)
+    VC_TZONO_CASE(5, 0)
     default: return VC_ERR_UNSUPPORTED;
   }
 #undef VC_TZONO_CASE
