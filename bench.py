@@ -81,6 +81,12 @@ def crown_kernel_name(B):
             'masks come from the zonotope passes)')
 
 
+def vz_sb(gg, xl, xh, dev):
+    """The zonotope bounds of a batch (the fused kernel)."""
+    from vibecheck_amd import verify_zono_bnb as vz
+    return vz._zono_sb(gg, xl, xh, dev, torch.float32)
+
+
 def run_rounds(gg, xl, xh, spec_ew, table, timers=None, keep=None):
     """Three BaB rounds; returns per-round stats.  ``keep`` (a list): each
     round's batch and step outputs are appended to it."""
@@ -1058,15 +1064,17 @@ def main():
     # only the large round's CROWN pass is the roofline's unit: the small
     # rounds' launches are not bracketed by events
     lib = _lib.load()
-    when = {'vc_mlp_tiled_crown': lambda b: lib.vc_mlp_tiled_crown_mode(b) == 0}
-    _lib.timing_begin(['vc_mlp_crown', 'vc_mlp_tiled_crown'], when=when)
+    large = lambda b: lib.vc_mlp_tiled_crown_mode(b) == 0
+    when = {'vc_mlp_tiled_crown': large, 'zonotope_pass': large}
+    timed_names = ['vc_mlp_crown', 'vc_mlp_tiled_crown', 'zonotope_pass']
+    _lib.timing_begin(timed_names, when=when)
     for _ in range(max(1, args.warmup)):
         run_rounds(gg, xl0, xh0, se, table)
     _lib.timing_end()
     seeded.zero_()
     mf.SEED_ROW = 0
     torch.cuda.synchronize()
-    _lib.timing_begin(['vc_mlp_crown', 'vc_mlp_tiled_crown'], when=when)
+    _lib.timing_begin(timed_names, when=when)
     t0 = time.perf_counter()
     stats = None
     for _ in range(args.steps):
@@ -1075,6 +1083,7 @@ def main():
     wall = time.perf_counter() - t0
     kt = _lib.timing_end()
     mf.SEED_COUNTER = None
+    zt = kt.pop('zonotope_pass', {})
     if kt.get('vc_mlp_tiled_crown', {}).get('launches'):
         # the dominant work is the CROWN pass of the large batch (the
         # layer-synchronous rows form); the small rounds run k_crown_dom
@@ -1093,6 +1102,46 @@ def main():
     kernel = {'vc_mlp_crown': 'k_mlp_crown', 'vc_mlp_tiled_crown': 'crown_rows_pass'}[entry]
     achieved = k['flops'] / k['seconds'] / 1e12 if k['seconds'] > 0 else 0.0
     traffic, traffic_note = measured_traffic(kernel)
+    roof_crown = {'kernel': (crown_kernel_name(N_DOMAINS) if entry == 'vc_mlp_tiled_crown'
+                             else 'k_mlp_crown (vc_mlp_crown)')
+                            + ': CROWN intermediate bounds + spec backward, fp32 MFMA',
+                  'bound': 'mfma', 'achieved': achieved, 'peak': FP32_MFMA_PEAK,
+                  'unit': 'TFLOP/s', 'frac': achieved / FP32_MFMA_PEAK,
+                  'traffic': traffic,
+                  'traffic_unit': 'bytes per launch (HBM, rocprofv3 FETCH_SIZE + WRITE_SIZE)',
+                  'traffic_note': traffic_note,
+                  'launches_per_step': k['launches'] / args.steps,
+                  'avg_launch_us': 1e6 * k['seconds'] / max(1, k['launches']),
+                  'ms_per_step': 1e3 * k['seconds'] / args.steps}
+    # the zonotope passes of the 65,536-box round, timed in the same steps
+    # (from an event before the native round to the CROWN pass's start):
+    # sum_l 2 d_{l+1} d_l K_l FLOP per domain, K_l = 1 + n_in + the domain's
+    # unstable neurons below layer l, from the round's bounds (outside the
+    # timed region; the same boxes every step)
+    roof_zono = None
+    if zt.get('launches'):
+        plan = mf.plan_for(gg, dev)
+        dims, n = plan.dims, plan.n
+        sbz = vz_sb(gg, xl0, xh0, dev)
+        unst = torch.stack([((sbz[L][0] < 0) & (sbz[L][1] > 0)).sum(1) for L in range(n)],
+                           1).double()
+        below = torch.cat([torch.zeros_like(unst[:, :1]), unst.cumsum(1)[:, :-1]], 1)
+        wz = torch.tensor([2.0 * dims[l + 1] * dims[l] for l in range(n)], device=dev,
+                          dtype=torch.float64)
+        zflop = float(((1 + dims[0] + below) * wz).sum())
+        zsec = zt['seconds'] / zt['launches']
+        ztraffic, znote = measured_traffic('zonotope_pass')
+        roof_zono = {'kernel': 'zonotope pass (k_zono_init, k_zono_tiled, k_zono_wide_tiled for '
+                               'the domains past 128 generator columns): the zonotope bounds '
+                               'of every relu, fp32 MFMA',
+                     'bound': 'mfma', 'achieved': zflop / zsec / 1e12, 'peak': FP32_MFMA_PEAK,
+                     'unit': 'TFLOP/s', 'frac': zflop / zsec / 1e12 / FP32_MFMA_PEAK,
+                     'traffic': ztraffic,
+                     'traffic_unit': 'bytes per launch (HBM, rocprofv3 FETCH_SIZE + WRITE_SIZE)',
+                     'traffic_note': znote,
+                     'launches_per_step': zt['launches'] / args.steps,
+                     'avg_launch_us': 1e6 * zsec,
+                     'ms_per_step': 1e3 * zt['seconds'] / args.steps}
 
     # outside the timed region: the rounds' outputs once more, for the
     # domains inside the zero band and the other kernels' rooflines
@@ -1115,16 +1164,10 @@ def main():
         'alpha': ({'step_open_leaves': alpha_rates['open'], 'all_65536': alpha_rates['all']}
                   if alpha_rates else None),
         'rounds': [dict(s, near_zero=z) for s, z in zip(stats, nz)],
-        'roofline': {'kernel': (crown_kernel_name(N_DOMAINS) if entry == 'vc_mlp_tiled_crown'
-                                else 'k_mlp_crown (vc_mlp_crown)')
-                               + ': CROWN intermediate bounds + spec backward, fp32 MFMA',
-                     'bound': 'mfma', 'achieved': achieved, 'peak': FP32_MFMA_PEAK,
-                     'unit': 'TFLOP/s', 'frac': achieved / FP32_MFMA_PEAK,
-                     'traffic': traffic,
-                     'traffic_unit': 'bytes per launch (HBM, rocprofv3 FETCH_SIZE + WRITE_SIZE)',
-                     'traffic_note': traffic_note,
-                     'launches_per_step': k['launches'] / args.steps,
-                     'avg_launch_us': 1e6 * k['seconds'] / max(1, k['launches'])},
+        # the work that takes the most time per step (both timed live)
+        'roofline': (roof_zono if roof_zono is not None
+                     and roof_zono['ms_per_step'] >= roof_crown['ms_per_step'] else roof_crown),
+        'rooflines_timed': [r for r in (roof_zono, roof_crown) if r is not None],
         'secondary': secondary,
     }
     if not args.no_cpu_baseline:

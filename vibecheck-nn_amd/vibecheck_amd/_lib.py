@@ -249,8 +249,8 @@ def timing_end():
     torch.cuda.synchronize()
     out = {}
     for n, lst in (rec or {}).items():
-        per = [(s.elapsed_time(e) / 1e3, f, a) for s, e, f, a in lst]
-        _EV_FREE.extend((s, e) for s, e, _, _ in lst)
+        per = [(s.elapsed_time(e) / 1e3, f, a) for s, e, f, a, _ in lst]
+        _EV_FREE.extend(pool for _, _, _, _, pool in lst)
         out[n] = {'launches': len(per), 'seconds': sum(p[0] for p in per),
                   'flops': sum(p[1] for p in per), 'per_launch': per}
     return out
@@ -278,9 +278,12 @@ def timing_events(name, batch=None):
     return _event_pair()
 
 
-def timing_add(name, events, flops, args):
-    """File a launch timed with timing_events."""
-    _timing[name].append((events[0], events[1], flops, args))
+def timing_add(name, events, flops, args, pool=None):
+    """File a launch timed with timing_events.  ``pool``: the event pair
+    that goes back to the pool, when the span's (start, end) borrows an
+    event of another record (default: the span's own pair)."""
+    _timing[name].append((events[0], events[1], flops, args,
+                          pool if pool is not None else tuple(events)))
 
 
 def call(name, *args):
@@ -290,7 +293,7 @@ def call(name, *args):
         s.record()
         rc = getattr(lib, name)(*args)
         e.record()
-        _timing[name].append((s, e, _FLOPS.get(name, lambda a: 0.0)(args), args))
+        _timing[name].append((s, e, _FLOPS.get(name, lambda a: 0.0)(args), args, (s, e)))
         check(rc, name)
         return
     check(getattr(lib, name)(*args), name)

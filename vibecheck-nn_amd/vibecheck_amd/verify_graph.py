@@ -299,8 +299,9 @@ class PhaseTimer:
     phase, so the profiled run keeps the native round and its timing.
     alpha's own share of the bound time is reported beside it."""
 
-    def __init__(self, device):
+    def __init__(self, device, widths=True):
         self.device = torch.device(device)
+        self.widths = widths    # the clip's width sums (one small device buffer per round)
         self.t0 = time.perf_counter()
         self.rounds = []        # (5 events, widths tensor or None)
         self.crown_closed = 0
@@ -422,9 +423,14 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
         seeds = mlp_fused.SEED_COUNTER[seed_row]
         mlp_fused.SEED_ROW += 1
     ev = _lib.timing_events('vc_mlp_tiled_crown', B)
+    # the zonotope passes' span: from an event recorded before the call to
+    # the CROWN pass's start, which the round records right after them
+    zev = _lib.timing_events('zonotope_pass', B) if ev else None
+    if zev:
+        zev[0].record()
     pev_arr = pev_p = widths = None
     if phase_timer is not None:
-        pev, widths = phase_timer.begin(clip=True)
+        pev, widths = phase_timer.begin(clip=phase_timer.widths)
         pev_arr, pev_p = host_array(ctypes.c_void_p, [e.cuda_event for e in pev])
     fail = ctypes.c_int32(-1)
     try:
@@ -452,6 +458,8 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
     if ev:
         spec = _lib.mlp_crown_flops(plan.dims, plan.n, B, [0] * plan.n, 0, Q)
         _lib.timing_add('vc_mlp_tiled_crown', ev, spec, (None, None, None, None, B, seed_row))
+        if zev:
+            _lib.timing_add('zonotope_pass', (zev[0], ev[0]), 0.0, (B,), pool=zev)
     n_open, n_eval, n_unc, nf, nu, n_deg = (int(c) for c in counts)
     if phase_timer is not None:
         phase_timer.closures(B, n_unc, nf)
