@@ -87,19 +87,29 @@ def vz_sb(gg, xl, xh, dev):
     return vz._zono_sb(gg, xl, xh, dev, torch.float32)
 
 
-def run_rounds(gg, xl, xh, spec_ew, table, timers=None, keep=None):
+LOOKAHEAD = False  # --lookahead: each round but the last bounds the next batch while alpha runs
+
+
+def run_rounds(gg, xl, xh, spec_ew, table, timers=None, keep=None, lookahead=None):
     """Three BaB rounds; returns per-round stats.  ``keep`` (a list): each
-    round's batch and step outputs are appended to it."""
+    round's batch and step outputs are appended to it.  With ``lookahead``
+    each round but the last bounds the next one's batch while its alpha
+    runs (the same results)."""
     from vibecheck_amd import verify_graph as vg
+    if lookahead is None:
+        lookahead = LOOKAHEAD
     stats = []
-    for _ in range(N_ROUNDS):
+    pre = None
+    for r in range(N_ROUNDS):
         B = xl.shape[0]
         if B == 0:
             stats.append({'B': 0, 'closed': 0, 'alpha_leaves': 0, 'alpha_iters': 0})
             continue
         st = vg.bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
                          clip_enabled=True, alpha_iters=ALPHA_ITERS, alpha_all=True,
-                         alpha_lr=ALPHA_LR, timers=timers)
+                         alpha_lr=ALPHA_LR, timers=timers,
+                         lookahead=lookahead and r + 1 < N_ROUNDS, pre=pre)
+        pre = st.get('lookahead')
         if keep is not None:
             keep.append((xl, xh, st))
         (lxl, lxh), (hxl, hxh) = st['low'], st['high']
@@ -998,6 +1008,10 @@ def main():
                     help='c1 (default): the headline 65,536-box ACAS step; the others print '
                          'their own line')
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--lookahead', action='store_true',
+                    help='each round but the last clips, splits and bounds the next batch on '
+                         'the main stream while its alpha runs on a second one (the same '
+                         'results)')
     ap.add_argument('--no-secondary', action='store_true',
                     help='after the timed steps, skip the extra pass over the rounds '
                          '(near-zero counts, secondary rooflines, alpha rates): a profile '
@@ -1014,6 +1028,8 @@ def main():
     ap.add_argument('--hybrid', action='store_true',
                     help='only time the hybrid replay on ACAS-Xu-shaped leaves (one JSON line)')
     args = ap.parse_args()
+    global LOOKAHEAD
+    LOOKAHEAD = args.lookahead
     if args.gpus != 1:
         print(f'bench.py measures one GPU only (this build has no multi-GPU path); '
               f'got --gpus {args.gpus}', file=sys.stderr)
@@ -1159,7 +1175,8 @@ def main():
         'dtype': 'f32', 'data': 'synthetic (seeded boxes and Kaiming-normal weights)',
         'config': {'workload': '5-50x6-5 ReLU MLP, 65,536 input boxes, 3 BaB rounds, '
                                'CROWN intermediate + alpha-CROWN 20 it lr 0.1 + clip + '
-                               'widest split', 'domains_per_step': domains},
+                               'widest split', 'domains_per_step': domains,
+                   'lookahead': LOOKAHEAD},
         'alpha_iters_per_s': alpha_rates['open']['iters_per_s'] if alpha_rates else None,
         'alpha': ({'step_open_leaves': alpha_rates['open'], 'all_65536': alpha_rates['all']}
                   if alpha_rates else None),

@@ -877,8 +877,9 @@ int vc_best_rows_with_A(float *best, const float *lb, float *best_A,
  * device, sized for B rows: lb (B, Q), A (B, Q, n_in), acc (B, Q), closed
  * (B), unclosed (the first counts[2] entries), feasible (per unclosed row),
  * xl_split/xh_split/ax (the first counts[3] rows), low/high children (the
- * first counts[4] rows).  counts (host int64[6]) = {open leaves, alpha
- * iterations evaluated, unclosed, feasible, split, degenerate}.  work:
+ * first counts[4] rows).  counts (host int64[7]) = {open leaves, alpha
+ * iterations evaluated, unclosed, feasible, split, degenerate, handed-over
+ * children (-1: no lookahead)}.  work:
  * vc_mlp_bab_round_workspace(dims, n_relu, B, Q) bytes of device memory;
  * stop_host: as for vc_mlp_tiled_alpha_run.  seed_rows (nullable): as for
  * vc_mlp_tiled_crown; crown_ev0/crown_ev1 (nullable hipEvent_t): recorded
@@ -902,9 +903,31 @@ int vc_best_rows_with_A(float *best, const float *lb, float *best_A,
  * (:12962-12969).  VC_ERR_UNSUPPORTED when the net can have more zonotope
  * generators than VC_ZONO_WIDE_COLS.  Replaces one iteration of
  * _input_split_batched_inner's loop body (verify_graph.py:12855-13382),
- * as bab_step restates it. */
+ * as bab_step restates it.
+ *
+ * Lookahead (la_work non-null, with aux_stream: another stream of the same
+ * device at the default priority).  When alpha runs, it and the raise of
+ * its rows go to aux_stream with every chunk enqueued at once (stop_host is
+ * not used), while `stream` clips and splits the leaves the CROWN bound
+ * leaves open and runs the bound phase on all their children (the high
+ * halves first, then the low ones: the order in which a LIFO worklist pops
+ * the two pushes).  After alpha, the children of the leaves it closed are
+ * dropped, and the bound phase of the others -- the next batch, in its
+ * order -- is left at the start of la_work for the next round's `pre`;
+ * counts[6] is their number (2 counts[4]).  Each box's bounds depend on that
+ * box alone, and alpha only closes leaves, so the round and the next one
+ * give the results they give without it.  la_work:
+ * vc_mlp_bab_round_lookahead_workspace(dims, n_relu, B, Q, la_cap) bytes;
+ * more than la_cap children (or a bound workspace beyond la_bytes) skip
+ * the lookahead (counts[6] = -1).  pre (nullable): the la_work of the
+ * previous round's call, whose counts[6] is this call's B, with xl/xh that
+ * round's high then low children: the round takes its bound phase from there
+ * (crown_ev0/crown_ev1 and seed_rows are then not used).  la_work must stay
+ * untouched until the next round's call has returned. */
 int64_t vc_mlp_bab_round_workspace(const int32_t *dims, int n_relu, int64_t B,
                                    int Q);
+int64_t vc_mlp_bab_round_lookahead_workspace(const int32_t *dims, int n_relu,
+                                             int64_t B, int Q, int64_t la_cap);
 int vc_mlp_bab_round(const int32_t *dims, int n_relu, const float *frag,
                      const float *bias_cat, int Q, const float *spec_rows,
                      const float *spec_acc, const int32_t *d_ptr,
@@ -917,7 +940,9 @@ int vc_mlp_bab_round(const int32_t *dims, int n_relu, const float *frag,
                      float *low_xl, float *low_xh, float *high_xl,
                      float *high_xh, uint64_t *seed_rows, void *crown_ev0,
                      void *crown_ev1, void *const *phase_ev, double *clip_widths,
-                     void *work, int64_t work_bytes, int32_t *stop_host,
+                     void *work, int64_t work_bytes, const void *pre,
+                     void *la_work, int64_t la_bytes, int64_t la_cap,
+                     vc_stream_t aux_stream, int32_t *stop_host,
                      int64_t *pinned, int64_t *counts, int32_t *fail_phase,
                      vc_stream_t stream);
 

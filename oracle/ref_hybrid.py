@@ -80,7 +80,8 @@ def full_freeze(xl, xh, gg, spec_ew, n_iters_per_layer=100, n_iters_spec=100, lr
     alphas on the layers below, initialised to CROWN's lower slopes, Adam on
     -sum(lb) with clamp, early stop on the sum of the best, then the layer's
     bounds intersected with the best; then the same loop on the spec rows.
-    The early stop reads the best's sum in fp64.  Returns (tight,
+    The early stop reads the best's sum as torch's fp32 sum (the reference's
+    own read, verify_hybrid_acasxu.py:210, 246).  Returns (tight,
     alpha_per_layer, alpha_spec, best_spec)."""
     B = xl.shape[0]
     dt = xl.dtype

@@ -1084,6 +1084,77 @@ def test_bab_round_native_matches_python_round_nets(gpu, net, B, alpha_iters):
     _native_round_vs_python(gpu, gg, xl, xh, n_out, alpha_iters)
 
 
+def _rounds(gg, xl, xh, se, table, n_rounds, alpha_iters, lookahead):
+    out = []
+    pre = None
+    for r in range(n_rounds):
+        if xl.shape[0] == 0:
+            break
+        st = vg.bab_step(xl, xh, gg, se, table, crown_intermediate=True, clip_enabled=True,
+                         alpha_iters=alpha_iters, alpha_all=True, alpha_lr=0.1,
+                         lookahead=lookahead and r + 1 < n_rounds, pre=pre)
+        pre = st.get('lookahead')
+        out.append((st, pre))
+        (lxl, lxh), (hxl, hxh) = st['low'], st['high']
+        xl, xh = torch.cat([hxl, lxl], 0), torch.cat([hxh, lxh], 0)
+    return out
+
+
+@pytest.mark.parametrize('case', ['acas65536', 'acas4096', 'net64', 'net44', 'cap'])
+def test_bab_rounds_lookahead_bit_identical(gpu, case):
+    """Rounds whose alpha runs on a second stream while the round bounds
+    all children of its CROWN-open leaves (the lookahead), each next round
+    taking that bound phase (pre) with the children of the leaves alpha
+    closed dropped, against the same rounds in order: every output of every
+    round equal bit for bit, every count equal.  The benchmark's 65,536
+    boxes have leaves that alpha closes; with a capacity below the children
+    count ('cap') the lookahead is skipped and the rounds run in order."""
+    old = vg.LOOKAHEAD_MAX_CHILDREN
+    try:
+        if case == 'acas65536':
+            gg = wk.acas_gg(device=gpu, dtype=F32)
+            xl, xh = wk.acas_boxes(65536, seed=1, device=gpu, dtype=F32)
+            n_out, alpha_iters = 5, 20
+        elif case in ('acas4096', 'cap'):
+            _, gg, xl, xh = acas(gpu, 4096, seed=23, scale=2.0)
+            xl, xh = xl.to(gpu), xh.to(gpu)
+            n_out, alpha_iters = 5, 20
+            if case == 'cap':
+                vg.LOOKAHEAD_MAX_CHILDREN = 8
+        else:
+            net = [5, 64, 64, 64, 5] if case == 'net64' else [4, 44, 44, 4]
+            gg, xl, xh, n_out = _rows_case(gpu, net, 1500 if case == 'net64' else 500, 2.0)
+            alpha_iters = 10
+        _, se, dq = spec_pair(n_out, gpu)
+        table = vg.DisjunctTable(dq, gpu)
+        seq = _rounds(gg, xl, xh, se, table, 3, alpha_iters, False)
+        la = _rounds(gg, xl, xh, se, table, 3, alpha_iters, True)
+    finally:
+        vg.LOOKAHEAD_MAX_CHILDREN = old
+    assert len(seq) == len(la)
+    closed_by_alpha = 0
+    for r, ((a, pa), (b, pb)) in enumerate(zip(la, seq)):
+        assert pb is None
+        nu = a['low'][0].shape[0]
+        if r + 1 < len(la) and a['n_alpha_leaves'] > 0 and case != 'cap':
+            assert pa is not None and pa['n'] == 2 * nu, (r, pa and pa['n'], nu)
+        if case == 'cap':
+            assert pa is None or 2 * nu <= 8
+        closed_by_alpha += a['n_alpha_leaves'] - a['unclosed'].numel()
+        for k in ('n_alpha_leaves', 'n_alpha_iters', 'n_degenerate'):
+            assert a[k] == b[k], (r, k)
+        for k in ('lb', 'A', 'acc', 'closed', 'unclosed', 'xl_split', 'xh_split', 'ax'):
+            assert torch.equal(a[k], b[k]), (r, k)
+        assert (a['feasible'] is None) == (b['feasible'] is None)
+        if a['feasible'] is not None:
+            assert torch.equal(a['feasible'], b['feasible'])
+        for x, y in zip(a['low'] + a['high'], b['low'] + b['high']):
+            assert torch.equal(x, y), r
+    print(f'{case}: {len(la)} rounds, {closed_by_alpha} leaves closed by alpha')
+    if case == 'acas65536':
+        assert closed_by_alpha > 0
+
+
 def test_bab_step_parity_c0(gpu, mlp_path):
     """Config-0 shape: 4096 ACAS boxes, CROWN intermediate, clip, split."""
     gg_c, gg_g, xl, xh = acas(gpu, 4096)

@@ -112,6 +112,16 @@ int scatter_max_close(float* lb, const int64_t* idx, const float* src, int64_t n
 // the feasible rows (idx_f, cnt_f) and the feasible rows with a usable split
 // axis (idx_s, cnt_s), in one launch up to 2^17 rows; split_tmp (n bytes)
 // is used above that.
+// vc_mlp_tiled_alpha_run with the small-batch kernel's workgroups held to
+// cu_budget compute units' worth (0: the whole device).
+int alpha_run(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+              int64_t B, const float* xl, const float* xh, const float* const* lo,
+              const float* const* hi, float* const* alpha, float* const* exp_avg,
+              float* const* exp_avg_sq, int Q, const float* spec_rows, const float* spec_acc,
+              float* lb_out, float* best, double b1, double b2, double eps, double lr,
+              double lr_decay, int n_iters, double early_stop_eps, float* ctl,
+              int32_t* stop_host, int cu_budget, vc_stream_t stream);
+
 int compact_feasible_split(const uint8_t* feasible, const uint8_t* usable, int64_t n,
                            int64_t* idx_f, int64_t* cnt_f, int64_t* idx_s, int64_t* cnt_s,
                            uint8_t* split_tmp, void* ws, int64_t ws_bytes, hipStream_t st);

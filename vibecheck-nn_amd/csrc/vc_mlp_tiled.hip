@@ -2973,7 +2973,8 @@ int alpha_prepare(const int32_t* dims, int n_relu, const float* frag, const floa
                   int64_t B, const float* xl, const float* xh, const float* const* lo,
                   const float* const* hi, float* const* alpha, float* const* exp_avg,
                   float* const* exp_avg_sq, float* const* grad, int Q, const float* spec_rows,
-                  const float* spec_acc, const float* lb_out, AlphaLaunch& L) {
+                  const float* spec_acc, const float* lb_out, AlphaLaunch& L,
+                  int cu_budget = 0) {
   TGeom& G = L.G;
   int rc = tiled_geom(dims, n_relu, G);
   if (rc != VC_OK) return rc;
@@ -2994,8 +2995,9 @@ int alpha_prepare(const int32_t* dims, int n_relu, const float* frag, const floa
     if (in && grad && !L.aa.grad[l]) return VC_ERR_ARG;
   }
   const size_t fixed = ((size_t)G.nfloats + (size_t)n_relu * FW) * sizeof(float);
-  // small batches: every domain in flight at once, MT wavefronts each
-  const int cus = vcm::cu_count();
+  // small batches: every domain in flight at once, MT wavefronts each, on
+  // at most cu_budget compute units' worth of workgroups when given
+  const int cus = cu_budget > 0 ? std::min(cu_budget, vcm::cu_count()) : vcm::cu_count();
   const size_t per = (size_t)alpha_quad_floats(n_relu, G.KS, Q, G.MT) * sizeof(float);
   const int fit = fixed + per <= 160 * 1024 ? (int)((160 * 1024 - fixed) / per) : 0;
   const int D = (int)std::min<int64_t>(std::min(AQD, fit), (B + cus - 1) / cus);
@@ -3104,21 +3106,19 @@ __global__ void k_alpha_ctl_init(float* ctl) {
 }
 }  // namespace
 
-extern "C" int vc_mlp_tiled_alpha_run(const int32_t* dims, int n_relu, const float* frag,
-                                      const float* bias_cat, int64_t B, const float* xl,
-                                      const float* xh, const float* const* lo,
-                                      const float* const* hi, float* const* alpha,
-                                      float* const* exp_avg, float* const* exp_avg_sq, int Q,
-                                      const float* spec_rows, const float* spec_acc,
-                                      float* lb_out, float* best, double b1, double b2,
-                                      double eps, double lr, double lr_decay, int n_iters,
-                                      double early_stop_eps, float* ctl, int32_t* stop_host,
-                                      vc_stream_t stream) {
+namespace vcm {
+int alpha_run(const int32_t* dims, int n_relu, const float* frag, const float* bias_cat,
+              int64_t B, const float* xl, const float* xh, const float* const* lo,
+              const float* const* hi, float* const* alpha, float* const* exp_avg,
+              float* const* exp_avg_sq, int Q, const float* spec_rows, const float* spec_acc,
+              float* lb_out, float* best, double b1, double b2, double eps, double lr,
+              double lr_decay, int n_iters, double early_stop_eps, float* ctl,
+              int32_t* stop_host, int cu_budget, vc_stream_t stream) {
   if (!best || !ctl || n_iters < 1) return VC_ERR_ARG;
   if (B < 0) return VC_ERR_ARG;
   AlphaLaunch L;
   int rc = alpha_prepare(dims, n_relu, frag, bias_cat, B, xl, xh, lo, hi, alpha, exp_avg,
-                         exp_avg_sq, nullptr, Q, spec_rows, spec_acc, lb_out, L);
+                         exp_avg_sq, nullptr, Q, spec_rows, spec_acc, lb_out, L, cu_budget);
   if (rc != VC_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(k_alpha_ctl_init, dim3(1), dim3(64), 0, st, ctl);
@@ -3158,6 +3158,22 @@ extern "C" int vc_mlp_tiled_alpha_run(const int32_t* dims, int n_relu, const flo
     if (rc != VC_OK) return rc;
   }
   return VC_OK;
+}
+}  // namespace vcm
+
+extern "C" int vc_mlp_tiled_alpha_run(const int32_t* dims, int n_relu, const float* frag,
+                                      const float* bias_cat, int64_t B, const float* xl,
+                                      const float* xh, const float* const* lo,
+                                      const float* const* hi, float* const* alpha,
+                                      float* const* exp_avg, float* const* exp_avg_sq, int Q,
+                                      const float* spec_rows, const float* spec_acc,
+                                      float* lb_out, float* best, double b1, double b2,
+                                      double eps, double lr, double lr_decay, int n_iters,
+                                      double early_stop_eps, float* ctl, int32_t* stop_host,
+                                      vc_stream_t stream) {
+  return vcm::alpha_run(dims, n_relu, frag, bias_cat, B, xl, xh, lo, hi, alpha, exp_avg,
+                        exp_avg_sq, Q, spec_rows, spec_acc, lb_out, best, b1, b2, eps, lr,
+                        lr_decay, n_iters, early_stop_eps, ctl, stop_host, 0, stream);
 }
 
 namespace {

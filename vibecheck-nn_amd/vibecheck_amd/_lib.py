@@ -118,9 +118,10 @@ SIGNATURES = {
     'vc_mlp_zono_wide': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P],
     'vc_mlp_tiled_zono_wide': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P],
     'vc_mlp_bab_round_workspace': [_P, _I, _L, _I],
+    'vc_mlp_bab_round_lookahead_workspace': [_P, _I, _L, _I, _L],
     'vc_mlp_bab_round': [_P, _I, _P, _P, _I, _P, _P, _P, _P, _I, _L, _P, _P, _I, _D, _D, _D,
                          _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                         _P, _P, _L, _P, _P, _P, _P, _P],
+                         _P, _P, _L, _P, _P, _L, _L, _P, _P, _P, _P, _P, _P],
     'vc_widest_axis': [_P, _P, _L, _I, _P, _P, _P],
     'vc_bisect': [_P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P],
 }
@@ -128,6 +129,7 @@ _RESTYPE = {'vc_compact_workspace': ctypes.c_int64,
             'vc_conv_t_pack_floats': ctypes.c_int64,
             'vc_mlp_crown_rows_workspace': ctypes.c_int64,
             'vc_mlp_bab_round_workspace': ctypes.c_int64,
+            'vc_mlp_bab_round_lookahead_workspace': ctypes.c_int64,
             'vc_mlp_frag_floats': ctypes.c_int64,
             'vc_mlp_tiled_floats': ctypes.c_int64}
 

@@ -287,6 +287,27 @@ class ChunkWorklist:
 # applies; switching this off runs the same entry points from Python.
 NATIVE_ROUND = True
 
+# Whether the driver asks the native round to bound the next batch while
+# alpha runs (bab_step's ``lookahead``).  Off: on the ACAS-Xu rounds alpha
+# and the children's bound phase compete for the same compute units (each
+# workgroup of either holds the net's weights in LDS), and the overlap
+# measured no faster than the rounds in order.
+LOOKAHEAD = False
+# The most children a lookahead bounds (beyond that the round runs in order).
+LOOKAHEAD_MAX_CHILDREN = 16384
+
+_AUX_STREAMS = {}
+
+
+def _aux_stream(dev):
+    """A second stream of the device, at the default priority (the
+    lookahead's alpha runs there)."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    s = _AUX_STREAMS.get(idx)
+    if s is None:
+        s = _AUX_STREAMS[idx] = torch.cuda.Stream(device=idx)
+    return s.cuda_stream
+
 
 class PhaseTimer:
     """The driver's per-phase profile (verify_graph.py:12814-12833,
@@ -378,12 +399,16 @@ def _tag_phase(e, phase):
 
 
 def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_lr_decay,
-                      phase_timer=None):
+                      phase_timer=None, lookahead=False, pre=None):
     """bab_step's round (crown intermediate bounds, clip, alpha-CROWN on
     every open leaf) as one call of the native round orchestration, for
     nets with the shape-specialised kernels; None where it does not apply.
     Same entry points in the same order as the Python round, so the same
-    results."""
+    results.  ``lookahead``: while alpha runs on a second stream, clip and
+    split the leaves the CROWN bound leaves open and run the bound phase on
+    all their children; the result's 'lookahead' then holds the bound
+    phase of the round's children (high then low) for the next round's
+    ``pre``."""
     from . import mlp_fused
     from . import verify_zono_bnb as vz
     dev = xl.device
@@ -415,19 +440,31 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
     lib = _lib.load()
     nws = int(lib.vc_mlp_bab_round_workspace(plan.dims_p, plan.n, B, Q))
     ws = torch.empty(max(nws, 8), dtype=torch.uint8, device=dev)
-    counts = (ctypes.c_int64 * 6)()
+    counts = (ctypes.c_int64 * 7)()
+    if pre is not None and (pre.get('n') != B or pre.get('plan') is not plan
+                            or pre.get('spec') is not spec_ew):
+        pre = None
+    la = None
+    la_bytes = la_cap = 0
+    if lookahead and alpha_iters > 0 and phase_timer is None and B > 0:
+        la_cap = min(2 * B, LOOKAHEAD_MAX_CHILDREN)
+        la_bytes = int(lib.vc_mlp_bab_round_lookahead_workspace(plan.dims_p, plan.n, B, Q,
+                                                                 la_cap))
+        la = torch.empty(max(la_bytes, 8), dtype=torch.uint8, device=dev)
     # work accounting and timing of the CROWN launch, as mlp_fused.crown does
-    seeds = seed_row = None
-    if mlp_fused.SEED_COUNTER is not None:
-        seed_row = mlp_fused.SEED_ROW
-        seeds = mlp_fused.SEED_COUNTER[seed_row]
-        mlp_fused.SEED_ROW += 1
-    ev = _lib.timing_events('vc_mlp_tiled_crown', B)
-    # the zonotope passes' span: from an event recorded before the call to
-    # the CROWN pass's start, which the round records right after them
-    zev = _lib.timing_events('zonotope_pass', B) if ev else None
-    if zev:
-        zev[0].record()
+    # (a handed-over bound phase ran inside the previous round's call)
+    seeds = seed_row = ev = zev = None
+    if pre is None:
+        if mlp_fused.SEED_COUNTER is not None:
+            seed_row = mlp_fused.SEED_ROW
+            seeds = mlp_fused.SEED_COUNTER[seed_row]
+            mlp_fused.SEED_ROW += 1
+        ev = _lib.timing_events('vc_mlp_tiled_crown', B)
+        # the zonotope passes' span: from an event recorded before the call
+        # to the CROWN pass's start, which the round records right after them
+        zev = _lib.timing_events('zonotope_pass', B) if ev else None
+        if zev:
+            zev[0].record()
     pev_arr = pev_p = widths = None
     if phase_timer is not None:
         pev, widths = phase_timer.begin(clip=phase_timer.widths)
@@ -441,7 +478,10 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
              p + o_flg, p + o_idx, p + o_flg + Bm, p_box, p_box + nb, p + o_idx + 8 * Bm,
              p_box + 2 * nb, p_box + 3 * nb, p_box + 4 * nb, p_box + 5 * nb, ptr(seeds),
              ev[0].cuda_event if ev else None, ev[1].cuda_event if ev else None, pev_p,
-             ptr(widths), ws.data_ptr(), nws, mlp_fused._stop_word().data_ptr(),
+             ptr(widths), ws.data_ptr(), nws,
+             pre['buf'].data_ptr() if pre is not None else None,
+             la.data_ptr() if la is not None else None, la_bytes, la_cap,
+             _aux_stream(dev) if la is not None else None, mlp_fused._stop_word().data_ptr(),
              mlp_fused._pinned_words().data_ptr(), ctypes.addressof(counts),
              ctypes.addressof(fail), stream())
     except RuntimeError as e:
@@ -460,7 +500,7 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
         _lib.timing_add('vc_mlp_tiled_crown', ev, spec, (None, None, None, None, B, seed_row))
         if zev:
             _lib.timing_add('zonotope_pass', (zev[0], ev[0]), 0.0, (B,), pool=zev)
-    n_open, n_eval, n_unc, nf, nu, n_deg = (int(c) for c in counts)
+    n_open, n_eval, n_unc, nf, nu, n_deg, n_next = (int(c) for c in counts)
     if phase_timer is not None:
         phase_timer.closures(B, n_unc, nf)
     # the views by absolute storage offsets (in elements of each dtype)
@@ -480,6 +520,8 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
            'low': (ast(fl, (nu, n_in), r, bo + 2 * nb), ast(fl, (nu, n_in), r, bo + 3 * nb)),
            'high': (ast(fl, (nu, n_in), r, bo + 4 * nb), ast(fl, (nu, n_in), r, bo + 5 * nb))}
     out['chunks'] = [out['low'], out['high']] if nu > 0 else []
+    out['lookahead'] = ({'buf': la, 'n': n_next, 'plan': plan, 'spec': spec_ew}
+                        if la is not None and n_next >= 0 else None)
     return out
 
 
@@ -506,7 +548,7 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
              clip_enabled=True, alpha_iters=0, alpha_all=False, alpha_eps=0.0,
              alpha_max_leaves=200, alpha_lr=0.25, alpha_lr_decay=0.98,
              timers=None, branch_sb=False, sb_margin=False, sb_thr=0.01, sb_mw=1.0,
-             split_depth=1, clip_iters=1, phase_timer=None):
+             split_depth=1, clip_iters=1, phase_timer=None, lookahead=False, pre=None):
     """One BaB iteration on a popped batch (verify_graph.py:12855-13423):
     bound, closure, optional alpha-CROWN on unclosed leaves (opportunistic:
     a RuntimeError or OOM inside it keeps the bound it had, as at
@@ -518,12 +560,20 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
     dict of device tensors (same keys as the oracle's bab_step; ``chunks``
     are the worklist pushes in order).  ``phase_timer`` (a PhaseTimer)
     records the round's phase events.  An error after the bound phase
-    carries ``vc_phase`` ('clip' or 'split')."""
+    carries ``vc_phase`` ('clip' or 'split').
+
+    ``lookahead`` (extension, native round only): while alpha runs, the
+    round also bounds every child of the leaves the CROWN bound leaves
+    open; the result's 'lookahead' (None when it did not run) is the bound
+    phase of the round's children in the order cat(high, low), which the
+    next call takes as ``pre`` when its batch is exactly that.  Each box's
+    bounds depend on that box alone, so the results are the same as
+    without it."""
     _widths(gg, xl.shape[1])
     if (NATIVE_ROUND and timers is None and crown_intermediate and clip_enabled
             and (alpha_iters == 0 or alpha_all) and not branch_sb and clip_iters == 1):
         out = _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr,
-                                alpha_lr_decay, phase_timer)
+                                alpha_lr_decay, phase_timer, lookahead=lookahead, pre=pre)
         if out is not None:
             return out
     pev = pw = None
@@ -736,6 +786,7 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
     xh0 = torch.as_tensor(spec.x_hi, dtype=dtype, device=dev).flatten()
     wl = ChunkWorklist(xl0, xh0)
     n_leaves = n_iters = n_open = 0
+    pre = None
     pt = None
     if (bool(_setting(settings, 'input_split_batched_phase_timing', False))
             or os.environ.get('VC_PHASE_TIMING', '') == '1'):
@@ -755,6 +806,11 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
             break
         B = min(batch_size, wl_n)
         xl_b, xh_b = wl.pop(B)
+        # a previous lookahead applies when this pop took exactly the two
+        # chunks it pushed (high, then low); with the worklist now empty, the
+        # next pop will be this round's children, so this round looks ahead
+        use_pre = pre if (pre is not None and pre['n'] == B and not wl) else None
+        pre = None
         try:
             # K > 1 only grows a queue that does not fill the batch
             # (verify_graph.py:13343-13344)
@@ -764,7 +820,8 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
                           branch_sb=branch_sb, sb_margin=sb_margin,
                           sb_thr=sb_thr, sb_mw=sb_mw,
                           split_depth=split_depth if B < batch_size else 1,
-                          clip_iters=clip_iters, phase_timer=pt)
+                          clip_iters=clip_iters, phase_timer=pt,
+                          lookahead=LOOKAHEAD and not wl, pre=use_pre)
         except RuntimeError as e:
             # torch.cuda.OutOfMemoryError is a RuntimeError; only the bound
             # phase's errors halve the batch
@@ -786,6 +843,7 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
         n_open += st['n_degenerate']
         for c in st['chunks']:
             wl.push(*c)
+        pre = st.get('lookahead')
         n_iters += 1
         if wl.size() > max_worklist:
             return done('unknown', {'phase': 'batched_worklist_overflow',
