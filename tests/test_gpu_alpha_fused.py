@@ -201,3 +201,46 @@ def test_fused_alpha_step_map_teacher_forced(gpu, B):
     n_checked = 6 * B * Q
     print(f'{kernel}: {totals[0]} scale escapes, {totals[1]} fp64 escapes of {n_checked}')
     assert totals[0] + totals[1] <= n_checked // 1000, totals
+
+
+def test_alpha_kernel_forms_bit_identical(gpu):
+    """One alpha iteration of the same 384 domains inside batches of 384
+    (the quad kernel's instance unrolled for six relu layers, two domains
+    per workgroup), 900 (the general quad kernel, four per workgroup) and
+    2,048 (k_alpha_tiled, one wavefront per domain): bounds, gradient and
+    Adam state equal bit for bit (each domain's iteration is its own)."""
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    sizes = (384, 900, 2048)
+    assert 384 <= 2 * n_cu and 2 * n_cu < 900 <= 4 * n_cu < 2048, n_cu
+    gg = wk.acas_gg(device=gpu, dtype=F32)
+    xl, xh = wk.acas_boxes(2048, seed=33, device=gpu, dtype=F32)
+    c, r = (xl + xh) / 2, (xh - xl) / 2
+    xl, xh = (c - 4 * r).contiguous(), (c + 4 * r).contiguous()
+    spec, _ = _util.spec_for(5, dtype=F32)
+    se = {q: (w.to(gpu), b) for q, (w, b) in spec.items()}
+    plan = mf.plan_for(gg, gpu)
+    Wq, bq = vz._spec_rows(se, gpu)
+    S, acc0 = mf.fold_spec(plan, Wq, bq)
+    Q = S.shape[0]
+    sb = vz._zono_sb(gg, xl, xh, gpu, F32)
+    Ls = sorted(sb)
+    out = {}
+    for B in sizes:
+        lo = [sb[L][0][:B].contiguous() for L in Ls]
+        hi = [sb[L][1][:B].contiguous() for L in Ls]
+        st = [[torch.zeros_like(t) for t in lo] for _ in range(3)]
+        gr = [torch.full_like(t, float('nan')) for t in lo]
+        lb = torch.empty(B, Q, device=gpu)
+        keep = [host_array(ctypes.c_void_p, [ptr(t) for t in ts]) for ts in (lo, hi, *st, gr)]
+        call('vc_mlp_tiled_alpha_iter', plan.dims_p, plan.n, ptr(plan.tfrag),
+             ptr(plan.bias_cat), B, ptr(xl[:B]), ptr(xh[:B]), *[k[1] for k in keep], Q,
+             ptr(S), ptr(acc0), ptr(lb), B1, B2, EPS, LR / (1 - B1), (1 - B2) ** 0.5, 1, None,
+             stream())
+        torch.cuda.synchronize()
+        out[B] = (lb[:384], [t[:384] for t in st[0] + st[1] + st[2] + gr])
+    ref_lb, ref_st = out[384]
+    for B in sizes[1:]:
+        lb, sts = out[B]
+        assert torch.equal(lb, ref_lb), (B, int((lb != ref_lb).sum()))
+        for k, (a, b) in enumerate(zip(sts, ref_st)):
+            assert torch.equal(a, b), (B, k)

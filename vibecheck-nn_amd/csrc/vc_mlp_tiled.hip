@@ -1111,8 +1111,12 @@ __device__ __forceinline__ void quad_exchange(float* xbuf, int w, int g, int r, 
   }
 }
 
-template <int MT, int KS, bool BROW>
-__global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
+// NL > 0: a net of exactly NL relu layers, every layer loop unrolled (the
+// layer widths then come from fixed kernel-argument offsets, read once,
+// instead of a scalar load inside each layer's MFMA chain), at most two
+// domains per workgroup.
+template <int MT, int KS, bool BROW, int NL = 0>
+__global__ __launch_bounds__(NL > 0 ? 2 * MT * 64 : AQD * 4 * 64) void k_alpha_quad(
     TGeom G, const float* __restrict__ gfrag, const float* __restrict__ gbias, int64_t B,
     const float* __restrict__ xl, const float* __restrict__ xh, TAlphaArgs aa, int Q,
     const float* __restrict__ spec_rows, const float* __restrict__ spec_acc,
@@ -1124,7 +1128,7 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int qd = wid / MT, w = wid - qd * MT;  // domain slot, owned M-tile
   const int g = lane >> 4, r = lane & 15;
-  const int n = G.n, d0 = G.d[0], dN = G.d[n];
+  const int n = NL > 0 ? NL : G.n, d0 = G.d[0], dN = G.d[n];
   const bool live = r < Q;
   float* ssl = sbias + n * FW + qd * alpha_quad_floats(n, KS, Q, MT);  // [l][ls, us, ut, un][FW]
   float* sad = ssl + n * 4 * FW;                                        // [l][alpha, m, v][FW]
@@ -1199,6 +1203,7 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
     double cz = 0.0;
     v4f GEw = v4f{0.f, 0.f, 0.f, 0.f};
     int xb = 0;
+#pragma unroll
     for (int l = n - 1; l >= 0; --l) {
       const float* sl = ssl + l * 4 * FW;
       float* pl = sP + l * KS * 4 * Q;
@@ -1289,6 +1294,7 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
     }
     // ---- forward gradient sweep, owned neurons; the Adam update of every
     // layer follows it (it changes only the next iteration's slopes)
+#pragma unroll
     for (int l = 0; l < n; ++l) {
       const int dW = G.d[l + 1];
       float* sl = ssl + l * 4 * FW;
@@ -1384,10 +1390,20 @@ __global__ __launch_bounds__(AQD * 4 * 64) void k_alpha_quad(
   }
 }
 
+// The quad kernel for n relu layers and D domains per workgroup: the
+// unrolled instance for the 50-wide variant at the depth of ACAS-Xu's nets
+// (6 relu layers), else the general one.
+constexpr int kQuadUnrolledV = 3, kQuadUnrolledN = 6;
+
 template <int V>
-const void* alpha_quad_fn() {
-  return reinterpret_cast<const void*>(
-      &k_alpha_quad<kVariants[V].MT, kVariants[V].KS, kVariants[V].brow != 0>);
+const void* alpha_quad_fn(int n, int D) {
+  constexpr int MT = kVariants[V].MT, KS = kVariants[V].KS;
+  constexpr bool BR = kVariants[V].brow != 0;
+  if constexpr (V == kQuadUnrolledV) {
+    if (n == kQuadUnrolledN && D <= 2)
+      return reinterpret_cast<const void*>(&k_alpha_quad<MT, KS, BR, kQuadUnrolledN>);
+  }
+  return reinterpret_cast<const void*>(&k_alpha_quad<MT, KS, BR>);
 }
 
 template <int V>
@@ -3005,12 +3021,12 @@ int alpha_prepare(const int32_t* dims, int n_relu, const float* frag, const floa
   if (B >= 1 && B <= (int64_t)cus * AQD && D >= 1) {
     const void* fq = nullptr;
     switch (G.variant) {
-      case 0: fq = alpha_quad_fn<0>(); break;
-      case 1: fq = alpha_quad_fn<1>(); break;
-      case 2: fq = alpha_quad_fn<2>(); break;
-      case 3: fq = alpha_quad_fn<3>(); break;
-      case 4: fq = alpha_quad_fn<4>(); break;
-      case 5: fq = alpha_quad_fn<5>(); break;
+      case 0: fq = alpha_quad_fn<0>(n_relu, D); break;
+      case 1: fq = alpha_quad_fn<1>(n_relu, D); break;
+      case 2: fq = alpha_quad_fn<2>(n_relu, D); break;
+      case 3: fq = alpha_quad_fn<3>(n_relu, D); break;
+      case 4: fq = alpha_quad_fn<4>(n_relu, D); break;
+      case 5: fq = alpha_quad_fn<5>(n_relu, D); break;
       default: return VC_ERR_UNSUPPORTED;
     }
     if (vcm::allow_max_lds(fq)) {
