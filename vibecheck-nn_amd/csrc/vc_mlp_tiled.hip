@@ -164,14 +164,16 @@ __device__ __forceinline__ double group_sum4_d(double v) {
 //   e = pos(x) ls + neg(x) us = x * (x < 0 ? us : ls),  acc += neg(x) ut
 // and, without the bias row, acc += e . bias.  sl: ls, us, ut [FW] each,
 // zero beyond the layer width; bl: the next fc's bias, zero-padded to FW.
-template <int KS, int NP, bool BROW>
+// SGN: the upper slopes carry a flag in their sign bit (alpha's unstable
+// neurons); their magnitude is the slope.
+template <int KS, int NP, bool BROW, bool SGN = false>
 __device__ __forceinline__ void relax_rows(const float* sl, const float* bl, int g,
                                            v4f (&F)[TNP][4], double (&acc)[TNP]) {
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const int t = ks >> 2, i = ks & 3;
     const int j = 16 * t + 4 * g + i;
-    const float ls = sl[j], us = sl[FW + j], ut = sl[2 * FW + j];
+    const float ls = sl[j], us = SGN ? fabsf(sl[FW + j]) : sl[FW + j], ut = sl[2 * FW + j];
     const float bj = BROW ? 0.f : bl[j];
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -662,7 +664,7 @@ __global__ __launch_bounds__(TNW * 64) void k_crown_dom(
 // the clamp to [0, 1].  Forward products read the backward fragments with a
 // lane permutation; with the bias row, the bias enters as a constant-1
 // entry of the gradient at index d_{l+1}.
-constexpr int ANW = 4;  // waves per workgroup
+constexpr int ANW = 8;  // waves per workgroup at most (as many as the LDS holds)
 
 struct TAlphaArgs {
   const float* lo[MAXL];
@@ -822,30 +824,30 @@ __device__ __forceinline__ void fc_forward_rem(const float4* fr, const float* wk
     for (int i = 0; i < 4; ++i) out[x][MF][i] = (g == 0 && i < MR) ? rem[x][i < MR ? i : 0] : 0.f;
 }
 
-// Per-wave LDS of the alpha kernels: slopes [l][ls_eff, us, ut, unstable][FW],
-// Adam state [l][alpha, m, v][FW], the pre-relaxation rows P_l
-// [l][ks][g][r < Q], d lb / d alpha of one layer [FW], the box [2 FW].
+// Per-wave LDS of k_alpha_tiled: slopes [l][ls_eff, us, ut][FW] (us with
+// the sign bit set on the unstable neurons: -0.0 for a zero slope), the
+// pre-relaxation rows P_l [l][ks][g][r < Q], d lb / d alpha of one layer
+// [FW], the box [2 FW].  alpha and its Adam state stay in global memory.
 __host__ __device__ inline int alpha_wsz(int n, int KS, int Q) {
-  return n * 7 * FW + n * KS * 4 * Q + 3 * FW;
+  return n * 3 * FW + n * KS * 4 * Q + 3 * FW;
 }
 
 struct AlphaLds {
-  float *ssl, *sad, *sP, *sga, *sx;
+  float *ssl, *sP, *sga, *sx;
 };
 
 __device__ __forceinline__ AlphaLds alpha_lds_at(float* w, int n, int KS, int Q) {
   AlphaLds a;
   a.ssl = w;
-  a.sad = a.ssl + n * 4 * FW;
-  a.sP = a.sad + n * 3 * FW;
+  a.sP = a.ssl + n * 3 * FW;
   a.sga = a.sP + n * KS * 4 * Q;
   a.sx = a.sga + FW;
   return a;
 }
 
-// The box and the per-neuron state of domain dom into the wave's LDS: the
-// relaxation of the starting bounds and alpha with its Adam state (init:
-// alpha = (up_s > 0.5) * unstable, state zero).
+// The box and the slopes of domain dom into the wave's LDS: the relaxation
+// of the starting bounds with the lower slope of the unstable neurons
+// alpha (init: alpha = (up_s > 0.5) * unstable).
 template <int KS>
 __device__ __forceinline__ void alpha_load(const TGeom& G, const TAlphaArgs& aa,
                                            const float* xl, const float* xh, int64_t dom,
@@ -856,53 +858,41 @@ __device__ __forceinline__ void alpha_load(const TGeom& G, const TAlphaArgs& aa,
 #pragma unroll 4
   for (int l = 0; l < n; ++l) {
     const int dW = G.d[l + 1];
-    float* sl = w.ssl + l * 4 * FW;
-    float* sa = w.sad + l * 3 * FW;
+    float* sl = w.ssl + l * 3 * FW;
     for (int j = lane; j < FW; j += 64) {
-      float ls = 0.f, us = 0.f, ut = 0.f, un = 0.f, a = 0.f, m1 = 0.f, m2 = 0.f;
+      float ls = 0.f, us = 0.f, ut = 0.f;
       if (j < dW) {
         const int64_t ai = dom * dW + j;
         const Relax s = relax(aa.lo[l][ai], aa.hi[l][ai]);
-        if (init) {
-          // first iteration: alpha = (up_s > 0.5) * unstable, Adam state zero
-          a = (s.unstable && s.up_s > 0.5f) ? 1.f : 0.f;
-        } else {
-          a = aa.alpha[l][ai];
-          m1 = aa.m1[l][ai];
-          m2 = aa.m2[l][ai];
-        }
+        // first iteration: alpha = (up_s > 0.5) * unstable
+        const float a =
+            init ? ((s.unstable && s.up_s > 0.5f) ? 1.f : 0.f) : aa.alpha[l][ai];
         ls = s.active ? 1.f : (s.unstable ? a : 0.f);
-        us = s.up_s;
+        us = s.unstable ? -s.up_s : s.up_s;
         ut = s.up_t;
-        un = s.unstable ? 1.f : 0.f;
       }
       sl[j] = ls;
       sl[FW + j] = us;
       sl[2 * FW + j] = ut;
-      sl[3 * FW + j] = un;
-      sa[j] = a;
-      sa[FW + j] = m1;
-      sa[2 * FW + j] = m2;
     }
   }
 }
 
-// One alpha-CROWN iteration of the wave's domain from its LDS state: the
+// One alpha-CROWN iteration of the wave's domain from its LDS slopes: the
 // spec backward keeping P_l, fc_0 with the concretization, the forward
-// gradient sweep and the Adam update of alpha (clamped to [0, 1]).  With
-// keep_ls the lower slopes of the unstable neurons follow the new alpha
-// (for a next iteration on the same LDS state).  Returns the lane's row
-// bound (rows r < Q, lanes g == 0).
+// gradient sweep and the Adam update of alpha (clamped to [0, 1]) on its
+// global state, which it writes back for every neuron (init: from alpha =
+// (up_s > 0.5) * unstable and a zero state).  Returns the lane's row bound
+// (rows r < Q, lanes g == 0).
 template <int MT, int KS, bool BROW>
 __device__ __forceinline__ double alpha_pass(const TGeom& G, const AlphaLds& w, const float* fr0,
                                              const float4* frh, const float* sbias, int Q,
                                              const float* spec_rows, const float* spec_acc,
-                                             const AdamConst& adam, bool keep_ls, int lane,
-                                             int g, int r, const TAlphaArgs& aa, int64_t dom) {
+                                             const AdamConst& adam, int init, int lane, int g,
+                                             int r, const TAlphaArgs& aa, int64_t dom) {
   const int n = G.n, d0 = G.d[0], dN = G.d[n];
   const bool live = r < Q;
   float* ssl = w.ssl;
-  float* sad = w.sad;
   float* sP = w.sP;
   float* sga = w.sga;
   const float* dxl = w.sx;
@@ -925,7 +915,7 @@ __device__ __forceinline__ double alpha_pass(const TGeom& G, const AlphaLds& w, 
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) pl[(ks * 4 + g) * Q + r] = F[0][ks >> 2][ks & 3];
     }
-    relax_rows<KS, 1, BROW>(ssl + l * 4 * FW, sbias + l * FW, g, F, acc);
+    relax_rows<KS, 1, BROW, true>(ssl + l * 3 * FW, sbias + l * FW, g, F, acc);
     if (l > 0) fc_hidden<MT, KS, 1, BROW>(frh + (l - 1) * KS * 64, lane, g, G.d[l], F, acc);
   }
   // ---- fc_0, concretization and gE_0 = W_0 gA + b_0, one input tile at a time
@@ -968,10 +958,25 @@ __device__ __forceinline__ double alpha_pass(const TGeom& G, const AlphaLds& w, 
       }
   }
   const double lbd = group_sum4_d(acc[0] + cz[0]);
-  // ---- forward gradient sweep with the Adam update per layer
+  // ---- forward gradient sweep with the Adam update per layer; each
+  // layer's alpha and Adam state are requested one layer ahead
+  float ca = 0.f, cm = 0.f, cv = 0.f;
+  if (!init && lane < G.d[1]) {
+    const int64_t ai = dom * G.d[1] + lane;
+    ca = aa.alpha[0][ai];
+    cm = aa.m1[0][ai];
+    cv = aa.m2[0][ai];
+  }
   for (int l = 0; l < n; ++l) {
     const int dW = G.d[l + 1];
-    float* sl = ssl + l * 4 * FW;
+    float* sl = ssl + l * 3 * FW;
+    float na = 0.f, nm = 0.f, nv = 0.f;
+    if (!init && l + 1 < n && lane < G.d[l + 2]) {
+      const int64_t ai = dom * G.d[l + 2] + lane;
+      na = aa.alpha[l + 1][ai];
+      nm = aa.m1[l + 1][ai];
+      nv = aa.m2[l + 1][ai];
+    }
     if (!BROW) {
       // bias of fc_l (l >= 0) added for live rows: gE_l += b_l
 #pragma unroll
@@ -990,25 +995,31 @@ __device__ __forceinline__ double alpha_pass(const TGeom& G, const AlphaLds& w, 
       const float s = row_sum16(ge * fmaxf(pv, 0.f));
       if (r == 0) sga[j] = s;
       const bool mp = pv >= 0.f, mn = pv <= 0.f;
-      float gp = ge * ((mp ? sl[j] : 0.f) + (mn ? sl[FW + j] : 0.f));
+      float gp = ge * ((mp ? sl[j] : 0.f) + (mn ? fabsf(sl[FW + j]) : 0.f));
       if (mn) gp = gp + sl[2 * FW + j];
       GE[t][i] = live ? gp : 0.f;
     }
     __threadfence_block();
     {
-      float* sa = sad + l * 3 * FW;
       const int j = lane;
-      const bool un = j < dW && sl[3 * FW + j] != 0.f;
-      if (un) {
-        float mi = sa[FW + j], vi = sa[2 * FW + j];
-        float pa = adam_update(sa[j], -sga[j], mi, vi, adam);
-        pa = fminf(fmaxf(pa, 0.f), 1.f);
-        sa[FW + j] = mi;
-        sa[2 * FW + j] = vi;
-        sa[j] = pa;
-        if (keep_ls) sl[j] = pa;  // unstable: ls_eff = alpha
+      if (j < dW) {
+        const float usg = sl[FW + j];
+        const bool un = signbit(usg);
+        float a = init ? ((un && fabsf(usg) > 0.5f) ? 1.f : 0.f) : ca;
+        float mi = cm, vi = cv;
+        if (un) {
+          const float pa = adam_update(a, -sga[j], mi, vi, adam);
+          a = fminf(fmaxf(pa, 0.f), 1.f);
+        }
+        const int64_t ai = dom * dW + j;
+        aa.alpha[l][ai] = a;
+        aa.m1[l][ai] = mi;
+        aa.m2[l][ai] = vi;
+        if (aa.grad[l]) aa.grad[l][ai] = un ? sga[j] : 0.f;
       }
-      if (aa.grad[l] && j < dW) aa.grad[l][dom * dW + j] = un ? sga[j] : 0.f;
+      ca = na;
+      cm = nm;
+      cv = nv;
     }
     __threadfence_block();
     if (l + 1 < n) {
@@ -1024,21 +1035,6 @@ __device__ __forceinline__ double alpha_pass(const TGeom& G, const AlphaLds& w, 
     }
   }
   return lbd;
-}
-
-// The updated Adam state of domain dom back to global memory (coalesced).
-__device__ __forceinline__ void alpha_store(const TGeom& G, const TAlphaArgs& aa, int64_t dom,
-                                            const AlphaLds& w, int lane) {
-  for (int l = 0; l < G.n; ++l) {
-    const int dW = G.d[l + 1];
-    const float* sa = w.sad + l * 3 * FW;
-    for (int j = lane; j < dW; j += 64) {
-      const int64_t ai = dom * dW + j;
-      aa.alpha[l][ai] = sa[j];
-      aa.m1[l][ai] = sa[FW + j];
-      aa.m2[l][ai] = sa[2 * FW + j];
-    }
-  }
 }
 
 template <int MT, int KS, bool BROW>
@@ -1063,13 +1059,13 @@ __global__ __launch_bounds__(ANW * 64) void k_alpha_tiled(
   __syncthreads();
   const float* fr0 = sfrag;
   const float4* frh = reinterpret_cast<const float4*>(sfrag + G.offh);
-  for (int64_t dom = (int64_t)blockIdx.x * ANW + wv; dom < B; dom += (int64_t)gridDim.x * ANW) {
+  const int nwv = blockDim.x >> 6;
+  for (int64_t dom = (int64_t)blockIdx.x * nwv + wv; dom < B; dom += (int64_t)gridDim.x * nwv) {
     alpha_load<KS>(G, aa, xl, xh, dom, init, w, lane);
     __threadfence_block();
     const double lbd = alpha_pass<MT, KS, BROW>(G, w, fr0, frh, sbias, Q, spec_rows, spec_acc,
-                                                adam, false, lane, g, r, aa, dom);
+                                                adam, init, lane, g, r, aa, dom);
     if (g == 0 && r < Q) lb_out[dom * Q + r] = (float)lbd;
-    alpha_store(G, aa, dom, w, lane);
     __threadfence_block();
   }
 }
@@ -3039,9 +3035,12 @@ int alpha_prepare(const int32_t* dims, int n_relu, const float* frag, const floa
       return VC_OK;
     }
   }
-  const size_t wsz = (size_t)alpha_wsz(n_relu, G.KS, Q);
-  L.lds = fixed + ANW * wsz * sizeof(float);
-  if (L.lds > 160 * 1024) return VC_ERR_UNSUPPORTED;
+  const size_t wsz = (size_t)alpha_wsz(n_relu, G.KS, Q) * sizeof(float);
+  const int nw = fixed + wsz <= 160 * 1024
+                     ? (int)std::min<size_t>(ANW, (160 * 1024 - fixed) / wsz)
+                     : 0;
+  if (nw < 1) return VC_ERR_UNSUPPORTED;
+  L.lds = fixed + nw * wsz;
   switch (G.variant) {
     case 0: L.fn = alpha_fn<0>(); break;
     case 1: L.fn = alpha_fn<1>(); break;
@@ -3053,8 +3052,8 @@ int alpha_prepare(const int32_t* dims, int n_relu, const float* frag, const floa
   }
   if (!vcm::allow_max_lds(L.fn)) return VC_ERR_UNSUPPORTED;
   L.D = 1;
-  L.grid = dim3(vcm::persistent_grid(B, L.lds, ANW));
-  L.block = dim3(ANW * 64);
+  L.grid = dim3(vcm::persistent_grid(B, L.lds, nw));
+  L.block = dim3(nw * 64);
   return VC_OK;
 }
 
