@@ -112,10 +112,14 @@ def run_rounds(gg, xl, xh, spec_ew, table, timers=None, keep=None, lookahead=Non
         pre = st.get('lookahead')
         if keep is not None:
             keep.append((xl, xh, st))
-        (lxl, lxh), (hxl, hxh) = st['low'], st['high']
         # next batch = the LIFO pop of [low chunk, high chunk]: high first
-        xl = torch.cat([hxl, lxl], 0)
-        xh = torch.cat([hxh, lxh], 0)
+        # (the native round leaves them so in one block)
+        if st.get('next') is not None:
+            xl, xh = st['next']
+        else:
+            (lxl, lxh), (hxl, hxh) = st['low'], st['high']
+            xl = torch.cat([hxl, lxl], 0)
+            xh = torch.cat([hxh, lxh], 0)
         stats.append({'B': B, 'closed': B - int(st['unclosed'].numel()),
                       'alpha_leaves': st['n_alpha_leaves'],
                       'alpha_iters': st['n_alpha_iters']})

@@ -877,7 +877,11 @@ int vc_best_rows_with_A(float *best, const float *lb, float *best_A,
  * device, sized for B rows: lb (B, Q), A (B, Q, n_in), acc (B, Q), closed
  * (B), unclosed (the first counts[2] entries), feasible (per unclosed row),
  * xl_split/xh_split/ax (the first counts[3] rows), low/high children (the
- * first counts[4] rows).  counts (host int64[7]) = {open leaves, alpha
+ * first counts[4] rows).  low_xl and low_xh both null: the low children
+ * follow the high ones in high_xl / high_xh (rows counts[4] .. 2 counts[4];
+ * each then holds 2 B rows), so the next batch in a LIFO worklist's pop
+ * order (high, then low) is one contiguous block instead of a
+ * concatenation.  counts (host int64[7]) = {open leaves, alpha
  * iterations evaluated, unclosed, feasible, split, degenerate, handed-over
  * children (-1: no lookahead)}.  work:
  * vc_mlp_bab_round_workspace(dims, n_relu, B, Q) bytes of device memory;

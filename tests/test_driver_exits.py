@@ -146,3 +146,32 @@ def test_errors_after_the_bound_phase_propagate(driver):
     # untagged (bound phase): halves as before
     verdict, det, calls = driver(lambda k, B: RuntimeError('bound'), input_split_batch_size=4)
     assert verdict == 'unknown' and len(calls) == 3
+
+
+def test_worklist_pop_joins_adjacent_chunks_without_copy():
+    """The product worklist pops [high, low] chunks that lie back to back in
+    one storage (the native round's layout) as a view of that block, with
+    the values torch.cat would give; chunks elsewhere are concatenated, and
+    the LIFO order (verify_graph.py:12695-12726) holds either way."""
+    blk = torch.arange(40, dtype=torch.float32)
+    high, low = blk[:12].view(3, 4), blk[12:20].view(2, 4)
+    other = torch.arange(100, 108, dtype=torch.float32).view(2, 4)
+    wl = vg.ChunkWorklist(torch.zeros(4), torch.ones(4))
+    wl.pop(1)
+    wl.push(low, low)
+    wl.push(high, high)
+    xl, xh = wl.pop(5)
+    assert torch.equal(xl, torch.cat([high, low], 0)) and torch.equal(xh, xl)
+    assert xl.untyped_storage().data_ptr() == blk.untyped_storage().data_ptr()
+    assert not wl
+    # a partial pop takes the lower chunk's last rows, which do not follow
+    # the upper chunk: concatenated
+    wl.push(other, other)
+    wl.push(low, low)
+    wl.push(high, high)
+    xl, _ = wl.pop(4)
+    assert xl.tolist() == torch.cat([high, low[-1:]], 0).tolist()
+    assert xl.untyped_storage().data_ptr() != blk.untyped_storage().data_ptr()
+    xl, _ = wl.pop(3)
+    assert xl.tolist() == torch.cat([low[:1], other], 0).tolist()
+    assert not wl

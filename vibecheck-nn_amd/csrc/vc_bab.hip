@@ -423,13 +423,17 @@ int bound_phase(const int32_t* dims, int n, const float* frag, const float* bias
 }
 
 // Where the clip and split phases write: the unclosed list, the feasible
-// flags, the feasible rows and the children.
+// flags, the feasible rows and the children (low_xl / low_xh null: right
+// after the nu high children, in high_xl / high_xh).
 struct TailOut {
   int64_t* unclosed;
   uint8_t* feasible;
   float *xl_split, *xh_split;
   int64_t* ax;
   float *low_xl, *low_xh, *high_xl, *high_xh;
+  float* low_at(float* low, float* high, int64_t nu, int n_in) const {
+    return low ? low : high + nu * (int64_t)n_in;
+  }
 };
 
 // The clip and split phases on the leaves `closed` leaves open: the
@@ -488,8 +492,9 @@ int tail_phases(const int32_t* dims, int Q, const int32_t* d_ptr, const int32_t*
   VC_TRY(mark(phase_ev, 3, st));
   phase = PH_SPLIT;
   if (nu > 0)
-    VC_TRY(vc_bisect(t.c_xl, t.c_xh, t.ax_u, t.idx2, nu, n_in, o.low_xl, o.low_xh, o.high_xl,
-                     o.high_xh, stream));
+    VC_TRY(vc_bisect(t.c_xl, t.c_xh, t.ax_u, t.idx2, nu, n_in,
+                     o.low_at(o.low_xl, o.high_xl, nu, n_in),
+                     o.low_at(o.low_xh, o.high_xh, nu, n_in), o.high_xl, o.high_xh, stream));
   VC_TRY(mark(phase_ev, 4, st));
   return VC_OK;
 }
@@ -534,8 +539,10 @@ int bab_round(const int32_t* dims, int n_relu, const float* frag, const float* b
   phase = PH_BOUND;
   if (!dims || !frag || !bias_cat || !spec_rows || !spec_acc || !d_ptr || !q_idx || !xl ||
       !xh || !lb || !A || !acc || !closed || !unclosed || !feasible || !xl_split ||
-      !xh_split || !ax || !low_xl || !low_xh || !high_xl || !high_xh || !work || !counts)
+      !xh_split || !ax || !high_xl || !high_xh || !work || !counts)
     return VC_ERR_ARG;
+  // the low children in their own arrays, or both after the high ones
+  if ((low_xl == nullptr) != (low_xh == nullptr)) return VC_ERR_ARG;
   if (n_relu < 1 || n_relu > MAXL || B < 0 || Q < 1 || n_disj < 0 || la_cap < 0)
     return VC_ERR_ARG;
   if (la_work && !aux_stream) return VC_ERR_ARG;
@@ -737,13 +744,18 @@ int bab_round(const int32_t* dims, int n_relu, const float* frag, const float* b
         VC_TRY(gather(fin, fout, fcols, 3, L.fidx, nf, stream));
       }
       if (nu > 0) {
-        // high children are the kept ones of the first half, low ones of the second
+        // high children are the kept ones of the first half, low ones of the
+        // second (both in one gather when the low ones follow the high ones)
         const float* cin[2] = {L.cxl, L.cxh};
         float* hout[2] = {high_xl, high_xh};
-        float* lout[2] = {low_xl, low_xh};
         const int32_t ccols[2] = {n_in, n_in};
-        VC_TRY(gather(cin, hout, ccols, 2, L.kidx, nu, stream));
-        VC_TRY(gather(cin, lout, ccols, 2, L.kidx + nu, nu, stream));
+        if (low_xl) {
+          float* lout[2] = {low_xl, low_xh};
+          VC_TRY(gather(cin, hout, ccols, 2, L.kidx, nu, stream));
+          VC_TRY(gather(cin, lout, ccols, 2, L.kidx + nu, nu, stream));
+        } else {
+          VC_TRY(gather(cin, hout, ccols, 2, L.kidx, n_keep, stream));
+        }
         // the next round's bound phase
         Carve hc{reinterpret_cast<char*>(la_work), 0};
         Handoff h;

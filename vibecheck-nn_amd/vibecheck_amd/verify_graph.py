@@ -241,6 +241,26 @@ def _widest_and_bisect(xl, xh):
     return B - nu, ax, (low_xl, low_xh), (high_xl, high_xh)
 
 
+def _join_rows(parts):
+    """torch.cat of 2-D row chunks, or a view when they lie back to back in
+    one storage (the native round leaves a round's high and low children so,
+    in the order they are popped)."""
+    a = parts[0]
+    if all(t.is_contiguous() for t in parts) and all(
+            t.dtype == a.dtype and t.shape[1:] == a.shape[1:] for t in parts):
+        base = a.untyped_storage().data_ptr()
+        end = a.storage_offset() + a.numel()
+        for t in parts[1:]:
+            if t.untyped_storage().data_ptr() != base or t.storage_offset() != end:
+                break
+            end += t.numel()
+        else:
+            rows = sum(int(t.shape[0]) for t in parts)
+            return torch.as_strided(a, (rows,) + tuple(a.shape[1:]), a.stride(),
+                                    a.storage_offset())
+    return torch.cat(parts, 0)
+
+
 class ChunkWorklist:
     """LIFO worklist of device-resident 2-D chunks
     (verify_graph.py:12695-12726)."""
@@ -277,7 +297,7 @@ class ChunkWorklist:
                 got = n
         if len(pl) == 1:
             return pl[0].contiguous(), ph[0].contiguous()
-        return torch.cat(pl, 0), torch.cat(ph, 0)
+        return _join_rows(pl), _join_rows(ph)
 
     def __bool__(self):
         return bool(self.xl)
@@ -427,8 +447,10 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
     # Between two rounds the GPU waits on this host code (each round ends
     # with the children's count read back), so the outputs are one
     # allocation addressed by offsets, and their views are made after the
-    # call: floats (lb, acc, A, 6 box arrays), then int64 indices [2, Bm],
-    # then flags [2, Bm], each 256-byte aligned.
+    # call: floats (lb, acc, A, the feasible rows' xl and xh, the children's
+    # xl and xh with 2 Bm rows each: high then low, so that the next batch
+    # in pop order is one block), then int64 indices [2, Bm], then flags
+    # [2, Bm], each 256-byte aligned.
     Bm = max(B, 1)
     nflt = Bm * (2 * Q + Q * n_in + 6 * n_in)
     o_idx = (4 * nflt + 255) & ~255
@@ -476,7 +498,7 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
              ptr(table.q_idx), table.n, B, ptr(xl), ptr(xh), int(alpha_iters),
              float(alpha_lr), float(alpha_lr_decay), 1e-6, p, p + 8 * Bm * Q, p + 4 * Bm * Q,
              p + o_flg, p + o_idx, p + o_flg + Bm, p_box, p_box + nb, p + o_idx + 8 * Bm,
-             p_box + 2 * nb, p_box + 3 * nb, p_box + 4 * nb, p_box + 5 * nb, ptr(seeds),
+             None, None, p_box + 2 * nb, p_box + 4 * nb, ptr(seeds),
              ev[0].cuda_event if ev else None, ev[1].cuda_event if ev else None, pev_p,
              ptr(widths), ws.data_ptr(), nws,
              pre['buf'].data_ptr() if pre is not None else None,
@@ -517,8 +539,12 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
            'feasible': ast(bl, (n_unc,), (1,), o_flg + Bm) if n_unc > 0 else None,
            'xl_split': ast(fl, (nf, n_in), r, bo), 'xh_split': ast(fl, (nf, n_in), r, bo + nb),
            'ax': ast(i64, (nf,), (1,), oi + Bm), 'n_degenerate': n_deg,
-           'low': (ast(fl, (nu, n_in), r, bo + 2 * nb), ast(fl, (nu, n_in), r, bo + 3 * nb)),
-           'high': (ast(fl, (nu, n_in), r, bo + 4 * nb), ast(fl, (nu, n_in), r, bo + 5 * nb))}
+           'low': (ast(fl, (nu, n_in), r, bo + 2 * nb + nu * n_in),
+                   ast(fl, (nu, n_in), r, bo + 4 * nb + nu * n_in)),
+           'high': (ast(fl, (nu, n_in), r, bo + 2 * nb), ast(fl, (nu, n_in), r, bo + 4 * nb)),
+           # the next batch in pop order (high, then low), without a copy
+           'next': (ast(fl, (2 * nu, n_in), r, bo + 2 * nb),
+                    ast(fl, (2 * nu, n_in), r, bo + 4 * nb))}
     out['chunks'] = [out['low'], out['high']] if nu > 0 else []
     out['lookahead'] = ({'buf': la, 'n': n_next, 'plan': plan, 'spec': spec_ew}
                         if la is not None and n_next >= 0 else None)
