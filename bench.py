@@ -87,17 +87,26 @@ def vz_sb(gg, xl, xh, dev):
     return vz._zono_sb(gg, xl, xh, dev, torch.float32)
 
 
-LOOKAHEAD = False  # --lookahead: each round but the last bounds the next batch while alpha runs
+# --lookahead: how each round but the last hands the next batch's bound
+# phase over (None: the driver's own setting, verify_graph.LOOKAHEAD)
+LOOKAHEAD = None
+
+
+def _lookahead_mode():
+    from vibecheck_amd import verify_graph as vg
+    m = LOOKAHEAD if LOOKAHEAD is not None else vg.LOOKAHEAD
+    return {True: 'overlap', False: 'off'}.get(m, m)
 
 
 def run_rounds(gg, xl, xh, spec_ew, table, timers=None, keep=None, lookahead=None):
     """Three BaB rounds; returns per-round stats.  ``keep`` (a list): each
-    round's batch and step outputs are appended to it.  With ``lookahead``
-    each round but the last bounds the next one's batch while its alpha
-    runs (the same results)."""
+    round's batch and step outputs are appended to it.  ``lookahead``
+    (default: the driver's setting): 'tail' -- each round but the last also
+    bounds the next batch after its split; 'overlap' -- while its alpha
+    runs; False -- off (the same results every way)."""
     from vibecheck_amd import verify_graph as vg
     if lookahead is None:
-        lookahead = LOOKAHEAD
+        lookahead = LOOKAHEAD if LOOKAHEAD is not None else vg.LOOKAHEAD
     stats = []
     pre = None
     for r in range(N_ROUNDS):
@@ -108,7 +117,7 @@ def run_rounds(gg, xl, xh, spec_ew, table, timers=None, keep=None, lookahead=Non
         st = vg.bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
                          clip_enabled=True, alpha_iters=ALPHA_ITERS, alpha_all=True,
                          alpha_lr=ALPHA_LR, timers=timers,
-                         lookahead=lookahead and r + 1 < N_ROUNDS, pre=pre)
+                         lookahead=lookahead if r + 1 < N_ROUNDS else False, pre=pre)
         pre = st.get('lookahead')
         if keep is not None:
             keep.append((xl, xh, st))
@@ -1012,10 +1021,11 @@ def main():
                     help='c1 (default): the headline 65,536-box ACAS step; the others print '
                          'their own line')
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--lookahead', action='store_true',
-                    help='each round but the last clips, splits and bounds the next batch on '
-                         'the main stream while its alpha runs on a second one (the same '
-                         'results)')
+    ap.add_argument('--lookahead', choices=['off', 'tail', 'overlap'], default=None,
+                    help="how each round but the last bounds the next batch (the same "
+                         "results): 'tail' after its split, on the same stream (the "
+                         "driver's default); 'overlap' on the main stream while its alpha "
+                         "runs on a second one; 'off' each round bounds its own batch")
     ap.add_argument('--no-secondary', action='store_true',
                     help='after the timed steps, skip the extra pass over the rounds '
                          '(near-zero counts, secondary rooflines, alpha rates): a profile '
@@ -1033,7 +1043,7 @@ def main():
                     help='only time the hybrid replay on ACAS-Xu-shaped leaves (one JSON line)')
     args = ap.parse_args()
     global LOOKAHEAD
-    LOOKAHEAD = args.lookahead
+    LOOKAHEAD = {None: None, 'off': False}.get(args.lookahead, args.lookahead)
     if args.gpus != 1:
         print(f'bench.py measures one GPU only (this build has no multi-GPU path); '
               f'got --gpus {args.gpus}', file=sys.stderr)
@@ -1180,7 +1190,7 @@ def main():
         'config': {'workload': '5-50x6-5 ReLU MLP, 65,536 input boxes, 3 BaB rounds, '
                                'CROWN intermediate + alpha-CROWN 20 it lr 0.1 + clip + '
                                'widest split', 'domains_per_step': domains,
-                   'lookahead': LOOKAHEAD},
+                   'lookahead': _lookahead_mode()},
         'alpha_iters_per_s': alpha_rates['open']['iters_per_s'] if alpha_rates else None,
         'alpha': ({'step_open_leaves': alpha_rates['open'], 'all_65536': alpha_rates['all']}
                   if alpha_rates else None),

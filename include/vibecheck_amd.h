@@ -927,7 +927,15 @@ int vc_best_rows_with_A(float *best, const float *lb, float *best_A,
  * previous round's call, whose counts[6] is this call's B, with xl/xh that
  * round's high then low children: the round takes its bound phase from there
  * (crown_ev0/crown_ev1 and seed_rows are then not used).  la_work must stay
- * untouched until the next round's call has returned. */
+ * untouched until the next round's call has returned.
+ *
+ * Tail bound (la_work non-null, aux_stream null, low_xl and low_xh null):
+ * no overlap; after the split, `stream` runs the bound phase on the
+ * 2 counts[4] children (high then low, the next batch as it is) and leaves
+ * it in la_work for the next call's `pre` (counts[6] = 2 counts[4]; -1
+ * above la_cap, or with phase_ev or clip_widths).  The GPU then works while
+ * the host returns from this call and makes the next one.  la_bytes as for
+ * the lookahead. */
 int64_t vc_mlp_bab_round_workspace(const int32_t *dims, int n_relu, int64_t B,
                                    int Q);
 int64_t vc_mlp_bab_round_lookahead_workspace(const int32_t *dims, int n_relu,

@@ -47,21 +47,23 @@ def test_acasxu_prop1_verified(gpu):
 
 def test_acasxu_prop1_lookahead_same_run(gpu, monkeypatch):
     """prop_1 with alpha-CROWN on every open leaf: the driver with the
-    native round's lookahead (each round bounds the next batch while its
-    alpha runs, whenever the next pop takes exactly its children) ends with
-    the same verdict, leaf and iteration counts as without it."""
+    native round's lookahead in either mode (each round bounds the next
+    batch after its split, or while its alpha runs, whenever the next pop
+    takes exactly its children) ends with the same verdict, leaf and
+    iteration counts as without it."""
     gg = onnx_net.load_onnx(NET, device=gpu, dtype=F32)
     spec = vnnlib.load_vnnlib(os.path.join(GOLD, 'prop_1.vnnlib'))
     settings = dict(SETTINGS, input_split_batched_alpha_iters=10,
                     input_split_batched_alpha_all_leaves=True,
                     input_split_batched_alpha_lr=0.1)
     runs = {}
-    for la in (False, True):
+    for la in (False, 'tail', 'overlap'):
         monkeypatch.setattr(vg, 'LOOKAHEAD', la)
         runs[la] = vg._input_split_batched(None, spec, settings, gg, gpu, F32)
-    print(f'prop_1 with alpha: {runs[False]} / lookahead {runs[True]}')
+    print(f'prop_1 with alpha: {runs[False]} / tail {runs["tail"]} / overlap {runs["overlap"]}')
     assert runs[False][0] == 'verified'
-    assert runs[True] == runs[False]
+    assert runs['tail'] == runs[False]
+    assert runs['overlap'] == runs[False]
 
 
 def test_acasxu_prop2_never_verified_and_witness_forward(gpu):

@@ -1092,7 +1092,7 @@ def _rounds(gg, xl, xh, se, table, n_rounds, alpha_iters, lookahead):
             break
         st = vg.bab_step(xl, xh, gg, se, table, crown_intermediate=True, clip_enabled=True,
                          alpha_iters=alpha_iters, alpha_all=True, alpha_lr=0.1,
-                         lookahead=lookahead and r + 1 < n_rounds, pre=pre)
+                         lookahead=lookahead if r + 1 < n_rounds else False, pre=pre)
         pre = st.get('lookahead')
         out.append((st, pre))
         (lxl, lxh), (hxl, hxh) = st['low'], st['high']
@@ -1100,15 +1100,17 @@ def _rounds(gg, xl, xh, se, table, n_rounds, alpha_iters, lookahead):
     return out
 
 
+@pytest.mark.parametrize('mode', ['overlap', 'tail'])
 @pytest.mark.parametrize('case', ['acas65536', 'acas4096', 'net64', 'net44', 'cap'])
-def test_bab_rounds_lookahead_bit_identical(gpu, case):
-    """Rounds whose alpha runs on a second stream while the round bounds
-    all children of its CROWN-open leaves (the lookahead), each next round
-    taking that bound phase (pre) with the children of the leaves alpha
-    closed dropped, against the same rounds in order: every output of every
-    round equal bit for bit, every count equal.  The benchmark's 65,536
-    boxes have leaves that alpha closes; with a capacity below the children
-    count ('cap') the lookahead is skipped and the rounds run in order."""
+def test_bab_rounds_lookahead_bit_identical(gpu, case, mode):
+    """Rounds that hand the next batch's bound phase over (pre) against the
+    same rounds in order: every output of every round equal bit for bit,
+    every count equal.  'overlap': alpha runs on a second stream while the
+    round bounds all children of its CROWN-open leaves, the children of
+    the leaves alpha closed dropped afterwards (the benchmark's 65,536
+    boxes have leaves that alpha closes); 'tail': the round bounds its
+    children after the split.  With a capacity below the children count
+    ('cap') the lookahead is skipped and the rounds run in order."""
     old = vg.LOOKAHEAD_MAX_CHILDREN
     try:
         if case == 'acas65536':
@@ -1128,7 +1130,7 @@ def test_bab_rounds_lookahead_bit_identical(gpu, case):
         _, se, dq = spec_pair(n_out, gpu)
         table = vg.DisjunctTable(dq, gpu)
         seq = _rounds(gg, xl, xh, se, table, 3, alpha_iters, False)
-        la = _rounds(gg, xl, xh, se, table, 3, alpha_iters, True)
+        la = _rounds(gg, xl, xh, se, table, 3, alpha_iters, mode)
     finally:
         vg.LOOKAHEAD_MAX_CHILDREN = old
     assert len(seq) == len(la)
@@ -1136,7 +1138,8 @@ def test_bab_rounds_lookahead_bit_identical(gpu, case):
     for r, ((a, pa), (b, pb)) in enumerate(zip(la, seq)):
         assert pb is None
         nu = a['low'][0].shape[0]
-        if r + 1 < len(la) and a['n_alpha_leaves'] > 0 and case != 'cap':
+        if (r + 1 < len(la) and (a['n_alpha_leaves'] > 0 or mode == 'tail') and nu > 0
+                and case != 'cap'):
             assert pa is not None and pa['n'] == 2 * nu, (r, pa and pa['n'], nu)
         if case == 'cap':
             assert pa is None or 2 * nu <= 8
@@ -1150,7 +1153,7 @@ def test_bab_rounds_lookahead_bit_identical(gpu, case):
             assert torch.equal(a['feasible'], b['feasible'])
         for x, y in zip(a['low'] + a['high'], b['low'] + b['high']):
             assert torch.equal(x, y), r
-    print(f'{case}: {len(la)} rounds, {closed_by_alpha} leaves closed by alpha')
+    print(f'{case} {mode}: {len(la)} rounds, {closed_by_alpha} leaves closed by alpha')
     if case == 'acas65536':
         assert closed_by_alpha > 0
 

@@ -545,7 +545,11 @@ int bab_round(const int32_t* dims, int n_relu, const float* frag, const float* b
   if ((low_xl == nullptr) != (low_xh == nullptr)) return VC_ERR_ARG;
   if (n_relu < 1 || n_relu > MAXL || B < 0 || Q < 1 || n_disj < 0 || la_cap < 0)
     return VC_ERR_ARG;
-  if (la_work && !aux_stream) return VC_ERR_ARG;
+  // la_work with aux_stream: the overlapped lookahead; without: the next
+  // round's bound phase after the split, on `stream` (the low children
+  // must follow the high ones, so that they are the next batch as it is)
+  const bool tail = la_work && !aux_stream;
+  if (tail && low_xl) return VC_ERR_ARG;
   const int64_t need = vc_mlp_bab_round_workspace(dims, n_relu, B, Q);
   if (need < 0) return (int)-need;
   if (work_bytes < need) return VC_ERR_OOM;
@@ -617,7 +621,7 @@ int bab_round(const int32_t* dims, int n_relu, const float* frag, const float* b
   // restricted to the leaves alpha leaves open (each leaf's clip and split
   // are its own, and every compaction keeps the order), and the next
   // round's bound phase is the children's restricted to theirs.
-  const bool look = la_work && n_open > 0 && !phase_ev && !clip_widths;
+  const bool look = la_work && !tail && n_open > 0 && !phase_ev && !clip_widths;
   hipStream_t ast = look ? (hipStream_t)aux_stream : st;
   EventPair ev;
   LookBufs L;
@@ -798,6 +802,29 @@ int bab_round(const int32_t* dims, int n_relu, const float* frag, const float* b
   counts[3] = nf;
   counts[4] = nu;
   counts[5] = nf - nu;
+  // ---- the next round's bound phase on the children (high then low, one
+  // block), its outputs where the next call's `pre` takes them: the GPU
+  // runs it while the host returns from this call and makes the next one
+  if (tail && nu > 0 && 2 * nu <= la_cap && !phase_ev && !clip_widths) {
+    const int64_t bn = 2 * nu;
+    Carve hc{reinterpret_cast<char*>(la_work), 0};
+    Handoff h;
+    carve_handoff(hc, h, dims, n, bn, Q);
+    Carve cc{nullptr, 0};
+    Handoff hcap;
+    carve_handoff(cc, hcap, dims, n, la_cap, Q);
+    Carve bc{reinterpret_cast<char*>(la_work), cc.used};
+    BoundBufs bb;
+    carve_bound(bc, bb, dims, n, bn);
+    if ((int64_t)bc.used > la_bytes) return VC_ERR_OOM;
+    for (int l = 0; l < n; ++l) {
+      bb.sb_lo[l] = h.sb_lo[l];
+      bb.sb_hi[l] = h.sb_hi[l];
+    }
+    VC_TRY(bound_phase(dims, n, frag, bias_cat, bn, high_xl, high_xh, bb, Q, spec_rows,
+                       spec_acc, h.lb, h.A, h.acc, nullptr, nullptr, nullptr, st));
+    counts[6] = bn;
+  }
   return VC_OK;
 }
 

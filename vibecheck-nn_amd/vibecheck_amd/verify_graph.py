@@ -307,12 +307,15 @@ class ChunkWorklist:
 # applies; switching this off runs the same entry points from Python.
 NATIVE_ROUND = True
 
-# Whether the driver asks the native round to bound the next batch while
-# alpha runs (bab_step's ``lookahead``).  Off: on the ACAS-Xu rounds alpha
-# and the children's bound phase compete for the same compute units (each
-# workgroup of either holds the net's weights in LDS), and the overlap
-# measured no faster than the rounds in order.
-LOOKAHEAD = False
+# How the driver's native rounds hand the next batch's bound phase over
+# (bab_step's ``lookahead``): 'tail' runs it at the end of each round's call
+# on the same stream, so the GPU has work while the host returns from one
+# call and makes the next; 'overlap' runs it while alpha runs on a second
+# stream (on the ACAS-Xu rounds measured no faster than the rounds in
+# order: alpha and the children's bound phase compete for the same compute
+# units, each workgroup of either holding the net's weights in LDS); False:
+# each round bounds its own batch.
+LOOKAHEAD = 'tail'
 # The most children a lookahead bounds (beyond that the round runs in order).
 LOOKAHEAD_MAX_CHILDREN = 16384
 
@@ -419,16 +422,17 @@ def _tag_phase(e, phase):
 
 
 def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_lr_decay,
-                      phase_timer=None, lookahead=False, pre=None):
+                      phase_timer=None, lookahead=False, pre=None, la_max=None):
     """bab_step's round (crown intermediate bounds, clip, alpha-CROWN on
     every open leaf) as one call of the native round orchestration, for
     nets with the shape-specialised kernels; None where it does not apply.
     Same entry points in the same order as the Python round, so the same
-    results.  ``lookahead``: while alpha runs on a second stream, clip and
-    split the leaves the CROWN bound leaves open and run the bound phase on
-    all their children; the result's 'lookahead' then holds the bound
-    phase of the round's children (high then low) for the next round's
-    ``pre``."""
+    results.  ``lookahead`` 'overlap' (or True): while alpha runs on a
+    second stream, clip and split the leaves the CROWN bound leaves open and
+    run the bound phase on all their children; 'tail': run the bound phase
+    on the children after the split.  Either way the result's 'lookahead'
+    then holds the bound phase of the round's children (high then low) for
+    the next round's ``pre``, when there are at most ``la_max`` of them."""
     from . import mlp_fused
     from . import verify_zono_bnb as vz
     dev = xl.device
@@ -466,13 +470,16 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
     if pre is not None and (pre.get('n') != B or pre.get('plan') is not plan
                             or pre.get('spec') is not spec_ew):
         pre = None
-    la = None
+    la = aux = None
     la_bytes = la_cap = 0
-    if lookahead and alpha_iters > 0 and phase_timer is None and B > 0:
-        la_cap = min(2 * B, LOOKAHEAD_MAX_CHILDREN)
+    mode = 'overlap' if lookahead is True else lookahead
+    if (mode in ('overlap', 'tail') and phase_timer is None and B > 0
+            and (mode == 'tail' or alpha_iters > 0)):
+        la_cap = min(2 * B, LOOKAHEAD_MAX_CHILDREN if la_max is None else int(la_max))
         la_bytes = int(lib.vc_mlp_bab_round_lookahead_workspace(plan.dims_p, plan.n, B, Q,
                                                                  la_cap))
         la = torch.empty(max(la_bytes, 8), dtype=torch.uint8, device=dev)
+        aux = _aux_stream(dev) if mode == 'overlap' else None
     # work accounting and timing of the CROWN launch, as mlp_fused.crown does
     # (a handed-over bound phase ran inside the previous round's call)
     seeds = seed_row = ev = zev = None
@@ -503,7 +510,7 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
              ptr(widths), ws.data_ptr(), nws,
              pre['buf'].data_ptr() if pre is not None else None,
              la.data_ptr() if la is not None else None, la_bytes, la_cap,
-             _aux_stream(dev) if la is not None else None, mlp_fused._stop_word().data_ptr(),
+             aux, mlp_fused._stop_word().data_ptr(),
              mlp_fused._pinned_words().data_ptr(), ctypes.addressof(counts),
              ctypes.addressof(fail), stream())
     except RuntimeError as e:
@@ -574,7 +581,8 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
              clip_enabled=True, alpha_iters=0, alpha_all=False, alpha_eps=0.0,
              alpha_max_leaves=200, alpha_lr=0.25, alpha_lr_decay=0.98,
              timers=None, branch_sb=False, sb_margin=False, sb_thr=0.01, sb_mw=1.0,
-             split_depth=1, clip_iters=1, phase_timer=None, lookahead=False, pre=None):
+             split_depth=1, clip_iters=1, phase_timer=None, lookahead=False, pre=None,
+             la_max=None):
     """One BaB iteration on a popped batch (verify_graph.py:12855-13423):
     bound, closure, optional alpha-CROWN on unclosed leaves (opportunistic:
     a RuntimeError or OOM inside it keeps the bound it had, as at
@@ -588,18 +596,21 @@ def bab_step(xl, xh, gg, spec_ew, table, crown_intermediate=True,
     records the round's phase events.  An error after the bound phase
     carries ``vc_phase`` ('clip' or 'split').
 
-    ``lookahead`` (extension, native round only): while alpha runs, the
-    round also bounds every child of the leaves the CROWN bound leaves
-    open; the result's 'lookahead' (None when it did not run) is the bound
-    phase of the round's children in the order cat(high, low), which the
-    next call takes as ``pre`` when its batch is exactly that.  Each box's
-    bounds depend on that box alone, so the results are the same as
+    ``lookahead`` (extension, native round only): 'tail' -- after the
+    split, the round also runs the bound phase of its children; 'overlap'
+    (or True) -- while alpha runs, the round bounds every child of the
+    leaves the CROWN bound leaves open.  The result's 'lookahead' (None
+    when it did not run, or with more than ``la_max`` children) is the
+    bound phase of the round's children in the order cat(high, low), which
+    the next call takes as ``pre`` when its batch is exactly that.  Each
+    box's bounds depend on that box alone, so the results are the same as
     without it."""
     _widths(gg, xl.shape[1])
     if (NATIVE_ROUND and timers is None and crown_intermediate and clip_enabled
             and (alpha_iters == 0 or alpha_all) and not branch_sb and clip_iters == 1):
         out = _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr,
-                                alpha_lr_decay, phase_timer, lookahead=lookahead, pre=pre)
+                                alpha_lr_decay, phase_timer, lookahead=lookahead, pre=pre,
+                                la_max=la_max)
         if out is not None:
             return out
     pev = pw = None
@@ -847,7 +858,8 @@ def _input_split_batched(graph, spec, settings, gg, device, dtype):
                           sb_thr=sb_thr, sb_mw=sb_mw,
                           split_depth=split_depth if B < batch_size else 1,
                           clip_iters=clip_iters, phase_timer=pt,
-                          lookahead=LOOKAHEAD and not wl, pre=use_pre)
+                          lookahead=LOOKAHEAD if not wl else False, pre=use_pre,
+                          la_max=min(batch_size, LOOKAHEAD_MAX_CHILDREN))
         except RuntimeError as e:
             # torch.cuda.OutOfMemoryError is a RuntimeError; only the bound
             # phase's errors halve the batch
