@@ -887,20 +887,30 @@ def test_relaxation_kernels_rows_and_domains(gpu, n, alpha_mode, with_beta):
                   scale=acc0.double().abs() + terms.abs().sum(-1))
 
 
-@pytest.mark.parametrize('n,R,B', [(5, 4, 3000), (13, 3, 777), (32, 1, 1000), (7, 300, 9),
-                                   (1, 1, 257)])
-def test_concretize_tiled_matches_thread_form(gpu, n, R, B):
-    """Narrow inputs: the LDS-tiled concretization (16-byte aligned A) and
-    the one-thread-per-row form (taken for an unaligned A) give the same
-    bits; both equal lb = acc + pos(A) xl + neg(A) xh within fp32 of the
-    fp64 value (verify_zono_bnb.py:5117-5134)."""
+@pytest.mark.parametrize('n,R,B,boff', [(5, 4, 3000, 0), (5, 4, 3001, 1), (13, 3, 777, 0),
+                                        (13, 3, 777, 2), (32, 1, 1000, 0), (7, 300, 9, 0),
+                                        (1, 1, 257, 0), (1, 1, 5000, 3), (20, 7, 300, 0)])
+def test_concretize_tiled_matches_thread_form(gpu, n, R, B, boff):
+    """Narrow inputs: the LDS-tiled concretization (16-byte aligned A; 2 or
+    1 rows per thread by width; float4 box loads when the box arrays are
+    16-byte aligned, boff = 0, else scalar ones) and the one-thread-per-row
+    form (taken for an unaligned A) give the same bits; both equal lb = acc
+    + pos(A) xl + neg(A) xh within fp32 of the fp64 value
+    (verify_zono_bnb.py:5117-5134).  The box arrays end where the data
+    does, so a tile's last float4 past their end must not be read."""
     M = B * R
     g = torch.Generator().manual_seed(n * 1000 + R)
     A = torch.randn(M, n, generator=g)
     acc = torch.randn(M, generator=g)
     xl = torch.rand(B, n, generator=g) * 2 - 1
     xh = xl + torch.rand(B, n, generator=g)
-    Ag, accg, xlg, xhg = (t.to(gpu).contiguous() for t in (A, acc, xl, xh))
+    Ag, accg = (t.to(gpu).contiguous() for t in (A, acc))
+    # each box array in its own allocation, ending with the data
+    xlg = torch.empty(B * n + boff, device=gpu)[boff:].view(B, n)
+    xhg = torch.empty(B * n + boff, device=gpu)[boff:].view(B, n)
+    xlg.copy_(xl)
+    xhg.copy_(xh)
+    assert (xlg.data_ptr() % 16 == 0) == (xhg.data_ptr() % 16 == 0) == (boff == 0)
     buf = torch.empty(M * n + 1, device=gpu)
     buf[1:] = Ag.reshape(-1)
     A_un = buf[1:].view(M, n)
