@@ -8,8 +8,11 @@
  *     (boxes); "R" is the number of backward rows per domain (spec queries
  *     Q, or 2k seeded rows); a backward row m belongs to domain m / R.
  *   - Every call is asynchronous on the given HIP stream (hipStream_t passed
- *     as void*) and returns a status code (VC_OK on success).  No call
- *     allocates device memory; scratch comes from caller workspaces.
+ *     as void*) and returns a status code (VC_OK on success).  Scratch comes
+ *     from caller workspaces; the only device memory the library allocates
+ *     is rocBLAS's own, when the first plain fp32 product (vc_backward_fc's
+ *     second phase) on a device and host thread creates its handle, kept
+ *     for the life of the process.
  *   - Each entry point names the reference function it replaces
  *     (src/vibecheck/<file>:<line>).
  */
@@ -179,9 +182,11 @@ int vc_rows_bias_dot(const float *ew, int64_t M, int R, int n, int shared,
  *       acc += e . bias (bias nullable),  ew_out (M, n_in) = e W,
  *   with W (n_out, n_in).  When relax_out is non-NULL the relaxed rows e
  *   are also written there (M, n_out); with a relu and n_out >= 64 the step
- *   then runs in two phases (the relaxation streams e into relax_out, and a
- *   plain MFMA GEMM reads it back), which is faster than relaxing inside
- *   the GEMM's loads, so callers that can spare the buffer should pass it.
+ *   then runs in two phases (the relaxation streams e into relax_out, and
+ *   rocBLAS's fp32 sgemm reads it back), which is faster than relaxing
+ *   inside the GEMM's loads, so callers that can spare the buffer should
+ *   pass it.  Without a relu, bias, relax_out or shared rows the product
+ *   is that sgemm alone.
  *   With ew_bcast != 0, ew_in is (R, n_out) and shared by every domain
  *   (row m reads row m % R).
  * Replaces the fc and relu branches of _spec_backward_graph_batched

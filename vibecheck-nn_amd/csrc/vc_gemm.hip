@@ -1,12 +1,55 @@
 // fp32 MFMA GEMMs of the fc layers: the interval forward, the zonotope
 // forward, the CROWN backward step (fused, or two-phase through relax_out),
-// and the alpha gradient sweep.  The GEMM core is vc_gemm_core.h.
+// and the alpha gradient sweep.  The GEMM core is vc_gemm_core.h; the
+// plain products (no arithmetic in the operand loads, no epilogue) run
+// rocBLAS's sgemm.
+#include <rocblas/rocblas.h>
+
 #include "vc_gemm_core.h"
 #include "vc_relax.h"
 
 namespace {
 
 using namespace vcg;
+
+// rocBLAS handles, one per device and host thread (the stream is handle
+// state, so threads on their own streams never share one), created on
+// first use and kept for the life of the process.
+constexpr int kMaxDevices = 64;
+thread_local rocblas_handle t_blas[kMaxDevices] = {};
+
+int blas_handle(rocblas_handle& out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return VC_ERR_LAUNCH;
+  if (!t_blas[dev]) {
+    rocblas_handle h = nullptr;
+    if (rocblas_create_handle(&h) != rocblas_status_success) return VC_ERR_LAUNCH;
+    t_blas[dev] = h;
+  }
+  out = t_blas[dev];
+  return VC_OK;
+}
+
+// C (M x N) = A (M x K) B (K x N), row-major fp32, on `st`: rocBLAS's
+// column-major sgemm computes C^T = B^T A^T from the same memory.  M is
+// taken in slices whose element counts stay within its 32-bit sizes.
+int plain_gemm(const float* A, int64_t M, int K, const float* B, int N, float* C,
+               hipStream_t st) {
+  if (M == 0) return VC_OK;
+  rocblas_handle h = nullptr;
+  const int rc = blas_handle(h);
+  if (rc != VC_OK) return rc;
+  if (rocblas_set_stream(h, st) != rocblas_status_success) return VC_ERR_LAUNCH;
+  const float one = 1.f, zero = 0.f;
+  const int64_t step = std::max<int64_t>(1, ((int64_t)1 << 30) / std::max(K, N));
+  for (int64_t m0 = 0; m0 < M; m0 += step) {
+    const int mm = (int)std::min<int64_t>(step, M - m0);
+    if (rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_none, N, mm, K, &one, B, N,
+                      A + m0 * K, K, &zero, C + m0 * N, N) != rocblas_status_success)
+      return VC_ERR_LAUNCH;
+  }
+  return VC_OK;
+}
 
 // vc_backward_fc runs its two-phase form (relaxed rows through relax_out)
 // from this row width up; narrower rows keep the fused prologue.
@@ -542,9 +585,7 @@ int backward_fc(const float* ew_in, int64_t M, int R, int n_out, const float* re
                            ew_in, M, R, n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group, n_groups,
                            beta, bias, ew_bcast, relax_out, acc);
       VC_LAUNCH_CHECK();
-      return launch_gemm<1, false>(1, M, n_in, n_out, LoadRow{relax_out, n_out}, LoadW{W, n_in},
-                                   EpStoreBias{nullptr, ew_out, n_in}, nullptr,
-                                   vec_ok({relax_out, W}, {n_out, n_in}), st);
+      return plain_gemm(relax_out, M, n_out, W, n_in, ew_out, st);
     }
     const int64_t grid = (M + RR - 1) / RR < kMaxGrid ? (M + RR - 1) / RR : kMaxGrid;
     if (v1)
@@ -556,14 +597,10 @@ int backward_fc(const float* ew_in, int64_t M, int R, int n_out, const float* re
                          n_out, relu_lo, relu_hi, alpha, alpha_per_row, alpha_group, n_groups, beta, bias,
                          ew_bcast, relax_out, acc);
     VC_LAUNCH_CHECK();
-    return launch_gemm<1, false>(1, M, n_in, n_out, LoadRow{relax_out, n_out}, LoadW{W, n_in},
-                                 EpStoreBias{nullptr, ew_out, n_in}, nullptr,
-                                 vec_ok({relax_out, W}, {n_out, n_in}), st);
+    return plain_gemm(relax_out, M, n_out, W, n_in, ew_out, st);
   }
   if (!relu_lo && !bias && !relax_out && !ew_bcast)
-    return launch_gemm<1, false>(1, M, n_in, n_out, LoadRow{ew_in, n_out}, LoadW{W, n_in},
-                                 EpStoreBias{nullptr, ew_out, n_in}, nullptr,
-                                 vec_ok({ew_in, W}, {n_out, n_in}), st);
+    return plain_gemm(ew_in, M, n_out, W, n_in, ew_out, st);
   LoadRelaxRow la{ew_in, n_out, R, relu_lo, relu_hi, alpha, beta, bias, alpha_per_row, relax_out,
                   ew_bcast, alpha_group, n_groups};
   const bool vec = vec_ok({ew_in, relu_lo, relu_hi, alpha, beta, W}, {n_out, n_in});
