@@ -780,6 +780,10 @@ LAYERWISE_MFMA = {
     'vc_alpha_grad_step': lambda a: 2.0 * a[2] * a[4] * a[11],
     # mid W^T and rad |W|^T: 4 B n_in n_out
     'vc_ibp_fc': lambda a: 4.0 * a[2] * a[3] * a[6],
+    # centre and K generator columns through W: 2 B n_out n_in (K + 1)
+    'vc_zono_fc': lambda a: 2.0 * a[2] * a[3] * a[7] * (a[4] + 1),
+    # the same through a conv: 2 B (Kg + 1)(C_out H_out W_out)(C_in kh kw)
+    'vc_zono_conv': lambda a: 2.0 * a[2] * (a[3] + 1) * a[9] * a[16] * a[17] * a[4] * a[10] * a[11],
     # 4 B (C_out H_out W_out)(C_in kh kw)
     'vc_ibp_conv': lambda a: 4.0 * a[2] * a[8] * a[15] * a[16] * a[3] * a[9] * a[10],
 }
@@ -1002,8 +1006,9 @@ def run_config(cfg, steps, warmup, cpu):
     else:
         rows = layerwise_roofline(step, steps)
         top = rows[0]
-        how = ('relaxation pass + rocBLAS sgemm' if top['entry'] == 'vc_backward_fc'
-               else 'MFMA GEMM core')
+        how = {'vc_backward_fc': 'relaxation pass + rocBLAS sgemm',
+               'vc_zono_fc': 'rocBLAS strided-batched sgemm for the generators'}.get(
+                   top['entry'], 'MFMA GEMM core')
         line['roofline'] = {'kernel': f'{top["entry"]} ({how})', 'bound': 'mfma',
                             'achieved': top['achieved'], 'peak': FP32_MFMA_PEAK,
                             'unit': 'TFLOP/s', 'frac': top['frac'], 'traffic': None,

@@ -11,8 +11,8 @@
  *     as void*) and returns a status code (VC_OK on success).  Scratch comes
  *     from caller workspaces; the only device memory the library allocates
  *     is rocBLAS's own, when the first plain fp32 product (vc_backward_fc's
- *     second phase) on a device and host thread creates its handle, kept
- *     for the life of the process.
+ *     second phase, vc_zono_fc's generator product) on a device and host
+ *     thread creates its handle, kept for the life of the process.
  *   - Each entry point names the reference function it replaces
  *     (src/vibecheck/<file>:<line>).
  */
@@ -95,7 +95,8 @@ int vc_zono_input(const float *xl, const float *xh, int64_t B, int n,
                   vc_stream_t stream);
 
 /* fc layer: c_out = c W^T + bias (B, n_out); G_out[b] = W G[b]
- * (B, n_out, K).  Replaces verify_zono_bnb.py:3169-3173. */
+ * (B, n_out, K), a plain batched product (rocBLAS's strided-batched
+ * sgemm).  Replaces verify_zono_bnb.py:3169-3173. */
 int vc_zono_fc(const float *c, const float *G, int64_t B, int n_in, int K,
                const float *W, const float *bias, int n_out, float *c_out,
                float *G_out, vc_stream_t stream);

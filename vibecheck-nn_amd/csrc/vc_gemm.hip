@@ -51,6 +51,30 @@ int plain_gemm(const float* A, int64_t M, int K, const float* B, int N, float* C
   return VC_OK;
 }
 
+// C[b] (M x N) = A (M x K) B[b] (K x N) for b < nb, row-major fp32, A shared
+// (rocBLAS's strided-batched sgemm: C[b]^T = B[b]^T A^T), in slices of the
+// batch that keep its 32-bit sizes in range.
+int plain_gemm_shared_a(const float* A, int M, int K, const float* B, int64_t nb, int N,
+                        float* C, hipStream_t st) {
+  if (nb == 0) return VC_OK;
+  rocblas_handle h = nullptr;
+  const int rc = blas_handle(h);
+  if (rc != VC_OK) return rc;
+  if (rocblas_set_stream(h, st) != rocblas_status_success) return VC_ERR_LAUNCH;
+  const float one = 1.f, zero = 0.f;
+  const int64_t sb = (int64_t)K * N, sc = (int64_t)M * N;
+  const int64_t step = std::max<int64_t>(1, std::min<int64_t>(((int64_t)1 << 30) / std::max(sb, sc),
+                                                              0x7fffffff));
+  for (int64_t b0 = 0; b0 < nb; b0 += step) {
+    const int cnt = (int)std::min<int64_t>(step, nb - b0);
+    if (rocblas_sgemm_strided_batched(h, rocblas_operation_none, rocblas_operation_none, N, M, K,
+                                      &one, B + b0 * sb, N, sb, A, K, 0, &zero, C + b0 * sc, N,
+                                      sc, cnt) != rocblas_status_success)
+      return VC_ERR_LAUNCH;
+  }
+  return VC_OK;
+}
+
 // vc_backward_fc runs its two-phase form (relaxed rows through relax_out)
 // from this row width up; narrower rows keep the fused prologue.
 constexpr int kTwoPhaseMinWidth = 64;
@@ -305,29 +329,6 @@ struct LoadWtAbs {  // B[k][n] = (W[n][k], |W[n][k]|), W (n_out, ld)
     }
   }
 };
-struct LoadGen {  // B[k][n] = G[bz][k][n]
-  static constexpr bool kTrans = false;
-  const float* G;
-  int64_t stride_b;
-  int ld;
-  struct Col {
-    int64_t o;
-  };
-  struct Raw {
-    float x[4];
-  };
-  __device__ Col col(int64_t bz, int n) const { return Col{bz * stride_b + n}; }
-  template <bool VEC>
-  __device__ void fetch(const Col& c, int k, int cnt, Raw& r) const {
-    float* o = r.x;
-    ld4<VEC>(G + c.o + (int64_t)k * ld, cnt, o);
-  }
-  __device__ static void finish(const Raw& r, float (*v)[4]) {
-    const float* x = r.x;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[0][j] = x[j];
-  }
-};
 
 // ------------------------------------------------------------- epilogues
 struct EpIbp {
@@ -338,14 +339,6 @@ struct EpIbp {
     const float mc = bias ? c[0] + bias[n] : c[0];
     lo[m * ld + n] = mc - c[1];
     hi[m * ld + n] = mc + c[1];
-  }
-};
-struct EpGen {
-  float* G;
-  int64_t stride_b;
-  int ld;
-  __device__ void operator()(int64_t bz, int64_t m, int n, const float* c) const {
-    G[bz * stride_b + m * ld + n] = c[0];
   }
 };
 
@@ -482,10 +475,9 @@ extern "C" int vc_zono_fc(const float* c, const float* G, int64_t B, int n_in, i
                                  vec_ok({c, W}, {n_in}), st);
   if (rc != VC_OK || K == 0 || B == 0) return rc;
   if (!G || !G_out) return VC_ERR_ARG;
-  return launch_gemm<1, false>(B, n_out, K, n_in, LoadRow{W, n_in},
-                               LoadGen{G, (int64_t)n_in * K, K},
-                               EpGen{G_out, (int64_t)n_out * K, K}, nullptr,
-                               vec_ok({W, G}, {n_in, K}), st);
+  // G_out[b] (n_out x K) = W (n_out x n_in) G[b] (n_in x K): a plain
+  // batched product with W shared
+  return plain_gemm_shared_a(W, n_out, n_in, G, B, K, G_out, st);
 }
 
 // Phase 1 for narrow rows (n <= 64): one 16-lane row of the wavefront per
