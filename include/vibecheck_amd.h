@@ -946,6 +946,15 @@ int64_t vc_mlp_bab_round_workspace(const int32_t *dims, int n_relu, int64_t B,
                                    int Q);
 int64_t vc_mlp_bab_round_lookahead_workspace(const int32_t *dims, int n_relu,
                                              int64_t B, int Q, int64_t la_cap);
+
+/* Byte offsets (off[0..2]) in la_work of the handed-over spec bound (B, Q),
+ * A (B, Q, n_in) and acc (B, Q) of B children.  A call given that la_work
+ * as `pre` with its lb, A and acc at those addresses reads and updates
+ * them in place instead of copying them (any other outputs are filled
+ * with copies).  Has no counterpart in the reference: the layout of the
+ * handoff between two native rounds. */
+int vc_mlp_bab_round_handoff_offsets(const int32_t *dims, int n_relu, int64_t B,
+                                     int Q, int64_t *off);
 int vc_mlp_bab_round(const int32_t *dims, int n_relu, const float *frag,
                      const float *bias_cat, int Q, const float *spec_rows,
                      const float *spec_acc, const int32_t *d_ptr,

@@ -78,3 +78,20 @@ def test_zono_wide_capacity_matches_header():
     text = open(os.path.join(ROOT, 'include', 'vibecheck_amd.h')).read()
     m = re.search(r'#define VC_ZONO_WIDE_COLS (\d+)', text)
     assert m and int(m.group(1)) == _lib.VC_ZONO_WIDE_COLS
+
+
+def test_round_handoff_offsets_layout():
+    """The handed-over spec bound, A and acc of B children inside la_work:
+    each array 256-byte aligned, in that order and back to back (sizes
+    rounded up to 256 bytes), so a caller can point a round's lb, A and
+    acc there; host arithmetic only."""
+    dims = (ctypes.c_int32 * 8)(5, 50, 50, 50, 50, 50, 50, 5)
+    for B, Q in ((810, 4), (1, 1), (65536, 9)):
+        off = (ctypes.c_int64 * 3)()
+        _lib.call('vc_mlp_bab_round_handoff_offsets', ctypes.addressof(dims), 6, B, Q,
+                  ctypes.addressof(off))
+        up = lambda nbytes: (nbytes + 255) // 256 * 256
+        assert list(off) == [0, up(4 * B * Q), up(4 * B * Q) + up(4 * B * Q * 5)], (B, Q)
+    with pytest.raises(ValueError):
+        _lib.call('vc_mlp_bab_round_handoff_offsets', ctypes.addressof(dims), 6, 4, 0,
+                  ctypes.addressof(off))

@@ -67,10 +67,12 @@ struct RoundBufs {
 
 // The next round's bound phase as a round with lookahead hands it over,
 // for its B kept children in the order of the next batch: the spec bound,
-// its input linearization and the zonotope bounds alpha starts from.
+// its input linearization and the zonotope bounds alpha starts from, and
+// the counters that round starts from (cnt[3], its open-leaf count, zero).
 struct Handoff {
   float *lb, *A, *acc;
   float *sb_lo[MAXL], *sb_hi[MAXL];
+  int64_t* cnt;  // [4]
 };
 
 // The lookahead's buffers: the handoff (reserved for cap rows, laid out for
@@ -167,6 +169,7 @@ void carve_handoff(Carve& c, Handoff& h, const int32_t* dims, int n, int64_t B, 
     h.sb_lo[l] = c.take<float>(B * dims[l + 1]);
     h.sb_hi[l] = c.take<float>(B * dims[l + 1]);
   }
+  h.cnt = c.take<int64_t>(4);
 }
 
 void carve_look(Carve& c, LookBufs& L, const int32_t* dims, int n, int64_t B, int Q,
@@ -221,6 +224,18 @@ extern "C" int64_t vc_mlp_bab_round_lookahead_workspace(const int32_t* dims, int
   c.used = at;
   carve_bound(c, bb, dims, n_relu, std::min<int64_t>(cap, (int64_t)vcm::cu_count() * 4));
   return (int64_t)std::max(big, c.used);
+}
+
+extern "C" int vc_mlp_bab_round_handoff_offsets(const int32_t* dims, int n_relu, int64_t B,
+                                                int Q, int64_t* off) {
+  if (!dims || !off || n_relu < 1 || n_relu > MAXL || B < 0 || Q < 1) return VC_ERR_ARG;
+  Carve c{reinterpret_cast<char*>(256), 0};  // any aligned base: offsets only
+  Handoff h;
+  carve_handoff(c, h, dims, n_relu, B, Q);
+  off[0] = reinterpret_cast<char*>(h.lb) - reinterpret_cast<char*>(256);
+  off[1] = reinterpret_cast<char*>(h.A) - reinterpret_cast<char*>(256);
+  off[2] = reinterpret_cast<char*>(h.acc) - reinterpret_cast<char*>(256);
+  return VC_OK;
 }
 
 namespace {
@@ -578,22 +593,26 @@ int bab_round(const int32_t* dims, int n_relu, const float* frag, const float* b
   carve(c, r, dims, n, B, Q);
 
   // ---- bound phase, or the one a previous round's lookahead handed over
+  // (its spec bound, A and acc read in place when the caller points lb, A
+  // and acc there: vc_mlp_bab_round_handoff_offsets)
   if (pre) {
     Carve hc{reinterpret_cast<char*>(const_cast<void*>(pre)), 0};
     Handoff h;
     carve_handoff(hc, h, dims, n, B, Q);
-    if (hipMemcpyAsync(lb, h.lb, sizeof(float) * B * Q, hipMemcpyDeviceToDevice, st) !=
-            hipSuccess ||
-        hipMemcpyAsync(A, h.A, sizeof(float) * B * Q * n_in, hipMemcpyDeviceToDevice, st) !=
-            hipSuccess ||
-        hipMemcpyAsync(acc, h.acc, sizeof(float) * B * Q, hipMemcpyDeviceToDevice, st) !=
-            hipSuccess ||
-        hipMemsetAsync(r.b.cnt, 0, sizeof(int64_t) * 4, st) != hipSuccess)
+    if ((lb != h.lb &&
+         hipMemcpyAsync(lb, h.lb, sizeof(float) * B * Q, hipMemcpyDeviceToDevice, st) !=
+             hipSuccess) ||
+        (A != h.A && hipMemcpyAsync(A, h.A, sizeof(float) * B * Q * n_in,
+                                    hipMemcpyDeviceToDevice, st) != hipSuccess) ||
+        (acc != h.acc &&
+         hipMemcpyAsync(acc, h.acc, sizeof(float) * B * Q, hipMemcpyDeviceToDevice, st) !=
+             hipSuccess))
       return VC_ERR_LAUNCH;
     for (int l = 0; l < n; ++l) {
       r.b.sb_lo[l] = h.sb_lo[l];
       r.b.sb_hi[l] = h.sb_hi[l];
     }
+    r.b.cnt = r.t.cnt = h.cnt;
   } else {
     VC_TRY(bound_phase(dims, n, frag, bias_cat, B, xl, xh, r.b, Q, spec_rows, spec_acc, lb, A,
                        acc, seed_rows, crown_ev0, crown_ev1, st));
@@ -775,6 +794,8 @@ int bab_round(const int32_t* dims, int n_relu, const float* frag, const float* b
           hcols[3 + 2 * l] = hcols[4 + 2 * l] = dims[l + 1];
         }
         VC_TRY(gather(hin, hto, hcols, 3 + 2 * n, L.kidx, n_keep, stream));
+        if (hipMemsetAsync(h.cnt, 0, sizeof(int64_t) * 4, st) != hipSuccess)
+          return VC_ERR_LAUNCH;
       }
       counts[0] = n_open;
       counts[1] = n_eval;
@@ -821,6 +842,7 @@ int bab_round(const int32_t* dims, int n_relu, const float* frag, const float* b
       bb.sb_lo[l] = h.sb_lo[l];
       bb.sb_hi[l] = h.sb_hi[l];
     }
+    bb.cnt = h.cnt;  // the zonotope pass's init clears cnt[3] for the next round
     VC_TRY(bound_phase(dims, n, frag, bias_cat, bn, high_xl, high_xh, bb, Q, spec_rows,
                        spec_acc, h.lb, h.A, h.acc, nullptr, nullptr, nullptr, st));
     counts[6] = bn;

@@ -119,6 +119,7 @@ SIGNATURES = {
     'vc_mlp_tiled_zono_wide': [_P, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P],
     'vc_mlp_bab_round_workspace': [_P, _I, _L, _I],
     'vc_mlp_bab_round_lookahead_workspace': [_P, _I, _L, _I, _L],
+    'vc_mlp_bab_round_handoff_offsets': [_P, _I, _L, _I, _P],
     'vc_mlp_bab_round': [_P, _I, _P, _P, _I, _P, _P, _P, _P, _I, _L, _P, _P, _I, _D, _D, _D,
                          _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                          _P, _P, _L, _P, _P, _L, _L, _P, _P, _P, _P, _P, _P],

@@ -470,6 +470,15 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
     if pre is not None and (pre.get('n') != B or pre.get('plan') is not plan
                             or pre.get('spec') is not spec_ew):
         pre = None
+    # with a handed-over bound phase, the round reads and updates its spec
+    # bound, A and acc where the previous call left them (no copies)
+    p_lb, p_A, p_acc = p, p + 8 * Bm * Q, p + 4 * Bm * Q
+    if pre is not None:
+        hoff = (ctypes.c_int64 * 3)()
+        call('vc_mlp_bab_round_handoff_offsets', plan.dims_p, plan.n, B, Q,
+             ctypes.addressof(hoff))
+        hp = pre['buf'].data_ptr()
+        p_lb, p_A, p_acc = hp + hoff[0], hp + hoff[1], hp + hoff[2]
     la = aux = None
     la_bytes = la_cap = 0
     mode = 'overlap' if lookahead is True else lookahead
@@ -503,7 +512,7 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
         call('vc_mlp_bab_round', plan.dims_p, plan.n, plan.tfrag.data_ptr(),
              plan.bias_cat.data_ptr(), Q, S.data_ptr(), acc0.data_ptr(), ptr(table.d_ptr),
              ptr(table.q_idx), table.n, B, ptr(xl), ptr(xh), int(alpha_iters),
-             float(alpha_lr), float(alpha_lr_decay), 1e-6, p, p + 8 * Bm * Q, p + 4 * Bm * Q,
+             float(alpha_lr), float(alpha_lr_decay), 1e-6, p_lb, p_A, p_acc,
              p + o_flg, p + o_idx, p + o_flg + Bm, p_box, p_box + nb, p + o_idx + 8 * Bm,
              None, None, p_box + 2 * nb, p_box + 4 * nb, ptr(seeds),
              ev[0].cuda_event if ev else None, ev[1].cuda_event if ev else None, pev_p,
@@ -538,9 +547,16 @@ def _bab_round_native(xl, xh, gg, spec_ew, table, alpha_iters, alpha_lr, alpha_l
     bl = buf[o_flg:].view(torch.bool)
     ast = torch.as_strided
     bo, nb, oi, r = Bm * (2 * Q + Q * n_in), Bm * n_in, o_idx // 8, (n_in, 1)
-    out = {'lb': ast(fl, (B, Q), (Q, 1), 0),
-           'A': ast(fl, (B, Q, n_in), (Q * n_in, n_in, 1), 2 * Bm * Q),
-           'acc': ast(fl, (B, Q), (Q, 1), Bm * Q),
+    if pre is None:
+        lb_v = ast(fl, (B, Q), (Q, 1), 0)
+        A_v = ast(fl, (B, Q, n_in), (Q * n_in, n_in, 1), 2 * Bm * Q)
+        acc_v = ast(fl, (B, Q), (Q, 1), Bm * Q)
+    else:
+        hf = pre['buf'].view(torch.float32)
+        lb_v = ast(hf, (B, Q), (Q, 1), hoff[0] // 4)
+        A_v = ast(hf, (B, Q, n_in), (Q * n_in, n_in, 1), hoff[1] // 4)
+        acc_v = ast(hf, (B, Q), (Q, 1), hoff[2] // 4)
+    out = {'lb': lb_v, 'A': A_v, 'acc': acc_v,
            'closed': ast(bl, (B,), (1,), o_flg), 'unclosed': ast(i64, (n_unc,), (1,), oi),
            'n_alpha_leaves': n_open, 'n_alpha_iters': n_eval,
            'feasible': ast(bl, (n_unc,), (1,), o_flg + Bm) if n_unc > 0 else None,
