@@ -169,12 +169,7 @@ __device__ __forceinline__ double group_sum4_d(double v) {
 template <int KS, int NP, bool BROW, bool SGN = false>
 __device__ __forceinline__ void relax_rows(const float* sl, const float* bl, int g,
                                            v4f (&F)[TNP][4], double (&acc)[TNP]) {
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    const int t = ks >> 2, i = ks & 3;
-    const int j = 16 * t + 4 * g + i;
-    const float ls = sl[j], us = SGN ? fabsf(sl[FW + j]) : sl[FW + j], ut = sl[2 * FW + j];
-    const float bj = BROW ? 0.f : bl[j];
+  const auto step = [&](int t, int i, float ls, float us, float ut, float bj) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const float x = F[p][t][i];
@@ -184,6 +179,48 @@ __device__ __forceinline__ void relax_rows(const float* sl, const float* bl, int
       acc[p] += (double)(en * ut);
       if (!BROW) acc[p] += (double)(e * bj);
       F[p][t][i] = e;
+    }
+  };
+  if constexpr (SGN) {
+    // one float per load (k_alpha_tiled keeps its third wavefront per SIMD)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int t = ks >> 2, i = ks & 3;
+      const int j = 16 * t + 4 * g + i;
+      step(t, i, sl[j], fabsf(sl[FW + j]), sl[2 * FW + j], BROW ? 0.f : bl[j]);
+    }
+  } else {
+    // a lane's neurons 16 t + 4 g + i of a tile are consecutive: one
+    // float4 per slope array and tile where the arrays are 16-byte aligned
+    // (the padding beyond KS holds zeros), else one float each
+    const bool al = ((reinterpret_cast<uintptr_t>(sl) | reinterpret_cast<uintptr_t>(bl)) & 15) == 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (4 * t >= KS) break;
+      const int j0 = 16 * t + 4 * g;
+      float ls[4], us[4], ut[4], bj[4];
+      if (al) {
+        const float4 l4 = *reinterpret_cast<const float4*>(sl + j0);
+        const float4 u4 = *reinterpret_cast<const float4*>(sl + FW + j0);
+        const float4 t4 = *reinterpret_cast<const float4*>(sl + 2 * FW + j0);
+        const float4 b4 =
+            BROW ? float4{0.f, 0.f, 0.f, 0.f} : *reinterpret_cast<const float4*>(bl + j0);
+        ls[0] = l4.x; ls[1] = l4.y; ls[2] = l4.z; ls[3] = l4.w;
+        us[0] = u4.x; us[1] = u4.y; us[2] = u4.z; us[3] = u4.w;
+        ut[0] = t4.x; ut[1] = t4.y; ut[2] = t4.z; ut[3] = t4.w;
+        bj[0] = b4.x; bj[1] = b4.y; bj[2] = b4.z; bj[3] = b4.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ls[i] = sl[j0 + i];
+          us[i] = sl[FW + j0 + i];
+          ut[i] = sl[2 * FW + j0 + i];
+          bj[i] = BROW ? 0.f : bl[j0 + i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * t + i < KS) step(t, i, ls[i], us[i], ut[i], bj[i]);
     }
   }
 }
@@ -1121,7 +1158,10 @@ __global__ __launch_bounds__(NL > 0 ? 2 * MT * 64 : AQD * 4 * 64) void k_alpha_q
   extern __shared__ float smem[];
   float* sfrag = smem;
   float* sbias = smem + G.nfloats;  // [n][FW], zero-padded
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  // the wave index as a scalar: the per-wave tile choices below are then
+  // uniform branches, and the loads of an unrolled loop can be issued
+  // together instead of one masked block at a time
+  const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int qd = wid / MT, w = wid - qd * MT;  // domain slot, owned M-tile
   const int g = lane >> 4, r = lane & 15;
   const int n = NL > 0 ? NL : G.n, d0 = G.d[0], dN = G.d[n];
@@ -1203,19 +1243,30 @@ __global__ __launch_bounds__(NL > 0 ? 2 * MT * 64 : AQD * 4 * 64) void k_alpha_q
     for (int l = n - 1; l >= 0; --l) {
       const float* sl = ssl + l * 4 * FW;
       float* pl = sP + l * KS * 4 * Q;
+      // the owned neurons' slopes (and bias) first, one float4 each (the
+      // padding neurons hold zeros), then the rows and their relaxation
+      const int j0 = 16 * w + 4 * g;
+      const float4 ls4 = *reinterpret_cast<const float4*>(sl + j0);
+      const float4 us4 = *reinterpret_cast<const float4*>(sl + FW + j0);
+      const float4 ut4 = *reinterpret_cast<const float4*>(sl + 2 * FW + j0);
+      const float4 bb4 = BROW ? float4{0.f, 0.f, 0.f, 0.f}
+                              : *reinterpret_cast<const float4*>(sbias + l * FW + j0);
+      const float lsa[4] = {ls4.x, ls4.y, ls4.z, ls4.w};
+      const float usa[4] = {us4.x, us4.y, us4.z, us4.w};
+      const float uta[4] = {ut4.x, ut4.y, ut4.z, ut4.w};
+      const float bba[4] = {bb4.x, bb4.y, bb4.z, bb4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * w + i < KS && has && live) pl[((4 * w + i) * 4 + g) * Q + r] = Fw[i];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int ks = 4 * w + i;
-        if (ks < KS) {
-          if (has && live) pl[(ks * 4 + g) * Q + r] = Fw[i];
-          const int j = 16 * w + 4 * g + i;
-          const float ls = sl[j], us = sl[FW + j], ut = sl[2 * FW + j];
+        if (4 * w + i < KS) {
           const float x = Fw[i];
           const bool ng = x < 0.f;
-          const float e = x * (ng ? us : ls);
+          const float e = x * (ng ? usa[i] : lsa[i]);
           const float en = ng ? x : 0.f;
-          acc += (double)(en * ut);
-          if (!BROW) acc += (double)(e * sbias[l * FW + j]);
+          acc += (double)(en * uta[i]);
+          if (!BROW) acc += (double)(e * bba[i]);
           Fw[i] = e;
         }
       }
@@ -1300,18 +1351,38 @@ __global__ __launch_bounds__(NL > 0 ? 2 * MT * 64 : AQD * 4 * 64) void k_alpha_q
           GEw[i] = live ? GEw[i] + sbias[l * FW + 16 * w + 4 * g + i] : 0.f;
       }
       const float* pl = sP + l * KS * 4 * Q;
+      // every load of the step first: the rows (a lane past the Q live
+      // rows reads row 0 and discards it) and the slopes, one float4 each
+      const int j0 = 16 * w + 4 * g;
+      const int rq = live ? r : 0;
+      float pva[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ks = 4 * w + i;
+        pva[i] = ks < KS ? pl[(ks * 4 + g) * Q + rq] : 0.f;
+      }
+      const float4 ls4 = *reinterpret_cast<const float4*>(sl + j0);
+      const float4 us4 = *reinterpret_cast<const float4*>(sl + FW + j0);
+      const float4 ut4 = *reinterpret_cast<const float4*>(sl + 2 * FW + j0);
+      const float lsa[4] = {ls4.x, ls4.y, ls4.z, ls4.w};
+      const float usa[4] = {us4.x, us4.y, us4.z, us4.w};
+      const float uta[4] = {ut4.x, ut4.y, ut4.z, ut4.w};
+      float sums[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pv = (has && live) ? pva[i] : 0.f;
+        sums[i] = row_sum16(GEw[i] * fmaxf(pv, 0.f));
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int ks = 4 * w + i;
         if (ks < KS) {
-          const int j = 16 * w + 4 * g + i;
-          const float pv = (has && live) ? pl[(ks * 4 + g) * Q + r] : 0.f;
+          const float pv = (has && live) ? pva[i] : 0.f;
           const float ge = GEw[i];
-          const float s = row_sum16(ge * fmaxf(pv, 0.f));
-          if (r == 0) sga[l * FW + j] = s;
+          if (r == 0) sga[l * FW + j0 + i] = sums[i];
           const bool mp = pv >= 0.f, mn = pv <= 0.f;
-          float gp = ge * ((mp ? sl[j] : 0.f) + (mn ? sl[FW + j] : 0.f));
-          if (mn) gp = gp + sl[2 * FW + j];
+          float gp = ge * ((mp ? lsa[i] : 0.f) + (mn ? usa[i] : 0.f));
+          if (mn) gp = gp + uta[i];
           GEw[i] = live ? gp : 0.f;
         }
       }
@@ -1345,24 +1416,68 @@ __global__ __launch_bounds__(NL > 0 ? 2 * MT * 64 : AQD * 4 * 64) void k_alpha_q
     // ---- Adam on the owned neurons of every layer, all lanes
     __threadfence_block();
     if (has) {
-      for (int k = lane; k < n * 16; k += 64) {
-        const int l = k >> 4, j = 16 * w + (k & 15);
-        const int dW = G.d[l + 1];
-        float* sl = ssl + l * 4 * FW;
-        float* sa = sad + l * 3 * FW;
-        const float gs = sga[l * FW + j];
-        const bool un = j < dW && sl[3 * FW + j] != 0.f;
-        if (un) {
-          float mi = sa[FW + j], vi = sa[2 * FW + j];
-          float pa = adam_update(sa[j], -gs, mi, vi, adam);
-          pa = fminf(fmaxf(pa, 0.f), 1.f);
-          sa[FW + j] = mi;
-          sa[2 * FW + j] = vi;
-          sa[j] = pa;
-          sl[j] = pa;  // unstable: the next iteration's lower slope is alpha
+      if constexpr (NL > 0) {
+        // lane k of pass p takes neuron slot 64 p + k (layer slot / 16);
+        // every pass's loads are issued before any update (each slot is
+        // its own); padding neurons carry no unstable flag
+        constexpr int NP = (NL * 16 + 63) / 64;
+        float gsv[NP], unv[NP], av[NP], mv[NP], vv[NP];
+#pragma unroll
+        for (int p2 = 0; p2 < NP; ++p2) {
+          const int k = lane + 64 * p2;
+          const bool ok = k < NL * 16;
+          const int kk = ok ? k : 0;
+          const int l = kk >> 4, j = 16 * w + (kk & 15);
+          const float* sa = sad + l * 3 * FW;
+          gsv[p2] = sga[l * FW + j];
+          unv[p2] = ok ? ssl[l * 4 * FW + 3 * FW + j] : 0.f;
+          av[p2] = sa[j];
+          mv[p2] = sa[FW + j];
+          vv[p2] = sa[2 * FW + j];
         }
-        // the last iteration of the launch leaves its gradient
-        if (aa.grad[l] && j < dW && t_it == ac.n - 1) aa.grad[l][dom * dW + j] = un ? gs : 0.f;
+#pragma unroll
+        for (int p2 = 0; p2 < NP; ++p2) {
+          const int k = lane + 64 * p2;
+          if (k >= NL * 16) continue;
+          const int l = k >> 4, j = 16 * w + (k & 15);
+          const float gs = gsv[p2];
+          const bool un = unv[p2] != 0.f;
+          if (un) {
+            float* sa = sad + l * 3 * FW;
+            float mi = mv[p2], vi = vv[p2];
+            float pa = adam_update(av[p2], -gs, mi, vi, adam);
+            pa = fminf(fmaxf(pa, 0.f), 1.f);
+            sa[FW + j] = mi;
+            sa[2 * FW + j] = vi;
+            sa[j] = pa;
+            ssl[l * 4 * FW + j] = pa;  // unstable: the next iteration's lower slope is alpha
+          }
+          // the last iteration of the launch leaves its gradient
+          if (aa.grad[l] && t_it == ac.n - 1) {
+            const int dW = G.d[l + 1];
+            if (j < dW) aa.grad[l][dom * dW + j] = un ? gs : 0.f;
+          }
+        }
+      } else {
+        for (int k = lane; k < n * 16; k += 64) {
+          const int l = k >> 4, j = 16 * w + (k & 15);
+          const int dW = G.d[l + 1];
+          float* sl = ssl + l * 4 * FW;
+          float* sa = sad + l * 3 * FW;
+          const float gs = sga[l * FW + j];
+          const bool un = j < dW && sl[3 * FW + j] != 0.f;
+          if (un) {
+            float mi = sa[FW + j], vi = sa[2 * FW + j];
+            float pa = adam_update(sa[j], -gs, mi, vi, adam);
+            pa = fminf(fmaxf(pa, 0.f), 1.f);
+            sa[FW + j] = mi;
+            sa[2 * FW + j] = vi;
+            sa[j] = pa;
+            sl[j] = pa;  // unstable: the next iteration's lower slope is alpha
+          }
+          // the last iteration of the launch leaves its gradient
+          if (aa.grad[l] && j < dW && t_it == ac.n - 1) aa.grad[l][dom * dW + j] = un ? gs : 0.f;
+        }
       }
     }
     __threadfence_block();
