@@ -422,6 +422,47 @@ def test_zono_parity_acas(gpu):
     assert torch.equal(cpu(gG) == 0, rG == 0)
 
 
+@pytest.mark.parametrize('K', [7, 300])
+def test_zono_relu_apply_exact(gpu, K):
+    """The zonotope ReLU's apply step (verify_zono_bnb.py:3185-3210), the
+    per-element form (short rows) and the one-wavefront-per-row form
+    (K + K_new >= 256), against the same operations in torch on the GPU,
+    bit for bit: G lam, the new generator mu at the row's rank, lam c + mu;
+    the unstable, dead and active rows all present."""
+    _st = _lib_stream
+    g = torch.Generator(device=gpu).manual_seed(K)
+    B, n = 37, 50
+    c = torch.randn(B, n, device=gpu, generator=g)
+    G = torch.randn(B, n, K, device=gpu, generator=g) * 0.3
+    c[0, :5] = -1000.0                     # dead rows
+    c[0, 5:10] = 1000.0                    # active rows
+    lo = torch.empty(B, n, device=gpu)
+    hi = torch.empty(B, n, device=gpu)
+    rank = torch.empty(B, n, dtype=torch.int32, device=gpu)
+    cnt = torch.empty(B, dtype=torch.int32, device=gpu)
+    call('vc_zono_relu_bounds', ptr(c), ptr(G), B, n, K, ptr(lo), ptr(hi), ptr(rank), ptr(cnt),
+         _st())
+    Kn = int(cnt.max())
+    assert Kn > 0
+    c_out = torch.empty(B, n, device=gpu)
+    G_out = torch.full((B, n, K + Kn), float('nan'), device=gpu)
+    call('vc_zono_relu_apply', ptr(c), ptr(G), ptr(lo), ptr(hi), ptr(rank), B, n, K, Kn,
+         ptr(c_out), ptr(G_out), _st())
+    ust = (lo < 0) & (hi > 0)
+    dead = hi <= 0
+    assert bool(ust.any()) and bool(dead.any()) and bool((~ust & ~dead).any())
+    lam = torch.where(ust, hi / (hi - lo), torch.where(dead, torch.zeros_like(hi),
+                                                       torch.ones_like(hi)))
+    mu = torch.where(ust, (-hi * lo) / (2.0 * (hi - lo)), torch.zeros_like(hi))
+    want = torch.zeros(B, n, K + Kn, device=gpu)
+    want[:, :, :K] = G * lam.unsqueeze(-1)
+    cols = torch.arange(Kn, device=gpu).view(1, 1, -1)
+    want[:, :, K:] = torch.where(ust.unsqueeze(-1) & (cols == rank.unsqueeze(-1).long()),
+                                 mu.unsqueeze(-1), torch.zeros((), device=gpu))
+    assert torch.equal(G_out, want)
+    assert torch.equal(c_out, lam * c + mu)
+
+
 # ----------------------------------------------------------------- a5-a8
 def test_spec_backward_parity_same_bounds(gpu):
     gg_c, gg_g, xl, xh = acas(gpu, 1024, scale=3.0)

@@ -90,6 +90,33 @@ __global__ void k_zono_apply(const float* c, const float* G, const float* lo, co
   }
 }
 
+// k_zono_apply for long rows (K + Kn >= 256): one wavefront per (b, j)
+// row, lambda and mu computed once per row (every lane the same values),
+// the row streamed with consecutive lanes on consecutive columns.  Same
+// operations per element as k_zono_apply, without its per-element 64-bit
+// division and relaxation.
+__global__ void k_zono_apply_rows(const float* c, const float* G, const float* lo,
+                                  const float* hi, const int32_t* rank, int64_t rows, int K,
+                                  int Kn, float* c_out, float* G_out) {
+#pragma clang fp contract(off)
+  const int Ko = K + Kn;
+  const int lane = threadIdx.x & 63;
+  for (int64_t row = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6; row < rows;
+       row += ((int64_t)gridDim.x * blockDim.x) >> 6) {
+    const float l = lo[row], h = hi[row];
+    const bool ust = l < 0.f && h > 0.f;
+    const bool dead = h <= 0.f;
+    const float lam = ust ? h / (h - l) : (dead ? 0.f : 1.f);
+    const float mu = ust ? (-h * l) / (2.f * (h - l)) : 0.f;
+    const float* g = G + row * K;
+    float* o = G_out + row * Ko;
+    for (int k = lane; k < K; k += 64) o[k] = g[k] * lam;
+    const int rk = ust ? rank[row] : -1;
+    for (int k = K + lane; k < Ko; k += 64) o[k] = (k - K == rk) ? mu : 0.f;
+    if (lane == 0) c_out[row] = lam * c[row] + mu;
+  }
+}
+
 }  // namespace
 
 extern "C" int vc_zono_relu_bounds(const float* c, const float* G, int64_t B, int n, int K,
@@ -117,8 +144,13 @@ extern "C" int vc_zono_relu_apply(const float* c, const float* G, const float* l
   if ((K + K_new > 0 && !G_out) || (K > 0 && !G)) return VC_ERR_ARG;
   if (B == 0) return VC_OK;
   const int64_t rows = B * (int64_t)n;
-  hipLaunchKernelGGL(k_zono_apply, dim3(vc_blocks(rows * (K + K_new > 0 ? K + K_new : 1), NT)), dim3(NT), 0,
-                     (hipStream_t)stream, c, G, lo, hi, rank, rows, K, K_new, c_out, G_out);
+  if (K + K_new >= 256)
+    hipLaunchKernelGGL(k_zono_apply_rows, dim3(vc_blocks(rows * 64, NT)), dim3(NT), 0,
+                       (hipStream_t)stream, c, G, lo, hi, rank, rows, K, K_new, c_out, G_out);
+  else
+    hipLaunchKernelGGL(k_zono_apply, dim3(vc_blocks(rows * (K + K_new > 0 ? K + K_new : 1), NT)),
+                       dim3(NT), 0, (hipStream_t)stream, c, G, lo, hi, rank, rows, K, K_new,
+                       c_out, G_out);
   VC_LAUNCH_CHECK();
   return VC_OK;
 }
