@@ -240,14 +240,20 @@ __device__ __forceinline__ void fc_hidden(const float4* fr, int lane, int g, int
   // MFMAs wins the arbitration, and the other wavefronts' relaxation VALU
   // work fills the matrix unit's gaps (2% faster on the CROWN rows pass)
   __builtin_amdgcn_s_setprio(1);
+  // each K-step's fragments requested one K-step ahead, so that the LDS
+  // read overlaps the current K-step's MFMAs instead of preceding them
+  float4 a4 = fr[swz(lane, 0)];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    const float4 a4 = fr[ks * 64 + swz(lane, ks)];
+    const float4 nx = ks + 1 < KS ? fr[(ks + 1) * 64 + swz(lane, ks + 1)] : a4;
+    // keep the scheduler from sinking that read below the MFMAs
+    __builtin_amdgcn_sched_barrier(0);
     const float a[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int p = 0; p < NP; ++p) o[p][mt] = mfma16x16x4(a[mt], F[p][ks >> 2][ks & 3], o[p][mt]);
+    a4 = nx;
   }
   __builtin_amdgcn_s_setprio(0);
   if (BROW) {
