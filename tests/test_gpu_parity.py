@@ -843,12 +843,15 @@ def test_alpha_small_batch_kernel_matches_large_batch_kernel(gpu, n_iters):
 
 
 # ----------------------------------------------------------------- a11-a14
-@pytest.mark.parametrize('n', [5, 12, 20])
-def test_clip_parity_identical_inputs(gpu, n):
-    """n = 5 and 12: the register kernels (boxes of at most 8 and 16 dims);
-    n = 20: the generic one.  B is not a multiple of the 64-box workgroup."""
+@pytest.mark.parametrize('n, Q', [(5, 4), (12, 4), (5, 16), (12, 8), (20, 4)])
+def test_clip_parity_identical_inputs(gpu, n, Q):
+    """Every clip kernel: one wavefront per box when the queries (rounded up
+    to a power of two) times the dims fit its 64 lanes (n = 5 and 12 with
+    Q = 4); else the register kernels for boxes of at most 8 and 16 dims
+    (n = 5, Q = 16; n = 12, Q = 8); n = 20: the generic one.  B is not a
+    multiple of the 64-box workgroup."""
     g = torch.Generator().manual_seed(3)
-    B, Q = 4109, 4
+    B = 4109
     xl = torch.rand(B, n, generator=g) - 1
     xh = xl + torch.rand(B, n, generator=g) + 0.01
     A = torch.randn(B, Q, n, generator=g)
@@ -871,7 +874,7 @@ def test_clip_parity_identical_inputs(gpu, n):
     assert torch.equal(cpu(gf), rf)
     assert_bounds(gl, rl, 'clip xl', ref64=rl64, scale=sc)
     assert_bounds(gh, rh, 'clip xh', ref64=rh64, scale=sc)
-    dq = {0: [0, 2], 1: [1], 2: [3]}
+    dq = {0: [0, 2], 1: [1], 2: [3, Q - 1]}
     rl, rh, rf = rbab.clip_leaves(xl, xh, A, b, dq)
     rl64, rh64, _ = rbab.clip_leaves(xl.double(), xh.double(), A.double(), b.double(), dq)
     tab = vg.DisjunctTable(dq, gpu)
@@ -879,6 +882,33 @@ def test_clip_parity_identical_inputs(gpu, n):
     assert torch.equal(cpu(gf), rf)
     assert_bounds(gl, rl, 'clip union xl', ref64=rl64, scale=sc)
     assert_bounds(gh, rh, 'clip union xh', ref64=rh64, scale=sc)
+
+
+@pytest.mark.parametrize('n', [5, 12])
+def test_clip_lane_kernel_matches_thread_kernel_bits(gpu, n):
+    """The one-wavefront-per-box clip against the one-thread-per-box
+    kernels on the same boxes and halfspaces: Q = 4 takes the lane kernel;
+    the same four queries followed by twelve more that no disjunct lists
+    (Q = 16: 16 x n lanes do not fit a wavefront) take the register kernel
+    (n = 5) or the generic one (n = 12).  Thresholds, minima and the
+    feasibility test are the same operations, so the boxes agree bit for
+    bit, for one disjunct and for a union of three.  Boxes with an upper
+    bound at exactly 0 test the sign of zero through the minima."""
+    g = torch.Generator().manual_seed(11 + n)
+    B = 1031
+    xl = torch.rand(B, n, generator=g) - 1
+    xh = xl + torch.rand(B, n, generator=g) + 0.01
+    xh[::7, 0] = 0.0
+    A16 = torch.randn(B, 16, n, generator=g)
+    b16 = torch.randn(B, 16, generator=g) - 1.0
+    A4, b4 = A16[:, :4].contiguous(), b16[:, :4].contiguous()
+    for dq in ({0: [0, 1, 2, 3]}, {0: [0, 2], 1: [1], 2: [3, 1]}):
+        tab = vg.DisjunctTable(dq, gpu)
+        l4, h4, f4 = vg._clip(xl.to(gpu), xh.to(gpu), A4.to(gpu), b4.to(gpu), tab)
+        l16, h16, f16 = vg._clip(xl.to(gpu), xh.to(gpu), A16.to(gpu), b16.to(gpu), tab)
+        assert torch.equal(cpu(f4), cpu(f16))
+        assert torch.equal(cpu(l4).view(torch.int32), cpu(l16).view(torch.int32))
+        assert torch.equal(cpu(h4).view(torch.int32), cpu(h16).view(torch.int32))
 
 
 @pytest.mark.parametrize('n', [1028, 36, 35])

@@ -1087,6 +1087,83 @@ __global__ __launch_bounds__(64) void k_clip_reg(const float* xl, const float* x
   }
 }
 
+// Boxes of n dims with at most QP queries (QP a power of two, QP n <= 64):
+// one wavefront per box, lane i QP + q taking query q on dimension i.
+// Each lane forms its query's total itself (the same sums in the same
+// order as k_clip_reg), its own threshold, and the minimum / maximum over
+// a disjunct's queries is a butterfly over the QP lanes of a dimension
+// (min and max do not depend on the order).  Same values as k_clip_reg; a
+// batch of a few hundred boxes takes one load round trip instead of a
+// serial loop per box.
+template <int QP>
+__global__ __launch_bounds__(256) void k_clip_lanes(const float* __restrict__ xl,
+                                                    const float* __restrict__ xh,
+                                                    const float* __restrict__ A,
+                                                    const float* __restrict__ bv, int64_t B,
+                                                    int Q, int n, const int32_t* dptr,
+                                                    const int32_t* qidx, int nd, float* xlo,
+                                                    float* xho, uint8_t* feas) {
+  const int lane = threadIdx.x & 63;
+  const int q = lane % QP, i = lane / QP;
+  const bool on = q < Q && i < n;
+  const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
+  for (int64_t b = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); b < B;
+       b += nw) {
+    const float* aq = A + (b * Q + (on ? q : 0)) * n;
+    const float* l = xl + b * n;
+    const float* h = xh + b * n;
+    const int ii = on ? i : 0;
+    const float a = aq[ii], li = l[ii], hi = h[ii];
+    const float bq = bv[b * Q + (on ? q : 0)];
+    float s1 = 0.f, s2 = 0.f;
+    for (int k = 0; k < n; ++k) {
+      const float ak = aq[k];
+      s1 += fmaxf(ak, 0.f) * l[k];
+      s2 += fminf(ak, 0.f) * h[k];
+    }
+    const float tq = s1 + s2;
+    const float contrib = fmaxf(a, 0.f) * li + fminf(a, 0.f) * hi;
+    const float other = tq - contrib;
+    const float safe = fabsf(a) > 1e-12f ? a : 1.f;
+    const float thr = (-bq - other) / safe;
+    const float hq = a > 1e-12f ? thr : hi;
+    const float lq = a < -1e-12f ? thr : li;
+    float ol = li, oh = hi;
+    bool any_feas = false;
+    for (int d = 0; d < nd; ++d) {
+      // this lane's query in disjunct d (listed once or more)
+      bool mem = false;
+      for (int t = dptr[d]; t < dptr[d + 1]; ++t) mem |= qidx[t] == q;
+      mem &= on;
+      float hm = mem ? hq : INFINITY, lm = mem ? lq : -INFINITY;
+#pragma unroll
+      for (int o = 1; o < QP; o <<= 1) {
+        hm = fminf(hm, __shfl_xor(hm, o, 64));
+        lm = fmaxf(lm, __shfl_xor(lm, o, 64));
+      }
+      hm = fminf(hm, hi);
+      lm = fmaxf(lm, li);
+      const bool empty = __ballot((mem && (tq + bq) > 0.f) || (on && lm > hm)) != 0ull;
+      if (nd == 1) {
+        ol = lm;
+        oh = hm;
+        any_feas = !empty;
+        break;
+      }
+      if (!empty) {
+        ol = any_feas ? fminf(ol, lm) : lm;
+        oh = any_feas ? fmaxf(oh, hm) : hm;
+        any_feas = true;
+      }
+    }
+    if (on && q == 0) {
+      xlo[b * n + i] = ol;
+      xho[b * n + i] = oh;
+    }
+    if (lane == 0) feas[b] = any_feas;
+  }
+}
+
 // ---- compaction: ascending positions of non-zero flags -------------------
 constexpr int CPT = 4;               // flags per thread
 constexpr int CCH = NT * CPT;        // flags per block
@@ -1699,6 +1776,31 @@ extern "C" int vc_clip_box(const float* xl, const float* xh, const float* A, con
   if (B < 0 || Q <= 0 || n <= 0 || n_disj <= 0) return VC_ERR_ARG;
   if (Q > CLIP_MAXQ) return VC_ERR_UNSUPPORTED;
   if (B == 0) return VC_OK;
+  int qp = 1;
+  while (qp < Q) qp <<= 1;
+  if (qp * n <= 64) {
+    // one wavefront per box
+    const int64_t nblk = std::min<int64_t>((B + 3) / 4, 65536);
+    hipStream_t st = (hipStream_t)stream;
+#define VC_CLIP_LANES(QP)                                                                     \
+  case QP:                                                                                    \
+    hipLaunchKernelGGL(k_clip_lanes<QP>, dim3((unsigned)nblk), dim3(256), 0, st, xl, xh, A, b, \
+                       B, Q, n, d_ptr, q_idx, n_disj, xl_out, xh_out, feasible);              \
+    break;
+    switch (qp) {
+      VC_CLIP_LANES(1)
+      VC_CLIP_LANES(2)
+      VC_CLIP_LANES(4)
+      VC_CLIP_LANES(8)
+      VC_CLIP_LANES(16)
+      VC_CLIP_LANES(32)
+      VC_CLIP_LANES(64)
+      default: return VC_ERR_UNSUPPORTED;
+    }
+#undef VC_CLIP_LANES
+    VC_LAUNCH_CHECK();
+    return VC_OK;
+  }
   const size_t rec_bytes = 64 * (size_t)((Q * n + Q) | 1) * sizeof(float);
   if (n <= 8 && rec_bytes <= 32768)
     hipLaunchKernelGGL(k_clip_reg<8>, dim3(vc_blocks(B, 64)), dim3(64), rec_bytes,
