@@ -640,15 +640,20 @@ __global__ void k_split_clamps(const int64_t* layer, const int64_t* neuron, cons
 // stopped test, so the launch makes one round trip to memory instead of
 // three per iteration (9.2 -> 6.3 us for 4 iterations over 1,644 bounds).
 // CACHED: n <= kCtlEpt * kCtlThreads, each thread's elements stay in
-// registers for the write; otherwise the write pass reads them again.
+// registers for the write; otherwise (1,024 threads) the write pass reads
+// them again, and with one iteration per launch (the one-wavefront-per-
+// domain alpha kernel's loop) best is written in the sweep itself, eight
+// loads per thread in flight (float4 where aligned).
 constexpr int kCtlThreads = 512;
+constexpr int kCtlThreadsBig = 1024;
 constexpr int kCtlEpt = 4;
 
 template <bool CACHED>
-__global__ __launch_bounds__(kCtlThreads) void k_alpha_control(
+__global__ __launch_bounds__(CACHED ? kCtlThreads : kCtlThreadsBig) void k_alpha_control(
     float* best, const float* lbs, int64_t n, int it0, int n_it, double eps, float* ctl,
     int32_t* stop_host, int32_t* progress) {
-  constexpr int NW = kCtlThreads / 64, E = CACHED ? kCtlEpt : 1;
+  constexpr int NTH = CACHED ? kCtlThreads : kCtlThreadsBig;
+  constexpr int NW = NTH / 64, E = CACHED ? kCtlEpt : 1;
   __shared__ float smax[VC_ALPHA_CHUNK][NW];
   __shared__ int sneg[VC_ALPHA_CHUNK][NW];
   __shared__ int s_last;
@@ -686,12 +691,50 @@ __global__ __launch_bounds__(kCtlThreads) void k_alpha_control(
       }
     }
   };
+  // one iteration, no cache: best written in the sweep (every iteration a
+  // launch takes is written, so the stop test does not gate the write)
+  const bool single = !CACHED && n_it == 1;
   if (CACHED) {
 #pragma unroll
     for (int e = 0; e < E; ++e)
       if (threadIdx.x + (int64_t)e * kCtlThreads < n) run(bv[e], xv[e], 0);
+  } else if (single) {
+    const auto one = [&](float b, float x) {
+      b = it0 == 0 ? x : fmaxf(b, x);
+      mx[0] = fmaxf(mx[0], b);
+      notpos[0] |= !(b > 0.f);
+      return b;
+    };
+    const bool v4 = ((reinterpret_cast<uintptr_t>(best) | reinterpret_cast<uintptr_t>(lbs)) & 15) == 0;
+    const int64_t n4 = v4 ? n / 4 : 0;
+    float4* b4 = reinterpret_cast<float4*>(best);
+    const float4* x4 = reinterpret_cast<const float4*>(lbs);
+    for (int64_t i0 = threadIdx.x; i0 < n4; i0 += 8 * NTH) {
+      float4 xv8[8], bv8[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t i = i0 + (int64_t)u * NTH;
+        const bool in = i < n4;
+        xv8[u] = in ? x4[i] : float4{0.f, 0.f, 0.f, 0.f};
+        bv8[u] = (in && it0 > 0) ? b4[i] : float4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t i = i0 + (int64_t)u * NTH;
+        if (i < n4) {
+          float4 o;
+          o.x = one(bv8[u].x, xv8[u].x);
+          o.y = one(bv8[u].y, xv8[u].y);
+          o.z = one(bv8[u].z, xv8[u].z);
+          o.w = one(bv8[u].w, xv8[u].w);
+          b4[i] = o;
+        }
+      }
+    }
+    for (int64_t i = 4 * n4 + threadIdx.x; i < n; i += NTH)
+      best[i] = one(it0 > 0 ? best[i] : 0.f, lbs[i]);
   } else {
-    for (int64_t i = threadIdx.x; i < n; i += kCtlThreads) run(it0 > 0 ? best[i] : 0.f, nullptr, i);
+    for (int64_t i = threadIdx.x; i < n; i += NTH) run(it0 > 0 ? best[i] : 0.f, nullptr, i);
   }
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
@@ -738,6 +781,7 @@ __global__ __launch_bounds__(kCtlThreads) void k_alpha_control(
     s_last = last;
   }
   __syncthreads();
+  if (single) return;
   const int last = s_last;
   const auto upto = [&](float b, const float* x, int64_t i) {
 #pragma unroll
@@ -756,7 +800,7 @@ __global__ __launch_bounds__(kCtlThreads) void k_alpha_control(
       if (i < n) upto(bv[e], xv[e], i);
     }
   } else {
-    for (int64_t i = threadIdx.x; i < n; i += kCtlThreads) upto(it0 > 0 ? best[i] : 0.f, nullptr, i);
+    for (int64_t i = threadIdx.x; i < n; i += NTH) upto(it0 > 0 ? best[i] : 0.f, nullptr, i);
   }
 }
 
@@ -766,8 +810,8 @@ void alpha_control_launch(float* best, const float* lbs, int64_t n, int it0, int
     hipLaunchKernelGGL(k_alpha_control<true>, dim3(1), dim3(kCtlThreads), 0, st, best, lbs, n,
                        it0, n_it, eps, ctl, stop_host, progress);
   else
-    hipLaunchKernelGGL(k_alpha_control<false>, dim3(1), dim3(kCtlThreads), 0, st, best, lbs, n,
-                       it0, n_it, eps, ctl, stop_host, progress);
+    hipLaunchKernelGGL(k_alpha_control<false>, dim3(1), dim3(kCtlThreadsBig), 0, st, best, lbs,
+                       n, it0, n_it, eps, ctl, stop_host, progress);
 }
 
 __global__ void k_best_update(float* best, const float* lb, int64_t n, int init, float* out2) {
