@@ -228,7 +228,11 @@ __device__ __forceinline__ void relax_rows(const float* sl, const float* bl, int
 // Backward through hidden fc_l: F (rows at fc_l's output, relaxed) <- A F
 // with A = [W_l^T; bias_l]; with the bias row, its output (row mb = d_l,
 // held by lane group (mb % 16) / 4) is the bias dot and goes to acc.
-template <int MT, int KS, int NP, bool BROW>
+// IDX: the bias row's entry (the same M-tile and component in every lane)
+// picked by register indexing (s_set_gpr_idx), else by a scalar switch
+// (k_alpha_tiled's instance, where the contiguous copy the indexing needs
+// costs its third wavefront per SIMD).
+template <int MT, int KS, int NP, bool BROW, bool IDX = true>
 __device__ __forceinline__ void fc_hidden(const float4* fr, int lane, int g, int mb,
                                           v4f (&F)[TNP][4], double (&acc)[TNP]) {
   v4f o[TNP][MT];
@@ -260,20 +264,30 @@ __device__ __forceinline__ void fc_hidden(const float4* fr, int lane, int g, int
     // the bias row's entry: (M-tile, component) is the same for every lane,
     // so a scalar branch picks it
     const bool mine = g == ((mb & 15) >> 2);
+    const int sel = __builtin_amdgcn_readfirstlane(((mb >> 4) << 2) | (mb & 3));
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       float v = 0.f;
-      switch (((mb >> 4) << 2) | (mb & 3)) {
-#define VC_BROW_CASE(C)                                   \
-  case C:                                                 \
+      if constexpr (IDX) {
+        float flat[4 * MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) flat[4 * mt + i] = o[p][mt][i];
+        v = sel < 4 * MT ? flat[sel < 4 * MT ? sel : 0] : 0.f;
+      } else {
+        switch (sel) {
+#define VC_BROW_CASE(C)                                               \
+  case C:                                                             \
     if ((C >> 2) < MT) v = o[p][(C >> 2) < MT ? (C >> 2) : 0][C & 3]; \
     break;
-        VC_BROW_CASE(0) VC_BROW_CASE(1) VC_BROW_CASE(2) VC_BROW_CASE(3)
-        VC_BROW_CASE(4) VC_BROW_CASE(5) VC_BROW_CASE(6) VC_BROW_CASE(7)
-        VC_BROW_CASE(8) VC_BROW_CASE(9) VC_BROW_CASE(10) VC_BROW_CASE(11)
-        VC_BROW_CASE(12) VC_BROW_CASE(13) VC_BROW_CASE(14) VC_BROW_CASE(15)
+          VC_BROW_CASE(0) VC_BROW_CASE(1) VC_BROW_CASE(2) VC_BROW_CASE(3)
+          VC_BROW_CASE(4) VC_BROW_CASE(5) VC_BROW_CASE(6) VC_BROW_CASE(7)
+          VC_BROW_CASE(8) VC_BROW_CASE(9) VC_BROW_CASE(10) VC_BROW_CASE(11)
+          VC_BROW_CASE(12) VC_BROW_CASE(13) VC_BROW_CASE(14) VC_BROW_CASE(15)
 #undef VC_BROW_CASE
-        default: break;
+          default: break;
+        }
       }
       if (mine) acc[p] += (double)v;
     }
@@ -959,7 +973,8 @@ __device__ __forceinline__ double alpha_pass(const TGeom& G, const AlphaLds& w, 
       for (int ks = 0; ks < KS; ++ks) pl[(ks * 4 + g) * Q + r] = F[0][ks >> 2][ks & 3];
     }
     relax_rows<KS, 1, BROW, true>(ssl + l * 3 * FW, sbias + l * FW, g, F, acc);
-    if (l > 0) fc_hidden<MT, KS, 1, BROW>(frh + (l - 1) * KS * 64, lane, g, G.d[l], F, acc);
+    if (l > 0)
+      fc_hidden<MT, KS, 1, BROW, false>(frh + (l - 1) * KS * 64, lane, g, G.d[l], F, acc);
   }
   // ---- fc_0, concretization and gE_0 = W_0 gA + b_0, one input tile at a time
   v4f GE[4];
