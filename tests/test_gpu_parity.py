@@ -846,10 +846,11 @@ def test_alpha_small_batch_kernel_matches_large_batch_kernel(gpu, n_iters):
 @pytest.mark.parametrize('n, Q', [(5, 4), (12, 4), (5, 16), (12, 8), (20, 4)])
 def test_clip_parity_identical_inputs(gpu, n, Q):
     """Every clip kernel: one wavefront per box when the queries (rounded up
-    to a power of two) times the dims fit its 64 lanes (n = 5 and 12 with
-    Q = 4); else the register kernels for boxes of at most 8 and 16 dims
-    (n = 5, Q = 16; n = 12, Q = 8); n = 20: the generic one.  B is not a
-    multiple of the 64-box workgroup."""
+    to a power of two) times the dims fit its 64 lanes and the batch is at
+    most 64 boxes per CU (n = 5 and 12 with Q = 4); else the register
+    kernels for boxes of at most 8 and 16 dims (n = 5, Q = 16; n = 12,
+    Q = 8); n = 20: the generic one.  B is not a multiple of the 64-box
+    workgroup."""
     g = torch.Generator().manual_seed(3)
     B = 4109
     xl = torch.rand(B, n, generator=g) - 1
