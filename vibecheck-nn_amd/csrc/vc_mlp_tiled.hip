@@ -262,7 +262,7 @@ __device__ __forceinline__ void fc_hidden(const float4* fr, int lane, int g, int
   __builtin_amdgcn_s_setprio(0);
   if (BROW) {
     // the bias row's entry: (M-tile, component) is the same for every lane,
-    // so a scalar branch picks it
+    // a scalar index (see IDX)
     const bool mine = g == ((mb & 15) >> 2);
     const int sel = __builtin_amdgcn_readfirstlane(((mb >> 4) << 2) | (mb & 3));
 #pragma unroll
