@@ -2313,20 +2313,6 @@ __device__ __forceinline__ uint32_t row_code(int64_t d, int neg, int j) {
   return ((uint32_t)d << 7) | ((uint32_t)neg << 6) | (uint32_t)j;
 }
 
-// The widest relu layer (the seeded-row bound buffer's stride).
-__host__ __device__ inline int rows_maxw(const TGeom& G) {
-  int maxw = 1;
-  for (int l = 1; l <= G.n; ++l) maxw = G.d[l] > maxw ? G.d[l] : maxw;
-  return maxw;
-}
-
-// Slot of the bound of row (domain d, negated, neuron j) in the seeded-row
-// bound buffer [B][2][maxw]: by neuron, so that the cut finds a domain's
-// bounds without the rows' packed offsets (no dependent load).
-__device__ __forceinline__ int64_t slb_slot(int64_t d, int neg, int j, int maxw) {
-  return (d * 2 + neg) * (int64_t)maxw + j;
-}
-
 // fc0_concretize for rows of different domains: the box values of the
 // lane's first-M-tile inputs (m = 4 g + i) come preloaded in registers,
 // further M-tiles (more than 16 inputs) read them from dxl / dxh.
@@ -2651,7 +2637,6 @@ __global__ __launch_bounds__(RNW * 64, 4) void k_crown_rows(
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int n = G.n, d0 = G.d[0];
-  const int maxw = rows_maxw(G);
   vcm::stage_float4(sfrag, gfrag, G.nfloats / 4);
   for (int k = threadIdx.x; k < n * FW; k += blockDim.x) {
     const int l = k / FW, j = k % FW;
@@ -2712,7 +2697,7 @@ __global__ __launch_bounds__(RNW * 64, 4) void k_crown_rows(
         }
     }
     const double lbd = group_sum4_d(acc[0] + cz[0]);
-    if (g == 0 && live) slb[slb_slot(d, (code >> 6) & 1u, j, maxw)] = (float)lbd;
+    if (g == 0 && live) slb[row] = (float)lbd;
   }
 }
 
@@ -2732,13 +2717,10 @@ __global__ __launch_bounds__(256) void k_rows_cut(TGeom G, int64_t B, int L, Row
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int dW = G.d[L + 1];
   const bool in = lane < dW;
-  const int maxw = rows_maxw(G);
   for (int64_t d0 = ((int64_t)blockIdx.x * 4 + wv) * 2; d0 < B; d0 += (int64_t)gridDim.x * 8) {
-    float lo[2], hi[2], sp[2], sn[2];
+    float lo[2], hi[2];
     uint64_t m[2], mn[2];
-    int64_t bn[2];
-    // every load at once: the seeded rows' bounds sit at their neuron's
-    // slot (a lane not seeded reads a slot it then ignores)
+    int64_t base[2], bn[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int64_t d = d0 + k;
@@ -2746,12 +2728,22 @@ __global__ __launch_bounds__(256) void k_rows_cut(TGeom G, int64_t B, int L, Row
       lo[k] = (v && in) ? rl.lo[L][d * dW + lane] : 0.f;
       hi[k] = (v && in) ? rl.hi[L][d * dW + lane] : 0.f;
       m[k] = (v && masks) ? masks[(int64_t)L * B + d] : 0ull;
-      sp[k] = (v && in && masks) ? slb[slb_slot(d, 0, lane, maxw)] : 0.f;
-      sn[k] = (v && in && masks) ? slb[slb_slot(d, 1, lane, maxw)] : 0.f;
+      base[k] = (v && masks)
+                    ? (int64_t)off[(int64_t)L * B + d] + bsum[L * nblk + (int)(d / RSCAN)]
+                    : 0;
       mn[k] = (v && wnext) ? masks[(int64_t)(L + 1) * B + d] : 0ull;
       bn[k] = (v && wnext) ? (int64_t)off[(int64_t)(L + 1) * B + d] +
                                  bsum[(L + 1) * nblk + (int)(d / RSCAN)]
                            : 0;
+    }
+    float sp[2], sn[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const bool seeded = in && ((m[k] >> lane) & 1ull);
+      const int cnt = __popcll(m[k]);
+      const int q = __popcll(m[k] & ((1ull << lane) - 1ull));
+      sp[k] = seeded ? slb[base[k] + q] : 0.f;
+      sn[k] = seeded ? slb[base[k] + cnt + q] : 0.f;
     }
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
