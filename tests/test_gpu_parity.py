@@ -842,6 +842,50 @@ def test_alpha_small_batch_kernel_matches_large_batch_kernel(gpu, n_iters):
         assert_adam_drift(small, big[:600], what)
 
 
+@pytest.mark.parametrize('n', [1000, 5000])
+@pytest.mark.parametrize('stop', ['eps', 'positive'])
+def test_alpha_control_best_and_stops(gpu, n, stop):
+    """vc_alpha_control, one iteration per call, in both of its launch forms
+    (n = 1,000: the bounds held in registers; 5,000: best written in the
+    sweep), against the loop bookkeeping of verify_zono_bnb.py:5252-5287
+    kept on the host: best = bound at it = 0, else max(best, bound); the
+    loop stops when every best bound is > 0, or when max(best) - the
+    previous max < eps (it > 0); ctl = {max, stopped, iterations, max};
+    once stopped, later calls change nothing.  max and the sign test are
+    exact, so every value must agree bit for bit."""
+    g = torch.Generator().manual_seed(n + (1 if stop == 'eps' else 2))
+    eps = 1e-3
+    base = torch.rand(n, generator=g) * 2 - 3.0      # all negative
+    steps = []
+    for it in range(8):
+        if stop == 'eps':
+            # the max rises by 0.5 up to iteration 4, then by 1e-4 < eps:
+            # the stop at iteration 5
+            lb = base + (0.5 * it if it < 4 else 2.0 + 1e-4 * (it - 3))
+        else:
+            # some bound <= 0 up to iteration 2 (base + 2.75 spans
+            # [-0.25, 1.75)), every one > 0 at iteration 3: the stop there
+            lb = base + (1.5 * it - 0.25)
+        steps.append(lb.float())
+    best_d = torch.zeros(n, device=gpu)
+    ctl_d = torch.tensor([-float('inf'), 0.0, 0.0, 0.0], device=gpu)
+    best = None
+    ctl = [-float('inf'), 0.0, 0.0, 0.0]
+    for it, lb in enumerate(steps):
+        lb_d = lb.to(gpu)
+        call('vc_alpha_control', ptr(best_d), ptr(lb_d), n, it, eps, ptr(ctl_d), None,
+             _lib_stream())
+        if ctl[1] == 0.0:
+            best = lb.clone() if it == 0 else torch.maximum(best, lb)
+            mx = float(best.max())
+            stopped = bool((best > 0).all()) or (it > 0 and mx - ctl[0] < eps)
+            ctl = [mx, 1.0 if stopped else 0.0, float(it + 1), mx]
+        got = cpu(ctl_d).tolist()
+        assert got == ctl, (it, got, ctl)
+        assert torch.equal(cpu(best_d).view(torch.int32), best.view(torch.int32)), it
+    assert ctl[1] == 1.0 and ctl[2] == (6.0 if stop == 'eps' else 4.0)
+
+
 # ----------------------------------------------------------------- a11-a14
 @pytest.mark.parametrize('n, Q', [(5, 4), (12, 4), (5, 16), (12, 8), (20, 4)])
 def test_clip_parity_identical_inputs(gpu, n, Q):
